@@ -1,0 +1,228 @@
+"""GPU parity of the MoE path, the logit reductions and the device-side generator (MI355X)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import moe_inputs as mi
+import oracle_lib
+import wzy_amd
+from oracle_lib import ptr
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def stream_ptr(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def device_layer(torch, wz, m, planes=None):
+    """Upload a MoeLayer; experts come from `planes` (host plane bytes) or the device generator."""
+    rec = wz.wzy_nvfp4_expert_bytes(m.D, m.F)
+    d = {}
+    d["router"] = dev(torch, m.router.view(np.int16))
+    d["sgate"] = dev(torch, m.sgate.view(np.int16))
+    for k, (q, s) in m.sh.items():
+        d[k + "_q"] = dev(torch, q)
+        d[k + "_s"] = dev(torch, s.view(np.int16))
+    if planes is not None:
+        d["experts"] = dev(torch, planes)
+    else:
+        d["experts"] = torch.empty(rec * m.E, dtype=torch.uint8, device="cuda")
+        wz.wzy_synth_experts_device(m.seed, m.layer, 0, m.E, m.D, m.F, d["experts"].data_ptr(), stream_ptr(torch))
+    w = wzy_amd.MoeWeights()
+    w.n_embd, w.n_ff, w.n_exp, w.top_k = m.D, m.F, m.E, m.K
+    w.router, w.sgate, w.experts = d["router"].data_ptr(), d["sgate"].data_ptr(), d["experts"].data_ptr()
+    w.sh_gate_q, w.sh_gate_s = d["gate_q"].data_ptr(), d["gate_s"].data_ptr()
+    w.sh_up_q, w.sh_up_s = d["up_q"].data_ptr(), d["up_s"].data_ptr()
+    w.sh_down_q, w.sh_down_s = d["down_q"].data_ptr(), d["down_s"].data_ptr()
+    return w, d
+
+
+def run_gpu_moe(torch, wz, w, x, T):
+    D, K = w.n_embd, w.top_k
+    xd = dev(torch, x.reshape(T, D))
+    comb = torch.empty(T * D, dtype=torch.float32, device="cuda")
+    ids = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    wts = torch.empty(T * K, dtype=torch.float32, device="cuda")
+    nws = wz.wzy_moe_workspace_bytes(D, w.n_ff, w.n_exp, K, T)
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
+    wz.wzy_moe_block(C.byref(w), xd.data_ptr(), T, comb.data_ptr(), ids.data_ptr(), wts.data_ptr(),
+                     ws.data_ptr(), nws, stream_ptr(torch))
+    torch.cuda.synchronize()
+    return host(comb), host(ids), host(wts)
+
+
+def check_ids(orc, logits, E, K, T, ids_gpu, ids_orc):
+    """Routed ids bit-exact, except a row whose oracle margin p_K - p_{K+1} is within float noise."""
+    probs = np.empty(T * E, np.float32); i2 = np.empty(T * K, np.int32); w2 = np.empty(T * K, np.float32)
+    orc.orc_router_topk(ptr(logits), E, K, T, ptr(i2), ptr(w2), ptr(probs))
+    exact_rows = 0
+    for t in range(T):
+        p = np.sort(probs[t * E:(t + 1) * E])[::-1]
+        margin = p[K - 1] - p[K] if K < E else 1.0
+        if margin > 1e-6 * p[0]:
+            assert set(ids_gpu[t * K:(t + 1) * K]) == set(ids_orc[t * K:(t + 1) * K]), t
+            np.testing.assert_array_equal(ids_gpu[t * K:(t + 1) * K], ids_orc[t * K:(t + 1) * K])
+            exact_rows += 1
+    return exact_rows
+
+
+def test_device_generator_matches_host(wz, cuda):
+    import torch
+    D, F = 2048, 512
+    rec = wz.wzy_nvfp4_expert_bytes(D, F)
+    buf = torch.empty(3 * rec, dtype=torch.uint8, device="cuda")
+    wz.wzy_synth_experts_device(0, 7, 100, 3, D, F, buf.data_ptr(), stream_ptr(torch))
+    got = host(buf)
+    for i in range(3):
+        ref = np.empty(rec, np.uint8)
+        wz.wzy_synth_expert_planes(0, 7, 100 + i, D, F, ref.ctypes.data)
+        np.testing.assert_array_equal(got[i * rec:(i + 1) * rec], ref)
+    # and the host repack of the reference-layout blob gives the same planes
+    blob = mi.expert_blob(wz, 0, 7, 101, D, F)
+    rp = np.empty(rec, np.uint8)
+    wz.wzy_nvfp4_repack_host(blob.ctypes.data, rp.ctypes.data, D, F)
+    np.testing.assert_array_equal(rp, got[rec:2 * rec])
+    n, kvd = 1000, 512
+    kq = torch.empty(n * kvd, dtype=torch.int8, device="cuda")
+    ks = torch.empty(n * kvd // 64, dtype=torch.int16, device="cuda")
+    wz.wzy_synth_kv_device(2, 3, 1, 4090, n, kvd, kq.data_ptr(), ks.data_ptr(), stream_ptr(torch))
+    hq = np.empty(n * kvd, np.int8); hs = np.empty(n * kvd // 64, np.uint16)
+    wz.wzy_synth_kv_host(2, 3, 1, 4090, n, kvd, hq.ctypes.data, hs.ctypes.data)
+    np.testing.assert_array_equal(host(kq), hq)
+    np.testing.assert_array_equal(host(ks).view(np.uint16), hs)
+    assert hq.min() == -127 and hq.max() == 127
+
+
+@pytest.mark.parametrize("cols,T", [(2048, 1), (512, 8), (320, 3), (8192, 2)])
+def test_quant_act_bit_exact(wz, orc, cuda, cols, T):
+    import torch
+    x = np.random.default_rng(cols + T).standard_normal(T * cols).astype(np.float32)
+    x[:32] = 0.0
+    xd = dev(torch, x)
+    q32 = torch.empty(T * cols, dtype=torch.int8, device="cuda"); s32 = torch.empty(T * cols // 32, device="cuda")
+    q16 = torch.empty(T * cols, dtype=torch.int8, device="cuda"); s16 = torch.empty(T * cols // 16, device="cuda")
+    wz.wzy_quant_act(xd.data_ptr(), q32.data_ptr(), s32.data_ptr(), q16.data_ptr(), s16.data_ptr(), cols, T,
+                     stream_ptr(torch))
+    r32 = np.empty(T * cols, np.int8); rs32 = np.empty(T * cols // 32, np.float32)
+    r16 = np.empty(T * cols, np.int8); rs16 = np.empty(T * cols // 16, np.float32)
+    orc.orc_quant_act(ptr(x), cols, T, ptr(r32), ptr(rs32), ptr(r16), ptr(rs16))
+    np.testing.assert_array_equal(host(q32), r32)
+    np.testing.assert_array_equal(host(s32), rs32)
+    np.testing.assert_array_equal(host(q16), r16)
+    np.testing.assert_array_equal(host(s16), rs16)
+
+
+@pytest.mark.parametrize("rows,cols,T", [(6144, 2048, 1), (2048, 6144, 4), (8192, 320, 8), (2048, 512, 2), (100, 96, 5)])
+def test_gemv_q8_parity(wz, orc, cuda, rows, cols, T):
+    import torch
+    codes = np.empty(rows * cols, np.int8); sc = np.empty(rows * cols // 32, np.uint16)
+    wz.wzy_synth_q8(3, 9, rows, cols, float(1 / np.sqrt(cols)), ptr(codes), ptr(sc))
+    x = np.random.default_rng(rows).standard_normal(T * cols).astype(np.float32)
+    q32 = np.empty(T * cols, np.int8); s32 = np.empty(T * cols // 32, np.float32)
+    orc.orc_quant_act(ptr(x), cols, T, ptr(q32), ptr(s32), None, None)
+    ref = np.empty(T * rows, np.float32)
+    orc.orc_gemv_q8(ptr(codes), ptr(sc), ptr(q32), ptr(s32), ptr(ref), rows, cols, T)
+    y = torch.empty(T * rows, device="cuda")
+    wz.wzy_gemv_q8(dev(torch, codes).data_ptr(), dev(torch, sc.view(np.int16)).data_ptr(), dev(torch, q32).data_ptr(),
+                   dev(torch, s32).data_ptr(), y.data_ptr(), rows, cols, T, 0, stream_ptr(torch))
+    np.testing.assert_allclose(host(y), ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("rows,cols,T", [(512, 2048, 1), (151936, 2048, 1), (128, 2048, 8), (4, 8192, 3), (33, 264, 2)])
+def test_gemv_bf16_parity(wz, orc, cuda, rows, cols, T):
+    import torch
+    W = np.empty(rows * cols, np.uint16)
+    wz.wzy_synth_normal_bf16(4, 1, rows * cols, 0.0, 0.02, ptr(W))
+    x = np.random.default_rng(cols).standard_normal(T * cols).astype(np.float32)
+    y = torch.empty(T * rows, device="cuda")
+    wz.wzy_gemv_bf16(dev(torch, W.view(np.int16)).data_ptr(), dev(torch, x).data_ptr(), y.data_ptr(), rows, cols, T, 0,
+                     stream_ptr(torch))
+    ref = np.empty(T * rows, np.float32)
+    orc.orc_gemv_bf16(ptr(W), ptr(x), ptr(ref), rows, cols, T)
+    np.testing.assert_allclose(host(y), ref, rtol=1e-5, atol=2e-5 * np.abs(ref).max())
+
+
+def test_moe_config1_parity(wz, orc, cuda):
+    """D=2048, 512 experts top-10, NFF=512, seed 0, one token."""
+    import torch
+    D, F, E, K, T = 2048, 512, 512, 10, 1
+    m = mi.make_layer(wz, 0, 0, D, F, E, K, blobs=[])
+    x = mi.make_x(wz, 0, 0, T, D).ravel()
+    # oracle routing first, then materialise only the routed experts on the host
+    logits = np.empty(T * E, np.float32)
+    orc.orc_gemv_bf16(ptr(m.router), ptr(x), ptr(logits), E, D, T)
+    ids0 = np.empty(T * K, np.int32); w0 = np.empty(T * K, np.float32)
+    orc.orc_router_topk(ptr(logits), E, K, T, ptr(ids0), ptr(w0), None)
+    for e in set(ids0.tolist()):
+        m.blobs[e] = mi.expert_blob(wz, 0, 0, e, D, F)
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
+    assert orc.orc_moe_block(C.byref(ow), ptr(x), T, ptr(comb_o), ptr(ids_o), ptr(wts_o), None, None) == 0
+    w, keep = device_layer(torch, wz, m)
+    comb, ids, wts = run_gpu_moe(torch, wz, w, x, T)
+    assert check_ids(orc, logits, E, K, T, ids, ids_o) == T
+    np.testing.assert_allclose(wts, wts_o, rtol=1e-4)
+    np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
+    err = np.abs(comb - comb_o).max() / np.abs(comb_o).max()
+    assert err < 2e-3, err
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
+def test_moe_multirow_parity(wz, orc, cuda, T):
+    """Window rows share experts (grouping path); experts uploaded from host-repacked blobs."""
+    import torch
+    D, F, E, K = 512, 128, 16, 4
+    m = mi.make_layer(wz, 21, 5, D, F, E, K)
+    x = mi.make_x(wz, 21, 5, T, D).ravel()
+    rec = wz.wzy_nvfp4_expert_bytes(D, F)
+    planes = np.empty(E * rec, np.uint8)
+    for e in range(E):
+        wz.wzy_nvfp4_repack_host(m.blobs[e].ctypes.data, planes[e * rec:].ctypes.data, D, F)
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
+    logits = np.empty(T * E, np.float32)
+    assert orc.orc_moe_block(C.byref(ow), ptr(x), T, ptr(comb_o), ptr(ids_o), ptr(wts_o), ptr(logits), None) == 0
+    w, keep = device_layer(torch, wz, m, planes=planes)
+    comb, ids, wts = run_gpu_moe(torch, wz, w, x, T)
+    exact = check_ids(orc, logits, E, K, T, ids, ids_o)
+    assert exact >= T - 1
+    if exact == T:
+        np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("V,T", [(151936, 1), (151936, 4), (248320, 2), (3000, 8)])
+def test_row_argmax_top16_parity(wz, orc, cuda, V, T):
+    import torch
+    rng = np.random.default_rng(V + T)
+    l = rng.standard_normal(T * V).astype(np.float32)
+    l[V // 2] = l[V // 3] = 40.0                # top tie in row 0 -> lower id
+    if T > 1:
+        l[V + 5:V + 40] = 30.0                  # 35-way tie at the top of row 1
+    ld = dev(torch, l)
+    g = torch.empty(T, dtype=torch.int32, device="cuda")
+    a = torch.empty(T, dtype=torch.int32, device="cuda")
+    tv = torch.empty(T * 16, device="cuda"); ti = torch.empty(T * 16, dtype=torch.int32, device="cuda")
+    wz.wzy_row_argmax(ld.data_ptr(), V, T, a.data_ptr(), stream_ptr(torch))
+    wz.wzy_row_top16(ld.data_ptr(), V, T, g.data_ptr(), tv.data_ptr(), ti.data_ptr(), stream_ptr(torch))
+    ra = np.empty(T, np.int32); rg = np.empty(T, np.int32); rv = np.empty(T * 16, np.float32); ri = np.empty(T * 16, np.int32)
+    orc.orc_row_argmax(ptr(l), V, T, ptr(ra))
+    orc.orc_row_top16(ptr(l), V, T, ptr(rg), ptr(rv), ptr(ri))
+    np.testing.assert_array_equal(host(a), ra)
+    np.testing.assert_array_equal(host(g), rg)
+    np.testing.assert_array_equal(host(ti), ri)
+    np.testing.assert_array_equal(host(tv), rv)
+    # second call reuses the arrival counters (they must be back at zero)
+    wz.wzy_row_argmax(ld.data_ptr(), V, T, a.data_ptr(), stream_ptr(torch))
+    np.testing.assert_array_equal(host(a), ra)

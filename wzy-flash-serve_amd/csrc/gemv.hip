@@ -1,0 +1,309 @@
+// gemv.hip -- activation quantisation and the dense decode GEMVs (Q8_0 and bf16) for gfx950.
+//
+// GEMV shape: one 64-lane wave owns RPW*G consecutive output rows, G = 64/LPR rows at a time
+// (LPR = lanes per row).  Every lane loads 16-32 contiguous weight bytes per row per step with
+// 128-bit loads, all RPW rows' loads are issued before any arithmetic so each wave keeps
+// RPW*16..32 bytes per lane in flight, and the T window rows reuse every weight load.
+// Partial sums are reduced across the LPR lanes with DPP/swizzle (no LDS).
+#include "wzy_device.h"
+#include "wzy_gemv.h"
+#include "wzy_host.h"
+
+using namespace wzy;
+
+// ---------------------------------------------------------------------------------------------
+// quant_act: one thread per 32-value block, emits the two per-16 blocks and the per-32 block.
+// reference: quant_act_multi (src/wzy_kernels_v2.cuh:58-107)
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) quant_act_kernel(const float* __restrict__ x, int8_t* __restrict__ q32,
+                                                        float* __restrict__ s32, int8_t* __restrict__ q16,
+                                                        float* __restrict__ s16, int n_blk32) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_blk32) return;
+    const float4* xp = (const float4*) (x + (size_t) g * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 f = xp[i];
+        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { a0 = fmaxf(a0, fabsf(v[i])); a1 = fmaxf(a1, fabsf(v[16 + i])); }
+    if (q16) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float am = h ? a1 : a0;
+            const float d = am / 127.0f;
+            const float inv = d > 0.f ? 127.0f / am : 0.f;
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                uint32_t pk = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    int q = rn_int(v[16 * h + 4 * k + j] * inv);
+                    q = max(-127, min(127, q));
+                    pk |= (uint32_t) (q & 0xFF) << (8 * j);
+                }
+                w[k] = pk;
+            }
+            *(uint4*) (q16 + (size_t) g * 32 + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
+            s16[2 * g + h] = d;
+        }
+    }
+    if (q32) {
+        const float am = fmaxf(a0, a1);
+        const float d = am / 127.0f;
+        const float inv = d > 0.f ? 127.0f / am : 0.f;
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t pk = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int q = rn_int(v[4 * k + j] * inv);
+                q = max(-127, min(127, q));
+                pk |= (uint32_t) (q & 0xFF) << (8 * j);
+            }
+            w[k] = pk;
+        }
+        uint4* o = (uint4*) (q32 + (size_t) g * 32);
+        o[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        o[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        s32[g] = d;
+    }
+}
+
+namespace wzy {
+int launch_quant_act(const float* x, int8_t* q32, float* s32, int8_t* q16, float* s16, int cols, int T,
+                     hipStream_t st) {
+    WZY_REQUIRE(x && cols > 0 && cols % 32 == 0 && T >= 1, "quant_act: cols must be a positive multiple of 32");
+    WZY_REQUIRE((q32 == nullptr) == (s32 == nullptr) && (q16 == nullptr) == (s16 == nullptr),
+                "quant_act: q/s outputs must be given in pairs");
+    const int n = cols / 32 * T;
+    hipLaunchKernelGGL(quant_act_kernel, dim3((n + 255) / 256), dim3(256), 0, st, x, q32, s32, q16, s16, n);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+}  // namespace wzy
+
+// ---------------------------------------------------------------------------------------------
+// Q8_0 GEMV.  reference: gemm_q8p_t / launch_gemm_q8p (src/wzy_kernels_v2.cuh:120-159,230-303):
+// per 32-block b: acc += fp16(scale) * xs[b] * sum(codes*xq); then a cross-lane sum per row.
+// ---------------------------------------------------------------------------------------------
+template <int LPR>
+WZY_DEV float seg_sum(float v) {
+    if constexpr (LPR == 16) return sum16(v);
+    else if constexpr (LPR == 32) return sum32(v);
+    else return wave_sum(v);
+}
+
+template <int T, int LPR, int RPW>
+__global__ void __launch_bounds__(256) gemv_q8_kernel(const int8_t* __restrict__ codes,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                      float* __restrict__ y, int rows, int cols, int y_stride) {
+    constexpr int G = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int li = lane % LPR, gi = lane / LPR;
+    const int nb = cols >> 5;
+    const int row0 = wave * RPW * G + gi;
+    float acc[RPW][T];
+#pragma unroll
+    for (int s = 0; s < RPW; ++s)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
+
+    for (int b = li; b < nb; b += LPR) {
+        int4 c0[RPW], c1[RPW];
+        float dw[RPW];
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) {
+            const int r = row0 + s * G;
+            if (r < rows) {
+                const int4* cp = (const int4*) (codes + (size_t) r * cols + (size_t) b * 32);
+                c0[s] = ld_stream_i4(cp);
+                c1[s] = ld_stream_i4(cp + 1);
+                dw[s] = h16_to_f(scales[(size_t) r * nb + b]);
+            } else {
+                c0[s] = c1[s] = make_int4(0, 0, 0, 0);
+                dw[s] = 0.f;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int4* xp = (const int4*) (xq + (size_t) t * cols + (size_t) b * 32);
+            const int4 x0 = xp[0], x1 = xp[1];
+            const float xsc = xs[(size_t) t * nb + b];
+#pragma unroll
+            for (int s = 0; s < RPW; ++s) {
+                const int isum = dot16(c1[s], x1) + dot16(c0[s], x0);
+                acc[s][t] = fmaf(dw[s] * xsc, (float) isum, acc[s][t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < RPW; ++s) {
+        const int r = row0 + s * G;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = seg_sum<LPR>(acc[s][t]);
+            if (li == 0 && r < rows) y[(size_t) t * y_stride + r] = v;
+        }
+    }
+}
+
+template <int T, int LPR, int RPW>
+static void launch_q8_t(const int8_t* codes, const uint16_t* scales, const int8_t* xq, const float* xs, float* y,
+                        int rows, int cols, int y_stride, hipStream_t st) {
+    constexpr int rows_per_wave = RPW * (64 / LPR);
+    const int waves = (rows + rows_per_wave - 1) / rows_per_wave;
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL((gemv_q8_kernel<T, LPR, RPW>), dim3(blocks), dim3(256), 0, st, codes, scales, xq, xs, y, rows,
+                       cols, y_stride);
+}
+
+template <int T>
+static void launch_q8_lpr(const int8_t* codes, const uint16_t* scales, const int8_t* xq, const float* xs, float* y,
+                          int rows, int cols, int y_stride, hipStream_t st) {
+    const int nb = cols / 32;
+    if (nb >= 64) launch_q8_t<T, 64, 4>(codes, scales, xq, xs, y, rows, cols, y_stride, st);
+    else if (nb > 16) launch_q8_t<T, 32, 2>(codes, scales, xq, xs, y, rows, cols, y_stride, st);
+    else launch_q8_t<T, 16, 2>(codes, scales, xq, xs, y, rows, cols, y_stride, st);
+}
+
+namespace wzy {
+int launch_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq, const float* xs, float* y, int rows,
+                   int cols, int T, int y_stride, hipStream_t st) {
+    WZY_REQUIRE(codes && scales && xq && xs && y, "gemv_q8: null pointer");
+    WZY_REQUIRE(rows > 0 && cols > 0 && cols % 32 == 0, "gemv_q8: rows > 0 and cols %% 32 == 0 required");
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "gemv_q8: T must be in [1, %d]", WZY_MAX_W);
+    if (y_stride == 0) y_stride = rows;
+    switch (T) {
+        case 1: launch_q8_lpr<1>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 2: launch_q8_lpr<2>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 3: launch_q8_lpr<3>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 4: launch_q8_lpr<4>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 5: launch_q8_lpr<5>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 6: launch_q8_lpr<6>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        case 7: launch_q8_lpr<7>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+        default: launch_q8_lpr<8>(codes, scales, xq, xs, y, rows, cols, y_stride, st); break;
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+}  // namespace wzy
+
+// ---------------------------------------------------------------------------------------------
+// bf16 GEMV.  reference: gemm_bf16_t / launch_gemm_bf16 (src/wzy_kernels_v2.cuh:307-387).
+// Optional extra row (Wx, yx): handled as row `rows`, written to yx[t] (used for the shared-expert
+// gate row next to the router).
+// ---------------------------------------------------------------------------------------------
+template <int T, int RPW>
+__global__ void __launch_bounds__(256) gemv_bf16_kernel(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                                        float* __restrict__ y, int rows, int cols, int y_stride,
+                                                        const uint16_t* __restrict__ Wx, float* __restrict__ yx) {
+    const int lane = threadIdx.x & 63;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int n8 = cols >> 3;
+    const int row0 = wave * RPW;
+    const int rows_tot = rows + (Wx ? 1 : 0);
+    float acc[RPW][T];
+#pragma unroll
+    for (int s = 0; s < RPW; ++s)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
+
+    for (int j = lane; j < n8; j += 64) {
+        uint4 w[RPW];
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) {
+            const int r = row0 + s;
+            if (r < rows) w[s] = ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j);
+            else if (r < rows_tot) w[s] = ((const uint4*) Wx)[j];
+            else w[s] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float4 xa = *(const float4*) (x + (size_t) t * cols + j * 8);
+            const float4 xb = *(const float4*) (x + (size_t) t * cols + j * 8 + 4);
+#pragma unroll
+            for (int s = 0; s < RPW; ++s) {
+                float a = acc[s][t];
+                a = fmaf(bf16_lo(w[s].x), xa.x, a);
+                a = fmaf(bf16_hi(w[s].x), xa.y, a);
+                a = fmaf(bf16_lo(w[s].y), xa.z, a);
+                a = fmaf(bf16_hi(w[s].y), xa.w, a);
+                a = fmaf(bf16_lo(w[s].z), xb.x, a);
+                a = fmaf(bf16_hi(w[s].z), xb.y, a);
+                a = fmaf(bf16_lo(w[s].w), xb.z, a);
+                a = fmaf(bf16_hi(w[s].w), xb.w, a);
+                acc[s][t] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < RPW; ++s) {
+        const int r = row0 + s;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[s][t]);
+            if (lane == 0) {
+                if (r < rows) y[(size_t) t * y_stride + r] = v;
+                else if (r < rows_tot) yx[t] = v;
+            }
+        }
+    }
+}
+
+template <int T>
+static void launch_bf16_t(const uint16_t* W, const float* x, float* y, int rows, int cols, int y_stride,
+                          const uint16_t* Wx, float* yx, hipStream_t st) {
+    constexpr int RPW = 4;
+    const int rows_tot = rows + (Wx ? 1 : 0);
+    const int waves = (rows_tot + RPW - 1) / RPW;
+    const int blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL((gemv_bf16_kernel<T, RPW>), dim3(blocks), dim3(256), 0, st, W, x, y, rows, cols, y_stride, Wx,
+                       yx);
+}
+
+namespace wzy {
+int launch_gemv_bf16(const uint16_t* W, const float* x, float* y, int rows, int cols, int T, int y_stride,
+                     const uint16_t* Wx, float* yx, hipStream_t st) {
+    WZY_REQUIRE(W && x && y, "gemv_bf16: null pointer");
+    WZY_REQUIRE(rows > 0 && cols > 0 && cols % 8 == 0, "gemv_bf16: rows > 0 and cols %% 8 == 0 required");
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "gemv_bf16: T must be in [1, %d]", WZY_MAX_W);
+    WZY_REQUIRE((Wx == nullptr) == (yx == nullptr), "gemv_bf16: extra row needs both Wx and yx");
+    if (y_stride == 0) y_stride = rows;
+    switch (T) {
+        case 1: launch_bf16_t<1>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 2: launch_bf16_t<2>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 3: launch_bf16_t<3>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 4: launch_bf16_t<4>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 5: launch_bf16_t<5>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 6: launch_bf16_t<6>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        case 7: launch_bf16_t<7>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+        default: launch_bf16_t<8>(W, x, y, rows, cols, y_stride, Wx, yx, st); break;
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+}  // namespace wzy
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------
+extern "C" int wzy_quant_act(const float* x, int8_t* q32, float* s32, int8_t* q16, float* s16, int cols, int T,
+                             void* stream) {
+    return launch_quant_act(x, q32, s32, q16, s16, cols, T, as_stream(stream));
+}
+extern "C" int wzy_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq, const float* xs, float* y,
+                           int rows, int cols, int T, int y_stride, void* stream) {
+    return launch_gemv_q8(codes, scales, xq, xs, y, rows, cols, T, y_stride, as_stream(stream));
+}
+extern "C" int wzy_gemv_bf16(const uint16_t* W, const float* x, float* y, int rows, int cols, int T, int y_stride,
+                             void* stream) {
+    return launch_gemv_bf16(W, x, y, rows, cols, T, y_stride, nullptr, nullptr, as_stream(stream));
+}

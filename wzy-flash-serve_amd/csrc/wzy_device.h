@@ -1,0 +1,222 @@
+// wzy_device.h -- gfx950 (CDNA4) device helpers shared by every kernel of the decode path.
+//
+// Wave-level primitives are written for 64-lane wavefronts: intra-row steps use DPP
+// (quad_perm / row_half_mirror / row_mirror), the row-16 step uses ds_swizzle and the
+// last step reads lane 32 with v_readlane, so a full 64-lane reduction never touches LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WZY_DEV __device__ __forceinline__
+
+namespace wzy {
+
+// ---------------------------------------------------------------------------------------------
+// bit casts and small formats
+// ---------------------------------------------------------------------------------------------
+WZY_DEV float as_f(int v) { return __builtin_bit_cast(float, v); }
+WZY_DEV int as_i(float v) { return __builtin_bit_cast(int, v); }
+WZY_DEV float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+WZY_DEV float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+WZY_DEV float bf16_to_f(uint16_t h) { return __builtin_bit_cast(float, (uint32_t) h << 16); }
+
+// IEEE binary16 <-> fp32 through the hardware conversion instructions (v_cvt_f32_f16 / v_cvt_f16_f32,
+// round-to-nearest-even).
+WZY_DEV float h16_to_f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+WZY_DEV uint16_t f_to_h16(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
+WZY_DEV float round_h16(float f) { return (float) (_Float16) f; }
+
+// round-half-even float -> int (the reference's __float2int_rn / _mm_cvtss_si32)
+WZY_DEV int rn_int(float x) { return (int) __builtin_rintf(x); }
+
+WZY_DEV float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+WZY_DEV float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+
+// ---------------------------------------------------------------------------------------------
+// DPP / swizzle wave reductions (64 lanes)
+// ---------------------------------------------------------------------------------------------
+// dpp_ctrl encodings (GCN3+ ISA): quad_perm = p0 | p1<<2 | p2<<4 | p3<<6, row_mirror 0x140,
+// row_half_mirror 0x141.  All four patterns read a valid lane, so bound_ctrl is irrelevant.
+template <int CTRL>
+WZY_DEV float dpp_f(float v) {
+    return as_f(__builtin_amdgcn_update_dpp(as_i(v), as_i(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+WZY_DEV int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7-i within each 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15-i within each 16
+// ds_swizzle bit-mode offset: and_mask | or_mask<<5 | xor_mask<<10 (operates inside 32-lane halves)
+constexpr int SWZ_XOR16 = (0x10 << 10) | 0x1F;
+constexpr int SWZ_XOR8 = (0x08 << 10) | 0x1F;
+
+template <int PAT>
+WZY_DEV float swz_f(float v) { return as_f(__builtin_amdgcn_ds_swizzle(as_i(v), PAT)); }
+template <int PAT>
+WZY_DEV int swz_i(int v) { return __builtin_amdgcn_ds_swizzle(v, PAT); }
+
+// Sum over each group of 16 consecutive lanes; every lane of the group gets the group sum.
+WZY_DEV float sum16(float v) {
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    v += dpp_f<DPP_HALF_MIRROR>(v);
+    v += dpp_f<DPP_MIRROR>(v);
+    return v;
+}
+// Sum over each group of 8 consecutive lanes.
+WZY_DEV float sum8(float v) {
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    v += dpp_f<DPP_HALF_MIRROR>(v);
+    return v;
+}
+// Sum over each group of 32 lanes (lanes 0-31 / 32-63).
+WZY_DEV float sum32(float v) {
+    v = sum16(v);
+    v += swz_f<SWZ_XOR16>(v);
+    return v;
+}
+// Full 64-lane sum, wave-uniform result.
+WZY_DEV float wave_sum(float v) {
+    v = sum32(v);
+    const float a = as_f(__builtin_amdgcn_readlane(as_i(v), 0));
+    const float b = as_f(__builtin_amdgcn_readlane(as_i(v), 32));
+    return a + b;
+}
+WZY_DEV float max16(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return v;
+}
+WZY_DEV float max32(float v) {
+    v = max16(v);
+    v = fmaxf(v, swz_f<SWZ_XOR16>(v));
+    return v;
+}
+WZY_DEV float wave_max(float v) {
+    v = max32(v);
+    const float a = as_f(__builtin_amdgcn_readlane(as_i(v), 0));
+    const float b = as_f(__builtin_amdgcn_readlane(as_i(v), 32));
+    return fmaxf(a, b);
+}
+
+// (value, index) argmax step: larger value wins, ties go to the lower index.
+WZY_DEV void amax_merge(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+// Full-wave argmax with lowest-index tie-break; result is wave-uniform.
+WZY_DEV void wave_argmax(float& bv, int& bi) {
+    amax_merge(bv, bi, dpp_f<DPP_XOR1>(bv), dpp_i<DPP_XOR1>(bi));
+    amax_merge(bv, bi, dpp_f<DPP_XOR2>(bv), dpp_i<DPP_XOR2>(bi));
+    amax_merge(bv, bi, dpp_f<DPP_HALF_MIRROR>(bv), dpp_i<DPP_HALF_MIRROR>(bi));
+    amax_merge(bv, bi, dpp_f<DPP_MIRROR>(bv), dpp_i<DPP_MIRROR>(bi));
+    amax_merge(bv, bi, swz_f<SWZ_XOR16>(bv), swz_i<SWZ_XOR16>(bi));
+    const float v32 = as_f(__builtin_amdgcn_readlane(as_i(bv), 32));
+    const int i32 = __builtin_amdgcn_readlane(bi, 32);
+    bv = as_f(__builtin_amdgcn_readlane(as_i(bv), 0));
+    bi = __builtin_amdgcn_readlane(bi, 0);
+    amax_merge(bv, bi, v32, i32);
+}
+
+// Block-wide sum for blockDim.x = NW*64 threads; `sh` must hold NW floats. Result on every thread.
+template <int NW>
+WZY_DEV float block_sum(float v, float* sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += sh[i];
+    __syncthreads();
+    return t;
+}
+template <int NW>
+WZY_DEV float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float t = sh[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) t = fmaxf(t, sh[i]);
+    __syncthreads();
+    return t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// streaming 128-bit loads: weights are read once per token, so they are loaded with the
+// non-temporal hint and do not displace activations in the caches.
+// ---------------------------------------------------------------------------------------------
+typedef int wzy_v4i __attribute__((ext_vector_type(4)));
+WZY_DEV int4 ld_stream_i4(const void* p) {
+    const wzy_v4i v = __builtin_nontemporal_load((const wzy_v4i*) p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+WZY_DEV uint4 ld_stream_u4(const void* p) {
+    const wzy_v4i v = __builtin_nontemporal_load((const wzy_v4i*) p);
+    return make_uint4((uint32_t) v.x, (uint32_t) v.y, (uint32_t) v.z, (uint32_t) v.w);
+}
+
+// ---------------------------------------------------------------------------------------------
+// int8 dot products (v_dot4_i32_i8)
+// ---------------------------------------------------------------------------------------------
+WZY_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+WZY_DEV int dot16(int4 a, int4 b) {
+    int s = dot4(a.x, b.x, 0);
+    s = dot4(a.y, b.y, s);
+    s = dot4(a.z, b.z, s);
+    return dot4(a.w, b.w, s);
+}
+
+// ---------------------------------------------------------------------------------------------
+// NVFP4 (e2m1 codes x e4m3 block scales)
+// ---------------------------------------------------------------------------------------------
+// e2m1 code -> 2*value as int8: {0,1,2,3,4,6,8,12, 0,-1,-2,-3,-4,-6,-8,-12}.
+// Eight packed nibbles (one uint32) expand to eight int8 lanes with v_perm_b32 table lookups:
+// the low 3 bits of each nibble select a magnitude byte from the 8-entry table, the sign bit
+// negates it.
+WZY_DEV uint32_t e2m1x4_mag(uint32_t sel4) {
+    // sel4: four 3-bit indices in the low 3 bits of each byte. perm selector byte k picks byte
+    // sel of {hi:lo} = {0x0C080604, 0x03020100}: 0..3 -> 0,1,2,3 ; 4..7 -> 4,6,8,12.
+    return __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel4);
+}
+// Expand the 4 nibbles sitting in the low nibble of each byte of `nib` (bits 0-3, 8-11, 16-19,
+// 24-27) into 4 signed int8 values (2*e2m1).
+WZY_DEV int e2m1x4(uint32_t nib) {
+    const uint32_t mag = e2m1x4_mag(nib & 0x07070707u);
+    // sign: bit 3 of each nibble, applied only to non-zero magnitudes so that negative zero (code 8)
+    // stays 0x00 and ~mag + 1 never carries across a byte boundary.
+    const uint32_t nz = (nib | (nib >> 1) | (nib >> 2)) & 0x01010101u;
+    const uint32_t sgn = (nib >> 3) & nz;
+    const uint32_t msk = sgn * 0xFFu;                  // 0xFF in negative bytes
+    return (int) ((mag ^ msk) + sgn);                  // two's complement per byte
+}
+// 8 code bytes of one 16-value sub-block (value k<8 = low nibble of byte k, value k>=8 = high
+// nibble of byte k-8) -> 16 int8 lanes in value order packed as int4 {v0..3, v4..7, v8..11, v12..15}.
+WZY_DEV int4 e2m1_sub16(uint32_t w0, uint32_t w1) {
+    int4 r;
+    r.x = e2m1x4(w0);
+    r.y = e2m1x4(w1);
+    r.z = e2m1x4(w0 >> 4);
+    r.w = e2m1x4(w1 >> 4);
+    return r;
+}
+
+// Unsigned e4m3 block scale (sign bit ignored), pre-multiplied by 0.5 to cancel the doubled e2m1
+// codes: e == 0 -> m * 2^-9, else (1 + m/8) * 2^(e-7); no NaN encoding is special-cased.
+WZY_DEV float ue4m3_half(uint32_t x) {
+    x &= 0x7Fu;
+    const uint32_t e = x >> 3, m = x & 7u;
+    // normal: build the fp32 directly: exponent (e-7-1)+127 (the -1 is the 0.5 factor), mantissa m<<20
+    const float nrm = __builtin_bit_cast(float, ((e + 119u) << 23) | (m << 20));
+    const float sub = (float) m * 0.0009765625f;       // m * 2^-9 * 0.5
+    return e ? nrm : sub;
+}
+
+}  // namespace wzy

@@ -1,0 +1,124 @@
+"""ctypes bindings of libwzy_amd.so, the MI355X decode-path library.
+
+The C ABI (include/wzy_kernels.h, include/wzy_synth.h, include/wzy_stage.h) takes plain pointers and
+sizes; these bindings pass integers (device pointers from any allocator, numpy buffer addresses)
+and raise WzyError on a negative status.  Loading fails loudly when the shared library has not been
+built: there is no CPU fallback behind this module.
+"""
+import ctypes as C
+import os
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libwzy_amd.so")
+
+WZY_MAX_W = 8
+
+
+class WzyError(RuntimeError):
+    pass
+
+
+P = C.c_void_p
+I32 = C.c_int
+I64 = C.c_int64
+U64 = C.c_uint64
+U32 = C.c_uint32
+F32 = C.c_float
+SZ = C.c_size_t
+
+
+class MoeWeights(C.Structure):
+    """struct wzy_moe_weights (include/wzy_kernels.h)"""
+    _fields_ = [
+        ("n_embd", I32), ("n_ff", I32), ("n_exp", I32), ("top_k", I32),
+        ("router", P), ("sgate", P), ("experts", P),
+        ("sh_gate_q", P), ("sh_gate_s", P),
+        ("sh_up_q", P), ("sh_up_s", P),
+        ("sh_down_q", P), ("sh_down_s", P),
+    ]
+
+
+# name -> (restype, argtypes, checked)
+_SIGS = {
+    "wzy_last_error": (C.c_char_p, [], False),
+    "wzy_version": (C.c_char_p, [], False),
+    # kernels
+    "wzy_quant_act": (I32, [P, P, P, P, P, I32, I32, P], True),
+    "wzy_gemv_q8": (I32, [P, P, P, P, P, I32, I32, I32, I32, P], True),
+    "wzy_gemv_bf16": (I32, [P, P, P, I32, I32, I32, I32, P], True),
+    "wzy_nvfp4_expert_bytes": (SZ, [I32, I32], False),
+    "wzy_nvfp4_blob_bytes": (SZ, [I32, I32], False),
+    "wzy_nvfp4_repack_host": (I32, [P, P, I32, I32], True),
+    "wzy_moe_workspace_bytes": (SZ, [I32, I32, I32, I32, I32], False),
+    "wzy_moe_block": (I32, [C.POINTER(MoeWeights), P, I32, P, P, P, P, SZ, P], True),
+    "wzy_moe_time_kernels": (I32, [C.POINTER(MoeWeights), I32, I32, P, SZ, I32, C.POINTER(F32),
+                                   C.POINTER(F32), P], True),
+    "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
+    "wzy_row_top16": (I32, [P, I32, I32, P, P, P, P], True),
+    # synth
+    "wzy_synth_hash": (U64, [U64, U64, U64], False),
+    "wzy_synth_stream": (U64, [U32, U32, U32], False),
+    "wzy_synth_normal": (None, [U64, U64, SZ, F32, F32, P], False),
+    "wzy_synth_uniform": (None, [U64, U64, SZ, F32, F32, P], False),
+    "wzy_synth_normal_bf16": (None, [U64, U64, SZ, F32, F32, P], False),
+    "wzy_synth_q8": (None, [U64, U64, I32, I32, F32, P, P], False),
+    "wzy_synth_expert_blob": (I32, [U64, I32, I32, I32, I32, P], True),
+    "wzy_synth_expert_planes": (I32, [U64, I32, I32, I32, I32, P], True),
+    "wzy_synth_experts_device": (I32, [U64, I32, I32, I32, I32, I32, P, P], True),
+    "wzy_synth_kv_host": (None, [U64, I32, I32, I64, I32, I32, P, P], False),
+    "wzy_synth_kv_device": (I32, [U64, I32, I32, I64, I32, I32, P, P, P], True),
+    "wzy_f32_to_f16": (C.c_uint16, [F32], False),
+    "wzy_f16_to_f32": (F32, [C.c_uint16], False),
+    "wzy_f32_to_bf16": (C.c_uint16, [F32], False),
+}
+
+
+class _Lib:
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise WzyError("libwzy_amd.so not built (%s); run __graft_entry__.build()" % path)
+        self.path = path
+        self.dll = C.CDLL(path)
+        for name, (res, args, checked) in _SIGS.items():
+            fn = getattr(self.dll, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, self._wrap(fn, name) if checked else fn)
+
+    def _wrap(self, fn, name):
+        def call(*a):
+            rc = fn(*a)
+            if rc != 0:
+                raise WzyError("%s failed (%d): %s" % (name, rc, self.dll.wzy_last_error().decode()))
+            return rc
+        call.__name__ = name
+        return call
+
+    def has(self, name):
+        return hasattr(self.dll, name)
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded library (process-wide singleton)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = _Lib()
+    return _LIB
+
+
+def ptr(x):
+    """Address of a numpy array / torch tensor / int / None as a ctypes-compatible int."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if hasattr(x, "ctypes"):
+        return x.ctypes.data
+    raise TypeError("cannot take the address of %r" % type(x))
