@@ -28,8 +28,10 @@ def orc():
 
 
 @pytest.fixture(scope="session")
-def cuda():
-    import torch
-    if not torch.cuda.is_available():
+def gpu(wz):
+    """Device 0 through libwzy_amd (GPU tests never import torch: one HIP runtime per process)."""
+    import wzy_amd
+    if wzy_amd.device_count() < 1:
         pytest.fail("GPU test collected but no GPU is visible")
-    return torch.device("cuda:0")
+    wz.wzy_dev_set(0)
+    return 0

@@ -12,52 +12,51 @@ from oracle_lib import ptr
 pytestmark = pytest.mark.gpu
 
 
-def dev(torch, a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+DA = wzy_amd.DeviceArray
+
+
+def dev(a):
+    return DA.from_numpy(a)
 
 
 def host(t):
-    return t.cpu().numpy()
+    return t.numpy()
 
 
-def stream_ptr(torch):
-    return torch.cuda.current_stream().cuda_stream
-
-
-def device_layer(torch, wz, m, planes=None):
+def device_layer(wz, m, planes=None):
     """Upload a MoeLayer; experts come from `planes` (host plane bytes) or the device generator."""
     rec = wz.wzy_nvfp4_expert_bytes(m.D, m.F)
     d = {}
-    d["router"] = dev(torch, m.router.view(np.int16))
-    d["sgate"] = dev(torch, m.sgate.view(np.int16))
+    d["router"] = dev(m.router.view(np.int16))
+    d["sgate"] = dev(m.sgate.view(np.int16))
     for k, (q, s) in m.sh.items():
-        d[k + "_q"] = dev(torch, q)
-        d[k + "_s"] = dev(torch, s.view(np.int16))
+        d[k + "_q"] = dev(q)
+        d[k + "_s"] = dev(s.view(np.int16))
     if planes is not None:
-        d["experts"] = dev(torch, planes)
+        d["experts"] = dev(planes)
     else:
-        d["experts"] = torch.empty(rec * m.E, dtype=torch.uint8, device="cuda")
-        wz.wzy_synth_experts_device(m.seed, m.layer, 0, m.E, m.D, m.F, d["experts"].data_ptr(), stream_ptr(torch))
+        d["experts"] = DA(rec * m.E, np.uint8)
+        wz.wzy_synth_experts_device(m.seed, m.layer, 0, m.E, m.D, m.F, d["experts"].ptr, None)
     w = wzy_amd.MoeWeights()
     w.n_embd, w.n_ff, w.n_exp, w.top_k = m.D, m.F, m.E, m.K
-    w.router, w.sgate, w.experts = d["router"].data_ptr(), d["sgate"].data_ptr(), d["experts"].data_ptr()
-    w.sh_gate_q, w.sh_gate_s = d["gate_q"].data_ptr(), d["gate_s"].data_ptr()
-    w.sh_up_q, w.sh_up_s = d["up_q"].data_ptr(), d["up_s"].data_ptr()
-    w.sh_down_q, w.sh_down_s = d["down_q"].data_ptr(), d["down_s"].data_ptr()
+    w.router, w.sgate, w.experts = d["router"].ptr, d["sgate"].ptr, d["experts"].ptr
+    w.sh_gate_q, w.sh_gate_s = d["gate_q"].ptr, d["gate_s"].ptr
+    w.sh_up_q, w.sh_up_s = d["up_q"].ptr, d["up_s"].ptr
+    w.sh_down_q, w.sh_down_s = d["down_q"].ptr, d["down_s"].ptr
     return w, d
 
 
-def run_gpu_moe(torch, wz, w, x, T):
+def run_gpu_moe(wz, w, x, T):
     D, K = w.n_embd, w.top_k
-    xd = dev(torch, x.reshape(T, D))
-    comb = torch.empty(T * D, dtype=torch.float32, device="cuda")
-    ids = torch.empty(T * K, dtype=torch.int32, device="cuda")
-    wts = torch.empty(T * K, dtype=torch.float32, device="cuda")
+    xd = dev(x.reshape(T, D))
+    comb = DA(T * D, np.float32)
+    ids = DA(T * K, np.int32)
+    wts = DA(T * K, np.float32)
     nws = wz.wzy_moe_workspace_bytes(D, w.n_ff, w.n_exp, K, T)
-    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
-    wz.wzy_moe_block(C.byref(w), xd.data_ptr(), T, comb.data_ptr(), ids.data_ptr(), wts.data_ptr(),
-                     ws.data_ptr(), nws, stream_ptr(torch))
-    torch.cuda.synchronize()
+    ws = DA(nws, np.uint8, zero=True)
+    wz.wzy_moe_block(C.byref(w), xd.ptr, T, comb.ptr, ids.ptr, wts.ptr,
+                     ws.ptr, nws, None)
+    wz.wzy_device_sync()
     return host(comb), host(ids), host(wts)
 
 
@@ -76,12 +75,11 @@ def check_ids(orc, logits, E, K, T, ids_gpu, ids_orc):
     return exact_rows
 
 
-def test_device_generator_matches_host(wz, cuda):
-    import torch
+def test_device_generator_matches_host(wz, gpu):
     D, F = 2048, 512
     rec = wz.wzy_nvfp4_expert_bytes(D, F)
-    buf = torch.empty(3 * rec, dtype=torch.uint8, device="cuda")
-    wz.wzy_synth_experts_device(0, 7, 100, 3, D, F, buf.data_ptr(), stream_ptr(torch))
+    buf = DA(3 * rec, np.uint8)
+    wz.wzy_synth_experts_device(0, 7, 100, 3, D, F, buf.ptr, None)
     got = host(buf)
     for i in range(3):
         ref = np.empty(rec, np.uint8)
@@ -93,9 +91,9 @@ def test_device_generator_matches_host(wz, cuda):
     wz.wzy_nvfp4_repack_host(blob.ctypes.data, rp.ctypes.data, D, F)
     np.testing.assert_array_equal(rp, got[rec:2 * rec])
     n, kvd = 1000, 512
-    kq = torch.empty(n * kvd, dtype=torch.int8, device="cuda")
-    ks = torch.empty(n * kvd // 64, dtype=torch.int16, device="cuda")
-    wz.wzy_synth_kv_device(2, 3, 1, 4090, n, kvd, kq.data_ptr(), ks.data_ptr(), stream_ptr(torch))
+    kq = DA(n * kvd, np.int8)
+    ks = DA(n * kvd // 64, np.int16)
+    wz.wzy_synth_kv_device(2, 3, 1, 4090, n, kvd, kq.ptr, ks.ptr, None)
     hq = np.empty(n * kvd, np.int8); hs = np.empty(n * kvd // 64, np.uint16)
     wz.wzy_synth_kv_host(2, 3, 1, 4090, n, kvd, hq.ctypes.data, hs.ctypes.data)
     np.testing.assert_array_equal(host(kq), hq)
@@ -104,15 +102,14 @@ def test_device_generator_matches_host(wz, cuda):
 
 
 @pytest.mark.parametrize("cols,T", [(2048, 1), (512, 8), (320, 3), (8192, 2)])
-def test_quant_act_bit_exact(wz, orc, cuda, cols, T):
-    import torch
+def test_quant_act_bit_exact(wz, orc, gpu, cols, T):
     x = np.random.default_rng(cols + T).standard_normal(T * cols).astype(np.float32)
     x[:32] = 0.0
-    xd = dev(torch, x)
-    q32 = torch.empty(T * cols, dtype=torch.int8, device="cuda"); s32 = torch.empty(T * cols // 32, device="cuda")
-    q16 = torch.empty(T * cols, dtype=torch.int8, device="cuda"); s16 = torch.empty(T * cols // 16, device="cuda")
-    wz.wzy_quant_act(xd.data_ptr(), q32.data_ptr(), s32.data_ptr(), q16.data_ptr(), s16.data_ptr(), cols, T,
-                     stream_ptr(torch))
+    xd = dev(x)
+    q32 = DA(T * cols, np.int8); s32 = DA(T * cols // 32, np.float32)
+    q16 = DA(T * cols, np.int8); s16 = DA(T * cols // 16, np.float32)
+    wz.wzy_quant_act(xd.ptr, q32.ptr, s32.ptr, q16.ptr, s16.ptr, cols, T,
+                     None)
     r32 = np.empty(T * cols, np.int8); rs32 = np.empty(T * cols // 32, np.float32)
     r16 = np.empty(T * cols, np.int8); rs16 = np.empty(T * cols // 16, np.float32)
     orc.orc_quant_act(ptr(x), cols, T, ptr(r32), ptr(rs32), ptr(r16), ptr(rs16))
@@ -123,8 +120,7 @@ def test_quant_act_bit_exact(wz, orc, cuda, cols, T):
 
 
 @pytest.mark.parametrize("rows,cols,T", [(6144, 2048, 1), (2048, 6144, 4), (8192, 320, 8), (2048, 512, 2), (100, 96, 5)])
-def test_gemv_q8_parity(wz, orc, cuda, rows, cols, T):
-    import torch
+def test_gemv_q8_parity(wz, orc, gpu, rows, cols, T):
     codes = np.empty(rows * cols, np.int8); sc = np.empty(rows * cols // 32, np.uint16)
     wz.wzy_synth_q8(3, 9, rows, cols, float(1 / np.sqrt(cols)), ptr(codes), ptr(sc))
     x = np.random.default_rng(rows).standard_normal(T * cols).astype(np.float32)
@@ -132,29 +128,27 @@ def test_gemv_q8_parity(wz, orc, cuda, rows, cols, T):
     orc.orc_quant_act(ptr(x), cols, T, ptr(q32), ptr(s32), None, None)
     ref = np.empty(T * rows, np.float32)
     orc.orc_gemv_q8(ptr(codes), ptr(sc), ptr(q32), ptr(s32), ptr(ref), rows, cols, T)
-    y = torch.empty(T * rows, device="cuda")
-    wz.wzy_gemv_q8(dev(torch, codes).data_ptr(), dev(torch, sc.view(np.int16)).data_ptr(), dev(torch, q32).data_ptr(),
-                   dev(torch, s32).data_ptr(), y.data_ptr(), rows, cols, T, 0, stream_ptr(torch))
+    y = DA(T * rows, np.float32)
+    bufs = [dev(codes), dev(sc.view(np.int16)), dev(q32), dev(s32)]     # keep alive during the call
+    wz.wzy_gemv_q8(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, y.ptr, rows, cols, T, 0, None)
     np.testing.assert_allclose(host(y), ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
 @pytest.mark.parametrize("rows,cols,T", [(512, 2048, 1), (151936, 2048, 1), (128, 2048, 8), (4, 8192, 3), (33, 264, 2)])
-def test_gemv_bf16_parity(wz, orc, cuda, rows, cols, T):
-    import torch
+def test_gemv_bf16_parity(wz, orc, gpu, rows, cols, T):
     W = np.empty(rows * cols, np.uint16)
     wz.wzy_synth_normal_bf16(4, 1, rows * cols, 0.0, 0.02, ptr(W))
     x = np.random.default_rng(cols).standard_normal(T * cols).astype(np.float32)
-    y = torch.empty(T * rows, device="cuda")
-    wz.wzy_gemv_bf16(dev(torch, W.view(np.int16)).data_ptr(), dev(torch, x).data_ptr(), y.data_ptr(), rows, cols, T, 0,
-                     stream_ptr(torch))
+    y = DA(T * rows, np.float32)
+    bufs = [dev(W.view(np.int16)), dev(x)]
+    wz.wzy_gemv_bf16(bufs[0].ptr, bufs[1].ptr, y.ptr, rows, cols, T, 0, None)
     ref = np.empty(T * rows, np.float32)
     orc.orc_gemv_bf16(ptr(W), ptr(x), ptr(ref), rows, cols, T)
     np.testing.assert_allclose(host(y), ref, rtol=1e-5, atol=2e-5 * np.abs(ref).max())
 
 
-def test_moe_config1_parity(wz, orc, cuda):
+def test_moe_config1_parity(wz, orc, gpu):
     """D=2048, 512 experts top-10, NFF=512, seed 0, one token."""
-    import torch
     D, F, E, K, T = 2048, 512, 512, 10, 1
     m = mi.make_layer(wz, 0, 0, D, F, E, K, blobs=[])
     x = mi.make_x(wz, 0, 0, T, D).ravel()
@@ -169,8 +163,8 @@ def test_moe_config1_parity(wz, orc, cuda):
     ow = mi.orc_weights(oracle_lib, m, arr)
     comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
     assert orc.orc_moe_block(C.byref(ow), ptr(x), T, ptr(comb_o), ptr(ids_o), ptr(wts_o), None, None) == 0
-    w, keep = device_layer(torch, wz, m)
-    comb, ids, wts = run_gpu_moe(torch, wz, w, x, T)
+    w, keep = device_layer(wz, m)
+    comb, ids, wts = run_gpu_moe(wz, w, x, T)
     assert check_ids(orc, logits, E, K, T, ids, ids_o) == T
     np.testing.assert_allclose(wts, wts_o, rtol=1e-4)
     np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
@@ -179,9 +173,8 @@ def test_moe_config1_parity(wz, orc, cuda):
 
 
 @pytest.mark.parametrize("T", [1, 2, 4, 8])
-def test_moe_multirow_parity(wz, orc, cuda, T):
+def test_moe_multirow_parity(wz, orc, gpu, T):
     """Window rows share experts (grouping path); experts uploaded from host-repacked blobs."""
-    import torch
     D, F, E, K = 512, 128, 16, 4
     m = mi.make_layer(wz, 21, 5, D, F, E, K)
     x = mi.make_x(wz, 21, 5, T, D).ravel()
@@ -194,8 +187,8 @@ def test_moe_multirow_parity(wz, orc, cuda, T):
     comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
     logits = np.empty(T * E, np.float32)
     assert orc.orc_moe_block(C.byref(ow), ptr(x), T, ptr(comb_o), ptr(ids_o), ptr(wts_o), ptr(logits), None) == 0
-    w, keep = device_layer(torch, wz, m, planes=planes)
-    comb, ids, wts = run_gpu_moe(torch, wz, w, x, T)
+    w, keep = device_layer(wz, m, planes=planes)
+    comb, ids, wts = run_gpu_moe(wz, w, x, T)
     exact = check_ids(orc, logits, E, K, T, ids, ids_o)
     assert exact >= T - 1
     if exact == T:
@@ -203,19 +196,18 @@ def test_moe_multirow_parity(wz, orc, cuda, T):
 
 
 @pytest.mark.parametrize("V,T", [(151936, 1), (151936, 4), (248320, 2), (3000, 8)])
-def test_row_argmax_top16_parity(wz, orc, cuda, V, T):
-    import torch
+def test_row_argmax_top16_parity(wz, orc, gpu, V, T):
     rng = np.random.default_rng(V + T)
     l = rng.standard_normal(T * V).astype(np.float32)
     l[V // 2] = l[V // 3] = 40.0                # top tie in row 0 -> lower id
     if T > 1:
         l[V + 5:V + 40] = 30.0                  # 35-way tie at the top of row 1
-    ld = dev(torch, l)
-    g = torch.empty(T, dtype=torch.int32, device="cuda")
-    a = torch.empty(T, dtype=torch.int32, device="cuda")
-    tv = torch.empty(T * 16, device="cuda"); ti = torch.empty(T * 16, dtype=torch.int32, device="cuda")
-    wz.wzy_row_argmax(ld.data_ptr(), V, T, a.data_ptr(), stream_ptr(torch))
-    wz.wzy_row_top16(ld.data_ptr(), V, T, g.data_ptr(), tv.data_ptr(), ti.data_ptr(), stream_ptr(torch))
+    ld = dev(l)
+    g = DA(T, np.int32)
+    a = DA(T, np.int32)
+    tv = DA(T * 16, np.float32); ti = DA(T * 16, np.int32)
+    wz.wzy_row_argmax(ld.ptr, V, T, a.ptr, None)
+    wz.wzy_row_top16(ld.ptr, V, T, g.ptr, tv.ptr, ti.ptr, None)
     ra = np.empty(T, np.int32); rg = np.empty(T, np.int32); rv = np.empty(T * 16, np.float32); ri = np.empty(T * 16, np.int32)
     orc.orc_row_argmax(ptr(l), V, T, ptr(ra))
     orc.orc_row_top16(ptr(l), V, T, ptr(rg), ptr(rv), ptr(ri))
@@ -224,5 +216,5 @@ def test_row_argmax_top16_parity(wz, orc, cuda, V, T):
     np.testing.assert_array_equal(host(ti), ri)
     np.testing.assert_array_equal(host(tv), rv)
     # second call reuses the arrival counters (they must be back at zero)
-    wz.wzy_row_argmax(ld.data_ptr(), V, T, a.data_ptr(), stream_ptr(torch))
+    wz.wzy_row_argmax(ld.ptr, V, T, a.ptr, None)
     np.testing.assert_array_equal(host(a), ra)

@@ -70,6 +70,23 @@ _SIGS = {
     "wzy_f32_to_f16": (C.c_uint16, [F32], False),
     "wzy_f16_to_f32": (F32, [C.c_uint16], False),
     "wzy_f32_to_bf16": (C.c_uint16, [F32], False),
+    # runtime plumbing
+    "wzy_dev_count": (I32, [C.POINTER(I32)], True),
+    "wzy_dev_set": (I32, [I32], True),
+    "wzy_dev_name": (I32, [I32, C.c_char_p, I32], True),
+    "wzy_mem_info": (I32, [C.POINTER(SZ), C.POINTER(SZ)], True),
+    "wzy_dev_malloc": (I32, [C.POINTER(P), SZ], True),
+    "wzy_dev_free": (I32, [P], True),
+    "wzy_memcpy_h2d": (I32, [P, P, SZ, P], True),
+    "wzy_memcpy_d2h": (I32, [P, P, SZ, P], True),
+    "wzy_memcpy_d2d": (I32, [P, P, SZ, P], True),
+    "wzy_memset": (I32, [P, I32, SZ, P], True),
+    "wzy_stream_create": (I32, [C.POINTER(P)], True),
+    "wzy_stream_destroy": (I32, [P], True),
+    "wzy_stream_sync": (I32, [P], True),
+    "wzy_device_sync": (I32, [], True),
+    "wzy_host_malloc": (I32, [C.POINTER(P), SZ], True),
+    "wzy_host_free": (I32, [P], True),
 }
 
 
@@ -112,13 +129,59 @@ def lib():
 
 
 def ptr(x):
-    """Address of a numpy array / torch tensor / int / None as a ctypes-compatible int."""
+    """Address of a numpy array / DeviceArray / int / None as a ctypes-compatible int."""
     if x is None:
         return None
     if isinstance(x, int):
         return x
-    if hasattr(x, "data_ptr"):
-        return x.data_ptr()
+    if isinstance(x, DeviceArray):
+        return x.ptr
     if hasattr(x, "ctypes"):
         return x.ctypes.data
     raise TypeError("cannot take the address of %r" % type(x))
+
+
+def device_count():
+    n = I32(0)
+    lib().wzy_dev_count(C.byref(n))
+    return n.value
+
+
+class DeviceArray:
+    """A device buffer owned through wzy_dev_malloc, with a numpy dtype and shape for convenience."""
+
+    def __init__(self, shape, dtype, zero=False):
+        import numpy as np
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if hasattr(shape, "__len__") else (int(shape),)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = P()
+        lib().wzy_dev_malloc(C.byref(p), max(self.nbytes, 1))
+        self.ptr = p.value
+        if zero:
+            lib().wzy_memset(self.ptr, 0, self.nbytes, None)
+
+    @classmethod
+    def from_numpy(cls, a):
+        import numpy as np
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        lib().wzy_memcpy_h2d(d.ptr, a.ctypes.data, d.nbytes, None)
+        return d
+
+    def numpy(self):
+        import numpy as np
+        out = np.empty(self.shape, self.dtype)
+        lib().wzy_memcpy_d2h(out.ctypes.data, self.ptr, self.nbytes, None)
+        return out
+
+    def free(self):
+        if getattr(self, "ptr", None):
+            lib().wzy_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
