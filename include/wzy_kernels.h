@@ -110,13 +110,98 @@ size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T
 int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Time the routed-expert GEMV kernels of wzy_moe_block over `iters` launches on `stream`, cycling
- * through `n_layers` weight sets (to defeat the 256 MB last-level cache), with hipEvents.  Returns
- * the mean duration per launch of the gate/up kernel and of the down kernel in microseconds
- * (host pointers).  The routing used is the one the last wzy_moe_block call on `workspace` produced. */
-int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, void* workspace,
+/* Time the expert kernels of wzy_moe_block with hipEvents on `stream`: `iters` iterations cycling
+ * through `n_layers` weight sets (so the 256 MB last-level cache cannot hold the experts), each
+ * iteration routing x [T x n_embd] through that layer's router first.  Returns the mean duration
+ * in microseconds of the gate/up launch and of the down+combine launch (host pointers).
+ * No counterpart in the reference: measurement support for the NVFP4 GEMV roofline. */
+int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, const float* x, void* workspace,
                          size_t workspace_bytes, int iters, float* us_gate_up, float* us_down,
                          void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Hyper-connection read
+ * ------------------------------------------------------------------------------------------- */
+
+/* One HC read of T rows (HC streams of D floats each, HCD = HC*D):
+ *   R_out = (R_in or bf16 embedding rows of toks broadcast to every stream) + bo * 2*sigmoid(inj_prev/HC)
+ *   xn[c] = R_out[c] * rsqrt(mean(R_out[c]^2) + eps) * norm_w[c]     -> nsc [T x HC] = the rsqrt
+ *   lo = silu((down . quant32(xn)) / HC)   [T x HCLR];  inj = inj_w . xn  [T x HC]  (inj_w nullable)
+ *   mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo))   [T x D]
+ * Exactly one of R_in / emb_table is non-NULL; bo/inj_prev (the pending HC write of the previous
+ * block) may be NULL.  R_out must not alias R_in.
+ * Replaces StageGpu::gr_read_fused + gr_write_multi (src/wzy_stage_v2.cuh:463-470;
+ * src/wzy_kernels_v2.cuh:409-454,632-827) and bcast_emb_to_r_kernel (src/wzy_stage_v2.cuh:326-332). */
+int wzy_hc_read(const float* R_in, const uint16_t* emb_table, const int* toks, int n_vocab, const float* bo,
+                const float* inj_prev, float* R_out, const float* norm_w, const int8_t* down_q,
+                const uint16_t* down_s, const uint16_t* inj_w, const int8_t* up_q, const uint16_t* up_s,
+                float* nsc, float* lo, float* inj, float* mixed, int D, int HC, int HCLR, float eps, int T,
+                void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * GDN (gated delta-rule) recurrence
+ * ------------------------------------------------------------------------------------------- */
+
+/* Fused decode step for T rows: 4-tap causal conv + SiLU over the raw q|k|v projection channels
+ * (history conv_hist [QKV x 3] updated), per-head L2 norm of q and k, decay = exp(softplus(alpha +
+ * dt) * ssm_a), beta = sigmoid(beta_raw) from ab_raw [T x 2*hv] (alpha | beta), then the delta-rule
+ * recurrence on state [hv][128][128] (S[h][key i][value j]), o * 1/sqrt(128), RMSNorm(gamma),
+ * * sigmoid(z) -> y [T x hv*128].  Optional per-step snapshots: state_snaps [T][hv][128][128],
+ * hist_snaps [T][QKV][3].  Head dim 128.
+ * Replaces fused_gdn_conv_l2_multi + fused_gdn_ab_multi + fused_gdn_step_norm_multi
+ * (src/wzy_kernels_v2.cuh:833-984). */
+int wzy_gdn_step(const float* qkv_raw, const float* z, const float* ab_raw, const float* dt, const float* ssm_a,
+                 const float* conv_w, float* conv_hist, float* state, const float* gamma, float eps, float* y,
+                 int hk, int hv, int T, float* state_snaps, float* hist_snaps, void* stream);
+
+/* Recurrence only, on already-activated q, k [T x hk*128], v [T x hv*128], decay/beta [T x hv]
+ * (z and gamma may be NULL: no gate / unit norm weight).
+ * Replaces fused_gdn_step_norm_multi (src/wzy_kernels_v2.cuh:908-984). */
+int wzy_gdn_recurrence(const float* q, const float* k, const float* v, const float* decay, const float* beta,
+                       const float* z, const float* gamma, float eps, float* state, float* y, int hk, int hv,
+                       int T, float* state_snaps, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * QSA sparse attention
+ * ------------------------------------------------------------------------------------------- */
+
+typedef struct wzy_qsa_dims {
+    int qh, kvh, hd, n_rot;                      /* 24, 2, 256, 64 */
+    int idx_heads, idx_dim, idx_blk, idx_topk;   /* 4, 128, 4, 2048 */
+    int ctx_max;                                 /* KV store / indexer capacity in cells */
+    int kv_ring, kv_sinks;                       /* 0, 0 = full-context store addressed by position;
+                                                    else ring of kv_ring slots with kv_sinks pinned */
+    float eps;
+} wzy_qsa_dims;
+
+/* Per-row preparation at positions pos[0] + t: RMSNorm + NeoX RoPE of the q heads (qg [T x qh*2*hd],
+ * q|gate per head, in place), of the k heads (kk [T x kvh*hd], in place) and of the indexer q heads
+ * (q_idx [T x idx_heads*idx_dim], in place); INT8 append of k and v (fp16 scale per 64 elements,
+ * scale rounded to fp16 first) into the KV store; indexer append of fp16(idx_raw) into idx_tail
+ * [idx_blk-1 x idx_dim], idx_dead [idx_dim] and the fp16 pooled keys idx_pooled
+ * [ctx_max/idx_blk + 2 x idx_dim].  cos_tab/sin_tab [ctx_max x n_rot/2].
+ * Replaces fused_head_norm_rope_multi, kv_append_int8_multi, qsa_indexer_append_multi
+ * (src/wzy_qsa_256k.cuh:50-209). */
+int wzy_qsa_prepare(const wzy_qsa_dims* dims, const int* pos, float* qg, float* kk, const float* vv, float* q_idx,
+                    const float* idx_raw, const float* q_norm, const float* k_norm, const float* iq_norm,
+                    const float* ik_norm, const float* cos_tab, const float* sin_tab, int8_t* kq, uint16_t* ks,
+                    int8_t* vq, uint16_t* vs, float* idx_tail, float* idx_dead, uint16_t* idx_pooled, int T,
+                    void* stream);
+
+/* Block scores (sum over indexer heads of relu(fp16 q . fp16 key)) and exact top-idx_topk cell
+ * selection per row: sel_ids [T x idx_topk] (first sel_cnt[t] valid), scores [T x max_b]
+ * (max_b >= ctx_max/idx_blk + 1).  Rows with n_kv <= idx_topk select 0..n_kv-1.
+ * Replaces pf_qsa_block_scores_wmma + pf_qsa_tail_score_kernel + qsa_block_topk_multi
+ * (src/wzy_qsa_wmma.cuh:492-612; src/wzy_qsa_256k.cuh:226-403). */
+int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const uint16_t* idx_pooled, const float* idx_dead,
+                   const float* q_idx, float* scores, int max_b, int* sel_ids, int* sel_cnt, int T, void* stream);
+
+/* GQA sparse attention over the selected cells: out [T x qh*hd] = softmax(q . k / 16) . v * sigmoid(gate).
+ * Replaces qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532). */
+size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T);
+int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const float* qg, const int8_t* kq, const uint16_t* ks,
+                   const int8_t* vq, const uint16_t* vs, const int* sel_ids, float* out, void* workspace,
+                   size_t workspace_bytes, int T, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Logit reductions

@@ -1,0 +1,108 @@
+/* wzy_stage.h -- C ABI of the layer executor ("stage") of the MI355X decode path.
+ *
+ * Replaces the reference's in-process StageGpu (src/wzy_stage_v2.cuh:334-1045; construction and
+ * weight loading in init_stage_weights_and_state / alloc_stage_expert_vram,
+ * src/wzy_engine_v2.cu:310-593).  Differences that follow from running on one MI355X:
+ *   - one stage owns all layers (no PP2 split, no peer handoff arguments);
+ *   - every NVFP4 expert of every layer is resident in HBM, so the cold-expert mailbox, the CPU
+ *     pool arguments and the expert cache disappear (service/promote are kept as no-op calls);
+ *   - the KV cache is a full-context INT8 store in HBM (no pinned host mirror);
+ *   - token embeddings are gathered on the GPU from token ids (host fp32 rows remain accepted).
+ * Errors are reported as negative status codes with wzy_last_error() (the reference exits the
+ * process); a host driver that wants the reference behaviour exits on any negative status.
+ * One stream and one host thread per handle; calls on a handle must be serialised.
+ *
+ * Synthetic model (BASELINE configurations): per-layer tensors and their initialisation are
+ * listed in DESIGN.md; wzy_stage_load_synthetic() fills weights and a prefilled decode state of
+ * n_ctx cells from a seed, deterministically (see wzy_synth.h).
+ */
+#ifndef WZY_STAGE_H
+#define WZY_STAGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct wzy_stage_cfg {
+    int n_layers;                              /* 48 */
+    int qsa_period;                            /* 4: layer l is QSA iff l % qsa_period == qsa_period-1
+                                                  (reference is_qsa_layer, src/wzy_engine_v2.cu:17) */
+    int n_embd;                                /* D = 2048 */
+    int hc, hc_lr;                             /* hyper-connection streams 4, low rank 320 */
+    int gdn_hk, gdn_hv;                        /* GDN key / value heads (head dim 128): 16, 16 */
+    int qsa_qh, qsa_kvh, qsa_hd, n_rot;        /* 24, 2, 256, 64 */
+    int idx_heads, idx_dim, idx_blk, idx_topk; /* 4, 128, 4, 2048 */
+    int n_exp, top_k, n_ff;                    /* 512, 10, 512 */
+    int n_vocab;                               /* 151936 */
+    int ctx_max;                               /* KV / indexer / RoPE capacity in cells */
+    int kv_ring, kv_sinks;                     /* 0, 0: full-context KV store */
+    float rope_theta, eps;                     /* 1e7, 1e-6 */
+} wzy_stage_cfg;
+
+typedef struct wzy_stage wzy_stage;
+
+/* The BASELINE synthetic model (config 4) with the given context capacity. */
+void wzy_stage_cfg_default(wzy_stage_cfg* cfg, int ctx_max);
+
+/* Allocate a stage on `device` (weights uninitialised until a load call). */
+int wzy_stage_create(const wzy_stage_cfg* cfg, int device, wzy_stage** out);
+int wzy_stage_destroy(wzy_stage* st);
+/* Device bytes held by the stage. */
+size_t wzy_stage_device_bytes(const wzy_stage* st);
+
+/* Random-initialise every weight from `seed` and synthesise a prefilled decode state of n_ctx
+ * cells (GDN conv/ssm state, INT8 KV cells 0..n_ctx-1, indexer keys).  0 <= n_ctx < ctx_max.
+ * (The reference loads a GGUF checkpoint here; a synthetic model is what the benchmarks use.) */
+int wzy_stage_load_synthetic(wzy_stage* st, uint64_t seed, int n_ctx);
+
+/* Enqueue the forward of T window rows at positions pos .. pos+T-1 (1 <= T <= 8):
+ *   toks [T] token ids (embedding gathered on the GPU), or emb [T x n_embd] fp32 rows (host
+ *   memory) when non-NULL; run_head: compute logits + greedy ids (+ top-16 when want_top16);
+ *   save_snaps: write per-row snapshots (at snap_offset + t) of GDN / indexer state for
+ *   commit_window_state.  Asynchronous: results are valid after wzy_stage_sync().
+ * Replaces StageGpu::record_forward (src/wzy_stage_v2.cuh:476-857). */
+int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb, const int* toks, int T, int run_head,
+                             int save_snaps, int want_top16, int snap_offset);
+/* Cold-expert servicing and VRAM promotion: nothing is cold on one MI355X (no-ops, kept so a
+ * reference driver links unchanged).  Replace StageGpu::service_cold_layers / promote_cold
+ * (src/wzy_stage_v2.cuh:932,960). */
+int wzy_stage_service_cold_layers(wzy_stage* st);
+int wzy_stage_promote_cold(wzy_stage* st);
+/* Keep the state after window row acc_idx (accepted prefix acc_idx+1 rows ending at position
+ * acc_pos): restores GDN conv/ssm snapshots and the indexer tail/placeholder/pooled keys.
+ * Replaces StageGpu::commit_window_state (src/wzy_stage_v2.cuh:939-958). */
+int wzy_stage_commit_window_state(wzy_stage* st, int acc_idx, int acc_pos);
+/* Zero the recurrent state (GDN conv/ssm, indexer tail/placeholder).
+ * Replaces StageGpu::reset_state (src/wzy_stage_v2.cuh:1031-1044). */
+int wzy_stage_reset_state(wzy_stage* st);
+int wzy_stage_sync(wzy_stage* st);
+
+/* Results of the last forward with run_head (after sync); host outputs. */
+int wzy_stage_greedy_ids(wzy_stage* st, int* out, int T);
+int wzy_stage_top16(wzy_stage* st, float* v, int* ids, int T);
+int wzy_stage_logits(wzy_stage* st, float* out, int T);          /* [T x n_vocab] */
+int wzy_stage_pre_head(wzy_stage* st, float* out, int T);        /* [T x hc x n_embd] residual before the head */
+
+/* Use hipGraphs for record_forward (default on): one graph per window shape, replayed. */
+int wzy_stage_set_graphs(wzy_stage* st, int enable);
+/* The stage's HIP stream (hipStream_t). */
+void* wzy_stage_stream(wzy_stage* st);
+
+/* Tensor access for checks and loaders: `name` as in the DESIGN.md tensor table, layer -1 for
+ * model-level tensors.  Byte size, device-to-host and host-to-device copies (synchronous). */
+size_t wzy_stage_tensor_bytes(wzy_stage* st, int layer, const char* name);
+int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name, void* host, size_t bytes);
+int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes);
+
+/* Measurement support (no reference counterpart): time the NVFP4 expert kernels of every layer's
+ * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the
+ * last forward's rows) -> mean microseconds of the gate/up launch and of the down launch. */
+int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WZY_STAGE_H */

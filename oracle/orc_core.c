@@ -111,6 +111,7 @@ void orc_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq, 
     for (int t = 0; t < T; ++t) {
         const int8_t* xt = xq + (size_t) t * cols;
         const float* st = xs + (size_t) t * nb;
+#pragma omp parallel for schedule(static) if (rows >= 256)
         for (int r = 0; r < rows; ++r) {
             const int8_t* c = codes + (size_t) r * cols;
             double acc = 0.0;
@@ -128,6 +129,7 @@ void orc_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq, 
 /* gemm_bf16_t (src/wzy_kernels_v2.cuh:307-337) */
 void orc_gemv_bf16(const uint16_t* W, const float* x, float* y, int rows, int cols, int T) {
     for (int t = 0; t < T; ++t)
+#pragma omp parallel for schedule(static) if (rows >= 256)
         for (int r = 0; r < rows; ++r) {
             const uint16_t* w = W + (size_t) r * cols;
             const float* xt = x + (size_t) t * cols;
@@ -223,8 +225,8 @@ void orc_expert_down(const uint8_t* blob, int D, int F, const int8_t* aq16, cons
  * silu_mul_quant32 (src/wzy_kernels_v2.cuh:1247-1280) -> routed experts -> combine
  * (src/wzy_kernels_v2.cuh:1281-1294): comb = shared*sigmoid(sg) + sum_{k, w!=0} w_k*part_k.
  * ---------------------------------------------------------------------------------------------- */
-int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
-                  float* logits_out, float* sg_out) {
+int orc_moe_block_fn(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
+                     float* logits_out, float* sg_out, orc_blob_fn blob_fn, void* blob_ctx, int layer) {
     const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k;
     int8_t* q32 = (int8_t*) malloc((size_t) T * D);
     float* s32 = (float*) malloc(sizeof(float) * (size_t) T * D / 32);
@@ -256,7 +258,9 @@ int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, 
 
     for (int t = 0; t < T && rc == 0; ++t)
         for (int k = 0; k < K; ++k) {
-            const uint8_t* blob = w->blobs[ids[t * K + k]];
+            const int e = ids[t * K + k];
+            const uint8_t* blob = w->blobs ? w->blobs[e] : NULL;
+            if (!blob && blob_fn) blob = blob_fn(blob_ctx, layer, e);
             if (!blob) { rc = -1; break; }
             orc_expert_gate_up(blob, D, F, q16 + (size_t) t * D, s16 + (size_t) t * (D / 16), aq, as, NULL);
             orc_expert_down(blob, D, F, aq, as, part + (size_t) (t * K + k) * D);
@@ -278,6 +282,11 @@ int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, 
     free(q32); free(s32); free(q16); free(s16); free(logits); free(sg); free(sff); free(sup); free(sact);
     free(sq); free(ss); free(shared); free(aq); free(as); free(part);
     return rc;
+}
+
+int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
+                  float* logits_out, float* sg_out) {
+    return orc_moe_block_fn(w, x, T, comb, ids, wts, logits_out, sg_out, NULL, NULL, 0);
 }
 
 /* ------------------------------------------------------------------------------------------------

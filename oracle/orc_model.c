@@ -1,0 +1,141 @@
+/* orc_model.c -- CPU oracle of one decode window through the whole model (StageGpu::record_forward,
+ * src/wzy_stage_v2.cuh:476-857, with every expert resident and the head run).  TEST
+ * INFRASTRUCTURE ONLY (see wzy_oracle.h). */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "wzy_oracle.h"
+
+static void q8_gemv_f(const int8_t* q, const uint16_t* s, const float* x, float* y, int rows, int cols, int T) {
+    int8_t* xq = (int8_t*) malloc((size_t) T * cols);
+    float* xs = (float*) malloc(sizeof(float) * (size_t) T * cols / 32);
+    orc_quant_act(x, cols, T, xq, xs, NULL, NULL);
+    orc_gemv_q8(q, s, xq, xs, y, rows, cols, T);
+    free(xq);
+    free(xs);
+}
+
+int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                      float* pre_head) {
+    const int D = m->n_embd, HC = m->hc, HCD = HC * D, L = m->hc_lr;
+    const int QKV = 2 * m->gdn_hk * 128 + m->gdn_hv * 128, GV = m->gdn_hv * 128;
+    const int QD = m->qsa_qh * m->qsa_hd, KVD = m->qsa_kvh * m->qsa_hd, hd = m->qsa_hd;
+    const int ID = m->idx_dim, IH = m->idx_heads;
+    if (T < 1 || T > 8 || pos < 0 || pos + T > m->ctx_max) return -1;
+
+    float* R[2];
+    R[0] = (float*) malloc(sizeof(float) * (size_t) T * HCD);
+    R[1] = (float*) malloc(sizeof(float) * (size_t) T * HCD);
+    float* nsc = (float*) malloc(sizeof(float) * (size_t) T * HC);
+    float* lo = (float*) malloc(sizeof(float) * (size_t) T * L);
+    float* inj_a = (float*) malloc(sizeof(float) * (size_t) T * HC);
+    float* inj_f = (float*) malloc(sizeof(float) * (size_t) T * HC);
+    float* mixed = (float*) malloc(sizeof(float) * (size_t) T * D);
+    float* block = (float*) malloc(sizeof(float) * (size_t) T * D);
+    float* comb = (float*) malloc(sizeof(float) * (size_t) T * D);
+    float* emb = (float*) malloc(sizeof(float) * (size_t) T * D);
+    float* qkv = (float*) malloc(sizeof(float) * (size_t) T * QKV);
+    float* z = (float*) malloc(sizeof(float) * (size_t) T * GV);
+    float* ab = (float*) malloc(sizeof(float) * (size_t) T * 2 * m->gdn_hv);
+    float* tmp = (float*) malloc(sizeof(float) * (size_t) T * (m->gdn_hv > 0 ? m->gdn_hv : 1));
+    float* y = (float*) malloc(sizeof(float) * (size_t) T * GV);
+    float* qg = (float*) malloc(sizeof(float) * (size_t) T * 2 * QD);
+    float* kk = (float*) malloc(sizeof(float) * (size_t) T * KVD);
+    float* vv = (float*) malloc(sizeof(float) * (size_t) T * KVD);
+    float* idx_raw = (float*) malloc(sizeof(float) * (size_t) T * ID);
+    float* q_idx = (float*) malloc(sizeof(float) * (size_t) T * IH * ID);
+    float* att = (float*) malloc(sizeof(float) * (size_t) T * QD);
+    float* scores = (float*) malloc(sizeof(float) * (size_t) (m->ctx_max / m->idx_blk + 2));
+    int* sel = (int*) malloc(sizeof(int) * (size_t) m->idx_topk);
+    int8_t* kq = (int8_t*) malloc((size_t) KVD);
+    uint16_t* ks = (uint16_t*) malloc(sizeof(uint16_t) * (size_t) KVD / 64);
+    int rc = 0, cur = 0;
+    const float* pend_bo = NULL;
+    const float* pend_inj = NULL;
+
+    for (int t = 0; t < T; ++t) {
+        int tok = toks[t];
+        tok = tok < 0 ? 0 : (tok >= m->n_vocab ? m->n_vocab - 1 : tok);
+        for (int d = 0; d < D; ++d) emb[(size_t) t * D + d] = orc_bf16_to_f32(m->emb[(size_t) tok * D + d]);
+    }
+
+    for (int l = 0; l < m->n_layers && rc == 0; ++l) {
+        const orc_layer* w = &m->layers[l];
+        /* attention half */
+        orc_hc_read(l == 0 ? NULL : R[cur], l == 0 ? emb : NULL, pend_bo, pend_inj, w->hc_norm[0], w->hc_down_q[0],
+                    w->hc_down_s[0], w->hc_inj[0], w->hc_up_q[0], w->hc_up_s[0], D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo,
+                    inj_a, mixed);
+        cur ^= 1;
+        if (!w->qsa) {
+            const int hv = m->gdn_hv;
+            q8_gemv_f(w->qkv_q, w->qkv_s, mixed, qkv, QKV, D, T);
+            q8_gemv_f(w->wgate_q, w->wgate_s, mixed, z, GV, D, T);
+            orc_gemv_bf16(w->alpha, mixed, tmp, hv, D, T);
+            for (int t = 0; t < T; ++t) memcpy(ab + (size_t) t * 2 * hv, tmp + (size_t) t * hv, sizeof(float) * hv);
+            orc_gemv_bf16(w->beta, mixed, tmp, hv, D, T);
+            for (int t = 0; t < T; ++t) memcpy(ab + (size_t) t * 2 * hv + hv, tmp + (size_t) t * hv, sizeof(float) * hv);
+            orc_gdn_step(qkv, z, ab, w->dt, w->ssm_a, w->conv_w, w->conv_hist, w->ssm, w->ssm_norm, m->eps, y, m->gdn_hk,
+                         hv, T);
+            q8_gemv_f(w->wout_q, w->wout_s, y, block, D, GV, T);
+        } else {
+            q8_gemv_f(w->wq_q, w->wq_s, mixed, qg, 2 * QD, D, T);
+            q8_gemv_f(w->wk_q, w->wk_s, mixed, kk, KVD, D, T);
+            q8_gemv_f(w->wv_q, w->wv_s, mixed, vv, KVD, D, T);
+            orc_gemv_bf16(w->idx_k, mixed, idx_raw, ID, D, T);
+            orc_gemv_bf16(w->idx_q, mixed, q_idx, IH * ID, D, T);
+            for (int t = 0; t < T; ++t) {
+                const int p = pos + t;
+                for (int h = 0; h < m->qsa_qh; ++h)
+                    orc_head_norm_rope(qg + (size_t) t * 2 * QD + (size_t) h * 2 * hd, hd, w->q_norm, m->cos_tab,
+                                       m->sin_tab, p, m->n_rot, m->eps);
+                for (int j = 0; j < m->qsa_kvh; ++j)
+                    orc_head_norm_rope(kk + (size_t) t * KVD + (size_t) j * hd, hd, w->k_norm, m->cos_tab, m->sin_tab, p,
+                                       m->n_rot, m->eps);
+                for (int i = 0; i < IH; ++i)
+                    orc_head_norm_rope(q_idx + (size_t) t * IH * ID + (size_t) i * ID, ID, w->idx_qn, m->cos_tab,
+                                       m->sin_tab, p, m->n_rot, m->eps);
+                orc_kv_quant_row(kk + (size_t) t * KVD, KVD, w->kq + (size_t) p * KVD, w->ks + (size_t) p * (KVD / 64));
+                orc_kv_quant_row(vv + (size_t) t * KVD, KVD, w->vq + (size_t) p * KVD, w->vs + (size_t) p * (KVD / 64));
+                orc_indexer_append(idx_raw + (size_t) t * ID, w->idx_kn, m->cos_tab, m->sin_tab, p, ID, m->idx_blk,
+                                   m->n_rot, m->eps, w->idx_tail, w->idx_dead, w->idx_pooled);
+            }
+            for (int t = 0; t < T; ++t) {
+                const int n_kv = pos + t + 1;
+                if (n_kv > m->idx_topk)
+                    orc_block_scores(w->idx_pooled, w->idx_dead, q_idx + (size_t) t * IH * ID, n_kv, IH, ID, m->idx_blk,
+                                     scores);
+                const int n = orc_topk_select(scores, n_kv, m->idx_blk, m->idx_topk, sel);
+                orc_attend(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh, hd,
+                           att + (size_t) t * QD);
+            }
+            q8_gemv_f(w->wo_q, w->wo_s, att, block, D, QD, T);
+        }
+        /* FFN half */
+        orc_hc_read(R[cur], NULL, block, inj_a, w->hc_norm[1], w->hc_down_q[1], w->hc_down_s[1], w->hc_inj[1],
+                    w->hc_up_q[1], w->hc_up_s[1], D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo, inj_f, mixed);
+        cur ^= 1;
+        orc_moe_weights mw;
+        mw.n_embd = D; mw.n_ff = m->n_ff; mw.n_exp = m->n_exp; mw.top_k = m->top_k;
+        mw.router = w->router; mw.sgate = w->sgate; mw.blobs = NULL;
+        mw.sh_gate_q = w->sh_gate_q; mw.sh_gate_s = w->sh_gate_s; mw.sh_up_q = w->sh_up_q; mw.sh_up_s = w->sh_up_s;
+        mw.sh_down_q = w->sh_down_q; mw.sh_down_s = w->sh_down_s;
+        int ids[8 * 64];
+        float wts[8 * 64];
+        rc = orc_moe_block_fn(&mw, mixed, T, comb, ids, wts, NULL, NULL, m->blob, m->blob_ctx, l);
+        pend_bo = comb;
+        pend_inj = inj_f;
+    }
+    if (rc == 0) {
+        orc_hc_read(R[cur], NULL, pend_bo, pend_inj, m->head_norm, m->head_down_q, m->head_down_s, NULL, m->head_up_q,
+                    m->head_up_s, D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo, NULL, mixed);
+        cur ^= 1;
+        if (pre_head) memcpy(pre_head, R[cur], sizeof(float) * (size_t) T * HCD);
+        orc_gemv_bf16(m->head, mixed, logits, m->n_vocab, D, T);
+        if (greedy) orc_row_argmax(logits, m->n_vocab, T, greedy);
+    }
+    free(R[0]); free(R[1]); free(nsc); free(lo); free(inj_a); free(inj_f); free(mixed); free(block); free(comb);
+    free(emb); free(qkv); free(z); free(ab); free(tmp); free(y); free(qg); free(kk); free(vv); free(idx_raw);
+    free(q_idx); free(att); free(scores); free(sel); free(kq); free(ks);
+    return rc;
+}

@@ -69,6 +69,79 @@ typedef struct orc_moe_weights {
  * logits_out [T x E], sg_out [T] optional. */
 int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   float* logits_out, float* sg_out);
+/* Same, fetching blobs that w->blobs does not hold (or all, when w->blobs is NULL) from blob_fn. */
+typedef const uint8_t* (*orc_blob_fn)(void* ctx, int layer, int expert);
+int orc_moe_block_fn(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
+                     float* logits_out, float* sg_out, orc_blob_fn blob_fn, void* blob_ctx, int layer);
+
+/* ---- hyper-connection read (src/wzy_kernels_v2.cuh:409-454,632-827): see orc_layers.c ---- */
+void orc_hc_read(const float* R_in, const float* emb_rows, const float* bo, const float* inj_prev, const float* norm_w,
+                 const int8_t* down_q, const uint16_t* down_s, const uint16_t* inj_w, const int8_t* up_q,
+                 const uint16_t* up_s, int D, int HC, int HCLR, float eps, int T, float* R_out, float* nsc, float* lo,
+                 float* inj, float* mixed);
+
+/* ---- GDN (src/wzy_kernels_v2.cuh:833-984); state S[h][i][j] ---- */
+void orc_gdn_step(const float* qkv_raw, const float* z, const float* ab_raw, const float* dt, const float* ssm_a,
+                  const float* conv_w, float* conv_hist, float* state, const float* gamma, float eps, float* y, int hk,
+                  int hv, int T);
+void orc_gdn_recurrence(const float* q, const float* k, const float* v, const float* decay, const float* beta,
+                        const float* z, const float* gamma, float eps, float* state, float* y, int hk, int hv, int T);
+
+/* ---- QSA (src/wzy_qsa_256k.cuh, src/wzy_qsa_wmma.cuh) ---- */
+void orc_rope_tables(int ctx, int n_rot, float theta, float* cos_tab, float* sin_tab);
+void orc_head_norm_rope(float* p, int hd, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
+                        int n_rot, float eps);
+void orc_kv_quant_row(const float* x, int n, int8_t* q, uint16_t* s);
+void orc_indexer_append(const float* raw, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
+                        int dim, int blk, int n_rot, float eps, float* tail, float* dead, uint16_t* pooled);
+void orc_block_scores(const uint16_t* pooled, const float* dead, const float* q_idx, int n_kv, int heads, int dim,
+                      int blk, float* scores);
+int orc_topk_select(const float* scores, int n_kv, int blk, int topk, int* sel);
+void orc_attend(const float* qg, const int8_t* kq, const uint16_t* ks, const int8_t* vq, const uint16_t* vs,
+                const int* sel, int n, int qh, int kvh, int hd, float* out);
+
+/* ---- whole decode window (StageGpu::record_forward with the head, src/wzy_stage_v2.cuh:476-857) ---- */
+typedef struct orc_layer {
+    int qsa;
+    const float* hc_norm[2];
+    const int8_t* hc_down_q[2]; const uint16_t* hc_down_s[2];
+    const int8_t* hc_up_q[2];   const uint16_t* hc_up_s[2];
+    const uint16_t* hc_inj[2];
+    /* GDN */
+    const int8_t* qkv_q;   const uint16_t* qkv_s;
+    const int8_t* wgate_q; const uint16_t* wgate_s;
+    const int8_t* wout_q;  const uint16_t* wout_s;
+    const uint16_t* alpha; const uint16_t* beta;
+    const float* ssm_a; const float* dt; const float* conv_w; const float* ssm_norm;
+    float* conv_hist; float* ssm;                       /* state, updated */
+    /* QSA */
+    const int8_t* wq_q; const uint16_t* wq_s; const int8_t* wk_q; const uint16_t* wk_s;
+    const int8_t* wv_q; const uint16_t* wv_s; const int8_t* wo_q; const uint16_t* wo_s;
+    const float* q_norm; const float* k_norm;
+    const uint16_t* idx_q; const uint16_t* idx_k; const float* idx_qn; const float* idx_kn;
+    int8_t* kq; uint16_t* ks; int8_t* vq; uint16_t* vs;  /* KV store [ctx_max x kvd], updated */
+    float* idx_tail; float* idx_dead; uint16_t* idx_pooled;  /* indexer state, updated */
+    /* MoE (expert blobs come from the model's blob_fn) */
+    const uint16_t* router; const uint16_t* sgate;
+    const int8_t* sh_gate_q; const uint16_t* sh_gate_s; const int8_t* sh_up_q; const uint16_t* sh_up_s;
+    const int8_t* sh_down_q; const uint16_t* sh_down_s;
+} orc_layer;
+
+typedef struct orc_model {
+    int n_layers, n_embd, hc, hc_lr, gdn_hk, gdn_hv, qsa_qh, qsa_kvh, qsa_hd, n_rot;
+    int idx_heads, idx_dim, idx_blk, idx_topk, n_exp, top_k, n_ff, n_vocab, ctx_max;
+    float eps;
+    orc_layer* layers;
+    const uint16_t* emb; const float* head_norm;
+    const int8_t* head_down_q; const uint16_t* head_down_s; const int8_t* head_up_q; const uint16_t* head_up_s;
+    const uint16_t* head;
+    const float* cos_tab; const float* sin_tab;
+    orc_blob_fn blob; void* blob_ctx;
+} orc_model;
+
+/* logits [T x n_vocab], greedy [T] and pre_head [T x hc x n_embd] (optional); returns 0 or -1. */
+int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                      float* pre_head);
 
 /* ---- logit reductions (src/wzy_kernels_v2.cuh:1873-1984) ---- */
 void orc_row_argmax(const float* logits, int nvocab, int T, int* out);

@@ -1,0 +1,153 @@
+"""Builds the CPU oracle's model (orc_model) from a loaded wzy_stage, for parity tests.
+
+Dense weights and the prefilled state are copied out of the stage (wzy_stage_read_tensor); the NVFP4
+experts are regenerated in the reference blob layout by the synthetic generator, on demand, for the
+experts the oracle routes to.  Test infrastructure only.
+"""
+import ctypes as C
+
+import numpy as np
+
+import oracle_lib
+
+P, I32, F32 = C.c_void_p, C.c_int, C.c_float
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("qsa", I32),
+                ("hc_norm", P * 2), ("hc_down_q", P * 2), ("hc_down_s", P * 2), ("hc_up_q", P * 2), ("hc_up_s", P * 2),
+                ("hc_inj", P * 2),
+                ("qkv_q", P), ("qkv_s", P), ("wgate_q", P), ("wgate_s", P), ("wout_q", P), ("wout_s", P),
+                ("alpha", P), ("beta", P), ("ssm_a", P), ("dt", P), ("conv_w", P), ("ssm_norm", P),
+                ("conv_hist", P), ("ssm", P),
+                ("wq_q", P), ("wq_s", P), ("wk_q", P), ("wk_s", P), ("wv_q", P), ("wv_s", P), ("wo_q", P), ("wo_s", P),
+                ("q_norm", P), ("k_norm", P), ("idx_q", P), ("idx_k", P), ("idx_qn", P), ("idx_kn", P),
+                ("kq", P), ("ks", P), ("vq", P), ("vs", P), ("idx_tail", P), ("idx_dead", P), ("idx_pooled", P),
+                ("router", P), ("sgate", P), ("sh_gate_q", P), ("sh_gate_s", P), ("sh_up_q", P), ("sh_up_s", P),
+                ("sh_down_q", P), ("sh_down_s", P)]
+
+
+BLOB_FN = C.CFUNCTYPE(P, P, I32, I32)
+
+
+class OrcModel(C.Structure):
+    _fields_ = [("n_layers", I32), ("n_embd", I32), ("hc", I32), ("hc_lr", I32), ("gdn_hk", I32), ("gdn_hv", I32),
+                ("qsa_qh", I32), ("qsa_kvh", I32), ("qsa_hd", I32), ("n_rot", I32),
+                ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32), ("n_exp", I32),
+                ("top_k", I32), ("n_ff", I32), ("n_vocab", I32), ("ctx_max", I32), ("eps", F32),
+                ("layers", C.POINTER(OrcLayer)),
+                ("emb", P), ("head_norm", P), ("head_down_q", P), ("head_down_s", P), ("head_up_q", P),
+                ("head_up_s", P), ("head", P), ("cos_tab", P), ("sin_tab", P),
+                ("blob", BLOB_FN), ("blob_ctx", P)]
+
+
+def is_qsa(cfg, l):
+    return (l % cfg.qsa_period) == cfg.qsa_period - 1
+
+
+class OracleModel:
+    """Holds the host copies and the orc_model struct; `forward` runs orc_model_forward."""
+
+    def __init__(self, wz, stage, cfg, seed):
+        self.wz, self.cfg, self.seed = wz, cfg, seed
+        self.keep = []
+        self.blobs = {}
+        st = stage
+
+        def rd(layer, name, dt):
+            a = st.read(layer, name, dt)
+            self.keep.append(a)
+            return a.ctypes.data
+
+        L = (OrcLayer * cfg.n_layers)()
+        for l in range(cfg.n_layers):
+            w = L[l]
+            w.qsa = 1 if is_qsa(cfg, l) else 0
+            for h in range(2):
+                w.hc_norm[h] = rd(l, "hc_norm%d" % h, np.float32)
+                w.hc_down_q[h] = rd(l, "hc_down%d.q" % h, np.int8)
+                w.hc_down_s[h] = rd(l, "hc_down%d.s" % h, np.uint16)
+                w.hc_up_q[h] = rd(l, "hc_up%d.q" % h, np.int8)
+                w.hc_up_s[h] = rd(l, "hc_up%d.s" % h, np.uint16)
+                w.hc_inj[h] = rd(l, "hc_inj%d" % h, np.uint16)
+            if not w.qsa:
+                for n in ("qkv", "wgate", "wout"):
+                    setattr(w, n + "_q", rd(l, n + ".q", np.int8))
+                    setattr(w, n + "_s", rd(l, n + ".s", np.uint16))
+                w.alpha, w.beta = rd(l, "alpha", np.uint16), rd(l, "beta", np.uint16)
+                w.ssm_a, w.dt = rd(l, "ssm_a", np.float32), rd(l, "dt_bias", np.float32)
+                w.conv_w, w.ssm_norm = rd(l, "conv1d", np.float32), rd(l, "ssm_norm", np.float32)
+                w.conv_hist, w.ssm = rd(l, "conv_hist", np.float32), rd(l, "ssm", np.float32)
+            else:
+                for n in ("wq", "wk", "wv", "wo"):
+                    setattr(w, n + "_q", rd(l, n + ".q", np.int8))
+                    setattr(w, n + "_s", rd(l, n + ".s", np.uint16))
+                w.q_norm, w.k_norm = rd(l, "q_norm", np.float32), rd(l, "k_norm", np.float32)
+                w.idx_q, w.idx_k = rd(l, "idx_q", np.uint16), rd(l, "idx_k", np.uint16)
+                w.idx_qn, w.idx_kn = rd(l, "idx_qn", np.float32), rd(l, "idx_kn", np.float32)
+                w.kq, w.ks = rd(l, "kv_k", np.int8), rd(l, "kv_ks", np.uint16)
+                w.vq, w.vs = rd(l, "kv_v", np.int8), rd(l, "kv_vs", np.uint16)
+                w.idx_tail, w.idx_dead = rd(l, "idx_tail", np.float32), rd(l, "idx_dead", np.float32)
+                w.idx_pooled = rd(l, "idx_pooled", np.uint16)
+            w.router, w.sgate = rd(l, "router", np.uint16), rd(l, "sgate", np.uint16)
+            for n in ("sh_gate", "sh_up", "sh_down"):
+                setattr(w, n + "_q", rd(l, n + ".q", np.int8))
+                setattr(w, n + "_s", rd(l, n + ".s", np.uint16))
+        self.layers = L
+        m = OrcModel()
+        for f in ("n_layers", "n_embd", "hc", "hc_lr", "gdn_hk", "gdn_hv", "qsa_qh", "qsa_kvh", "qsa_hd", "n_rot",
+                  "idx_heads", "idx_dim", "idx_blk", "idx_topk", "n_exp", "top_k", "n_ff", "n_vocab", "ctx_max", "eps"):
+            setattr(m, f, getattr(cfg, f))
+        m.layers = C.cast(L, C.POINTER(OrcLayer))
+        m.emb, m.head_norm = rd(-1, "emb", np.uint16), rd(-1, "head_norm", np.float32)
+        m.head_down_q, m.head_down_s = rd(-1, "head_down.q", np.int8), rd(-1, "head_down.s", np.uint16)
+        m.head_up_q, m.head_up_s = rd(-1, "head_up.q", np.int8), rd(-1, "head_up.s", np.uint16)
+        m.head = rd(-1, "head", np.uint16)
+        m.cos_tab, m.sin_tab = rd(-1, "rope_cos", np.float32), rd(-1, "rope_sin", np.float32)
+
+        def blob_fn(ctx, layer, e):
+            key = (layer, e)
+            b = self.blobs.get(key)
+            if b is None:
+                b = np.empty(wz.wzy_nvfp4_blob_bytes(cfg.n_embd, cfg.n_ff), np.uint8)
+                wz.wzy_synth_expert_blob(self.seed, layer, e, cfg.n_embd, cfg.n_ff, b.ctypes.data)
+                self.blobs[key] = b
+            return b.ctypes.data
+
+        self._blob_cb = BLOB_FN(blob_fn)
+        m.blob = self._blob_cb
+        m.blob_ctx = None
+        self.model = m
+        self.orc = oracle_lib.load()
+        self.orc.orc_model_forward.restype = I32
+        self.orc.orc_model_forward.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P]
+
+    def forward(self, pos, toks):
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        T = len(toks)
+        logits = np.empty((T, self.cfg.n_vocab), np.float32)
+        greedy = np.empty(T, np.int32)
+        pre = np.empty((T, self.cfg.hc, self.cfg.n_embd), np.float32)
+        rc = self.orc.orc_model_forward(C.byref(self.model), pos, toks.ctypes.data, T, logits.ctypes.data,
+                                        greedy.ctypes.data, pre.ctypes.data)
+        assert rc == 0, "orc_model_forward failed"
+        return logits, greedy, pre
+
+
+def small_cfg(wz_mod, ctx_max=1024, n_layers=4, topk=64):
+    """A small instance of the synthetic architecture for parity tests (QSA every 2nd layer)."""
+    c = wz_mod.StageCfg()
+    c.n_layers, c.qsa_period, c.n_embd, c.hc, c.hc_lr = n_layers, 2, 256, 4, 64
+    c.gdn_hk, c.gdn_hv = 2, 2
+    c.qsa_qh, c.qsa_kvh, c.qsa_hd, c.n_rot = 4, 2, 256, 64
+    c.idx_heads, c.idx_dim, c.idx_blk, c.idx_topk = 4, 128, 4, topk
+    c.n_exp, c.top_k, c.n_ff, c.n_vocab = 16, 4, 128, 1000
+    c.ctx_max, c.kv_ring, c.kv_sinks = ctx_max, 0, 0
+    c.rope_theta, c.eps = 1e7, 1e-6
+    return c
+
+
+def near_tie(logits_row, tol):
+    """True when the top-2 logits are within tol (greedy choice not determined by the oracle)."""
+    s = np.sort(logits_row)[::-1]
+    return (s[0] - s[1]) <= tol

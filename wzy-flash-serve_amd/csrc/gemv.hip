@@ -307,3 +307,180 @@ extern "C" int wzy_gemv_bf16(const uint16_t* W, const float* x, float* y, int ro
                              void* stream) {
     return launch_gemv_bf16(W, x, y, rows, cols, T, y_stride, nullptr, nullptr, as_stream(stream));
 }
+
+// ---------------------------------------------------------------------------------------------
+// Multi-segment GEMV over fp32 activations (projection groups: GDN qkv|z|alpha|beta, QSA
+// q|k|v|idx_k|idx_q, router|sgate, out-projections).  Q8_0 segments quantise x per 32 inside the
+// lane (same float operations as quant_act), so no separate quantisation launch is needed.
+// ---------------------------------------------------------------------------------------------
+namespace {
+WZY_DEV void quant32_f(const float* __restrict__ xp, int4& q0, int4& q1, float& d) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 f = ((const float4*) xp)[i];
+        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(v[i]));
+    d = am / 127.0f;
+    const float inv = d > 0.f ? 127.0f / am : 0.f;
+    int w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pk |= (uint32_t) (max(-127, min(127, rn_int(v[4 * k + j] * inv))) & 0xFF) << (8 * j);
+        w[k] = (int) pk;
+    }
+    q0 = make_int4(w[0], w[1], w[2], w[3]);
+    q1 = make_int4(w[4], w[5], w[6], w[7]);
+}
+}  // namespace
+
+template <int T, int NBL, int RPW>
+__global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const float* __restrict__ x, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < GEMV_MAX_SEGS; ++i)
+        if (i < segs.n && wave >= segs.seg[i].wave0) si = i;
+    const GemvSeg& sg = segs.seg[si];
+    const int row0 = (wave - sg.wave0) * RPW;
+    if (row0 >= sg.rows) return;
+    float acc[RPW][T];
+#pragma unroll
+    for (int s = 0; s < RPW; ++s)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
+
+    if (sg.kind == GEMV_Q8) {
+        const int nb = cols >> 5;
+        const int8_t* W = (const int8_t*) sg.w;
+        int4 c0[NBL][RPW], c1[NBL][RPW];
+        float dw[NBL][RPW];
+#pragma unroll
+        for (int i = 0; i < NBL; ++i) {
+            const int b = lane + 64 * i;
+#pragma unroll
+            for (int s = 0; s < RPW; ++s) {
+                const int r = row0 + s;
+                if (b < nb && r < sg.rows) {
+                    const int4* cp = (const int4*) (W + (size_t) r * cols + (size_t) b * 32);
+                    c0[i][s] = ld_stream_i4(cp);
+                    c1[i][s] = ld_stream_i4(cp + 1);
+                    dw[i][s] = h16_to_f(sg.s[(size_t) r * nb + b]);
+                } else {
+                    c0[i][s] = c1[i][s] = make_int4(0, 0, 0, 0);
+                    dw[i][s] = 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NBL; ++i) {
+            const int b = lane + 64 * i;
+            if (b >= nb) continue;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                int4 x0, x1;
+                float xs;
+                quant32_f(x + (size_t) t * cols + (size_t) b * 32, x0, x1, xs);
+#pragma unroll
+                for (int s = 0; s < RPW; ++s)
+                    acc[s][t] = fmaf(dw[i][s] * xs, (float) (dot16(c1[i][s], x1) + dot16(c0[i][s], x0)), acc[s][t]);
+            }
+        }
+    } else {
+        const uint16_t* W = (const uint16_t*) sg.w;
+        const int n8 = cols >> 3;
+        for (int j0 = 0; j0 < n8; j0 += 64 * 4) {
+            uint4 wv[4][RPW];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + lane + 64 * u;
+#pragma unroll
+                for (int s = 0; s < RPW; ++s) {
+                    const int r = row0 + s;
+                    wv[u][s] = (j < n8 && r < sg.rows) ? ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j)
+                                                       : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + lane + 64 * u;
+                if (j >= n8) continue;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float4 xa = *(const float4*) (x + (size_t) t * cols + j * 8);
+                    const float4 xb = *(const float4*) (x + (size_t) t * cols + j * 8 + 4);
+#pragma unroll
+                    for (int s = 0; s < RPW; ++s) {
+                        float a = acc[s][t];
+                        a = fmaf(bf16_lo(wv[u][s].x), xa.x, a);
+                        a = fmaf(bf16_hi(wv[u][s].x), xa.y, a);
+                        a = fmaf(bf16_lo(wv[u][s].y), xa.z, a);
+                        a = fmaf(bf16_hi(wv[u][s].y), xa.w, a);
+                        a = fmaf(bf16_lo(wv[u][s].z), xb.x, a);
+                        a = fmaf(bf16_hi(wv[u][s].z), xb.y, a);
+                        a = fmaf(bf16_lo(wv[u][s].w), xb.z, a);
+                        a = fmaf(bf16_hi(wv[u][s].w), xb.w, a);
+                        acc[s][t] = a;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < RPW; ++s) {
+        const int r = row0 + s;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[s][t]);
+            if (lane == 0 && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
+        }
+    }
+}
+
+template <int T>
+static void launch_segs_t(const GemvSegs& segs, int waves, int nbl, const float* x, int cols, hipStream_t st) {
+    const int blocks = (waves + 3) / 4;
+    switch (nbl) {
+        case 1: hipLaunchKernelGGL((gemv_segs_kernel<T, 1, 4>), dim3(blocks), dim3(256), 0, st, segs, x, cols); break;
+        case 2: hipLaunchKernelGGL((gemv_segs_kernel<T, 2, 2>), dim3(blocks), dim3(256), 0, st, segs, x, cols); break;
+        case 3: hipLaunchKernelGGL((gemv_segs_kernel<T, 3, 2>), dim3(blocks), dim3(256), 0, st, segs, x, cols); break;
+        default: hipLaunchKernelGGL((gemv_segs_kernel<T, 4, 1>), dim3(blocks), dim3(256), 0, st, segs, x, cols); break;
+    }
+}
+
+namespace wzy {
+int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t st) {
+    WZY_REQUIRE(x && segs.n >= 1 && segs.n <= GEMV_MAX_SEGS, "gemv_segs: bad segment list");
+    WZY_REQUIRE(cols >= 32 && cols % 32 == 0 && cols <= 8192, "gemv_segs: cols must be a multiple of 32 in [32, 8192]");
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "gemv_segs: T out of range");
+    const int nbl = (cols / 32 + 63) / 64;
+    const int rpw = nbl == 1 ? 4 : (nbl <= 3 ? 2 : 1);
+    int waves = 0;
+    for (int i = 0; i < segs.n; ++i) {
+        GemvSeg& s = segs.seg[i];
+        WZY_REQUIRE(s.w && s.y && s.rows > 0, "gemv_segs: segment %d incomplete", i);
+        WZY_REQUIRE(s.kind == GEMV_BF16 || s.s, "gemv_segs: Q8 segment %d without scales", i);
+        if (s.y_stride == 0) s.y_stride = s.rows;
+        s.wave0 = waves;
+        waves += (s.rows + rpw - 1) / rpw;
+    }
+    switch (T) {
+        case 1: launch_segs_t<1>(segs, waves, nbl, x, cols, st); break;
+        case 2: launch_segs_t<2>(segs, waves, nbl, x, cols, st); break;
+        case 3: launch_segs_t<3>(segs, waves, nbl, x, cols, st); break;
+        case 4: launch_segs_t<4>(segs, waves, nbl, x, cols, st); break;
+        case 5: launch_segs_t<5>(segs, waves, nbl, x, cols, st); break;
+        case 6: launch_segs_t<6>(segs, waves, nbl, x, cols, st); break;
+        case 7: launch_segs_t<7>(segs, waves, nbl, x, cols, st); break;
+        default: launch_segs_t<8>(segs, waves, nbl, x, cols, st); break;
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+}  // namespace wzy

@@ -1,0 +1,584 @@
+// qsa.hip -- QSA sparse-attention decode kernels for gfx950.
+//
+//  qsa_prep   one launch, workgroup roles: q heads (RMSNorm + NeoX RoPE on the first n_rot dims),
+//             kv heads (same on k, then per-64 INT8 quantisation of k and v into the KV store),
+//             indexer q heads (RMSNorm + RoPE), and the indexer append (fp16-rounded key, 4-token
+//             mean pooling, RMSNorm, RoPE at the block start, open-block placeholder).
+//             reference: fused_head_norm_rope_multi, kv_append_int8_multi, qsa_indexer_append_multi
+//             (src/wzy_qsa_256k.cuh:50-209)
+//  qsa_score  score[b] = sum_h relu(fp16(q_h) . fp16(key_b)) for complete blocks (fp32 accumulate,
+//             v_dot2_f32_f16), the open block against the fp32 placeholder key (+1e9 if partial).
+//             Keys are stored as fp16 (the reference rounds its fp32 keys to fp16 when scoring), so
+//             the scan reads 256 bytes per block.
+//             reference: pf_qsa_block_scores_wmma, pf_qsa_tail_score_kernel (src/wzy_qsa_wmma.cuh:492-612)
+//  qsa_topk   exact top-`topk` cells: 4 x 8-bit radix select over order-preserving keys of the block
+//             scores with block weights, ties at the threshold filled in the reference's
+//             256-thread-strided order.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
+//  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, row) computes
+//             the 12 GQA heads' scores from INT8 K, local softmax and the INT8 V sum; qsa_combine
+//             merges the chunks and applies sigmoid(gate).
+//             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532)
+#include "wzy_device.h"
+#include "wzy_host.h"
+#include "wzy_qsa.h"
+
+using namespace wzy;
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+namespace {
+
+WZY_DEV size_t kv_slot(int p, const QsaDims& dm) {
+    if (dm.ring_cap <= 0) return (size_t) p;
+    if (dm.ring_cap <= 2 * dm.sinks) return (size_t) (p % dm.ring_cap);
+    if (p < dm.sinks) return (size_t) p;
+    return (size_t) (dm.sinks + (p - dm.sinks) % (dm.ring_cap - dm.sinks));
+}
+
+// RMSNorm(gamma) + NeoX RoPE (pairs i, i + n_rot/2) of one head vector p[0..hd) in place.
+// 256 threads, thread i owns element i.
+WZY_DEV void norm_rope(float* p, int hd, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
+                       int n_rot, float eps, float* s_vals, float* s_red) {
+    const int i = threadIdx.x;
+    const float x = i < hd ? p[i] : 0.f;
+    const float ss = block_sum<4>(x * x, s_red);
+    const float sc = 1.0f / sqrtf(ss / (float) hd + eps);
+    const float v = x * (sc * (i < hd ? gamma[i] : 0.f));
+    if (i < hd) s_vals[i] = v;
+    __syncthreads();
+    const int half = n_rot / 2;
+    if (i < hd) {
+        float y = v;
+        if (i < n_rot) {
+            const int pr = i % half;
+            const float c = cos_tab[(size_t) pos * half + pr], s = sin_tab[(size_t) pos * half + pr];
+            const float a = s_vals[pr], d = s_vals[pr + half];
+            y = (i < half) ? (a * c - d * s) : (a * s + d * c);
+        }
+        p[i] = y;
+    }
+    __syncthreads();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// prep
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
+    __shared__ float s_vals[256];
+    __shared__ float s_red[4];
+    const QsaDims& dm = a.dm;
+    const int wg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int base = *a.pos;
+    const int hd = dm.hd, kvd = dm.kvh * dm.hd;
+
+    if (wg < dm.qh) {
+        for (int t = 0; t < T; ++t) {
+            const int pos = base + t;
+            if (pos < 0 || pos >= dm.ctx_max) continue;
+            norm_rope(a.qg + (size_t) t * dm.qh * 2 * hd + (size_t) wg * 2 * hd, hd, a.q_norm, a.cos_tab, a.sin_tab,
+                      pos, dm.n_rot, dm.eps, s_vals, s_red);
+        }
+        return;
+    }
+    if (wg < dm.qh + dm.kvh) {
+        const int j = wg - dm.qh;
+        for (int t = 0; t < T; ++t) {
+            const int pos = base + t;
+            if (pos < 0 || pos >= dm.ctx_max) continue;
+            float* kp = a.kk + (size_t) t * kvd + (size_t) j * hd;
+            norm_rope(kp, hd, a.k_norm, a.cos_tab, a.sin_tab, pos, dm.n_rot, dm.eps, s_vals, s_red);
+            // per-64 INT8 quantisation: one wave per 64-element group (hd = 256 -> 4 groups)
+            if (tid < hd) {
+                const float kv = kp[tid];
+                const float vv = a.vv[(size_t) t * kvd + (size_t) j * hd + tid];
+                const float kmax = wave_max(fabsf(kv)), vmax = wave_max(fabsf(vv));
+                const uint16_t kh = f_to_h16(kmax / 127.0f), vh = f_to_h16(vmax / 127.0f);
+                const float kdq = h16_to_f(kh), vdq = h16_to_f(vh);
+                const int kqi = kdq > 0.f ? max(-127, min(127, rn_int(kv / kdq))) : 0;
+                const int vqi = vdq > 0.f ? max(-127, min(127, rn_int(vv / vdq))) : 0;
+                const size_t slot = kv_slot(pos, dm);
+                a.kv.kq[slot * kvd + (size_t) j * hd + tid] = (int8_t) kqi;
+                a.kv.vq[slot * kvd + (size_t) j * hd + tid] = (int8_t) vqi;
+                if (lane == 0) {
+                    a.kv.ks[slot * (kvd / 64) + (size_t) j * (hd / 64) + w] = kh;
+                    a.kv.vs[slot * (kvd / 64) + (size_t) j * (hd / 64) + w] = vh;
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    if (wg < dm.qh + dm.kvh + dm.ih) {
+        const int i = wg - dm.qh - dm.kvh;
+        for (int t = 0; t < T; ++t) {
+            const int pos = base + t;
+            if (pos < 0 || pos >= dm.ctx_max) continue;
+            norm_rope(a.q_idx + (size_t) t * dm.ih * dm.idim + (size_t) i * dm.idim, dm.idim, a.iq_norm, a.cos_tab,
+                      a.sin_tab, pos, dm.n_rot, dm.eps, s_vals, s_red);
+        }
+        return;
+    }
+    // indexer append (one workgroup, thread d owns key dim d)
+    const int D = dm.idim, B = dm.iblk, half = dm.n_rot / 2;
+    const int d = tid;
+    for (int t = 0; t < T; ++t) {
+        const int pos = base + t;
+        if (pos < 0 || pos >= dm.ctx_max) continue;
+        const float incoming = d < D ? round_h16(a.idx_raw[(size_t) t * D + d]) : 0.f;
+        const int slot = pos % B;
+        if (d < D && slot < B - 1) a.ix.tail[slot * D + d] = incoming;
+        const int b = pos / B;
+        if (pos == 0 || slot == B - 1) {
+            float sum = 0.f;
+            if (d < D) {
+                sum = (pos == 0) ? incoming : a.ix.tail[d];
+                for (int jj = 1; jj < B; ++jj) sum = sum + ((pos == 0 || jj == B - 1) ? incoming : a.ix.tail[jj * D + d]);
+            }
+            const float mean = sum * (1.0f / (float) B);
+            const float ss = block_sum<4>(mean * mean, s_red);
+            const float sc = 1.0f / sqrtf(ss / (float) D + dm.eps);
+            const float val = d < D ? sc * mean * a.ik_norm[d] : 0.f;
+            s_vals[d] = val;
+            __syncthreads();
+            if (d < D) {
+                const int rope_pos = (pos == 0) ? 0 : B * b;
+                float y = val;
+                if (d < dm.n_rot) {
+                    const int pr = d % half;
+                    const float c = a.cos_tab[(size_t) rope_pos * half + pr], s = a.sin_tab[(size_t) rope_pos * half + pr];
+                    const float x0 = s_vals[pr], z0 = s_vals[pr + half];
+                    y = (d < half) ? (x0 * c - z0 * s) : (x0 * s + z0 * c);
+                }
+                a.ix.pooled[(size_t) b * D + d] = f_to_h16(y);
+                if (pos == 0) a.ix.dead[d] = y;
+                else a.ix.pooled[(size_t) (b + 1) * D + d] = f_to_h16(a.ix.dead[d]);
+            }
+            __syncthreads();
+        }
+        if (a.ix.tail_snaps && d < D) {
+            for (int jj = 0; jj < B - 1; ++jj)
+                a.ix.tail_snaps[((size_t) t * (B - 1) + jj) * D + d] = a.ix.tail[jj * D + d];
+            a.ix.dead_snaps[(size_t) t * D + d] = a.ix.dead[d];
+            a.ix.pool_snaps[((size_t) t * 2 + 0) * D + d] = a.ix.pooled[(size_t) b * D + d];
+            a.ix.pool_snaps[((size_t) t * 2 + 1) * D + d] = a.ix.pooled[(size_t) (b + 1) * D + d];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// block scores
+// ---------------------------------------------------------------------------------------------
+constexpr int SC_BLOCKS_PER_WG = 64;
+
+template <int T>
+__global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
+    __shared__ h2_t s_q[T][4][64];          // fp16 indexer queries, ih <= 4, idim <= 128
+    const QsaDims& dm = a.dm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int base = *a.pos;
+    const int D = dm.idim, B = dm.iblk, IH = dm.ih;
+    const int n_kv_max = base + T;
+    if (n_kv_max <= dm.topk) return;                    // short context: identity selection
+    const int b0 = blockIdx.x * SC_BLOCKS_PER_WG;
+    const bool tail_wg = blockIdx.x == 0;
+    if (b0 >= n_kv_max / B && !tail_wg) return;
+
+    for (int i = tid; i < T * IH * (D / 2); i += blockDim.x) {
+        const int t = i / (IH * (D / 2)), r = i % (IH * (D / 2));
+        const int h = r / (D / 2), k = r % (D / 2);
+        const float* q = a.q_idx + (size_t) t * IH * D + (size_t) h * D + 2 * k;
+        h2_t v;
+        v.x = (_Float16) q[0];
+        v.y = (_Float16) q[1];
+        s_q[t][h][k] = v;
+    }
+    __syncthreads();
+
+    // complete blocks: 16 lanes per block (8 halves each), 4 blocks per wave-iteration
+    const int li = lane & 15;
+    for (int it = 0; it < SC_BLOCKS_PER_WG / 16; ++it) {
+        const int b = b0 + w * 16 + it * 4 + (lane >> 4);
+        if (b >= a.max_b || b >= n_kv_max / B) continue;
+        const uint4 kraw = *(const uint4*) (a.pooled + (size_t) b * D + 8 * li);
+        const h2_t k0 = __builtin_bit_cast(h2_t, kraw.x), k1 = __builtin_bit_cast(h2_t, kraw.y);
+        const h2_t k2 = __builtin_bit_cast(h2_t, kraw.z), k3 = __builtin_bit_cast(h2_t, kraw.w);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int n_kv = base + t + 1;
+            float score = 0.f;
+            for (int h = 0; h < IH; ++h) {
+                float dd = 0.f;
+                dd = __builtin_amdgcn_fdot2(s_q[t][h][4 * li + 0], k0, dd, false);
+                dd = __builtin_amdgcn_fdot2(s_q[t][h][4 * li + 1], k1, dd, false);
+                dd = __builtin_amdgcn_fdot2(s_q[t][h][4 * li + 2], k2, dd, false);
+                dd = __builtin_amdgcn_fdot2(s_q[t][h][4 * li + 3], k3, dd, false);
+                dd = sum16(dd);
+                score += dd > 0.f ? dd : 0.f;
+            }
+            if (li == 0 && n_kv > dm.topk && b < n_kv / B) a.scores[(size_t) t * a.max_b + b] = score;
+        }
+    }
+    // open block: fp32 dot with the placeholder key (wave t handles row t)
+    if (tail_wg) {
+        for (int t = w; t < T; t += 4) {
+            const int n_kv = base + t + 1;
+            const int nbid = n_kv / B;
+            if (n_kv <= dm.topk || nbid >= a.max_b) continue;
+            float score = 0.f;
+            for (int h = 0; h < IH; ++h) {
+                float p = 0.f;
+                for (int k = lane; k < D; k += 64) p = fmaf(a.dead[k], a.q_idx[(size_t) t * IH * D + (size_t) h * D + k], p);
+                p = wave_sum(p);
+                score += p > 0.f ? p : 0.f;
+            }
+            if (n_kv % B != 0) score += 1e9f;
+            if (lane == 0) a.scores[(size_t) t * a.max_b + nbid] = score;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// exact top-k cell selection (one 256-thread workgroup per row)
+// ---------------------------------------------------------------------------------------------
+WZY_DEV uint32_t order_key(float s) {
+    const float v = s + 0.0f;                       // -0 -> +0
+    if (!(v == v)) return 0u;                       // NaN sorts lowest
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inclusive prefix sum over the 256 threads in thread order (4 waves), result per thread.
+WZY_DEV int block_scan_incl(int v, int* s_w) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_w[w] = x;
+    __syncthreads();
+    int before = 0;
+    for (int i = 0; i < w; ++i) before += s_w[i];
+    __syncthreads();
+    return x + before;
+}
+
+__global__ void __launch_bounds__(256) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
+                                                       const float* __restrict__ scores, int max_b,
+                                                       int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
+    __shared__ int hist[256];
+    __shared__ int s_digit, s_above;
+    __shared__ int s_w[4];
+    const int t = threadIdx.x;
+    const int row = blockIdx.x;
+    const int n_kv = *pos_dev + row + 1;
+    const int K = dm.topk, B = dm.iblk;
+    const int width = min(n_kv, K);
+    int* out = sel_ids + (size_t) row * K;
+    if (t == 0) sel_cnt[row] = width;
+    if (n_kv <= K) {
+        for (int j = t; j < n_kv; j += 256) out[j] = j;
+        return;
+    }
+    const int n_bid = n_kv / B;
+    const int nb = n_bid + 1;
+    const float* sc = scores + (size_t) row * max_b;
+    auto weight = [&](int b) { return b < n_bid ? B : (n_kv - n_bid * B); };
+
+    uint32_t prefix = 0;
+    int above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[t] = 0;
+        __syncthreads();
+        const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
+        for (int b = t; b < nb; b += 256) {
+            const int wgt = weight(b);
+            if (wgt == 0) continue;
+            const uint32_t k = order_key(sc[b]);
+            if ((k & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(k >> shift) & 255u], wgt);
+        }
+        __syncthreads();
+        if (t == 0) {
+            int cum = above, dg = 255;
+            for (; dg > 0; --dg) {
+                if (cum + hist[dg] >= width) break;
+                cum += hist[dg];
+            }
+            s_digit = dg;
+            s_above = cum;
+        }
+        __syncthreads();
+        prefix |= (uint32_t) s_digit << shift;
+        above = s_above;
+        __syncthreads();
+    }
+
+    // weights strictly above the threshold key, and at it, per thread (thread-strided blocks)
+    const uint32_t thr = prefix;
+    const int eq_budget = width - above;
+    int gt = 0, eq = 0;
+    for (int b = t; b < nb; b += 256) {
+        const int wgt = weight(b);
+        if (wgt == 0) continue;
+        const uint32_t k = order_key(sc[b]);
+        if (k > thr) gt += wgt;
+        else if (k == thr) eq += wgt;
+    }
+    const int eq_excl = block_scan_incl(eq, s_w) - eq;
+    const int my_eq = max(0, min(eq, eq_budget - eq_excl));
+    const int sel = gt + my_eq;
+    int wpos = block_scan_incl(sel, s_w) - sel;
+    int eq_left = my_eq;
+    for (int b = t; b < nb; b += 256) {
+        const int wgt = weight(b);
+        if (wgt == 0) continue;
+        const uint32_t k = order_key(sc[b]);
+        if (k > thr) {
+            for (int c = 0; c < wgt; ++c) out[wpos++] = b * B + c;
+        } else if (k == thr && eq_left > 0) {
+            const int take = min(wgt, eq_left);
+            for (int c = 0; c < take; ++c) out[wpos++] = b * B + c;
+            eq_left -= take;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// sparse attention
+// ---------------------------------------------------------------------------------------------
+constexpr int ATT_GQ_MAX = 16;
+
+__global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
+    __shared__ float s_q[ATT_GQ_MAX][256];
+    __shared__ float s_sc[ATT_GQ_MAX][QSA_ATT_CHUNK];
+    __shared__ size_t s_slot[QSA_ATT_CHUNK];
+    const QsaDims& dm = a.dm;
+    const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hd = dm.hd, kvd = dm.kvh * hd, gq = dm.qh / dm.kvh;
+    const int n_kv = *a.pos + t + 1;
+    const int width = min(n_kv, dm.topk);
+    const int c0 = c * QSA_ATT_CHUNK;
+    if (c0 >= width) return;
+    const int ncell = min(QSA_ATT_CHUNK, width - c0);
+    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+
+    for (int i = tid; i < gq * hd; i += blockDim.x) {
+        const int hh = i / hd, d = i % hd;
+        s_q[hh][d] = a.qg[(size_t) t * dm.qh * 2 * hd + (size_t) (j * gq + hh) * 2 * hd + d];
+    }
+    if (tid < QSA_ATT_CHUNK) {
+        const int idx = c0 + tid;
+        const int p = tid < ncell ? (n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx]) : 0;
+        s_slot[tid] = kv_slot(p, dm);
+    }
+    __syncthreads();
+
+    // scores: 16 lanes per cell (16 dims each), 4 cells per wave-iteration
+    const int li = lane & 15;
+    const int g = (16 * li) / 64;
+    for (int it = 0; it < QSA_ATT_CHUNK / 16; ++it) {
+        const int cell = w * 16 + it * 4 + (lane >> 4);
+        const bool valid = cell < ncell;
+        int4 kr = make_int4(0, 0, 0, 0);
+        float ksc = 0.f;
+        if (valid) {
+            kr = *(const int4*) (a.kv.kq + s_slot[cell] * kvd + (size_t) j * hd + 16 * li);
+            ksc = h16_to_f(a.kv.ks[s_slot[cell] * (kvd / 64) + (size_t) j * (hd / 64) + g]);
+        }
+        float kf[16];
+        const int8_t* kb = (const int8_t*) &kr;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) kf[k] = (float) kb[k];
+        for (int hh = 0; hh < gq; ++hh) {
+            float p = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) p = fmaf(kf[k], s_q[hh][16 * li + k], p);
+            p = sum16(p * ksc);
+            if (li == 0) s_sc[hh][cell] = valid ? p * 0.0625f : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // local softmax per head: wave w handles heads w, w+4, ...; lane = cell
+    float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 2;
+    for (int hh = w; hh < gq; hh += 4) {
+        const float s = s_sc[hh][lane];
+        const float m = wave_max(s);
+        const float e = lane < ncell ? __expf(s - m) : 0.f;
+        const float l = wave_sum(e);
+        s_sc[hh][lane] = e;
+        if (lane == 0) { ml[hh * 2] = m; ml[hh * 2 + 1] = l; }
+    }
+    __syncthreads();
+    // V: thread d owns output dim d for all gq heads
+    if (tid < hd) {
+        float acc[ATT_GQ_MAX];
+#pragma unroll
+        for (int hh = 0; hh < ATT_GQ_MAX; ++hh) acc[hh] = 0.f;
+        const int gv = tid / 64;
+        for (int cell = 0; cell < ncell; ++cell) {
+            const size_t sl = s_slot[cell];
+            const float vsc = h16_to_f(a.kv.vs[sl * (kvd / 64) + (size_t) j * (hd / 64) + gv]);
+            const float v = (float) a.kv.vq[sl * kvd + (size_t) j * hd + tid];
+#pragma unroll
+            for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
+                if (hh < gq) acc[hh] = fmaf(s_sc[hh][cell] * vsc, v, acc[hh]);
+        }
+        float* po = a.part + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * hd;
+        for (int hh = 0; hh < gq; ++hh) po[(size_t) hh * hd + tid] = acc[hh];
+    }
+}
+
+__global__ void __launch_bounds__(256) qsa_combine_kernel(QsaAttnArgs a) {
+    const QsaDims& dm = a.dm;
+    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+    const int hd = dm.hd, gq = dm.qh / dm.kvh, j = h / gq, hh = h % gq;
+    const int n_kv = *a.pos + t + 1;
+    const int width = min(n_kv, dm.topk);
+    const int nch_all = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    const int nch = (width + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    const float* ml = a.part_ml + (((size_t) t * dm.kvh + j) * nch_all) * gq * 2;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, ml[((size_t) c * gq + hh) * 2]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        const float f = __expf(ml[((size_t) c * gq + hh) * 2] - M);
+        L = fmaf(ml[((size_t) c * gq + hh) * 2 + 1], f, L);
+        if (d < hd) O = fmaf(a.part[((((size_t) t * dm.kvh + j) * nch_all + c) * gq + hh) * hd + d], f, O);
+    }
+    if (d < hd) {
+        const float gate = a.qg[(size_t) t * dm.qh * 2 * hd + (size_t) h * 2 * hd + hd + d];
+        a.out[(size_t) t * dm.qh * hd + (size_t) h * hd + d] = (O * (1.0f / L)) / (1.0f + __expf(-gate));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------
+namespace wzy {
+
+static int check_dims(const QsaDims& dm) {
+    WZY_REQUIRE(dm.hd == 256 && dm.qh % dm.kvh == 0 && dm.qh / dm.kvh <= ATT_GQ_MAX, "qsa: head layout unsupported");
+    WZY_REQUIRE(dm.idim <= 128 && dm.idim % 8 == 0 && dm.ih <= 4 && dm.iblk >= 2, "qsa: indexer layout unsupported");
+    WZY_REQUIRE(dm.n_rot % 2 == 0 && dm.n_rot <= dm.idim && dm.n_rot <= dm.hd, "qsa: bad n_rot");
+    WZY_REQUIRE(dm.topk >= 1 && dm.ctx_max >= 1, "qsa: bad topk/ctx");
+    return WZY_OK;
+}
+
+int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
+    WZY_TRY(check_dims(a.dm));
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_prep: T out of range");
+    const int n_wg = a.dm.qh + a.dm.kvh + a.dm.ih + 1;
+    hipLaunchKernelGGL(qsa_prep_kernel, dim3(n_wg), dim3(256), 0, st, a, T);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
+    WZY_TRY(check_dims(a.dm));
+    const int grid = (a.max_b + SC_BLOCKS_PER_WG - 1) / SC_BLOCKS_PER_WG;
+    switch (T) {
+#define C_(TT) case TT: hipLaunchKernelGGL((qsa_score_kernel<TT>), dim3(grid), dim3(256), 0, st, a); break;
+        C_(1) C_(2) C_(3) C_(4) C_(5) C_(6) C_(7)
+        default: hipLaunchKernelGGL((qsa_score_kernel<8>), dim3(grid), dim3(256), 0, st, a); break;
+#undef C_
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
+                    int T, hipStream_t st) {
+    WZY_TRY(check_dims(dm));
+    hipLaunchKernelGGL(qsa_topk_kernel, dim3(T), dim3(256), 0, st, dm, pos, scores, max_b, sel_ids, sel_cnt);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+size_t qsa_attn_part_floats(const QsaDims& dm, int T) {
+    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    return (size_t) T * dm.kvh * nch * dm.qh / dm.kvh * dm.hd;
+}
+
+int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st) {
+    WZY_TRY(check_dims(a.dm));
+    const int nch = (a.dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh, T), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(qsa_combine_kernel, dim3(a.dm.qh, T), dim3(256), 0, st, a);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+}  // namespace wzy
+
+// ---------------------------------------------------------------------------------------------
+// C ABI (device pointers; `pos` is a device int holding the position of row 0)
+// ---------------------------------------------------------------------------------------------
+static QsaDims dims_of(int qh, int kvh, int hd, int n_rot, int ih, int idim, int iblk, int topk, int ctx_max,
+                       int ring_cap, int sinks, float eps) {
+    QsaDims d;
+    d.qh = qh; d.kvh = kvh; d.hd = hd; d.n_rot = n_rot; d.ih = ih; d.idim = idim; d.iblk = iblk; d.topk = topk;
+    d.ctx_max = ctx_max; d.ring_cap = ring_cap; d.sinks = sinks; d.eps = eps;
+    return d;
+}
+
+extern "C" int wzy_qsa_prepare(const wzy_qsa_dims* dims, const int* pos, float* qg, float* kk, const float* vv,
+                               float* q_idx, const float* idx_raw, const float* q_norm, const float* k_norm,
+                               const float* iq_norm, const float* ik_norm, const float* cos_tab, const float* sin_tab,
+                               int8_t* kq, uint16_t* ks, int8_t* vq, uint16_t* vs, float* idx_tail, float* idx_dead,
+                               uint16_t* idx_pooled, int T, void* stream) {
+    WZY_REQUIRE(dims && pos && qg && kk && vv && q_idx && idx_raw && kq && ks && vq && vs && idx_tail && idx_dead &&
+                    idx_pooled && cos_tab && sin_tab && q_norm && k_norm && iq_norm && ik_norm,
+                "wzy_qsa_prepare: null pointer");
+    QsaPrepArgs a{};
+    a.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
+                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    a.pos = pos; a.qg = qg; a.kk = kk; a.vv = vv; a.q_idx = q_idx; a.idx_raw = idx_raw;
+    a.q_norm = q_norm; a.k_norm = k_norm; a.iq_norm = iq_norm; a.ik_norm = ik_norm;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab;
+    a.kv = QsaKv{kq, ks, vq, vs};
+    a.ix.tail = idx_tail; a.ix.dead = idx_dead; a.ix.pooled = idx_pooled;
+    return launch_qsa_prep(a, T, as_stream(stream));
+}
+
+extern "C" int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const uint16_t* idx_pooled,
+                              const float* idx_dead, const float* q_idx, float* scores, int max_b, int* sel_ids,
+                              int* sel_cnt, int T, void* stream) {
+    WZY_REQUIRE(dims && pos && idx_pooled && idx_dead && q_idx && scores && sel_ids && sel_cnt,
+                "wzy_qsa_select: null pointer");
+    QsaScoreArgs s{};
+    s.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
+                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    WZY_REQUIRE(max_b >= dims->ctx_max / dims->idx_blk + 1, "wzy_qsa_select: max_b too small");
+    s.pos = pos; s.pooled = idx_pooled; s.dead = idx_dead; s.q_idx = q_idx; s.scores = scores; s.max_b = max_b;
+    hipStream_t st = as_stream(stream);
+    WZY_TRY(launch_qsa_score(s, T, st));
+    return launch_qsa_topk(s.dm, pos, scores, max_b, sel_ids, sel_cnt, T, st);
+}
+
+extern "C" size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T) {
+    QsaDims d = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
+                        dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    const size_t pf = qsa_attn_part_floats(d, T);
+    return (pf + pf / d.hd * 2) * sizeof(float) + 512;
+}
+
+extern "C" int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const float* qg, const int8_t* kq,
+                              const uint16_t* ks, const int8_t* vq, const uint16_t* vs, const int* sel_ids, float* out,
+                              void* workspace, size_t workspace_bytes, int T, void* stream) {
+    WZY_REQUIRE(dims && pos && qg && kq && ks && vq && vs && sel_ids && out && workspace,
+                "wzy_qsa_attend: null pointer");
+    WZY_REQUIRE(workspace_bytes >= wzy_qsa_attend_workspace_bytes(dims, T), "wzy_qsa_attend: workspace too small");
+    QsaAttnArgs a{};
+    a.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
+                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    a.pos = pos; a.qg = qg; a.kv = QsaKv{(int8_t*) kq, (uint16_t*) ks, (int8_t*) vq, (uint16_t*) vs};
+    a.sel_ids = sel_ids; a.out = out;
+    const size_t pf = qsa_attn_part_floats(a.dm, T);
+    a.part = (float*) workspace;
+    a.part_ml = a.part + pf;
+    return launch_qsa_attn(a, T, as_stream(stream));
+}

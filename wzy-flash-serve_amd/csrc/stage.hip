@@ -1,0 +1,813 @@
+// stage.hip -- the decode-path layer executor (StageGpu replacement) for one MI355X.
+//
+// Owns every weight, state and scratch buffer of the model in HBM and enqueues the per-layer
+// kernel sequence of a forward on one stream; each window shape is captured once into a hipGraph
+// and replayed.  Per layer (T window rows):
+//   attention half:  hc_pre(fold previous FFN block) -> hc_post -> projections (one multi-segment
+//                    GEMV) -> GDN step | QSA prep, score, top-k, attention -> out-projection
+//   FFN half:        hc_pre(fold attention block) -> hc_post -> router GEMV -> MoE gate/up -> down
+// Head: hc_pre(fold last FFN block) -> hc_post -> bf16 LM head GEMV -> argmax / top-16.
+// reference: StageGpu (src/wzy_stage_v2.cuh:334-1045), record_forward (:476-857).
+#include <math.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/wzy_stage.h"
+#include "../../include/wzy_synth.h"
+#include "wzy_gdn.h"
+#include "wzy_gemv.h"
+#include "wzy_hc.h"
+#include "wzy_host.h"
+#include "wzy_moe.h"
+#include "wzy_qsa.h"
+#include "wzy_reduce.h"
+#include "wzy_synth_impl.h"
+
+using namespace wzy;
+
+namespace {
+
+enum DType { DT_F32, DT_BF16, DT_F16, DT_I8, DT_U8, DT_I32 };
+size_t dt_size(DType t) { return (t == DT_F32 || t == DT_I32) ? 4 : (t == DT_BF16 || t == DT_F16) ? 2 : 1; }
+
+struct Tensor {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+// Synthetic-model tensor ids (stream sub-ids of WZY_S_DENSE / WZY_S_STATE)
+enum TensorId {
+    TI_ROUTER = 0, TI_SGATE = 1, TI_SH_GATE = 2, TI_SH_UP = 3, TI_SH_DOWN = 4,
+    TI_HC_NORM = 10, TI_HC_DOWN = 11, TI_HC_UP = 12, TI_HC_INJ = 13,   // + 10*half
+    TI_QKV = 30, TI_WGATE = 31, TI_WOUT = 32, TI_ALPHA = 33, TI_BETA = 34, TI_SSM_A = 35, TI_DT = 36,
+    TI_CONV = 37, TI_SSM_NORM = 38,
+    TI_WQ = 40, TI_WK = 41, TI_WV = 42, TI_WO = 43, TI_QNORM = 44, TI_KNORM = 45, TI_IDXQ = 46, TI_IDXK = 47,
+    TI_IDXQN = 48, TI_IDXKN = 49,
+    TI_EMB = 60, TI_HEAD_NORM = 61, TI_HEAD_DOWN = 62, TI_HEAD_UP = 63, TI_HEAD = 64,
+    TS_CONV = 70, TS_SSM = 71, TS_TAIL = 72, TS_DEAD = 73, TS_POOLED = 74,
+};
+constexpr uint32_t MODEL_LAYER = 0xFFFF;
+
+struct Q8 {
+    int8_t* q = nullptr;
+    uint16_t* s = nullptr;
+    int rows = 0, cols = 0;
+};
+
+struct Layer {
+    bool qsa = false;
+    int local = -1;                 // index among GDN or QSA layers
+    float* hc_norm[2] = {nullptr, nullptr};
+    Q8 hc_down[2], hc_up[2];
+    uint16_t* hc_inj[2] = {nullptr, nullptr};
+    // GDN
+    Q8 qkv, wgate, wout;
+    uint16_t *alpha = nullptr, *beta = nullptr;
+    float *ssm_a = nullptr, *dt = nullptr, *conv_w = nullptr, *ssm_norm = nullptr;
+    float *conv_hist = nullptr, *ssm = nullptr;     // state
+    // QSA
+    Q8 wq, wk, wv, wo;
+    float *q_norm = nullptr, *k_norm = nullptr, *idx_qn = nullptr, *idx_kn = nullptr;
+    uint16_t *idx_q = nullptr, *idx_k = nullptr;
+    QsaKv kv{};
+    QsaIdx ix{};
+    // MoE
+    wzy_moe_weights moe{};
+};
+
+}  // namespace
+
+struct wzy_stage {
+    wzy_stage_cfg cfg{};
+    int dev = 0;
+    hipStream_t stream = nullptr;
+    bool graphs = true;
+    size_t dev_bytes = 0;
+    std::vector<void*> allocs;
+    std::map<std::pair<int, std::string>, Tensor> tensors;
+
+    // derived dims
+    int D = 0, HCD = 0, QKV = 0, GV = 0, QD = 0, KVD = 0, max_b = 0, n_gdn = 0, n_qsa = 0;
+    QsaDims qd{};
+
+    std::vector<Layer> L;
+    uint8_t* experts = nullptr;     // all layers' NVFP4 expert records
+    size_t expert_rec = 0;
+    uint16_t* emb = nullptr;
+    float* head_norm = nullptr;
+    Q8 head_down, head_up;
+    uint16_t* head = nullptr;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+
+    // activations / scratch (MAX_W rows)
+    float* R[2] = {nullptr, nullptr};
+    int r_pre_head = 0;             // which R buffer holds the pre-head residual
+    float *nsc = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
+    float *qkv = nullptr, *z = nullptr, *ab = nullptr, *y = nullptr, *block = nullptr, *comb = nullptr;
+    float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
+    float *att_part = nullptr, *att_ml = nullptr, *att_out = nullptr;
+    int *sel_ids = nullptr, *sel_cnt = nullptr;
+    void* moe_ws = nullptr;
+    MoeWs mws{};
+    float* logits = nullptr;
+    void* red_ws = nullptr;
+    float* emb_rows = nullptr;
+    // snapshots
+    float *conv_snaps = nullptr, *ssm_snaps = nullptr;
+    float *tail_snaps = nullptr, *dead_snaps = nullptr;
+    uint16_t* pool_snaps = nullptr;
+    // step inputs / outputs
+    int* d_step = nullptr;          // [0] = pos, [1..8] = toks
+    int* h_step = nullptr;          // pinned
+    int* h_greedy = nullptr;        // pinned, device-visible
+    float* h_top_v = nullptr;
+    int* h_top_i = nullptr;
+    int* d_greedy = nullptr;        // device views of the pinned outputs
+    float* d_top_v = nullptr;
+    int* d_top_i = nullptr;
+    int last_T = 0;
+    bool have_head = false;
+    bool loaded = false;
+
+    std::map<unsigned long long, hipGraphExec_t> graph_execs;
+
+    bool profiling = false;         // direct launches instead of graphs
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+
+    ~wzy_stage();
+    int alloc(void** p, size_t bytes, bool zero = true);
+    template <class T>
+    int alloc_t(T** p, size_t n, bool zero = true) { return alloc((void**) p, n * sizeof(T), zero); }
+    int reg(int layer, const char* name, void* p, size_t bytes) {
+        tensors[{layer, std::string(name)}] = Tensor{p, bytes};
+        return WZY_OK;
+    }
+    int alloc_q8(Q8& m, int rows, int cols, int layer, const char* name);
+    int init_buffers();
+    int enqueue(int T, bool emb_host, bool run_head, bool save_snaps, bool want_top16, int snap_offset);
+};
+
+wzy_stage::~wzy_stage() {
+    (void) hipSetDevice(dev);
+    for (auto& kv : graph_execs)
+        if (kv.second) (void) hipGraphExecDestroy(kv.second);
+    for (void* p : allocs) (void) hipFree(p);
+    if (h_step) (void) hipHostFree(h_step);
+    if (h_greedy) (void) hipHostFree(h_greedy);
+    if (h_top_v) (void) hipHostFree(h_top_v);
+    if (h_top_i) (void) hipHostFree(h_top_i);
+    for (auto& e : ev)
+        if (e) (void) hipEventDestroy(e);
+    if (stream) (void) hipStreamDestroy(stream);
+}
+
+int wzy_stage::alloc(void** p, size_t bytes, bool zero) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 16;
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        (void) hipGetLastError();
+        *p = nullptr;
+        set_error("stage: hipMalloc(%zu) failed (%.2f GiB already held)", bytes, dev_bytes / 1073741824.0);
+        return WZY_ENOMEM;
+    }
+    allocs.push_back(*p);
+    dev_bytes += bytes;
+    if (zero) WZY_HIP_TRY(hipMemset(*p, 0, bytes));
+    return WZY_OK;
+}
+
+int wzy_stage::alloc_q8(Q8& m, int rows, int cols, int layer, const char* name) {
+    m.rows = rows;
+    m.cols = cols;
+    WZY_TRY(alloc_t(&m.q, (size_t) rows * cols, false));
+    WZY_TRY(alloc_t(&m.s, (size_t) rows * cols / 32, false));
+    std::string n(name);
+    reg(layer, (n + ".q").c_str(), m.q, (size_t) rows * cols);
+    reg(layer, (n + ".s").c_str(), m.s, (size_t) rows * cols / 32 * 2);
+    return WZY_OK;
+}
+
+static int validate(const wzy_stage_cfg& c) {
+    WZY_REQUIRE(c.n_layers >= 1 && c.n_layers <= 4096 && c.qsa_period >= 1, "stage: bad layer count / period");
+    WZY_REQUIRE(c.n_embd >= 256 && c.n_embd % 256 == 0 && c.n_embd <= 8192, "stage: n_embd must be a multiple of 256 <= 8192");
+    WZY_REQUIRE(c.hc >= 1 && c.hc <= 4 && c.hc_lr % 32 == 0 && c.hc_lr <= 512 && c.hc * c.n_embd <= 16384,
+                "stage: bad hyper-connection shape");
+    WZY_REQUIRE(c.gdn_hk >= 1 && c.gdn_hv % c.gdn_hk == 0, "stage: bad GDN heads");
+    WZY_REQUIRE(c.qsa_hd == 256 && c.qsa_qh % c.qsa_kvh == 0 && c.qsa_qh / c.qsa_kvh <= 16, "stage: bad QSA heads");
+    WZY_REQUIRE(c.idx_dim <= 128 && c.idx_heads <= 4 && c.idx_blk >= 2 && c.idx_topk >= 1, "stage: bad indexer");
+    WZY_REQUIRE(c.n_exp >= 1 && c.n_exp <= 1024 && c.top_k >= 1 && c.top_k <= MOE_MAX_K && c.n_ff % 64 == 0,
+                "stage: bad MoE shape");
+    WZY_REQUIRE(c.n_vocab >= 16 && c.ctx_max >= 8, "stage: bad vocab / context");
+    WZY_REQUIRE(2 * c.qsa_qh * c.qsa_hd <= 16384 && c.n_embd * 1 <= 8192, "stage: projection too wide");
+    WZY_REQUIRE((c.n_vocab + 2047) / 2048 * 16 <= 2048, "stage: n_vocab too large for the top-16 merge");
+    return WZY_OK;
+}
+
+int wzy_stage::init_buffers() {
+    const wzy_stage_cfg& c = cfg;
+    D = c.n_embd;
+    HCD = c.hc * D;
+    QKV = 2 * c.gdn_hk * 128 + c.gdn_hv * 128;
+    GV = c.gdn_hv * 128;
+    QD = c.qsa_qh * c.qsa_hd;
+    KVD = c.qsa_kvh * c.qsa_hd;
+    max_b = c.ctx_max / c.idx_blk + 2;
+    qd.qh = c.qsa_qh; qd.kvh = c.qsa_kvh; qd.hd = c.qsa_hd; qd.n_rot = c.n_rot;
+    qd.ih = c.idx_heads; qd.idim = c.idx_dim; qd.iblk = c.idx_blk; qd.topk = c.idx_topk;
+    qd.ctx_max = c.ctx_max; qd.ring_cap = c.kv_ring; qd.sinks = c.kv_sinks; qd.eps = c.eps;
+    const size_t kv_slots = c.kv_ring > 0 ? (size_t) c.kv_ring : (size_t) c.ctx_max;
+    const int W = WZY_MAX_W;
+
+    L.resize(c.n_layers);
+    n_gdn = n_qsa = 0;
+    expert_rec = wzy_nvfp4_expert_bytes(D, c.n_ff);
+    WZY_TRY(alloc_t(&experts, expert_rec * c.n_exp * c.n_layers, false));
+    reg(-1, "experts", experts, expert_rec * c.n_exp * c.n_layers);
+    char nm[64];
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer& w = L[l];
+        w.qsa = (l % c.qsa_period) == c.qsa_period - 1;
+        w.local = w.qsa ? n_qsa++ : n_gdn++;
+        for (int h = 0; h < 2; ++h) {
+            snprintf(nm, sizeof nm, "hc_norm%d", h);
+            WZY_TRY(alloc_t(&w.hc_norm[h], HCD, false)); reg(l, nm, w.hc_norm[h], HCD * 4);
+            snprintf(nm, sizeof nm, "hc_down%d", h);
+            WZY_TRY(alloc_q8(w.hc_down[h], c.hc_lr, HCD, l, nm));
+            snprintf(nm, sizeof nm, "hc_up%d", h);
+            WZY_TRY(alloc_q8(w.hc_up[h], HCD, c.hc_lr, l, nm));
+            snprintf(nm, sizeof nm, "hc_inj%d", h);
+            WZY_TRY(alloc_t(&w.hc_inj[h], (size_t) c.hc * HCD, false)); reg(l, nm, w.hc_inj[h], (size_t) c.hc * HCD * 2);
+        }
+        if (!w.qsa) {
+            WZY_TRY(alloc_q8(w.qkv, QKV, D, l, "qkv"));
+            WZY_TRY(alloc_q8(w.wgate, GV, D, l, "wgate"));
+            WZY_TRY(alloc_q8(w.wout, D, GV, l, "wout"));
+            WZY_TRY(alloc_t(&w.alpha, (size_t) c.gdn_hv * D, false)); reg(l, "alpha", w.alpha, (size_t) c.gdn_hv * D * 2);
+            WZY_TRY(alloc_t(&w.beta, (size_t) c.gdn_hv * D, false)); reg(l, "beta", w.beta, (size_t) c.gdn_hv * D * 2);
+            WZY_TRY(alloc_t(&w.ssm_a, c.gdn_hv, false)); reg(l, "ssm_a", w.ssm_a, c.gdn_hv * 4);
+            WZY_TRY(alloc_t(&w.dt, c.gdn_hv, false)); reg(l, "dt_bias", w.dt, c.gdn_hv * 4);
+            WZY_TRY(alloc_t(&w.conv_w, (size_t) QKV * 4, false)); reg(l, "conv1d", w.conv_w, (size_t) QKV * 16);
+            WZY_TRY(alloc_t(&w.ssm_norm, 128, false)); reg(l, "ssm_norm", w.ssm_norm, 512);
+            WZY_TRY(alloc_t(&w.conv_hist, (size_t) QKV * 3)); reg(l, "conv_hist", w.conv_hist, (size_t) QKV * 12);
+            WZY_TRY(alloc_t(&w.ssm, (size_t) c.gdn_hv * 128 * 128)); reg(l, "ssm", w.ssm, (size_t) c.gdn_hv * 128 * 128 * 4);
+        } else {
+            WZY_TRY(alloc_q8(w.wq, 2 * QD, D, l, "wq"));
+            WZY_TRY(alloc_q8(w.wk, KVD, D, l, "wk"));
+            WZY_TRY(alloc_q8(w.wv, KVD, D, l, "wv"));
+            WZY_TRY(alloc_q8(w.wo, D, QD, l, "wo"));
+            WZY_TRY(alloc_t(&w.q_norm, c.qsa_hd, false)); reg(l, "q_norm", w.q_norm, c.qsa_hd * 4);
+            WZY_TRY(alloc_t(&w.k_norm, c.qsa_hd, false)); reg(l, "k_norm", w.k_norm, c.qsa_hd * 4);
+            WZY_TRY(alloc_t(&w.idx_q, (size_t) c.idx_heads * c.idx_dim * D, false));
+            reg(l, "idx_q", w.idx_q, (size_t) c.idx_heads * c.idx_dim * D * 2);
+            WZY_TRY(alloc_t(&w.idx_k, (size_t) c.idx_dim * D, false)); reg(l, "idx_k", w.idx_k, (size_t) c.idx_dim * D * 2);
+            WZY_TRY(alloc_t(&w.idx_qn, c.idx_dim, false)); reg(l, "idx_qn", w.idx_qn, c.idx_dim * 4);
+            WZY_TRY(alloc_t(&w.idx_kn, c.idx_dim, false)); reg(l, "idx_kn", w.idx_kn, c.idx_dim * 4);
+            WZY_TRY(alloc_t(&w.kv.kq, kv_slots * KVD)); reg(l, "kv_k", w.kv.kq, kv_slots * KVD);
+            WZY_TRY(alloc_t(&w.kv.ks, kv_slots * (KVD / 64))); reg(l, "kv_ks", w.kv.ks, kv_slots * (KVD / 64) * 2);
+            WZY_TRY(alloc_t(&w.kv.vq, kv_slots * KVD)); reg(l, "kv_v", w.kv.vq, kv_slots * KVD);
+            WZY_TRY(alloc_t(&w.kv.vs, kv_slots * (KVD / 64))); reg(l, "kv_vs", w.kv.vs, kv_slots * (KVD / 64) * 2);
+            WZY_TRY(alloc_t(&w.ix.tail, (size_t) (c.idx_blk - 1) * c.idx_dim));
+            reg(l, "idx_tail", w.ix.tail, (size_t) (c.idx_blk - 1) * c.idx_dim * 4);
+            WZY_TRY(alloc_t(&w.ix.dead, c.idx_dim)); reg(l, "idx_dead", w.ix.dead, c.idx_dim * 4);
+            WZY_TRY(alloc_t(&w.ix.pooled, (size_t) max_b * c.idx_dim));
+            reg(l, "idx_pooled", w.ix.pooled, (size_t) max_b * c.idx_dim * 2);
+        }
+        wzy_moe_weights& m = w.moe;
+        m.n_embd = D; m.n_ff = c.n_ff; m.n_exp = c.n_exp; m.top_k = c.top_k;
+        uint16_t* router = nullptr;
+        uint16_t* sgate = nullptr;
+        WZY_TRY(alloc_t(&router, (size_t) c.n_exp * D, false)); reg(l, "router", router, (size_t) c.n_exp * D * 2);
+        WZY_TRY(alloc_t(&sgate, D, false)); reg(l, "sgate", sgate, D * 2);
+        m.router = router; m.sgate = sgate;
+        Q8 g, u, dn;
+        WZY_TRY(alloc_q8(g, c.n_ff, D, l, "sh_gate"));
+        WZY_TRY(alloc_q8(u, c.n_ff, D, l, "sh_up"));
+        WZY_TRY(alloc_q8(dn, D, c.n_ff, l, "sh_down"));
+        m.sh_gate_q = g.q; m.sh_gate_s = g.s; m.sh_up_q = u.q; m.sh_up_s = u.s; m.sh_down_q = dn.q; m.sh_down_s = dn.s;
+        m.experts = experts + (size_t) l * c.n_exp * expert_rec;
+    }
+    WZY_TRY(alloc_t(&emb, (size_t) c.n_vocab * D, false)); reg(-1, "emb", emb, (size_t) c.n_vocab * D * 2);
+    WZY_TRY(alloc_t(&head_norm, HCD, false)); reg(-1, "head_norm", head_norm, HCD * 4);
+    WZY_TRY(alloc_q8(head_down, c.hc_lr, HCD, -1, "head_down"));
+    WZY_TRY(alloc_q8(head_up, HCD, c.hc_lr, -1, "head_up"));
+    WZY_TRY(alloc_t(&head, (size_t) c.n_vocab * D, false)); reg(-1, "head", head, (size_t) c.n_vocab * D * 2);
+
+    // RoPE tables: fp64 angles rounded to fp32 (src/wzy_qsa_256k.cuh:34-46)
+    {
+        const int half = c.n_rot / 2;
+        std::vector<float> hc((size_t) c.ctx_max * half), hs((size_t) c.ctx_max * half);
+        std::vector<double> inv(half);
+        for (int i = 0; i < half; ++i) inv[i] = pow((double) c.rope_theta, -2.0 * (double) i / (double) c.n_rot);
+        for (int p = 0; p < c.ctx_max; ++p)
+            for (int i = 0; i < half; ++i) {
+                const double ang = (double) p * inv[i];
+                hc[(size_t) p * half + i] = (float) cos(ang);
+                hs[(size_t) p * half + i] = (float) sin(ang);
+            }
+        WZY_TRY(alloc_t(&cos_tab, hc.size(), false));
+        WZY_TRY(alloc_t(&sin_tab, hs.size(), false));
+        WZY_HIP_TRY(hipMemcpy(cos_tab, hc.data(), hc.size() * 4, hipMemcpyHostToDevice));
+        WZY_HIP_TRY(hipMemcpy(sin_tab, hs.data(), hs.size() * 4, hipMemcpyHostToDevice));
+        reg(-1, "rope_cos", cos_tab, hc.size() * 4);
+        reg(-1, "rope_sin", sin_tab, hs.size() * 4);
+    }
+
+    // activations
+    WZY_TRY(alloc_t(&R[0], (size_t) W * HCD)); WZY_TRY(alloc_t(&R[1], (size_t) W * HCD));
+    WZY_TRY(alloc_t(&nsc, (size_t) W * c.hc));
+    WZY_TRY(alloc_t(&lo, (size_t) W * c.hc_lr));
+    WZY_TRY(alloc_t(&inj_a, (size_t) W * c.hc)); WZY_TRY(alloc_t(&inj_f, (size_t) W * c.hc));
+    WZY_TRY(alloc_t(&mixed, (size_t) W * D));
+    WZY_TRY(alloc_t(&qkv, (size_t) W * QKV)); WZY_TRY(alloc_t(&z, (size_t) W * GV));
+    WZY_TRY(alloc_t(&ab, (size_t) W * 2 * c.gdn_hv)); WZY_TRY(alloc_t(&y, (size_t) W * GV));
+    WZY_TRY(alloc_t(&block, (size_t) W * D)); WZY_TRY(alloc_t(&comb, (size_t) W * D));
+    WZY_TRY(alloc_t(&qg, (size_t) W * 2 * QD)); WZY_TRY(alloc_t(&kk, (size_t) W * KVD)); WZY_TRY(alloc_t(&vv, (size_t) W * KVD));
+    WZY_TRY(alloc_t(&idx_raw, (size_t) W * c.idx_dim)); WZY_TRY(alloc_t(&q_idx, (size_t) W * c.idx_heads * c.idx_dim));
+    WZY_TRY(alloc_t(&scores, (size_t) W * max_b));
+    WZY_TRY(alloc_t(&sel_ids, (size_t) W * c.idx_topk)); WZY_TRY(alloc_t(&sel_cnt, W));
+    const size_t pf = qsa_attn_part_floats(qd, W);
+    WZY_TRY(alloc_t(&att_part, pf)); WZY_TRY(alloc_t(&att_ml, pf / c.qsa_hd * 2));
+    WZY_TRY(alloc_t(&att_out, (size_t) W * QD));
+    size_t need = 0;
+    moe_ws_carve(nullptr, 0, D, c.n_ff, c.n_exp, c.top_k, W, &need);
+    WZY_TRY(alloc(&moe_ws, need + 256));
+    mws = moe_ws_carve(moe_ws, need + 256, D, c.n_ff, c.n_exp, c.top_k, W, nullptr);
+    WZY_TRY(alloc_t(&logits, (size_t) W * c.n_vocab));
+    WZY_TRY(alloc(&red_ws, reduce_ws_bytes(c.n_vocab, W)));
+    WZY_TRY(alloc_t(&emb_rows, (size_t) W * D));
+    // speculative-window snapshots
+    if (n_gdn > 0) {
+        WZY_TRY(alloc_t(&conv_snaps, (size_t) n_gdn * W * QKV * 3));
+        WZY_TRY(alloc_t(&ssm_snaps, (size_t) n_gdn * W * c.gdn_hv * 128 * 128));
+    }
+    if (n_qsa > 0) {
+        WZY_TRY(alloc_t(&tail_snaps, (size_t) n_qsa * W * (c.idx_blk - 1) * c.idx_dim));
+        WZY_TRY(alloc_t(&dead_snaps, (size_t) n_qsa * W * c.idx_dim));
+        WZY_TRY(alloc_t(&pool_snaps, (size_t) n_qsa * W * 2 * c.idx_dim));
+    }
+    WZY_TRY(alloc_t(&d_step, 16));
+    WZY_HIP_TRY(hipHostMalloc((void**) &h_step, 64, hipHostMallocDefault));
+    WZY_HIP_TRY(hipHostMalloc((void**) &h_greedy, W * sizeof(int), hipHostMallocMapped));
+    WZY_HIP_TRY(hipHostMalloc((void**) &h_top_v, W * 16 * sizeof(float), hipHostMallocMapped));
+    WZY_HIP_TRY(hipHostMalloc((void**) &h_top_i, W * 16 * sizeof(int), hipHostMallocMapped));
+    WZY_HIP_TRY(hipHostGetDevicePointer((void**) &d_greedy, h_greedy, 0));
+    WZY_HIP_TRY(hipHostGetDevicePointer((void**) &d_top_v, h_top_v, 0));
+    WZY_HIP_TRY(hipHostGetDevicePointer((void**) &d_top_i, h_top_i, 0));
+    memset(h_greedy, 0, W * sizeof(int));
+    for (auto& e : ev) WZY_HIP_TRY(hipEventCreate(&e));
+    return WZY_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// forward enqueue
+// ------------------------------------------------------------------------------------------------
+int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, bool want_top16, int snap_offset) {
+    const wzy_stage_cfg& c = cfg;
+    hipStream_t st = stream;
+    const int* d_pos = d_step;
+    const int* d_toks = d_step + 1;
+    int cur = 0;                    // R buffer holding the current residual
+    const float* pend_bo = nullptr;
+    const float* pend_inj = nullptr;
+
+    auto hc_read = [&](const float* norm_w, const Q8& down, const uint16_t* inj_w, const Q8& up, float* inj_out,
+                       bool first) -> int {
+        HcPreArgs a{};
+        if (first) {
+            if (emb_host) a.emb_rows = emb_rows;
+            else { a.emb_table = emb; a.toks = d_toks; a.n_vocab = c.n_vocab; }
+        } else {
+            a.R_in = R[cur];
+        }
+        a.bo = pend_bo; a.inj_prev = pend_inj;
+        a.R_out = R[cur ^ 1];
+        a.norm_w = norm_w; a.down_q = down.q; a.down_s = down.s; a.inj_w = inj_w;
+        a.nsc = nsc; a.lo = lo; a.inj = inj_out;
+        a.D = D; a.HC = c.hc; a.HCLR = c.hc_lr; a.eps = c.eps;
+        WZY_TRY(launch_hc_pre(a, T, st));
+        cur ^= 1;
+        HcPostArgs b{};
+        b.R = R[cur]; b.nsc = nsc; b.norm_w = norm_w; b.up_q = up.q; b.up_s = up.s; b.lo = lo; b.mixed = mixed;
+        b.D = D; b.HC = c.hc; b.HCLR = c.hc_lr;
+        return launch_hc_post(b, T, st);
+    };
+
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer& w = L[l];
+        // ---------------- attention half ----------------
+        WZY_TRY(hc_read(w.hc_norm[0], w.hc_down[0], w.hc_inj[0], w.hc_up[0], inj_a, l == 0));
+        if (!w.qsa) {
+            GemvSegs s;
+            s.n = 4;
+            s.seg[0] = GemvSeg{w.qkv.q, w.qkv.s, qkv, QKV, GEMV_Q8, QKV, 0};
+            s.seg[1] = GemvSeg{w.wgate.q, w.wgate.s, z, GV, GEMV_Q8, GV, 0};
+            s.seg[2] = GemvSeg{w.alpha, nullptr, ab, c.gdn_hv, GEMV_BF16, 2 * c.gdn_hv, 0};
+            s.seg[3] = GemvSeg{w.beta, nullptr, ab + c.gdn_hv, c.gdn_hv, GEMV_BF16, 2 * c.gdn_hv, 0};
+            WZY_TRY(launch_gemv_segs(s, mixed, D, T, st));
+            GdnArgs g{};
+            g.qkv = qkv; g.ab = ab; g.dt = w.dt; g.ssm_a = w.ssm_a; g.conv_w = w.conv_w; g.conv_hist = w.conv_hist;
+            g.z = z; g.gamma = w.ssm_norm; g.eps = c.eps; g.state = w.ssm; g.y = y;
+            g.hk = c.gdn_hk; g.hv = c.gdn_hv; g.S = 128; g.T = T;
+            if (save_snaps) {
+                g.hist_snaps = conv_snaps + ((size_t) w.local * WZY_MAX_W + snap_offset) * QKV * 3;
+                g.state_snaps = ssm_snaps + ((size_t) w.local * WZY_MAX_W + snap_offset) * c.gdn_hv * 128 * 128;
+            }
+            WZY_TRY(launch_gdn(g, true, st));
+            GemvSegs o;
+            o.n = 1;
+            o.seg[0] = GemvSeg{w.wout.q, w.wout.s, block, D, GEMV_Q8, D, 0};
+            WZY_TRY(launch_gemv_segs(o, y, GV, T, st));
+        } else {
+            GemvSegs s;
+            s.n = 5;
+            s.seg[0] = GemvSeg{w.wq.q, w.wq.s, qg, 2 * QD, GEMV_Q8, 2 * QD, 0};
+            s.seg[1] = GemvSeg{w.wk.q, w.wk.s, kk, KVD, GEMV_Q8, KVD, 0};
+            s.seg[2] = GemvSeg{w.wv.q, w.wv.s, vv, KVD, GEMV_Q8, KVD, 0};
+            s.seg[3] = GemvSeg{w.idx_k, nullptr, idx_raw, c.idx_dim, GEMV_BF16, c.idx_dim, 0};
+            s.seg[4] = GemvSeg{w.idx_q, nullptr, q_idx, c.idx_heads * c.idx_dim, GEMV_BF16, c.idx_heads * c.idx_dim, 0};
+            WZY_TRY(launch_gemv_segs(s, mixed, D, T, st));
+            QsaPrepArgs p{};
+            p.dm = qd; p.pos = d_pos; p.qg = qg; p.kk = kk; p.vv = vv; p.q_idx = q_idx; p.idx_raw = idx_raw;
+            p.q_norm = w.q_norm; p.k_norm = w.k_norm; p.iq_norm = w.idx_qn; p.ik_norm = w.idx_kn;
+            p.cos_tab = cos_tab; p.sin_tab = sin_tab; p.kv = w.kv; p.ix = w.ix;
+            if (save_snaps) {
+                const size_t sl = (size_t) w.local * WZY_MAX_W + snap_offset;
+                p.ix.tail_snaps = tail_snaps + sl * (c.idx_blk - 1) * c.idx_dim;
+                p.ix.dead_snaps = dead_snaps + sl * c.idx_dim;
+                p.ix.pool_snaps = pool_snaps + sl * 2 * c.idx_dim;
+            }
+            WZY_TRY(launch_qsa_prep(p, T, st));
+            QsaScoreArgs sa{};
+            sa.dm = qd; sa.pos = d_pos; sa.pooled = w.ix.pooled; sa.dead = w.ix.dead; sa.q_idx = q_idx;
+            sa.scores = scores; sa.max_b = max_b;
+            WZY_TRY(launch_qsa_score(sa, T, st));
+            WZY_TRY(launch_qsa_topk(qd, d_pos, scores, max_b, sel_ids, sel_cnt, T, st));
+            QsaAttnArgs at{};
+            at.dm = qd; at.pos = d_pos; at.qg = qg; at.kv = w.kv; at.sel_ids = sel_ids; at.part = att_part;
+            at.part_ml = att_ml; at.out = att_out;
+            WZY_TRY(launch_qsa_attn(at, T, st));
+            GemvSegs o;
+            o.n = 1;
+            o.seg[0] = GemvSeg{w.wo.q, w.wo.s, block, D, GEMV_Q8, D, 0};
+            WZY_TRY(launch_gemv_segs(o, att_out, QD, T, st));
+        }
+        pend_bo = block;
+        pend_inj = inj_a;
+        // ---------------- FFN half ----------------
+        WZY_TRY(hc_read(w.hc_norm[1], w.hc_down[1], w.hc_inj[1], w.hc_up[1], inj_f, false));
+        WZY_TRY(moe_launch_route(&w.moe, mws, mixed, T, st));
+        WZY_TRY(moe_launch_experts(&w.moe, mws, mixed, T, comb, st));
+        pend_bo = comb;
+        pend_inj = inj_f;
+    }
+    if (run_head) {
+        WZY_TRY(hc_read(head_norm, head_down, nullptr, head_up, nullptr, false));
+        r_pre_head = cur;
+        GemvSegs h;
+        h.n = 1;
+        h.seg[0] = GemvSeg{head, nullptr, logits, c.n_vocab, GEMV_BF16, c.n_vocab, 0};
+        WZY_TRY(launch_gemv_segs(h, mixed, D, T, st));
+        WZY_TRY(launch_row_reduce(logits, c.n_vocab, T, want_top16, d_greedy, want_top16 ? d_top_v : nullptr,
+                                  want_top16 ? d_top_i : nullptr, red_ws, st));
+    }
+    return WZY_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// synthetic model
+// ------------------------------------------------------------------------------------------------
+namespace {
+struct Gen {
+    wzy_stage* s;
+    uint64_t seed;
+    std::vector<char> buf;
+    int upload(void* dst, const void* src, size_t bytes) {
+        WZY_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+        return WZY_OK;
+    }
+    uint64_t stream(uint32_t kind, int layer, uint32_t sub) {
+        return wzy_stream(kind, layer < 0 ? MODEL_LAYER : (uint32_t) layer, sub);
+    }
+    int normal_f32(float* dst, size_t n, int layer, uint32_t id, float mean, float sd, uint32_t kind = WZY_S_DENSE) {
+        buf.resize(n * 4);
+        wzy_synth_normal(seed, stream(kind, layer, id), n, mean, sd, (float*) buf.data());
+        return upload(dst, buf.data(), n * 4);
+    }
+    int uniform_f32(float* dst, size_t n, int layer, uint32_t id, float lo, float hi) {
+        buf.resize(n * 4);
+        wzy_synth_uniform(seed, stream(WZY_S_DENSE, layer, id), n, lo, hi, (float*) buf.data());
+        return upload(dst, buf.data(), n * 4);
+    }
+    int normal_bf16(uint16_t* dst, size_t n, int layer, uint32_t id, float sd) {
+        buf.resize(n * 2);
+        wzy_synth_normal_bf16(seed, stream(WZY_S_DENSE, layer, id), n, 0.f, sd, (uint16_t*) buf.data());
+        return upload(dst, buf.data(), n * 2);
+    }
+    int q8(const Q8& m, int layer, uint32_t id) {
+        const size_t n = (size_t) m.rows * m.cols;
+        buf.resize(n + n / 32 * 2);
+        wzy_synth_q8(seed, stream(WZY_S_DENSE, layer, id), m.rows, m.cols, (float) (1.0 / sqrt((double) m.cols)),
+                     (int8_t*) buf.data(), (uint16_t*) (buf.data() + n));
+        WZY_TRY(upload(m.q, buf.data(), n));
+        return upload(m.s, buf.data() + n, n / 32 * 2);
+    }
+};
+}  // namespace
+
+static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
+    const wzy_stage_cfg& c = s->cfg;
+    WZY_REQUIRE(n_ctx >= 0 && n_ctx < c.ctx_max, "load_synthetic: n_ctx must be in [0, ctx_max)");
+    WZY_HIP_TRY(hipSetDevice(s->dev));
+    Gen g{s, seed, {}};
+    const int D = s->D;
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer& w = s->L[l];
+        for (int h = 0; h < 2; ++h) {
+            WZY_TRY(g.normal_f32(w.hc_norm[h], s->HCD, l, TI_HC_NORM + 10 * h, 1.0f, 0.02f));
+            WZY_TRY(g.q8(w.hc_down[h], l, TI_HC_DOWN + 10 * h));
+            WZY_TRY(g.q8(w.hc_up[h], l, TI_HC_UP + 10 * h));
+            WZY_TRY(g.normal_bf16(w.hc_inj[h], (size_t) c.hc * s->HCD, l, TI_HC_INJ + 10 * h,
+                                  (float) (1.0 / sqrt((double) s->HCD))));
+        }
+        if (!w.qsa) {
+            WZY_TRY(g.q8(w.qkv, l, TI_QKV));
+            WZY_TRY(g.q8(w.wgate, l, TI_WGATE));
+            WZY_TRY(g.q8(w.wout, l, TI_WOUT));
+            WZY_TRY(g.normal_bf16(w.alpha, (size_t) c.gdn_hv * D, l, TI_ALPHA, (float) (1.0 / sqrt((double) D))));
+            WZY_TRY(g.normal_bf16(w.beta, (size_t) c.gdn_hv * D, l, TI_BETA, (float) (1.0 / sqrt((double) D))));
+            WZY_TRY(g.uniform_f32(w.ssm_a, c.gdn_hv, l, TI_SSM_A, -2.0f, -1.0f));
+            WZY_TRY(g.normal_f32(w.dt, c.gdn_hv, l, TI_DT, -3.0f, 0.5f));
+            WZY_TRY(g.normal_f32(w.conv_w, (size_t) s->QKV * 4, l, TI_CONV, 0.0f, 0.5f));
+            WZY_TRY(g.normal_f32(w.ssm_norm, 128, l, TI_SSM_NORM, 1.0f, 0.02f));
+            // prefilled recurrent state
+            WZY_TRY(g.normal_f32(w.conv_hist, (size_t) s->QKV * 3, l, TS_CONV, 0.0f, 1.0f, WZY_S_STATE));
+            WZY_TRY(g.normal_f32(w.ssm, (size_t) c.gdn_hv * 128 * 128, l, TS_SSM, 0.0f, 0.1f, WZY_S_STATE));
+        } else {
+            WZY_TRY(g.q8(w.wq, l, TI_WQ));
+            WZY_TRY(g.q8(w.wk, l, TI_WK));
+            WZY_TRY(g.q8(w.wv, l, TI_WV));
+            WZY_TRY(g.q8(w.wo, l, TI_WO));
+            WZY_TRY(g.normal_f32(w.q_norm, c.qsa_hd, l, TI_QNORM, 1.0f, 0.02f));
+            WZY_TRY(g.normal_f32(w.k_norm, c.qsa_hd, l, TI_KNORM, 1.0f, 0.02f));
+            WZY_TRY(g.normal_bf16(w.idx_q, (size_t) c.idx_heads * c.idx_dim * D, l, TI_IDXQ, (float) (1.0 / sqrt((double) D))));
+            WZY_TRY(g.normal_bf16(w.idx_k, (size_t) c.idx_dim * D, l, TI_IDXK, (float) (1.0 / sqrt((double) D))));
+            WZY_TRY(g.normal_f32(w.idx_qn, c.idx_dim, l, TI_IDXQN, 1.0f, 0.02f));
+            WZY_TRY(g.normal_f32(w.idx_kn, c.idx_dim, l, TI_IDXKN, 1.0f, 0.02f));
+            // prefilled context: INT8 KV cells 0..n_ctx-1, indexer keys of complete blocks,
+            // placeholder key, partial-block tail
+            if (n_ctx > 0) {
+                const int slots = c.kv_ring > 0 ? std::min(n_ctx, c.kv_ring) : n_ctx;
+                if (c.kv_ring > 0 && n_ctx > c.kv_ring) {
+                    set_error("load_synthetic: a prefilled context larger than the KV ring is not supported");
+                    return WZY_EINVAL;
+                }
+                WZY_TRY(wzy_synth_kv_device(seed, l, 0, 0, slots, s->KVD, w.kv.kq, w.kv.ks, s->stream));
+                WZY_TRY(wzy_synth_kv_device(seed, l, 1, 0, slots, s->KVD, w.kv.vq, w.kv.vs, s->stream));
+            }
+            const int nblk = n_ctx / c.idx_blk;
+            std::vector<float> keys((size_t) (nblk + 1) * c.idx_dim);
+            wzy_synth_normal(seed, g.stream(WZY_S_STATE, l, TS_POOLED), keys.size(), 0.0f, 1.0f, keys.data());
+            std::vector<uint16_t> k16((size_t) s->max_b * c.idx_dim, 0);
+            for (size_t i = 0; i < keys.size(); ++i) k16[i] = wzy_f32_to_f16(keys[i]);
+            WZY_TRY(g.normal_f32(w.ix.dead, c.idx_dim, l, TS_DEAD, 0.0f, 1.0f, WZY_S_STATE));
+            std::vector<float> dead(c.idx_dim);
+            WZY_HIP_TRY(hipMemcpy(dead.data(), w.ix.dead, c.idx_dim * 4, hipMemcpyDeviceToHost));
+            if (n_ctx > 0)
+                for (int d = 0; d < c.idx_dim; ++d) k16[(size_t) nblk * c.idx_dim + d] = wzy_f32_to_f16(dead[d]);
+            WZY_TRY(g.upload(w.ix.pooled, k16.data(), k16.size() * 2));
+            WZY_TRY(g.normal_f32(w.ix.tail, (size_t) (c.idx_blk - 1) * c.idx_dim, l, TS_TAIL, 0.0f, 1.0f, WZY_S_STATE));
+        }
+        WZY_TRY(g.normal_bf16((uint16_t*) w.moe.router, (size_t) c.n_exp * D, l, TI_ROUTER, 0.02f));
+        WZY_TRY(g.normal_bf16((uint16_t*) w.moe.sgate, D, l, TI_SGATE, 0.02f));
+        Q8 m;
+        m.rows = c.n_ff; m.cols = D;
+        m.q = (int8_t*) w.moe.sh_gate_q; m.s = (uint16_t*) w.moe.sh_gate_s;
+        WZY_TRY(g.q8(m, l, TI_SH_GATE));
+        m.q = (int8_t*) w.moe.sh_up_q; m.s = (uint16_t*) w.moe.sh_up_s;
+        WZY_TRY(g.q8(m, l, TI_SH_UP));
+        m.rows = D; m.cols = c.n_ff;
+        m.q = (int8_t*) w.moe.sh_down_q; m.s = (uint16_t*) w.moe.sh_down_s;
+        WZY_TRY(g.q8(m, l, TI_SH_DOWN));
+        for (int e0 = 0; e0 < c.n_exp; e0 += 4096) {
+            const int ne = std::min(4096, c.n_exp - e0);
+            WZY_TRY(wzy_synth_experts_device(seed, l, e0, ne, D, c.n_ff, (uint8_t*) w.moe.experts + (size_t) e0 * s->expert_rec,
+                                             s->stream));
+        }
+    }
+    WZY_TRY(g.normal_bf16(s->emb, (size_t) c.n_vocab * D, -1, TI_EMB, 1.0f));
+    WZY_TRY(g.normal_f32(s->head_norm, s->HCD, -1, TI_HEAD_NORM, 1.0f, 0.02f));
+    WZY_TRY(g.q8(s->head_down, -1, TI_HEAD_DOWN));
+    WZY_TRY(g.q8(s->head_up, -1, TI_HEAD_UP));
+    WZY_TRY(g.normal_bf16(s->head, (size_t) c.n_vocab * D, -1, TI_HEAD, (float) (1.0 / sqrt((double) D))));
+    WZY_HIP_TRY(hipStreamSynchronize(s->stream));
+    s->loaded = true;
+    return WZY_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// C ABI
+// ------------------------------------------------------------------------------------------------
+extern "C" void wzy_stage_cfg_default(wzy_stage_cfg* c, int ctx_max) {
+    memset(c, 0, sizeof *c);
+    c->n_layers = 48; c->qsa_period = 4; c->n_embd = 2048; c->hc = 4; c->hc_lr = 320;
+    c->gdn_hk = 16; c->gdn_hv = 16; c->qsa_qh = 24; c->qsa_kvh = 2; c->qsa_hd = 256; c->n_rot = 64;
+    c->idx_heads = 4; c->idx_dim = 128; c->idx_blk = 4; c->idx_topk = 2048;
+    c->n_exp = 512; c->top_k = 10; c->n_ff = 512; c->n_vocab = 151936;
+    c->ctx_max = ctx_max; c->kv_ring = 0; c->kv_sinks = 0; c->rope_theta = 1e7f; c->eps = 1e-6f;
+}
+
+extern "C" int wzy_stage_create(const wzy_stage_cfg* cfg, int device, wzy_stage** out) {
+    WZY_REQUIRE(cfg && out, "wzy_stage_create: null argument");
+    *out = nullptr;
+    WZY_TRY(validate(*cfg));
+    WZY_HIP_TRY(hipSetDevice(device));
+    std::unique_ptr<wzy_stage> s(new wzy_stage());
+    s->cfg = *cfg;
+    s->dev = device;
+    WZY_HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    WZY_TRY(s->init_buffers());
+    *out = s.release();
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_destroy(wzy_stage* st) {
+    delete st;
+    return WZY_OK;
+}
+
+extern "C" size_t wzy_stage_device_bytes(const wzy_stage* st) { return st ? st->dev_bytes : 0; }
+
+extern "C" int wzy_stage_load_synthetic(wzy_stage* st, uint64_t seed, int n_ctx) {
+    WZY_REQUIRE(st, "wzy_stage_load_synthetic: null stage");
+    return load_synthetic(st, seed, n_ctx);
+}
+
+extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb, const int* toks, int T, int run_head,
+                                        int save_snaps, int want_top16, int snap_offset) {
+    WZY_REQUIRE(st && st->loaded, "record_forward: stage not loaded");
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "record_forward: T must be in [1, %d]", WZY_MAX_W);
+    WZY_REQUIRE(emb || toks, "record_forward: need token ids or embedding rows");
+    WZY_REQUIRE(pos >= 0 && pos + T <= st->cfg.ctx_max, "record_forward: positions [%d, %d) exceed ctx_max %d", pos,
+                pos + T, st->cfg.ctx_max);
+    WZY_REQUIRE(!save_snaps || (snap_offset >= 0 && snap_offset + T <= WZY_MAX_W), "record_forward: bad snap_offset");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    st->h_step[0] = pos;
+    for (int t = 0; t < T; ++t) st->h_step[1 + t] = toks ? toks[t] : 0;
+    WZY_HIP_TRY(hipMemcpyAsync(st->d_step, st->h_step, (1 + WZY_MAX_W) * sizeof(int), hipMemcpyHostToDevice, st->stream));
+    if (emb) WZY_HIP_TRY(hipMemcpyAsync(st->emb_rows, emb, (size_t) T * st->D * 4, hipMemcpyHostToDevice, st->stream));
+    st->last_T = T;
+    st->have_head = run_head != 0;
+    const bool use_graph = st->graphs && !st->profiling;
+    if (!use_graph) return st->enqueue(T, emb != nullptr, run_head, save_snaps, want_top16, snap_offset);
+    const unsigned long long key = ((unsigned long long) T << 16) | ((unsigned long long) snap_offset << 8) |
+                                   (emb ? 16ull : 0ull) | (run_head ? 4ull : 0ull) | (want_top16 ? 2ull : 0ull) |
+                                   (save_snaps ? 1ull : 0ull);
+    auto it = st->graph_execs.find(key);
+    if (it == st->graph_execs.end()) {
+        WZY_HIP_TRY(hipStreamBeginCapture(st->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = st->enqueue(T, emb != nullptr, run_head, save_snaps, want_top16, snap_offset);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(st->stream, &g);
+        if (rc != WZY_OK) {
+            if (g) (void) hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) {
+            set_error("record_forward: graph capture failed: %s", hipGetErrorString(e));
+            return WZY_EHIP;
+        }
+        hipGraphExec_t ex = nullptr;
+        const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        (void) hipGraphDestroy(g);
+        if (ie != hipSuccess) {
+            set_error("record_forward: graph instantiate failed: %s", hipGetErrorString(ie));
+            return WZY_EHIP;
+        }
+        it = st->graph_execs.emplace(key, ex).first;
+    }
+    WZY_HIP_TRY(hipGraphLaunch(it->second, st->stream));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_service_cold_layers(wzy_stage* st) { return st ? WZY_OK : WZY_EINVAL; }
+extern "C" int wzy_stage_promote_cold(wzy_stage* st) { return st ? WZY_OK : WZY_EINVAL; }
+
+extern "C" int wzy_stage_commit_window_state(wzy_stage* st, int acc_idx, int acc_pos) {
+    WZY_REQUIRE(st && acc_idx >= 0 && acc_idx < WZY_MAX_W, "commit_window_state: bad arguments");
+    const wzy_stage_cfg& c = st->cfg;
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    for (Layer& w : st->L) {
+        if (!w.qsa) {
+            const size_t sl = (size_t) w.local * WZY_MAX_W + acc_idx;
+            WZY_HIP_TRY(hipMemcpyAsync(w.conv_hist, st->conv_snaps + sl * st->QKV * 3, (size_t) st->QKV * 12,
+                                       hipMemcpyDeviceToDevice, st->stream));
+            WZY_HIP_TRY(hipMemcpyAsync(w.ssm, st->ssm_snaps + sl * c.gdn_hv * 128 * 128, (size_t) c.gdn_hv * 128 * 128 * 4,
+                                       hipMemcpyDeviceToDevice, st->stream));
+        } else if (acc_pos >= 0) {
+            const size_t sl = (size_t) w.local * WZY_MAX_W + acc_idx;
+            WZY_HIP_TRY(hipMemcpyAsync(w.ix.tail, st->tail_snaps + sl * (c.idx_blk - 1) * c.idx_dim,
+                                       (size_t) (c.idx_blk - 1) * c.idx_dim * 4, hipMemcpyDeviceToDevice, st->stream));
+            WZY_HIP_TRY(hipMemcpyAsync(w.ix.dead, st->dead_snaps + sl * c.idx_dim, (size_t) c.idx_dim * 4,
+                                       hipMemcpyDeviceToDevice, st->stream));
+            const int b = acc_pos / c.idx_blk;
+            WZY_HIP_TRY(hipMemcpyAsync(w.ix.pooled + (size_t) b * c.idx_dim, st->pool_snaps + sl * 2 * c.idx_dim,
+                                       (size_t) 2 * c.idx_dim * 2, hipMemcpyDeviceToDevice, st->stream));
+        }
+    }
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_reset_state(wzy_stage* st) {
+    WZY_REQUIRE(st, "reset_state: null stage");
+    const wzy_stage_cfg& c = st->cfg;
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    for (Layer& w : st->L) {
+        if (!w.qsa) {
+            WZY_HIP_TRY(hipMemsetAsync(w.conv_hist, 0, (size_t) st->QKV * 12, st->stream));
+            WZY_HIP_TRY(hipMemsetAsync(w.ssm, 0, (size_t) c.gdn_hv * 128 * 128 * 4, st->stream));
+        } else {
+            WZY_HIP_TRY(hipMemsetAsync(w.ix.tail, 0, (size_t) (c.idx_blk - 1) * c.idx_dim * 4, st->stream));
+            WZY_HIP_TRY(hipMemsetAsync(w.ix.dead, 0, (size_t) c.idx_dim * 4, st->stream));
+        }
+    }
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_sync(wzy_stage* st) {
+    WZY_REQUIRE(st, "sync: null stage");
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_greedy_ids(wzy_stage* st, int* out, int T) {
+    WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_head, "greedy_ids: no head output for %d rows", T);
+    memcpy(out, st->h_greedy, T * sizeof(int));
+    return WZY_OK;
+}
+extern "C" int wzy_stage_top16(wzy_stage* st, float* v, int* ids, int T) {
+    WZY_REQUIRE(st && v && ids && T >= 1 && T <= st->last_T && st->have_head, "top16: no head output");
+    memcpy(v, st->h_top_v, (size_t) T * 16 * sizeof(float));
+    memcpy(ids, st->h_top_i, (size_t) T * 16 * sizeof(int));
+    return WZY_OK;
+}
+extern "C" int wzy_stage_logits(wzy_stage* st, float* out, int T) {
+    WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_head, "logits: no head output");
+    WZY_HIP_TRY(hipMemcpy(out, st->logits, (size_t) T * st->cfg.n_vocab * 4, hipMemcpyDeviceToHost));
+    return WZY_OK;
+}
+extern "C" int wzy_stage_pre_head(wzy_stage* st, float* out, int T) {
+    WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_head, "pre_head: no head output");
+    WZY_HIP_TRY(hipMemcpy(out, st->R[st->r_pre_head], (size_t) T * st->HCD * 4, hipMemcpyDeviceToHost));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_set_graphs(wzy_stage* st, int enable) {
+    WZY_REQUIRE(st, "set_graphs: null stage");
+    st->graphs = enable != 0;
+    return WZY_OK;
+}
+extern "C" void* wzy_stage_stream(wzy_stage* st) { return st ? (void*) st->stream : nullptr; }
+
+static Tensor* find_tensor(wzy_stage* st, int layer, const char* name) {
+    auto it = st->tensors.find({layer, std::string(name)});
+    return it == st->tensors.end() ? nullptr : &it->second;
+}
+extern "C" size_t wzy_stage_tensor_bytes(wzy_stage* st, int layer, const char* name) {
+    if (!st || !name) return 0;
+    Tensor* t = find_tensor(st, layer, name);
+    return t ? t->bytes : 0;
+}
+extern "C" int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name, void* host, size_t bytes) {
+    WZY_REQUIRE(st && name && host, "read_tensor: null argument");
+    Tensor* t = find_tensor(st, layer, name);
+    WZY_REQUIRE(t, "read_tensor: no tensor %s in layer %d", name, layer);
+    WZY_REQUIRE(bytes <= t->bytes, "read_tensor: %zu bytes requested, tensor has %zu", bytes, t->bytes);
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    WZY_HIP_TRY(hipMemcpy(host, t->p, bytes, hipMemcpyDeviceToHost));
+    return WZY_OK;
+}
+extern "C" int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes) {
+    WZY_REQUIRE(st && name && host, "write_tensor: null argument");
+    Tensor* t = find_tensor(st, layer, name);
+    WZY_REQUIRE(t, "write_tensor: no tensor %s in layer %d", name, layer);
+    WZY_REQUIRE(bytes <= t->bytes, "write_tensor: %zu bytes given, tensor has %zu", bytes, t->bytes);
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    WZY_HIP_TRY(hipMemcpy(t->p, host, bytes, hipMemcpyHostToDevice));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down) {
+    WZY_REQUIRE(st && st->loaded && iters >= 1 && us_gate_up && us_down, "time_moe: bad arguments");
+    const int T = st->last_T > 0 ? st->last_T : 1;
+    std::vector<wzy_moe_weights> ws;
+    for (Layer& w : st->L) ws.push_back(w.moe);
+    size_t need = 0;
+    moe_ws_carve(nullptr, 0, st->D, st->cfg.n_ff, st->cfg.n_exp, st->cfg.top_k, WZY_MAX_W, &need);
+    return wzy_moe_time_kernels(ws.data(), (int) ws.size(), T, st->mixed, st->moe_ws, need + 256, iters, us_gate_up,
+                                us_down, st->stream);
+}

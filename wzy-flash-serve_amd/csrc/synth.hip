@@ -67,6 +67,16 @@ static inline double normal_at(uint64_t seed, uint64_t stream, uint64_t i) {
     return (i & 1) ? r * sin(a) : r * cos(a);
 }
 
+// Box-Muller pair (z0, z1) for elements 2p, 2p+1
+static inline void normal_pair(uint64_t seed, uint64_t stream, uint64_t p, double& z0, double& z1) {
+    const double u1 = 1.0 - (double) (wzy_hash3(seed, stream, 2 * p) >> 11) * (1.0 / 9007199254740992.0);
+    const double u2 = (double) (wzy_hash3(seed, stream, 2 * p + 1) >> 11) * (1.0 / 9007199254740992.0);
+    const double r = sqrt(-2.0 * log(u1));
+    const double a = 6.283185307179586476925286766559 * u2;
+    z0 = r * cos(a);
+    z1 = r * sin(a);
+}
+
 extern "C" void wzy_synth_normal(uint64_t seed, uint64_t stream, size_t n, float mean, float std, float* out) {
     parallel_for(n, [&](size_t b, size_t e) {
         for (size_t i = b; i < e; ++i) out[i] = (float) ((double) mean + (double) std * normal_at(seed, stream, i));
@@ -93,10 +103,12 @@ extern "C" void wzy_synth_q8(uint64_t seed, uint64_t stream, int rows, int cols,
         for (size_t blk = b; blk < e; ++blk) {
             float v[32];
             float amax = 0.f;
-            for (int i = 0; i < 32; ++i) {
-                const uint64_t idx = blk * 32 + (uint64_t) i;
-                v[i] = bf16f(wzy_f32_to_bf16((float) ((double) std * normal_at(seed, stream, idx))));
-                amax = fmaxf(amax, fabsf(v[i]));
+            for (int i = 0; i < 32; i += 2) {
+                double z0, z1;
+                normal_pair(seed, stream, (blk * 32 + (uint64_t) i) >> 1, z0, z1);
+                v[i] = bf16f(wzy_f32_to_bf16((float) ((double) std * z0)));
+                v[i + 1] = bf16f(wzy_f32_to_bf16((float) ((double) std * z1)));
+                amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
             }
             const uint16_t sh = wzy_f32_to_f16(amax / 127.0f);
             const float d = wzy_f16_to_f32(sh);

@@ -11,3 +11,25 @@ int launch_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq
 int launch_gemv_bf16(const uint16_t* W, const float* x, float* y, int rows, int cols, int T, int y_stride,
                      const uint16_t* Wx, float* yx, hipStream_t st);
 }  // namespace wzy
+
+namespace wzy {
+// One weight matrix of a multi-segment GEMV launch.
+struct GemvSeg {
+    const void* w;          // Q8_0 codes (int8) or bf16 weights, [rows x cols]
+    const uint16_t* s;      // Q8_0 fp16 scales [rows x cols/32]; null for bf16
+    float* y;               // out: y[t*y_stride + r]
+    int rows;
+    int kind;               // GEMV_Q8 or GEMV_BF16
+    int y_stride;
+    int wave0;              // first wave of this segment (filled by launch_gemv_segs)
+};
+enum { GEMV_Q8 = 0, GEMV_BF16 = 1 };
+constexpr int GEMV_MAX_SEGS = 8;
+struct GemvSegs {
+    GemvSeg seg[GEMV_MAX_SEGS];
+    int n = 0;
+};
+// y_seg = W_seg . x for every segment; x fp32 [T x cols] is quantised per 32 inside each lane for
+// Q8_0 segments (bit-identical to quant_act + gemv_q8).  cols % 32 == 0, cols <= 8192.
+int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t st);
+}  // namespace wzy

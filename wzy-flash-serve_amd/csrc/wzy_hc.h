@@ -1,0 +1,42 @@
+// wzy_hc.h -- internal launchers of the hyper-connection read (hc_pre + hc_post).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wzy {
+
+struct HcPreArgs {
+    const float* R_in;          // [T][HC][D] residual streams, or null in embedding mode
+    const uint16_t* emb_table;  // bf16 [n_vocab][D]: layer-0 input broadcast to every stream
+    const int* toks;            // device [T] token ids (embedding mode)
+    int n_vocab;
+    const float* emb_rows;      // fp32 [T][D] rows broadcast to every stream (alternative input)
+    const float* bo;            // pending write: block output [T][D] (nullable)
+    const float* inj_prev;      // pending write gates [T][HC]
+    float* R_out;               // [T][HC][D] = R_in + bo * 2*sigmoid(inj_prev/HC)
+    const float* norm_w;        // [HC][D]
+    const int8_t* down_q;       // Q8_0 [HCLR][HC*D]
+    const uint16_t* down_s;
+    const uint16_t* inj_w;      // bf16 [HC][HC*D] (nullable: the head has no inject)
+    float* nsc;                 // [T][HC] rsqrt(mean(R_out^2) + eps)
+    float* lo;                  // [T][HCLR] silu(down . xn / HC)
+    float* inj;                 // [T][HC]
+    int D, HC, HCLR;
+    float eps;
+};
+
+struct HcPostArgs {
+    const float* R;             // R_out of hc_pre
+    const float* nsc;
+    const float* norm_w;
+    const int8_t* up_q;         // Q8_0 [HC*D][HCLR]
+    const uint16_t* up_s;
+    const float* lo;            // [T][HCLR]
+    float* mixed;               // [T][D]
+    int D, HC, HCLR;
+};
+
+int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st);
+int launch_hc_post(const HcPostArgs& a, int T, hipStream_t st);
+
+}  // namespace wzy

@@ -1,0 +1,74 @@
+// wzy_qsa.h -- internal interface of the QSA (sparse attention) decode kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wzy {
+
+constexpr int QSA_ATT_CHUNK = 64;      // selected cells per attention workgroup
+
+struct QsaDims {
+    int qh, kvh, hd, n_rot;            // 24, 2, 256, 64
+    int ih, idim, iblk, topk;          // indexer heads/dim (4, 128), block (4), top-k cells (2048)
+    int ctx_max;                       // capacity of the KV store / indexer
+    int ring_cap, sinks;               // 0 = full-context store addressed by position
+    float eps;
+};
+
+// KV store of one QSA layer: cells addressed by kv_slot(p)
+struct QsaKv {
+    int8_t* kq; uint16_t* ks;          // [slots][KVD], [slots][KVD/64] fp16 bits
+    int8_t* vq; uint16_t* vs;
+};
+// indexer state of one QSA layer
+struct QsaIdx {
+    float* tail;                       // [iblk-1][idim]
+    float* dead;                       // [idim]
+    uint16_t* pooled;                  // [ctx_max/iblk + 2][idim] fp16 bits
+    float* tail_snaps;                 // optional [T][iblk-1][idim]
+    float* dead_snaps;                 // optional [T][idim]
+    uint16_t* pool_snaps;              // optional [T][2][idim]
+};
+
+struct QsaPrepArgs {
+    QsaDims dm;
+    const int* pos;                    // device: base position of row 0
+    float* qg;                         // [T][qh*2*hd] q|gate per head (q normalised+roped in place)
+    float* kk;                         // [T][kvh*hd] (normalised+roped in place)
+    const float* vv;                   // [T][kvh*hd]
+    float* q_idx;                      // [T][ih*idim] (normalised+roped in place)
+    const float* idx_raw;              // [T][idim]
+    const float* q_norm, *k_norm, *iq_norm, *ik_norm;
+    const float* cos_tab, *sin_tab;    // [ctx_max][n_rot/2]
+    QsaKv kv;
+    QsaIdx ix;
+};
+int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st);
+
+struct QsaScoreArgs {
+    QsaDims dm;
+    const int* pos;
+    const uint16_t* pooled;            // fp16 keys
+    const float* dead;
+    const float* q_idx;                // [T][ih*idim]
+    float* scores;                     // [T][max_b]
+    int max_b;                         // ctx_max/iblk + 2
+};
+int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st);
+int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
+                    int T, hipStream_t st);
+
+struct QsaAttnArgs {
+    QsaDims dm;
+    const int* pos;
+    const float* qg;                   // [T][qh*2*hd]
+    QsaKv kv;
+    const int* sel_ids;                // [T][topk]
+    float* part;                       // [T][kvh][nch][gq][hd] partial outputs
+    float* part_ml;                    // [T][kvh][nch][gq][2] (max, sum)
+    float* out;                        // [T][qh*hd]
+};
+size_t qsa_attn_part_floats(const QsaDims& dm, int T);
+int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st);
+
+}  // namespace wzy

@@ -38,8 +38,54 @@ class MoeWeights(C.Structure):
     ]
 
 
+class QsaDims(C.Structure):
+    """struct wzy_qsa_dims (include/wzy_kernels.h)"""
+    _fields_ = [("qh", I32), ("kvh", I32), ("hd", I32), ("n_rot", I32),
+                ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
+                ("ctx_max", I32), ("kv_ring", I32), ("kv_sinks", I32), ("eps", F32)]
+
+
+class StageCfg(C.Structure):
+    """struct wzy_stage_cfg (include/wzy_stage.h)"""
+    _fields_ = [("n_layers", I32), ("qsa_period", I32), ("n_embd", I32), ("hc", I32), ("hc_lr", I32),
+                ("gdn_hk", I32), ("gdn_hv", I32), ("qsa_qh", I32), ("qsa_kvh", I32), ("qsa_hd", I32),
+                ("n_rot", I32), ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
+                ("n_exp", I32), ("top_k", I32), ("n_ff", I32), ("n_vocab", I32), ("ctx_max", I32),
+                ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32)]
+
+
 # name -> (restype, argtypes, checked)
 _SIGS = {
+    # stage
+    "wzy_stage_cfg_default": (None, [C.POINTER(StageCfg), I32], False),
+    "wzy_stage_create": (I32, [C.POINTER(StageCfg), I32, C.POINTER(P)], True),
+    "wzy_stage_destroy": (I32, [P], True),
+    "wzy_stage_device_bytes": (SZ, [P], False),
+    "wzy_stage_load_synthetic": (I32, [P, U64, I32], True),
+    "wzy_stage_record_forward": (I32, [P, I32, P, P, I32, I32, I32, I32, I32], True),
+    "wzy_stage_service_cold_layers": (I32, [P], True),
+    "wzy_stage_promote_cold": (I32, [P], True),
+    "wzy_stage_commit_window_state": (I32, [P, I32, I32], True),
+    "wzy_stage_reset_state": (I32, [P], True),
+    "wzy_stage_sync": (I32, [P], True),
+    "wzy_stage_greedy_ids": (I32, [P, P, I32], True),
+    "wzy_stage_top16": (I32, [P, P, P, I32], True),
+    "wzy_stage_logits": (I32, [P, P, I32], True),
+    "wzy_stage_pre_head": (I32, [P, P, I32], True),
+    "wzy_stage_set_graphs": (I32, [P, I32], True),
+    "wzy_stage_stream": (P, [P], False),
+    "wzy_stage_tensor_bytes": (SZ, [P, I32, C.c_char_p], False),
+    "wzy_stage_read_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
+    "wzy_stage_write_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
+    "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32)], True),
+    # layer kernels
+    "wzy_hc_read": (I32, [P, P, P, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P], True),
+    "wzy_gdn_step": (I32, [P, P, P, P, P, P, P, P, P, F32, P, I32, I32, I32, P, P, P], True),
+    "wzy_gdn_recurrence": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32, P, P], True),
+    "wzy_qsa_prepare": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, P], True),
+    "wzy_qsa_select": (I32, [C.POINTER(QsaDims), P, P, P, P, P, I32, P, P, I32, P], True),
+    "wzy_qsa_attend_workspace_bytes": (SZ, [C.POINTER(QsaDims), I32], False),
+    "wzy_qsa_attend": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, SZ, I32, P], True),
     "wzy_last_error": (C.c_char_p, [], False),
     "wzy_version": (C.c_char_p, [], False),
     # kernels
@@ -51,7 +97,7 @@ _SIGS = {
     "wzy_nvfp4_repack_host": (I32, [P, P, I32, I32], True),
     "wzy_moe_workspace_bytes": (SZ, [I32, I32, I32, I32, I32], False),
     "wzy_moe_block": (I32, [C.POINTER(MoeWeights), P, I32, P, P, P, P, SZ, P], True),
-    "wzy_moe_time_kernels": (I32, [C.POINTER(MoeWeights), I32, I32, P, SZ, I32, C.POINTER(F32),
+    "wzy_moe_time_kernels": (I32, [C.POINTER(MoeWeights), I32, I32, P, P, SZ, I32, C.POINTER(F32),
                                    C.POINTER(F32), P], True),
     "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
     "wzy_row_top16": (I32, [P, I32, I32, P, P, P, P], True),
@@ -185,3 +231,83 @@ class DeviceArray:
             self.free()
         except Exception:
             pass
+
+
+class Stage:
+    """Owning handle of a wzy_stage (include/wzy_stage.h)."""
+
+    def __init__(self, cfg, device=0):
+        self.lib = lib()
+        self.cfg = cfg
+        h = P()
+        self.lib.wzy_stage_create(C.byref(cfg), device, C.byref(h))
+        self.h = h.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.wzy_stage_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load_synthetic(self, seed, n_ctx):
+        self.lib.wzy_stage_load_synthetic(self.h, seed, n_ctx)
+
+    def forward(self, pos, toks, run_head=True, save_snaps=False, want_top16=False, snap_offset=0, emb=None):
+        import numpy as np
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        e = None if emb is None else np.ascontiguousarray(emb, dtype=np.float32)
+        self.lib.wzy_stage_record_forward(self.h, int(pos), ptr(e), toks.ctypes.data, len(toks), int(run_head),
+                                          int(save_snaps), int(want_top16), int(snap_offset))
+
+    def sync(self):
+        self.lib.wzy_stage_sync(self.h)
+
+    def greedy(self, T):
+        import numpy as np
+        out = np.empty(T, np.int32)
+        self.lib.wzy_stage_greedy_ids(self.h, out.ctypes.data, T)
+        return out
+
+    def top16(self, T):
+        import numpy as np
+        v = np.empty(T * 16, np.float32)
+        i = np.empty(T * 16, np.int32)
+        self.lib.wzy_stage_top16(self.h, v.ctypes.data, i.ctypes.data, T)
+        return v.reshape(T, 16), i.reshape(T, 16)
+
+    def logits(self, T):
+        import numpy as np
+        out = np.empty((T, self.cfg.n_vocab), np.float32)
+        self.lib.wzy_stage_logits(self.h, out.ctypes.data, T)
+        return out
+
+    def pre_head(self, T):
+        import numpy as np
+        out = np.empty((T, self.cfg.hc, self.cfg.n_embd), np.float32)
+        self.lib.wzy_stage_pre_head(self.h, out.ctypes.data, T)
+        return out
+
+    def read(self, layer, name, dtype):
+        import numpy as np
+        n = self.lib.wzy_stage_tensor_bytes(self.h, layer, name.encode())
+        if n == 0:
+            raise WzyError("no tensor %s in layer %d" % (name, layer))
+        out = np.empty(n // np.dtype(dtype).itemsize, dtype)
+        self.lib.wzy_stage_read_tensor(self.h, layer, name.encode(), out.ctypes.data, out.nbytes)
+        return out
+
+    def write(self, layer, name, arr):
+        import numpy as np
+        a = np.ascontiguousarray(arr)
+        self.lib.wzy_stage_write_tensor(self.h, layer, name.encode(), a.ctypes.data, a.nbytes)
+
+
+def default_cfg(ctx_max):
+    c = StageCfg()
+    lib().wzy_stage_cfg_default(C.byref(c), ctx_max)
+    return c
