@@ -29,6 +29,16 @@ _SIGS = {
     "orc_expert_gate_up": (None, [P, I32, I32, P, P, P, P, P]),
     "orc_expert_down": (None, [P, I32, I32, P, P, P]),
     "orc_moe_block": (I32, [C.POINTER(OrcMoeWeights), P, I32, P, P, P, P, P]),
+    "orc_hc_read": (None, [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, P, P, P, P]),
+    "orc_gdn_step": (None, [P, P, P, P, P, P, P, P, P, F32, P, I32, I32, I32]),
+    "orc_gdn_recurrence": (None, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32]),
+    "orc_rope_tables": (None, [I32, I32, F32, P, P]),
+    "orc_head_norm_rope": (None, [P, I32, P, P, P, I32, I32, F32]),
+    "orc_kv_quant_row": (None, [P, I32, P, P]),
+    "orc_indexer_append": (None, [P, P, P, P, I32, I32, I32, I32, F32, P, P, P]),
+    "orc_block_scores": (None, [P, P, P, I32, I32, I32, I32, P]),
+    "orc_topk_select": (I32, [P, I32, I32, I32, P]),
+    "orc_attend": (None, [P, P, P, P, P, P, I32, I32, I32, I32, P]),
     "orc_row_argmax": (None, [P, I32, I32, P]),
     "orc_row_top16": (None, [P, I32, I32, P, P, P]),
     "orc_cpu_pool_create": (P, [I32, I32, I32]),

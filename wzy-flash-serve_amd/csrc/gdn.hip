@@ -147,18 +147,19 @@ __global__ void __launch_bounds__(512) gdn_kernel(GdnArgs a) {
             }
             s_red2[rg][col] = o;
             __syncthreads();
-            if (rg == 0) {
-                const float oc = (s_red2[0][col] + s_red2[1][col] + s_red2[2][col] + s_red2[3][col]) * 0.08838834764831845f;
+            float oc = 0.f;
+            if (rg == 0) {                  // waves 0-1 own the 128 output columns
+                oc = (s_red2[0][col] + s_red2[1][col] + s_red2[2][col] + s_red2[3][col]) * 0.08838834764831845f;
                 const float sq = wave_sum(oc * oc);
                 if (lane == 0) s_w[8 + wv] = sq;
-                __syncthreads();            // every wave passes exactly one barrier in this branch pair
+            }
+            __syncthreads();
+            if (rg == 0) {
                 const float ss = s_w[8] + s_w[9];
                 const float scale = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
                 const float zz = a.z ? a.z[(size_t) t * HV * GS + h * GS + col] : 0.0f;
                 const float gate = a.z ? 1.0f / (1.0f + __expf(-zz)) : 1.0f;
                 a.y[(size_t) t * HV * GS + h * GS + col] = oc * scale * gm * gate;
-            } else {
-                __syncthreads();
             }
             __syncthreads();
         }

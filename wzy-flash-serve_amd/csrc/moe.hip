@@ -132,8 +132,9 @@ WZY_DEV void route_window(const float* __restrict__ logits, int E, int K, int T,
                 if (of) ++gidx;
             }
         }
-        if (first) { r.gexp[gidx] = id; r.gcnt[gidx] = cnt; }
-        r.gmem[gidx][slot] = tid;
+        // an expert occurs at most once per row (cnt <= T); the clamp only guards non-finite logits
+        if (first) { r.gexp[gidx] = id; r.gcnt[gidx] = min(cnt, WZY_MAX_W); }
+        if (slot < WZY_MAX_W) r.gmem[gidx][slot] = tid;
     }
     if (tid == 0) {
         int ng = 0;

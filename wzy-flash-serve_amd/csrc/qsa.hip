@@ -479,6 +479,8 @@ int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
 
 int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
     WZY_TRY(check_dims(a.dm));
+    WZY_REQUIRE(a.dm.idim == 128, "qsa_score: indexer key width must be 128");
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_score: T out of range");
     const int grid = (a.max_b + SC_BLOCKS_PER_WG - 1) / SC_BLOCKS_PER_WG;
     switch (T) {
 #define C_(TT) case TT: hipLaunchKernelGGL((qsa_score_kernel<TT>), dim3(grid), dim3(256), 0, st, a); break;
@@ -493,6 +495,7 @@ int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
 int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
                     int T, hipStream_t st) {
     WZY_TRY(check_dims(dm));
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_topk: T out of range");
     hipLaunchKernelGGL(qsa_topk_kernel, dim3(T), dim3(256), 0, st, dm, pos, scores, max_b, sel_ids, sel_cnt);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
@@ -505,6 +508,7 @@ size_t qsa_attn_part_floats(const QsaDims& dm, int T) {
 
 int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st) {
     WZY_TRY(check_dims(a.dm));
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_attn: T out of range");
     const int nch = (a.dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
     hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh, T), dim3(256), 0, st, a);
     hipLaunchKernelGGL(qsa_combine_kernel, dim3(a.dm.qh, T), dim3(256), 0, st, a);
