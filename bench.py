@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Decode benchmark of the MI355X build (one GPU).
+
+Workload: the synthetic 48-layer decoder (36 GDN + 12 QSA layers, NVFP4 MoE
+with 512 experts / top-10 + a shared expert in every layer, vocab 151936, bf16 LM head), one
+sequence at a 32K-token prefilled context, greedy token loop.  A step is one decode token: one
+replay of the captured forward graph, the host reading the greedy id back and feeding it in as the
+next token.  The timed region is `--steps` such steps after `--warmup` untimed ones, bracketed by
+device synchronisation.
+
+Beside the tok/s line it reports
+  roofline      the MoE gate/up kernel (the largest contributor to the step, 48 launches per token)
+                timed live with HIP events on the stage's own stream, against 8 TB/s;
+  cpu_baseline  the AVX2/FMA restatement of the reference CPU MoE pool (oracle/cpu_moe_pool.cpp)
+                on BASELINE config 1 (one token, 10 routed experts), timed on this host for a
+                bounded ~10 s sample.
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "wzy-flash-serve_amd"))
+
+HBM_PEAK_GBS = 8000.0
+D, F, E, K = 2048, 512, 512, 10
+# bytes one moe_gate_up launch must read at T=1: 10 routed experts' gate+up e2m1 codes and e4m3
+# scales (2*F*D/2 + 2*F*D/16) + their 16-byte tail, the shared expert's Q8_0 gate+up (2*F*D
+# codes + 2*F*D/32 fp16 scales), the router logits (E fp32) and the activation row (D fp32).
+GU_BYTES = K * (2 * F * D // 2 + 2 * F * D // 16 + 16) + (2 * F * D + 2 * F * D // 32 * 2) + E * 4 + D * 4
+# bytes one moe_down launch must read: routed down codes+scales, shared down Q8_0, the requantised
+# activations, and the output row written
+DN_BYTES = K * (D * F // 2 + D * F // 16) + (D * F + D * F // 32 * 2) + K * (F + F // 16 * 4) + D * 4
+# routed-expert bytes of one token-layer (the BASELINE config-1 roofline basis)
+ROUTED_BYTES = K * (3 * F * D // 2 + 3 * F * D // 16 + 16)
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(2, min(15, n, 16))
+
+
+def cpu_baseline(wz, seconds):
+    """Time the restated reference CPU MoE pool on config 1 (seed 0) for about `seconds`."""
+    import numpy as np
+    orc = C.CDLL(os.path.join(ROOT, "oracle", "liboracle.so"))
+    P, I32 = C.c_void_p, C.c_int
+    orc.orc_cpu_pool_create.restype = P
+    orc.orc_cpu_pool_create.argtypes = [I32, I32, I32]
+    orc.orc_cpu_pool_destroy.argtypes = [P]
+    orc.orc_cpu_pool_run.restype = I32
+    orc.orc_cpu_pool_run.argtypes = [P, P, P, P, I32, I32, P, P, P]
+    orc.orc_gemv_bf16.argtypes = [P, P, P, I32, I32, I32]
+    orc.orc_router_topk.argtypes = [P, I32, I32, I32, P, P, P]
+    orc.orc_quant_act.argtypes = [P, I32, I32, P, P, P, P]
+    seed, layer = 0, 0
+    router = np.empty(E * D, np.uint16)
+    wz.wzy_synth_normal_bf16(seed, wz.wzy_synth_stream(5, layer, 0), E * D, 0.0, 0.02, router.ctypes.data)
+    xh = np.empty(D, np.uint16)
+    wz.wzy_synth_normal_bf16(seed, wz.wzy_synth_stream(7, layer, 0), D, 0.0, 1.0, xh.ctypes.data)
+    x = (xh.astype(np.uint32) << 16).view(np.float32).copy()
+    logits = np.empty(E, np.float32)
+    orc.orc_gemv_bf16(router.ctypes.data, x.ctypes.data, logits.ctypes.data, E, D, 1)
+    ids = np.empty(K, np.int32)
+    wts = np.empty(K, np.float32)
+    orc.orc_router_topk(logits.ctypes.data, E, K, 1, ids.ctypes.data, wts.ctypes.data, None)
+    q32 = np.empty(D, np.int8)
+    s32 = np.empty(D // 32, np.float32)
+    q16 = np.empty(D, np.int8)
+    s16 = np.empty(D // 16, np.float32)
+    orc.orc_quant_act(x.ctypes.data, D, 1, q32.ctypes.data, s32.ctypes.data, q16.ctypes.data, s16.ctypes.data)
+    nb = wz.wzy_nvfp4_blob_bytes(D, F)
+    blobs = [np.empty(nb, np.uint8) for _ in range(E)]
+    for e in set(ids.tolist()):
+        wz.wzy_synth_expert_blob(seed, layer, e, D, F, blobs[e].ctypes.data)
+    arr = (C.c_void_p * E)(*[b.ctypes.data for b in blobs])
+    out = np.empty(D, np.float32)
+    n = cpu_threads()
+    pool = orc.orc_cpu_pool_create(n, D, F)
+    if not pool:
+        return None
+    try:
+        args = (pool, C.cast(arr, C.c_void_p).value, ids.ctypes.data, wts.ctypes.data, 1, K, q16.ctypes.data,
+                s16.ctypes.data, out.ctypes.data)
+        for _ in range(20):
+            orc.orc_cpu_pool_run(*args)
+        times = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            for _ in range(10):
+                orc.orc_cpu_pool_run(*args)
+            times.append((time.perf_counter() - t0) / 10)
+    finally:
+        orc.orc_cpu_pool_destroy(pool)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(ROUTED_BYTES / med / 1e9, 2),
+        "unit": "GB/s (NVFP4 MoE, routed experts, 1 token-layer)",
+        "cores": n,
+        "kind": "port",
+        "us_per_token_layer": round(med * 1e6, 1),
+        "sample": "config 1 (seed 0, 1 token, top-10 of 512, D=2048 F=512), %d x 10 calls over %.0f s, median" % (
+            len(times), seconds),
+    }
+
+
+def pmc_traffic(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", "moe_gate_up_decode_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch ") and kernel_prefix in line:
+                    return float(line.split()[1])
+    except OSError:
+        return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--n-ctx", type=int, default=32768)
+    ap.add_argument("--seed", type=int, default=3)
+    ap.add_argument("--moe-iters", type=int, default=480, help="gate/up + down launches timed for the roofline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true", help="direct kernel launches instead of graph replay")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU (all 512x48 experts resident in one MI355X's HBM); "
+              "multi-GPU runs are not part of it -- use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import wzy_amd
+    wz = wzy_amd.lib()
+    if wzy_amd.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    wz.wzy_dev_set(0)
+
+    ctx_max = args.n_ctx + args.warmup + args.steps + 64
+    cfg = wzy_amd.default_cfg(ctx_max)
+    t0 = time.perf_counter()
+    st = wzy_amd.Stage(cfg)
+    if args.no_graphs:
+        wz.wzy_stage_set_graphs(st.h, 0)
+    st.load_synthetic(args.seed, args.n_ctx)
+    t_load = time.perf_counter() - t0
+    print("bench: stage loaded (%.1f GiB on device) in %.1f s" % (wz.wzy_stage_device_bytes(st.h) / 2**30, t_load),
+          file=sys.stderr, flush=True)
+
+    pos = args.n_ctx
+    tok = int(args.seed) % cfg.n_vocab
+    h_tok = np.zeros(1, np.int32)
+    toks = []
+
+    def step():
+        nonlocal pos, tok
+        h_tok[0] = tok
+        wz.wzy_stage_record_forward(st.h, pos, None, h_tok.ctypes.data, 1, 1, 0, 0, 0)
+        wz.wzy_stage_sync(st.h)
+        wz.wzy_stage_greedy_ids(st.h, h_tok.ctypes.data, 1)
+        tok = int(h_tok[0])
+        pos += 1
+        return tok
+
+    for _ in range(args.warmup):
+        step()
+    wz.wzy_device_sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        toks.append(step())
+    wz.wzy_device_sync()
+    elapsed = time.perf_counter() - t0
+    print("bench: %d steps in %.3f s" % (args.steps, elapsed), file=sys.stderr, flush=True)
+
+    # live MoE kernel timing with HIP events on the stage stream (activations of the last step)
+    us_gu, us_dn = C.c_float(0), C.c_float(0)
+    wz.wzy_stage_time_moe(st.h, args.moe_iters, C.byref(us_gu), C.byref(us_dn))
+    gu_gbs = GU_BYTES / (us_gu.value * 1e-6) / 1e9
+    dn_gbs = DN_BYTES / (us_dn.value * 1e-6) / 1e9
+    st.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(wz, args.cpu_seconds)
+
+    tok_s = args.steps / elapsed
+    out = {
+        "metric": "greedy decode tok/s (1 GPU, 32K ctx) + NVFP4 MoE GEMV HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 * elapsed / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e2m1/int8/bf16 weights, int32+fp32 accumulate",
+        "data": "synthetic (seeded random-init weights and 32K prefilled KV/state, no checkpoint)",
+        "config": {"workload": "config 4: synthetic 48-layer decoder (36 GDN + 12 QSA, NVFP4 MoE 512x top-10 + "
+                               "shared, vocab 151936), 1 sequence, %d-token prefilled context, greedy, T=1"
+                               % args.n_ctx,
+                   "n_ctx": args.n_ctx, "seed": args.seed, "graphs": not args.no_graphs},
+        "roofline": {
+            "kernel": "moe_gate_up_kernel<1>",
+            "bound": "hbm",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": pmc_traffic("moe_gate_up_kernel"),
+            "algorithmic_bytes": GU_BYTES,
+            "us_per_launch": round(us_gu.value, 3),
+            "launches_timed": args.moe_iters,
+            "moe_down": {"achieved": round(dn_gbs, 1), "us_per_launch": round(us_dn.value, 3),
+                         "algorithmic_bytes": DN_BYTES},
+            "moe_routed_gbs": round(ROUTED_BYTES / ((us_gu.value + us_dn.value) * 1e-6) / 1e9, 1),
+        },
+        "cpu_baseline": cpu,
+        "greedy_tokens_head": toks[:8],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

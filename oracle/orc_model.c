@@ -7,6 +7,57 @@
 
 #include "wzy_oracle.h"
 
+static int cmp_desc_f(const void* a, const void* b) {
+    const float x = *(const float*) a, y = *(const float*) b;
+    return x < y ? 1 : (x > y ? -1 : 0);
+}
+
+/* Gap between the k-th and (k+1)-th largest of v[0..n) (k >= 1), +huge if n <= k. */
+static float kth_gap(const float* v, int n, int k) {
+    if (n <= k) return 1e30f;
+    float* s = (float*) malloc(sizeof(float) * (size_t) n);
+    memcpy(s, v, sizeof(float) * (size_t) n);
+    qsort(s, (size_t) n, sizeof(float), cmp_desc_f);
+    const float g = s[k - 1] - s[k];
+    free(s);
+    return g;
+}
+
+/* Relative score gap around the top-k threshold block of one row (how far a block score would have
+ * to move to change the selected cell set); +huge when the row selects every cell. */
+static float select_margin(const float* scores, int n_kv, int blk, int topk) {
+    if (n_kv <= topk) return 1e30f;
+    const int nbid = n_kv / blk, nb = nbid + 1;
+    float* s = (float*) malloc(sizeof(float) * (size_t) nb);
+    int* w = (int*) malloc(sizeof(int) * (size_t) nb);
+    int n = 0;
+    for (int b = 0; b < nb; ++b) {
+        const int wb = b < nbid ? blk : n_kv - nbid * blk;
+        if (wb > 0) { s[n] = scores[b]; w[n] = wb; ++n; }
+    }
+    /* sort (score, weight) pairs by score, descending (insertion sort keeps it dependency-free) */
+    for (int i = 1; i < n; ++i) {
+        const float sv = s[i];
+        const int wv = w[i];
+        int j = i - 1;
+        while (j >= 0 && s[j] < sv) { s[j + 1] = s[j]; w[j + 1] = w[j]; --j; }
+        s[j + 1] = sv; w[j + 1] = wv;
+    }
+    long cum = 0;
+    int jt = n - 1;
+    for (int i = 0; i < n; ++i) {
+        cum += w[i];
+        if (cum >= topk) { jt = i; break; }
+    }
+    float gap = 1e30f;
+    if (jt > 0) gap = fminf(gap, s[jt - 1] - s[jt]);
+    if (jt + 1 < n) gap = fminf(gap, s[jt] - s[jt + 1]);
+    const float scale = fmaxf(fabsf(s[jt]), 1e-30f);
+    free(s);
+    free(w);
+    return gap / scale;
+}
+
 static void q8_gemv_f(const int8_t* q, const uint16_t* s, const float* x, float* y, int rows, int cols, int T) {
     int8_t* xq = (int8_t*) malloc((size_t) T * cols);
     float* xs = (float*) malloc(sizeof(float) * (size_t) T * cols / 32);
@@ -18,6 +69,11 @@ static void q8_gemv_f(const int8_t* q, const uint16_t* s, const float* x, float*
 
 int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                       float* pre_head) {
+    return orc_model_forward_dbg(m, pos, toks, T, logits, greedy, pre_head, NULL, NULL);
+}
+
+int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                          float* pre_head, float* dbg, float* margins) {
     const int D = m->n_embd, HC = m->hc, HCD = HC * D, L = m->hc_lr;
     const int QKV = 2 * m->gdn_hk * 128 + m->gdn_hv * 128, GV = m->gdn_hv * 128;
     const int QD = m->qsa_qh * m->qsa_hd, KVD = m->qsa_kvh * m->qsa_hd, hd = m->qsa_hd;
@@ -67,6 +123,8 @@ int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float
                     w->hc_down_s[0], w->hc_inj[0], w->hc_up_q[0], w->hc_up_s[0], D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo,
                     inj_a, mixed);
         cur ^= 1;
+        float* dl = dbg ? dbg + (size_t) l * 4 * T * D : NULL;   /* [mixed_a | block | mixed_f | comb] */
+        if (dl) memcpy(dl, mixed, sizeof(float) * (size_t) T * D);
         if (!w->qsa) {
             const int hv = m->gdn_hv;
             q8_gemv_f(w->qkv_q, w->qkv_s, mixed, qkv, QKV, D, T);
@@ -106,15 +164,18 @@ int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float
                     orc_block_scores(w->idx_pooled, w->idx_dead, q_idx + (size_t) t * IH * ID, n_kv, IH, ID, m->idx_blk,
                                      scores);
                 const int n = orc_topk_select(scores, n_kv, m->idx_blk, m->idx_topk, sel);
+                if (margins) margins[((size_t) l * T + t) * 2 + 1] = select_margin(scores, n_kv, m->idx_blk, m->idx_topk);
                 orc_attend(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh, hd,
                            att + (size_t) t * QD);
             }
             q8_gemv_f(w->wo_q, w->wo_s, att, block, D, QD, T);
         }
         /* FFN half */
+        if (dl) memcpy(dl + (size_t) T * D, block, sizeof(float) * (size_t) T * D);
         orc_hc_read(R[cur], NULL, block, inj_a, w->hc_norm[1], w->hc_down_q[1], w->hc_down_s[1], w->hc_inj[1],
                     w->hc_up_q[1], w->hc_up_s[1], D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo, inj_f, mixed);
         cur ^= 1;
+        if (dl) memcpy(dl + (size_t) 2 * T * D, mixed, sizeof(float) * (size_t) T * D);
         orc_moe_weights mw;
         mw.n_embd = D; mw.n_ff = m->n_ff; mw.n_exp = m->n_exp; mw.top_k = m->top_k;
         mw.router = w->router; mw.sgate = w->sgate; mw.blobs = NULL;
@@ -122,7 +183,15 @@ int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float
         mw.sh_down_q = w->sh_down_q; mw.sh_down_s = w->sh_down_s;
         int ids[8 * 64];
         float wts[8 * 64];
-        rc = orc_moe_block_fn(&mw, mixed, T, comb, ids, wts, NULL, NULL, m->blob, m->blob_ctx, l);
+        float* rl = (float*) malloc(sizeof(float) * (size_t) T * m->n_exp);
+        rc = orc_moe_block_fn(&mw, mixed, T, comb, ids, wts, rl, NULL, m->blob, m->blob_ctx, l);
+        if (margins)
+            for (int t = 0; t < T; ++t) {
+                margins[((size_t) l * T + t) * 2 + 0] = kth_gap(rl + (size_t) t * m->n_exp, m->n_exp, m->top_k);
+                if (!w->qsa) margins[((size_t) l * T + t) * 2 + 1] = 1e30f;
+            }
+        free(rl);
+        if (dl) memcpy(dl + (size_t) 3 * T * D, comb, sizeof(float) * (size_t) T * D);
         pend_bo = comb;
         pend_inj = inj_f;
     }

@@ -142,6 +142,13 @@ typedef struct orc_model {
 /* logits [T x n_vocab], greedy [T] and pre_head [T x hc x n_embd] (optional); returns 0 or -1. */
 int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                       float* pre_head);
+/* Same, also recording per layer l at dbg + l*4*T*n_embd (optional): the attention-half mixed
+ * input, the attention block output, the FFN-half mixed input and the MoE output, each [T x n_embd];
+ * and at margins + (l*T + t)*2 (optional) the discrete-decision margins of row t: the router logit
+ * gap between the top_k-th and (top_k+1)-th expert, and the relative indexer score gap around the
+ * top-k threshold block (1e30 when nothing is selected against). */
+int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                          float* pre_head, float* dbg, float* margins);
 
 /* ---- logit reductions (src/wzy_kernels_v2.cuh:1873-1984) ---- */
 void orc_row_argmax(const float* logits, int nvocab, int T, int* out);

@@ -52,11 +52,13 @@ class OracleModel:
         self.wz, self.cfg, self.seed = wz, cfg, seed
         self.keep = []
         self.blobs = {}
+        self.arrays = {}          # (layer, name) -> host array the oracle reads / updates in place
         st = stage
 
         def rd(layer, name, dt):
             a = st.read(layer, name, dt)
             self.keep.append(a)
+            self.arrays[(layer, name)] = a
             return a.ctypes.data
 
         L = (OrcLayer * cfg.n_layers)()
@@ -119,25 +121,43 @@ class OracleModel:
         m.blob_ctx = None
         self.model = m
         self.orc = oracle_lib.load()
-        self.orc.orc_model_forward.restype = I32
-        self.orc.orc_model_forward.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P]
+        self.orc.orc_model_forward_dbg.restype = I32
+        self.orc.orc_model_forward_dbg.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P, P, P]
+        self.last_layers = None
+        self.last_margins = None
 
     def forward(self, pos, toks):
+        """logits [T x V], greedy [T], pre-head residual [T x hc x D].  Per-layer activations
+        [n_layers x 4 x T x D] (attention mixed, block, FFN mixed, MoE out) are kept in last_layers and
+        the discrete-decision margins [n_layers x T x 2] (router logit gap, relative indexer score gap)
+        in last_margins."""
         toks = np.ascontiguousarray(toks, dtype=np.int32)
         T = len(toks)
         logits = np.empty((T, self.cfg.n_vocab), np.float32)
         greedy = np.empty(T, np.int32)
         pre = np.empty((T, self.cfg.hc, self.cfg.n_embd), np.float32)
-        rc = self.orc.orc_model_forward(C.byref(self.model), pos, toks.ctypes.data, T, logits.ctypes.data,
-                                        greedy.ctypes.data, pre.ctypes.data)
+        dbg = np.empty((self.cfg.n_layers, 4, T, self.cfg.n_embd), np.float32)
+        mg = np.empty((self.cfg.n_layers, T, 2), np.float32)
+        rc = self.orc.orc_model_forward_dbg(C.byref(self.model), pos, toks.ctypes.data, T, logits.ctypes.data,
+                                            greedy.ctypes.data, pre.ctypes.data, dbg.ctypes.data, mg.ctypes.data)
         assert rc == 0, "orc_model_forward failed"
+        self.last_layers = dbg
+        self.last_margins = mg
         return logits, greedy, pre
 
+    def decidable_rows(self, router_gap=0.02, select_gap=1e-3):
+        """Rows of the last forward whose every routing / selection decision has a margin that the
+        float-reordering drift between two implementations cannot cross."""
+        mg = self.last_margins
+        ok = (mg[:, :, 0] > router_gap).all(axis=0) & (mg[:, :, 1] > select_gap).all(axis=0)
+        return ok
 
-def small_cfg(wz_mod, ctx_max=1024, n_layers=4, topk=64):
-    """A small instance of the synthetic architecture for parity tests (QSA every 2nd layer)."""
+
+def small_cfg(wz_mod, ctx_max=1024, n_layers=4, topk=64, qsa_period=2):
+    """A small instance of the synthetic architecture for parity tests (QSA every qsa_period-th layer;
+    n_layers=1 with qsa_period=1 is a single QSA layer, with qsa_period=2 a single GDN layer)."""
     c = wz_mod.StageCfg()
-    c.n_layers, c.qsa_period, c.n_embd, c.hc, c.hc_lr = n_layers, 2, 256, 4, 64
+    c.n_layers, c.qsa_period, c.n_embd, c.hc, c.hc_lr = n_layers, qsa_period, 256, 4, 64
     c.gdn_hk, c.gdn_hv = 2, 2
     c.qsa_qh, c.qsa_kvh, c.qsa_hd, c.n_rot = 4, 2, 256, 64
     c.idx_heads, c.idx_dim, c.idx_blk, c.idx_topk = 4, 128, 4, topk

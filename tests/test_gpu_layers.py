@@ -52,7 +52,9 @@ def q8(wz, seed, rows, cols):
 # hyper-connection read
 # ------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("D,HC,HCLR,T,mode", [(512, 4, 64, 3, "emb"), (512, 4, 64, 3, "fold"), (512, 4, 64, 2, "head"),
-                                             (2048, 4, 320, 1, "fold"), (2048, 4, 320, 4, "emb")])
+                                             (2048, 4, 320, 1, "fold"), (2048, 4, 320, 4, "emb"),
+                                             (2048, 4, 320, 8, "fold"), (4096, 4, 128, 3, "fold"),
+                                             (256, 4, 32, 6, "head")])
 def test_hc_read(wz, orc, gpu, D, HC, HCLR, T, mode):
     print("case hc_read D=%d HC=%d HCLR=%d T=%d mode=%s" % (D, HC, HCLR, T, mode), flush=True)
     rng = np.random.default_rng(D + 7 * T)
@@ -262,7 +264,8 @@ def test_qsa_prepare(wz, orc, gpu, pos, T):
 
 @pytest.mark.parametrize("ctx,pos,T,topk,zero_q", [(1024, 700, 3, 64, False), (1024, 10, 2, 64, False),
                                                    (4096, 2001, 4, 256, True), (4096, 2999, 2, 2048, False),
-                                                   (1024, 63, 3, 64, False), (4096, 4000, 8, 2048, True)])
+                                                   (1024, 63, 3, 64, False), (4096, 4000, 8, 2048, True),
+                                                   (262144, 100000, 2, 2048, False), (65536, 40000, 4, 2048, False)])
 def test_qsa_select(wz, orc, gpu, ctx, pos, T, topk, zero_q):
     print("case qsa_select ctx=%d pos=%d T=%d topk=%d zero_q=%s" % (ctx, pos, T, topk, zero_q), flush=True)
     dm = qsa_dims(ctx, topk)

@@ -2,23 +2,38 @@
 on small instances of the synthetic architecture (MI355X; C ABI only, no torch).
 
 The oracle model is built from the stage's own tensors after load_synthetic, so both sides start
-from the same weights and prefilled state and then evolve their state independently."""
+from the same weights and prefilled state and then evolve their state independently.
+
+Two implementations of this model cannot agree bit for bit: fp32 sums run in different orders, and
+every activation is requantised to int8 (per 16/32/64 values) several times per layer, so a last-bit
+difference occasionally moves one code by one step.  Within one layer that stays far inside the
+tolerance; across layers the differences compound and can eventually cross a near-tie of a discrete
+decision (router top-k, indexer top-k).  Hence:
+  * single-layer models (one GDN or one QSA layer) are compared strictly, over several steps;
+  * multi-layer models are compared strictly on every row whose routing / selection decisions all
+    have a margin (measured by the oracle) that the drift cannot cross; rows that follow an
+    undecidable row are not compared, because their state already differs.
+Tolerance (north star: floats rel 2e-2 / abs 1e-2 on hidden states and logits), applied to the
+whole vector: max|gpu - oracle| <= 1e-2 + 2e-2 * max|oracle|."""
 import numpy as np
 import pytest
 
 import wzy_amd
-from stage_oracle import OracleModel, near_tie, small_cfg
+from stage_oracle import OracleModel, is_qsa, near_tie, small_cfg
 
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 2e-2, 1e-2
+SINGLE = {"gdn": 2, "qsa": 1}      # qsa_period of a one-layer model of that kind
 
 
-def check_logits(tag, g, o):
-    err = np.abs(g.astype(np.float64) - o)
-    print("%s: logits max abs err %.3g (max |ref| %.3g)" % (tag, err.max(), np.abs(o).max()), flush=True)
-    bad = err > ATOL + RTOL * np.abs(o)
-    assert not bad.any(), "%s: %d logits outside tolerance (worst %.3g)" % (tag, bad.sum(), err.max())
+def check_close(tag, g, o):
+    g = np.asarray(g, np.float64)
+    o = np.asarray(o, np.float64)
+    err = np.abs(g - o).max()
+    scale = np.abs(o).max()
+    print("%s: max abs err %.3g (max |ref| %.3g)" % (tag, err, scale), flush=True)
+    assert err <= ATOL + RTOL * scale, "%s: error %.3g above %.3g" % (tag, err, ATOL + RTOL * scale)
 
 
 def check_greedy(tag, g_ids, o_logits):
@@ -30,35 +45,112 @@ def check_greedy(tag, g_ids, o_logits):
                 "%s row %d: greedy %d vs oracle %d (logits %.5f vs %.5f)" % (tag, t, gid, ref, row[gid], row[ref])
 
 
-@pytest.mark.parametrize("n_ctx,topk,graphs", [(600, 64, True), (40, 64, True), (600, 64, False)])
-def test_stage_decode_parity(wz, gpu, n_ctx, topk, graphs):
-    print("case stage_decode n_ctx=%d topk=%d graphs=%s" % (n_ctx, topk, graphs), flush=True)
-    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=topk)
+def check_top16(st, g_logits, g_ids, T):
+    tv, ti = st.top16(T)
+    for t in range(T):
+        assert ti[t, 0] == g_ids[t]
+        assert (np.diff(tv[t]) <= 0).all()
+        assert np.array_equal(g_logits[t, ti[t]], tv[t])
+
+
+@pytest.mark.parametrize("kind,n_ctx,graphs", [("gdn", 600, True), ("qsa", 600, True), ("qsa", 40, True),
+                                               ("qsa", 1021, False), ("gdn", 600, False)])
+def test_stage_single_layer_decode(wz, gpu, kind, n_ctx, graphs):
+    print("case single_layer_decode kind=%s n_ctx=%d graphs=%s" % (kind, n_ctx, graphs), flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1100, n_layers=1, topk=64, qsa_period=SINGLE[kind])
     st = wzy_amd.Stage(cfg)
     try:
         st.lib.wzy_stage_set_graphs(st.h, int(graphs))
         seed = 1234
         st.load_synthetic(seed, n_ctx)
         orc = OracleModel(wz, st, cfg, seed)
-        rng = np.random.default_rng(n_ctx)
-        toks = rng.integers(0, cfg.n_vocab, 4)
+        toks = np.random.default_rng(n_ctx).integers(0, cfg.n_vocab, 6)
         pos = n_ctx
         for step, tok in enumerate(toks):
             st.forward(pos, [tok], want_top16=True)
             st.sync()
             g_logits, g_ids = st.logits(1), st.greedy(1)
-            g_pre = st.pre_head(1)
-            o_logits, o_ids, o_pre = orc.forward(pos, [tok])
+            o_logits, _, o_pre = orc.forward(pos, [tok])
             tag = "step %d pos %d" % (step, pos)
-            err = np.abs(g_pre - o_pre).max()
-            print("%s: pre-head residual max abs err %.3g (max %.3g)" % (tag, err, np.abs(o_pre).max()))
-            check_logits(tag, g_logits, o_logits)
+            check_close(tag + " pre-head", st.pre_head(1), o_pre)
+            check_close(tag + " logits", g_logits, o_logits)
             check_greedy(tag, g_ids, o_logits)
-            tv, ti = st.top16(1)
-            assert ti[0, 0] == g_ids[0]
-            assert (np.diff(tv[0]) <= 0).all()
-            assert np.array_equal(g_logits[0, ti[0]], tv[0])
+            check_top16(st, g_logits, g_ids, 1)
             pos += 1
+    finally:
+        st.close()
+
+
+@pytest.mark.parametrize("kind", ["gdn", "qsa"])
+def test_stage_single_layer_window_commit(wz, gpu, kind):
+    """A T=4 window with snapshots, commit after its second row, then two decode steps: matches the
+    oracle that decoded only the two accepted rows."""
+    print("case single_layer_window kind=%s" % kind, flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=1, topk=64, qsa_period=SINGLE[kind])
+    st = wzy_amd.Stage(cfg)
+    try:
+        seed = 77
+        n_ctx = 601                      # window rows cross an indexer block boundary
+        st.load_synthetic(seed, n_ctx)
+        orc_full = OracleModel(wz, st, cfg, seed)
+        orc_acc = OracleModel(wz, st, cfg, seed)
+        win = np.array([11, 222, 333, 444], np.int32)
+        st.forward(n_ctx, win, save_snaps=True, want_top16=True)
+        st.sync()
+        g4, gid4 = st.logits(4), st.greedy(4)
+        o4, _, _ = orc_full.forward(n_ctx, win)
+        for t in range(4):
+            check_close("window row %d" % t, g4[t], o4[t])
+        check_greedy("window", gid4, o4)
+        check_top16(st, g4, gid4, 4)
+        # accept rows 0 and 1 (last accepted position n_ctx + 1)
+        st.lib.wzy_stage_commit_window_state(st.h, 1, n_ctx + 1)
+        orc_acc.forward(n_ctx, win[:2])
+        for step, tok in enumerate([555, 7]):
+            pos = n_ctx + 2 + step
+            st.forward(pos, [tok])
+            st.sync()
+            o1, _, _ = orc_acc.forward(pos, [tok])
+            check_close("after commit, pos %d" % pos, st.logits(1), o1)
+            check_greedy("after commit", st.greedy(1), o1)
+    finally:
+        st.close()
+
+
+@pytest.mark.parametrize("seed,n_ctx", [(1234, 600), (77, 601), (5, 300)])
+def test_stage_multilayer_decode(wz, gpu, seed, n_ctx):
+    """Four layers (GDN, QSA, GDN, QSA): four single-token steps then a T=4 window; every decidable
+    row matches the oracle."""
+    print("case multilayer seed=%d n_ctx=%d" % (seed, n_ctx), flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(seed, n_ctx)
+        orc = OracleModel(wz, st, cfg, seed)
+        rng = np.random.default_rng(seed)
+        pos, checked, skipped, tainted = n_ctx, 0, 0, False
+        windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
+        for w in windows:
+            T = len(w)
+            st.forward(pos, w, want_top16=True)
+            st.sync()
+            g, gid = st.logits(T), st.greedy(T)
+            o, _, _ = orc.forward(pos, w)
+            ok = orc.decidable_rows()
+            for t in range(T):
+                tag = "pos %d row %d" % (pos, t)
+                if tainted or not ok[t]:
+                    tainted = True
+                    skipped += 1
+                    print("%s: skipped (min router gap %.3g, min select gap %.3g)" % (
+                        tag, orc.last_margins[:, t, 0].min(), orc.last_margins[:, t, 1].min()), flush=True)
+                    continue
+                check_close(tag, g[t], o[t])
+                check_greedy(tag, gid[t:t + 1], o[t:t + 1])
+                checked += 1
+            check_top16(st, g, gid, T)
+            pos += T
+        print("multilayer: %d rows checked, %d skipped" % (checked, skipped), flush=True)
     finally:
         st.close()
 
@@ -88,39 +180,6 @@ def test_stage_graph_replay_matches_eager(wz, gpu):
         assert np.array_equal(a, b)
 
 
-def test_stage_window_and_commit(wz, gpu):
-    """A T=4 window with snapshots, commit after its second row, then a decode step: matches the oracle
-    that decoded only the two accepted rows."""
-    print("case stage_window_commit", flush=True)
-    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
-    st = wzy_amd.Stage(cfg)
-    try:
-        seed = 77
-        n_ctx = 601                      # window rows cross an indexer block boundary
-        st.load_synthetic(seed, n_ctx)
-        orc_full = OracleModel(wz, st, cfg, seed)
-        orc_acc = OracleModel(wz, st, cfg, seed)
-        win = np.array([11, 222, 333, 444], np.int32)
-        st.forward(n_ctx, win, save_snaps=True, want_top16=True)
-        st.sync()
-        g4 = st.logits(4)
-        o4, _, _ = orc_full.forward(n_ctx, win)
-        check_logits("window", g4, o4)
-        check_greedy("window", st.greedy(4), o4)
-        # accept rows 0 and 1 (last accepted position n_ctx + 1)
-        st.lib.wzy_stage_commit_window_state(st.h, 1, n_ctx + 1)
-        orc_acc.forward(n_ctx, win[:2])
-        nxt = np.array([555], np.int32)
-        st.forward(n_ctx + 2, nxt)
-        st.sync()
-        g1 = st.logits(1)
-        o1, _, _ = orc_acc.forward(n_ctx + 2, nxt)
-        check_logits("after commit", g1, o1)
-        check_greedy("after commit", st.greedy(1), o1)
-    finally:
-        st.close()
-
-
 def test_stage_errors(wz, gpu):
     """Host-side argument checks return errors instead of launching."""
     cfg = small_cfg(wzy_amd, ctx_max=256, n_layers=2, topk=64)
@@ -135,5 +194,86 @@ def test_stage_errors(wz, gpu):
             st.forward(10, list(range(9)))             # wider than the window limit
         with pytest.raises(wzy_amd.WzyError):
             st.read(0, "no_such_tensor", np.float32)
+    finally:
+        st.close()
+
+
+def test_stage_qsa_kernels_in_situ(wz, orc, gpu):
+    """Consecutive decode steps of a GDN+QSA stage: after each step, the QSA layer's block scores,
+    cell selection and attention output are recomputed by the oracle from the stage's own inputs."""
+    from oracle_lib import ptr
+    print("case stage_qsa_in_situ", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=2, topk=64)
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(5, 600)
+        QD = cfg.qsa_qh * cfg.qsa_hd
+        max_b = cfg.ctx_max // cfg.idx_blk + 2
+        for step, pos in enumerate([600, 601, 602, 603, 604]):
+            st.forward(pos, [7 + step])
+            st.sync()
+            n_kv = pos + 1
+            qg = st.read(-1, "act.qg", np.float32)[:2 * QD]
+            qi = st.read(-1, "act.q_idx", np.float32)[:cfg.idx_heads * cfg.idx_dim]
+            sc = st.read(-1, "act.scores", np.float32)[:max_b]
+            sel = st.read(-1, "act.sel_ids", np.int32)[:cfg.idx_topk]
+            cnt = st.read(-1, "act.sel_cnt", np.int32)[0]
+            att = st.read(-1, "act.att_out", np.float32)[:QD]
+            pooled = st.read(1, "idx_pooled", np.uint16)
+            dead = st.read(1, "idx_dead", np.float32)
+            kq, ks = st.read(1, "kv_k", np.int8), st.read(1, "kv_ks", np.uint16)
+            vq, vs = st.read(1, "kv_v", np.int8), st.read(1, "kv_vs", np.uint16)
+            osc = np.zeros(max_b, np.float32)
+            orc.orc_block_scores(ptr(pooled), ptr(dead), ptr(qi), n_kv, cfg.idx_heads, cfg.idx_dim, cfg.idx_blk,
+                                 ptr(osc))
+            nb = n_kv // cfg.idx_blk + 1
+            err = np.abs(sc[:nb] - osc[:nb]) / np.maximum(1.0, np.abs(osc[:nb]))
+            print("step %d: score rel err %.3g" % (step, err.max()), flush=True)
+            assert err.max() < 1e-4, "step %d scores" % step
+            osel = np.zeros(cfg.idx_topk, np.int32)
+            n = orc.orc_topk_select(ptr(sc), n_kv, cfg.idx_blk, cfg.idx_topk, ptr(osel))
+            assert cnt == n == min(n_kv, cfg.idx_topk)
+            assert (sel[:n] == osel[:n]).all(), "step %d selection differs" % step
+            oatt = np.empty(QD, np.float32)
+            orc.orc_attend(ptr(qg), ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(np.ascontiguousarray(sel[:n])), n,
+                           cfg.qsa_qh, cfg.qsa_kvh, cfg.qsa_hd, ptr(oatt))
+            aerr = np.abs(att - oatt).max()
+            print("step %d: attention max abs err %.3g (max %.3g)" % (step, aerr, np.abs(oatt).max()), flush=True)
+            assert aerr < 1e-3, "step %d attention" % step
+    finally:
+        st.close()
+
+
+STATE_TENSORS = {False: [("conv_hist", np.float32), ("ssm", np.float32)],
+                 True: [("kv_k", np.int8), ("kv_ks", np.uint16), ("kv_v", np.int8), ("kv_vs", np.uint16),
+                        ("idx_tail", np.float32), ("idx_dead", np.float32), ("idx_pooled", np.uint16)]}
+
+
+@pytest.mark.parametrize("kind", ["gdn", "qsa"])
+def test_stage_state_tracks_oracle(wz, gpu, kind):
+    """After every decode step of a one-layer model, each recurrent / KV / indexer state tensor of the
+    stage matches the oracle model's copy: float state closely, int8 codes within one step, fp16
+    scales and keys within one ulp (one-step requantisation flips)."""
+    print("case stage_state kind=%s" % kind, flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=1, topk=64, qsa_period=SINGLE[kind])
+    st = wzy_amd.Stage(cfg)
+    try:
+        seed = 21
+        st.load_synthetic(seed, 600)
+        orc = OracleModel(wz, st, cfg, seed)
+        for step in range(5):
+            pos = 600 + step
+            st.forward(pos, [100 + step])
+            st.sync()
+            orc.forward(pos, [100 + step])
+            for name, dt in STATE_TENSORS[is_qsa(cfg, 0)]:
+                g = st.read(0, name, dt).astype(np.float64)
+                o = orc.arrays[(0, name)].astype(np.float64)
+                d = np.abs(g - o)
+                print("  step %d %-10s max diff %.3g, %d differ" % (step, name, d.max(), int((d > 0).sum())), flush=True)
+                if dt == np.float32:
+                    assert d.max() <= 1e-3 * max(1.0, np.abs(o).max()), name
+                else:
+                    assert d.max() <= 1, name
     finally:
         st.close()

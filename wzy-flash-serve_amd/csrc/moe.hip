@@ -1,17 +1,19 @@
 // moe.hip -- NVFP4 mixture-of-experts decode block for gfx950.
 //
 // Launch sequence of wzy_moe_block (T window rows, K routed experts per row), three launches:
-//   1. gemv_segs    router logits [T x E] (bf16) + the shared-expert gate scalar row
-//   2. moe_gate_up  every workgroup recomputes the window routing in LDS (softmax top-K, weights,
-//                   groups: each distinct expert of the window once, with its (row, slot) members,
-//                   so its weights stream from HBM once); workgroup (group, 16-row tile) runs the
-//                   gate+up NVFP4 GEMV on activations quantised per 16 inside the lane, SwiGLU and
-//                   the per-16 int8 requant; extra workgroups run the Q8_0 shared expert
-//   3. moe_down     workgroup = 16 output rows for all groups + the shared expert, combine in LDS:
+//   1. moe_router   router logits [T x E] (bf16 weights, fp32 x) + the shared-expert gate scalar,
+//                   one wave per 4 rows; the last workgroup to finish (device-scope counter) runs
+//                   the softmax top-K per row and groups the T*K routed entries by expert (each
+//                   distinct expert of the window once, with its (row, slot) members, so its
+//                   weights stream from HBM once)
+//   2. moe_gate_up  workgroup (group, 16-row tile) runs the gate+up NVFP4 GEMV on activations
+//                   quantised per 16 inside the lane, SwiGLU and the per-16 int8 requant; extra
+//                   workgroups run the Q8_0 shared expert
+//   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, combine in LDS:
 //                   comb = sigmoid(sgate)*shared + sum_k w_k*part_k  (k in routed order).
-// All GEMVs are wave-per-row with 128-bit code loads (16 bytes = 32 e2m1 values per lane) and
-// e4m3 scales from a separate plane, e2m1 -> int8 expansion with v_perm_b32, v_dot4_i32_i8 dots.
-// No MFMA: at one token per expert these are bandwidth-bound GEMVs.
+// All expert GEMVs are wave-per-row with 128-bit code loads (16 bytes = 32 e2m1 values per lane)
+// and e4m3 scales from a separate plane, e2m1 -> int8 expansion with v_perm_b32, v_dot4_i32_i8
+// dots.  No MFMA: at one token per expert these are bandwidth-bound GEMVs.
 #include "wzy_device.h"
 #include "wzy_gemv.h"
 #include "wzy_host.h"
@@ -21,7 +23,9 @@ using namespace wzy;
 
 namespace {
 
-constexpr int TILE_D = 16;   // output rows of one down workgroup (4 waves x 4 rows x 16 lanes)
+constexpr int DN_TILE = 8;    // output rows of one down workgroup
+constexpr int DN_BATCH = 4;   // work items whose loads a 16-lane slot issues together
+constexpr int MAX_ENT = WZY_MAX_W * MOE_MAX_K;
 
 struct MoeOffsets {
     size_t gu_codes, gu_scales, dn_codes, dn_scales, tail, rec;
@@ -47,105 +51,19 @@ WZY_DEV float nvfp4_chunk_fma(const int4 wa, const int4 wb, float wsa, float wsb
     return acc;
 }
 
-}  // namespace
-
-// ---------------------------------------------------------------------------------------------
-// Window routing, recomputed in LDS by every workgroup that needs it (no extra launch):
-// softmax top-K per row (reference: router_top10_fast_multi, src/wzy_kernels_v2.cuh:989-1090) and
-// the grouping of the T*K routed entries by expert (reference: split_route_hit_cold_kernel /
-// group_experts_kernel, src/wzy_cpu_moe.cuh:74-127, src/wzy_kernels_v2.cuh:1390-1423).  Groups are
-// in ascending expert id and members in entry order, so every workgroup derives the same list;
-// the reference's atomicAdd group order does not affect its results because the combine sums in
-// routed-slot order.
-// ---------------------------------------------------------------------------------------------
-struct RouteLds {
-    int ids[WZY_MAX_W * MOE_MAX_K];
-    float w[WZY_MAX_W * MOE_MAX_K];
-    int n_groups;
-    int gexp[WZY_MAX_W * MOE_MAX_K];
-    int gcnt[WZY_MAX_W * MOE_MAX_K];
-    int gmem[WZY_MAX_W * MOE_MAX_K][WZY_MAX_W];
-};
-
-// blockDim.x = 256 (4 waves); wave w routes rows w, w+4.
-WZY_DEV void route_window(const float* __restrict__ logits, int E, int K, int T, RouteLds& r) {
-    constexpr int MAXV = 16;   // E <= 1024
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int t = wv; t < T; t += 4) {
-        const float* x = logits + (size_t) t * E;
-        float p[MAXV];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < MAXV; ++i) {
-            const int idx = lane + 64 * i;
-            p[i] = idx < E ? x[idx] : -INFINITY;
-            mx = fmaxf(mx, p[i]);
-        }
-        mx = wave_max(mx);
-        float es = 0.f;
-#pragma unroll
-        for (int i = 0; i < MAXV; ++i) {
-            if (lane + 64 * i < E) { p[i] = __expf(p[i] - mx); es += p[i]; }
-            else p[i] = -3.f;
-        }
-        es = wave_sum(es);
-        const float inv = 1.0f / es;
-#pragma unroll
-        for (int i = 0; i < MAXV; ++i)
-            if (lane + 64 * i < E) p[i] *= inv;
-        float wsum = 0.f;
-        for (int k = 0; k < K; ++k) {
-            float bv = -4.f;
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int i = 0; i < MAXV; ++i)
-                if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
-            wave_argmax(bv, bi);
-            if (bi >= E) bi = 0;                         // non-finite logits: keep the id in range
-#pragma unroll
-            for (int i = 0; i < MAXV; ++i)
-                if (lane + 64 * i == bi) p[i] = -2.f;
-            if (lane == 0) { r.ids[t * K + k] = bi; r.w[t * K + k] = bv; }
-            wsum += bv;
-        }
-        const float sc = fmaxf(wsum, 6.103515625e-05f);
-        if (lane < K) r.w[t * K + lane] = r.w[t * K + lane] / sc;
-    }
+// Exclusive count of `pred` over threads 0..255 in thread order (4 waves); `total` = full count.
+WZY_DEV int excl_count256(bool pred, int* s_c, int& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const unsigned long long m = __ballot(pred);
+    const int within = __popcll(m & ((1ull << lane) - 1ull));
+    if (lane == 0) s_c[w] = __popcll(m);
     __syncthreads();
-    const int n_ent = T * K;
-    if (tid < n_ent) {
-        const int id = r.ids[tid];
-        bool first = true;
-        int slot = 0, cnt = 0, gidx = 0;
-        for (int f = 0; f < n_ent; ++f) {
-            const int o = r.ids[f];
-            if (o == id) {
-                ++cnt;
-                if (f < tid) { first = false; ++slot; }
-            }
-        }
-        for (int f = 0; f < n_ent; ++f) {
-            const int o = r.ids[f];
-            if (o < id) {
-                bool of = true;
-                for (int f2 = 0; f2 < f; ++f2) if (r.ids[f2] == o) { of = false; break; }
-                if (of) ++gidx;
-            }
-        }
-        // an expert occurs at most once per row (cnt <= T); the clamp only guards non-finite logits
-        if (first) { r.gexp[gidx] = id; r.gcnt[gidx] = min(cnt, WZY_MAX_W); }
-        if (slot < WZY_MAX_W) r.gmem[gidx][slot] = tid;
-    }
-    if (tid == 0) {
-        int ng = 0;
-        for (int f = 0; f < n_ent; ++f) {
-            bool of = true;
-            for (int f2 = 0; f2 < f; ++f2) if (r.ids[f2] == r.ids[f]) { of = false; break; }
-            if (of) ++ng;
-        }
-        r.n_groups = ng;
-    }
+    int before = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) before += (i < w) ? s_c[i] : 0;
+    total = s_c[0] + s_c[1] + s_c[2] + s_c[3];
     __syncthreads();
+    return before + within;
 }
 
 // per-16 int8 quantisation of 32 fp32 values held by one lane (two 16-blocks)
@@ -201,43 +119,196 @@ WZY_DEV void quant32x1_lane(const float* __restrict__ xp, int4& q0, int4& q1, fl
     q1 = make_int4(w[4], w[5], w[6], w[7]);
 }
 
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// router: logits + shared gate scalar, then (last workgroup) softmax top-K per row
+// (reference: router_top10_fast_multi, src/wzy_kernels_v2.cuh:989-1090) and the grouping of the
+// routed entries by expert (reference: split_route_hit_cold_kernel / group_experts_kernel,
+// src/wzy_cpu_moe.cuh:74-127, src/wzy_kernels_v2.cuh:1390-1423).  Groups are numbered in order
+// of first occurrence and members in entry order; the combine sums in routed-slot order, so the
+// numbering does not affect any result.
+// ---------------------------------------------------------------------------------------------
+template <int T>
+__global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
+    __shared__ int s_ids[MAX_ENT];
+    __shared__ float s_w[MAX_ENT];
+    __shared__ int s_gidx[MAX_ENT];
+    __shared__ int s_c[4];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int D = a.D, E = a.E, K = a.K;
+
+    // ---- logits: wave owns rows row0 .. row0+3 (row E = shared gate) ----
+    {
+        const int row0 = (blockIdx.x * 4 + wv) * 4;
+        const int n8 = D >> 3;
+        float acc[4][T];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
+        for (int j0 = 0; j0 < n8; j0 += 256) {
+            uint4 wv4[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + lane + 64 * u;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int r = row0 + s;
+                    const uint16_t* W = r < E ? a.router + (size_t) r * D : a.sgate;
+                    wv4[u][s] = (j < n8 && r <= E) ? ld_stream_u4((const uint4*) W + j) : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + lane + 64 * u;
+                if (j >= n8) continue;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float4 xa = *(const float4*) (a.x + (size_t) t * D + j * 8);
+                    const float4 xb = *(const float4*) (a.x + (size_t) t * D + j * 8 + 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        float v = acc[s][t];
+                        v = fmaf(bf16_lo(wv4[u][s].x), xa.x, v);
+                        v = fmaf(bf16_hi(wv4[u][s].x), xa.y, v);
+                        v = fmaf(bf16_lo(wv4[u][s].y), xa.z, v);
+                        v = fmaf(bf16_hi(wv4[u][s].y), xa.w, v);
+                        v = fmaf(bf16_lo(wv4[u][s].z), xb.x, v);
+                        v = fmaf(bf16_hi(wv4[u][s].z), xb.y, v);
+                        v = fmaf(bf16_lo(wv4[u][s].w), xb.z, v);
+                        v = fmaf(bf16_hi(wv4[u][s].w), xb.w, v);
+                        acc[s][t] = v;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = row0 + s;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float v = wave_sum(acc[s][t]);
+                if (lane == 0 && r < E) a.logits[(size_t) t * E + r] = v;
+                if (lane == 0 && r == E) a.sg[t] = v;
+            }
+        }
+    }
+
+    // ---- completion: the last workgroup routes ----
+    __builtin_amdgcn_s_waitcnt(0);          // this wave's stores have left the CU
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();                    // publish the workgroup's logits device-wide
+        s_last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();                        // acquire every workgroup's logits
+
+    // softmax top-K per row: wave wv routes rows wv, wv+4
+    for (int t = wv; t < T; t += 4) {
+        constexpr int MAXV = 16;            // E <= 1024
+        const float* x = a.logits + (size_t) t * E;
+        float p[MAXV];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) {
+            const int idx = lane + 64 * i;
+            p[i] = idx < E ? x[idx] : -INFINITY;
+            mx = fmaxf(mx, p[i]);
+        }
+        mx = wave_max(mx);
+        float es = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) {
+            if (lane + 64 * i < E) { p[i] = __expf(p[i] - mx); es += p[i]; }
+            else p[i] = -3.f;
+        }
+        es = wave_sum(es);
+        const float inv = 1.0f / es;
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i)
+            if (lane + 64 * i < E) p[i] *= inv;
+        float wsum = 0.f;
+        for (int k = 0; k < K; ++k) {
+            float bv = -4.f;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < MAXV; ++i)
+                if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
+            wave_argmax(bv, bi);
+            if (bi >= E) bi = 0;                         // non-finite logits: keep the id in range
+#pragma unroll
+            for (int i = 0; i < MAXV; ++i)
+                if (lane + 64 * i == bi) p[i] = -2.f;
+            if (lane == 0) { s_ids[t * K + k] = bi; s_w[t * K + k] = bv; }
+            wsum += bv;
+        }
+        const float sc = fmaxf(wsum, 6.103515625e-05f);
+        if (lane < K) s_w[t * K + lane] = s_w[t * K + lane] / sc;
+    }
+    __syncthreads();
+
+    // grouping: leader = first entry of an expert, slot = rank among the expert's entries
+    const int n_ent = T * K;
+    int id = -1, leader = 0, slot = 0, cnt = 0;
+    if (tid < n_ent) {
+        id = s_ids[tid];
+        leader = tid;
+        bool seen = false;
+        for (int f = 0; f < n_ent; ++f) {
+            if (s_ids[f] != id) continue;
+            if (!seen) { leader = f; seen = true; }
+            if (f < tid) ++slot;
+            ++cnt;
+        }
+        a.ids[tid] = id;
+        a.wts[tid] = s_w[tid];
+    }
+    const bool lead = tid < n_ent && leader == tid;
+    int n_groups = 0;
+    const int g_lead = excl_count256(lead, s_c, n_groups);
+    if (lead) s_gidx[tid] = g_lead;
+    __syncthreads();
+    if (tid < n_ent) {
+        const int g = s_gidx[leader];
+        if (slot < WZY_MAX_W) a.grp_mem[g * WZY_MAX_W + slot] = tid;
+        if (lead) {
+            a.grp_exp[g] = id;
+            a.grp_cnt[g] = min(cnt, WZY_MAX_W);     // an expert occurs at most once per row
+        }
+    }
+    if (tid == 0) {
+        *a.n_groups = n_groups;
+        *a.counter = 0u;                    // ready for the next launch
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // gate/up.  Routed workgroups: one (group, 16-row tile); wave w owns rows j = 16*tile + 4w .. +3
 // of both gate and up, so SwiGLU and the 16-wide requant stay inside the workgroup.
 // reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
 // Shared workgroups: 32 rows of the Q8_0 shared gate/up, SwiGLU, per-32 requant.
 // reference: launch_gemm_q8p x2 + silu_mul_quant32_multi (src/wzy_stage_v2.cuh:711-713;
-// src/wzy_kernels_v2.cuh:1247-1280).  Workgroup 0 also publishes the routing for moe_down.
+// src/wzy_kernels_v2.cuh:1247-1280).
 // ---------------------------------------------------------------------------------------------
 template <int T>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
-    __shared__ RouteLds r;
     __shared__ float s_act[WZY_MAX_W][32];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bid = blockIdx.x;
     const int D = a.D, F = a.F, K = a.K;
-    const bool routed = bid < a.n_routed_wg;
-    const int tiles = F / 16;
-    const int g = routed ? bid / tiles : 0;
-    if (routed && g >= T * K) return;
 
-    route_window(a.logits, a.E, K, T, r);
-    if (bid == 0) {
-        const int n_ent = T * K;
-        for (int i = tid; i < n_ent; i += blockDim.x) {
-            a.ids[i] = r.ids[i];
-            a.wts[i] = r.w[i];
-            a.grp_exp[i] = i < r.n_groups ? r.gexp[i] : 0;
-            a.grp_cnt[i] = i < r.n_groups ? r.gcnt[i] : 0;
-            for (int m = 0; m < WZY_MAX_W; ++m) a.grp_mem[i * WZY_MAX_W + m] = (i < r.n_groups && m < r.gcnt[i]) ? r.gmem[i][m] : 0;
-        }
-        if (tid == 0) *a.n_groups = r.n_groups;
-    }
-
-    if (routed) {
-        const int jt = bid - g * tiles;
-        if (g >= r.n_groups) return;
-        const int e = r.gexp[g], cnt = r.gcnt[g];
+    if (bid < a.n_routed_wg) {
+        const int tiles = F / 16;
+        const int g = bid / tiles, jt = bid - g * tiles;
+        if (g >= *a.n_groups) return;                 // workgroup-uniform
+        const int e = a.grp_exp[g], cnt = a.grp_cnt[g];
+        int mem[T];
+#pragma unroll
+        for (int m = 0; m < T; ++m) mem[m] = m < cnt ? a.grp_mem[g * WZY_MAX_W + m] : 0;
         const MoeOffsets o = moe_offsets(D, F);
         const uint8_t* rec = a.experts + (size_t) e * o.rec;
         const float sc_gate = ((const float*) (rec + o.tail))[0];
@@ -263,8 +334,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             float xsa[T], xsb[T];
 #pragma unroll
             for (int m = 0; m < T; ++m)
-                if (m < cnt)
-                    quant16x2_lane(a.x + (size_t) (r.gmem[g][m] / K) * D + (size_t) c * 32, xa[m], xb[m], xsa[m], xsb[m]);
+                if (m < cnt) quant16x2_lane(a.x + (size_t) (mem[m] / K) * D + (size_t) c * 32, xa[m], xb[m], xsa[m], xsb[m]);
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int4 wa = e2m1_sub16((uint32_t) code[rr].x, (uint32_t) code[rr].y);
@@ -294,7 +364,9 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             const float d = amax / 127.0f;
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
-            const int f = r.gmem[g][m];
+            int f = 0;
+#pragma unroll
+            for (int mm = 0; mm < T; ++mm) if (mm == m) f = mem[mm];
             a.aq16[(size_t) f * F + jt * 16 + jj] = (int8_t) q;
             if (jj == 0) a.as16[(size_t) f * (F / 16) + jt] = d;
         }
@@ -359,91 +431,117 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// down + combine.  Workgroup = 16 output rows for every group and the shared expert, so the
+// down + combine.  Workgroup = DN_TILE output rows for every group and the shared expert, so the
 // combine comb = sigmoid(sgate)*shared + sum_k w_k * part_k (routed-slot order) stays in LDS.
-// Work items (group, quad of 4 rows) are dealt round-robin to the 4 waves; 16 lanes per row.
+// Work items (group or shared, row) go round-robin to sixteen 16-lane slots; a slot issues the
+// loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
+// (F = 512: 16 chunks per row).
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
 // ---------------------------------------------------------------------------------------------
 template <int T>
 __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
-    __shared__ float s_part[WZY_MAX_W * MOE_MAX_K][TILE_D];
-    __shared__ float s_sh[WZY_MAX_W][TILE_D];
-    __shared__ int s_gexp[WZY_MAX_W * MOE_MAX_K], s_gcnt[WZY_MAX_W * MOE_MAX_K];
-    __shared__ int s_gmem[WZY_MAX_W * MOE_MAX_K][WZY_MAX_W];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float s_part[MAX_ENT][DN_TILE];
+    __shared__ float s_sh[WZY_MAX_W][DN_TILE];
+    __shared__ int s_gexp[MAX_ENT], s_gcnt[MAX_ENT];
+    __shared__ int s_gmem[MAX_ENT][WZY_MAX_W];
+    const int tid = threadIdx.x;
     const int D = a.D, F = a.F, K = a.K;
-    const int d0 = blockIdx.x * TILE_D;
+    const int d0 = blockIdx.x * DN_TILE;
     const int ng = *a.n_groups;
     for (int i = tid; i < ng; i += blockDim.x) {
         s_gexp[i] = a.grp_exp[i];
         s_gcnt[i] = a.grp_cnt[i];
+#pragma unroll
         for (int m = 0; m < WZY_MAX_W; ++m) s_gmem[i][m] = a.grp_mem[i * WZY_MAX_W + m];
     }
     __syncthreads();
     const MoeOffsets o = moe_offsets(D, F);
-    const int li = lane & 15, rq = lane >> 4;
-    const int n_items = (ng + 1) * (TILE_D / 4);   // +1: shared expert
-    for (int item = w; item < n_items; item += 4) {
-        const int g = item / (TILE_D / 4), quad = item % (TILE_D / 4);
-        const int rl = quad * 4 + rq;                // local row
-        const int d = d0 + rl;
-        if (g < ng) {
-            const int e = s_gexp[g], cnt = s_gcnt[g];
-            const uint8_t* rec = a.experts + (size_t) e * o.rec;
-            const float sc_down = ((const float*) (rec + o.tail))[2];
-            float acc[T];
+    const int slot = tid >> 4, li = tid & 15;
+    const int nchunk = F / 32;
+    const int n_items = (ng + 1) * DN_TILE;          // group ng = shared expert
+    for (int i0 = slot; i0 < n_items; i0 += 16 * DN_BATCH) {
+        float acc[DN_BATCH][T];
+        float sdn[DN_BATCH];
 #pragma unroll
-            for (int m = 0; m < T; ++m) acc[m] = 0.f;
-            for (int c = li; c < F / 32; c += 16) {
-                const int4 code = ld_stream_i4(rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16);
-                const uint32_t s2 = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
-                const int4 wa = e2m1_sub16((uint32_t) code.x, (uint32_t) code.y);
-                const int4 wb = e2m1_sub16((uint32_t) code.z, (uint32_t) code.w);
-                const float wsa = ue4m3_half(s2 & 0xFFu), wsb = ue4m3_half(s2 >> 8);
+        for (int b = 0; b < DN_BATCH; ++b) {
+            sdn[b] = 0.f;
 #pragma unroll
-                for (int m = 0; m < T; ++m) {
-                    if (m < cnt) {
-                        const int f = s_gmem[g][m];
-                        const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
-                        const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
-                        acc[m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xp[0], xp[1], xs.x, xs.y, acc[m]);
+            for (int m = 0; m < T; ++m) acc[b][m] = 0.f;
+        }
+        for (int c = li; c < nchunk; c += 16) {
+            int4 c0[DN_BATCH], c1[DN_BATCH];
+            float wsa[DN_BATCH], wsb[DN_BATCH];
+#pragma unroll
+            for (int b = 0; b < DN_BATCH; ++b) {
+                const int item = i0 + 16 * b;
+                c0[b] = c1[b] = make_int4(0, 0, 0, 0);
+                wsa[b] = wsb[b] = 0.f;
+                if (item < n_items) {
+                    const int g = item / DN_TILE, d = d0 + item % DN_TILE;
+                    if (g < ng) {
+                        const uint8_t* rec = a.experts + (size_t) s_gexp[g] * o.rec;
+                        c0[b] = ld_stream_i4(rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16);
+                        const uint32_t s2 = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
+                        wsa[b] = ue4m3_half(s2 & 0xFFu);
+                        wsb[b] = ue4m3_half(s2 >> 8);
+                        sdn[b] = ((const float*) (rec + o.tail))[2];
+                    } else {
+                        const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
+                        c0[b] = ld_stream_i4(cp);
+                        c1[b] = ld_stream_i4(cp + 1);
+                        wsa[b] = h16_to_f(a.shd_s[(size_t) d * nchunk + c]);
                     }
                 }
             }
 #pragma unroll
+            for (int b = 0; b < DN_BATCH; ++b) {
+                const int item = i0 + 16 * b;
+                if (item >= n_items) continue;
+                const int g = item / DN_TILE;
+                if (g < ng) {
+                    const int4 wa = e2m1_sub16((uint32_t) c0[b].x, (uint32_t) c0[b].y);
+                    const int4 wb = e2m1_sub16((uint32_t) c0[b].z, (uint32_t) c0[b].w);
+                    const int cnt = s_gcnt[g];
+#pragma unroll
+                    for (int m = 0; m < T; ++m) {
+                        if (m < cnt) {
+                            const int f = s_gmem[g][m];
+                            const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
+                            const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
+                            acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa[b], wsb[b], xp[0], xp[1], xs.x, xs.y, acc[b][m]);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) c * 32);
+                        const float xsc = a.shs32[(size_t) t * nchunk + c];
+                        acc[b][t] = fmaf(wsa[b] * xsc, (float) (dot16(c0[b], xp[0]) + dot16(c1[b], xp[1])), acc[b][t]);
+                    }
+                }
+            }
+        }
+        // 16-lane sums (every lane of a slot holds the same item, so the groups are uniform)
+#pragma unroll
+        for (int b = 0; b < DN_BATCH; ++b) {
+            const int item = i0 + 16 * b;
+            const bool valid = item < n_items;
+            const int g = valid ? item / DN_TILE : 0, rl = item % DN_TILE;
+            const int cnt = (valid && g < ng) ? s_gcnt[g] : T;
+#pragma unroll
             for (int m = 0; m < T; ++m) {
-                if (m < cnt) {
-                    const float v = sum16(acc[m]) * sc_down;
-                    if (li == 0) s_part[s_gmem[g][m]][rl] = v;
+                const float v = sum16(acc[b][m]);
+                if (li == 0 && valid && m < cnt) {
+                    if (g < ng) s_part[s_gmem[g][m]][rl] = v * sdn[b];
+                    else s_sh[m][rl] = v;
                 }
-            }
-        } else {
-            const int nb = F / 32;
-            float acc[T];
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = 0.f;
-            for (int b = li; b < nb; b += 16) {
-                const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) b * 32);
-                const int4 c0 = ld_stream_i4(cp), c1 = ld_stream_i4(cp + 1);
-                const float dw = h16_to_f(a.shd_s[(size_t) d * nb + b]);
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) b * 32);
-                    const float xsc = a.shs32[(size_t) t * nb + b];
-                    acc[t] = fmaf(dw * xsc, (float) (dot16(c0, xp[0]) + dot16(c1, xp[1])), acc[t]);
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float v = sum16(acc[t]);
-                if (li == 0) s_sh[t][rl] = v;
             }
         }
     }
     __syncthreads();
-    if (tid < T * TILE_D) {
-        const int t = tid / TILE_D, rl = tid % TILE_D;
+    if (tid < T * DN_TILE) {
+        const int t = tid / DN_TILE, rl = tid % DN_TILE;
         float s = s_sh[t][rl] * sigmoidf_(a.sg[t]);
         for (int k = 0; k < K; ++k) {
             const float wk = a.wts[t * K + k];
@@ -470,6 +568,7 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
     w.grp_exp = a.take<int>(n_ent);
     w.grp_cnt = a.take<int>(n_ent);
     w.grp_mem = a.take<int>((size_t) n_ent * WZY_MAX_W);
+    w.counter = a.take<unsigned int>(1);
     w.aq16 = a.take<int8_t>((size_t) n_ent * F);
     w.as16 = a.take<float>((size_t) n_ent * F / 16);
     w.shq32 = a.take<int8_t>((size_t) T * F);
@@ -492,20 +591,38 @@ int moe_check(const wzy_moe_weights* w, int T) {
     return WZY_OK;
 }
 
+template <int T>
+static void launch_rt_t(const MoeRtArgs& a, hipStream_t st) {
+    const int blocks = (a.E + 1 + 15) / 16;
+    hipLaunchKernelGGL((moe_router_kernel<T>), dim3(blocks), dim3(256), 0, st, a);
+}
+
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st) {
-    GemvSegs segs;
-    segs.n = 2;
-    segs.seg[0] = GemvSeg{w->router, nullptr, ws.logits, w->n_exp, GEMV_BF16, 0, 0};
-    segs.seg[1] = GemvSeg{w->sgate, nullptr, ws.sg, 1, GEMV_BF16, 1, 0};
-    return launch_gemv_segs(segs, x, w->n_embd, T, st);
+    MoeRtArgs a{};
+    a.router = w->router; a.sgate = w->sgate; a.x = x; a.D = w->n_embd; a.E = w->n_exp; a.K = w->top_k;
+    a.logits = ws.logits; a.sg = ws.sg; a.ids = ws.ids; a.wts = ws.wts;
+    a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
+    a.counter = ws.counter;
+    switch (T) {
+        case 1: launch_rt_t<1>(a, st); break;
+        case 2: launch_rt_t<2>(a, st); break;
+        case 3: launch_rt_t<3>(a, st); break;
+        case 4: launch_rt_t<4>(a, st); break;
+        case 5: launch_rt_t<5>(a, st); break;
+        case 6: launch_rt_t<6>(a, st); break;
+        case 7: launch_rt_t<7>(a, st); break;
+        default: launch_rt_t<8>(a, st); break;
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
 }
 
 static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T) {
     MoeGuArgs a{};
-    a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.E = w->n_exp; a.K = w->top_k;
-    a.logits = ws.logits; a.x = x;
-    a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt;
-    a.grp_mem = ws.grp_mem; a.aq16 = ws.aq16; a.as16 = ws.as16;
+    a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.K = w->top_k;
+    a.x = x;
+    a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
+    a.aq16 = ws.aq16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shq32 = ws.shq32; a.shs32 = ws.shs32;
     a.n_routed_wg = (w->n_ff / 16) * T * w->top_k;
@@ -526,7 +643,7 @@ static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
 }
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((moe_down_kernel<T>), dim3(a.D / TILE_D), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((moe_down_kernel<T>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
 }
 
 static void launch_gu(const MoeGuArgs& a, int T, hipStream_t st) {
@@ -573,6 +690,7 @@ extern "C" int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, fl
                              void* workspace, size_t workspace_bytes, void* stream) {
     WZY_TRY(moe_check(w, T));
     WZY_REQUIRE(x && comb && workspace, "wzy_moe_block: null pointer");
+    WZY_REQUIRE(w->n_embd % DN_TILE == 0, "wzy_moe_block: n_embd must be a multiple of %d", DN_TILE);
     size_t need = 0;
     MoeWs ws = moe_ws_carve(workspace, workspace_bytes, w->n_embd, w->n_ff, w->n_exp, w->top_k, T, &need);
     WZY_REQUIRE(need <= workspace_bytes, "wzy_moe_block: workspace too small (%zu < %zu)", workspace_bytes, need);

@@ -1,4 +1,4 @@
-// qsa.hip -- QSA sparse-attention decode kernels for gfx950.
+// qsa.hip -- QSA sparse-attention decode: per-row preparation and indexer block scores (gfx950).
 //
 //  qsa_prep   one launch, workgroup roles: q heads (RMSNorm + NeoX RoPE on the first n_rot dims),
 //             kv heads (same on k, then per-64 INT8 quantisation of k and v into the KV store),
@@ -11,13 +11,7 @@
 //             Keys are stored as fp16 (the reference rounds its fp32 keys to fp16 when scoring), so
 //             the scan reads 256 bytes per block.
 //             reference: pf_qsa_block_scores_wmma, pf_qsa_tail_score_kernel (src/wzy_qsa_wmma.cuh:492-612)
-//  qsa_topk   exact top-`topk` cells: 4 x 8-bit radix select over order-preserving keys of the block
-//             scores with block weights, ties at the threshold filled in the reference's
-//             256-thread-strided order.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
-//  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, row) computes
-//             the 12 GQA heads' scores from INT8 K, local softmax and the INT8 V sum; qsa_combine
-//             merges the chunks and applies sigmoid(gate).
-//             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532)
+// Selection and attention live in qsa_attn.hip.
 #include "wzy_device.h"
 #include "wzy_host.h"
 #include "wzy_qsa.h"
@@ -27,13 +21,6 @@ using namespace wzy;
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 namespace {
-
-WZY_DEV size_t kv_slot(int p, const QsaDims& dm) {
-    if (dm.ring_cap <= 0) return (size_t) p;
-    if (dm.ring_cap <= 2 * dm.sinks) return (size_t) (p % dm.ring_cap);
-    if (p < dm.sinks) return (size_t) p;
-    return (size_t) (dm.sinks + (p - dm.sinks) % (dm.ring_cap - dm.sinks));
-}
 
 // RMSNorm(gamma) + NeoX RoPE (pairs i, i + n_rot/2) of one head vector p[0..hd) in place.
 // 256 threads, thread i owns element i.
@@ -98,7 +85,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
                 const float kdq = h16_to_f(kh), vdq = h16_to_f(vh);
                 const int kqi = kdq > 0.f ? max(-127, min(127, rn_int(kv / kdq))) : 0;
                 const int vqi = vdq > 0.f ? max(-127, min(127, rn_int(vv / vdq))) : 0;
-                const size_t slot = kv_slot(pos, dm);
+                const size_t slot = qsa_kv_slot(pos, dm);
                 a.kv.kq[slot * kvd + (size_t) j * hd + tid] = (int8_t) kqi;
                 a.kv.vq[slot * kvd + (size_t) j * hd + tid] = (int8_t) vqi;
                 if (lane == 0) {
@@ -174,7 +161,7 @@ constexpr int SC_BLOCKS_PER_WG = 64;
 
 template <int T>
 __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
-    __shared__ h2_t s_q[T][4][64];          // fp16 indexer queries, ih <= 4, idim <= 128
+    __shared__ h2_t s_q[T][4][64];          // fp16 indexer queries, ih <= 4, idim = 128
     const QsaDims& dm = a.dm;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int base = *a.pos;
@@ -240,228 +227,13 @@ __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// exact top-k cell selection (one 256-thread workgroup per row)
-// ---------------------------------------------------------------------------------------------
-WZY_DEV uint32_t order_key(float s) {
-    const float v = s + 0.0f;                       // -0 -> +0
-    if (!(v == v)) return 0u;                       // NaN sorts lowest
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Inclusive prefix sum over the 256 threads in thread order (4 waves), result per thread.
-WZY_DEV int block_scan_incl(int v, int* s_w) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
-    if (lane == 63) s_w[w] = x;
-    __syncthreads();
-    int before = 0;
-    for (int i = 0; i < w; ++i) before += s_w[i];
-    __syncthreads();
-    return x + before;
-}
-
-__global__ void __launch_bounds__(256) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
-                                                       const float* __restrict__ scores, int max_b,
-                                                       int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
-    __shared__ int hist[256];
-    __shared__ int s_digit, s_above;
-    __shared__ int s_w[4];
-    const int t = threadIdx.x;
-    const int row = blockIdx.x;
-    const int n_kv = *pos_dev + row + 1;
-    const int K = dm.topk, B = dm.iblk;
-    const int width = min(n_kv, K);
-    int* out = sel_ids + (size_t) row * K;
-    if (t == 0) sel_cnt[row] = width;
-    if (n_kv <= K) {
-        for (int j = t; j < n_kv; j += 256) out[j] = j;
-        return;
-    }
-    const int n_bid = n_kv / B;
-    const int nb = n_bid + 1;
-    const float* sc = scores + (size_t) row * max_b;
-    auto weight = [&](int b) { return b < n_bid ? B : (n_kv - n_bid * B); };
-
-    uint32_t prefix = 0;
-    int above = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[t] = 0;
-        __syncthreads();
-        const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
-        for (int b = t; b < nb; b += 256) {
-            const int wgt = weight(b);
-            if (wgt == 0) continue;
-            const uint32_t k = order_key(sc[b]);
-            if ((k & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(k >> shift) & 255u], wgt);
-        }
-        __syncthreads();
-        if (t == 0) {
-            int cum = above, dg = 255;
-            for (; dg > 0; --dg) {
-                if (cum + hist[dg] >= width) break;
-                cum += hist[dg];
-            }
-            s_digit = dg;
-            s_above = cum;
-        }
-        __syncthreads();
-        prefix |= (uint32_t) s_digit << shift;
-        above = s_above;
-        __syncthreads();
-    }
-
-    // weights strictly above the threshold key, and at it, per thread (thread-strided blocks)
-    const uint32_t thr = prefix;
-    const int eq_budget = width - above;
-    int gt = 0, eq = 0;
-    for (int b = t; b < nb; b += 256) {
-        const int wgt = weight(b);
-        if (wgt == 0) continue;
-        const uint32_t k = order_key(sc[b]);
-        if (k > thr) gt += wgt;
-        else if (k == thr) eq += wgt;
-    }
-    const int eq_excl = block_scan_incl(eq, s_w) - eq;
-    const int my_eq = max(0, min(eq, eq_budget - eq_excl));
-    const int sel = gt + my_eq;
-    int wpos = block_scan_incl(sel, s_w) - sel;
-    int eq_left = my_eq;
-    for (int b = t; b < nb; b += 256) {
-        const int wgt = weight(b);
-        if (wgt == 0) continue;
-        const uint32_t k = order_key(sc[b]);
-        if (k > thr) {
-            for (int c = 0; c < wgt; ++c) out[wpos++] = b * B + c;
-        } else if (k == thr && eq_left > 0) {
-            const int take = min(wgt, eq_left);
-            for (int c = 0; c < take; ++c) out[wpos++] = b * B + c;
-            eq_left -= take;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// sparse attention
-// ---------------------------------------------------------------------------------------------
-constexpr int ATT_GQ_MAX = 16;
-
-__global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
-    __shared__ float s_q[ATT_GQ_MAX][256];
-    __shared__ float s_sc[ATT_GQ_MAX][QSA_ATT_CHUNK];
-    __shared__ size_t s_slot[QSA_ATT_CHUNK];
-    const QsaDims& dm = a.dm;
-    const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int hd = dm.hd, kvd = dm.kvh * hd, gq = dm.qh / dm.kvh;
-    const int n_kv = *a.pos + t + 1;
-    const int width = min(n_kv, dm.topk);
-    const int c0 = c * QSA_ATT_CHUNK;
-    if (c0 >= width) return;
-    const int ncell = min(QSA_ATT_CHUNK, width - c0);
-    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-
-    for (int i = tid; i < gq * hd; i += blockDim.x) {
-        const int hh = i / hd, d = i % hd;
-        s_q[hh][d] = a.qg[(size_t) t * dm.qh * 2 * hd + (size_t) (j * gq + hh) * 2 * hd + d];
-    }
-    if (tid < QSA_ATT_CHUNK) {
-        const int idx = c0 + tid;
-        const int p = tid < ncell ? (n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx]) : 0;
-        s_slot[tid] = kv_slot(p, dm);
-    }
-    __syncthreads();
-
-    // scores: 16 lanes per cell (16 dims each), 4 cells per wave-iteration
-    const int li = lane & 15;
-    const int g = (16 * li) / 64;
-    for (int it = 0; it < QSA_ATT_CHUNK / 16; ++it) {
-        const int cell = w * 16 + it * 4 + (lane >> 4);
-        const bool valid = cell < ncell;
-        int4 kr = make_int4(0, 0, 0, 0);
-        float ksc = 0.f;
-        if (valid) {
-            kr = *(const int4*) (a.kv.kq + s_slot[cell] * kvd + (size_t) j * hd + 16 * li);
-            ksc = h16_to_f(a.kv.ks[s_slot[cell] * (kvd / 64) + (size_t) j * (hd / 64) + g]);
-        }
-        float kf[16];
-        const int8_t* kb = (const int8_t*) &kr;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) kf[k] = (float) kb[k];
-        for (int hh = 0; hh < gq; ++hh) {
-            float p = 0.f;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) p = fmaf(kf[k], s_q[hh][16 * li + k], p);
-            p = sum16(p * ksc);
-            if (li == 0) s_sc[hh][cell] = valid ? p * 0.0625f : -INFINITY;
-        }
-    }
-    __syncthreads();
-    // local softmax per head: wave w handles heads w, w+4, ...; lane = cell
-    float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 2;
-    for (int hh = w; hh < gq; hh += 4) {
-        const float s = s_sc[hh][lane];
-        const float m = wave_max(s);
-        const float e = lane < ncell ? __expf(s - m) : 0.f;
-        const float l = wave_sum(e);
-        s_sc[hh][lane] = e;
-        if (lane == 0) { ml[hh * 2] = m; ml[hh * 2 + 1] = l; }
-    }
-    __syncthreads();
-    // V: thread d owns output dim d for all gq heads
-    if (tid < hd) {
-        float acc[ATT_GQ_MAX];
-#pragma unroll
-        for (int hh = 0; hh < ATT_GQ_MAX; ++hh) acc[hh] = 0.f;
-        const int gv = tid / 64;
-        for (int cell = 0; cell < ncell; ++cell) {
-            const size_t sl = s_slot[cell];
-            const float vsc = h16_to_f(a.kv.vs[sl * (kvd / 64) + (size_t) j * (hd / 64) + gv]);
-            const float v = (float) a.kv.vq[sl * kvd + (size_t) j * hd + tid];
-#pragma unroll
-            for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
-                if (hh < gq) acc[hh] = fmaf(s_sc[hh][cell] * vsc, v, acc[hh]);
-        }
-        float* po = a.part + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * hd;
-        for (int hh = 0; hh < gq; ++hh) po[(size_t) hh * hd + tid] = acc[hh];
-    }
-}
-
-__global__ void __launch_bounds__(256) qsa_combine_kernel(QsaAttnArgs a) {
-    const QsaDims& dm = a.dm;
-    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-    const int hd = dm.hd, gq = dm.qh / dm.kvh, j = h / gq, hh = h % gq;
-    const int n_kv = *a.pos + t + 1;
-    const int width = min(n_kv, dm.topk);
-    const int nch_all = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-    const int nch = (width + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-    const float* ml = a.part_ml + (((size_t) t * dm.kvh + j) * nch_all) * gq * 2;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, ml[((size_t) c * gq + hh) * 2]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < nch; ++c) {
-        const float f = __expf(ml[((size_t) c * gq + hh) * 2] - M);
-        L = fmaf(ml[((size_t) c * gq + hh) * 2 + 1], f, L);
-        if (d < hd) O = fmaf(a.part[((((size_t) t * dm.kvh + j) * nch_all + c) * gq + hh) * hd + d], f, O);
-    }
-    if (d < hd) {
-        const float gate = a.qg[(size_t) t * dm.qh * 2 * hd + (size_t) h * 2 * hd + hd + d];
-        a.out[(size_t) t * dm.qh * hd + (size_t) h * hd + d] = (O * (1.0f / L)) / (1.0f + __expf(-gate));
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------------------------
 namespace wzy {
 
-static int check_dims(const QsaDims& dm) {
-    WZY_REQUIRE(dm.hd == 256 && dm.qh % dm.kvh == 0 && dm.qh / dm.kvh <= ATT_GQ_MAX, "qsa: head layout unsupported");
+int qsa_check_dims(const QsaDims& dm) {
+    WZY_REQUIRE(dm.hd == 256 && dm.kvh >= 1 && dm.qh % dm.kvh == 0 && dm.qh / dm.kvh <= 16,
+                "qsa: head layout unsupported (hd 256, at most 16 q heads per kv head)");
     WZY_REQUIRE(dm.idim <= 128 && dm.idim % 8 == 0 && dm.ih <= 4 && dm.iblk >= 2, "qsa: indexer layout unsupported");
     WZY_REQUIRE(dm.n_rot % 2 == 0 && dm.n_rot <= dm.idim && dm.n_rot <= dm.hd, "qsa: bad n_rot");
     WZY_REQUIRE(dm.topk >= 1 && dm.ctx_max >= 1, "qsa: bad topk/ctx");
@@ -469,7 +241,7 @@ static int check_dims(const QsaDims& dm) {
 }
 
 int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
-    WZY_TRY(check_dims(a.dm));
+    WZY_TRY(qsa_check_dims(a.dm));
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_prep: T out of range");
     const int n_wg = a.dm.qh + a.dm.kvh + a.dm.ih + 1;
     hipLaunchKernelGGL(qsa_prep_kernel, dim3(n_wg), dim3(256), 0, st, a, T);
@@ -478,7 +250,7 @@ int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
 }
 
 int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
-    WZY_TRY(check_dims(a.dm));
+    WZY_TRY(qsa_check_dims(a.dm));
     WZY_REQUIRE(a.dm.idim == 128, "qsa_score: indexer key width must be 128");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_score: T out of range");
     const int grid = (a.max_b + SC_BLOCKS_PER_WG - 1) / SC_BLOCKS_PER_WG;
@@ -492,40 +264,16 @@ int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
     return WZY_OK;
 }
 
-int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
-                    int T, hipStream_t st) {
-    WZY_TRY(check_dims(dm));
-    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_topk: T out of range");
-    hipLaunchKernelGGL(qsa_topk_kernel, dim3(T), dim3(256), 0, st, dm, pos, scores, max_b, sel_ids, sel_cnt);
-    WZY_LAUNCH_CHECK();
-    return WZY_OK;
-}
-
-size_t qsa_attn_part_floats(const QsaDims& dm, int T) {
-    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-    return (size_t) T * dm.kvh * nch * dm.qh / dm.kvh * dm.hd;
-}
-
-int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st) {
-    WZY_TRY(check_dims(a.dm));
-    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_attn: T out of range");
-    const int nch = (a.dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-    hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh, T), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(qsa_combine_kernel, dim3(a.dm.qh, T), dim3(256), 0, st, a);
-    WZY_LAUNCH_CHECK();
-    return WZY_OK;
-}
-
 }  // namespace wzy
 
 // ---------------------------------------------------------------------------------------------
 // C ABI (device pointers; `pos` is a device int holding the position of row 0)
 // ---------------------------------------------------------------------------------------------
-static QsaDims dims_of(int qh, int kvh, int hd, int n_rot, int ih, int idim, int iblk, int topk, int ctx_max,
-                       int ring_cap, int sinks, float eps) {
+static QsaDims dims_of(const wzy_qsa_dims* s) {
     QsaDims d;
-    d.qh = qh; d.kvh = kvh; d.hd = hd; d.n_rot = n_rot; d.ih = ih; d.idim = idim; d.iblk = iblk; d.topk = topk;
-    d.ctx_max = ctx_max; d.ring_cap = ring_cap; d.sinks = sinks; d.eps = eps;
+    d.qh = s->qh; d.kvh = s->kvh; d.hd = s->hd; d.n_rot = s->n_rot;
+    d.ih = s->idx_heads; d.idim = s->idx_dim; d.iblk = s->idx_blk; d.topk = s->idx_topk;
+    d.ctx_max = s->ctx_max; d.ring_cap = s->kv_ring; d.sinks = s->kv_sinks; d.eps = s->eps;
     return d;
 }
 
@@ -538,8 +286,7 @@ extern "C" int wzy_qsa_prepare(const wzy_qsa_dims* dims, const int* pos, float* 
                     idx_pooled && cos_tab && sin_tab && q_norm && k_norm && iq_norm && ik_norm,
                 "wzy_qsa_prepare: null pointer");
     QsaPrepArgs a{};
-    a.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
-                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    a.dm = dims_of(dims);
     a.pos = pos; a.qg = qg; a.kk = kk; a.vv = vv; a.q_idx = q_idx; a.idx_raw = idx_raw;
     a.q_norm = q_norm; a.k_norm = k_norm; a.iq_norm = iq_norm; a.ik_norm = ik_norm;
     a.cos_tab = cos_tab; a.sin_tab = sin_tab;
@@ -554,8 +301,7 @@ extern "C" int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const ui
     WZY_REQUIRE(dims && pos && idx_pooled && idx_dead && q_idx && scores && sel_ids && sel_cnt,
                 "wzy_qsa_select: null pointer");
     QsaScoreArgs s{};
-    s.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
-                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    s.dm = dims_of(dims);
     WZY_REQUIRE(max_b >= dims->ctx_max / dims->idx_blk + 1, "wzy_qsa_select: max_b too small");
     s.pos = pos; s.pooled = idx_pooled; s.dead = idx_dead; s.q_idx = q_idx; s.scores = scores; s.max_b = max_b;
     hipStream_t st = as_stream(stream);
@@ -564,8 +310,7 @@ extern "C" int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const ui
 }
 
 extern "C" size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T) {
-    QsaDims d = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
-                        dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    const QsaDims d = dims_of(dims);
     const size_t pf = qsa_attn_part_floats(d, T);
     return (pf + pf / d.hd * 2) * sizeof(float) + 512;
 }
@@ -577,8 +322,7 @@ extern "C" int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const fl
                 "wzy_qsa_attend: null pointer");
     WZY_REQUIRE(workspace_bytes >= wzy_qsa_attend_workspace_bytes(dims, T), "wzy_qsa_attend: workspace too small");
     QsaAttnArgs a{};
-    a.dm = dims_of(dims->qh, dims->kvh, dims->hd, dims->n_rot, dims->idx_heads, dims->idx_dim, dims->idx_blk,
-                   dims->idx_topk, dims->ctx_max, dims->kv_ring, dims->kv_sinks, dims->eps);
+    a.dm = dims_of(dims);
     a.pos = pos; a.qg = qg; a.kv = QsaKv{(int8_t*) kq, (uint16_t*) ks, (int8_t*) vq, (uint16_t*) vs};
     a.sel_ids = sel_ids; a.out = out;
     const size_t pf = qsa_attn_part_floats(a.dm, T);

@@ -1,0 +1,359 @@
+// qsa_attn.hip -- QSA cell selection and sparse attention for gfx950.
+//
+//  qsa_topk   exact top-`topk` cells of one row, one 1024-thread workgroup: the block scores are
+//             loaded once into registers as order-preserving keys, a 4 x 8-bit radix select finds
+//             the threshold key (LDS histogram per pass, parallel suffix scan over the 256 bins),
+//             then every block above the threshold is taken whole and blocks at the threshold are
+//             filled in the reference's tie order.  The reference walks the blocks with 256 threads,
+//             thread t owning blocks t, t+256, ... and emitting them thread-major; here thread
+//             4t+s owns the s-th quarter of thread t's blocks, so a scan in thread order reproduces
+//             that order exactly.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
+//  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, row) stages
+//             the chunk's INT8 K and V rows in LDS with one round of 128-bit loads, computes the
+//             GQA heads' scores (lane = cell), a local softmax, and the INT8 V sum (thread = dim).
+//  qsa_combine merges the chunks (max / sum rescaling) and applies sigmoid(gate).
+//             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532)
+#include "wzy_device.h"
+#include "wzy_host.h"
+#include "wzy_qsa.h"
+
+using namespace wzy;
+
+namespace {
+
+constexpr int TK_THREADS = 1024;
+constexpr int TK_MAXJ_SMALL = 16;    // blocks per thread: 16384 blocks (65532 cells at 4 per block)
+constexpr int TK_MAXJ_LARGE = 66;    // 67584 blocks (270332 cells); keys partly spill to scratch
+constexpr int ATT_GQ_MAX = 16;       // q heads per kv head
+constexpr int ATT_ROW = 256 + 16;    // LDS bytes per cell row (hd = 256 codes + pad against bank conflicts)
+constexpr int ATT_CH_MAX = 32;       // chunks per row: topk <= 2048
+
+WZY_DEV uint32_t order_key(float s) {
+    const float v = s + 0.0f;                       // -0 -> +0
+    if (!(v == v)) return 0u;                       // NaN sorts lowest
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inclusive prefix sum over the NW*64 threads in thread order; s_w holds NW ints.
+template <int NW>
+WZY_DEV int block_scan_incl(int v, int* s_w) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_w[w] = x;
+    __syncthreads();
+    int before = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) before += (i < w) ? s_w[i] : 0;
+    __syncthreads();
+    return x + before;
+}
+
+// Number of threads of the NW-wave workgroup with `pred` set (wave ballots summed in LDS).
+template <int NW>
+WZY_DEV int block_count(bool pred, int* s_c) {
+    const unsigned long long m = __ballot(pred);
+    if ((threadIdx.x & 63) == 0) s_c[threadIdx.x >> 6] = __popcll(m);
+    __syncthreads();
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) n += s_c[i];
+    __syncthreads();
+    return n;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// exact top-k cell selection, one workgroup per row; TK_MAXJ = blocks held per thread
+// ---------------------------------------------------------------------------------------------
+template <int TK_MAXJ>
+__global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
+                                                              const float* __restrict__ scores, int max_b,
+                                                              int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
+    __shared__ int hist[256];
+    __shared__ int s_w[TK_THREADS / 64];
+    __shared__ int s_c[TK_THREADS / 64];
+    __shared__ int s_digit, s_above;
+    const int p = threadIdx.x, row = blockIdx.x;
+    const int n_kv = *pos_dev + row + 1;
+    const int K = dm.topk, B = dm.iblk;
+    const int width = min(n_kv, K);
+    int* out = sel_ids + (size_t) row * K;
+    if (p == 0) sel_cnt[row] = width;
+    if (n_kv <= K) {                                 // short context: every cell, in order
+        for (int j = p; j < n_kv; j += TK_THREADS) out[j] = j;
+        return;
+    }
+    const int n_bid = n_kv / B, nb = min(n_bid + 1, max_b);   // complete blocks + the open block
+    const int tt = p >> 2, sub = p & 3;
+    const int J = (nb + 255) / 256, J4 = (J + 3) / 4;
+    const int j0 = sub * J4, j1 = min(J, j0 + J4);
+    const float* sc = scores + (size_t) row * max_b;
+
+    // weight (cells) of this thread's q-th block: B for complete blocks, the open block's fill, 0 past the end
+    auto wgt = [&](int q) -> int {
+        const int b = tt + 256 * (j0 + q);
+        return ((j0 + q) < j1 && b < nb) ? (b < n_bid ? B : n_kv - n_bid * B) : 0;
+    };
+    uint32_t key[TK_MAXJ];
+#pragma unroll
+    for (int q = 0; q < TK_MAXJ; ++q) {
+        const int b = tt + 256 * (j0 + q);
+        key[q] = ((j0 + q) < j1 && b < nb) ? order_key(sc[b]) : 0u;
+    }
+
+    uint32_t prefix = 0;
+    int above = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (p < 256) hist[p] = 0;
+        __syncthreads();
+        const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
+#pragma unroll
+        for (int q = 0; q < TK_MAXJ; ++q)
+            if (wgt(q) > 0 && (key[q] & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key[q] >> shift) & 255u], wgt(q));
+        __syncthreads();
+        // thread i < 256 takes digit 255 - i; S = weight of candidates with digit >= 255 - i
+        const int h = p < 256 ? hist[255 - p] : 0;
+        const int S = block_scan_incl<TK_THREADS / 64>(h, s_w);
+        const bool ok = p < 256 && above + S >= width;
+        const int n_ok = block_count<TK_THREADS / 64>(ok, s_c);
+        const int istar = n_ok > 0 ? 256 - n_ok : 255;   // first (highest) digit reaching the width
+        if (p == istar) {
+            s_digit = 255 - p;
+            s_above = above + S - h;
+        }
+        __syncthreads();
+        prefix |= (uint32_t) s_digit << shift;
+        above = s_above;
+        __syncthreads();
+    }
+
+    const uint32_t thr = prefix;
+    const int eq_budget = width - above;
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int q = 0; q < TK_MAXJ; ++q) {
+        const int wq = wgt(q);
+        if (wq == 0) continue;
+        if (key[q] > thr) gt += wq;
+        else if (key[q] == thr) eq += wq;
+    }
+    const int eq_excl = block_scan_incl<TK_THREADS / 64>(eq, s_w) - eq;
+    const int my_eq = max(0, min(eq, eq_budget - eq_excl));
+    const int sel = gt + my_eq;
+    int wpos = block_scan_incl<TK_THREADS / 64>(sel, s_w) - sel;
+    int eq_left = my_eq;
+#pragma unroll
+    for (int q = 0; q < TK_MAXJ; ++q) {
+        const int wq = wgt(q);
+        if (wq == 0) continue;
+        const int b = tt + 256 * (j0 + q);
+        if (key[q] > thr) {
+            for (int c = 0; c < wq; ++c) out[wpos++] = b * B + c;
+        } else if (key[q] == thr && eq_left > 0) {
+            const int take = min(wq, eq_left);
+            for (int c = 0; c < take; ++c) out[wpos++] = b * B + c;
+            eq_left -= take;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// sparse attention over one chunk of 64 selected cells
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
+    __shared__ __align__(16) int8_t s_k[QSA_ATT_CHUNK * ATT_ROW];
+    __shared__ __align__(16) int8_t s_v[QSA_ATT_CHUNK * ATT_ROW];
+    __shared__ float s_ks[QSA_ATT_CHUNK][4], s_vs[QSA_ATT_CHUNK][4];
+    __shared__ __align__(16) float s_q[ATT_GQ_MAX][256];
+    __shared__ float s_p[ATT_GQ_MAX][QSA_ATT_CHUNK];
+    __shared__ long long s_slot[QSA_ATT_CHUNK];
+    const QsaDims& dm = a.dm;
+    const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int kvd = dm.kvh * 256, gq = dm.qh / dm.kvh;
+    const int n_kv = *a.pos + t + 1;
+    const int width = min(n_kv, dm.topk);
+    const int c0 = c * QSA_ATT_CHUNK;
+    if (c0 >= width) return;                         // workgroup-uniform
+    const int ncell = min(QSA_ATT_CHUNK, width - c0);
+    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+
+    if (tid < QSA_ATT_CHUNK) {
+        const int idx = c0 + tid;
+        long long sl = -1;
+        if (tid < ncell) sl = (long long) qsa_kv_slot(n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx], dm);
+        s_slot[tid] = sl;
+    }
+    for (int i = tid; i < gq * 64; i += 256) {
+        const int hh = i >> 6, d4 = i & 63;
+        *(float4*) &s_q[hh][4 * d4] =
+            *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + hh) * 512 + 4 * d4);
+    }
+    __syncthreads();
+
+    // K and V rows of the chunk: 64 cells x 16 int4 each, 4 per thread, one round of loads
+    {
+        int4 kr[4], vr[4];
+        const int part = tid & 15;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const long long sl = s_slot[(tid >> 4) + 16 * k];
+            if (sl >= 0) {
+                const size_t off = (size_t) sl * kvd + (size_t) j * 256 + (size_t) part * 16;
+                kr[k] = *(const int4*) (a.kv.kq + off);
+                vr[k] = *(const int4*) (a.kv.vq + off);
+            } else {
+                kr[k] = vr[k] = make_int4(0, 0, 0, 0);
+            }
+        }
+        const int cs = tid >> 2, g = tid & 3;
+        const long long sls = s_slot[cs];
+        const float ksc = sls >= 0 ? h16_to_f(a.kv.ks[(size_t) sls * (kvd / 64) + (size_t) j * 4 + g]) : 0.f;
+        const float vsc = sls >= 0 ? h16_to_f(a.kv.vs[(size_t) sls * (kvd / 64) + (size_t) j * 4 + g]) : 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int cell = (tid >> 4) + 16 * k;
+            *(int4*) (s_k + cell * ATT_ROW + part * 16) = kr[k];
+            *(int4*) (s_v + cell * ATT_ROW + part * 16) = vr[k];
+        }
+        s_ks[cs][g] = ksc;
+        s_vs[cs][g] = vsc;
+    }
+    __syncthreads();
+
+    // scores and local softmax: lane = cell, wave w owns heads w, w+4, w+8, w+12
+    {
+        const int cell = lane;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float ag[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                const int part = 4 * g + pp;
+                const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
+                const int8_t* kb = (const int8_t*) &kv;
+                float kf[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) kf[e] = (float) kb[e];
+#pragma unroll
+                for (int hh = 0; hh < 4; ++hh) {
+                    const int h = w + 4 * hh;
+                    if (h < gq) {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) ag[hh] = fmaf(kf[e], s_q[h][part * 16 + e], ag[hh]);
+                    }
+                }
+            }
+            const float ks = s_ks[cell][g];
+#pragma unroll
+            for (int hh = 0; hh < 4; ++hh) acc[hh] = fmaf(ag[hh], ks, acc[hh]);
+        }
+        float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 2;
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+            const int h = w + 4 * hh;
+            if (h >= gq) break;                      // wave-uniform
+            const float s = cell < ncell ? acc[hh] * 0.0625f : -INFINITY;
+            const float m = wave_max(s);
+            const float e = cell < ncell ? __expf(s - m) : 0.f;
+            const float l = wave_sum(e);
+            s_p[h][cell] = e;
+            if (lane == 0) { ml[h * 2] = m; ml[h * 2 + 1] = l; }
+        }
+    }
+    __syncthreads();
+
+    // V: thread d owns output dim d for every head
+    {
+        const int d = tid;
+        float o[ATT_GQ_MAX];
+#pragma unroll
+        for (int hh = 0; hh < ATT_GQ_MAX; ++hh) o[hh] = 0.f;
+        for (int cell = 0; cell < ncell; ++cell) {
+            const float pv = (float) s_v[cell * ATT_ROW + d] * s_vs[cell][d >> 6];
+#pragma unroll
+            for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
+                if (hh < gq) o[hh] = fmaf(s_p[hh][cell], pv, o[hh]);
+        }
+        float* po = a.part + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 256;
+#pragma unroll
+        for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
+            if (hh < gq) po[(size_t) hh * 256 + d] = o[hh];
+    }
+}
+
+// merge the chunks of one (q head, row): thread d = output dim
+__global__ void __launch_bounds__(256) qsa_combine_kernel(QsaAttnArgs a) {
+    const QsaDims& dm = a.dm;
+    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x, lane = d & 63;
+    const int gq = dm.qh / dm.kvh, j = h / gq, hh = h % gq;
+    const int n_kv = *a.pos + t + 1;
+    const int width = min(n_kv, dm.topk);
+    const int nch_all = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    const int nch = (width + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    const size_t base = ((size_t) t * dm.kvh + j) * nch_all;
+    // chunk statistics: lane c holds chunk c
+    const float m_c = lane < nch ? a.part_ml[((base + lane) * gq + hh) * 2] : -INFINITY;
+    const float l_c = lane < nch ? a.part_ml[((base + lane) * gq + hh) * 2 + 1] : 0.f;
+    float part[ATT_CH_MAX];
+#pragma unroll
+    for (int c = 0; c < ATT_CH_MAX; ++c)
+        part[c] = c < nch ? a.part[((base + c) * gq + hh) * 256 + d] : 0.f;
+    const float M = wave_max(m_c);
+    const float f_c = lane < nch ? __expf(m_c - M) : 0.f;
+    const float L = wave_sum(l_c * f_c);
+    float O = 0.f;
+#pragma unroll
+    for (int c = 0; c < ATT_CH_MAX; ++c)
+        if (c < nch) O = fmaf(part[c], as_f(__builtin_amdgcn_readlane(as_i(f_c), c)), O);
+    const float gate = a.qg[(size_t) t * dm.qh * 512 + (size_t) h * 512 + 256 + d];
+    a.out[(size_t) t * dm.qh * 256 + (size_t) h * 256 + d] = (O * (1.0f / L)) / (1.0f + __expf(-gate));
+}
+
+// ---------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------
+namespace wzy {
+
+int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
+                    int T, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(dm));
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_topk: T out of range");
+    const int per_thread = ((max_b + 255) / 256 + 3) / 4;   // blocks a thread holds at the largest context
+    WZY_REQUIRE(per_thread <= TK_MAXJ_LARGE, "qsa_topk: %d indexer blocks exceed the selection capacity %d", max_b,
+                TK_THREADS * TK_MAXJ_LARGE);
+    if (per_thread <= TK_MAXJ_SMALL)
+        hipLaunchKernelGGL((qsa_topk_kernel<TK_MAXJ_SMALL>), dim3(T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b,
+                           sel_ids, sel_cnt);
+    else
+        hipLaunchKernelGGL((qsa_topk_kernel<TK_MAXJ_LARGE>), dim3(T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b,
+                           sel_ids, sel_cnt);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+size_t qsa_attn_part_floats(const QsaDims& dm, int T) {
+    const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    return (size_t) T * dm.kvh * nch * dm.qh / dm.kvh * dm.hd;
+}
+
+int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a.dm));
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_attn: T out of range");
+    WZY_REQUIRE(a.dm.topk <= ATT_CH_MAX * QSA_ATT_CHUNK, "qsa_attn: topk above %d", ATT_CH_MAX * QSA_ATT_CHUNK);
+    const int nch = (a.dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh, T), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(qsa_combine_kernel, dim3(a.dm.qh, T), dim3(256), 0, st, a);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+}  // namespace wzy

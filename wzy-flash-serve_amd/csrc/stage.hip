@@ -194,7 +194,7 @@ int wzy_stage::alloc_q8(Q8& m, int rows, int cols, int layer, const char* name) 
 static int validate(const wzy_stage_cfg& c) {
     WZY_REQUIRE(c.n_layers >= 1 && c.n_layers <= 4096 && c.qsa_period >= 1, "stage: bad layer count / period");
     WZY_REQUIRE(c.n_embd >= 256 && c.n_embd % 256 == 0 && c.n_embd <= 8192, "stage: n_embd must be a multiple of 256 <= 8192");
-    WZY_REQUIRE(c.hc >= 1 && c.hc <= 4 && c.hc_lr % 32 == 0 && c.hc_lr <= 512 && c.hc * c.n_embd <= 16384,
+    WZY_REQUIRE(c.hc == 4 && c.hc_lr % 32 == 0 && c.hc_lr >= 32 && c.hc_lr <= 512 && c.n_embd <= 4096,
                 "stage: bad hyper-connection shape");
     WZY_REQUIRE(c.gdn_hk >= 1 && c.gdn_hv % c.gdn_hk == 0, "stage: bad GDN heads");
     WZY_REQUIRE(c.qsa_hd == 256 && c.qsa_qh % c.qsa_kvh == 0 && c.qsa_qh / c.qsa_kvh <= 16, "stage: bad QSA heads");
@@ -339,6 +339,25 @@ int wzy_stage::init_buffers() {
     WZY_TRY(alloc_t(&logits, (size_t) W * c.n_vocab));
     WZY_TRY(alloc(&red_ws, reduce_ws_bytes(c.n_vocab, W)));
     WZY_TRY(alloc_t(&emb_rows, (size_t) W * D));
+    // activation buffers, readable after a forward (they hold the last layer that wrote them)
+    reg(-1, "act.mixed", mixed, (size_t) W * D * 4);
+    reg(-1, "act.block", block, (size_t) W * D * 4);
+    reg(-1, "act.comb", comb, (size_t) W * D * 4);
+    reg(-1, "act.qg", qg, (size_t) W * 2 * QD * 4);
+    reg(-1, "act.q_idx", q_idx, (size_t) W * c.idx_heads * c.idx_dim * 4);
+    reg(-1, "act.scores", scores, (size_t) W * max_b * 4);
+    reg(-1, "act.sel_ids", sel_ids, (size_t) W * c.idx_topk * 4);
+    reg(-1, "act.sel_cnt", sel_cnt, (size_t) W * 4);
+    reg(-1, "act.att_out", att_out, (size_t) W * QD * 4);
+    reg(-1, "act.y", y, (size_t) W * GV * 4);
+    reg(-1, "act.moe_logits", mws.logits, (size_t) W * c.n_exp * 4);
+    reg(-1, "act.moe_sg", mws.sg, (size_t) W * 4);
+    reg(-1, "act.moe_ids", mws.ids, (size_t) W * c.top_k * 4);
+    reg(-1, "act.moe_wts", mws.wts, (size_t) W * c.top_k * 4);
+    reg(-1, "act.moe_groups", mws.n_groups, 4);
+    reg(-1, "act.moe_grp_exp", mws.grp_exp, (size_t) W * c.top_k * 4);
+    reg(-1, "act.moe_grp_cnt", mws.grp_cnt, (size_t) W * c.top_k * 4);
+    reg(-1, "act.moe_grp_mem", mws.grp_mem, (size_t) W * c.top_k * WZY_MAX_W * 4);
     // speculative-window snapshots
     if (n_gdn > 0) {
         WZY_TRY(alloc_t(&conv_snaps, (size_t) n_gdn * W * QKV * 3));

@@ -15,7 +15,18 @@ struct QsaDims {
     float eps;
 };
 
-// KV store of one QSA layer: cells addressed by kv_slot(p)
+// Storage slot of context position p: the position itself for a full-context store; with a ring,
+// positions below `sinks` are pinned and the rest cycle through the remaining ring_cap - sinks slots.
+__device__ __forceinline__ size_t qsa_kv_slot(int p, const QsaDims& dm) {
+    if (dm.ring_cap <= 0) return (size_t) p;
+    if (dm.ring_cap <= 2 * dm.sinks) return (size_t) (p % dm.ring_cap);
+    if (p < dm.sinks) return (size_t) p;
+    return (size_t) (dm.sinks + (p - dm.sinks) % (dm.ring_cap - dm.sinks));
+}
+
+int qsa_check_dims(const QsaDims& dm);
+
+// KV store of one QSA layer: cells addressed by qsa_kv_slot(p)
 struct QsaKv {
     int8_t* kq; uint16_t* ks;          // [slots][KVD], [slots][KVD/64] fp16 bits
     int8_t* vq; uint16_t* vs;
