@@ -314,6 +314,28 @@ extern "C" int wzy_gemv_bf16(const uint16_t* W, const float* x, float* y, int ro
 // lane (same float operations as quant_act), so no separate quantisation launch is needed.
 // ---------------------------------------------------------------------------------------------
 namespace {
+WZY_DEV void quant32_v(const float4 (&xv)[8], int4& q0, int4& q1, float& d) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[4 * i] = xv[i].x; v[4 * i + 1] = xv[i].y; v[4 * i + 2] = xv[i].z; v[4 * i + 3] = xv[i].w;
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(v[i]));
+    d = am / 127.0f;
+    const float inv = d > 0.f ? 127.0f / am : 0.f;
+    int w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pk |= (uint32_t) (max(-127, min(127, rn_int(v[4 * k + j] * inv))) & 0xFF) << (8 * j);
+        w[k] = (int) pk;
+    }
+    q0 = make_int4(w[0], w[1], w[2], w[3]);
+    q1 = make_int4(w[4], w[5], w[6], w[7]);
+}
 WZY_DEV void quant32_f(const float* __restrict__ xp, int4& q0, int4& q1, float& d) {
     float v[32];
 #pragma unroll
@@ -357,54 +379,74 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
         for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
 
     if (sg.kind == GEMV_Q8) {
+        // Every load is issued before any of its results is used (indices are clamped into the
+        // matrix instead of branching, and the fp16 scales are converted afterwards), so the
+        // wave has all its weight bytes in flight at once.
         const int nb = cols >> 5;
         const int8_t* W = (const int8_t*) sg.w;
         int4 c0[NBL][RPW], c1[NBL][RPW];
-        float dw[NBL][RPW];
+        uint16_t sraw[NBL][RPW];
 #pragma unroll
         for (int i = 0; i < NBL; ++i) {
-            const int b = lane + 64 * i;
+            const int b = min(lane + 64 * i, nb - 1);
 #pragma unroll
             for (int s = 0; s < RPW; ++s) {
-                const int r = row0 + s;
-                if (b < nb && r < sg.rows) {
-                    const int4* cp = (const int4*) (W + (size_t) r * cols + (size_t) b * 32);
-                    c0[i][s] = ld_stream_i4(cp);
-                    c1[i][s] = ld_stream_i4(cp + 1);
-                    dw[i][s] = h16_to_f(sg.s[(size_t) r * nb + b]);
-                } else {
-                    c0[i][s] = c1[i][s] = make_int4(0, 0, 0, 0);
-                    dw[i][s] = 0.f;
-                }
+                const int r = min(row0 + s, sg.rows - 1);
+                const int4* cp = (const int4*) (W + (size_t) r * cols + (size_t) b * 32);
+                c0[i][s] = ld_stream_i4(cp);
+                c1[i][s] = ld_stream_i4(cp + 1);
+                sraw[i][s] = sg.s[(size_t) r * nb + b];
+            }
+        }
+        // single-row windows: the activations' loads join the weights' in flight
+        constexpr int TX = (T == 1) ? NBL : 1;
+        float4 xv[TX][8];
+        if (T == 1) {
+#pragma unroll
+            for (int i = 0; i < TX; ++i) {
+                const int b = min(lane + 64 * i, nb - 1);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) xv[i][k] = ((const float4*) (x + (size_t) b * 32))[k];
             }
         }
 #pragma unroll
         for (int i = 0; i < NBL; ++i) {
-            const int b = lane + 64 * i;
-            if (b >= nb) continue;
+            if (lane + 64 * i >= nb) continue;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 int4 x0, x1;
                 float xs;
-                quant32_f(x + (size_t) t * cols + (size_t) b * 32, x0, x1, xs);
+                if (T == 1) quant32_v(xv[T == 1 ? i : 0], x0, x1, xs);
+                else quant32_f(x + (size_t) t * cols + (size_t) (lane + 64 * i) * 32, x0, x1, xs);
 #pragma unroll
                 for (int s = 0; s < RPW; ++s)
-                    acc[s][t] = fmaf(dw[i][s] * xs, (float) (dot16(c1[i][s], x1) + dot16(c0[i][s], x0)), acc[s][t]);
+                    acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c1[i][s], x1) + dot16(c0[i][s], x0)),
+                                     acc[s][t]);
             }
         }
     } else {
         const uint16_t* W = (const uint16_t*) sg.w;
         const int n8 = cols >> 3;
         for (int j0 = 0; j0 < n8; j0 += 64 * 4) {
+            // all loads first (clamped indices, no branches), then the arithmetic
             uint4 wv[4][RPW];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int j = j0 + lane + 64 * u;
+                const int j = min(j0 + lane + 64 * u, n8 - 1);
 #pragma unroll
                 for (int s = 0; s < RPW; ++s) {
-                    const int r = row0 + s;
-                    wv[u][s] = (j < n8 && r < sg.rows) ? ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j)
-                                                       : make_uint4(0, 0, 0, 0);
+                    const int r = min(row0 + s, sg.rows - 1);
+                    wv[u][s] = ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j);
+                }
+            }
+            constexpr int TX = (T == 1) ? 4 : 1;
+            float4 xr[TX][2];
+            if (T == 1) {
+#pragma unroll
+                for (int u = 0; u < TX; ++u) {
+                    const int j = min(j0 + lane + 64 * u, n8 - 1);
+                    xr[u][0] = *(const float4*) (x + j * 8);
+                    xr[u][1] = *(const float4*) (x + j * 8 + 4);
                 }
             }
 #pragma unroll
@@ -413,8 +455,8 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
                 if (j >= n8) continue;
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
-                    const float4 xa = *(const float4*) (x + (size_t) t * cols + j * 8);
-                    const float4 xb = *(const float4*) (x + (size_t) t * cols + j * 8 + 4);
+                    const float4 xa = T == 1 ? xr[T == 1 ? u : 0][0] : *(const float4*) (x + (size_t) t * cols + j * 8);
+                    const float4 xb = T == 1 ? xr[T == 1 ? u : 0][1] : *(const float4*) (x + (size_t) t * cols + j * 8 + 4);
 #pragma unroll
                     for (int s = 0; s < RPW; ++s) {
                         float a = acc[s][t];

@@ -7,12 +7,13 @@
 //   hc_pre : R_out = R_in + bo * 2*sigmoid(inj_prev/HC)           (the pending write, or the
 //            embedding broadcast on layer 0), per-stream RMS scale, xn = R_out*scale*w,
 //            lo = silu(down . quant32(xn) / HC), inj = inj_w . xn.
-//            Every workgroup first issues the loads of its own `down` rows (they do not depend on
-//            the activations), then rebuilds quant32(xn) for the whole window in LDS from L2
-//            (coalesced float4 reads, 32 KB per row), so no cross-workgroup synchronisation is
-//            needed; workgroup w writes every gridDim-th 32-block of R_out.
+//            Every workgroup rebuilds quant32(xn) for the window in LDS (the residual is 32 KB per
+//            row and L2-resident), so no cross-workgroup synchronisation is needed; workgroup w
+//            writes every gridDim-th 32-block of R_out.
 //   hc_post: mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)); lo is quantised
 //            once per workgroup into LDS.
+// Both kernels issue every global load a row needs before using any of them (indices clamped
+// instead of branching, fp16 scales converted afterwards): one memory round trip per window row.
 #include <algorithm>
 
 #include "wzy_device.h"
@@ -23,7 +24,7 @@ using namespace wzy;
 
 namespace {
 
-constexpr int HC4 = 4;           // stream count of the hyper-connection
+constexpr int HC4 = 4;            // stream count of the hyper-connection
 
 // Per-32 int8 quantisation (reference per-32 rule: d = amax/127, q = rint(x * 127/amax)).
 WZY_DEV void quant32_vals(const float (&v)[32], int4& q0, int4& q1, float& d) {
@@ -47,154 +48,164 @@ WZY_DEV void quant32_vals(const float (&v)[32], int4& q0, int4& q1, float& d) {
     q1 = make_int4(w[4], w[5], w[6], w[7]);
 }
 
-// Four residual values of row t, stream c, positions d..d+3 before the norm: R_in (+ fold) or the
-// embedding row broadcast to every stream.
-WZY_DEV float4 hc_in4(const HcPreArgs& a, int t, int c, int d, float gw) {
-    float4 v;
-    if (a.emb_rows) {
-        v = *(const float4*) (a.emb_rows + (size_t) t * a.D + d);
-    } else if (a.emb_table) {
-        int tok = a.toks[t];
-        tok = tok < 0 ? 0 : (tok >= a.n_vocab ? a.n_vocab - 1 : tok);
-        const uint2 h = *(const uint2*) (a.emb_table + (size_t) tok * a.D + d);
-        v = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
-    } else {
-        v = *(const float4*) (a.R_in + ((size_t) t * HC4 + c) * a.D + d);
-    }
-    if (a.bo) {
-        const float4 b = *(const float4*) (a.bo + (size_t) t * a.D + d);
-        v.x = fmaf(b.x, gw, v.x);
-        v.y = fmaf(b.y, gw, v.y);
-        v.z = fmaf(b.z, gw, v.z);
-        v.w = fmaf(b.w, gw, v.w);
-    }
-    return v;
-}
-
 }  // namespace
 
-// T window rows (<= 4 per launch), D <= DC.  256 threads; wave w of workgroup g owns down rows
+// T window rows (<= 4 per launch), D <= DC.  256 threads; thread tid owns the 32-value blocks
+// b = tid + 256k of the flattened [HC*D] row; wave w of workgroup g owns down rows
 // (4g + w) * RPW .. + RPW - 1.  Dynamic LDS: int8 xq [T][4D] then fp32 xs [T][4D/32].
 template <int T, int DC, int RPW>
 __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
-    constexpr int KMAX = DC / 1024;          // float4s per thread per stream in the norm pass
-    constexpr int NBL = DC * HC4 / 32 / 64;  // 32-blocks per lane of one down row
+    constexpr int NBK = DC >= 2048 ? DC / 2048 : 1;   // 32-blocks per thread
+    constexpr int NBL = DC / 512;                      // 32-blocks per lane of one down row
     extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ float s_red[4][T * HC4];
+    __shared__ float s_seg[WZY_MAX_W][64];             // sums of 8 consecutive blocks (256 values)
     __shared__ float s_nsc[T * HC4];
-    __shared__ float s_gw[T * HC4];
     __shared__ float s_inj[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int D = a.D, HCD = HC4 * D, nb = HCD / 32, D4 = D / 4, L = a.HCLR;
+    const int D = a.D, HCD = HC4 * D, nb = HCD / 32, L = a.HCLR, spb = D / 256;
     int8_t* s_xq = (int8_t*) s_dyn;
     float* s_xs = (float*) (s_dyn + (size_t) T * HCD);
+    const bool fold = a.bo != nullptr;
+    const bool do_inj = a.inj_w != nullptr && blockIdx.x < HC4;
 
-    // 0. this wave's down rows, loaded before anything else
+    // 0. this wave's down rows (raw codes and fp16 scales), issued first
     const int row0 = (blockIdx.x * 4 + w) * RPW;
     int4 c0[NBL][RPW], c1[NBL][RPW];
-    float dw[NBL][RPW];
+    uint16_t sraw[NBL][RPW];
 #pragma unroll
     for (int i = 0; i < NBL; ++i) {
-        const int b = lane + 64 * i;
+        const int b = min(lane + 64 * i, nb - 1);
 #pragma unroll
         for (int s = 0; s < RPW; ++s) {
-            const int r = row0 + s;
-            if (b < nb && r < L) {
-                const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) b * 32);
-                c0[i][s] = ld_stream_i4(cp);
-                c1[i][s] = ld_stream_i4(cp + 1);
-                dw[i][s] = h16_to_f(a.down_s[(size_t) r * nb + b]);
-            } else {
-                c0[i][s] = c1[i][s] = make_int4(0, 0, 0, 0);
-                dw[i][s] = 0.f;
-            }
+            const int r = min(row0 + s, L - 1);
+            const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) b * 32);
+            c0[i][s] = ld_stream_i4(cp);
+            c1[i][s] = ld_stream_i4(cp + 1);
+            sraw[i][s] = a.down_s[(size_t) r * nb + b];
+        }
+    }
+    // 1. row-independent inputs of this thread's blocks: norm weights, inject weights
+    float4 nw[NBK][8];
+    uint4 iw[NBK][4];
+#pragma unroll
+    for (int k = 0; k < NBK; ++k) {
+        const int b = min(tid + 256 * k, nb - 1);
+        const int c = (32 * b) / D, d0 = (32 * b) % D;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nw[k][j] = *(const float4*) (a.norm_w + (size_t) c * D + d0 + 4 * j);
+        if (do_inj) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                iw[k][j] = *(const uint4*) (a.inj_w + (size_t) blockIdx.x * HCD + (size_t) 32 * b + 8 * j);
         }
     }
 
-    // 1. fold gates 2*sigmoid(inj_prev/HC)
-    if (tid < T * HC4) s_gw[tid] = a.bo ? 2.0f / (1.0f + __expf(-a.inj_prev[tid] / (float) HC4)) : 0.f;
-    __syncthreads();
-
-    // 2. per-stream sums of squares
-    float ss[T][HC4];
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int c = 0; c < HC4; ++c) {
-            float acc = 0.f;
-#pragma unroll
-            for (int k = 0; k < KMAX; ++k) {
-                const int j = tid + 256 * k;
-                if (j < D4) {
-                    const float4 v = hc_in4(a, t, c, 4 * j, s_gw[t * HC4 + c]);
-                    acc = fmaf(v.x, v.x, acc);
-                    acc = fmaf(v.y, v.y, acc);
-                    acc = fmaf(v.z, v.z, acc);
-                    acc = fmaf(v.w, v.w, acc);
-                }
-            }
-            ss[t][c] = acc;
-        }
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int c = 0; c < HC4; ++c) {
-            const float v = wave_sum(ss[t][c]);
-            if (lane == 0) s_red[w][t * HC4 + c] = v;
-        }
-    __syncthreads();
-    if (tid < T * HC4) {
-        const float tot = s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid];
-        const float sc = 1.0f / sqrtf(tot / (float) D + a.eps);
-        s_nsc[tid] = sc;
-        if (blockIdx.x == 0) a.nsc[tid] = sc;
-    }
-    __syncthreads();
-
-    // 3. xn = R_out * scale * w quantised per 32 into LDS; R_out blocks; inject row blockIdx.x
-    const bool do_inj = a.inj_w != nullptr && blockIdx.x < HC4;
     float inj_acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) inj_acc[t] = 0.f;
-    for (int b = tid; b < nb; b += 256) {
-        const int c = (32 * b) / D, d0 = (32 * b) % D;
-        float4 nw[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) nw[k] = *(const float4*) (a.norm_w + (size_t) c * D + d0 + 4 * k);
-        float iw[32];
-        if (do_inj) {
+    for (int t = 0; t < T; ++t) {
+        // 2. residual (or embedding) and fold inputs of this row
+        float4 rv[NBK][8], bv[NBK][8];
+        float ip[NBK];
+        int tok = 0;
+        if (a.emb_table) {
+            tok = a.toks[t];
+            tok = tok < 0 ? 0 : (tok >= a.n_vocab ? a.n_vocab - 1 : tok);
+        }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint4 u = *(const uint4*) (a.inj_w + (size_t) blockIdx.x * HCD + (size_t) 32 * b + 8 * k);
-                iw[8 * k + 0] = bf16_lo(u.x); iw[8 * k + 1] = bf16_hi(u.x);
-                iw[8 * k + 2] = bf16_lo(u.y); iw[8 * k + 3] = bf16_hi(u.y);
-                iw[8 * k + 4] = bf16_lo(u.z); iw[8 * k + 5] = bf16_hi(u.z);
-                iw[8 * k + 6] = bf16_lo(u.w); iw[8 * k + 7] = bf16_hi(u.w);
+        for (int k = 0; k < NBK; ++k) {
+            const int b = min(tid + 256 * k, nb - 1);
+            const int c = (32 * b) / D, d0 = (32 * b) % D;
+            if (a.emb_table) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint2 h = *(const uint2*) (a.emb_table + (size_t) tok * D + d0 + 4 * j);
+                    rv[k][j] = make_float4(__builtin_bit_cast(float, h.x), __builtin_bit_cast(float, h.y), 0.f, 0.f);
+                }
+            } else if (a.emb_rows) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) rv[k][j] = *(const float4*) (a.emb_rows + (size_t) t * D + d0 + 4 * j);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    rv[k][j] = *(const float4*) (a.R_in + ((size_t) t * HC4 + c) * D + d0 + 4 * j);
+            }
+            if (fold) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bv[k][j] = *(const float4*) (a.bo + (size_t) t * D + d0 + 4 * j);
+                ip[k] = a.inj_prev[t * HC4 + c];
             }
         }
-        const bool write_r = (b % gridDim.x) == blockIdx.x;
+        // 3. folded values and the per-thread sums of squares
+        float v[NBK][32];
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float gw = s_gw[t * HC4 + c], sc = s_nsc[t * HC4 + c];
-            float4 v4[8];
+        for (int k = 0; k < NBK; ++k) {
+            const float gw = fold ? 2.0f / (1.0f + __expf(-ip[k] / (float) HC4)) : 0.f;
+            float ss = 0.f;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v4[k] = hc_in4(a, t, c, d0 + 4 * k, gw);
-            if (write_r) {
-                float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) *(float4*) (ro + 4 * k) = v4[k];
+            for (int j = 0; j < 8; ++j) {
+                float4 x = rv[k][j];
+                if (a.emb_table) {
+                    const uint32_t lo = __builtin_bit_cast(uint32_t, x.x), hi = __builtin_bit_cast(uint32_t, x.y);
+                    x = make_float4(bf16_lo(lo), bf16_hi(lo), bf16_lo(hi), bf16_hi(hi));
+                }
+                if (fold) {
+                    x.x = fmaf(bv[k][j].x, gw, x.x);
+                    x.y = fmaf(bv[k][j].y, gw, x.y);
+                    x.z = fmaf(bv[k][j].z, gw, x.z);
+                    x.w = fmaf(bv[k][j].w, gw, x.w);
+                }
+                v[k][4 * j + 0] = x.x; v[k][4 * j + 1] = x.y; v[k][4 * j + 2] = x.z; v[k][4 * j + 3] = x.w;
+                ss = fmaf(x.x, x.x, ss);
+                ss = fmaf(x.y, x.y, ss);
+                ss = fmaf(x.z, x.z, ss);
+                ss = fmaf(x.w, x.w, ss);
             }
+            // 4. sums over 8 consecutive blocks (never straddle a stream: D % 256 == 0)
+            ss = sum8(ss);
+            const int b = tid + 256 * k;
+            if ((lane & 7) == 0 && b < nb) s_seg[t][b >> 3] = ss;
+        }
+        __syncthreads();
+        if (tid < HC4) {
+            float tot = 0.f;
+            for (int i = 0; i < spb; ++i) tot += s_seg[t][tid * spb + i];
+            const float sc = 1.0f / sqrtf(tot / (float) D + a.eps);
+            s_nsc[t * HC4 + tid] = sc;
+            if (blockIdx.x == 0) a.nsc[t * HC4 + tid] = sc;
+        }
+        __syncthreads();
+        // 5. xn quantised per 32 into LDS, inject partial, R_out blocks
+#pragma unroll
+        for (int k = 0; k < NBK; ++k) {
+            const int b = tid + 256 * k;
+            if (b >= nb) continue;
+            const int c = (32 * b) / D, d0 = (32 * b) % D;
+            const float sc = s_nsc[t * HC4 + c];
             float xn[32];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                xn[4 * k + 0] = v4[k].x * sc * nw[k].x;
-                xn[4 * k + 1] = v4[k].y * sc * nw[k].y;
-                xn[4 * k + 2] = v4[k].z * sc * nw[k].z;
-                xn[4 * k + 3] = v4[k].w * sc * nw[k].w;
+            for (int j = 0; j < 8; ++j) {
+                xn[4 * j + 0] = v[k][4 * j + 0] * sc * nw[k][j].x;
+                xn[4 * j + 1] = v[k][4 * j + 1] * sc * nw[k][j].y;
+                xn[4 * j + 2] = v[k][4 * j + 2] * sc * nw[k][j].z;
+                xn[4 * j + 3] = v[k][4 * j + 3] * sc * nw[k][j].w;
             }
             if (do_inj) {
 #pragma unroll
-                for (int k = 0; k < 32; ++k) inj_acc[t] = fmaf(iw[k], xn[k], inj_acc[t]);
+                for (int j = 0; j < 4; ++j) {
+                    const uint4 u = iw[k][j];
+                    float acc = inj_acc[t];
+                    acc = fmaf(bf16_lo(u.x), xn[8 * j + 0], acc);
+                    acc = fmaf(bf16_hi(u.x), xn[8 * j + 1], acc);
+                    acc = fmaf(bf16_lo(u.y), xn[8 * j + 2], acc);
+                    acc = fmaf(bf16_hi(u.y), xn[8 * j + 3], acc);
+                    acc = fmaf(bf16_lo(u.z), xn[8 * j + 4], acc);
+                    acc = fmaf(bf16_hi(u.z), xn[8 * j + 5], acc);
+                    acc = fmaf(bf16_lo(u.w), xn[8 * j + 6], acc);
+                    acc = fmaf(bf16_hi(u.w), xn[8 * j + 7], acc);
+                    inj_acc[t] = acc;
+                }
             }
             int4 q0, q1;
             float xs;
@@ -203,6 +214,12 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
             dst[0] = q0;
             dst[1] = q1;
             s_xs[t * nb + b] = xs;
+            if ((b % gridDim.x) == blockIdx.x) {
+                float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    *(float4*) (ro + 4 * j) = make_float4(v[k][4 * j], v[k][4 * j + 1], v[k][4 * j + 2], v[k][4 * j + 3]);
+            }
         }
     }
     if (do_inj) {                             // workgroup-uniform branch
@@ -214,7 +231,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
     }
     __syncthreads();
 
-    // 4. down rows: lo = silu(down . xq / HC)
+    // 6. down rows: lo = silu(down . xq / HC)
     float acc[RPW][T];
 #pragma unroll
     for (int s = 0; s < RPW; ++s)
@@ -231,7 +248,8 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
             const float xs = s_xs[t * nb + b];
 #pragma unroll
             for (int s = 0; s < RPW; ++s)
-                acc[s][t] = fmaf(dw[i][s] * xs, (float) (dot16(c0[i][s], x0) + dot16(c1[i][s], x1)), acc[s][t]);
+                acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c0[i][s], x0) + dot16(c1[i][s], x1)),
+                                 acc[s][t]);
         }
     }
 #pragma unroll
@@ -255,56 +273,59 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
     const int wave = (blockIdx.x * blockDim.x + tid) >> 6;
     const int D = a.D, L = a.HCLR, nb = L / 32;
     const int li = lane & 15, c = lane >> 4;
+    const int lb = min(li, nb - 1);
 
-    // weights and the per-position inputs of both outputs first
+    // every load first: weights, the residual / scale / norm inputs of xn, and lo
     int4 c0[2], c1[2];
-    float dw[2], xn[2][T];
+    uint16_t sraw[2];
+    float rr[2][T], nwv[2], nscv[T];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const int d = wave * 2 + k;
+        const int d = min(wave * 2 + k, D - 1);
         const size_t row = (size_t) c * D + d;
-        if (d < D && li < nb) {
-            const int4* cp = (const int4*) (a.up_q + row * L + (size_t) li * 32);
-            c0[k] = ld_stream_i4(cp);
-            c1[k] = ld_stream_i4(cp + 1);
-            dw[k] = h16_to_f(a.up_s[row * nb + li]);
-        } else {
-            c0[k] = c1[k] = make_int4(0, 0, 0, 0);
-            dw[k] = 0.f;
-        }
+        const int4* cp = (const int4*) (a.up_q + row * L + (size_t) lb * 32);
+        c0[k] = ld_stream_i4(cp);
+        c1[k] = ld_stream_i4(cp + 1);
+        sraw[k] = a.up_s[row * nb + lb];
+        nwv[k] = a.norm_w[row];
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-            xn[k][t] = (d < D && li == 0)
-                           ? a.R[((size_t) t * HC4 + c) * D + d] * a.nsc[t * HC4 + c] * a.norm_w[(size_t) c * D + d]
-                           : 0.f;
+        for (int t = 0; t < T; ++t) rr[k][t] = a.R[((size_t) t * HC4 + c) * D + d];
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) nscv[t] = a.nsc[t * HC4 + c];
+    float4 lv[8];
+    const int lt = min(tid / nb, T - 1), lbb = tid % nb;
+    if (tid < T * nb) {                      // issued after every other load of the wave
+#pragma unroll
+        for (int k = 0; k < 8; ++k) lv[k] = *(const float4*) (a.lo + (size_t) lt * L + 32 * lbb + 4 * k);
     }
     // quant32(lo) once per workgroup
     if (tid < T * nb) {
-        const int t = tid / nb, b = tid % nb;
         float v[32];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float4 f = *(const float4*) (a.lo + (size_t) t * L + 32 * b + 4 * k);
-            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+            v[4 * k] = lv[k].x; v[4 * k + 1] = lv[k].y; v[4 * k + 2] = lv[k].z; v[4 * k + 3] = lv[k].w;
         }
         int4 q0, q1;
         float xs;
         quant32_vals(v, q0, q1, xs);
-        s_lq[t][2 * b] = q0;
-        s_lq[t][2 * b + 1] = q1;
-        s_ls[t][b] = xs;
+        s_lq[lt][2 * lbb] = q0;
+        s_lq[lt][2 * lbb + 1] = q1;
+        s_ls[lt][lbb] = xs;
     }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int d = wave * 2 + k;
         if (d >= D) break;                   // wave-uniform
+        const float dw = h16_to_f(sraw[k]);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             float acc = 0.f;
-            if (li < nb) acc = dw[k] * s_ls[t][li] * (float) (dot16(c0[k], s_lq[t][2 * li]) + dot16(c1[k], s_lq[t][2 * li + 1]));
+            if (li < nb) acc = dw * s_ls[t][li] * (float) (dot16(c0[k], s_lq[t][2 * li]) + dot16(c1[k], s_lq[t][2 * li + 1]));
             const float s = sum16(acc);      // every lane of the 16-lane group holds stream c's sum
-            const float g = (li == 0) ? xn[k][t] / (1.0f + __expf(-s)) : 0.f;
+            const float xn = rr[k][t] * nscv[t] * nwv[k];
+            const float g = (li == 0) ? xn / (1.0f + __expf(-s)) : 0.f;
             // gather the four streams (lanes 0, 16, 32, 48) in the reference's pairing
             // (g0 + g2) + (g1 + g3)  (src/wzy_kernels_v2.cuh:806-809)
             const float g0 = as_f(__builtin_amdgcn_readlane(as_i(g), 0));
@@ -319,30 +340,28 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
 namespace wzy {
 
 namespace {
-constexpr int PRE_RPW = 2;
-
-template <int T, int DC>
+template <int T, int DC, int RPW>
 void launch_pre_tdc(const HcPreArgs& a, hipStream_t st) {
     const int HCD = HC4 * a.D;
-    const int rows_wg = 4 * PRE_RPW;
+    const int rows_wg = 4 * RPW;
     int blocks = (a.HCLR + rows_wg - 1) / rows_wg;
     if (a.inj_w && blocks < HC4) blocks = HC4;
     const size_t lds = (size_t) T * HCD + (size_t) T * (HCD / 32) * sizeof(float);
-    hipLaunchKernelGGL((hc_pre_kernel<T, DC, PRE_RPW>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((hc_pre_kernel<T, DC, RPW>), dim3(blocks), dim3(256), lds, st, a);
 }
 template <int T>
 void launch_pre_t(const HcPreArgs& a, hipStream_t st) {
-    if (a.D <= 1024) launch_pre_tdc<T, 1024>(a, st);
-    else if (a.D <= 2048) launch_pre_tdc<T, 2048>(a, st);
-    else launch_pre_tdc<T, 4096>(a, st);
+    if (a.D <= 1024) launch_pre_tdc<T, 1024, 2>(a, st);
+    else if (a.D <= 2048) launch_pre_tdc<T, 2048, 2>(a, st);
+    else launch_pre_tdc<T, 4096, 1>(a, st);
 }
 }  // namespace
 
 int launch_hc_pre(const HcPreArgs& a0, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "hc_pre: T out of range");
-    WZY_REQUIRE(a0.HC == HC4 && a0.D % 32 == 0 && a0.D >= 32 && a0.D <= 4096 && a0.HCLR % 32 == 0 && a0.HCLR >= 32 &&
-                    a0.HCLR <= 512,
-                "hc_pre: unsupported shape (HC must be 4, D a multiple of 32 <= 4096, HCLR a multiple of 32 <= 512)");
+    WZY_REQUIRE(a0.HC == HC4 && a0.D % 256 == 0 && a0.D >= 256 && a0.D <= 4096 && a0.HCLR % 32 == 0 &&
+                    a0.HCLR >= 32 && a0.HCLR <= 512,
+                "hc_pre: unsupported shape (HC must be 4, D a multiple of 256 <= 4096, HCLR a multiple of 32 <= 512)");
     WZY_REQUIRE((a0.R_in != nullptr) + (a0.emb_table != nullptr) + (a0.emb_rows != nullptr) == 1,
                 "hc_pre: exactly one of R_in / emb_table / emb_rows");
     WZY_REQUIRE(!a0.emb_table || a0.toks, "hc_pre: embedding mode needs toks");

@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             for (int t = 0; t < T; ++t) acc[rr][t] = 0.f;
         for (int b = lane; b < nb; b += 64) {
             int4 c0[8], c1[8];
-            float dw[8];
+            uint16_t sraw[8];
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int8_t* q = (rr < 4) ? a.shg_q : a.shu_q;
@@ -395,7 +395,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
                 const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) b * 32);
                 c0[rr] = ld_stream_i4(cp);
                 c1[rr] = ld_stream_i4(cp + 1);
-                dw[rr] = h16_to_f(s[(size_t) row * nb + b]);
+                sraw[rr] = s[(size_t) row * nb + b];       // converted after every load is issued
             }
 #pragma unroll
             for (int t = 0; t < T; ++t) {
@@ -404,7 +404,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
                 quant32x1_lane(a.x + (size_t) t * D + (size_t) b * 32, x0, x1, xsc);
 #pragma unroll
                 for (int rr = 0; rr < 8; ++rr)
-                    acc[rr][t] = fmaf(dw[rr] * xsc, (float) (dot16(c0[rr], x0) + dot16(c1[rr], x1)), acc[rr][t]);
+                    acc[rr][t] = fmaf(h16_to_f(sraw[rr]) * xsc, (float) (dot16(c0[rr], x0) + dot16(c1[rr], x1)),
+                                      acc[rr][t]);
             }
         }
 #pragma unroll
@@ -470,27 +471,40 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             for (int m = 0; m < T; ++m) acc[b][m] = 0.f;
         }
         for (int c = li; c < nchunk; c += 16) {
+            // loads of all DN_BATCH items first (raw scales; for single-row windows also the
+            // activations), arithmetic afterwards
             int4 c0[DN_BATCH], c1[DN_BATCH];
-            float wsa[DN_BATCH], wsb[DN_BATCH];
+            uint32_t sraw[DN_BATCH];
+            constexpr int BX = (T == 1) ? DN_BATCH : 1;
+            int4 xa0[BX], xa1[BX];
+            float2 xsv[BX];
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
-                const int item = i0 + 16 * b;
-                c0[b] = c1[b] = make_int4(0, 0, 0, 0);
-                wsa[b] = wsb[b] = 0.f;
-                if (item < n_items) {
-                    const int g = item / DN_TILE, d = d0 + item % DN_TILE;
-                    if (g < ng) {
-                        const uint8_t* rec = a.experts + (size_t) s_gexp[g] * o.rec;
-                        c0[b] = ld_stream_i4(rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16);
-                        const uint32_t s2 = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
-                        wsa[b] = ue4m3_half(s2 & 0xFFu);
-                        wsb[b] = ue4m3_half(s2 >> 8);
-                        sdn[b] = ((const float*) (rec + o.tail))[2];
-                    } else {
-                        const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
-                        c0[b] = ld_stream_i4(cp);
-                        c1[b] = ld_stream_i4(cp + 1);
-                        wsa[b] = h16_to_f(a.shd_s[(size_t) d * nchunk + c]);
+                const int item = min(i0 + 16 * b, n_items - 1);
+                const int g = item / DN_TILE, d = d0 + item % DN_TILE;
+                if (g < ng) {
+                    const uint8_t* rec = a.experts + (size_t) s_gexp[g] * o.rec;
+                    c0[b] = ld_stream_i4(rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16);
+                    c1[b] = make_int4(0, 0, 0, 0);
+                    sraw[b] = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
+                    sdn[b] = ((const float*) (rec + o.tail))[2];
+                    if (T == 1) {
+                        const int f = s_gmem[g][0];
+                        const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
+                        xa0[T == 1 ? b : 0] = xp[0];
+                        xa1[T == 1 ? b : 0] = xp[1];
+                        xsv[T == 1 ? b : 0] = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
+                    }
+                } else {
+                    const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
+                    c0[b] = ld_stream_i4(cp);
+                    c1[b] = ld_stream_i4(cp + 1);
+                    sraw[b] = a.shd_s[(size_t) d * nchunk + c];
+                    if (T == 1) {
+                        const int4* xp = (const int4*) (a.shq32 + (size_t) c * 32);
+                        xa0[T == 1 ? b : 0] = xp[0];
+                        xa1[T == 1 ? b : 0] = xp[1];
+                        xsv[T == 1 ? b : 0] = make_float2(a.shs32[c], 0.f);
                     }
                 }
             }
@@ -502,22 +516,34 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                 if (g < ng) {
                     const int4 wa = e2m1_sub16((uint32_t) c0[b].x, (uint32_t) c0[b].y);
                     const int4 wb = e2m1_sub16((uint32_t) c0[b].z, (uint32_t) c0[b].w);
-                    const int cnt = s_gcnt[g];
+                    const float wsa = ue4m3_half(sraw[b] & 0xFFu), wsb = ue4m3_half(sraw[b] >> 8);
+                    if (T == 1) {
+                        const int bx = T == 1 ? b : 0;
+                        acc[b][0] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xa0[bx], xa1[bx], xsv[bx].x, xsv[bx].y, acc[b][0]);
+                    } else {
+                        const int cnt = s_gcnt[g];
 #pragma unroll
-                    for (int m = 0; m < T; ++m) {
-                        if (m < cnt) {
-                            const int f = s_gmem[g][m];
-                            const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
-                            const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
-                            acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa[b], wsb[b], xp[0], xp[1], xs.x, xs.y, acc[b][m]);
+                        for (int m = 0; m < T; ++m) {
+                            if (m < cnt) {
+                                const int f = s_gmem[g][m];
+                                const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
+                                const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
+                                acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xp[0], xp[1], xs.x, xs.y, acc[b][m]);
+                            }
                         }
                     }
                 } else {
+                    const float dw = h16_to_f((uint16_t) sraw[b]);
+                    if (T == 1) {
+                        const int bx = T == 1 ? b : 0;
+                        acc[b][0] = fmaf(dw * xsv[bx].x, (float) (dot16(c0[b], xa0[bx]) + dot16(c1[b], xa1[bx])), acc[b][0]);
+                    } else {
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) c * 32);
-                        const float xsc = a.shs32[(size_t) t * nchunk + c];
-                        acc[b][t] = fmaf(wsa[b] * xsc, (float) (dot16(c0[b], xp[0]) + dot16(c1[b], xp[1])), acc[b][t]);
+                        for (int t = 0; t < T; ++t) {
+                            const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) c * 32);
+                            const float xsc = a.shs32[(size_t) t * nchunk + c];
+                            acc[b][t] = fmaf(dw * xsc, (float) (dot16(c0[b], xp[0]) + dot16(c1[b], xp[1])), acc[b][t]);
+                        }
                     }
                 }
             }

@@ -183,12 +183,22 @@ __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
     }
     __syncthreads();
 
-    // complete blocks: 16 lanes per block (8 halves each), 4 blocks per wave-iteration
+    // complete blocks: 16 lanes per block (8 halves each), 4 blocks per wave-iteration; the keys of
+    // all iterations are loaded before any is used
     const int li = lane & 15;
-    for (int it = 0; it < SC_BLOCKS_PER_WG / 16; ++it) {
+    constexpr int NIT = SC_BLOCKS_PER_WG / 16;
+    const int b_lim = min(a.max_b, n_kv_max / B);
+    uint4 kr[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int b = min(b0 + w * 16 + it * 4 + (lane >> 4), max(b_lim - 1, 0));
+        kr[it] = *(const uint4*) (a.pooled + (size_t) b * D + 8 * li);
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
         const int b = b0 + w * 16 + it * 4 + (lane >> 4);
-        if (b >= a.max_b || b >= n_kv_max / B) continue;
-        const uint4 kraw = *(const uint4*) (a.pooled + (size_t) b * D + 8 * li);
+        if (b >= b_lim) continue;
+        const uint4 kraw = kr[it];
         const h2_t k0 = __builtin_bit_cast(h2_t, kraw.x), k1 = __builtin_bit_cast(h2_t, kraw.y);
         const h2_t k2 = __builtin_bit_cast(h2_t, kraw.z), k3 = __builtin_bit_cast(h2_t, kraw.w);
 #pragma unroll

@@ -35,36 +35,24 @@ WZY_DEV uint32_t order_key(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Inclusive prefix sum over the NW*64 threads in thread order; s_w holds NW ints.
+// Two inclusive prefix sums at once over the NW*64 threads in thread order (one barrier pair).
 template <int NW>
-WZY_DEV int block_scan_incl(int v, int* s_w) {
+WZY_DEV void block_scan_incl2(int& x, int& y, int* s_x, int* s_y) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int x = v;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
+        const int a = __shfl_up(x, o, 64), b = __shfl_up(y, o, 64);
+        if (lane >= o) { x += a; y += b; }
     }
-    if (lane == 63) s_w[w] = x;
+    if (lane == 63) { s_x[w] = x; s_y[w] = y; }
     __syncthreads();
-    int before = 0;
+    int bx = 0, by = 0;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) before += (i < w) ? s_w[i] : 0;
+    for (int i = 0; i < NW; ++i)
+        if (i < w) { bx += s_x[i]; by += s_y[i]; }
     __syncthreads();
-    return x + before;
-}
-
-// Number of threads of the NW-wave workgroup with `pred` set (wave ballots summed in LDS).
-template <int NW>
-WZY_DEV int block_count(bool pred, int* s_c) {
-    const unsigned long long m = __ballot(pred);
-    if ((threadIdx.x & 63) == 0) s_c[threadIdx.x >> 6] = __popcll(m);
-    __syncthreads();
-    int n = 0;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) n += s_c[i];
-    __syncthreads();
-    return n;
+    x += bx;
+    y += by;
 }
 
 }  // namespace
@@ -110,28 +98,49 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
 
     uint32_t prefix = 0;
     int above = 0;
+    if (p < 256) hist[p] = 0;
+    __syncthreads();
     for (int shift = 24; shift >= 0; shift -= 8) {
-        if (p < 256) hist[p] = 0;
-        __syncthreads();
         const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
 #pragma unroll
         for (int q = 0; q < TK_MAXJ; ++q)
             if (wgt(q) > 0 && (key[q] & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key[q] >> shift) & 255u], wgt(q));
         __syncthreads();
-        // thread i < 256 takes digit 255 - i; S = weight of candidates with digit >= 255 - i
-        const int h = p < 256 ? hist[255 - p] : 0;
-        const int S = block_scan_incl<TK_THREADS / 64>(h, s_w);
-        const bool ok = p < 256 && above + S >= width;
-        const int n_ok = block_count<TK_THREADS / 64>(ok, s_c);
-        const int istar = n_ok > 0 ? 256 - n_ok : 255;   // first (highest) digit reaching the width
-        if (p == istar) {
-            s_digit = 255 - p;
-            s_above = above + S - h;
+        // wave 0 picks the digit: lane l holds digits 255-4l .. 252-4l (highest first); the
+        // threshold digit is the highest one at which the weight at or above it reaches the width
+        if (p < 64) {
+            const int l = p;
+            int h[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[j] = hist[255 - 4 * l - j];
+                hist[255 - 4 * l - j] = 0;           // cleared for the next pass
+            }
+            const int s4 = h[0] + h[1] + h[2] + h[3];
+            int incl = s4;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o, 64);
+                if (l >= o) incl += y;
+            }
+            int cum = above + incl - s4;             // weight of digits above this lane's first
+            int jl = -1, base_above = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (jl < 0 && cum + h[j] >= width) { jl = j; base_above = cum; }
+                cum += h[j];
+            }
+            const unsigned long long m = __ballot(jl >= 0);
+            const int lstar = m ? __ffsll((long long) m) - 1 : 63;
+            if (l == lstar) {
+                const int js = jl >= 0 ? jl : 3;
+                s_digit = 255 - 4 * l - js;
+                s_above = jl >= 0 ? base_above : cum - h[3];
+            }
         }
         __syncthreads();
         prefix |= (uint32_t) s_digit << shift;
         above = s_above;
-        __syncthreads();
     }
 
     const uint32_t thr = prefix;
@@ -144,10 +153,13 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
         if (key[q] > thr) gt += wq;
         else if (key[q] == thr) eq += wq;
     }
-    const int eq_excl = block_scan_incl<TK_THREADS / 64>(eq, s_w) - eq;
+    // one dual scan: the threshold-tied cells a thread may take are what is left of the budget
+    // after the threads before it, and its output offset is gt_excl + min(eq_excl, eq_budget)
+    int gt_incl = gt, eq_incl = eq;
+    block_scan_incl2<TK_THREADS / 64>(gt_incl, eq_incl, s_w, s_c);
+    const int eq_excl = eq_incl - eq;
     const int my_eq = max(0, min(eq, eq_budget - eq_excl));
-    const int sel = gt + my_eq;
-    int wpos = block_scan_incl<TK_THREADS / 64>(sel, s_w) - sel;
+    int wpos = (gt_incl - gt) + min(eq_excl, eq_budget);
     int eq_left = my_eq;
 #pragma unroll
     for (int q = 0; q < TK_MAXJ; ++q) {
@@ -172,7 +184,7 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     __shared__ __align__(16) int8_t s_v[QSA_ATT_CHUNK * ATT_ROW];
     __shared__ float s_ks[QSA_ATT_CHUNK][4], s_vs[QSA_ATT_CHUNK][4];
     __shared__ __align__(16) float s_q[ATT_GQ_MAX][256];
-    __shared__ float s_p[ATT_GQ_MAX][QSA_ATT_CHUNK];
+    __shared__ __align__(16) float s_p[QSA_ATT_CHUNK][ATT_GQ_MAX];   // softmax weights, [cell][head]
     __shared__ long long s_slot[QSA_ATT_CHUNK];
     const QsaDims& dm = a.dm;
     const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
@@ -191,10 +203,11 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
         if (tid < ncell) sl = (long long) qsa_kv_slot(n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx], dm);
         s_slot[tid] = sl;
     }
-    for (int i = tid; i < gq * 64; i += 256) {
+    for (int i = tid; i < ATT_GQ_MAX * 64; i += 256) {        // rows >= gq are zero
         const int hh = i >> 6, d4 = i & 63;
         *(float4*) &s_q[hh][4 * d4] =
-            *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + hh) * 512 + 4 * d4);
+            hh < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + hh) * 512 + 4 * d4)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
 
@@ -232,10 +245,10 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     {
         const int cell = lane;
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
+#pragma unroll 1
         for (int g = 0; g < 4; ++g) {
             float ag[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
+#pragma unroll 1
             for (int pp = 0; pp < 4; ++pp) {
                 const int part = 4 * g + pp;
                 const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
@@ -244,12 +257,15 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) kf[e] = (float) kb[e];
 #pragma unroll
-                for (int hh = 0; hh < 4; ++hh) {
-                    const int h = w + 4 * hh;
-                    if (h < gq) {
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) ag[hh] = fmaf(kf[e], s_q[h][part * 16 + e], ag[hh]);
-                    }
+                for (int hh = 0; hh < 4; ++hh) {     // heads past gq read zero rows of s_q
+                    const float4* qp = (const float4*) &s_q[w + 4 * hh][part * 16];
+                    const float4 q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
+                    float x = ag[hh];
+                    x = fmaf(kf[0], q0.x, x); x = fmaf(kf[1], q0.y, x); x = fmaf(kf[2], q0.z, x); x = fmaf(kf[3], q0.w, x);
+                    x = fmaf(kf[4], q1.x, x); x = fmaf(kf[5], q1.y, x); x = fmaf(kf[6], q1.z, x); x = fmaf(kf[7], q1.w, x);
+                    x = fmaf(kf[8], q2.x, x); x = fmaf(kf[9], q2.y, x); x = fmaf(kf[10], q2.z, x); x = fmaf(kf[11], q2.w, x);
+                    x = fmaf(kf[12], q3.x, x); x = fmaf(kf[13], q3.y, x); x = fmaf(kf[14], q3.z, x); x = fmaf(kf[15], q3.w, x);
+                    ag[hh] = x;
                 }
             }
             const float ks = s_ks[cell][g];
@@ -260,12 +276,15 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
 #pragma unroll
         for (int hh = 0; hh < 4; ++hh) {
             const int h = w + 4 * hh;
-            if (h >= gq) break;                      // wave-uniform
+            if (h >= gq) {                           // wave-uniform
+                s_p[cell][h] = 0.f;
+                continue;
+            }
             const float s = cell < ncell ? acc[hh] * 0.0625f : -INFINITY;
             const float m = wave_max(s);
             const float e = cell < ncell ? __expf(s - m) : 0.f;
             const float l = wave_sum(e);
-            s_p[h][cell] = e;
+            s_p[cell][h] = e;
             if (lane == 0) { ml[h * 2] = m; ml[h * 2 + 1] = l; }
         }
     }
@@ -277,11 +296,18 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
         float o[ATT_GQ_MAX];
 #pragma unroll
         for (int hh = 0; hh < ATT_GQ_MAX; ++hh) o[hh] = 0.f;
+#pragma unroll 4
         for (int cell = 0; cell < ncell; ++cell) {
             const float pv = (float) s_v[cell * ATT_ROW + d] * s_vs[cell][d >> 6];
+            const float4* pp = (const float4*) s_p[cell];
 #pragma unroll
-            for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
-                if (hh < gq) o[hh] = fmaf(s_p[hh][cell], pv, o[hh]);
+            for (int q4 = 0; q4 < ATT_GQ_MAX / 4; ++q4) {
+                const float4 p = pp[q4];
+                o[4 * q4 + 0] = fmaf(p.x, pv, o[4 * q4 + 0]);
+                o[4 * q4 + 1] = fmaf(p.y, pv, o[4 * q4 + 1]);
+                o[4 * q4 + 2] = fmaf(p.z, pv, o[4 * q4 + 2]);
+                o[4 * q4 + 3] = fmaf(p.w, pv, o[4 * q4 + 3]);
+            }
         }
         float* po = a.part + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 256;
 #pragma unroll
