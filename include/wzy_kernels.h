@@ -96,8 +96,7 @@ typedef struct wzy_moe_weights {
     const int8_t* sh_down_q;  const uint16_t* sh_down_s;   /* Q8_0 [n_embd x n_ff]  */
 } wzy_moe_weights;
 
-/* Bytes of device workspace wzy_moe_block needs for T rows.  Zero the workspace once before its
- * first use (it holds a completion counter that every call leaves at zero); calls that share a
+/* Bytes of device workspace wzy_moe_block needs for T rows (n_embd <= 2048).  Calls that share a
  * workspace must not overlap. */
 size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T);
 

@@ -485,6 +485,154 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
     }
 }
 
+// Same GEMV with the activations staged once per workgroup in LDS: the fp32 rows (for bf16
+// segments, split into the two float4 halves of each 8-column group) and their per-32 int8
+// quantisation (for Q8_0 segments, split into the two 16-byte halves of each block), so lanes
+// read 16 consecutive bytes each (no LDS bank conflicts) and the L2 serves x once per workgroup
+// instead of once per wave.  Each wave issues its weight loads before the staging barrier.
+// flags: bit 0 = the launch has Q8_0 segments, bit 1 = it has bf16 segments.
+template <int T, int NBL, int RPW>
+__global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const float* __restrict__ x, int cols,
+                                                            int flags) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = (blockIdx.x * blockDim.x + tid) >> 6;
+    const int nb = cols >> 5, n8 = cols >> 3;
+    float4* s_xf = (float4*) s_dyn;                                            // [T][2][n8]
+    int4* s_xq = (int4*) (s_dyn + ((flags & 2) ? (size_t) T * cols * 4 : 0));  // [T][2][nb]
+    float* s_xs = (float*) ((unsigned char*) s_xq + ((flags & 1) ? (size_t) T * cols : 0));   // [T][nb]
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < GEMV_MAX_SEGS; ++i)
+        if (i < segs.n && wave >= segs.seg[i].wave0) si = i;
+    const GemvSeg& sg = segs.seg[si];
+    const int row0 = (wave - sg.wave0) * RPW;
+    const bool active = row0 < sg.rows;
+    const bool q8 = sg.kind == GEMV_Q8;
+
+    // 1. weights (wave-uniform branches; clamped indices; raw scales)
+    int4 c0[NBL][RPW], c1[NBL][RPW];
+    uint16_t sraw[NBL][RPW];
+    constexpr int NU = NBL * 4;                           // uint4 (8 bf16) per lane per row: cols/8/64
+    uint4 wv[NU][RPW];
+    if (active && q8) {
+        const int8_t* W = (const int8_t*) sg.w;
+#pragma unroll
+        for (int i = 0; i < NBL; ++i) {
+            const int b = min(lane + 64 * i, nb - 1);
+#pragma unroll
+            for (int s = 0; s < RPW; ++s) {
+                const int r = min(row0 + s, sg.rows - 1);
+                const int4* cp = (const int4*) (W + (size_t) r * cols + (size_t) b * 32);
+                c0[i][s] = ld_stream_i4(cp);
+                c1[i][s] = ld_stream_i4(cp + 1);
+                sraw[i][s] = sg.s[(size_t) r * nb + b];
+            }
+        }
+    } else if (active) {
+        const uint16_t* W = (const uint16_t*) sg.w;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int j = min(lane + 64 * u, n8 - 1);
+#pragma unroll
+            for (int s = 0; s < RPW; ++s) {
+                const int r = min(row0 + s, sg.rows - 1);
+                wv[u][s] = ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j);
+            }
+        }
+    }
+    // 2. stage x: thread i owns 32-column block i of the window
+    for (int i = tid; i < T * nb; i += 256) {
+        const int t = i / nb, b = i - t * nb;
+        float4 v4[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v4[k] = ((const float4*) (x + (size_t) t * cols + (size_t) b * 32))[k];
+        if (flags & 2) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                s_xf[((size_t) t * 2 + 0) * n8 + 4 * b + k] = v4[2 * k];
+                s_xf[((size_t) t * 2 + 1) * n8 + 4 * b + k] = v4[2 * k + 1];
+            }
+        }
+        if (flags & 1) {
+            int4 q0, q1;
+            float xs;
+            quant32_v(v4, q0, q1, xs);
+            s_xq[((size_t) t * 2 + 0) * nb + b] = q0;
+            s_xq[((size_t) t * 2 + 1) * nb + b] = q1;
+            s_xs[(size_t) t * nb + b] = xs;
+        }
+    }
+    __syncthreads();
+    if (!active) return;
+
+    float acc[RPW][T];
+#pragma unroll
+    for (int s = 0; s < RPW; ++s)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
+    if (q8) {
+#pragma unroll
+        for (int i = 0; i < NBL; ++i) {
+            const int b = lane + 64 * i;
+            if (b >= nb) continue;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const int4 x0 = s_xq[((size_t) t * 2 + 0) * nb + b], x1 = s_xq[((size_t) t * 2 + 1) * nb + b];
+                const float xs = s_xs[(size_t) t * nb + b];
+#pragma unroll
+                for (int s = 0; s < RPW; ++s)
+                    acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c1[i][s], x1) + dot16(c0[i][s], x0)),
+                                     acc[s][t]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int j = lane + 64 * u;
+            if (j >= n8) continue;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float4 xa = s_xf[((size_t) t * 2 + 0) * n8 + j], xb = s_xf[((size_t) t * 2 + 1) * n8 + j];
+#pragma unroll
+                for (int s = 0; s < RPW; ++s) {
+                    float v = acc[s][t];
+                    v = fmaf(bf16_lo(wv[u][s].x), xa.x, v);
+                    v = fmaf(bf16_hi(wv[u][s].x), xa.y, v);
+                    v = fmaf(bf16_lo(wv[u][s].y), xa.z, v);
+                    v = fmaf(bf16_hi(wv[u][s].y), xa.w, v);
+                    v = fmaf(bf16_lo(wv[u][s].z), xb.x, v);
+                    v = fmaf(bf16_hi(wv[u][s].z), xb.y, v);
+                    v = fmaf(bf16_lo(wv[u][s].w), xb.z, v);
+                    v = fmaf(bf16_hi(wv[u][s].w), xb.w, v);
+                    acc[s][t] = v;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < RPW; ++s) {
+        const int r = row0 + s;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[s][t]);
+            if (lane == 0 && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
+        }
+    }
+}
+
+template <int T>
+static void launch_segs_lds_t(const GemvSegs& segs, int waves, int nbl, const float* x, int cols, int flags,
+                              size_t lds, hipStream_t st) {
+    const int blocks = (waves + 3) / 4;
+    switch (nbl) {
+        case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        case 2: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 2, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        case 3: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 3, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 1>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+    }
+}
+
 template <int T>
 static void launch_segs_t(const GemvSegs& segs, int waves, int nbl, const float* x, int cols, hipStream_t st) {
     const int blocks = (waves + 3) / 4;
@@ -511,6 +659,24 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
         if (s.y_stride == 0) s.y_stride = s.rows;
         s.wave0 = waves;
         waves += (s.rows + rpw - 1) / rpw;
+    }
+    int flags = 0;
+    for (int i = 0; i < segs.n; ++i) flags |= segs.seg[i].kind == GEMV_Q8 ? 1 : 2;
+    const size_t lds = (size_t) T * cols * (((flags & 2) ? 4 : 0) + ((flags & 1) ? 1 : 0)) +
+                       ((flags & 1) ? (size_t) T * (cols / 32) * 4 : 0);
+    if (lds <= 48 * 1024) {
+        switch (T) {
+            case 1: launch_segs_lds_t<1>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 2: launch_segs_lds_t<2>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 3: launch_segs_lds_t<3>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 4: launch_segs_lds_t<4>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 5: launch_segs_lds_t<5>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 6: launch_segs_lds_t<6>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 7: launch_segs_lds_t<7>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            default: launch_segs_lds_t<8>(segs, waves, nbl, x, cols, flags, lds, st); break;
+        }
+        WZY_LAUNCH_CHECK();
+        return WZY_OK;
     }
     switch (T) {
         case 1: launch_segs_t<1>(segs, waves, nbl, x, cols, st); break;

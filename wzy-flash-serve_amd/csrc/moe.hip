@@ -1,19 +1,20 @@
 // moe.hip -- NVFP4 mixture-of-experts decode block for gfx950.
 //
 // Launch sequence of wzy_moe_block (T window rows, K routed experts per row), three launches:
-//   1. moe_router   router logits [T x E] (bf16 weights, fp32 x) + the shared-expert gate scalar,
-//                   one wave per 4 rows; the last workgroup to finish (device-scope counter) runs
-//                   the softmax top-K per row and groups the T*K routed entries by expert (each
-//                   distinct expert of the window once, with its (row, slot) members, so its
-//                   weights stream from HBM once)
-//   2. moe_gate_up  workgroup (group, 16-row tile) runs the gate+up NVFP4 GEMV on activations
-//                   quantised per 16 inside the lane, SwiGLU and the per-16 int8 requant; extra
-//                   workgroups run the Q8_0 shared expert
-//   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, combine in LDS:
+//   1. gemv_segs    router logits [T x E] (bf16) + the shared-expert gate scalar row
+//   2. moe_gate_up  routed workgroup (group, 16-row tile): prefetches the logits, stages x
+//                   quantised per 16 in LDS, routes the window in LDS (softmax top-K, weights,
+//                   groups: each distinct expert of the window once, with its (row, slot) members,
+//                   so its weights stream from HBM once), then runs the gate+up NVFP4 GEMV, SwiGLU
+//                   and the per-16 int8 requant of its 16 rows; workgroup 0 publishes the routing.
+//                   Shared workgroups run the Q8_0 shared expert on x quantised per 32.
+//   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, activations
+//                   staged in LDS, combine in LDS:
 //                   comb = sigmoid(sgate)*shared + sum_k w_k*part_k  (k in routed order).
 // All expert GEMVs are wave-per-row with 128-bit code loads (16 bytes = 32 e2m1 values per lane)
 // and e4m3 scales from a separate plane, e2m1 -> int8 expansion with v_perm_b32, v_dot4_i32_i8
-// dots.  No MFMA: at one token per expert these are bandwidth-bound GEMVs.
+// dots; every weight load of a lane is issued before any is used.  No MFMA: at one token per
+// expert these are bandwidth-bound GEMVs.
 #include "wzy_device.h"
 #include "wzy_gemv.h"
 #include "wzy_host.h"
@@ -26,6 +27,7 @@ namespace {
 constexpr int DN_TILE = 8;    // output rows of one down workgroup
 constexpr int DN_BATCH = 4;   // work items whose loads a 16-lane slot issues together
 constexpr int MAX_ENT = WZY_MAX_W * MOE_MAX_K;
+constexpr int DN_STAGE_BYTES = 24 * 1024;   // activation staging limit of moe_down
 
 struct MoeOffsets {
     size_t gu_codes, gu_scales, dn_codes, dn_scales, tail, rec;
@@ -66,14 +68,27 @@ WZY_DEV int excl_count256(bool pred, int* s_c, int& total) {
     return before + within;
 }
 
-// per-16 int8 quantisation of 32 fp32 values held by one lane (two 16-blocks)
-WZY_DEV void quant16x2_lane(const float* __restrict__ xp, int4& qa, int4& qb, float& sa, float& sb) {
-    float v[32];
+// int8 quantisation, reference rule d = amax/127, q = rint(x * 127/amax) clamped to +-127.
+// 32 values -> two 16-value halves with one shared per-32 scale
+WZY_DEV void quant32_halves(const float (&v)[32], int4& qa, int4& qb, float& d) {
+    float am = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = ((const float4*) xp)[i];
-        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(v[i]));
+    d = am / 127.0f;
+    const float inv = d > 0.f ? 127.0f / am : 0.f;
+    int w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pk |= (uint32_t) (max(-127, min(127, rn_int(v[4 * k + j] * inv))) & 0xFF) << (8 * j);
+        w[k] = (int) pk;
     }
+    qa = make_int4(w[0], w[1], w[2], w[3]);
+    qb = make_int4(w[4], w[5], w[6], w[7]);
+}
+// 32 values -> two 16-value halves, each with its own per-16 scale
+WZY_DEV void quant16_halves(const float (&v)[32], int4& qa, int4& qb, float& da, float& db) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         float am = 0.f;
@@ -90,201 +105,121 @@ WZY_DEV void quant16x2_lane(const float* __restrict__ xp, int4& qa, int4& qb, fl
                 pk |= (uint32_t) (max(-127, min(127, rn_int(v[16 * h + 4 * k + j] * inv))) & 0xFF) << (8 * j);
             w[k] = (int) pk;
         }
-        if (h == 0) { qa = make_int4(w[0], w[1], w[2], w[3]); sa = d; }
-        else { qb = make_int4(w[0], w[1], w[2], w[3]); sb = d; }
+        if (h == 0) { qa = make_int4(w[0], w[1], w[2], w[3]); da = d; }
+        else { qb = make_int4(w[0], w[1], w[2], w[3]); db = d; }
     }
 }
-// per-32 int8 quantisation of 32 fp32 values held by one lane
-WZY_DEV void quant32x1_lane(const float* __restrict__ xp, int4& q0, int4& q1, float& s) {
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = ((const float4*) xp)[i];
-        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-    }
-    float am = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(v[i]));
-    s = am / 127.0f;
-    const float inv = s > 0.f ? 127.0f / am : 0.f;
-    int w[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t pk = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pk |= (uint32_t) (max(-127, min(127, rn_int(v[4 * k + j] * inv))) & 0xFF) << (8 * j);
-        w[k] = (int) pk;
-    }
-    q0 = make_int4(w[0], w[1], w[2], w[3]);
-    q1 = make_int4(w[4], w[5], w[6], w[7]);
-}
 
-}  // namespace
+// Window routing in LDS.  Softmax top-K per row (reference: router_top10_fast_multi,
+// src/wzy_kernels_v2.cuh:989-1090), then the grouping of the routed entries by expert (reference:
+// split_route_hit_cold_kernel / group_experts_kernel, src/wzy_cpu_moe.cuh:74-127,
+// src/wzy_kernels_v2.cuh:1390-1423).  Groups are numbered in order of first occurrence and members
+// in entry order; the combine sums in routed-slot order, so the numbering affects no result.
+struct RouteLds {
+    int ids[MAX_ENT];
+    float w[MAX_ENT];
+    int gidx[MAX_ENT];
+    int gexp[MAX_ENT];
+    int gcnt[MAX_ENT];
+    int gmem[MAX_ENT][WZY_MAX_W];
+    int n_groups;
+    int c[4];
+};
 
-// ---------------------------------------------------------------------------------------------
-// router: logits + shared gate scalar, then (last workgroup) softmax top-K per row
-// (reference: router_top10_fast_multi, src/wzy_kernels_v2.cuh:989-1090) and the grouping of the
-// routed entries by expert (reference: split_route_hit_cold_kernel / group_experts_kernel,
-// src/wzy_cpu_moe.cuh:74-127, src/wzy_kernels_v2.cuh:1390-1423).  Groups are numbered in order
-// of first occurrence and members in entry order; the combine sums in routed-slot order, so the
-// numbering does not affect any result.
-// ---------------------------------------------------------------------------------------------
+constexpr int RT_V = 16;      // logits per lane (E <= 1024)
+
+// wave wv prefetches rows wv, wv+4 of the logits (issued before anything uses them)
 template <int T>
-__global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
-    __shared__ int s_ids[MAX_ENT];
-    __shared__ float s_w[MAX_ENT];
-    __shared__ int s_gidx[MAX_ENT];
-    __shared__ int s_c[4];
-    __shared__ int s_last;
+WZY_DEV void route_prefetch(const float* __restrict__ logits, int E, float (&p)[(T + 3) / 4][RT_V]) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int rr = 0; rr < (T + 3) / 4; ++rr) {
+        const int t = wv + 4 * rr;
+#pragma unroll
+        for (int i = 0; i < RT_V; ++i) {
+            const int idx = lane + 64 * i;
+            p[rr][i] = (t < T && idx < E) ? logits[(size_t) t * E + idx] : -INFINITY;
+        }
+    }
+}
+
+template <int T>
+WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RT_V], int E, int K, RouteLds& r) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int D = a.D, E = a.E, K = a.K;
-
-    // ---- logits: wave owns rows row0 .. row0+3 (row E = shared gate) ----
-    {
-        const int row0 = (blockIdx.x * 4 + wv) * 4;
-        const int n8 = D >> 3;
-        float acc[4][T];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[s][t] = 0.f;
-        for (int j0 = 0; j0 < n8; j0 += 256) {
-            uint4 wv4[4][4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = j0 + lane + 64 * u;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const int r = row0 + s;
-                    const uint16_t* W = r < E ? a.router + (size_t) r * D : a.sgate;
-                    wv4[u][s] = (j < n8 && r <= E) ? ld_stream_u4((const uint4*) W + j) : make_uint4(0, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = j0 + lane + 64 * u;
-                if (j >= n8) continue;
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const float4 xa = *(const float4*) (a.x + (size_t) t * D + j * 8);
-                    const float4 xb = *(const float4*) (a.x + (size_t) t * D + j * 8 + 4);
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        float v = acc[s][t];
-                        v = fmaf(bf16_lo(wv4[u][s].x), xa.x, v);
-                        v = fmaf(bf16_hi(wv4[u][s].x), xa.y, v);
-                        v = fmaf(bf16_lo(wv4[u][s].y), xa.z, v);
-                        v = fmaf(bf16_hi(wv4[u][s].y), xa.w, v);
-                        v = fmaf(bf16_lo(wv4[u][s].z), xb.x, v);
-                        v = fmaf(bf16_hi(wv4[u][s].z), xb.y, v);
-                        v = fmaf(bf16_lo(wv4[u][s].w), xb.z, v);
-                        v = fmaf(bf16_hi(wv4[u][s].w), xb.w, v);
-                        acc[s][t] = v;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int r = row0 + s;
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float v = wave_sum(acc[s][t]);
-                if (lane == 0 && r < E) a.logits[(size_t) t * E + r] = v;
-                if (lane == 0 && r == E) a.sg[t] = v;
-            }
-        }
-    }
-
-    // ---- completion: the last workgroup routes ----
-    __builtin_amdgcn_s_waitcnt(0);          // this wave's stores have left the CU
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();                    // publish the workgroup's logits device-wide
-        s_last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();                        // acquire every workgroup's logits
-
-    // softmax top-K per row: wave wv routes rows wv, wv+4
-    for (int t = wv; t < T; t += 4) {
-        constexpr int MAXV = 16;            // E <= 1024
-        const float* x = a.logits + (size_t) t * E;
-        float p[MAXV];
+    for (int rr = 0; rr < (T + 3) / 4; ++rr) {
+        const int t = wv + 4 * rr;
+        if (t >= T) continue;                            // wave-uniform
         float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < MAXV; ++i) {
-            const int idx = lane + 64 * i;
-            p[i] = idx < E ? x[idx] : -INFINITY;
-            mx = fmaxf(mx, p[i]);
-        }
+        for (int i = 0; i < RT_V; ++i) mx = fmaxf(mx, p[rr][i]);
         mx = wave_max(mx);
         float es = 0.f;
 #pragma unroll
-        for (int i = 0; i < MAXV; ++i) {
-            if (lane + 64 * i < E) { p[i] = __expf(p[i] - mx); es += p[i]; }
-            else p[i] = -3.f;
+        for (int i = 0; i < RT_V; ++i) {
+            if (lane + 64 * i < E) { p[rr][i] = __expf(p[rr][i] - mx); es += p[rr][i]; }
+            else p[rr][i] = -3.f;
         }
         es = wave_sum(es);
         const float inv = 1.0f / es;
 #pragma unroll
-        for (int i = 0; i < MAXV; ++i)
-            if (lane + 64 * i < E) p[i] *= inv;
+        for (int i = 0; i < RT_V; ++i)
+            if (lane + 64 * i < E) p[rr][i] *= inv;
         float wsum = 0.f;
         for (int k = 0; k < K; ++k) {
             float bv = -4.f;
             int bi = 0x7fffffff;
 #pragma unroll
-            for (int i = 0; i < MAXV; ++i)
-                if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
+            for (int i = 0; i < RT_V; ++i)
+                if (p[rr][i] > bv) { bv = p[rr][i]; bi = lane + 64 * i; }
             wave_argmax(bv, bi);
             if (bi >= E) bi = 0;                         // non-finite logits: keep the id in range
 #pragma unroll
-            for (int i = 0; i < MAXV; ++i)
-                if (lane + 64 * i == bi) p[i] = -2.f;
-            if (lane == 0) { s_ids[t * K + k] = bi; s_w[t * K + k] = bv; }
+            for (int i = 0; i < RT_V; ++i)
+                if (lane + 64 * i == bi) p[rr][i] = -2.f;
+            if (lane == 0) { r.ids[t * K + k] = bi; r.w[t * K + k] = bv; }
             wsum += bv;
         }
         const float sc = fmaxf(wsum, 6.103515625e-05f);
-        if (lane < K) s_w[t * K + lane] = s_w[t * K + lane] / sc;
+        if (lane < K) r.w[t * K + lane] = r.w[t * K + lane] / sc;
     }
     __syncthreads();
-
     // grouping: leader = first entry of an expert, slot = rank among the expert's entries
     const int n_ent = T * K;
     int id = -1, leader = 0, slot = 0, cnt = 0;
     if (tid < n_ent) {
-        id = s_ids[tid];
+        id = r.ids[tid];
         leader = tid;
-        bool seen = false;
-        for (int f = 0; f < n_ent; ++f) {
-            if (s_ids[f] != id) continue;
-            if (!seen) { leader = f; seen = true; }
-            if (f < tid) ++slot;
-            ++cnt;
+        if (T == 1) {                                    // the K experts of one row are distinct
+            cnt = 1;
+        } else {
+            bool seen = false;
+            for (int f = 0; f < n_ent; ++f) {
+                if (r.ids[f] != id) continue;
+                if (!seen) { leader = f; seen = true; }
+                if (f < tid) ++slot;
+                ++cnt;
+            }
         }
-        a.ids[tid] = id;
-        a.wts[tid] = s_w[tid];
     }
     const bool lead = tid < n_ent && leader == tid;
     int n_groups = 0;
-    const int g_lead = excl_count256(lead, s_c, n_groups);
-    if (lead) s_gidx[tid] = g_lead;
+    const int g_lead = excl_count256(lead, r.c, n_groups);
+    if (lead) r.gidx[tid] = g_lead;
     __syncthreads();
     if (tid < n_ent) {
-        const int g = s_gidx[leader];
-        if (slot < WZY_MAX_W) a.grp_mem[g * WZY_MAX_W + slot] = tid;
+        const int g = r.gidx[leader];
+        if (slot < WZY_MAX_W) r.gmem[g][slot] = tid;
         if (lead) {
-            a.grp_exp[g] = id;
-            a.grp_cnt[g] = min(cnt, WZY_MAX_W);     // an expert occurs at most once per row
+            r.gexp[g] = id;
+            r.gcnt[g] = min(cnt, WZY_MAX_W);             // an expert occurs at most once per row
         }
     }
-    if (tid == 0) {
-        *a.n_groups = n_groups;
-        *a.counter = 0u;                    // ready for the next launch
-    }
+    if (tid == 0) r.n_groups = n_groups;
+    __syncthreads();
 }
+
+}  // namespace
 
 // ---------------------------------------------------------------------------------------------
 // gate/up.  Routed workgroups: one (group, 16-row tile); wave w owns rows j = 16*tile + 4w .. +3
@@ -293,35 +228,69 @@ __global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
 // Shared workgroups: 32 rows of the Q8_0 shared gate/up, SwiGLU, per-32 requant.
 // reference: launch_gemm_q8p x2 + silu_mul_quant32_multi (src/wzy_stage_v2.cuh:711-713;
 // src/wzy_kernels_v2.cuh:1247-1280).
+// Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
+// scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
 // ---------------------------------------------------------------------------------------------
 template <int T>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    __shared__ RouteLds r;
     __shared__ float s_act[WZY_MAX_W][32];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bid = blockIdx.x;
     const int D = a.D, F = a.F, K = a.K;
+    const int nc = D / 32;
+    int4* s_qa = (int4*) s_dyn;
+    int4* s_qb = s_qa + (size_t) T * nc;
+    float* s_sc = (float*) (s_qb + (size_t) T * nc);
 
     if (bid < a.n_routed_wg) {
+        float p[(T + 3) / 4][RT_V];
+        route_prefetch<T>(a.logits, a.E, p);
+        // stage x quantised per 16
+        for (int i = tid; i < T * nc; i += 256) {
+            const int t = i / nc, c = i - t * nc;
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 f = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+            }
+            int4 qa, qb;
+            float da, db;
+            quant16_halves(v, qa, qb, da, db);
+            s_qa[i] = qa;
+            s_qb[i] = qb;
+            ((float2*) s_sc)[i] = make_float2(da, db);
+        }
+        route_compute<T>(p, a.E, K, r);
+        if (bid == 0) {                                  // publish the routing for moe_down
+            const int n_ent = T * K;
+            for (int i = tid; i < n_ent; i += blockDim.x) {
+                a.ids[i] = r.ids[i];
+                a.wts[i] = r.w[i];
+                if (i < r.n_groups) {
+                    a.grp_exp[i] = r.gexp[i];
+                    a.grp_cnt[i] = r.gcnt[i];
+                    for (int m = 0; m < WZY_MAX_W; ++m) a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
+                }
+            }
+            if (tid == 0) *a.n_groups = r.n_groups;
+        }
         const int tiles = F / 16;
         const int g = bid / tiles, jt = bid - g * tiles;
-        if (g >= *a.n_groups) return;                 // workgroup-uniform
-        const int e = a.grp_exp[g], cnt = a.grp_cnt[g];
-        int mem[T];
-#pragma unroll
-        for (int m = 0; m < T; ++m) mem[m] = m < cnt ? a.grp_mem[g * WZY_MAX_W + m] : 0;
+        if (g >= r.n_groups) return;                     // workgroup-uniform
+        const int e = r.gexp[g], cnt = r.gcnt[g];
         const MoeOffsets o = moe_offsets(D, F);
         const uint8_t* rec = a.experts + (size_t) e * o.rec;
-        const float sc_gate = ((const float*) (rec + o.tail))[0];
-        const float sc_up = ((const float*) (rec + o.tail))[1];
         const int j0 = jt * 16 + 4 * w;
         float acc[8][T];
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr)
 #pragma unroll
             for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
-
-        const int nchunk = D / 32;
-        for (int c = lane; c < nchunk; c += 64) {
+        float sc_gate = 0.f, sc_up = 0.f;
+        for (int c = lane; c < nc; c += 64) {
             int4 code[8];
             uint32_t sc2[8];
 #pragma unroll
@@ -330,21 +299,25 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
                 code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
                 sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
             }
-            int4 xa[T], xb[T];
-            float xsa[T], xsb[T];
-#pragma unroll
-            for (int m = 0; m < T; ++m)
-                if (m < cnt) quant16x2_lane(a.x + (size_t) (mem[m] / K) * D + (size_t) c * 32, xa[m], xb[m], xsa[m], xsb[m]);
+            sc_gate = ((const float*) (rec + o.tail))[0];
+            sc_up = ((const float*) (rec + o.tail))[1];
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int4 wa = e2m1_sub16((uint32_t) code[rr].x, (uint32_t) code[rr].y);
                 const int4 wb = e2m1_sub16((uint32_t) code[rr].z, (uint32_t) code[rr].w);
                 const float wsa = ue4m3_half(sc2[rr] & 0xFFu), wsb = ue4m3_half(sc2[rr] >> 8);
 #pragma unroll
-                for (int m = 0; m < T; ++m)
-                    if (m < cnt) acc[rr][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xa[m], xb[m], xsa[m], xsb[m], acc[rr][m]);
+                for (int m = 0; m < T; ++m) {
+                    if (m < cnt) {
+                        const int xi = (r.gmem[g][m] / K) * nc + c;
+                        const float2 xs = ((const float2*) s_sc)[xi];
+                        acc[rr][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, s_qa[xi], s_qb[xi], xs.x, xs.y, acc[rr][m]);
+                    }
+                }
             }
         }
+        sc_gate = __shfl(sc_gate, 0, 64);
+        sc_up = __shfl(sc_up, 0, 64);
 #pragma unroll
         for (int m = 0; m < T; ++m) {
             if (m < cnt) {
@@ -364,9 +337,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             const float d = amax / 127.0f;
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
-            int f = 0;
-#pragma unroll
-            for (int mm = 0; mm < T; ++mm) if (mm == m) f = mem[mm];
+            const int f = r.gmem[g][m];
             a.aq16[(size_t) f * F + jt * 16 + jj] = (int8_t) q;
             if (jj == 0) a.as16[(size_t) f * (F / 16) + jt] = d;
         }
@@ -375,37 +346,57 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
 
     // shared expert: rows j in [32*sb, 32*sb + 32), wave w owns j = 32*sb + 8w .. +7 (two halves of 4)
     const int sb = bid - a.n_routed_wg;
-    const int nb = D / 32;
-#pragma unroll 1
+    int4 c0[2][8], c1[2][8];
+    uint16_t sraw[2][8];
+    const int bl = min(lane, nc - 1);
+#pragma unroll
     for (int half = 0; half < 2; ++half) {
         const int j0 = 32 * sb + 8 * w + 4 * half;
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int8_t* q = (rr < 4) ? a.shg_q : a.shu_q;
+            const uint16_t* s = (rr < 4) ? a.shg_s : a.shu_s;
+            const int row = j0 + (rr & 3);
+            const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) bl * 32);
+            c0[half][rr] = ld_stream_i4(cp);
+            c1[half][rr] = ld_stream_i4(cp + 1);
+            sraw[half][rr] = s[(size_t) row * nc + bl];
+        }
+    }
+    // stage x quantised per 32
+    for (int i = tid; i < T * nc; i += 256) {
+        const int t = i / nc, c = i - t * nc;
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 f = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+        int4 qa, qb;
+        float d;
+        quant32_halves(v, qa, qb, d);
+        s_qa[i] = qa;
+        s_qb[i] = qb;
+        s_sc[i] = d;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
         float acc[8][T];
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr)
 #pragma unroll
             for (int t = 0; t < T; ++t) acc[rr][t] = 0.f;
-        for (int b = lane; b < nb; b += 64) {
-            int4 c0[8], c1[8];
-            uint16_t sraw[8];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int8_t* q = (rr < 4) ? a.shg_q : a.shu_q;
-                const uint16_t* s = (rr < 4) ? a.shg_s : a.shu_s;
-                const int row = j0 + (rr & 3);
-                const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) b * 32);
-                c0[rr] = ld_stream_i4(cp);
-                c1[rr] = ld_stream_i4(cp + 1);
-                sraw[rr] = s[(size_t) row * nb + b];       // converted after every load is issued
-            }
+        for (int b = lane; b < nc; b += 64) {            // D <= 2048: one 32-block per lane
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                int4 x0, x1;
-                float xsc;
-                quant32x1_lane(a.x + (size_t) t * D + (size_t) b * 32, x0, x1, xsc);
+                const int xi = t * nc + b;
+                const int4 x0 = s_qa[xi], x1 = s_qb[xi];
+                const float xsc = s_sc[xi];
 #pragma unroll
                 for (int rr = 0; rr < 8; ++rr)
-                    acc[rr][t] = fmaf(h16_to_f(sraw[rr]) * xsc, (float) (dot16(c0[rr], x0) + dot16(c1[rr], x1)),
-                                      acc[rr][t]);
+                    acc[rr][t] = fmaf(h16_to_f(sraw[half][rr]) * xsc,
+                                      (float) (dot16(c0[half][rr], x0) + dot16(c1[half][rr], x1)), acc[rr][t]);
             }
         }
 #pragma unroll
@@ -436,12 +427,15 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
 // combine comb = sigmoid(sgate)*shared + sum_k w_k * part_k (routed-slot order) stays in LDS.
 // Work items (group or shared, row) go round-robin to sixteen 16-lane slots; a slot issues the
 // loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
-// (F = 512: 16 chunks per row).
+// (F = 512: 16 chunks per row).  STAGE: the routed and shared activations are copied to LDS first
+// (dynamic LDS: aq halves [n_ent][F/32] x2 int4, as [n_ent][F/16] float, shq halves [T][F/32] x2
+// int4, shs [T][F/32] float).
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
 // ---------------------------------------------------------------------------------------------
-template <int T>
+template <int T, bool STAGE>
 __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_part[MAX_ENT][DN_TILE];
     __shared__ float s_sh[WZY_MAX_W][DN_TILE];
     __shared__ int s_gexp[MAX_ENT], s_gcnt[MAX_ENT];
@@ -449,17 +443,37 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     const int tid = threadIdx.x;
     const int D = a.D, F = a.F, K = a.K;
     const int d0 = blockIdx.x * DN_TILE;
+    const int nchunk = F / 32, n_ent = T * K;
     const int ng = *a.n_groups;
+    int4* s_aqa = (int4*) s_dyn;
+    int4* s_aqb = s_aqa + (size_t) n_ent * nchunk;
+    float* s_as = (float*) (s_aqb + (size_t) n_ent * nchunk);
+    int4* s_sha = (int4*) (s_as + (size_t) n_ent * (F / 16));
+    int4* s_shb = s_sha + (size_t) T * nchunk;
+    float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
     for (int i = tid; i < ng; i += blockDim.x) {
         s_gexp[i] = a.grp_exp[i];
         s_gcnt[i] = a.grp_cnt[i];
 #pragma unroll
         for (int m = 0; m < WZY_MAX_W; ++m) s_gmem[i][m] = a.grp_mem[i * WZY_MAX_W + m];
     }
+    if (STAGE) {
+        for (int i = tid; i < n_ent * nchunk; i += 256) {
+            const int4* xp = (const int4*) (a.aq16 + (size_t) i * 32);
+            s_aqa[i] = xp[0];
+            s_aqb[i] = xp[1];
+        }
+        for (int i = tid; i < n_ent * (F / 16) / 4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
+        for (int i = tid; i < T * nchunk; i += 256) {
+            const int4* xp = (const int4*) (a.shq32 + (size_t) i * 32);
+            s_sha[i] = xp[0];
+            s_shb[i] = xp[1];
+            s_shs[i] = a.shs32[i];
+        }
+    }
     __syncthreads();
     const MoeOffsets o = moe_offsets(D, F);
     const int slot = tid >> 4, li = tid & 15;
-    const int nchunk = F / 32;
     const int n_items = (ng + 1) * DN_TILE;          // group ng = shared expert
     for (int i0 = slot; i0 < n_items; i0 += 16 * DN_BATCH) {
         float acc[DN_BATCH][T];
@@ -471,13 +485,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             for (int m = 0; m < T; ++m) acc[b][m] = 0.f;
         }
         for (int c = li; c < nchunk; c += 16) {
-            // loads of all DN_BATCH items first (raw scales; for single-row windows also the
-            // activations), arithmetic afterwards
+            // the weight loads of all DN_BATCH items first (raw scales), arithmetic afterwards
             int4 c0[DN_BATCH], c1[DN_BATCH];
             uint32_t sraw[DN_BATCH];
-            constexpr int BX = (T == 1) ? DN_BATCH : 1;
-            int4 xa0[BX], xa1[BX];
-            float2 xsv[BX];
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
                 const int item = min(i0 + 16 * b, n_items - 1);
@@ -488,24 +498,11 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                     c1[b] = make_int4(0, 0, 0, 0);
                     sraw[b] = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
                     sdn[b] = ((const float*) (rec + o.tail))[2];
-                    if (T == 1) {
-                        const int f = s_gmem[g][0];
-                        const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
-                        xa0[T == 1 ? b : 0] = xp[0];
-                        xa1[T == 1 ? b : 0] = xp[1];
-                        xsv[T == 1 ? b : 0] = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
-                    }
                 } else {
                     const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
                     c0[b] = ld_stream_i4(cp);
                     c1[b] = ld_stream_i4(cp + 1);
                     sraw[b] = a.shd_s[(size_t) d * nchunk + c];
-                    if (T == 1) {
-                        const int4* xp = (const int4*) (a.shq32 + (size_t) c * 32);
-                        xa0[T == 1 ? b : 0] = xp[0];
-                        xa1[T == 1 ? b : 0] = xp[1];
-                        xsv[T == 1 ? b : 0] = make_float2(a.shs32[c], 0.f);
-                    }
                 }
             }
 #pragma unroll
@@ -517,15 +514,16 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                     const int4 wa = e2m1_sub16((uint32_t) c0[b].x, (uint32_t) c0[b].y);
                     const int4 wb = e2m1_sub16((uint32_t) c0[b].z, (uint32_t) c0[b].w);
                     const float wsa = ue4m3_half(sraw[b] & 0xFFu), wsb = ue4m3_half(sraw[b] >> 8);
-                    if (T == 1) {
-                        const int bx = T == 1 ? b : 0;
-                        acc[b][0] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xa0[bx], xa1[bx], xsv[bx].x, xsv[bx].y, acc[b][0]);
-                    } else {
-                        const int cnt = s_gcnt[g];
+                    const int cnt = s_gcnt[g];
 #pragma unroll
-                        for (int m = 0; m < T; ++m) {
-                            if (m < cnt) {
-                                const int f = s_gmem[g][m];
+                    for (int m = 0; m < T; ++m) {
+                        if (m < cnt) {
+                            const int f = s_gmem[g][m];
+                            if (STAGE) {
+                                const int xi = f * nchunk + c;
+                                const float2 xs = ((const float2*) s_as)[xi];
+                                acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, s_aqa[xi], s_aqb[xi], xs.x, xs.y, acc[b][m]);
+                            } else {
                                 const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
                                 const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
                                 acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xp[0], xp[1], xs.x, xs.y, acc[b][m]);
@@ -534,12 +532,13 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                     }
                 } else {
                     const float dw = h16_to_f((uint16_t) sraw[b]);
-                    if (T == 1) {
-                        const int bx = T == 1 ? b : 0;
-                        acc[b][0] = fmaf(dw * xsv[bx].x, (float) (dot16(c0[b], xa0[bx]) + dot16(c1[b], xa1[bx])), acc[b][0]);
-                    } else {
 #pragma unroll
-                        for (int t = 0; t < T; ++t) {
+                    for (int t = 0; t < T; ++t) {
+                        if (STAGE) {
+                            const int xi = t * nchunk + c;
+                            acc[b][t] = fmaf(dw * s_shs[xi], (float) (dot16(c0[b], s_sha[xi]) + dot16(c1[b], s_shb[xi])),
+                                             acc[b][t]);
+                        } else {
                             const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) c * 32);
                             const float xsc = a.shs32[(size_t) t * nchunk + c];
                             acc[b][t] = fmaf(dw * xsc, (float) (dot16(c0[b], xp[0]) + dot16(c1[b], xp[1])), acc[b][t]);
@@ -594,7 +593,6 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
     w.grp_exp = a.take<int>(n_ent);
     w.grp_cnt = a.take<int>(n_ent);
     w.grp_mem = a.take<int>((size_t) n_ent * WZY_MAX_W);
-    w.counter = a.take<unsigned int>(1);
     w.aq16 = a.take<int8_t>((size_t) n_ent * F);
     w.as16 = a.take<float>((size_t) n_ent * F / 16);
     w.shq32 = a.take<int8_t>((size_t) T * F);
@@ -606,7 +604,8 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
 int moe_check(const wzy_moe_weights* w, int T) {
     WZY_REQUIRE(w != nullptr, "moe: null weights");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "moe: T must be in [1, %d]", WZY_MAX_W);
-    WZY_REQUIRE(w->n_embd % 256 == 0 && w->n_embd >= 256 && w->n_embd <= 8192, "moe: n_embd must be a multiple of 256 <= 8192");
+    WZY_REQUIRE(w->n_embd % 256 == 0 && w->n_embd >= 256 && w->n_embd <= 2048,
+                "moe: n_embd must be a multiple of 256 <= 2048");
     WZY_REQUIRE(w->n_ff % 64 == 0 && w->n_ff >= 64, "moe: n_ff must be a multiple of 64");
     WZY_REQUIRE(w->n_exp >= 1 && w->n_exp <= 1024, "moe: n_exp must be in [1, 1024]");
     WZY_REQUIRE(w->top_k >= 1 && w->top_k <= MOE_MAX_K && w->top_k <= w->n_exp, "moe: top_k must be in [1, %d]",
@@ -617,38 +616,20 @@ int moe_check(const wzy_moe_weights* w, int T) {
     return WZY_OK;
 }
 
-template <int T>
-static void launch_rt_t(const MoeRtArgs& a, hipStream_t st) {
-    const int blocks = (a.E + 1 + 15) / 16;
-    hipLaunchKernelGGL((moe_router_kernel<T>), dim3(blocks), dim3(256), 0, st, a);
-}
-
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st) {
-    MoeRtArgs a{};
-    a.router = w->router; a.sgate = w->sgate; a.x = x; a.D = w->n_embd; a.E = w->n_exp; a.K = w->top_k;
-    a.logits = ws.logits; a.sg = ws.sg; a.ids = ws.ids; a.wts = ws.wts;
-    a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
-    a.counter = ws.counter;
-    switch (T) {
-        case 1: launch_rt_t<1>(a, st); break;
-        case 2: launch_rt_t<2>(a, st); break;
-        case 3: launch_rt_t<3>(a, st); break;
-        case 4: launch_rt_t<4>(a, st); break;
-        case 5: launch_rt_t<5>(a, st); break;
-        case 6: launch_rt_t<6>(a, st); break;
-        case 7: launch_rt_t<7>(a, st); break;
-        default: launch_rt_t<8>(a, st); break;
-    }
-    WZY_LAUNCH_CHECK();
-    return WZY_OK;
+    GemvSegs segs;
+    segs.n = 2;
+    segs.seg[0] = GemvSeg{w->router, nullptr, ws.logits, w->n_exp, GEMV_BF16, 0, 0};
+    segs.seg[1] = GemvSeg{w->sgate, nullptr, ws.sg, 1, GEMV_BF16, 1, 0};
+    return launch_gemv_segs(segs, x, w->n_embd, T, st);
 }
 
 static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T) {
     MoeGuArgs a{};
-    a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.K = w->top_k;
-    a.x = x;
-    a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
-    a.aq16 = ws.aq16; a.as16 = ws.as16;
+    a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.E = w->n_exp; a.K = w->top_k;
+    a.x = x; a.logits = ws.logits;
+    a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt;
+    a.grp_mem = ws.grp_mem; a.aq16 = ws.aq16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shq32 = ws.shq32; a.shs32 = ws.shs32;
     a.n_routed_wg = (w->n_ff / 16) * T * w->top_k;
@@ -665,11 +646,18 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
 
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((moe_gate_up_kernel<T>), dim3(a.n_routed_wg + a.F / 32), dim3(256), 0, st, a);
+    const size_t lds = (size_t) T * (a.D / 32) * (2 * sizeof(int4) + sizeof(float2));
+    hipLaunchKernelGGL((moe_gate_up_kernel<T>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
 }
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((moe_down_kernel<T>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
+    const int n_ent = T * a.K, nchunk = a.F / 32;
+    const size_t lds = (size_t) n_ent * nchunk * 2 * sizeof(int4) + (size_t) n_ent * (a.F / 16) * sizeof(float) +
+                       (size_t) T * nchunk * (2 * sizeof(int4) + sizeof(float));
+    if (lds <= (size_t) DN_STAGE_BYTES)
+        hipLaunchKernelGGL((moe_down_kernel<T, true>), dim3(a.D / DN_TILE), dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((moe_down_kernel<T, false>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
 }
 
 static void launch_gu(const MoeGuArgs& a, int T, hipStream_t st) {
@@ -716,7 +704,6 @@ extern "C" int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, fl
                              void* workspace, size_t workspace_bytes, void* stream) {
     WZY_TRY(moe_check(w, T));
     WZY_REQUIRE(x && comb && workspace, "wzy_moe_block: null pointer");
-    WZY_REQUIRE(w->n_embd % DN_TILE == 0, "wzy_moe_block: n_embd must be a multiple of %d", DN_TILE);
     size_t need = 0;
     MoeWs ws = moe_ws_carve(workspace, workspace_bytes, w->n_embd, w->n_ff, w->n_exp, w->top_k, T, &need);
     WZY_REQUIRE(need <= workspace_bytes, "wzy_moe_block: workspace too small (%zu < %zu)", workspace_bytes, need);

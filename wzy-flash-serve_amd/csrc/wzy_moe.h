@@ -10,26 +10,19 @@
 
 namespace wzy {
 
-// Device scratch of one MoE block call, carved from a workspace.  The workspace must be zeroed
-// before its first use; the kernels leave `counter` at zero again when they finish.
+// Device scratch of one MoE block call, carved from a workspace.
 struct MoeWs {
     float* logits; float* sg;             // router logits [T x E], shared gate scalar [T]
     int* ids;      float* wts;            // [T x K] routed experts and renormalised weights
     int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // distinct experts of the window
-    unsigned int* counter;                // router workgroups done (last one routes)
     int8_t* aq16;  float* as16;           // SwiGLU activations per routed entry, per-16 int8
     int8_t* shq32; float* shs32;          // shared-expert SwiGLU activation, per-32 int8
 };
 
-struct MoeRtArgs {
-    const uint16_t* router; const uint16_t* sgate; const float* x; int D, E, K;
-    float* logits; float* sg; int* ids; float* wts;
-    int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem; unsigned int* counter;
-};
 struct MoeGuArgs {
-    const uint8_t* experts; int D, F, K;
-    const float* x;
-    const int* n_groups; const int* grp_exp; const int* grp_cnt; const int* grp_mem;
+    const uint8_t* experts; int D, F, E, K;
+    const float* x; const float* logits;
+    int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // published by workgroup 0
     int8_t* aq16; float* as16;
     const int8_t* shg_q; const uint16_t* shg_s; const int8_t* shu_q; const uint16_t* shu_s;
     int8_t* shq32; float* shs32;
@@ -45,9 +38,9 @@ struct MoeDnArgs {
 
 MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, size_t* need);
 int moe_check(const wzy_moe_weights* w, int T);
-// router GEMV (+ shared gate row) over fp32 x [T x D], softmax top-K and expert grouping
+// router GEMV (+ shared gate row) over fp32 x [T x D]
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st);
-// gate/up + down + combine into comb [T x D]
+// routing + gate/up, down + combine into comb [T x D]
 int moe_launch_experts(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, float* comb, hipStream_t st);
 
 }  // namespace wzy
