@@ -9,7 +9,7 @@
 //            lo = silu(down . quant32(xn) / HC), inj = inj_w . xn.
 //            Every workgroup rebuilds quant32(xn) for the window in LDS (the residual is 32 KB per
 //            row and L2-resident), so no cross-workgroup synchronisation is needed; workgroup w
-//            writes every gridDim-th 32-block of R_out.
+//            writes every gridDim-th 32-block of R_out; four extra workgroups compute inj.
 //   hc_post: mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)); lo is quantised
 //            once per workgroup into LDS.
 // Both kernels issue every global load a row needs before using any of them (indices clamped
@@ -66,22 +66,30 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
     int8_t* s_xq = (int8_t*) s_dyn;
     float* s_xs = (float*) (s_dyn + (size_t) T * HCD);
     const bool fold = a.bo != nullptr;
-    const bool do_inj = a.inj_w != nullptr && blockIdx.x < HC4;
+    // workgroups [0, n_row_wg) own down rows; the HC workgroups after them (inject weights only)
+    // compute inj row blockIdx.x - n_row_wg
+    const int n_row_wg = (L + 4 * RPW - 1) / (4 * RPW);
+    const bool has_rows = (int) blockIdx.x < n_row_wg;
+    const bool do_inj = !has_rows && a.inj_w != nullptr;
+    const int inj_row = blockIdx.x - n_row_wg;
+    const bool wave_stream = NBK == 1 && D == 64 * 32;   // wave w owns all of stream w
 
     // 0. this wave's down rows (raw codes and fp16 scales), issued first
     const int row0 = (blockIdx.x * 4 + w) * RPW;
     int4 c0[NBL][RPW], c1[NBL][RPW];
     uint16_t sraw[NBL][RPW];
+    if (has_rows) {
 #pragma unroll
-    for (int i = 0; i < NBL; ++i) {
-        const int b = min(lane + 64 * i, nb - 1);
+        for (int i = 0; i < NBL; ++i) {
+            const int b = min(lane + 64 * i, nb - 1);
 #pragma unroll
-        for (int s = 0; s < RPW; ++s) {
-            const int r = min(row0 + s, L - 1);
-            const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) b * 32);
-            c0[i][s] = ld_stream_i4(cp);
-            c1[i][s] = ld_stream_i4(cp + 1);
-            sraw[i][s] = a.down_s[(size_t) r * nb + b];
+            for (int s = 0; s < RPW; ++s) {
+                const int r = min(row0 + s, L - 1);
+                const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) b * 32);
+                c0[i][s] = ld_stream_i4(cp);
+                c1[i][s] = ld_stream_i4(cp + 1);
+                sraw[i][s] = a.down_s[(size_t) r * nb + b];
+            }
         }
     }
     // 1. row-independent inputs of this thread's blocks: norm weights, inject weights
@@ -96,7 +104,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
         if (do_inj) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                iw[k][j] = *(const uint4*) (a.inj_w + (size_t) blockIdx.x * HCD + (size_t) 32 * b + 8 * j);
+                iw[k][j] = *(const uint4*) (a.inj_w + (size_t) inj_row * HCD + (size_t) 32 * b + 8 * j);
         }
     }
 
@@ -139,6 +147,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
         }
         // 3. folded values and the per-thread sums of squares
         float v[NBK][32];
+        float sc_w = 0.f;
 #pragma unroll
         for (int k = 0; k < NBK; ++k) {
             const float gw = fold ? 2.0f / (1.0f + __expf(-ip[k] / (float) HC4)) : 0.f;
@@ -162,27 +171,36 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
                 ss = fmaf(x.z, x.z, ss);
                 ss = fmaf(x.w, x.w, ss);
             }
-            // 4. sums over 8 consecutive blocks (never straddle a stream: D % 256 == 0)
-            ss = sum8(ss);
-            const int b = tid + 256 * k;
-            if ((lane & 7) == 0 && b < nb) s_seg[t][b >> 3] = ss;
+            // 4. per-stream sums.  D = 2048 with one block per thread: wave w holds exactly stream w,
+            //    so the sum is a wave reduction; otherwise sums over 8 consecutive blocks (never
+            //    straddling a stream, D % 256 == 0) are combined through LDS.
+            if (wave_stream) {
+                sc_w = 1.0f / sqrtf(wave_sum(ss) / (float) D + a.eps);
+                if (lane == 0 && blockIdx.x == 0) a.nsc[t * HC4 + w] = sc_w;
+            } else {
+                ss = sum8(ss);
+                const int b = tid + 256 * k;
+                if ((lane & 7) == 0 && b < nb) s_seg[t][b >> 3] = ss;
+            }
         }
-        __syncthreads();
-        if (tid < HC4) {
-            float tot = 0.f;
-            for (int i = 0; i < spb; ++i) tot += s_seg[t][tid * spb + i];
-            const float sc = 1.0f / sqrtf(tot / (float) D + a.eps);
-            s_nsc[t * HC4 + tid] = sc;
-            if (blockIdx.x == 0) a.nsc[t * HC4 + tid] = sc;
+        if (!wave_stream) {
+            __syncthreads();
+            if (tid < HC4) {
+                float tot = 0.f;
+                for (int i = 0; i < spb; ++i) tot += s_seg[t][tid * spb + i];
+                const float sc = 1.0f / sqrtf(tot / (float) D + a.eps);
+                s_nsc[t * HC4 + tid] = sc;
+                if (blockIdx.x == 0) a.nsc[t * HC4 + tid] = sc;
+            }
+            __syncthreads();
         }
-        __syncthreads();
         // 5. xn quantised per 32 into LDS, inject partial, R_out blocks
 #pragma unroll
         for (int k = 0; k < NBK; ++k) {
             const int b = tid + 256 * k;
             if (b >= nb) continue;
             const int c = (32 * b) / D, d0 = (32 * b) % D;
-            const float sc = s_nsc[t * HC4 + c];
+            const float sc = wave_stream ? sc_w : s_nsc[t * HC4 + c];
             float xn[32];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -207,13 +225,15 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
                     inj_acc[t] = acc;
                 }
             }
-            int4 q0, q1;
-            float xs;
-            quant32_vals(xn, q0, q1, xs);
-            int4* dst = (int4*) (s_xq + (size_t) t * HCD + (size_t) 32 * b);
-            dst[0] = q0;
-            dst[1] = q1;
-            s_xs[t * nb + b] = xs;
+            if (has_rows) {
+                int4 q0, q1;
+                float xs;
+                quant32_vals(xn, q0, q1, xs);
+                int4* dst = (int4*) (s_xq + (size_t) t * HCD + (size_t) 32 * b);
+                dst[0] = q0;
+                dst[1] = q1;
+                s_xs[t * nb + b] = xs;
+            }
             if ((b % gridDim.x) == blockIdx.x) {
                 float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
 #pragma unroll
@@ -226,8 +246,9 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float s = block_sum<4>(inj_acc[t], s_inj);
-            if (tid == 0) a.inj[t * HC4 + blockIdx.x] = s;
+            if (tid == 0) a.inj[t * HC4 + inj_row] = s;
         }
+        return;
     }
     __syncthreads();
 
@@ -344,8 +365,7 @@ template <int T, int DC, int RPW>
 void launch_pre_tdc(const HcPreArgs& a, hipStream_t st) {
     const int HCD = HC4 * a.D;
     const int rows_wg = 4 * RPW;
-    int blocks = (a.HCLR + rows_wg - 1) / rows_wg;
-    if (a.inj_w && blocks < HC4) blocks = HC4;
+    const int blocks = (a.HCLR + rows_wg - 1) / rows_wg + (a.inj_w ? HC4 : 0);
     const size_t lds = (size_t) T * HCD + (size_t) T * (HCD / 32) * sizeof(float);
     hipLaunchKernelGGL((hc_pre_kernel<T, DC, RPW>), dim3(blocks), dim3(256), lds, st, a);
 }

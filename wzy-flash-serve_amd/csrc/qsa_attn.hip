@@ -2,15 +2,16 @@
 //
 //  qsa_topk   exact top-`topk` cells of one row, one 1024-thread workgroup: the block scores are
 //             loaded once into registers as order-preserving keys, a 4 x 8-bit radix select finds
-//             the threshold key (LDS histogram per pass, parallel suffix scan over the 256 bins),
+//             the threshold key (per-wave LDS histograms per pass, digit found by one wave),
 //             then every block above the threshold is taken whole and blocks at the threshold are
 //             filled in the reference's tie order.  The reference walks the blocks with 256 threads,
 //             thread t owning blocks t, t+256, ... and emitting them thread-major; here thread
 //             4t+s owns the s-th quarter of thread t's blocks, so a scan in thread order reproduces
 //             that order exactly.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
-//  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, row) stages
-//             the chunk's INT8 K and V rows in LDS with one round of 128-bit loads, computes the
-//             GQA heads' scores (lane = cell), a local softmax, and the INT8 V sum (thread = dim).
+//  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, slice of 4
+//             q heads, row) stages the chunk's INT8 K and V rows in LDS with one round of 128-bit
+//             loads, computes its heads' scores (wave = head, lane = cell), a local softmax, and the
+//             INT8 V sum (thread = dim).
 //  qsa_combine merges the chunks (max / sum rescaling) and applies sigmoid(gate).
 //             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532)
 #include "wzy_device.h"
@@ -25,6 +26,7 @@ constexpr int TK_THREADS = 1024;
 constexpr int TK_MAXJ_SMALL = 16;    // blocks per thread: 16384 blocks (65532 cells at 4 per block)
 constexpr int TK_MAXJ_LARGE = 66;    // 67584 blocks (270332 cells); keys partly spill to scratch
 constexpr int ATT_GQ_MAX = 16;       // q heads per kv head
+constexpr int ATT_HPW = 4;           // q heads per attention workgroup (one per wave in the score phase)
 constexpr int ATT_ROW = 256 + 16;    // LDS bytes per cell row (hd = 256 codes + pad against bank conflicts)
 constexpr int ATT_CH_MAX = 32;       // chunks per row: topk <= 2048
 
@@ -64,7 +66,7 @@ template <int TK_MAXJ>
 __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
                                                               const float* __restrict__ scores, int max_b,
                                                               int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
-    __shared__ int hist[256];
+    __shared__ int hist[TK_THREADS / 64][256];      // one histogram per wave (no cross-wave atomic contention)
     __shared__ int s_w[TK_THREADS / 64];
     __shared__ int s_c[TK_THREADS / 64];
     __shared__ int s_digit, s_above;
@@ -98,13 +100,13 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
 
     uint32_t prefix = 0;
     int above = 0;
-    if (p < 256) hist[p] = 0;
+    for (int i = p; i < (TK_THREADS / 64) * 256; i += TK_THREADS) (&hist[0][0])[i] = 0;
     __syncthreads();
     for (int shift = 24; shift >= 0; shift -= 8) {
         const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
 #pragma unroll
         for (int q = 0; q < TK_MAXJ; ++q)
-            if (wgt(q) > 0 && (key[q] & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[(key[q] >> shift) & 255u], wgt(q));
+            if (wgt(q) > 0 && (key[q] & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[p >> 6][(key[q] >> shift) & 255u], wgt(q));
         __syncthreads();
         // wave 0 picks the digit: lane l holds digits 255-4l .. 252-4l (highest first); the
         // threshold digit is the highest one at which the weight at or above it reaches the width
@@ -113,8 +115,13 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
             int h[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                h[j] = hist[255 - 4 * l - j];
-                hist[255 - 4 * l - j] = 0;           // cleared for the next pass
+                int sum = 0;
+#pragma unroll
+                for (int wv = 0; wv < TK_THREADS / 64; ++wv) {
+                    sum += hist[wv][255 - 4 * l - j];
+                    hist[wv][255 - 4 * l - j] = 0;   // cleared for the next pass
+                }
+                h[j] = sum;
             }
             const int s4 = h[0] + h[1] + h[2] + h[3];
             int incl = s4;
@@ -183,13 +190,14 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     __shared__ __align__(16) int8_t s_k[QSA_ATT_CHUNK * ATT_ROW];
     __shared__ __align__(16) int8_t s_v[QSA_ATT_CHUNK * ATT_ROW];
     __shared__ float s_ks[QSA_ATT_CHUNK][4], s_vs[QSA_ATT_CHUNK][4];
-    __shared__ __align__(16) float s_q[ATT_GQ_MAX][256];
-    __shared__ __align__(16) float s_p[QSA_ATT_CHUNK][ATT_GQ_MAX];   // softmax weights, [cell][head]
+    __shared__ __align__(16) float s_q[ATT_HPW][256];
+    __shared__ __align__(16) float s_p[QSA_ATT_CHUNK][ATT_HPW];   // softmax weights, [cell][head]
     __shared__ long long s_slot[QSA_ATT_CHUNK];
     const QsaDims& dm = a.dm;
-    const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
+    const int gq = dm.qh / dm.kvh, nhs = (gq + ATT_HPW - 1) / ATT_HPW;
+    const int c = blockIdx.x, j = blockIdx.y / nhs, hs = blockIdx.y % nhs, t = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int kvd = dm.kvh * 256, gq = dm.qh / dm.kvh;
+    const int kvd = dm.kvh * 256;
     const int n_kv = *a.pos + t + 1;
     const int width = min(n_kv, dm.topk);
     const int c0 = c * QSA_ATT_CHUNK;
@@ -203,11 +211,11 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
         if (tid < ncell) sl = (long long) qsa_kv_slot(n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx], dm);
         s_slot[tid] = sl;
     }
-    for (int i = tid; i < ATT_GQ_MAX * 64; i += 256) {        // rows >= gq are zero
-        const int hh = i >> 6, d4 = i & 63;
+    {                                                // this slice's heads; rows past gq are zero
+        const int hh = tid >> 6, d4 = tid & 63, h = hs * ATT_HPW + hh;
         *(float4*) &s_q[hh][4 * d4] =
-            hh < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + hh) * 512 + 4 * d4)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
+            h < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + h) * 512 + 4 * d4)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
 
@@ -218,101 +226,87 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const long long sl = s_slot[(tid >> 4) + 16 * k];
-            if (sl >= 0) {
-                const size_t off = (size_t) sl * kvd + (size_t) j * 256 + (size_t) part * 16;
-                kr[k] = *(const int4*) (a.kv.kq + off);
-                vr[k] = *(const int4*) (a.kv.vq + off);
-            } else {
-                kr[k] = vr[k] = make_int4(0, 0, 0, 0);
-            }
+            const size_t off = (size_t) (sl >= 0 ? sl : 0) * kvd + (size_t) j * 256 + (size_t) part * 16;
+            kr[k] = *(const int4*) (a.kv.kq + off);
+            vr[k] = *(const int4*) (a.kv.vq + off);
         }
         const int cs = tid >> 2, g = tid & 3;
         const long long sls = s_slot[cs];
-        const float ksc = sls >= 0 ? h16_to_f(a.kv.ks[(size_t) sls * (kvd / 64) + (size_t) j * 4 + g]) : 0.f;
-        const float vsc = sls >= 0 ? h16_to_f(a.kv.vs[(size_t) sls * (kvd / 64) + (size_t) j * 4 + g]) : 0.f;
+        const size_t soff = (size_t) (sls >= 0 ? sls : 0) * (kvd / 64) + (size_t) j * 4 + g;
+        const uint16_t kh = a.kv.ks[soff], vh = a.kv.vs[soff];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int cell = (tid >> 4) + 16 * k;
-            *(int4*) (s_k + cell * ATT_ROW + part * 16) = kr[k];
-            *(int4*) (s_v + cell * ATT_ROW + part * 16) = vr[k];
+            const bool ok = s_slot[cell] >= 0;
+            *(int4*) (s_k + cell * ATT_ROW + part * 16) = ok ? kr[k] : make_int4(0, 0, 0, 0);
+            *(int4*) (s_v + cell * ATT_ROW + part * 16) = ok ? vr[k] : make_int4(0, 0, 0, 0);
         }
-        s_ks[cs][g] = ksc;
-        s_vs[cs][g] = vsc;
+        s_ks[cs][g] = sls >= 0 ? h16_to_f(kh) : 0.f;
+        s_vs[cs][g] = sls >= 0 ? h16_to_f(vh) : 0.f;
     }
     __syncthreads();
 
-    // scores and local softmax: lane = cell, wave w owns heads w, w+4, w+8, w+12
+    // scores and local softmax: lane = cell, wave w owns head hs*ATT_HPW + w
     {
         const int cell = lane;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        float acc = 0.f;
 #pragma unroll 1
         for (int g = 0; g < 4; ++g) {
-            float ag[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
+            float ag = 0.f;
+#pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
                 const int part = 4 * g + pp;
                 const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
                 const int8_t* kb = (const int8_t*) &kv;
-                float kf[16];
-#pragma unroll
-                for (int e = 0; e < 16; ++e) kf[e] = (float) kb[e];
-#pragma unroll
-                for (int hh = 0; hh < 4; ++hh) {     // heads past gq read zero rows of s_q
-                    const float4* qp = (const float4*) &s_q[w + 4 * hh][part * 16];
-                    const float4 q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
-                    float x = ag[hh];
-                    x = fmaf(kf[0], q0.x, x); x = fmaf(kf[1], q0.y, x); x = fmaf(kf[2], q0.z, x); x = fmaf(kf[3], q0.w, x);
-                    x = fmaf(kf[4], q1.x, x); x = fmaf(kf[5], q1.y, x); x = fmaf(kf[6], q1.z, x); x = fmaf(kf[7], q1.w, x);
-                    x = fmaf(kf[8], q2.x, x); x = fmaf(kf[9], q2.y, x); x = fmaf(kf[10], q2.z, x); x = fmaf(kf[11], q2.w, x);
-                    x = fmaf(kf[12], q3.x, x); x = fmaf(kf[13], q3.y, x); x = fmaf(kf[14], q3.z, x); x = fmaf(kf[15], q3.w, x);
-                    ag[hh] = x;
-                }
+                const float4* qp = (const float4*) &s_q[w][part * 16];
+                const float4 q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
+                ag = fmaf((float) kb[0], q0.x, ag); ag = fmaf((float) kb[1], q0.y, ag);
+                ag = fmaf((float) kb[2], q0.z, ag); ag = fmaf((float) kb[3], q0.w, ag);
+                ag = fmaf((float) kb[4], q1.x, ag); ag = fmaf((float) kb[5], q1.y, ag);
+                ag = fmaf((float) kb[6], q1.z, ag); ag = fmaf((float) kb[7], q1.w, ag);
+                ag = fmaf((float) kb[8], q2.x, ag); ag = fmaf((float) kb[9], q2.y, ag);
+                ag = fmaf((float) kb[10], q2.z, ag); ag = fmaf((float) kb[11], q2.w, ag);
+                ag = fmaf((float) kb[12], q3.x, ag); ag = fmaf((float) kb[13], q3.y, ag);
+                ag = fmaf((float) kb[14], q3.z, ag); ag = fmaf((float) kb[15], q3.w, ag);
             }
-            const float ks = s_ks[cell][g];
-#pragma unroll
-            for (int hh = 0; hh < 4; ++hh) acc[hh] = fmaf(ag[hh], ks, acc[hh]);
+            acc = fmaf(ag, s_ks[cell][g], acc);
         }
-        float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 2;
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
-            const int h = w + 4 * hh;
-            if (h >= gq) {                           // wave-uniform
-                s_p[cell][h] = 0.f;
-                continue;
-            }
-            const float s = cell < ncell ? acc[hh] * 0.0625f : -INFINITY;
+        const int h = hs * ATT_HPW + w;
+        if (h < gq) {                                // wave-uniform
+            const float s = cell < ncell ? acc * 0.0625f : -INFINITY;
             const float m = wave_max(s);
             const float e = cell < ncell ? __expf(s - m) : 0.f;
             const float l = wave_sum(e);
-            s_p[cell][h] = e;
-            if (lane == 0) { ml[h * 2] = m; ml[h * 2 + 1] = l; }
+            s_p[cell][w] = e;
+            float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq + h) * 2;
+            if (lane == 0) { ml[0] = m; ml[1] = l; }
+        } else {
+            s_p[cell][w] = 0.f;
         }
     }
     __syncthreads();
 
-    // V: thread d owns output dim d for every head
+    // V: thread d owns output dim d for the slice's heads
     {
         const int d = tid;
-        float o[ATT_GQ_MAX];
+        float o[ATT_HPW];
 #pragma unroll
-        for (int hh = 0; hh < ATT_GQ_MAX; ++hh) o[hh] = 0.f;
+        for (int hh = 0; hh < ATT_HPW; ++hh) o[hh] = 0.f;
 #pragma unroll 4
         for (int cell = 0; cell < ncell; ++cell) {
             const float pv = (float) s_v[cell * ATT_ROW + d] * s_vs[cell][d >> 6];
-            const float4* pp = (const float4*) s_p[cell];
-#pragma unroll
-            for (int q4 = 0; q4 < ATT_GQ_MAX / 4; ++q4) {
-                const float4 p = pp[q4];
-                o[4 * q4 + 0] = fmaf(p.x, pv, o[4 * q4 + 0]);
-                o[4 * q4 + 1] = fmaf(p.y, pv, o[4 * q4 + 1]);
-                o[4 * q4 + 2] = fmaf(p.z, pv, o[4 * q4 + 2]);
-                o[4 * q4 + 3] = fmaf(p.w, pv, o[4 * q4 + 3]);
-            }
+            const float4 p = *(const float4*) s_p[cell];
+            o[0] = fmaf(p.x, pv, o[0]);
+            o[1] = fmaf(p.y, pv, o[1]);
+            o[2] = fmaf(p.z, pv, o[2]);
+            o[3] = fmaf(p.w, pv, o[3]);
         }
         float* po = a.part + ((((size_t) t * dm.kvh + j) * nch + c) * gq) * 256;
 #pragma unroll
-        for (int hh = 0; hh < ATT_GQ_MAX; ++hh)
-            if (hh < gq) po[(size_t) hh * 256 + d] = o[hh];
+        for (int hh = 0; hh < ATT_HPW; ++hh) {
+            const int h = hs * ATT_HPW + hh;
+            if (h < gq) po[(size_t) h * 256 + d] = o[hh];
+        }
     }
 }
 
@@ -376,7 +370,8 @@ int launch_qsa_attn(const QsaAttnArgs& a, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_attn: T out of range");
     WZY_REQUIRE(a.dm.topk <= ATT_CH_MAX * QSA_ATT_CHUNK, "qsa_attn: topk above %d", ATT_CH_MAX * QSA_ATT_CHUNK);
     const int nch = (a.dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
-    hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh, T), dim3(256), 0, st, a);
+    const int nhs = (a.dm.qh / a.dm.kvh + ATT_HPW - 1) / ATT_HPW;
+    hipLaunchKernelGGL(qsa_attn_kernel, dim3(nch, a.dm.kvh * nhs, T), dim3(256), 0, st, a);
     hipLaunchKernelGGL(qsa_combine_kernel, dim3(a.dm.qh, T), dim3(256), 0, st, a);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
