@@ -139,6 +139,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graphs", action="store_true", help="direct kernel launches instead of graph replay")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the run, 3 device-to-device copies of this many MiB (the known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU (all 512x48 experts resident in one MI355X's HBM); "
@@ -195,6 +198,16 @@ def main():
     gu_gbs = GU_BYTES / (us_gu.value * 1e-6) / 1e9
     dn_gbs = DN_BYTES / (us_dn.value * 1e-6) / 1e9
     st.close()
+
+    if args.calib_copy_mib > 0:
+        nb = args.calib_copy_mib << 20
+        src, dst = wzy_amd.DeviceArray(nb, np.uint8, zero=True), wzy_amd.DeviceArray(nb, np.uint8)
+        for _ in range(3):
+            wz.wzy_memcpy_d2d(dst.ptr, src.ptr, nb, None)
+        wz.wzy_device_sync()
+        src.free()
+        dst.free()
+        print("bench: calibration copies of %d MiB done" % args.calib_copy_mib, file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -12,9 +12,9 @@
  * process); a host driver that wants the reference behaviour exits on any negative status.
  * One stream and one host thread per handle; calls on a handle must be serialised.
  *
- * Synthetic model (BASELINE configurations): per-layer tensors and their initialisation are
- * listed in DESIGN.md; wzy_stage_load_synthetic() fills weights and a prefilled decode state of
- * n_ctx cells from a seed, deterministically (see wzy_synth.h).
+ * Synthetic model: wzy_stage_load_synthetic() fills every weight and a prefilled decode state of
+ * n_ctx cells from a seed, deterministically, one generator sub-stream per (tensor, layer)
+ * (see wzy_synth.h).
  */
 #ifndef WZY_STAGE_H
 #define WZY_STAGE_H
@@ -54,7 +54,8 @@ int wzy_stage_destroy(wzy_stage* st);
 size_t wzy_stage_device_bytes(const wzy_stage* st);
 
 /* Random-initialise every weight from `seed` and synthesise a prefilled decode state of n_ctx
- * cells (GDN conv/ssm state, INT8 KV cells 0..n_ctx-1, indexer keys).  0 <= n_ctx < ctx_max.
+ * cells (GDN conv/ssm state, INT8 KV cells 0..n_ctx-1, indexer keys).  0 <= n_ctx < ctx_max;
+ * n_ctx == 0 leaves the state empty, as after wzy_stage_reset_state().
  * (The reference loads a GGUF checkpoint here; a synthetic model is what the benchmarks use.) */
 int wzy_stage_load_synthetic(wzy_stage* st, uint64_t seed, int n_ctx);
 
@@ -91,8 +92,13 @@ int wzy_stage_set_graphs(wzy_stage* st, int enable);
 /* The stage's HIP stream (hipStream_t). */
 void* wzy_stage_stream(wzy_stage* st);
 
-/* Tensor access for checks and loaders: `name` as in the DESIGN.md tensor table, layer -1 for
- * model-level tensors.  Byte size, device-to-host and host-to-device copies (synchronous). */
+/* Tensor access for checks and loaders, by (layer, name); layer -1 for model-level tensors.
+ * Per layer: "<proj>.q"/"<proj>.s" (Q8_0 codes / fp16 scales of a dense projection), hc_norm*,
+ * hc_inj*, GDN alpha, beta, ssm_a, dt_bias, conv1d, ssm_norm, conv_hist, ssm; QSA q_norm, k_norm,
+ * idx_q, idx_k, idx_qn, idx_kn, kv_k, kv_ks, kv_v, kv_vs, idx_tail, idx_dead, idx_pooled; MoE
+ * router, sgate.  Model level: experts, emb, head_norm, head, rope_cos, rope_sin, and the "act.*"
+ * activation buffers of the last forward.  wzy_stage_tensor_bytes() returns 0 for an unknown name.
+ * Byte size, device-to-host and host-to-device copies (synchronous). */
 size_t wzy_stage_tensor_bytes(wzy_stage* st, int layer, const char* name);
 int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name, void* host, size_t bytes);
 int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes);

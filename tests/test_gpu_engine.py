@@ -1,0 +1,317 @@
+"""The decode engine process end to end on the GPU: the stream protocol as the reference supervisor and
+client speak it (serve/server.py:360-380,480-510; serve/engine_client.py), with the emitted token
+streams checked two ways:
+  - bit-exact against an in-process stage of the same library replaying the engine's schedule
+    (prefill windows of up to 8 rows, then one row per step): the engine's loop adds no drift;
+  - against the CPU oracle, teacher-forced on the engine's tokens, for every row whose routing and
+    selection decisions are decidable (the float tolerance of the multi-layer stage tests).
+"""
+import json
+import os
+import queue
+import signal
+import subprocess
+import threading
+import time
+
+import numpy as np
+import pytest
+
+import wzy_amd
+from stage_oracle import OracleModel, near_tie, small_cfg
+from test_gpu_stage import check_close
+
+pytestmark = pytest.mark.gpu
+
+ENGINE = os.path.join(wzy_amd.PKG_DIR, "wzy_engine")
+SEED = 21
+CFG_FIELDS = [f for f, _ in wzy_amd.StageCfg._fields_]
+
+
+def cfg_spec(c):
+    return ",".join("%s=%s" % (f, getattr(c, f)) for f in CFG_FIELDS)
+
+
+class EngineProc:
+    """The engine as a child process; one reader thread queues its stdout lines."""
+
+    def __init__(self, cfg, *args, env=None):
+        if not os.path.exists(ENGINE):
+            pytest.fail("wzy_engine not built; run __graft_entry__.build()")
+        e = dict(os.environ)
+        e.update(env or {})
+        self.p = subprocess.Popen([ENGINE, "--cfg", cfg_spec(cfg), "--model-seed", str(SEED)] + list(args),
+                                  stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                  text=True, bufsize=1, env=e)
+        self.q = queue.Queue()
+        self.err = []
+        threading.Thread(target=self._pump, args=(self.p.stdout, self.q), daemon=True).start()
+        threading.Thread(target=self._pump, args=(self.p.stderr, None), daemon=True).start()
+        ready = self.line(timeout=180)
+        assert ready.startswith("READY "), ready
+        self.ready = json.loads(ready[6:])
+
+    def _pump(self, stream, q):
+        for raw in stream:
+            if q is None:
+                self.err.append(raw.rstrip("\n"))
+            else:
+                q.put(raw.rstrip("\n"))
+        if q is not None:
+            q.put(None)
+
+    def send(self, line):
+        self.p.stdin.write(line + "\n")
+        self.p.stdin.flush()
+
+    def line(self, timeout=120):
+        try:
+            ln = self.q.get(timeout=timeout)
+        except queue.Empty:
+            raise AssertionError("engine silent for %ds; stderr tail: %s" % (timeout, self.err[-10:]))
+        if ln is None:
+            raise AssertionError("engine exited (rc=%s); stderr tail: %s" % (self.p.poll(), self.err[-10:]))
+        return ln
+
+    def request(self, obj):
+        """Send one JSON request; return (PREFILL dict, [tokens], DONE dict) of the single-stream form."""
+        self.send(json.dumps(obj, separators=(",", ":")))
+        pf, toks = None, []
+        while True:
+            ln = self.line()
+            if ln.startswith("PREFILL "):
+                pf = json.loads(ln[8:])
+            elif ln.startswith("TOK "):
+                toks.append(int(ln.split()[-1]))
+            elif ln.startswith("DONE "):
+                return pf, toks, json.loads(ln[5:])
+
+    def close(self):
+        if self.p.poll() is None:
+            try:
+                self.send("QUIT")
+                self.p.wait(timeout=60)
+            except Exception:
+                self.p.kill()
+                self.p.wait(timeout=30)
+        return self.p.returncode
+
+
+def greedy_req(ids, n, **kw):
+    r = {"ids": [int(i) for i in ids], "max_tokens": n, "temperature": 0.0, "top_p": 0.0, "top_k": 0,
+         "min_p": 0.0, "repetition_penalty": 1.0, "spec": 7, "spec_min_p": 0.72, "stop": []}
+    r.update(kw)
+    return r
+
+
+class Replay:
+    """An in-process stage + the oracle, driven with the engine's schedule for one request."""
+
+    def __init__(self, wz, cfg):
+        self.cfg = cfg
+        self.st = wzy_amd.Stage(cfg)
+        self.st.load_synthetic(SEED, 0)
+        self.orc = OracleModel(wz, self.st, cfg, SEED)
+        self.checked = self.skipped = 0
+        self.tainted = False
+
+    def prefill(self, ids, start):
+        for p in range(start, len(ids) - 1, 8):
+            w = list(ids[p:min(p + 8, len(ids) - 1)])
+            self.st.forward(p, w, run_head=False)
+            self.orc.forward(p, w)
+            self.tainted |= not self.orc.decidable_rows().all()
+
+    def step(self, tok, pos):
+        """Forward one row with the head: returns the stage's greedy token; checks the oracle."""
+        self.st.forward(pos, [tok])
+        self.st.sync()
+        g, gid = self.st.logits(1), self.st.greedy(1)
+        o, og, _ = self.orc.forward(pos, [tok])
+        self.tainted |= not self.orc.decidable_rows()[0]
+        if self.tainted or near_tie(o[0], 0.05):
+            self.skipped += 1
+        else:
+            check_close("engine pos %d" % pos, g[0], o[0])
+            assert gid[0] == og[0], "pos %d: greedy %d vs oracle %d" % (pos, gid[0], og[0])
+            self.checked += 1
+        return int(gid[0])
+
+    def close(self):
+        self.st.close()
+
+
+def test_engine_commands_and_legacy_lines(wz, gpu):
+    print("case engine_commands", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=512, n_layers=2, topk=64)
+    eng = EngineProc(cfg)
+    try:
+        r = eng.ready
+        assert r["ctx_max"] == 512 and r["gpus"] == 1 and r["mtp"] is False and "sessions" not in r
+        for cmd, want in (("PING", "PONG"), ("RESET", "OK"), ("SAVE_PROFILE", "OK"), ("PING", "PONG")):
+            eng.send(cmd)
+            assert eng.line() == want
+        eng.send('{"ids":[],"max_tokens":5}')
+        assert eng.line() == 'DONE {"generated":0,"finish":"stop"}'
+        eng.send("")                                   # empty lines are ignored
+        eng.send("7 8 9 12")                           # legacy: 3 prompt ids, 12 total -> 9 new, greedy
+        ln = eng.line()
+        assert ln.startswith("output :"), ln
+        toks = [int(t) for t in ln[len("output :"):].split()]
+        assert len(toks) == 9 and all(0 <= t < cfg.n_vocab for t in toks)
+        assert eng.line() == "END"
+        eng.send("7 8")                                # one prompt id, total 8 -> 7 new tokens
+        ln = eng.line()
+        assert ln.startswith("output :") and len(ln[len("output :"):].split()) == 7
+        assert eng.line() == "END"
+    finally:
+        assert eng.close() == 0
+
+
+def test_engine_greedy_stream_parity_and_prefix_reuse(wz, gpu):
+    print("case engine_greedy", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.n_vocab, 13)]
+    eng = EngineProc(cfg)
+    rep = Replay(wz, cfg)
+    try:
+        pf, toks, done = eng.request(greedy_req(prompt, 10))
+        assert pf["prompt_tokens"] == 13 and pf["reused"] == 0 and pf["read"] == 13
+        assert done["generated"] == 10 == len(toks) and done["finish"] == "length"
+        assert done["prompt_tokens"] == 13 and done["active_tokens"] == 13 + 9
+        assert done["draft_n"] == 0 and done["vram_hit"] == 1.0 and done["decode_ms"] > 0
+        # replay: prompt windows, then one row per emitted token
+        rep.prefill(prompt, 0)
+        expect = [rep.step(prompt[-1], len(prompt) - 1)]
+        for i, t in enumerate(toks[:-1]):
+            expect.append(rep.step(t, len(prompt) + i))
+        assert toks == expect, "engine %s vs in-process stage %s" % (toks, expect)
+
+        # the follow-up prompt extends the resident state: only its new ids are read
+        follow = prompt + toks[:-1] + [3, 141]
+        pf2, toks2, done2 = eng.request(greedy_req(follow, 4))
+        assert pf2["reused"] == 22 and pf2["read"] == len(follow) - 22, pf2
+        rep.prefill(follow, 22)
+        expect2 = [rep.step(follow[-1], len(follow) - 1)]
+        for i, t in enumerate(toks2[:-1]):
+            expect2.append(rep.step(t, len(follow) + i))
+        assert toks2 == expect2
+        assert done2["reused"] == 22 and done2["generated"] == 4
+
+        # no_reuse restarts from an empty state and reproduces the first stream exactly
+        _, toks3, done3 = eng.request(greedy_req(prompt, 10, no_reuse=1))
+        assert toks3 == toks and done3["reused"] == 0
+        # rows after an undecidable routing/selection decision are skipped (their state may differ
+        # legitimately); the stage tests cover the oracle comparison in depth
+        print("engine greedy: %d rows checked against the oracle, %d skipped" % (rep.checked, rep.skipped),
+              flush=True)
+    finally:
+        rep.close()
+        assert eng.close() == 0
+
+
+def test_engine_stop_ids_and_sampling(wz, gpu):
+    print("case engine_stop_sampling", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=2, topk=64)
+    prompt = [11, 12, 13, 14, 15]
+    eng = EngineProc(cfg, "--seed", "1234")
+    try:
+        _, toks, _ = eng.request(greedy_req(prompt, 6, no_reuse=1))
+        stop = toks[2]
+        first = toks.index(stop)
+        _, toks_s, done_s = eng.request(greedy_req(prompt, 6, no_reuse=1, stop=[stop]))
+        assert toks_s == toks[:first] and done_s["finish"] == "stop" and done_s["generated"] == first
+        # sampled requests: top-16 path (top_k <= 16) and full-vocabulary path (top_k 40 / penalty)
+        for kw in ({"temperature": 0.8, "top_k": 8, "top_p": 0.95, "min_p": 0.0},
+                   {"temperature": 0.8, "top_k": 40, "top_p": 0.95, "min_p": 0.0},
+                   {"temperature": 0.7, "top_k": 8, "repetition_penalty": 1.3}):
+            _, ts, dn = eng.request(greedy_req(prompt, 12, no_reuse=1, **kw))
+            assert len(ts) == 12 and dn["finish"] == "length" and all(0 <= t < cfg.n_vocab for t in ts)
+    finally:
+        assert eng.close() == 0
+    # the same sampling seed reproduces the same sampled stream in a fresh process
+    streams = []
+    for _ in range(2):
+        eng = EngineProc(cfg, "--seed", "99")
+        try:
+            streams.append(eng.request(greedy_req(prompt, 8, temperature=0.9, top_k=12, top_p=1.0))[1])
+        finally:
+            assert eng.close() == 0
+    assert streams[0] == streams[1]
+
+
+def test_engine_multiplexed_protocol(wz, gpu):
+    """--batch: requests carry "req", lines are TOK <req> <id> / PREFILL / DONE with "req" routed as the
+    reference client routes them (serve/engine_client.py:71-85); CANCEL and PING are served while a
+    request decodes."""
+    print("case engine_multiplexed", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=2, topk=64)
+    eng = EngineProc(cfg, "--batch")
+    try:
+        assert eng.ready["sessions"] == 1
+
+        def rid_of(line):
+            if line.startswith("TOK "):
+                return int(line.split()[1])
+            if line.startswith(("PREFILL ", "DONE ")):
+                return int(json.loads(line[line.index(" ") + 1:]).get("req", 0))
+            return -1
+
+        eng.send(json.dumps(dict(greedy_req([1, 2, 3], 5), req=1), separators=(",", ":")))
+        eng.send(json.dumps(dict(greedy_req([4, 5, 6, 7], 3), req=2), separators=(",", ":")))
+        eng.send(json.dumps(dict(greedy_req([8, 9], 400), req=3), separators=(",", ":")))
+        eng.send(json.dumps(dict(greedy_req([8, 9], 400), req=4), separators=(",", ":")))
+        eng.send("PING")
+        seen = {1: [], 2: [], 3: [], 4: []}
+        done = {}
+        pongs = 0
+        t0 = time.time()
+        cancelled_3 = False
+        while len(done) < 3 and time.time() - t0 < 120:
+            ln = eng.line()
+            if ln == "PONG":
+                pongs += 1
+                continue
+            rid = rid_of(ln)
+            assert rid in seen, ln
+            seen[rid].append(ln)
+            if ln.startswith("TOK ") and rid == 3 and not cancelled_3:
+                eng.send("CANCEL 4")                   # still queued: dropped without any line
+                eng.send("CANCEL 3")                   # decoding: ends with finish "cancelled"
+                cancelled_3 = True
+            if ln.startswith("DONE "):
+                done[rid] = json.loads(ln[5:])
+        assert pongs == 1
+        assert done[1]["generated"] == 5 and done[1]["finish"] == "length" and "decode_tps" not in done[1]
+        assert done[2]["generated"] == 3
+        assert done[3]["finish"] == "cancelled" and done[3]["generated"] < 400
+        for rid in (1, 2, 3):
+            assert seen[rid][0].startswith("PREFILL ") and json.loads(seen[rid][0][8:])["req"] == rid
+            toks = [ln for ln in seen[rid] if ln.startswith("TOK ")]
+            assert len(toks) == done[rid]["generated"]
+        eng.send("PING")
+        assert eng.line(timeout=30) == "PONG"
+        assert seen[4] == []
+    finally:
+        assert eng.close() == 0
+
+
+def test_engine_sigusr1_cancels(wz, gpu):
+    print("case engine_sigusr1", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=2048, n_layers=2, topk=64)
+    eng = EngineProc(cfg)
+    try:
+        eng.send(json.dumps(greedy_req([1, 2, 3], 1500), separators=(",", ":")))
+        assert eng.line().startswith("PREFILL ")
+        assert eng.line().startswith("TOK ")
+        eng.p.send_signal(signal.SIGUSR1)
+        while True:
+            ln = eng.line()
+            if ln.startswith("DONE "):
+                d = json.loads(ln[5:])
+                break
+        assert d["finish"] == "cancelled" and d["generated"] < 1500
+        eng.send("PING")
+        assert eng.line() == "PONG"
+    finally:
+        assert eng.close() == 0

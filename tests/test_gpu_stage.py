@@ -180,6 +180,30 @@ def test_stage_graph_replay_matches_eager(wz, gpu):
         assert np.array_equal(a, b)
 
 
+def test_stage_back_to_back_forwards_match_synced(wz, gpu):
+    """Forwards enqueued without a host sync between them (a prompt prefilled window by window) see
+    their own positions and tokens: same results as with a sync after every window."""
+    print("case stage_back_to_back", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    toks = [int(t) for t in np.random.default_rng(8).integers(0, cfg.n_vocab, 45)]
+    outs = []
+    for sync_each in (True, False):
+        st = wzy_amd.Stage(cfg)
+        try:
+            st.load_synthetic(17, 0)
+            for p in range(0, 44, 8):
+                st.forward(p, toks[p:min(p + 8, 44)], run_head=False)
+                if sync_each:
+                    st.sync()
+            st.forward(44, toks[44:45])
+            st.sync()
+            outs.append((st.logits(1), st.read(0, "ssm", np.float32), st.read(1, "kv_k", np.int8)))
+        finally:
+            st.close()
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+
+
 def test_stage_errors(wz, gpu):
     """Host-side argument checks return errors instead of launching."""
     cfg = small_cfg(wzy_amd, ctx_max=256, n_layers=2, topk=64)

@@ -1,0 +1,466 @@
+// engine_main.cpp -- wzy_engine: the decode engine process.  Reads the stream protocol on stdin,
+// drives the one-GPU stage (include/wzy_stage.h) and writes PREFILL / TOK / DONE lines on stdout.
+//
+// Replaces the reference's serve-mode main loop (src/wzy_engine_v2.cu:1632-2440) and the
+// multiplexed batch engine's protocol front end (src/wzy_batch_engine.cu:1028-1079,465-566).
+// One GPU holds every layer and expert, so a request runs as: reset or reuse the resident state,
+// prefill the prompt in windows of up to WZY_MAX_W rows, then one greedy/sampled row per step.
+//
+// Options (flags override the environment):
+//   --ctx N        / WZY_CTX          context capacity in cells (default 262144)
+//   --batch        / WZY_BATCH>0      multiplexed protocol: "req" ids, TOK <req> <id>, CANCEL <req>
+//   --model-seed S / WZY_MODEL_SEED   seed of the synthetic model weights (default 3)
+//   --seed S       / WZY_SEED         seed of the sampling generator (default: random_device)
+//   --cfg k=v,...  / WZY_CFG          overrides of wzy_stage_cfg fields (e.g. n_layers=4,n_embd=256)
+//   --device D     / WZY_DEVICE       HIP device (default 0)
+//   --no-graphs    / WZY_GRAPHS=0     launch kernels one by one instead of replaying hipGraphs
+//   WZY_DEC_PROF=1                    per-request decode profile line on stderr
+// Exit status: 0 after QUIT/EXIT or end of input, 1 on any stage error (message on stderr), 2 on
+// bad options.
+#include <math.h>
+#include <signal.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <deque>
+#include <iostream>
+#include <mutex>
+#include <random>
+#include <set>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/wzy_engine.h"
+#include "../../include/wzy_kernels.h"
+#include "../../include/wzy_runtime.h"
+#include "../../include/wzy_stage.h"
+
+namespace {
+
+volatile sig_atomic_t g_sigusr1 = 0;
+void on_sigusr1(int) { g_sigusr1 = 1; }
+
+std::mutex g_out;
+// Every protocol line goes through here so that lines written by the stdin reader (PONG in
+// multiplexed mode) never interleave with the decode loop's.
+void say(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void say(const char* fmt, ...) {
+    std::lock_guard<std::mutex> lk(g_out);
+    va_list ap;
+    va_start(ap, fmt);
+    vfprintf(stdout, fmt, ap);
+    va_end(ap);
+    fflush(stdout);
+}
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+[[noreturn]] void die(const char* what) {
+    fprintf(stderr, "[wzy-engine] %s failed: %s\n", what, wzy_last_error());
+    fflush(stderr);
+    exit(1);
+}
+void check(int rc, const char* what) {
+    if (rc < 0) die(what);
+}
+
+struct Options {
+    int ctx = 262144;
+    bool batch = false;
+    uint64_t model_seed = 3;
+    bool have_seed = false;
+    uint64_t seed = 0;
+    std::string cfg;
+    int device = 0;
+    bool graphs = true;
+    bool prof = false;
+};
+
+// "k=v,k=v" onto wzy_stage_cfg by field name.
+bool apply_cfg(wzy_stage_cfg& c, const std::string& spec) {
+    struct F {
+        const char* name;
+        int* i;
+        float* f;
+    } fields[] = {
+        {"n_layers", &c.n_layers, nullptr},   {"qsa_period", &c.qsa_period, nullptr},
+        {"n_embd", &c.n_embd, nullptr},       {"hc", &c.hc, nullptr},
+        {"hc_lr", &c.hc_lr, nullptr},         {"gdn_hk", &c.gdn_hk, nullptr},
+        {"gdn_hv", &c.gdn_hv, nullptr},       {"qsa_qh", &c.qsa_qh, nullptr},
+        {"qsa_kvh", &c.qsa_kvh, nullptr},     {"qsa_hd", &c.qsa_hd, nullptr},
+        {"n_rot", &c.n_rot, nullptr},         {"idx_heads", &c.idx_heads, nullptr},
+        {"idx_dim", &c.idx_dim, nullptr},     {"idx_blk", &c.idx_blk, nullptr},
+        {"idx_topk", &c.idx_topk, nullptr},   {"n_exp", &c.n_exp, nullptr},
+        {"top_k", &c.top_k, nullptr},         {"n_ff", &c.n_ff, nullptr},
+        {"n_vocab", &c.n_vocab, nullptr},     {"ctx_max", &c.ctx_max, nullptr},
+        {"kv_ring", &c.kv_ring, nullptr},     {"kv_sinks", &c.kv_sinks, nullptr},
+        {"rope_theta", nullptr, &c.rope_theta}, {"eps", nullptr, &c.eps},
+    };
+    size_t at = 0;
+    while (at < spec.size()) {
+        size_t end = spec.find(',', at);
+        if (end == std::string::npos) end = spec.size();
+        const std::string kv = spec.substr(at, end - at);
+        at = end + 1;
+        if (kv.empty()) continue;
+        const size_t eq = kv.find('=');
+        if (eq == std::string::npos) return false;
+        const std::string k = kv.substr(0, eq), v = kv.substr(eq + 1);
+        bool hit = false;
+        for (const F& f : fields) {
+            if (k != f.name) continue;
+            if (f.i) *f.i = atoi(v.c_str());
+            else *f.f = (float) atof(v.c_str());
+            hit = true;
+        }
+        if (!hit) return false;
+    }
+    return true;
+}
+
+int parse_options(int argc, char** argv, Options& o) {
+    if (const char* e = getenv("WZY_CTX")) o.ctx = atoi(e);
+    if (const char* e = getenv("WZY_BATCH")) o.batch = atoi(e) > 0;
+    if (const char* e = getenv("WZY_MODEL_SEED")) o.model_seed = strtoull(e, nullptr, 10);
+    if (const char* e = getenv("WZY_SEED")) o.have_seed = true, o.seed = strtoull(e, nullptr, 10);
+    if (const char* e = getenv("WZY_CFG")) o.cfg = e;
+    if (const char* e = getenv("WZY_DEVICE")) o.device = atoi(e);
+    if (const char* e = getenv("WZY_GRAPHS")) o.graphs = atoi(e) != 0;
+    if (const char* e = getenv("WZY_DEC_PROF")) o.prof = atoi(e) != 0;
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        auto val = [&]() -> const char* {
+            if (i + 1 >= argc) {
+                fprintf(stderr, "[wzy-engine] %s needs a value\n", a.c_str());
+                exit(2);
+            }
+            return argv[++i];
+        };
+        if (a == "--ctx") o.ctx = atoi(val());
+        else if (a == "--batch") o.batch = true;
+        else if (a == "--model-seed") o.model_seed = strtoull(val(), nullptr, 10);
+        else if (a == "--seed") o.have_seed = true, o.seed = strtoull(val(), nullptr, 10);
+        else if (a == "--cfg") o.cfg = val();
+        else if (a == "--device") o.device = atoi(val());
+        else if (a == "--no-graphs") o.graphs = false;
+        else {
+            fprintf(stderr, "[wzy-engine] unknown option %s\n", a.c_str());
+            return 2;
+        }
+    }
+    return 0;
+}
+
+// Input lines handed from the stdin reader to the request loop.
+struct Inbox {
+    std::mutex mu;
+    std::condition_variable cv;
+    std::deque<std::string> lines;
+    std::set<int> cancels;       // multiplexed CANCEL targets not yet consumed
+    bool eof = false;
+    std::atomic<bool> quit{false};
+};
+
+class Engine {
+  public:
+    Engine(const Options& o, wzy_stage* st, const wzy_stage_cfg& c, Inbox& in)
+        : o_(o), st_(st), c_(c), in_(in), rng_(o.have_seed ? o.seed : std::random_device{}()) {
+        logits_.resize((size_t) WZY_MAX_W * c.n_vocab);
+    }
+
+    // One request line (JSON or legacy), answered in the single-stream or multiplexed form.
+    void run(const std::string& line) {
+        wzy_request r;
+        std::vector<int> ids(line.size() / 2 + 8);
+        wzy_engine_parse_line(line.c_str(), &r, ids.data(), (int) ids.size());
+        ids.resize(std::min<size_t>(r.n_ids, ids.size()));
+        const int req = (o_.batch && r.json) ? r.req : -1;
+        g_sigusr1 = 0;
+        if (r.has_emb_file) fprintf(stderr, "[wzy-engine] emb_file ignored: image embeddings are not supported\n");
+        if (ids.empty()) {
+            if (r.json) emit_fmt(WZY_FMT_DONE_EMPTY, base_fields(req));
+            else say("output :\nEND\n");
+            return;
+        }
+        if ((int) ids.size() >= c_.ctx_max - 16) ids.erase(ids.begin(), ids.end() - (c_.ctx_max - 128));
+        const wzy_gen_cfg& g = r.cfg;
+        const int n = (int) ids.size();
+
+        int reused = g.no_reuse ? 0 : wzy_engine_reuse_prefix(state_.data(), (int) state_.size(), ids.data(), n);
+        if (reused == 0) {
+            check(wzy_stage_reset_state(st_), "reset_state");
+            state_.clear();
+        }
+        const auto t_pf0 = Clock::now();
+        for (int p = reused; p < n - 1; p += WZY_MAX_W) {
+            const int T = std::min(WZY_MAX_W, n - 1 - p);
+            check(wzy_stage_record_forward(st_, p, nullptr, &ids[p], T, 0, 0, 0, 0), "record_forward(prefill)");
+        }
+        state_.insert(state_.end(), ids.begin() + reused, ids.end() - 1);
+
+        const bool no_rep = fabsf(g.rep_pen - 1.0f) < 1e-5f;
+        mode_ = (no_rep && g.temp <= 1e-5f) ? kGreedy : (no_rep && g.top_k > 0 && g.top_k <= 16) ? kTop16 : kFull;
+        std::vector<int> hist(ids);
+        int cur = forward_and_pick(ids[n - 1], n - 1, g, hist);
+        state_.push_back(ids[n - 1]);
+        const double pf_ms = ms_since(t_pf0);
+
+        wzy_line_fields f = base_fields(req);
+        f.prompt_tokens = n;
+        f.reused = reused;
+        f.read = n - reused;
+        f.prompt_ms = pf_ms;
+        if (r.json) emit_fmt(WZY_FMT_PREFILL, f);
+        else say("output :");
+
+        const auto t_dec0 = Clock::now();
+        int generated = 0, pos = n;
+        const char* finish = "length";
+        double fwd_ms = 0.0;
+        auto is_stop = [&](int t) {
+            for (int i = 0; i < g.n_stops; ++i)
+                if (g.stops[i] == t) return true;
+            return false;
+        };
+        while (generated < g.max_new && pos < c_.ctx_max - 8) {
+            if (cancelled(req)) {
+                finish = "cancelled";
+                break;
+            }
+            if (is_stop(cur)) {
+                finish = "stop";
+                break;
+            }
+            ++generated;
+            hist.push_back(cur);
+            if (!r.json) say(" %d", cur);
+            else if (req >= 0) say("TOK %d %d\n", req, cur);
+            else say("TOK %d\n", cur);
+            if (generated >= g.max_new || pos >= c_.ctx_max - 8) {
+                finish = "length";
+                break;
+            }
+            const auto t_f = Clock::now();
+            const int next = forward_and_pick(cur, pos, g, hist);
+            fwd_ms += ms_since(t_f);
+            state_.push_back(cur);
+            if (is_stop(next)) {
+                finish = "stop";
+                break;
+            }
+            if (cancelled(req)) {
+                finish = "cancelled";
+                break;
+            }
+            ++pos;
+            cur = next;
+        }
+        if (in_.quit.load() && o_.batch) return;   // QUIT in multiplexed mode ends the process without DONE
+        {
+            std::lock_guard<std::mutex> lk(in_.mu);   // a CANCEL that arrived after the last check is void
+            in_.cancels.erase(req);
+        }
+        const double dec_ms = ms_since(t_dec0);
+        if (o_.prof)
+            fprintf(stderr, "[DEC-PROF gen=%d wins=%d (1.00 tok/win)] total=%.1fms (%.2f ms/win) | stage=%.2fms\n",
+                    generated, std::max(generated - 1, 0), dec_ms, generated > 1 ? dec_ms / (generated - 1) : 0.0,
+                    fwd_ms);
+        if (!r.json) {
+            say("\nEND\n");
+            return;
+        }
+        f.generated = generated;
+        f.decode_ms = dec_ms;
+        f.active_tokens = (int) state_.size();
+        f.finish = finish;
+        emit_fmt(WZY_FMT_DONE, f);
+    }
+
+    void reset() {
+        check(wzy_stage_reset_state(st_), "reset_state");
+        check(wzy_stage_sync(st_), "sync");
+        state_.clear();
+    }
+
+  private:
+    enum Mode { kGreedy, kTop16, kFull };
+
+    // Forward one window row at `pos` with the head and pick the next token (no draft to verify).
+    int forward_and_pick(int tok, int pos, const wzy_gen_cfg& g, const std::vector<int>& hist) {
+        check(wzy_stage_record_forward(st_, pos, nullptr, &tok, 1, 1, 0, mode_ == kTop16, 0), "record_forward");
+        check(wzy_stage_sync(st_), "sync");
+        int out = 0;
+        if (mode_ == kGreedy) {
+            check(wzy_stage_greedy_ids(st_, &out, 1), "greedy_ids");
+            return out;
+        }
+        const float u = std::uniform_real_distribution<float>(0.f, 1.f)(rng_);
+        if (mode_ == kTop16) {
+            float v[16];
+            int id[16];
+            check(wzy_stage_top16(st_, v, id, 1), "top16");
+            check(wzy_engine_verify_top16(v, id, &g, hist.data(), (int) hist.size(), -1, u, &out), "sample");
+        } else {
+            check(wzy_stage_logits(st_, logits_.data(), 1), "logits");
+            check(wzy_engine_verify_full(logits_.data(), c_.n_vocab, &g, hist.data(), (int) hist.size(), -1, u, &out),
+                  "sample");
+        }
+        return out;
+    }
+
+    bool cancelled(int req) {
+        if (g_sigusr1) return true;
+        if (in_.quit.load() && o_.batch) return true;
+        std::lock_guard<std::mutex> lk(in_.mu);
+        auto it = in_.cancels.find(req);
+        if (it == in_.cancels.end()) return false;
+        in_.cancels.erase(it);
+        return true;
+    }
+
+    wzy_line_fields base_fields(int req) const {
+        wzy_line_fields f;
+        memset(&f, 0, sizeof(f));
+        f.req = req;
+        f.vram_hit = 1.0;        // every expert is resident in HBM
+        f.finish = "stop";
+        return f;
+    }
+
+    void emit_fmt(int what, const wzy_line_fields& f) {
+        char buf[1024];
+        if (wzy_engine_format(what, &f, buf, sizeof(buf)) < 0) die("format");
+        say("%s", buf);
+    }
+
+    const Options& o_;
+    wzy_stage* st_;
+    wzy_stage_cfg c_;
+    Inbox& in_;
+    std::mt19937 rng_;
+    Mode mode_ = kGreedy;
+    std::vector<int> state_;      // tokens whose cells the resident state holds
+    std::vector<float> logits_;
+};
+
+// stdin reader: in multiplexed mode PING, CANCEL and QUIT are answered / recorded immediately (the
+// decode loop keeps running); everything else is queued for the request loop in arrival order.
+void read_stdin(Inbox& in, bool batch) {
+    std::string line;
+    while (std::getline(std::cin, line)) {
+        if (line.empty()) continue;
+        if (batch) {
+            wzy_request r;
+            const int kind = wzy_engine_parse_line(line.c_str(), &r, nullptr, 0);
+            if (kind == WZY_LINE_PING) {
+                say("PONG\n");
+                continue;
+            }
+            if (kind == WZY_LINE_CANCEL) {
+                std::lock_guard<std::mutex> lk(in.mu);
+                bool queued = false;
+                for (auto it = in.lines.begin(); it != in.lines.end(); ++it) {
+                    wzy_request q;
+                    if (wzy_engine_parse_line(it->c_str(), &q, nullptr, 0) == WZY_LINE_REQUEST && q.json &&
+                        q.req == r.req) {
+                        in.lines.erase(it);          // not started: drop it (no lines are owed for it)
+                        queued = true;
+                        break;
+                    }
+                }
+                if (!queued) in.cancels.insert(r.req);
+                continue;
+            }
+            if (kind == WZY_LINE_QUIT) in.quit.store(true);
+        }
+        {
+            std::lock_guard<std::mutex> lk(in.mu);
+            in.lines.push_back(line);
+        }
+        in.cv.notify_all();
+        if (batch && in.quit.load()) break;
+    }
+    {
+        std::lock_guard<std::mutex> lk(in.mu);
+        in.eof = true;
+    }
+    in.cv.notify_all();
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const auto t_boot0 = Clock::now();
+    Options o;
+    if (int rc = parse_options(argc, argv, o)) return rc;
+
+    wzy_stage_cfg c;
+    wzy_stage_cfg_default(&c, o.ctx);
+    if (!apply_cfg(c, o.cfg)) {
+        fprintf(stderr, "[wzy-engine] bad --cfg/WZY_CFG \"%s\"\n", o.cfg.c_str());
+        return 2;
+    }
+    int ndev = 0;
+    check(wzy_dev_count(&ndev), "device count");
+    if (ndev < 1 || o.device >= ndev) {
+        fprintf(stderr, "[wzy-engine] no HIP device %d (found %d)\n", o.device, ndev);
+        return 1;
+    }
+    wzy_stage* st = nullptr;
+    check(wzy_stage_create(&c, o.device, &st), "stage_create");
+    check(wzy_stage_load_synthetic(st, o.model_seed, 0), "load_synthetic");
+    check(wzy_stage_set_graphs(st, o.graphs ? 1 : 0), "set_graphs");
+    check(wzy_stage_sync(st), "sync");
+    signal(SIGUSR1, on_sigusr1);
+
+    const double boot_s = ms_since(t_boot0) / 1000.0;
+    if (o.batch)
+        say("READY {\"engine\":\"wzy-mi355x-batch\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":false,"
+            "\"ctx_max\":%d,\"boot_s\":%.2f,\"sessions\":1}\n",
+            c.n_layers, c.n_layers * c.n_exp, c.ctx_max, boot_s);
+    else
+        say("READY {\"engine\":\"wzy-mi355x\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":false,"
+            "\"ctx_max\":%d,\"boot_s\":%.2f}\n",
+            c.n_layers, c.n_layers * c.n_exp, c.ctx_max, boot_s);
+
+    Inbox in;
+    Engine eng(o, st, c, in);
+    std::thread reader(read_stdin, std::ref(in), o.batch);
+    reader.detach();   // blocked in getline at exit; the process ends with main
+    for (;;) {
+        std::string line;
+        {
+            std::unique_lock<std::mutex> lk(in.mu);
+            in.cv.wait(lk, [&] { return !in.lines.empty() || in.eof; });
+            if (in.lines.empty()) break;
+            line = std::move(in.lines.front());
+            in.lines.pop_front();
+        }
+        wzy_request r;
+        const int kind = wzy_engine_parse_line(line.c_str(), &r, nullptr, 0);
+        if (kind == WZY_LINE_QUIT) break;
+        if (kind == WZY_LINE_PING) say("PONG\n");
+        else if (kind == WZY_LINE_RESET) {
+            eng.reset();
+            say("OK\n");
+        } else if (kind == WZY_LINE_SAVE_PROFILE) {
+            say("OK\n");        // no expert-placement profile: every expert is resident
+        } else if (kind == WZY_LINE_REQUEST) {
+            eng.run(line);
+        }
+        if (in.quit.load()) break;
+    }
+    check(wzy_stage_sync(st), "sync");
+    wzy_stage_destroy(st);
+    return 0;
+}

@@ -25,7 +25,6 @@ namespace {
 constexpr int TK_THREADS = 1024;
 constexpr int TK_MAXJ_SMALL = 16;    // blocks per thread: 16384 blocks (65532 cells at 4 per block)
 constexpr int TK_MAXJ_LARGE = 66;    // 67584 blocks (270332 cells); keys partly spill to scratch
-constexpr int ATT_GQ_MAX = 16;       // q heads per kv head
 constexpr int ATT_HPW = 4;           // q heads per attention workgroup (one per wave in the score phase)
 constexpr int ATT_ROW = 256 + 16;    // LDS bytes per cell row (hd = 256 codes + pad against bank conflicts)
 constexpr int ATT_CH_MAX = 32;       // chunks per row: topk <= 2048

@@ -121,8 +121,15 @@ struct wzy_stage {
     float *tail_snaps = nullptr, *dead_snaps = nullptr;
     uint16_t* pool_snaps = nullptr;
     // step inputs / outputs
-    int* d_step = nullptr;          // [0] = pos, [1..8] = toks
-    int* h_step = nullptr;          // pinned
+    // Step parameters ([0] = pos, [1..8] = toks) are staged through a ring of pinned host slots:
+    // forwards enqueued back to back must not overwrite a slot whose copy has not run yet, so each
+    // slot carries an event recorded after its copy and is waited on before reuse.
+    static constexpr int STEP_SLOTS = 32, STEP_INTS = 16;
+    int* d_step = nullptr;
+    int* h_step = nullptr;          // pinned [STEP_SLOTS x STEP_INTS]
+    hipEvent_t step_ev[STEP_SLOTS] = {};
+    bool step_pending[STEP_SLOTS] = {};
+    int step_slot = 0;
     int* h_greedy = nullptr;        // pinned, device-visible
     float* h_top_v = nullptr;
     int* h_top_i = nullptr;
@@ -161,6 +168,8 @@ wzy_stage::~wzy_stage() {
     if (h_top_v) (void) hipHostFree(h_top_v);
     if (h_top_i) (void) hipHostFree(h_top_i);
     for (auto& e : ev)
+        if (e) (void) hipEventDestroy(e);
+    for (auto& e : step_ev)
         if (e) (void) hipEventDestroy(e);
     if (stream) (void) hipStreamDestroy(stream);
 }
@@ -369,7 +378,8 @@ int wzy_stage::init_buffers() {
         WZY_TRY(alloc_t(&pool_snaps, (size_t) n_qsa * W * 2 * c.idx_dim));
     }
     WZY_TRY(alloc_t(&d_step, 16));
-    WZY_HIP_TRY(hipHostMalloc((void**) &h_step, 64, hipHostMallocDefault));
+    WZY_HIP_TRY(hipHostMalloc((void**) &h_step, STEP_SLOTS * STEP_INTS * sizeof(int), hipHostMallocDefault));
+    for (auto& e : step_ev) WZY_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     WZY_HIP_TRY(hipHostMalloc((void**) &h_greedy, W * sizeof(int), hipHostMallocMapped));
     WZY_HIP_TRY(hipHostMalloc((void**) &h_top_v, W * 16 * sizeof(float), hipHostMallocMapped));
     WZY_HIP_TRY(hipHostMalloc((void**) &h_top_i, W * 16 * sizeof(int), hipHostMallocMapped));
@@ -624,6 +634,11 @@ static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
     WZY_TRY(g.normal_bf16(s->head, (size_t) c.n_vocab * D, -1, TI_HEAD, (float) (1.0 / sqrt((double) D))));
     WZY_HIP_TRY(hipStreamSynchronize(s->stream));
     s->loaded = true;
+    // an empty context has no history: recurrent state and indexer tail start at zero
+    if (n_ctx == 0) {
+        WZY_TRY(wzy_stage_reset_state(s));
+        WZY_HIP_TRY(hipStreamSynchronize(s->stream));
+    }
     return WZY_OK;
 }
 
@@ -674,9 +689,15 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
                 pos + T, st->cfg.ctx_max);
     WZY_REQUIRE(!save_snaps || (snap_offset >= 0 && snap_offset + T <= WZY_MAX_W), "record_forward: bad snap_offset");
     WZY_HIP_TRY(hipSetDevice(st->dev));
-    st->h_step[0] = pos;
-    for (int t = 0; t < T; ++t) st->h_step[1 + t] = toks ? toks[t] : 0;
-    WZY_HIP_TRY(hipMemcpyAsync(st->d_step, st->h_step, (1 + WZY_MAX_W) * sizeof(int), hipMemcpyHostToDevice, st->stream));
+    const int slot = st->step_slot;
+    st->step_slot = (slot + 1) % wzy_stage::STEP_SLOTS;
+    if (st->step_pending[slot]) WZY_HIP_TRY(hipEventSynchronize(st->step_ev[slot]));
+    int* hs = st->h_step + (size_t) slot * wzy_stage::STEP_INTS;
+    hs[0] = pos;
+    for (int t = 0; t < WZY_MAX_W; ++t) hs[1 + t] = (toks && t < T) ? toks[t] : 0;
+    WZY_HIP_TRY(hipMemcpyAsync(st->d_step, hs, (1 + WZY_MAX_W) * sizeof(int), hipMemcpyHostToDevice, st->stream));
+    WZY_HIP_TRY(hipEventRecord(st->step_ev[slot], st->stream));
+    st->step_pending[slot] = true;
     if (emb) WZY_HIP_TRY(hipMemcpyAsync(st->emb_rows, emb, (size_t) T * st->D * 4, hipMemcpyHostToDevice, st->stream));
     st->last_T = T;
     st->have_head = run_head != 0;

@@ -54,8 +54,44 @@ class StageCfg(C.Structure):
                 ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32)]
 
 
+WZY_MAX_STOPS = 64
+
+
+class GenCfg(C.Structure):
+    """struct wzy_gen_cfg (include/wzy_engine.h)"""
+    _fields_ = [("max_new", I32), ("temp", F32), ("top_p", F32), ("top_k", I32), ("min_p", F32),
+                ("rep_pen", F32), ("spec_min_p", F32), ("spec_k", I32), ("no_reuse", I32),
+                ("n_stops", I32), ("stops", I32 * WZY_MAX_STOPS)]
+
+
+class Request(C.Structure):
+    """struct wzy_request (include/wzy_engine.h)"""
+    _fields_ = [("json", I32), ("has_req", I32), ("req", I32), ("n_ids", I32), ("cfg", GenCfg),
+                ("has_emb_file", I32)]
+
+
+class LineFields(C.Structure):
+    """struct wzy_line_fields (include/wzy_engine.h)"""
+    _fields_ = [("req", I32), ("generated", I32), ("prompt_tokens", I32), ("reused", I32), ("read", I32),
+                ("prompt_ms", C.c_double), ("decode_ms", C.c_double), ("draft_n", C.c_longlong),
+                ("draft_accepted", C.c_longlong), ("promoted", C.c_longlong), ("vram_hit", C.c_double),
+                ("restored_park", I32), ("parked_tokens", I32), ("active_tokens", I32),
+                ("finish", C.c_char_p)]
+
+
+LINE_KINDS = {0: "SKIP", 1: "PING", 2: "RESET", 3: "SAVE_PROFILE", 4: "QUIT", 5: "CANCEL", 6: "REQUEST"}
+FMT_PREFILL, FMT_DONE, FMT_DONE_EMPTY = 1, 2, 3
+
 # name -> (restype, argtypes, checked)
 _SIGS = {
+    # engine host logic
+    "wzy_engine_cfg_default": (None, [C.POINTER(GenCfg)], False),
+    "wzy_engine_parse_line": (I32, [C.c_char_p, C.POINTER(Request), P, I32], False),
+    "wzy_engine_target_dist": (I32, [P, I32, C.POINTER(GenCfg), P, I32, P, P, I32], False),
+    "wzy_engine_verify_full": (I32, [P, I32, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
+    "wzy_engine_verify_top16": (I32, [P, P, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
+    "wzy_engine_reuse_prefix": (I32, [P, I32, P, I32], False),
+    "wzy_engine_format": (I32, [I32, C.POINTER(LineFields), C.c_char_p, I32], False),
     # stage
     "wzy_stage_cfg_default": (None, [C.POINTER(StageCfg), I32], False),
     "wzy_stage_create": (I32, [C.POINTER(StageCfg), I32, C.POINTER(P)], True),
