@@ -111,10 +111,12 @@ size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T
 int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Time the expert kernels of wzy_moe_block with hipEvents on `stream`: `iters` iterations cycling
- * through `n_layers` weight sets (so the 256 MB last-level cache cannot hold the experts), each
- * iteration routing x [T x n_embd] through that layer's router first.  Returns the mean duration
- * in microseconds of the gate/up launch and of the down+combine launch (host pointers).
+/* Time the expert kernels of wzy_moe_block with hipEvents on `stream`.  The router logits of x
+ * [T x n_embd] are computed for every layer first; then `iters` gate/up launches run back to back
+ * cycling through the `n_layers` weight sets (so the 256 MB last-level cache cannot hold the
+ * experts), each routing with its own layer's logits, and then `iters` down+combine launches the
+ * same way.  Returns the mean duration in microseconds of one gate/up launch and of one down launch
+ * (host pointers).  Layers must share one shape.  Allocates (and frees) its own scratch.
  * No counterpart in the reference: measurement support for the NVFP4 GEMV roofline. */
 int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, const float* x, void* workspace,
                          size_t workspace_bytes, int iters, float* us_gate_up, float* us_down,

@@ -218,3 +218,27 @@ def test_row_argmax_top16_parity(wz, orc, gpu, V, T):
     # second call reuses the arrival counters (they must be back at zero)
     wz.wzy_row_argmax(ld.ptr, V, T, a.ptr, None)
     np.testing.assert_array_equal(host(a), ra)
+
+
+def test_moe_time_kernels_bursts(wz, gpu):
+    """The measurement entry point reports positive, plausible durations and leaves the block
+    usable: the MoE block gives bit-identical results before and after it."""
+    D, F, E, K, T = 512, 128, 16, 4, 1
+    layers, keep = [], []
+    for l in range(3):
+        m = mi.make_layer(wz, 5, l, D, F, E, K, blobs=[])
+        w, d = device_layer(wz, m)
+        layers.append(w)
+        keep.append(d)
+    arr = (wzy_amd.MoeWeights * 3)(*layers)
+    x = mi.make_x(wz, 5, 0, T, D).ravel()
+    before = run_gpu_moe(wz, layers[0], x, T)
+    xd = dev(x)
+    nws = wz.wzy_moe_workspace_bytes(D, F, E, K, T)
+    ws = DA(nws, np.uint8, zero=True)
+    gu, dn = C.c_float(0), C.c_float(0)
+    wz.wzy_moe_time_kernels(arr, 3, T, xd.ptr, ws.ptr, nws, 12, C.byref(gu), C.byref(dn), None)
+    assert 0.5 < gu.value < 1000 and 0.5 < dn.value < 1000, (gu.value, dn.value)
+    after = run_gpu_moe(wz, layers[0], x, T)
+    for a, b in zip(before, after):
+        assert np.array_equal(a, b)

@@ -180,6 +180,34 @@ def test_stage_graph_replay_matches_eager(wz, gpu):
         assert np.array_equal(a, b)
 
 
+def test_oracle_model_window_equals_steps(wz, gpu):
+    """Pins the oracle model's composition: a T-row window gives the same logits and state as T
+    single-row steps (each row sees exactly the cells before it, the recurrent state is carried row
+    by row).  The stage is only the source of the weights and the prefilled state."""
+    print("case oracle_window_vs_steps", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(31, 598)          # the window crosses an indexer block boundary (cells 598..602)
+        win, steps = OracleModel(wz, st, cfg, 31), OracleModel(wz, st, cfg, 31)
+    finally:
+        st.close()
+    toks = [11, 503, 77, 902, 5]
+    lw, gw, pw = win.forward(598, toks)
+    for t, tok in enumerate(toks):
+        ls, gs, ps = steps.forward(598 + t, [tok])
+        np.testing.assert_allclose(ls[0], lw[t], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(ps[0], pw[t], rtol=1e-5, atol=1e-5)
+        assert gs[0] == gw[t]
+    for (layer, name), a in win.arrays.items():
+        if name in ("ssm", "conv_hist", "idx_tail", "idx_dead", "idx_pooled", "kv_k", "kv_v", "kv_ks", "kv_vs"):
+            b = steps.arrays[(layer, name)]
+            if a.dtype.kind == "f":
+                np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6, err_msg="%s layer %d" % (name, layer))
+            else:
+                assert np.array_equal(a, b), "%s layer %d" % (name, layer)
+
+
 def test_stage_back_to_back_forwards_match_synced(wz, gpu):
     """Forwards enqueued without a host sync between them (a prompt prefilled window by window) see
     their own positions and tokens: same results as with a sync after every window."""

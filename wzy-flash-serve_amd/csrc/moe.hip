@@ -726,36 +726,65 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
                             layers[0].top_k, T, &need);
     WZY_REQUIRE(need <= workspace_bytes, "wzy_moe_time_kernels: workspace too small");
     hipStream_t st = as_stream(stream);
+    const int E = layers[0].n_exp;
+    for (int l = 1; l < n_layers; ++l)
+        WZY_REQUIRE(layers[l].n_embd == layers[0].n_embd && layers[l].n_ff == layers[0].n_ff &&
+                        layers[l].n_exp == E && layers[l].top_k == layers[0].top_k,
+                    "wzy_moe_time_kernels: layers must share one shape");
+    // Router logits of every layer are computed first, one buffer per layer, so that the timed
+    // region holds nothing but back-to-back launches of one kernel: `iters` gate/up launches cycling
+    // through the layers (each routing with its own layer's logits), then `iters` down launches
+    // (each with its own layer's weights, reading the routing the last gate/up published).  Two
+    // events per burst: their own cost is spread over `iters` launches.
     float* comb = nullptr;
+    float* lgt = nullptr;
     WZY_HIP_TRY(hipMalloc(&comb, sizeof(float) * (size_t) T * layers[0].n_embd));
-    hipEvent_t ev[3];
-    for (auto& e : ev) WZY_HIP_TRY(hipEventCreate(&e));
-    double tot_gu = 0.0, tot_dn = 0.0;
+    if (hipMalloc(&lgt, sizeof(float) * (size_t) n_layers * T * (E + 1)) != hipSuccess) {
+        (void) hipFree(comb);
+        set_error("wzy_moe_time_kernels: out of device memory");
+        return WZY_ENOMEM;
+    }
+    auto layer_ws = [&](int l) {
+        MoeWs w = ws;
+        w.logits = lgt + (size_t) l * T * E;
+        w.sg = lgt + (size_t) n_layers * T * E + (size_t) l * T;
+        return w;
+    };
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int rc = WZY_OK;
-    for (int it = 0; it < iters && rc == WZY_OK; ++it) {
-        const wzy_moe_weights* w = &layers[it % n_layers];
-        rc = moe_launch_route(w, ws, x, T, st);
-        if (rc != WZY_OK) break;
+    for (auto& e : ev)
+        if (rc == WZY_OK && hipEventCreate(&e) != hipSuccess) rc = WZY_EHIP;
+    for (int l = 0; l < n_layers && rc == WZY_OK; ++l) rc = moe_launch_route(&layers[l], layer_ws(l), x, T, st);
+    if (rc == WZY_OK) {
+        launch_gu(gu_args(&layers[0], layer_ws(0), x, T), T, st);         // warm-up of both kernels
+        launch_dn(dn_args(&layers[0], layer_ws(0), comb), T, st);
         (void) hipEventRecord(ev[0], st);
-        launch_gu(gu_args(w, ws, x, T), T, st);
+        for (int it = 0; it < iters; ++it) {
+            const int l = it % n_layers;
+            launch_gu(gu_args(&layers[l], layer_ws(l), x, T), T, st);
+        }
         (void) hipEventRecord(ev[1], st);
-        launch_dn(dn_args(w, ws, comb), T, st);
+        for (int it = 0; it < iters; ++it) {
+            const int l = it % n_layers;
+            launch_dn(dn_args(&layers[l], layer_ws(l), comb), T, st);
+        }
         (void) hipEventRecord(ev[2], st);
         if (hipGetLastError() != hipSuccess || hipEventSynchronize(ev[2]) != hipSuccess) {
             set_error("wzy_moe_time_kernels: launch failed");
             rc = WZY_EHIP;
-            break;
         }
-        float a = 0.f, b = 0.f;
+    }
+    float a = 0.f, b = 0.f;
+    if (rc == WZY_OK) {
         (void) hipEventElapsedTime(&a, ev[0], ev[1]);
         (void) hipEventElapsedTime(&b, ev[1], ev[2]);
-        tot_gu += a;
-        tot_dn += b;
     }
-    for (auto& e : ev) (void) hipEventDestroy(e);
+    for (auto& e : ev)
+        if (e) (void) hipEventDestroy(e);
+    (void) hipFree(lgt);
     (void) hipFree(comb);
     if (rc != WZY_OK) return rc;
-    *us_gate_up = (float) (1000.0 * tot_gu / iters);
-    *us_down = (float) (1000.0 * tot_dn / iters);
+    *us_gate_up = 1000.0f * a / (float) iters;
+    *us_down = 1000.0f * b / (float) iters;
     return WZY_OK;
 }
