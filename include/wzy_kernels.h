@@ -132,14 +132,18 @@ int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, con
  *   lo = silu((down . quant32(xn)) / HC)   [T x HCLR];  inj = inj_w . xn  [T x HC]  (inj_w nullable)
  *   mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo))   [T x D]
  * Exactly one of R_in / emb_table is non-NULL; bo/inj_prev (the pending HC write of the previous
- * block) may be NULL.  R_out must not alias R_in.
+ * block) may be NULL.  R_out must not alias R_in.  HC = 4; D in {256, 512, 1024, 2048, 4096};
+ * HCLR a multiple of 32 up to 512.  The down projection is accumulated per source stream (four
+ * partials, summed in a fixed order) in `workspace` (wzy_hc_read_workspace_bytes() bytes; calls
+ * sharing a workspace must not overlap).
  * Replaces StageGpu::gr_read_fused + gr_write_multi (src/wzy_stage_v2.cuh:463-470;
  * src/wzy_kernels_v2.cuh:409-454,632-827) and bcast_emb_to_r_kernel (src/wzy_stage_v2.cuh:326-332). */
+size_t wzy_hc_read_workspace_bytes(int HC, int HCLR, int T);
 int wzy_hc_read(const float* R_in, const uint16_t* emb_table, const int* toks, int n_vocab, const float* bo,
                 const float* inj_prev, float* R_out, const float* norm_w, const int8_t* down_q,
                 const uint16_t* down_s, const uint16_t* inj_w, const int8_t* up_q, const uint16_t* up_s,
                 float* nsc, float* lo, float* inj, float* mixed, int D, int HC, int HCLR, float eps, int T,
-                void* stream);
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * GDN (gated delta-rule) recurrence

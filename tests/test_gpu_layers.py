@@ -76,12 +76,15 @@ def test_hc_read(wz, orc, gpu, D, HC, HCLR, T, mode):
         d["inj_w"] = dev(inj_w)
     R_out, nsc, lo = DA((T, HC, D), np.float32), DA((T, HC), np.float32), DA((T, HCLR), np.float32)
     inj, mixed = DA((T, HC), np.float32), DA((T, D), np.float32)
+    nws = wz.wzy_hc_read_workspace_bytes(HC, HCLR, T)
+    ws = DA(nws, np.uint8)
     emb_mode = mode == "emb"
     wz.wzy_hc_read(None if emb_mode else d["R_in"].ptr, d["emb"].ptr if emb_mode else None,
                    d["toks"].ptr if emb_mode else None, V, None if emb_mode else d["bo"].ptr,
                    None if emb_mode else d["inj_prev"].ptr, R_out.ptr, d["norm_w"].ptr, d["dq"].ptr, d["ds"].ptr,
                    d["inj_w"].ptr if inj_w is not None else None, d["uq"].ptr, d["us"].ptr, nsc.ptr, lo.ptr,
-                   inj.ptr if inj_w is not None else None, mixed.ptr, D, HC, HCLR, C.c_float(1e-6), T, None)
+                   inj.ptr if inj_w is not None else None, mixed.ptr, D, HC, HCLR, C.c_float(1e-6), T, ws.ptr, nws,
+                   None)
     wz.wzy_device_sync()
 
     o_R, o_nsc, o_lo = np.empty((T, HC, D), np.float32), np.empty((T, HC), np.float32), np.empty((T, HCLR), np.float32)

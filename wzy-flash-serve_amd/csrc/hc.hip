@@ -4,16 +4,19 @@
 // up+mean) and writes them with a fifth (src/wzy_stage_v2.cuh:463-470, src/wzy_kernels_v2.cuh:
 // 409-454,632-827).  Here a read is two launches and the pending write is folded into the next read:
 //
-//   hc_pre : R_out = R_in + bo * 2*sigmoid(inj_prev/HC)           (the pending write, or the
-//            embedding broadcast on layer 0), per-stream RMS scale, xn = R_out*scale*w,
-//            lo = silu(down . quant32(xn) / HC), inj = inj_w . xn.
-//            Every workgroup rebuilds quant32(xn) for the window in LDS (the residual is 32 KB per
-//            row and L2-resident), so no cross-workgroup synchronisation is needed; workgroup w
-//            writes every gridDim-th 32-block of R_out; four extra workgroups compute inj.
-//   hc_post: mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)); lo is quantised
-//            once per workgroup into LDS.
-// Both kernels issue every global load a row needs before using any of them (indices clamped
-// instead of branching, fp16 scales converted afterwards): one memory round trip per window row.
+//   hc_pre : split by stream.  Workgroup (c, rb) loads only stream c of the residual (the pending
+//            write R_out = R_in + bo * 2*sigmoid(inj_prev/HC) folded in, or the embedding broadcast
+//            on layer 0), forms its RMS scale and xn = R_out*scale*w, quantises xn per 32 into LDS
+//            and multiplies it with stream c's columns of 4*RPW rows of `down`:
+//                lo_part[t][c][r] = down[r, c*D : (c+1)*D] . quant32(xn_c).
+//            Workgroup (c, NRB) writes stream c of R_out, its scale nsc[t][c], and the inject
+//            partials inj_part[t][c][o] = inj_w[o, c*D : (c+1)*D] . xn_c.
+//            Each workgroup moves one stream's activations (3 x D floats), not all four.
+//   hc_post: lo = silu(((p0 + p1) + (p2 + p3)) / HC) from the four partials, quantised per 32 once
+//            per workgroup into LDS; mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)).
+//            Workgroup 0 also writes lo and the summed inj.
+// Every global load a row needs is issued before any of them is used (indices clamped instead of
+// branching, fp16 scales converted afterwards).
 #include <algorithm>
 
 #include "wzy_device.h"
@@ -48,211 +51,215 @@ WZY_DEV void quant32_vals(const float (&v)[32], int4& q0, int4& q1, float& d) {
     q1 = make_int4(w[4], w[5], w[6], w[7]);
 }
 
+// N consecutive fp32 values (N in {1, 2, 4, 8, 16}; p aligned to 4*N bytes)
+template <int N>
+WZY_DEV void ld_f32(const float* p, float (&v)[N]) {
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int k = 0; k < N / 4; ++k) {
+            const float4 f = ((const float4*) p)[k];
+            v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+        }
+    } else if constexpr (N == 2) {
+        const float2 f = *(const float2*) p;
+        v[0] = f.x; v[1] = f.y;
+    } else {
+        v[0] = p[0];
+    }
+}
+// N consecutive bf16 values as raw 32-bit words (N/2 words, one half-filled word when N == 1)
+template <int N>
+struct Bf16Raw {
+    uint32_t w[N >= 2 ? N / 2 : 1];
+};
+template <int N>
+WZY_DEV Bf16Raw<N> ld_bf16_raw(const uint16_t* p) {
+    Bf16Raw<N> r;
+    if constexpr (N >= 8) {
+#pragma unroll
+        for (int k = 0; k < N / 8; ++k) {
+            const uint4 u = ((const uint4*) p)[k];
+            r.w[4 * k] = u.x; r.w[4 * k + 1] = u.y; r.w[4 * k + 2] = u.z; r.w[4 * k + 3] = u.w;
+        }
+    } else if constexpr (N == 4) {
+        const uint2 u = *(const uint2*) p;
+        r.w[0] = u.x; r.w[1] = u.y;
+    } else if constexpr (N == 2) {
+        r.w[0] = *(const uint32_t*) p;
+    } else {
+        r.w[0] = p[0];
+    }
+    return r;
+}
+template <int N>
+WZY_DEV float bf16_at(const Bf16Raw<N>& r, int j) {
+    return (j & 1) ? bf16_hi(r.w[j >> 1]) : bf16_lo(r.w[j >> 1]);
+}
+
+// max over aligned groups of G consecutive lanes (G in {1, 2, 4, 8, 16, 32})
+template <int G>
+WZY_DEV float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    if constexpr (G >= 32) v = fmaxf(v, swz_f<SWZ_XOR16>(v));
+    return v;
+}
+
+// sum of 4 values per thread over the 256-thread workgroup; results valid on thread 0
+WZY_DEV void block_sum4_t0(float (&v)[4], float (*sh)[4]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 0; o < 4; ++o) v[o] = wave_sum(v[o]);
+    if (lane == 0)
+#pragma unroll
+        for (int o = 0; o < 4; ++o) sh[w][o] = v[o];
+    __syncthreads();
+    if (threadIdx.x == 0)
+#pragma unroll
+        for (int o = 0; o < 4; ++o) v[o] = (sh[0][o] + sh[1][o]) + (sh[2][o] + sh[3][o]);
+}
+
 }  // namespace
 
-// T window rows (<= 4 per launch), D <= DC.  256 threads; thread tid owns the 32-value blocks
-// b = tid + 256k of the flattened [HC*D] row; wave w of workgroup g owns down rows
-// (4g + w) * RPW .. + RPW - 1.  Dynamic LDS: int8 xq [T][4D] then fp32 xs [T][4D/32].
-template <int T, int DC, int RPW>
+// T window rows; VPT = D/256 values of the stream per thread; NBL = 32-blocks per lane of one
+// down row (D/32/64 rounded up); RPW down rows per wave.  Workgroup b: stream c = b % 4, row block
+// rb = b / 4 (rows rb*4*RPW ..), rb == NRB is the stream's R_out / nsc / inject workgroup.
+// Dynamic LDS (row workgroups): int8 xq [T][D] then fp32 xs [T][D/32].
+template <int T, int VPT, int NBL, int RPW>
 __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
-    constexpr int NBK = DC >= 2048 ? DC / 2048 : 1;   // 32-blocks per thread
-    constexpr int NBL = DC / 512;                      // 32-blocks per lane of one down row
     extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ float s_seg[WZY_MAX_W][64];             // sums of 8 consecutive blocks (256 values)
-    __shared__ float s_nsc[T * HC4];
-    __shared__ float s_inj[4];
+    __shared__ float s_red[4][4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int D = a.D, HCD = HC4 * D, nb = HCD / 32, L = a.HCLR, spb = D / 256;
+    const int D = a.D, HCD = HC4 * D, NB = D / 32, L = a.HCLR;
+    constexpr int G = 32 / VPT;                        // threads per 32-block
+    const int c = blockIdx.x & 3, rb = blockIdx.x >> 2;
+    const int nrb = (L + 4 * RPW - 1) / (4 * RPW);
+    const bool aux = rb >= nrb;                        // workgroup-uniform
+    const bool do_inj = aux && a.inj_w != nullptr;
     int8_t* s_xq = (int8_t*) s_dyn;
-    float* s_xs = (float*) (s_dyn + (size_t) T * HCD);
+    float* s_xs = (float*) (s_dyn + (size_t) T * D);
     const bool fold = a.bo != nullptr;
-    // workgroups [0, n_row_wg) own down rows; the HC workgroups after them (inject weights only)
-    // compute inj row blockIdx.x - n_row_wg
-    const int n_row_wg = (L + 4 * RPW - 1) / (4 * RPW);
-    const bool has_rows = (int) blockIdx.x < n_row_wg;
-    const bool do_inj = !has_rows && a.inj_w != nullptr;
-    const int inj_row = blockIdx.x - n_row_wg;
-    const bool wave_stream = NBK == 1 && D == 64 * 32;   // wave w owns all of stream w
+    const int d0 = tid * VPT;                          // this thread's values: d0 .. d0+VPT-1 of stream c
 
-    // 0. this wave's down rows (raw codes and fp16 scales), issued first
-    const int row0 = (blockIdx.x * 4 + w) * RPW;
+    // 0. this wave's down rows (raw codes and fp16 scales of stream c's columns), issued first
+    const int row0 = (rb * 4 + w) * RPW;
     int4 c0[NBL][RPW], c1[NBL][RPW];
     uint16_t sraw[NBL][RPW];
-    if (has_rows) {
+    if (!aux) {
 #pragma unroll
         for (int i = 0; i < NBL; ++i) {
-            const int b = min(lane + 64 * i, nb - 1);
+            const int b = min(lane + 64 * i, NB - 1);
 #pragma unroll
             for (int s = 0; s < RPW; ++s) {
                 const int r = min(row0 + s, L - 1);
-                const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) b * 32);
+                const int4* cp = (const int4*) (a.down_q + (size_t) r * HCD + (size_t) c * D + (size_t) b * 32);
                 c0[i][s] = ld_stream_i4(cp);
                 c1[i][s] = ld_stream_i4(cp + 1);
-                sraw[i][s] = a.down_s[(size_t) r * nb + b];
+                sraw[i][s] = a.down_s[(size_t) r * (HCD / 32) + (size_t) c * NB + b];
             }
         }
     }
-    // 1. row-independent inputs of this thread's blocks: norm weights, inject weights
-    float4 nw[NBK][8];
-    uint4 iw[NBK][4];
+    // 1. row-independent inputs: norm weights, inject weights
+    float nw[VPT];
+    ld_f32<VPT>(a.norm_w + (size_t) c * D + d0, nw);
+    Bf16Raw<VPT> iw[4];
+    if (do_inj) {
 #pragma unroll
-    for (int k = 0; k < NBK; ++k) {
-        const int b = min(tid + 256 * k, nb - 1);
-        const int c = (32 * b) / D, d0 = (32 * b) % D;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) nw[k][j] = *(const float4*) (a.norm_w + (size_t) c * D + d0 + 4 * j);
-        if (do_inj) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                iw[k][j] = *(const uint4*) (a.inj_w + (size_t) inj_row * HCD + (size_t) 32 * b + 8 * j);
-        }
+        for (int o = 0; o < 4; ++o) iw[o] = ld_bf16_raw<VPT>(a.inj_w + (size_t) o * HCD + (size_t) c * D + d0);
     }
 
-    float inj_acc[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) inj_acc[t] = 0.f;
-#pragma unroll
+#pragma unroll 1
     for (int t = 0; t < T; ++t) {
         // 2. residual (or embedding) and fold inputs of this row
-        float4 rv[NBK][8], bv[NBK][8];
-        float ip[NBK];
-        int tok = 0;
+        float v[VPT], bv[VPT];
+        float ip = 0.f;
         if (a.emb_table) {
-            tok = a.toks[t];
+            int tok = a.toks[t];
             tok = tok < 0 ? 0 : (tok >= a.n_vocab ? a.n_vocab - 1 : tok);
+            const Bf16Raw<VPT> e = ld_bf16_raw<VPT>(a.emb_table + (size_t) tok * D + d0);
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) v[j] = bf16_at<VPT>(e, j);
+        } else if (a.emb_rows) {
+            ld_f32<VPT>(a.emb_rows + (size_t) t * D + d0, v);
+        } else {
+            ld_f32<VPT>(a.R_in + ((size_t) t * HC4 + c) * D + d0, v);
         }
+        if (fold) {
+            ld_f32<VPT>(a.bo + (size_t) t * D + d0, bv);
+            ip = a.inj_prev[t * HC4 + c];
+            const float gw = 2.0f / (1.0f + __expf(-ip / (float) HC4));
 #pragma unroll
-        for (int k = 0; k < NBK; ++k) {
-            const int b = min(tid + 256 * k, nb - 1);
-            const int c = (32 * b) / D, d0 = (32 * b) % D;
-            if (a.emb_table) {
+            for (int j = 0; j < VPT; ++j) v[j] = fmaf(bv[j], gw, v[j]);
+        }
+        // 3. stream scale
+        float ss = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint2 h = *(const uint2*) (a.emb_table + (size_t) tok * D + d0 + 4 * j);
-                    rv[k][j] = make_float4(__builtin_bit_cast(float, h.x), __builtin_bit_cast(float, h.y), 0.f, 0.f);
-                }
-            } else if (a.emb_rows) {
+        for (int j = 0; j < VPT; ++j) ss = fmaf(v[j], v[j], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) s_red[w][0] = ss;
+        __syncthreads();
+        const float sc = 1.0f / sqrtf(((s_red[0][0] + s_red[1][0]) + (s_red[2][0] + s_red[3][0])) / (float) D + a.eps);
+        __syncthreads();                              // s_red is reused below
+        float xn[VPT];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) rv[k][j] = *(const float4*) (a.emb_rows + (size_t) t * D + d0 + 4 * j);
+        for (int j = 0; j < VPT; ++j) xn[j] = v[j] * sc * nw[j];
+
+        if (aux) {
+            float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
+            if constexpr (VPT >= 4) {
+#pragma unroll
+                for (int k = 0; k < VPT / 4; ++k)
+                    ((float4*) ro)[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    rv[k][j] = *(const float4*) (a.R_in + ((size_t) t * HC4 + c) * D + d0 + 4 * j);
+                for (int j = 0; j < VPT; ++j) ro[j] = v[j];
             }
-            if (fold) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) bv[k][j] = *(const float4*) (a.bo + (size_t) t * D + d0 + 4 * j);
-                ip[k] = a.inj_prev[t * HC4 + c];
-            }
-        }
-        // 3. folded values and the per-thread sums of squares
-        float v[NBK][32];
-        float sc_w = 0.f;
-#pragma unroll
-        for (int k = 0; k < NBK; ++k) {
-            const float gw = fold ? 2.0f / (1.0f + __expf(-ip[k] / (float) HC4)) : 0.f;
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float4 x = rv[k][j];
-                if (a.emb_table) {
-                    const uint32_t lo = __builtin_bit_cast(uint32_t, x.x), hi = __builtin_bit_cast(uint32_t, x.y);
-                    x = make_float4(bf16_lo(lo), bf16_hi(lo), bf16_lo(hi), bf16_hi(hi));
-                }
-                if (fold) {
-                    x.x = fmaf(bv[k][j].x, gw, x.x);
-                    x.y = fmaf(bv[k][j].y, gw, x.y);
-                    x.z = fmaf(bv[k][j].z, gw, x.z);
-                    x.w = fmaf(bv[k][j].w, gw, x.w);
-                }
-                v[k][4 * j + 0] = x.x; v[k][4 * j + 1] = x.y; v[k][4 * j + 2] = x.z; v[k][4 * j + 3] = x.w;
-                ss = fmaf(x.x, x.x, ss);
-                ss = fmaf(x.y, x.y, ss);
-                ss = fmaf(x.z, x.z, ss);
-                ss = fmaf(x.w, x.w, ss);
-            }
-            // 4. per-stream sums.  D = 2048 with one block per thread: wave w holds exactly stream w,
-            //    so the sum is a wave reduction; otherwise sums over 8 consecutive blocks (never
-            //    straddling a stream, D % 256 == 0) are combined through LDS.
-            if (wave_stream) {
-                sc_w = 1.0f / sqrtf(wave_sum(ss) / (float) D + a.eps);
-                if (lane == 0 && blockIdx.x == 0) a.nsc[t * HC4 + w] = sc_w;
-            } else {
-                ss = sum8(ss);
-                const int b = tid + 256 * k;
-                if ((lane & 7) == 0 && b < nb) s_seg[t][b >> 3] = ss;
-            }
-        }
-        if (!wave_stream) {
-            __syncthreads();
-            if (tid < HC4) {
-                float tot = 0.f;
-                for (int i = 0; i < spb; ++i) tot += s_seg[t][tid * spb + i];
-                const float sc = 1.0f / sqrtf(tot / (float) D + a.eps);
-                s_nsc[t * HC4 + tid] = sc;
-                if (blockIdx.x == 0) a.nsc[t * HC4 + tid] = sc;
-            }
-            __syncthreads();
-        }
-        // 5. xn quantised per 32 into LDS, inject partial, R_out blocks
-#pragma unroll
-        for (int k = 0; k < NBK; ++k) {
-            const int b = tid + 256 * k;
-            if (b >= nb) continue;
-            const int c = (32 * b) / D, d0 = (32 * b) % D;
-            const float sc = wave_stream ? sc_w : s_nsc[t * HC4 + c];
-            float xn[32];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                xn[4 * j + 0] = v[k][4 * j + 0] * sc * nw[k][j].x;
-                xn[4 * j + 1] = v[k][4 * j + 1] * sc * nw[k][j].y;
-                xn[4 * j + 2] = v[k][4 * j + 2] * sc * nw[k][j].z;
-                xn[4 * j + 3] = v[k][4 * j + 3] * sc * nw[k][j].w;
-            }
+            if (tid == 0) a.nsc[t * HC4 + c] = sc;
             if (do_inj) {
+                float acc[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint4 u = iw[k][j];
-                    float acc = inj_acc[t];
-                    acc = fmaf(bf16_lo(u.x), xn[8 * j + 0], acc);
-                    acc = fmaf(bf16_hi(u.x), xn[8 * j + 1], acc);
-                    acc = fmaf(bf16_lo(u.y), xn[8 * j + 2], acc);
-                    acc = fmaf(bf16_hi(u.y), xn[8 * j + 3], acc);
-                    acc = fmaf(bf16_lo(u.z), xn[8 * j + 4], acc);
-                    acc = fmaf(bf16_hi(u.z), xn[8 * j + 5], acc);
-                    acc = fmaf(bf16_lo(u.w), xn[8 * j + 6], acc);
-                    acc = fmaf(bf16_hi(u.w), xn[8 * j + 7], acc);
-                    inj_acc[t] = acc;
+                for (int o = 0; o < 4; ++o) {
+                    acc[o] = 0.f;
+#pragma unroll
+                    for (int j = 0; j < VPT; ++j) acc[o] = fmaf(bf16_at<VPT>(iw[o], j), xn[j], acc[o]);
                 }
-            }
-            if (has_rows) {
-                int4 q0, q1;
-                float xs;
-                quant32_vals(xn, q0, q1, xs);
-                int4* dst = (int4*) (s_xq + (size_t) t * HCD + (size_t) 32 * b);
-                dst[0] = q0;
-                dst[1] = q1;
-                s_xs[t * nb + b] = xs;
-            }
-            if ((b % gridDim.x) == blockIdx.x) {
-                float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
+                block_sum4_t0(acc, s_red);
+                if (tid == 0)
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    *(float4*) (ro + 4 * j) = make_float4(v[k][4 * j], v[k][4 * j + 1], v[k][4 * j + 2], v[k][4 * j + 3]);
+                    for (int o = 0; o < 4; ++o) a.inj_part[((size_t) t * HC4 + c) * HC4 + o] = acc[o];
+                __syncthreads();                      // s_red free for the next row
             }
+            continue;
         }
-    }
-    if (do_inj) {                             // workgroup-uniform branch
+        // 4. quant32(xn) into LDS: G consecutive threads share one 32-block
+        float am = 0.f;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float s = block_sum<4>(inj_acc[t], s_inj);
-            if (tid == 0) a.inj[t * HC4 + inj_row] = s;
+        for (int j = 0; j < VPT; ++j) am = fmaxf(am, fabsf(xn[j]));
+        am = group_max<G>(am);
+        const float dq = am / 127.0f;
+        const float inv = dq > 0.f ? 127.0f / am : 0.f;
+        uint32_t pk[(VPT + 3) / 4];
+#pragma unroll
+        for (int k = 0; k < (VPT + 3) / 4; ++k) pk[k] = 0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int q = max(-127, min(127, rn_int(xn[j] * inv)));
+            pk[j >> 2] |= (uint32_t) (q & 0xFF) << (8 * (j & 3));
         }
-        return;
+        int8_t* dst = s_xq + (size_t) t * D + d0;
+        if constexpr (VPT == 16) *(int4*) dst = make_int4((int) pk[0], (int) pk[1], (int) pk[2], (int) pk[3]);
+        else if constexpr (VPT == 8) *(int2*) dst = make_int2((int) pk[0], (int) pk[1]);
+        else if constexpr (VPT == 4) *(int*) dst = (int) pk[0];
+        else if constexpr (VPT == 2) *(int16_t*) dst = (int16_t) pk[0];
+        else *dst = (int8_t) pk[0];
+        if ((tid % G) == 0) s_xs[t * NB + tid / G] = dq;
     }
+    if (aux) return;                                   // workgroup-uniform
     __syncthreads();
 
-    // 6. down rows: lo = silu(down . xq / HC)
+    // 5. partial down dots of stream c's columns
     float acc[RPW][T];
 #pragma unroll
     for (int s = 0; s < RPW; ++s)
@@ -261,12 +268,12 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
 #pragma unroll
     for (int i = 0; i < NBL; ++i) {
         const int b = lane + 64 * i;
-        if (b >= nb) continue;
+        if (b >= NB) continue;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int4* xp = (const int4*) (s_xq + (size_t) t * HCD + (size_t) 32 * b);
+            const int4* xp = (const int4*) (s_xq + (size_t) t * D + (size_t) 32 * b);
             const int4 x0 = xp[0], x1 = xp[1];
-            const float xs = s_xs[t * nb + b];
+            const float xs = s_xs[t * NB + b];
 #pragma unroll
             for (int s = 0; s < RPW; ++s)
                 acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c0[i][s], x0) + dot16(c1[i][s], x1)),
@@ -278,8 +285,8 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
         const int r = row0 + s;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const float v = wave_sum(acc[s][t]) / (float) HC4;
-            if (lane == 0 && r < L) a.lo[(size_t) t * L + r] = v / (1.0f + __expf(-v));
+            const float v = wave_sum(acc[s][t]);
+            if (lane == 0 && r < L) a.lo_part[((size_t) t * HC4 + c) * L + r] = v;
         }
     }
 }
@@ -296,7 +303,7 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
     const int li = lane & 15, c = lane >> 4;
     const int lb = min(li, nb - 1);
 
-    // every load first: weights, the residual / scale / norm inputs of xn, and lo
+    // every load first: weights, the residual / scale / norm inputs of xn, and the lo partials
     int4 c0[2], c1[2];
     uint16_t sraw[2];
     float rr[2][T], nwv[2], nscv[T];
@@ -314,18 +321,27 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) nscv[t] = a.nsc[t * HC4 + c];
-    float4 lv[8];
+    const bool stager = tid < T * nb;
     const int lt = min(tid / nb, T - 1), lbb = tid % nb;
-    if (tid < T * nb) {                      // issued after every other load of the wave
+    float v[32];
+    if (stager) {                            // issued after every other load of the wave
+        float4 pv[HC4][8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) lv[k] = *(const float4*) (a.lo + (size_t) lt * L + 32 * lbb + 4 * k);
-    }
-    // quant32(lo) once per workgroup
-    if (tid < T * nb) {
-        float v[32];
+        for (int s = 0; s < HC4; ++s)
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                pv[s][k] = *(const float4*) (a.lo_part + ((size_t) lt * HC4 + s) * L + 32 * lbb + 4 * k);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            v[4 * k] = lv[k].x; v[4 * k + 1] = lv[k].y; v[4 * k + 2] = lv[k].z; v[4 * k + 3] = lv[k].w;
+            const float4 p0 = pv[0][k], p1 = pv[1][k], p2 = pv[2][k], p3 = pv[3][k];
+            const float4 sum = make_float4((p0.x + p1.x) + (p2.x + p3.x), (p0.y + p1.y) + (p2.y + p3.y),
+                                           (p0.z + p1.z) + (p2.z + p3.z), (p0.w + p1.w) + (p2.w + p3.w));
+            const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x = s4[j] / (float) HC4;
+                v[4 * k + j] = x / (1.0f + __expf(-x));
+            }
         }
         int4 q0, q1;
         float xs;
@@ -333,6 +349,16 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
         s_lq[lt][2 * lbb] = q0;
         s_lq[lt][2 * lbb + 1] = q1;
         s_ls[lt][lbb] = xs;
+        if (blockIdx.x == 0 && a.lo) {
+            float* lo = a.lo + (size_t) lt * L + 32 * lbb;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ((float4*) lo)[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        }
+    }
+    if (blockIdx.x == 0 && a.inj && tid >= 256 - T * HC4) {   // summed inject of row t, output o
+        const int j = tid - (256 - T * HC4), t = j / HC4, o = j % HC4;
+        const float* ip = a.inj_part + (size_t) t * HC4 * HC4 + o;
+        a.inj[t * HC4 + o] = (ip[0] + ip[HC4]) + (ip[2 * HC4] + ip[3 * HC4]);
     }
     __syncthreads();
 #pragma unroll
@@ -361,54 +387,57 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
 namespace wzy {
 
 namespace {
-template <int T, int DC, int RPW>
-void launch_pre_tdc(const HcPreArgs& a, hipStream_t st) {
-    const int HCD = HC4 * a.D;
-    const int rows_wg = 4 * RPW;
-    const int blocks = (a.HCLR + rows_wg - 1) / rows_wg + (a.inj_w ? HC4 : 0);
-    const size_t lds = (size_t) T * HCD + (size_t) T * (HCD / 32) * sizeof(float);
-    hipLaunchKernelGGL((hc_pre_kernel<T, DC, RPW>), dim3(blocks), dim3(256), lds, st, a);
+constexpr int PRE_RPW = 2;
+
+template <int T, int VPT>
+void launch_pre_tv(const HcPreArgs& a, hipStream_t st) {
+    constexpr int NBL = (VPT * 8 + 63) / 64;          // D/32 blocks over 64 lanes (D = 256*VPT)
+    const int nrb = (a.HCLR + 4 * PRE_RPW - 1) / (4 * PRE_RPW);
+    const size_t lds = (size_t) T * a.D + (size_t) T * (a.D / 32) * sizeof(float);
+    hipLaunchKernelGGL((hc_pre_kernel<T, VPT, NBL, PRE_RPW>), dim3(HC4 * (nrb + 1)), dim3(256), lds, st, a);
 }
 template <int T>
 void launch_pre_t(const HcPreArgs& a, hipStream_t st) {
-    if (a.D <= 1024) launch_pre_tdc<T, 1024, 2>(a, st);
-    else if (a.D <= 2048) launch_pre_tdc<T, 2048, 2>(a, st);
-    else launch_pre_tdc<T, 4096, 1>(a, st);
+    switch (a.D / 256) {
+        case 1: launch_pre_tv<T, 1>(a, st); break;
+        case 2: launch_pre_tv<T, 2>(a, st); break;
+        case 4: launch_pre_tv<T, 4>(a, st); break;
+        case 8: launch_pre_tv<T, 8>(a, st); break;
+        default: launch_pre_tv<T, 16>(a, st); break;
+    }
 }
 }  // namespace
 
-int launch_hc_pre(const HcPreArgs& a0, int T, hipStream_t st) {
+size_t hc_workspace_bytes(int HC, int HCLR, int T) {
+    return align_up((size_t) T * HC * HCLR * sizeof(float), 256) + align_up((size_t) T * HC * HC * sizeof(float), 256);
+}
+void hc_carve_workspace(void* ws, int HC, int HCLR, int T, float** lo_part, float** inj_part) {
+    *lo_part = (float*) ws;
+    *inj_part = (float*) ((char*) ws + align_up((size_t) T * HC * HCLR * sizeof(float), 256));
+}
+
+int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "hc_pre: T out of range");
-    WZY_REQUIRE(a0.HC == HC4 && a0.D % 256 == 0 && a0.D >= 256 && a0.D <= 4096 && a0.HCLR % 32 == 0 &&
-                    a0.HCLR >= 32 && a0.HCLR <= 512,
-                "hc_pre: unsupported shape (HC must be 4, D a multiple of 256 <= 4096, HCLR a multiple of 32 <= 512)");
-    WZY_REQUIRE((a0.R_in != nullptr) + (a0.emb_table != nullptr) + (a0.emb_rows != nullptr) == 1,
+    const int vpt = a.D / 256;
+    WZY_REQUIRE(a.HC == HC4 && a.D % 256 == 0 && (vpt == 1 || vpt == 2 || vpt == 4 || vpt == 8 || vpt == 16) &&
+                    a.HCLR % 32 == 0 && a.HCLR >= 32 && a.HCLR <= 512,
+                "hc_pre: unsupported shape (HC must be 4, D one of 256/512/1024/2048/4096, HCLR a multiple of 32 "
+                "<= 512)");
+    WZY_REQUIRE((a.R_in != nullptr) + (a.emb_table != nullptr) + (a.emb_rows != nullptr) == 1,
                 "hc_pre: exactly one of R_in / emb_table / emb_rows");
-    WZY_REQUIRE(!a0.emb_table || a0.toks, "hc_pre: embedding mode needs toks");
-    WZY_REQUIRE(!a0.bo || a0.inj_prev, "hc_pre: fold needs inj_prev");
-    WZY_REQUIRE(a0.R_out && a0.norm_w && a0.down_q && a0.down_s && a0.nsc && a0.lo, "hc_pre: null pointer");
-    WZY_REQUIRE(!a0.inj_w || a0.inj, "hc_pre: inject weights need an inj output");
-    // rows per launch so that the LDS copy of quant32(xn) stays within 40 KB
-    const int HCD = HC4 * a0.D;
-    const int tb = std::max(1, std::min(4, (40 * 1024) / (HCD + HCD / 8)));
-    for (int t0 = 0; t0 < T; t0 += tb) {
-        const int n = std::min(tb, T - t0);
-        HcPreArgs a = a0;
-        if (a.R_in) a.R_in += (size_t) t0 * HCD;
-        if (a.toks) a.toks += t0;
-        if (a.emb_rows) a.emb_rows += (size_t) t0 * a.D;
-        if (a.bo) a.bo += (size_t) t0 * a.D;
-        if (a.inj_prev) a.inj_prev += (size_t) t0 * HC4;
-        a.R_out += (size_t) t0 * HCD;
-        a.nsc += (size_t) t0 * HC4;
-        a.lo += (size_t) t0 * a.HCLR;
-        if (a.inj) a.inj += (size_t) t0 * HC4;
-        switch (n) {
-            case 1: launch_pre_t<1>(a, st); break;
-            case 2: launch_pre_t<2>(a, st); break;
-            case 3: launch_pre_t<3>(a, st); break;
-            default: launch_pre_t<4>(a, st); break;
-        }
+    WZY_REQUIRE(!a.emb_table || a.toks, "hc_pre: embedding mode needs toks");
+    WZY_REQUIRE(!a.bo || a.inj_prev, "hc_pre: fold needs inj_prev");
+    WZY_REQUIRE(a.R_out && a.norm_w && a.down_q && a.down_s && a.nsc && a.lo_part, "hc_pre: null pointer");
+    WZY_REQUIRE(!a.inj_w || a.inj_part, "hc_pre: inject weights need an inj_part output");
+    switch (T) {
+        case 1: launch_pre_t<1>(a, st); break;
+        case 2: launch_pre_t<2>(a, st); break;
+        case 3: launch_pre_t<3>(a, st); break;
+        case 4: launch_pre_t<4>(a, st); break;
+        case 5: launch_pre_t<5>(a, st); break;
+        case 6: launch_pre_t<6>(a, st); break;
+        case 7: launch_pre_t<7>(a, st); break;
+        default: launch_pre_t<8>(a, st); break;
     }
     WZY_LAUNCH_CHECK();
     return WZY_OK;
@@ -417,7 +446,8 @@ int launch_hc_pre(const HcPreArgs& a0, int T, hipStream_t st) {
 int launch_hc_post(const HcPostArgs& a, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "hc_post: T out of range");
     WZY_REQUIRE(a.HC == HC4 && a.HCLR % 32 == 0 && a.HCLR >= 32 && a.HCLR <= 512, "hc_post: unsupported shape");
-    WZY_REQUIRE(a.R && a.nsc && a.norm_w && a.up_q && a.up_s && a.lo && a.mixed, "hc_post: null pointer");
+    WZY_REQUIRE(a.R && a.nsc && a.norm_w && a.up_q && a.up_s && a.lo_part && a.mixed, "hc_post: null pointer");
+    WZY_REQUIRE(!a.inj || a.inj_part, "hc_post: inj output needs inj_part");
     const int waves = (a.D + 1) / 2;
     const int blocks = (waves + 3) / 4;
     switch (T) {
@@ -435,20 +465,28 @@ int launch_hc_post(const HcPostArgs& a, int T, hipStream_t st) {
 // ---------------------------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------------------------
+extern "C" size_t wzy_hc_read_workspace_bytes(int HC, int HCLR, int T) { return hc_workspace_bytes(HC, HCLR, T); }
+
 extern "C" int wzy_hc_read(const float* R_in, const uint16_t* emb_table, const int* toks, int n_vocab,
                            const float* bo, const float* inj_prev, float* R_out, const float* norm_w,
                            const int8_t* down_q, const uint16_t* down_s, const uint16_t* inj_w,
                            const int8_t* up_q, const uint16_t* up_s, float* nsc, float* lo, float* inj,
-                           float* mixed, int D, int HC, int HCLR, float eps, int T, void* stream) {
+                           float* mixed, int D, int HC, int HCLR, float eps, int T, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    WZY_REQUIRE(workspace && workspace_bytes >= hc_workspace_bytes(HC, HCLR, T),
+                "wzy_hc_read: workspace of wzy_hc_read_workspace_bytes() bytes required");
+    WZY_REQUIRE(!inj_w || inj, "wzy_hc_read: inject weights need an inj output");
     HcPreArgs a{};
     a.R_in = R_in; a.emb_table = emb_table; a.toks = toks; a.n_vocab = n_vocab;
     a.bo = bo; a.inj_prev = inj_prev; a.R_out = R_out; a.norm_w = norm_w;
-    a.down_q = down_q; a.down_s = down_s; a.inj_w = inj_w; a.nsc = nsc; a.lo = lo; a.inj = inj;
+    a.down_q = down_q; a.down_s = down_s; a.inj_w = inj_w; a.nsc = nsc;
+    hc_carve_workspace(workspace, HC, HCLR, T, &a.lo_part, &a.inj_part);
     a.D = D; a.HC = HC; a.HCLR = HCLR; a.eps = eps;
     hipStream_t st = as_stream(stream);
     WZY_TRY(launch_hc_pre(a, T, st));
     HcPostArgs b{};
-    b.R = R_out; b.nsc = nsc; b.norm_w = norm_w; b.up_q = up_q; b.up_s = up_s; b.lo = lo; b.mixed = mixed;
+    b.R = R_out; b.nsc = nsc; b.norm_w = norm_w; b.up_q = up_q; b.up_s = up_s; b.lo_part = a.lo_part;
+    b.inj_part = inj_w ? a.inj_part : nullptr; b.lo = lo; b.inj = inj_w ? inj : nullptr; b.mixed = mixed;
     b.D = D; b.HC = HC; b.HCLR = HCLR;
     return launch_hc_post(b, T, st);
 }

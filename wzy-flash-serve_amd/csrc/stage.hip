@@ -107,6 +107,7 @@ struct wzy_stage {
     float* R[2] = {nullptr, nullptr};
     int r_pre_head = 0;             // which R buffer holds the pre-head residual
     float *nsc = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
+    float *lo_part = nullptr, *inj_part = nullptr;   // HC read partials (per source stream)
     float *qkv = nullptr, *z = nullptr, *ab = nullptr, *y = nullptr, *block = nullptr, *comb = nullptr;
     float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
     float *att_part = nullptr, *att_ml = nullptr, *att_out = nullptr;
@@ -329,6 +330,11 @@ int wzy_stage::init_buffers() {
     WZY_TRY(alloc_t(&R[0], (size_t) W * HCD)); WZY_TRY(alloc_t(&R[1], (size_t) W * HCD));
     WZY_TRY(alloc_t(&nsc, (size_t) W * c.hc));
     WZY_TRY(alloc_t(&lo, (size_t) W * c.hc_lr));
+    {
+        void* hw = nullptr;
+        WZY_TRY(alloc(&hw, hc_workspace_bytes(c.hc, c.hc_lr, W)));
+        hc_carve_workspace(hw, c.hc, c.hc_lr, W, &lo_part, &inj_part);
+    }
     WZY_TRY(alloc_t(&inj_a, (size_t) W * c.hc)); WZY_TRY(alloc_t(&inj_f, (size_t) W * c.hc));
     WZY_TRY(alloc_t(&mixed, (size_t) W * D));
     WZY_TRY(alloc_t(&qkv, (size_t) W * QKV)); WZY_TRY(alloc_t(&z, (size_t) W * GV));
@@ -415,12 +421,13 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
         a.bo = pend_bo; a.inj_prev = pend_inj;
         a.R_out = R[cur ^ 1];
         a.norm_w = norm_w; a.down_q = down.q; a.down_s = down.s; a.inj_w = inj_w;
-        a.nsc = nsc; a.lo = lo; a.inj = inj_out;
+        a.nsc = nsc; a.lo_part = lo_part; a.inj_part = inj_part;
         a.D = D; a.HC = c.hc; a.HCLR = c.hc_lr; a.eps = c.eps;
         WZY_TRY(launch_hc_pre(a, T, st));
         cur ^= 1;
         HcPostArgs b{};
-        b.R = R[cur]; b.nsc = nsc; b.norm_w = norm_w; b.up_q = up.q; b.up_s = up.s; b.lo = lo; b.mixed = mixed;
+        b.R = R[cur]; b.nsc = nsc; b.norm_w = norm_w; b.up_q = up.q; b.up_s = up.s; b.lo_part = lo_part;
+        b.inj_part = inj_out ? inj_part : nullptr; b.lo = lo; b.inj = inj_out; b.mixed = mixed;
         b.D = D; b.HC = c.hc; b.HCLR = c.hc_lr;
         return launch_hc_post(b, T, st);
     };

@@ -1,6 +1,7 @@
 // wzy_hc.h -- internal launchers of the hyper-connection read (hc_pre + hc_post).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace wzy {
@@ -19,8 +20,8 @@ struct HcPreArgs {
     const uint16_t* down_s;
     const uint16_t* inj_w;      // bf16 [HC][HC*D] (nullable: the head has no inject)
     float* nsc;                 // [T][HC] rsqrt(mean(R_out^2) + eps)
-    float* lo;                  // [T][HCLR] silu(down . xn / HC)
-    float* inj;                 // [T][HC]
+    float* lo_part;             // [T][HC][HCLR] per-stream partials of down . quant32(xn)
+    float* inj_part;            // [T][HC src stream][HC out] per-stream partials of inj_w . xn
     int D, HC, HCLR;
     float eps;
 };
@@ -31,10 +32,17 @@ struct HcPostArgs {
     const float* norm_w;
     const int8_t* up_q;         // Q8_0 [HC*D][HCLR]
     const uint16_t* up_s;
-    const float* lo;            // [T][HCLR]
+    const float* lo_part;       // hc_pre partials
+    const float* inj_part;      // hc_pre inject partials (nullable with inj)
+    float* lo;                  // [T][HCLR] silu(sum of partials / HC) (nullable)
+    float* inj;                 // [T][HC] summed inject (nullable)
     float* mixed;               // [T][D]
     int D, HC, HCLR;
 };
+
+// Device bytes of the partial buffers for T rows, and their carving from one workspace.
+size_t hc_workspace_bytes(int HC, int HCLR, int T);
+void hc_carve_workspace(void* ws, int HC, int HCLR, int T, float** lo_part, float** inj_part);
 
 int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st);
 int launch_hc_post(const HcPostArgs& a, int T, hipStream_t st);

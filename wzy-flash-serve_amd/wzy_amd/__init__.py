@@ -115,7 +115,8 @@ _SIGS = {
     "wzy_stage_write_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32)], True),
     # layer kernels
-    "wzy_hc_read": (I32, [P, P, P, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P], True),
+    "wzy_hc_read_workspace_bytes": (SZ, [I32, I32, I32], False),
+    "wzy_hc_read": (I32, [P, P, P, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, SZ, P], True),
     "wzy_gdn_step": (I32, [P, P, P, P, P, P, P, P, P, F32, P, I32, I32, I32, P, P, P], True),
     "wzy_gdn_recurrence": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32, P, P], True),
     "wzy_qsa_prepare": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, P], True),
