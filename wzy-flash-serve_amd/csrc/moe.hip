@@ -126,62 +126,119 @@ struct RouteLds {
     int c[4];
 };
 
-constexpr int RT_V = 16;      // logits per lane (E <= 1024)
-
+// Logits of one row per wave: RV per lane (lane + 64*i), RV = 8 for E <= 512, 16 for E <= 1024.
 // wave wv prefetches rows wv, wv+4 of the logits (issued before anything uses them)
-template <int T>
-WZY_DEV void route_prefetch(const float* __restrict__ logits, int E, float (&p)[(T + 3) / 4][RT_V]) {
+template <int T, int RV>
+WZY_DEV void route_prefetch(const float* __restrict__ logits, int E, float (&p)[(T + 3) / 4][RV]) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
     for (int rr = 0; rr < (T + 3) / 4; ++rr) {
         const int t = wv + 4 * rr;
 #pragma unroll
-        for (int i = 0; i < RT_V; ++i) {
+        for (int i = 0; i < RV; ++i) {
             const int idx = lane + 64 * i;
             p[rr][i] = (t < T && idx < E) ? logits[(size_t) t * E + idx] : -INFINITY;
         }
     }
 }
 
-template <int T>
-WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RT_V], int E, int K, RouteLds& r) {
+// Routing key of one (probability, expert id): probabilities are >= 0, so their float bits order
+// like the values; the low word ranks lower ids first.  Key 0 ranks below every real entry.
+WZY_DEV uint64_t route_key(float p, int id) {
+    return ((uint64_t) __builtin_bit_cast(uint32_t, p) << 32) | (uint32_t) (0xFFFFFFFFu - (uint32_t) id);
+}
+
+// Bitonic sort of RV keys into descending order, in registers.
+template <int RV>
+WZY_DEV void sort_keys_desc(uint64_t (&k)[RV]) {
+#pragma unroll
+    for (int s = 2; s <= RV; s <<= 1)
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < RV; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const bool desc = (i & s) == 0;
+                    const uint64_t a = k[i], b = k[l];
+                    const bool sw = desc ? (b > a) : (a > b);
+                    k[i] = sw ? b : a;
+                    k[l] = sw ? a : b;
+                }
+            }
+}
+
+// Softmax top-K of one row in one wave (ranking: probability desc, expert id asc).  Every lane
+// sorts the keys of its RV probabilities once; each of the K rounds is one DPP wave maximum over the
+// lane heads, and the lane holding the winner pops its head.  Lane k ends with the k-th routed
+// (id, probability); wsum is their sum in rank order.
+template <int RV>
+WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, float& wsum) {
+    const int lane = threadIdx.x & 63;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < RV; ++i) mx = fmaxf(mx, p[i]);
+    mx = wave_max(mx);
+    float es = 0.f;
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+        if (lane + 64 * i < E) { p[i] = __expf(p[i] - mx); es += p[i]; }
+    }
+    es = wave_sum(es);
+    const float inv = 1.0f / es;
+    uint64_t key[RV];
+#pragma unroll
+    for (int i = 0; i < RV; ++i) key[i] = (lane + 64 * i < E) ? route_key(p[i] * inv, lane + 64 * i) : 0ull;
+    sort_keys_desc<RV>(key);
+    wsum = 0.f;
+    my_id = 0;
+    my_w = 0.f;
+    for (int k = 0; k < K; ++k) {
+        const uint64_t top = wave_max_u64(key[0]);
+        const bool pop = key[0] == top;
+#pragma unroll
+        for (int i = 0; i + 1 < RV; ++i) key[i] = pop ? key[i + 1] : key[i];
+        key[RV - 1] = pop ? 0ull : key[RV - 1];
+        const float bv = __builtin_bit_cast(float, (uint32_t) (top >> 32));
+        int bi = (int) (0xFFFFFFFFu - (uint32_t) top);
+        if (bi >= E || bi < 0) bi = 0;                   // non-finite logits: keep the id in range
+        if (lane == k) { my_id = bi; my_w = bv; }
+        wsum += bv;
+    }
+}
+
+template <int T, int RV>
+WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& r) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (T == 1) {
+        // one row: its K experts are distinct, so each is its own group with one member
+        if (wv == 0) {
+            int my_id;
+            float my_w, wsum;
+            route_row<RV>(p[0], E, K, my_id, my_w, wsum);
+            const float sc = fmaxf(wsum, 6.103515625e-05f);
+            if (lane < K) {
+                r.ids[lane] = my_id;
+                r.w[lane] = my_w / sc;
+                r.gidx[lane] = lane;
+                r.gexp[lane] = my_id;
+                r.gcnt[lane] = 1;
+                r.gmem[lane][0] = lane;
+            }
+            if (lane == 0) r.n_groups = K;
+        }
+        __syncthreads();
+        return;
+    }
 #pragma unroll
     for (int rr = 0; rr < (T + 3) / 4; ++rr) {
         const int t = wv + 4 * rr;
         if (t >= T) continue;                            // wave-uniform
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < RT_V; ++i) mx = fmaxf(mx, p[rr][i]);
-        mx = wave_max(mx);
-        float es = 0.f;
-#pragma unroll
-        for (int i = 0; i < RT_V; ++i) {
-            if (lane + 64 * i < E) { p[rr][i] = __expf(p[rr][i] - mx); es += p[rr][i]; }
-            else p[rr][i] = -3.f;
-        }
-        es = wave_sum(es);
-        const float inv = 1.0f / es;
-#pragma unroll
-        for (int i = 0; i < RT_V; ++i)
-            if (lane + 64 * i < E) p[rr][i] *= inv;
-        float wsum = 0.f;
-        for (int k = 0; k < K; ++k) {
-            float bv = -4.f;
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int i = 0; i < RT_V; ++i)
-                if (p[rr][i] > bv) { bv = p[rr][i]; bi = lane + 64 * i; }
-            wave_argmax(bv, bi);
-            if (bi >= E) bi = 0;                         // non-finite logits: keep the id in range
-#pragma unroll
-            for (int i = 0; i < RT_V; ++i)
-                if (lane + 64 * i == bi) p[rr][i] = -2.f;
-            if (lane == 0) { r.ids[t * K + k] = bi; r.w[t * K + k] = bv; }
-            wsum += bv;
-        }
+        int my_id;
+        float my_w, wsum;
+        route_row<RV>(p[rr], E, K, my_id, my_w, wsum);
         const float sc = fmaxf(wsum, 6.103515625e-05f);
-        if (lane < K) r.w[t * K + lane] = r.w[t * K + lane] / sc;
+        if (lane < K) { r.ids[t * K + lane] = my_id; r.w[t * K + lane] = my_w / sc; }
     }
     __syncthreads();
     // grouping: leader = first entry of an expert, slot = rank among the expert's entries
@@ -190,16 +247,12 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RT_V], int E, int K, RouteLds
     if (tid < n_ent) {
         id = r.ids[tid];
         leader = tid;
-        if (T == 1) {                                    // the K experts of one row are distinct
-            cnt = 1;
-        } else {
-            bool seen = false;
-            for (int f = 0; f < n_ent; ++f) {
-                if (r.ids[f] != id) continue;
-                if (!seen) { leader = f; seen = true; }
-                if (f < tid) ++slot;
-                ++cnt;
-            }
+        bool seen = false;
+        for (int f = 0; f < n_ent; ++f) {
+            if (r.ids[f] != id) continue;
+            if (!seen) { leader = f; seen = true; }
+            if (f < tid) ++slot;
+            ++cnt;
         }
     }
     const bool lead = tid < n_ent && leader == tid;
@@ -231,7 +284,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RT_V], int E, int K, RouteLds
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
 // scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
 // ---------------------------------------------------------------------------------------------
-template <int T>
+template <int T, int RV>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ RouteLds r;
@@ -245,10 +298,11 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
     float* s_sc = (float*) (s_qb + (size_t) T * nc);
 
     if (bid < a.n_routed_wg) {
-        float p[(T + 3) / 4][RT_V];
-        route_prefetch<T>(a.logits, a.E, p);
-        // stage x quantised per 16
-        for (int i = tid; i < T * nc; i += 256) {
+        float p[(T + 3) / 4][RV];
+        route_prefetch<T, RV>(a.logits, a.E, p);
+        // stage x quantised per 16, starting at wave 1 so that a one-row window stages on a wave that
+        // does not route
+        for (int i = (tid + 192) & 255; i < T * nc; i += 256) {
             const int t = i / nc, c = i - t * nc;
             float v[32];
 #pragma unroll
@@ -263,7 +317,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             s_qb[i] = qb;
             ((float2*) s_sc)[i] = make_float2(da, db);
         }
-        route_compute<T>(p, a.E, K, r);
+        route_compute<T, RV>(p, a.E, K, r);
         if (bid == 0) {                                  // publish the routing for moe_down
             const int n_ent = T * K;
             for (int i = tid; i < n_ent; i += blockDim.x) {
@@ -647,7 +701,10 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (2 * sizeof(int4) + sizeof(float2));
-    hipLaunchKernelGGL((moe_gate_up_kernel<T>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
+    if (a.E <= 512)
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
 }
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {

@@ -105,9 +105,12 @@ WZY_DEV float wave_max(float v) {
     return fmaxf(a, b);
 }
 
-// (value, index) argmax step: larger value wins, ties go to the lower index.
+// (value, index) argmax step: larger value wins, ties go to the lower index.  Branch-free: the
+// bitwise combination keeps the compiler from turning the test into divergent control flow.
 WZY_DEV void amax_merge(float& bv, int& bi, float ov, int oi) {
-    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
+    bv = take ? ov : bv;
+    bi = take ? oi : bi;
 }
 // Full-wave argmax with lowest-index tie-break; result is wave-uniform.
 WZY_DEV void wave_argmax(float& bv, int& bi) {
@@ -121,6 +124,31 @@ WZY_DEV void wave_argmax(float& bv, int& bi) {
     bv = as_f(__builtin_amdgcn_readlane(as_i(bv), 0));
     bi = __builtin_amdgcn_readlane(bi, 0);
     amax_merge(bv, bi, v32, i32);
+}
+
+// 64-bit DPP move (both halves with the same control); rows outside ROWMASK keep their own value.
+constexpr int DPP_ROW_BCAST15 = 0x142; // lane 15 of each row -> the next row
+constexpr int DPP_ROW_BCAST31 = 0x143; // lane 31 -> rows 2 and 3
+template <int CTRL, int ROWMASK>
+WZY_DEV uint64_t dpp_u64(uint64_t v) {
+    const int lo = (int) (uint32_t) v, hi = (int) (uint32_t) (v >> 32);
+    const uint32_t l2 = (uint32_t) __builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xF, false);
+    const uint32_t h2 = (uint32_t) __builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xF, false);
+    return ((uint64_t) h2 << 32) | l2;
+}
+WZY_DEV uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// Full-wave maximum of a 64-bit key with DPP only (no LDS swizzle): lane 63 ends with the maximum,
+// which is returned to every lane.
+WZY_DEV uint64_t wave_max_u64(uint64_t k) {
+    k = max_u64(k, dpp_u64<DPP_XOR1, 0xF>(k));
+    k = max_u64(k, dpp_u64<DPP_XOR2, 0xF>(k));
+    k = max_u64(k, dpp_u64<DPP_HALF_MIRROR, 0xF>(k));
+    k = max_u64(k, dpp_u64<DPP_MIRROR, 0xF>(k));
+    k = max_u64(k, dpp_u64<DPP_ROW_BCAST15, 0xA>(k));
+    k = max_u64(k, dpp_u64<DPP_ROW_BCAST31, 0xC>(k));
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) k, 63);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (k >> 32), 63);
+    return ((uint64_t) hi << 32) | lo;
 }
 
 // Block-wide sum for blockDim.x = NW*64 threads; `sh` must hold NW floats. Result on every thread.
