@@ -25,7 +25,10 @@ using namespace wzy;
 namespace {
 
 constexpr int DN_TILE = 8;    // output rows of one down workgroup
-constexpr int DN_BATCH = 4;   // work items whose loads a 16-lane slot issues together
+// work items whose loads a 16-lane slot issues together: a one-row window's 11 x 8 items fit in
+// one batch of 6 per slot, so every weight load of the workgroup is issued at once
+template <int T>
+constexpr int dn_batch() { return T == 1 ? 6 : 4; }
 constexpr int MAX_ENT = WZY_MAX_W * MOE_MAX_K;
 constexpr int DN_STAGE_BYTES = 24 * 1024;   // activation staging limit of moe_down
 
@@ -498,6 +501,8 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     const int D = a.D, F = a.F, K = a.K;
     const int d0 = blockIdx.x * DN_TILE;
     const int nchunk = F / 32, n_ent = T * K;
+    constexpr int DN_BATCH = dn_batch<T>();
+    // the group tables of every possible group are loaded without waiting for the group count
     const int ng = *a.n_groups;
     int4* s_aqa = (int4*) s_dyn;
     int4* s_aqb = s_aqa + (size_t) n_ent * nchunk;
@@ -505,7 +510,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     int4* s_sha = (int4*) (s_as + (size_t) n_ent * (F / 16));
     int4* s_shb = s_sha + (size_t) T * nchunk;
     float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
-    for (int i = tid; i < ng; i += blockDim.x) {
+    for (int i = tid; i < n_ent; i += blockDim.x) {
         s_gexp[i] = a.grp_exp[i];
         s_gcnt[i] = a.grp_cnt[i];
 #pragma unroll
