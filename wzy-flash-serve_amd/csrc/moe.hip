@@ -490,13 +490,14 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
 // ---------------------------------------------------------------------------------------------
-template <int T, bool STAGE>
+template <int T, bool STAGE, int CI>
 __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_part[MAX_ENT][DN_TILE];
     __shared__ float s_sh[WZY_MAX_W][DN_TILE];
     __shared__ int s_gexp[MAX_ENT], s_gcnt[MAX_ENT];
     __shared__ int s_gmem[MAX_ENT][WZY_MAX_W];
+    __shared__ float s_wts[MAX_ENT], s_sg[WZY_MAX_W];
     const int tid = threadIdx.x;
     const int D = a.D, F = a.F, K = a.K;
     const int d0 = blockIdx.x * DN_TILE;
@@ -515,7 +516,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         s_gcnt[i] = a.grp_cnt[i];
 #pragma unroll
         for (int m = 0; m < WZY_MAX_W; ++m) s_gmem[i][m] = a.grp_mem[i * WZY_MAX_W + m];
+        s_wts[i] = a.wts[i];
     }
+    if (tid < T) s_sg[tid] = a.sg[tid];
     if (STAGE) {
         for (int i = tid; i < n_ent * nchunk; i += 256) {
             const int4* xp = (const int4*) (a.aq16 + (size_t) i * 32);
@@ -539,35 +542,44 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         float sdn[DN_BATCH];
 #pragma unroll
         for (int b = 0; b < DN_BATCH; ++b) {
-            sdn[b] = 0.f;
+            // tensor scale of the item's expert, loaded with the first codes (shared items read
+            // expert 0's and ignore it)
+            const int item = min(i0 + 16 * b, n_items - 1);
+            const int g = item / DN_TILE;
+            const uint8_t* rec = a.experts + (g < ng ? (size_t) s_gexp[g] * o.rec : 0);
+            sdn[b] = ((const float*) (rec + o.tail))[2];
 #pragma unroll
             for (int m = 0; m < T; ++m) acc[b][m] = 0.f;
         }
-        for (int c = li; c < nchunk; c += 16) {
-            // the weight loads of all DN_BATCH items first (raw scales), arithmetic afterwards
+        // CI = nchunk/16 rounded up chunk rounds per lane, unrolled (a loop here would make every
+        // round wait for the previous round's loads)
+#pragma unroll
+        for (int ci = 0; ci < CI; ++ci) {
+            const bool cvalid = li + 16 * ci < nchunk;
+            const int c = min(li + 16 * ci, nchunk - 1);
+            // the weight loads of all DN_BATCH items first (raw scales), arithmetic afterwards.  Routed
+            // and shared items load through one selected pointer (32 code bytes, one 16-bit scale
+            // word, one tail float): no divergent branch, so no load waits for an earlier one.
             int4 c0[DN_BATCH], c1[DN_BATCH];
             uint32_t sraw[DN_BATCH];
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
                 const int item = min(i0 + 16 * b, n_items - 1);
                 const int g = item / DN_TILE, d = d0 + item % DN_TILE;
-                if (g < ng) {
-                    const uint8_t* rec = a.experts + (size_t) s_gexp[g] * o.rec;
-                    c0[b] = ld_stream_i4(rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16);
-                    c1[b] = make_int4(0, 0, 0, 0);
-                    sraw[b] = *(const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c);
-                    sdn[b] = ((const float*) (rec + o.tail))[2];
-                } else {
-                    const int4* cp = (const int4*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
-                    c0[b] = ld_stream_i4(cp);
-                    c1[b] = ld_stream_i4(cp + 1);
-                    sraw[b] = a.shd_s[(size_t) d * nchunk + c];
-                }
+                const bool routed = g < ng;
+                const uint8_t* rec = a.experts + (routed ? (size_t) s_gexp[g] * o.rec : 0);
+                const uint8_t* cp = routed ? rec + o.dn_codes + (size_t) d * (F / 2) + (size_t) c * 16
+                                           : (const uint8_t*) (a.shd_q + (size_t) d * F + (size_t) c * 32);
+                const uint16_t* sp = routed ? (const uint16_t*) (rec + o.dn_scales + (size_t) d * (F / 16) + 2 * c)
+                                            : a.shd_s + (size_t) d * nchunk + c;
+                c0[b] = ld_stream_i4((const int4*) cp);
+                c1[b] = ld_stream_i4((const int4*) cp + 1);
+                sraw[b] = *sp;
             }
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
                 const int item = i0 + 16 * b;
-                if (item >= n_items) continue;
+                if (item >= n_items || !cvalid) continue;
                 const int g = item / DN_TILE;
                 if (g < ng) {
                     const int4 wa = e2m1_sub16((uint32_t) c0[b].x, (uint32_t) c0[b].y);
@@ -626,9 +638,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     __syncthreads();
     if (tid < T * DN_TILE) {
         const int t = tid / DN_TILE, rl = tid % DN_TILE;
-        float s = s_sh[t][rl] * sigmoidf_(a.sg[t]);
+        float s = s_sh[t][rl] * sigmoidf_(s_sg[t]);
         for (int k = 0; k < K; ++k) {
-            const float wk = a.wts[t * K + k];
+            const float wk = s_wts[t * K + k];
             if (wk != 0.0f) s += wk * s_part[t * K + k][rl];
         }
         a.comb[(size_t) t * D + d0 + rl] = s;
@@ -665,7 +677,7 @@ int moe_check(const wzy_moe_weights* w, int T) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "moe: T must be in [1, %d]", WZY_MAX_W);
     WZY_REQUIRE(w->n_embd % 256 == 0 && w->n_embd >= 256 && w->n_embd <= 2048,
                 "moe: n_embd must be a multiple of 256 <= 2048");
-    WZY_REQUIRE(w->n_ff % 64 == 0 && w->n_ff >= 64, "moe: n_ff must be a multiple of 64");
+    WZY_REQUIRE(w->n_ff % 64 == 0 && w->n_ff >= 64 && w->n_ff <= 2048, "moe: n_ff must be a multiple of 64 <= 2048");
     WZY_REQUIRE(w->n_exp >= 1 && w->n_exp <= 1024, "moe: n_exp must be in [1, 1024]");
     WZY_REQUIRE(w->top_k >= 1 && w->top_k <= MOE_MAX_K && w->top_k <= w->n_exp, "moe: top_k must be in [1, %d]",
                 MOE_MAX_K);
@@ -711,15 +723,24 @@ static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     else
         hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
 }
+template <int T, int CI>
+static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
+    if (lds <= (size_t) DN_STAGE_BYTES)
+        hipLaunchKernelGGL((moe_down_kernel<T, true, CI>), dim3(a.D / DN_TILE), dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((moe_down_kernel<T, false, CI>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
+}
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
     const int n_ent = T * a.K, nchunk = a.F / 32;
     const size_t lds = (size_t) n_ent * nchunk * 2 * sizeof(int4) + (size_t) n_ent * (a.F / 16) * sizeof(float) +
                        (size_t) T * nchunk * (2 * sizeof(int4) + sizeof(float));
-    if (lds <= (size_t) DN_STAGE_BYTES)
-        hipLaunchKernelGGL((moe_down_kernel<T, true>), dim3(a.D / DN_TILE), dim3(256), lds, st, a);
-    else
-        hipLaunchKernelGGL((moe_down_kernel<T, false>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
+    switch ((nchunk + 15) / 16) {
+        case 1: launch_dn_tc<T, 1>(a, lds, st); break;
+        case 2: launch_dn_tc<T, 2>(a, lds, st); break;
+        case 3: launch_dn_tc<T, 3>(a, lds, st); break;
+        default: launch_dn_tc<T, 4>(a, lds, st); break;
+    }
 }
 
 static void launch_gu(const MoeGuArgs& a, int T, hipStream_t st) {
