@@ -359,17 +359,31 @@ WZY_DEV void quant32_f(const float* __restrict__ xp, int4& q0, int4& q1, float& 
     q0 = make_int4(w[0], w[1], w[2], w[3]);
     q1 = make_int4(w[4], w[5], w[6], w[7]);
 }
+// The segment that owns (wave-uniform) `wave`, chosen by selects over the kernel-argument copy so
+// that every field comes from scalar loads issued at kernel entry: a dynamically indexed
+// segs.seg[si] would be read with dependent vector loads before the first weight load.
+__device__ __forceinline__ GemvSeg pick_seg(const GemvSegs& segs, int wave) {
+    GemvSeg sg = segs.seg[0];
+#pragma unroll
+    for (int i = 1; i < GEMV_MAX_SEGS; ++i) {
+        const bool take = (i < segs.n) & (wave >= segs.seg[i].wave0);
+        sg.w = take ? segs.seg[i].w : sg.w;
+        sg.s = take ? segs.seg[i].s : sg.s;
+        sg.y = take ? segs.seg[i].y : sg.y;
+        sg.rows = take ? segs.seg[i].rows : sg.rows;
+        sg.kind = take ? segs.seg[i].kind : sg.kind;
+        sg.y_stride = take ? segs.seg[i].y_stride : sg.y_stride;
+        sg.wave0 = take ? segs.seg[i].wave0 : sg.wave0;
+    }
+    return sg;
+}
 }  // namespace
 
 template <int T, int NBL, int RPW>
 __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const float* __restrict__ x, int cols) {
     const int lane = threadIdx.x & 63;
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    int si = 0;
-#pragma unroll
-    for (int i = 1; i < GEMV_MAX_SEGS; ++i)
-        if (i < segs.n && wave >= segs.seg[i].wave0) si = i;
-    const GemvSeg& sg = segs.seg[si];
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const GemvSeg sg = pick_seg(segs, wave);
     const int row0 = (wave - sg.wave0) * RPW;
     if (row0 >= sg.rows) return;
     float acc[RPW][T];
@@ -385,7 +399,7 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
         const int nb = cols >> 5;
         const int8_t* W = (const int8_t*) sg.w;
         int4 c0[NBL][RPW], c1[NBL][RPW];
-        uint16_t sraw[NBL][RPW];
+        uint32_t sraw[NBL][RPW];     // 16-bit scales held in 32-bit registers (no packing that waits for the load)
 #pragma unroll
         for (int i = 0; i < NBL; ++i) {
             const int b = min(lane + 64 * i, nb - 1);
@@ -496,23 +510,19 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
                                                             int flags) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = (blockIdx.x * blockDim.x + tid) >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + tid) >> 6);
     const int nb = cols >> 5, n8 = cols >> 3;
     float4* s_xf = (float4*) s_dyn;                                            // [T][2][n8]
     int4* s_xq = (int4*) (s_dyn + ((flags & 2) ? (size_t) T * cols * 4 : 0));  // [T][2][nb]
     float* s_xs = (float*) ((unsigned char*) s_xq + ((flags & 1) ? (size_t) T * cols : 0));   // [T][nb]
-    int si = 0;
-#pragma unroll
-    for (int i = 1; i < GEMV_MAX_SEGS; ++i)
-        if (i < segs.n && wave >= segs.seg[i].wave0) si = i;
-    const GemvSeg& sg = segs.seg[si];
+    const GemvSeg sg = pick_seg(segs, wave);
     const int row0 = (wave - sg.wave0) * RPW;
     const bool active = row0 < sg.rows;
     const bool q8 = sg.kind == GEMV_Q8;
 
     // 1. weights (wave-uniform branches; clamped indices; raw scales)
     int4 c0[NBL][RPW], c1[NBL][RPW];
-    uint16_t sraw[NBL][RPW];
+    uint32_t sraw[NBL][RPW];         // 16-bit scales held in 32-bit registers (no packing that waits for the load)
     constexpr int NU = NBL * 4;                           // uint4 (8 bf16) per lane per row: cols/8/64
     uint4 wv[NU][RPW];
     if (active && q8) {
@@ -541,12 +551,17 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             }
         }
     }
-    // 2. stage x: thread i owns 32-column block i of the window
-    for (int i = tid; i < T * nb; i += 256) {
-        const int t = i / nb, b = i - t * nb;
-        float4 v4[8];
+    // 2. stage x: thread i owns 32-column block i of the window.  The first item is loaded in
+    //    straight-line code right behind the weights (clamped: always a valid address), so both are
+    //    in flight together; a loop here would wait for the weights at its header before loading x.
+    //    Only windows with more than 256 blocks (T > 1) loop for more.
+    const int nitem = T * nb;
+    const int i0 = min(tid, nitem - 1);
+    const int t0 = i0 / nb, b0 = i0 - t0 * nb;
+    float4 xv[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v4[k] = ((const float4*) (x + (size_t) t * cols + (size_t) b * 32))[k];
+    for (int k = 0; k < 8; ++k) xv[k] = ((const float4*) (x + (size_t) t0 * cols + (size_t) b0 * 32))[k];
+    auto stage = [&](const float4 (&v4)[8], int t, int b) {
         if (flags & 2) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -562,9 +577,25 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             s_xq[((size_t) t * 2 + 1) * nb + b] = q1;
             s_xs[(size_t) t * nb + b] = xs;
         }
+    };
+    if (tid < nitem) stage(xv, t0, b0);
+    if (T > 1) {
+        for (int i = tid + 256; i < nitem; i += 256) {
+            const int t = i / nb, b = i - t * nb;
+            float4 v4[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v4[k] = ((const float4*) (x + (size_t) t * cols + (size_t) b * 32))[k];
+            stage(v4, t, b);
+        }
     }
     __syncthreads();
     if (!active) return;
+    // Pin the raw scales here: without this the compiler converts them inside the load branch,
+    // which waits for the loads before the rest are issued.
+#pragma unroll
+    for (int i = 0; i < NBL; ++i)
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) asm volatile("" : "+v"(sraw[i][s]));
 
     float acc[RPW][T];
 #pragma unroll

@@ -146,7 +146,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
     // 0. this wave's down rows (raw codes and fp16 scales of stream c's columns), issued first
     const int row0 = (rb * 4 + w) * RPW;
     int4 c0[NBL][RPW], c1[NBL][RPW];
-    uint16_t sraw[NBL][RPW];
+    uint32_t sraw[NBL][RPW];         // 16-bit scales held in 32-bit registers (no packing that waits for the load)
     if (!aux) {
 #pragma unroll
         for (int i = 0; i < NBL; ++i) {
@@ -305,7 +305,7 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
 
     // every load first: weights, the residual / scale / norm inputs of xn, and the lo partials
     int4 c0[2], c1[2];
-    uint16_t sraw[2];
+    uint32_t sraw[2];                // 16-bit scales in 32-bit registers (no packing that waits for the load)
     float rr[2][T], nwv[2], nscv[T];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {

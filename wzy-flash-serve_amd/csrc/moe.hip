@@ -133,14 +133,21 @@ struct RouteLds {
 // wave wv prefetches rows wv, wv+4 of the logits (issued before anything uses them)
 template <int T, int RV>
 WZY_DEV void route_prefetch(const float* __restrict__ logits, int E, float (&p)[(T + 3) / 4][RV]) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int rr = 0; rr < (T + 3) / 4; ++rr) {
         const int t = wv + 4 * rr;
+        if (t >= T) {                                    // wave-uniform
+#pragma unroll
+            for (int i = 0; i < RV; ++i) p[rr][i] = -INFINITY;
+            continue;
+        }
+        // clamped index, unconditional load: a per-lane branch around each load would order them
 #pragma unroll
         for (int i = 0; i < RV; ++i) {
             const int idx = lane + 64 * i;
-            p[rr][i] = (t < T && idx < E) ? logits[(size_t) t * E + idx] : -INFINITY;
+            const float v = logits[(size_t) t * E + min(idx, E - 1)];
+            p[rr][i] = idx < E ? v : -INFINITY;
         }
     }
 }
@@ -304,14 +311,13 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
         float p[(T + 3) / 4][RV];
         route_prefetch<T, RV>(a.logits, a.E, p);
         // stage x quantised per 16, starting at wave 1 so that a one-row window stages on a wave that
-        // does not route
-        for (int i = (tid + 192) & 255; i < T * nc; i += 256) {
-            const int t = i / nc, c = i - t * nc;
+        // does not route.  The first item is loaded in straight-line code (a loop header would wait
+        // for the logits before requesting x); only windows of more than 256 blocks loop.
+        auto stage16 = [&](const float4 (&f4)[8], int i) {
             float v[32];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const float4 f = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
-                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+                v[4 * k] = f4[k].x; v[4 * k + 1] = f4[k].y; v[4 * k + 2] = f4[k].z; v[4 * k + 3] = f4[k].w;
             }
             int4 qa, qb;
             float da, db;
@@ -319,8 +325,50 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             s_qa[i] = qa;
             s_qb[i] = qb;
             ((float2*) s_sc)[i] = make_float2(da, db);
+        };
+        if (((__builtin_amdgcn_readfirstlane(tid) + 192) & 255) < T * nc) {   // wave-uniform: a wave with no item skips
+            const int i = (tid + 192) & 255;
+            const int ic = min(i, T * nc - 1);
+            const int t = ic / nc, c = ic - t * nc;
+            float4 f4[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) f4[k] = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
+            if (i < T * nc) stage16(f4, i);
+        }
+        if (T > 1) {
+            for (int i = ((tid + 192) & 255) + 256; i < T * nc; i += 256) {
+                const int t = i / nc, c = i - t * nc;
+                float4 f4[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) f4[k] = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
+                stage16(f4, i);
+            }
         }
         route_compute<T, RV>(p, a.E, K, r);
+        const int tiles = F / 16;
+        const int g = bid / tiles, jt = bid - g * tiles;
+        if (g >= r.n_groups) return;                     // workgroup-uniform (workgroup 0 has g = 0)
+        const int e = __builtin_amdgcn_readfirstlane(r.gexp[g]), cnt = r.gcnt[g];
+        const MoeOffsets o = moe_offsets(D, F);
+        const uint8_t* rec = a.experts + (size_t) e * o.rec;
+        const int j0 = jt * 16 + 4 * w;
+        float acc[8][T];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
+        // D <= 2048: one 32-column chunk per lane (clamped, loads unconditional)
+        const int c = min(lane, nc - 1);
+        int4 code[8];
+        uint32_t sc2[8];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int row = (rr < 4) ? (j0 + rr) : (F + j0 + rr - 4);
+            code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
+            sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+        }
+        const float sc_gate = ((const float*) (rec + o.tail))[0];
+        const float sc_up = ((const float*) (rec + o.tail))[1];
         if (bid == 0) {                                  // publish the routing for moe_down
             const int n_ent = T * K;
             for (int i = tid; i < n_ent; i += blockDim.x) {
@@ -334,30 +382,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             }
             if (tid == 0) *a.n_groups = r.n_groups;
         }
-        const int tiles = F / 16;
-        const int g = bid / tiles, jt = bid - g * tiles;
-        if (g >= r.n_groups) return;                     // workgroup-uniform
-        const int e = r.gexp[g], cnt = r.gcnt[g];
-        const MoeOffsets o = moe_offsets(D, F);
-        const uint8_t* rec = a.experts + (size_t) e * o.rec;
-        const int j0 = jt * 16 + 4 * w;
-        float acc[8][T];
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-#pragma unroll
-            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
-        float sc_gate = 0.f, sc_up = 0.f;
-        for (int c = lane; c < nc; c += 64) {
-            int4 code[8];
-            uint32_t sc2[8];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int row = (rr < 4) ? (j0 + rr) : (F + j0 + rr - 4);
-                code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
-                sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
-            }
-            sc_gate = ((const float*) (rec + o.tail))[0];
-            sc_up = ((const float*) (rec + o.tail))[1];
+        if (lane < nc) {
 #pragma unroll
             for (int rr = 0; rr < 8; ++rr) {
                 const int4 wa = e2m1_sub16((uint32_t) code[rr].x, (uint32_t) code[rr].y);
@@ -373,8 +398,6 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
                 }
             }
         }
-        sc_gate = __shfl(sc_gate, 0, 64);
-        sc_up = __shfl(sc_up, 0, 64);
 #pragma unroll
         for (int m = 0; m < T; ++m) {
             if (m < cnt) {
@@ -404,7 +427,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
     // shared expert: rows j in [32*sb, 32*sb + 32), wave w owns j = 32*sb + 8w .. +7 (two halves of 4)
     const int sb = bid - a.n_routed_wg;
     int4 c0[2][8], c1[2][8];
-    uint16_t sraw[2][8];
+    uint32_t sraw[2][8];             // 16-bit scales in 32-bit registers (no packing that waits for the load)
     const int bl = min(lane, nc - 1);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -511,22 +534,67 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     int4* s_sha = (int4*) (s_as + (size_t) n_ent * (F / 16));
     int4* s_shb = s_sha + (size_t) T * nchunk;
     float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
-    for (int i = tid; i < n_ent; i += blockDim.x) {
+    // Item `tid` of every table and staging copy is loaded (clamped index, no branch) before the
+    // first LDS write: a stride loop per table would wait for one table's loads before requesting
+    // the next.  Only copies of more than 256 items loop for the rest.
+    const int n_aq = n_ent * nchunk, n_as4 = n_ent * (F / 16) / 4, n_sh = T * nchunk;
+    {
+        const int ie = min(tid, n_ent - 1);
+        const int gexp = a.grp_exp[ie], gcnt = a.grp_cnt[ie];
+        int gmem[WZY_MAX_W];
+#pragma unroll
+        for (int m = 0; m < WZY_MAX_W; ++m) gmem[m] = a.grp_mem[ie * WZY_MAX_W + m];
+        const float wt = a.wts[ie], sgv = a.sg[min(tid, T - 1)];
+        int4 xa, xb, ha, hb;
+        float4 xs4;
+        float hs;
+        if (STAGE) {
+            const int4* xp = (const int4*) (a.aq16 + (size_t) min(tid, n_aq - 1) * 32);
+            xa = xp[0];
+            xb = xp[1];
+            xs4 = ((const float4*) a.as16)[min(tid, n_as4 - 1)];
+            const int ih = min(tid, n_sh - 1);
+            const int4* hp = (const int4*) (a.shq32 + (size_t) ih * 32);
+            ha = hp[0];
+            hb = hp[1];
+            hs = a.shs32[ih];
+        }
+        if (tid < n_ent) {
+            s_gexp[tid] = gexp;
+            s_gcnt[tid] = gcnt;
+#pragma unroll
+            for (int m = 0; m < WZY_MAX_W; ++m) s_gmem[tid][m] = gmem[m];
+            s_wts[tid] = wt;
+        }
+        if (tid < T) s_sg[tid] = sgv;
+        if (STAGE) {
+            if (tid < n_aq) {
+                s_aqa[tid] = xa;
+                s_aqb[tid] = xb;
+            }
+            if (tid < n_as4) ((float4*) s_as)[tid] = xs4;
+            if (tid < n_sh) {
+                s_sha[tid] = ha;
+                s_shb[tid] = hb;
+                s_shs[tid] = hs;
+            }
+        }
+    }
+    for (int i = tid + 256; i < n_ent; i += 256) {
         s_gexp[i] = a.grp_exp[i];
         s_gcnt[i] = a.grp_cnt[i];
 #pragma unroll
         for (int m = 0; m < WZY_MAX_W; ++m) s_gmem[i][m] = a.grp_mem[i * WZY_MAX_W + m];
         s_wts[i] = a.wts[i];
     }
-    if (tid < T) s_sg[tid] = a.sg[tid];
     if (STAGE) {
-        for (int i = tid; i < n_ent * nchunk; i += 256) {
+        for (int i = tid + 256; i < n_aq; i += 256) {
             const int4* xp = (const int4*) (a.aq16 + (size_t) i * 32);
             s_aqa[i] = xp[0];
             s_aqb[i] = xp[1];
         }
-        for (int i = tid; i < n_ent * (F / 16) / 4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
-        for (int i = tid; i < T * nchunk; i += 256) {
+        for (int i = tid + 256; i < n_as4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
+        for (int i = tid + 256; i < n_sh; i += 256) {
             const int4* xp = (const int4*) (a.shq32 + (size_t) i * 32);
             s_sha[i] = xp[0];
             s_shb[i] = xp[1];

@@ -90,11 +90,16 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
         const int b = tt + 256 * (j0 + q);
         return ((j0 + q) < j1 && b < nb) ? (b < n_bid ? B : n_kv - n_bid * B) : 0;
     };
+    // every score load is issued before the first key is formed (clamped index, no branch around
+    // a load, so no load waits for an earlier one)
+    float sv[TK_MAXJ];
+#pragma unroll
+    for (int q = 0; q < TK_MAXJ; ++q) sv[q] = sc[min(tt + 256 * (j0 + q), nb - 1)];
     uint32_t key[TK_MAXJ];
 #pragma unroll
     for (int q = 0; q < TK_MAXJ; ++q) {
         const int b = tt + 256 * (j0 + q);
-        key[q] = ((j0 + q) < j1 && b < nb) ? order_key(sc[b]) : 0u;
+        key[q] = ((j0 + q) < j1 && b < nb) ? order_key(sv[q]) : 0u;
     }
 
     uint32_t prefix = 0;
