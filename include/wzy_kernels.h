@@ -203,6 +203,12 @@ int wzy_qsa_prepare(const wzy_qsa_dims* dims, const int* pos, float* qg, float* 
 int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const uint16_t* idx_pooled, const float* idx_dead,
                    const float* q_idx, float* scores, int max_b, int* sel_ids, int* sel_cnt, int T, void* stream);
 
+/* Exact top-idx_topk cell selection alone, over caller-supplied block scores [T x max_b] (row t's
+ * context is pos[0] + t + 1 cells; its blocks 0 .. n_kv/idx_blk hold the scores): the second half
+ * of wzy_qsa_select.  Replaces qsa_block_topk_multi (src/wzy_qsa_256k.cuh:266-403). */
+int wzy_qsa_topk(const wzy_qsa_dims* dims, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
+                 int T, void* stream);
+
 /* GQA sparse attention over the selected cells: out [T x qh*hd] = softmax(q . k / 16) . v * sigmoid(gate).
  * Replaces qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532). */
 size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T);

@@ -305,6 +305,61 @@ def test_qsa_select(wz, orc, gpu, ctx, pos, T, topk, zero_q):
         assert len(set(gsel[t, :width].tolist())) == width and gsel[t, :width].max() < n_kv
 
 
+def topk_scores(kind, nb, rng):
+    """Block scores that stress the threshold search: ties, a narrow cluster, a huge range, specials."""
+    if kind == "gauss":
+        return rng.normal(0, 2, nb).astype(np.float32)
+    if kind == "levels":                                 # few values: large tied sets at the threshold
+        return rng.integers(0, 4, nb).astype(np.float32)
+    if kind == "relu":                                   # indexer-like: non-negative, many exact zeros
+        return np.maximum(rng.normal(0, 1, (nb, 4)), 0).sum(1).astype(np.float32)
+    if kind == "wide":                                   # keys spread over the whole 32-bit range
+        return (np.sign(rng.normal(size=nb)) * np.exp(rng.uniform(-80, 80, nb))).astype(np.float32)
+    if kind == "ulps":                                   # a cluster 1 ulp apart: single-key bins
+        return (np.float32(1.0) + rng.permutation(nb).astype(np.float32) * np.float32(2.0 ** -23)).astype(np.float32)
+    if kind == "heavy_tie":                              # one value held by thousands of blocks at the threshold
+        s = rng.normal(0, 1, nb).astype(np.float32)
+        s[rng.choice(nb, nb // 2, replace=False)] = np.float32(0.25)
+        return s
+    if kind == "specials":
+        s = rng.normal(0, 1, nb).astype(np.float32)
+        idx = rng.choice(nb, 40, replace=False)
+        s[idx[:10]] = np.nan
+        s[idx[10:20]] = np.inf
+        s[idx[20:30]] = -np.inf
+        s[idx[30:35]] = -0.0
+        s[idx[35:]] = 0.0
+        return s
+    if kind == "equal":
+        return np.full(nb, 3.5, np.float32)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["gauss", "levels", "relu", "wide", "ulps", "heavy_tie", "specials", "equal"])
+@pytest.mark.parametrize("ctx,pos,T,topk", [(33400, 32768, 1, 2048), (4096, 3001, 3, 256), (262144, 150001, 2, 2048)])
+def test_qsa_topk_score_patterns(wz, orc, gpu, kind, ctx, pos, T, topk):
+    print("case qsa_topk kind=%s ctx=%d pos=%d T=%d topk=%d" % (kind, ctx, pos, T, topk), flush=True)
+    dm = qsa_dims(ctx, topk)
+    blk = dm.idx_blk
+    max_b = ctx // blk + 2
+    rng = np.random.default_rng(pos + T + len(kind))
+    scores = np.zeros((T, max_b), np.float32)
+    for t in range(T):
+        nb = (pos + t + 1) // blk + 1
+        scores[t, :nb] = topk_scores(kind, nb, rng)
+    d_sc, d_pos = dev(scores), dev(np.array([pos], np.int32))
+    sel, cnt = DA((T, topk), np.int32, zero=True), DA(T, np.int32, zero=True)
+    assert wz.wzy_qsa_topk(C.byref(dm), d_pos.ptr, d_sc.ptr, max_b, sel.ptr, cnt.ptr, T, None) == 0
+    wz.wzy_device_sync()
+    gsel, gcnt = sel.numpy(), cnt.numpy()
+    for t in range(T):
+        n_kv = pos + t + 1
+        osel = np.empty(topk, np.int32)
+        n = orc.orc_topk_select(ptr(np.ascontiguousarray(scores[t])), n_kv, blk, topk, ptr(osel))
+        assert gcnt[t] == n
+        assert (gsel[t, :n] == osel[:n]).all(), "row %d: selection differs" % t
+
+
 @pytest.mark.parametrize("qh,kvh,pos,T,topk", [(4, 2, 700, 3, 64), (24, 2, 3000, 2, 2048), (24, 2, 100, 1, 2048),
                                                (8, 1, 300, 4, 256)])
 def test_qsa_attend(wz, orc, gpu, qh, kvh, pos, T, topk):

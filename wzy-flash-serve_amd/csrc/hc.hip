@@ -13,7 +13,7 @@
 //            partials inj_part[t][c][o] = inj_w[o, c*D : (c+1)*D] . xn_c.
 //            Each workgroup moves one stream's activations (3 x D floats), not all four.
 //   hc_post: lo = silu(((p0 + p1) + (p2 + p3)) / HC) from the four partials, quantised per 32 once
-//            per workgroup into LDS; mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)).
+//            per workgroup into LDS (two values per thread); mixed[d] = 0.25 * sum_c xn[c][d] * sigmoid(up[c*D+d] . quant32(lo)).
 //            Workgroup 0 also writes lo and the summed inj.
 // Every global load a row needs is issued before any of them is used (indices clamped instead of
 // branching, fp16 scales converted afterwards).
@@ -28,28 +28,6 @@ using namespace wzy;
 namespace {
 
 constexpr int HC4 = 4;            // stream count of the hyper-connection
-
-// Per-32 int8 quantisation (reference per-32 rule: d = amax/127, q = rint(x * 127/amax)).
-WZY_DEV void quant32_vals(const float (&v)[32], int4& q0, int4& q1, float& d) {
-    float am = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(v[i]));
-    d = am / 127.0f;
-    const float inv = d > 0.f ? 127.0f / am : 0.f;
-    int w[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t pk = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int q = max(-127, min(127, rn_int(v[4 * k + j] * inv)));
-            pk |= (uint32_t) (q & 0xFF) << (8 * j);
-        }
-        w[k] = (int) pk;
-    }
-    q0 = make_int4(w[0], w[1], w[2], w[3]);
-    q1 = make_int4(w[4], w[5], w[6], w[7]);
-}
 
 // N consecutive fp32 values (N in {1, 2, 4, 8, 16}; p aligned to 4*N bytes)
 template <int N>
@@ -321,44 +299,47 @@ __global__ void __launch_bounds__(256) hc_post_kernel(HcPostArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) nscv[t] = a.nsc[t * HC4 + c];
-    const bool stager = tid < T * nb;
-    const int lt = min(tid / nb, T - 1), lbb = tid % nb;
-    float v[32];
-    if (stager) {                            // issued after every other load of the wave
-        float4 pv[HC4][8];
+    // inject partials of (row t, output o) for thread 256 - T*HC + t*HC + o, loaded by every thread
+    // (clamped) so that workgroup 0 does not wait for them after its other loads
+    float ipv[HC4];
+    {
+        const int j = max(0, tid - (256 - T * HC4)), t = j / HC4, o = j % HC4;
+        const float* ip = a.inj_part + (size_t) t * HC4 * HC4 + o;
 #pragma unroll
-        for (int s = 0; s < HC4; ++s)
+        for (int s = 0; s < HC4; ++s) ipv[s] = a.inj ? ip[s * HC4] : 0.f;
+    }
+    // lo partials: thread tid owns values 2*tid and 2*tid+1 of every row (16 threads per 32-block),
+    // so the silu and the requantisation are spread over the whole workgroup
+    const bool lo_thr = 2 * tid < L;
+    const int lj = min(2 * tid, L - 2);
+    float2 pv[T][HC4];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                pv[s][k] = *(const float4*) (a.lo_part + ((size_t) lt * HC4 + s) * L + 32 * lbb + 4 * k);
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 p0 = pv[0][k], p1 = pv[1][k], p2 = pv[2][k], p3 = pv[3][k];
-            const float4 sum = make_float4((p0.x + p1.x) + (p2.x + p3.x), (p0.y + p1.y) + (p2.y + p3.y),
-                                           (p0.z + p1.z) + (p2.z + p3.z), (p0.w + p1.w) + (p2.w + p3.w));
-            const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+        for (int s = 0; s < HC4; ++s) pv[t][s] = *(const float2*) (a.lo_part + ((size_t) t * HC4 + s) * L + lj);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float x = s4[j] / (float) HC4;
-                v[4 * k + j] = x / (1.0f + __expf(-x));
-            }
+    for (int t = 0; t < T; ++t) {
+        float v[2];
+        const float p0[2] = {pv[t][0].x, pv[t][0].y}, p1[2] = {pv[t][1].x, pv[t][1].y};
+        const float p2[2] = {pv[t][2].x, pv[t][2].y}, p3[2] = {pv[t][3].x, pv[t][3].y};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float x = ((p0[j] + p1[j]) + (p2[j] + p3[j])) / (float) HC4;
+            v[j] = x / (1.0f + __expf(-x));
         }
-        int4 q0, q1;
-        float xs;
-        quant32_vals(v, q0, q1, xs);
-        s_lq[lt][2 * lbb] = q0;
-        s_lq[lt][2 * lbb + 1] = q1;
-        s_ls[lt][lbb] = xs;
-        if (blockIdx.x == 0 && a.lo) {
-            float* lo = a.lo + (size_t) lt * L + 32 * lbb;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) ((float4*) lo)[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        const float am = group_max<16>(fmaxf(fabsf(v[0]), fabsf(v[1])));
+        const float dq = am / 127.0f;
+        const float inv = dq > 0.f ? 127.0f / am : 0.f;
+        const int q0 = max(-127, min(127, rn_int(v[0] * inv))), q1 = max(-127, min(127, rn_int(v[1] * inv)));
+        if (lo_thr) {
+            *(uint16_t*) ((unsigned char*) &s_lq[t][0] + 2 * tid) = (uint16_t) ((q0 & 0xFF) | ((q1 & 0xFF) << 8));
+            if ((tid & 15) == 0) s_ls[t][tid >> 4] = dq;
+            if (blockIdx.x == 0 && a.lo) *(float2*) (a.lo + (size_t) t * L + 2 * tid) = make_float2(v[0], v[1]);
         }
     }
     if (blockIdx.x == 0 && a.inj && tid >= 256 - T * HC4) {   // summed inject of row t, output o
         const int j = tid - (256 - T * HC4), t = j / HC4, o = j % HC4;
-        const float* ip = a.inj_part + (size_t) t * HC4 * HC4 + o;
-        a.inj[t * HC4 + o] = (ip[0] + ip[HC4]) + (ip[2 * HC4] + ip[3 * HC4]);
+        a.inj[t * HC4 + o] = (ipv[0] + ipv[1]) + (ipv[2] + ipv[3]);
     }
     __syncthreads();
 #pragma unroll

@@ -319,6 +319,13 @@ extern "C" int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const ui
     return launch_qsa_topk(s.dm, pos, scores, max_b, sel_ids, sel_cnt, T, st);
 }
 
+extern "C" int wzy_qsa_topk(const wzy_qsa_dims* dims, const int* pos, const float* scores, int max_b, int* sel_ids,
+                            int* sel_cnt, int T, void* stream) {
+    WZY_REQUIRE(dims && pos && scores && sel_ids && sel_cnt, "wzy_qsa_topk: null pointer");
+    WZY_REQUIRE(max_b >= dims->ctx_max / dims->idx_blk + 1, "wzy_qsa_topk: max_b too small");
+    return launch_qsa_topk(dims_of(dims), pos, scores, max_b, sel_ids, sel_cnt, T, as_stream(stream));
+}
+
 extern "C" size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T) {
     const QsaDims d = dims_of(dims);
     const size_t pf = qsa_attn_part_floats(d, T);

@@ -1,10 +1,10 @@
 // qsa_attn.hip -- QSA cell selection and sparse attention for gfx950.
 //
 //  qsa_topk   exact top-`topk` cells of one row, one 1024-thread workgroup: the block scores are
-//             loaded once into registers as order-preserving keys, a 4 x 8-bit radix select finds
-//             the threshold key (per-wave LDS histograms per pass, digit found by one wave),
-//             then every block above the threshold is taken whole and blocks at the threshold are
-//             filled in the reference's tie order.  The reference walks the blocks with 256 threads,
+//             loaded once into registers as order-preserving keys, 2048-bin histograms over the
+//             keys' own range (narrowed pass by pass) and a final ranking of the few blocks left
+//             find the threshold key, then every block above the threshold is taken whole and
+//             blocks at the threshold are filled in the reference's tie order.  The reference walks the blocks with 256 threads,
 //             thread t owning blocks t, t+256, ... and emitting them thread-major; here thread
 //             4t+s owns the s-th quarter of thread t's blocks, so a scan in thread order reproduces
 //             that order exactly.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
@@ -36,40 +36,81 @@ WZY_DEV uint32_t order_key(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Two inclusive prefix sums at once over the NW*64 threads in thread order (one barrier pair).
+// Inclusive prefix sum over the 64 lanes in lane order, DPP only: shifts by 1, 2, 4, 8 inside each
+// row of 16, then lane 15 of rows 0 / 2 into rows 1 / 3 and lane 31 into rows 2 and 3.  Lanes a
+// shift would read from outside the row (or rows outside the mask) add the `old` operand, 0.
+WZY_DEV int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_ROW_BCAST15, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_ROW_BCAST31, 0xC, 0xF, false);
+    return v;
+}
+
+// Two inclusive prefix sums at once over the NW*64 threads in thread order (one barrier).  The
+// caller separates consecutive calls (and later writes of s_x / s_y) by a barrier.
 template <int NW>
 WZY_DEV void block_scan_incl2(int& x, int& y, int* s_x, int* s_y) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int a = __shfl_up(x, o, 64), b = __shfl_up(y, o, 64);
-        if (lane >= o) { x += a; y += b; }
-    }
+    x = wave_incl_scan(x);
+    y = wave_incl_scan(y);
     if (lane == 63) { s_x[w] = x; s_y[w] = y; }
     __syncthreads();
     int bx = 0, by = 0;
 #pragma unroll
     for (int i = 0; i < NW; ++i)
         if (i < w) { bx += s_x[i]; by += s_y[i]; }
-    __syncthreads();
     x += bx;
     y += by;
 }
 
+WZY_DEV uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, (uint32_t) dpp_i<DPP_XOR1>((int) v));
+    v = min(v, (uint32_t) dpp_i<DPP_XOR2>((int) v));
+    v = min(v, (uint32_t) dpp_i<DPP_HALF_MIRROR>((int) v));
+    v = min(v, (uint32_t) dpp_i<DPP_MIRROR>((int) v));
+    v = min(v, (uint32_t) swz_i<SWZ_XOR16>((int) v));
+    return min((uint32_t) __builtin_amdgcn_readlane((int) v, 0), (uint32_t) __builtin_amdgcn_readlane((int) v, 32));
+}
+WZY_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t) dpp_i<DPP_XOR1>((int) v));
+    v = max(v, (uint32_t) dpp_i<DPP_XOR2>((int) v));
+    v = max(v, (uint32_t) dpp_i<DPP_HALF_MIRROR>((int) v));
+    v = max(v, (uint32_t) dpp_i<DPP_MIRROR>((int) v));
+    v = max(v, (uint32_t) swz_i<SWZ_XOR16>((int) v));
+    return max((uint32_t) __builtin_amdgcn_readlane((int) v, 0), (uint32_t) __builtin_amdgcn_readlane((int) v, 32));
+}
+
+constexpr int TK_NBIN = 2 * TK_THREADS;   // histogram bins per pass (two per thread in the scan)
+constexpr int TK_LOG_NBIN = 11;
+constexpr int TK_CAND = 256;               // threshold-bin weight at which the pass loop hands over to ranking
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// exact top-k cell selection, one workgroup per row; TK_MAXJ = blocks held per thread
+// exact top-k cell selection, one workgroup per row; TK_MAXJ = blocks held per thread.
+// Threshold search: the order keys of the row's blocks span [kmin, kmax]; a pass histograms the
+// keys of a window [lo, lo + TK_NBIN << shift) into TK_NBIN bins of 2^shift keys (block weights =
+// cells), and one scan from the top bin down finds the bin holding the width-th cell.  The window
+// narrows to that bin; once its weight is at most TK_CAND (or a bin is a single key) its few blocks
+// are ranked against each other directly.  The threshold is the key value thr with
+// weight(key > thr) < width <= weight(key >= thr), the same value a digit-by-digit radix select finds.
 // ---------------------------------------------------------------------------------------------
 template <int TK_MAXJ>
 __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
                                                               const float* __restrict__ scores, int max_b,
                                                               int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
-    __shared__ int hist[TK_THREADS / 64][256];      // one histogram per wave (no cross-wave atomic contention)
-    __shared__ int s_w[TK_THREADS / 64];
-    __shared__ int s_c[TK_THREADS / 64];
-    __shared__ int s_digit, s_above;
-    const int p = threadIdx.x, row = blockIdx.x;
+    constexpr int NW = TK_THREADS / 64;
+    __shared__ int hist[TK_NBIN];
+    __shared__ uint32_t s_ck[TK_CAND];
+    __shared__ int s_cw[TK_CAND];
+    __shared__ int s_w[NW], s_c[NW];
+    __shared__ uint32_t s_mn[NW], s_mx[NW];
+    __shared__ int s_bin, s_above, s_cnt, s_ncand;
+    __shared__ uint32_t s_thr;
+    const int p = threadIdx.x, row = blockIdx.x, lane = p & 63, w = p >> 6;
     const int n_kv = *pos_dev + row + 1;
     const int K = dm.topk, B = dm.iblk;
     const int width = min(n_kv, K);
@@ -95,66 +136,86 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
     float sv[TK_MAXJ];
 #pragma unroll
     for (int q = 0; q < TK_MAXJ; ++q) sv[q] = sc[min(tt + 256 * (j0 + q), nb - 1)];
+    for (int i = p; i < TK_NBIN; i += TK_THREADS) hist[i] = 0;
+    if (p == 0) s_ncand = 0;
     uint32_t key[TK_MAXJ];
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
 #pragma unroll
     for (int q = 0; q < TK_MAXJ; ++q) {
-        const int b = tt + 256 * (j0 + q);
-        key[q] = ((j0 + q) < j1 && b < nb) ? order_key(sv[q]) : 0u;
+        key[q] = order_key(sv[q]);
+        if (wgt(q) > 0) { mn = min(mn, key[q]); mx = max(mx, key[q]); }
     }
-
-    uint32_t prefix = 0;
-    int above = 0;
-    for (int i = p; i < (TK_THREADS / 64) * 256; i += TK_THREADS) (&hist[0][0])[i] = 0;
+    mn = wave_min_u32(mn);
+    mx = wave_max_u32(mx);
+    if (lane == 0) { s_mn[w] = mn; s_mx[w] = mx; }
     __syncthreads();
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        const uint32_t hi_mask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
 #pragma unroll
-        for (int q = 0; q < TK_MAXJ; ++q)
-            if (wgt(q) > 0 && (key[q] & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[p >> 6][(key[q] >> shift) & 255u], wgt(q));
+    for (int i = 0; i < NW; ++i) { mn = min(mn, s_mn[i]); mx = max(mx, s_mx[i]); }
+
+    // window passes: at most three (shift 21 -> 10 -> 0)
+    uint32_t lo = mn;
+    const uint32_t range = mx - mn;
+    int shift = range ? max(0, 32 - __builtin_clz(range) - TK_LOG_NBIN) : 0;
+    int above = 0, cnt = 0;
+    uint32_t thr = mn;                               // one key value in the whole row: no pass needed
+    bool ranked = false;
+    while (range != 0) {
+#pragma unroll
+        for (int q = 0; q < TK_MAXJ; ++q) {
+            const uint32_t d = key[q] - lo;
+            if (wgt(q) > 0 && key[q] >= lo && (d >> shift) < (uint32_t) TK_NBIN) atomicAdd(&hist[d >> shift], wgt(q));
+        }
         __syncthreads();
-        // wave 0 picks the digit: lane l holds digits 255-4l .. 252-4l (highest first); the
-        // threshold digit is the highest one at which the weight at or above it reaches the width
-        if (p < 64) {
-            const int l = p;
-            int h[4];
+        // thread p owns bins TK_NBIN-1-2p (h1) and TK_NBIN-2-2p (h0): thread order = descending keys
+        const int b1 = TK_NBIN - 1 - 2 * p, b0 = b1 - 1;
+        const int h1 = hist[b1], h0 = hist[b0];
+        hist[b1] = 0;                                // cleared for the next pass
+        hist[b0] = 0;
+        int incl = h1 + h0, dummy = 0;
+        block_scan_incl2<NW>(incl, dummy, s_w, s_c);
+        const int before = above + incl - (h1 + h0);
+        if (before < width && before + h1 >= width) { s_bin = b1; s_above = before; s_cnt = h1; }
+        if (before + h1 < width && before + h1 + h0 >= width) { s_bin = b0; s_above = before + h1; s_cnt = h0; }
+        __syncthreads();
+        lo += (uint32_t) __builtin_amdgcn_readfirstlane(s_bin) << shift;
+        above = __builtin_amdgcn_readfirstlane(s_above);
+        cnt = __builtin_amdgcn_readfirstlane(s_cnt);
+        if (shift == 0) { thr = lo; break; }         // the bin is one key value
+        if (cnt <= TK_CAND) { ranked = true; break; }
+        shift = max(0, shift - TK_LOG_NBIN);
+    }
+    if (ranked) {
+        // the threshold bin [lo, lo + 2^shift) holds at most TK_CAND cells, so at most TK_CAND blocks:
+        // gather them, and each ranks itself against the others
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int sum = 0;
-#pragma unroll
-                for (int wv = 0; wv < TK_THREADS / 64; ++wv) {
-                    sum += hist[wv][255 - 4 * l - j];
-                    hist[wv][255 - 4 * l - j] = 0;   // cleared for the next pass
-                }
-                h[j] = sum;
-            }
-            const int s4 = h[0] + h[1] + h[2] + h[3];
-            int incl = s4;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(incl, o, 64);
-                if (l >= o) incl += y;
-            }
-            int cum = above + incl - s4;             // weight of digits above this lane's first
-            int jl = -1, base_above = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (jl < 0 && cum + h[j] >= width) { jl = j; base_above = cum; }
-                cum += h[j];
-            }
-            const unsigned long long m = __ballot(jl >= 0);
-            const int lstar = m ? __ffsll((long long) m) - 1 : 63;
-            if (l == lstar) {
-                const int js = jl >= 0 ? jl : 3;
-                s_digit = 255 - 4 * l - js;
-                s_above = jl >= 0 ? base_above : cum - h[3];
+        for (int q = 0; q < TK_MAXJ; ++q) {
+            if (wgt(q) > 0 && key[q] >= lo && ((key[q] - lo) >> shift) == 0u) {
+                const int slot = atomicAdd(&s_ncand, 1);
+                s_ck[slot] = key[q];
+                s_cw[slot] = wgt(q);
             }
         }
         __syncthreads();
-        prefix |= (uint32_t) s_digit << shift;
+        const int nc = s_ncand;
+        if (p < nc) {
+            const uint32_t k = s_ck[p];
+            int gtw = 0, eqw = 0;
+            for (int j = 0; j < nc; ++j) {
+                const uint32_t kj = s_ck[j];
+                const int wj = s_cw[j];
+                gtw += kj > k ? wj : 0;
+                eqw += kj == k ? wj : 0;
+            }
+            if (above + gtw < width && above + gtw + eqw >= width) {   // every such block holds the same key
+                s_thr = k;
+                s_above = above + gtw;
+            }
+        }
+        __syncthreads();
+        thr = s_thr;
         above = s_above;
     }
 
-    const uint32_t thr = prefix;
     const int eq_budget = width - above;
     int gt = 0, eq = 0;
 #pragma unroll
@@ -167,7 +228,7 @@ __global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const 
     // one dual scan: the threshold-tied cells a thread may take are what is left of the budget
     // after the threads before it, and its output offset is gt_excl + min(eq_excl, eq_budget)
     int gt_incl = gt, eq_incl = eq;
-    block_scan_incl2<TK_THREADS / 64>(gt_incl, eq_incl, s_w, s_c);
+    block_scan_incl2<NW>(gt_incl, eq_incl, s_w, s_c);
     const int eq_excl = eq_incl - eq;
     const int my_eq = max(0, min(eq, eq_budget - eq_excl));
     int wpos = (gt_incl - gt) + min(eq_excl, eq_budget);

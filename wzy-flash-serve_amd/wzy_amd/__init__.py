@@ -121,6 +121,7 @@ _SIGS = {
     "wzy_gdn_recurrence": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32, P, P], True),
     "wzy_qsa_prepare": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, P], True),
     "wzy_qsa_select": (I32, [C.POINTER(QsaDims), P, P, P, P, P, I32, P, P, I32, P], True),
+    "wzy_qsa_topk": (I32, [C.POINTER(QsaDims), P, P, I32, P, P, I32, P], True),
     "wzy_qsa_attend_workspace_bytes": (SZ, [C.POINTER(QsaDims), I32], False),
     "wzy_qsa_attend": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, SZ, I32, P], True),
     "wzy_last_error": (C.c_char_p, [], False),
