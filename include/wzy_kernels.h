@@ -64,6 +64,23 @@ int wzy_gemv_q8(const int8_t* codes, const uint16_t* scales, const int8_t* xq, c
 int wzy_gemv_bf16(const uint16_t* W, const float* x, float* y, int rows, int cols, int T,
                   int y_stride, void* stream);
 
+/* One projection group in one launch: segment i computes y_i[t*y_stride_i + r] = W_i[r,:] . x[t,:]
+ * over the same fp32 activations x [T x cols], with Q8_0 weights (kind WZY_GEMV_Q8: int8 codes
+ * [rows x cols] and fp16 scale bits [rows x cols/32]; x quantised per 32 exactly as wzy_quant_act
+ * does) or bf16 weights (kind WZY_GEMV_BF16, s = NULL).  1 <= n_segs <= 8, cols % 32 == 0,
+ * 32 <= cols <= 8192, 1 <= T <= WZY_MAX_W; y_stride == 0 means rows.
+ * Replaces a group's quant_act_multi + launch_gemm_q8p / launch_gemm_bf16 sequence
+ * (src/wzy_stage_v2.cuh:609-611, 630-633, 449-460). */
+#define WZY_GEMV_Q8 0
+#define WZY_GEMV_BF16 1
+typedef struct {
+    const void* w;
+    const uint16_t* s;
+    float* y;
+    int rows, kind, y_stride;
+} wzy_gemv_seg;
+int wzy_gemv_segs(const wzy_gemv_seg* segs, int n_segs, const float* x, int cols, int T, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * NVFP4 mixture of experts (decode)
  * ------------------------------------------------------------------------------------------- */

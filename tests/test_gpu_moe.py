@@ -147,6 +147,48 @@ def test_gemv_bf16_parity(wz, orc, gpu, rows, cols, T):
     np.testing.assert_allclose(host(y), ref, rtol=1e-5, atol=2e-5 * np.abs(ref).max())
 
 
+@pytest.mark.parametrize("cols,T,kinds", [(2048, 1, "qqbb"), (2048, 1, "qqqbb"), (2048, 4, "qb"), (6144, 1, "q"),
+                                           (6144, 3, "bq"), (4096, 2, "qbq"), (8192, 1, "qb"), (8192, 8, "bq"),
+                                           (512, 8, "q"), (96, 5, "bqb"), (2048, 1, "b"), (2048, 8, "qqbb")])
+def test_gemv_segs_parity(wz, orc, gpu, cols, T, kinds):
+    """Projection groups in one launch: every segment against the oracle's Q8_0 / bf16 GEMV."""
+    print("case gemv_segs cols=%d T=%d kinds=%s" % (cols, T, kinds), flush=True)
+    rng = np.random.default_rng(cols * 10 + T)
+    x = rng.standard_normal(T * cols).astype(np.float32)
+    x[:32] = 0.0                                          # an all-zero 32-block
+    q32 = np.empty(T * cols, np.int8); s32 = np.empty(T * cols // 32, np.float32)
+    orc.orc_quant_act(ptr(x), cols, T, ptr(q32), ptr(s32), None, None)
+    segs = (wzy_amd.GemvSeg * len(kinds))()
+    keep, refs, outs = [dev(x)], [], []
+    for i, k in enumerate(kinds):
+        rows = int(rng.choice([1, 3, 33, 130, 517, 2048]))
+        stride = rows + (i % 2) * 5
+        y = DA(T * stride, np.float32, zero=True)
+        ref = np.empty(T * rows, np.float32)
+        if k == "q":
+            codes = np.empty(rows * cols, np.int8); sc = np.empty(rows * cols // 32, np.uint16)
+            wz.wzy_synth_q8(5, i, rows, cols, float(1 / np.sqrt(cols)), ptr(codes), ptr(sc))
+            orc.orc_gemv_q8(ptr(codes), ptr(sc), ptr(q32), ptr(s32), ptr(ref), rows, cols, T)
+            dw, ds = dev(codes), dev(sc.view(np.int16))
+            keep += [dw, ds]
+            segs[i] = wzy_amd.GemvSeg(dw.ptr, ds.ptr, y.ptr, rows, wzy_amd.GEMV_Q8, stride)
+        else:
+            W = np.empty(rows * cols, np.uint16)
+            wz.wzy_synth_normal_bf16(6, i, rows * cols, 0.0, 0.02, ptr(W))
+            orc.orc_gemv_bf16(ptr(W), ptr(x), ptr(ref), rows, cols, T)
+            dw = dev(W.view(np.int16))
+            keep.append(dw)
+            segs[i] = wzy_amd.GemvSeg(dw.ptr, None, y.ptr, rows, wzy_amd.GEMV_BF16, stride)
+        refs.append((ref.reshape(T, rows), rows, stride, k))
+        outs.append(y)
+    assert wz.wzy_gemv_segs(segs, len(kinds), keep[0].ptr, cols, T, None) == 0
+    wz.wzy_device_sync()
+    for (ref, rows, stride, k), y in zip(refs, outs):
+        got = host(y).reshape(T, stride)
+        np.testing.assert_allclose(got[:, :rows], ref, rtol=1e-5, atol=2e-5 * max(np.abs(ref).max(), 1e-30))
+        assert not got[:, rows:].any(), "wrote outside the segment's rows"
+
+
 def test_moe_config1_parity(wz, orc, gpu):
     """D=2048, 512 experts top-10, NFF=512, seed 0, one token."""
     D, F, E, K, T = 2048, 512, 512, 10, 1

@@ -504,10 +504,16 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
 // quantisation (for Q8_0 segments, split into the two 16-byte halves of each block), so lanes
 // read 16 consecutive bytes each (no LDS bank conflicts) and the L2 serves x once per workgroup
 // instead of once per wave.  Each wave issues its weight loads before the staging barrier.
+// Registers are kept low so that every workgroup of a launch is resident at once: Q8_0 and bf16
+// weights share one array (a Q8_0 wave holds RPW rows of 32 code bytes per 32-block, a bf16 wave
+// RPW/2 rows of 64 bytes), and x is staged by four threads per 32-column block (8 values each).
 // flags: bit 0 = the launch has Q8_0 segments, bit 1 = it has bf16 segments.
 template <int T, int NBL, int RPW>
 __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const float* __restrict__ x, int cols,
                                                             int flags) {
+    static_assert(RPW % 2 == 0, "a bf16 wave holds RPW/2 rows");
+    constexpr int RPWB = RPW / 2;
+    constexpr int NR = 2 * NBL * RPW;                 // uint4 weight registers per lane
     extern __shared__ __align__(16) unsigned char s_dyn[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + tid) >> 6);
@@ -516,15 +522,15 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
     int4* s_xq = (int4*) (s_dyn + ((flags & 2) ? (size_t) T * cols * 4 : 0));  // [T][2][nb]
     float* s_xs = (float*) ((unsigned char*) s_xq + ((flags & 1) ? (size_t) T * cols : 0));   // [T][nb]
     const GemvSeg sg = pick_seg(segs, wave);
-    const int row0 = (wave - sg.wave0) * RPW;
-    const bool active = row0 < sg.rows;
     const bool q8 = sg.kind == GEMV_Q8;
+    const int row0 = (wave - sg.wave0) * (q8 ? RPW : RPWB);
+    const bool active = row0 < sg.rows;
 
-    // 1. weights (wave-uniform branches; clamped indices; raw scales)
-    int4 c0[NBL][RPW], c1[NBL][RPW];
+    // 1. weights (wave-uniform branches; clamped indices; raw scales).  Q8_0: wr[2*(i*RPW+s)+h] =
+    //    half h of 32-block lane+64i of row row0+s.  bf16: wr[u*RPWB+s] = 8 columns 8*(lane+64u).. of
+    //    row row0+s.
+    uint4 wr[NR];
     uint32_t sraw[NBL][RPW];         // 16-bit scales held in 32-bit registers (no packing that waits for the load)
-    constexpr int NU = NBL * 4;                           // uint4 (8 bf16) per lane per row: cols/8/64
-    uint4 wv[NU][RPW];
     if (active && q8) {
         const int8_t* W = (const int8_t*) sg.w;
 #pragma unroll
@@ -533,59 +539,76 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
 #pragma unroll
             for (int s = 0; s < RPW; ++s) {
                 const int r = min(row0 + s, sg.rows - 1);
-                const int4* cp = (const int4*) (W + (size_t) r * cols + (size_t) b * 32);
-                c0[i][s] = ld_stream_i4(cp);
-                c1[i][s] = ld_stream_i4(cp + 1);
+                const uint4* cp = (const uint4*) (W + (size_t) r * cols + (size_t) b * 32);
+                wr[2 * (i * RPW + s)] = ld_stream_u4(cp);
+                wr[2 * (i * RPW + s) + 1] = ld_stream_u4(cp + 1);
                 sraw[i][s] = sg.s[(size_t) r * nb + b];
             }
         }
     } else if (active) {
         const uint16_t* W = (const uint16_t*) sg.w;
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
+        for (int u = 0; u < 4 * NBL; ++u) {
             const int j = min(lane + 64 * u, n8 - 1);
 #pragma unroll
-            for (int s = 0; s < RPW; ++s) {
+            for (int s = 0; s < RPWB; ++s) {
                 const int r = min(row0 + s, sg.rows - 1);
-                wv[u][s] = ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j);
+                wr[u * RPWB + s] = ld_stream_u4((const uint4*) (W + (size_t) r * cols) + j);
             }
         }
     }
-    // 2. stage x: thread i owns 32-column block i of the window.  The first item is loaded in
-    //    straight-line code right behind the weights (clamped: always a valid address), so both are
-    //    in flight together; a loop here would wait for the weights at its header before loading x.
-    //    Only windows with more than 256 blocks (T > 1) loop for more.
-    const int nitem = T * nb;
-    const int i0 = min(tid, nitem - 1);
-    const int t0 = i0 / nb, b0 = i0 - t0 * nb;
-    float4 xv[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) xv[k] = ((const float4*) (x + (size_t) t0 * cols + (size_t) b0 * 32))[k];
-    auto stage = [&](const float4 (&v4)[8], int t, int b) {
+    // 2. stage x: four threads per 32-column block, thread k of block b holding columns 32b+8k ..
+    //    32b+8k+7.  The first item is loaded in straight-line code right behind the weights
+    //    (clamped: always a valid address), so both are in flight together; a loop here would wait
+    //    for the weights at its header before loading x.  Only windows of more than one row loop.
+    const int nitem = T * nb * 4;
+    auto stage = [&](const float4& va, const float4& vb, int i) {
+        const int t = i / (nb * 4), r = i - t * (nb * 4), b = r >> 2, k = r & 3;
         if (flags & 2) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                s_xf[((size_t) t * 2 + 0) * n8 + 4 * b + k] = v4[2 * k];
-                s_xf[((size_t) t * 2 + 1) * n8 + 4 * b + k] = v4[2 * k + 1];
-            }
+            s_xf[((size_t) t * 2 + 0) * n8 + 4 * b + k] = va;
+            s_xf[((size_t) t * 2 + 1) * n8 + 4 * b + k] = vb;
         }
         if (flags & 1) {
-            int4 q0, q1;
-            float xs;
-            quant32_v(v4, q0, q1, xs);
-            s_xq[((size_t) t * 2 + 0) * nb + b] = q0;
-            s_xq[((size_t) t * 2 + 1) * nb + b] = q1;
-            s_xs[(size_t) t * nb + b] = xs;
+            // per-32 quantisation (d = amax/127, q = rint(x*127/amax)); the 4 threads of a block are
+            // 4 consecutive lanes, so the block max is a 4-lane DPP max
+            const float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+            float am = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) am = fmaxf(am, fabsf(v[j]));
+            am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+            am = fmaxf(am, dpp_f<DPP_XOR2>(am));
+            const float d = am / 127.0f;
+            const float inv = d > 0.f ? 127.0f / am : 0.f;
+            uint32_t pk[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                pk[j >> 2] |= (uint32_t) (max(-127, min(127, rn_int(v[j] * inv))) & 0xFF) << (8 * (j & 3));
+            int2* dst = (int2*) &s_xq[((size_t) t * 2 + (k >> 1)) * nb + b] + (k & 1);
+            *dst = make_int2((int) pk[0], (int) pk[1]);
+            if (k == 0) s_xs[(size_t) t * nb + b] = d;
         }
     };
-    if (tid < nitem) stage(xv, t0, b0);
-    if (T > 1) {
-        for (int i = tid + 256; i < nitem; i += 256) {
-            const int t = i / nb, b = i - t * nb;
-            float4 v4[8];
+    {
+        // NBL items per thread cover one row (nb*4 <= 256*NBL); nitem % 4 == 0, so a 4-lane group is
+        // all in or all out
+        float4 xa[NBL], xb[NBL];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v4[k] = ((const float4*) (x + (size_t) t * cols + (size_t) b * 32))[k];
-            stage(v4, t, b);
+        for (int k = 0; k < NBL; ++k) {
+            const int i = min(tid + 256 * k, nitem - 1);
+            const int t = i / (nb * 4), r = i - t * (nb * 4);
+            const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
+            xa[k] = xp[0];
+            xb[k] = xp[1];
+        }
+#pragma unroll
+        for (int k = 0; k < NBL; ++k)
+            if (tid + 256 * k < nitem) stage(xa[k], xb[k], tid + 256 * k);
+    }
+    if (T * nb * 4 > 256 * NBL) {
+        for (int i = tid + 256 * NBL; i < nitem; i += 256) {
+            const int t = i / (nb * 4), r = i - t * (nb * 4);
+            const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
+            stage(xp[0], xp[1], i);
         }
     }
     __syncthreads();
@@ -612,42 +635,47 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
                 const int4 x0 = s_xq[((size_t) t * 2 + 0) * nb + b], x1 = s_xq[((size_t) t * 2 + 1) * nb + b];
                 const float xs = s_xs[(size_t) t * nb + b];
 #pragma unroll
-                for (int s = 0; s < RPW; ++s)
-                    acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c1[i][s], x1) + dot16(c0[i][s], x0)),
-                                     acc[s][t]);
+                for (int s = 0; s < RPW; ++s) {
+                    const uint4 a0 = wr[2 * (i * RPW + s)], a1 = wr[2 * (i * RPW + s) + 1];
+                    const int4 c0 = make_int4((int) a0.x, (int) a0.y, (int) a0.z, (int) a0.w);
+                    const int4 c1 = make_int4((int) a1.x, (int) a1.y, (int) a1.z, (int) a1.w);
+                    acc[s][t] = fmaf(h16_to_f(sraw[i][s]) * xs, (float) (dot16(c1, x1) + dot16(c0, x0)), acc[s][t]);
+                }
             }
         }
     } else {
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
+        for (int u = 0; u < 4 * NBL; ++u) {
             const int j = lane + 64 * u;
             if (j >= n8) continue;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const float4 xa = s_xf[((size_t) t * 2 + 0) * n8 + j], xb = s_xf[((size_t) t * 2 + 1) * n8 + j];
 #pragma unroll
-                for (int s = 0; s < RPW; ++s) {
+                for (int s = 0; s < RPWB; ++s) {
+                    const uint4 wv = wr[u * RPWB + s];
                     float v = acc[s][t];
-                    v = fmaf(bf16_lo(wv[u][s].x), xa.x, v);
-                    v = fmaf(bf16_hi(wv[u][s].x), xa.y, v);
-                    v = fmaf(bf16_lo(wv[u][s].y), xa.z, v);
-                    v = fmaf(bf16_hi(wv[u][s].y), xa.w, v);
-                    v = fmaf(bf16_lo(wv[u][s].z), xb.x, v);
-                    v = fmaf(bf16_hi(wv[u][s].z), xb.y, v);
-                    v = fmaf(bf16_lo(wv[u][s].w), xb.z, v);
-                    v = fmaf(bf16_hi(wv[u][s].w), xb.w, v);
+                    v = fmaf(bf16_lo(wv.x), xa.x, v);
+                    v = fmaf(bf16_hi(wv.x), xa.y, v);
+                    v = fmaf(bf16_lo(wv.y), xa.z, v);
+                    v = fmaf(bf16_hi(wv.y), xa.w, v);
+                    v = fmaf(bf16_lo(wv.z), xb.x, v);
+                    v = fmaf(bf16_hi(wv.z), xb.y, v);
+                    v = fmaf(bf16_lo(wv.w), xb.z, v);
+                    v = fmaf(bf16_hi(wv.w), xb.w, v);
                     acc[s][t] = v;
                 }
             }
         }
     }
+    const int rpw = q8 ? RPW : RPWB;
 #pragma unroll
     for (int s = 0; s < RPW; ++s) {
         const int r = row0 + s;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float v = wave_sum(acc[s][t]);
-            if (lane == 0 && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
+            if (lane == 0 && s < rpw && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
         }
     }
 }
@@ -660,7 +688,7 @@ static void launch_segs_lds_t(const GemvSegs& segs, int waves, int nbl, const fl
         case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
         case 2: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 2, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
         case 3: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 3, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
-        default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 1>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
     }
 }
 
@@ -681,7 +709,14 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     WZY_REQUIRE(cols >= 32 && cols % 32 == 0 && cols <= 8192, "gemv_segs: cols must be a multiple of 32 in [32, 8192]");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "gemv_segs: T out of range");
     const int nbl = (cols / 32 + 63) / 64;
-    const int rpw = nbl == 1 ? 4 : (nbl <= 3 ? 2 : 1);
+    int flags = 0;
+    for (int i = 0; i < segs.n; ++i) flags |= segs.seg[i].kind == GEMV_Q8 ? 1 : 2;
+    const size_t lds = (size_t) T * cols * (((flags & 2) ? 4 : 0) + ((flags & 1) ? 1 : 0)) +
+                       ((flags & 1) ? (size_t) T * (cols / 32) * 4 : 0);
+    const bool use_lds = lds <= 48 * 1024;
+    // rows per wave: the LDS kernel holds RPW Q8_0 rows or RPW/2 bf16 rows per wave (RPW = 4 for one
+    // 32-block per lane, else 2); the other kernel RPW rows of either kind (4 / 2 / 1)
+    const int rpw = nbl == 1 ? 4 : (use_lds || nbl <= 3 ? 2 : 1);
     int waves = 0;
     for (int i = 0; i < segs.n; ++i) {
         GemvSeg& s = segs.seg[i];
@@ -689,13 +724,10 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
         WZY_REQUIRE(s.kind == GEMV_BF16 || s.s, "gemv_segs: Q8 segment %d without scales", i);
         if (s.y_stride == 0) s.y_stride = s.rows;
         s.wave0 = waves;
-        waves += (s.rows + rpw - 1) / rpw;
+        const int r = (use_lds && s.kind == GEMV_BF16) ? rpw / 2 : rpw;
+        waves += (s.rows + r - 1) / r;
     }
-    int flags = 0;
-    for (int i = 0; i < segs.n; ++i) flags |= segs.seg[i].kind == GEMV_Q8 ? 1 : 2;
-    const size_t lds = (size_t) T * cols * (((flags & 2) ? 4 : 0) + ((flags & 1) ? 1 : 0)) +
-                       ((flags & 1) ? (size_t) T * (cols / 32) * 4 : 0);
-    if (lds <= 48 * 1024) {
+    if (use_lds) {
         switch (T) {
             case 1: launch_segs_lds_t<1>(segs, waves, nbl, x, cols, flags, lds, st); break;
             case 2: launch_segs_lds_t<2>(segs, waves, nbl, x, cols, flags, lds, st); break;
@@ -723,3 +755,17 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     return WZY_OK;
 }
 }  // namespace wzy
+
+extern "C" int wzy_gemv_segs(const wzy_gemv_seg* segs, int n_segs, const float* x, int cols, int T, void* stream) {
+    WZY_REQUIRE(segs && n_segs >= 1 && n_segs <= GEMV_MAX_SEGS, "wzy_gemv_segs: 1 to %d segments required",
+                GEMV_MAX_SEGS);
+    GemvSegs g;
+    g.n = n_segs;
+    for (int i = 0; i < n_segs; ++i) {
+        const wzy_gemv_seg& a = segs[i];
+        WZY_REQUIRE(a.kind == WZY_GEMV_Q8 || a.kind == WZY_GEMV_BF16, "wzy_gemv_segs: segment %d has unknown kind %d",
+                    i, a.kind);
+        g.seg[i] = GemvSeg{a.w, a.s, a.y, a.rows, a.kind == WZY_GEMV_Q8 ? GEMV_Q8 : GEMV_BF16, a.y_stride, 0};
+    }
+    return launch_gemv_segs(g, x, cols, T, as_stream(stream));
+}

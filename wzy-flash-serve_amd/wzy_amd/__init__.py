@@ -38,6 +38,14 @@ class MoeWeights(C.Structure):
     ]
 
 
+class GemvSeg(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("y", C.c_void_p), ("rows", C.c_int), ("kind", C.c_int),
+                ("y_stride", C.c_int)]
+
+
+GEMV_Q8, GEMV_BF16 = 0, 1
+
+
 class QsaDims(C.Structure):
     """struct wzy_qsa_dims (include/wzy_kernels.h)"""
     _fields_ = [("qh", I32), ("kvh", I32), ("hd", I32), ("n_rot", I32),
@@ -122,6 +130,7 @@ _SIGS = {
     "wzy_qsa_prepare": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, P], True),
     "wzy_qsa_select": (I32, [C.POINTER(QsaDims), P, P, P, P, P, I32, P, P, I32, P], True),
     "wzy_qsa_topk": (I32, [C.POINTER(QsaDims), P, P, I32, P, P, I32, P], True),
+    "wzy_gemv_segs": (I32, [C.POINTER(GemvSeg), I32, P, I32, I32, P], True),
     "wzy_qsa_attend_workspace_bytes": (SZ, [C.POINTER(QsaDims), I32], False),
     "wzy_qsa_attend": (I32, [C.POINTER(QsaDims), P, P, P, P, P, P, P, P, P, SZ, I32, P], True),
     "wzy_last_error": (C.c_char_p, [], False),
