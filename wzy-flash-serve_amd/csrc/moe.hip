@@ -200,17 +200,37 @@ WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, fl
 #pragma unroll
     for (int i = 0; i < RV; ++i) key[i] = (lane + 64 * i < E) ? route_key(p[i] * inv, lane + 64 * i) : 0ull;
     sort_keys_desc<RV>(key);
+    uint32_t hi[RV], lo[RV];
+#pragma unroll
+    for (int i = 0; i < RV; ++i) { hi[i] = (uint32_t) (key[i] >> 32); lo[i] = (uint32_t) key[i]; }
     wsum = 0.f;
     my_id = 0;
     my_w = 0.f;
     for (int k = 0; k < K; ++k) {
-        const uint64_t top = wave_max_u64(key[0]);
-        const bool pop = key[0] == top;
+        // the largest head: a 32-bit DPP maximum of the probability words, then (only when several
+        // lanes hold that probability) of the id words among them; the winner lane is unique
+        const uint32_t m = wave_max_u32(hi[0]);
+        const bool at_m = hi[0] == m;
+        uint64_t win = __ballot(at_m);
+        if (__popcll(win) > 1) {                          // wave-uniform
+            const uint32_t m2 = wave_max_u32(at_m ? lo[0] : 0u);
+            win = __ballot(at_m && lo[0] == m2);
+        }
+        const int wl = __ffsll((long long) win) - 1;
+        const uint32_t wlo = (uint32_t) __builtin_amdgcn_readlane((int) lo[0], wl);
+        // the winner lane pops its head.  The shift is written with a mask rather than selects of
+        // neighbouring keys, which the compiler would turn into a per-lane head index that selects
+        // every key through a compare chain.
+        const uint32_t pm = 0u - (uint32_t) (lane == wl);
 #pragma unroll
-        for (int i = 0; i + 1 < RV; ++i) key[i] = pop ? key[i + 1] : key[i];
-        key[RV - 1] = pop ? 0ull : key[RV - 1];
-        const float bv = __builtin_bit_cast(float, (uint32_t) (top >> 32));
-        int bi = (int) (0xFFFFFFFFu - (uint32_t) top);
+        for (int i = 0; i + 1 < RV; ++i) {
+            hi[i] ^= (hi[i] ^ hi[i + 1]) & pm;
+            lo[i] ^= (lo[i] ^ lo[i + 1]) & pm;
+        }
+        hi[RV - 1] &= ~pm;
+        lo[RV - 1] &= ~pm;
+        const float bv = __builtin_bit_cast(float, m);
+        int bi = (int) (0xFFFFFFFFu - wlo);
         if (bi >= E || bi < 0) bi = 0;                   // non-finite logits: keep the id in range
         if (lane == k) { my_id = bi; my_w = bv; }
         wsum += bv;

@@ -66,22 +66,8 @@ WZY_DEV void block_scan_incl2(int& x, int& y, int* s_x, int* s_y) {
     y += by;
 }
 
-WZY_DEV uint32_t wave_min_u32(uint32_t v) {
-    v = min(v, (uint32_t) dpp_i<DPP_XOR1>((int) v));
-    v = min(v, (uint32_t) dpp_i<DPP_XOR2>((int) v));
-    v = min(v, (uint32_t) dpp_i<DPP_HALF_MIRROR>((int) v));
-    v = min(v, (uint32_t) dpp_i<DPP_MIRROR>((int) v));
-    v = min(v, (uint32_t) swz_i<SWZ_XOR16>((int) v));
-    return min((uint32_t) __builtin_amdgcn_readlane((int) v, 0), (uint32_t) __builtin_amdgcn_readlane((int) v, 32));
-}
-WZY_DEV uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t) dpp_i<DPP_XOR1>((int) v));
-    v = max(v, (uint32_t) dpp_i<DPP_XOR2>((int) v));
-    v = max(v, (uint32_t) dpp_i<DPP_HALF_MIRROR>((int) v));
-    v = max(v, (uint32_t) dpp_i<DPP_MIRROR>((int) v));
-    v = max(v, (uint32_t) swz_i<SWZ_XOR16>((int) v));
-    return max((uint32_t) __builtin_amdgcn_readlane((int) v, 0), (uint32_t) __builtin_amdgcn_readlane((int) v, 32));
-}
+// Full-wave minimum of a 32-bit unsigned value (the complement of a maximum).
+WZY_DEV uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
 constexpr int TK_NBIN = 2 * TK_THREADS;   // histogram bins per pass (two per thread in the scan)
 constexpr int TK_LOG_NBIN = 11;

@@ -151,6 +151,24 @@ WZY_DEV uint64_t wave_max_u64(uint64_t k) {
     return ((uint64_t) hi << 32) | lo;
 }
 
+// Full-wave maximum of a 32-bit unsigned value with DPP only; lane 63 ends with the maximum, which is
+// returned to every lane (wave-uniform).
+// (Lanes of rows outside a row mask read 0, the identity of an unsigned maximum, so the moves can
+// fold into the max instructions.)
+template <int CTRL, int ROWMASK>
+WZY_DEV uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, ROWMASK, 0xF, false);
+}
+WZY_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<DPP_XOR1, 0xF>(v));
+    v = max(v, dpp_u32<DPP_XOR2, 0xF>(v));
+    v = max(v, dpp_u32<DPP_HALF_MIRROR, 0xF>(v));
+    v = max(v, dpp_u32<DPP_MIRROR, 0xF>(v));
+    v = max(v, dpp_u32<DPP_ROW_BCAST15, 0xA>(v));
+    v = max(v, dpp_u32<DPP_ROW_BCAST31, 0xC>(v));
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
+}
+
 // Block-wide sum for blockDim.x = NW*64 threads; `sh` must hold NW floats. Result on every thread.
 template <int NW>
 WZY_DEV float block_sum(float v, float* sh) {
