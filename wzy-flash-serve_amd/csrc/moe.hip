@@ -12,9 +12,10 @@
 //                   staged in LDS, combine in LDS:
 //                   comb = sigmoid(sgate)*shared + sum_k w_k*part_k  (k in routed order).
 // All expert GEMVs are wave-per-row with 128-bit code loads (16 bytes = 32 e2m1 values per lane)
-// and e4m3 scales from a separate plane, e2m1 -> int8 expansion with v_perm_b32, v_dot4_i32_i8
-// dots; every weight load of a lane is issued before any is used.  No MFMA: at one token per
-// expert these are bandwidth-bound GEMVs.
+// and e4m3 scales from a separate plane; e2m1 codes are expanded by the fp4 -> f16 conversion
+// instruction and dotted with f16 activation pairs (v_dot2_f32_f16, exact integer sums); every
+// weight load of a lane is issued before any is used.  No MFMA: at one token per expert these are
+// bandwidth-bound GEMVs.
 #include "wzy_device.h"
 #include "wzy_gemv.h"
 #include "wzy_host.h"
@@ -30,7 +31,7 @@ constexpr int DN_TILE = 8;    // output rows of one down workgroup
 template <int T>
 constexpr int dn_batch() { return T == 1 ? 6 : 4; }
 constexpr int MAX_ENT = WZY_MAX_W * MOE_MAX_K;
-constexpr int DN_STAGE_BYTES = 24 * 1024;   // activation staging limit of moe_down
+constexpr int DN_STAGE_BYTES = 48 * 1024;   // activation staging limit of moe_down
 
 struct MoeOffsets {
     size_t gu_codes, gu_scales, dn_codes, dn_scales, tail, rec;
@@ -46,13 +47,33 @@ WZY_DEV MoeOffsets moe_offsets(int D, int F) {
     return o;
 }
 
-// Dot of one 32-value NVFP4 chunk (16 code bytes, 2 e4m3 scales) with 32 int8 activations
-// (two per-16 scales), accumulated the way the reference does per 16-block:
+// Dot of one 32-value NVFP4 chunk (16 code bytes, 2 e4m3 scales) with 32 int8 activations (two
+// per-16 scales), accumulated the way the reference does per 16-block:
 // acc = fma(ws * xs, isum, acc)   (src/wzy_kernels_v2.cuh:1646-1647).
-WZY_DEV float nvfp4_chunk_fma(const int4 wa, const int4 wb, float wsa, float wsb, int4 xa, int4 xb, float xsa,
-                              float xsb, float acc) {
-    acc = fmaf(wsa * xsa, (float) dot16(wa, xa), acc);
-    acc = fmaf(wsb * xsb, (float) dot16(wb, xb), acc);
+// The e2m1 codes are expanded by the hardware fp4 -> f16 conversion with scale 2, which gives the
+// doubled codes 2*e2m1 (integers -12..12; ue4m3_half carries the matching 0.5), and the int8
+// activations are held as f16 pairs: pair p of a 16-value sub-block is (x_p, x_{p+8}), matching code
+// byte p (value p in its low nibble, p+8 in its high one).  Every product and partial sum is an
+// integer below 2^24, so each f32 dot-2 chain equals the integer dot isum exactly.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+template <int J>
+WZY_DEV half2_t fp4x2_h(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, J); }
+WZY_DEV float e2m1_dot16_h(uint32_t w0, uint32_t w1, const half2_t* xp) {
+    float a = 0.f, b = 0.f;                            // two chains for ILP (exact either way)
+    a = __builtin_amdgcn_fdot2(fp4x2_h<0>(w0), xp[0], a, false);
+    b = __builtin_amdgcn_fdot2(fp4x2_h<0>(w1), xp[4], b, false);
+    a = __builtin_amdgcn_fdot2(fp4x2_h<1>(w0), xp[1], a, false);
+    b = __builtin_amdgcn_fdot2(fp4x2_h<1>(w1), xp[5], b, false);
+    a = __builtin_amdgcn_fdot2(fp4x2_h<2>(w0), xp[2], a, false);
+    b = __builtin_amdgcn_fdot2(fp4x2_h<2>(w1), xp[6], b, false);
+    a = __builtin_amdgcn_fdot2(fp4x2_h<3>(w0), xp[3], a, false);
+    b = __builtin_amdgcn_fdot2(fp4x2_h<3>(w1), xp[7], b, false);
+    return a + b;
+}
+WZY_DEV float nvfp4_chunk_fma_h(const uint4 c, float wsa, float wsb, const half2_t (&xp)[16], float xsa, float xsb,
+                                float acc) {
+    acc = fmaf(wsa * xsa, e2m1_dot16_h(c.x, c.y, &xp[0]), acc);
+    acc = fmaf(wsb * xsb, e2m1_dot16_h(c.z, c.w, &xp[8]), acc);
     return acc;
 }
 
@@ -90,8 +111,9 @@ WZY_DEV void quant32_halves(const float (&v)[32], int4& qa, int4& qb, float& d) 
     qa = make_int4(w[0], w[1], w[2], w[3]);
     qb = make_int4(w[4], w[5], w[6], w[7]);
 }
-// 32 values -> two 16-value halves, each with its own per-16 scale
-WZY_DEV void quant16_halves(const float (&v)[32], int4& qa, int4& qb, float& da, float& db) {
+// 32 values -> two 16-value halves, each quantised to int8 with its own per-16 scale, written as
+// the f16 pairs of nvfp4_chunk_fma_h: xp[8h + p] = (q[16h + p], q[16h + p + 8]).
+WZY_DEV void quant16_pairs(const float (&v)[32], half2_t (&xp)[16], float& da, float& db) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         float am = 0.f;
@@ -99,17 +121,17 @@ WZY_DEV void quant16_halves(const float (&v)[32], int4& qa, int4& qb, float& da,
         for (int i = 0; i < 16; ++i) am = fmaxf(am, fabsf(v[16 * h + i]));
         const float d = am / 127.0f;
         const float inv = d > 0.f ? 127.0f / am : 0.f;
-        int w[4];
+        int q[16];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t pk = 0;
+        for (int i = 0; i < 16; ++i) q[i] = max(-127, min(127, rn_int(v[16 * h + i] * inv)));
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                pk |= (uint32_t) (max(-127, min(127, rn_int(v[16 * h + 4 * k + j] * inv))) & 0xFF) << (8 * j);
-            w[k] = (int) pk;
+        for (int p = 0; p < 8; ++p) {
+            half2_t t;
+            t.x = (_Float16) (float) q[p];
+            t.y = (_Float16) (float) q[p + 8];
+            xp[8 * h + p] = t;
         }
-        if (h == 0) { qa = make_int4(w[0], w[1], w[2], w[3]); da = d; }
-        else { qb = make_int4(w[0], w[1], w[2], w[3]); db = d; }
+        if (h == 0) da = d; else db = d;
     }
 }
 
@@ -323,6 +345,10 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
     const int bid = blockIdx.x;
     const int D = a.D, F = a.F, K = a.K;
     const int nc = D / 32;
+    // routed path: f16 activation pairs [T*nc][16] then per-16 scales [T*nc] float2; shared path:
+    // per-32 int8 halves [T*nc] int4 x2 then per-32 scales [T*nc] float (same allocation)
+    half2_t* s_xh = (half2_t*) s_dyn;
+    float2* s_xs2 = (float2*) (s_xh + (size_t) T * nc * 16);
     int4* s_qa = (int4*) s_dyn;
     int4* s_qb = s_qa + (size_t) T * nc;
     float* s_sc = (float*) (s_qb + (size_t) T * nc);
@@ -339,12 +365,16 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             for (int k = 0; k < 8; ++k) {
                 v[4 * k] = f4[k].x; v[4 * k + 1] = f4[k].y; v[4 * k + 2] = f4[k].z; v[4 * k + 3] = f4[k].w;
             }
-            int4 qa, qb;
+            half2_t xp[16];
             float da, db;
-            quant16_halves(v, qa, qb, da, db);
-            s_qa[i] = qa;
-            s_qb[i] = qb;
-            ((float2*) s_sc)[i] = make_float2(da, db);
+            quant16_pairs(v, xp, da, db);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xp[4 * k]),
+                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 1]),
+                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 2]),
+                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 3]));
+            s_xs2[i] = make_float2(da, db);
         };
         if (((__builtin_amdgcn_readfirstlane(tid) + 192) & 255) < T * nc) {   // wave-uniform: a wave with no item skips
             const int i = (tid + 192) & 255;
@@ -404,16 +434,25 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
         }
         if (lane < nc) {
 #pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int4 wa = e2m1_sub16((uint32_t) code[rr].x, (uint32_t) code[rr].y);
-                const int4 wb = e2m1_sub16((uint32_t) code[rr].z, (uint32_t) code[rr].w);
-                const float wsa = ue4m3_half(sc2[rr] & 0xFFu), wsb = ue4m3_half(sc2[rr] >> 8);
+            for (int m = 0; m < T; ++m) {
+                if (m < cnt) {
+                    const int xi = (r.gmem[g][m] / K) * nc + c;
+                    half2_t xp[16];
 #pragma unroll
-                for (int m = 0; m < T; ++m) {
-                    if (m < cnt) {
-                        const int xi = (r.gmem[g][m] / K) * nc + c;
-                        const float2 xs = ((const float2*) s_sc)[xi];
-                        acc[rr][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, s_qa[xi], s_qb[xi], xs.x, xs.y, acc[rr][m]);
+                    for (int k = 0; k < 4; ++k) {
+                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[k];
+                        xp[4 * k] = __builtin_bit_cast(half2_t, u.x);
+                        xp[4 * k + 1] = __builtin_bit_cast(half2_t, u.y);
+                        xp[4 * k + 2] = __builtin_bit_cast(half2_t, u.z);
+                        xp[4 * k + 3] = __builtin_bit_cast(half2_t, u.w);
+                    }
+                    const float2 xs = s_xs2[xi];
+#pragma unroll
+                    for (int rr = 0; rr < 8; ++rr) {
+                        const float wsa = ue4m3_half(sc2[rr] & 0xFFu), wsb = ue4m3_half(sc2[rr] >> 8);
+                        const uint4 cu = make_uint4((uint32_t) code[rr].x, (uint32_t) code[rr].y, (uint32_t) code[rr].z,
+                                                    (uint32_t) code[rr].w);
+                        acc[rr][m] = nvfp4_chunk_fma_h(cu, wsa, wsb, xp, xs.x, xs.y, acc[rr][m]);
                     }
                 }
             }
@@ -438,7 +477,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
             const int f = r.gmem[g][m];
-            a.aq16[(size_t) f * F + jt * 16 + jj] = (int8_t) q;
+            a.ah16[((size_t) f * (F / 16) + jt) * 16 + (jj & 7) * 2 + (jj >> 3)] =
+                __builtin_bit_cast(uint16_t, (_Float16) (float) q);
             if (jj == 0) a.as16[(size_t) f * (F / 16) + jt] = d;
         }
         return;
@@ -528,8 +568,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
 // Work items (group or shared, row) go round-robin to sixteen 16-lane slots; a slot issues the
 // loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
 // (F = 512: 16 chunks per row).  STAGE: the routed and shared activations are copied to LDS first
-// (dynamic LDS: aq halves [n_ent][F/32] x2 int4, as [n_ent][F/16] float, shq halves [T][F/32] x2
-// int4, shs [T][F/32] float).
+// (dynamic LDS: routed activations as f16 pairs [n_ent][F/32][16], as [n_ent][F/16] float, shq
+// halves [T][F/32] x2 int4, shs [T][F/32] float).
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
 // ---------------------------------------------------------------------------------------------
@@ -548,9 +588,8 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     constexpr int DN_BATCH = dn_batch<T>();
     // the group tables of every possible group are loaded without waiting for the group count
     const int ng = *a.n_groups;
-    int4* s_aqa = (int4*) s_dyn;
-    int4* s_aqb = s_aqa + (size_t) n_ent * nchunk;
-    float* s_as = (float*) (s_aqb + (size_t) n_ent * nchunk);
+    uint4* s_ah = (uint4*) s_dyn;                     // [n_ent * nchunk][4]: 16 f16 pairs per chunk
+    float* s_as = (float*) (s_ah + (size_t) n_ent * nchunk * 4);
     int4* s_sha = (int4*) (s_as + (size_t) n_ent * (F / 16));
     int4* s_shb = s_sha + (size_t) T * nchunk;
     float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
@@ -565,13 +604,14 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
 #pragma unroll
         for (int m = 0; m < WZY_MAX_W; ++m) gmem[m] = a.grp_mem[ie * WZY_MAX_W + m];
         const float wt = a.wts[ie], sgv = a.sg[min(tid, T - 1)];
-        int4 xa, xb, ha, hb;
+        uint4 xh[4];
+        int4 ha, hb;
         float4 xs4;
         float hs;
         if (STAGE) {
-            const int4* xp = (const int4*) (a.aq16 + (size_t) min(tid, n_aq - 1) * 32);
-            xa = xp[0];
-            xb = xp[1];
+            const uint4* xp = (const uint4*) (a.ah16 + (size_t) min(tid, n_aq - 1) * 32);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xh[k] = xp[k];
             xs4 = ((const float4*) a.as16)[min(tid, n_as4 - 1)];
             const int ih = min(tid, n_sh - 1);
             const int4* hp = (const int4*) (a.shq32 + (size_t) ih * 32);
@@ -588,10 +628,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         }
         if (tid < T) s_sg[tid] = sgv;
         if (STAGE) {
-            if (tid < n_aq) {
-                s_aqa[tid] = xa;
-                s_aqb[tid] = xb;
-            }
+            if (tid < n_aq)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) s_ah[(size_t) tid * 4 + k] = xh[k];
             if (tid < n_as4) ((float4*) s_as)[tid] = xs4;
             if (tid < n_sh) {
                 s_sha[tid] = ha;
@@ -609,9 +648,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     }
     if (STAGE) {
         for (int i = tid + 256; i < n_aq; i += 256) {
-            const int4* xp = (const int4*) (a.aq16 + (size_t) i * 32);
-            s_aqa[i] = xp[0];
-            s_aqb[i] = xp[1];
+            const uint4* xp = (const uint4*) (a.ah16 + (size_t) i * 32);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s_ah[(size_t) i * 4 + k] = xp[k];
         }
         for (int i = tid + 256; i < n_as4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
         for (int i = tid + 256; i < n_sh; i += 256) {
@@ -670,23 +709,28 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                 if (item >= n_items || !cvalid) continue;
                 const int g = item / DN_TILE;
                 if (g < ng) {
-                    const int4 wa = e2m1_sub16((uint32_t) c0[b].x, (uint32_t) c0[b].y);
-                    const int4 wb = e2m1_sub16((uint32_t) c0[b].z, (uint32_t) c0[b].w);
+                    const uint4 cu = make_uint4((uint32_t) c0[b].x, (uint32_t) c0[b].y, (uint32_t) c0[b].z,
+                                                (uint32_t) c0[b].w);
                     const float wsa = ue4m3_half(sraw[b] & 0xFFu), wsb = ue4m3_half(sraw[b] >> 8);
                     const int cnt = s_gcnt[g];
 #pragma unroll
                     for (int m = 0; m < T; ++m) {
                         if (m < cnt) {
                             const int f = s_gmem[g][m];
-                            if (STAGE) {
-                                const int xi = f * nchunk + c;
-                                const float2 xs = ((const float2*) s_as)[xi];
-                                acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, s_aqa[xi], s_aqb[xi], xs.x, xs.y, acc[b][m]);
-                            } else {
-                                const int4* xp = (const int4*) (a.aq16 + (size_t) f * F + (size_t) c * 32);
-                                const float2 xs = *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
-                                acc[b][m] = nvfp4_chunk_fma(wa, wb, wsa, wsb, xp[0], xp[1], xs.x, xs.y, acc[b][m]);
+                            const int xi = f * nchunk + c;
+                            const uint4* xq = STAGE ? s_ah + (size_t) xi * 4 : (const uint4*) (a.ah16 + (size_t) xi * 32);
+                            const float2 xs = STAGE ? ((const float2*) s_as)[xi]
+                                                    : *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
+                            half2_t xp[16];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const uint4 u = xq[k];
+                                xp[4 * k] = __builtin_bit_cast(half2_t, u.x);
+                                xp[4 * k + 1] = __builtin_bit_cast(half2_t, u.y);
+                                xp[4 * k + 2] = __builtin_bit_cast(half2_t, u.z);
+                                xp[4 * k + 3] = __builtin_bit_cast(half2_t, u.w);
                             }
+                            acc[b][m] = nvfp4_chunk_fma_h(cu, wsa, wsb, xp, xs.x, xs.y, acc[b][m]);
                         }
                     }
                 } else {
@@ -752,7 +796,7 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
     w.grp_exp = a.take<int>(n_ent);
     w.grp_cnt = a.take<int>(n_ent);
     w.grp_mem = a.take<int>((size_t) n_ent * WZY_MAX_W);
-    w.aq16 = a.take<int8_t>((size_t) n_ent * F);
+    w.ah16 = a.take<uint16_t>((size_t) n_ent * F);
     w.as16 = a.take<float>((size_t) n_ent * F / 16);
     w.shq32 = a.take<int8_t>((size_t) T * F);
     w.shs32 = a.take<float>((size_t) T * F / 32);
@@ -788,7 +832,7 @@ static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float*
     a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.E = w->n_exp; a.K = w->top_k;
     a.x = x; a.logits = ws.logits;
     a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt;
-    a.grp_mem = ws.grp_mem; a.aq16 = ws.aq16; a.as16 = ws.as16;
+    a.grp_mem = ws.grp_mem; a.ah16 = ws.ah16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shq32 = ws.shq32; a.shs32 = ws.shs32;
     a.n_routed_wg = (w->n_ff / 16) * T * w->top_k;
@@ -798,14 +842,14 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
     MoeDnArgs a{};
     a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.K = w->top_k;
     a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
-    a.aq16 = ws.aq16; a.as16 = ws.as16; a.shd_q = w->sh_down_q; a.shd_s = w->sh_down_s;
+    a.ah16 = ws.ah16; a.as16 = ws.as16; a.shd_q = w->sh_down_q; a.shd_s = w->sh_down_s;
     a.shq32 = ws.shq32; a.shs32 = ws.shs32; a.wts = ws.wts; a.sg = ws.sg; a.comb = comb;
     return a;
 }
 
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
-    const size_t lds = (size_t) T * (a.D / 32) * (2 * sizeof(int4) + sizeof(float2));
+    const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
     if (a.E <= 512)
         hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
     else
@@ -821,7 +865,7 @@ static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
     const int n_ent = T * a.K, nchunk = a.F / 32;
-    const size_t lds = (size_t) n_ent * nchunk * 2 * sizeof(int4) + (size_t) n_ent * (a.F / 16) * sizeof(float) +
+    const size_t lds = (size_t) n_ent * nchunk * 4 * sizeof(uint4) + (size_t) n_ent * (a.F / 16) * sizeof(float) +
                        (size_t) T * nchunk * (2 * sizeof(int4) + sizeof(float));
     switch ((nchunk + 15) / 16) {
         case 1: launch_dn_tc<T, 1>(a, lds, st); break;

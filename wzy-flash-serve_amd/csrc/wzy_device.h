@@ -223,37 +223,6 @@ WZY_DEV int dot16(int4 a, int4 b) {
 // ---------------------------------------------------------------------------------------------
 // NVFP4 (e2m1 codes x e4m3 block scales)
 // ---------------------------------------------------------------------------------------------
-// e2m1 code -> 2*value as int8: {0,1,2,3,4,6,8,12, 0,-1,-2,-3,-4,-6,-8,-12}.
-// Eight packed nibbles (one uint32) expand to eight int8 lanes with v_perm_b32 table lookups:
-// the low 3 bits of each nibble select a magnitude byte from the 8-entry table, the sign bit
-// negates it.
-WZY_DEV uint32_t e2m1x4_mag(uint32_t sel4) {
-    // sel4: four 3-bit indices in the low 3 bits of each byte. perm selector byte k picks byte
-    // sel of {hi:lo} = {0x0C080604, 0x03020100}: 0..3 -> 0,1,2,3 ; 4..7 -> 4,6,8,12.
-    return __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel4);
-}
-// Expand the 4 nibbles sitting in the low nibble of each byte of `nib` (bits 0-3, 8-11, 16-19,
-// 24-27) into 4 signed int8 values (2*e2m1).
-WZY_DEV int e2m1x4(uint32_t nib) {
-    const uint32_t mag = e2m1x4_mag(nib & 0x07070707u);
-    // sign: bit 3 of each nibble, applied only to non-zero magnitudes so that negative zero (code 8)
-    // stays 0x00 and ~mag + 1 never carries across a byte boundary.
-    const uint32_t nz = (nib | (nib >> 1) | (nib >> 2)) & 0x01010101u;
-    const uint32_t sgn = (nib >> 3) & nz;
-    const uint32_t msk = sgn * 0xFFu;                  // 0xFF in negative bytes
-    return (int) ((mag ^ msk) + sgn);                  // two's complement per byte
-}
-// 8 code bytes of one 16-value sub-block (value k<8 = low nibble of byte k, value k>=8 = high
-// nibble of byte k-8) -> 16 int8 lanes in value order packed as int4 {v0..3, v4..7, v8..11, v12..15}.
-WZY_DEV int4 e2m1_sub16(uint32_t w0, uint32_t w1) {
-    int4 r;
-    r.x = e2m1x4(w0);
-    r.y = e2m1x4(w1);
-    r.z = e2m1x4(w0 >> 4);
-    r.w = e2m1x4(w1 >> 4);
-    return r;
-}
-
 // Unsigned e4m3 block scale (sign bit ignored), pre-multiplied by 0.5 to cancel the doubled e2m1
 // codes: e == 0 -> m * 2^-9, else (1 + m/8) * 2^(e-7); no NaN encoding is special-cased.
 WZY_DEV float ue4m3_half(uint32_t x) {

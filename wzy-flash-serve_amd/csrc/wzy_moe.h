@@ -15,7 +15,8 @@ struct MoeWs {
     float* logits; float* sg;             // router logits [T x E], shared gate scalar [T]
     int* ids;      float* wts;            // [T x K] routed experts and renormalised weights
     int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // distinct experts of the window
-    int8_t* aq16;  float* as16;           // SwiGLU activations per routed entry, per-16 int8
+    uint16_t* ah16; float* as16;          // SwiGLU activations per routed entry: per-16 int8 values held
+                                          // as f16 pairs [n_ent][F/16][8][2] (x_p, x_p+8), and their scales
     int8_t* shq32; float* shs32;          // shared-expert SwiGLU activation, per-32 int8
 };
 
@@ -23,7 +24,7 @@ struct MoeGuArgs {
     const uint8_t* experts; int D, F, E, K;
     const float* x; const float* logits;
     int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // published by workgroup 0
-    int8_t* aq16; float* as16;
+    uint16_t* ah16; float* as16;
     const int8_t* shg_q; const uint16_t* shg_s; const int8_t* shu_q; const uint16_t* shu_s;
     int8_t* shq32; float* shs32;
     int n_routed_wg;
@@ -31,7 +32,7 @@ struct MoeGuArgs {
 struct MoeDnArgs {
     const uint8_t* experts; int D, F, K;
     const int* n_groups; const int* grp_exp; const int* grp_cnt; const int* grp_mem;
-    const int8_t* aq16; const float* as16;
+    const uint16_t* ah16; const float* as16;
     const int8_t* shd_q; const uint16_t* shd_s; const int8_t* shq32; const float* shs32;
     const float* wts; const float* sg; float* comb;
 };
