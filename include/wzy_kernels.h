@@ -128,6 +128,13 @@ size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T
 int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Softmax top-k routing alone, over router logits [T x n_exp] (fp32): ids [T x top_k] in rank
+ * order (probability descending, ties to the lower expert id) and wts [T x top_k] = p_k /
+ * max(sum_k p_k, 2^-14).  The same device routing wzy_moe_block runs inside its gate/up launch.
+ * n_exp <= 1024, top_k <= 32, T <= WZY_MAX_W.
+ * Replaces router_top10_fast_multi (src/wzy_kernels_v2.cuh:989-1090). */
+int wzy_moe_route(const float* logits, int n_exp, int top_k, int T, int* ids, float* wts, void* stream);
+
 /* Time the expert kernels of wzy_moe_block with hipEvents on `stream`.  The router logits of x
  * [T x n_embd] are computed for every layer first; then `iters` gate/up launches run back to back
  * cycling through the `n_layers` weight sets (so the 256 MB last-level cache cannot hold the

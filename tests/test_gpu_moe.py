@@ -189,6 +189,47 @@ def test_gemv_segs_parity(wz, orc, gpu, cols, T, kinds):
         assert not got[:, rows:].any(), "wrote outside the segment's rows"
 
 
+def route_logits(kind, E, T, rng):
+    if kind == "gauss":
+        return rng.normal(0, 2, (T, E)).astype(np.float32)
+    if kind == "levels":                                  # a few values: exact ties broken by id
+        return rng.integers(0, 6, (T, E)).astype(np.float32)
+    if kind == "top_tie":                                 # 100 experts share the top probability
+        l = rng.normal(-5, 1, (T, E)).astype(np.float32)
+        for t in range(T):
+            l[t, rng.choice(E, min(100, E), replace=False)] = 3.0
+        return l
+    if kind == "equal":
+        return np.full((T, E), 0.5, np.float32)
+    if kind == "spread":                                  # probabilities spanning many binades
+        return rng.uniform(-60, 10, (T, E)).astype(np.float32)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["gauss", "levels", "top_tie", "equal", "spread"])
+@pytest.mark.parametrize("E,K,T", [(512, 10, 1), (512, 10, 4), (1024, 32, 2), (64, 8, 3), (16, 10, 1), (512, 1, 8)])
+def test_moe_route_patterns(wz, orc, gpu, kind, E, K, T):
+    print("case moe_route kind=%s E=%d K=%d T=%d" % (kind, E, K, T), flush=True)
+    rng = np.random.default_rng(E * 7 + K * 3 + T + len(kind))
+    logits = route_logits(kind, E, T, rng)
+    ids, wts = DA(T * K, np.int32, zero=True), DA(T * K, np.float32, zero=True)
+    d = dev(logits)
+    assert wz.wzy_moe_route(d.ptr, E, K, T, ids.ptr, wts.ptr, None) == 0
+    wz.wzy_device_sync()
+    gi, gw = host(ids), host(wts)
+    oi, ow = np.empty(T * K, np.int32), np.empty(T * K, np.float32)
+    orc.orc_router_topk(ptr(logits), E, K, T, ptr(oi), ptr(ow), None)
+    if kind in ("levels", "top_tie", "equal"):            # exact ties: equal probabilities on both sides
+        np.testing.assert_array_equal(gi, oi)
+    else:                                                 # rows whose K-th margin is above float noise
+        check_ids(orc, logits.ravel(), E, K, T, gi, oi)
+    for t in range(T):
+        row = gi[t * K:(t + 1) * K]
+        assert len(set(row.tolist())) == K and row.min() >= 0 and row.max() < E
+    same = gi == oi
+    np.testing.assert_allclose(gw[same], ow[same], rtol=1e-5, atol=1e-7)
+
+
 def test_moe_config1_parity(wz, orc, gpu):
     """D=2048, 512 experts top-10, NFF=512, seed 0, one token."""
     D, F, E, K, T = 2048, 512, 512, 10, 1

@@ -149,6 +149,7 @@ struct RouteLds {
     int gmem[MAX_ENT][WZY_MAX_W];
     int n_groups;
     int c[4];
+    uint64_t cand[4][64];          // per-wave candidate keys of route_row
 };
 
 // Logits of one row per wave: RV per lane (lane + 64*i), RV = 8 for E <= 512, 16 for E <= 1024.
@@ -201,11 +202,16 @@ WZY_DEV void sort_keys_desc(uint64_t (&k)[RV]) {
 }
 
 // Softmax top-K of one row in one wave (ranking: probability desc, expert id asc).  Every lane
-// sorts the keys of its RV probabilities once; each of the K rounds is one DPP wave maximum over the
-// lane heads, and the lane holding the winner pops its head.  Lane k ends with the k-th routed
-// (id, probability); wsum is their sum in rank order.
+// sorts the keys of its RV probabilities once.  Candidates: thr = the K-th largest probability word
+// among the 64 lane heads with its low 18 bits cleared (bisection on ballot counts over bits 29..18;
+// probabilities are <= 1, so bits 31 and 30 are clear); the K largest heads are K distinct keys
+// >= thr, so every key with a probability word >= thr is a superset of the top K.  When at most 64
+// keys qualify, they are gathered into `cand` (this wave's LDS scratch) and each ranks itself
+// against the others (broadcast by readlane); otherwise K rounds each take the DPP wave maximum
+// over the lane heads and the winner lane pops its head.  Lane k ends with the k-th routed (id, probability); wsum is their sum
+// in rank order.
 template <int RV>
-WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, float& wsum) {
+WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, float& wsum, uint64_t* cand) {
     const int lane = threadIdx.x & 63;
     float mx = -INFINITY;
 #pragma unroll
@@ -228,6 +234,51 @@ WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, fl
     wsum = 0.f;
     my_id = 0;
     my_w = 0.f;
+
+    uint32_t thr = 0;
+#pragma unroll
+    for (int b = 29; b >= 18; --b) {
+        const uint32_t c = thr | (1u << b);
+        thr = __popcll(__ballot(hi[0] >= c)) >= K ? c : thr;       // wave-uniform
+    }
+    uint64_t bal[RV];
+    int n_cand = 0;
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+        bal[i] = __ballot(hi[i] >= thr);
+        n_cand += __popcll(bal[i]);
+    }
+    if (n_cand <= 64) {                                             // wave-uniform
+        int base = 0;
+#pragma unroll
+        for (int i = 0; i < RV; ++i) {
+            const int below = __builtin_amdgcn_mbcnt_hi((uint32_t) (bal[i] >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t) bal[i], 0));
+            if (hi[i] >= thr) cand[base + below] = key[i];
+            base += __popcll(bal[i]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const uint64_t mine = lane < n_cand ? cand[lane] : 0ull;
+        int rank = 0;
+        for (int j = 0; j < n_cand; ++j) {
+            const uint32_t jl = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) mine, j);
+            const uint32_t jh = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (mine >> 32), j);
+            rank += ((((uint64_t) jh << 32) | jl) > mine) ? 1 : 0;
+        }
+        rank = lane < n_cand ? rank : 64;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (rank < K) cand[rank] = mine;                            // distinct keys: distinct ranks
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (lane < K) {
+            const uint64_t kk = cand[lane];
+            my_w = __builtin_bit_cast(float, (uint32_t) (kk >> 32));
+            int bi = (int) (0xFFFFFFFFu - (uint32_t) kk);
+            if (bi >= E || bi < 0) bi = 0;                          // non-finite logits: keep the id in range
+            my_id = bi;
+        }
+        for (int k = 0; k < K; ++k) wsum += as_f(__builtin_amdgcn_readlane(as_i(my_w), k));
+        return;
+    }
     for (int k = 0; k < K; ++k) {
         // the largest head: a 32-bit DPP maximum of the probability words, then (only when several
         // lanes hold that probability) of the id words among them; the winner lane is unique
@@ -267,7 +318,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
         if (wv == 0) {
             int my_id;
             float my_w, wsum;
-            route_row<RV>(p[0], E, K, my_id, my_w, wsum);
+            route_row<RV>(p[0], E, K, my_id, my_w, wsum, r.cand[0]);
             const float sc = fmaxf(wsum, 6.103515625e-05f);
             if (lane < K) {
                 r.ids[lane] = my_id;
@@ -288,7 +339,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
         if (t >= T) continue;                            // wave-uniform
         int my_id;
         float my_w, wsum;
-        route_row<RV>(p[rr], E, K, my_id, my_w, wsum);
+        route_row<RV>(p[rr], E, K, my_id, my_w, wsum, r.cand[wv]);
         const float sc = fmaxf(wsum, 6.103515625e-05f);
         if (lane < K) { r.ids[t * K + lane] = my_id; r.w[t * K + lane] = my_w / sc; }
     }
@@ -779,6 +830,20 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     }
 }
 
+// Routing alone (the device routing of moe_gate_up): one workgroup, window rows in waves.
+template <int T, int RV>
+__global__ void __launch_bounds__(256) moe_route_kernel(const float* __restrict__ logits, int E, int K,
+                                                        int* __restrict__ ids, float* __restrict__ wts) {
+    __shared__ RouteLds r;
+    float p[(T + 3) / 4][RV];
+    route_prefetch<T, RV>(logits, E, p);
+    route_compute<T, RV>(p, E, K, r);
+    for (int i = threadIdx.x; i < T * K; i += blockDim.x) {
+        ids[i] = r.ids[i];
+        wts[i] = r.w[i];
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------------------------
@@ -1001,5 +1066,32 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
     if (rc != WZY_OK) return rc;
     *us_gate_up = 1000.0f * a / (float) iters;
     *us_down = 1000.0f * b / (float) iters;
+    return WZY_OK;
+}
+
+template <int T>
+static void launch_route_t(const float* logits, int E, int K, int* ids, float* wts, hipStream_t st) {
+    if (E <= 512) hipLaunchKernelGGL((moe_route_kernel<T, 8>), dim3(1), dim3(256), 0, st, logits, E, K, ids, wts);
+    else hipLaunchKernelGGL((moe_route_kernel<T, 16>), dim3(1), dim3(256), 0, st, logits, E, K, ids, wts);
+}
+
+extern "C" int wzy_moe_route(const float* logits, int n_exp, int top_k, int T, int* ids, float* wts, void* stream) {
+    WZY_REQUIRE(logits && ids && wts, "wzy_moe_route: null pointer");
+    WZY_REQUIRE(n_exp >= 1 && n_exp <= 1024, "wzy_moe_route: n_exp must be in [1, 1024]");
+    WZY_REQUIRE(top_k >= 1 && top_k <= MOE_MAX_K && top_k <= n_exp, "wzy_moe_route: top_k must be in [1, %d]",
+                MOE_MAX_K);
+    WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "wzy_moe_route: T must be in [1, %d]", WZY_MAX_W);
+    hipStream_t st = as_stream(stream);
+    switch (T) {
+        case 1: launch_route_t<1>(logits, n_exp, top_k, ids, wts, st); break;
+        case 2: launch_route_t<2>(logits, n_exp, top_k, ids, wts, st); break;
+        case 3: launch_route_t<3>(logits, n_exp, top_k, ids, wts, st); break;
+        case 4: launch_route_t<4>(logits, n_exp, top_k, ids, wts, st); break;
+        case 5: launch_route_t<5>(logits, n_exp, top_k, ids, wts, st); break;
+        case 6: launch_route_t<6>(logits, n_exp, top_k, ids, wts, st); break;
+        case 7: launch_route_t<7>(logits, n_exp, top_k, ids, wts, st); break;
+        default: launch_route_t<8>(logits, n_exp, top_k, ids, wts, st); break;
+    }
+    WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
