@@ -1,11 +1,23 @@
 // gdn.hip -- gated delta-rule (GDN) decode step for gfx950.
 //
-// One 512-thread workgroup per key head kh; it runs the value heads kh, kh+HK, ... in turn.  The 128x128 fp32 state of the
-// head lives in VGPRs for the whole window: thread (col j, row group g) holds S[32g .. 32g+31][j]
-// and the state touches HBM once on entry and once on exit (plus optional per-step snapshots for
-// speculative verify).  In the fused mode the workgroup first runs, for its own 384 channels, the
-// 4-tap causal depthwise conv + SiLU + per-head L2 norm and the decay/beta gates, so the raw
-// projection output goes straight into the recurrence.
+// The 128x128 fp32 state of a value head is split by columns over GDN_NQ workgroups (256 threads
+// each): workgroup (h, cq) owns columns 32*cq .. 32*cq+31, and thread (column c = lane % 32, row
+// group rg = 2*wave + lane / 32) holds S[16*rg .. 16*rg+15][32*cq + c] in VGPRs for the whole
+// window.  The columns of the recurrence are independent, so a head's state moves through 4 CUs
+// (16 KB each) instead of one.  Every global load of a workgroup (its state block, conv inputs,
+// gates) is issued at entry, before any is used; the state touches HBM once on entry and once on
+// exit (plus optional per-step snapshots for speculative verify).
+// In the fused mode each workgroup first runs the 4-tap causal depthwise conv + SiLU of the 256 q/k
+// channels of its key head and of its own 32 v channels, the per-head L2 norms of q and k, and the
+// decay/beta gates.  The v history belongs to one workgroup and is updated in place.  The q/k
+// history is read by every workgroup of the key head, so it is written by the last of them: each
+// workgroup increments the key head's counter once its history reads have been consumed, and the
+// one that sees the count complete writes the new history and resets the counter (no workgroup
+// waits for another).
+// The output RMS norm spans the head's 128 columns, i.e. four workgroups: the kernel writes
+// o * 1/sqrt(128) and, per (row, head, column quarter), the partial sum of its squares; the norm
+// and gate y = o * rsqrt(sum/128 + eps) * gamma * sigmoid(z) are applied by the consumer (the
+// out-projection GEMV's staging in the stage, gdn_norm_kernel for the standalone entry points).
 //
 // Per step t:  S *= decay;  kv_j = sum_i S_ij k_i;  delta_j = (v_j - kv_j) * beta;
 //              S_ij += k_i delta_j;  o_j = sum_i S_ij q_i;  o *= 1/sqrt(128);
@@ -18,170 +30,220 @@
 
 using namespace wzy;
 
-constexpr int GS = 128;   // state / head dim
+constexpr int GS = 128;              // state / head dim
+constexpr int QC = GS / GDN_NQ;      // state columns per workgroup
+constexpr int GDN_MAX_HK = 1024;
+constexpr int GDN_MAX_HV = 1024;
+
+// Completion counters of the shared q/k conv history, one per key head; every launch leaves them
+// at zero.  Launches on one device must not overlap.
+__device__ int g_gdn_qk_sync[GDN_MAX_HK];
+// Partial sums of squares of the standalone entry points ([T][HV][GDN_NQ]).
+__device__ float g_gdn_ss[WZY_MAX_W * GDN_MAX_HV * GDN_NQ];
 
 template <bool FUSED>
-__global__ void __launch_bounds__(512) gdn_kernel(GdnArgs a) {
-    __shared__ float s_q[WZY_MAX_W][GS], s_k[WZY_MAX_W][GS], s_v[WZY_MAX_W][GS];
+__global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__ o_ss) {
+    __shared__ float s_q[WZY_MAX_W][GS], s_k[WZY_MAX_W][GS], s_v[WZY_MAX_W][QC];
     __shared__ float s_dec[WZY_MAX_W], s_beta[WZY_MAX_W];
-    __shared__ float s_red[4][GS];
-    __shared__ float s_red2[4][GS];
-    __shared__ float s_w[16];
-    const int kh = blockIdx.x;                      // key head; value heads kh, kh+HK, ...
+    __shared__ float s_w[WZY_MAX_W][4];
+    __shared__ float s_kv[8][QC], s_o[8][QC];
+    __shared__ int s_last;
+    const int h = blockIdx.x / GDN_NQ, cq = blockIdx.x % GDN_NQ;
     const int HK = a.hk, HV = a.hv, T = a.T;
+    const int kh = h % HK;
     const int QKV = 2 * HK * GS + HV * GS;
-    const int tid = threadIdx.x;
-    const int col = tid & (GS - 1), rg = tid >> 7;  // 4 row groups of 32
-    const int lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c = lane & (QC - 1), rg = 2 * wv + (lane >> 5);
+    const int j = cq * QC + c;                      // state column of this thread
 
-    // ---- q, k of this key head ----
+    // ---- 0. every load, issued before any is used ----
+    float s[16];
+    float* sbase = a.state + (size_t) h * GS * GS + (size_t) (16 * rg) * GS + j;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = sbase[(size_t) r * GS];
+    // q/k channel tid (q for tid < 128); v channel 32*cq + (tid % 32) of head h; gates on threads 128 + t
+    const int qk_ch = (tid < GS ? 0 : HK * GS - GS) + kh * GS + tid;
+    const int v_ch = 2 * HK * GS + h * GS + cq * QC + (tid & (QC - 1));
+    float qh[3], qw[4], vh[3], vw[4], qx[WZY_MAX_W], vx[WZY_MAX_W];
+    float g_a, g_b, g_dt = 0.f, g_sa = 0.f;
+    const int tg = min(max(tid - GS, 0), T - 1);
     if (FUSED) {
-        // 4-tap causal conv + SiLU on the q and k channels (this workgroup owns their history)
-        if (tid < 2 * GS) {
-            const int part = tid / GS, i = tid % GS;
-            const int ch = part * HK * GS + kh * GS + i;
-            float h0 = a.conv_hist[ch * 3 + 0], h1 = a.conv_hist[ch * 3 + 1], h2 = a.conv_hist[ch * 3 + 2];
-            const float w0 = a.conv_w[ch * 4 + 0], w1 = a.conv_w[ch * 4 + 1], w2 = a.conv_w[ch * 4 + 2], w3 = a.conv_w[ch * 4 + 3];
-            for (int t = 0; t < T; ++t) {
-                const float x = a.qkv[(size_t) t * QKV + ch];
-                const float sum = h0 * w0 + h1 * w1 + h2 * w2 + x * w3;
-                h0 = h1; h1 = h2; h2 = x;
-                (part == 0 ? s_q : s_k)[t][i] = sum / (1.0f + __expf(-sum));
+#pragma unroll
+        for (int i = 0; i < 3; ++i) { qh[i] = a.conv_hist[qk_ch * 3 + i]; vh[i] = a.conv_hist[v_ch * 3 + i]; }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { qw[i] = a.conv_w[qk_ch * 4 + i]; vw[i] = a.conv_w[v_ch * 4 + i]; }
+#pragma unroll
+        for (int t = 0; t < WZY_MAX_W; ++t) {
+            const int tc = t < T ? t : 0;
+            qx[t] = a.qkv[(size_t) tc * QKV + qk_ch];
+            vx[t] = a.qkv[(size_t) tc * QKV + v_ch];
+        }
+        g_a = a.ab[(size_t) tg * 2 * HV + h];
+        g_b = a.ab[(size_t) tg * 2 * HV + HV + h];
+        g_dt = a.dt[h];
+        g_sa = a.ssm_a[h];
+    } else {
+#pragma unroll
+        for (int t = 0; t < WZY_MAX_W; ++t) {
+            const int tc = t < T ? t : 0;
+            qx[t] = tid < GS ? a.q[(size_t) tc * HK * GS + kh * GS + tid] : a.k[(size_t) tc * HK * GS + kh * GS + tid - GS];
+            vx[t] = a.v[(size_t) tc * HV * GS + h * GS + cq * QC + (tid & (QC - 1))];
+        }
+        g_a = a.decay[tg * HV + h];
+        g_b = a.beta[tg * HV + h];
+    }
+
+    // ---- 1. conv + SiLU (fused), L2 norms of q and k, gates ----
+    int qk_order = 0;
+    if (FUSED) {
+        float h0 = qh[0], h1 = qh[1], h2 = qh[2];
+        float u0 = vh[0], u1 = vh[1], u2 = vh[2];
+#pragma unroll
+        for (int t = 0; t < WZY_MAX_W; ++t) {
+            if (t >= T) break;
+            const float sum = h0 * qw[0] + h1 * qw[1] + h2 * qw[2] + qx[t] * qw[3];
+            h0 = h1; h1 = h2; h2 = qx[t];
+            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = sum / (1.0f + __expf(-sum));
+            if (tid < QC) {
+                const float sv = u0 * vw[0] + u1 * vw[1] + u2 * vw[2] + vx[t] * vw[3];
+                u0 = u1; u1 = u2; u2 = vx[t];
+                s_v[t][tid] = sv / (1.0f + __expf(-sv));
                 if (a.hist_snaps) {
-                    float* hs = a.hist_snaps + (size_t) t * QKV * 3 + (size_t) ch * 3;
-                    hs[0] = h0; hs[1] = h1; hs[2] = h2;
+                    float* hs = a.hist_snaps + (size_t) t * QKV * 3 + (size_t) v_ch * 3;
+                    hs[0] = u0; hs[1] = u1; hs[2] = u2;
                 }
             }
-            a.conv_hist[ch * 3 + 0] = h0; a.conv_hist[ch * 3 + 1] = h1; a.conv_hist[ch * 3 + 2] = h2;
+            if (a.hist_snaps && h == kh && cq == 0) {   // q/k snapshots: one writer per key head
+                float* hs = a.hist_snaps + (size_t) t * QKV * 3 + (size_t) qk_ch * 3;
+                hs[0] = h0; hs[1] = h1; hs[2] = h2;
+            }
+        }
+        if (tid < QC) {                                 // own v history
+            a.conv_hist[v_ch * 3 + 0] = u0; a.conv_hist[v_ch * 3 + 1] = u1; a.conv_hist[v_ch * 3 + 2] = u2;
+        }
+        qh[0] = h0; qh[1] = h1; qh[2] = h2;             // new q/k history, written by the last workgroup
+        if (tid >= GS && tid < GS + T) {
+            const float av = g_a + g_dt;
+            const float sp = av > 20.0f ? av : log1pf(__expf(av));
+            s_dec[tid - GS] = __expf(sp * g_sa);
+            s_beta[tid - GS] = 1.0f / (1.0f + __expf(-g_b));
         }
         __syncthreads();
+        // every wave has consumed its reads of the shared history: count this workgroup.  A relaxed
+        // device-scope count is enough: the last workgroup's history writes depend on the count it
+        // sees, and every other workgroup's reads returned before its count (the new values are
+        // needed by the next launch only).  The result is used only at the end.
+        if (tid == 0)
+            qk_order = __hip_atomic_fetch_add(&g_gdn_qk_sync[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // per-head L2 norm of q and k: waves 0-1 reduce q, waves 2-3 reduce k
         for (int t = 0; t < T; ++t) {
-            if (tid < 2 * GS) {
-                const float y = (tid < GS) ? s_q[t][tid] : s_k[t][tid - GS];
-                const float sq = wave_sum(y * y);
-                if (lane == 0) s_w[wv] = sq;
-            }
-            __syncthreads();
-            if (tid < 2 * GS) {
-                const float ss = (tid < GS) ? (s_w[0] + s_w[1]) : (s_w[2] + s_w[3]);
-                const float r = 1.0f / sqrtf(ss + a.eps);
-                if (tid < GS) s_q[t][tid] *= r; else s_k[t][tid - GS] *= r;
-            }
-            __syncthreads();
-        }
-    } else {
-        for (int i = tid; i < T * GS; i += blockDim.x) {
-            const int t = i / GS, j = i % GS;
-            s_q[t][j] = a.q[(size_t) t * HK * GS + kh * GS + j];
-            s_k[t][j] = a.k[(size_t) t * HK * GS + kh * GS + j];
-        }
-    }
-    const float gm = a.gamma ? a.gamma[col] : 1.0f;
-
-    for (int h = kh; h < HV; h += HK) {
-        // ---- v of value head h, gates ----
-        if (FUSED) {
-            if (tid < GS) {
-                const int ch = 2 * HK * GS + h * GS + tid;
-                float h0 = a.conv_hist[ch * 3 + 0], h1 = a.conv_hist[ch * 3 + 1], h2 = a.conv_hist[ch * 3 + 2];
-                const float w0 = a.conv_w[ch * 4 + 0], w1 = a.conv_w[ch * 4 + 1], w2 = a.conv_w[ch * 4 + 2], w3 = a.conv_w[ch * 4 + 3];
-                for (int t = 0; t < T; ++t) {
-                    const float x = a.qkv[(size_t) t * QKV + ch];
-                    const float sum = h0 * w0 + h1 * w1 + h2 * w2 + x * w3;
-                    h0 = h1; h1 = h2; h2 = x;
-                    s_v[t][tid] = sum / (1.0f + __expf(-sum));
-                    if (a.hist_snaps) {
-                        float* hs = a.hist_snaps + (size_t) t * QKV * 3 + (size_t) ch * 3;
-                        hs[0] = h0; hs[1] = h1; hs[2] = h2;
-                    }
-                }
-                a.conv_hist[ch * 3 + 0] = h0; a.conv_hist[ch * 3 + 1] = h1; a.conv_hist[ch * 3 + 2] = h2;
-            } else if (tid >= 256 && tid < 256 + T) {
-                const int t = tid - 256;
-                const float av = a.ab[(size_t) t * 2 * HV + h] + a.dt[h];
-                const float sp = av > 20.0f ? av : log1pf(__expf(av));
-                s_dec[t] = __expf(sp * a.ssm_a[h]);
-                s_beta[t] = 1.0f / (1.0f + __expf(-a.ab[(size_t) t * 2 * HV + HV + h]));
-            }
-        } else {
-            for (int i = tid; i < T * GS; i += blockDim.x) {
-                const int t = i / GS, j = i % GS;
-                s_v[t][j] = a.v[(size_t) t * HV * GS + h * GS + j];
-            }
-            if (tid < T) {
-                s_dec[tid] = a.decay[tid * HV + h];
-                s_beta[tid] = a.beta[tid * HV + h];
-            }
+            const float y = (tid < GS ? s_q : s_k)[t][tid & (GS - 1)];
+            const float sq = wave_sum(y * y);
+            if (lane == 0) s_w[t][wv] = sq;
         }
         __syncthreads();
-
-        // ---- recurrence, state in registers ----
-        float s[32];
-        float* base = a.state + (size_t) h * GS * GS + (size_t) (rg * 32) * GS + col;
-#pragma unroll
-        for (int r = 0; r < 32; ++r) s[r] = base[(size_t) r * GS];
-
         for (int t = 0; t < T; ++t) {
-            const float dec = s_dec[t], beta = s_beta[t];
-            float kv = 0.f;
-#pragma unroll
-            for (int r = 0; r < 32; ++r) {
-                s[r] *= dec;
-                kv = fmaf(s[r], s_k[t][rg * 32 + r], kv);
-            }
-            s_red[rg][col] = kv;
-            __syncthreads();
-            const float kv_col = s_red[0][col] + s_red[1][col] + s_red[2][col] + s_red[3][col];
-            const float delta = (s_v[t][col] - kv_col) * beta;
-            float o = 0.f;
-#pragma unroll
-            for (int r = 0; r < 32; ++r) {
-                s[r] = fmaf(s_k[t][rg * 32 + r], delta, s[r]);
-                o = fmaf(s[r], s_q[t][rg * 32 + r], o);
-            }
-            if (a.state_snaps) {
-                float* sb = a.state_snaps + (size_t) t * HV * GS * GS + (size_t) h * GS * GS + (size_t) (rg * 32) * GS + col;
-#pragma unroll
-                for (int r = 0; r < 32; ++r) sb[(size_t) r * GS] = s[r];
-            }
-            s_red2[rg][col] = o;
-            __syncthreads();
-            float oc = 0.f;
-            if (rg == 0) {                  // waves 0-1 own the 128 output columns
-                oc = (s_red2[0][col] + s_red2[1][col] + s_red2[2][col] + s_red2[3][col]) * 0.08838834764831845f;
-                const float sq = wave_sum(oc * oc);
-                if (lane == 0) s_w[8 + wv] = sq;
-            }
-            __syncthreads();
-            if (rg == 0) {
-                const float ss = s_w[8] + s_w[9];
-                const float scale = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
-                const float zz = a.z ? a.z[(size_t) t * HV * GS + h * GS + col] : 0.0f;
-                const float gate = a.z ? 1.0f / (1.0f + __expf(-zz)) : 1.0f;
-                a.y[(size_t) t * HV * GS + h * GS + col] = oc * scale * gm * gate;
-            }
-            __syncthreads();
+            const float ss = (tid < GS) ? (s_w[t][0] + s_w[t][1]) : (s_w[t][2] + s_w[t][3]);
+            const float r = 1.0f / sqrtf(ss + a.eps);
+            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] *= r;
         }
+    } else {
 #pragma unroll
-        for (int r = 0; r < 32; ++r) base[(size_t) r * GS] = s[r];
-        __syncthreads();                    // s_v / s_dec reuse by the next value head
+        for (int t = 0; t < WZY_MAX_W; ++t) {
+            if (t >= T) break;
+            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = qx[t];
+            if (tid < QC) s_v[t][tid] = vx[t];
+        }
+        if (tid >= GS && tid < GS + T) { s_dec[tid - GS] = g_a; s_beta[tid - GS] = g_b; }
     }
+    __syncthreads();
+
+    // ---- 2. recurrence: thread (column c, row group rg) ----
+    for (int t = 0; t < T; ++t) {
+        const float dec = s_dec[t], beta = s_beta[t];
+        const float4* k4 = (const float4*) &s_k[t][16 * rg];
+        const float4* q4 = (const float4*) &s_q[t][16 * rg];
+        float kv = 0.f;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 kk = k4[r4];
+            s[4 * r4 + 0] *= dec; kv = fmaf(s[4 * r4 + 0], kk.x, kv);
+            s[4 * r4 + 1] *= dec; kv = fmaf(s[4 * r4 + 1], kk.y, kv);
+            s[4 * r4 + 2] *= dec; kv = fmaf(s[4 * r4 + 2], kk.z, kv);
+            s[4 * r4 + 3] *= dec; kv = fmaf(s[4 * r4 + 3], kk.w, kv);
+        }
+        s_kv[rg][c] = kv;
+        __syncthreads();
+        const float kvc = ((s_kv[0][c] + s_kv[1][c]) + (s_kv[2][c] + s_kv[3][c])) +
+                          ((s_kv[4][c] + s_kv[5][c]) + (s_kv[6][c] + s_kv[7][c]));
+        const float delta = (s_v[t][c] - kvc) * beta;
+        float o = 0.f;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const float4 kk = k4[r4], qq = q4[r4];
+            s[4 * r4 + 0] = fmaf(kk.x, delta, s[4 * r4 + 0]); o = fmaf(s[4 * r4 + 0], qq.x, o);
+            s[4 * r4 + 1] = fmaf(kk.y, delta, s[4 * r4 + 1]); o = fmaf(s[4 * r4 + 1], qq.y, o);
+            s[4 * r4 + 2] = fmaf(kk.z, delta, s[4 * r4 + 2]); o = fmaf(s[4 * r4 + 2], qq.z, o);
+            s[4 * r4 + 3] = fmaf(kk.w, delta, s[4 * r4 + 3]); o = fmaf(s[4 * r4 + 3], qq.w, o);
+        }
+        if (a.state_snaps) {
+            float* sb = a.state_snaps + (size_t) t * HV * GS * GS + (size_t) h * GS * GS + (size_t) (16 * rg) * GS + j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sb[(size_t) r * GS] = s[r];
+        }
+        s_o[rg][c] = o;
+        __syncthreads();
+        if (tid < QC) {                                 // wave 0, lanes 0-31: the 32 columns
+            const float oc = (((s_o[0][c] + s_o[1][c]) + (s_o[2][c] + s_o[3][c])) +
+                              ((s_o[4][c] + s_o[5][c]) + (s_o[6][c] + s_o[7][c]))) * 0.08838834764831845f;
+            a.y[(size_t) t * HV * GS + h * GS + j] = oc;
+            const float sq = sum32(oc * oc);
+            if (tid == 0) o_ss[((size_t) t * HV + h) * GDN_NQ + cq] = sq;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sbase[(size_t) r * GS] = s[r];
+
+    // ---- 3. the last workgroup of the key head writes the shared q/k history ----
+    if (FUSED) {
+        if (tid == 0) s_last = qk_order == (HV / HK) * GDN_NQ - 1;
+        __syncthreads();
+        if (s_last) {
+            a.conv_hist[qk_ch * 3 + 0] = qh[0]; a.conv_hist[qk_ch * 3 + 1] = qh[1]; a.conv_hist[qk_ch * 3 + 2] = qh[2];
+            if (tid == 0) __hip_atomic_store(&g_gdn_qk_sync[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// y = o * rsqrt(sum of the head's GDN_NQ partial sums / 128 + eps) * gamma * sigmoid(z), in place.
+__global__ void __launch_bounds__(128) gdn_norm_kernel(float* __restrict__ y, const float* __restrict__ o_ss,
+                                                       const float* __restrict__ z, const float* __restrict__ gamma,
+                                                       float eps, int HV) {
+    const int t = blockIdx.y, h = blockIdx.x, col = threadIdx.x;
+    const size_t i = (size_t) t * HV * GS + (size_t) h * GS + col;
+    y[i] = gdn_norm_gate(y[i], o_ss + ((size_t) t * HV + h) * GDN_NQ, z ? z[i] : 0.0f, z != nullptr,
+                         gamma ? gamma[col] : 1.0f, eps);
 }
 
 namespace wzy {
 int launch_gdn(const GdnArgs& a, bool fused, hipStream_t st) {
     WZY_REQUIRE(a.T >= 1 && a.T <= WZY_MAX_W, "gdn: T out of range");
     WZY_REQUIRE(a.S == GS, "gdn: state dim must be 128");
-    WZY_REQUIRE(a.hk >= 1 && a.hv >= a.hk && a.hv % a.hk == 0 && a.hv <= 1024, "gdn: bad head counts");
+    WZY_REQUIRE(a.hk >= 1 && a.hk <= GDN_MAX_HK && a.hv >= a.hk && a.hv % a.hk == 0 && a.hv <= GDN_MAX_HV,
+                "gdn: bad head counts");
     WZY_REQUIRE(a.state && a.y, "gdn: null state/output");
+    float* ss = a.o_ss;
+    if (!ss) WZY_HIP_TRY(hipGetSymbolAddress((void**) &ss, HIP_SYMBOL(g_gdn_ss)));
+    const dim3 grid(a.hv * GDN_NQ);
     if (fused) {
         WZY_REQUIRE(a.qkv && a.ab && a.dt && a.ssm_a && a.conv_w && a.conv_hist, "gdn: fused mode inputs missing");
-        hipLaunchKernelGGL(gdn_kernel<true>, dim3(a.hk), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(gdn_kernel<true>, grid, dim3(256), 0, st, a, ss);
     } else {
         WZY_REQUIRE(a.q && a.k && a.v && a.decay && a.beta, "gdn: recurrence inputs missing");
-        hipLaunchKernelGGL(gdn_kernel<false>, dim3(a.hk), dim3(512), 0, st, a);
+        hipLaunchKernelGGL(gdn_kernel<false>, grid, dim3(256), 0, st, a, ss);
     }
+    if (!a.o_ss)
+        hipLaunchKernelGGL(gdn_norm_kernel, dim3(a.hv, a.T), dim3(GS), 0, st, a.y, ss, a.z, a.gamma, a.eps, a.hv);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }

@@ -6,6 +6,7 @@
 // RPW*16..32 bytes per lane in flight, and the T window rows reuse every weight load.
 // Partial sums are reduced across the LPR lanes with DPP/swizzle (no LDS).
 #include "wzy_device.h"
+#include "wzy_gdn.h"
 #include "wzy_gemv.h"
 #include "wzy_host.h"
 
@@ -588,6 +589,30 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             if (k == 0) s_xs[(size_t) t * nb + b] = d;
         }
     };
+    // GDN staging transform: x = gdn_norm_gate(o, ss, z, gamma) element-wise (8 columns per item)
+    const GemvGdnIn& gn = segs.gdn;
+    const bool gdn = gn.ss != nullptr;                 // launch-uniform
+    auto gdn_apply = [&](float4& va, float4& vb, const float4& za, const float4& zb, const float4& ga,
+                         const float4& gb, const float4& ssv) {
+        const float ss[4] = {ssv.x, ssv.y, ssv.z, ssv.w};
+        const bool hz = gn.z != nullptr;
+        va = make_float4(gdn_norm_gate(va.x, ss, za.x, hz, ga.x, gn.eps), gdn_norm_gate(va.y, ss, za.y, hz, ga.y, gn.eps),
+                         gdn_norm_gate(va.z, ss, za.z, hz, ga.z, gn.eps), gdn_norm_gate(va.w, ss, za.w, hz, ga.w, gn.eps));
+        vb = make_float4(gdn_norm_gate(vb.x, ss, zb.x, hz, gb.x, gn.eps), gdn_norm_gate(vb.y, ss, zb.y, hz, gb.y, gn.eps),
+                         gdn_norm_gate(vb.z, ss, zb.z, hz, gb.z, gn.eps), gdn_norm_gate(vb.w, ss, zb.w, hz, gb.w, gn.eps));
+    };
+    // the transform's inputs of item (t, r): z at the same place, gamma at column (8r) % 128,
+    // the partial sums of head (8r) / 128
+    auto gdn_load = [&](int t, int r, float4& za, float4& zb, float4& ga, float4& gb, float4& ssv) {
+        const float4 one = make_float4(1.f, 1.f, 1.f, 1.f), zero = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4* zp = (const float4*) (gn.z + (size_t) t * cols + (size_t) r * 8);
+        za = gn.z ? zp[0] : zero;
+        zb = gn.z ? zp[1] : zero;
+        const float4* gp = (const float4*) (gn.gamma + (r * 8) % 128);
+        ga = gn.gamma ? gp[0] : one;
+        gb = gn.gamma ? gp[1] : one;
+        ssv = *(const float4*) (gn.ss + ((size_t) t * (cols / 128) + (r * 8) / 128) * GDN_NQ);
+    };
     {
         // NBL items per thread cover one row (nb*4 <= 256*NBL); nitem % 4 == 0, so a 4-lane group is
         // all in or all out
@@ -600,6 +625,17 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             xa[k] = xp[0];
             xb[k] = xp[1];
         }
+        if (gdn) {
+            float4 za[NBL], zb[NBL], ga[NBL], gb[NBL], ssv[NBL];
+#pragma unroll
+            for (int k = 0; k < NBL; ++k) {
+                const int i = min(tid + 256 * k, nitem - 1);
+                const int t = i / (nb * 4), r = i - t * (nb * 4);
+                gdn_load(t, r, za[k], zb[k], ga[k], gb[k], ssv[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < NBL; ++k) gdn_apply(xa[k], xb[k], za[k], zb[k], ga[k], gb[k], ssv[k]);
+        }
 #pragma unroll
         for (int k = 0; k < NBL; ++k)
             if (tid + 256 * k < nitem) stage(xa[k], xb[k], tid + 256 * k);
@@ -608,7 +644,13 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
         for (int i = tid + 256 * NBL; i < nitem; i += 256) {
             const int t = i / (nb * 4), r = i - t * (nb * 4);
             const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
-            stage(xp[0], xp[1], i);
+            float4 va = xp[0], vb = xp[1];
+            if (gdn) {
+                float4 za, zb, ga, gb, ssv;
+                gdn_load(t, r, za, zb, ga, gb, ssv);
+                gdn_apply(va, vb, za, zb, ga, gb, ssv);
+            }
+            stage(va, vb, i);
         }
     }
     __syncthreads();
@@ -714,6 +756,7 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     const size_t lds = (size_t) T * cols * (((flags & 2) ? 4 : 0) + ((flags & 1) ? 1 : 0)) +
                        ((flags & 1) ? (size_t) T * (cols / 32) * 4 : 0);
     const bool use_lds = lds <= 48 * 1024;
+    WZY_REQUIRE(!segs.gdn.ss || (use_lds && cols % 128 == 0), "gemv_segs: the GDN staging transform needs the LDS path");
     // rows per wave: the LDS kernel holds RPW Q8_0 rows or RPW/2 bf16 rows per wave (RPW = 4 for one
     // 32-block per lane, else 2); the other kernel RPW rows of either kind (4 / 2 / 1)
     const int rpw = nbl == 1 ? 4 : (use_lds || nbl <= 3 ? 2 : 1);

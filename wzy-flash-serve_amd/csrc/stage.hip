@@ -109,6 +109,7 @@ struct wzy_stage {
     float *nsc = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
     float *lo_part = nullptr, *inj_part = nullptr;   // HC read partials (per source stream)
     float *qkv = nullptr, *z = nullptr, *ab = nullptr, *y = nullptr, *block = nullptr, *comb = nullptr;
+    float* gdn_ss = nullptr;     // [W][hv][GDN_NQ] partial sums of the GDN output norm
     float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
     float *att_part = nullptr, *att_ml = nullptr, *att_out = nullptr;
     int *sel_ids = nullptr, *sel_cnt = nullptr;
@@ -339,6 +340,7 @@ int wzy_stage::init_buffers() {
     WZY_TRY(alloc_t(&mixed, (size_t) W * D));
     WZY_TRY(alloc_t(&qkv, (size_t) W * QKV)); WZY_TRY(alloc_t(&z, (size_t) W * GV));
     WZY_TRY(alloc_t(&ab, (size_t) W * 2 * c.gdn_hv)); WZY_TRY(alloc_t(&y, (size_t) W * GV));
+    WZY_TRY(alloc_t(&gdn_ss, (size_t) W * c.gdn_hv * GDN_NQ));
     WZY_TRY(alloc_t(&block, (size_t) W * D)); WZY_TRY(alloc_t(&comb, (size_t) W * D));
     WZY_TRY(alloc_t(&qg, (size_t) W * 2 * QD)); WZY_TRY(alloc_t(&kk, (size_t) W * KVD)); WZY_TRY(alloc_t(&vv, (size_t) W * KVD));
     WZY_TRY(alloc_t(&idx_raw, (size_t) W * c.idx_dim)); WZY_TRY(alloc_t(&q_idx, (size_t) W * c.idx_heads * c.idx_dim));
@@ -364,7 +366,8 @@ int wzy_stage::init_buffers() {
     reg(-1, "act.sel_ids", sel_ids, (size_t) W * c.idx_topk * 4);
     reg(-1, "act.sel_cnt", sel_cnt, (size_t) W * 4);
     reg(-1, "act.att_out", att_out, (size_t) W * QD * 4);
-    reg(-1, "act.y", y, (size_t) W * GV * 4);
+    reg(-1, "act.gdn_o", y, (size_t) W * GV * 4);           // GDN output before its RMS norm and gate
+    reg(-1, "act.gdn_ss", gdn_ss, (size_t) W * c.gdn_hv * GDN_NQ * 4);
     reg(-1, "act.moe_logits", mws.logits, (size_t) W * c.n_exp * 4);
     reg(-1, "act.moe_sg", mws.sg, (size_t) W * 4);
     reg(-1, "act.moe_ids", mws.ids, (size_t) W * c.top_k * 4);
@@ -446,7 +449,7 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             WZY_TRY(launch_gemv_segs(s, mixed, D, T, st));
             GdnArgs g{};
             g.qkv = qkv; g.ab = ab; g.dt = w.dt; g.ssm_a = w.ssm_a; g.conv_w = w.conv_w; g.conv_hist = w.conv_hist;
-            g.z = z; g.gamma = w.ssm_norm; g.eps = c.eps; g.state = w.ssm; g.y = y;
+            g.z = z; g.gamma = w.ssm_norm; g.eps = c.eps; g.state = w.ssm; g.y = y; g.o_ss = gdn_ss;
             g.hk = c.gdn_hk; g.hv = c.gdn_hv; g.S = 128; g.T = T;
             if (save_snaps) {
                 g.hist_snaps = conv_snaps + ((size_t) w.local * WZY_MAX_W + snap_offset) * QKV * 3;
@@ -456,6 +459,7 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             GemvSegs o;
             o.n = 1;
             o.seg[0] = GemvSeg{w.wout.q, w.wout.s, block, D, GEMV_Q8, D, 0};
+            o.gdn.ss = gdn_ss; o.gdn.z = z; o.gdn.gamma = w.ssm_norm; o.gdn.eps = c.eps;   // RMS norm + gate of y
             WZY_TRY(launch_gemv_segs(o, y, GV, T, st));
         } else {
             GemvSegs s;

@@ -24,8 +24,22 @@ struct GdnArgs {
     float eps;
     float* state;            // [HV][S][S] head-major, S[h][i (key)][j (value)]
     float* state_snaps;      // optional [T][HV][S][S]
-    float* y;                // [T][HV*S]
+    float* y;                // [T][HV*S]: the output, or o * 1/sqrt(S) when o_ss is set
+    float* o_ss;             // optional [T][HV][GDN_NQ]: partial sums of (o/sqrt(S))^2 per column
+                             // quarter; set = the caller applies gdn_norm_gate, null = y is final
     int hk, hv, S, T;
 };
+constexpr int GDN_NQ = 4;    // workgroups (column quarters) per value head
+static_assert(GDN_NQ == 4, "gdn_norm_gate sums four partials");
 int launch_gdn(const GdnArgs& a, bool fused, hipStream_t st);
+
+// The RMS norm and output gate of one value of a head from its GDN_NQ partial sums:
+// o * rsqrt(sum/128 + eps) * gamma * sigmoid(z)  (sigmoid(z) = 1 without a gate).
+__device__ __forceinline__ float gdn_norm_gate(float o, const float* ss, float z, bool has_z, float gamma,
+                                               float eps) {
+    const float sum = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+    const float scale = 1.0f / sqrtf(sum * (1.0f / 128.0f) + eps);
+    const float gate = has_z ? 1.0f / (1.0f + __expf(-z)) : 1.0f;
+    return o * scale * gamma * gate;
+}
 }  // namespace wzy

@@ -25,9 +25,19 @@ struct GemvSeg {
 };
 enum { GEMV_Q8 = 0, GEMV_BF16 = 1 };
 constexpr int GEMV_MAX_SEGS = 8;
+// Optional activation transform of the LDS-staged GEMV: x[t][c] is not read as is but computed
+// from a GDN output, x = gdn_norm_gate(o[t][c], ss[t][c/128][..], z[t][c], gamma[c%128]) (the
+// out-projection applies the GDN RMS norm and output gate while staging its input).
+struct GemvGdnIn {
+    const float* ss = nullptr;      // [T][cols/128][GDN_NQ] partial sums of squares (null: off)
+    const float* z = nullptr;       // [T][cols] output gate (null: no gate)
+    const float* gamma = nullptr;   // [128] norm weight (null: 1)
+    float eps = 0.f;
+};
 struct GemvSegs {
     GemvSeg seg[GEMV_MAX_SEGS];
     int n = 0;
+    GemvGdnIn gdn;
 };
 // y_seg = W_seg . x for every segment; x fp32 [T x cols] is quantised per 32 inside each lane for
 // Q8_0 segments (bit-identical to quant_act + gemv_q8).  cols % 32 == 0, cols <= 8192.
