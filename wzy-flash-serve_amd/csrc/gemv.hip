@@ -375,6 +375,7 @@ __device__ __forceinline__ GemvSeg pick_seg(const GemvSegs& segs, int wave) {
         sg.kind = take ? segs.seg[i].kind : sg.kind;
         sg.y_stride = take ? segs.seg[i].y_stride : sg.y_stride;
         sg.wave0 = take ? segs.seg[i].wave0 : sg.wave0;
+        sg.act = take ? segs.seg[i].act : sg.act;
     }
     return sg;
 }
@@ -495,7 +496,7 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float v = wave_sum(acc[s][t]);
-            if (lane == 0 && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
+            if (lane == 0 && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = sg.act == GEMV_ACT_SIGMOID ? gdn_gate(v) : v;
         }
     }
 }
@@ -508,8 +509,9 @@ __global__ void __launch_bounds__(256) gemv_segs_kernel(GemvSegs segs, const flo
 // Registers are kept low so that every workgroup of a launch is resident at once: Q8_0 and bf16
 // weights share one array (a Q8_0 wave holds RPW rows of 32 code bytes per 32-block, a bf16 wave
 // RPW/2 rows of 64 bytes), and x is staged by four threads per 32-column block (8 values each).
-// flags: bit 0 = the launch has Q8_0 segments, bit 1 = it has bf16 segments.
-template <int T, int NBL, int RPW>
+// flags: bit 0 = the launch has Q8_0 segments, bit 1 = it has bf16 segments.  GDN: the staging
+// applies segs.gdn (the GDN output norm and gate) to x.
+template <int T, int NBL, int RPW, bool GDN>
 __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const float* __restrict__ x, int cols,
                                                             int flags) {
     static_assert(RPW % 2 == 0, "a bf16 wave holds RPW/2 rows");
@@ -589,28 +591,29 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             if (k == 0) s_xs[(size_t) t * nb + b] = d;
         }
     };
-    // GDN staging transform: x = gdn_norm_gate(o, ss, z, gamma) element-wise (8 columns per item)
+    // GDN staging transform: x = gdn_norm_gate(o, ss, z, gamma) element-wise (8 columns of one head
+    // per item).  Absent z / gamma read x instead (loads stay unconditional) and are replaced by the
+    // neutral values after the load.
     const GemvGdnIn& gn = segs.gdn;
-    const bool gdn = gn.ss != nullptr;                 // launch-uniform
-    auto gdn_apply = [&](float4& va, float4& vb, const float4& za, const float4& zb, const float4& ga,
-                         const float4& gb, const float4& ssv) {
+    auto gdn_apply = [&](float4& va, float4& vb, float4 za, float4 zb, float4 ga, float4 gb, const float4& ssv) {
         const float ss[4] = {ssv.x, ssv.y, ssv.z, ssv.w};
-        const bool hz = gn.z != nullptr;
-        va = make_float4(gdn_norm_gate(va.x, ss, za.x, hz, ga.x, gn.eps), gdn_norm_gate(va.y, ss, za.y, hz, ga.y, gn.eps),
-                         gdn_norm_gate(va.z, ss, za.z, hz, ga.z, gn.eps), gdn_norm_gate(va.w, ss, za.w, hz, ga.w, gn.eps));
-        vb = make_float4(gdn_norm_gate(vb.x, ss, zb.x, hz, gb.x, gn.eps), gdn_norm_gate(vb.y, ss, zb.y, hz, gb.y, gn.eps),
-                         gdn_norm_gate(vb.z, ss, zb.z, hz, gb.z, gn.eps), gdn_norm_gate(vb.w, ss, zb.w, hz, gb.w, gn.eps));
+        const float sc = gdn_norm_scale(ss, gn.eps);  // one head per item: one scale
+        if (!gn.gamma) ga = gb = make_float4(1.f, 1.f, 1.f, 1.f);
+        auto gate = [&](float z) { return !gn.z ? 1.0f : (gn.z_is_gate ? z : gdn_gate(z)); };
+        va = make_float4(va.x * sc * ga.x * gate(za.x), va.y * sc * ga.y * gate(za.y), va.z * sc * ga.z * gate(za.z),
+                         va.w * sc * ga.w * gate(za.w));
+        vb = make_float4(vb.x * sc * gb.x * gate(zb.x), vb.y * sc * gb.y * gate(zb.y), vb.z * sc * gb.z * gate(zb.z),
+                         vb.w * sc * gb.w * gate(zb.w));
     };
     // the transform's inputs of item (t, r): z at the same place, gamma at column (8r) % 128,
     // the partial sums of head (8r) / 128
     auto gdn_load = [&](int t, int r, float4& za, float4& zb, float4& ga, float4& gb, float4& ssv) {
-        const float4 one = make_float4(1.f, 1.f, 1.f, 1.f), zero = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4* zp = (const float4*) (gn.z + (size_t) t * cols + (size_t) r * 8);
-        za = gn.z ? zp[0] : zero;
-        zb = gn.z ? zp[1] : zero;
-        const float4* gp = (const float4*) (gn.gamma + (r * 8) % 128);
-        ga = gn.gamma ? gp[0] : one;
-        gb = gn.gamma ? gp[1] : one;
+        const float4* zp = (const float4*) ((gn.z ? gn.z : x) + (size_t) t * cols + (size_t) r * 8);
+        za = zp[0];
+        zb = zp[1];
+        const float4* gp = (const float4*) ((gn.gamma ? gn.gamma : x) + (r * 8) % 128);
+        ga = gp[0];
+        gb = gp[1];
         ssv = *(const float4*) (gn.ss + ((size_t) t * (cols / 128) + (r * 8) / 128) * GDN_NQ);
     };
     {
@@ -625,7 +628,7 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             xa[k] = xp[0];
             xb[k] = xp[1];
         }
-        if (gdn) {
+        if constexpr (GDN) {
             float4 za[NBL], zb[NBL], ga[NBL], gb[NBL], ssv[NBL];
 #pragma unroll
             for (int k = 0; k < NBL; ++k) {
@@ -645,7 +648,7 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             const int t = i / (nb * 4), r = i - t * (nb * 4);
             const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
             float4 va = xp[0], vb = xp[1];
-            if (gdn) {
+            if constexpr (GDN) {
                 float4 za, zb, ga, gb, ssv;
                 gdn_load(t, r, za, zb, ga, gb, ssv);
                 gdn_apply(va, vb, za, zb, ga, gb, ssv);
@@ -717,7 +720,8 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const float v = wave_sum(acc[s][t]);
-            if (lane == 0 && s < rpw && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = v;
+            if (lane == 0 && s < rpw && r < sg.rows)
+                sg.y[(size_t) t * sg.y_stride + r] = sg.act == GEMV_ACT_SIGMOID ? gdn_gate(v) : v;
         }
     }
 }
@@ -726,11 +730,20 @@ template <int T>
 static void launch_segs_lds_t(const GemvSegs& segs, int waves, int nbl, const float* x, int cols, int flags,
                               size_t lds, hipStream_t st) {
     const int blocks = (waves + 3) / 4;
+    if (segs.gdn.ss) {
+        switch (nbl) {
+            case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+            case 2: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 2, 2, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+            case 3: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 3, 2, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+            default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 2, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        }
+        return;
+    }
     switch (nbl) {
-        case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
-        case 2: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 2, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
-        case 3: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 3, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
-        default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 2>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4, false>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        case 2: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 2, 2, false>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        case 3: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 3, 2, false>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
+        default: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 4, 2, false>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
     }
 }
 

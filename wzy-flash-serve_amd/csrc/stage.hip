@@ -443,7 +443,7 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             GemvSegs s;
             s.n = 4;
             s.seg[0] = GemvSeg{w.qkv.q, w.qkv.s, qkv, QKV, GEMV_Q8, QKV, 0};
-            s.seg[1] = GemvSeg{w.wgate.q, w.wgate.s, z, GV, GEMV_Q8, GV, 0};
+            s.seg[1] = GemvSeg{w.wgate.q, w.wgate.s, z, GV, GEMV_Q8, GV, 0, GEMV_ACT_SIGMOID};   // z holds sigmoid(z)
             s.seg[2] = GemvSeg{w.alpha, nullptr, ab, c.gdn_hv, GEMV_BF16, 2 * c.gdn_hv, 0};
             s.seg[3] = GemvSeg{w.beta, nullptr, ab + c.gdn_hv, c.gdn_hv, GEMV_BF16, 2 * c.gdn_hv, 0};
             WZY_TRY(launch_gemv_segs(s, mixed, D, T, st));
@@ -459,7 +459,8 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             GemvSegs o;
             o.n = 1;
             o.seg[0] = GemvSeg{w.wout.q, w.wout.s, block, D, GEMV_Q8, D, 0};
-            o.gdn.ss = gdn_ss; o.gdn.z = z; o.gdn.gamma = w.ssm_norm; o.gdn.eps = c.eps;   // RMS norm + gate of y
+            o.gdn.ss = gdn_ss; o.gdn.z = z; o.gdn.z_is_gate = true;             // RMS norm + gate of y
+            o.gdn.gamma = w.ssm_norm; o.gdn.eps = c.eps;
             WZY_TRY(launch_gemv_segs(o, y, GV, T, st));
         } else {
             GemvSegs s;

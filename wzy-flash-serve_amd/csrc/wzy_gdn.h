@@ -35,11 +35,13 @@ int launch_gdn(const GdnArgs& a, bool fused, hipStream_t st);
 
 // The RMS norm and output gate of one value of a head from its GDN_NQ partial sums:
 // o * rsqrt(sum/128 + eps) * gamma * sigmoid(z)  (sigmoid(z) = 1 without a gate).
+__device__ __forceinline__ float gdn_norm_scale(const float* ss, float eps) {
+    const float sum = (ss[0] + ss[1]) + (ss[2] + ss[3]);
+    return 1.0f / sqrtf(sum * (1.0f / 128.0f) + eps);
+}
+__device__ __forceinline__ float gdn_gate(float z) { return 1.0f / (1.0f + __expf(-z)); }
 __device__ __forceinline__ float gdn_norm_gate(float o, const float* ss, float z, bool has_z, float gamma,
                                                float eps) {
-    const float sum = (ss[0] + ss[1]) + (ss[2] + ss[3]);
-    const float scale = 1.0f / sqrtf(sum * (1.0f / 128.0f) + eps);
-    const float gate = has_z ? 1.0f / (1.0f + __expf(-z)) : 1.0f;
-    return o * scale * gamma * gate;
+    return o * gdn_norm_scale(ss, eps) * gamma * (has_z ? gdn_gate(z) : 1.0f);
 }
 }  // namespace wzy

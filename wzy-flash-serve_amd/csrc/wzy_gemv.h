@@ -22,8 +22,10 @@ struct GemvSeg {
     int kind;               // GEMV_Q8 or GEMV_BF16
     int y_stride;
     int wave0;              // first wave of this segment (filled by launch_gemv_segs)
+    int act = 0;            // GEMV_ACT_*: applied to every output of the segment
 };
 enum { GEMV_Q8 = 0, GEMV_BF16 = 1 };
+enum { GEMV_ACT_NONE = 0, GEMV_ACT_SIGMOID = 1 };
 constexpr int GEMV_MAX_SEGS = 8;
 // Optional activation transform of the LDS-staged GEMV: x[t][c] is not read as is but computed
 // from a GDN output, x = gdn_norm_gate(o[t][c], ss[t][c/128][..], z[t][c], gamma[c%128]) (the
@@ -31,6 +33,7 @@ constexpr int GEMV_MAX_SEGS = 8;
 struct GemvGdnIn {
     const float* ss = nullptr;      // [T][cols/128][GDN_NQ] partial sums of squares (null: off)
     const float* z = nullptr;       // [T][cols] output gate (null: no gate)
+    bool z_is_gate = false;         // z already holds sigmoid(z)
     const float* gamma = nullptr;   // [128] norm weight (null: 1)
     float eps = 0.f;
 };
