@@ -128,6 +128,22 @@ size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T
 int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of device workspace wzy_moe_prefill needs for a chunk of n_tok tokens. */
+size_t wzy_moe_prefill_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int n_tok);
+
+/* MoE block for a prefill chunk of n_tok rows of x [n_tok x n_embd] (fp32), on MFMA:
+ * x rounded to bf16 -> router logits (bf16 GEMM) -> softmax top-k per token (the decode rule) ->
+ * entries grouped by expert into 64-token tiles -> routed gate|up (NVFP4 dequantised to bf16 in
+ * LDS) + SwiGLU (bf16) -> down -> comb = sigmoid(sgate.x) * shared(x) + sum_k w_k * expert_k(x);
+ * the shared expert's Q8_0 weights are dequantised to bf16 the same way.  The routed terms are
+ * added with fp32 atomics, so their summation order varies between runs.  n_embd, n_ff multiples
+ * of 64; n_exp a multiple of 64 up to 1024.  ids / wts [n_tok x top_k] may be NULL.
+ * Replaces the prefill MoE of run_stage_prefill: pf_moe_count/scan/tile builders,
+ * pf_moe_gu_wmma_kernel, pf_moe_down_wmma_kernel, pf_init_shared_comb_kernel and the router /
+ * shared-expert dense GEMMs (src/wzy_prefill_tc.cuh:99-443), fp16 replaced by bf16. */
+int wzy_moe_prefill(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, int* ids, float* wts,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Softmax top-k routing alone, over router logits [T x n_exp] (fp32): ids [T x top_k] in rank
  * order (probability descending, ties to the lower expert id) and wts [T x top_k] = p_k /
  * max(sum_k p_k, 2^-14).  The same device routing wzy_moe_block runs inside its gate/up launch.

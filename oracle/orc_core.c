@@ -290,6 +290,101 @@ int orc_moe_block(const orc_moe_weights* w, const float* x, int T, float* comb, 
 }
 
 /* ------------------------------------------------------------------------------------------------
+ * Prefill MoE block with this build's bf16 numerics (the reference prefill, src/wzy_prefill_tc.cuh:
+ * 230-443, computes the same terms in fp16): x rounded to bf16; router logits = bf16 router .
+ * bf16(x) and sg = bf16 sgate . bf16(x); top-k as orc_router_topk; routed expert weights
+ * dequantised exactly (e2m1 * e4m3 scale * tensor scale has at most 8 significant bits, so the
+ * bf16 value is exact); shared Q8_0 weights dequantised and rounded to bf16; SwiGLU outputs
+ * rounded to bf16; comb = sigmoid(sg) * shared + sum_k w_k * expert_k.  Sums in double.
+ * ---------------------------------------------------------------------------------------------- */
+static float round_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+    memcpy(&f, &u, 4);
+    return f;
+}
+/* value k of row `row` of a reference-layout NVFP4 plane with rows of `cols` values */
+static float nvfp4_value(const uint8_t* row, int k, float tscale) {
+    const uint8_t* blk = row + 36 * (k / 64);
+    const int s = (k % 64) / 16, kk = k % 16;
+    const uint8_t* cb = blk + 4 + 8 * s;
+    const int nib = (kk < 8) ? (cb[kk] & 15) : (cb[kk - 8] >> 4);
+    return (float) orc_e2m1x2(nib) * orc_ue4m3_half(blk[s]) * tscale;
+}
+static float q8_bf16_value(const int8_t* q, const uint16_t* s, int cols, int r, int k) {
+    return round_bf16((float) q[(size_t) r * cols + k] * orc_f16_to_f32(s[(size_t) r * (cols / 32) + k / 32]));
+}
+
+int orc_moe_prefill(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts) {
+    const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k;
+    float* xb = (float*) malloc(sizeof(float) * (size_t) D);
+    float* logits = (float*) malloc(sizeof(float) * (size_t) T * E);
+    float* sg = (float*) malloc(sizeof(float) * (size_t) T);
+    float* act = (float*) malloc(sizeof(float) * (size_t) F);
+    double* out = (double*) malloc(sizeof(double) * (size_t) D);
+    int rc = 0;
+    for (int t = 0; t < T; ++t) {
+        for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
+        for (int e = 0; e < E; ++e) {
+            double a = 0.0;
+            for (int d = 0; d < D; ++d) a += (double) orc_bf16_to_f32(w->router[(size_t) e * D + d]) * xb[d];
+            logits[(size_t) t * E + e] = (float) a;
+        }
+        double g = 0.0;
+        for (int d = 0; d < D; ++d) g += (double) orc_bf16_to_f32(w->sgate[d]) * xb[d];
+        sg[t] = (float) g;
+    }
+    orc_router_topk(logits, E, K, T, ids, wts, NULL);
+    for (int t = 0; t < T && rc == 0; ++t) {
+        for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
+        /* shared expert */
+        for (int j = 0; j < F; ++j) {
+            double g = 0.0, u = 0.0;
+            for (int d = 0; d < D; ++d) {
+                g += (double) q8_bf16_value(w->sh_gate_q, w->sh_gate_s, D, j, d) * xb[d];
+                u += (double) q8_bf16_value(w->sh_up_q, w->sh_up_s, D, j, d) * xb[d];
+            }
+            act[j] = round_bf16(silu_f((float) g) * (float) u);
+        }
+        const double gate = (double) sigmoid_f(sg[t]);
+        for (int d = 0; d < D; ++d) {
+            double s = 0.0;
+            for (int j = 0; j < F; ++j) s += (double) q8_bf16_value(w->sh_down_q, w->sh_down_s, F, d, j) * act[j];
+            out[d] = (double) (float) s * gate;
+        }
+        /* routed experts */
+        for (int k = 0; k < K; ++k) {
+            const int e = ids[t * K + k];
+            const uint8_t* blob = w->blobs ? w->blobs[e] : NULL;
+            if (!blob) { rc = -1; break; }
+            const int gu_row = D / 64 * 36, d_row = F / 64 * 36;
+            const float* tail = (const float*) (blob + orc_blob_bytes(D, F) - 16);
+            for (int j = 0; j < F; ++j) {
+                double g = 0.0, u = 0.0;
+                const uint8_t* rg = blob + (size_t) j * gu_row;
+                const uint8_t* ru = blob + (size_t) (F + j) * gu_row;
+                for (int d = 0; d < D; ++d) {
+                    g += (double) nvfp4_value(rg, d, tail[0]) * xb[d];
+                    u += (double) nvfp4_value(ru, d, tail[1]) * xb[d];
+                }
+                act[j] = round_bf16(silu_f((float) g) * (float) u);
+            }
+            const uint8_t* dn = blob + (size_t) 2 * F * gu_row;
+            for (int d = 0; d < D; ++d) {
+                double s = 0.0;
+                const uint8_t* rd = dn + (size_t) d * d_row;
+                for (int j = 0; j < F; ++j) s += (double) nvfp4_value(rd, j, tail[2]) * act[j];
+                out[d] += (double) wts[t * K + k] * (double) (float) s;
+            }
+        }
+        for (int d = 0; d < D; ++d) comb[(size_t) t * D + d] = (float) out[d];
+    }
+    free(xb); free(logits); free(sg); free(act); free(out);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------------------------------
  * logit reductions: row_argmax_multi_kernel / row_top16_multi_kernel
  * (src/wzy_kernels_v2.cuh:1873-1984): larger value wins, ties -> lower vocab id.
  * ---------------------------------------------------------------------------------------------- */

@@ -74,6 +74,10 @@ typedef const uint8_t* (*orc_blob_fn)(void* ctx, int layer, int expert);
 int orc_moe_block_fn(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                      float* logits_out, float* sg_out, orc_blob_fn blob_fn, void* blob_ctx, int layer);
 
+/* Prefill MoE block with bf16 numerics (see orc_core.c); needs every routed blob in w->blobs.
+ * Returns 0, or -1 if a routed blob is NULL. */
+int orc_moe_prefill(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts);
+
 /* ---- hyper-connection read (src/wzy_kernels_v2.cuh:409-454,632-827): see orc_layers.c ---- */
 void orc_hc_read(const float* R_in, const float* emb_rows, const float* bo, const float* inj_prev, const float* norm_w,
                  const int8_t* down_q, const uint16_t* down_s, const uint16_t* inj_w, const int8_t* up_q,

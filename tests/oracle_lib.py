@@ -29,6 +29,7 @@ _SIGS = {
     "orc_expert_gate_up": (None, [P, I32, I32, P, P, P, P, P]),
     "orc_expert_down": (None, [P, I32, I32, P, P, P]),
     "orc_moe_block": (I32, [C.POINTER(OrcMoeWeights), P, I32, P, P, P, P, P]),
+    "orc_moe_prefill": (I32, [C.POINTER(OrcMoeWeights), P, I32, P, P, P]),
     "orc_hc_read": (None, [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, P, P, P, P]),
     "orc_gdn_step": (None, [P, P, P, P, P, P, P, P, P, F32, P, I32, I32, I32]),
     "orc_gdn_recurrence": (None, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32]),

@@ -325,3 +325,105 @@ def test_moe_time_kernels_bursts(wz, gpu):
     after = run_gpu_moe(wz, layers[0], x, T)
     for a, b in zip(before, after):
         assert np.array_equal(a, b)
+
+
+def run_gpu_prefill(wz, w, x, N):
+    D, K = w.n_embd, w.top_k
+    xd = dev(x.reshape(N, D))
+    comb = DA(N * D, np.float32)
+    ids = DA(N * K, np.int32)
+    wts = DA(N * K, np.float32)
+    nws = wz.wzy_moe_prefill_workspace_bytes(D, w.n_ff, w.n_exp, K, N)
+    ws = DA(nws, np.uint8)
+    wz.wzy_moe_prefill(C.byref(w), xd.ptr, N, comb.ptr, ids.ptr, wts.ptr, ws.ptr, nws, None)
+    wz.wzy_device_sync()
+    return host(comb), host(ids), host(wts)
+
+
+def prefill_logits(m, x):
+    """Router logits of bf16-rounded rows (the prefill path's A operand), fp64 sums."""
+    X = bf16_round64(x.reshape(-1, m.D))
+    R = (m.router.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(m.E, m.D)
+    return (X @ R.T).astype(np.float32)
+
+
+def bf16_round64(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("D,F,E,K,N", [
+    (256, 128, 64, 4, 1),          # one token, one partial row tile
+    (256, 128, 64, 4, 130),        # ragged: 3 row tiles, the last of 2 rows
+    (256, 128, 64, 8, 600),        # experts with more than 64 entries -> several tiles per expert
+    (512, 192, 128, 6, 77),
+])
+def test_moe_prefill_parity(wz, orc, gpu, D, F, E, K, N):
+    """Chunked-prefill MoE block (MFMA, NVFP4 -> bf16) against the bf16 prefill oracle."""
+    print(f"prefill D={D} F={F} E={E} K={K} N={N}", flush=True)
+    m = mi.make_layer(wz, 31, 2, D, F, E, K)
+    x = (mi.make_x(wz, 31, 2, N, D) * 1.37 + 0.01).astype(np.float32)     # not bf16 already
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    comb_o = np.empty(N * D, np.float32); ids_o = np.empty(N * K, np.int32); wts_o = np.empty(N * K, np.float32)
+    assert orc.orc_moe_prefill(C.byref(ow), ptr(x.ravel()), N, ptr(comb_o), ptr(ids_o), ptr(wts_o)) == 0
+    w, keep = device_layer(wz, m)
+    comb, ids, wts = run_gpu_prefill(wz, w, x, N)
+    logits = prefill_logits(m, x).ravel()
+    exact = check_ids(orc, logits, E, K, N, ids, ids_o)
+    assert exact >= N - max(1, N // 50), (exact, N)
+    rows = np.array([np.array_equal(ids[t * K:(t + 1) * K], ids_o[t * K:(t + 1) * K]) for t in range(N)])
+    wr = np.repeat(rows, K)
+    np.testing.assert_allclose(wts[wr], wts_o[wr], rtol=1e-4, atol=1e-6)
+    cr = np.repeat(rows, D)
+    np.testing.assert_allclose(comb[cr], comb_o[cr], rtol=2e-2, atol=1e-2)
+    err = np.abs(comb[cr] - comb_o[cr]).max() / np.abs(comb_o[cr]).max()
+    assert err < 3e-3, err
+    # a second call on the same workspace (tile table and counts rebuilt, comb re-initialised)
+    # (the routed down-projection adds with float atomics: comb may differ in its last bits)
+    c2, i2, w2 = run_gpu_prefill(wz, w, x, N)
+    np.testing.assert_array_equal(i2, ids)
+    np.testing.assert_array_equal(w2, wts)
+    np.testing.assert_allclose(c2, comb, rtol=1e-5, atol=1e-5 * np.abs(comb).max())
+
+
+def test_moe_prefill_config1_shape(wz, orc, gpu):
+    """The BASELINE layer shape (D=2048, 512 experts top-10, NFF=512) on an 8-token chunk."""
+    D, F, E, K, N = 2048, 512, 512, 10, 8
+    print(f"prefill config1 shape N={N}", flush=True)
+    m = mi.make_layer(wz, 0, 3, D, F, E, K, blobs=[])
+    x = mi.make_x(wz, 0, 3, N, D)
+    logits = prefill_logits(m, x)
+    need = set()
+    for t in range(N):
+        need.update(np.argsort(-logits[t], kind="stable")[:K + 4].tolist())
+    for e in need:
+        m.blobs[e] = mi.expert_blob(wz, 0, 3, e, D, F)
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    comb_o = np.empty(N * D, np.float32); ids_o = np.empty(N * K, np.int32); wts_o = np.empty(N * K, np.float32)
+    assert orc.orc_moe_prefill(C.byref(ow), ptr(x.ravel()), N, ptr(comb_o), ptr(ids_o), ptr(wts_o)) == 0
+    w, keep = device_layer(wz, m)
+    comb, ids, wts = run_gpu_prefill(wz, w, x, N)
+    assert check_ids(orc, logits.ravel(), E, K, N, ids, ids_o) == N
+    np.testing.assert_allclose(wts, wts_o, rtol=1e-4)
+    np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
+    err = np.abs(comb - comb_o).max() / np.abs(comb_o).max()
+    assert err < 3e-3, err
+
+
+def test_moe_prefill_rejects_bad_shapes(wz, gpu):
+    D, F, E, K = 256, 128, 48, 4                  # 48 experts: not a multiple of 64
+    m = mi.make_layer(wz, 1, 0, D, F, 64, K, blobs=[])
+    w, keep = device_layer(wz, m)
+    w.n_exp = E
+    x = dev(np.zeros((2, D), np.float32))
+    out = DA(2 * D, np.float32)
+    nws = wz.wzy_moe_prefill_workspace_bytes(D, F, 64, K, 2)
+    ws = DA(nws, np.uint8)
+    with pytest.raises(wzy_amd.WzyError):
+        wz.wzy_moe_prefill(C.byref(w), x.ptr, 2, out.ptr, None, None, ws.ptr, nws, None)
+    w.n_exp = 64
+    with pytest.raises(wzy_amd.WzyError):
+        wz.wzy_moe_prefill(C.byref(w), x.ptr, 2, out.ptr, None, None, ws.ptr, 16, None)

@@ -139,6 +139,46 @@ def test_moe_block_composition(orc, wz):
     np.testing.assert_allclose(wts.reshape(T, K).sum(1), 1.0, rtol=1e-6)
 
 
+def bf16_round64(a):
+    """float32 -> bf16 (round to nearest even) -> float64, through numpy bit operations."""
+    u = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return u.view(np.float32).astype(np.float64)
+
+
+def test_moe_prefill_composition(orc, wz):
+    """The prefill oracle against a numpy restatement built from the pinned decoders: bf16 x,
+    exact NVFP4 values, Q8_0 weights rounded to bf16, SwiGLU rounded to bf16."""
+    D, F, E, K, T = 256, 128, 16, 4, 5
+    m = mi.make_layer(wz, 5, 1, D, F, E, K)
+    x = mi.make_x(wz, 5, 1, T, D)
+    x = (x * 1.37 + 0.01).astype(np.float32)            # not already bf16: the rounding matters
+    arr = mi.blob_ptr_array(m)
+    w = mi.orc_weights(oracle_lib, m, arr)
+    comb = np.empty(T * D, np.float32); ids = np.empty(T * K, np.int32); wts = np.empty(T * K, np.float32)
+    assert orc.orc_moe_prefill(C.byref(w), ptr(x.ravel()), T, ptr(comb), ptr(ids), ptr(wts)) == 0
+    X = bf16_round64(x)
+    logits = (X @ refmath.bf16_bits_to_f64(m.router).reshape(E, D).T).astype(np.float32)
+    i2 = np.empty(T * K, np.int32); w2 = np.empty(T * K, np.float32)
+    orc.orc_router_topk(ptr(logits.ravel()), E, K, T, ptr(i2), ptr(w2), None)
+    np.testing.assert_array_equal(ids, i2)
+    np.testing.assert_allclose(wts, w2, rtol=1e-6)
+    sg = X @ refmath.bf16_bits_to_f64(m.sgate)
+    Wg = bf16_round64(refmath.q8_dense(*m.sh["gate"], F, D)); Wu = bf16_round64(refmath.q8_dense(*m.sh["up"], F, D))
+    Wd = bf16_round64(refmath.q8_dense(*m.sh["down"], D, F))
+    for t in range(T):
+        g, u = Wg @ X[t], Wu @ X[t]
+        a = bf16_round64(g / (1 + np.exp(-g)) * u)
+        acc = (Wd @ a) / (1 + np.exp(-sg[t]))
+        for k in range(K):
+            gate, up, down = refmath.blob_dense(m.blobs[ids[t * K + k]], D, F)
+            assert np.array_equal(bf16_round64(gate), gate)      # NVFP4 values are exact in bf16
+            ge, ue = gate @ X[t], up @ X[t]
+            ae = bf16_round64(ge / (1 + np.exp(-ge)) * ue)
+            acc = acc + wts[t * K + k] * (down @ ae)
+        np.testing.assert_allclose(comb[t * D:(t + 1) * D], acc, rtol=1e-4, atol=1e-4 * np.abs(acc).max())
+
+
 def test_cpu_pool_matches_oracle_experts(orc, wz):
     D, F, E, K, T = 512, 128, 32, 6, 2
     m = mi.make_layer(wz, 13, 1, D, F, E, K)

@@ -10,6 +10,23 @@
 
 namespace wzy {
 
+// Byte offsets of the planes of one expert record (wzy_nvfp4_expert_bytes): gate|up codes
+// [2F x D/2], gate|up e4m3 scales [2F x D/16], down codes [D x F/2], down scales [D x F/16], fp32
+// tensor scales (gate, up, down, unused).
+struct MoeOffsets {
+    size_t gu_codes, gu_scales, dn_codes, dn_scales, tail, rec;
+};
+__host__ __device__ inline MoeOffsets moe_offsets(int D, int F) {
+    MoeOffsets o;
+    o.gu_codes = 0;
+    o.gu_scales = (size_t) 2 * F * (D / 2);
+    o.dn_codes = o.gu_scales + (size_t) 2 * F * (D / 16);
+    o.dn_scales = o.dn_codes + (size_t) D * (F / 2);
+    o.tail = o.dn_scales + (size_t) D * (F / 16);
+    o.rec = o.tail + 16;
+    return o;
+}
+
 // Device scratch of one MoE block call, carved from a workspace.
 struct MoeWs {
     float* logits; float* sg;             // router logits [T x E], shared gate scalar [T]
