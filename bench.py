@@ -13,7 +13,10 @@ Beside the tok/s line it reports
                 timed live with HIP events on the stage's own stream, against 8 TB/s;
   cpu_baseline  the AVX2/FMA restatement of the reference CPU MoE pool (oracle/cpu_moe_pool.cpp)
                 on BASELINE config 1 (one token, 10 routed experts), timed on this host for a
-                bounded ~10 s sample.
+                bounded ~10 s sample;
+  prefill_moe   BASELINE config 5's chunked-prefill MoE block (8,192 tokens, one layer) on MFMA:
+                per-launch-group HIP event times, routed-expert TFLOP/s against the 2.5 PFLOP/s
+                dense bf16 MFMA peak.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
@@ -37,6 +40,48 @@ GU_BYTES = K * (2 * F * D // 2 + 2 * F * D // 16 + 16) + (2 * F * D + 2 * F * D 
 DN_BYTES = K * (D * F // 2 + D * F // 16) + (D * F + D * F // 32 * 2) + K * (F + F // 16 * 4) + D * 4
 # routed-expert bytes of one token-layer (the BASELINE config-1 roofline basis)
 ROUTED_BYTES = K * (3 * F * D // 2 + 3 * F * D // 16 + 16)
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PF_STAGES = ("x_to_bf16", "router_gemm", "route", "tiles", "shared_gate_up", "shared_down", "routed_gate_up",
+             "routed_down")
+
+
+def prefill_moe(wz, st, n_tok, iters, seed):
+    """Config-5 chunked-prefill MoE on layer 0 of the loaded stage: n_tok rows of N(0,1) x, every
+    launch group timed with HIP events (wzy_moe_prefill_time)."""
+    import numpy as np
+    import wzy_amd
+    w = wzy_amd.MoeWeights()
+    wz.wzy_stage_moe_weights(st.h, 0, C.byref(w))
+    x = np.random.default_rng(seed).standard_normal((n_tok, D), dtype=np.float32)
+    xd = wzy_amd.DeviceArray.from_numpy(x)
+    comb = wzy_amd.DeviceArray(n_tok * D, np.float32)
+    nws = wz.wzy_moe_prefill_workspace_bytes(D, F, E, K, n_tok)
+    ws = wzy_amd.DeviceArray(nws, np.uint8)
+    us = (C.c_float * len(PF_STAGES))()
+    wz.wzy_moe_prefill_time(C.byref(w), xd.ptr, n_tok, comb.ptr, ws.ptr, nws, iters, us, None)
+    for a in (xd, comb, ws):
+        a.free()
+    st_us = {k: round(us[i], 2) for i, k in enumerate(PF_STAGES)}
+    total = sum(us[i] for i in range(len(PF_STAGES)))
+    routed_us = us[6] + us[7]
+    routed_flop = 2.0 * n_tok * K * D * 3 * F            # gate+up (2F rows) and down (F cols)
+    block_flop = routed_flop + 2.0 * n_tok * (E * D + 3 * F * D)
+    gu_flop = 2.0 * n_tok * K * D * 2 * F
+    return {
+        "workload": "config 5 chunked-prefill MoE block, one layer (D=2048, 512 experts top-10, NFF=512, "
+                    "shared expert), %d tokens" % n_tok,
+        "n_tok": n_tok, "iters": iters, "us_total": round(total, 1),
+        "tok_s_layer": round(n_tok / (total * 1e-6), 0),
+        "routed_gflop": round(routed_flop / 1e9, 1),
+        "routed_tflops": round(routed_flop / (routed_us * 1e-6) / 1e12, 1),
+        "routed_frac": round(routed_flop / (routed_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "routed_gate_up_tflops": round(gu_flop / (us[6] * 1e-6) / 1e12, 1),
+        "block_tflops": round(block_flop / (total * 1e-6) / 1e12, 1),
+        "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+        "us_stages": st_us,
+    }
 
 
 def cpu_threads():
@@ -139,6 +184,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graphs", action="store_true", help="direct kernel launches instead of graph replay")
+    ap.add_argument("--prefill-tokens", type=int, default=8192, help="config-5 prefill MoE chunk (0: skip)")
+    ap.add_argument("--prefill-iters", type=int, default=5)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, 3 device-to-device copies of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
@@ -197,6 +244,11 @@ def main():
     wz.wzy_stage_time_moe(st.h, args.moe_iters, C.byref(us_gu), C.byref(us_dn))
     gu_gbs = GU_BYTES / (us_gu.value * 1e-6) / 1e9
     dn_gbs = DN_BYTES / (us_dn.value * 1e-6) / 1e9
+    pf = None
+    if args.prefill_tokens > 0:
+        pf = prefill_moe(wz, st, args.prefill_tokens, args.prefill_iters, args.seed)
+        print("bench: prefill MoE %d tokens: %.1f us" % (args.prefill_tokens, pf["us_total"]), file=sys.stderr,
+              flush=True)
     st.close()
 
     if args.calib_copy_mib > 0:
@@ -247,6 +299,7 @@ def main():
             "moe_routed_gbs": round(ROUTED_BYTES / ((us_gu.value + us_dn.value) * 1e-6) / 1e9, 1),
         },
         "cpu_baseline": cpu,
+        "prefill_moe": pf,
         "greedy_tokens_head": toks[:8],
     }
     print(json.dumps(out), flush=True)

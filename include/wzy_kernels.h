@@ -133,16 +133,25 @@ size_t wzy_moe_prefill_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_
 
 /* MoE block for a prefill chunk of n_tok rows of x [n_tok x n_embd] (fp32), on MFMA:
  * x rounded to bf16 -> router logits (bf16 GEMM) -> softmax top-k per token (the decode rule) ->
- * entries grouped by expert into 64-token tiles -> routed gate|up (NVFP4 dequantised to bf16 in
- * LDS) + SwiGLU (bf16) -> down -> comb = sigmoid(sgate.x) * shared(x) + sum_k w_k * expert_k(x);
- * the shared expert's Q8_0 weights are dequantised to bf16 the same way.  The routed terms are
- * added with fp32 atomics, so their summation order varies between runs.  n_embd, n_ff multiples
- * of 64; n_exp a multiple of 64 up to 1024.  ids / wts [n_tok x top_k] may be NULL.
+ * entries grouped by expert into tiles of up to 128 -> routed gate|up (NVFP4 dequantised to bf16
+ * MFMA operands; the fp32 tensor scale applied to the accumulators) + SwiGLU (bf16) -> down, fp32
+ * per entry -> comb = sigmoid(sgate.x) * shared(x) + sum_k w_k * expert_k(x), summed per token in
+ * slot order (results do not depend on the order entries reach their expert); the shared expert's
+ * Q8_0 weights are dequantised to bf16 (rounded).  n_embd a multiple of 256, n_ff a multiple of
+ * 128, n_exp a multiple of 64 up to 1024.  ids / wts [n_tok x top_k] may be NULL.
  * Replaces the prefill MoE of run_stage_prefill: pf_moe_count/scan/tile builders,
  * pf_moe_gu_wmma_kernel, pf_moe_down_wmma_kernel, pf_init_shared_comb_kernel and the router /
  * shared-expert dense GEMMs (src/wzy_prefill_tc.cuh:99-443), fp16 replaced by bf16. */
 int wzy_moe_prefill(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, int* ids, float* wts,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Measurement: `iters` runs of wzy_moe_prefill (after one untimed run) with HIP events between
+ * its launch groups on `stream`; us_stages[8] = mean microseconds of
+ *   0 x -> bf16, 1 router GEMM, 2 routing + shared gate, 3 expert tiles and entry lists,
+ *   4 shared gate|up, 5 shared down, 6 routed gate|up, 7 routed down + per-token combine.
+ * Counterpart of the reference's WZY_PF_PROF phase timers (src/wzy_prefill_tc.cuh:734-741). */
+int wzy_moe_prefill_time(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, void* workspace,
+                         size_t workspace_bytes, int iters, float* us_stages, void* stream);
 
 /* Softmax top-k routing alone, over router logits [T x n_exp] (fp32): ids [T x top_k] in rank
  * order (probability descending, ties to the lower expert id) and wts [T x top_k] = p_k /

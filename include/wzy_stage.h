@@ -22,6 +22,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "wzy_kernels.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -107,6 +109,11 @@ int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const voi
  * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the
  * last forward's rows) -> mean microseconds of the gate/up launch and of the down launch. */
 int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down);
+
+/* Measurement support (no reference counterpart): the device pointers of one layer's MoE weights
+ * (router, shared gate, shared expert, expert records), for the standalone MoE entry points of
+ * wzy_kernels.h.  The pointers stay valid until wzy_stage_destroy. */
+int wzy_stage_moe_weights(wzy_stage* st, int layer, wzy_moe_weights* out);
 
 #ifdef __cplusplus
 }

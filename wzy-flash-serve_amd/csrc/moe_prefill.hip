@@ -28,45 +28,48 @@ using namespace wzy;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 namespace {
 
-constexpr int PB = 64;             // tile rows (M), weight rows (N) and K step
+constexpr int PB = 64;             // dense GEMM: tile rows (M), weight rows (N) and K step
 constexpr int PB_LD = PB + 8;      // LDS row stride in bf16 (16-byte aligned rows, staggered banks)
 constexpr int PF_MAX_E = 1024;
+constexpr int MT = 128;            // expert GEMM: entries per tile (4 MFMA row blocks of 32)
+constexpr int EK = 32;             // expert GEMM: K step (two MFMA k16 slices)
+constexpr int EA_LD = EK + 8;      // LDS row stride of the staged activations, bf16
 
-enum { PW_BF16 = 0, PW_Q8 = 1, PW_FP4 = 2 };                        // weight formats
-enum { PE_F32 = 0, PE_SWIGLU = 1, PE_ATOMIC = 2, PE_SHARED = 3 };   // epilogues
+enum { PW_BF16 = 0, PW_Q8 = 1 };                      // dense weight formats
+enum { PE_F32 = 0, PE_SWIGLU = 1, PE_SHARED = 2 };    // dense epilogues
 
 struct PfTile {
-    int e, off, cnt, pad;          // expert, first entry, entries (<= 64)
+    int e, off, cnt, pad;          // expert, first entry position, entries (<= MT)
 };
 
+// Dense GEMM y = A . W^T over rows m0 .. m0+63 of A [a_rows x K] (bf16).
 struct PfGemmArgs {
-    // A: bf16 activation rows of length K.  Dense: rows m0 .. m0+63 of [a_rows x K].  Expert tiles:
-    // entry rows off .. off+cnt-1, either gathered from a through tok (entry -> token) or read from
-    // a directly (a_by_entry).
     const uint16_t* a;
     int a_rows, K;
-    const int* tok;
-    bool a_by_entry;
-    // B: weight rows of length K.  BF16 / Q8: w (+ ws fp16 scales per 32) and, for SwiGLU, w2/ws2
-    // for the up rows.  FP4: expert records, codes/scales plane offsets, first row of the plane.
+    // weight rows of length K: bf16, or Q8_0 codes + fp16 scales per 32; SwiGLU: w2/ws2 = up rows
     const void* w; const uint16_t* ws;
     const void* w2; const uint16_t* ws2;
+    int n_rows;                    // weight rows (F32 epilogue bound)
+    float* y; int y_ld;            // F32 / SHARED: y[row * y_ld + n]
+    uint16_t* act; int act_ld;     // SWIGLU: act[row * act_ld + j]
+    const float* sg;               // SHARED: gate scalar per row
+};
+
+// Routed-expert GEMM over expert tiles.  Gate|up: A rows = x rows of the entries' tokens, output
+// SwiGLU activations per entry; down: A rows = activations per entry, output fp32 per entry.
+struct PfExpArgs {
     const uint8_t* experts;
     size_t rec, codes_off, scales_off, tail_off;
-    int tail_gate, tail_up;        // tensor scale index of the gate (or only) rows and of the up rows
-    int up_row0;                   // FP4 SwiGLU: first up row of the plane (= F)
-    int n_rows;                    // weight rows (dense F32 epilogue bound)
-    // expert tiles (null: dense)
-    const PfTile* tiles;
-    const int* n_tiles;
-    // outputs
-    float* y; int y_ld;            // F32 / SHARED / ATOMIC: y[row * y_ld + n]
-    uint16_t* act; int act_ld;     // SWIGLU: act[(row) * act_ld + j]
-    const float* wt;               // ATOMIC: weight of each entry
-    const float* sg;               // SHARED: gate scalar per token
+    int K;                         // reduction length: n_embd (gate|up) or n_ff (down)
+    int F;                         // gate|up: first up row of the plane
+    int gx;                        // column blocks per tile
+    const PfTile* tiles; const int* n_tiles;
+    const uint16_t* a; const int* tok;
+    uint16_t* act; float* y; int ld_out;
 };
 
 WZY_DEV uint16_t f_to_bf16(float f) {                // round to nearest even (finite inputs)
@@ -74,63 +77,37 @@ WZY_DEV uint16_t f_to_bf16(float f) {                // round to nearest even (f
     return (uint16_t) ((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 WZY_DEV float bf16_bits_to_f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+WZY_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
-// Weight chunk of one staging thread: 16 consecutive k of one weight row, as bf16.
-template <int WK>
+// Weight chunk of one dense staging thread: 16 consecutive k of one weight row.
 struct WRaw {
-    uint4 u[2];                    // BF16: 2 x 8 bf16; Q8: u[0] = 16 int8; FP4: u[0].x/.y = 8 code bytes
-    uint32_t s;                    // Q8: fp16 scale bits; FP4: e4m3 scale byte
+    uint4 u[2];                    // BF16: 2 x 8 bf16; Q8: u[0] = 16 int8
+    uint32_t s;                    // Q8: fp16 scale bits
 };
 
 template <int WK>
-WZY_DEV WRaw<WK> load_w(const PfGemmArgs& a, const uint8_t* rec, int row, bool up, int k0) {
-    WRaw<WK> r;
-    if constexpr (WK == PW_FP4) {
-        const uint8_t* cp = rec + a.codes_off + (size_t) row * (a.K / 2) + (size_t) (k0 / 16) * 8;
-        const uint2 c = *(const uint2*) cp;
-        r.u[0] = make_uint4(c.x, c.y, 0u, 0u);
-        r.s = rec[a.scales_off + (size_t) row * (a.K / 16) + k0 / 16];
-    } else if constexpr (WK == PW_Q8) {
+WZY_DEV WRaw load_w(const PfGemmArgs& a, int row, bool up, int k0) {
+    WRaw r;
+    if constexpr (WK == PW_Q8) {
         const int8_t* q = (const int8_t*) (up ? a.w2 : a.w);
         const uint16_t* sc = up ? a.ws2 : a.ws;
         r.u[0] = *(const uint4*) (q + (size_t) row * a.K + k0);
+        r.u[1] = make_uint4(0, 0, 0, 0);
         r.s = sc[(size_t) row * (a.K / 32) + k0 / 32];
     } else {
         const uint16_t* w = (const uint16_t*) (up ? a.w2 : a.w);
         const uint4* p = (const uint4*) (w + (size_t) row * a.K + k0);
         r.u[0] = p[0];
         r.u[1] = p[1];
+        r.s = 0;
     }
     return r;
 }
 
-// dequantise to 16 bf16 (two uint4 in k order)
+// dequantise to 16 bf16 (two uint4 in k order); Q8_0 values code * fp16 scale rounded to bf16
 template <int WK>
-WZY_DEV void dequant_w(const WRaw<WK>& r, float tscale, uint4 (&o)[2]) {
-    if constexpr (WK == PW_FP4) {
-        // byte j of the sub-block: value j in the low nibble, value j+8 in the high nibble
-        const float sc = ue4m3_half(r.s) * 2.0f * tscale;
-        uint16_t v[16];
-        const uint32_t w0 = r.u[0].x, w1 = r.u[0].y;
-        bf16x2_t p[8];
-        p[0] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, 1.0f, 0);
-        p[1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, 1.0f, 1);
-        p[2] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, 1.0f, 2);
-        p[3] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w0, 1.0f, 3);
-        p[4] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w1, 1.0f, 0);
-        p[5] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w1, 1.0f, 1);
-        p[6] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w1, 1.0f, 2);
-        p[7] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w1, 1.0f, 3);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = f_to_bf16((float) p[j].x * sc);
-            v[j + 8] = f_to_bf16((float) p[j].y * sc);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            o[h] = make_uint4(v[8 * h] | ((uint32_t) v[8 * h + 1] << 16), v[8 * h + 2] | ((uint32_t) v[8 * h + 3] << 16),
-                              v[8 * h + 4] | ((uint32_t) v[8 * h + 5] << 16), v[8 * h + 6] | ((uint32_t) v[8 * h + 7] << 16));
-    } else if constexpr (WK == PW_Q8) {
+WZY_DEV void dequant_w(const WRaw& r, uint4 (&o)[2]) {
+    if constexpr (WK == PW_Q8) {
         const float sc = h16_to_f((uint16_t) r.s);
         const uint32_t q[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w};
         uint16_t v[16];
@@ -146,39 +123,22 @@ WZY_DEV void dequant_w(const WRaw<WK>& r, float tscale, uint4 (&o)[2]) {
     }
 }
 
+// Dense GEMM tile: 64 rows x 64 weight rows (SwiGLU: 32 gate + the matching 32 up rows), K stepped
+// by 64 through two LDS buffers, each wave a 32 x 32 block.
 template <int WK, int EPI>
 __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
     __shared__ __align__(16) uint16_t sA[2][PB][PB_LD];
     __shared__ __align__(16) uint16_t sB[2][PB][PB_LD];
-    __shared__ int s_tok[PB];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w & 1, wn = w >> 1;
-
-    // ---- tile ----
-    int e = 0, row0 = 0, cnt = 0;
-    if (a.tiles) {
-        if ((int) blockIdx.y >= *a.n_tiles) return;               // workgroup-uniform
-        const PfTile t = a.tiles[blockIdx.y];
-        e = t.e; row0 = t.off; cnt = t.cnt;
-    } else {
-        row0 = blockIdx.y * PB;
-        cnt = min(PB, a.a_rows - row0);
-    }
-    if (tid < PB) s_tok[tid] = (a.tiles && tid < cnt) ? a.tok[row0 + tid] : 0;
-    const uint8_t* rec = a.experts ? a.experts + (size_t) e * a.rec : nullptr;
-    // weight rows of this workgroup: SwiGLU = 32 gate rows j0.. and the matching 32 up rows
+    const int row0 = blockIdx.y * PB;
+    const int cnt = min(PB, a.a_rows - row0);
     const int n0 = EPI == PE_SWIGLU ? blockIdx.x * 32 : blockIdx.x * PB;
     const int sr = tid >> 2, sk = (tid & 3) * 16;                // staging: row sr, k sk .. sk+15
     const bool up = EPI == PE_SWIGLU && sr >= 32;
-    const int wrow = EPI == PE_SWIGLU ? (up ? (WK == PW_FP4 ? a.up_row0 : 0) + n0 + sr - 32 : n0 + sr)
-                                      : min(n0 + sr, a.n_rows - 1);
-    float tsc = 1.0f;
-    if constexpr (WK == PW_FP4) tsc = ((const float*) (rec + a.tail_off))[up ? a.tail_up : a.tail_gate];
-    __syncthreads();
-    // A row of this staging thread (zero beyond the tile)
+    const int wrow = EPI == PE_SWIGLU ? n0 + sr - (up ? 32 : 0) : min(n0 + sr, a.n_rows - 1);
     const bool a_ok = sr < cnt;
-    const int arow = a.tiles ? (a.a_by_entry ? row0 + sr : s_tok[sr]) : row0 + sr;
-    const uint16_t* ap = a.a + (size_t) (a_ok ? arow : 0) * a.K + sk;
+    const uint16_t* ap = a.a + (size_t) (a_ok ? row0 + sr : 0) * a.K + sk;
 
     f32x16_t acc;
 #pragma unroll
@@ -190,18 +150,18 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
         x[0] = a_ok ? p[0] : make_uint4(0, 0, 0, 0);
         x[1] = a_ok ? p[1] : make_uint4(0, 0, 0, 0);
     };
-    auto store = [&](int buf, const uint4 (&x)[2], const WRaw<WK>& wr) {
+    auto store = [&](int buf, const uint4 (&x)[2], const WRaw& wr) {
         *(uint4*) &sA[buf][sr][sk] = x[0];
         *(uint4*) &sA[buf][sr][sk + 8] = x[1];
         uint4 o[2];
-        dequant_w<WK>(wr, tsc, o);
+        dequant_w<WK>(wr, o);
         *(uint4*) &sB[buf][sr][sk] = o[0];
         *(uint4*) &sB[buf][sr][sk + 8] = o[1];
     };
 
     uint4 xa[2];
     load_a(0, xa);
-    WRaw<WK> wr = load_w<WK>(a, rec, wrow, up, sk);
+    WRaw wr = load_w<WK>(a, wrow, up, sk);
     store(0, xa, wr);
     __syncthreads();
     for (int ks = 0; ks < nk; ++ks) {
@@ -209,7 +169,7 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
         const bool more = ks + 1 < nk;
         if (more) {                                              // next step's loads first
             load_a(ks + 1, xa);
-            wr = load_w<WK>(a, rec, wrow, up, (ks + 1) * PB + sk);
+            wr = load_w<WK>(a, wrow, up, (ks + 1) * PB + sk);
         }
 #pragma unroll
         for (int kk = 0; kk < PB / 16; ++kk) {
@@ -234,14 +194,14 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
             uint32_t pk[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                uint16_t h[2];
+                uint16_t hv[2];
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
                     const int j = j8 + 2 * q + b;
                     const float g = sC[m * LDC + j], u = sC[m * LDC + 32 + j];
-                    h[b] = f_to_bf16(g / (1.0f + __expf(-g)) * u);
+                    hv[b] = f_to_bf16(g / (1.0f + __expf(-g)) * u);
                 }
-                pk[q] = h[0] | ((uint32_t) h[1] << 16);
+                pk[q] = hv[0] | ((uint32_t) hv[1] << 16);
             }
             *(uint4*) (a.act + (size_t) (row0 + m) * a.act_ld + n0 + j8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         }
@@ -253,17 +213,203 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
             if (m >= cnt) continue;
             if constexpr (EPI == PE_F32) {
                 if (n < a.n_rows) a.y[(size_t) (row0 + m) * a.y_ld + n] = acc[i];
-            } else if constexpr (EPI == PE_SHARED) {
+            } else {
                 const float sg = a.sg[row0 + m];
                 a.y[(size_t) (row0 + m) * a.y_ld + n] = acc[i] / (1.0f + __expf(-sg));
-            } else {
-                atomicAdd(&a.y[(size_t) s_tok[m] * a.y_ld + n], a.wt[row0 + m] * acc[i]);
             }
         }
     }
 }
 
-__global__ void __launch_bounds__(256) pf_cvt_kernel(const float* __restrict__ x, uint16_t* __restrict__ xb, size_t n) {
+// MFMA B fragment (8 consecutive k of one weight row) from one 16-value NVFP4 sub-block: bytes
+// w0 (0..3), w1 (4..7), byte i = value i (low nibble) | value i+8 (high nibble).  The lane half
+// sa = 0 takes values 0..7, sa = 4 values 8..15: the nibbles are regrouped so that byte i holds
+// values i and i+4 of the lane's eight, each converted pair is scaled by the e4m3 block scale (the
+// product of a 2-bit and a 4-bit significand: exact in fp32 and in bf16), and the high halves are
+// packed in k order.
+WZY_DEV bf16x8_t fp4_frag(uint32_t w0, uint32_t w1, uint32_t sa, float sc) {
+    const uint32_t d = ((w0 >> sa) & 0x0F0F0F0Fu) | (((w1 >> sa) & 0x0F0F0F0Fu) << 4);
+    float2_t p[4];
+    p[0] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 0);
+    p[1] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 1);
+    p[2] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 2);
+    p[3] = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, 1.0f, 3);
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        b[i] = f_bits(p[i].x * sc);            // value i
+        b[i + 4] = f_bits(p[i].y * sc);        // value i + 4
+    }
+    uint4 q;
+    q.x = __builtin_amdgcn_perm(b[1], b[0], 0x07060302u);
+    q.y = __builtin_amdgcn_perm(b[3], b[2], 0x07060302u);
+    q.z = __builtin_amdgcn_perm(b[5], b[4], 0x07060302u);
+    q.w = __builtin_amdgcn_perm(b[7], b[6], 0x07060302u);
+    return __builtin_bit_cast(bf16x8_t, q);
+}
+
+// Two e4m3 block scales (bytes 0 and 1 of s) as fp32: the scaled fp8 -> f32 conversion with unit
+// scale decodes OCP e4m3; the sign bit is ignored and code 0x7F (NaN in OCP, 480 in the unsigned
+// reading) maps to 480 through the NaN-discarding min.
+WZY_DEV float2_t e4m3x2(uint32_t s) {
+    const float2_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(s & 0x7F7Fu, 1.0f, false);
+    return float2_t{fminf(v.x, 480.0f), fminf(v.y, 480.0f)};
+}
+
+struct ExpLane {                   // per-lane view of one expert tile
+    const uint8_t* c0; const uint8_t* c1;          // codes of the lane's two weight rows
+    const uint16_t* s0; const uint16_t* s1;        // their block scales (two per K step)
+    const uint16_t* ap;                            // the staging thread's activation row (+ k offset)
+    int nk, cnt, row0, col, sr, sk;
+    bool a_ok;
+    uint32_t sa;
+    float ts0, ts1;
+};
+
+// K loop and epilogue of one tile with NMB active 32-entry row blocks.
+template <bool DOWN, int NMB>
+WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane& c, uint16_t (*sA)[MT][EA_LD]) {
+    const int lane = threadIdx.x & 63, h = lane >> 5;
+    // weight codes of K steps ks (cur), ks+1 (nxt): 16 bytes + two scale bytes per row
+    uint4 c0c = *(const uint4*) c.c0, c1c = *(const uint4*) c.c1;
+    uint32_t s0c = c.s0[0], s1c = c.s1[0];
+    uint4 c0n = make_uint4(0, 0, 0, 0), c1n = c0n;
+    uint32_t s0n = 0, s1n = 0;
+    if (c.nk > 1) {
+        c0n = *(const uint4*) (c.c0 + EK / 2);
+        c1n = *(const uint4*) (c.c1 + EK / 2);
+        s0n = c.s0[1];
+        s1n = c.s1[1];
+    }
+    uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = xa0;
+    f32x16_t acc[NMB][2];
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mb][0][i] = acc[mb][1][i] = 0.f;
+
+    for (int ks = 0; ks < c.nk; ++ks) {
+        const int buf = ks & 1;
+        // this step's activation fragments first (LDS), then the loads of later steps
+        bf16x8_t av[2][NMB];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb)
+                av[kk][mb] = *(const bf16x8_t*) &sA[buf][mb * 32 + (lane & 31)][kk * 16 + h * 8];
+        uint4 c0f = make_uint4(0, 0, 0, 0), c1f = c0f;
+        uint32_t s0f = 0, s1f = 0;
+        if (ks + 2 < c.nk) {                                        // weights two steps ahead
+            c0f = *(const uint4*) (c.c0 + (size_t) (ks + 2) * (EK / 2));
+            c1f = *(const uint4*) (c.c1 + (size_t) (ks + 2) * (EK / 2));
+            s0f = c.s0[ks + 2];
+            s1f = c.s1[ks + 2];
+        }
+        if (ks + 1 < c.nk && c.a_ok) {                              // activations one step ahead
+            xa0 = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK);
+            xa1 = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK + 8);
+        }
+        const float2_t sc0 = e4m3x2(s0c), sc1 = e4m3x2(s1c);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const bf16x8_t b0 = fp4_frag(kk ? c0c.z : c0c.x, kk ? c0c.w : c0c.y, c.sa, kk ? sc0.y : sc0.x);
+            const bf16x8_t b1 = fp4_frag(kk ? c1c.z : c1c.x, kk ? c1c.w : c1c.y, c.sa, kk ? sc1.y : sc1.x);
+#pragma unroll
+            for (int mb = 0; mb < NMB; ++mb) {
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][mb], b0, acc[mb][0], 0, 0, 0);
+                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][mb], b1, acc[mb][1], 0, 0, 0);
+            }
+        }
+        if (ks + 1 < c.nk) {
+            *(uint4*) &sA[buf ^ 1][c.sr][c.sk] = c.a_ok ? xa0 : make_uint4(0, 0, 0, 0);
+            *(uint4*) &sA[buf ^ 1][c.sr][c.sk + 8] = c.a_ok ? xa1 : make_uint4(0, 0, 0, 0);
+        }
+        c0c = c0n; c1c = c1n; s0c = s0n; s1c = s1n;
+        c0n = c0f; c1n = c1f; s0n = s0f; s1n = s1f;
+        __syncthreads();
+    }
+
+    // acc[mb][*][i] = C[entry mb*32 + 8*(i/4) + 4*h + i%4][weight row block column lane%32]
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (row < c.cnt) {
+                if constexpr (DOWN) {
+                    float* yp = a.y + (size_t) (c.row0 + row) * a.ld_out + c.col;
+                    yp[0] = acc[mb][0][i] * c.ts0;
+                    yp[32] = acc[mb][1][i] * c.ts1;
+                } else {
+                    const float g = acc[mb][0][i] * c.ts0, u = acc[mb][1][i] * c.ts1;
+                    a.act[(size_t) (c.row0 + row) * a.ld_out + c.col] = f_to_bf16(g / (1.0f + __expf(-g)) * u);
+                }
+            }
+        }
+    }
+}
+
+// Routed-expert GEMM.  Workgroup = one expert tile (<= 128 entries) x one column block; wave w
+// owns two 32-row weight blocks (gate|up: gate rows j0+32w.. and the matching up rows, so SwiGLU
+// is elementwise in registers; down: rows n0+64w .. +63) for all active 32-entry row blocks of the
+// tile (the count selects a specialised loop).  The weights never pass through LDS: each lane loads
+// the codes of its own row, two K steps ahead, and dequantises them into its MFMA B fragment; the
+// activation rows of the tile are staged in LDS (double buffered) and shared by the four waves.
+// Workgroups are numbered so that consecutive workgroups of one XCD take the column blocks of one
+// tile (its activation rows stay in that XCD's L2).  The tensor scale is applied to the fp32
+// accumulators.
+template <bool DOWN>
+__global__ void __launch_bounds__(256, 2) pf_expert_kernel(PfExpArgs a) {
+    __shared__ __align__(16) uint16_t sA[2][MT][EA_LD];
+    __shared__ int s_row[MT];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int L = blockIdx.x, jx = L >> 3;
+    const int ti = (jx / a.gx) * 8 + (L & 7), nb = jx % a.gx;
+    if (ti >= *a.n_tiles) return;                                   // workgroup-uniform
+    const PfTile t = a.tiles[ti];
+    ExpLane c;
+    c.cnt = t.cnt;
+    c.row0 = t.off;
+    if (tid < MT) s_row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid]) : 0;
+    const uint8_t* rec = a.experts + (size_t) t.e * a.rec;
+    c.col = DOWN ? nb * 256 + w * 64 + (lane & 31) : nb * 128 + w * 32 + (lane & 31);
+    const int r0 = c.col, r1 = DOWN ? c.col + 32 : a.F + c.col;
+    const float* tail = (const float*) (rec + a.tail_off);
+    c.ts0 = DOWN ? tail[2] : tail[0];
+    c.ts1 = DOWN ? tail[2] : tail[1];
+    c.c0 = rec + a.codes_off + (size_t) r0 * (a.K / 2);
+    c.c1 = rec + a.codes_off + (size_t) r1 * (a.K / 2);
+    c.s0 = (const uint16_t*) (rec + a.scales_off + (size_t) r0 * (a.K / 16));
+    c.s1 = (const uint16_t*) (rec + a.scales_off + (size_t) r1 * (a.K / 16));
+    c.nk = a.K / EK;
+    c.sa = 4u * h;
+    __syncthreads();
+    c.sr = tid >> 1;                                                // staging: entry sr, k sk .. sk+15
+    c.sk = (tid & 1) * 16;
+    c.a_ok = c.sr < c.cnt;
+    c.ap = a.a + (size_t) s_row[c.sr] * a.K + c.sk;
+    uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = xa0;
+    if (c.a_ok) {
+        xa0 = *(const uint4*) c.ap;
+        xa1 = *(const uint4*) (c.ap + 8);
+    }
+    *(uint4*) &sA[0][c.sr][c.sk] = xa0;
+    *(uint4*) &sA[0][c.sr][c.sk + 8] = xa1;
+    __syncthreads();
+    switch ((c.cnt + 31) >> 5) {                                    // workgroup-uniform
+        case 1: expert_tile<DOWN, 1>(a, c, sA); break;
+        case 2: expert_tile<DOWN, 2>(a, c, sA); break;
+        case 3: expert_tile<DOWN, 3>(a, c, sA); break;
+        default: expert_tile<DOWN, 4>(a, c, sA); break;
+    }
+}
+
+// x fp32 -> bf16; workgroup 0 also clears the per-expert entry counts
+__global__ void __launch_bounds__(256) pf_cvt_kernel(const float* __restrict__ x, uint16_t* __restrict__ xb, size_t n,
+                                                     int* __restrict__ cnt, int E) {
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < E; i += 256) cnt[i] = 0;
     const size_t i = ((size_t) blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     const float4 v = *(const float4*) (x + i);
@@ -271,12 +417,14 @@ __global__ void __launch_bounds__(256) pf_cvt_kernel(const float* __restrict__ x
                                     f_to_bf16(v.z) | ((uint32_t) f_to_bf16(v.w) << 16));
 }
 
-// one wave per token: routing of its logits row and the shared-expert gate
+// one wave per token: routing of its logits row, the shared-expert gate, and a slot per entry in
+// its expert's list (rank = arrival order at the expert's counter)
 template <int RV>
 __global__ void __launch_bounds__(256) pf_route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ xb,
                                                        const uint16_t* __restrict__ sgate, int N, int E, int K, int D,
                                                        int* __restrict__ ids, float* __restrict__ wts,
-                                                       float* __restrict__ sg) {
+                                                       float* __restrict__ sg, int* __restrict__ cnt,
+                                                       int* __restrict__ rank) {
     __shared__ uint64_t cand[4][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + w;
@@ -299,49 +447,73 @@ __global__ void __launch_bounds__(256) pf_route_kernel(const float* __restrict__
     if (lane < K) {
         ids[(size_t) t * K + lane] = my_id;
         wts[(size_t) t * K + lane] = my_w / sc;
+        rank[(size_t) t * K + lane] = atomicAdd(&cnt[my_id], 1);
     }
 }
 
-// entries (token, slot) grouped by expert: 64-entry tiles, entry token and weight per position
-__global__ void __launch_bounds__(1024) pf_group_kernel(const int* __restrict__ ids, const float* __restrict__ wts,
-                                                        int n_ent, int K, int E, int* __restrict__ ent_tok,
-                                                        float* __restrict__ ent_wt, PfTile* __restrict__ tiles,
-                                                        int* __restrict__ n_tiles) {
-    __shared__ int cnt[PF_MAX_E], off[PF_MAX_E], toff[PF_MAX_E], s_tot[2];
-    const int tid = threadIdx.x;
-    for (int i = tid; i < E; i += 1024) cnt[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < n_ent; i += 1024) atomicAdd(&cnt[ids[i]], 1);
-    __syncthreads();
-    if (tid == 0) {                                               // E <= 1024 prefix sums, once per chunk
-        int o = 0, to = 0;
-        for (int i = 0; i < E; ++i) {
-            off[i] = o;
-            toff[i] = to;
-            o += cnt[i];
-            to += (cnt[i] + PB - 1) / PB;
-        }
-        s_tot[0] = to;
+// one workgroup: exclusive scans of the entry counts and of the tiles per expert -> each expert's
+// first entry position and its MT-entry tiles
+__global__ void __launch_bounds__(1024) pf_tiles_kernel(const int* __restrict__ cnt, int E, int* __restrict__ exp_off,
+                                                        PfTile* __restrict__ tiles, int* __restrict__ n_tiles) {
+    __shared__ uint64_t s_w[16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = tid < E ? cnt[tid] : 0;
+    const int nt = (c + MT - 1) / MT;
+    const uint64_t v = ((uint64_t) c << 24) | (uint64_t) nt;       // both sums in one scan
+    uint64_t s = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t o = __shfl_up(s, d);
+        if (lane >= d) s += o;
     }
+    if (lane == 63) s_w[w] = s;
     __syncthreads();
-    for (int i = tid; i < E; i += 1024) {
-        const int c = cnt[i];
-        for (int q = 0; q * PB < c; ++q) tiles[toff[i] + q] = PfTile{i, off[i] + q * PB, min(PB, c - q * PB), 0};
+    uint64_t base = 0;
+    for (int i = 0; i < w; ++i) base += s_w[i];
+    const uint64_t ex = base + s - v;
+    const int off = (int) (ex >> 24), toff = (int) (ex & 0xFFFFFFu);
+    if (tid < E) {
+        exp_off[tid] = off;
+        for (int q = 0; q < nt; ++q) tiles[toff + q] = PfTile{tid, off + q * MT, min(MT, c - q * MT), 0};
     }
-    if (tid == 0) *n_tiles = s_tot[0];
-    __syncthreads();
-    for (int i = tid; i < n_ent; i += 1024) {                     // cnt becomes the fill cursor
-        const int e = ids[i];
-        const int pos = off[e] + atomicSub(&cnt[e], 1) - 1;
-        ent_tok[pos] = i / K;
-        ent_wt[pos] = wts[i];
+    if (tid == 1023) *n_tiles = (int) ((base + s) & 0xFFFFFFu);
+}
+
+// entry i = (token i / K, slot i % K) -> its position in the expert-sorted list
+__global__ void __launch_bounds__(256) pf_scatter_kernel(const int* __restrict__ ids, const int* __restrict__ rank,
+                                                         const int* __restrict__ exp_off, int n_ent, int K,
+                                                         int* __restrict__ ent_tok, int* __restrict__ ent_pos) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_ent) return;
+    const int pos = exp_off[ids[i]] + rank[i];
+    ent_tok[pos] = i / K;
+    ent_pos[i] = pos;
+}
+
+// comb[t] += sum_k w_k * y[pos(t, k)] in slot order (comb holds the gated shared expert)
+__global__ void __launch_bounds__(256) pf_combine_kernel(const float* __restrict__ y, const int* __restrict__ ent_pos,
+                                                         const float* __restrict__ wts, int K, int D,
+                                                         float* __restrict__ comb) {
+    const int t = blockIdx.y;
+    const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d >= D) return;
+    float4 acc = *(const float4*) (comb + (size_t) t * D + d);
+    for (int k = 0; k < K; ++k) {
+        const int p = ent_pos[(size_t) t * K + k];
+        const float wk = wts[(size_t) t * K + k];
+        const float4 v = *(const float4*) (y + (size_t) p * D + d);
+        acc.x = fmaf(wk, v.x, acc.x);
+        acc.y = fmaf(wk, v.y, acc.y);
+        acc.z = fmaf(wk, v.z, acc.z);
+        acc.w = fmaf(wk, v.w, acc.w);
     }
+    *(float4*) (comb + (size_t) t * D + d) = acc;
 }
 
 struct PfWs {
     uint16_t* xb; float* logits; float* sg; int* ids; float* wts;
-    int* ent_tok; float* ent_wt; PfTile* tiles; int* n_tiles;
-    uint16_t* act; uint16_t* sh_act;
+    int* cnt; int* exp_off; int* rank; int* ent_tok; int* ent_pos; PfTile* tiles; int* n_tiles;
+    uint16_t* act; uint16_t* sh_act; float* y;
     int max_tiles;
 };
 
@@ -349,18 +521,22 @@ PfWs pf_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int N, size
     Arena a(base, cap);
     PfWs w;
     const size_t n_ent = (size_t) N * K;
-    w.max_tiles = (int) (n_ent / PB + E);
+    w.max_tiles = (int) (n_ent / MT + E);
     w.xb = a.take<uint16_t>((size_t) N * D);
     w.logits = a.take<float>((size_t) N * E);
     w.sg = a.take<float>(N);
     w.ids = a.take<int>(n_ent);
     w.wts = a.take<float>(n_ent);
+    w.cnt = a.take<int>(E);
+    w.exp_off = a.take<int>(E);
+    w.rank = a.take<int>(n_ent);
     w.ent_tok = a.take<int>(n_ent);
-    w.ent_wt = a.take<float>(n_ent);
+    w.ent_pos = a.take<int>(n_ent);
     w.tiles = a.take<PfTile>(w.max_tiles);
     w.n_tiles = a.take<int>(1);
     w.act = a.take<uint16_t>(n_ent * F);
     w.sh_act = a.take<uint16_t>((size_t) N * F);
+    w.y = a.take<float>(n_ent * D);
     if (need) *need = a.off;
     return w;
 }
@@ -368,6 +544,12 @@ PfWs pf_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int N, size
 template <int WK, int EPI>
 void launch_pf(const PfGemmArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((pf_gemm_kernel<WK, EPI>), grid, dim3(256), 0, st, a);
+}
+
+template <bool DOWN>
+void launch_expert(const PfExpArgs& a, int max_tiles, hipStream_t st) {
+    const unsigned n = (unsigned) (a.gx * ((max_tiles + 7) / 8) * 8);
+    hipLaunchKernelGGL((pf_expert_kernel<DOWN>), dim3(n), dim3(256), 0, st, a);
 }
 
 }  // namespace
@@ -381,28 +563,41 @@ extern "C" size_t wzy_moe_prefill_workspace_bytes(int n_embd, int n_ff, int n_ex
     return need + 256;
 }
 
-extern "C" int wzy_moe_prefill(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, int* ids, float* wts,
-                               void* workspace, size_t workspace_bytes, void* stream) {
-    WZY_REQUIRE(w && x && comb && workspace, "wzy_moe_prefill: null pointer");
+namespace {
+
+constexpr int PF_N_STAGES = 8;     // timing groups of pf_enqueue
+
+int pf_check(const wzy_moe_weights* w, int N) {
+    WZY_REQUIRE(w, "wzy_moe_prefill: null weights");
     WZY_REQUIRE(w->router && w->sgate && w->experts && w->sh_gate_q && w->sh_gate_s && w->sh_up_q && w->sh_up_s &&
                     w->sh_down_q && w->sh_down_s,
                 "wzy_moe_prefill: null weight pointer");
-    const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k, N = n_tok;
-    WZY_REQUIRE(N >= 1, "wzy_moe_prefill: n_tok must be positive");
-    WZY_REQUIRE(D % 64 == 0 && D >= 64 && F % 64 == 0 && F >= 64, "wzy_moe_prefill: n_embd and n_ff must be multiples of 64");
+    const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k;
+    WZY_REQUIRE(N >= 1 && (int64_t) N * K <= (1 << 26), "wzy_moe_prefill: n_tok must be in [1, 2^26 / top_k]");
+    WZY_REQUIRE(D % 256 == 0 && D >= 256 && F % 128 == 0 && F >= 128,
+                "wzy_moe_prefill: n_embd must be a multiple of 256 and n_ff a multiple of 128");
     WZY_REQUIRE(E >= 1 && E <= PF_MAX_E && E % 64 == 0, "wzy_moe_prefill: n_exp must be a multiple of 64 up to %d",
                 PF_MAX_E);
     WZY_REQUIRE(K >= 1 && K <= MOE_MAX_K && K <= E, "wzy_moe_prefill: top_k must be in [1, %d]", MOE_MAX_K);
-    WZY_REQUIRE(workspace_bytes >= wzy_moe_prefill_workspace_bytes(D, F, E, K, N), "wzy_moe_prefill: workspace too small");
-    hipStream_t st = as_stream(stream);
-    size_t need = 0;
-    char* base = (char*) workspace + (256 - (uintptr_t) workspace % 256) % 256;
-    const PfWs ws = pf_ws_carve(base, workspace_bytes - 256, D, F, E, K, N, &need);
+    return WZY_OK;
+}
+
+// The launch sequence; with `ev`, event i is recorded before launch group i and event PF_N_STAGES
+// after the last one.
+void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, const PfWs& ws, hipStream_t st,
+                hipEvent_t* ev) {
+    const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k;
+    const int n_ent = N * K;
     const MoeOffsets o = moe_offsets(D, F);
     const int mt = (N + PB - 1) / PB;
-
+    auto mark = [&](int i) {
+        if (ev) (void) hipEventRecord(ev[i], st);
+    };
     const size_t nx = (size_t) N * D;
-    hipLaunchKernelGGL(pf_cvt_kernel, dim3((unsigned) ((nx / 4 + 255) / 256)), dim3(256), 0, st, x, ws.xb, nx);
+    mark(0);
+    hipLaunchKernelGGL(pf_cvt_kernel, dim3((unsigned) ((nx / 4 + 255) / 256)), dim3(256), 0, st, x, ws.xb, nx, ws.cnt,
+                       E);
+    mark(1);
     {   // router logits
         PfGemmArgs a{};
         a.a = ws.xb; a.a_rows = N; a.K = D;
@@ -410,44 +605,111 @@ extern "C" int wzy_moe_prefill(const wzy_moe_weights* w, const float* x, int n_t
         a.y = ws.logits; a.y_ld = E;
         launch_pf<PW_BF16, PE_F32>(a, dim3(E / PB, mt), st);
     }
+    mark(2);
     if (E <= 512)
         hipLaunchKernelGGL((pf_route_kernel<8>), dim3((N + 3) / 4), dim3(256), 0, st, ws.logits, ws.xb, w->sgate, N, E, K,
-                           D, ws.ids, ws.wts, ws.sg);
+                           D, ws.ids, ws.wts, ws.sg, ws.cnt, ws.rank);
     else
         hipLaunchKernelGGL((pf_route_kernel<16>), dim3((N + 3) / 4), dim3(256), 0, st, ws.logits, ws.xb, w->sgate, N, E, K,
-                           D, ws.ids, ws.wts, ws.sg);
-    hipLaunchKernelGGL(pf_group_kernel, dim3(1), dim3(1024), 0, st, ws.ids, ws.wts, N * K, K, E, ws.ent_tok, ws.ent_wt,
-                       ws.tiles, ws.n_tiles);
-    {   // shared expert gate|up + SwiGLU, then down -> comb = sigmoid(sg) * shared
+                           D, ws.ids, ws.wts, ws.sg, ws.cnt, ws.rank);
+    mark(3);
+    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, st, ws.cnt, E, ws.exp_off, ws.tiles, ws.n_tiles);
+    hipLaunchKernelGGL(pf_scatter_kernel, dim3((unsigned) ((n_ent + 255) / 256)), dim3(256), 0, st, ws.ids, ws.rank,
+                       ws.exp_off, n_ent, K, ws.ent_tok, ws.ent_pos);
+    // shared expert gate|up + SwiGLU, then down -> comb = sigmoid(sg) * shared
+    mark(4);
+    {
         PfGemmArgs a{};
         a.a = ws.xb; a.a_rows = N; a.K = D;
         a.w = w->sh_gate_q; a.ws = w->sh_gate_s; a.w2 = w->sh_up_q; a.ws2 = w->sh_up_s; a.n_rows = F;
         a.act = ws.sh_act; a.act_ld = F;
         launch_pf<PW_Q8, PE_SWIGLU>(a, dim3(F / 32, mt), st);
+    }
+    mark(5);
+    {
         PfGemmArgs b{};
         b.a = ws.sh_act; b.a_rows = N; b.K = F;
         b.w = w->sh_down_q; b.ws = w->sh_down_s; b.n_rows = D;
         b.y = comb; b.y_ld = D; b.sg = ws.sg;
         launch_pf<PW_Q8, PE_SHARED>(b, dim3(D / PB, mt), st);
     }
-    {   // routed experts: gate|up + SwiGLU per tile, then down, weighted, added into comb
-        PfGemmArgs a{};
-        a.a = ws.xb; a.K = D; a.tok = ws.ent_tok;
+    // routed experts: gate|up + SwiGLU per tile, down per tile, then the per-token weighted sum
+    mark(6);
+    {
+        PfExpArgs a{};
         a.experts = w->experts; a.rec = o.rec; a.codes_off = o.gu_codes; a.scales_off = o.gu_scales;
-        a.tail_off = o.tail; a.tail_gate = 0; a.tail_up = 1; a.up_row0 = F; a.n_rows = 2 * F;
+        a.tail_off = o.tail; a.K = D; a.F = F; a.gx = F / 128;
         a.tiles = ws.tiles; a.n_tiles = ws.n_tiles;
-        a.act = ws.act; a.act_ld = F;
-        launch_pf<PW_FP4, PE_SWIGLU>(a, dim3(F / 32, ws.max_tiles), st);
-        PfGemmArgs b{};
-        b.a = ws.act; b.a_by_entry = true; b.K = F; b.tok = ws.ent_tok;
-        b.experts = w->experts; b.rec = o.rec; b.codes_off = o.dn_codes; b.scales_off = o.dn_scales;
-        b.tail_off = o.tail; b.tail_gate = 2; b.tail_up = 2; b.n_rows = D;
-        b.tiles = ws.tiles; b.n_tiles = ws.n_tiles;
-        b.y = comb; b.y_ld = D; b.wt = ws.ent_wt;
-        launch_pf<PW_FP4, PE_ATOMIC>(b, dim3(D / PB, ws.max_tiles), st);
+        a.a = ws.xb; a.tok = ws.ent_tok;
+        a.act = ws.act; a.ld_out = F;
+        launch_expert<false>(a, ws.max_tiles, st);
     }
+    mark(7);
+    {
+        PfExpArgs b{};
+        b.experts = w->experts; b.rec = o.rec; b.codes_off = o.dn_codes; b.scales_off = o.dn_scales;
+        b.tail_off = o.tail; b.K = F; b.F = 0; b.gx = D / 256;
+        b.tiles = ws.tiles; b.n_tiles = ws.n_tiles;
+        b.a = ws.act; b.tok = nullptr;
+        b.y = ws.y; b.ld_out = D;
+        launch_expert<true>(b, ws.max_tiles, st);
+        hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned) ((D / 4 + 255) / 256), (unsigned) N), dim3(256), 0, st,
+                           ws.y, ws.ent_pos, ws.wts, K, D, comb);
+    }
+    mark(8);
+}
+
+PfWs pf_ws_for(const wzy_moe_weights* w, int N, void* workspace, size_t workspace_bytes) {
+    char* base = (char*) workspace + (256 - (uintptr_t) workspace % 256) % 256;
+    return pf_ws_carve(base, workspace_bytes - 256, w->n_embd, w->n_ff, w->n_exp, w->top_k, N, nullptr);
+}
+
+}  // namespace
+
+extern "C" int wzy_moe_prefill(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, int* ids, float* wts,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    WZY_REQUIRE(x && comb && workspace, "wzy_moe_prefill: null pointer");
+    WZY_TRY(pf_check(w, n_tok));
+    const int N = n_tok, K = w->top_k;
+    WZY_REQUIRE(workspace_bytes >= wzy_moe_prefill_workspace_bytes(w->n_embd, w->n_ff, w->n_exp, K, N),
+                "wzy_moe_prefill: workspace too small");
+    hipStream_t st = as_stream(stream);
+    const PfWs ws = pf_ws_for(w, N, workspace, workspace_bytes);
+    pf_enqueue(w, x, N, comb, ws, st, nullptr);
     if (ids) WZY_HIP_TRY(hipMemcpyAsync(ids, ws.ids, (size_t) N * K * sizeof(int), hipMemcpyDeviceToDevice, st));
     if (wts) WZY_HIP_TRY(hipMemcpyAsync(wts, ws.wts, (size_t) N * K * sizeof(float), hipMemcpyDeviceToDevice, st));
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+extern "C" int wzy_moe_prefill_time(const wzy_moe_weights* w, const float* x, int n_tok, float* comb, void* workspace,
+                                    size_t workspace_bytes, int iters, float* us_stages, void* stream) {
+    WZY_REQUIRE(x && comb && workspace && us_stages && iters >= 1, "wzy_moe_prefill_time: bad arguments");
+    WZY_TRY(pf_check(w, n_tok));
+    WZY_REQUIRE(workspace_bytes >= wzy_moe_prefill_workspace_bytes(w->n_embd, w->n_ff, w->n_exp, w->top_k, n_tok),
+                "wzy_moe_prefill_time: workspace too small");
+    hipStream_t st = as_stream(stream);
+    const PfWs ws = pf_ws_for(w, n_tok, workspace, workspace_bytes);
+    hipEvent_t ev[PF_N_STAGES + 1];
+    for (int i = 0; i <= PF_N_STAGES; ++i) WZY_HIP_TRY(hipEventCreate(&ev[i]));
+    double acc[PF_N_STAGES] = {};
+    int rc = WZY_OK;
+    pf_enqueue(w, x, n_tok, comb, ws, st, nullptr);                 // warm-up
+    for (int it = 0; it < iters && rc == WZY_OK; ++it) {
+        pf_enqueue(w, x, n_tok, comb, ws, st, ev);
+        if (hipEventSynchronize(ev[PF_N_STAGES]) != hipSuccess) { rc = WZY_EHIP; break; }
+        for (int i = 0; i < PF_N_STAGES; ++i) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) != hipSuccess) { rc = WZY_EHIP; break; }
+            acc[i] += ms;
+        }
+    }
+    for (int i = 0; i <= PF_N_STAGES; ++i) (void) hipEventDestroy(ev[i]);
+    if (rc != WZY_OK) {
+        set_error("wzy_moe_prefill_time: event timing failed");
+        return rc;
+    }
+    for (int i = 0; i < PF_N_STAGES; ++i) us_stages[i] = (float) (1000.0 * acc[i] / iters);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }

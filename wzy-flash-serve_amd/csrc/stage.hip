@@ -853,6 +853,13 @@ extern "C" int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name
     return WZY_OK;
 }
 
+extern "C" int wzy_stage_moe_weights(wzy_stage* st, int layer, wzy_moe_weights* out) {
+    WZY_REQUIRE(st && st->loaded && out, "moe_weights: bad arguments");
+    WZY_REQUIRE(layer >= 0 && layer < (int) st->L.size(), "moe_weights: layer %d out of range", layer);
+    *out = st->L[layer].moe;
+    return WZY_OK;
+}
+
 extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down) {
     WZY_REQUIRE(st && st->loaded && iters >= 1 && us_gate_up && us_down, "time_moe: bad arguments");
     const int T = st->last_T > 0 ? st->last_T : 1;

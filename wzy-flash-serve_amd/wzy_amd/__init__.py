@@ -147,6 +147,8 @@ _SIGS = {
     "wzy_moe_route": (I32, [P, I32, I32, I32, P, P, P], True),
     "wzy_moe_prefill_workspace_bytes": (SZ, [I32, I32, I32, I32, I32], False),
     "wzy_moe_prefill": (I32, [C.POINTER(MoeWeights), P, I32, P, P, P, P, SZ, P], True),
+    "wzy_moe_prefill_time": (I32, [C.POINTER(MoeWeights), P, I32, P, P, SZ, I32, C.POINTER(F32), P], True),
+    "wzy_stage_moe_weights": (I32, [P, I32, C.POINTER(MoeWeights)], True),
     "wzy_moe_time_kernels": (I32, [C.POINTER(MoeWeights), I32, I32, P, P, SZ, I32, C.POINTER(F32),
                                    C.POINTER(F32), P], True),
     "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
