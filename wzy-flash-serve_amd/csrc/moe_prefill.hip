@@ -35,8 +35,8 @@ namespace {
 constexpr int PB = 64;             // dense GEMM: tile rows (M), weight rows (N) and K step
 constexpr int PB_LD = PB + 8;      // LDS row stride in bf16 (16-byte aligned rows, staggered banks)
 constexpr int PF_MAX_E = 1024;
-constexpr int MT = 128;            // expert GEMM: entries per tile (4 MFMA row blocks of 32)
-constexpr int EK = 32;             // expert GEMM: K step (two MFMA k16 slices)
+constexpr int MT = 256;            // expert GEMM: entries per tile (8 MFMA row blocks of 32)
+constexpr int EK = 64;             // expert GEMM: K step between barriers (four MFMA k16 slices)
 constexpr int EA_LD = EK + 8;      // LDS row stride of the staged activations, bf16
 
 enum { PW_BF16 = 0, PW_Q8 = 1 };                      // dense weight formats
@@ -72,9 +72,8 @@ struct PfExpArgs {
     uint16_t* act; float* y; int ld_out;
 };
 
-WZY_DEV uint16_t f_to_bf16(float f) {                // round to nearest even (finite inputs)
-    const uint32_t u = __builtin_bit_cast(uint32_t, f);
-    return (uint16_t) ((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+WZY_DEV uint16_t f_to_bf16(float f) {                // hardware conversion, round to nearest even
+    return __builtin_bit_cast(uint16_t, (__bf16) f);
 }
 WZY_DEV float bf16_bits_to_f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
 WZY_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
@@ -256,152 +255,178 @@ WZY_DEV float2_t e4m3x2(uint32_t s) {
     return float2_t{fminf(v.x, 480.0f), fminf(v.y, 480.0f)};
 }
 
-struct ExpLane {                   // per-lane view of one expert tile
-    const uint8_t* c0; const uint8_t* c1;          // codes of the lane's two weight rows
-    const uint16_t* s0; const uint16_t* s1;        // their block scales (two per K step)
-    const uint16_t* ap;                            // the staging thread's activation row (+ k offset)
+constexpr int EKB = 128;           // expert GEMM: weight chunk (k values) staged through LDS
+constexpr int EB_LD = EKB / 2 + 16;  // LDS bytes per weight row of a chunk: 64 code bytes + pad
+constexpr int EROWS = 256;         // weight rows per workgroup (8 waves x 32)
+constexpr int ETHR = 512;          // threads per expert workgroup
+
+struct ExpLane {                   // per-thread view of one expert tile
+    const uint8_t* crow0;          // staging: code bytes of the two (row, 16-byte piece) slots, chunk 0
+    const uint8_t* crow1;
+    const uint8_t* srow;           // staging (threads < 256): block scales of row `tid`, chunk 0
+    const uint16_t* ap;            // staging: activation row of entry sr (+ k offset sk)
+    int lr;                        // the lane's weight row (local) = its B fragment column
     int nk, cnt, row0, col, sr, sk;
     bool a_ok;
     uint32_t sa;
-    float ts0, ts1;
+    float ts;
+};
+
+struct ExpLds {
+    uint16_t a[2][MT][EA_LD];      // activation rows, one K step (64) per buffer
+    uint8_t b[2][EROWS][EB_LD];    // weight codes, one chunk (128) per buffer
+    uint2 s[2][EROWS];             // the chunk's 8 block scales per weight row
+    int row[MT];
 };
 
 // K loop and epilogue of one tile with NMB active 32-entry row blocks.
 template <bool DOWN, int NMB>
-WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane& c, uint16_t (*sA)[MT][EA_LD]) {
-    const int lane = threadIdx.x & 63, h = lane >> 5;
-    // weight codes of K steps ks (cur), ks+1 (nxt): 16 bytes + two scale bytes per row
-    uint4 c0c = *(const uint4*) c.c0, c1c = *(const uint4*) c.c1;
-    uint32_t s0c = c.s0[0], s1c = c.s1[0];
-    uint4 c0n = make_uint4(0, 0, 0, 0), c1n = c0n;
-    uint32_t s0n = 0, s1n = 0;
-    if (c.nk > 1) {
-        c0n = *(const uint4*) (c.c0 + EK / 2);
-        c1n = *(const uint4*) (c.c1 + EK / 2);
-        s0n = c.s0[1];
-        s1n = c.s1[1];
-    }
-    uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = xa0;
-    f32x16_t acc[NMB][2];
+WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
+    const int nkc = c.nk / (EKB / EK);                              // weight chunks
+    uint4 bq0 = make_uint4(0, 0, 0, 0), bq1 = bq0;
+    uint2 bs = make_uint2(0, 0);
+    f32x16_t acc[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[mb][0][i] = acc[mb][1][i] = 0.f;
+        for (int i = 0; i < 16; ++i) acc[mb][i] = 0.f;
 
-    for (int ks = 0; ks < c.nk; ++ks) {
-        const int buf = ks & 1;
-        // this step's activation fragments first (LDS), then the loads of later steps
-        bf16x8_t av[2][NMB];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int mb = 0; mb < NMB; ++mb)
-                av[kk][mb] = *(const bf16x8_t*) &sA[buf][mb * 32 + (lane & 31)][kk * 16 + h * 8];
-        uint4 c0f = make_uint4(0, 0, 0, 0), c1f = c0f;
-        uint32_t s0f = 0, s1f = 0;
-        if (ks + 2 < c.nk) {                                        // weights two steps ahead
-            c0f = *(const uint4*) (c.c0 + (size_t) (ks + 2) * (EK / 2));
-            c1f = *(const uint4*) (c.c1 + (size_t) (ks + 2) * (EK / 2));
-            s0f = c.s0[ks + 2];
-            s1f = c.s1[ks + 2];
+    for (int kc = 0; kc < nkc; ++kc) {
+        const int bb = kc & 1;
+        const bool more_b = kc + 1 < nkc;
+        if (more_b) {                                               // next weight chunk, coalesced
+            bq0 = *(const uint4*) (c.crow0 + (size_t) (kc + 1) * (EKB / 2));
+            bq1 = *(const uint4*) (c.crow1 + (size_t) (kc + 1) * (EKB / 2));
+            if (tid < EROWS) bs = *(const uint2*) (c.srow + (size_t) (kc + 1) * (EKB / 16));
         }
-        if (ks + 1 < c.nk && c.a_ok) {                              // activations one step ahead
-            xa0 = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK);
-            xa1 = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK + 8);
-        }
-        const float2_t sc0 = e4m3x2(s0c), sc1 = e4m3x2(s1c);
+        const uint2 sw = L.s[bb][c.lr];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const bf16x8_t b0 = fp4_frag(kk ? c0c.z : c0c.x, kk ? c0c.w : c0c.y, c.sa, kk ? sc0.y : sc0.x);
-            const bf16x8_t b1 = fp4_frag(kk ? c1c.z : c1c.x, kk ? c1c.w : c1c.y, c.sa, kk ? sc1.y : sc1.x);
+        for (int st = 0; st < EKB / EK; ++st) {
+            const int ks = kc * (EKB / EK) + st;
+            const int ab = ks & 1;
+            uint4 xn[4];                                            // activations one step ahead
 #pragma unroll
-            for (int mb = 0; mb < NMB; ++mb) {
-                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][mb], b0, acc[mb][0], 0, 0, 0);
-                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[kk][mb], b1, acc[mb][1], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) xn[i] = make_uint4(0, 0, 0, 0);
+            if (ks + 1 < c.nk && c.a_ok) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xn[i] = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK + 8 * i);
             }
+            // k16 slices 4st .. 4st+3 of the lane's row: 8 code bytes and one scale byte each
+            const uint2 q0 = *(const uint2*) &L.b[bb][c.lr][st * 32];
+            const uint2 q1 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 8];
+            const uint2 q2 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 16];
+            const uint2 q3 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 24];
+            const uint32_t sv = st ? sw.y : sw.x;
+            const float2_t sc01 = e4m3x2(sv), sc23 = e4m3x2(sv >> 16);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const uint2 qq = kk == 0 ? q0 : kk == 1 ? q1 : kk == 2 ? q2 : q3;
+                const float scv = kk == 0 ? sc01.x : kk == 1 ? sc01.y : kk == 2 ? sc23.x : sc23.y;
+                const bf16x8_t b = fp4_frag(qq.x, qq.y, c.sa, scv);
+#pragma unroll
+                for (int mb = 0; mb < NMB; ++mb) {
+                    const bf16x8_t av = *(const bf16x8_t*) &L.a[ab][mb * 32 + (lane & 31)][kk * 16 + h * 8];
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b, acc[mb], 0, 0, 0);
+                }
+            }
+            if (ks + 1 < c.nk) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *(uint4*) &L.a[ab ^ 1][c.sr][c.sk + 8 * i] = xn[i];
+            }
+            if (st == EKB / EK - 1 && more_b) {                     // the next chunk into the other buffer
+                *(uint4*) &L.b[bb ^ 1][tid >> 2][(tid & 3) * 16] = bq0;
+                *(uint4*) &L.b[bb ^ 1][(ETHR + tid) >> 2][(tid & 3) * 16] = bq1;
+                if (tid < EROWS) L.s[bb ^ 1][tid] = bs;
+            }
+            __syncthreads();
         }
-        if (ks + 1 < c.nk) {
-            *(uint4*) &sA[buf ^ 1][c.sr][c.sk] = c.a_ok ? xa0 : make_uint4(0, 0, 0, 0);
-            *(uint4*) &sA[buf ^ 1][c.sr][c.sk + 8] = c.a_ok ? xa1 : make_uint4(0, 0, 0, 0);
-        }
-        c0c = c0n; c1c = c1n; s0c = s0n; s1c = s1n;
-        c0n = c0f; c1n = c1f; s0n = s0f; s1n = s1f;
-        __syncthreads();
     }
 
-    // acc[mb][*][i] = C[entry mb*32 + 8*(i/4) + 4*h + i%4][weight row block column lane%32]
+    // acc[mb][i] = C[entry mb*32 + 8*(i/4) + 4*h + i%4][column lane%32 of the wave's weight block]
+    const bool gate_lane = (lane & 16) == 0;
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int row = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (row < c.cnt) {
-                if constexpr (DOWN) {
-                    float* yp = a.y + (size_t) (c.row0 + row) * a.ld_out + c.col;
-                    yp[0] = acc[mb][0][i] * c.ts0;
-                    yp[32] = acc[mb][1][i] * c.ts1;
-                } else {
-                    const float g = acc[mb][0][i] * c.ts0, u = acc[mb][1][i] * c.ts1;
-                    a.act[(size_t) (c.row0 + row) * a.ld_out + c.col] = f_to_bf16(g / (1.0f + __expf(-g)) * u);
-                }
+            const float v = acc[mb][i] * c.ts;
+            if constexpr (DOWN) {
+                if (row < c.cnt) a.y[(size_t) (c.row0 + row) * a.ld_out + c.col] = v;
+            } else {
+                // the matching up value from lane l ^ 16 (swizzle bit-mask mode: and 0x1F, xor 0x10)
+                const float u = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle((int) f_bits(v), 0x401F));
+                if (gate_lane && row < c.cnt)
+                    a.act[(size_t) (c.row0 + row) * a.ld_out + c.col] =
+                        f_to_bf16(v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)) * u);
             }
         }
     }
 }
 
-// Routed-expert GEMM.  Workgroup = one expert tile (<= 128 entries) x one column block; wave w
-// owns two 32-row weight blocks (gate|up: gate rows j0+32w.. and the matching up rows, so SwiGLU
-// is elementwise in registers; down: rows n0+64w .. +63) for all active 32-entry row blocks of the
-// tile (the count selects a specialised loop).  The weights never pass through LDS: each lane loads
-// the codes of its own row, two K steps ahead, and dequantises them into its MFMA B fragment; the
-// activation rows of the tile are staged in LDS (double buffered) and shared by the four waves.
-// Workgroups are numbered so that consecutive workgroups of one XCD take the column blocks of one
-// tile (its activation rows stay in that XCD's L2).  The tensor scale is applied to the fp32
-// accumulators.
+// Routed-expert GEMM.  Workgroup = one expert tile (<= 256 entries) x 256 weight rows, 8 waves; wave
+// w owns one 32-row weight block (gate|up: 16 gate rows j0+16w.. in columns 0..15 and the matching
+// 16 up rows in columns 16..31, paired for SwiGLU across lanes l, l^16; down: rows n0+32w .. +31)
+// for all active 32-entry row blocks of the tile (the count selects a specialised loop), so each
+// dequantised B fragment feeds up to 8 MFMAs.  Weight codes move in 128-k chunks: each row's 64
+// code bytes are read as four 16-byte pieces by four adjacent threads (whole 64-byte segments), one
+// chunk ahead, into LDS; each lane then takes its row's 8 bytes per k16 slice from LDS and
+// dequantises them into its MFMA B fragment.  The activation rows of the tile are staged in LDS two
+// 32-k steps ahead and shared by the eight waves.  Workgroups are numbered so that consecutive
+// workgroups of one XCD take the column blocks of one tile (its activation rows stay in that XCD's
+// L2).  The tensor scale is applied to the fp32 accumulators.
 template <bool DOWN>
-__global__ void __launch_bounds__(256, 2) pf_expert_kernel(PfExpArgs a) {
-    __shared__ __align__(16) uint16_t sA[2][MT][EA_LD];
-    __shared__ int s_row[MT];
+__global__ void __launch_bounds__(ETHR, 1) pf_expert_kernel(PfExpArgs a) {
+    __shared__ __align__(16) ExpLds L;
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int L = blockIdx.x, jx = L >> 3;
-    const int ti = (jx / a.gx) * 8 + (L & 7), nb = jx % a.gx;
+    const int bx = blockIdx.x, jx = bx >> 3;
+    const int ti = (jx / a.gx) * 8 + (bx & 7), nb = jx % a.gx;
     if (ti >= *a.n_tiles) return;                                   // workgroup-uniform
     const PfTile t = a.tiles[ti];
     ExpLane c;
     c.cnt = t.cnt;
     c.row0 = t.off;
-    if (tid < MT) s_row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid]) : 0;
+    if (tid < MT) L.row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid]) : 0;
     const uint8_t* rec = a.experts + (size_t) t.e * a.rec;
-    c.col = DOWN ? nb * 256 + w * 64 + (lane & 31) : nb * 128 + w * 32 + (lane & 31);
-    const int r0 = c.col, r1 = DOWN ? c.col + 32 : a.F + c.col;
+    // local weight row lr = 32w + column -> plane row: gate|up: columns 0..15 gate rows j0+16w+col,
+    // columns 16..31 up rows F+j0+16w+col-16; down: n0 + lr
+    auto grow = [&](int lr) {
+        const int wl = lr >> 5, cl = lr & 31;
+        return DOWN ? nb * EROWS + lr : (cl < 16 ? nb * 128 + wl * 16 + cl : a.F + nb * 128 + wl * 16 + cl - 16);
+    };
+    c.lr = w * 32 + (lane & 31);
+    c.col = DOWN ? nb * EROWS + c.lr : nb * 128 + w * 16 + (lane & 15);
     const float* tail = (const float*) (rec + a.tail_off);
-    c.ts0 = DOWN ? tail[2] : tail[0];
-    c.ts1 = DOWN ? tail[2] : tail[1];
-    c.c0 = rec + a.codes_off + (size_t) r0 * (a.K / 2);
-    c.c1 = rec + a.codes_off + (size_t) r1 * (a.K / 2);
-    c.s0 = (const uint16_t*) (rec + a.scales_off + (size_t) r0 * (a.K / 16));
-    c.s1 = (const uint16_t*) (rec + a.scales_off + (size_t) r1 * (a.K / 16));
+    c.ts = DOWN ? tail[2] : ((lane & 16) ? tail[1] : tail[0]);
+    const uint8_t* codes = rec + a.codes_off;
+    c.crow0 = codes + (size_t) grow(tid >> 2) * (a.K / 2) + (tid & 3) * 16;
+    c.crow1 = codes + (size_t) grow((ETHR + tid) >> 2) * (a.K / 2) + (tid & 3) * 16;
+    c.srow = rec + a.scales_off + (size_t) grow(tid & (EROWS - 1)) * (a.K / 16);
     c.nk = a.K / EK;
     c.sa = 4u * h;
+    // weight chunk 0
+    *(uint4*) &L.b[0][tid >> 2][(tid & 3) * 16] = *(const uint4*) c.crow0;
+    *(uint4*) &L.b[0][(ETHR + tid) >> 2][(tid & 3) * 16] = *(const uint4*) c.crow1;
+    if (tid < EROWS) L.s[0][tid] = *(const uint2*) c.srow;
     __syncthreads();
-    c.sr = tid >> 1;                                                // staging: entry sr, k sk .. sk+15
-    c.sk = (tid & 1) * 16;
+    c.sr = tid >> 1;                                                // staging: entry sr, k sk .. sk+31
+    c.sk = (tid & 1) * 32;
     c.a_ok = c.sr < c.cnt;
-    c.ap = a.a + (size_t) s_row[c.sr] * a.K + c.sk;
-    uint4 xa0 = make_uint4(0, 0, 0, 0), xa1 = xa0;
-    if (c.a_ok) {
-        xa0 = *(const uint4*) c.ap;
-        xa1 = *(const uint4*) (c.ap + 8);
-    }
-    *(uint4*) &sA[0][c.sr][c.sk] = xa0;
-    *(uint4*) &sA[0][c.sr][c.sk + 8] = xa1;
+    c.ap = a.a + (size_t) L.row[c.sr] * a.K + c.sk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *(uint4*) &L.a[0][c.sr][c.sk + 8 * i] = c.a_ok ? *(const uint4*) (c.ap + 8 * i) : make_uint4(0, 0, 0, 0);
     __syncthreads();
     switch ((c.cnt + 31) >> 5) {                                    // workgroup-uniform
-        case 1: expert_tile<DOWN, 1>(a, c, sA); break;
-        case 2: expert_tile<DOWN, 2>(a, c, sA); break;
-        case 3: expert_tile<DOWN, 3>(a, c, sA); break;
-        default: expert_tile<DOWN, 4>(a, c, sA); break;
+        case 1: expert_tile<DOWN, 1>(a, c, L); break;
+        case 2: expert_tile<DOWN, 2>(a, c, L); break;
+        case 3: expert_tile<DOWN, 3>(a, c, L); break;
+        case 4: expert_tile<DOWN, 4>(a, c, L); break;
+        case 5: expert_tile<DOWN, 5>(a, c, L); break;
+        case 6: expert_tile<DOWN, 6>(a, c, L); break;
+        case 7: expert_tile<DOWN, 7>(a, c, L); break;
+        default: expert_tile<DOWN, 8>(a, c, L); break;
     }
 }
 
@@ -549,7 +574,7 @@ void launch_pf(const PfGemmArgs& a, dim3 grid, hipStream_t st) {
 template <bool DOWN>
 void launch_expert(const PfExpArgs& a, int max_tiles, hipStream_t st) {
     const unsigned n = (unsigned) (a.gx * ((max_tiles + 7) / 8) * 8);
-    hipLaunchKernelGGL((pf_expert_kernel<DOWN>), dim3(n), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pf_expert_kernel<DOWN>), dim3(n), dim3(ETHR), 0, st, a);
 }
 
 }  // namespace
