@@ -68,8 +68,9 @@ struct PfExpArgs {
     int F;                         // gate|up: first up row of the plane
     int gx;                        // column blocks per tile
     const PfTile* tiles; const int* n_tiles;
-    const uint16_t* a; const int* tok;
-    uint16_t* act; float* y; int ld_out;
+    const uint16_t* a;
+    const int* tok; int topk;      // gate|up: entry position -> token * K + slot
+    uint16_t* act; float* y; int ld_out;   // outputs per entry position
 };
 
 WZY_DEV uint16_t f_to_bf16(float f) {                // hardware conversion, round to nearest even
@@ -276,7 +277,7 @@ struct ExpLds {
     uint16_t a[2][MT][EA_LD];      // activation rows, one K step (64) per buffer
     uint8_t b[2][EROWS][EB_LD];    // weight codes, one chunk (128) per buffer
     uint2 s[2][EROWS];             // the chunk's 8 block scales per weight row
-    int row[MT];
+    int row[MT];                   // A row of each tile entry (gate|up: its token; down: its position)
 };
 
 // K loop and epilogue of one tile with NMB active 32-entry row blocks.
@@ -387,7 +388,7 @@ __global__ void __launch_bounds__(ETHR, 1) pf_expert_kernel(PfExpArgs a) {
     ExpLane c;
     c.cnt = t.cnt;
     c.row0 = t.off;
-    if (tid < MT) L.row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid]) : 0;
+    if (tid < MT) L.row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid] / a.topk) : 0;
     const uint8_t* rec = a.experts + (size_t) t.e * a.rec;
     // local weight row lr = 32w + column -> plane row: gate|up: columns 0..15 gate rows j0+16w+col,
     // columns 16..31 up rows F+j0+16w+col-16; down: n0 + lr
@@ -430,11 +431,11 @@ __global__ void __launch_bounds__(ETHR, 1) pf_expert_kernel(PfExpArgs a) {
     }
 }
 
-// x fp32 -> bf16; workgroup 0 also clears the per-expert entry counts
+// x fp32 -> bf16; workgroup 0 also clears the per-expert entry cursors
 __global__ void __launch_bounds__(256) pf_cvt_kernel(const float* __restrict__ x, uint16_t* __restrict__ xb, size_t n,
-                                                     int* __restrict__ cnt, int E) {
+                                                     int* __restrict__ cursor, int E) {
     if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < E; i += 256) cnt[i] = 0;
+        for (int i = threadIdx.x; i < E; i += 256) cursor[i] = 0;
     const size_t i = ((size_t) blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     const float4 v = *(const float4*) (x + i);
@@ -442,14 +443,12 @@ __global__ void __launch_bounds__(256) pf_cvt_kernel(const float* __restrict__ x
                                     f_to_bf16(v.z) | ((uint32_t) f_to_bf16(v.w) << 16));
 }
 
-// one wave per token: routing of its logits row, the shared-expert gate, and a slot per entry in
-// its expert's list (rank = arrival order at the expert's counter)
+// one wave per token: routing of its logits row and the shared-expert gate
 template <int RV>
 __global__ void __launch_bounds__(256) pf_route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ xb,
                                                        const uint16_t* __restrict__ sgate, int N, int E, int K, int D,
                                                        int* __restrict__ ids, float* __restrict__ wts,
-                                                       float* __restrict__ sg, int* __restrict__ cnt,
-                                                       int* __restrict__ rank) {
+                                                       float* __restrict__ sg) {
     __shared__ uint64_t cand[4][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + w;
@@ -472,7 +471,27 @@ __global__ void __launch_bounds__(256) pf_route_kernel(const float* __restrict__
     if (lane < K) {
         ids[(size_t) t * K + lane] = my_id;
         wts[(size_t) t * K + lane] = my_w / sc;
-        rank[(size_t) t * K + lane] = atomicAdd(&cnt[my_id], 1);
+    }
+}
+
+constexpr int PF_HCHUNK = 1024;    // entries per histogram workgroup
+
+// entries [g*1024, (g+1)*1024): each entry's rank among the entries of its expert in this workgroup
+// (LDS counters), then one atomic add per expert reserves the workgroup's run in the expert's list
+// (cursor ends as the expert's entry count)
+__global__ void __launch_bounds__(256) pf_hist_kernel(const int* __restrict__ ids, int n_ent, int E,
+                                                      int* __restrict__ cursor, int* __restrict__ wg_base,
+                                                      int* __restrict__ rank) {
+    __shared__ int h[PF_MAX_E];
+    const int tid = threadIdx.x, g = blockIdx.x;
+    for (int i = tid; i < E; i += 256) h[i] = 0;
+    __syncthreads();
+    const int i0 = g * PF_HCHUNK, i1 = min(n_ent, i0 + PF_HCHUNK);
+    for (int i = i0 + tid; i < i1; i += 256) rank[i] = atomicAdd(&h[ids[i]], 1);
+    __syncthreads();
+    for (int i = tid; i < E; i += 256) {
+        const int c = h[i];
+        wg_base[(size_t) g * E + i] = c ? atomicAdd(&cursor[i], c) : 0;
     }
 }
 
@@ -504,18 +523,22 @@ __global__ void __launch_bounds__(1024) pf_tiles_kernel(const int* __restrict__ 
     if (tid == 1023) *n_tiles = (int) ((base + s) & 0xFFFFFFu);
 }
 
-// entry i = (token i / K, slot i % K) -> its position in the expert-sorted list
+// entry i = (token i / K, slot i % K) <-> its position in the expert-sorted list
 __global__ void __launch_bounds__(256) pf_scatter_kernel(const int* __restrict__ ids, const int* __restrict__ rank,
-                                                         const int* __restrict__ exp_off, int n_ent, int K,
-                                                         int* __restrict__ ent_tok, int* __restrict__ ent_pos) {
+                                                         const int* __restrict__ wg_base,
+                                                         const int* __restrict__ exp_off, int n_ent, int K, int E,
+                                                         int* __restrict__ ent_idx, int* __restrict__ ent_pos) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n_ent) return;
-    const int pos = exp_off[ids[i]] + rank[i];
-    ent_tok[pos] = i / K;
+    const int e = ids[i];
+    const int pos = exp_off[e] + wg_base[(size_t) (i / PF_HCHUNK) * E + e] + rank[i];
+    ent_idx[pos] = i;
     ent_pos[i] = pos;
 }
 
-// comb[t] += sum_k w_k * y[pos(t, k)] in slot order (comb holds the gated shared expert)
+// comb[t] += sum_k w_k * y[pos(t, k)] in slot order (comb holds the gated shared expert); the K
+// row loads of a thread are issued together (KU slots per pass)
+template <int KU>
 __global__ void __launch_bounds__(256) pf_combine_kernel(const float* __restrict__ y, const int* __restrict__ ent_pos,
                                                          const float* __restrict__ wts, int K, int D,
                                                          float* __restrict__ comb) {
@@ -523,23 +546,32 @@ __global__ void __launch_bounds__(256) pf_combine_kernel(const float* __restrict
     const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d >= D) return;
     float4 acc = *(const float4*) (comb + (size_t) t * D + d);
-    for (int k = 0; k < K; ++k) {
-        const int p = ent_pos[(size_t) t * K + k];
-        const float wk = wts[(size_t) t * K + k];
-        const float4 v = *(const float4*) (y + (size_t) p * D + d);
-        acc.x = fmaf(wk, v.x, acc.x);
-        acc.y = fmaf(wk, v.y, acc.y);
-        acc.z = fmaf(wk, v.z, acc.z);
-        acc.w = fmaf(wk, v.w, acc.w);
+    for (int k0 = 0; k0 < K; k0 += KU) {
+        float4 v[KU];
+        float wk[KU];
+#pragma unroll
+        for (int j = 0; j < KU; ++j) {
+            const int k = min(k0 + j, K - 1);
+            const int p = ent_pos[(size_t) t * K + k];
+            wk[j] = k0 + j < K ? wts[(size_t) t * K + k] : 0.f;
+            v[j] = *(const float4*) (y + (size_t) p * D + d);
+        }
+#pragma unroll
+        for (int j = 0; j < KU; ++j) {
+            acc.x = fmaf(wk[j], v[j].x, acc.x);
+            acc.y = fmaf(wk[j], v[j].y, acc.y);
+            acc.z = fmaf(wk[j], v[j].z, acc.z);
+            acc.w = fmaf(wk[j], v[j].w, acc.w);
+        }
     }
     *(float4*) (comb + (size_t) t * D + d) = acc;
 }
 
 struct PfWs {
     uint16_t* xb; float* logits; float* sg; int* ids; float* wts;
-    int* cnt; int* exp_off; int* rank; int* ent_tok; int* ent_pos; PfTile* tiles; int* n_tiles;
+    int* cursor; int* exp_off; int* wg_base; int* rank; int* ent_idx; int* ent_pos; PfTile* tiles; int* n_tiles;
     uint16_t* act; uint16_t* sh_act; float* y;
-    int max_tiles;
+    int max_tiles, n_wg;
 };
 
 PfWs pf_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int N, size_t* need) {
@@ -552,10 +584,12 @@ PfWs pf_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int N, size
     w.sg = a.take<float>(N);
     w.ids = a.take<int>(n_ent);
     w.wts = a.take<float>(n_ent);
-    w.cnt = a.take<int>(E);
+    w.n_wg = (int) ((n_ent + PF_HCHUNK - 1) / PF_HCHUNK);
+    w.cursor = a.take<int>(E);
     w.exp_off = a.take<int>(E);
+    w.wg_base = a.take<int>((size_t) w.n_wg * E);
     w.rank = a.take<int>(n_ent);
-    w.ent_tok = a.take<int>(n_ent);
+    w.ent_idx = a.take<int>(n_ent);
     w.ent_pos = a.take<int>(n_ent);
     w.tiles = a.take<PfTile>(w.max_tiles);
     w.n_tiles = a.take<int>(1);
@@ -620,8 +654,8 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
     };
     const size_t nx = (size_t) N * D;
     mark(0);
-    hipLaunchKernelGGL(pf_cvt_kernel, dim3((unsigned) ((nx / 4 + 255) / 256)), dim3(256), 0, st, x, ws.xb, nx, ws.cnt,
-                       E);
+    hipLaunchKernelGGL(pf_cvt_kernel, dim3((unsigned) ((nx / 4 + 255) / 256)), dim3(256), 0, st, x, ws.xb, nx,
+                       ws.cursor, E);
     mark(1);
     {   // router logits
         PfGemmArgs a{};
@@ -633,14 +667,16 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
     mark(2);
     if (E <= 512)
         hipLaunchKernelGGL((pf_route_kernel<8>), dim3((N + 3) / 4), dim3(256), 0, st, ws.logits, ws.xb, w->sgate, N, E, K,
-                           D, ws.ids, ws.wts, ws.sg, ws.cnt, ws.rank);
+                           D, ws.ids, ws.wts, ws.sg);
     else
         hipLaunchKernelGGL((pf_route_kernel<16>), dim3((N + 3) / 4), dim3(256), 0, st, ws.logits, ws.xb, w->sgate, N, E, K,
-                           D, ws.ids, ws.wts, ws.sg, ws.cnt, ws.rank);
+                           D, ws.ids, ws.wts, ws.sg);
     mark(3);
-    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, st, ws.cnt, E, ws.exp_off, ws.tiles, ws.n_tiles);
+    hipLaunchKernelGGL(pf_hist_kernel, dim3((unsigned) ws.n_wg), dim3(256), 0, st, ws.ids, n_ent, E, ws.cursor,
+                       ws.wg_base, ws.rank);
+    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, st, ws.cursor, E, ws.exp_off, ws.tiles, ws.n_tiles);
     hipLaunchKernelGGL(pf_scatter_kernel, dim3((unsigned) ((n_ent + 255) / 256)), dim3(256), 0, st, ws.ids, ws.rank,
-                       ws.exp_off, n_ent, K, ws.ent_tok, ws.ent_pos);
+                       ws.wg_base, ws.exp_off, n_ent, K, E, ws.ent_idx, ws.ent_pos);
     // shared expert gate|up + SwiGLU, then down -> comb = sigmoid(sg) * shared
     mark(4);
     {
@@ -665,7 +701,7 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
         a.experts = w->experts; a.rec = o.rec; a.codes_off = o.gu_codes; a.scales_off = o.gu_scales;
         a.tail_off = o.tail; a.K = D; a.F = F; a.gx = F / 128;
         a.tiles = ws.tiles; a.n_tiles = ws.n_tiles;
-        a.a = ws.xb; a.tok = ws.ent_tok;
+        a.a = ws.xb; a.tok = ws.ent_idx; a.topk = K;
         a.act = ws.act; a.ld_out = F;
         launch_expert<false>(a, ws.max_tiles, st);
     }
@@ -675,11 +711,11 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
         b.experts = w->experts; b.rec = o.rec; b.codes_off = o.dn_codes; b.scales_off = o.dn_scales;
         b.tail_off = o.tail; b.K = F; b.F = 0; b.gx = D / 256;
         b.tiles = ws.tiles; b.n_tiles = ws.n_tiles;
-        b.a = ws.act; b.tok = nullptr;
+        b.a = ws.act; b.tok = nullptr; b.topk = K;
         b.y = ws.y; b.ld_out = D;
         launch_expert<true>(b, ws.max_tiles, st);
-        hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned) ((D / 4 + 255) / 256), (unsigned) N), dim3(256), 0, st,
-                           ws.y, ws.ent_pos, ws.wts, K, D, comb);
+        hipLaunchKernelGGL((pf_combine_kernel<8>), dim3((unsigned) ((D / 4 + 255) / 256), (unsigned) N), dim3(256), 0,
+                           st, ws.y, ws.ent_pos, ws.wts, K, D, comb);
     }
     mark(8);
 }
