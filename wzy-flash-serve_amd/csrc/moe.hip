@@ -82,6 +82,14 @@ WZY_DEV int excl_count256(bool pred, int* s_c, int& total) {
 
 // int8 quantisation, reference rule d = amax/127, q = rint(x * 127/amax) clamped to +-127.
 // 32 values -> two 16-value halves with one shared per-32 scale
+constexpr int SH_J = 8;            // shared-expert SwiGLU outputs per gate/up workgroup
+
+// moe_down dynamic LDS: the shared activation's per-32 scales, padded to 16 bytes
+__host__ __device__ inline int dn_shs_floats(int T, int nchunk) { return (T * nchunk + 3) / 4 * 4; }
+__host__ __device__ inline size_t dn_shared_lds(int T, int nchunk) {
+    return (size_t) T * nchunk * 2 * sizeof(int4) + (size_t) dn_shs_floats(T, nchunk) * sizeof(float);
+}
+
 WZY_DEV void quant32_halves(const float (&v)[32], int4& qa, int4& qb, float& d) {
     float am = 0.f;
 #pragma unroll
@@ -98,6 +106,26 @@ WZY_DEV void quant32_halves(const float (&v)[32], int4& qa, int4& qb, float& d) 
     }
     qa = make_int4(w[0], w[1], w[2], w[3]);
     qb = make_int4(w[4], w[5], w[6], w[7]);
+}
+// The same per-32 quantisation with 4 lanes per block (a lane quad): lane q of the quad holds values
+// 8q .. 8q+7 and gets their 8 codes (bytes 8q .. 8q+7 of the block) and the block scale.
+WZY_DEV uint2 quant32_quad(const float (&v)[8], float& d) {
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_XOR2>(am));
+    d = am / 127.0f;
+    const float inv = d > 0.f ? 127.0f / am : 0.f;
+    uint32_t w[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        uint32_t pk = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pk |= (uint32_t) (max(-127, min(127, rn_int(v[4 * k + j] * inv))) & 0xFF) << (8 * j);
+        w[k] = pk;
+    }
+    return make_uint2(w[0], w[1]);
 }
 // 32 values -> two 16-value halves, each quantised to int8 with its own per-16 scale, written as
 // the f16 pairs of nvfp4_chunk_fma_h: xp[8h + p] = (q[16h + p], q[16h + p + 8]).
@@ -234,7 +262,8 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 // gate/up.  Routed workgroups: one (group, 16-row tile); wave w owns rows j = 16*tile + 4w .. +3
 // of both gate and up, so SwiGLU and the 16-wide requant stay inside the workgroup.
 // reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
-// Shared workgroups: 32 rows of the Q8_0 shared gate/up, SwiGLU, per-32 requant.
+// Shared workgroups: 8 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32 requant of
+// silu_mul_quant32_multi runs in moe_down, so the 2.2 MB shared stream spreads over F/8 workgroups).
 // reference: launch_gemm_q8p x2 + silu_mul_quant32_multi (src/wzy_stage_v2.cuh:711-713;
 // src/wzy_kernels_v2.cuh:1247-1280).
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
@@ -388,24 +417,22 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
         return;
     }
 
-    // shared expert: rows j in [32*sb, 32*sb + 32), wave w owns j = 32*sb + 8w .. +7 (two halves of 4)
+    // shared expert: rows j in [8*sb, 8*sb + 8), wave w owns j = 8*sb + 2w, +1 (gate and up rows);
+    // one 32-block of x per lane.  The SwiGLU values go out as fp32; moe_down quantises them per 32.
     const int sb = bid - a.n_routed_wg;
-    int4 c0[2][8], c1[2][8];
-    uint32_t sraw[2][8];             // 16-bit scales in 32-bit registers (no packing that waits for the load)
+    int4 c0[4], c1[4];
+    uint32_t sraw[4];                // 16-bit scales in 32-bit registers (no packing that waits for the load)
     const int bl = min(lane, nc - 1);
+    const int j0 = SH_J * sb + 2 * w;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        const int j0 = 32 * sb + 8 * w + 4 * half;
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const int8_t* q = (rr < 4) ? a.shg_q : a.shu_q;
-            const uint16_t* s = (rr < 4) ? a.shg_s : a.shu_s;
-            const int row = j0 + (rr & 3);
-            const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) bl * 32);
-            c0[half][rr] = ld_stream_i4(cp);
-            c1[half][rr] = ld_stream_i4(cp + 1);
-            sraw[half][rr] = s[(size_t) row * nc + bl];
-        }
+    for (int rr = 0; rr < 4; ++rr) {
+        const int8_t* q = (rr < 2) ? a.shg_q : a.shu_q;
+        const uint16_t* s = (rr < 2) ? a.shg_s : a.shu_s;
+        const int row = j0 + (rr & 1);
+        const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) bl * 32);
+        c0[rr] = ld_stream_i4(cp);
+        c1[rr] = ld_stream_i4(cp + 1);
+        sraw[rr] = s[(size_t) row * nc + bl];
     }
     // stage x quantised per 32
     for (int i = tid; i < T * nc; i += 256) {
@@ -424,45 +451,31 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
         s_sc[i] = d;
     }
     __syncthreads();
+    float acc[4][T];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        float acc[8][T];
+    for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[rr][t] = 0.f;
-        for (int b = lane; b < nc; b += 64) {            // D <= 2048: one 32-block per lane
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const int xi = t * nc + b;
-                const int4 x0 = s_qa[xi], x1 = s_qb[xi];
-                const float xsc = s_sc[xi];
-#pragma unroll
-                for (int rr = 0; rr < 8; ++rr)
-                    acc[rr][t] = fmaf(h16_to_f(sraw[half][rr]) * xsc,
-                                      (float) (dot16(c0[half][rr], x0) + dot16(c1[half][rr], x1)), acc[rr][t]);
-            }
-        }
+        for (int t = 0; t < T; ++t) acc[rr][t] = 0.f;
+    for (int b = lane; b < nc; b += 64) {                // D <= 2048: one 32-block per lane
 #pragma unroll
         for (int t = 0; t < T; ++t) {
+            const int xi = t * nc + b;
+            const int4 x0 = s_qa[xi], x1 = s_qb[xi];
+            const float xsc = s_sc[xi];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float gv = wave_sum(acc[q][t]);
-                const float uv = wave_sum(acc[4 + q][t]);
-                if (lane == 0) s_act[t][8 * w + 4 * half + q] = siluf_(gv) * uv;
-            }
+            for (int rr = 0; rr < 4; ++rr)
+                acc[rr][t] = fmaf(h16_to_f(sraw[rr]) * xsc, (float) (dot16(c0[rr], x0) + dot16(c1[rr], x1)),
+                                  acc[rr][t]);
         }
     }
-    __syncthreads();
-    if (tid < T * 32) {
-        const int t = tid >> 5, jj = tid & 31;
-        const float v = s_act[t][jj];
-        const float amax = max32(fabsf(v));
-        const float d = amax / 127.0f;
-        const float inv = d > 0.f ? 127.0f / amax : 0.f;
-        const int q = max(-127, min(127, rn_int(v * inv)));
-        a.shq32[(size_t) t * F + 32 * sb + jj] = (int8_t) q;
-        if (jj == 0) a.shs32[(size_t) t * (F / 32) + sb] = d;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float gv = wave_sum(acc[q][t]);
+            const float uv = wave_sum(acc[2 + q][t]);
+            if (lane == 0) a.shact[(size_t) t * F + j0 + q] = siluf_(gv) * uv;
+        }
     }
 }
 
@@ -492,11 +505,12 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     constexpr int DN_BATCH = dn_batch<T>();
     // the group tables of every possible group are loaded without waiting for the group count
     const int ng = *a.n_groups;
-    uint4* s_ah = (uint4*) s_dyn;                     // [n_ent * nchunk][4]: 16 f16 pairs per chunk
-    float* s_as = (float*) (s_ah + (size_t) n_ent * nchunk * 4);
-    int4* s_sha = (int4*) (s_as + (size_t) n_ent * (F / 16));
+    // shared activation quantised per 32 (both variants), then (STAGE) the routed activations
+    int4* s_sha = (int4*) s_dyn;                      // [T * nchunk] first / second 16-byte halves
     int4* s_shb = s_sha + (size_t) T * nchunk;
     float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
+    uint4* s_ah = (uint4*) (s_shs + dn_shs_floats(T, nchunk));   // [n_ent * nchunk][4]: 16 f16 pairs per chunk
+    float* s_as = (float*) (s_ah + (size_t) n_ent * nchunk * 4);
     // Item `tid` of every table and staging copy is loaded (clamped index, no branch) before the
     // first LDS write: a stride loop per table would wait for one table's loads before requesting
     // the next.  Only copies of more than 256 items loop for the rest.
@@ -509,19 +523,19 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         for (int m = 0; m < WZY_MAX_W; ++m) gmem[m] = a.grp_mem[ie * WZY_MAX_W + m];
         const float wt = a.wts[ie], sgv = a.sg[min(tid, T - 1)];
         uint4 xh[4];
-        int4 ha, hb;
         float4 xs4;
-        float hs;
         if (STAGE) {
             const uint4* xp = (const uint4*) (a.ah16 + (size_t) min(tid, n_aq - 1) * 32);
 #pragma unroll
             for (int k = 0; k < 4; ++k) xh[k] = xp[k];
             xs4 = ((const float4*) a.as16)[min(tid, n_as4 - 1)];
-            const int ih = min(tid, n_sh - 1);
-            const int4* hp = (const int4*) (a.shq32 + (size_t) ih * 32);
-            ha = hp[0];
-            hb = hp[1];
-            hs = a.shs32[ih];
+        }
+        float hv[8];                                  // shared activations 8q .. 8q+7 of block tid/4
+        {
+            const float4* hp = (const float4*) (a.shact + (size_t) min(tid >> 2, n_sh - 1) * 32 + (tid & 3) * 8);
+            const float4 f0 = hp[0], f1 = hp[1];
+            hv[0] = f0.x; hv[1] = f0.y; hv[2] = f0.z; hv[3] = f0.w;
+            hv[4] = f1.x; hv[5] = f1.y; hv[6] = f1.z; hv[7] = f1.w;
         }
         if (tid < n_ent) {
             s_gexp[tid] = gexp;
@@ -536,10 +550,14 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) s_ah[(size_t) tid * 4 + k] = xh[k];
             if (tid < n_as4) ((float4*) s_as)[tid] = xs4;
-            if (tid < n_sh) {
-                s_sha[tid] = ha;
-                s_shb[tid] = hb;
-                s_shs[tid] = hs;
+        }
+        {                                             // silu_mul_quant32: d = amax/127, q = rint(v*127/amax)
+            float hs;
+            const uint2 hq = quant32_quad(hv, hs);    // all lanes: the quad max reads its neighbours
+            const int ib = tid >> 2, q = tid & 3;
+            if (tid < 4 * n_sh) {
+                ((uint2*) (q < 2 ? s_sha : s_shb))[ib * 2 + (q & 1)] = hq;
+                if (q == 0) s_shs[ib] = hs;
             }
         }
     }
@@ -557,12 +575,16 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             for (int k = 0; k < 4; ++k) s_ah[(size_t) i * 4 + k] = xp[k];
         }
         for (int i = tid + 256; i < n_as4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
-        for (int i = tid + 256; i < n_sh; i += 256) {
-            const int4* xp = (const int4*) (a.shq32 + (size_t) i * 32);
-            s_sha[i] = xp[0];
-            s_shb[i] = xp[1];
-            s_shs[i] = a.shs32[i];
-        }
+    }
+    for (int i = tid + 256; i < 4 * n_sh; i += 256) {  // whole quads leave the loop together
+        const float4* hp = (const float4*) (a.shact + (size_t) (i >> 2) * 32 + (i & 3) * 8);
+        const float4 f0 = hp[0], f1 = hp[1];
+        const float hv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        float hs;
+        const uint2 hq = quant32_quad(hv, hs);
+        const int ib = i >> 2, q = i & 3;
+        ((uint2*) (q < 2 ? s_sha : s_shb))[ib * 2 + (q & 1)] = hq;
+        if (q == 0) s_shs[ib] = hs;
     }
     __syncthreads();
     const MoeOffsets o = moe_offsets(D, F);
@@ -641,15 +663,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
                     const float dw = h16_to_f((uint16_t) sraw[b]);
 #pragma unroll
                     for (int t = 0; t < T; ++t) {
-                        if (STAGE) {
-                            const int xi = t * nchunk + c;
-                            acc[b][t] = fmaf(dw * s_shs[xi], (float) (dot16(c0[b], s_sha[xi]) + dot16(c1[b], s_shb[xi])),
-                                             acc[b][t]);
-                        } else {
-                            const int4* xp = (const int4*) (a.shq32 + (size_t) t * F + (size_t) c * 32);
-                            const float xsc = a.shs32[(size_t) t * nchunk + c];
-                            acc[b][t] = fmaf(dw * xsc, (float) (dot16(c0[b], xp[0]) + dot16(c1[b], xp[1])), acc[b][t]);
-                        }
+                        const int xi = t * nchunk + c;
+                        acc[b][t] = fmaf(dw * s_shs[xi], (float) (dot16(c0[b], s_sha[xi]) + dot16(c1[b], s_shb[xi])),
+                                         acc[b][t]);
                     }
                 }
             }
@@ -716,8 +732,7 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
     w.grp_mem = a.take<int>((size_t) n_ent * WZY_MAX_W);
     w.ah16 = a.take<uint16_t>((size_t) n_ent * F);
     w.as16 = a.take<float>((size_t) n_ent * F / 16);
-    w.shq32 = a.take<int8_t>((size_t) T * F);
-    w.shs32 = a.take<float>((size_t) T * F / 32);
+    w.shact = a.take<float>((size_t) T * F);
     if (need) *need = a.off;
     return w;
 }
@@ -752,7 +767,7 @@ static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float*
     a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt;
     a.grp_mem = ws.grp_mem; a.ah16 = ws.ah16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
-    a.shq32 = ws.shq32; a.shs32 = ws.shs32;
+    a.shact = ws.shact;
     a.n_routed_wg = (w->n_ff / 16) * T * w->top_k;
     return a;
 }
@@ -761,7 +776,7 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
     a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.K = w->top_k;
     a.n_groups = ws.n_groups; a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
     a.ah16 = ws.ah16; a.as16 = ws.as16; a.shd_q = w->sh_down_q; a.shd_s = w->sh_down_s;
-    a.shq32 = ws.shq32; a.shs32 = ws.shs32; a.wts = ws.wts; a.sg = ws.sg; a.comb = comb;
+    a.shact = ws.shact; a.wts = ws.wts; a.sg = ws.sg; a.comb = comb;
     return a;
 }
 
@@ -769,22 +784,23 @@ template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
     if (a.E <= 512)
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / SH_J), dim3(256), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / 32), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / SH_J), dim3(256), lds, st, a);
 }
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
+    const size_t lds_sh = dn_shared_lds(T, a.F / 32);
     if (lds <= (size_t) DN_STAGE_BYTES)
         hipLaunchKernelGGL((moe_down_kernel<T, true, CI>), dim3(a.D / DN_TILE), dim3(256), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_down_kernel<T, false, CI>), dim3(a.D / DN_TILE), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((moe_down_kernel<T, false, CI>), dim3(a.D / DN_TILE), dim3(256), lds_sh, st, a);
 }
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
     const int n_ent = T * a.K, nchunk = a.F / 32;
-    const size_t lds = (size_t) n_ent * nchunk * 4 * sizeof(uint4) + (size_t) n_ent * (a.F / 16) * sizeof(float) +
-                       (size_t) T * nchunk * (2 * sizeof(int4) + sizeof(float));
+    const size_t lds = dn_shared_lds(T, nchunk) + (size_t) n_ent * nchunk * 4 * sizeof(uint4) +
+                       (size_t) n_ent * (a.F / 16) * sizeof(float);
     switch ((nchunk + 15) / 16) {
         case 1: launch_dn_tc<T, 1>(a, lds, st); break;
         case 2: launch_dn_tc<T, 2>(a, lds, st); break;

@@ -34,7 +34,8 @@ struct MoeWs {
     int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // distinct experts of the window
     uint16_t* ah16; float* as16;          // SwiGLU activations per routed entry: per-16 int8 values held
                                           // as f16 pairs [n_ent][F/16][8][2] (x_p, x_p+8), and their scales
-    int8_t* shq32; float* shs32;          // shared-expert SwiGLU activation, per-32 int8
+    float* shact;                         // shared-expert SwiGLU activation [T][F] (fp32; per-32
+                                          // int8 quantisation happens in moe_down)
 };
 
 struct MoeGuArgs {
@@ -43,14 +44,14 @@ struct MoeGuArgs {
     int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // published by workgroup 0
     uint16_t* ah16; float* as16;
     const int8_t* shg_q; const uint16_t* shg_s; const int8_t* shu_q; const uint16_t* shu_s;
-    int8_t* shq32; float* shs32;
+    float* shact;
     int n_routed_wg;
 };
 struct MoeDnArgs {
     const uint8_t* experts; int D, F, K;
     const int* n_groups; const int* grp_exp; const int* grp_cnt; const int* grp_mem;
     const uint16_t* ah16; const float* as16;
-    const int8_t* shd_q; const uint16_t* shd_s; const int8_t* shq32; const float* shs32;
+    const int8_t* shd_q; const uint16_t* shd_s; const float* shact;
     const float* wts; const float* sg; float* comb;
 };
 
