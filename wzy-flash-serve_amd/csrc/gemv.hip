@@ -727,9 +727,16 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
 }
 
 template <int T>
-static void launch_segs_lds_t(const GemvSegs& segs, int waves, int nbl, const float* x, int cols, int flags,
+static void launch_segs_lds_t(const GemvSegs& segs, int waves, int nbl, int rpw, const float* x, int cols, int flags,
                               size_t lds, hipStream_t st) {
     const int blocks = (waves + 3) / 4;
+    if (nbl == 1 && rpw == 2) {          // a small projection spread over more workgroups
+        if (segs.gdn.ss)
+            hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 2, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags);
+        else
+            hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 2, false>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags);
+        return;
+    }
     if (segs.gdn.ss) {
         switch (nbl) {
             case 1: hipLaunchKernelGGL((gemv_segs_lds_kernel<T, 1, 4, true>), dim3(blocks), dim3(256), lds, st, segs, x, cols, flags); break;
@@ -759,6 +766,8 @@ static void launch_segs_t(const GemvSegs& segs, int waves, int nbl, const float*
 }
 
 namespace wzy {
+constexpr int GEMV_FILL_WGS = 256;      // one workgroup per CU of an MI355X
+
 int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t st) {
     WZY_REQUIRE(x && segs.n >= 1 && segs.n <= GEMV_MAX_SEGS, "gemv_segs: bad segment list");
     WZY_REQUIRE(cols >= 32 && cols % 32 == 0 && cols <= 8192, "gemv_segs: cols must be a multiple of 32 in [32, 8192]");
@@ -771,8 +780,19 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     const bool use_lds = lds <= 48 * 1024;
     WZY_REQUIRE(!segs.gdn.ss || (use_lds && cols % 128 == 0), "gemv_segs: the GDN staging transform needs the LDS path");
     // rows per wave: the LDS kernel holds RPW Q8_0 rows or RPW/2 bf16 rows per wave (RPW = 4 for one
-    // 32-block per lane, else 2); the other kernel RPW rows of either kind (4 / 2 / 1)
-    const int rpw = nbl == 1 ? 4 : (use_lds || nbl <= 3 ? 2 : 1);
+    // 32-block per lane, else 2; 2 also when 4 would leave CUs without a workgroup); the other kernel
+    // RPW rows of either kind (4 / 2 / 1)
+    int rpw = nbl == 1 ? 4 : (use_lds || nbl <= 3 ? 2 : 1);
+    auto count_waves = [&](int rp) {
+        int wv = 0;
+        for (int i = 0; i < segs.n; ++i) {
+            const GemvSeg& s = segs.seg[i];
+            const int r = (use_lds && s.kind == GEMV_BF16) ? rp / 2 : rp;
+            wv += (s.rows + r - 1) / r;
+        }
+        return wv;
+    };
+    if (use_lds && nbl == 1 && (count_waves(4) + 3) / 4 < GEMV_FILL_WGS) rpw = 2;
     int waves = 0;
     for (int i = 0; i < segs.n; ++i) {
         GemvSeg& s = segs.seg[i];
@@ -785,14 +805,14 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     }
     if (use_lds) {
         switch (T) {
-            case 1: launch_segs_lds_t<1>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 2: launch_segs_lds_t<2>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 3: launch_segs_lds_t<3>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 4: launch_segs_lds_t<4>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 5: launch_segs_lds_t<5>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 6: launch_segs_lds_t<6>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            case 7: launch_segs_lds_t<7>(segs, waves, nbl, x, cols, flags, lds, st); break;
-            default: launch_segs_lds_t<8>(segs, waves, nbl, x, cols, flags, lds, st); break;
+            case 1: launch_segs_lds_t<1>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 2: launch_segs_lds_t<2>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 3: launch_segs_lds_t<3>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 4: launch_segs_lds_t<4>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 5: launch_segs_lds_t<5>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 6: launch_segs_lds_t<6>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            case 7: launch_segs_lds_t<7>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
+            default: launch_segs_lds_t<8>(segs, waves, nbl, rpw, x, cols, flags, lds, st); break;
         }
         WZY_LAUNCH_CHECK();
         return WZY_OK;
