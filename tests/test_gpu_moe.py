@@ -456,3 +456,22 @@ def test_moe_prefill_tensor_scales(wz, orc, gpu):
     np.testing.assert_allclose(comb[cr], comb_o[cr], rtol=2e-2, atol=1e-2)
     err = np.abs(comb[cr] - comb_o[cr]).max() / np.abs(comb_o[cr]).max()
     assert err < 3e-3, err
+
+
+def test_moe_prefill_time_entry(wz, gpu):
+    """The measurement entry point reports a positive time for every launch group and leaves the
+    same (bit-identical) block output as a plain call."""
+    D, F, E, K, N = 256, 128, 64, 4, 300
+    m = mi.make_layer(wz, 6, 0, D, F, E, K, blobs=[])
+    w, keep = device_layer(wz, m)
+    x = mi.make_x(wz, 6, 0, N, D)
+    comb0, ids0, _ = run_gpu_prefill(wz, w, x, N)
+    xd = dev(x)
+    comb = DA(N * D, np.float32)
+    nws = wz.wzy_moe_prefill_workspace_bytes(D, F, E, K, N)
+    ws = DA(nws, np.uint8)
+    us = (C.c_float * 8)()
+    wz.wzy_moe_prefill_time(C.byref(w), xd.ptr, N, comb.ptr, ws.ptr, nws, 3, us, None)
+    wz.wzy_device_sync()
+    assert all(0.0 < us[i] < 1e5 for i in range(8)), list(us)
+    np.testing.assert_array_equal(host(comb), comb0)

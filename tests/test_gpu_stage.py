@@ -15,6 +15,8 @@ decision (router top-k, indexer top-k).  Hence:
     undecidable row are not compared, because their state already differs.
 Tolerance (north star: floats rel 2e-2 / abs 1e-2 on hidden states and logits), applied to the
 whole vector: max|gpu - oracle| <= 1e-2 + 2e-2 * max|oracle|."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -327,5 +329,45 @@ def test_stage_state_tracks_oracle(wz, gpu, kind):
                     assert d.max() <= 1e-3 * max(1.0, np.abs(o).max()), name
                 else:
                     assert d.max() <= 1, name
+    finally:
+        st.close()
+
+
+def test_stage_moe_weights_prefill_matches_decode(wz, gpu):
+    """A loaded stage hands out a layer's MoE weights; the prefill block on them agrees with the
+    decode block on the same rows (bf16 vs int8 activations: within the float tolerance)."""
+    cfg = small_cfg(wzy_amd, ctx_max=256, n_layers=2, topk=64)
+    cfg.n_exp = 64
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(3, 16)
+        w = wzy_amd.MoeWeights()
+        wz.wzy_stage_moe_weights(st.h, 1, C.byref(w))
+        assert (w.n_embd, w.n_ff, w.n_exp, w.top_k) == (256, 128, 64, 4) and w.experts and w.router
+        with pytest.raises(wzy_amd.WzyError):
+            wz.wzy_stage_moe_weights(st.h, 2, C.byref(wzy_amd.MoeWeights()))
+        T, D, K = 8, 256, 4
+        x = np.random.default_rng(5).standard_normal((T, D)).astype(np.float32)
+        xd = wzy_amd.DeviceArray.from_numpy(x)
+        outs = []
+        for prefill in (True, False):
+            comb = wzy_amd.DeviceArray(T * D, np.float32)
+            ids = wzy_amd.DeviceArray(T * K, np.int32)
+            wts = wzy_amd.DeviceArray(T * K, np.float32)
+            if prefill:
+                nws = wz.wzy_moe_prefill_workspace_bytes(D, 128, 64, K, T)
+                ws = wzy_amd.DeviceArray(nws, np.uint8)
+                wz.wzy_moe_prefill(C.byref(w), xd.ptr, T, comb.ptr, ids.ptr, wts.ptr, ws.ptr, nws, None)
+            else:
+                nws = wz.wzy_moe_workspace_bytes(D, 128, 64, K, T)
+                ws = wzy_amd.DeviceArray(nws, np.uint8, zero=True)
+                wz.wzy_moe_block(C.byref(w), xd.ptr, T, comb.ptr, ids.ptr, wts.ptr, ws.ptr, nws, None)
+            wz.wzy_device_sync()
+            outs.append((comb.numpy(), ids.numpy(), wts.numpy()))
+        (cp, ip, wp), (cd, idd, wd) = outs
+        same = [np.array_equal(np.sort(ip[t * K:(t + 1) * K]), np.sort(idd[t * K:(t + 1) * K])) for t in range(T)]
+        assert sum(same) >= T - 1, same
+        rows = np.repeat(np.array(same), D)
+        check_close("prefill vs decode MoE", cp[rows], cd[rows])
     finally:
         st.close()
