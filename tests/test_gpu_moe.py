@@ -475,3 +475,36 @@ def test_moe_prefill_time_entry(wz, gpu):
     wz.wzy_device_sync()
     assert all(0.0 < us[i] < 1e5 for i in range(8)), list(us)
     np.testing.assert_array_equal(host(comb), comb0)
+
+
+def test_moe_prefill_full_chunk_rows(wz, orc, gpu):
+    """BASELINE config 5 at full size: one 8,192-token chunk through the BASELINE layer.  A token's
+    output depends on its own row only (tiles mix tokens, sums do not), so sampled rows equal, bit for
+    bit, the same rows run as a chunk of their own; and those rows match the oracle."""
+    D, F, E, K, N = 2048, 512, 512, 10, 8192
+    print(f"prefill full chunk N={N}", flush=True)
+    m = mi.make_layer(wz, 4, 2, D, F, E, K, blobs=[])
+    w, keep = device_layer(wz, m)
+    x = np.random.default_rng(11).standard_normal((N, D)).astype(np.float32)
+    comb, ids, wts = run_gpu_prefill(wz, w, x, N)
+    pick = np.array([0, 1, 777, 4096, 5000, N - 2, N - 1])
+    c2, i2, w2 = run_gpu_prefill(wz, w, x[pick], len(pick))
+    np.testing.assert_array_equal(i2.reshape(-1, K), ids.reshape(N, K)[pick])
+    np.testing.assert_array_equal(w2.reshape(-1, K), wts.reshape(N, K)[pick])
+    np.testing.assert_array_equal(c2.reshape(-1, D), comb.reshape(N, D)[pick])
+    # oracle on the sampled rows (their routed experts materialised on the host)
+    xs = np.ascontiguousarray(x[pick])
+    logits = prefill_logits(m, xs)
+    for t in range(len(pick)):
+        for e in np.argsort(-logits[t], kind="stable")[:K + 4].tolist():
+            if e not in m.blobs:
+                m.blobs[e] = mi.expert_blob(wz, 4, 2, e, D, F)
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    T = len(pick)
+    comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
+    assert orc.orc_moe_prefill(C.byref(ow), ptr(xs.ravel()), T, ptr(comb_o), ptr(ids_o), ptr(wts_o)) == 0
+    assert check_ids(orc, logits.ravel(), E, K, T, i2, ids_o) == T
+    np.testing.assert_allclose(c2, comb_o, rtol=2e-2, atol=1e-2)
+    err = np.abs(c2 - comb_o).max() / np.abs(comb_o).max()
+    assert err < 3e-3, err
