@@ -5,17 +5,17 @@
 //   2. pf_gemm     router logits [N x E] = x . router^T                      (bf16 weights)
 //   3. pf_route    per token, one wave: softmax top-K (the decode routing: probability desc, id asc,
 //                  weights renormalised by max(sum, 2^-14)) and the shared-expert gate sg = sgate . x
-//   4. pf_group    one workgroup: entries (token, slot) grouped by expert into 64-entry tiles
-//   5. pf_gemm     shared expert gate|up (Q8_0 -> bf16) with SwiGLU epilogue -> sh_act bf16 [N x F]
-//   6. pf_gemm     shared expert down (Q8_0 -> bf16) -> comb = sigmoid(sg) * shared   (initialises comb)
-//   7. pf_gemm     routed gate|up per tile (NVFP4 -> bf16) with SwiGLU epilogue -> act bf16 [N*K x F]
-//   8. pf_gemm     routed down per tile (NVFP4 -> bf16) -> comb += w_k * expert_k  (fp32 atomics)
-// pf_gemm: workgroup tile 64 rows (tokens / entries) x 64 weight rows, K stepped by 64 through two
-// LDS buffers; each of the 4 waves owns a 32 x 32 block accumulated by v_mfma_f32_32x32x16_bf16.
-// Weights are dequantised to bf16 while staged: e2m1 codes through the fp4 -> bf16 conversion
-// instruction times the e4m3 block scale and the tensor scale (exact: at most 8 significant bits),
-// Q8_0 codes times their fp16 scale (rounded to bf16).  The next K step's global loads are issued
-// before the current step's MFMAs.
+//   4. pf_hist, pf_tiles, pf_scatter: entries (token, slot) grouped by expert into tiles of up to
+//                  256 (LDS-histogram ranks, one reserving atomic per expert and workgroup, one scan)
+//   5. pf_expert<gate|up, Q8_0>  shared expert, dense 128-token blocks, SwiGLU -> sh_act bf16 [N x F]
+//   6. pf_expert<down, Q8_0>     shared expert, dense 256-token blocks -> comb = sigmoid(sg) * shared
+//   7. pf_expert<gate|up, NVFP4> routed, one expert tile per workgroup, SwiGLU -> act bf16 [N*K x F]
+//   8. pf_expert<down, NVFP4>    routed -> y fp32 [N*K x D] per entry; pf_combine: comb[t] +=
+//                  sum_k w_k * y[pos(t, k)] in slot order (no float atomics)
+// pf_expert: 8 waves, 256 weight rows per workgroup, up to 256 A rows; weights staged through LDS in
+// coalesced 128-k chunks and dequantised by each lane into its v_mfma_f32_32x32x16_bf16 B fragment
+// (e2m1 x e4m3 block scale is exact in bf16, the fp32 tensor scale goes onto the accumulators;
+// Q8_0 code x fp16 scale is rounded to bf16).  pf_gemm: 64 x 64 LDS-tiled bf16 GEMM (router).
 // reference: pf_moe_gu_wmma_kernel, pf_moe_down_wmma_kernel, the tile builder and the shared/router
 // prefill GEMMs (src/wzy_prefill_tc.cuh:99-443), with fp16 replaced by bf16.
 #include "wzy_device.h"
@@ -32,45 +32,43 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 
 namespace {
 
-constexpr int PB = 64;             // dense GEMM: tile rows (M), weight rows (N) and K step
+constexpr int PB = 64;             // router GEMM: tile rows (M), weight rows (N) and K step
 constexpr int PB_LD = PB + 8;      // LDS row stride in bf16 (16-byte aligned rows, staggered banks)
 constexpr int PF_MAX_E = 1024;
 constexpr int MT = 256;            // expert GEMM: entries per tile (8 MFMA row blocks of 32)
 constexpr int EK = 64;             // expert GEMM: K step between barriers (four MFMA k16 slices)
 constexpr int EA_LD = EK + 8;      // LDS row stride of the staged activations, bf16
 
-enum { PW_BF16 = 0, PW_Q8 = 1 };                      // dense weight formats
-enum { PE_F32 = 0, PE_SWIGLU = 1, PE_SHARED = 2 };    // dense epilogues
-
 struct PfTile {
     int e, off, cnt, pad;          // expert, first entry position, entries (<= MT)
 };
 
-// Dense GEMM y = A . W^T over rows m0 .. m0+63 of A [a_rows x K] (bf16).
+// Router GEMM logits = A . W^T over rows m0 .. m0+63 of A [a_rows x K] (bf16), bf16 weights.
 struct PfGemmArgs {
     const uint16_t* a;
     int a_rows, K;
-    // weight rows of length K: bf16, or Q8_0 codes + fp16 scales per 32; SwiGLU: w2/ws2 = up rows
-    const void* w; const uint16_t* ws;
-    const void* w2; const uint16_t* ws2;
-    int n_rows;                    // weight rows (F32 epilogue bound)
-    float* y; int y_ld;            // F32 / SHARED: y[row * y_ld + n]
-    uint16_t* act; int act_ld;     // SWIGLU: act[row * act_ld + j]
-    const float* sg;               // SHARED: gate scalar per row
+    const uint16_t* w;             // weight rows of length K
+    int n_rows;                    // weight rows
+    float* y; int y_ld;            // y[row * y_ld + n]
 };
 
 // Routed-expert GEMM over expert tiles.  Gate|up: A rows = x rows of the entries' tokens, output
 // SwiGLU activations per entry; down: A rows = activations per entry, output fp32 per entry.
+// Also the dense (shared-expert) GEMMs: tiles = consecutive blocks of `a_rows` token rows, Q8_0
+// weights (gate|up: w / w2 rows, down: w rows), outputs per token row.
 struct PfExpArgs {
     const uint8_t* experts;
     size_t rec, codes_off, scales_off, tail_off;
     int K;                         // reduction length: n_embd (gate|up) or n_ff (down)
     int F;                         // gate|up: first up row of the plane
     int gx;                        // column blocks per tile
-    const PfTile* tiles; const int* n_tiles;
+    const PfTile* tiles; const int* n_tiles;   // expert tiles (null: dense blocks of dense_mt of a_rows rows)
+    int a_rows, dense_mt;
     const uint16_t* a;
     const int* tok; int topk;      // gate|up: entry position -> token * K + slot
-    uint16_t* act; float* y; int ld_out;   // outputs per entry position
+    const int8_t* w; const uint16_t* ws; const int8_t* w2; const uint16_t* ws2;   // Q8_0 weights
+    uint16_t* act; float* y; int ld_out;   // outputs per entry position (dense: per token row)
+    const float* sg;               // dense down: y = acc * sigmoid(sg[row])
 };
 
 WZY_DEV uint16_t f_to_bf16(float f) {                // hardware conversion, round to nearest even
@@ -79,53 +77,8 @@ WZY_DEV uint16_t f_to_bf16(float f) {                // hardware conversion, rou
 WZY_DEV float bf16_bits_to_f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
 WZY_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
-// Weight chunk of one dense staging thread: 16 consecutive k of one weight row.
-struct WRaw {
-    uint4 u[2];                    // BF16: 2 x 8 bf16; Q8: u[0] = 16 int8
-    uint32_t s;                    // Q8: fp16 scale bits
-};
-
-template <int WK>
-WZY_DEV WRaw load_w(const PfGemmArgs& a, int row, bool up, int k0) {
-    WRaw r;
-    if constexpr (WK == PW_Q8) {
-        const int8_t* q = (const int8_t*) (up ? a.w2 : a.w);
-        const uint16_t* sc = up ? a.ws2 : a.ws;
-        r.u[0] = *(const uint4*) (q + (size_t) row * a.K + k0);
-        r.u[1] = make_uint4(0, 0, 0, 0);
-        r.s = sc[(size_t) row * (a.K / 32) + k0 / 32];
-    } else {
-        const uint16_t* w = (const uint16_t*) (up ? a.w2 : a.w);
-        const uint4* p = (const uint4*) (w + (size_t) row * a.K + k0);
-        r.u[0] = p[0];
-        r.u[1] = p[1];
-        r.s = 0;
-    }
-    return r;
-}
-
-// dequantise to 16 bf16 (two uint4 in k order); Q8_0 values code * fp16 scale rounded to bf16
-template <int WK>
-WZY_DEV void dequant_w(const WRaw& r, uint4 (&o)[2]) {
-    if constexpr (WK == PW_Q8) {
-        const float sc = h16_to_f((uint16_t) r.s);
-        const uint32_t q[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w};
-        uint16_t v[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = f_to_bf16((float) (int8_t) (q[j >> 2] >> (8 * (j & 3))) * sc);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            o[h] = make_uint4(v[8 * h] | ((uint32_t) v[8 * h + 1] << 16), v[8 * h + 2] | ((uint32_t) v[8 * h + 3] << 16),
-                              v[8 * h + 4] | ((uint32_t) v[8 * h + 5] << 16), v[8 * h + 6] | ((uint32_t) v[8 * h + 7] << 16));
-    } else {
-        o[0] = r.u[0];
-        o[1] = r.u[1];
-    }
-}
-
-// Dense GEMM tile: 64 rows x 64 weight rows (SwiGLU: 32 gate + the matching 32 up rows), K stepped
-// by 64 through two LDS buffers, each wave a 32 x 32 block.
-template <int WK, int EPI>
+// Router GEMM tile: 64 rows x 64 weight rows, K stepped by 64 through two LDS buffers, each wave a
+// 32 x 32 block.
 __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
     __shared__ __align__(16) uint16_t sA[2][PB][PB_LD];
     __shared__ __align__(16) uint16_t sB[2][PB][PB_LD];
@@ -133,91 +86,58 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
     const int wm = w & 1, wn = w >> 1;
     const int row0 = blockIdx.y * PB;
     const int cnt = min(PB, a.a_rows - row0);
-    const int n0 = EPI == PE_SWIGLU ? blockIdx.x * 32 : blockIdx.x * PB;
+    const int n0 = blockIdx.x * PB;
     const int sr = tid >> 2, sk = (tid & 3) * 16;                // staging: row sr, k sk .. sk+15
-    const bool up = EPI == PE_SWIGLU && sr >= 32;
-    const int wrow = EPI == PE_SWIGLU ? n0 + sr - (up ? 32 : 0) : min(n0 + sr, a.n_rows - 1);
+    const int wrow = min(n0 + sr, a.n_rows - 1);
     const bool a_ok = sr < cnt;
     const uint16_t* ap = a.a + (size_t) (a_ok ? row0 + sr : 0) * a.K + sk;
+    const uint16_t* wp = a.w + (size_t) wrow * a.K + sk;
 
     f32x16_t acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     const int nk = a.K / PB;
 
-    auto load_a = [&](int ks, uint4 (&x)[2]) {
+    uint4 xa[2], xw[2];
+    auto load = [&](int ks) {
         const uint4* p = (const uint4*) (ap + (size_t) ks * PB);
-        x[0] = a_ok ? p[0] : make_uint4(0, 0, 0, 0);
-        x[1] = a_ok ? p[1] : make_uint4(0, 0, 0, 0);
+        xa[0] = a_ok ? p[0] : make_uint4(0, 0, 0, 0);
+        xa[1] = a_ok ? p[1] : make_uint4(0, 0, 0, 0);
+        const uint4* q = (const uint4*) (wp + (size_t) ks * PB);
+        xw[0] = q[0];
+        xw[1] = q[1];
     };
-    auto store = [&](int buf, const uint4 (&x)[2], const WRaw& wr) {
-        *(uint4*) &sA[buf][sr][sk] = x[0];
-        *(uint4*) &sA[buf][sr][sk + 8] = x[1];
-        uint4 o[2];
-        dequant_w<WK>(wr, o);
-        *(uint4*) &sB[buf][sr][sk] = o[0];
-        *(uint4*) &sB[buf][sr][sk + 8] = o[1];
+    auto store = [&](int buf) {
+        *(uint4*) &sA[buf][sr][sk] = xa[0];
+        *(uint4*) &sA[buf][sr][sk + 8] = xa[1];
+        *(uint4*) &sB[buf][sr][sk] = xw[0];
+        *(uint4*) &sB[buf][sr][sk + 8] = xw[1];
     };
 
-    uint4 xa[2];
-    load_a(0, xa);
-    WRaw wr = load_w<WK>(a, wrow, up, sk);
-    store(0, xa, wr);
+    load(0);
+    store(0);
     __syncthreads();
     for (int ks = 0; ks < nk; ++ks) {
         const int buf = ks & 1;
         const bool more = ks + 1 < nk;
-        if (more) {                                              // next step's loads first
-            load_a(ks + 1, xa);
-            wr = load_w<WK>(a, wrow, up, (ks + 1) * PB + sk);
-        }
+        if (more) load(ks + 1);                                  // next step's loads first
 #pragma unroll
         for (int kk = 0; kk < PB / 16; ++kk) {
             const bf16x8_t av = *(const bf16x8_t*) &sA[buf][wm * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
             const bf16x8_t bv = *(const bf16x8_t*) &sB[buf][wn * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
         }
-        if (more) store(buf ^ 1, xa, wr);
+        if (more) store(buf ^ 1);
         __syncthreads();
     }
 
-    // ---- epilogue: acc[i] = C[row 8*(i/4) + 4*(lane/32) + i%4][col lane%32] of the wave's block ----
+    // acc[i] = C[row 8*(i/4) + 4*(lane/32) + i%4][col lane%32] of the wave's block
     const int col = wn * 32 + (lane & 31);
-    if constexpr (EPI == PE_SWIGLU) {
-        float* sC = (float*) &sA[0][0][0];                          // [64][68] fp32, after the loop
-        constexpr int LDC = PB + 4;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sC[(wm * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i & 3)) * LDC + col] = acc[i];
-        __syncthreads();
-        const int m = tid >> 2, j8 = (tid & 3) * 8;                // 8 activations of row m
-        if (m < cnt) {
-            uint32_t pk[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                uint16_t hv[2];
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int j = j8 + 2 * q + b;
-                    const float g = sC[m * LDC + j], u = sC[m * LDC + 32 + j];
-                    hv[b] = f_to_bf16(g / (1.0f + __expf(-g)) * u);
-                }
-                pk[q] = hv[0] | ((uint32_t) hv[1] << 16);
-            }
-            *(uint4*) (a.act + (size_t) (row0 + m) * a.act_ld + n0 + j8) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = wm * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i & 3);
-            const int n = n0 + col;
-            if (m >= cnt) continue;
-            if constexpr (EPI == PE_F32) {
-                if (n < a.n_rows) a.y[(size_t) (row0 + m) * a.y_ld + n] = acc[i];
-            } else {
-                const float sg = a.sg[row0 + m];
-                a.y[(size_t) (row0 + m) * a.y_ld + n] = acc[i] / (1.0f + __expf(-sg));
-            }
-        }
+    for (int i = 0; i < 16; ++i) {
+        const int m = wm * 32 + 8 * (i / 4) + 4 * (lane >> 5) + (i & 3);
+        const int n = n0 + col;
+        if (m < cnt && n < a.n_rows) a.y[(size_t) (row0 + m) * a.y_ld + n] = acc[i];
     }
 }
 
@@ -257,13 +177,19 @@ WZY_DEV float2_t e4m3x2(uint32_t s) {
 }
 
 constexpr int EKB = 128;           // expert GEMM: weight chunk (k values) staged through LDS
-constexpr int EB_LD = EKB / 2 + 16;  // LDS bytes per weight row of a chunk: 64 code bytes + pad
 constexpr int EROWS = 256;         // weight rows per workgroup (8 waves x 32)
 constexpr int ETHR = 512;          // threads per expert workgroup
+enum { WF_FP4 = 0, WF_Q8 = 1 };    // weight formats of the expert GEMM
+
+// Bytes of one weight row per chunk (codes), and 16-byte pieces per thread to stage a chunk.
+template <int WF> constexpr int chunk_bytes() { return WF == WF_FP4 ? EKB / 2 : EKB; }
+template <int WF> constexpr int pieces_per_thread() { return chunk_bytes<WF>() * EROWS / 16 / ETHR; }
 
 struct ExpLane {                   // per-thread view of one expert tile
-    const uint8_t* crow0;          // staging: code bytes of the two (row, 16-byte piece) slots, chunk 0
+    const uint8_t* crow0;          // staging: code bytes of the (row, 16-byte piece) slots, chunk 0
     const uint8_t* crow1;
+    const uint8_t* crow2;          // (Q8 only)
+    const uint8_t* crow3;
     const uint8_t* srow;           // staging (threads < 256): block scales of row `tid`, chunk 0
     const uint16_t* ap;            // staging: activation row of entry sr (+ k offset sk)
     int lr;                        // the lane's weight row (local) = its B fragment column
@@ -273,19 +199,35 @@ struct ExpLane {                   // per-thread view of one expert tile
     float ts;
 };
 
+template <int WF>
 struct ExpLds {
-    uint16_t a[2][MT][EA_LD];      // activation rows, one K step (64) per buffer
-    uint8_t b[2][EROWS][EB_LD];    // weight codes, one chunk (128) per buffer
-    uint2 s[2][EROWS];             // the chunk's 8 block scales per weight row
-    int row[MT];                   // A row of each tile entry (gate|up: its token; down: its position)
+    uint16_t a[2][MT][EA_LD];                        // activation rows, one K step (64) per buffer
+    uint8_t b[2][EROWS][chunk_bytes<WF>() + 16];     // weight codes, one chunk (128 k) per buffer
+    uint2 s[2][EROWS];                               // the chunk's block scales per weight row (8 bytes)
+    int row[MT];                                     // A row of each tile entry
 };
 
+// MFMA B fragment from 8 Q8_0 codes (one k16 half) times their fp16 block scale, rounded to bf16
+// (code * scale is exact in fp32; the bf16 rounding is the dense reference's dequantisation).
+WZY_DEV bf16x8_t q8_frag(uint2 q, float sc) {
+    uint32_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = i < 2 ? q.x : q.y;
+        const float v0 = (float) (int8_t) (w >> (16 * (i & 1))) * sc;
+        const float v1 = (float) (int8_t) (w >> (16 * (i & 1) + 8)) * sc;
+        b[i] = (uint32_t) f_to_bf16(v0) | ((uint32_t) f_to_bf16(v1) << 16);
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(b[0], b[1], b[2], b[3]));
+}
+
 // K loop and epilogue of one tile with NMB active 32-entry row blocks.
-template <bool DOWN, int NMB>
-WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
+template <bool DOWN, int WF, int NMB>
+WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds<WF>& L) {
+    constexpr int CB = chunk_bytes<WF>(), NP = pieces_per_thread<WF>(), PPR = CB / 16;
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
     const int nkc = c.nk / (EKB / EK);                              // weight chunks
-    uint4 bq0 = make_uint4(0, 0, 0, 0), bq1 = bq0;
+    uint4 bq0 = make_uint4(0, 0, 0, 0), bq1 = bq0, bq2 = bq0, bq3 = bq0;
     uint2 bs = make_uint2(0, 0);
     f32x16_t acc[NMB];
 #pragma unroll
@@ -297,9 +239,14 @@ WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
         const int bb = kc & 1;
         const bool more_b = kc + 1 < nkc;
         if (more_b) {                                               // next weight chunk, coalesced
-            bq0 = *(const uint4*) (c.crow0 + (size_t) (kc + 1) * (EKB / 2));
-            bq1 = *(const uint4*) (c.crow1 + (size_t) (kc + 1) * (EKB / 2));
-            if (tid < EROWS) bs = *(const uint2*) (c.srow + (size_t) (kc + 1) * (EKB / 16));
+            const size_t o = (size_t) (kc + 1) * CB;
+            bq0 = *(const uint4*) (c.crow0 + o);
+            bq1 = *(const uint4*) (c.crow1 + o);
+            if constexpr (NP == 4) {
+                bq2 = *(const uint4*) (c.crow2 + o);
+                bq3 = *(const uint4*) (c.crow3 + o);
+            }
+            if (tid < EROWS) bs = *(const uint2*) (c.srow + (size_t) (kc + 1) * 8);
         }
         const uint2 sw = L.s[bb][c.lr];
 #pragma unroll
@@ -313,22 +260,33 @@ WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) xn[i] = *(const uint4*) (c.ap + (size_t) (ks + 1) * EK + 8 * i);
             }
-            // k16 slices 4st .. 4st+3 of the lane's row: 8 code bytes and one scale byte each
-            const uint2 q0 = *(const uint2*) &L.b[bb][c.lr][st * 32];
-            const uint2 q1 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 8];
-            const uint2 q2 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 16];
-            const uint2 q3 = *(const uint2*) &L.b[bb][c.lr][st * 32 + 24];
-            const uint32_t sv = st ? sw.y : sw.x;
-            const float2_t sc01 = e4m3x2(sv), sc23 = e4m3x2(sv >> 16);
+            bf16x8_t bfr[4];                                        // B fragments of k16 slices 4st .. 4st+3
+            if constexpr (WF == WF_FP4) {
+                // 8 code bytes and one e4m3 scale per slice
+                const uint32_t sv = st ? sw.y : sw.x;
+                const float2_t sc01 = e4m3x2(sv), sc23 = e4m3x2(sv >> 16);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint2 qq = *(const uint2*) &L.b[bb][c.lr][st * 32 + 8 * kk];
+                    const float scv = kk == 0 ? sc01.x : kk == 1 ? sc01.y : kk == 2 ? sc23.x : sc23.y;
+                    bfr[kk] = fp4_frag(qq.x, qq.y, c.sa, scv);
+                }
+            } else {
+                // 16 code bytes per slice (this lane's 8 at byte 8h); one fp16 scale per two slices
+                const uint32_t sv = st ? sw.y : sw.x;
+                const float s0 = h16_to_f((uint16_t) sv), s1 = h16_to_f((uint16_t) (sv >> 16));
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint2 qq = *(const uint2*) &L.b[bb][c.lr][st * 64 + 16 * kk + 8 * h];
+                    bfr[kk] = q8_frag(qq, kk < 2 ? s0 : s1);
+                }
+            }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const uint2 qq = kk == 0 ? q0 : kk == 1 ? q1 : kk == 2 ? q2 : q3;
-                const float scv = kk == 0 ? sc01.x : kk == 1 ? sc01.y : kk == 2 ? sc23.x : sc23.y;
-                const bf16x8_t b = fp4_frag(qq.x, qq.y, c.sa, scv);
 #pragma unroll
                 for (int mb = 0; mb < NMB; ++mb) {
                     const bf16x8_t av = *(const bf16x8_t*) &L.a[ab][mb * 32 + (lane & 31)][kk * 16 + h * 8];
-                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b, acc[mb], 0, 0, 0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bfr[kk], acc[mb], 0, 0, 0);
                 }
             }
             if (ks + 1 < c.nk) {
@@ -336,8 +294,12 @@ WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
                 for (int i = 0; i < 4; ++i) *(uint4*) &L.a[ab ^ 1][c.sr][c.sk + 8 * i] = xn[i];
             }
             if (st == EKB / EK - 1 && more_b) {                     // the next chunk into the other buffer
-                *(uint4*) &L.b[bb ^ 1][tid >> 2][(tid & 3) * 16] = bq0;
-                *(uint4*) &L.b[bb ^ 1][(ETHR + tid) >> 2][(tid & 3) * 16] = bq1;
+                *(uint4*) &L.b[bb ^ 1][tid / PPR][(tid % PPR) * 16] = bq0;
+                *(uint4*) &L.b[bb ^ 1][(ETHR + tid) / PPR][(tid % PPR) * 16] = bq1;
+                if constexpr (NP == 4) {
+                    *(uint4*) &L.b[bb ^ 1][(2 * ETHR + tid) / PPR][(tid % PPR) * 16] = bq2;
+                    *(uint4*) &L.b[bb ^ 1][(3 * ETHR + tid) / PPR][(tid % PPR) * 16] = bq3;
+                }
                 if (tid < EROWS) L.s[bb ^ 1][tid] = bs;
             }
             __syncthreads();
@@ -353,9 +315,12 @@ WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
             const int row = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
             const float v = acc[mb][i] * c.ts;
             if constexpr (DOWN) {
-                if (row < c.cnt) a.y[(size_t) (c.row0 + row) * a.ld_out + c.col] = v;
+                if (row < c.cnt) {
+                    const size_t r = (size_t) (c.row0 + row);
+                    a.y[r * a.ld_out + c.col] = a.sg ? v / (1.0f + __expf(-a.sg[r])) : v;
+                }
             } else {
-                // the matching up value from lane l ^ 16 (swizzle bit-mask mode: and 0x1F, xor 0x10)
+                // the matching up value from lane l ^ 16 (swizzle bit-mode: and 0x1F, xor 0x10)
                 const float u = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle((int) f_bits(v), 0x401F));
                 if (gate_lane && row < c.cnt)
                     a.act[(size_t) (c.row0 + row) * a.ld_out + c.col] =
@@ -369,46 +334,80 @@ WZY_DEV void expert_tile(const PfExpArgs& a, const ExpLane c, ExpLds& L) {
 // w owns one 32-row weight block (gate|up: 16 gate rows j0+16w.. in columns 0..15 and the matching
 // 16 up rows in columns 16..31, paired for SwiGLU across lanes l, l^16; down: rows n0+32w .. +31)
 // for all active 32-entry row blocks of the tile (the count selects a specialised loop), so each
-// dequantised B fragment feeds up to 8 MFMAs.  Weight codes move in 128-k chunks: each row's 64
-// code bytes are read as four 16-byte pieces by four adjacent threads (whole 64-byte segments), one
-// chunk ahead, into LDS; each lane then takes its row's 8 bytes per k16 slice from LDS and
-// dequantises them into its MFMA B fragment.  The activation rows of the tile are staged in LDS two
-// 32-k steps ahead and shared by the eight waves.  Workgroups are numbered so that consecutive
-// workgroups of one XCD take the column blocks of one tile (its activation rows stay in that XCD's
-// L2).  The tensor scale is applied to the fp32 accumulators.
-template <bool DOWN>
+// dequantised B fragment feeds up to 8 MFMAs.  Weight codes move in 128-k chunks: each row's code
+// bytes are read as 16-byte pieces by adjacent threads (whole 64-byte segments), one chunk ahead,
+// into LDS; each lane then takes its row's bytes per k16 slice from LDS and dequantises them into
+// its MFMA B fragment.  The activation rows of the tile are staged in LDS one 64-k step ahead and
+// shared by the eight waves.  Workgroups are numbered so that consecutive workgroups of one XCD take
+// the column blocks of one tile (its activation rows stay in that XCD's L2).  The tensor scale is
+// applied to the fp32 accumulators.  WF_Q8 with a null tile list runs the dense shared-expert
+// GEMMs over consecutive blocks of token rows.
+template <bool DOWN, int WF>
 __global__ void __launch_bounds__(ETHR, 1) pf_expert_kernel(PfExpArgs a) {
-    __shared__ __align__(16) ExpLds L;
+    constexpr int CB = chunk_bytes<WF>(), NP = pieces_per_thread<WF>(), PPR = CB / 16;
+    __shared__ __align__(16) ExpLds<WF> L;
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int bx = blockIdx.x, jx = bx >> 3;
     const int ti = (jx / a.gx) * 8 + (bx & 7), nb = jx % a.gx;
-    if (ti >= *a.n_tiles) return;                                   // workgroup-uniform
-    const PfTile t = a.tiles[ti];
+    const bool dense = a.tiles == nullptr;
+    if (ti >= (dense ? (a.a_rows + a.dense_mt - 1) / a.dense_mt : *a.n_tiles)) return;   // workgroup-uniform
     ExpLane c;
-    c.cnt = t.cnt;
-    c.row0 = t.off;
-    if (tid < MT) L.row[tid] = tid < c.cnt ? (DOWN ? c.row0 + tid : a.tok[c.row0 + tid] / a.topk) : 0;
-    const uint8_t* rec = a.experts + (size_t) t.e * a.rec;
-    // local weight row lr = 32w + column -> plane row: gate|up: columns 0..15 gate rows j0+16w+col,
-    // columns 16..31 up rows F+j0+16w+col-16; down: n0 + lr
-    auto grow = [&](int lr) {
+    int e = 0;
+    if (dense) {
+        c.row0 = ti * a.dense_mt;
+        c.cnt = min(a.dense_mt, a.a_rows - c.row0);
+    } else {
+        const PfTile t = a.tiles[ti];
+        c.cnt = t.cnt;
+        c.row0 = t.off;
+        e = t.e;
+    }
+    if (tid < MT)
+        L.row[tid] = tid < c.cnt ? ((DOWN || dense) ? c.row0 + tid : a.tok[c.row0 + tid] / a.topk) : 0;
+    const uint8_t* rec = a.experts + (size_t) e * a.rec;
+    // local weight row lr = 32w + column -> weight row: gate|up: columns 0..15 gate rows
+    // j0+16w+col, columns 16..31 up rows (plane row F+j0+16w+col-16, or the w2 matrix); down: n0 + lr
+    auto wrow = [&](int lr, bool& up) {
         const int wl = lr >> 5, cl = lr & 31;
-        return DOWN ? nb * EROWS + lr : (cl < 16 ? nb * 128 + wl * 16 + cl : a.F + nb * 128 + wl * 16 + cl - 16);
+        up = !DOWN && cl >= 16;
+        return DOWN ? nb * EROWS + lr : nb * 128 + wl * 16 + (cl & 15);
+    };
+    auto code_row = [&](int lr) -> const uint8_t* {
+        bool up;
+        const int r = wrow(lr, up);
+        if constexpr (WF == WF_FP4) return rec + a.codes_off + (size_t) (up ? a.F + r : r) * (a.K / 2);
+        else return (const uint8_t*) ((up ? a.w2 : a.w) + (size_t) r * a.K);
+    };
+    auto scale_row = [&](int lr) -> const uint8_t* {
+        bool up;
+        const int r = wrow(lr, up);
+        if constexpr (WF == WF_FP4) return rec + a.scales_off + (size_t) (up ? a.F + r : r) * (a.K / 16);
+        else return (const uint8_t*) ((up ? a.ws2 : a.ws) + (size_t) r * (a.K / 32));
     };
     c.lr = w * 32 + (lane & 31);
     c.col = DOWN ? nb * EROWS + c.lr : nb * 128 + w * 16 + (lane & 15);
-    const float* tail = (const float*) (rec + a.tail_off);
-    c.ts = DOWN ? tail[2] : ((lane & 16) ? tail[1] : tail[0]);
-    const uint8_t* codes = rec + a.codes_off;
-    c.crow0 = codes + (size_t) grow(tid >> 2) * (a.K / 2) + (tid & 3) * 16;
-    c.crow1 = codes + (size_t) grow((ETHR + tid) >> 2) * (a.K / 2) + (tid & 3) * 16;
-    c.srow = rec + a.scales_off + (size_t) grow(tid & (EROWS - 1)) * (a.K / 16);
+    if constexpr (WF == WF_FP4) {
+        const float* tail = (const float*) (rec + a.tail_off);
+        c.ts = DOWN ? tail[2] : ((lane & 16) ? tail[1] : tail[0]);
+    } else {
+        c.ts = 1.0f;
+    }
+    const int pp = (tid % PPR) * 16;
+    c.crow0 = code_row(tid / PPR) + pp;
+    c.crow1 = code_row((ETHR + tid) / PPR) + pp;
+    c.crow2 = NP == 4 ? code_row((2 * ETHR + tid) / PPR) + pp : c.crow0;
+    c.crow3 = NP == 4 ? code_row((3 * ETHR + tid) / PPR) + pp : c.crow0;
+    c.srow = scale_row(tid & (EROWS - 1));
     c.nk = a.K / EK;
     c.sa = 4u * h;
     // weight chunk 0
-    *(uint4*) &L.b[0][tid >> 2][(tid & 3) * 16] = *(const uint4*) c.crow0;
-    *(uint4*) &L.b[0][(ETHR + tid) >> 2][(tid & 3) * 16] = *(const uint4*) c.crow1;
+    *(uint4*) &L.b[0][tid / PPR][pp] = *(const uint4*) c.crow0;
+    *(uint4*) &L.b[0][(ETHR + tid) / PPR][pp] = *(const uint4*) c.crow1;
+    if constexpr (NP == 4) {
+        *(uint4*) &L.b[0][(2 * ETHR + tid) / PPR][pp] = *(const uint4*) c.crow2;
+        *(uint4*) &L.b[0][(3 * ETHR + tid) / PPR][pp] = *(const uint4*) c.crow3;
+    }
     if (tid < EROWS) L.s[0][tid] = *(const uint2*) c.srow;
     __syncthreads();
     c.sr = tid >> 1;                                                // staging: entry sr, k sk .. sk+31
@@ -420,14 +419,14 @@ __global__ void __launch_bounds__(ETHR, 1) pf_expert_kernel(PfExpArgs a) {
         *(uint4*) &L.a[0][c.sr][c.sk + 8 * i] = c.a_ok ? *(const uint4*) (c.ap + 8 * i) : make_uint4(0, 0, 0, 0);
     __syncthreads();
     switch ((c.cnt + 31) >> 5) {                                    // workgroup-uniform
-        case 1: expert_tile<DOWN, 1>(a, c, L); break;
-        case 2: expert_tile<DOWN, 2>(a, c, L); break;
-        case 3: expert_tile<DOWN, 3>(a, c, L); break;
-        case 4: expert_tile<DOWN, 4>(a, c, L); break;
-        case 5: expert_tile<DOWN, 5>(a, c, L); break;
-        case 6: expert_tile<DOWN, 6>(a, c, L); break;
-        case 7: expert_tile<DOWN, 7>(a, c, L); break;
-        default: expert_tile<DOWN, 8>(a, c, L); break;
+        case 1: expert_tile<DOWN, WF, 1>(a, c, L); break;
+        case 2: expert_tile<DOWN, WF, 2>(a, c, L); break;
+        case 3: expert_tile<DOWN, WF, 3>(a, c, L); break;
+        case 4: expert_tile<DOWN, WF, 4>(a, c, L); break;
+        case 5: expert_tile<DOWN, WF, 5>(a, c, L); break;
+        case 6: expert_tile<DOWN, WF, 6>(a, c, L); break;
+        case 7: expert_tile<DOWN, WF, 7>(a, c, L); break;
+        default: expert_tile<DOWN, WF, 8>(a, c, L); break;
     }
 }
 
@@ -600,15 +599,16 @@ PfWs pf_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int N, size
     return w;
 }
 
-template <int WK, int EPI>
-void launch_pf(const PfGemmArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((pf_gemm_kernel<WK, EPI>), grid, dim3(256), 0, st, a);
-}
-
 template <bool DOWN>
 void launch_expert(const PfExpArgs& a, int max_tiles, hipStream_t st) {
     const unsigned n = (unsigned) (a.gx * ((max_tiles + 7) / 8) * 8);
-    hipLaunchKernelGGL((pf_expert_kernel<DOWN>), dim3(n), dim3(ETHR), 0, st, a);
+    hipLaunchKernelGGL((pf_expert_kernel<DOWN, WF_FP4>), dim3(n), dim3(ETHR), 0, st, a);
+}
+template <bool DOWN>
+void launch_dense_q8(const PfExpArgs& a, hipStream_t st) {
+    const int nt = (a.a_rows + a.dense_mt - 1) / a.dense_mt;
+    const unsigned n = (unsigned) (a.gx * ((nt + 7) / 8) * 8);
+    hipLaunchKernelGGL((pf_expert_kernel<DOWN, WF_Q8>), dim3(n), dim3(ETHR), 0, st, a);
 }
 
 }  // namespace
@@ -662,7 +662,7 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
         a.a = ws.xb; a.a_rows = N; a.K = D;
         a.w = w->router; a.n_rows = E;
         a.y = ws.logits; a.y_ld = E;
-        launch_pf<PW_BF16, PE_F32>(a, dim3(E / PB, mt), st);
+        hipLaunchKernelGGL(pf_gemm_kernel, dim3(E / PB, mt), dim3(256), 0, st, a);
     }
     mark(2);
     if (E <= 512)
@@ -677,22 +677,25 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
     hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(1024), 0, st, ws.cursor, E, ws.exp_off, ws.tiles, ws.n_tiles);
     hipLaunchKernelGGL(pf_scatter_kernel, dim3((unsigned) ((n_ent + 255) / 256)), dim3(256), 0, st, ws.ids, ws.rank,
                        ws.wg_base, ws.exp_off, n_ent, K, E, ws.ent_idx, ws.ent_pos);
-    // shared expert gate|up + SwiGLU, then down -> comb = sigmoid(sg) * shared
+    // shared expert gate|up + SwiGLU, then down -> comb = sigmoid(sg) * shared (dense Q8_0 tiles)
     mark(4);
     {
-        PfGemmArgs a{};
-        a.a = ws.xb; a.a_rows = N; a.K = D;
-        a.w = w->sh_gate_q; a.ws = w->sh_gate_s; a.w2 = w->sh_up_q; a.ws2 = w->sh_up_s; a.n_rows = F;
-        a.act = ws.sh_act; a.act_ld = F;
-        launch_pf<PW_Q8, PE_SWIGLU>(a, dim3(F / 32, mt), st);
+        PfExpArgs a{};
+        a.experts = w->experts; a.K = D; a.F = F; a.gx = F / 128;
+        a.a_rows = N; a.dense_mt = MT / 2; a.a = ws.xb;     // 128-row blocks: F/128 x N/128 workgroups
+        a.w = (const int8_t*) w->sh_gate_q; a.ws = (const uint16_t*) w->sh_gate_s;
+        a.w2 = (const int8_t*) w->sh_up_q; a.ws2 = (const uint16_t*) w->sh_up_s;
+        a.act = ws.sh_act; a.ld_out = F;
+        launch_dense_q8<false>(a, st);
     }
     mark(5);
     {
-        PfGemmArgs b{};
-        b.a = ws.sh_act; b.a_rows = N; b.K = F;
-        b.w = w->sh_down_q; b.ws = w->sh_down_s; b.n_rows = D;
-        b.y = comb; b.y_ld = D; b.sg = ws.sg;
-        launch_pf<PW_Q8, PE_SHARED>(b, dim3(D / PB, mt), st);
+        PfExpArgs b{};
+        b.experts = w->experts; b.K = F; b.gx = D / EROWS;
+        b.a_rows = N; b.dense_mt = MT; b.a = ws.sh_act;
+        b.w = (const int8_t*) w->sh_down_q; b.ws = (const uint16_t*) w->sh_down_s;
+        b.y = comb; b.ld_out = D; b.sg = ws.sg;
+        launch_dense_q8<true>(b, st);
     }
     // routed experts: gate|up + SwiGLU per tile, down per tile, then the per-token weighted sum
     mark(6);
