@@ -98,36 +98,37 @@ __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     const int nk = a.K / PB;
 
-    uint4 xa[2], xw[2];
-    auto load = [&](int ks) {
-        const uint4* p = (const uint4*) (ap + (size_t) ks * PB);
-        xa[0] = a_ok ? p[0] : make_uint4(0, 0, 0, 0);
-        xa[1] = a_ok ? p[1] : make_uint4(0, 0, 0, 0);
-        const uint4* q = (const uint4*) (wp + (size_t) ks * PB);
-        xw[0] = q[0];
-        xw[1] = q[1];
-    };
-    auto store = [&](int buf) {
-        *(uint4*) &sA[buf][sr][sk] = xa[0];
-        *(uint4*) &sA[buf][sr][sk + 8] = xa[1];
-        *(uint4*) &sB[buf][sr][sk] = xw[0];
-        *(uint4*) &sB[buf][sr][sk + 8] = xw[1];
-    };
-
-    load(0);
-    store(0);
+    // staging registers (scalars: an array captured by a lambda would live in scratch memory)
+    uint4 xa0 = a_ok ? *(const uint4*) ap : make_uint4(0, 0, 0, 0);
+    uint4 xa1 = a_ok ? *(const uint4*) (ap + 8) : make_uint4(0, 0, 0, 0);
+    uint4 xw0 = *(const uint4*) wp, xw1 = *(const uint4*) (wp + 8);
+    *(uint4*) &sA[0][sr][sk] = xa0;
+    *(uint4*) &sA[0][sr][sk + 8] = xa1;
+    *(uint4*) &sB[0][sr][sk] = xw0;
+    *(uint4*) &sB[0][sr][sk + 8] = xw1;
     __syncthreads();
     for (int ks = 0; ks < nk; ++ks) {
         const int buf = ks & 1;
         const bool more = ks + 1 < nk;
-        if (more) load(ks + 1);                                  // next step's loads first
+        if (more) {                                              // next step's loads first
+            const size_t o = (size_t) (ks + 1) * PB;
+            xa0 = a_ok ? *(const uint4*) (ap + o) : make_uint4(0, 0, 0, 0);
+            xa1 = a_ok ? *(const uint4*) (ap + o + 8) : make_uint4(0, 0, 0, 0);
+            xw0 = *(const uint4*) (wp + o);
+            xw1 = *(const uint4*) (wp + o + 8);
+        }
 #pragma unroll
         for (int kk = 0; kk < PB / 16; ++kk) {
             const bf16x8_t av = *(const bf16x8_t*) &sA[buf][wm * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
             const bf16x8_t bv = *(const bf16x8_t*) &sB[buf][wn * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
         }
-        if (more) store(buf ^ 1);
+        if (more) {
+            *(uint4*) &sA[buf ^ 1][sr][sk] = xa0;
+            *(uint4*) &sA[buf ^ 1][sr][sk + 8] = xa1;
+            *(uint4*) &sB[buf ^ 1][sr][sk] = xw0;
+            *(uint4*) &sB[buf ^ 1][sr][sk + 8] = xw1;
+        }
         __syncthreads();
     }
 
