@@ -359,6 +359,7 @@ def bf16_round64(a):
     (256, 128, 64, 8, 600),
     (256, 128, 64, 8, 1100),       # ~137 entries per expert: most experts span two 128-entry tiles
     (512, 256, 128, 6, 77),
+    (256, 128, 64, 12, 300),       # K = 12: a full 8-slot combine pass, then a predicated one
     (256, 128, 1024, 8, 192),      # 1024 experts: the 16-key routing variant, most experts with 1-3 entries
 ])
 def test_moe_prefill_parity(wz, orc, gpu, D, F, E, K, N):

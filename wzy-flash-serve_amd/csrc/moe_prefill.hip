@@ -536,9 +536,9 @@ __global__ void __launch_bounds__(256) pf_scatter_kernel(const int* __restrict__
     ent_pos[i] = pos;
 }
 
-// comb[t] += sum_k w_k * y[pos(t, k)] in slot order (comb holds the gated shared expert); the K
-// row loads of a thread are issued together (KU slots per pass)
-template <int KU>
+// comb[t] += sum_k w_k * y[pos(t, k)] in slot order (comb holds the gated shared expert). A pass issues the
+// row loads of KU slots together; EXACT means K is a multiple of KU, so no slot load is predicated.
+template <int KU, bool EXACT>
 __global__ void __launch_bounds__(256) pf_combine_kernel(const float* __restrict__ y, const int* __restrict__ ent_pos,
                                                          const float* __restrict__ wts, int K, int D,
                                                          float* __restrict__ comb) {
@@ -546,22 +546,30 @@ __global__ void __launch_bounds__(256) pf_combine_kernel(const float* __restrict
     const int d = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d >= D) return;
     float4 acc = *(const float4*) (comb + (size_t) t * D + d);
+    const int* pt = ent_pos + (size_t) t * K;
+    const float* wt = wts + (size_t) t * K;
     for (int k0 = 0; k0 < K; k0 += KU) {
+        const int n = EXACT ? KU : min(KU, K - k0);   // uniform over the workgroup
         float4 v[KU];
         float wk[KU];
 #pragma unroll
         for (int j = 0; j < KU; ++j) {
-            const int k = min(k0 + j, K - 1);
-            const int p = ent_pos[(size_t) t * K + k];
-            wk[j] = k0 + j < K ? wts[(size_t) t * K + k] : 0.f;
-            v[j] = *(const float4*) (y + (size_t) p * D + d);
+            if (EXACT || j < n) {
+                wk[j] = wt[k0 + j];
+                v[j] = *(const float4*) (y + (size_t) pt[k0 + j] * D + d);
+            } else {
+                wk[j] = 0.f;
+                v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
 #pragma unroll
         for (int j = 0; j < KU; ++j) {
-            acc.x = fmaf(wk[j], v[j].x, acc.x);
-            acc.y = fmaf(wk[j], v[j].y, acc.y);
-            acc.z = fmaf(wk[j], v[j].z, acc.z);
-            acc.w = fmaf(wk[j], v[j].w, acc.w);
+            if (EXACT || j < n) {
+                acc.x = fmaf(wk[j], v[j].x, acc.x);
+                acc.y = fmaf(wk[j], v[j].y, acc.y);
+                acc.z = fmaf(wk[j], v[j].z, acc.z);
+                acc.w = fmaf(wk[j], v[j].w, acc.w);
+            }
         }
     }
     *(float4*) (comb + (size_t) t * D + d) = acc;
@@ -718,8 +726,13 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
         b.a = ws.act; b.tok = nullptr; b.topk = K;
         b.y = ws.y; b.ld_out = D;
         launch_expert<true>(b, ws.max_tiles, st);
-        hipLaunchKernelGGL((pf_combine_kernel<8>), dim3((unsigned) ((D / 4 + 255) / 256), (unsigned) N), dim3(256), 0,
-                           st, ws.y, ws.ent_pos, ws.wts, K, D, comb);
+        const dim3 cg((unsigned) ((D / 4 + 255) / 256), (unsigned) N);
+        if (K == 10)
+            hipLaunchKernelGGL((pf_combine_kernel<10, true>), cg, dim3(256), 0, st, ws.y, ws.ent_pos, ws.wts, K, D, comb);
+        else if (K % 8 == 0)
+            hipLaunchKernelGGL((pf_combine_kernel<8, true>), cg, dim3(256), 0, st, ws.y, ws.ent_pos, ws.wts, K, D, comb);
+        else
+            hipLaunchKernelGGL((pf_combine_kernel<8, false>), cg, dim3(256), 0, st, ws.y, ws.ent_pos, ws.wts, K, D, comb);
     }
     mark(8);
 }
