@@ -360,6 +360,7 @@ def bf16_round64(a):
     (256, 128, 64, 8, 1100),       # ~137 entries per expert: most experts span two 128-entry tiles
     (512, 256, 128, 6, 77),
     (256, 128, 64, 12, 300),       # K = 12: a full 8-slot combine pass, then a predicated one
+    (256, 128, 128, 8, 1000),      # 16 router A tiles (XCD-grouped router blocks), the last of 40 rows
     (256, 128, 1024, 8, 192),      # 1024 experts: the 16-key routing variant, most experts with 1-3 entries
 ])
 def test_moe_prefill_parity(wz, orc, gpu, D, F, E, K, N):
@@ -430,6 +431,12 @@ def test_moe_prefill_rejects_bad_shapes(wz, gpu):
     w.n_exp = 64
     with pytest.raises(wzy_amd.WzyError):
         wz.wzy_moe_prefill(C.byref(w), x.ptr, 2, out.ptr, None, None, ws.ptr, 16, None)
+    with pytest.raises(wzy_amd.WzyError):                            # an empty chunk
+        wz.wzy_moe_prefill(C.byref(w), x.ptr, 0, out.ptr, None, None, ws.ptr, nws, None)
+    w.top_k = 33                                                     # above the 32-slot maximum
+    with pytest.raises(wzy_amd.WzyError):
+        wz.wzy_moe_prefill(C.byref(w), x.ptr, 2, out.ptr, None, None, ws.ptr, nws, None)
+    w.top_k = K
 
 
 def test_moe_prefill_tensor_scales(wz, orc, gpu):

@@ -50,6 +50,7 @@ struct PfGemmArgs {
     const uint16_t* w;             // weight rows of length K
     int n_rows;                    // weight rows
     float* y; int y_ld;            // y[row * y_ld + n]
+    int ncb, mt;                   // 64-wide weight-row blocks and 64-row A tiles (grid = ncb * mt)
 };
 
 // Routed-expert GEMM over expert tiles.  Gate|up: A rows = x rows of the entries' tokens, output
@@ -78,15 +79,27 @@ WZY_DEV float bf16_bits_to_f(uint32_t h) { return __builtin_bit_cast(float, h <<
 WZY_DEV uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 
 // Router GEMM tile: 64 rows x 64 weight rows, K stepped by 64 through two LDS buffers, each wave a
-// 32 x 32 block.
+// 32 x 32 block.  Workgroups go to the 8 XCDs in turn (workgroup b on XCD b % 8); when the A tile count
+// is a multiple of 8, XCD x runs the ncb weight blocks of A tiles x, x + 8, ... back to back, so each
+// A tile is fetched into one XCD's L2 once instead of once per weight block.
 __global__ void __launch_bounds__(256) pf_gemm_kernel(PfGemmArgs a) {
     __shared__ __align__(16) uint16_t sA[2][PB][PB_LD];
     __shared__ __align__(16) uint16_t sB[2][PB][PB_LD];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w & 1, wn = w >> 1;
-    const int row0 = blockIdx.y * PB;
+    const int b = blockIdx.x;
+    int rt, cb;
+    if ((a.mt & 7) == 0) {
+        const int s = b >> 3;
+        rt = (s / a.ncb) * 8 + (b & 7);
+        cb = s % a.ncb;
+    } else {
+        rt = b / a.ncb;
+        cb = b % a.ncb;
+    }
+    const int row0 = rt * PB;
     const int cnt = min(PB, a.a_rows - row0);
-    const int n0 = blockIdx.x * PB;
+    const int n0 = cb * PB;
     const int sr = tid >> 2, sk = (tid & 3) * 16;                // staging: row sr, k sk .. sk+15
     const int wrow = min(n0 + sr, a.n_rows - 1);
     const bool a_ok = sr < cnt;
@@ -647,6 +660,8 @@ int pf_check(const wzy_moe_weights* w, int N) {
     WZY_REQUIRE(E >= 1 && E <= PF_MAX_E && E % 64 == 0, "wzy_moe_prefill: n_exp must be a multiple of 64 up to %d",
                 PF_MAX_E);
     WZY_REQUIRE(K >= 1 && K <= MOE_MAX_K && K <= E, "wzy_moe_prefill: top_k must be in [1, %d]", MOE_MAX_K);
+    WZY_REQUIRE((int64_t) (E / PB) * ((N + PB - 1) / PB) * 256 <= INT32_MAX && (int64_t) N * D <= INT32_MAX,
+                "wzy_moe_prefill: n_tok x n_embd exceeds the launch grids");
     return WZY_OK;
 }
 
@@ -671,7 +686,8 @@ void pf_enqueue(const wzy_moe_weights* w, const float* x, int N, float* comb, co
         a.a = ws.xb; a.a_rows = N; a.K = D;
         a.w = w->router; a.n_rows = E;
         a.y = ws.logits; a.y_ld = E;
-        hipLaunchKernelGGL(pf_gemm_kernel, dim3(E / PB, mt), dim3(256), 0, st, a);
+        a.ncb = E / PB; a.mt = mt;
+        hipLaunchKernelGGL(pf_gemm_kernel, dim3((unsigned) (a.ncb * mt)), dim3(256), 0, st, a);
     }
     mark(2);
     if (E <= 512)
