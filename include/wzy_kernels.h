@@ -133,12 +133,14 @@ size_t wzy_moe_prefill_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_
 
 /* MoE block for a prefill chunk of n_tok rows of x [n_tok x n_embd] (fp32), on MFMA:
  * x rounded to bf16 -> router logits (bf16 GEMM) -> softmax top-k per token (the decode rule) ->
- * entries grouped by expert into tiles of up to 128 -> routed gate|up (NVFP4 dequantised to bf16
+ * entries grouped by expert into tiles of up to 256 -> routed gate|up (NVFP4 dequantised to bf16
  * MFMA operands; the fp32 tensor scale applied to the accumulators) + SwiGLU (bf16) -> down, fp32
  * per entry -> comb = sigmoid(sgate.x) * shared(x) + sum_k w_k * expert_k(x), summed per token in
  * slot order (results do not depend on the order entries reach their expert); the shared expert's
  * Q8_0 weights are dequantised to bf16 (rounded).  n_embd a multiple of 256, n_ff a multiple of
- * 128, n_exp a multiple of 64 up to 1024.  ids / wts [n_tok x top_k] may be NULL.
+ * 128, n_exp a multiple of 64 up to 1024, top_k in [1, min(32, n_exp)]; n_tok >= 1 (an empty chunk
+ * is an error), n_tok * top_k <= 2^26 and n_tok * n_embd < 2^31.  ids / wts [n_tok x top_k] may be
+ * NULL.  Shapes outside these limits return an error before anything is launched.
  * Replaces the prefill MoE of run_stage_prefill: pf_moe_count/scan/tile builders,
  * pf_moe_gu_wmma_kernel, pf_moe_down_wmma_kernel, pf_init_shared_comb_kernel and the router /
  * shared-expert dense GEMMs (src/wzy_prefill_tc.cuh:99-443), fp16 replaced by bf16. */

@@ -347,6 +347,23 @@ def prefill_logits(m, x):
     return (X @ R.T).astype(np.float32)
 
 
+def assert_prefill_close(g, o, D, rtol=2e-2, atol=1e-2):
+    """Prefill block outputs against the oracle, rows of D values.  Elementwise |g - o| <= atol +
+    rtol * |o|, except where the two round a SwiGLU activation that sits on a bf16 rounding tie in
+    opposite directions (their fp32 sums differ in order): that moves the token's outputs by one bf16
+    ulp of the activation times its down column, which can exceed the elementwise bound on the
+    token's small outputs.  Such elements must be fewer than 1 in 10^4 and within atol + rtol *
+    max |o| over their token row."""
+    g = np.asarray(g, np.float64).reshape(-1, D)
+    o = np.asarray(o, np.float64).reshape(-1, D)
+    d = np.abs(g - o)
+    out = d > atol + rtol * np.abs(o)
+    n_out = int(out.sum())
+    assert n_out <= d.size // 10000, "%d of %d outside the elementwise tolerance" % (n_out, d.size)
+    row_bound = atol + rtol * np.abs(o).max(axis=1, keepdims=True)
+    assert (d <= row_bound).all(), "max error %.3g above the row bound" % (d - row_bound).max()
+
+
 def bf16_round64(a):
     u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
@@ -357,7 +374,8 @@ def bf16_round64(a):
     (256, 128, 64, 4, 1),          # one token, one partial row tile
     (256, 128, 64, 4, 130),        # ragged: 3 row tiles, the last of 2 rows
     (256, 128, 64, 8, 600),
-    (256, 128, 64, 8, 1100),       # ~137 entries per expert: most experts span two 128-entry tiles
+    (256, 128, 64, 8, 1100),       # ~137 entries per expert: one partly filled 256-entry tile each
+    (256, 128, 64, 8, 2100),       # ~262 entries per expert: about half span two 256-entry tiles
     (512, 256, 128, 6, 77),
     (256, 128, 64, 12, 300),       # K = 12: a full 8-slot combine pass, then a predicated one
     (256, 128, 128, 8, 1000),      # 16 router A tiles (XCD-grouped router blocks), the last of 40 rows
@@ -377,11 +395,13 @@ def test_moe_prefill_parity(wz, orc, gpu, D, F, E, K, N):
     logits = prefill_logits(m, x).ravel()
     exact = check_ids(orc, logits, E, K, N, ids, ids_o)
     assert exact >= N - max(1, N // 50), (exact, N)
+    if N * K > 256 * E:                 # the case meant to split experts over two tiles does so
+        assert np.bincount(ids_o, minlength=E).max() > 256
     rows = np.array([np.array_equal(ids[t * K:(t + 1) * K], ids_o[t * K:(t + 1) * K]) for t in range(N)])
     wr = np.repeat(rows, K)
     np.testing.assert_allclose(wts[wr], wts_o[wr], rtol=1e-4, atol=1e-6)
     cr = np.repeat(rows, D)
-    np.testing.assert_allclose(comb[cr], comb_o[cr], rtol=2e-2, atol=1e-2)
+    assert_prefill_close(comb[cr], comb_o[cr], D)
     err = np.abs(comb[cr] - comb_o[cr]).max() / np.abs(comb_o[cr]).max()
     assert err < 3e-3, err
     # a second call on the same workspace (counts, tiles and lists rebuilt, comb re-initialised):
@@ -461,7 +481,7 @@ def test_moe_prefill_tensor_scales(wz, orc, gpu):
     assert check_ids(orc, logits, E, K, N, ids, ids_o) >= N - 1
     rows = np.array([np.array_equal(ids[t * K:(t + 1) * K], ids_o[t * K:(t + 1) * K]) for t in range(N)])
     cr = np.repeat(rows, D)
-    np.testing.assert_allclose(comb[cr], comb_o[cr], rtol=2e-2, atol=1e-2)
+    assert_prefill_close(comb[cr], comb_o[cr], D)
     err = np.abs(comb[cr] - comb_o[cr]).max() / np.abs(comb_o[cr]).max()
     assert err < 3e-3, err
 
