@@ -66,23 +66,27 @@ WZY_DEV float nvfp4_chunk_fma_h(const uint4 c, float wsa, float wsb, const half2
 }
 
 // Exclusive count of `pred` over threads 0..255 in thread order (4 waves); `total` = full count.
-WZY_DEV int excl_count256(bool pred, int* s_c, int& total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+WZY_DEV int excl_count_wg(bool pred, int* s_c, int& total) {     // s_c: 8 ints; workgroups of <= 8 waves
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (int) (blockDim.x >> 6);
     const unsigned long long m = __ballot(pred);
     const int within = __popcll(m & ((1ull << lane) - 1ull));
     if (lane == 0) s_c[w] = __popcll(m);
     __syncthreads();
-    int before = 0;
+    int before = 0, all = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) before += (i < w) ? s_c[i] : 0;
-    total = s_c[0] + s_c[1] + s_c[2] + s_c[3];
+    for (int i = 0; i < 8; ++i) {
+        const int ci = i < nw ? s_c[i] : 0;
+        before += (i < w) ? ci : 0;
+        all += ci;
+    }
+    total = all;
     __syncthreads();
     return before + within;
 }
 
 // int8 quantisation, reference rule d = amax/127, q = rint(x * 127/amax) clamped to +-127.
 // 32 values -> two 16-value halves with one shared per-32 scale
-constexpr int SH_J = 8;            // shared-expert SwiGLU outputs per gate/up workgroup
+constexpr int SH_J = 16;           // shared-expert SwiGLU outputs per gate/up workgroup (2 per wave)
 
 // moe_down dynamic LDS: the shared activation's per-32 scales, padded to 16 bytes
 __host__ __device__ inline int dn_shs_floats(int T, int nchunk) { return (T * nchunk + 3) / 4 * 4; }
@@ -164,19 +168,20 @@ struct RouteLds {
     int gcnt[MAX_ENT];
     int gmem[MAX_ENT][WZY_MAX_W];
     int n_groups;
-    int c[4];
-    uint64_t cand[4][64];          // per-wave candidate keys of route_row
+    int c[8];
+    uint64_t cand[4][64];          // per-wave candidate keys of route_row (waves 0-3 route)
 };
 
 // Logits of one row per wave: RV per lane (lane + 64*i), RV = 8 for E <= 512, 16 for E <= 1024.
-// wave wv prefetches rows wv, wv+4 of the logits (issued before anything uses them)
+// wave wv < 4 prefetches rows wv, wv+4 of the logits (issued before anything uses them); waves 4..7
+// of an eight-wave workgroup route nothing
 template <int T, int RV>
 WZY_DEV void route_prefetch(const float* __restrict__ logits, int E, float (&p)[(T + 3) / 4][RV]) {
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int rr = 0; rr < (T + 3) / 4; ++rr) {
         const int t = wv + 4 * rr;
-        if (t >= T) {                                    // wave-uniform
+        if (wv >= 4 || t >= T) {                         // wave-uniform
 #pragma unroll
             for (int i = 0; i < RV; ++i) p[rr][i] = -INFINITY;
             continue;
@@ -217,7 +222,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 #pragma unroll
     for (int rr = 0; rr < (T + 3) / 4; ++rr) {
         const int t = wv + 4 * rr;
-        if (t >= T) continue;                            // wave-uniform
+        if (wv >= 4 || t >= T) continue;                 // wave-uniform
         int my_id;
         float my_w, wsum;
         route_row<RV>(p[rr], E, K, my_id, my_w, wsum, r.cand[wv]);
@@ -241,7 +246,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
     }
     const bool lead = tid < n_ent && leader == tid;
     int n_groups = 0;
-    const int g_lead = excl_count256(lead, r.c, n_groups);
+    const int g_lead = excl_count_wg(lead, r.c, n_groups);
     if (lead) r.gidx[tid] = g_lead;
     __syncthreads();
     if (tid < n_ent) {
@@ -259,18 +264,20 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// gate/up.  Routed workgroups: one (group, 16-row tile); wave w owns rows j = 16*tile + 4w .. +3
-// of both gate and up, so SwiGLU and the 16-wide requant stay inside the workgroup.
+// gate/up, eight waves per workgroup.  Routed workgroups: one (group, 32-row tile); wave w owns rows
+// j = 32*tile + 4w .. +3 of both gate and up, so SwiGLU and the 16-wide requant (two 16-row blocks)
+// stay inside the workgroup.  With 32-row tiles the launch has few enough workgroups (10 experts x 16
+// + 32 shared at the BASELINE shapes) that each gets a CU of its own.
 // reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
-// Shared workgroups: 8 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32 requant of
-// silu_mul_quant32_multi runs in moe_down, so the 2.2 MB shared stream spreads over F/8 workgroups).
+// Shared workgroups: 16 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32 requant of
+// silu_mul_quant32_multi runs in moe_down, so the 2.2 MB shared stream spreads over F/16 workgroups).
 // reference: launch_gemm_q8p x2 + silu_mul_quant32_multi (src/wzy_stage_v2.cuh:711-713;
 // src/wzy_kernels_v2.cuh:1247-1280).
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
 // scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
 // ---------------------------------------------------------------------------------------------
 template <int T, int RV>
-__global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
+__global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ RouteLds r;
     __shared__ float s_act[WZY_MAX_W][32];
@@ -309,7 +316,8 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
                                                                    __builtin_bit_cast(uint32_t, xp[4 * k + 3]));
             s_xs2[i] = make_float2(da, db);
         };
-        if (((__builtin_amdgcn_readfirstlane(tid) + 192) & 255) < T * nc) {   // wave-uniform: a wave with no item skips
+        const int tid0 = __builtin_amdgcn_readfirstlane(tid);
+        if (tid0 < 256 && ((tid0 + 192) & 255) < T * nc) {   // wave-uniform: a wave with no item skips
             const int i = (tid + 192) & 255;
             const int ic = min(i, T * nc - 1);
             const int t = ic / nc, c = ic - t * nc;
@@ -318,7 +326,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             for (int k = 0; k < 8; ++k) f4[k] = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
             if (i < T * nc) stage16(f4, i);
         }
-        if (T > 1) {
+        if (T > 1 && tid0 < 256) {
             for (int i = ((tid + 192) & 255) + 256; i < T * nc; i += 256) {
                 const int t = i / nc, c = i - t * nc;
                 float4 f4[8];
@@ -328,13 +336,13 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             }
         }
         route_compute<T, RV>(p, a.E, K, r);
-        const int tiles = F / 16;
+        const int tiles = F / 32;
         const int g = bid / tiles, jt = bid - g * tiles;
         if (g >= r.n_groups) return;                     // workgroup-uniform (workgroup 0 has g = 0)
         const int e = __builtin_amdgcn_readfirstlane(r.gexp[g]), cnt = r.gcnt[g];
         const MoeOffsets o = moe_offsets(D, F);
         const uint8_t* rec = a.experts + (size_t) e * o.rec;
-        const int j0 = jt * 16 + 4 * w;
+        const int j0 = jt * 32 + 4 * w;
         float acc[8][T];
 #pragma unroll
         for (int rr = 0; rr < 8; ++rr)
@@ -402,22 +410,23 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
             }
         }
         __syncthreads();
-        if (tid < cnt * 16) {
-            const int m = tid >> 4, jj = tid & 15;
+        if (tid < cnt * 32) {                            // one 16-lane row per (member, 16-row block)
+            const int m = tid >> 5, jj = tid & 31, jl = jj & 15;
+            const int blk = 2 * jt + (jj >> 4);          // 16-row block of the F rows
             const float v = s_act[m][jj];
             const float amax = max16(fabsf(v));
             const float d = amax / 127.0f;
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
             const int f = r.gmem[g][m];
-            a.ah16[((size_t) f * (F / 16) + jt) * 16 + (jj & 7) * 2 + (jj >> 3)] =
+            a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
                 __builtin_bit_cast(uint16_t, (_Float16) (float) q);
-            if (jj == 0) a.as16[(size_t) f * (F / 16) + jt] = d;
+            if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
         }
         return;
     }
 
-    // shared expert: rows j in [8*sb, 8*sb + 8), wave w owns j = 8*sb + 2w, +1 (gate and up rows);
+    // shared expert: rows j in [16*sb, 16*sb + 16), wave w owns j = 16*sb + 2w, +1 (gate and up rows);
     // one 32-block of x per lane.  The SwiGLU values go out as fp32; moe_down quantises them per 32.
     const int sb = bid - a.n_routed_wg;
     int4 c0[4], c1[4];
@@ -435,7 +444,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(MoeGuArgs a) {
         sraw[rr] = s[(size_t) row * nc + bl];
     }
     // stage x quantised per 32
-    for (int i = tid; i < T * nc; i += 256) {
+    for (int i = tid; i < T * nc; i += (int) blockDim.x) {
         const int t = i / nc, c = i - t * nc;
         float v[32];
 #pragma unroll
@@ -768,7 +777,7 @@ static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float*
     a.grp_mem = ws.grp_mem; a.ah16 = ws.ah16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shact = ws.shact;
-    a.n_routed_wg = (w->n_ff / 16) * T * w->top_k;
+    a.n_routed_wg = (w->n_ff / 32) * T * w->top_k;
     return a;
 }
 static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb) {
@@ -784,9 +793,9 @@ template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
     if (a.E <= 512)
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / SH_J), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / SH_J), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
 }
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
