@@ -92,6 +92,18 @@ def cpu_threads():
     return max(2, min(15, n, 16))
 
 
+def cpu_model():
+    """Host CPU model name (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(wz, seconds):
     """Time the restated reference CPU MoE pool on config 1 (seed 0) for about `seconds`."""
     import numpy as np
@@ -151,6 +163,7 @@ def cpu_baseline(wz, seconds):
         "value": round(ROUTED_BYTES / med / 1e9, 2),
         "unit": "GB/s (NVFP4 MoE, routed experts, 1 token-layer)",
         "cores": n,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "us_per_token_layer": round(med * 1e6, 1),
         "sample": "config 1 (seed 0, 1 token, top-10 of 512, D=2048 F=512), %d x 10 calls over %.0f s, median" % (

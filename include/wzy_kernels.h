@@ -3,7 +3,9 @@
  * Every entry point enqueues hand-written HIP kernels on `stream` (a hipStream_t passed as void*,
  * NULL = the null stream) and returns a status code: WZY_OK (0) or a negative WZY_E* value, with a
  * message available from wzy_last_error().  All data pointers are DEVICE pointers unless stated
- * otherwise; no call allocates device memory, synchronizes, or takes ownership.
+ * otherwise; no call synchronizes or takes ownership, and none allocates device memory except
+ * wzy_row_argmax / wzy_row_top16 (a per-device scratch, allocated on first use) and the measurement
+ * call wzy_moe_time_kernels.
  *
  * Each function names the reference interface it replaces (reference = liaoyangr8-ai/wzy-flash-serve,
  * paths relative to its root).  The reference exposes these as `launch_*` helpers or bare
@@ -227,8 +229,11 @@ typedef struct wzy_qsa_dims {
     int qh, kvh, hd, n_rot;                      /* 24, 2, 256, 64 */
     int idx_heads, idx_dim, idx_blk, idx_topk;   /* 4, 128, 4, 2048 */
     int ctx_max;                                 /* KV store / indexer capacity in cells */
-    int kv_ring, kv_sinks;                       /* 0, 0 = full-context store addressed by position;
-                                                    else ring of kv_ring slots with kv_sinks pinned */
+    int kv_ring, kv_sinks;                       /* 0, 0 = full-context store addressed by position.
+                                                    A ring (kv_ring slots, kv_sinks pinned) is accepted
+                                                    only when it never wraps, ctx_max <= kv_ring; else
+                                                    every entry point returns WZY_EINVAL (a wrapped slot
+                                                    would serve a newer cell's K/V) */
     float eps;
 } wzy_qsa_dims;
 
@@ -272,11 +277,15 @@ int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const float* qg, co
  * ------------------------------------------------------------------------------------------- */
 
 /* Greedy argmax per row over `nvocab` logits (ties -> lowest index).
+ * Scratch: a per-device buffer of row counters and partial results, hipMalloc-ed (and zeroed) on the
+ * first call on a device and re-allocated when a call needs more; shared by wzy_row_argmax and
+ * wzy_row_top16, so calls on one device must not overlap in time.
  * Replaces row_argmax_multi_kernel (src/wzy_kernels_v2.cuh:1873-1905). */
 int wzy_row_argmax(const float* logits, int nvocab, int T, int* out_ids, void* stream);
 
 /* Top-16 (value desc, ties -> lower index) per row plus greedy id (= rank 0).  Any output may be
- * NULL.  Replaces row_top16_multi_kernel (src/wzy_kernels_v2.cuh:1909-1984). */
+ * NULL.  Same per-device scratch as wzy_row_argmax.
+ * Replaces row_top16_multi_kernel (src/wzy_kernels_v2.cuh:1909-1984). */
 int wzy_row_top16(const float* logits, int nvocab, int T, int* out_greedy, float* top_v,
                   int* top_i, void* stream);
 

@@ -40,7 +40,8 @@ typedef struct wzy_stage_cfg {
     int n_exp, top_k, n_ff;                    /* 512, 10, 512 */
     int n_vocab;                               /* 151936 */
     int ctx_max;                               /* KV / indexer / RoPE capacity in cells */
-    int kv_ring, kv_sinks;                     /* 0, 0: full-context KV store */
+    int kv_ring, kv_sinks;                     /* 0, 0: full-context KV store (a ring is rejected
+                                                  unless ctx_max <= kv_ring, i.e. it never wraps) */
     float rope_theta, eps;                     /* 1e7, 1e-6 */
 } wzy_stage_cfg;
 

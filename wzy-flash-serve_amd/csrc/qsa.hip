@@ -247,6 +247,19 @@ int qsa_check_dims(const QsaDims& dm) {
     WZY_REQUIRE(dm.idim <= 128 && dm.idim % 8 == 0 && dm.ih <= 4 && dm.iblk >= 2, "qsa: indexer layout unsupported");
     WZY_REQUIRE(dm.n_rot % 2 == 0 && dm.n_rot <= dm.idim && dm.n_rot <= dm.hd, "qsa: bad n_rot");
     WZY_REQUIRE(dm.topk >= 1 && dm.ctx_max >= 1, "qsa: bad topk/ctx");
+    return qsa_check_ring(dm.ctx_max, dm.ring_cap, dm.sinks);
+}
+
+int qsa_check_ring(int ctx_max, int ring_cap, int sinks) {
+    if (ring_cap == 0) {
+        WZY_REQUIRE(sinks == 0, "qsa: kv_sinks %d given without a KV ring", sinks);
+        return WZY_OK;
+    }
+    WZY_REQUIRE(ring_cap > 0 && sinks >= 0 && sinks < ring_cap, "qsa: bad KV ring (kv_ring %d, kv_sinks %d)",
+                ring_cap, sinks);
+    WZY_REQUIRE(ctx_max <= ring_cap,
+                "qsa: a KV ring of %d cells cannot hold ctx_max %d; cells past the ring would read newer cells "
+                "(use kv_ring 0: the full-context store)", ring_cap, ctx_max);
     return WZY_OK;
 }
 

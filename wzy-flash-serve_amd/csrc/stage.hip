@@ -215,7 +215,7 @@ static int validate(const wzy_stage_cfg& c) {
     WZY_REQUIRE(c.n_vocab >= 16 && c.ctx_max >= 8, "stage: bad vocab / context");
     WZY_REQUIRE(2 * c.qsa_qh * c.qsa_hd <= 16384 && c.n_embd * 1 <= 8192, "stage: projection too wide");
     WZY_REQUIRE((c.n_vocab + 2047) / 2048 * 16 <= 2048, "stage: n_vocab too large for the top-16 merge");
-    return WZY_OK;
+    return qsa_check_ring(c.ctx_max, c.kv_ring, c.kv_sinks);
 }
 
 int wzy_stage::init_buffers() {
@@ -601,13 +601,9 @@ static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
             // prefilled context: INT8 KV cells 0..n_ctx-1, indexer keys of complete blocks,
             // placeholder key, partial-block tail
             if (n_ctx > 0) {
-                const int slots = c.kv_ring > 0 ? std::min(n_ctx, c.kv_ring) : n_ctx;
-                if (c.kv_ring > 0 && n_ctx > c.kv_ring) {
-                    set_error("load_synthetic: a prefilled context larger than the KV ring is not supported");
-                    return WZY_EINVAL;
-                }
-                WZY_TRY(wzy_synth_kv_device(seed, l, 0, 0, slots, s->KVD, w.kv.kq, w.kv.ks, s->stream));
-                WZY_TRY(wzy_synth_kv_device(seed, l, 1, 0, slots, s->KVD, w.kv.vq, w.kv.vs, s->stream));
+                // a stage's KV ring never wraps (validate), so cell p is slot p
+                WZY_TRY(wzy_synth_kv_device(seed, l, 0, 0, n_ctx, s->KVD, w.kv.kq, w.kv.ks, s->stream));
+                WZY_TRY(wzy_synth_kv_device(seed, l, 1, 0, n_ctx, s->KVD, w.kv.vq, w.kv.vs, s->stream));
             }
             const int nblk = n_ctx / c.idx_blk;
             std::vector<float> keys((size_t) (nblk + 1) * c.idx_dim);

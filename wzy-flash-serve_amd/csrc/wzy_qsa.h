@@ -26,6 +26,12 @@ __device__ __forceinline__ size_t qsa_kv_slot(int p, const QsaDims& dm) {
 
 int qsa_check_dims(const QsaDims& dm);
 
+// A KV ring is accepted only when it never wraps (ctx_max <= ring_cap, so every position keeps its
+// own slot and qsa_kv_slot(p) == p).  A wrapping ring would hand a selected cell older than the ring
+// the K/V of a newer cell: the reference reads such cells from its pinned host mirror
+// (src/wzy_qsa_256k.cuh:17-29), which this build replaces with a full-context store in HBM.
+int qsa_check_ring(int ctx_max, int ring_cap, int sinks);
+
 // KV store of one QSA layer: cells addressed by qsa_kv_slot(p)
 struct QsaKv {
     int8_t* kq; uint16_t* ks;          // [slots][KVD], [slots][KVD/64] fp16 bits
