@@ -289,6 +289,17 @@ int wzy_row_argmax(const float* logits, int nvocab, int T, int* out_ids, void* s
 int wzy_row_top16(const float* logits, int nvocab, int T, int* out_greedy, float* top_v,
                   int* top_i, void* stream);
 
+/* wzy_row_top16 without any allocation: the same kernels and results, with the scratch (row
+ * counters and partial results) in a fixed 131,328-byte device array in the library instead of a
+ * hipMalloc-ed buffer, so it can run where hipMalloc cannot (under HIP graph capture, in tight
+ * serving loops, in harnesses that forbid allocation).  Limits: 1 <= T <= 8, 1 <= nvocab <= 262,144;
+ * larger calls return WZY_EINVAL before anything is launched.  Every call on a device shares that
+ * device's array, so calls that overlap in time on one device race.  The first call on a device also
+ * enqueues one small kernel that clears the counters.
+ * No counterpart in the reference: it exists for callers that cannot allocate. */
+int wzy_row_top16_noalloc(const float* logits, int nvocab, int T, int* out_greedy, float* top_v,
+                          int* top_i, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

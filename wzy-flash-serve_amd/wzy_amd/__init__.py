@@ -153,6 +153,7 @@ _SIGS = {
                                    C.POINTER(F32), P], True),
     "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
     "wzy_row_top16": (I32, [P, I32, I32, P, P, P, P], True),
+    "wzy_row_top16_noalloc": (I32, [P, I32, I32, P, P, P, P], True),
     # synth
     "wzy_synth_hash": (U64, [U64, U64, U64], False),
     "wzy_synth_stream": (U64, [U32, U32, U32], False),
