@@ -272,6 +272,36 @@ int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const float* qg, co
                    const int8_t* vq, const uint16_t* vs, const int* sel_ids, float* out, void* workspace,
                    size_t workspace_bytes, int T, void* stream);
 
+/* Measurement (no reference counterpart): `steps` decode steps of `n_layers`
+ * independent GDN layers, step-major (every layer's step s before any layer's step s+1), T rows per
+ * launch, through the wzy_gdn_recurrence kernels, in one burst on `stream` between two HIP events.
+ * The layers share one set of inputs q, k [steps x hk*128], v [steps x hv*128], decay / beta
+ * [steps x hv] (the duration does not depend on the values); states [n_layers][hv][128][128] are
+ * updated; y [steps x hv*128].  us_per_layer_step = burst time / (n_layers * steps), including the
+ * output-norm kernel; us_kernel_only (nullable) = the same without it.  Allocates a small scratch. */
+int wzy_gdn_time_recurrence(const float* q, const float* k, const float* v, const float* decay, const float* beta,
+                            float* states, float* y, int hk, int hv, int n_layers, int steps, int T,
+                            float* us_per_layer_step, float* us_kernel_only, void* stream);
+
+/* One QSA layer's decode state and activations for wzy_qsa_time_decode (device pointers; the same
+ * meaning as the arguments of wzy_qsa_prepare / wzy_qsa_select / wzy_qsa_attend, T = 1). */
+typedef struct wzy_qsa_layer {
+    float* qg; float* kk; const float* vv; float* q_idx; const float* idx_raw;
+    const float* q_norm; const float* k_norm; const float* iq_norm; const float* ik_norm;
+    const float* cos_tab; const float* sin_tab;
+    int8_t* kq; uint16_t* ks; int8_t* vq; uint16_t* vs;
+    float* idx_tail; float* idx_dead; uint16_t* idx_pooled;
+    float* scores; int max_b; int* sel_ids; int* sel_cnt;
+    float* out; void* workspace; size_t workspace_bytes;
+} wzy_qsa_layer;
+
+/* Measurement (no reference counterpart): one decode token of one QSA layer at
+ * position *pos, stage by stage, each stage `iters` times back to back between two HIP events:
+ * us_stages[4] = mean microseconds of prepare (norms, RoPE, KV + indexer append), block scores,
+ * exact top-idx_topk, sparse attention (with its chunk merge). */
+int wzy_qsa_time_decode(const wzy_qsa_dims* dims, const wzy_qsa_layer* layer, const int* pos, int iters,
+                        float* us_stages, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Logit reductions
  * ------------------------------------------------------------------------------------------- */

@@ -90,6 +90,21 @@ int wzy_stage_top16(wzy_stage* st, float* v, int* ids, int T);
 int wzy_stage_logits(wzy_stage* st, float* out, int T);          /* [T x n_vocab] */
 int wzy_stage_pre_head(wzy_stage* st, float* out, int T);        /* [T x hc x n_embd] residual before the head */
 
+/* Per-layer trace of the following forwards (debugging and layer-by-layer parity checks; forwards
+ * run as direct launches while it is on).  Each forward then leaves, readable with
+ * wzy_stage_read_tensor(st, -1, name): "trace.mixed_a" / "trace.block" / "trace.mixed_f" /
+ * "trace.comb" fp32 [n_layers][8][n_embd] (attention HC read output, attention block output, FFN
+ * HC read output, MoE output), "trace.R_a" / "trace.R_f" fp32 [n_layers][8][hc][n_embd] (the
+ * residual streams after the attention / FFN HC read, i.e. with the pending write folded in),
+ * "trace.inj_a" / "trace.inj_f" fp32 [n_layers][8][hc] (the inject vectors), "trace.moe_logits"
+ * fp32 [n_layers][8][n_exp], "trace.moe_ids" int32
+ * / "trace.moe_wts" fp32 [n_layers][8][top_k], and per QSA layer (in layer order) "trace.scores"
+ * fp32 [n_qsa][8][ctx_max/idx_blk + 2], "trace.sel_ids" int32 [n_qsa][8][idx_topk], "trace.sel_cnt"
+ * int32 [n_qsa][8]; rows 0..T-1 of each [8] block are valid.  The first enable allocates the
+ * buffers.  Counterpart of the reference's per-layer route probe (WZY_DBG_TOPS, dbg_probe_layer,
+ * src/wzy_stage_v2.cuh:754-760; src/wzy_kernels_v2.cuh:1986-1991). */
+int wzy_stage_set_trace(wzy_stage* st, int enable);
+
 /* Use hipGraphs for record_forward (default on): one graph per window shape, replayed. */
 int wzy_stage_set_graphs(wzy_stage* st, int enable);
 /* The stage's HIP stream (hipStream_t). */
@@ -105,6 +120,9 @@ void* wzy_stage_stream(wzy_stage* st);
 size_t wzy_stage_tensor_bytes(wzy_stage* st, int layer, const char* name);
 int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name, void* host, size_t bytes);
 int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes);
+/* Bytes [offset, offset + bytes) of a tensor, device to host (synchronous). */
+int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset, void* host,
+                                size_t bytes);
 
 /* Measurement support (no reference counterpart): time the NVFP4 expert kernels of every layer's
  * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the

@@ -74,6 +74,17 @@ int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float
 
 int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                           float* pre_head, float* dbg, float* margins) {
+    orc_trace tr;
+    memset(&tr, 0, sizeof tr);
+    tr.dbg = dbg;
+    tr.margins = margins;
+    return orc_model_forward_trace(m, pos, toks, T, logits, greedy, pre_head, &tr);
+}
+
+int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                            float* pre_head, const orc_trace* tr) {
+    float* dbg = tr ? tr->dbg : NULL;
+    float* margins = tr ? tr->margins : NULL;
     const int D = m->n_embd, HC = m->hc, HCD = HC * D, L = m->hc_lr;
     const int QKV = 2 * m->gdn_hk * 128 + m->gdn_hv * 128, GV = m->gdn_hv * 128;
     const int QD = m->qsa_qh * m->qsa_hd, KVD = m->qsa_kvh * m->qsa_hd, hd = m->qsa_hd;
@@ -106,7 +117,8 @@ int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, f
     int* sel = (int*) malloc(sizeof(int) * (size_t) m->idx_topk);
     int8_t* kq = (int8_t*) malloc((size_t) KVD);
     uint16_t* ks = (uint16_t*) malloc(sizeof(uint16_t) * (size_t) KVD / 64);
-    int rc = 0, cur = 0;
+    int rc = 0, cur = 0, qsa_i = 0;
+    const int max_b = m->ctx_max / m->idx_blk + 2;
     const float* pend_bo = NULL;
     const float* pend_inj = NULL;
 
@@ -165,10 +177,23 @@ int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, f
                                      scores);
                 const int n = orc_topk_select(scores, n_kv, m->idx_blk, m->idx_topk, sel);
                 if (margins) margins[((size_t) l * T + t) * 2 + 1] = select_margin(scores, n_kv, m->idx_blk, m->idx_topk);
+                if (tr && tr->scores) {
+                    float* dst = tr->scores + ((size_t) qsa_i * T + t) * max_b;
+                    memset(dst, 0, sizeof(float) * (size_t) max_b);
+                    if (n_kv > m->idx_topk)
+                        memcpy(dst, scores, sizeof(float) * (size_t) (n_kv / m->idx_blk + 1));
+                }
+                if (tr && tr->sel) {
+                    int* dst = tr->sel + ((size_t) qsa_i * T + t) * m->idx_topk;
+                    memset(dst, 0, sizeof(int) * (size_t) m->idx_topk);
+                    memcpy(dst, sel, sizeof(int) * (size_t) n);
+                }
+                if (tr && tr->n_sel) tr->n_sel[(size_t) qsa_i * T + t] = n;
                 orc_attend(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh, hd,
                            att + (size_t) t * QD);
             }
             q8_gemv_f(w->wo_q, w->wo_s, att, block, D, QD, T);
+            ++qsa_i;
         }
         /* FFN half */
         if (dl) memcpy(dl + (size_t) T * D, block, sizeof(float) * (size_t) T * D);
@@ -190,6 +215,10 @@ int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, f
                 margins[((size_t) l * T + t) * 2 + 0] = kth_gap(rl + (size_t) t * m->n_exp, m->n_exp, m->top_k);
                 if (!w->qsa) margins[((size_t) l * T + t) * 2 + 1] = 1e30f;
             }
+        if (tr && tr->router_logits)
+            memcpy(tr->router_logits + (size_t) l * T * m->n_exp, rl, sizeof(float) * (size_t) T * m->n_exp);
+        if (tr && tr->ids) memcpy(tr->ids + (size_t) l * T * m->top_k, ids, sizeof(int) * (size_t) T * m->top_k);
+        if (tr && tr->wts) memcpy(tr->wts + (size_t) l * T * m->top_k, wts, sizeof(float) * (size_t) T * m->top_k);
         free(rl);
         if (dl) memcpy(dl + (size_t) 3 * T * D, comb, sizeof(float) * (size_t) T * D);
         pend_bo = comb;

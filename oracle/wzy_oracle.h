@@ -154,6 +154,26 @@ int orc_model_forward(const orc_model* m, int pos, const int* toks, int T, float
 int orc_model_forward_dbg(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                           float* pre_head, float* dbg, float* margins);
 
+/* Per-layer record of one window (every pointer optional):
+ *   dbg [L][4][T][D]: attention HC read output, attention block, FFN HC read output, MoE output;
+ *   margins [L][T][2]: router gap between the top_k-th and next logit, relative indexer score gap
+ *   around the top-k threshold (1e30 when not applicable);
+ *   router_logits [L][T][n_exp], ids / wts [L][T][top_k];
+ *   per QSA layer q (layer order): scores [q][T][ctx_max/idx_blk + 2] (zero when the row selects
+ *   every cell), sel [q][T][idx_topk], n_sel [q][T]. */
+typedef struct orc_trace {
+    float* dbg;
+    float* margins;
+    float* router_logits;
+    int* ids;
+    float* wts;
+    float* scores;
+    int* sel;
+    int* n_sel;
+} orc_trace;
+int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
+                            float* pre_head, const orc_trace* tr);
+
 /* ---- logit reductions (src/wzy_kernels_v2.cuh:1873-1984) ---- */
 void orc_row_argmax(const float* logits, int nvocab, int T, int* out);
 void orc_row_top16(const float* logits, int nvocab, int T, int* greedy, float* top_v, int* top_i);

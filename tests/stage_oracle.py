@@ -41,6 +41,11 @@ class OrcModel(C.Structure):
                 ("blob", BLOB_FN), ("blob_ctx", P)]
 
 
+class OrcTrace(C.Structure):
+    _fields_ = [("dbg", P), ("margins", P), ("router_logits", P), ("ids", P), ("wts", P), ("scores", P), ("sel", P),
+                ("n_sel", P)]
+
+
 def is_qsa(cfg, l):
     return (l % cfg.qsa_period) == cfg.qsa_period - 1
 
@@ -123,8 +128,11 @@ class OracleModel:
         self.orc = oracle_lib.load()
         self.orc.orc_model_forward_dbg.restype = I32
         self.orc.orc_model_forward_dbg.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P, P, P]
+        self.orc.orc_model_forward_trace.restype = I32
+        self.orc.orc_model_forward_trace.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P, C.POINTER(OrcTrace)]
         self.last_layers = None
         self.last_margins = None
+        self.qsa_layers = [l for l in range(cfg.n_layers) if is_qsa(cfg, l)]
 
     def forward(self, pos, toks):
         """logits [T x V], greedy [T], pre-head residual [T x hc x D].  Per-layer activations
@@ -144,6 +152,34 @@ class OracleModel:
         self.last_layers = dbg
         self.last_margins = mg
         return logits, greedy, pre
+
+    def forward_trace(self, pos, toks):
+        """logits [T x V], greedy [T], pre-head [T x hc x D] and the per-layer trace (dict of arrays:
+        hidden [L,4,T,D], router_logits [L,T,E], ids / wts [L,T,K], scores [nq,T,max_b], sel [nq,T,topk],
+        n_sel [nq,T])."""
+        cfg = self.cfg
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        T, L, nq = len(toks), cfg.n_layers, max(1, len(self.qsa_layers))
+        max_b = cfg.ctx_max // cfg.idx_blk + 2
+        logits = np.empty((T, cfg.n_vocab), np.float32)
+        greedy = np.empty(T, np.int32)
+        pre = np.empty((T, cfg.hc, cfg.n_embd), np.float32)
+        tr = {"hidden": np.empty((L, 4, T, cfg.n_embd), np.float32),
+              "margins": np.empty((L, T, 2), np.float32),
+              "router_logits": np.empty((L, T, cfg.n_exp), np.float32),
+              "ids": np.empty((L, T, cfg.top_k), np.int32),
+              "wts": np.empty((L, T, cfg.top_k), np.float32),
+              "scores": np.zeros((nq, T, max_b), np.float32),
+              "sel": np.zeros((nq, T, cfg.idx_topk), np.int32),
+              "n_sel": np.zeros((nq, T), np.int32)}
+        ot = OrcTrace(*[tr[k].ctypes.data for k in ("hidden", "margins", "router_logits", "ids", "wts", "scores", "sel",
+                                                     "n_sel")])
+        rc = self.orc.orc_model_forward_trace(C.byref(self.model), pos, toks.ctypes.data, T, logits.ctypes.data,
+                                              greedy.ctypes.data, pre.ctypes.data, C.byref(ot))
+        assert rc == 0, "orc_model_forward_trace failed"
+        self.last_layers = tr["hidden"]
+        self.last_margins = tr["margins"]
+        return logits, greedy, pre, tr
 
     def decidable_rows(self, router_gap=0.02, select_gap=1e-3):
         """Rows of the last forward whose every routing / selection decision has a margin that the

@@ -1,0 +1,328 @@
+"""Teacher-forced, layer-by-layer parity of one decode row of a GPU stage against the oracle primitives.
+
+Free-running comparisons of a deep model cannot hold every element of every layer to a float
+tolerance: the path requantises activations to int8 (per 16 / 32 values) several times per layer,
+and when two implementations' fp32 sums differ in the last bit, a value sitting on a rounding
+boundary takes different codes on the two sides.  In this synthetic model the MoE block has a large
+gain (its outputs reach |x| ~ 130), so one flipped code moves the MoE output by ~0.3 and the
+difference then grows layer after layer.  Measured at the BASELINE shapes: a layer whose input
+differs by 5e-7 gave MoE outputs 0.36 apart, while the same layer fed the identical input agreed
+to 3e-5.
+
+This checker therefore recomputes every component of every layer from the GPU's own inputs: the
+stage's per-layer trace (wzy_stage_set_trace) supplies the residual streams, HC read outputs,
+injects, block and MoE outputs, and the stage's state tensors supply the pre-row recurrent state.
+For each layer l of a single-row forward at position pos:
+
+  attention HC read   oracle(R_f[l-1] (embedding rows for l = 0), comb[l-1], inj_f[l-1])  vs  R_a, mixed_a, inj_a
+  attention block     GDN: Q8 qkv / z, bf16 alpha / beta, fused step on the pre-row conv history and
+                      state, out-projection; QSA: projections, norms + RoPE, KV append, indexer
+                      append, block scores, top-2048 (bit-exact on the GPU's scores), attention over
+                      the GPU's selected cells, out-projection                          vs  block
+  state update        GDN conv history and state; QSA KV cell at pos, indexer tail / placeholder /
+                      pooled keys                                                      vs  the stage's post-row state
+  FFN HC read         oracle(R_a[l], block[l], inj_a[l])                               vs  R_f, mixed_f, inj_f
+  MoE                 router top-k (bit-exact unless the oracle's top_k-th gap is within twice the
+                      measured router-logit error) and the block output               vs  ids, wts, comb
+and then the head: oracle(R_f[L-1], comb[L-1], inj_f[L-1]) -> head HC read -> LM head vs the
+stage's pre-head residual, logits and greedy id.
+
+Tolerance: elementwise |gpu - oracle| <= ATOL + RTOL * max(|oracle|, rms(oracle row)) -- the north
+star's rel 2e-2 / abs 1e-2, with the relative term floored at the row's RMS: a component that
+requantises its input (every Q8 / NVFP4 GEMV) can still see a one-step code difference when an
+internal fp32 sum lands on a rounding boundary, which moves its outputs by about 1% of the row's
+scale, not of each element.  The largest plain elementwise excess is reported beside it.  Integer
+state (KV codes, fp16 keys / scales) may differ by one step for the same reason."""
+import ctypes as C
+
+import numpy as np
+
+import oracle_lib
+from oracle_lib import OrcMoeWeights, ptr
+
+RTOL, ATOL = 2e-2, 1e-2
+
+
+def bf16_to_f32(h):
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def row_excess(g, o):
+    """Largest excess over ATOL + RTOL * max(|o|, rms(o)), elementwise, and the plain elementwise one."""
+    g = np.asarray(g, np.float64).ravel()
+    o = np.asarray(o, np.float64).ravel()
+    d = np.abs(g - o)
+    rms = float(np.sqrt((o * o).mean())) if o.size else 0.0
+    floor = (d - (ATOL + RTOL * np.maximum(np.abs(o), rms))).max()
+    plain = (d - (ATOL + RTOL * np.abs(o))).max()
+    return float(floor), float(plain)
+
+
+class TeacherForced:
+    """Holds the weights (from an OracleModel built before any oracle forward) and the stage's
+    pre-row state; check_row() verifies one single-row forward that the stage has just run."""
+
+    def __init__(self, wz, st, cfg, om):
+        self.wz, self.st, self.cfg, self.om = wz, st, cfg, om
+        self.orc = oracle_lib.load()
+        self.A = om.arrays
+        self.qsa_layers = list(om.qsa_layers)
+        self.state = {}
+        for (l, name), a in om.arrays.items():
+            if name in ("conv_hist", "ssm", "idx_tail", "idx_dead", "idx_pooled", "kv_k", "kv_ks", "kv_v", "kv_vs"):
+                self.state[(l, name)] = a.copy()
+        self.worst = {}
+        self.worst_plain = {}
+        self.counts = {"layers": 0, "router_ties": 0, "select_ties": 0, "greedy_ties": 0, "rows": 0, "kv_flips": 0,
+                       "key_ulps": 0}
+        D = cfg.n_embd
+        self.cos = om.arrays[(-1, "rope_cos")]
+        self.sin = om.arrays[(-1, "rope_sin")]
+        self.emb = om.arrays[(-1, "emb")].reshape(cfg.n_vocab, D)
+
+    def sync_from_stage(self):
+        """Take the stage's current recurrent / KV / indexer state as the next row's pre-row state (after
+        windows that check_row does not cover, such as multi-row prefill windows)."""
+        for (l, name), a in self.state.items():
+            self.state[(l, name)] = self.st.read(l, name, a.dtype)
+
+    # -------------------------------------------------------------------------------------------
+    def _cmp(self, what, g, o, tag, plain=False):
+        v, p = row_excess(g, o)
+        if plain:
+            v = p
+        self.worst[what] = max(self.worst.get(what, -np.inf), v)
+        self.worst_plain[what] = max(self.worst_plain.get(what, -np.inf), p)
+        assert v <= 0, "%s: %s beyond tolerance by %.3g (max abs err %.3g)" % (
+            tag, what, v, float(np.abs(np.asarray(g, np.float64) - o).max()))
+
+    def _q8(self, name, l, x, rows):
+        cols = x.size
+        x = np.ascontiguousarray(x, np.float32)
+        xq = np.empty(cols, np.int8)
+        xs = np.empty(cols // 32, np.float32)
+        self.orc.orc_quant_act(ptr(x), cols, 1, ptr(xq), ptr(xs), None, None)
+        y = np.empty(rows, np.float32)
+        self.orc.orc_gemv_q8(ptr(self.A[(l, name + ".q")]), ptr(self.A[(l, name + ".s")]), ptr(xq), ptr(xs), ptr(y),
+                             rows, cols, 1)
+        return y
+
+    def _bf16(self, w, x, rows):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(rows, np.float32)
+        self.orc.orc_gemv_bf16(ptr(w), ptr(x), ptr(y), rows, x.size, 1)
+        return y
+
+    def _hc_read(self, l, h, R_in, emb_rows, bo, inj_prev, with_inj=True):
+        cfg, D = self.cfg, self.cfg.n_embd
+        HC, L = cfg.hc, cfg.hc_lr
+        if l >= 0:
+            norm, dq, ds = self.A[(l, "hc_norm%d" % h)], self.A[(l, "hc_down%d.q" % h)], self.A[(l, "hc_down%d.s" % h)]
+            uq, us, inj_w = self.A[(l, "hc_up%d.q" % h)], self.A[(l, "hc_up%d.s" % h)], self.A[(l, "hc_inj%d" % h)]
+        else:
+            norm, dq, ds = self.A[(-1, "head_norm")], self.A[(-1, "head_down.q")], self.A[(-1, "head_down.s")]
+            uq, us, inj_w = self.A[(-1, "head_up.q")], self.A[(-1, "head_up.s")], None
+        keep = [np.ascontiguousarray(a, np.float32) if a is not None else None for a in (R_in, emb_rows, bo, inj_prev)]
+        R_out = np.empty(HC * D, np.float32)
+        nsc = np.empty(HC, np.float32)
+        lo = np.empty(L, np.float32)
+        inj = np.empty(HC, np.float32)
+        mixed = np.empty(D, np.float32)
+        self.orc.orc_hc_read(ptr(keep[0]), ptr(keep[1]), ptr(keep[2]), ptr(keep[3]), ptr(norm), ptr(dq), ptr(ds),
+                             ptr(inj_w) if (with_inj and inj_w is not None) else None, ptr(uq), ptr(us), D, HC, L,
+                             cfg.eps, 1, ptr(R_out), ptr(nsc), ptr(lo),
+                             ptr(inj) if (with_inj and inj_w is not None) else None, ptr(mixed))
+        return R_out, mixed, inj
+
+    # -------------------------------------------------------------------------------------------
+    def check_row(self, tag, pos, tok, g, g_logits, g_greedy, g_pre):
+        """g: the stage trace of a T = 1 forward at `pos` (layer_parity.gpu_trace plus R_a, R_f, inj_a, inj_f)."""
+        cfg, st, orc = self.cfg, self.st, self.orc
+        D, HC = cfg.n_embd, cfg.hc
+        QKV, GV = 2 * cfg.gdn_hk * 128 + cfg.gdn_hv * 128, cfg.gdn_hv * 128
+        QD, KVD, hd = cfg.qsa_qh * cfg.qsa_hd, cfg.qsa_kvh * cfg.qsa_hd, cfg.qsa_hd
+        IH, ID, blk, topk = cfg.idx_heads, cfg.idx_dim, cfg.idx_blk, cfg.idx_topk
+        max_b = cfg.ctx_max // blk + 2
+        n_kv = pos + 1
+        self.counts["rows"] += 1
+        new_state = {}
+        for l in range(cfg.n_layers):
+            t = "%s layer %d" % (tag, l)
+            # ---- attention HC read
+            if l == 0:
+                emb_row = bf16_to_f32(self.emb[tok])
+                R_a, mixa, inj_a = self._hc_read(l, 0, None, emb_row, None, None)
+            else:
+                R_a, mixa, inj_a = self._hc_read(l, 0, g["R_f"][l - 1, 0], None, g["hidden"][l - 1, 3, 0],
+                                                 g["inj_f"][l - 1, 0])
+            self._cmp("attention R", g["R_a"][l, 0], R_a, t)
+            self._cmp("attention HC read", g["hidden"][l, 0, 0], mixa, t)
+            self._cmp("attention inject", g["inj_a"][l, 0], inj_a, t)
+            xa = np.ascontiguousarray(g["hidden"][l, 0, 0])
+            # ---- attention block on the GPU's mixed_a and pre-row state
+            if l not in self.qsa_layers:
+                qkv = self._q8("qkv", l, xa, QKV)
+                z = self._q8("wgate", l, xa, GV)
+                ab = np.concatenate([self._bf16(self.A[(l, "alpha")], xa, cfg.gdn_hv),
+                                     self._bf16(self.A[(l, "beta")], xa, cfg.gdn_hv)]).astype(np.float32)
+                hist = self.state[(l, "conv_hist")].copy()
+                ssm = self.state[(l, "ssm")].copy()
+                y = np.empty(GV, np.float32)
+                orc.orc_gdn_step(ptr(qkv), ptr(z), ptr(ab), ptr(self.A[(l, "dt_bias")]), ptr(self.A[(l, "ssm_a")]),
+                                 ptr(self.A[(l, "conv1d")]), ptr(hist), ptr(ssm), ptr(self.A[(l, "ssm_norm")]), cfg.eps,
+                                 ptr(y), cfg.gdn_hk, cfg.gdn_hv, 1)
+                block = self._q8("wout", l, y, D)
+                g_hist, g_ssm = st.read(l, "conv_hist", np.float32), st.read(l, "ssm", np.float32)
+                self._cmp("GDN conv history", g_hist, hist, t)
+                self._cmp("GDN state", g_ssm, ssm, t)
+                new_state[(l, "conv_hist")], new_state[(l, "ssm")] = g_hist, g_ssm
+            else:
+                qi = self.qsa_layers.index(l)
+                qg = self._q8("wq", l, xa, 2 * QD)
+                kk = self._q8("wk", l, xa, KVD)
+                vv = self._q8("wv", l, xa, KVD)
+                idx_raw = self._bf16(self.A[(l, "idx_k")], xa, ID)
+                q_idx = self._bf16(self.A[(l, "idx_q")], xa, IH * ID)
+                for h in range(cfg.qsa_qh):
+                    orc.orc_head_norm_rope(qg[h * 2 * hd:].ctypes.data, hd, ptr(self.A[(l, "q_norm")]), ptr(self.cos),
+                                           ptr(self.sin), pos, cfg.n_rot, cfg.eps)
+                for j in range(cfg.qsa_kvh):
+                    orc.orc_head_norm_rope(kk[j * hd:].ctypes.data, hd, ptr(self.A[(l, "k_norm")]), ptr(self.cos),
+                                           ptr(self.sin), pos, cfg.n_rot, cfg.eps)
+                for i in range(IH):
+                    orc.orc_head_norm_rope(q_idx[i * ID:].ctypes.data, ID, ptr(self.A[(l, "idx_qn")]), ptr(self.cos),
+                                           ptr(self.sin), pos, cfg.n_rot, cfg.eps)
+                # KV cell at pos: the oracle's quantisation of its k / v vs the stage's bytes
+                ok, oks = np.zeros(KVD, np.int8), np.zeros(KVD // 64, np.uint16)
+                ov, ovs = np.zeros(KVD, np.int8), np.zeros(KVD // 64, np.uint16)
+                orc.orc_kv_quant_row(ptr(kk), KVD, ptr(ok), ptr(oks))
+                orc.orc_kv_quant_row(ptr(vv), KVD, ptr(ov), ptr(ovs))
+                gcell = {n: st.read_range(l, n, dt, pos * w, w) for n, dt, w in
+                         (("kv_k", np.int8, KVD), ("kv_v", np.int8, KVD), ("kv_ks", np.uint16, KVD // 64),
+                          ("kv_vs", np.uint16, KVD // 64))}
+                for n, o in (("kv_k", ok), ("kv_v", ov), ("kv_ks", oks), ("kv_vs", ovs)):
+                    dd = np.abs(gcell[n].astype(np.int32) - o.astype(np.int32))
+                    assert dd.max() <= 1, "%s: KV %s of cell %d differs by %d steps" % (t, n, pos, dd.max())
+                    self.counts["kv_flips"] += int((dd > 0).sum())
+                for n in ("kv_k", "kv_v", "kv_ks", "kv_vs"):
+                    w = gcell[n].size
+                    arr = self.state[(l, n)]
+                    arr[pos * w:(pos + 1) * w] = gcell[n]
+                    new_state[(l, n)] = arr
+                # indexer append on the pre-row indexer state
+                tail, dead = self.state[(l, "idx_tail")].copy(), self.state[(l, "idx_dead")].copy()
+                pooled = self.state[(l, "idx_pooled")].copy()
+                orc.orc_indexer_append(ptr(idx_raw), ptr(self.A[(l, "idx_kn")]), ptr(self.cos), ptr(self.sin), pos, ID,
+                                       blk, cfg.n_rot, cfg.eps, ptr(tail), ptr(dead), ptr(pooled))
+                g_tail, g_dead = st.read(l, "idx_tail", np.float32), st.read(l, "idx_dead", np.float32)
+                g_pooled = st.read(l, "idx_pooled", np.uint16)
+                self._cmp("indexer tail", g_tail, tail, t)
+                self._cmp("indexer placeholder", g_dead, dead, t)
+                dk = np.abs(g_pooled.astype(np.int32) - pooled.astype(np.int32))
+                assert dk.max() <= 1, "%s: pooled indexer keys differ by %d fp16 steps" % (t, dk.max())
+                self.counts["key_ulps"] += int((dk > 0).sum())
+                new_state[(l, "idx_tail")], new_state[(l, "idx_dead")], new_state[(l, "idx_pooled")] = \
+                    g_tail, g_dead, g_pooled
+                # block scores on the stage's post-row keys, then the selection
+                scores = np.zeros(max_b, np.float32)
+                if n_kv > topk:
+                    orc.orc_block_scores(ptr(g_pooled), ptr(g_dead), ptr(q_idx), n_kv, IH, ID, blk, ptr(scores))
+                nb = n_kv // blk + 1
+                gsc = np.ascontiguousarray(g["scores"][qi, 0])
+                if n_kv > topk:
+                    # no requantisation between the fp16 keys and the scores (and the open block's +1e9
+                    # forcing would dominate a row RMS): plain elementwise
+                    self._cmp("block scores", gsc[:nb], scores[:nb], t, plain=True)
+                gsel = np.ascontiguousarray(g["sel"][qi, 0])
+                n = int(g["n_sel"][qi, 0])
+                assert n == min(n_kv, topk), "%s: selection count %d" % (t, n)
+                own = np.zeros(topk, np.int32)
+                assert orc.orc_topk_select(ptr(gsc), n_kv, blk, topk, ptr(own)) == n
+                assert np.array_equal(own[:n], gsel[:n]), "%s: top-k of the stage's own scores differs" % t
+                osel = np.zeros(topk, np.int32)
+                orc.orc_topk_select(ptr(scores), n_kv, blk, topk, ptr(osel))
+                if not np.array_equal(osel[:n], gsel[:n]):
+                    from layer_parity import threshold_gap
+                    gap = threshold_gap(scores, n_kv, blk, topk)
+                    err = float(np.abs(gsc[:nb].astype(np.float64) - scores[:nb]).max())
+                    assert gap <= 2 * err, "%s: selected cells differ, gap %.3g > 2 x score error %.3g" % (t, gap, err)
+                    self.counts["select_ties"] += 1
+                att = np.empty(QD, np.float32)
+                sel = np.ascontiguousarray(gsel[:n])
+                S = self.state
+                orc.orc_attend(ptr(qg), ptr(S[(l, "kv_k")]), ptr(S[(l, "kv_ks")]), ptr(S[(l, "kv_v")]),
+                               ptr(S[(l, "kv_vs")]), ptr(sel), n, cfg.qsa_qh, cfg.qsa_kvh, hd, ptr(att))
+                block = self._q8("wo", l, att, D)
+            self._cmp("attention block", g["hidden"][l, 1, 0], block, t)
+            # ---- FFN HC read on the GPU's attention-half outputs
+            R_f, mixf, inj_f = self._hc_read(l, 1, g["R_a"][l, 0], None, g["hidden"][l, 1, 0], g["inj_a"][l, 0])
+            self._cmp("FFN R", g["R_f"][l, 0], R_f, t)
+            self._cmp("FFN HC read", g["hidden"][l, 2, 0], mixf, t)
+            self._cmp("FFN inject", g["inj_f"][l, 0], inj_f, t)
+            # ---- MoE on the GPU's mixed_f
+            xf = np.ascontiguousarray(g["hidden"][l, 2, 0])
+            comb, ids, wts, logits = self._moe(l, xf)
+            gi = g["ids"][l, 0]
+            if not np.array_equal(gi, ids):
+                gl = g["router_logits"][l, 0].astype(np.float64)
+                err = float(np.abs(gl - logits).max())
+                s = np.sort(logits.astype(np.float64))[::-1]
+                K = cfg.top_k
+                if set(gi.tolist()) == set(ids.tolist()):
+                    for a, b in zip(gi, ids):
+                        assert a == b or abs(logits[a] - logits[b]) <= 2 * err, "%s: expert order" % t
+                    self._cmp("MoE output", g["hidden"][l, 3, 0], comb, t)
+                else:
+                    assert s[K - 1] - s[K] <= 2 * err, "%s: experts %s vs %s, gap %.3g > 2 x logit error %.3g" % (
+                        t, sorted(gi.tolist()), sorted(ids.tolist()), s[K - 1] - s[K], err)
+                    self.counts["router_ties"] += 1
+            else:
+                self._cmp("router weights", g["wts"][l, 0], wts, t)
+                self._cmp("MoE output", g["hidden"][l, 3, 0], comb, t)
+            self.counts["layers"] += 1
+        # ---- head
+        L = cfg.n_layers
+        R_h, mixh, _ = self._hc_read(-1, 0, g["R_f"][L - 1, 0], None, g["hidden"][L - 1, 3, 0], g["inj_f"][L - 1, 0],
+                                     with_inj=False)
+        # pre-head residual = R_f[L-1] with the last MoE write folded in (the head read's R_out)
+        self._cmp("pre-head residual", g_pre.ravel(), R_h, tag)
+        logits = self._bf16(self.A[(-1, "head")], mixh, cfg.n_vocab)
+        self._cmp("logits", g_logits.ravel(), logits, tag)
+        ref = int(np.argmax(logits))
+        gid = int(g_greedy[0])
+        if gid != ref:
+            err = float(np.abs(g_logits.ravel().astype(np.float64) - logits).max())
+            gap = float(logits[ref]) - float(logits[gid])
+            assert gap <= 2 * err, "%s: greedy %d vs %d, gap %.3g > 2 x logit error %.3g" % (tag, gid, ref, gap, err)
+            self.counts["greedy_ties"] += 1
+        # teacher forcing: the next row starts from the stage's own post-row state
+        self.state.update(new_state)
+
+    def _moe(self, l, x):
+        cfg, A = self.cfg, self.A
+        D, F, E, K = cfg.n_embd, cfg.n_ff, cfg.n_exp, cfg.top_k
+        ow = OrcMoeWeights()
+        ow.n_embd, ow.n_ff, ow.n_exp, ow.top_k = D, F, E, K
+        ow.router, ow.sgate = ptr(A[(l, "router")]), ptr(A[(l, "sgate")])
+        ow.blobs = None
+        for n in ("sh_gate", "sh_up", "sh_down"):
+            setattr(ow, n + "_q", ptr(A[(l, n + ".q")]))
+            setattr(ow, n + "_s", ptr(A[(l, n + ".s")]))
+        comb = np.empty(D, np.float32)
+        ids = np.empty(K, np.int32)
+        wts = np.empty(K, np.float32)
+        logits = np.empty(E, np.float32)
+        fn = self.orc.orc_moe_block_fn
+        fn.restype = C.c_int
+        cb = self.om._blob_cb                      # the oracle model's expert-blob callback (kept alive there)
+        fn.argtypes = [C.POINTER(OrcMoeWeights), C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                       C.c_void_p, type(cb), C.c_void_p, C.c_int]
+        assert fn(C.byref(ow), ptr(x), 1, ptr(comb), ptr(ids), ptr(wts), ptr(logits), None, cb, None, l) == 0
+        return comb, ids, wts, logits
+
+    def summary(self):
+        w = ", ".join("%s %.3g (plain %.3g)" % (k, self.worst[k], self.worst_plain[k]) for k in self.worst)
+        return ("teacher-forced: %d rows, %d layer-rows; near ties: router %d, selection %d, greedy %d; KV codes "
+                "one step apart %d, pooled keys one fp16 step apart %d; worst tolerance excess (<= 0 passes): %s" % (
+                    self.counts["rows"], self.counts["layers"], self.counts["router_ties"], self.counts["select_ties"],
+                    self.counts["greedy_ties"], self.counts["kv_flips"], self.counts["key_ulps"], w))

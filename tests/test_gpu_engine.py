@@ -3,8 +3,11 @@ client speak it (serve/server.py:360-380,480-510; serve/engine_client.py), with 
 streams checked two ways:
   - bit-exact against an in-process stage of the same library replaying the engine's schedule
     (prefill windows of up to 8 rows, then one row per step): the engine's loop adds no drift;
-  - against the CPU oracle, teacher-forced on the engine's tokens, for every row whose routing and
-    selection decisions are decidable (the float tolerance of the multi-layer stage tests).
+  - against the CPU oracle on the engine's tokens: every single-row step component by component from
+    the stage's own inputs and pre-row state (teacher_forced.TeacherForced, within the float
+    tolerance), and every window free-running through both sides' per-layer traces
+    (layer_parity.LayerParity: expert ids and selected cells bit-exact, near ties excluded only
+    within twice the measured error).
 """
 import json
 import os
@@ -18,8 +21,9 @@ import numpy as np
 import pytest
 
 import wzy_amd
-from stage_oracle import OracleModel, near_tie, small_cfg
-from test_gpu_stage import check_close
+from layer_parity import LayerParity, gpu_trace
+from stage_oracle import OracleModel, small_cfg
+from teacher_forced import TeacherForced
 
 pytestmark = pytest.mark.gpu
 
@@ -105,36 +109,38 @@ def greedy_req(ids, n, **kw):
 
 
 class Replay:
-    """An in-process stage + the oracle, driven with the engine's schedule for one request."""
+    """An in-process stage + the oracle, driven with the engine's schedule for one request; every
+    window is traced on both sides and compared layer by layer (layer_parity.LayerParity)."""
 
     def __init__(self, wz, cfg):
         self.cfg = cfg
         self.st = wzy_amd.Stage(cfg)
         self.st.load_synthetic(SEED, 0)
+        self.st.lib.wzy_stage_set_trace(self.st.h, 1)
         self.orc = OracleModel(wz, self.st, cfg, SEED)
-        self.checked = self.skipped = 0
-        self.tainted = False
+        self.tf = TeacherForced(wz, self.st, cfg, self.orc)
+        self.par = LayerParity(cfg, self.orc.qsa_layers, hidden="report")
 
     def prefill(self, ids, start):
         for p in range(start, len(ids) - 1, 8):
             w = list(ids[p:min(p + 8, len(ids) - 1)])
             self.st.forward(p, w, run_head=False)
-            self.orc.forward(p, w)
-            self.tainted |= not self.orc.decidable_rows().all()
+            self.st.sync()
+            gt = gpu_trace(self.st, self.cfg, len(w), len(self.orc.qsa_layers))
+            _, _, _, ot = self.orc.forward_trace(p, w)
+            self.par.window("prefill pos %d" % p, p, gt, ot, None, None, None, T=len(w))
+        self.tf.sync_from_stage()
 
     def step(self, tok, pos):
-        """Forward one row with the head: returns the stage's greedy token; checks the oracle."""
+        """Forward one row with the head: returns the stage's greedy token; checks it teacher-forced
+        (every component on the stage's own inputs) and free-running (decisions) against the oracle."""
         self.st.forward(pos, [tok])
         self.st.sync()
         g, gid = self.st.logits(1), self.st.greedy(1)
-        o, og, _ = self.orc.forward(pos, [tok])
-        self.tainted |= not self.orc.decidable_rows()[0]
-        if self.tainted or near_tie(o[0], 0.05):
-            self.skipped += 1
-        else:
-            check_close("engine pos %d" % pos, g[0], o[0])
-            assert gid[0] == og[0], "pos %d: greedy %d vs oracle %d" % (pos, gid[0], og[0])
-            self.checked += 1
+        gt = gpu_trace(self.st, self.cfg, 1, len(self.orc.qsa_layers))
+        self.tf.check_row("engine pos %d" % pos, pos, tok, gt, g, gid, self.st.pre_head(1))
+        o, _, _, ot = self.orc.forward_trace(pos, [tok])
+        self.par.window("engine pos %d" % pos, pos, gt, ot, g, o, gid)
         return int(gid[0])
 
     def close(self):
@@ -201,10 +207,9 @@ def test_engine_greedy_stream_parity_and_prefix_reuse(wz, gpu):
         # no_reuse restarts from an empty state and reproduces the first stream exactly
         _, toks3, done3 = eng.request(greedy_req(prompt, 10, no_reuse=1))
         assert toks3 == toks and done3["reused"] == 0
-        # rows after an undecidable routing/selection decision are skipped (their state may differ
-        # legitimately); the stage tests cover the oracle comparison in depth
-        print("engine greedy: %d rows checked against the oracle, %d skipped" % (rep.checked, rep.skipped),
-              flush=True)
+        print("engine greedy vs oracle, free-running: " + rep.par.summary(), flush=True)
+        print("engine greedy vs oracle: " + rep.tf.summary(), flush=True)
+        assert rep.tf.counts["rows"] == 14 and rep.tf.counts["layers"] == 14 * 4, rep.tf.summary()
     finally:
         rep.close()
         assert eng.close() == 0

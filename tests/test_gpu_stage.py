@@ -1,50 +1,53 @@
-"""GPU parity of the whole decode window (wzy_stage_record_forward) against the CPU oracle model,
-on small instances of the synthetic architecture (MI355X; C ABI only, no torch).
+"""GPU parity of the whole decode window (wzy_stage_record_forward) against the CPU oracle model
+(MI355X; C ABI only, no torch): small instances of the synthetic architecture and the BASELINE shapes
+(D=2048, HC 4x320, GDN 16/16, QSA 24/2/256, indexer 4x128 top-2048, 512 experts top-10, NFF 512,
+vocab 151,936) at a 32,768-cell prefilled context, up to the full 48-layer model.
 
 The oracle model is built from the stage's own tensors after load_synthetic, so both sides start
 from the same weights and prefilled state and then evolve their state independently.
 
 Two implementations of this model cannot agree bit for bit: fp32 sums run in different orders, and
-every activation is requantised to int8 (per 16/32/64 values) several times per layer, so a last-bit
-difference occasionally moves one code by one step.  Within one layer that stays far inside the
-tolerance; across layers the differences compound and can eventually cross a near-tie of a discrete
-decision (router top-k, indexer top-k).  Hence:
-  * single-layer models (one GDN or one QSA layer) are compared strictly, over several steps;
-  * multi-layer models are compared strictly on every row whose routing / selection decisions all
-    have a margin (measured by the oracle) that the drift cannot cross; rows that follow an
-    undecidable row are not compared, because their state already differs.
-Tolerance (north star: floats rel 2e-2 / abs 1e-2 on hidden states and logits), applied to the
-whole vector: max|gpu - oracle| <= 1e-2 + 2e-2 * max|oracle|."""
+every activation is requantised to int8 several times per layer, so a last-bit difference
+occasionally moves one code by one step.  Multi-layer comparisons therefore go layer by layer
+through a per-layer trace of both sides (layer_parity.LayerParity): hidden states within the float
+tolerance elementwise, expert ids and selected cells bit-exact, and the only exclusions are
+decisions whose oracle margin is within twice the error measured at that decision.  Tolerance (north
+star): |gpu - oracle| <= 1e-2 + 2e-2 |oracle| elementwise on hidden states and logits."""
 import ctypes as C
+import time
 
 import numpy as np
 import pytest
 
 import wzy_amd
-from stage_oracle import OracleModel, is_qsa, near_tie, small_cfg
+from layer_parity import ATOL, RTOL, LayerParity, excess, gpu_trace
+from stage_oracle import OracleModel, is_qsa, small_cfg
+from teacher_forced import TeacherForced
 
 pytestmark = pytest.mark.gpu
 
-RTOL, ATOL = 2e-2, 1e-2
 SINGLE = {"gdn": 2, "qsa": 1}      # qsa_period of a one-layer model of that kind
 
 
 def check_close(tag, g, o):
-    g = np.asarray(g, np.float64)
-    o = np.asarray(o, np.float64)
-    err = np.abs(g - o).max()
-    scale = np.abs(o).max()
-    print("%s: max abs err %.3g (max |ref| %.3g)" % (tag, err, scale), flush=True)
-    assert err <= ATOL + RTOL * scale, "%s: error %.3g above %.3g" % (tag, err, ATOL + RTOL * scale)
+    """Elementwise |g - o| <= ATOL + RTOL |o|."""
+    v = excess(g, o)
+    err = float(np.abs(np.asarray(g, np.float64) - np.asarray(o, np.float64)).max())
+    print("%s: max abs err %.3g, tolerance excess %.3g" % (tag, err, v), flush=True)
+    assert v <= 0, "%s: beyond tolerance by %.3g" % (tag, v)
 
 
-def check_greedy(tag, g_ids, o_logits):
+def check_greedy(tag, g_ids, g_logits, o_logits):
+    """Greedy ids equal the oracle's argmax, unless the oracle's gap to the GPU's pick is within twice
+    the logit error measured on that row."""
     for t, gid in enumerate(g_ids):
-        row = o_logits[t]
+        row = np.asarray(o_logits[t], np.float64)
         ref = int(np.argmax(row))
         if gid != ref:
-            assert near_tie(row, 2 * ATOL) and row[gid] >= row[ref] - 2 * ATOL, \
-                "%s row %d: greedy %d vs oracle %d (logits %.5f vs %.5f)" % (tag, t, gid, ref, row[gid], row[ref])
+            err = float(np.abs(np.asarray(g_logits[t], np.float64) - row).max())
+            gap = row[ref] - row[gid]
+            assert gap <= 2 * err, "%s row %d: greedy %d vs oracle %d, gap %.3g > 2 x logit error %.3g" % (
+                tag, t, gid, ref, gap, err)
 
 
 def check_top16(st, g_logits, g_ids, T):
@@ -76,7 +79,7 @@ def test_stage_single_layer_decode(wz, gpu, kind, n_ctx, graphs):
             tag = "step %d pos %d" % (step, pos)
             check_close(tag + " pre-head", st.pre_head(1), o_pre)
             check_close(tag + " logits", g_logits, o_logits)
-            check_greedy(tag, g_ids, o_logits)
+            check_greedy(tag, g_ids, g_logits, o_logits)
             check_top16(st, g_logits, g_ids, 1)
             pos += 1
     finally:
@@ -103,7 +106,7 @@ def test_stage_single_layer_window_commit(wz, gpu, kind):
         o4, _, _ = orc_full.forward(n_ctx, win)
         for t in range(4):
             check_close("window row %d" % t, g4[t], o4[t])
-        check_greedy("window", gid4, o4)
+        check_greedy("window", gid4, g4, o4)
         check_top16(st, g4, gid4, 4)
         # accept rows 0 and 1 (last accepted position n_ctx + 1)
         st.lib.wzy_stage_commit_window_state(st.h, 1, n_ctx + 1)
@@ -113,48 +116,132 @@ def test_stage_single_layer_window_commit(wz, gpu, kind):
             st.forward(pos, [tok])
             st.sync()
             o1, _, _ = orc_acc.forward(pos, [tok])
-            check_close("after commit, pos %d" % pos, st.logits(1), o1)
-            check_greedy("after commit", st.greedy(1), o1)
+            g1 = st.logits(1)
+            check_close("after commit, pos %d" % pos, g1, o1)
+            check_greedy("after commit", st.greedy(1), g1, o1)
+    finally:
+        st.close()
+
+
+def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=False):
+    """Load a stage, trace every window on both sides and compare layer by layer (free-running).  With
+    greedy_feed, each single-row window's token is the GPU's greedy id of the previous row.  With
+    teacher, every single-row window is also checked component by component against the oracle fed
+    the GPU's own inputs and pre-row state (teacher_forced.TeacherForced), and the free-running
+    hidden-state differences are reported rather than asserted.  Returns (free-running, teacher)."""
+    st = wzy_amd.Stage(cfg)
+    try:
+        t0 = time.time()
+        st.load_synthetic(seed, n_ctx)
+        st.lib.wzy_stage_set_trace(st.h, 1)
+        orc = OracleModel(wz, st, cfg, seed)
+        tf = TeacherForced(wz, st, cfg, orc) if teacher else None
+        print("stage + oracle model ready in %.1f s" % (time.time() - t0), flush=True)
+        par = LayerParity(cfg, orc.qsa_layers, hidden="report" if teacher else "elementwise")
+        pos, prev = n_ctx, None
+        for w in windows:
+            if greedy_feed and len(w) == 1 and prev is not None:
+                w = [prev]
+            T = len(w)
+            t0 = time.time()
+            st.forward(pos, w, want_top16=True)
+            st.sync()
+            g_logits, g_ids = st.logits(T), st.greedy(T)
+            gt = gpu_trace(st, cfg, T, len(orc.qsa_layers))
+            t1 = time.time()
+            if tf is not None and T == 1:
+                tf.check_row("pos %d" % pos, pos, w[0], gt, g_logits, g_ids, st.pre_head(1))
+                print("pos %d teacher-forced (%.1f s): %s" % (pos, time.time() - t1, tf.summary()), flush=True)
+            t1 = time.time()
+            o_logits, _, _, ot = orc.forward_trace(pos, w)
+            t2 = time.time()
+            par.window("pos %d" % pos, pos, gt, ot, g_logits, o_logits, g_ids)
+            check_top16(st, g_logits, g_ids, T)
+            print("pos %d T=%d: gpu %.1f s, oracle %.1f s; %s" % (pos, T, t1 - t0, t2 - t1, par.summary()), flush=True)
+            if teacher:
+                print("  free-running drift by layer (tolerance excess): %s" % par.drift_profile(), flush=True)
+            prev = int(g_ids[-1])
+            pos += T
+        return par, tf
     finally:
         st.close()
 
 
 @pytest.mark.parametrize("seed,n_ctx", [(1234, 600), (77, 601), (5, 300)])
 def test_stage_multilayer_decode(wz, gpu, seed, n_ctx):
-    """Four layers (GDN, QSA, GDN, QSA): four single-token steps then a T=4 window; every decidable
-    row matches the oracle."""
+    """Four layers (GDN, QSA, GDN, QSA): four single-token steps then a T=4 window, compared layer by
+    layer."""
     print("case multilayer seed=%d n_ctx=%d" % (seed, n_ctx), flush=True)
     cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
-    st = wzy_amd.Stage(cfg)
-    try:
-        st.load_synthetic(seed, n_ctx)
-        orc = OracleModel(wz, st, cfg, seed)
-        rng = np.random.default_rng(seed)
-        pos, checked, skipped, tainted = n_ctx, 0, 0, False
-        windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
-        for w in windows:
-            T = len(w)
-            st.forward(pos, w, want_top16=True)
+    rng = np.random.default_rng(seed)
+    windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
+    par, _ = run_layer_parity(wz, cfg, seed, n_ctx, windows)
+    print("multilayer: " + par.summary(), flush=True)
+    assert par.rows_full >= 6 and par.layers_compared >= 28, par.summary()
+
+
+def baseline_cfg(n_layers, ctx_max=32768 + 64):
+    cfg = wzy_amd.default_cfg(ctx_max)
+    cfg.n_layers = n_layers
+    return cfg
+
+
+@pytest.mark.timeout(900)
+def test_stage_baseline_shapes_4_layers(wz, gpu):
+    """BASELINE shapes, layers GDN, GDN, GDN, QSA at a 32,768-cell prefilled context: four single-token
+    steps, each checked component by component (teacher-forced), then a T=4 window; the discrete
+    decisions of every row are compared free-running."""
+    print("case baseline_4_layers", flush=True)
+    cfg = baseline_cfg(4)
+    rng = np.random.default_rng(41)
+    windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
+    par, tf = run_layer_parity(wz, cfg, 41, 32768, windows, teacher=True)
+    print("baseline 4 layers: " + par.summary(), flush=True)
+    print("baseline 4 layers: " + tf.summary(), flush=True)
+    assert tf.counts["rows"] == 4 and tf.counts["layers"] == 16
+    assert par.router_compared >= 12 and par.select_compared >= 3, par.summary()
+
+
+@pytest.mark.timeout(1200)
+def test_stage_baseline_48_layers_greedy(wz, gpu):
+    """The BASELINE config-4 model (48 layers: 36 GDN + 12 QSA, 512 experts top-10, vocab 151,936) at a
+    32,768-cell prefilled context: a greedy chain of four single-token steps (each fed the GPU's
+    greedy id) and a T=4 window, compared layer by layer with the oracle."""
+    print("case baseline_48_layers", flush=True)
+    cfg = baseline_cfg(48)
+    windows = [[11], [None], [None], [None], [5, 150000, 77, 4096]]
+    par, tf = run_layer_parity(wz, cfg, 3, 32768, windows, greedy_feed=True, teacher=True)
+    print("baseline 48 layers: " + par.summary(), flush=True)
+    print("baseline 48 layers: " + tf.summary(), flush=True)
+    # every component of every layer of the four greedy steps, teacher-forced
+    assert tf.counts["rows"] == 4 and tf.counts["layers"] == 4 * 48
+    # free-running: the first row's decisions are compared until the first near tie
+    assert par.router_compared >= 12 and par.select_compared >= 3, par.summary()
+
+
+def test_stage_baseline_shapes_graph_replay_matches_eager(wz, gpu):
+    """At the BASELINE shapes, graph replays and direct launches give bit-identical logits."""
+    print("case baseline_graph_vs_eager", flush=True)
+    cfg = baseline_cfg(4, ctx_max=4096)
+    outs = []
+    for graphs in (1, 0):
+        st = wzy_amd.Stage(cfg)
+        try:
+            st.lib.wzy_stage_set_graphs(st.h, graphs)
+            st.load_synthetic(9, 3000)
+            seq = []
+            for i, tok in enumerate([5, 17, 900]):
+                st.forward(3000 + i, [tok])
+                st.sync()
+                seq.append(st.logits(1))
+            st.forward(3003, [1, 2, 3, 4])
             st.sync()
-            g, gid = st.logits(T), st.greedy(T)
-            o, _, _ = orc.forward(pos, w)
-            ok = orc.decidable_rows()
-            for t in range(T):
-                tag = "pos %d row %d" % (pos, t)
-                if tainted or not ok[t]:
-                    tainted = True
-                    skipped += 1
-                    print("%s: skipped (min router gap %.3g, min select gap %.3g)" % (
-                        tag, orc.last_margins[:, t, 0].min(), orc.last_margins[:, t, 1].min()), flush=True)
-                    continue
-                check_close(tag, g[t], o[t])
-                check_greedy(tag, gid[t:t + 1], o[t:t + 1])
-                checked += 1
-            check_top16(st, g, gid, T)
-            pos += T
-        print("multilayer: %d rows checked, %d skipped" % (checked, skipped), flush=True)
-    finally:
-        st.close()
+            seq.append(st.logits(4))
+            outs.append(seq)
+        finally:
+            st.close()
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
 
 
 def test_stage_graph_replay_matches_eager(wz, gpu):
@@ -368,6 +455,10 @@ def test_stage_moe_weights_prefill_matches_decode(wz, gpu):
         same = [np.array_equal(np.sort(ip[t * K:(t + 1) * K]), np.sort(idd[t * K:(t + 1) * K])) for t in range(T)]
         assert sum(same) >= T - 1, same
         rows = np.repeat(np.array(same), D)
-        check_close("prefill vs decode MoE", cp[rows], cd[rows])
+        # bf16 (prefill) vs per-16 int8 (decode) activations: the two paths round differently, so
+        # they are held to the tolerance over the whole vector, not elementwise
+        err, scale = np.abs(cp[rows] - cd[rows]).max(), np.abs(cd[rows]).max()
+        print("prefill vs decode MoE: max abs err %.3g (max %.3g)" % (err, scale), flush=True)
+        assert err <= ATOL + RTOL * scale
     finally:
         st.close()

@@ -147,6 +147,16 @@ struct wzy_stage {
     bool profiling = false;         // direct launches instead of graphs
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
 
+    // per-layer trace of the last forward (direct launches while on): HC read outputs, block and
+    // MoE outputs [n_layers][W][D], router logits / ids / weights [n_layers][W][E or K], and per QSA
+    // layer the block scores [n_qsa][W][max_b], selected cells [n_qsa][W][topk] and counts [n_qsa][W]
+    bool trace = false;
+    float *tr_mixa = nullptr, *tr_block = nullptr, *tr_mixf = nullptr, *tr_comb = nullptr;
+    float *tr_ra = nullptr, *tr_rf = nullptr, *tr_inja = nullptr, *tr_injf = nullptr;
+    float *tr_logits = nullptr, *tr_wts = nullptr, *tr_scores = nullptr;
+    int *tr_ids = nullptr, *tr_sel = nullptr, *tr_cnt = nullptr;
+    int trace_alloc();
+
     ~wzy_stage();
     int alloc(void** p, size_t bytes, bool zero = true);
     template <class T>
@@ -435,10 +445,21 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
         return launch_hc_post(b, T, st);
     };
 
+    // trace copies (direct launches only): n elements of `src` into row block (slot, 0..T) of `dst`
+    auto tr = [&](void* dst, const void* src, int slot, size_t per_row, size_t elt) -> int {
+        if (!trace) return WZY_OK;
+        WZY_HIP_TRY(hipMemcpyAsync((char*) dst + ((size_t) slot * WZY_MAX_W) * per_row * elt, src,
+                                   (size_t) T * per_row * elt, hipMemcpyDeviceToDevice, st));
+        return WZY_OK;
+    };
+
     for (int l = 0; l < c.n_layers; ++l) {
         Layer& w = L[l];
         // ---------------- attention half ----------------
         WZY_TRY(hc_read(w.hc_norm[0], w.hc_down[0], w.hc_inj[0], w.hc_up[0], inj_a, l == 0));
+        WZY_TRY(tr(tr_mixa, mixed, l, D, 4));
+        WZY_TRY(tr(tr_ra, R[cur], l, HCD, 4));
+        WZY_TRY(tr(tr_inja, inj_a, l, c.hc, 4));
         if (!w.qsa) {
             GemvSegs s;
             s.n = 4;
@@ -487,6 +508,9 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             sa.scores = scores; sa.max_b = max_b;
             WZY_TRY(launch_qsa_score(sa, T, st));
             WZY_TRY(launch_qsa_topk(qd, d_pos, scores, max_b, sel_ids, sel_cnt, T, st));
+            WZY_TRY(tr(tr_scores, scores, w.local, max_b, 4));
+            WZY_TRY(tr(tr_sel, sel_ids, w.local, c.idx_topk, 4));
+            WZY_TRY(tr(tr_cnt, sel_cnt, w.local, 1, 4));
             QsaAttnArgs at{};
             at.dm = qd; at.pos = d_pos; at.qg = qg; at.kv = w.kv; at.sel_ids = sel_ids; at.part = att_part;
             at.part_ml = att_ml; at.out = att_out;
@@ -496,12 +520,20 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
             o.seg[0] = GemvSeg{w.wo.q, w.wo.s, block, D, GEMV_Q8, D, 0};
             WZY_TRY(launch_gemv_segs(o, att_out, QD, T, st));
         }
+        WZY_TRY(tr(tr_block, block, l, D, 4));
         pend_bo = block;
         pend_inj = inj_a;
         // ---------------- FFN half ----------------
         WZY_TRY(hc_read(w.hc_norm[1], w.hc_down[1], w.hc_inj[1], w.hc_up[1], inj_f, false));
+        WZY_TRY(tr(tr_mixf, mixed, l, D, 4));
+        WZY_TRY(tr(tr_rf, R[cur], l, HCD, 4));
+        WZY_TRY(tr(tr_injf, inj_f, l, c.hc, 4));
         WZY_TRY(moe_launch_route(&w.moe, mws, mixed, T, st));
         WZY_TRY(moe_launch_experts(&w.moe, mws, mixed, T, comb, st));
+        WZY_TRY(tr(tr_logits, mws.logits, l, c.n_exp, 4));
+        WZY_TRY(tr(tr_ids, mws.ids, l, c.top_k, 4));
+        WZY_TRY(tr(tr_wts, mws.wts, l, c.top_k, 4));
+        WZY_TRY(tr(tr_comb, comb, l, D, 4));
         pend_bo = comb;
         pend_inj = inj_f;
     }
@@ -709,7 +741,7 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
     if (emb) WZY_HIP_TRY(hipMemcpyAsync(st->emb_rows, emb, (size_t) T * st->D * 4, hipMemcpyHostToDevice, st->stream));
     st->last_T = T;
     st->have_head = run_head != 0;
-    const bool use_graph = st->graphs && !st->profiling;
+    const bool use_graph = st->graphs && !st->profiling && !st->trace;
     if (!use_graph) return st->enqueue(T, emb != nullptr, run_head, save_snaps, want_top16, snap_offset);
     const unsigned long long key = ((unsigned long long) T << 16) | ((unsigned long long) snap_offset << 8) |
                                    (emb ? 16ull : 0ull) | (run_head ? 4ull : 0ull) | (want_top16 ? 2ull : 0ull) |
@@ -738,6 +770,35 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
         it = st->graph_execs.emplace(key, ex).first;
     }
     WZY_HIP_TRY(hipGraphLaunch(it->second, st->stream));
+    return WZY_OK;
+}
+
+int wzy_stage::trace_alloc() {
+    if (tr_mixa) return WZY_OK;
+    const wzy_stage_cfg& c = cfg;
+    const size_t W = WZY_MAX_W, nl = (size_t) c.n_layers, nq = (size_t) (n_qsa > 0 ? n_qsa : 1);
+    WZY_TRY(alloc_t(&tr_mixa, nl * W * D)); reg(-1, "trace.mixed_a", tr_mixa, nl * W * D * 4);
+    WZY_TRY(alloc_t(&tr_block, nl * W * D)); reg(-1, "trace.block", tr_block, nl * W * D * 4);
+    WZY_TRY(alloc_t(&tr_mixf, nl * W * D)); reg(-1, "trace.mixed_f", tr_mixf, nl * W * D * 4);
+    WZY_TRY(alloc_t(&tr_comb, nl * W * D)); reg(-1, "trace.comb", tr_comb, nl * W * D * 4);
+    WZY_TRY(alloc_t(&tr_ra, nl * W * HCD)); reg(-1, "trace.R_a", tr_ra, nl * W * HCD * 4);
+    WZY_TRY(alloc_t(&tr_rf, nl * W * HCD)); reg(-1, "trace.R_f", tr_rf, nl * W * HCD * 4);
+    WZY_TRY(alloc_t(&tr_inja, nl * W * c.hc)); reg(-1, "trace.inj_a", tr_inja, nl * W * c.hc * 4);
+    WZY_TRY(alloc_t(&tr_injf, nl * W * c.hc)); reg(-1, "trace.inj_f", tr_injf, nl * W * c.hc * 4);
+    WZY_TRY(alloc_t(&tr_logits, nl * W * c.n_exp)); reg(-1, "trace.moe_logits", tr_logits, nl * W * c.n_exp * 4);
+    WZY_TRY(alloc_t(&tr_ids, nl * W * c.top_k)); reg(-1, "trace.moe_ids", tr_ids, nl * W * c.top_k * 4);
+    WZY_TRY(alloc_t(&tr_wts, nl * W * c.top_k)); reg(-1, "trace.moe_wts", tr_wts, nl * W * c.top_k * 4);
+    WZY_TRY(alloc_t(&tr_scores, nq * W * max_b)); reg(-1, "trace.scores", tr_scores, nq * W * max_b * 4);
+    WZY_TRY(alloc_t(&tr_sel, nq * W * c.idx_topk)); reg(-1, "trace.sel_ids", tr_sel, nq * W * c.idx_topk * 4);
+    WZY_TRY(alloc_t(&tr_cnt, nq * W)); reg(-1, "trace.sel_cnt", tr_cnt, nq * W * 4);
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_set_trace(wzy_stage* st, int enable) {
+    WZY_REQUIRE(st, "set_trace: null stage");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    if (enable) WZY_TRY(st->trace_alloc());
+    st->trace = enable != 0;
     return WZY_OK;
 }
 
@@ -837,6 +898,18 @@ extern "C" int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name,
     WZY_REQUIRE(bytes <= t->bytes, "read_tensor: %zu bytes requested, tensor has %zu", bytes, t->bytes);
     WZY_HIP_TRY(hipStreamSynchronize(st->stream));
     WZY_HIP_TRY(hipMemcpy(host, t->p, bytes, hipMemcpyDeviceToHost));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset, void* host,
+                                           size_t bytes) {
+    WZY_REQUIRE(st && name && host, "read_tensor_range: null argument");
+    Tensor* t = find_tensor(st, layer, name);
+    WZY_REQUIRE(t, "read_tensor_range: no tensor %s in layer %d", name, layer);
+    WZY_REQUIRE(offset <= t->bytes && bytes <= t->bytes - offset,
+                "read_tensor_range: [%zu, +%zu) outside the tensor's %zu bytes", offset, bytes, t->bytes);
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    WZY_HIP_TRY(hipMemcpy(host, (const char*) t->p + offset, bytes, hipMemcpyDeviceToHost));
     return WZY_OK;
 }
 extern "C" int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes) {

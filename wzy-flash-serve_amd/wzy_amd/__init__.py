@@ -53,6 +53,15 @@ class QsaDims(C.Structure):
                 ("ctx_max", I32), ("kv_ring", I32), ("kv_sinks", I32), ("eps", F32)]
 
 
+class QsaLayer(C.Structure):
+    """struct wzy_qsa_layer (include/wzy_kernels.h)"""
+    _fields_ = [("qg", P), ("kk", P), ("vv", P), ("q_idx", P), ("idx_raw", P),
+                ("q_norm", P), ("k_norm", P), ("iq_norm", P), ("ik_norm", P), ("cos_tab", P), ("sin_tab", P),
+                ("kq", P), ("ks", P), ("vq", P), ("vs", P), ("idx_tail", P), ("idx_dead", P), ("idx_pooled", P),
+                ("scores", P), ("max_b", I32), ("sel_ids", P), ("sel_cnt", P), ("out", P), ("workspace", P),
+                ("workspace_bytes", SZ)]
+
+
 class StageCfg(C.Structure):
     """struct wzy_stage_cfg (include/wzy_stage.h)"""
     _fields_ = [("n_layers", I32), ("qsa_period", I32), ("n_embd", I32), ("hc", I32), ("hc_lr", I32),
@@ -117,6 +126,8 @@ _SIGS = {
     "wzy_stage_logits": (I32, [P, P, I32], True),
     "wzy_stage_pre_head": (I32, [P, P, I32], True),
     "wzy_stage_set_graphs": (I32, [P, I32], True),
+    "wzy_stage_set_trace": (I32, [P, I32], True),
+    "wzy_stage_read_tensor_range": (I32, [P, I32, C.c_char_p, SZ, P, SZ], True),
     "wzy_stage_stream": (P, [P], False),
     "wzy_stage_tensor_bytes": (SZ, [P, I32, C.c_char_p], False),
     "wzy_stage_read_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
@@ -154,6 +165,8 @@ _SIGS = {
     "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
     "wzy_row_top16": (I32, [P, I32, I32, P, P, P, P], True),
     "wzy_row_top16_noalloc": (I32, [P, I32, I32, P, P, P, P], True),
+    "wzy_gdn_time_recurrence": (I32, [P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P, P, P], True),
+    "wzy_qsa_time_decode": (I32, [C.POINTER(QsaDims), C.POINTER(QsaLayer), P, I32, P, P], True),
     # synth
     "wzy_synth_hash": (U64, [U64, U64, U64], False),
     "wzy_synth_stream": (U64, [U32, U32, U32], False),
@@ -352,6 +365,14 @@ class Stage:
             raise WzyError("no tensor %s in layer %d" % (name, layer))
         out = np.empty(n // np.dtype(dtype).itemsize, dtype)
         self.lib.wzy_stage_read_tensor(self.h, layer, name.encode(), out.ctypes.data, out.nbytes)
+        return out
+
+    def read_range(self, layer, name, dtype, first, count):
+        """Elements [first, first + count) of a tensor."""
+        import numpy as np
+        it = np.dtype(dtype).itemsize
+        out = np.empty(count, dtype)
+        self.lib.wzy_stage_read_tensor_range(self.h, layer, name.encode(), first * it, out.ctypes.data, count * it)
         return out
 
     def write(self, layer, name, arr):
