@@ -261,7 +261,10 @@ int wzy_qsa_select(const wzy_qsa_dims* dims, const int* pos, const uint16_t* idx
 
 /* Exact top-idx_topk cell selection alone, over caller-supplied block scores [T x max_b] (row t's
  * context is pos[0] + t + 1 cells; its blocks 0 .. n_kv/idx_blk hold the scores): the second half
- * of wzy_qsa_select.  Replaces qsa_block_topk_multi (src/wzy_qsa_256k.cuh:266-403). */
+ * of wzy_qsa_select.  Rows longer than 16,384 blocks are histogrammed by several workgroups that
+ * meet in per-device state of the library (row histograms, arrival counters, candidate lists), so
+ * selections on one device (this call, wzy_qsa_select, a stage forward) must not overlap in time.
+ * max_b <= 64 x 16,384.  Replaces qsa_block_topk_multi (src/wzy_qsa_256k.cuh:266-403). */
 int wzy_qsa_topk(const wzy_qsa_dims* dims, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
                  int T, void* stream);
 

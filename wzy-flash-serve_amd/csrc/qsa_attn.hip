@@ -1,13 +1,9 @@
 // qsa_attn.hip -- QSA cell selection and sparse attention for gfx950.
 //
-//  qsa_topk   exact top-`topk` cells of one row, one 1024-thread workgroup: the block scores are
-//             loaded once into registers as order-preserving keys, 2048-bin histograms over the
-//             keys' own range (narrowed pass by pass) and a final ranking of the few blocks left
-//             find the threshold key, then every block above the threshold is taken whole and
-//             blocks at the threshold are filled in the reference's tie order.  The reference walks the blocks with 256 threads,
-//             thread t owning blocks t, t+256, ... and emitting them thread-major; here thread
-//             4t+s owns the s-th quarter of thread t's blocks, so a scan in thread order reproduces
-//             that order exactly.  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
+//  qsa_topk   exact top-`topk` cells of each row: a multi-workgroup histogram of the 12-bit key
+//             prefixes finds the threshold's prefix bin, then one workgroup per row resolves the
+//             rest of the threshold key and writes the selection in the reference's order (see
+//             the section below).  reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
 //  qsa_attn   split-K sparse attention: workgroup (chunk of 64 selected cells, kv head, slice of 4
 //             q heads, row) stages the chunk's INT8 K and V rows in LDS with one round of 128-bit
 //             loads, computes its heads' scores (wave = head, lane = cell), a local softmax, and the
@@ -22,9 +18,6 @@ using namespace wzy;
 
 namespace {
 
-constexpr int TK_THREADS = 1024;
-constexpr int TK_MAXJ_SMALL = 16;    // blocks per thread: 16384 blocks (65532 cells at 4 per block)
-constexpr int TK_MAXJ_LARGE = 66;    // 67584 blocks (270332 cells); keys partly spill to scratch
 constexpr int ATT_HPW = 4;           // q heads per attention workgroup (one per wave in the score phase)
 constexpr int ATT_ROW = 256 + 16;    // LDS bytes per cell row (hd = 256 codes + pad against bank conflicts)
 constexpr int ATT_CH_MAX = 32;       // chunks per row: topk <= 2048
@@ -69,169 +62,389 @@ WZY_DEV void block_scan_incl2(int& x, int& y, int* s_x, int* s_y) {
 // Full-wave minimum of a 32-bit unsigned value (the complement of a maximum).
 WZY_DEV uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
-constexpr int TK_NBIN = 2 * TK_THREADS;   // histogram bins per pass (two per thread in the scan)
-constexpr int TK_LOG_NBIN = 11;
-constexpr int TK_CAND = 256;               // threshold-bin weight at which the pass loop hands over to ranking
-
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
-// exact top-k cell selection, one workgroup per row; TK_MAXJ = blocks held per thread.
-// Threshold search: the order keys of the row's blocks span [kmin, kmax]; a pass histograms the
-// keys of a window [lo, lo + TK_NBIN << shift) into TK_NBIN bins of 2^shift keys (block weights =
-// cells), and one scan from the top bin down finds the bin holding the width-th cell.  The window
-// narrows to that bin; once its weight is at most TK_CAND (or a bin is a single key) its few blocks
-// are ranked against each other directly.  The threshold is the key value thr with
-// weight(key > thr) < width <= weight(key >= thr), the same value a digit-by-digit radix select finds.
+// exact top-k cell selection: a radix select on the order keys of the block scores, most
+// significant bits first (12 + 12 + 8 bits), block weights = cells.  The threshold is the key
+// value thr with weight(key > thr) < width <= weight(key >= thr); blocks above it are taken whole
+// and blocks at it are filled in the reference's tie order.
+//
+// One launch, workgroups of 1,024 threads, each holding 16,384 blocks of a row in registers
+// (thread p: blocks base + 1024 q + p).  Level 1 is a 4,096-bin histogram of the 12-bit key
+// prefixes.  A row that fits one workgroup (up to 65,536 cells) keeps it in LDS; a longer row's
+// workgroups add their histograms to the row's histogram in device memory and the last one to
+// arrive carries on alone.  That workgroup lists the blocks at or above the threshold's prefix bin
+// (usually ~1,000 of them) in LDS, resolves the remaining 20 bits over the list, and writes each
+// selected block at its offset in the reference's order: the reference walks the blocks with 256
+// threads, thread t emitting blocks t, t+256, ... in turn, so block b's cells follow the cells of
+// the selected blocks of walkers t' < b mod 256 and of walker b mod 256 before it (ties at the
+// threshold take the remaining budget in that order).  When the bin holds more blocks than the
+// list, the selection sweeps every key of the row instead (heavy ties).
+// reference: qsa_block_topk_multi (src/wzy_qsa_256k.cuh:226-403)
 // ---------------------------------------------------------------------------------------------
-template <int TK_MAXJ>
-__global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
-                                                              const float* __restrict__ scores, int max_b,
-                                                              int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
-    constexpr int NW = TK_THREADS / 64;
-    __shared__ int hist[TK_NBIN];
-    __shared__ uint32_t s_ck[TK_CAND];
-    __shared__ int s_cw[TK_CAND];
-    __shared__ int s_w[NW], s_c[NW];
-    __shared__ uint32_t s_mn[NW], s_mx[NW];
-    __shared__ int s_bin, s_above, s_cnt, s_ncand;
-    __shared__ uint32_t s_thr;
-    const int p = threadIdx.x, row = blockIdx.x, lane = p & 63, w = p >> 6;
-    const int n_kv = *pos_dev + row + 1;
-    const int K = dm.topk, B = dm.iblk;
-    const int width = min(n_kv, K);
-    int* out = sel_ids + (size_t) row * K;
-    if (p == 0) sel_cnt[row] = width;
-    if (n_kv <= K) {                                 // short context: every cell, in order
-        for (int j = p; j < n_kv; j += TK_THREADS) out[j] = j;
-        return;
+namespace {
+constexpr int TK_L1_SHIFT = 20, TK_L1_BINS = 4096;     // level 1: key bits 31..20
+constexpr int TK_L2_BINS = 4096;                       // level 2: bits 19..8
+constexpr int TK_L3_BINS = 256;                        // level 3: bits 7..0
+constexpr int TK_THREADS = 1024, TK_NW = TK_THREADS / 64, TK_PER = 16;
+constexpr int TK_CHUNK = TK_THREADS * TK_PER;          // blocks per workgroup
+constexpr int TK_LIST = 4096;                          // listed blocks (LDS)
+constexpr int TK_BATCH = 16;                           // loads in flight per thread in a sweep
+
+WZY_DEV int tk_weight(int b, int n_bid, int nb, int n_kv, int B) {
+    return b < n_bid ? B : (b < nb ? n_kv - n_bid * B : 0);
+}
+
+// Bins owned NPER per thread in descending order (thread 0 holds the highest).  Finds the bin where
+// the weight counted from the top, starting at `base`, reaches `width`; the owner writes (bin,
+// weight above it, its weight) to s_res.  One barrier inside; the caller syncs before reading s_res.
+template <int NPER>
+WZY_DEV void tk_find(const int* hist, int nbins, int base, int width, int* s_w, int* s_c, int* s_res) {
+    const int p = threadIdx.x;
+    int c[NPER];
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < NPER; ++k) {
+        const int bin = nbins - 1 - NPER * p - k;
+        c[k] = bin >= 0 ? hist[bin] : 0;
+        sum += c[k];
     }
-    const int n_bid = n_kv / B, nb = min(n_bid + 1, max_b);   // complete blocks + the open block
+    int incl = sum, dummy = 0;
+    block_scan_incl2<TK_NW>(incl, dummy, s_w, s_c);
+    int acc = base + incl - sum;
+#pragma unroll
+    for (int k = 0; k < NPER; ++k) {
+        const int bin = nbins - 1 - NPER * p - k;
+        if (bin >= 0 && acc < width && acc + c[k] >= width) { s_res[0] = bin; s_res[1] = acc; s_res[2] = c[k]; }
+        acc += c[k];
+    }
+}
+
+struct TkShared {
+    int hist[TK_L2_BINS];
+    uint32_t lkey[TK_LIST];
+    int lblk[TK_LIST];                                 // block ids (list) or weights (sweep candidates)
+    uint32_t bucket[TK_LIST];                          // block << 1 | above-threshold flag
+    int c_gt[256], c_eq[256], c_n[256], c_fill[256];
+    int s_w[TK_NW], s_c[TK_NW], s_res[3];
+    int s_n, s_last;
+};
+}  // namespace
+
+// Row histograms and arrival counters of the multi-workgroup rows (one per window row).  Every
+// launch leaves both at zero; launches on one device must not overlap.
+__device__ int g_tk_hist[WZY_MAX_W * TK_L1_BINS];
+__device__ unsigned g_tk_arrive[WZY_MAX_W];
+// Per workgroup of a multi-workgroup row: its blocks at or above its own level-1 bin, (key, block),
+// and their count (-1: more than TK_LOCAL).  A block of the row's selection is in its workgroup's
+// own top `width` cells, so it is in that workgroup's list.
+constexpr int TK_LOCAL = 2048, TK_MAX_WG = 64;       // up to 64 x 16,384 blocks per row
+__device__ uint2 g_tk_cand[WZY_MAX_W * TK_MAX_WG * TK_LOCAL];
+__device__ int g_tk_cand_n[WZY_MAX_W * TK_MAX_WG];
+
+// Levels 2 and 3 over the n listed blocks (LDS), then the output.  b1 / above1: the level-1 bin
+// and the weight above it.
+WZY_DEV void tk_finish_list(TkShared& S, int n, uint32_t b1, int above1, int n_kv, int width, int B, int* out) {
+    const int p = threadIdx.x;
+    const int n_bid = n_kv / B, nb = n_bid + 1;
+    for (int i = p; i < TK_L2_BINS; i += TK_THREADS) S.hist[i] = 0;
+    if (p < 256) { S.c_gt[p] = 0; S.c_eq[p] = 0; S.c_n[p] = 0; S.c_fill[p] = 0; }
+    __syncthreads();
+    for (int i = p; i < n; i += TK_THREADS) {
+        const uint32_t k = S.lkey[i];
+        if ((k >> TK_L1_SHIFT) == b1) atomicAdd(&S.hist[(k >> 8) & 0xFFF], tk_weight(S.lblk[i], n_bid, nb, n_kv, B));
+    }
+    __syncthreads();
+    tk_find<TK_L2_BINS / TK_THREADS>(S.hist, TK_L2_BINS, above1, width, S.s_w, S.s_c, S.s_res);
+    __syncthreads();
+    const uint32_t pre24 = (b1 << 12) | (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+    const int above2 = __builtin_amdgcn_readfirstlane(S.s_res[1]);
+    if (p < TK_L3_BINS) S.hist[p] = 0;
+    __syncthreads();
+    for (int i = p; i < n; i += TK_THREADS) {
+        const uint32_t k = S.lkey[i];
+        if ((k >> 8) == pre24) atomicAdd(&S.hist[k & 0xFF], tk_weight(S.lblk[i], n_bid, nb, n_kv, B));
+    }
+    __syncthreads();
+    tk_find<1>(S.hist, TK_L3_BINS, above2, width, S.s_w, S.s_c, S.s_res);
+    __syncthreads();
+    const uint32_t thr = (pre24 << 8) | (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+    const int budget = width - __builtin_amdgcn_readfirstlane(S.s_res[1]);
+    // per-walker totals of the cells above / at the threshold and bucket sizes
+    for (int i = p; i < n; i += TK_THREADS) {
+        const uint32_t k = S.lkey[i];
+        if (k >= thr) {
+            const int b = S.lblk[i], t = b & 255;
+            atomicAdd(k > thr ? &S.c_gt[t] : &S.c_eq[t], tk_weight(b, n_bid, nb, n_kv, B));
+            atomicAdd(&S.c_n[t], 1);
+        }
+    }
+    __syncthreads();
+    {   // exclusive scan over the 256 walkers (threads 0..255 hold one each)
+        const int g = p < 256 ? S.c_gt[p] : 0, e = p < 256 ? S.c_eq[p] : 0, nn = p < 256 ? S.c_n[p] : 0;
+        int gi = g, ei = e;
+        block_scan_incl2<TK_NW>(gi, ei, S.s_w, S.s_c);
+        __syncthreads();
+        int ni = nn, dummy = 0;
+        block_scan_incl2<TK_NW>(ni, dummy, S.s_w, S.s_c);
+        __syncthreads();
+        if (p < 256) { S.c_gt[p] = gi - g; S.c_eq[p] = ei - e; S.c_n[p] = ni - nn; }
+    }
+    __syncthreads();
+    for (int i = p; i < n; i += TK_THREADS) {
+        const uint32_t k = S.lkey[i];
+        if (k >= thr) {
+            const int b = S.lblk[i], t = b & 255;
+            S.bucket[S.c_n[t] + atomicAdd(&S.c_fill[t], 1)] = ((uint32_t) b << 1) | (k > thr ? 1u : 0u);
+        }
+    }
+    __syncthreads();
+    for (int i = p; i < n; i += TK_THREADS) {
+        const uint32_t k = S.lkey[i];
+        if (k < thr) continue;
+        const int b = S.lblk[i], t = b & 255, j = b >> 8, w = tk_weight(b, n_bid, nb, n_kv, B);
+        int gt_before = S.c_gt[t], eq_before = S.c_eq[t];
+        const int s0 = S.c_n[t], s1 = s0 + S.c_fill[t];
+        for (int q = s0; q < s1; ++q) {
+            const uint32_t e = S.bucket[q];
+            const int bb = (int) (e >> 1);
+            if ((bb >> 8) < j) {
+                const int wb = tk_weight(bb, n_bid, nb, n_kv, B);
+                if (e & 1u) gt_before += wb; else eq_before += wb;
+            }
+        }
+        const int off = gt_before + min(eq_before, budget);
+        const int take = k > thr ? w : max(0, min(w, budget - eq_before));
+        for (int c = 0; c < take; ++c) out[off + c] = b * B + c;
+    }
+}
+
+// Levels 2 and 3 and the output by sweeping every key of the row (the threshold bin holds more
+// blocks than the list).  Thread 4t+s walks the s-th quarter of reference walker t's blocks.
+WZY_DEV void tk_finish_sweep(TkShared& S, const float* sc, uint32_t b1, int above1, int cnt1, int n_kv, int width,
+                             int B, int* out) {
+    const int p = threadIdx.x;
+    const int n_bid = n_kv / B, nb = n_bid + 1;
     const int tt = p >> 2, sub = p & 3;
     const int J = (nb + 255) / 256, J4 = (J + 3) / 4;
-    const int j0 = sub * J4, j1 = min(J, j0 + J4);
-    const float* sc = scores + (size_t) row * max_b;
-
-    // weight (cells) of this thread's q-th block: B for complete blocks, the open block's fill, 0 past the end
-    auto wgt = [&](int q) -> int {
-        const int b = tt + 256 * (j0 + q);
-        return ((j0 + q) < j1 && b < nb) ? (b < n_bid ? B : n_kv - n_bid * B) : 0;
+    const int j0 = sub * J4, nq = max(0, min(J, j0 + J4) - j0);
+    auto blk = [&](int q) { return tt + 256 * (j0 + q); };
+    auto sweep = [&](auto&& f) {
+        for (int q0 = 0; q0 < nq; q0 += TK_BATCH) {
+            float v[TK_BATCH];
+#pragma unroll
+            for (int u = 0; u < TK_BATCH; ++u) v[u] = sc[min(blk(q0 + u), nb - 1)];
+#pragma unroll
+            for (int u = 0; u < TK_BATCH; ++u)
+                f(q0 + u, order_key(v[u]), q0 + u < nq ? tk_weight(blk(q0 + u), n_bid, nb, n_kv, B) : 0);
+        }
     };
-    // every score load is issued before the first key is formed (clamped index, no branch around
-    // a load, so no load waits for an earlier one)
-    float sv[TK_MAXJ];
-#pragma unroll
-    for (int q = 0; q < TK_MAXJ; ++q) sv[q] = sc[min(tt + 256 * (j0 + q), nb - 1)];
-    for (int i = p; i < TK_NBIN; i += TK_THREADS) hist[i] = 0;
-    if (p == 0) s_ncand = 0;
-    uint32_t key[TK_MAXJ];
-    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
-#pragma unroll
-    for (int q = 0; q < TK_MAXJ; ++q) {
-        key[q] = order_key(sv[q]);
-        if (wgt(q) > 0) { mn = min(mn, key[q]); mx = max(mx, key[q]); }
-    }
-    mn = wave_min_u32(mn);
-    mx = wave_max_u32(mx);
-    if (lane == 0) { s_mn[w] = mn; s_mx[w] = mx; }
+    for (int i = p; i < TK_L2_BINS; i += TK_THREADS) S.hist[i] = 0;
+    if (p == 0) S.s_n = 0;
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NW; ++i) { mn = min(mn, s_mn[i]); mx = max(mx, s_mx[i]); }
-
-    // window passes: at most three (shift 21 -> 10 -> 0)
-    uint32_t lo = mn;
-    const uint32_t range = mx - mn;
-    int shift = range ? max(0, 32 - __builtin_clz(range) - TK_LOG_NBIN) : 0;
-    int above = 0, cnt = 0;
-    uint32_t thr = mn;                               // one key value in the whole row: no pass needed
-    bool ranked = false;
-    while (range != 0) {
-#pragma unroll
-        for (int q = 0; q < TK_MAXJ; ++q) {
-            const uint32_t d = key[q] - lo;
-            if (wgt(q) > 0 && key[q] >= lo && (d >> shift) < (uint32_t) TK_NBIN) atomicAdd(&hist[d >> shift], wgt(q));
+    const bool list = cnt1 <= TK_LIST;               // cells; every listed block holds at least one
+    sweep([&](int, uint32_t k, int w) {
+        if (w > 0 && (k >> TK_L1_SHIFT) == b1) {
+            atomicAdd(&S.hist[(k >> 8) & 0xFFF], w);
+            if (list) {
+                const int slot = atomicAdd(&S.s_n, 1);
+                S.lkey[slot] = k;
+                S.lblk[slot] = w;
+            }
         }
-        __syncthreads();
-        // thread p owns bins TK_NBIN-1-2p (h1) and TK_NBIN-2-2p (h0): thread order = descending keys
-        const int b1 = TK_NBIN - 1 - 2 * p, b0 = b1 - 1;
-        const int h1 = hist[b1], h0 = hist[b0];
-        hist[b1] = 0;                                // cleared for the next pass
-        hist[b0] = 0;
-        int incl = h1 + h0, dummy = 0;
-        block_scan_incl2<NW>(incl, dummy, s_w, s_c);
-        const int before = above + incl - (h1 + h0);
-        if (before < width && before + h1 >= width) { s_bin = b1; s_above = before; s_cnt = h1; }
-        if (before + h1 < width && before + h1 + h0 >= width) { s_bin = b0; s_above = before + h1; s_cnt = h0; }
-        __syncthreads();
-        lo += (uint32_t) __builtin_amdgcn_readfirstlane(s_bin) << shift;
-        above = __builtin_amdgcn_readfirstlane(s_above);
-        cnt = __builtin_amdgcn_readfirstlane(s_cnt);
-        if (shift == 0) { thr = lo; break; }         // the bin is one key value
-        if (cnt <= TK_CAND) { ranked = true; break; }
-        shift = max(0, shift - TK_LOG_NBIN);
+    });
+    __syncthreads();
+    tk_find<TK_L2_BINS / TK_THREADS>(S.hist, TK_L2_BINS, above1, width, S.s_w, S.s_c, S.s_res);
+    __syncthreads();
+    const uint32_t pre24 = (b1 << 12) | (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+    const int above2 = __builtin_amdgcn_readfirstlane(S.s_res[1]);
+    if (p < TK_L3_BINS) S.hist[p] = 0;
+    const int nc = S.s_n;
+    __syncthreads();
+    if (list) {
+        for (int i = p; i < nc; i += TK_THREADS)
+            if ((S.lkey[i] >> 8) == pre24) atomicAdd(&S.hist[S.lkey[i] & 0xFF], S.lblk[i]);
+    } else {
+        sweep([&](int, uint32_t k, int w) {
+            if (w > 0 && (k >> 8) == pre24) atomicAdd(&S.hist[k & 0xFF], w);
+        });
     }
-    if (ranked) {
-        // the threshold bin [lo, lo + 2^shift) holds at most TK_CAND cells, so at most TK_CAND blocks:
-        // gather them, and each ranks itself against the others
-#pragma unroll
-        for (int q = 0; q < TK_MAXJ; ++q) {
-            if (wgt(q) > 0 && key[q] >= lo && ((key[q] - lo) >> shift) == 0u) {
-                const int slot = atomicAdd(&s_ncand, 1);
-                s_ck[slot] = key[q];
-                s_cw[slot] = wgt(q);
-            }
-        }
-        __syncthreads();
-        const int nc = s_ncand;
-        if (p < nc) {
-            const uint32_t k = s_ck[p];
-            int gtw = 0, eqw = 0;
-            for (int j = 0; j < nc; ++j) {
-                const uint32_t kj = s_ck[j];
-                const int wj = s_cw[j];
-                gtw += kj > k ? wj : 0;
-                eqw += kj == k ? wj : 0;
-            }
-            if (above + gtw < width && above + gtw + eqw >= width) {   // every such block holds the same key
-                s_thr = k;
-                s_above = above + gtw;
-            }
-        }
-        __syncthreads();
-        thr = s_thr;
-        above = s_above;
-    }
-
+    __syncthreads();
+    tk_find<1>(S.hist, TK_L3_BINS, above2, width, S.s_w, S.s_c, S.s_res);
+    __syncthreads();
+    const uint32_t thr = (pre24 << 8) | (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+    const int above = __builtin_amdgcn_readfirstlane(S.s_res[1]);
+    // the threshold-tied cells a thread may take are what is left of the budget after the threads
+    // before it, and its output offset is gt_excl + min(eq_excl, eq_budget)
     const int eq_budget = width - above;
     int gt = 0, eq = 0;
-#pragma unroll
-    for (int q = 0; q < TK_MAXJ; ++q) {
-        const int wq = wgt(q);
-        if (wq == 0) continue;
-        if (key[q] > thr) gt += wq;
-        else if (key[q] == thr) eq += wq;
-    }
-    // one dual scan: the threshold-tied cells a thread may take are what is left of the budget
-    // after the threads before it, and its output offset is gt_excl + min(eq_excl, eq_budget)
+    sweep([&](int, uint32_t k, int w) {
+        gt += k > thr ? w : 0;
+        eq += k == thr ? w : 0;
+    });
     int gt_incl = gt, eq_incl = eq;
-    block_scan_incl2<NW>(gt_incl, eq_incl, s_w, s_c);
+    block_scan_incl2<TK_NW>(gt_incl, eq_incl, S.s_w, S.s_c);
     const int eq_excl = eq_incl - eq;
-    const int my_eq = max(0, min(eq, eq_budget - eq_excl));
+    int eq_left = max(0, min(eq, eq_budget - eq_excl));
     int wpos = (gt_incl - gt) + min(eq_excl, eq_budget);
-    int eq_left = my_eq;
-#pragma unroll
-    for (int q = 0; q < TK_MAXJ; ++q) {
-        const int wq = wgt(q);
-        if (wq == 0) continue;
-        const int b = tt + 256 * (j0 + q);
-        if (key[q] > thr) {
-            for (int c = 0; c < wq; ++c) out[wpos++] = b * B + c;
-        } else if (key[q] == thr && eq_left > 0) {
-            const int take = min(wq, eq_left);
+    sweep([&](int q, uint32_t k, int w) {
+        if (w == 0) return;
+        const int b = blk(q);
+        if (k > thr) {
+            for (int c = 0; c < w; ++c) out[wpos++] = b * B + c;
+        } else if (k == thr && eq_left > 0) {
+            const int take = min(w, eq_left);
             for (int c = 0; c < take; ++c) out[wpos++] = b * B + c;
             eq_left -= take;
         }
+    });
+}
+
+__global__ void __launch_bounds__(TK_THREADS) qsa_topk_kernel(QsaDims dm, const int* __restrict__ pos_dev,
+                                                             const float* __restrict__ scores, int max_b,
+                                                             int* __restrict__ ghist, unsigned* __restrict__ garrive,
+                                                             int* __restrict__ sel_ids, int* __restrict__ sel_cnt) {
+    __shared__ TkShared S;
+    const int p = threadIdx.x, row = blockIdx.y, G = gridDim.x;
+    const int n_kv = *pos_dev + row + 1, K = dm.topk, B = dm.iblk;
+    const int width = min(n_kv, K);
+    int* out = sel_ids + (size_t) row * K;
+    if (n_kv <= K) {                                 // short context: every cell, in order
+        if (blockIdx.x == 0) {
+            if (p == 0) sel_cnt[row] = width;
+            for (int j = p; j < n_kv; j += TK_THREADS) out[j] = j;
+        }
+        return;                                      // every workgroup of the row leaves here
     }
+    const int n_bid = n_kv / B, nb = min(n_bid + 1, max_b);
+    const bool single = nb <= TK_CHUNK;              // the row fits one workgroup's registers
+    if (single && blockIdx.x > 0) return;            // (launched for a longer row of the window)
+    const float* sc = scores + (size_t) row * max_b;
+    const int base = blockIdx.x * TK_CHUNK + p;
+    // this workgroup's keys: every load issued before the first is used
+    float v[TK_PER];
+#pragma unroll
+    for (int q = 0; q < TK_PER; ++q) v[q] = sc[min(base + q * TK_THREADS, nb - 1)];
+    for (int i = p; i < TK_L1_BINS; i += TK_THREADS) S.hist[i] = 0;
+    if (p == 0) S.s_n = 0;
+    __syncthreads();
+    uint32_t key[TK_PER];
+#pragma unroll
+    for (int q = 0; q < TK_PER; ++q) {
+        key[q] = order_key(v[q]);
+        const int w = tk_weight(base + q * TK_THREADS, n_bid, nb, n_kv, B);
+        if (w > 0) atomicAdd(&S.hist[key[q] >> TK_L1_SHIFT], w);
+    }
+    __syncthreads();
+    if (!single) {
+        // this workgroup's own candidates (blocks at or above its own level-1 bin), listed in
+        // device memory for the last workgroup
+        tk_find<TK_L1_BINS / TK_THREADS>(S.hist, TK_L1_BINS, 0, width, S.s_w, S.s_c, S.s_res);
+        __syncthreads();
+        const uint32_t lb1 = (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+        unsigned keep = 0u;
+#pragma unroll
+        for (int q = 0; q < TK_PER; ++q)
+            if (tk_weight(base + q * TK_THREADS, n_bid, nb, n_kv, B) > 0 && (key[q] >> TK_L1_SHIFT) >= lb1)
+                keep |= 1u << q;
+        const int cnt = __builtin_popcount(keep);
+        int incl = cnt, dummy = 0;
+        block_scan_incl2<TK_NW>(incl, dummy, S.s_w, S.s_c);
+        if (p == TK_THREADS - 1) S.s_n = incl;       // blocks this workgroup lists
+        __syncthreads();
+        const int total = S.s_n;
+        if (total <= TK_LOCAL) {
+            uint2* L = g_tk_cand + ((size_t) row * TK_MAX_WG + blockIdx.x) * TK_LOCAL;
+            int slot = incl - cnt;
+#pragma unroll
+            for (int q = 0; q < TK_PER; ++q)
+                if (keep & (1u << q)) L[slot++] = make_uint2(key[q], (uint32_t) (base + q * TK_THREADS));
+        }
+        if (p == 0) g_tk_cand_n[(size_t) row * TK_MAX_WG + blockIdx.x] = total <= TK_LOCAL ? total : -1;
+        // add this histogram to the row's; the last workgroup to arrive takes the row from here
+        int* gh = ghist + (size_t) row * TK_L1_BINS;
+        for (int i = p; i < TK_L1_BINS; i += TK_THREADS) {
+            const int c = S.hist[i];
+            if (c) atomicAdd(&gh[i], c);
+        }
+        __threadfence();
+        __syncthreads();
+        if (p == 0) S.s_last = atomicAdd(&garrive[row], 1u) == (unsigned) (G - 1);
+        __syncthreads();
+        if (!S.s_last) return;
+        __threadfence();
+        int c[TK_L1_BINS / TK_THREADS];
+#pragma unroll
+        for (int k = 0; k < TK_L1_BINS / TK_THREADS; ++k) c[k] = gh[p + k * TK_THREADS];   // all loads first
+        if (p < G && g_tk_cand_n[(size_t) row * TK_MAX_WG + p] < 0) S.s_last = -1;     // a list overflowed
+        if (p == 0) S.s_n = 0;                       // (read by every thread before the last barrier)
+#pragma unroll
+        for (int k = 0; k < TK_L1_BINS / TK_THREADS; ++k) {
+            S.hist[p + k * TK_THREADS] = c[k];
+            gh[p + k * TK_THREADS] = 0;
+        }
+        if (p == 0) garrive[row] = 0u;
+        __syncthreads();
+    }
+    if (p == 0) sel_cnt[row] = width;
+    tk_find<TK_L1_BINS / TK_THREADS>(S.hist, TK_L1_BINS, 0, width, S.s_w, S.s_c, S.s_res);
+    __syncthreads();
+    const uint32_t b1 = (uint32_t) __builtin_amdgcn_readfirstlane(S.s_res[0]);
+    const int above1 = __builtin_amdgcn_readfirstlane(S.s_res[1]);
+    const int cnt1 = __builtin_amdgcn_readfirstlane(S.s_res[2]);
+    if (above1 + cnt1 > TK_LIST) {                    // more candidate blocks than the list holds
+        tk_finish_sweep(S, sc, b1, above1, cnt1, n_kv, width, B, out);
+        return;
+    }
+    // list the blocks at or above the level-1 bin
+    if (single) {
+        unsigned keep = 0u;
+#pragma unroll
+        for (int q = 0; q < TK_PER; ++q)
+            if (tk_weight(base + q * TK_THREADS, n_bid, nb, n_kv, B) > 0 && (key[q] >> TK_L1_SHIFT) >= b1)
+                keep |= 1u << q;
+        const int cnt = __builtin_popcount(keep);
+        int incl = cnt, dummy = 0;
+        block_scan_incl2<TK_NW>(incl, dummy, S.s_w, S.s_c);
+        int slot = incl - cnt;
+#pragma unroll
+        for (int q = 0; q < TK_PER; ++q)
+            if (keep & (1u << q)) { S.lkey[slot] = key[q]; S.lblk[slot] = base + q * TK_THREADS; ++slot; }
+        if (p == TK_THREADS - 1) S.s_n = incl;
+    } else if (S.s_last >= 0) {
+        // the workgroups' own lists hold every candidate: keep those at or above the row's bin
+        const uint2* L = g_tk_cand + (size_t) row * TK_MAX_WG * TK_LOCAL;
+        for (int i = p; i < G * TK_LOCAL; i += TK_THREADS) {
+            const int g = i / TK_LOCAL;
+            if (i - g * TK_LOCAL < g_tk_cand_n[(size_t) row * TK_MAX_WG + g]) {
+                const uint2 e = L[i];
+                if ((e.x >> TK_L1_SHIFT) >= b1) {
+                    const int slot = atomicAdd(&S.s_n, 1);
+                    S.lkey[slot] = e.x;
+                    S.lblk[slot] = (int) e.y;
+                }
+            }
+        }
+    } else {
+        for (int b0 = p; b0 < nb; b0 += TK_THREADS * TK_BATCH) {
+            float u[TK_BATCH];
+#pragma unroll
+            for (int i = 0; i < TK_BATCH; ++i) u[i] = sc[min(b0 + i * TK_THREADS, nb - 1)];
+#pragma unroll
+            for (int i = 0; i < TK_BATCH; ++i) {
+                const int b = b0 + i * TK_THREADS;
+                const uint32_t k = order_key(u[i]);
+                if (b < nb && tk_weight(b, n_bid, nb, n_kv, B) > 0 && (k >> TK_L1_SHIFT) >= b1) {
+                    const int slot = atomicAdd(&S.s_n, 1);
+                    S.lkey[slot] = k;
+                    S.lblk[slot] = b;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    tk_finish_list(S, S.s_n, b1, above1, n_kv, width, B, out);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -398,15 +611,15 @@ int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int 
                     int T, hipStream_t st) {
     WZY_TRY(qsa_check_dims(dm));
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_topk: T out of range");
-    const int per_thread = ((max_b + 255) / 256 + 3) / 4;   // blocks a thread holds at the largest context
-    WZY_REQUIRE(per_thread <= TK_MAXJ_LARGE, "qsa_topk: %d indexer blocks exceed the selection capacity %d", max_b,
-                TK_THREADS * TK_MAXJ_LARGE);
-    if (per_thread <= TK_MAXJ_SMALL)
-        hipLaunchKernelGGL((qsa_topk_kernel<TK_MAXJ_SMALL>), dim3(T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b,
-                           sel_ids, sel_cnt);
-    else
-        hipLaunchKernelGGL((qsa_topk_kernel<TK_MAXJ_LARGE>), dim3(T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b,
-                           sel_ids, sel_cnt);
+    WZY_REQUIRE(max_b >= 1 && max_b <= (1 << 22), "qsa_topk: max_b %d out of range", max_b);
+    int* hist = nullptr;
+    unsigned* arrive = nullptr;
+    WZY_HIP_TRY(hipGetSymbolAddress((void**) &hist, HIP_SYMBOL(g_tk_hist)));
+    WZY_HIP_TRY(hipGetSymbolAddress((void**) &arrive, HIP_SYMBOL(g_tk_arrive)));
+    const int G = (max_b + TK_CHUNK - 1) / TK_CHUNK;
+    WZY_REQUIRE(G <= TK_MAX_WG, "qsa_topk: %d indexer blocks exceed %d", max_b, TK_MAX_WG * TK_CHUNK);
+    hipLaunchKernelGGL(qsa_topk_kernel, dim3(G, T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b, hist, arrive,
+                       sel_ids, sel_cnt);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
