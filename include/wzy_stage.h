@@ -64,7 +64,9 @@ int wzy_stage_load_synthetic(wzy_stage* st, uint64_t seed, int n_ctx);
 
 /* Enqueue the forward of T window rows at positions pos .. pos+T-1 (1 <= T <= 8):
  *   toks [T] token ids (embedding gathered on the GPU), or emb [T x n_embd] fp32 rows (host
- *   memory) when non-NULL; run_head: compute logits + greedy ids (+ top-16 when want_top16);
+ *   memory) when non-NULL; run_head 1: compute logits + greedy ids (+ top-16 when want_top16);
+ *   run_head 2: only the pre-head residual rows (the head's hyper-connection fold, no logits), the
+ *   input of wzy_stage_mtp_front during prefill;
  *   save_snaps: write per-row snapshots (at snap_offset + t) of GDN / indexer state for
  *   commit_window_state.  Asynchronous: results are valid after wzy_stage_sync().
  * Replaces StageGpu::record_forward (src/wzy_stage_v2.cuh:476-857). */
@@ -123,6 +125,40 @@ int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const voi
 /* Bytes [offset, offset + bytes) of a tensor, device to host (synchronous). */
 int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset, void* host,
                                 size_t bytes);
+
+/* ---- MTP speculative drafter (MtpEngine, src/wzy_mtp.cuh:405-754) ----
+ * One extra decoder layer (attention over its own 1,024-cell INT8 KV ring, MoE of n_exp Q2_0
+ * experts + a Q8_0 shared expert, hyper-connections) and a Q8_0 draft head over n_dvocab rows of
+ * the main vocabulary.  Cell p embeds the token at p+1 and reads the main model's pre-head
+ * residual at p; it proposes the token at p+2.
+ *
+ * wzy_stage_mtp_init: allocate and random-initialise the drafter from `seed` (the reference loads
+ *   dense.txt/dense.bin, experts.bin and the draft vocabulary, MtpEngine::init, :459-645); the
+ *   draft head is the Q8_0 quantisation of main LM-head rows dvocab[i] = i*n_vocab/n_dvocab.
+ * wzy_stage_mtp_reset: empty the KV ring and its floor (MtpEngine::reset_kv, :647-656).
+ * wzy_stage_mtp_set_floor: first cell the ring attention may read (d_kv_floor, set by
+ *   seed_mtp_tail, src/wzy_engine_v2.cu:1266-1290).
+ * wzy_stage_mtp_front: K/V append of cells cell0 .. cell0+n_cells-1 (n_cells <= 8), embedding
+ *   next_toks[i] with pre-head residual row src_row0+i of the last forward (which must have run
+ *   with run_head 1 or 2) (MtpEngine::run_front_kv, :658-683).  Asynchronous.
+ * wzy_stage_mtp_draft: `depth` chained draft steps (1..8): the first at `cell` embedding `tok`
+ *   with pre-head row src_row of the last forward (src_row < 0: the residual the previous draft
+ *   step left), each further step at the next cell embedding the previous draft.  Writes the
+ *   drafted token ids and their top-1 probabilities 1/sum(exp(l - max)) (synchronous)
+ *   (run_front_kv + run_rest_row0 + head reduction, :658-733,293-403; the chain of mtp_propose,
+ *   src/wzy_engine_v2.cu:1428-1470, without its confidence gates, which the caller applies).
+ * wzy_stage_mtp_propose: catch-up + chain of mtp_propose (src/wzy_engine_v2.cu:1384-1427): the
+ *   front over cells cell0 .. cell0+n_cells-2 (rows 0 .. n_cells-2 of the last forward), then
+ *   wzy_stage_mtp_draft at cell0+n_cells-1 with row n_cells-1.
+ * Readable tensors (wzy_stage_read_tensor, layer -1): "mtp.*" weights and the "mtp.act.*"
+ * activations of the last step. */
+int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab);
+int wzy_stage_mtp_reset(wzy_stage* st);
+int wzy_stage_mtp_set_floor(wzy_stage* st, int kv_floor);
+int wzy_stage_mtp_front(wzy_stage* st, int cell0, const int* next_toks, int n_cells, int src_row0);
+int wzy_stage_mtp_draft(wzy_stage* st, int cell, int tok, int src_row, int depth, int* out_toks, float* out_probs);
+int wzy_stage_mtp_propose(wzy_stage* st, int cell0, int n_cells, const int* next_toks, int depth, int* out_toks,
+                          float* out_probs);
 
 /* Measurement support (no reference counterpart): time the NVFP4 expert kernels of every layer's
  * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the

@@ -41,6 +41,14 @@ int wzy_synth_expert_planes(uint64_t seed, int layer, int expert, int n_embd, in
 int wzy_synth_experts_device(uint64_t seed, int layer, int first_expert, int n_experts, int n_embd,
                              int n_ff, uint8_t* dev, void* stream);
 
+/* MTP Q2_0 expert blob bytes: 3*D*F/4 code bytes + 3*D*F/64 fp16 scales (src/wzy_mtp.cuh:6-10). */
+size_t wzy_q2_expert_bytes(int n_embd, int n_ff);
+/* One MTP Q2_0 expert: uniform 2-bit codes, fp16 scales (1 + m/1024) * 2^e with uniform 10-bit m and
+ * e = floor(log2(1/sqrt(reduction dim))).  Host version and bulk device version (identical bytes). */
+int wzy_synth_q2_expert(uint64_t seed, int expert, int n_embd, int n_ff, uint8_t* blob);
+int wzy_synth_q2_experts_device(uint64_t seed, int first_expert, int n_experts, int n_embd, int n_ff, uint8_t* dev,
+                                void* stream);
+
 /* Synthetic INT8 KV cells [n_cells x kvd] codes uniform over [-127,127] and fp16 scales per 64
  * elements, for positions first_pos.. (host / device versions, identical bytes). */
 void wzy_synth_kv_host(uint64_t seed, int layer, int is_v, int64_t first_pos, int n_cells, int kvd,

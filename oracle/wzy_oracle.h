@@ -174,6 +174,53 @@ typedef struct orc_trace {
 int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                             float* pre_head, const orc_trace* tr);
 
+/* ---- MTP drafter (src/wzy_mtp.cuh) ---- */
+/* Q2_0 expert blob size: 3*D*F/4 code bytes + 3*D*F/64 fp16 scales (src/wzy_mtp.cuh:6-10) */
+size_t orc_q2_blob_bytes(int D, int F);
+int orc_q2_code(const uint8_t* codes, int k);
+/* per-32 activations in, per-32 SwiGLU activations out (src/wzy_mtp.cuh:85-158) */
+void orc_q2_expert_gate_up(const uint8_t* blob, int D, int F, const int8_t* xq32, const float* xs32, int8_t* aq32,
+                           float* as32, float* act_out);
+/* src/wzy_mtp.cuh:160-207 */
+void orc_q2_expert_down(const uint8_t* blob, int D, int F, const int8_t* aq32, const float* as32, float* out);
+
+typedef struct orc_mtp {
+    int n_embd, hc, hc_lr, qsa_qh, qsa_kvh, qsa_hd, n_rot, n_exp, top_k, n_ff, n_vocab, n_dv, ring;
+    float eps;
+    const uint16_t* emb;                        /* bf16 [n_vocab x D] (the main model's table) */
+    const float* pre_norm_emb;                  /* [D] */
+    const float* pre_norm_hid;                  /* [hc x D] */
+    const int8_t* fc_emb_q; const uint16_t* fc_emb_s;
+    const int8_t* fc_hid_q; const uint16_t* fc_hid_s;
+    /* hyper-connections: 0 attention, 1 MLP, 2 final mixer (no inject weight) */
+    const float* hc_norm[3];
+    const int8_t* hc_down_q[3]; const uint16_t* hc_down_s[3];
+    const int8_t* hc_up_q[3];   const uint16_t* hc_up_s[3];
+    const uint16_t* hc_inj[2];
+    const int8_t* wq_q; const uint16_t* wq_s; const int8_t* wk_q; const uint16_t* wk_s;
+    const int8_t* wv_q; const uint16_t* wv_s; const int8_t* wo_q; const uint16_t* wo_s;
+    const float* q_norm; const float* k_norm;
+    const uint16_t* router; const uint16_t* sgate;
+    const int8_t* sh_gate_q; const uint16_t* sh_gate_s; const int8_t* sh_up_q; const uint16_t* sh_up_s;
+    const int8_t* sh_down_q; const uint16_t* sh_down_s;
+    const uint8_t* experts;                     /* n_exp Q2_0 blobs back to back */
+    const int8_t* head_q; const uint16_t* head_s; /* Q8_0 draft head [n_dv x D] */
+    const int* dvocab;                          /* [n_dv] token ids (NULL = identity) */
+    const float* cos_tab; const float* sin_tab;
+    /* state, updated: INT8 KV ring [ring x kvd] with fp16 per-64 scales, attention floor */
+    int8_t* kq; uint16_t* ks; int8_t* vq; uint16_t* vs;
+    int kv_floor;
+} orc_mtp;
+
+/* K/V append of T cells pos..pos+T-1 (src/wzy_mtp.cuh:658-683).  toks [T] are the embedded tokens,
+ * Rin [T x hc x D] the residuals; R [T x hc x D], mixed [T x D], inj [T x hc] receive the front's
+ * outputs. */
+void orc_mtp_front(orc_mtp* m, int pos, const int* toks, const float* Rin, int T, float* R, float* mixed, float* inj);
+/* One chained draft step at cell pos (src/wzy_mtp.cuh:687-733): R_out [hc x D] is the next step's
+ * residual, sample [D] the draft head input, logits [n_dv]. */
+int orc_mtp_step(orc_mtp* m, int pos, int tok, const float* Rin, float* R_out, float* sample, float* logits,
+                 int* out_tok, float* out_prob);
+
 /* ---- logit reductions (src/wzy_kernels_v2.cuh:1873-1984) ---- */
 void orc_row_argmax(const float* logits, int nvocab, int T, int* out);
 void orc_row_top16(const float* logits, int nvocab, int T, int* greedy, float* top_v, int* top_i);

@@ -42,6 +42,12 @@ _SIGS = {
     "orc_attend": (None, [P, P, P, P, P, P, I32, I32, I32, I32, P]),
     "orc_row_argmax": (None, [P, I32, I32, P]),
     "orc_row_top16": (None, [P, I32, I32, P, P, P]),
+    "orc_q2_blob_bytes": (SZ, [I32, I32]),
+    "orc_q2_code": (I32, [P, I32]),
+    "orc_q2_expert_gate_up": (None, [P, I32, I32, P, P, P, P, P]),
+    "orc_q2_expert_down": (None, [P, I32, I32, P, P, P]),
+    "orc_mtp_front": (None, [P, I32, P, P, I32, P, P, P]),
+    "orc_mtp_step": (I32, [P, I32, I32, P, P, P, P, P, P]),
     "orc_cpu_pool_create": (P, [I32, I32, I32]),
     "orc_cpu_pool_destroy": (None, [P]),
     "orc_cpu_pool_threads": (I32, [P]),

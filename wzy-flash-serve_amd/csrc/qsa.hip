@@ -61,6 +61,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
     const int hd = dm.hd, kvd = dm.kvh * dm.hd;
 
     if (wg < dm.qh) {
+        if (!a.qg) return;
         for (int t = 0; t < T; ++t) {
             const int pos = base + t;
             if (pos < 0 || pos >= dm.ctx_max) continue;
@@ -107,6 +108,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
         }
         return;
     }
+    if (dm.window > 0) return;                      // no indexer in window mode
     // indexer append (one workgroup, thread d owns key dim d)
     const int D = dm.idim, B = dm.iblk, half = dm.n_rot / 2;
     const int d = tid;
@@ -247,6 +249,12 @@ int qsa_check_dims(const QsaDims& dm) {
     WZY_REQUIRE(dm.idim <= 128 && dm.idim % 8 == 0 && dm.ih <= 4 && dm.iblk >= 2, "qsa: indexer layout unsupported");
     WZY_REQUIRE(dm.n_rot % 2 == 0 && dm.n_rot <= dm.idim && dm.n_rot <= dm.hd, "qsa: bad n_rot");
     WZY_REQUIRE(dm.topk >= 1 && dm.ctx_max >= 1, "qsa: bad topk/ctx");
+    if (dm.window > 0) {
+        // a sliding window reads only the last `window` cells, so its ring may wrap
+        WZY_REQUIRE(dm.ih == 0 && dm.sinks == 0 && dm.topk == dm.window && dm.window <= dm.ring_cap,
+                    "qsa: window mode needs no indexer, no sinks, topk == window <= kv ring");
+        return WZY_OK;
+    }
     return qsa_check_ring(dm.ctx_max, dm.ring_cap, dm.sinks);
 }
 
@@ -266,7 +274,7 @@ int qsa_check_ring(int ctx_max, int ring_cap, int sinks) {
 int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
     WZY_TRY(qsa_check_dims(a.dm));
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_prep: T out of range");
-    const int n_wg = a.dm.qh + a.dm.kvh + a.dm.ih + 1;
+    const int n_wg = a.dm.qh + a.dm.kvh + a.dm.ih + (a.dm.window > 0 ? 0 : 1);
     hipLaunchKernelGGL(qsa_prep_kernel, dim3(n_wg), dim3(256), 0, st, a, T);
     WZY_LAUNCH_CHECK();
     return WZY_OK;

@@ -463,7 +463,8 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int kvd = dm.kvh * 256;
     const int n_kv = *a.pos + t + 1;
-    const int width = min(n_kv, dm.topk);
+    int p0, width;
+    qsa_span(dm, n_kv, a.floor, p0, width);
     const int c0 = c * QSA_ATT_CHUNK;
     if (c0 >= width) return;                         // workgroup-uniform
     const int ncell = min(QSA_ATT_CHUNK, width - c0);
@@ -472,7 +473,10 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     if (tid < QSA_ATT_CHUNK) {
         const int idx = c0 + tid;
         long long sl = -1;
-        if (tid < ncell) sl = (long long) qsa_kv_slot(n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx], dm);
+        if (tid < ncell) {
+            const int p = dm.window > 0 ? p0 + idx : (n_kv <= dm.topk ? idx : a.sel_ids[(size_t) t * dm.topk + idx]);
+            sl = (long long) qsa_kv_slot(p, dm);
+        }
         s_slot[tid] = sl;
     }
     {                                                // this slice's heads; rows past gq are zero
@@ -580,9 +584,14 @@ __global__ void __launch_bounds__(256) qsa_combine_kernel(QsaAttnArgs a) {
     const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x, lane = d & 63;
     const int gq = dm.qh / dm.kvh, j = h / gq, hh = h % gq;
     const int n_kv = *a.pos + t + 1;
-    const int width = min(n_kv, dm.topk);
+    int p0, width;
+    qsa_span(dm, n_kv, a.floor, p0, width);
     const int nch_all = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
     const int nch = (width + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    if (nch == 0) {                                  // nothing attended (a floor above the row)
+        a.out[(size_t) t * dm.qh * 256 + (size_t) h * 256 + d] = 0.f;
+        return;
+    }
     const size_t base = ((size_t) t * dm.kvh + j) * nch_all;
     // chunk statistics: lane c holds chunk c
     const float m_c = lane < nch ? a.part_ml[((base + lane) * gq + hh) * 2] : -INFINITY;

@@ -11,6 +11,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <iterator>
 #include <map>
 #include <memory>
 #include <string>
@@ -23,6 +24,7 @@
 #include "wzy_hc.h"
 #include "wzy_host.h"
 #include "wzy_moe.h"
+#include "wzy_mtp.h"
 #include "wzy_qsa.h"
 #include "wzy_reduce.h"
 #include "wzy_synth_impl.h"
@@ -139,8 +141,10 @@ struct wzy_stage {
     float* d_top_v = nullptr;
     int* d_top_i = nullptr;
     int last_T = 0;
-    bool have_head = false;
+    bool have_head = false;         // last forward ran the LM head (logits, greedy ids)
+    bool have_pre_head = false;     // last forward left its pre-head residual rows in R[r_pre_head]
     bool loaded = false;
+    MtpState* mtp = nullptr;        // MTP drafter (wzy_stage_mtp_init)
 
     std::map<unsigned long long, hipGraphExec_t> graph_execs;
 
@@ -167,11 +171,13 @@ struct wzy_stage {
     }
     int alloc_q8(Q8& m, int rows, int cols, int layer, const char* name);
     int init_buffers();
-    int enqueue(int T, bool emb_host, bool run_head, bool save_snaps, bool want_top16, int snap_offset);
+    int enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool want_top16, int snap_offset);
 };
 
 wzy_stage::~wzy_stage() {
     (void) hipSetDevice(dev);
+    if (stream) (void) hipStreamSynchronize(stream);
+    delete mtp;
     for (auto& kv : graph_execs)
         if (kv.second) (void) hipGraphExecDestroy(kv.second);
     for (void* p : allocs) (void) hipFree(p);
@@ -413,7 +419,7 @@ int wzy_stage::init_buffers() {
 // ------------------------------------------------------------------------------------------------
 // forward enqueue
 // ------------------------------------------------------------------------------------------------
-int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, bool want_top16, int snap_offset) {
+int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool want_top16, int snap_offset) {
     const wzy_stage_cfg& c = cfg;
     hipStream_t st = stream;
     const int* d_pos = d_step;
@@ -540,6 +546,7 @@ int wzy_stage::enqueue(int T, bool emb_host, bool run_head, bool save_snaps, boo
     if (run_head) {
         WZY_TRY(hc_read(head_norm, head_down, nullptr, head_up, nullptr, false));
         r_pre_head = cur;
+        if (run_head == 2) return WZY_OK;          // pre-head residual only (MTP seeding)
         GemvSegs h;
         h.n = 1;
         h.seg[0] = GemvSeg{head, nullptr, logits, c.n_vocab, GEMV_BF16, c.n_vocab, 0};
@@ -739,12 +746,14 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
     WZY_HIP_TRY(hipEventRecord(st->step_ev[slot], st->stream));
     st->step_pending[slot] = true;
     if (emb) WZY_HIP_TRY(hipMemcpyAsync(st->emb_rows, emb, (size_t) T * st->D * 4, hipMemcpyHostToDevice, st->stream));
+    WZY_REQUIRE(run_head >= 0 && run_head <= 2, "record_forward: run_head must be 0, 1 or 2");
     st->last_T = T;
-    st->have_head = run_head != 0;
+    st->have_head = run_head == 1;
+    st->have_pre_head = run_head != 0;
     const bool use_graph = st->graphs && !st->profiling && !st->trace;
     if (!use_graph) return st->enqueue(T, emb != nullptr, run_head, save_snaps, want_top16, snap_offset);
     const unsigned long long key = ((unsigned long long) T << 16) | ((unsigned long long) snap_offset << 8) |
-                                   (emb ? 16ull : 0ull) | (run_head ? 4ull : 0ull) | (want_top16 ? 2ull : 0ull) |
+                                   (emb ? 16ull : 0ull) | ((unsigned long long) run_head << 2) | (want_top16 ? 2ull : 0ull) |
                                    (save_snaps ? 1ull : 0ull);
     auto it = st->graph_execs.find(key);
     if (it == st->graph_execs.end()) {
@@ -870,7 +879,7 @@ extern "C" int wzy_stage_logits(wzy_stage* st, float* out, int T) {
     return WZY_OK;
 }
 extern "C" int wzy_stage_pre_head(wzy_stage* st, float* out, int T) {
-    WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_head, "pre_head: no head output");
+    WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_pre_head, "pre_head: no pre-head output");
     WZY_HIP_TRY(hipMemcpy(out, st->R[st->r_pre_head], (size_t) T * st->HCD * 4, hipMemcpyDeviceToHost));
     return WZY_OK;
 }
@@ -878,7 +887,96 @@ extern "C" int wzy_stage_pre_head(wzy_stage* st, float* out, int T) {
 extern "C" int wzy_stage_set_graphs(wzy_stage* st, int enable) {
     WZY_REQUIRE(st, "set_graphs: null stage");
     st->graphs = enable != 0;
+    if (st->mtp) st->mtp->graphs = st->graphs;
     return WZY_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// MTP drafter
+// ------------------------------------------------------------------------------------------------
+extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
+    WZY_REQUIRE(st && st->loaded, "mtp_init: stage not loaded");
+    WZY_REQUIRE(!st->mtp, "mtp_init: the drafter is already initialised");
+    const wzy_stage_cfg& c = st->cfg;
+    WZY_REQUIRE(n_dvocab >= 1 && n_dvocab <= c.n_vocab, "mtp_init: n_dvocab must be in [1, %d]", c.n_vocab);
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    std::unique_ptr<MtpState> m(new MtpState);
+    m->reg = [st](const char* n, void* p, size_t b) { st->reg(-1, n, p, b); };
+    MtpDims d{};
+    d.D = c.n_embd; d.HC = c.hc; d.HCLR = c.hc_lr;
+    d.qh = c.qsa_qh; d.kvh = c.qsa_kvh; d.hd = c.qsa_hd; d.n_rot = c.n_rot;
+    d.E = c.n_exp; d.K = c.top_k; d.F = c.n_ff;
+    d.n_vocab = c.n_vocab; d.n_dv = n_dvocab; d.ctx_max = c.ctx_max; d.eps = c.eps;
+    int rc = m->init(d, st->stream, st->emb, st->cos_tab, st->sin_tab);
+    if (rc == WZY_OK) rc = m->load_synthetic(seed, st->head);
+    if (rc != WZY_OK) {                 // the drafter's memory goes with m: drop its registry entries
+        for (auto it = st->tensors.begin(); it != st->tensors.end();)
+            it = it->first.second.rfind("mtp.", 0) == 0 ? st->tensors.erase(it) : std::next(it);
+        return rc;
+    }
+    m->graphs = st->graphs;
+    st->dev_bytes += m->dev_bytes;
+    st->mtp = m.release();
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_mtp_reset(wzy_stage* st) {
+    WZY_REQUIRE(st && st->mtp, "mtp_reset: no drafter");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    return st->mtp->reset_kv();
+}
+
+extern "C" int wzy_stage_mtp_set_floor(wzy_stage* st, int kv_floor) {
+    WZY_REQUIRE(st && st->mtp, "mtp_set_floor: no drafter");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    return st->mtp->set_floor(kv_floor);
+}
+
+// rows [src_row0, src_row0 + n) of the last forward's pre-head residual -> the drafter's input rows
+static int mtp_take_rows(wzy_stage* st, int src_row0, int n) {
+    WZY_REQUIRE(st->have_pre_head && src_row0 >= 0 && src_row0 + n <= st->last_T,
+                "mtp: rows [%d, %d) are not pre-head rows of the last forward (%d rows%s)", src_row0, src_row0 + n,
+                st->last_T, st->have_pre_head ? "" : ", run without the head");
+    WZY_HIP_TRY(hipMemcpyAsync(st->mtp->rin, st->R[st->r_pre_head] + (size_t) src_row0 * st->HCD,
+                               (size_t) n * st->HCD * 4, hipMemcpyDeviceToDevice, st->stream));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_mtp_front(wzy_stage* st, int cell0, const int* next_toks, int n_cells, int src_row0) {
+    WZY_REQUIRE(st && st->mtp, "mtp_front: no drafter");
+    WZY_REQUIRE(next_toks && n_cells >= 1 && n_cells <= WZY_MAX_W, "mtp_front: n_cells must be in [1, %d]", WZY_MAX_W);
+    WZY_REQUIRE(cell0 >= 0 && cell0 + n_cells <= st->cfg.ctx_max, "mtp_front: cells beyond ctx_max");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    WZY_TRY(mtp_take_rows(st, src_row0, n_cells));
+    WZY_TRY(st->mtp->set_ctl(cell0, next_toks, n_cells));
+    return st->mtp->enqueue_front(n_cells, false);
+}
+
+extern "C" int wzy_stage_mtp_draft(wzy_stage* st, int cell, int tok, int src_row, int depth, int* out_toks,
+                                   float* out_probs) {
+    WZY_REQUIRE(st && st->mtp, "mtp_draft: no drafter");
+    WZY_REQUIRE(depth >= 1 && depth <= MTP_MAX_CHAIN, "mtp_draft: depth must be in [1, %d]", MTP_MAX_CHAIN);
+    WZY_REQUIRE(cell >= 0 && cell + depth <= st->cfg.ctx_max, "mtp_draft: cells beyond ctx_max");
+    WZY_REQUIRE(out_toks && out_probs, "mtp_draft: null output");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    if (src_row >= 0) WZY_TRY(mtp_take_rows(st, src_row, 1));
+    WZY_TRY(st->mtp->set_ctl(cell, &tok, 1));
+    WZY_TRY(st->mtp->enqueue_steps(depth));
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    memcpy(out_toks, st->mtp->h_tok, (size_t) depth * sizeof(int));
+    memcpy(out_probs, st->mtp->h_prob, (size_t) depth * sizeof(float));
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_mtp_propose(wzy_stage* st, int cell0, int n_cells, const int* next_toks, int depth,
+                                     int* out_toks, float* out_probs) {
+    WZY_REQUIRE(st && st->mtp, "mtp_propose: no drafter");
+    WZY_REQUIRE(next_toks && n_cells >= 1 && n_cells <= WZY_MAX_W, "mtp_propose: n_cells must be in [1, %d]",
+                WZY_MAX_W);
+    if (n_cells > 1) WZY_TRY(wzy_stage_mtp_front(st, cell0, next_toks, n_cells - 1, 0));
+    return wzy_stage_mtp_draft(st, cell0 + n_cells - 1, next_toks[n_cells - 1], n_cells - 1, depth, out_toks,
+                               out_probs);
 }
 extern "C" void* wzy_stage_stream(wzy_stage* st) { return st ? (void*) st->stream : nullptr; }
 

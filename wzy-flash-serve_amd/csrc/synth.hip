@@ -289,6 +289,52 @@ extern "C" int wzy_synth_experts_device(uint64_t seed, int layer, int first_expe
 }
 
 // ---------------------------------------------------------------------------------------------
+// MTP Q2_0 experts
+// ---------------------------------------------------------------------------------------------
+extern "C" size_t wzy_q2_expert_bytes(int n_embd, int n_ff) {
+    return (size_t) 3 * n_embd * n_ff / 4 + (size_t) 3 * n_embd * n_ff / 64 * 2;
+}
+
+// byte `i` of a Q2_0 blob of (D, F)
+WZY_HD uint8_t q2_blob_byte(uint64_t seed, int expert, int D, int F, size_t i) {
+    const size_t n_gu_c = (size_t) 2 * F * (D / 4), n_dn_c = (size_t) D * (F / 4), n_gu_s = (size_t) 2 * F * (D / 64);
+    if (i < n_gu_c) return wzy_q2_code_byte(seed, expert, 0, i);
+    if (i < n_gu_c + n_dn_c) return wzy_q2_code_byte(seed, expert, 1, i - n_gu_c);
+    size_t j = i - n_gu_c - n_dn_c;
+    const int part = j < n_gu_s * 2 ? 2 : 3;
+    if (part == 3) j -= n_gu_s * 2;
+    const uint16_t h = wzy_q2_scale_h16(seed, expert, part, j >> 1, wzy_q2_scale_exp(part == 2 ? D : F));
+    return (uint8_t) (h >> (8 * (j & 1)));
+}
+
+extern "C" int wzy_synth_q2_expert(uint64_t seed, int expert, int n_embd, int n_ff, uint8_t* blob) {
+    WZY_REQUIRE(blob && n_embd % 64 == 0 && n_ff % 64 == 0, "wzy_synth_q2_expert: bad arguments");
+    const size_t n = wzy_q2_expert_bytes(n_embd, n_ff);
+    for (size_t i = 0; i < n; ++i) blob[i] = q2_blob_byte(seed, expert, n_embd, n_ff, i);
+    return WZY_OK;
+}
+
+__global__ void synth_q2_kernel(uint64_t seed, int first_expert, int D, int F, size_t rec, uint8_t* __restrict__ dev) {
+    const int e = blockIdx.y;
+    uint8_t* out = dev + (size_t) e * rec;
+    for (size_t w = (size_t) blockIdx.x * blockDim.x + threadIdx.x; w < rec / 8; w += (size_t) gridDim.x * blockDim.x) {
+        uint64_t q = 0;
+        for (int k = 0; k < 8; ++k) q |= (uint64_t) q2_blob_byte(seed, first_expert + e, D, F, w * 8 + k) << (8 * k);
+        *(uint64_t*) (out + w * 8) = q;
+    }
+}
+
+extern "C" int wzy_synth_q2_experts_device(uint64_t seed, int first_expert, int n_experts, int n_embd, int n_ff,
+                                           uint8_t* dev, void* stream) {
+    WZY_REQUIRE(dev && n_experts > 0 && n_experts <= 65535, "wzy_synth_q2_experts_device: bad arguments");
+    WZY_REQUIRE(n_embd % 64 == 0 && n_ff % 64 == 0, "wzy_synth_q2_experts_device: dims must be multiples of 64");
+    hipLaunchKernelGGL(synth_q2_kernel, dim3(256, n_experts), dim3(256), 0, as_stream(stream), seed, first_expert,
+                       n_embd, n_ff, wzy_q2_expert_bytes(n_embd, n_ff), dev);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
 // INT8 KV cells
 // ---------------------------------------------------------------------------------------------
 extern "C" void wzy_synth_kv_host(uint64_t seed, int layer, int is_v, int64_t first_pos, int n_cells, int kvd,

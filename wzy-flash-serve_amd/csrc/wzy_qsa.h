@@ -13,7 +13,23 @@ struct QsaDims {
     int ctx_max;                       // capacity of the KV store / indexer
     int ring_cap, sinks;               // 0 = full-context store addressed by position
     float eps;
+    int window = 0;                    // > 0: dense sliding-window attention over the last `window`
+                                       // cells (no indexer; the ring may wrap, window <= ring_cap)
 };
+
+// Attended span of a row whose context holds n_kv cells: positions p0 .. p0 + width - 1.  Sparse
+// mode: the first min(n_kv, topk) entries (all cells when n_kv <= topk, else the selected ids);
+// window mode: max(floor, n_kv - window) .. n_kv - 1.
+__device__ __forceinline__ void qsa_span(const QsaDims& dm, int n_kv, const int* floor, int& p0, int& width) {
+    if (dm.window > 0) {
+        p0 = max(n_kv - dm.window, 0);
+        if (floor) p0 = max(p0, *floor);
+        width = max(n_kv - p0, 0);
+    } else {
+        p0 = 0;
+        width = min(n_kv, dm.topk);
+    }
+}
 
 // Storage slot of context position p: the position itself for a full-context store; with a ring,
 // positions below `sinks` are pinned and the rest cycle through the remaining ring_cap - sinks slots.
@@ -50,7 +66,8 @@ struct QsaIdx {
 struct QsaPrepArgs {
     QsaDims dm;
     const int* pos;                    // device: base position of row 0
-    float* qg;                         // [T][qh*2*hd] q|gate per head (q normalised+roped in place)
+    float* qg;                         // [T][qh*2*hd] q|gate per head (q normalised+roped in place;
+                                       // null: k/v only)
     float* kk;                         // [T][kvh*hd] (normalised+roped in place)
     const float* vv;                   // [T][kvh*hd]
     float* q_idx;                      // [T][ih*idim] (normalised+roped in place)
@@ -80,7 +97,8 @@ struct QsaAttnArgs {
     const int* pos;
     const float* qg;                   // [T][qh*2*hd]
     QsaKv kv;
-    const int* sel_ids;                // [T][topk]
+    const int* sel_ids;                // [T][topk] (sparse mode)
+    const int* floor = nullptr;        // window mode: device lower bound of the attended positions
     float* part;                       // [T][kvh][nch][gq][hd] partial outputs
     float* part_ml;                    // [T][kvh][nch][gq][2] (max, sum)
     float* out;                        // [T][qh*hd]

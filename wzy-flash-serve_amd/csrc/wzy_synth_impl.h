@@ -30,6 +30,8 @@ enum {
     WZY_S_DENSE = 5,      // sub = tensor id (see wzy_synth.h)
     WZY_S_STATE = 6,
     WZY_S_INPUT = 7,
+    WZY_S_Q2 = 8,         // MTP Q2_0 experts: sub = expert*4 + part (0 gate/up codes, 1 down codes,
+                          // 2 gate/up scales, 3 down scales)
 };
 WZY_HD uint64_t wzy_stream(uint32_t kind, uint32_t layer, uint32_t sub) {
     return ((uint64_t) kind << 48) | ((uint64_t) (layer & 0xFFFFu) << 32) | (uint64_t) sub;
@@ -84,4 +86,25 @@ WZY_HD uint16_t wzy_kv_scale_h16(uint64_t seed, int layer, int is_v, int64_t pos
     const uint32_t v = 512u + u10;                                    // [512, 1536)
     if (v < 1024u) return (uint16_t) ((8u << 10) | ((v - 512u) << 1));          // (1 + (v-512)/512) * 2^-7
     return (uint16_t) ((9u << 10) | (v - 1024u));                               // (1 + (v-1024)/1024) * 2^-6
+}
+
+// ---- MTP Q2_0 experts (blob layout: gate/up codes [2F][D/4], down codes [D][F/4], gate/up fp16
+// scales [2F][D/64], down fp16 scales [D][F/64]) ----
+// Code byte `lin` of part 0 (gate/up) or 1 (down): four uniform 2-bit codes, 8 bytes per hash.
+WZY_HD uint8_t wzy_q2_code_byte(uint64_t seed, int expert, int part, uint64_t lin) {
+    const uint64_t h = wzy_hash3(seed, wzy_stream(WZY_S_Q2, 0, (uint32_t) (expert * 4 + part)), lin >> 3);
+    return (uint8_t) (h >> (8 * (lin & 7)));
+}
+// fp16 bits of scale `lin` of part 2 (gate/up, reduction dim D) or 3 (down, reduction dim F):
+// (1 + m/1024) * 2^e with a uniform 10-bit m and e = floor(log2(1/sqrt(cols))) passed as `e`, so the
+// dequantised weights (code - 1) * scale have a standard deviation near 1/sqrt(cols).
+WZY_HD uint16_t wzy_q2_scale_h16(uint64_t seed, int expert, int part, uint64_t lin, int e) {
+    const uint64_t h = wzy_hash3(seed, wzy_stream(WZY_S_Q2, 0, (uint32_t) (expert * 4 + part)), lin);
+    return (uint16_t) (((uint32_t) (e + 15) << 10) | (uint32_t) (h >> 54));
+}
+// floor(log2(1/sqrt(cols))) for cols a power of two times 1 or 2 (exact integer arithmetic)
+WZY_HD int wzy_q2_scale_exp(int cols) {
+    int l = 0;
+    while ((1 << (l + 1)) <= cols) ++l;     // l = floor(log2(cols))
+    return -((l + 1) / 2);                  // -ceil(l/2): 2048 (l=11) -> -6, 512 (l=9) -> -5
 }

@@ -133,6 +133,12 @@ _SIGS = {
     "wzy_stage_read_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_write_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32)], True),
+    "wzy_stage_mtp_init": (I32, [P, U64, I32], True),
+    "wzy_stage_mtp_reset": (I32, [P], True),
+    "wzy_stage_mtp_set_floor": (I32, [P, I32], True),
+    "wzy_stage_mtp_front": (I32, [P, I32, P, I32, I32], True),
+    "wzy_stage_mtp_draft": (I32, [P, I32, I32, I32, I32, P, P], True),
+    "wzy_stage_mtp_propose": (I32, [P, I32, I32, P, I32, P, P], True),
     # layer kernels
     "wzy_hc_read_workspace_bytes": (SZ, [I32, I32, I32], False),
     "wzy_hc_read": (I32, [P, P, P, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, SZ, P], True),
@@ -175,6 +181,9 @@ _SIGS = {
     "wzy_synth_normal_bf16": (None, [U64, U64, SZ, F32, F32, P], False),
     "wzy_synth_q8": (None, [U64, U64, I32, I32, F32, P, P], False),
     "wzy_synth_expert_blob": (I32, [U64, I32, I32, I32, I32, P], True),
+    "wzy_q2_expert_bytes": (SZ, [I32, I32], False),
+    "wzy_synth_q2_expert": (I32, [U64, I32, I32, I32, P], True),
+    "wzy_synth_q2_experts_device": (I32, [U64, I32, I32, I32, I32, P, P], True),
     "wzy_synth_expert_planes": (I32, [U64, I32, I32, I32, I32, P], True),
     "wzy_synth_experts_device": (I32, [U64, I32, I32, I32, I32, I32, P, P], True),
     "wzy_synth_kv_host": (None, [U64, I32, I32, I64, I32, I32, P, P], False),
@@ -379,6 +388,39 @@ class Stage:
         import numpy as np
         a = np.ascontiguousarray(arr)
         self.lib.wzy_stage_write_tensor(self.h, layer, name.encode(), a.ctypes.data, a.nbytes)
+
+    # ---- MTP drafter ----
+    def mtp_init(self, seed, n_dvocab):
+        self.lib.wzy_stage_mtp_init(self.h, int(seed), int(n_dvocab))
+
+    def mtp_reset(self):
+        self.lib.wzy_stage_mtp_reset(self.h)
+
+    def mtp_set_floor(self, floor):
+        self.lib.wzy_stage_mtp_set_floor(self.h, int(floor))
+
+    def mtp_front(self, cell0, next_toks, src_row0=0):
+        import numpy as np
+        t = np.ascontiguousarray(next_toks, dtype=np.int32)
+        self.lib.wzy_stage_mtp_front(self.h, int(cell0), t.ctypes.data, len(t), int(src_row0))
+
+    def mtp_draft(self, cell, tok, src_row, depth):
+        """-> (token ids [depth], probabilities [depth])"""
+        import numpy as np
+        toks = np.empty(depth, np.int32)
+        probs = np.empty(depth, np.float32)
+        self.lib.wzy_stage_mtp_draft(self.h, int(cell), int(tok), int(src_row), int(depth), toks.ctypes.data,
+                                     probs.ctypes.data)
+        return toks, probs
+
+    def mtp_propose(self, cell0, next_toks, depth):
+        import numpy as np
+        t = np.ascontiguousarray(next_toks, dtype=np.int32)
+        toks = np.empty(depth, np.int32)
+        probs = np.empty(depth, np.float32)
+        self.lib.wzy_stage_mtp_propose(self.h, int(cell0), len(t), t.ctypes.data, int(depth), toks.ctypes.data,
+                                       probs.ctypes.data)
+        return toks, probs
 
 
 def default_cfg(ctx_max):
