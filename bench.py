@@ -16,7 +16,11 @@ Beside the tok/s line it reports
                 bounded ~10 s sample;
   prefill_moe   BASELINE config 5's chunked-prefill MoE block (8,192 tokens, one layer) on MFMA:
                 per-launch-group HIP event times, routed-expert TFLOP/s against the 2.5 PFLOP/s
-                dense bf16 MFMA peak.
+                dense bf16 MFMA peak;
+  mtp_config5   BASELINE config 5's decode half: the MTP drafter at a fixed depth of 3 with T=4 verify
+                windows on the same stage (tok/s, acceptance, per-window split, and one draft step's
+                HBM bytes / event-timed duration against 8 TB/s);
+  gdn_config2, qsa_262k   BASELINE configs 2 and 3 at their own workloads.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
@@ -207,6 +211,104 @@ def qsa_262k(wz, seed=2, iters=50):
     return out
 
 
+def mtp_step_bytes(cfg, n_dv, window):
+    """Algorithmic HBM bytes of one draft step: every drafter weight once (Q8_0 rows at 34 B per 32
+    values, bf16, the routed Q2_0 experts), the draft-head logits written and read once, and the ring
+    cells of the attention window (INT8 K and V with fp16 per-64 scales)."""
+    D, HC, L = cfg.n_embd, cfg.hc, cfg.hc_lr
+    QD, KVD, F, E, K = cfg.qsa_qh * cfg.qsa_hd, cfg.qsa_kvh * cfg.qsa_hd, cfg.n_ff, cfg.n_exp, cfg.top_k
+    q8 = lambda r, c: r * c * 34 // 32
+    b = 2 * q8(D, D) + q8(2 * QD, D) + 2 * q8(KVD, D) + q8(D, QD)
+    b += 3 * (q8(L, HC * D) + q8(HC * D, L)) + 2 * HC * HC * D * 2
+    b += E * D * 2 + D * 2 + 3 * q8(F, D)
+    b += K * (3 * D * F // 4 + 3 * D * F // 64 * 2)
+    b += q8(n_dv, D) + 2 * 4 * n_dv
+    b += window * 2 * (KVD + KVD // 64 * 2)
+    return b
+
+
+def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_cells=64, time_iters=64):
+    """BASELINE config 5's decode half on the loaded config-4 stage: the MTP drafter (512 Q2_0
+    experts, 114,452-row draft head) seeded on `seed_cells` prompt cells appended to the prefilled
+    context (attention floor at the first of them, as a long prompt's tail seeding does), then
+    `windows` speculative windows at a fixed depth of 3: catch-up + 3 chained drafts, one T = 4
+    verify forward, greedy rank-1 acceptance, commit of the accepted prefix."""
+    import numpy as np
+    t0 = time.perf_counter()
+    st.mtp_init(seed, n_dv)
+    t_init = time.perf_counter() - t0
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, cfg.n_vocab, seed_cells + 1)]
+    st.mtp_set_floor(pos0)
+    for p in range(0, seed_cells, 8):
+        st.forward(pos0 + p, prompt[p:p + 8], run_head=2)
+        st.mtp_front(pos0 + p, prompt[p + 1:p + 9], 0)
+    pos = pos0 + seed_cells
+    st.forward(pos, [prompt[-1]])
+    st.sync()
+    cur = int(st.greedy(1)[0])
+    unfed0, unfed = pos, [cur]
+    pos += 1
+    emitted = accepted = offered = 0
+    t_prop = t_win = 0.0
+
+    def window():
+        nonlocal cur, unfed0, unfed, pos, emitted, accepted, offered, t_prop, t_win
+        ta = time.perf_counter()
+        d, _ = st.mtp_propose(unfed0, unfed, depth)
+        tb = time.perf_counter()
+        win = [cur] + [int(x) for x in d]
+        st.forward(pos, win, save_snaps=True)
+        st.sync()
+        g = st.greedy(len(win))
+        n_acc = 0
+        while n_acc < depth and int(g[n_acc]) == win[n_acc + 1]:
+            n_acc += 1
+        acc_rows = 1 + n_acc
+        if acc_rows < len(win):
+            st.lib.wzy_stage_commit_window_state(st.h, acc_rows - 1, pos + acc_rows - 1)
+        t_prop += tb - ta
+        t_win += time.perf_counter() - tb
+        emitted += acc_rows
+        accepted += n_acc
+        offered += depth
+        unfed0, unfed = pos, win[1:acc_rows] + [int(g[n_acc])]
+        pos += acc_rows
+        cur = int(g[n_acc])
+
+    for _ in range(4):
+        window()
+    emitted = accepted = offered = 0
+    t_prop = t_win = 0.0
+    wz.wzy_device_sync()
+    t0 = time.perf_counter()
+    for _ in range(windows):
+        window()
+    wz.wzy_device_sync()
+    el = time.perf_counter() - t0
+    us = C.c_float(0)
+    wz.wzy_stage_mtp_time(st.h, pos, cur, -1, time_iters, C.byref(us))
+    nb = mtp_step_bytes(cfg, n_dv, min(pos - pos0, 1024))
+    acc = accepted / offered if offered else 0.0
+    # tokens per window for a per-draft acceptance a (rank-1, stop at the first rejection): 1+a+a^2+a^3
+    proj = {("a=%.1f" % a): round((1 + a + a * a + a ** 3) / (el / windows), 1) for a in (0.5, 0.7, 0.9)}
+    return {"workload": "config 5 decode: config-4 model + MTP drafter (512 Q2_0 experts top-10, shared expert, "
+                        "114,452-row Q8_0 draft head), fixed depth 3, T=4 verify windows, greedy rank-1 acceptance, "
+                        "%d seeded prompt cells after a %d-cell prefilled context" % (seed_cells, pos0),
+            "windows": windows, "tok_s": round(emitted / el, 2), "ms_per_window": round(1000 * el / windows, 4),
+            "tokens_per_window": round(emitted / windows, 4), "acceptance": round(acc, 4),
+            "drafts_offered": offered, "drafts_accepted": accepted,
+            "ms_propose": round(1000 * t_prop / windows, 4), "ms_verify_window": round(1000 * t_win / windows, 4),
+            "mtp_step": {"us": round(us.value, 3), "bytes": nb, "achieved_gbs": round(nb / (us.value * 1e-6) / 1e9, 1),
+                         "frac": round(nb / (us.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "timed_steps": time_iters},
+            "init_s": round(t_init, 2),
+            "tok_s_at_acceptance": proj,
+            "note": ("the synthetic drafter is random-initialised, so its drafts match the random main model's "
+                     "greedy tokens about 1 time in 10^5 and measured acceptance is ~0; tok_s is the cost of "
+                     "offering 3 drafts per window.  tok_s_at_acceptance is the measured window time with "
+                     "1+a+a^2+a^3 tokens per window (a projection, not a measurement).")}
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -323,6 +425,7 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=8192, help="config-5 prefill MoE chunk (0: skip)")
     ap.add_argument("--prefill-iters", type=int, default=5)
     ap.add_argument("--no-configs23", action="store_true", help="skip the config-2 GDN and config-3 QSA legs")
+    ap.add_argument("--mtp-windows", type=int, default=64, help="config-5 speculative windows (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, 3 device-to-device copies of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
@@ -340,7 +443,7 @@ def main():
         sys.exit(1)
     wz.wzy_dev_set(0)
 
-    ctx_max = args.n_ctx + args.warmup + args.steps + 64
+    ctx_max = args.n_ctx + args.warmup + args.steps + 64 + 8 * (args.mtp_windows + 4) + 64 + 64 + 128
     cfg = wzy_amd.default_cfg(ctx_max)
     t0 = time.perf_counter()
     st = wzy_amd.Stage(cfg)
@@ -386,6 +489,11 @@ def main():
         pf = prefill_moe(wz, st, args.prefill_tokens, args.prefill_iters, args.seed)
         print("bench: prefill MoE %d tokens: %.1f us" % (args.prefill_tokens, pf["us_total"]), file=sys.stderr,
               flush=True)
+    mtp5 = None
+    if args.mtp_windows > 0:
+        mtp5 = mtp_config5(wz, st, cfg, pos, args.mtp_windows)
+        print("bench: config 5 MTP depth 3: %.1f tok/s, %.3f ms per window, step %.1f us" % (
+            mtp5["tok_s"], mtp5["ms_per_window"], mtp5["mtp_step"]["us"]), file=sys.stderr, flush=True)
     st.close()
 
     gdn2 = qsa3 = None
@@ -449,6 +557,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "prefill_moe": pf,
+        "mtp_config5": mtp5,
         "gdn_config2": gdn2,
         "qsa_262k": qsa3,
         "greedy_tokens_head": toks[:8],

@@ -89,6 +89,23 @@ int wzy_engine_verify_top16(const float* top_v, const int* top_i, const wzy_gen_
  * prefix of ids[0 .. n_ids-2], else 0 (src/wzy_engine_v2.cu:1963-1970). */
 int wzy_engine_reuse_prefix(const int* state, int n_state, const int* ids, int n_ids);
 
+/* Tunables of the drafter's confidence gates (the reference reads them from WZY_SPEC_DEPTH,
+ * WZY_SPEC_MIN_P and WZY_SPEC_GATE, src/wzy_engine_v2.cu:1436-1450). */
+typedef struct wzy_spec_gates {
+    int depth;                   /* chain length cap (5) */
+    float min_p;                 /* first-draft probability floor (0.30, lowered by spec_min_p) */
+    float gate;                  /* scale of the deeper explore / keep / cumulative gates (1.0) */
+} wzy_spec_gates;
+void wzy_engine_spec_gates_default(wzy_spec_gates* g);
+
+/* The confidence gates of mtp_propose (src/wzy_engine_v2.cu:1428-1475) over a computed draft chain:
+ * toks / probs [n] are the chain's drafts and top-1 probabilities (step j at cell last_cell + j),
+ * next_tok the confirmed token the first step embedded.  Returns how many leading drafts are
+ * offered for verification (0 .. min(n, gates->depth, max_drafts)); gates NULL = defaults.  The
+ * chain needs min(gates->depth, max_drafts) steps for the answer to be the reference's. */
+int wzy_engine_mtp_gate(const int* toks, const float* probs, int n, int next_tok, int last_cell, int ctx_max,
+                        const wzy_gen_cfg* cfg, int max_drafts, const wzy_spec_gates* gates);
+
 /* Values printed in PREFILL / DONE lines. */
 typedef struct wzy_line_fields {
     int req;                     /* >= 0: multiplexed form with "req"; -1: single-stream form */

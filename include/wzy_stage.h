@@ -159,6 +159,10 @@ int wzy_stage_mtp_front(wzy_stage* st, int cell0, const int* next_toks, int n_ce
 int wzy_stage_mtp_draft(wzy_stage* st, int cell, int tok, int src_row, int depth, int* out_toks, float* out_probs);
 int wzy_stage_mtp_propose(wzy_stage* st, int cell0, int n_cells, const int* next_toks, int depth, int* out_toks,
                           float* out_probs);
+/* Measurement support (no reference counterpart): mean device time of one draft step over `iters`
+ * chained steps from `cell` (src_row as in wzy_stage_mtp_draft), bracketed by HIP events on the
+ * stage stream.  The steps write ring cells cell .. cell+iters. */
+int wzy_stage_mtp_time(wzy_stage* st, int cell, int tok, int src_row, int iters, float* us_per_step);
 
 /* Measurement support (no reference counterpart): time the NVFP4 expert kernels of every layer's
  * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the

@@ -296,3 +296,46 @@ def test_engine_binary_rejects_bad_options():
     for args in (["--cfg", "no_such_field=3"], ["--frobnicate"]):
         p = subprocess.run([ENGINE] + args, input="", capture_output=True, text=True, timeout=60)
         assert p.returncode == 2 and p.stdout == ""
+
+
+def _gate(wz, toks, probs, next_tok=-5, last_cell=100, ctx_max=10000, max_drafts=7, spec_min_p=0.72, stops=(),
+          depth=5, min_p=0.30, gate=1.0):
+    c = cfg(wz, spec_min_p=spec_min_p)
+    c.n_stops = len(stops)
+    for i, s in enumerate(stops):
+        c.stops[i] = s
+    t = np.array(toks, np.int32)
+    p = np.array(probs, np.float32)
+    g = wzy_amd.SpecGates(depth, min_p, gate)
+    return wz.wzy_engine_mtp_gate(t.ctypes.data, p.ctypes.data, len(t), next_tok, last_cell, ctx_max, C.byref(c),
+                                  max_drafts, C.byref(g))
+
+
+def test_mtp_gates_follow_mtp_propose(wz):
+    """mtp_propose's gates (src/wzy_engine_v2.cu:1428-1475) on hand-built chains."""
+    hi = [0.9] * 7
+    assert _gate(wz, [1, 2, 3, 4, 5, 6, 7], hi) == 5                   # chain cap WZY_SPEC_DEPTH = 5
+    assert _gate(wz, [1, 2, 3, 4, 5, 6, 7], hi, max_drafts=3) == 3
+    assert _gate(wz, [1, 2, 3, 4, 5, 6, 7], hi, depth=7) == 7
+    assert _gate(wz, [1, 2, 3], [0.29, 0.9, 0.9]) == 0                  # first draft below 0.30
+    assert _gate(wz, [1, 2, 3], [0.29, 0.9, 0.9], min_p=0.2) == 1       # then the j=1 explore gate (0.34)
+    assert _gate(wz, [1, 2, 3], [0.25, 0.9, 0.9], spec_min_p=0.2) == 2  # a low spec_min_p lowers the gates;
+                                                                        # the cumulative one (0.24) stops j=2
+    assert _gate(wz, [7, 2, 3], [0.84, 0.9, 0.9], next_tok=7) == 0      # repeats the confirmed token, p < 0.85
+    assert _gate(wz, [7, 2, 3], [0.86, 0.9, 0.9], next_tok=7) == 3
+    assert _gate(wz, [1, 1, 3], hi) == 1                                # a draft equal to the previous one
+    assert _gate(wz, [1, 2, 1, 4], hi) == 2                             # a draft equal to the one two back
+    assert _gate(wz, [1, 2, 9, 4], hi, stops=(9,)) == 2                 # a stop id ends the chain
+    assert _gate(wz, [9, 2], hi, stops=(9,)) == 0
+    # explore gate of step j on the previous draft's probability: j=1 0.34, j=2 0.46, j=3 0.65, j=4 0.78
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.9, 0.9, 0.9, 0.64, 0.9]) == 4
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.9, 0.45, 0.9, 0.9, 0.9]) == 2
+    # keep gate of step j on its own probability: j=1 0.36, j=2 0.48, j=3 0.62, j=4 0.74
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.9, 0.35, 0.9, 0.9, 0.9]) == 1
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.9, 0.9, 0.9, 0.9, 0.73]) == 4
+    # cumulative gate: j=2 0.24, j=3 0.36, j=4 0.48
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.5, 0.47, 0.9, 0.9, 0.9]) == 2  # cum 0.235 < 0.24 at j=2
+    # WZY_SPEC_GATE scales the deeper gates
+    assert _gate(wz, [1, 2, 3, 4, 5], [0.9, 0.9, 0.9, 0.64, 0.9], gate=0.5) == 5
+    # the context end stops the chain (last_cell + j >= ctx_max - 4)
+    assert _gate(wz, [1, 2, 3, 4, 5], hi, last_cell=100, ctx_max=106) == 2

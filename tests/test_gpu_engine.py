@@ -320,3 +320,39 @@ def test_engine_sigusr1_cancels(wz, gpu):
         assert eng.line() == "PONG"
     finally:
         assert eng.close() == 0
+
+
+def test_engine_mtp_speculative_decoding_is_lossless(wz, gpu):
+    """With the MTP drafter (fixed depth 3, and the reference's confidence gates) the greedy stream is
+    the plain engine's, token for token: drafts are verified in one T = W window with rank-1
+    acceptance and a rejected suffix's state is discarded (commit_window_state).  The prompt's cells
+    seed the drafter's ring during prefill (run_head 2 windows + fronts)."""
+    print("case engine_mtp", flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    prompt = [int(t) for t in np.random.default_rng(6).integers(0, cfg.n_vocab, 29)]
+    streams = {}
+    for name, args in (("plain", []), ("fixed3", ["--spec-depth", "3"]), ("gated", ["--mtp"])):
+        eng = EngineProc(cfg, *args, env={"WZY_MTP_DVOCAB": "800"})
+        try:
+            assert eng.ready["mtp"] == (name != "plain")
+            pf, toks, done = eng.request(greedy_req(prompt, 24, no_reuse=1))
+            streams[name] = (toks, done)
+            # a follow-up prompt that extends the state reuses it, drafter ring included
+            _, toks2, done2 = eng.request(greedy_req(prompt + toks[:-1] + [5], 9))
+            streams[name + "_reuse"] = (toks2, done2)
+        finally:
+            assert eng.close() == 0
+    base = streams["plain"][0]
+    for name in ("fixed3", "gated"):
+        toks, done = streams[name]
+        assert toks == base, "%s stream %s vs plain %s" % (name, toks, base)
+        assert streams[name + "_reuse"][0] == streams["plain_reuse"][0]
+        assert done["generated"] == 24 and done["draft_accepted"] <= done["draft_n"]
+    # fixed depth: every window but the last offers 3 drafts (none is a stop id here)
+    d = streams["fixed3"][1]
+    wins = d["generated"] - 1 - d["draft_accepted"]
+    assert d["draft_n"] >= 3 * (wins - 1), d
+    assert streams["plain"][1]["draft_n"] == 0
+    print("mtp engine: fixed3 drafts %d accepted %d; gated drafts %d accepted %d" % (
+        d["draft_n"], d["draft_accepted"], streams["gated"][1]["draft_n"], streams["gated"][1]["draft_accepted"]),
+        flush=True)

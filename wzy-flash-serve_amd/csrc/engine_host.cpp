@@ -350,6 +350,54 @@ extern "C" int wzy_engine_reuse_prefix(const int* state, int n_state, const int*
     return m == n_state ? m : 0;
 }
 
+extern "C" int wzy_engine_mtp_gate(const int* toks, const float* probs, int n, int next_tok, int last_cell,
+                                   int ctx_max, const wzy_gen_cfg* cfg, int max_drafts,
+                                   const wzy_spec_gates* gates) {
+    if (!toks || !probs || !cfg || n < 1 || max_drafts < 1) return 0;
+    wzy_spec_gates g;
+    if (gates) g = *gates;
+    else wzy_engine_spec_gates_default(&g);
+    auto is_stop = [&](int id) {
+        for (int i = 0; i < cfg->n_stops && i < WZY_MAX_STOPS; ++i)
+            if (cfg->stops[i] == id) return true;
+        return false;
+    };
+    int d_tok = toks[0];
+    float d_prob = probs[0];
+    if (is_stop(d_tok)) return 0;
+    if (d_prob < std::min(g.min_p, cfg->spec_min_p)) return 0;
+    if (d_tok == next_tok && d_prob < 0.85f) return 0;
+    int kept = 1;
+    float cum = d_prob;
+    const int cap = std::min(g.depth, std::max(1, max_drafts));
+    const float smp = cfg->spec_min_p;
+    for (int j = 1; j < cap && j < n; ++j) {
+        const float explore_p = ((j == 1) ? std::min(0.34f, smp) : (j == 2) ? std::min(0.46f, smp)
+                                 : (j == 3) ? 0.65f : 0.78f) * g.gate;
+        const float min_cum = ((j <= 1) ? 0.0f : (j == 2) ? 0.24f : (j == 3) ? 0.36f : 0.48f) * g.gate;
+        if (d_prob < explore_p || cum < min_cum) break;
+        if (last_cell + j >= ctx_max - 4) break;
+        const int prev_d = d_tok;
+        d_tok = toks[j];
+        d_prob = probs[j];
+        if (is_stop(d_tok) || d_tok == prev_d) break;
+        if (kept >= 2 && d_tok == toks[kept - 2]) break;
+        const float keep_p = ((j == 1) ? std::min(0.36f, smp) : (j == 2) ? std::min(0.48f, smp)
+                              : (j == 3) ? 0.62f : 0.74f) * g.gate;
+        if (d_prob < keep_p) break;
+        ++kept;
+        cum *= d_prob;
+    }
+    return kept;
+}
+
+extern "C" void wzy_engine_spec_gates_default(wzy_spec_gates* g) {
+    if (!g) return;
+    g->depth = 5;
+    g->min_p = 0.30f;
+    g->gate = 1.0f;
+}
+
 extern "C" int wzy_engine_format(int what, const wzy_line_fields* f, char* buf, int cap) {
     if (!f || !buf || cap <= 0) return WZY_EINVAL;
     int n = -1;

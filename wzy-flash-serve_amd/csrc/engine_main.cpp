@@ -14,6 +14,11 @@
 //   --cfg k=v,...  / WZY_CFG          overrides of wzy_stage_cfg fields (e.g. n_layers=4,n_embd=256)
 //   --device D     / WZY_DEVICE       HIP device (default 0)
 //   --no-graphs    / WZY_GRAPHS=0     launch kernels one by one instead of replaying hipGraphs
+//   --mtp          / WZY_MTP=1        MTP speculative decoding: the drafter proposes up to `spec` tokens
+//                                     per window under the reference's confidence gates
+//                                     (WZY_SPEC_DEPTH, WZY_SPEC_MIN_P, WZY_SPEC_GATE, WZY_ADAPT_DEPTH)
+//   --spec-depth K / WZY_SPEC_FIXED=K every window offers exactly K drafts (no confidence gates)
+//   WZY_MTP_DVOCAB=N                  draft-vocabulary rows (default min(114452, n_vocab))
 //   WZY_DEC_PROF=1                    per-request decode profile line on stderr
 // Exit status: 0 after QUIT/EXIT or end of input, 1 on any stage error (message on stderr), 2 on
 // bad options.
@@ -84,6 +89,11 @@ struct Options {
     int device = 0;
     bool graphs = true;
     bool prof = false;
+    bool mtp = false;
+    int spec_fixed = 0;           // > 0: fixed draft depth
+    int mtp_dvocab = 114452;
+    wzy_spec_gates gates{5, 0.30f, 1.0f};
+    bool adapt_depth = true;
 };
 
 // "k=v,k=v" onto wzy_stage_cfg by field name.
@@ -137,6 +147,13 @@ int parse_options(int argc, char** argv, Options& o) {
     if (const char* e = getenv("WZY_DEVICE")) o.device = atoi(e);
     if (const char* e = getenv("WZY_GRAPHS")) o.graphs = atoi(e) != 0;
     if (const char* e = getenv("WZY_DEC_PROF")) o.prof = atoi(e) != 0;
+    if (const char* e = getenv("WZY_MTP")) o.mtp = atoi(e) != 0;
+    if (const char* e = getenv("WZY_SPEC_FIXED")) o.spec_fixed = atoi(e);
+    if (const char* e = getenv("WZY_MTP_DVOCAB")) o.mtp_dvocab = atoi(e);
+    if (const char* e = getenv("WZY_SPEC_DEPTH")) o.gates.depth = atoi(e);
+    if (const char* e = getenv("WZY_SPEC_MIN_P")) o.gates.min_p = (float) atof(e);
+    if (const char* e = getenv("WZY_SPEC_GATE")) o.gates.gate = (float) atof(e);
+    if (const char* e = getenv("WZY_ADAPT_DEPTH")) o.adapt_depth = atoi(e) != 0;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto val = [&]() -> const char* {
@@ -153,11 +170,16 @@ int parse_options(int argc, char** argv, Options& o) {
         else if (a == "--cfg") o.cfg = val();
         else if (a == "--device") o.device = atoi(val());
         else if (a == "--no-graphs") o.graphs = false;
+        else if (a == "--mtp") o.mtp = true;
+        else if (a == "--spec-depth") o.spec_fixed = atoi(val()), o.mtp = true;
         else {
             fprintf(stderr, "[wzy-engine] unknown option %s\n", a.c_str());
             return 2;
         }
     }
+    if (o.spec_fixed > 0) o.mtp = true;
+    o.spec_fixed = std::min(o.spec_fixed, WZY_MAX_W - 1);
+    o.gates.depth = std::max(1, std::min(o.gates.depth, WZY_MAX_W - 1));
     return 0;
 }
 
@@ -202,16 +224,34 @@ class Engine {
             state_.clear();
         }
         const auto t_pf0 = Clock::now();
+        // Prompt cells in windows of up to WZY_MAX_W rows.  With the drafter, windows that reach the
+        // last kMtpSeedTail cells also leave their pre-head residuals, which seed the drafter's ring
+        // (seed_mtp_tail, src/wzy_engine_v2.cu:1266-1290).
+        const int tail_floor = std::max(0, n - 1 - kMtpSeedTail);
+        if (o_.mtp && reused == 0) check(wzy_stage_mtp_reset(st_), "mtp_reset");
         for (int p = reused; p < n - 1; p += WZY_MAX_W) {
             const int T = std::min(WZY_MAX_W, n - 1 - p);
-            check(wzy_stage_record_forward(st_, p, nullptr, &ids[p], T, 0, 0, 0, 0), "record_forward(prefill)");
+            const bool seed = o_.mtp && p + T > tail_floor;
+            check(wzy_stage_record_forward(st_, p, nullptr, &ids[p], T, seed ? 2 : 0, 0, 0, 0), "record_forward(prefill)");
+            if (seed) {
+                const int sub0 = std::max(0, tail_floor - p);
+                if (p + sub0 == tail_floor && tail_floor > 0) check(wzy_stage_mtp_set_floor(st_, tail_floor), "mtp_floor");
+                check(wzy_stage_mtp_front(st_, p + sub0, &ids[p + sub0 + 1], T - sub0, sub0), "mtp_front");
+            }
         }
         state_.insert(state_.end(), ids.begin() + reused, ids.end() - 1);
 
         const bool no_rep = fabsf(g.rep_pen - 1.0f) < 1e-5f;
         mode_ = (no_rep && g.temp <= 1e-5f) ? kGreedy : (no_rep && g.top_k > 0 && g.top_k <= 16) ? kTop16 : kFull;
         std::vector<int> hist(ids);
-        int cur = forward_and_pick(ids[n - 1], n - 1, g, hist);
+        int cur = 0;
+        {
+            const int last = ids[n - 1];
+            check(wzy_stage_record_forward(st_, n - 1, nullptr, &last, 1, 1, 0, mode_ == kTop16, 0), "record_forward");
+            check(wzy_stage_sync(st_), "sync");
+            read_rows(1);
+            pick_row(0, -1, g, hist, &cur);
+        }
         state_.push_back(ids[n - 1]);
         const double pf_ms = ms_since(t_pf0);
 
@@ -223,16 +263,29 @@ class Engine {
         if (r.json) emit_fmt(WZY_FMT_PREFILL, f);
         else say("output :");
 
+        // Decode loop (src/wzy_engine_v2.cu:2119-2205): emit the current token, let the drafter
+        // propose, verify the window [cur, drafts...] in one forward with rank-1 acceptance, keep the
+        // state of the accepted prefix.  Without the drafter every window is the single row [cur].
         const auto t_dec0 = Clock::now();
-        int generated = 0, pos = n;
+        int generated = 0, cur_pos = n, wins = 0;
         const char* finish = "length";
-        double fwd_ms = 0.0;
+        double fwd_ms = 0.0, mtp_ms = 0.0;
+        float acc_ema = 0.5f;
+        long long drafts_offered = 0, drafts_accepted = 0;
+        int unfed_cell0 = n - 1;                      // drafter catch-up: cells whose next token is known
+        std::vector<int> unfed_next{cur};
+        std::vector<int> drafts, win;
         auto is_stop = [&](int t) {
             for (int i = 0; i < g.n_stops; ++i)
                 if (g.stops[i] == t) return true;
             return false;
         };
-        while (generated < g.max_new && pos < c_.ctx_max - 8) {
+        auto emit = [&](int t) {
+            if (!r.json) say(" %d", t);
+            else if (req >= 0) say("TOK %d %d\n", req, t);
+            else say("TOK %d\n", t);
+        };
+        while (generated < g.max_new && cur_pos < c_.ctx_max - 8) {
             if (cancelled(req)) {
                 finish = "cancelled";
                 break;
@@ -243,27 +296,80 @@ class Engine {
             }
             ++generated;
             hist.push_back(cur);
-            if (!r.json) say(" %d", cur);
-            else if (req >= 0) say("TOK %d %d\n", req, cur);
-            else say("TOK %d\n", cur);
-            if (generated >= g.max_new || pos >= c_.ctx_max - 8) {
+            emit(cur);
+            if (generated >= g.max_new || cur_pos >= c_.ctx_max - 8) {
                 finish = "length";
                 break;
             }
-            const auto t_f = Clock::now();
-            const int next = forward_and_pick(cur, pos, g, hist);
-            fwd_ms += ms_since(t_f);
-            state_.push_back(cur);
-            if (is_stop(next)) {
-                finish = "stop";
-                break;
+            drafts.clear();
+            if (o_.mtp) {
+                int want_k = std::min(o_.spec_fixed > 0 ? o_.spec_fixed : std::min(g.spec_k, WZY_MAX_W - 1),
+                                      g.max_new - generated);
+                if (o_.spec_fixed <= 0 && o_.adapt_depth && want_k > 2) {
+                    if (acc_ema < 0.35f) want_k = 2;
+                    else if (acc_ema < 0.55f) want_k = std::min(want_k, 3);
+                }
+                const auto t_m = Clock::now();
+                propose(unfed_cell0, unfed_next, want_k, g, drafts);
+                mtp_ms += ms_since(t_m);
             }
+            drafts_offered += (long long) drafts.size();
+            win.assign(1, cur);
+            win.insert(win.end(), drafts.begin(), drafts.end());
+            const int W = (int) win.size();
+            const auto t_f = Clock::now();
+            check(wzy_stage_record_forward(st_, cur_pos, nullptr, win.data(), W, 1, W > 1 ? 1 : 0, mode_ == kTop16, 0),
+                  "record_forward");
+            check(wzy_stage_sync(st_), "sync");
+            read_rows(W);
+            fwd_ms += ms_since(t_f);
+            ++wins;
+            int n_acc = 0, bonus = 0;
+            bool hit_stop = false;
+            for (int j = 0; j < W; ++j) {
+                const int d_cand = (j + 1 < W) ? win[j + 1] : -1;
+                int sampled = 0;
+                const bool ok = pick_row(j, d_cand, g, hist, &sampled);
+                if (j + 1 < W && ok) {
+                    if (is_stop(sampled)) {
+                        hit_stop = true;
+                        finish = "stop";
+                        break;
+                    }
+                    ++n_acc;
+                    ++drafts_accepted;
+                    ++generated;
+                    hist.push_back(sampled);
+                    emit(sampled);
+                    if (generated >= g.max_new) {
+                        bonus = sampled;
+                        break;
+                    }
+                } else {
+                    bonus = sampled;
+                    if (is_stop(bonus)) {
+                        hit_stop = true;
+                        finish = "stop";
+                    }
+                    break;
+                }
+            }
+            const int acc_rows = std::min(W, 1 + n_acc);
+            if (!drafts.empty()) acc_ema = 0.7f * acc_ema + 0.3f * (float) n_acc / (float) drafts.size();
+            // all rows accepted: the state after the last row is already in place
+            if (W > 1 && acc_rows < W)
+                check(wzy_stage_commit_window_state(st_, acc_rows - 1, cur_pos + acc_rows - 1), "commit_window_state");
+            state_.insert(state_.end(), win.begin(), win.begin() + acc_rows);
+            if (hit_stop || generated >= g.max_new) break;
             if (cancelled(req)) {
                 finish = "cancelled";
                 break;
             }
-            ++pos;
-            cur = next;
+            unfed_cell0 = cur_pos;
+            unfed_next.assign(win.begin() + 1, win.begin() + acc_rows);
+            unfed_next.push_back(bonus);
+            cur_pos += acc_rows;
+            cur = bonus;
         }
         if (in_.quit.load() && o_.batch) return;   // QUIT in multiplexed mode ends the process without DONE
         {
@@ -272,15 +378,19 @@ class Engine {
         }
         const double dec_ms = ms_since(t_dec0);
         if (o_.prof)
-            fprintf(stderr, "[DEC-PROF gen=%d wins=%d (1.00 tok/win)] total=%.1fms (%.2f ms/win) | stage=%.2fms\n",
-                    generated, std::max(generated - 1, 0), dec_ms, generated > 1 ? dec_ms / (generated - 1) : 0.0,
-                    fwd_ms);
+            fprintf(stderr,
+                    "[DEC-PROF gen=%d wins=%d (%.2f tok/win)] total=%.1fms (%.2f ms/win) | stage=%.2fms mtp=%.2fms "
+                    "drafts=%lld accepted=%lld\n",
+                    generated, wins, wins > 0 ? (double) (generated - 1) / wins : 0.0, dec_ms,
+                    wins > 0 ? dec_ms / wins : 0.0, fwd_ms, mtp_ms, drafts_offered, drafts_accepted);
         if (!r.json) {
             say("\nEND\n");
             return;
         }
         f.generated = generated;
         f.decode_ms = dec_ms;
+        f.draft_n = drafts_offered;
+        f.draft_accepted = drafts_accepted;
         f.active_tokens = (int) state_.size();
         f.finish = finish;
         emit_fmt(WZY_FMT_DONE, f);
@@ -288,6 +398,7 @@ class Engine {
 
     void reset() {
         check(wzy_stage_reset_state(st_), "reset_state");
+        if (o_.mtp) check(wzy_stage_mtp_reset(st_), "mtp_reset");
         check(wzy_stage_sync(st_), "sync");
         state_.clear();
     }
@@ -295,27 +406,68 @@ class Engine {
   private:
     enum Mode { kGreedy, kTop16, kFull };
 
-    // Forward one window row at `pos` with the head and pick the next token (no draft to verify).
-    int forward_and_pick(int tok, int pos, const wzy_gen_cfg& g, const std::vector<int>& hist) {
-        check(wzy_stage_record_forward(st_, pos, nullptr, &tok, 1, 1, 0, mode_ == kTop16, 0), "record_forward");
-        check(wzy_stage_sync(st_), "sync");
-        int out = 0;
+    static constexpr int kMtpSeedTail = 512;   // prompt cells seeded into the drafter (src/wzy_mtp.cuh:12)
+
+    // Head outputs of the W rows of the last forward, as the selection mode needs them.
+    void read_rows(int W) {
+        if (mode_ == kGreedy) check(wzy_stage_greedy_ids(st_, greedy_, W), "greedy_ids");
+        else if (mode_ == kTop16) check(wzy_stage_top16(st_, top_v_, top_i_, W), "top16");
+        else check(wzy_stage_logits(st_, logits_.data(), W), "logits");
+    }
+
+    // Select row j's token and verify `draft` against it (-1: nothing to verify).  Rank-1
+    // acceptance: the draft is kept when it is the token this row selects.
+    bool pick_row(int j, int draft, const wzy_gen_cfg& g, const std::vector<int>& hist, int* out) {
         if (mode_ == kGreedy) {
-            check(wzy_stage_greedy_ids(st_, &out, 1), "greedy_ids");
-            return out;
+            *out = greedy_[j];
+            return draft >= 0 && draft == *out;
         }
         const float u = std::uniform_real_distribution<float>(0.f, 1.f)(rng_);
-        if (mode_ == kTop16) {
-            float v[16];
-            int id[16];
-            check(wzy_stage_top16(st_, v, id, 1), "top16");
-            check(wzy_engine_verify_top16(v, id, &g, hist.data(), (int) hist.size(), -1, u, &out), "sample");
-        } else {
-            check(wzy_stage_logits(st_, logits_.data(), 1), "logits");
-            check(wzy_engine_verify_full(logits_.data(), c_.n_vocab, &g, hist.data(), (int) hist.size(), -1, u, &out),
-                  "sample");
+        int acc = 0;
+        if (mode_ == kTop16)
+            acc = wzy_engine_verify_top16(top_v_ + 16 * j, top_i_ + 16 * j, &g, hist.data(), (int) hist.size(), draft,
+                                          u, out);
+        else
+            acc = wzy_engine_verify_full(logits_.data() + (size_t) j * c_.n_vocab, c_.n_vocab, &g, hist.data(),
+                                         (int) hist.size(), draft, u, out);
+        check(acc, "sample");
+        return acc == 1;
+    }
+
+    // mtp_propose (src/wzy_engine_v2.cu:1384-1475): catch the drafter up on the cells whose next
+    // token became known, draft from the last of them, keep the drafts the confidence gates pass.
+    // The chain runs on the device without host round trips; the gates, which only truncate it,
+    // are applied to its outputs (first step alone, the rest only when the first passes).
+    void propose(int cell0, const std::vector<int>& next, int want_k, const wzy_gen_cfg& g, std::vector<int>& drafts) {
+        drafts.clear();
+        const int n_cells = (int) next.size();
+        if (want_k <= 0 || n_cells <= 0) return;
+        const int last_cell = cell0 + n_cells - 1;
+        if (n_cells > 1) check(wzy_stage_mtp_front(st_, cell0, next.data(), n_cells - 1, 0), "mtp_front");
+        int toks[WZY_MAX_W + 1];
+        float probs[WZY_MAX_W + 1];
+        const int room = c_.ctx_max - 4 - last_cell;       // steps at cells last_cell .. ctx_max - 5
+        if (o_.spec_fixed > 0) {
+            const int depth = std::min(want_k, room);
+            if (depth < 1) return;
+            check(wzy_stage_mtp_draft(st_, last_cell, next.back(), n_cells - 1, depth, toks, probs), "mtp_draft");
+            for (int j = 0; j < depth; ++j) {
+                bool stop = false;
+                for (int i = 0; i < g.n_stops; ++i) stop |= g.stops[i] == toks[j];
+                if (stop) break;
+                drafts.push_back(toks[j]);
+            }
+            return;
         }
-        return out;
+        if (room < 1) return;
+        check(wzy_stage_mtp_draft(st_, last_cell, next.back(), n_cells - 1, 1, toks, probs), "mtp_draft");
+        if (wzy_engine_mtp_gate(toks, probs, 1, next.back(), last_cell, c_.ctx_max, &g, want_k, &o_.gates) < 1) return;
+        const int more = std::min(std::min(o_.gates.depth, want_k) - 1, room - 1);
+        if (more > 0)
+            check(wzy_stage_mtp_draft(st_, last_cell + 1, toks[0], -1, more, toks + 1, probs + 1), "mtp_draft");
+        const int kept = wzy_engine_mtp_gate(toks, probs, 1 + std::max(more, 0), next.back(), last_cell, c_.ctx_max, &g,
+                                             want_k, &o_.gates);
+        drafts.assign(toks, toks + kept);
     }
 
     bool cancelled(int req) {
@@ -351,6 +503,9 @@ class Engine {
     Mode mode_ = kGreedy;
     std::vector<int> state_;      // tokens whose cells the resident state holds
     std::vector<float> logits_;
+    int greedy_[WZY_MAX_W] = {};
+    float top_v_[WZY_MAX_W * 16] = {};
+    int top_i_[WZY_MAX_W * 16] = {};
 };
 
 // stdin reader: in multiplexed mode PING, CANCEL and QUIT are answered / recorded immediately (the
@@ -419,19 +574,23 @@ int main(int argc, char** argv) {
     wzy_stage* st = nullptr;
     check(wzy_stage_create(&c, o.device, &st), "stage_create");
     check(wzy_stage_load_synthetic(st, o.model_seed, 0), "load_synthetic");
+    if (o.mtp) {
+        const int n_dv = std::max(1, std::min(o.mtp_dvocab, c.n_vocab));
+        check(wzy_stage_mtp_init(st, o.model_seed + 1, n_dv), "mtp_init");
+    }
     check(wzy_stage_set_graphs(st, o.graphs ? 1 : 0), "set_graphs");
     check(wzy_stage_sync(st), "sync");
     signal(SIGUSR1, on_sigusr1);
 
     const double boot_s = ms_since(t_boot0) / 1000.0;
     if (o.batch)
-        say("READY {\"engine\":\"wzy-mi355x-batch\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":false,"
+        say("READY {\"engine\":\"wzy-mi355x-batch\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":%s,"
             "\"ctx_max\":%d,\"boot_s\":%.2f,\"sessions\":1}\n",
-            c.n_layers, c.n_layers * c.n_exp, c.ctx_max, boot_s);
+            c.n_layers, c.n_layers * c.n_exp, o.mtp ? "true" : "false", c.ctx_max, boot_s);
     else
-        say("READY {\"engine\":\"wzy-mi355x\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":false,"
+        say("READY {\"engine\":\"wzy-mi355x\",\"gpus\":1,\"split\":%d,\"vram_slots\":%d,\"mtp\":%s,"
             "\"ctx_max\":%d,\"boot_s\":%.2f}\n",
-            c.n_layers, c.n_layers * c.n_exp, c.ctx_max, boot_s);
+            c.n_layers, c.n_layers * c.n_exp, o.mtp ? "true" : "false", c.ctx_max, boot_s);
 
     Inbox in;
     Engine eng(o, st, c, in);

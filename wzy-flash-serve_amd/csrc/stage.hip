@@ -11,6 +11,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <iterator>
 #include <map>
 #include <memory>
@@ -967,6 +968,31 @@ extern "C" int wzy_stage_mtp_draft(wzy_stage* st, int cell, int tok, int src_row
     memcpy(out_toks, st->mtp->h_tok, (size_t) depth * sizeof(int));
     memcpy(out_probs, st->mtp->h_prob, (size_t) depth * sizeof(float));
     return WZY_OK;
+}
+
+extern "C" int wzy_stage_mtp_time(wzy_stage* st, int cell, int tok, int src_row, int iters, float* us_per_step) {
+    WZY_REQUIRE(st && st->mtp && us_per_step, "mtp_time: no drafter");
+    WZY_REQUIRE(iters >= 1 && iters <= 4096 && cell >= 0 && cell + iters + 1 <= st->cfg.ctx_max,
+                "mtp_time: iters must be in [1, 4096] with every cell below ctx_max");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    if (src_row >= 0) WZY_TRY(mtp_take_rows(st, src_row, 1));
+    WZY_TRY(st->mtp->set_ctl(cell, &tok, 1));
+    WZY_TRY(st->mtp->enqueue_steps(1));          // warm-up (and graph instantiation)
+    hipEvent_t a = nullptr, b = nullptr;
+    WZY_HIP_TRY(hipEventCreate(&a));
+    int rc = hipEventCreate(&b) == hipSuccess ? WZY_OK : WZY_EHIP;
+    if (rc == WZY_OK && hipEventRecord(a, st->stream) != hipSuccess) rc = WZY_EHIP;
+    for (int done = 0; rc == WZY_OK && done < iters; done += MTP_MAX_CHAIN)
+        rc = st->mtp->enqueue_steps(std::min(MTP_MAX_CHAIN, iters - done));
+    if (rc == WZY_OK && hipEventRecord(b, st->stream) != hipSuccess) rc = WZY_EHIP;
+    float ms = 0.f;
+    if (rc == WZY_OK && (hipEventSynchronize(b) != hipSuccess || hipEventElapsedTime(&ms, a, b) != hipSuccess))
+        rc = WZY_EHIP;
+    (void) hipEventDestroy(a);
+    if (b) (void) hipEventDestroy(b);
+    if (rc == WZY_EHIP) set_error("mtp_time: HIP event failure");
+    if (rc == WZY_OK) *us_per_step = 1000.0f * ms / (float) iters;
+    return rc;
 }
 
 extern "C" int wzy_stage_mtp_propose(wzy_stage* st, int cell0, int n_cells, const int* next_toks, int depth,

@@ -81,6 +81,11 @@ class GenCfg(C.Structure):
                 ("n_stops", I32), ("stops", I32 * WZY_MAX_STOPS)]
 
 
+class SpecGates(C.Structure):
+    """struct wzy_spec_gates (include/wzy_engine.h)"""
+    _fields_ = [("depth", I32), ("min_p", F32), ("gate", F32)]
+
+
 class Request(C.Structure):
     """struct wzy_request (include/wzy_engine.h)"""
     _fields_ = [("json", I32), ("has_req", I32), ("req", I32), ("n_ids", I32), ("cfg", GenCfg),
@@ -108,6 +113,8 @@ _SIGS = {
     "wzy_engine_verify_full": (I32, [P, I32, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
     "wzy_engine_verify_top16": (I32, [P, P, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
     "wzy_engine_reuse_prefix": (I32, [P, I32, P, I32], False),
+    "wzy_engine_spec_gates_default": (None, [C.POINTER(SpecGates)], False),
+    "wzy_engine_mtp_gate": (I32, [P, P, I32, I32, I32, I32, C.POINTER(GenCfg), I32, C.POINTER(SpecGates)], False),
     "wzy_engine_format": (I32, [I32, C.POINTER(LineFields), C.c_char_p, I32], False),
     # stage
     "wzy_stage_cfg_default": (None, [C.POINTER(StageCfg), I32], False),
@@ -139,6 +146,7 @@ _SIGS = {
     "wzy_stage_mtp_front": (I32, [P, I32, P, I32, I32], True),
     "wzy_stage_mtp_draft": (I32, [P, I32, I32, I32, I32, P, P], True),
     "wzy_stage_mtp_propose": (I32, [P, I32, I32, P, I32, P, P], True),
+    "wzy_stage_mtp_time": (I32, [P, I32, I32, I32, I32, C.POINTER(F32)], True),
     # layer kernels
     "wzy_hc_read_workspace_bytes": (SZ, [I32, I32, I32], False),
     "wzy_hc_read": (I32, [P, P, P, I32, P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, SZ, P], True),
