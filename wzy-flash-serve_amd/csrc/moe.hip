@@ -1,12 +1,13 @@
 // moe.hip -- NVFP4 mixture-of-experts decode block for gfx950.
 //
 // Launch sequence of wzy_moe_block (T window rows, K routed experts per row), three launches:
-//   1. gemv_segs    router logits [T x E] (bf16) + the shared-expert gate scalar row
-//   2. moe_gate_up  routed workgroup (group, 16-row tile): prefetches the logits, stages x
-//                   quantised per 16 in LDS, routes the window in LDS (softmax top-K, weights,
-//                   groups: each distinct expert of the window once, with its (row, slot) members,
-//                   so its weights stream from HBM once), then runs the gate+up NVFP4 GEMV, SwiGLU
-//                   and the per-16 int8 requant of its 16 rows; workgroup 0 publishes the routing.
+//   1. moe_router   router logits [T x E] (bf16, one row per wave) + the shared-expert gate scalar
+//                   row; the last workgroup to finish routes the window once (softmax top-K,
+//                   weights, groups: each distinct expert of the window once, with its (row, slot)
+//                   members, so its weights stream from HBM once) and publishes the tables.
+//   2. moe_gate_up  routed workgroup (group, 32-row tile): reads its group's expert and issues the
+//                   weight loads at entry, stages its member rows of x quantised per 16 in LDS
+//                   meanwhile, then the gate+up NVFP4 GEMV, SwiGLU and the per-16 int8 requant.
 //                   Shared workgroups run the Q8_0 shared expert on x quantised per 32.
 //   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, activations
 //                   staged in LDS, combine in LDS:
@@ -27,6 +28,14 @@ using namespace wzy;
 namespace {
 
 constexpr int DN_TILE = 8;    // output rows of one down workgroup
+
+struct MoeRtArgs {
+    const uint16_t* router; const uint16_t* sgate; const float* x;
+    int D, E, K;
+    float* logits; float* sg;
+    int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;
+    unsigned* arrive;
+};
 // work items whose loads a 16-lane slot issues together: a one-row window's 11 x 8 items fit in
 // one batch of 6 per slot, so every weight load of the workgroup is issued at once
 template <int T>
@@ -276,10 +285,9 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
 // scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
 // ---------------------------------------------------------------------------------------------
-template <int T, int RV>
+template <int T>
 __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ RouteLds r;
     __shared__ float s_act[WZY_MAX_W][32];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bid = blockIdx.x;
@@ -294,61 +302,18 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     float* s_sc = (float*) (s_qb + (size_t) T * nc);
 
     if (bid < a.n_routed_wg) {
-        float p[(T + 3) / 4][RV];
-        route_prefetch<T, RV>(a.logits, a.E, p);
-        // stage x quantised per 16, starting at wave 1 so that a one-row window stages on a wave that
-        // does not route.  The first item is loaded in straight-line code (a loop header would wait
-        // for the logits before requesting x); only windows of more than 256 blocks loop.
-        auto stage16 = [&](const float4 (&f4)[8], int i) {
-            float v[32];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                v[4 * k] = f4[k].x; v[4 * k + 1] = f4[k].y; v[4 * k + 2] = f4[k].z; v[4 * k + 3] = f4[k].w;
-            }
-            half2_t xp[16];
-            float da, db;
-            quant16_pairs(v, xp, da, db);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xp[4 * k]),
-                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 1]),
-                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 2]),
-                                                                   __builtin_bit_cast(uint32_t, xp[4 * k + 3]));
-            s_xs2[i] = make_float2(da, db);
-        };
-        const int tid0 = __builtin_amdgcn_readfirstlane(tid);
-        if (tid0 < 256 && ((tid0 + 192) & 255) < T * nc) {   // wave-uniform: a wave with no item skips
-            const int i = (tid + 192) & 255;
-            const int ic = min(i, T * nc - 1);
-            const int t = ic / nc, c = ic - t * nc;
-            float4 f4[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) f4[k] = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
-            if (i < T * nc) stage16(f4, i);
-        }
-        if (T > 1 && tid0 < 256) {
-            for (int i = ((tid + 192) & 255) + 256; i < T * nc; i += 256) {
-                const int t = i / nc, c = i - t * nc;
-                float4 f4[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) f4[k] = ((const float4*) (a.x + (size_t) t * D + (size_t) c * 32))[k];
-                stage16(f4, i);
-            }
-        }
-        route_compute<T, RV>(p, a.E, K, r);
         const int tiles = F / 32;
         const int g = bid / tiles, jt = bid - g * tiles;
-        if (g >= r.n_groups) return;                     // workgroup-uniform (workgroup 0 has g = 0)
-        const int e = __builtin_amdgcn_readfirstlane(r.gexp[g]), cnt = r.gcnt[g];
+        // routing tables published by moe_router: group g's expert, member count and entries
+        const int ng = *a.n_groups;
+        const int e = __builtin_amdgcn_readfirstlane(a.grp_exp[g]);
+        if (g >= ng) return;                             // workgroup-uniform
+        const int cnt = a.grp_cnt[g];
         const MoeOffsets o = moe_offsets(D, F);
         const uint8_t* rec = a.experts + (size_t) e * o.rec;
         const int j0 = jt * 32 + 4 * w;
-        float acc[8][T];
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-#pragma unroll
-            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
-        // D <= 2048: one 32-column chunk per lane (clamped, loads unconditional)
+        // D <= 2048: one 32-column chunk per lane (clamped, loads unconditional); every weight load
+        // of the lane is issued before x is staged
         const int c = min(lane, nc - 1);
         int4 code[8];
         uint32_t sc2[8];
@@ -360,24 +325,39 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
         }
         const float sc_gate = ((const float*) (rec + o.tail))[0];
         const float sc_up = ((const float*) (rec + o.tail))[1];
-        if (bid == 0) {                                  // publish the routing for moe_down
-            const int n_ent = T * K;
-            for (int i = tid; i < n_ent; i += blockDim.x) {
-                a.ids[i] = r.ids[i];
-                a.wts[i] = r.w[i];
-                if (i < r.n_groups) {
-                    a.grp_exp[i] = r.gexp[i];
-                    a.grp_cnt[i] = r.gcnt[i];
-                    for (int m = 0; m < WZY_MAX_W; ++m) a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
-                }
+        // stage the member rows of x quantised per 16 (member m's chunk c at s_xh[(m * nc + c) * 16])
+        for (int i = tid; i < cnt * nc; i += (int) blockDim.x) {
+            const int m = i / nc, cc = i - m * nc;
+            const int t = a.grp_mem[g * WZY_MAX_W + m] / K;
+            const float4* xp = (const float4*) (a.x + (size_t) t * D + (size_t) cc * 32);
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float4 f = xp[k];
+                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
             }
-            if (tid == 0) *a.n_groups = r.n_groups;
+            half2_t xq[16];
+            float da, db;
+            quant16_pairs(v, xq, da, db);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xq[4 * k]),
+                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 1]),
+                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 2]),
+                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 3]));
+            s_xs2[i] = make_float2(da, db);
         }
+        __syncthreads();
+        float acc[8][T];
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
         if (lane < nc) {
 #pragma unroll
             for (int m = 0; m < T; ++m) {
                 if (m < cnt) {
-                    const int xi = (r.gmem[g][m] / K) * nc + c;
+                    const int xi = m * nc + c;
                     half2_t xp[16];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
@@ -418,7 +398,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
             const float d = amax / 127.0f;
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
-            const int f = r.gmem[g][m];
+            const int f = a.grp_mem[g * WZY_MAX_W + m];
             a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
                 __builtin_bit_cast(uint16_t, (_Float16) (float) q);
             if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
@@ -485,6 +465,93 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
             const float uv = wave_sum(acc[2 + q][t]);
             if (lane == 0) a.shact[(size_t) t * F + j0 + q] = siluf_(gv) * uv;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// router: logits [T x E] = bf16 W . x (fp32 accumulate) and the shared-expert gate scalar, one row per
+// wave (rows 0..E-1 the router, row E the shared gate); the last workgroup to finish routes the
+// window and publishes ids / weights / groups for moe_gate_up and moe_down.  The arrival counter is
+// file-scope device memory (zero at load, reset by the routing workgroup): router launches on one
+// device must not overlap.
+// reference: launch_gemm_bf16 (router) + router_top10_fast_multi + the grouping
+// (src/wzy_stage_v2.cuh:699-706; src/wzy_kernels_v2.cuh:307-337,989-1090; src/wzy_cpu_moe.cuh:74-127)
+// ---------------------------------------------------------------------------------------------
+constexpr int RT_ROWS = 4;          // rows per workgroup (one per wave)
+constexpr int RT_MAXP = 8;          // 8-value pieces per lane: D <= 4096
+__device__ unsigned g_rt_arrive[1];
+
+template <int T, int RV>
+__global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
+    __shared__ RouteLds r;
+    __shared__ bool s_last;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int D = a.D, E = a.E;
+    const int row = blockIdx.x * RT_ROWS + w;
+    if (row <= E) {                                      // wave-uniform
+        const uint16_t* wr = row < E ? a.router + (size_t) row * D : a.sgate;
+        const int npc = D / 8;
+        uint4 wv[RT_MAXP];
+#pragma unroll
+        for (int j = 0; j < RT_MAXP; ++j) {
+            const int pc = min(lane + 64 * j, npc - 1);
+            wv[j] = ld_stream_u4(wr + (size_t) pc * 8);
+        }
+        float acc[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = 0.f;
+#pragma unroll
+        for (int j = 0; j < RT_MAXP; ++j) {
+            const int pc = lane + 64 * j;
+            if (pc < npc) {
+                const uint32_t q[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float4* xp = (const float4*) (a.x + (size_t) t * D + (size_t) pc * 8);
+                    const float4 x0 = xp[0], x1 = xp[1];
+                    float s = acc[t];
+                    s = fmaf(bf16_lo(q[0]), x0.x, s); s = fmaf(bf16_hi(q[0]), x0.y, s);
+                    s = fmaf(bf16_lo(q[1]), x0.z, s); s = fmaf(bf16_hi(q[1]), x0.w, s);
+                    s = fmaf(bf16_lo(q[2]), x1.x, s); s = fmaf(bf16_hi(q[2]), x1.y, s);
+                    s = fmaf(bf16_lo(q[3]), x1.z, s); s = fmaf(bf16_hi(q[3]), x1.w, s);
+                    acc[t] = s;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float v = wave_sum(acc[t]);
+            if (lane == 0) {
+                if (row < E) a.logits[(size_t) t * E + row] = v;
+                else a.sg[t] = v;
+            }
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(a.arrive, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    float p[(T + 3) / 4][RV];
+    route_prefetch<T, RV>(a.logits, E, p);
+    route_compute<T, RV>(p, E, a.K, r);
+    const int n_ent = T * a.K;
+    for (int i = tid; i < n_ent; i += blockDim.x) {
+        a.ids[i] = r.ids[i];
+        a.wts[i] = r.w[i];
+        if (i < r.n_groups) {
+            a.grp_exp[i] = r.gexp[i];
+            a.grp_cnt[i] = r.gcnt[i];
+            for (int m = 0; m < WZY_MAX_W; ++m) a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
+        } else {
+            a.grp_exp[i] = 0;                            // unused groups: a valid expert id for readers
+            a.grp_cnt[i] = 0;
+        }
+    }
+    if (tid == 0) {
+        *a.n_groups = r.n_groups;
+        *a.arrive = 0u;
     }
 }
 
@@ -761,12 +828,33 @@ int moe_check(const wzy_moe_weights* w, int T) {
     return WZY_OK;
 }
 
+template <int T>
+static void launch_rt_t(const MoeRtArgs& a, hipStream_t st) {
+    const dim3 grid((a.E + 1 + RT_ROWS - 1) / RT_ROWS);
+    if (a.E <= 512) hipLaunchKernelGGL((moe_router_kernel<T, 8>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((moe_router_kernel<T, 16>), grid, dim3(256), 0, st, a);
+}
+
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st) {
-    GemvSegs segs;
-    segs.n = 2;
-    segs.seg[0] = GemvSeg{w->router, nullptr, ws.logits, w->n_exp, GEMV_BF16, 0, 0};
-    segs.seg[1] = GemvSeg{w->sgate, nullptr, ws.sg, 1, GEMV_BF16, 1, 0};
-    return launch_gemv_segs(segs, x, w->n_embd, T, st);
+    WZY_REQUIRE(w->n_embd % 8 == 0 && w->n_embd <= 64 * 8 * RT_MAXP, "moe router: n_embd above %d",
+                64 * 8 * RT_MAXP);
+    MoeRtArgs a{};
+    a.router = w->router; a.sgate = w->sgate; a.x = x; a.D = w->n_embd; a.E = w->n_exp; a.K = w->top_k;
+    a.logits = ws.logits; a.sg = ws.sg; a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups;
+    a.grp_exp = ws.grp_exp; a.grp_cnt = ws.grp_cnt; a.grp_mem = ws.grp_mem;
+    WZY_HIP_TRY(hipGetSymbolAddress((void**) &a.arrive, HIP_SYMBOL(g_rt_arrive)));
+    switch (T) {
+        case 1: launch_rt_t<1>(a, st); break;
+        case 2: launch_rt_t<2>(a, st); break;
+        case 3: launch_rt_t<3>(a, st); break;
+        case 4: launch_rt_t<4>(a, st); break;
+        case 5: launch_rt_t<5>(a, st); break;
+        case 6: launch_rt_t<6>(a, st); break;
+        case 7: launch_rt_t<7>(a, st); break;
+        default: launch_rt_t<8>(a, st); break;
+    }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
 }
 
 static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T) {
@@ -792,10 +880,7 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
-    if (a.E <= 512)
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 8>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
-    else
-        hipLaunchKernelGGL((moe_gate_up_kernel<T, 16>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
+    hipLaunchKernelGGL((moe_gate_up_kernel<T>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
 }
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
@@ -889,24 +974,23 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
         WZY_REQUIRE(layers[l].n_embd == layers[0].n_embd && layers[l].n_ff == layers[0].n_ff &&
                         layers[l].n_exp == E && layers[l].top_k == layers[0].top_k,
                     "wzy_moe_time_kernels: layers must share one shape");
-    // Router logits of every layer are computed first, one buffer per layer, so that the timed
-    // region holds nothing but back-to-back launches of one kernel: `iters` gate/up launches cycling
-    // through the layers (each routing with its own layer's logits), then `iters` down launches
-    // (each with its own layer's weights, reading the routing the last gate/up published).  Two
-    // events per burst: their own cost is spread over `iters` launches.
+    // Every layer is routed first into a workspace of its own, so that the timed region holds nothing
+    // but back-to-back launches of one kernel: `iters` gate/up launches cycling through the layers
+    // (each with its own layer's routing), then `iters` down launches (each reading the activations
+    // its layer's last gate/up wrote).  Two events per burst: their own cost is spread over `iters`
+    // launches.
+    (void) ws;
     float* comb = nullptr;
-    float* lgt = nullptr;
+    unsigned char* lws = nullptr;
     WZY_HIP_TRY(hipMalloc(&comb, sizeof(float) * (size_t) T * layers[0].n_embd));
-    if (hipMalloc(&lgt, sizeof(float) * (size_t) n_layers * T * (E + 1)) != hipSuccess) {
+    const size_t per = align_up(need, 256);
+    if (hipMalloc(&lws, per * n_layers) != hipSuccess) {
         (void) hipFree(comb);
         set_error("wzy_moe_time_kernels: out of device memory");
         return WZY_ENOMEM;
     }
     auto layer_ws = [&](int l) {
-        MoeWs w = ws;
-        w.logits = lgt + (size_t) l * T * E;
-        w.sg = lgt + (size_t) n_layers * T * E + (size_t) l * T;
-        return w;
+        return moe_ws_carve(lws + per * l, per, layers[0].n_embd, layers[0].n_ff, E, layers[0].top_k, T, nullptr);
     };
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int rc = WZY_OK;
@@ -939,7 +1023,7 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
     }
     for (auto& e : ev)
         if (e) (void) hipEventDestroy(e);
-    (void) hipFree(lgt);
+    (void) hipFree(lws);
     (void) hipFree(comb);
     if (rc != WZY_OK) return rc;
     *us_gate_up = 1000.0f * a / (float) iters;

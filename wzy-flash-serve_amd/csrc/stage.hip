@@ -55,6 +55,29 @@ enum TensorId {
 };
 constexpr uint32_t MODEL_LAYER = 0xFFFF;
 
+// One copy of commit_window_state: dst <- src + acc_idx * src_stride (bytes; multiples of 16).
+// pooled: the destination moves by (acc_pos / idx_blk) * pooled_row bytes, and the job only runs for
+// acc_pos >= 0 (the indexer state of a QSA layer).
+struct CommitJob {
+    unsigned char* dst;
+    const unsigned char* src;
+    size_t src_stride, bytes;
+    int qsa, pooled;
+};
+constexpr int COMMIT_WGS = 64;         // workgroups per copy job
+
+// every job of commit_window_state in one launch: grid (COMMIT_WGS, jobs)
+__global__ void __launch_bounds__(256) commit_kernel(const CommitJob* __restrict__ jobs, int acc_idx, int acc_pos,
+                                                     int idx_blk, int pooled_row) {
+    const CommitJob j = jobs[blockIdx.y];
+    if (j.qsa && acc_pos < 0) return;
+    unsigned char* dst = j.dst + (j.pooled ? (size_t) (acc_pos / idx_blk) * pooled_row : 0);
+    const uint4* src = (const uint4*) (j.src + (size_t) acc_idx * j.src_stride);
+    const size_t n = j.bytes / 16;
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t) COMMIT_WGS * 256)
+        ((uint4*) dst)[i] = src[i];
+}
+
 struct Q8 {
     int8_t* q = nullptr;
     uint16_t* s = nullptr;
@@ -148,6 +171,8 @@ struct wzy_stage {
     MtpState* mtp = nullptr;        // MTP drafter (wzy_stage_mtp_init)
 
     std::map<unsigned long long, hipGraphExec_t> graph_execs;
+    CommitJob* commit_jobs = nullptr;   // device table of commit_window_state's copies
+    int n_commit_jobs = 0;
 
     bool profiling = false;         // direct launches instead of graphs
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -402,6 +427,35 @@ int wzy_stage::init_buffers() {
         WZY_TRY(alloc_t(&tail_snaps, (size_t) n_qsa * W * (c.idx_blk - 1) * c.idx_dim));
         WZY_TRY(alloc_t(&dead_snaps, (size_t) n_qsa * W * c.idx_dim));
         WZY_TRY(alloc_t(&pool_snaps, (size_t) n_qsa * W * 2 * c.idx_dim));
+    }
+    {   // copies of commit_window_state, one table entry each
+        std::vector<CommitJob> jobs;
+        for (const Layer& w : L) {
+            if (!w.qsa) {
+                const size_t sl = (size_t) w.local * W;
+                jobs.push_back(CommitJob{(unsigned char*) w.conv_hist, (const unsigned char*) (conv_snaps + sl * QKV * 3),
+                                         (size_t) QKV * 12, (size_t) QKV * 12, 0, 0});
+                jobs.push_back(CommitJob{(unsigned char*) w.ssm,
+                                         (const unsigned char*) (ssm_snaps + sl * c.gdn_hv * 128 * 128),
+                                         (size_t) c.gdn_hv * 128 * 128 * 4, (size_t) c.gdn_hv * 128 * 128 * 4, 0, 0});
+            } else {
+                const size_t sl = (size_t) w.local * W;
+                jobs.push_back(CommitJob{(unsigned char*) w.ix.tail,
+                                         (const unsigned char*) (tail_snaps + sl * (c.idx_blk - 1) * c.idx_dim),
+                                         (size_t) (c.idx_blk - 1) * c.idx_dim * 4, (size_t) (c.idx_blk - 1) * c.idx_dim * 4,
+                                         1, 0});
+                jobs.push_back(CommitJob{(unsigned char*) w.ix.dead, (const unsigned char*) (dead_snaps + sl * c.idx_dim),
+                                         (size_t) c.idx_dim * 4, (size_t) c.idx_dim * 4, 1, 0});
+                jobs.push_back(CommitJob{(unsigned char*) w.ix.pooled,
+                                         (const unsigned char*) (pool_snaps + sl * 2 * c.idx_dim),
+                                         (size_t) 2 * c.idx_dim * 2, (size_t) 2 * c.idx_dim * 2, 1, 1});
+            }
+        }
+        for (const CommitJob& j : jobs)
+            WZY_REQUIRE(j.bytes % 16 == 0 && j.src_stride % 16 == 0, "stage: snapshot sizes must be multiples of 16 bytes");
+        n_commit_jobs = (int) jobs.size();
+        WZY_TRY(alloc_t(&commit_jobs, jobs.size(), false));
+        WZY_HIP_TRY(hipMemcpy(commit_jobs, jobs.data(), jobs.size() * sizeof(CommitJob), hipMemcpyHostToDevice));
     }
     WZY_TRY(alloc_t(&d_step, 16));
     WZY_HIP_TRY(hipHostMalloc((void**) &h_step, STEP_SLOTS * STEP_INTS * sizeof(int), hipHostMallocDefault));
@@ -817,26 +871,15 @@ extern "C" int wzy_stage_promote_cold(wzy_stage* st) { return st ? WZY_OK : WZY_
 
 extern "C" int wzy_stage_commit_window_state(wzy_stage* st, int acc_idx, int acc_pos) {
     WZY_REQUIRE(st && acc_idx >= 0 && acc_idx < WZY_MAX_W, "commit_window_state: bad arguments");
+    WZY_REQUIRE(acc_pos < st->cfg.ctx_max, "commit_window_state: acc_pos beyond ctx_max");
     const wzy_stage_cfg& c = st->cfg;
     WZY_HIP_TRY(hipSetDevice(st->dev));
-    for (Layer& w : st->L) {
-        if (!w.qsa) {
-            const size_t sl = (size_t) w.local * WZY_MAX_W + acc_idx;
-            WZY_HIP_TRY(hipMemcpyAsync(w.conv_hist, st->conv_snaps + sl * st->QKV * 3, (size_t) st->QKV * 12,
-                                       hipMemcpyDeviceToDevice, st->stream));
-            WZY_HIP_TRY(hipMemcpyAsync(w.ssm, st->ssm_snaps + sl * c.gdn_hv * 128 * 128, (size_t) c.gdn_hv * 128 * 128 * 4,
-                                       hipMemcpyDeviceToDevice, st->stream));
-        } else if (acc_pos >= 0) {
-            const size_t sl = (size_t) w.local * WZY_MAX_W + acc_idx;
-            WZY_HIP_TRY(hipMemcpyAsync(w.ix.tail, st->tail_snaps + sl * (c.idx_blk - 1) * c.idx_dim,
-                                       (size_t) (c.idx_blk - 1) * c.idx_dim * 4, hipMemcpyDeviceToDevice, st->stream));
-            WZY_HIP_TRY(hipMemcpyAsync(w.ix.dead, st->dead_snaps + sl * c.idx_dim, (size_t) c.idx_dim * 4,
-                                       hipMemcpyDeviceToDevice, st->stream));
-            const int b = acc_pos / c.idx_blk;
-            WZY_HIP_TRY(hipMemcpyAsync(w.ix.pooled + (size_t) b * c.idx_dim, st->pool_snaps + sl * 2 * c.idx_dim,
-                                       (size_t) 2 * c.idx_dim * 2, hipMemcpyDeviceToDevice, st->stream));
-        }
-    }
+    if (st->n_commit_jobs == 0) return WZY_OK;
+    // every snapshot copy in one launch (GDN conv history + state; indexer tail, placeholder, pooled
+    // keys of the block holding acc_pos)
+    hipLaunchKernelGGL(commit_kernel, dim3(COMMIT_WGS, st->n_commit_jobs), dim3(256), 0, st->stream, st->commit_jobs,
+                       acc_idx, acc_pos, c.idx_blk, c.idx_dim * 2);
+    WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
 

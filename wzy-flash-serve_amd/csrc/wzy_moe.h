@@ -41,7 +41,7 @@ struct MoeWs {
 struct MoeGuArgs {
     const uint8_t* experts; int D, F, E, K;
     const float* x; const float* logits;
-    int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // published by workgroup 0
+    int* ids; float* wts; int* n_groups; int* grp_exp; int* grp_cnt; int* grp_mem;   // published by moe_router
     uint16_t* ah16; float* as16;
     const int8_t* shg_q; const uint16_t* shg_s; const int8_t* shu_q; const uint16_t* shu_s;
     float* shact;
@@ -57,7 +57,8 @@ struct MoeDnArgs {
 
 MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, size_t* need);
 int moe_check(const wzy_moe_weights* w, int T);
-// router GEMV (+ shared gate row) over fp32 x [T x D]
+// router GEMV (+ shared gate row) over fp32 x [T x D], then the window routing into ws (ids, wts,
+// groups); launches on one device must not overlap (file-scope arrival counter)
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st);
 // routing + gate/up, down + combine into comb [T x D]
 int moe_launch_experts(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, float* comb, hipStream_t st);
