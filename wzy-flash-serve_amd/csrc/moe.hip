@@ -1,14 +1,17 @@
 // moe.hip -- NVFP4 mixture-of-experts decode block for gfx950.
 //
 // Launch sequence of wzy_moe_block (T window rows, K routed experts per row), three launches:
-//   1. moe_router   router logits [T x E] (bf16, one row per wave) + the shared-expert gate scalar
-//                   row; the last workgroup to finish routes the window once (softmax top-K,
-//                   weights, groups: each distinct expert of the window once, with its (row, slot)
-//                   members, so its weights stream from HBM once) and publishes the tables.
-//   2. moe_gate_up  routed workgroup (group, 32-row tile): reads its group's expert and issues the
-//                   weight loads at entry, stages its member rows of x quantised per 16 in LDS
-//                   meanwhile, then the gate+up NVFP4 GEMV, SwiGLU and the per-16 int8 requant.
-//                   Shared workgroups run the Q8_0 shared expert on x quantised per 32.
+//   1. router       logits [T x E] (bf16) + the shared-expert gate scalar row.  T > 1: moe_router,
+//                   whose last workgroup to finish routes the window once (softmax top-K, weights,
+//                   groups: each distinct expert of the window once, with its (row, slot) members,
+//                   so its weights stream from HBM once) and publishes the tables.  T = 1: a plain
+//                   gemv_segs launch, and every gate/up workgroup routes the row itself (one routing
+//                   pass plus a cross-workgroup handoff costs more than the in-workgroup routing).
+//   2. moe_gate_up  routed workgroup (group, 32-row tile): T > 1 reads its group's expert and issues
+//                   the weight loads at entry, staging its member rows of x quantised per 16 in LDS
+//                   meanwhile; T = 1 prefetches the logits, stages x, routes, then loads (workgroup 0
+//                   publishes the routing).  Then the gate+up NVFP4 GEMV, SwiGLU and the per-16 int8
+//                   requant.  Shared workgroups run the Q8_0 shared expert on x quantised per 32.
 //   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, activations
 //                   staged in LDS, combine in LDS:
 //                   comb = sigmoid(sgate)*shared + sum_k w_k*part_k  (k in routed order).
@@ -285,10 +288,11 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
 // scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
 // ---------------------------------------------------------------------------------------------
-template <int T>
+template <int T, bool ROUTE, int RV>
 __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_act[WZY_MAX_W][32];
+    __shared__ int s_mem[WZY_MAX_W];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bid = blockIdx.x;
     const int D = a.D, F = a.F, K = a.K;
@@ -304,31 +308,23 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     if (bid < a.n_routed_wg) {
         const int tiles = F / 32;
         const int g = bid / tiles, jt = bid - g * tiles;
-        // routing tables published by moe_router: group g's expert, member count and entries
-        const int ng = *a.n_groups;
-        const int e = __builtin_amdgcn_readfirstlane(a.grp_exp[g]);
-        if (g >= ng) return;                             // workgroup-uniform
-        const int cnt = a.grp_cnt[g];
-        const MoeOffsets o = moe_offsets(D, F);
-        const uint8_t* rec = a.experts + (size_t) e * o.rec;
+        const int c = min(lane, nc - 1);                 // D <= 2048: one 32-column chunk per lane
         const int j0 = jt * 32 + 4 * w;
-        // D <= 2048: one 32-column chunk per lane (clamped, loads unconditional); every weight load
-        // of the lane is issued before x is staged
-        const int c = min(lane, nc - 1);
+        const MoeOffsets o = moe_offsets(D, F);
+        int e = 0, cnt = 0;
         int4 code[8];
         uint32_t sc2[8];
+        // the weight loads of the lane (clamped, unconditional), issued as soon as the expert is known
+        auto load_weights = [&](const uint8_t* rec) {
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const int row = (rr < 4) ? (j0 + rr) : (F + j0 + rr - 4);
-            code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
-            sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
-        }
-        const float sc_gate = ((const float*) (rec + o.tail))[0];
-        const float sc_up = ((const float*) (rec + o.tail))[1];
-        // stage the member rows of x quantised per 16 (member m's chunk c at s_xh[(m * nc + c) * 16])
-        for (int i = tid; i < cnt * nc; i += (int) blockDim.x) {
-            const int m = i / nc, cc = i - m * nc;
-            const int t = a.grp_mem[g * WZY_MAX_W + m] / K;
+            for (int rr = 0; rr < 8; ++rr) {
+                const int row = (rr < 4) ? (j0 + rr) : (F + j0 + rr - 4);
+                code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
+                sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+            }
+        };
+        // chunk `cc` of x row `t` quantised per 16 into LDS slot i
+        auto stage16 = [&](int t, int cc, int i) {
             const float4* xp = (const float4*) (a.x + (size_t) t * D + (size_t) cc * 32);
             float v[32];
 #pragma unroll
@@ -346,7 +342,52 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
                                                                    __builtin_bit_cast(uint32_t, xq[4 * k + 2]),
                                                                    __builtin_bit_cast(uint32_t, xq[4 * k + 3]));
             s_xs2[i] = make_float2(da, db);
+        };
+        if constexpr (ROUTE) {
+            // in-workgroup routing (one-row windows): the logits are prefetched, x is staged while they
+            // arrive, every workgroup routes the row (workgroup 0 publishes the tables for moe_down)
+            __shared__ RouteLds r;
+            float p[(T + 3) / 4][RV];
+            route_prefetch<T, RV>(a.logits, a.E, p);
+            if (tid < 256)                               // item 0 on wave 1: wave 0 routes the first row
+                for (int i = (tid + 192) & 255; i < T * nc; i += 256) stage16(i / nc, i % nc, i);
+            route_compute<T, RV>(p, a.E, K, r);
+            if (g >= r.n_groups) return;                 // workgroup-uniform (workgroup 0 has g = 0)
+            e = __builtin_amdgcn_readfirstlane(r.gexp[g]);
+            cnt = r.gcnt[g];
+            load_weights(a.experts + (size_t) e * o.rec);
+            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? r.gmem[g][tid] : 0;
+            if (bid == 0) {
+                const int n_ent = T * K;
+                for (int i = tid; i < n_ent; i += blockDim.x) {
+                    a.ids[i] = r.ids[i];
+                    a.wts[i] = r.w[i];
+                    if (i < r.n_groups) {
+                        a.grp_exp[i] = r.gexp[i];
+                        a.grp_cnt[i] = r.gcnt[i];
+                        for (int m = 0; m < WZY_MAX_W; ++m)
+                            a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
+                    }
+                }
+                if (tid == 0) *a.n_groups = r.n_groups;
+            }
+        } else {
+            // routing tables published by moe_router: the expert is known at entry, its weights are
+            // requested before x is staged (member m's chunk cc at LDS slot m * nc + cc)
+            const int ng = *a.n_groups;
+            e = __builtin_amdgcn_readfirstlane(a.grp_exp[g]);
+            if (g >= ng) return;                         // workgroup-uniform
+            cnt = a.grp_cnt[g];
+            load_weights(a.experts + (size_t) e * o.rec);
+            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? a.grp_mem[g * WZY_MAX_W + tid] : 0;
+            for (int i = tid; i < cnt * nc; i += (int) blockDim.x) {
+                const int m = i / nc;
+                stage16(a.grp_mem[g * WZY_MAX_W + m] / K, i - m * nc, i);
+            }
         }
+        const uint8_t* rec = a.experts + (size_t) e * o.rec;
+        const float sc_gate = ((const float*) (rec + o.tail))[0];
+        const float sc_up = ((const float*) (rec + o.tail))[1];
         __syncthreads();
         float acc[8][T];
 #pragma unroll
@@ -357,7 +398,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
 #pragma unroll
             for (int m = 0; m < T; ++m) {
                 if (m < cnt) {
-                    const int xi = m * nc + c;
+                    const int xi = (ROUTE ? s_mem[m] / K : m) * nc + c;
                     half2_t xp[16];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
@@ -398,7 +439,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
             const float d = amax / 127.0f;
             const float inv = d > 0.f ? 127.0f / amax : 0.f;
             const int q = max(-127, min(127, rn_int(v * inv)));
-            const int f = a.grp_mem[g * WZY_MAX_W + m];
+            const int f = s_mem[m];
             a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
                 __builtin_bit_cast(uint16_t, (_Float16) (float) q);
             if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
@@ -478,58 +519,76 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
 // (src/wzy_stage_v2.cuh:699-706; src/wzy_kernels_v2.cuh:307-337,989-1090; src/wzy_cpu_moe.cuh:74-127)
 // ---------------------------------------------------------------------------------------------
 constexpr int RT_ROWS = 4;          // rows per workgroup (one per wave)
-constexpr int RT_MAXP = 8;          // 8-value pieces per lane: D <= 4096
+constexpr int RT_XROWS = 2;         // rows of x staged in LDS per pass
 __device__ unsigned g_rt_arrive[1];
 
-template <int T, int RV>
+// NP = 8-value weight pieces per lane (D <= 512 * NP).  Every weight load of the wave is issued first;
+// x comes from LDS, RT_XROWS rows per pass.
+template <int T, int RV, int NP>
 __global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
     __shared__ RouteLds r;
     __shared__ bool s_last;
+    __shared__ __align__(16) float s_x[RT_XROWS * 512 * NP];
+    __shared__ float s_out[RT_ROWS][T];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = a.D, E = a.E;
     const int row = blockIdx.x * RT_ROWS + w;
-    if (row <= E) {                                      // wave-uniform
-        const uint16_t* wr = row < E ? a.router + (size_t) row * D : a.sgate;
-        const int npc = D / 8;
-        uint4 wv[RT_MAXP];
+    const int npc = D / 8;
+    const bool active = row <= E;                        // rows 0..E-1 router, E the shared gate
+    const uint16_t* wr = row < E ? a.router + (size_t) row * D : a.sgate;
+    uint4 wv[NP];
 #pragma unroll
-        for (int j = 0; j < RT_MAXP; ++j) {
-            const int pc = min(lane + 64 * j, npc - 1);
-            wv[j] = ld_stream_u4(wr + (size_t) pc * 8);
-        }
-        float acc[T];
+    for (int j = 0; j < NP; ++j) {
+        const int pc = lane + 64 * j;
+        wv[j] = (active && pc < npc) ? ld_stream_u4(wr + (size_t) pc * 8) : make_uint4(0, 0, 0, 0);
+    }
+    float acc[T];
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc[t] = 0.f;
+    for (int t = 0; t < T; ++t) acc[t] = 0.f;
 #pragma unroll
-        for (int j = 0; j < RT_MAXP; ++j) {
+    for (int t0 = 0; t0 < T; t0 += RT_XROWS) {
+        const int nr = min(RT_XROWS, T - t0);
+        for (int i = tid; i < nr * D / 4; i += 256) ((float4*) s_x)[i] = ((const float4*) (a.x + (size_t) t0 * D))[i];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
             const int pc = lane + 64 * j;
             if (pc < npc) {
                 const uint32_t q[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
 #pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    const float4* xp = (const float4*) (a.x + (size_t) t * D + (size_t) pc * 8);
-                    const float4 x0 = xp[0], x1 = xp[1];
-                    float s = acc[t];
-                    s = fmaf(bf16_lo(q[0]), x0.x, s); s = fmaf(bf16_hi(q[0]), x0.y, s);
-                    s = fmaf(bf16_lo(q[1]), x0.z, s); s = fmaf(bf16_hi(q[1]), x0.w, s);
-                    s = fmaf(bf16_lo(q[2]), x1.x, s); s = fmaf(bf16_hi(q[2]), x1.y, s);
-                    s = fmaf(bf16_lo(q[3]), x1.z, s); s = fmaf(bf16_hi(q[3]), x1.w, s);
-                    acc[t] = s;
+                for (int tt = 0; tt < RT_XROWS; ++tt) {
+                    if (t0 + tt < T) {
+                        const float4* xp = (const float4*) (s_x + (size_t) tt * D + (size_t) pc * 8);
+                        const float4 x0 = xp[0], x1 = xp[1];
+                        float s = acc[t0 + tt];
+                        s = fmaf(bf16_lo(q[0]), x0.x, s); s = fmaf(bf16_hi(q[0]), x0.y, s);
+                        s = fmaf(bf16_lo(q[1]), x0.z, s); s = fmaf(bf16_hi(q[1]), x0.w, s);
+                        s = fmaf(bf16_lo(q[2]), x1.x, s); s = fmaf(bf16_hi(q[2]), x1.y, s);
+                        s = fmaf(bf16_lo(q[3]), x1.z, s); s = fmaf(bf16_hi(q[3]), x1.w, s);
+                        acc[t0 + tt] = s;
+                    }
                 }
             }
         }
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float v = wave_sum(acc[t]);
-            if (lane == 0) {
-                if (row < E) a.logits[(size_t) t * E + row] = v;
-                else a.sg[t] = v;
-            }
-        }
+        __syncthreads();
     }
-    __threadfence();
+    // the workgroup's outputs go to global memory from wave 0 alone, so that one release fence (an
+    // agent-scope fence writes back L2) covers every store before the arrival
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0) s_out[w][t] = v;
+    }
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(a.arrive, 1u) == gridDim.x - 1;
+    if (w == 0) {
+        if (lane < RT_ROWS * T) {
+            const int rw = blockIdx.x * RT_ROWS + lane / T, t = lane % T;
+            if (rw < E) a.logits[(size_t) t * E + rw] = s_out[lane / T][t];
+            else if (rw == E) a.sg[t] = s_out[lane / T][t];
+        }
+        __threadfence();
+        if (lane == 0) s_last = atomicAdd(a.arrive, 1u) == gridDim.x - 1;
+    }
     __syncthreads();
     if (!s_last) return;
     __threadfence();
@@ -828,16 +887,27 @@ int moe_check(const wzy_moe_weights* w, int T) {
     return WZY_OK;
 }
 
+template <int T, int NP>
+static void launch_rt_tn(const MoeRtArgs& a, hipStream_t st) {
+    const dim3 grid((a.E + 1 + RT_ROWS - 1) / RT_ROWS);
+    if (a.E <= 512) hipLaunchKernelGGL((moe_router_kernel<T, 8, NP>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((moe_router_kernel<T, 16, NP>), grid, dim3(256), 0, st, a);
+}
 template <int T>
 static void launch_rt_t(const MoeRtArgs& a, hipStream_t st) {
-    const dim3 grid((a.E + 1 + RT_ROWS - 1) / RT_ROWS);
-    if (a.E <= 512) hipLaunchKernelGGL((moe_router_kernel<T, 8>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((moe_router_kernel<T, 16>), grid, dim3(256), 0, st, a);
+    if (a.D <= 2048) launch_rt_tn<T, 4>(a, st);
+    else launch_rt_tn<T, 8>(a, st);
 }
 
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st) {
-    WZY_REQUIRE(w->n_embd % 8 == 0 && w->n_embd <= 64 * 8 * RT_MAXP, "moe router: n_embd above %d",
-                64 * 8 * RT_MAXP);
+    if (T == 1) {                                    // logits only; moe_gate_up routes
+        GemvSegs segs;
+        segs.n = 2;
+        segs.seg[0] = GemvSeg{w->router, nullptr, ws.logits, w->n_exp, GEMV_BF16, 0, 0};
+        segs.seg[1] = GemvSeg{w->sgate, nullptr, ws.sg, 1, GEMV_BF16, 1, 0};
+        return launch_gemv_segs(segs, x, w->n_embd, T, st);
+    }
+    WZY_REQUIRE(w->n_embd % 8 == 0 && w->n_embd <= 4096, "moe router: n_embd must be a multiple of 8 <= 4096");
     MoeRtArgs a{};
     a.router = w->router; a.sgate = w->sgate; a.x = x; a.D = w->n_embd; a.E = w->n_exp; a.K = w->top_k;
     a.logits = ws.logits; a.sg = ws.sg; a.ids = ws.ids; a.wts = ws.wts; a.n_groups = ws.n_groups;
@@ -877,10 +947,15 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
     return a;
 }
 
+// One-row windows route inside every gate/up workgroup (the router is a plain GEMV: a separate
+// routing pass costs more than it saves at T = 1); windows of several rows route once in moe_router.
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
-    hipLaunchKernelGGL((moe_gate_up_kernel<T>), dim3(a.n_routed_wg + a.F / SH_J), dim3(512), lds, st, a);
+    const dim3 grid(a.n_routed_wg + a.F / SH_J);
+    if (T > 1) hipLaunchKernelGGL((moe_gate_up_kernel<T, false, 8>), grid, dim3(512), lds, st, a);
+    else if (a.E <= 512) hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 8>), grid, dim3(512), lds, st, a);
+    else hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 16>), grid, dim3(512), lds, st, a);
 }
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
