@@ -54,7 +54,9 @@ def q8(wz, seed, rows, cols):
 @pytest.mark.parametrize("D,HC,HCLR,T,mode", [(512, 4, 64, 3, "emb"), (512, 4, 64, 3, "fold"), (512, 4, 64, 2, "head"),
                                              (2048, 4, 320, 1, "fold"), (2048, 4, 320, 4, "emb"),
                                              (2048, 4, 320, 8, "fold"), (4096, 4, 128, 3, "fold"),
-                                             (256, 4, 32, 6, "head")])
+                                             (256, 4, 32, 6, "head"), (2560, 4, 320, 1, "fold"),
+                                             (2560, 4, 320, 4, "emb"), (2560, 4, 320, 2, "head"),
+                                             (768, 4, 64, 3, "fold"), (5120, 4, 96, 1, "fold")])
 def test_hc_read(wz, orc, gpu, D, HC, HCLR, T, mode):
     print("case hc_read D=%d HC=%d HCLR=%d T=%d mode=%s" % (D, HC, HCLR, T, mode), flush=True)
     rng = np.random.default_rng(D + 7 * T)
@@ -121,7 +123,8 @@ def gdn_inputs(hk, hv, T, seed):
     )
 
 
-@pytest.mark.parametrize("hk,hv,T", [(2, 2, 1), (2, 4, 3), (16, 16, 1), (16, 16, 4), (4, 8, 8)])
+@pytest.mark.parametrize("hk,hv,T", [(2, 2, 1), (2, 4, 3), (16, 16, 1), (16, 16, 4), (4, 8, 8), (16, 48, 1),
+                                     (16, 48, 4)])
 def test_gdn_step(wz, orc, gpu, hk, hv, T):
     print("case gdn_step hk=%d hv=%d T=%d" % (hk, hv, T), flush=True)
     a = gdn_inputs(hk, hv, T, 100 * hk + hv + T)

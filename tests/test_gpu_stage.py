@@ -219,6 +219,31 @@ def test_stage_baseline_48_layers_greedy(wz, gpu):
     assert par.router_compared >= 12 and par.select_compared >= 3, par.summary()
 
 
+def real_cfg(n_layers, ctx_max):
+    """The reference model's real shapes (src/wzy_kernels_v2.cuh:8-19): NE 2560, NFF 640, 48 GDN value
+    heads over 16 key heads, vocab 248,320; everything else as the BASELINE model."""
+    cfg = wzy_amd.default_cfg(ctx_max)
+    cfg.n_layers = n_layers
+    cfg.n_embd, cfg.n_ff, cfg.gdn_hv, cfg.n_vocab = 2560, 640, 48, 248320
+    return cfg
+
+
+@pytest.mark.timeout(900)
+def test_stage_reference_real_shape_4_layers(wz, gpu):
+    """The reference's real shape, layers GDN, GDN, GDN, QSA at a 6,000-cell prefilled context: three
+    single-token steps checked component by component (teacher-forced) and a T=4 window, with the
+    discrete decisions compared free-running."""
+    print("case real_shape_4_layers", flush=True)
+    cfg = real_cfg(4, 6144)
+    rng = np.random.default_rng(52)
+    windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 3)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
+    par, tf = run_layer_parity(wz, cfg, 52, 6000, windows, teacher=True)
+    print("real shape 4 layers: " + par.summary(), flush=True)
+    print("real shape 4 layers: " + tf.summary(), flush=True)
+    assert tf.counts["rows"] == 3 and tf.counts["layers"] == 12
+    assert par.router_compared >= 8 and par.select_compared >= 2, par.summary()
+
+
 def test_stage_baseline_shapes_graph_replay_matches_eager(wz, gpu):
     """At the BASELINE shapes, graph replays and direct launches give bit-identical logits."""
     print("case baseline_graph_vs_eager", flush=True)

@@ -85,7 +85,18 @@ WZY_DEV float group_max(float v) {
     return v;
 }
 
-// sum of 4 values per thread over the 256-thread workgroup; results valid on thread 0
+// sum over the NW waves of a workgroup (four waves: the pairing (w0 + w1) + (w2 + w3))
+template <int NW>
+WZY_DEV float waves_sum(const float (*sh)[4], int o) {
+    if constexpr (NW == 4) return (sh[0][o] + sh[1][o]) + (sh[2][o] + sh[3][o]);
+    float s = sh[0][o];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) s += sh[i][o];
+    return s;
+}
+
+// sum of 4 values per thread over the NW-wave workgroup; results valid on thread 0
+template <int NW>
 WZY_DEV void block_sum4_t0(float (&v)[4], float (*sh)[4]) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
@@ -96,24 +107,24 @@ WZY_DEV void block_sum4_t0(float (&v)[4], float (*sh)[4]) {
     __syncthreads();
     if (threadIdx.x == 0)
 #pragma unroll
-        for (int o = 0; o < 4; ++o) v[o] = (sh[0][o] + sh[1][o]) + (sh[2][o] + sh[3][o]);
+        for (int o = 0; o < 4; ++o) v[o] = waves_sum<NW>(sh, o);
 }
 
 }  // namespace
 
-// T window rows; VPT = D/256 values of the stream per thread; NBL = 32-blocks per lane of one
-// down row (D/32/64 rounded up); RPW down rows per wave.  Workgroup b: stream c = b % 4, row block
-// rb = b / 4 (rows rb*4*RPW ..), rb == NRB is the stream's R_out / nsc / inject workgroup.
-// Dynamic LDS (row workgroups): int8 xq [T][D] then fp32 xs [T][D/32].
-template <int T, int VPT, int NBL, int RPW>
-__global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
+// T window rows; NW waves per workgroup; VPT = D/(64*NW) values of the stream per thread; NBL =
+// 32-blocks per lane of one down row (D/32/64 rounded up); RPW down rows per wave.  Workgroup b:
+// stream c = b % 4, row block rb = b / 4 (rows rb*NW*RPW ..), rb == NRB is the stream's R_out / nsc /
+// inject workgroup.  Dynamic LDS (row workgroups): int8 xq [T][D] then fp32 xs [T][D/32].
+template <int T, int VPT, int NBL, int RPW, int NW>
+__global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ float s_red[4][4];
+    __shared__ float s_red[NW][4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = a.D, HCD = HC4 * D, NB = D / 32, L = a.HCLR;
     constexpr int G = 32 / VPT;                        // threads per 32-block
     const int c = blockIdx.x & 3, rb = blockIdx.x >> 2;
-    const int nrb = (L + 4 * RPW - 1) / (4 * RPW);
+    const int nrb = (L + NW * RPW - 1) / (NW * RPW);
     const bool aux = rb >= nrb;                        // workgroup-uniform
     const bool do_inj = aux && a.inj_w != nullptr;
     int8_t* s_xq = (int8_t*) s_dyn;
@@ -122,7 +133,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
     const int d0 = tid * VPT;                          // this thread's values: d0 .. d0+VPT-1 of stream c
 
     // 0. this wave's down rows (raw codes and fp16 scales of stream c's columns), issued first
-    const int row0 = (rb * 4 + w) * RPW;
+    const int row0 = (rb * NW + w) * RPW;
     int4 c0[NBL][RPW], c1[NBL][RPW];
     uint32_t sraw[NBL][RPW];         // 16-bit scales held in 32-bit registers (no packing that waits for the load)
     if (!aux) {
@@ -178,7 +189,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
         ss = wave_sum(ss);
         if (lane == 0) s_red[w][0] = ss;
         __syncthreads();
-        const float sc = 1.0f / sqrtf(((s_red[0][0] + s_red[1][0]) + (s_red[2][0] + s_red[3][0])) / (float) D + a.eps);
+        const float sc = 1.0f / sqrtf(waves_sum<NW>(s_red, 0) / (float) D + a.eps);
         __syncthreads();                              // s_red is reused below
         float xn[VPT];
 #pragma unroll
@@ -203,7 +214,7 @@ __global__ void __launch_bounds__(256) hc_pre_kernel(HcPreArgs a) {
 #pragma unroll
                     for (int j = 0; j < VPT; ++j) acc[o] = fmaf(bf16_at<VPT>(iw[o], j), xn[j], acc[o]);
                 }
-                block_sum4_t0(acc, s_red);
+                block_sum4_t0<NW>(acc, s_red);
                 if (tid == 0)
 #pragma unroll
                     for (int o = 0; o < 4; ++o) a.inj_part[((size_t) t * HC4 + c) * HC4 + o] = acc[o];
@@ -370,21 +381,52 @@ namespace wzy {
 namespace {
 constexpr int PRE_RPW = 2;
 
-template <int T, int VPT>
+template <int T, int VPT, int NW>
 void launch_pre_tv(const HcPreArgs& a, hipStream_t st) {
-    constexpr int NBL = (VPT * 8 + 63) / 64;          // D/32 blocks over 64 lanes (D = 256*VPT)
-    const int nrb = (a.HCLR + 4 * PRE_RPW - 1) / (4 * PRE_RPW);
+    constexpr int NBL = (2 * NW * VPT + 63) / 64;     // D/32 = 2*NW*VPT blocks over 64 lanes (D = 64*NW*VPT)
+    const int nrb = (a.HCLR + NW * PRE_RPW - 1) / (NW * PRE_RPW);
     const size_t lds = (size_t) T * a.D + (size_t) T * (a.D / 32) * sizeof(float);
-    hipLaunchKernelGGL((hc_pre_kernel<T, VPT, NBL, PRE_RPW>), dim3(HC4 * (nrb + 1)), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((hc_pre_kernel<T, VPT, NBL, PRE_RPW, NW>), dim3(HC4 * (nrb + 1)), dim3(64 * NW), lds, st, a);
+}
+// (waves per workgroup, values per thread) of a stream width D: four waves when D/256 is a power of
+// two (256 .. 4096), else five (D = 1280, 2560, 5120) or three (D = 768, 1536, 3072) waves
+bool pre_shape(int D, int& nw, int& vpt) {
+    for (int w : {4, 5, 3}) {
+        if (D <= 0 || D % (64 * w)) continue;
+        const int v = D / (64 * w);
+        if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) {
+            if (w != 4 && v < 4) continue;               // instantiated: 5 or 3 waves with 4, 8 or 16 values
+            nw = w;
+            vpt = v;
+            return true;
+        }
+    }
+    return false;
 }
 template <int T>
 void launch_pre_t(const HcPreArgs& a, hipStream_t st) {
-    switch (a.D / 256) {
-        case 1: launch_pre_tv<T, 1>(a, st); break;
-        case 2: launch_pre_tv<T, 2>(a, st); break;
-        case 4: launch_pre_tv<T, 4>(a, st); break;
-        case 8: launch_pre_tv<T, 8>(a, st); break;
-        default: launch_pre_tv<T, 16>(a, st); break;
+    int nw = 0, vpt = 0;
+    pre_shape(a.D, nw, vpt);
+    if (nw == 5) {
+        switch (vpt) {
+            case 4: launch_pre_tv<T, 4, 5>(a, st); break;
+            case 8: launch_pre_tv<T, 8, 5>(a, st); break;
+            default: launch_pre_tv<T, 16, 5>(a, st); break;
+        }
+    } else if (nw == 3) {
+        switch (vpt) {
+            case 4: launch_pre_tv<T, 4, 3>(a, st); break;
+            case 8: launch_pre_tv<T, 8, 3>(a, st); break;
+            default: launch_pre_tv<T, 16, 3>(a, st); break;
+        }
+    } else {
+        switch (vpt) {
+            case 1: launch_pre_tv<T, 1, 4>(a, st); break;
+            case 2: launch_pre_tv<T, 2, 4>(a, st); break;
+            case 4: launch_pre_tv<T, 4, 4>(a, st); break;
+            case 8: launch_pre_tv<T, 8, 4>(a, st); break;
+            default: launch_pre_tv<T, 16, 4>(a, st); break;
+        }
     }
 }
 }  // namespace
@@ -399,11 +441,11 @@ void hc_carve_workspace(void* ws, int HC, int HCLR, int T, float** lo_part, floa
 
 int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "hc_pre: T out of range");
-    const int vpt = a.D / 256;
-    WZY_REQUIRE(a.HC == HC4 && a.D % 256 == 0 && (vpt == 1 || vpt == 2 || vpt == 4 || vpt == 8 || vpt == 16) &&
+    int nw = 0, vpt = 0;
+    WZY_REQUIRE(a.HC == HC4 && pre_shape(a.D, nw, vpt) &&
                     a.HCLR % 32 == 0 && a.HCLR >= 32 && a.HCLR <= 512,
-                "hc_pre: unsupported shape (HC must be 4, D one of 256/512/1024/2048/4096, HCLR a multiple of 32 "
-                "<= 512)");
+                "hc_pre: unsupported shape (HC must be 4, D one of 256/512/768/1024/1280/1536/2048/2560/3072/4096/"
+                "5120, HCLR a multiple of 32 <= 512)");
     WZY_REQUIRE((a.R_in != nullptr) + (a.emb_table != nullptr) + (a.emb_rows != nullptr) == 1,
                 "hc_pre: exactly one of R_in / emb_table / emb_rows");
     WZY_REQUIRE(!a.emb_table || a.toks, "hc_pre: embedding mode needs toks");

@@ -98,7 +98,11 @@ WZY_DEV int excl_count_wg(bool pred, int* s_c, int& total) {     // s_c: 8 ints;
 
 // int8 quantisation, reference rule d = amax/127, q = rint(x * 127/amax) clamped to +-127.
 // 32 values -> two 16-value halves with one shared per-32 scale
-constexpr int SH_J = 16;           // shared-expert SwiGLU outputs per gate/up workgroup (2 per wave)
+// Rows per gate/up workgroup.  A lane holds NCL 32-column chunks of every row it dots (NCL = 1 for
+// D <= 2048, 2 for D <= 4096); with two chunks a wave takes half as many rows, so that its weight
+// registers stay the same.
+__host__ __device__ constexpr int gu_tile_rows(int ncl) { return 32 / ncl; }   // routed F-rows (gate and up)
+__host__ __device__ constexpr int sh_tile_rows(int ncl) { return 16 / ncl; }   // shared-expert SwiGLU outputs
 
 // moe_down dynamic LDS: the shared activation's per-32 scales, padded to 16 bytes
 __host__ __device__ inline int dn_shs_floats(int T, int nchunk) { return (T * nchunk + 3) / 4 * 4; }
@@ -278,7 +282,7 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 // ---------------------------------------------------------------------------------------------
 // gate/up, eight waves per workgroup.  Routed workgroups: one (group, 32-row tile); wave w owns rows
 // j = 32*tile + 4w .. +3 of both gate and up, so SwiGLU and the 16-wide requant (two 16-row blocks)
-// stay inside the workgroup.  With 32-row tiles the launch has few enough workgroups (10 experts x 16
+// stay inside the workgroup (D > 2048: 16-row tiles, two rows per wave).  With 32-row tiles the launch has few enough workgroups (10 experts x 16
 // + 32 shared at the BASELINE shapes) that each gets a CU of its own.
 // reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
 // Shared workgroups: 16 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32 requant of
@@ -287,8 +291,9 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
 // src/wzy_kernels_v2.cuh:1247-1280).
 // Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
 // scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
+// NCL = 32-column chunks of x per lane: 1 for D <= 2048, 2 for D <= 4096 (the reference's NE = 2560).
 // ---------------------------------------------------------------------------------------------
-template <int T, bool ROUTE, int RV>
+template <int T, bool ROUTE, int RV, int NCL>
 __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_act[WZY_MAX_W][32];
@@ -306,21 +311,26 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
     float* s_sc = (float*) (s_qb + (size_t) T * nc);
 
     if (bid < a.n_routed_wg) {
-        const int tiles = F / 32;
+        constexpr int TR = gu_tile_rows(NCL), RPW = TR / 8;     // tile rows; gate (and up) rows per wave
+        const int tiles = F / TR;
         const int g = bid / tiles, jt = bid - g * tiles;
-        const int c = min(lane, nc - 1);                 // D <= 2048: one 32-column chunk per lane
-        const int j0 = jt * 32 + 4 * w;
+        const int j0 = jt * TR + RPW * w;
         const MoeOffsets o = moe_offsets(D, F);
         int e = 0, cnt = 0;
-        int4 code[8];
-        uint32_t sc2[8];
+        // lane chunks c = lane, lane + 64; rows rr < RPW gate j0 + rr, the others up j0 + rr - RPW
+        int4 code[NCL][2 * RPW];
+        uint32_t sc2[NCL][2 * RPW];
         // the weight loads of the lane (clamped, unconditional), issued as soon as the expert is known
         auto load_weights = [&](const uint8_t* rec) {
 #pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int row = (rr < 4) ? (j0 + rr) : (F + j0 + rr - 4);
-                code[rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
-                sc2[rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+            for (int k = 0; k < NCL; ++k) {
+                const int c = min(lane + 64 * k, nc - 1);
+#pragma unroll
+                for (int rr = 0; rr < 2 * RPW; ++rr) {
+                    const int row = (rr < RPW) ? (j0 + rr) : (F + j0 + rr - RPW);
+                    code[k][rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
+                    sc2[k][rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+                }
             }
         };
         // chunk `cc` of x row `t` quantised per 16 into LDS slot i
@@ -389,31 +399,35 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
         const float sc_gate = ((const float*) (rec + o.tail))[0];
         const float sc_up = ((const float*) (rec + o.tail))[1];
         __syncthreads();
-        float acc[8][T];
+        float acc[2 * RPW][T];
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
+        for (int rr = 0; rr < 2 * RPW; ++rr)
 #pragma unroll
             for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
-        if (lane < nc) {
+#pragma unroll
+        for (int k = 0; k < NCL; ++k) {
+            const int c = lane + 64 * k;
+            if (c >= nc) continue;
 #pragma unroll
             for (int m = 0; m < T; ++m) {
                 if (m < cnt) {
                     const int xi = (ROUTE ? s_mem[m] / K : m) * nc + c;
                     half2_t xp[16];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[k];
-                        xp[4 * k] = __builtin_bit_cast(half2_t, u.x);
-                        xp[4 * k + 1] = __builtin_bit_cast(half2_t, u.y);
-                        xp[4 * k + 2] = __builtin_bit_cast(half2_t, u.z);
-                        xp[4 * k + 3] = __builtin_bit_cast(half2_t, u.w);
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
+                        xp[4 * q] = __builtin_bit_cast(half2_t, u.x);
+                        xp[4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
+                        xp[4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
+                        xp[4 * q + 3] = __builtin_bit_cast(half2_t, u.w);
                     }
                     const float2 xs = s_xs2[xi];
 #pragma unroll
-                    for (int rr = 0; rr < 8; ++rr) {
-                        const float wsa = ue4m3_half(sc2[rr] & 0xFFu), wsb = ue4m3_half(sc2[rr] >> 8);
-                        const uint4 cu = make_uint4((uint32_t) code[rr].x, (uint32_t) code[rr].y, (uint32_t) code[rr].z,
-                                                    (uint32_t) code[rr].w);
+                    for (int rr = 0; rr < 2 * RPW; ++rr) {
+                        const uint32_t sw = sc2[k][rr];
+                        const int4 cw = code[k][rr];
+                        const float wsa = ue4m3_half(sw & 0xFFu), wsb = ue4m3_half(sw >> 8);
+                        const uint4 cu = make_uint4((uint32_t) cw.x, (uint32_t) cw.y, (uint32_t) cw.z, (uint32_t) cw.w);
                         acc[rr][m] = nvfp4_chunk_fma_h(cu, wsa, wsb, xp, xs.x, xs.y, acc[rr][m]);
                     }
                 }
@@ -423,17 +437,17 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
         for (int m = 0; m < T; ++m) {
             if (m < cnt) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < RPW; ++q) {
                     const float gv = wave_sum(acc[q][m]) * sc_gate;
-                    const float uv = wave_sum(acc[4 + q][m]) * sc_up;
-                    if (lane == 0) s_act[m][4 * w + q] = siluf_(gv) * uv;
+                    const float uv = wave_sum(acc[RPW + q][m]) * sc_up;
+                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
                 }
             }
         }
         __syncthreads();
-        if (tid < cnt * 32) {                            // one 16-lane row per (member, 16-row block)
-            const int m = tid >> 5, jj = tid & 31, jl = jj & 15;
-            const int blk = 2 * jt + (jj >> 4);          // 16-row block of the F rows
+        if (tid < cnt * TR) {                            // one 16-lane row per (member, 16-row block)
+            const int m = tid / TR, jj = tid % TR, jl = jj & 15;
+            const int blk = (TR / 16) * jt + (jj >> 4);  // 16-row block of the F rows
             const float v = s_act[m][jj];
             const float amax = max16(fabsf(v));
             const float d = amax / 127.0f;
@@ -447,22 +461,27 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
         return;
     }
 
-    // shared expert: rows j in [16*sb, 16*sb + 16), wave w owns j = 16*sb + 2w, +1 (gate and up rows);
-    // one 32-block of x per lane.  The SwiGLU values go out as fp32; moe_down quantises them per 32.
+    // shared expert: rows j in [SJ*sb, SJ*sb + SJ) (SJ = 16, or 8 for D > 2048), wave w owns SRW = SJ/8
+    // consecutive rows of both gate and up; NCL 32-blocks of x per lane.  The SwiGLU values go out as
+    // fp32; moe_down quantises them per 32.
     const int sb = bid - a.n_routed_wg;
-    int4 c0[4], c1[4];
-    uint32_t sraw[4];                // 16-bit scales in 32-bit registers (no packing that waits for the load)
-    const int bl = min(lane, nc - 1);
-    const int j0 = SH_J * sb + 2 * w;
+    constexpr int SJ = sh_tile_rows(NCL), SRW = SJ / 8;
+    int4 c0[NCL][2 * SRW], c1[NCL][2 * SRW];
+    uint32_t sraw[NCL][2 * SRW];     // 16-bit scales in 32-bit registers (no packing that waits for the load)
+    const int j0 = SJ * sb + SRW * w;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        const int8_t* q = (rr < 2) ? a.shg_q : a.shu_q;
-        const uint16_t* s = (rr < 2) ? a.shg_s : a.shu_s;
-        const int row = j0 + (rr & 1);
-        const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) bl * 32);
-        c0[rr] = ld_stream_i4(cp);
-        c1[rr] = ld_stream_i4(cp + 1);
-        sraw[rr] = s[(size_t) row * nc + bl];
+    for (int k = 0; k < NCL; ++k) {
+        const int bl = min(lane + 64 * k, nc - 1);
+#pragma unroll
+        for (int rr = 0; rr < 2 * SRW; ++rr) {
+            const int8_t* q = (rr < SRW) ? a.shg_q : a.shu_q;
+            const uint16_t* s = (rr < SRW) ? a.shg_s : a.shu_s;
+            const int row = j0 + rr % SRW;
+            const int4* cp = (const int4*) (q + (size_t) row * D + (size_t) bl * 32);
+            c0[k][rr] = ld_stream_i4(cp);
+            c1[k][rr] = ld_stream_i4(cp + 1);
+            sraw[k][rr] = s[(size_t) row * nc + bl];
+        }
     }
     // stage x quantised per 32
     for (int i = tid; i < T * nc; i += (int) blockDim.x) {
@@ -481,29 +500,32 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
         s_sc[i] = d;
     }
     __syncthreads();
-    float acc[4][T];
+    float acc[2 * SRW][T];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
+    for (int rr = 0; rr < 2 * SRW; ++rr)
 #pragma unroll
         for (int t = 0; t < T; ++t) acc[rr][t] = 0.f;
-    for (int b = lane; b < nc; b += 64) {                // D <= 2048: one 32-block per lane
+#pragma unroll
+    for (int k = 0; k < NCL; ++k) {
+        const int b = lane + 64 * k;                     // the lane's 32-blocks of x
+        if (b >= nc) continue;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int xi = t * nc + b;
             const int4 x0 = s_qa[xi], x1 = s_qb[xi];
             const float xsc = s_sc[xi];
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                acc[rr][t] = fmaf(h16_to_f(sraw[rr]) * xsc, (float) (dot16(c0[rr], x0) + dot16(c1[rr], x1)),
+            for (int rr = 0; rr < 2 * SRW; ++rr)
+                acc[rr][t] = fmaf(h16_to_f(sraw[k][rr]) * xsc, (float) (dot16(c0[k][rr], x0) + dot16(c1[k][rr], x1)),
                                   acc[rr][t]);
         }
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < SRW; ++q) {
             const float gv = wave_sum(acc[q][t]);
-            const float uv = wave_sum(acc[2 + q][t]);
+            const float uv = wave_sum(acc[SRW + q][t]);
             if (lane == 0) a.shact[(size_t) t * F + j0 + q] = siluf_(gv) * uv;
         }
     }
@@ -875,8 +897,8 @@ MoeWs moe_ws_carve(void* base, size_t cap, int D, int F, int E, int K, int T, si
 int moe_check(const wzy_moe_weights* w, int T) {
     WZY_REQUIRE(w != nullptr, "moe: null weights");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "moe: T must be in [1, %d]", WZY_MAX_W);
-    WZY_REQUIRE(w->n_embd % 256 == 0 && w->n_embd >= 256 && w->n_embd <= 2048,
-                "moe: n_embd must be a multiple of 256 <= 2048");
+    WZY_REQUIRE(w->n_embd % 256 == 0 && w->n_embd >= 256 && w->n_embd <= 4096,
+                "moe: n_embd must be a multiple of 256 <= 4096");
     WZY_REQUIRE(w->n_ff % 64 == 0 && w->n_ff >= 64 && w->n_ff <= 2048, "moe: n_ff must be a multiple of 64 <= 2048");
     WZY_REQUIRE(w->n_exp >= 1 && w->n_exp <= 1024, "moe: n_exp must be in [1, 1024]");
     WZY_REQUIRE(w->top_k >= 1 && w->top_k <= MOE_MAX_K && w->top_k <= w->n_exp, "moe: top_k must be in [1, %d]",
@@ -935,7 +957,7 @@ static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float*
     a.grp_mem = ws.grp_mem; a.ah16 = ws.ah16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shact = ws.shact;
-    a.n_routed_wg = (w->n_ff / 32) * T * w->top_k;
+    a.n_routed_wg = (w->n_ff / gu_tile_rows(w->n_embd > 2048 ? 2 : 1)) * T * w->top_k;
     return a;
 }
 static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb) {
@@ -949,13 +971,18 @@ static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb)
 
 // One-row windows route inside every gate/up workgroup (the router is a plain GEMV: a separate
 // routing pass costs more than it saves at T = 1); windows of several rows route once in moe_router.
+template <int T, int NCL>
+static void launch_gu_tn(const MoeGuArgs& a, hipStream_t st) {
+    const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
+    const dim3 grid(a.n_routed_wg + a.F / sh_tile_rows(NCL));
+    if (T > 1) hipLaunchKernelGGL((moe_gate_up_kernel<T, false, 8, NCL>), grid, dim3(512), lds, st, a);
+    else if (a.E <= 512) hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 8, NCL>), grid, dim3(512), lds, st, a);
+    else hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 16, NCL>), grid, dim3(512), lds, st, a);
+}
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
-    const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
-    const dim3 grid(a.n_routed_wg + a.F / SH_J);
-    if (T > 1) hipLaunchKernelGGL((moe_gate_up_kernel<T, false, 8>), grid, dim3(512), lds, st, a);
-    else if (a.E <= 512) hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 8>), grid, dim3(512), lds, st, a);
-    else hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 16>), grid, dim3(512), lds, st, a);
+    if (a.D <= 2048) launch_gu_tn<T, 1>(a, st);
+    else launch_gu_tn<T, 2>(a, st);
 }
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
