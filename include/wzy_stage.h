@@ -43,6 +43,13 @@ typedef struct wzy_stage_cfg {
     int kv_ring, kv_sinks;                     /* 0, 0: full-context KV store (a ring is rejected
                                                   unless ctx_max <= kv_ring, i.e. it never wraps) */
     float rope_theta, eps;                     /* 1e7, 1e-6 */
+    int emb_q8;                                /* 0: token embedding table bf16 ("emb"); 1: Q8_0 ("emb.q"
+                                                  codes + "emb.s" fp16 scales per 32), gathered and
+                                                  dequantised on the GPU as d*q (stage_one_emb,
+                                                  src/wzy_engine_v2.cu:861-873) */
+    int head_q8;                               /* 0: LM head bf16 ("head", BASELINE); 1: Q8_0 ("head.q" /
+                                                  "head.s", the reference's output.weight,
+                                                  src/wzy_stage_v2.cuh:804-815) */
 } wzy_stage_cfg;
 
 typedef struct wzy_stage wzy_stage;
@@ -122,9 +129,11 @@ void* wzy_stage_stream(wzy_stage* st);
 size_t wzy_stage_tensor_bytes(wzy_stage* st, int layer, const char* name);
 int wzy_stage_read_tensor(wzy_stage* st, int layer, const char* name, void* host, size_t bytes);
 int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes);
-/* Bytes [offset, offset + bytes) of a tensor, device to host (synchronous). */
+/* Bytes [offset, offset + bytes) of a tensor, device to host / host to device (synchronous). */
 int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset, void* host,
                                 size_t bytes);
+int wzy_stage_write_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset, const void* host,
+                                 size_t bytes);
 
 /* ---- MTP speculative drafter (MtpEngine, src/wzy_mtp.cuh:405-754) ----
  * One extra decoder layer (attention over its own 1,024-cell INT8 KV ring, MoE of n_exp Q2_0
@@ -153,6 +162,11 @@ int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char* name, size
  * Readable tensors (wzy_stage_read_tensor, layer -1): "mtp.*" weights and the "mtp.act.*"
  * activations of the last step. */
 int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab);
+/* The drafter for weights from files (wzy_stage_mtp_load in wzy_loader.h, or a host's own loader):
+ * allocated with the draft vocabulary dvocab[n_dvocab] (main-vocabulary ids) and its draft head
+ * (those rows of the main LM head: Q8_0 rows as they are, bf16 rows quantised to Q8_0), the KV
+ * ring empty; every other "mtp.*" weight must then be written with wzy_stage_write_tensor. */
+int wzy_stage_mtp_init_vocab(wzy_stage* st, const int* dvocab, int n_dvocab);
 int wzy_stage_mtp_reset(wzy_stage* st);
 int wzy_stage_mtp_set_floor(wzy_stage* st, int kv_floor);
 int wzy_stage_mtp_front(wzy_stage* st, int cell0, const int* next_toks, int n_cells, int src_row0);

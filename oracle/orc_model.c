@@ -124,6 +124,13 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
 
     for (int t = 0; t < T; ++t) {
         int tok = toks[t];
+        if (m->emb_q) {                                    /* stage_one_emb, src/wzy_engine_v2.cu:861-873 */
+            if (tok < 0 || tok >= m->n_vocab) tok = 0;
+            for (int d = 0; d < D; ++d)
+                emb[(size_t) t * D + d] = orc_f16_to_f32(m->emb_s[((size_t) tok * D + d) / 32]) *
+                                          (float) m->emb_q[(size_t) tok * D + d];
+            continue;
+        }
         tok = tok < 0 ? 0 : (tok >= m->n_vocab ? m->n_vocab - 1 : tok);
         for (int d = 0; d < D; ++d) emb[(size_t) t * D + d] = orc_bf16_to_f32(m->emb[(size_t) tok * D + d]);
     }
@@ -229,7 +236,8 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
                     m->head_up_s, D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo, NULL, mixed);
         cur ^= 1;
         if (pre_head) memcpy(pre_head, R[cur], sizeof(float) * (size_t) T * HCD);
-        orc_gemv_bf16(m->head, mixed, logits, m->n_vocab, D, T);
+        if (m->head_q) q8_gemv_f(m->head_q, m->head_s, mixed, logits, m->n_vocab, D, T);
+        else orc_gemv_bf16(m->head, mixed, logits, m->n_vocab, D, T);
         if (greedy) orc_row_argmax(logits, m->n_vocab, T, greedy);
     }
     free(R[0]); free(R[1]); free(nsc); free(lo); free(inj_a); free(inj_f); free(mixed); free(block); free(comb);

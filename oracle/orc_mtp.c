@@ -103,7 +103,9 @@ void orc_mtp_front(orc_mtp* m, int pos, const int* toks, const float* Rin, int T
     for (int t = 0; t < T; ++t) {
         int tok = toks[t];
         if (tok < 0 || tok >= m->n_vocab) tok = 0; /* stage_one_emb, src/wzy_engine_v2.cu:862-863 */
-        for (int d = 0; d < D; ++d) emb[d] = orc_bf16_to_f32(m->emb[(size_t) tok * D + d]);
+        for (int d = 0; d < D; ++d)
+            emb[d] = m->emb_q ? orc_f16_to_f32(m->emb_s[((size_t) tok * D + d) / 32]) * (float) m->emb_q[(size_t) tok * D + d]
+                              : orc_bf16_to_f32(m->emb[(size_t) tok * D + d]);
         rms_rows(emb, m->pre_norm_emb, en, D, m->eps);
         q8_proj(m->fc_emb_q, m->fc_emb_s, en, e2, D, D);
         for (int c = 0; c < HC; ++c) {

@@ -141,6 +141,11 @@ typedef struct orc_model {
     const uint16_t* head;
     const float* cos_tab; const float* sin_tab;
     orc_blob_fn blob; void* blob_ctx;
+    /* Q8_0 token embedding / LM head (codes + fp16 per-32 scales), used instead of emb / head when
+     * not NULL: the embedding row is d*q with an out-of-range id reading row 0 (stage_one_emb,
+     * src/wzy_engine_v2.cu:861-873), the head is dense_q8 (src/wzy_stage_v2.cuh:804-815) */
+    const int8_t* emb_q; const uint16_t* emb_s;
+    const int8_t* head_q; const uint16_t* head_s;
 } orc_model;
 
 /* logits [T x n_vocab], greedy [T] and pre_head [T x hc x n_embd] (optional); returns 0 or -1. */
@@ -210,6 +215,7 @@ typedef struct orc_mtp {
     /* state, updated: INT8 KV ring [ring x kvd] with fp16 per-64 scales, attention floor */
     int8_t* kq; uint16_t* ks; int8_t* vq; uint16_t* vs;
     int kv_floor;
+    const int8_t* emb_q; const uint16_t* emb_s;  /* Q8_0 main embedding table, used instead of emb when not NULL */
 } orc_mtp;
 
 /* K/V append of T cells pos..pos+T-1 (src/wzy_mtp.cuh:658-683).  toks [T] are the embedded tokens,

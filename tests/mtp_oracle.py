@@ -23,7 +23,7 @@ class OrcMtp(C.Structure):
                 ("q_norm", P), ("k_norm", P), ("router", P), ("sgate", P),
                 ("sh_gate_q", P), ("sh_gate_s", P), ("sh_up_q", P), ("sh_up_s", P), ("sh_down_q", P), ("sh_down_s", P),
                 ("experts", P), ("head_q", P), ("head_s", P), ("dvocab", P), ("cos_tab", P), ("sin_tab", P),
-                ("kq", P), ("ks", P), ("vq", P), ("vs", P), ("kv_floor", I32)]
+                ("kq", P), ("ks", P), ("vq", P), ("vs", P), ("kv_floor", I32), ("emb_q", P), ("emb_s", P)]
 
 
 # (tensor name, dtype) of every drafter weight, as the stage registers them
@@ -57,7 +57,11 @@ class OracleMtp:
         m.ring, m.eps = RING, d["eps"]
         A = self.a
         p = lambda k: A[k].ctypes.data
-        m.emb, m.pre_norm_emb, m.pre_norm_hid = p("emb"), p("pre_norm_emb"), p("pre_norm_hid")
+        if "emb.q" in A:                               # a Q8_0 main embedding table
+            m.emb_q, m.emb_s = p("emb.q"), p("emb.s")
+        else:
+            m.emb = p("emb")
+        m.pre_norm_emb, m.pre_norm_hid = p("pre_norm_emb"), p("pre_norm_hid")
         m.fc_emb_q, m.fc_emb_s, m.fc_hid_q, m.fc_hid_s = p("fc_emb.q"), p("fc_emb.s"), p("fc_hid.q"), p("fc_hid.s")
         for h in range(3):
             m.hc_norm[h] = p("hc_norm%d" % h)
@@ -88,7 +92,10 @@ class OracleMtp:
             a[n] = stage.read(-1, "mtp." + n, np.uint16)
         a["experts"] = stage.read(-1, "mtp.experts", np.uint8)
         a["dvocab"] = stage.read(-1, "mtp.dvocab", np.int32)
-        a["emb"] = stage.read(-1, "emb", np.uint16)
+        if cfg.emb_q8:
+            a["emb.q"], a["emb.s"] = stage.read(-1, "emb.q", np.int8), stage.read(-1, "emb.s", np.uint16)
+        else:
+            a["emb"] = stage.read(-1, "emb", np.uint16)
         a["rope_cos"] = stage.read(-1, "rope_cos", np.float32)
         a["rope_sin"] = stage.read(-1, "rope_sin", np.float32)
         return cls(mtp_dims(cfg, n_dv), a)

@@ -38,7 +38,8 @@ class OrcModel(C.Structure):
                 ("layers", C.POINTER(OrcLayer)),
                 ("emb", P), ("head_norm", P), ("head_down_q", P), ("head_down_s", P), ("head_up_q", P),
                 ("head_up_s", P), ("head", P), ("cos_tab", P), ("sin_tab", P),
-                ("blob", BLOB_FN), ("blob_ctx", P)]
+                ("blob", BLOB_FN), ("blob_ctx", P),
+                ("emb_q", P), ("emb_s", P), ("head_q", P), ("head_s", P)]
 
 
 class OrcTrace(C.Structure):
@@ -106,10 +107,17 @@ class OracleModel:
                   "idx_heads", "idx_dim", "idx_blk", "idx_topk", "n_exp", "top_k", "n_ff", "n_vocab", "ctx_max", "eps"):
             setattr(m, f, getattr(cfg, f))
         m.layers = C.cast(L, C.POINTER(OrcLayer))
-        m.emb, m.head_norm = rd(-1, "emb", np.uint16), rd(-1, "head_norm", np.float32)
+        if cfg.emb_q8:
+            m.emb_q, m.emb_s = rd(-1, "emb.q", np.int8), rd(-1, "emb.s", np.uint16)
+        else:
+            m.emb = rd(-1, "emb", np.uint16)
+        m.head_norm = rd(-1, "head_norm", np.float32)
         m.head_down_q, m.head_down_s = rd(-1, "head_down.q", np.int8), rd(-1, "head_down.s", np.uint16)
         m.head_up_q, m.head_up_s = rd(-1, "head_up.q", np.int8), rd(-1, "head_up.s", np.uint16)
-        m.head = rd(-1, "head", np.uint16)
+        if cfg.head_q8:
+            m.head_q, m.head_s = rd(-1, "head.q", np.int8), rd(-1, "head.s", np.uint16)
+        else:
+            m.head = rd(-1, "head", np.uint16)
         m.cos_tab, m.sin_tab = rd(-1, "rope_cos", np.float32), rd(-1, "rope_sin", np.float32)
 
         def blob_fn(ctx, layer, e):

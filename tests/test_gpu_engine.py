@@ -39,12 +39,13 @@ def cfg_spec(c):
 class EngineProc:
     """The engine as a child process; one reader thread queues its stdout lines."""
 
-    def __init__(self, cfg, *args, env=None):
+    def __init__(self, cfg, *args, env=None, model_dir=None):
         if not os.path.exists(ENGINE):
             pytest.fail("wzy_engine not built; run __graft_entry__.build()")
         e = dict(os.environ)
         e.update(env or {})
-        self.p = subprocess.Popen([ENGINE, "--cfg", cfg_spec(cfg), "--model-seed", str(SEED)] + list(args),
+        model = ["--model-dir", str(model_dir)] if model_dir else ["--cfg", cfg_spec(cfg), "--model-seed", str(SEED)]
+        self.p = subprocess.Popen([ENGINE] + model + list(args),
                                   stdin=subprocess.PIPE, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
                                   text=True, bufsize=1, env=e)
         self.q = queue.Queue()
@@ -356,3 +357,44 @@ def test_engine_mtp_speculative_decoding_is_lossless(wz, gpu):
     print("mtp engine: fixed3 drafts %d accepted %d; gated drafts %d accepted %d" % (
         d["draft_n"], d["draft_accepted"], streams["gated"][1]["draft_n"], streams["gated"][1]["draft_accepted"]),
         flush=True)
+
+
+def test_engine_real_weight_files(wz, gpu, tmp_path):
+    """--model-dir with the reference's files (qwen-nvfp4-gptq-dense.gguf with Q8_0 embedding and head,
+    pack/experts.bin, mtp/ and its draft vocabulary): the stage shapes come from the checkpoint, the
+    greedy stream equals an in-process stage loaded from the same files and driven with the engine's
+    schedule, and MTP drafting from the loaded drafter leaves the stream unchanged."""
+    print("case engine_real_weights", flush=True)
+    import gguf_file as gf
+    ref = small_cfg(wzy_amd, ctx_max=512, n_layers=4, topk=64)
+    ck = gf.Checkpoint(wz, ref, 23, str(tmp_path), emb_q8=True, head_q8=True, with_mtp=True, n_dv=400)
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, ref.n_vocab, 11)]
+    streams = {}
+    for name, args in (("plain", []), ("mtp", ["--spec-depth", "2"])):
+        eng = EngineProc(None, "--ctx", "512", *args, model_dir=tmp_path)
+        try:
+            assert eng.ready["mtp"] == (name == "mtp") and eng.ready["split"] == 4
+            _, toks, done = eng.request(greedy_req(prompt, 12))
+            streams[name] = toks
+            assert done["generated"] == 12
+        finally:
+            assert eng.close() == 0
+    assert streams["mtp"] == streams["plain"]
+    # the in-process stage from the same files, the engine's schedule
+    import ctypes as C
+    cfg = wzy_amd.StageCfg()
+    wz.wzy_stage_cfg_from_gguf(str(ck.gguf).encode(), 512, C.byref(cfg))
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_gguf(ck.gguf, ck.experts)
+        for p in range(0, len(prompt) - 1, 8):
+            st.forward(p, prompt[p:min(p + 8, len(prompt) - 1)], run_head=False)
+        expect, tok = [], prompt[-1]
+        for i in range(12):
+            st.forward(len(prompt) - 1 + i, [tok])
+            st.sync()
+            tok = int(st.greedy(1)[0])
+            expect.append(tok)
+        assert streams["plain"] == expect, (streams["plain"], expect)
+    finally:
+        st.close()

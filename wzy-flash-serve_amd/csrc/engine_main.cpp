@@ -10,6 +10,10 @@
 //   --ctx N        / WZY_CTX          context capacity in cells (default 262144)
 //   --batch        / WZY_BATCH>0      multiplexed protocol: "req" ids, TOK <req> <id>, CANCEL <req>
 //   --model-seed S / WZY_MODEL_SEED   seed of the synthetic model weights (default 3)
+//   --model-dir D  / WZY_MODEL_DIR    real weights instead, in the reference's layout: D/qwen-nvfp4-gptq-
+//                                     dense.gguf (shapes from its tensors), D/pack/experts.bin,
+//                                     D/token-embd-bf16.gguf when present, and with --mtp D/mtp/ and the
+//                                     draft vocabulary WZY_DRAFT_VOCAB (default D/mtp/draft_vocab.bin)
 //   --seed S       / WZY_SEED         seed of the sampling generator (default: random_device)
 //   --cfg k=v,...  / WZY_CFG          overrides of wzy_stage_cfg fields (e.g. n_layers=4,n_embd=256)
 //   --device D     / WZY_DEVICE       HIP device (default 0)
@@ -29,6 +33,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <atomic>
 #include <chrono>
@@ -44,6 +49,7 @@
 
 #include "../../include/wzy_engine.h"
 #include "../../include/wzy_kernels.h"
+#include "../../include/wzy_loader.h"
 #include "../../include/wzy_runtime.h"
 #include "../../include/wzy_stage.h"
 
@@ -86,6 +92,8 @@ struct Options {
     bool have_seed = false;
     uint64_t seed = 0;
     std::string cfg;
+    std::string model_dir;        // real weights (empty: synthetic)
+    std::string dvocab;           // MTP draft vocabulary file (real weights)
     int device = 0;
     bool graphs = true;
     bool prof = false;
@@ -115,6 +123,7 @@ bool apply_cfg(wzy_stage_cfg& c, const std::string& spec) {
         {"n_vocab", &c.n_vocab, nullptr},     {"ctx_max", &c.ctx_max, nullptr},
         {"kv_ring", &c.kv_ring, nullptr},     {"kv_sinks", &c.kv_sinks, nullptr},
         {"rope_theta", nullptr, &c.rope_theta}, {"eps", nullptr, &c.eps},
+        {"emb_q8", &c.emb_q8, nullptr},       {"head_q8", &c.head_q8, nullptr},
     };
     size_t at = 0;
     while (at < spec.size()) {
@@ -144,6 +153,8 @@ int parse_options(int argc, char** argv, Options& o) {
     if (const char* e = getenv("WZY_MODEL_SEED")) o.model_seed = strtoull(e, nullptr, 10);
     if (const char* e = getenv("WZY_SEED")) o.have_seed = true, o.seed = strtoull(e, nullptr, 10);
     if (const char* e = getenv("WZY_CFG")) o.cfg = e;
+    if (const char* e = getenv("WZY_MODEL_DIR")) o.model_dir = e;
+    if (const char* e = getenv("WZY_DRAFT_VOCAB")) o.dvocab = e;
     if (const char* e = getenv("WZY_DEVICE")) o.device = atoi(e);
     if (const char* e = getenv("WZY_GRAPHS")) o.graphs = atoi(e) != 0;
     if (const char* e = getenv("WZY_DEC_PROF")) o.prof = atoi(e) != 0;
@@ -168,6 +179,7 @@ int parse_options(int argc, char** argv, Options& o) {
         else if (a == "--model-seed") o.model_seed = strtoull(val(), nullptr, 10);
         else if (a == "--seed") o.have_seed = true, o.seed = strtoull(val(), nullptr, 10);
         else if (a == "--cfg") o.cfg = val();
+        else if (a == "--model-dir") o.model_dir = val();
         else if (a == "--device") o.device = atoi(val());
         else if (a == "--no-graphs") o.graphs = false;
         else if (a == "--mtp") o.mtp = true;
@@ -561,6 +573,12 @@ int main(int argc, char** argv) {
 
     wzy_stage_cfg c;
     wzy_stage_cfg_default(&c, o.ctx);
+    const std::string gguf = o.model_dir + "/qwen-nvfp4-gptq-dense.gguf", emb_file = o.model_dir + "/token-embd-bf16.gguf";
+    const bool have_emb_file = !o.model_dir.empty() && access(emb_file.c_str(), R_OK) == 0;
+    if (!o.model_dir.empty()) {
+        check(wzy_stage_cfg_from_gguf(gguf.c_str(), o.ctx, &c), "cfg_from_gguf");
+        if (have_emb_file) c.emb_q8 = 0;              // the bf16 table replaces the Q8_0 one
+    }
     if (!apply_cfg(c, o.cfg)) {
         fprintf(stderr, "[wzy-engine] bad --cfg/WZY_CFG \"%s\"\n", o.cfg.c_str());
         return 2;
@@ -573,10 +591,20 @@ int main(int argc, char** argv) {
     }
     wzy_stage* st = nullptr;
     check(wzy_stage_create(&c, o.device, &st), "stage_create");
-    check(wzy_stage_load_synthetic(st, o.model_seed, 0), "load_synthetic");
-    if (o.mtp) {
+    if (o.model_dir.empty()) {
+        check(wzy_stage_load_synthetic(st, o.model_seed, 0), "load_synthetic");
+    } else {
+        const std::string experts = o.model_dir + "/pack/experts.bin";
+        check(wzy_stage_load_gguf(st, gguf.c_str(), experts.c_str(), have_emb_file ? emb_file.c_str() : nullptr),
+              "load_gguf");
+    }
+    if (o.mtp && o.model_dir.empty()) {
         const int n_dv = std::max(1, std::min(o.mtp_dvocab, c.n_vocab));
         check(wzy_stage_mtp_init(st, o.model_seed + 1, n_dv), "mtp_init");
+    } else if (o.mtp) {
+        const std::string dir = o.model_dir + "/mtp";
+        const std::string dv = o.dvocab.empty() ? dir + "/draft_vocab.bin" : o.dvocab;
+        check(wzy_stage_mtp_load(st, dir.c_str(), dv.c_str()), "mtp_load");
     }
     check(wzy_stage_set_graphs(st, o.graphs ? 1 : 0), "set_graphs");
     check(wzy_stage_sync(st), "sync");

@@ -73,6 +73,21 @@ template <int N>
 WZY_DEV float bf16_at(const Bf16Raw<N>& r, int j) {
     return (j & 1) ? bf16_hi(r.w[j >> 1]) : bf16_lo(r.w[j >> 1]);
 }
+// N consecutive int8 values as floats (N in {1, 2, 4, 8, 16}; p aligned to N bytes)
+template <int N>
+WZY_DEV void ld_i8_f(const int8_t* p, float (&v)[N]) {
+    if constexpr (N >= 4) {
+        uint32_t w[N / 4];
+        if constexpr (N == 16) { const uint4 u = *(const uint4*) p; w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w; }
+        else if constexpr (N == 8) { const uint2 u = *(const uint2*) p; w[0] = u.x; w[1] = u.y; }
+        else w[0] = *(const uint32_t*) p;
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = (float) (int8_t) (w[j >> 2] >> (8 * (j & 3)));
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = (float) p[j];
+    }
+}
 
 // max over aligned groups of G consecutive lanes (G in {1, 2, 4, 8, 16, 32})
 template <int G>
@@ -170,6 +185,15 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
             const Bf16Raw<VPT> e = ld_bf16_raw<VPT>(a.emb_table + (size_t) tok * D + d0);
 #pragma unroll
             for (int j = 0; j < VPT; ++j) v[j] = bf16_at<VPT>(e, j);
+        } else if (a.emb_q) {
+            // Q8_0 row: d * q per 32-block, an out-of-range id reads row 0 (stage_one_emb,
+            // src/wzy_engine_v2.cu:861-873); a thread's VPT values lie in one 32-block
+            int tok = a.toks[t];
+            if (tok < 0 || tok >= a.n_vocab) tok = 0;
+            ld_i8_f<VPT>(a.emb_q + (size_t) tok * D + d0, v);
+            const float d = h16_to_f(a.emb_s[(size_t) tok * (D / 32) + d0 / 32]);
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) v[j] = d * v[j];
         } else if (a.emb_rows) {
             ld_f32<VPT>(a.emb_rows + (size_t) t * D + d0, v);
         } else {
@@ -446,9 +470,10 @@ int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st) {
                     a.HCLR % 32 == 0 && a.HCLR >= 32 && a.HCLR <= 512,
                 "hc_pre: unsupported shape (HC must be 4, D one of 256/512/768/1024/1280/1536/2048/2560/3072/4096/"
                 "5120, HCLR a multiple of 32 <= 512)");
-    WZY_REQUIRE((a.R_in != nullptr) + (a.emb_table != nullptr) + (a.emb_rows != nullptr) == 1,
-                "hc_pre: exactly one of R_in / emb_table / emb_rows");
-    WZY_REQUIRE(!a.emb_table || a.toks, "hc_pre: embedding mode needs toks");
+    WZY_REQUIRE((a.R_in != nullptr) + (a.emb_table != nullptr) + (a.emb_q != nullptr) + (a.emb_rows != nullptr) == 1,
+                "hc_pre: exactly one of R_in / emb_table / emb_q / emb_rows");
+    WZY_REQUIRE(!(a.emb_table || a.emb_q) || a.toks, "hc_pre: embedding mode needs toks");
+    WZY_REQUIRE(!a.emb_q || a.emb_s, "hc_pre: a Q8_0 embedding table needs its scales");
     WZY_REQUIRE(!a.bo || a.inj_prev, "hc_pre: fold needs inj_prev");
     WZY_REQUIRE(a.R_out && a.norm_w && a.down_q && a.down_s && a.nsc && a.lo_part, "hc_pre: null pointer");
     WZY_REQUIRE(!a.inj_w || a.inj_part, "hc_pre: inject weights need an inj_part output");

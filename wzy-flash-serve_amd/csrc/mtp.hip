@@ -57,7 +57,9 @@ WZY_DEV float max8(float v) {
 // RMSNorm of the embedded tokens and of the residual streams (mtp_rms_norm_rows, src/wzy_mtp.cuh:16-37)
 // ---------------------------------------------------------------------------------------------
 struct MtpInArgs {
-    const uint16_t* emb;
+    const uint16_t* emb;              // bf16 table, or null with the Q8_0 table emb_q / emb_s
+    const int8_t* emb_q;
+    const uint16_t* emb_s;
     int n_vocab;
     const int* toks;                  // [T]
     const float* rin;                 // [T][HC][D]
@@ -76,14 +78,18 @@ __global__ void __launch_bounds__(256) mtp_in_kernel(MtpInArgs a) {
     if (r == 0) {
         int tok = a.toks[t];
         if (tok < 0 || tok >= a.n_vocab) tok = 0;     // stage_one_emb, src/wzy_engine_v2.cu:862-863
-        const uint16_t* src = a.emb + (size_t) tok * D;
+        // embedding value d of the row: bf16, or d * q of the Q8_0 row (stage_one_emb)
+        auto ev = [&](int d) -> float {
+            if (a.emb) return bf16_to_f(a.emb[(size_t) tok * D + d]);
+            return h16_to_f(a.emb_s[(size_t) tok * (D / 32) + d / 32]) * (float) a.emb_q[(size_t) tok * D + d];
+        };
         float ss = 0.f;
         for (int d = tid; d < D; d += 256) {
-            const float v = bf16_to_f(src[d]);
+            const float v = ev(d);
             ss = fmaf(v, v, ss);
         }
         const float sc = 1.0f / sqrtf(block_sum<4>(ss, s_red) / (float) D + a.eps);
-        for (int d = tid; d < D; d += 256) a.en[(size_t) t * D + d] = bf16_to_f(src[d]) * sc * a.g_emb[d];
+        for (int d = tid; d < D; d += 256) a.en[(size_t) t * D + d] = ev(d) * sc * a.g_emb[d];
         return;
     }
     const int c = r - 1;
@@ -467,6 +473,21 @@ __global__ void __launch_bounds__(256) mtp_head_q8_kernel(const uint16_t* __rest
     }
 }
 
+// Draft-head rows copied from a Q8_0 main head (MtpEngine::init, src/wzy_mtp.cuh:543-556): one
+// 32-block per 32 lanes, codes and scale as they are.
+__global__ void __launch_bounds__(256) mtp_head_rows_kernel(const int8_t* __restrict__ main_q,
+                                                            const uint16_t* __restrict__ main_s,
+                                                            const int* __restrict__ dvocab, int D, size_t n_blocks,
+                                                            int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+    const size_t blk = (size_t) blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    if (blk >= n_blocks) return;
+    const size_t row = blk / (D / 32), b = blk % (D / 32);
+    const size_t src = (size_t) dvocab[row] * (D / 32) + b;
+    codes[blk * 32 + lane] = main_q[src * 32 + lane];
+    if (lane == 0) scales[blk] = main_s[src];
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------
@@ -510,11 +531,13 @@ int MtpState::alloc_q8(MtpQ8& m, int rows, int cols, const char* name) {
     return WZY_OK;
 }
 
-int MtpState::init(const MtpDims& d, hipStream_t stream, const uint16_t* emb_table, const float* cos_t,
-                   const float* sin_t) {
+int MtpState::init(const MtpDims& d, hipStream_t stream, const MtpMain& m, const float* cos_t, const float* sin_t) {
     c = d;
     st = stream;
-    emb = emb_table;
+    main = m;
+    WZY_REQUIRE((m.emb != nullptr) != (m.emb_q != nullptr && m.emb_s != nullptr) &&
+                    (m.head != nullptr) != (m.head_q != nullptr && m.head_s != nullptr),
+                "mtp: one bf16 or one Q8_0 main embedding table and LM head required");
     cos_tab = cos_t;
     sin_tab = sin_t;
     WZY_REQUIRE(c.D % 256 == 0 && c.D >= 256 && c.D <= 8192, "mtp: n_embd must be a multiple of 256 <= 8192");
@@ -657,7 +680,23 @@ struct MtpGen {
 };
 }  // namespace
 
-int MtpState::load_synthetic(uint64_t seed, const uint16_t* main_head) {
+int MtpState::build_head(const int* ids) {
+    for (int i = 0; i < c.n_dv; ++i)
+        WZY_REQUIRE(ids[i] >= 0 && ids[i] < c.n_vocab, "mtp: draft vocabulary id %d at row %d out of range", ids[i], i);
+    WZY_HIP_TRY(hipMemcpy(dvocab, ids, (size_t) c.n_dv * 4, hipMemcpyHostToDevice));
+    const size_t nb = (size_t) c.n_dv * (c.D / 32);
+    if (main.head_q)
+        hipLaunchKernelGGL(mtp_head_rows_kernel, dim3((unsigned) ((nb + 7) / 8)), dim3(256), 0, st, main.head_q,
+                           main.head_s, dvocab, c.D, nb, head.q, head.s);
+    else
+        hipLaunchKernelGGL(mtp_head_q8_kernel, dim3((unsigned) ((nb + 7) / 8)), dim3(256), 0, st, main.head, dvocab,
+                           c.D, nb, head.q, head.s);
+    WZY_LAUNCH_CHECK();
+    WZY_HIP_TRY(hipStreamSynchronize(st));
+    return WZY_OK;
+}
+
+int MtpState::load_synthetic(uint64_t seed) {
     const int HCD = c.HC * c.D;
     MtpGen g{seed, {}};
     WZY_TRY(g.normal_f32(pre_norm_emb, c.D, MI_PRE_EMB, 1.0f, 0.02f));
@@ -688,11 +727,7 @@ int MtpState::load_synthetic(uint64_t seed, const uint16_t* main_head) {
     // draft vocabulary: n_dv ids spread evenly over the main vocabulary (identity when n_dv == n_vocab)
     std::vector<int> dv(c.n_dv);
     for (int i = 0; i < c.n_dv; ++i) dv[i] = (int) ((int64_t) i * c.n_vocab / c.n_dv);
-    WZY_HIP_TRY(hipMemcpy(dvocab, dv.data(), dv.size() * 4, hipMemcpyHostToDevice));
-    const size_t nb = (size_t) c.n_dv * (c.D / 32);
-    hipLaunchKernelGGL(mtp_head_q8_kernel, dim3((unsigned) ((nb + 7) / 8)), dim3(256), 0, st, main_head, dvocab, c.D,
-                       nb, head.q, head.s);
-    WZY_LAUNCH_CHECK();
+    WZY_TRY(build_head(dv.data()));
     WZY_TRY(reset_kv());
     WZY_HIP_TRY(hipStreamSynchronize(st));
     loaded = true;
@@ -768,7 +803,8 @@ int hc_read(const MtpState& m, int h, const float* R_in, const float* bo, const 
 int MtpState::enqueue_front(int T, bool with_q) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W && (!with_q || T == 1), "mtp: bad front rows");
     const int D = c.D, HCD = c.HC * D, QD = c.qh * c.hd, KVD = c.kvh * c.hd;
-    MtpInArgs ia{emb, c.n_vocab, d_ctl + 1, rin, pre_norm_emb, pre_norm_hid, en, hn, D, c.HC, c.eps};
+    MtpInArgs ia{main.emb, main.emb_q, main.emb_s, c.n_vocab, d_ctl + 1, rin, pre_norm_emb, pre_norm_hid, en, hn, D,
+                 c.HC, c.eps};
     hipLaunchKernelGGL(mtp_in_kernel, dim3(1 + c.HC, T), dim3(256), 0, st, ia);
     WZY_LAUNCH_CHECK();
     {

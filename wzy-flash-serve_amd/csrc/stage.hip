@@ -26,6 +26,7 @@
 #include "wzy_host.h"
 #include "wzy_moe.h"
 #include "wzy_mtp.h"
+#include "wzy_stage_int.h"
 #include "wzy_qsa.h"
 #include "wzy_reduce.h"
 #include "wzy_synth_impl.h"
@@ -123,10 +124,12 @@ struct wzy_stage {
     std::vector<Layer> L;
     uint8_t* experts = nullptr;     // all layers' NVFP4 expert records
     size_t expert_rec = 0;
-    uint16_t* emb = nullptr;
+    uint16_t* emb = nullptr;        // bf16 token embeddings (cfg.emb_q8 == 0)
+    Q8 emb8;                        // Q8_0 token embeddings (cfg.emb_q8 == 1)
     float* head_norm = nullptr;
     Q8 head_down, head_up;
-    uint16_t* head = nullptr;
+    uint16_t* head = nullptr;       // bf16 LM head (cfg.head_q8 == 0)
+    Q8 head8;                       // Q8_0 LM head (cfg.head_q8 == 1)
     float *cos_tab = nullptr, *sin_tab = nullptr;
 
     // activations / scratch (MAX_W rows)
@@ -343,11 +346,13 @@ int wzy_stage::init_buffers() {
         m.sh_gate_q = g.q; m.sh_gate_s = g.s; m.sh_up_q = u.q; m.sh_up_s = u.s; m.sh_down_q = dn.q; m.sh_down_s = dn.s;
         m.experts = experts + (size_t) l * c.n_exp * expert_rec;
     }
-    WZY_TRY(alloc_t(&emb, (size_t) c.n_vocab * D, false)); reg(-1, "emb", emb, (size_t) c.n_vocab * D * 2);
+    if (c.emb_q8) WZY_TRY(alloc_q8(emb8, c.n_vocab, D, -1, "emb"));
+    else { WZY_TRY(alloc_t(&emb, (size_t) c.n_vocab * D, false)); reg(-1, "emb", emb, (size_t) c.n_vocab * D * 2); }
     WZY_TRY(alloc_t(&head_norm, HCD, false)); reg(-1, "head_norm", head_norm, HCD * 4);
     WZY_TRY(alloc_q8(head_down, c.hc_lr, HCD, -1, "head_down"));
     WZY_TRY(alloc_q8(head_up, HCD, c.hc_lr, -1, "head_up"));
-    WZY_TRY(alloc_t(&head, (size_t) c.n_vocab * D, false)); reg(-1, "head", head, (size_t) c.n_vocab * D * 2);
+    if (c.head_q8) WZY_TRY(alloc_q8(head8, c.n_vocab, D, -1, "head"));
+    else { WZY_TRY(alloc_t(&head, (size_t) c.n_vocab * D, false)); reg(-1, "head", head, (size_t) c.n_vocab * D * 2); }
 
     // RoPE tables: fp64 angles rounded to fp32 (src/wzy_qsa_256k.cuh:34-46)
     {
@@ -488,6 +493,7 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
         HcPreArgs a{};
         if (first) {
             if (emb_host) a.emb_rows = emb_rows;
+            else if (c.emb_q8) { a.emb_q = emb8.q; a.emb_s = emb8.s; a.toks = d_toks; a.n_vocab = c.n_vocab; }
             else { a.emb_table = emb; a.toks = d_toks; a.n_vocab = c.n_vocab; }
         } else {
             a.R_in = R[cur];
@@ -604,7 +610,8 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
         if (run_head == 2) return WZY_OK;          // pre-head residual only (MTP seeding)
         GemvSegs h;
         h.n = 1;
-        h.seg[0] = GemvSeg{head, nullptr, logits, c.n_vocab, GEMV_BF16, c.n_vocab, 0};
+        h.seg[0] = c.head_q8 ? GemvSeg{head8.q, head8.s, logits, c.n_vocab, GEMV_Q8, c.n_vocab, 0}
+                             : GemvSeg{head, nullptr, logits, c.n_vocab, GEMV_BF16, c.n_vocab, 0};
         WZY_TRY(launch_gemv_segs(h, mixed, D, T, st));
         WZY_TRY(launch_row_reduce(logits, c.n_vocab, T, want_top16, d_greedy, want_top16 ? d_top_v : nullptr,
                                   want_top16 ? d_top_i : nullptr, red_ws, st));
@@ -642,10 +649,11 @@ struct Gen {
         wzy_synth_normal_bf16(seed, stream(WZY_S_DENSE, layer, id), n, 0.f, sd, (uint16_t*) buf.data());
         return upload(dst, buf.data(), n * 2);
     }
-    int q8(const Q8& m, int layer, uint32_t id) {
+    // Q8_0 rows of scale `sd` (default 1/sqrt(cols))
+    int q8(const Q8& m, int layer, uint32_t id, float sd = 0.f) {
         const size_t n = (size_t) m.rows * m.cols;
         buf.resize(n + n / 32 * 2);
-        wzy_synth_q8(seed, stream(WZY_S_DENSE, layer, id), m.rows, m.cols, (float) (1.0 / sqrt((double) m.cols)),
+        wzy_synth_q8(seed, stream(WZY_S_DENSE, layer, id), m.rows, m.cols, sd > 0.f ? sd : (float) (1.0 / sqrt((double) m.cols)),
                      (int8_t*) buf.data(), (uint16_t*) (buf.data() + n));
         WZY_TRY(upload(m.q, buf.data(), n));
         return upload(m.s, buf.data() + n, n / 32 * 2);
@@ -729,11 +737,13 @@ static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
                                              s->stream));
         }
     }
-    WZY_TRY(g.normal_bf16(s->emb, (size_t) c.n_vocab * D, -1, TI_EMB, 1.0f));
+    if (c.emb_q8) WZY_TRY(g.q8(s->emb8, -1, TI_EMB, 1.0f));
+    else WZY_TRY(g.normal_bf16(s->emb, (size_t) c.n_vocab * D, -1, TI_EMB, 1.0f));
     WZY_TRY(g.normal_f32(s->head_norm, s->HCD, -1, TI_HEAD_NORM, 1.0f, 0.02f));
     WZY_TRY(g.q8(s->head_down, -1, TI_HEAD_DOWN));
     WZY_TRY(g.q8(s->head_up, -1, TI_HEAD_UP));
-    WZY_TRY(g.normal_bf16(s->head, (size_t) c.n_vocab * D, -1, TI_HEAD, (float) (1.0 / sqrt((double) D))));
+    if (c.head_q8) WZY_TRY(g.q8(s->head8, -1, TI_HEAD));
+    else WZY_TRY(g.normal_bf16(s->head, (size_t) c.n_vocab * D, -1, TI_HEAD, (float) (1.0 / sqrt((double) D))));
     WZY_HIP_TRY(hipStreamSynchronize(s->stream));
     s->loaded = true;
     // an empty context has no history: recurrent state and indexer tail start at zero
@@ -938,7 +948,9 @@ extern "C" int wzy_stage_set_graphs(wzy_stage* st, int enable) {
 // ------------------------------------------------------------------------------------------------
 // MTP drafter
 // ------------------------------------------------------------------------------------------------
-extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
+// Allocate the drafter and fill it: from `seed` (synthetic), or, with `ids`, only its draft head
+// (vocabulary ids[n_dvocab]) for a loader that then writes every "mtp.*" weight.
+static int mtp_create(wzy_stage* st, uint64_t seed, int n_dvocab, const int* ids) {
     WZY_REQUIRE(st && st->loaded, "mtp_init: stage not loaded");
     WZY_REQUIRE(!st->mtp, "mtp_init: the drafter is already initialised");
     const wzy_stage_cfg& c = st->cfg;
@@ -952,8 +964,16 @@ extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
     d.qh = c.qsa_qh; d.kvh = c.qsa_kvh; d.hd = c.qsa_hd; d.n_rot = c.n_rot;
     d.E = c.n_exp; d.K = c.top_k; d.F = c.n_ff;
     d.n_vocab = c.n_vocab; d.n_dv = n_dvocab; d.ctx_max = c.ctx_max; d.eps = c.eps;
-    int rc = m->init(d, st->stream, st->emb, st->cos_tab, st->sin_tab);
-    if (rc == WZY_OK) rc = m->load_synthetic(seed, st->head);
+    MtpMain mm{};
+    if (c.emb_q8) { mm.emb_q = st->emb8.q; mm.emb_s = st->emb8.s; } else mm.emb = st->emb;
+    if (c.head_q8) { mm.head_q = st->head8.q; mm.head_s = st->head8.s; } else mm.head = st->head;
+    int rc = m->init(d, st->stream, mm, st->cos_tab, st->sin_tab);
+    if (rc == WZY_OK) rc = ids ? m->build_head(ids) : m->load_synthetic(seed);
+    if (rc == WZY_OK && ids) {
+        rc = m->reset_kv();
+        if (rc == WZY_OK && hipStreamSynchronize(st->stream) != hipSuccess) rc = WZY_EHIP;
+        m->loaded = rc == WZY_OK;
+    }
     if (rc != WZY_OK) {                 // the drafter's memory goes with m: drop its registry entries
         for (auto it = st->tensors.begin(); it != st->tensors.end();)
             it = it->first.second.rfind("mtp.", 0) == 0 ? st->tensors.erase(it) : std::next(it);
@@ -963,6 +983,38 @@ extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
     st->dev_bytes += m->dev_bytes;
     st->mtp = m.release();
     return WZY_OK;
+}
+
+extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
+    return mtp_create(st, seed, n_dvocab, nullptr);
+}
+
+namespace wzy {
+const wzy_stage_cfg* stage_cfg(const wzy_stage* st) { return &st->cfg; }
+int stage_set_loaded(wzy_stage* st, bool loaded) {
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    st->loaded = false;
+    if (!loaded) return WZY_OK;
+    st->loaded = true;
+    WZY_TRY(wzy_stage_reset_state(st));
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    return WZY_OK;
+}
+void stage_mtp_drop(wzy_stage* st) {
+    if (!st->mtp) return;
+    (void) hipStreamSynchronize(st->stream);
+    st->dev_bytes -= st->mtp->dev_bytes;
+    delete st->mtp;
+    st->mtp = nullptr;
+    for (auto it = st->tensors.begin(); it != st->tensors.end();)
+        it = it->first.second.rfind("mtp.", 0) == 0 ? st->tensors.erase(it) : std::next(it);
+}
+}  // namespace wzy
+
+extern "C" int wzy_stage_mtp_init_vocab(wzy_stage* st, const int* dvocab, int n_dvocab) {
+    WZY_REQUIRE(dvocab, "mtp_init_vocab: null draft vocabulary");
+    return mtp_create(st, 0, n_dvocab, dvocab);
 }
 
 extern "C" int wzy_stage_mtp_reset(wzy_stage* st) {
@@ -1077,6 +1129,17 @@ extern "C" int wzy_stage_read_tensor_range(wzy_stage* st, int layer, const char*
                 "read_tensor_range: [%zu, +%zu) outside the tensor's %zu bytes", offset, bytes, t->bytes);
     WZY_HIP_TRY(hipStreamSynchronize(st->stream));
     WZY_HIP_TRY(hipMemcpy(host, (const char*) t->p + offset, bytes, hipMemcpyDeviceToHost));
+    return WZY_OK;
+}
+extern "C" int wzy_stage_write_tensor_range(wzy_stage* st, int layer, const char* name, size_t offset,
+                                            const void* host, size_t bytes) {
+    WZY_REQUIRE(st && name && host, "write_tensor_range: null argument");
+    Tensor* t = find_tensor(st, layer, name);
+    WZY_REQUIRE(t, "write_tensor_range: no tensor %s in layer %d", name, layer);
+    WZY_REQUIRE(offset <= t->bytes && bytes <= t->bytes - offset,
+                "write_tensor_range: [%zu, +%zu) outside the tensor's %zu bytes", offset, bytes, t->bytes);
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    WZY_HIP_TRY(hipMemcpy((char*) t->p + offset, host, bytes, hipMemcpyHostToDevice));
     return WZY_OK;
 }
 extern "C" int wzy_stage_write_tensor(wzy_stage* st, int layer, const char* name, const void* host, size_t bytes) {

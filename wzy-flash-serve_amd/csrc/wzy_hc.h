@@ -11,6 +11,8 @@ struct HcPreArgs {
     const uint16_t* emb_table;  // bf16 [n_vocab][D]: layer-0 input broadcast to every stream
     const int* toks;            // device [T] token ids (embedding mode)
     int n_vocab;
+    const int8_t* emb_q;        // Q8_0 table [n_vocab][D] codes + emb_s fp16 [n_vocab][D/32] scales:
+    const uint16_t* emb_s;      //   layer-0 input d*q (alternative to emb_table)
     const float* emb_rows;      // fp32 [T][D] rows broadcast to every stream (alternative input)
     const float* bo;            // pending write: block output [T][D] (nullable)
     const float* inj_prev;      // pending write gates [T][HC]

@@ -31,10 +31,16 @@ struct MtpDims {
     float eps;
 };
 
+// The main model's token embedding and LM head, each bf16 or Q8_0 (codes + fp16 per-32 scales).
+struct MtpMain {
+    const uint16_t* emb; const int8_t* emb_q; const uint16_t* emb_s;
+    const uint16_t* head; const int8_t* head_q; const uint16_t* head_s;
+};
+
 struct MtpState {
     MtpDims c{};
     hipStream_t st = nullptr;
-    const uint16_t* emb = nullptr;                 // main model bf16 embedding table [n_vocab][D]
+    MtpMain main{};                                // main model tables [n_vocab][D]
     const float* cos_tab = nullptr;
     const float* sin_tab = nullptr;
     std::vector<void*> allocs;
@@ -95,10 +101,12 @@ struct MtpState {
     int alloc_t(T** p, size_t n, bool zero = true) { return alloc((void**) p, n * sizeof(T), zero); }
     int alloc_q8(MtpQ8& m, int rows, int cols, const char* name);
 
-    int init(const MtpDims& d, hipStream_t stream, const uint16_t* emb_table, const float* cos_t, const float* sin_t);
-    // seeded synthetic weights; the draft head holds the Q8_0 rows of `main_head` (bf16 [n_vocab][D])
-    // picked by the draft vocabulary
-    int load_synthetic(uint64_t seed, const uint16_t* main_head);
+    int init(const MtpDims& d, hipStream_t stream, const MtpMain& m, const float* cos_t, const float* sin_t);
+    // draft vocabulary ids[n_dv] (host) and the draft head rows: the main head's Q8_0 rows copied, or
+    // its bf16 rows quantised to Q8_0
+    int build_head(const int* ids);
+    // seeded synthetic weights, draft vocabulary spread evenly over the main vocabulary
+    int load_synthetic(uint64_t seed);
     int reset_kv();
     int set_floor(int floor);
     // stage (cell0, toks[0..n)) into the control block, chain slot 0

@@ -68,7 +68,8 @@ class StageCfg(C.Structure):
                 ("gdn_hk", I32), ("gdn_hv", I32), ("qsa_qh", I32), ("qsa_kvh", I32), ("qsa_hd", I32),
                 ("n_rot", I32), ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
                 ("n_exp", I32), ("top_k", I32), ("n_ff", I32), ("n_vocab", I32), ("ctx_max", I32),
-                ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32)]
+                ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32),
+                ("emb_q8", I32), ("head_q8", I32)]
 
 
 WZY_MAX_STOPS = 64
@@ -135,12 +136,14 @@ _SIGS = {
     "wzy_stage_set_graphs": (I32, [P, I32], True),
     "wzy_stage_set_trace": (I32, [P, I32], True),
     "wzy_stage_read_tensor_range": (I32, [P, I32, C.c_char_p, SZ, P, SZ], True),
+    "wzy_stage_write_tensor_range": (I32, [P, I32, C.c_char_p, SZ, P, SZ], True),
     "wzy_stage_stream": (P, [P], False),
     "wzy_stage_tensor_bytes": (SZ, [P, I32, C.c_char_p], False),
     "wzy_stage_read_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_write_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32)], True),
     "wzy_stage_mtp_init": (I32, [P, U64, I32], True),
+    "wzy_stage_mtp_init_vocab": (I32, [P, P, I32], True),
     "wzy_stage_mtp_reset": (I32, [P], True),
     "wzy_stage_mtp_set_floor": (I32, [P, I32], True),
     "wzy_stage_mtp_front": (I32, [P, I32, P, I32, I32], True),
@@ -199,6 +202,24 @@ _SIGS = {
     "wzy_f32_to_f16": (C.c_uint16, [F32], False),
     "wzy_f16_to_f32": (F32, [C.c_uint16], False),
     "wzy_f32_to_bf16": (C.c_uint16, [F32], False),
+    # real-weight loaders
+    "wzy_gguf_open": (I32, [C.c_char_p, C.POINTER(P)], True),
+    "wzy_gguf_close": (None, [P], False),
+    "wzy_gguf_n_tensors": (I32, [P], False),
+    "wzy_gguf_find": (I32, [P, C.c_char_p], False),
+    "wzy_gguf_tensor_info": (I32, [P, I32, C.POINTER(C.c_char_p), C.POINTER(I32), C.POINTER(I64), C.POINTER(I32),
+                                   C.POINTER(SZ)], True),
+    "wzy_gguf_tensor_data": (P, [P, I32], False),
+    "wzy_gguf_get_int": (I32, [P, C.c_char_p, C.POINTER(I64)], False),
+    "wzy_gguf_get_float": (I32, [P, C.c_char_p, C.POINTER(C.c_double)], False),
+    "wzy_gguf_get_str": (I32, [P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(SZ)], False),
+    "wzy_q8_0_split": (None, [P, SZ, P, P], False),
+    "wzy_bf16_to_q8_0": (None, [P, SZ, P, P], False),
+    "wzy_bf16_from_f32": (None, [P, SZ, P], False),
+    "wzy_to_f32": (I32, [I32, P, SZ, P], True),
+    "wzy_stage_cfg_from_gguf": (I32, [C.c_char_p, I32, C.POINTER(StageCfg)], True),
+    "wzy_stage_load_gguf": (I32, [P, C.c_char_p, C.c_char_p, C.c_char_p], True),
+    "wzy_stage_mtp_load": (I32, [P, C.c_char_p, C.c_char_p], True),
     # runtime plumbing
     "wzy_dev_count": (I32, [C.POINTER(I32)], True),
     "wzy_dev_set": (I32, [I32], True),
@@ -340,6 +361,11 @@ class Stage:
     def load_synthetic(self, seed, n_ctx):
         self.lib.wzy_stage_load_synthetic(self.h, seed, n_ctx)
 
+    def load_gguf(self, gguf_path, experts_path, emb_path=None):
+        """Real weights: the GGUF checkpoint, the NVFP4 expert pack and optionally a bf16 embedding file."""
+        self.lib.wzy_stage_load_gguf(self.h, str(gguf_path).encode(), str(experts_path).encode(),
+                                     None if emb_path is None else str(emb_path).encode())
+
     def forward(self, pos, toks, run_head=True, save_snaps=False, want_top16=False, snap_offset=0, emb=None):
         import numpy as np
         toks = np.ascontiguousarray(toks, dtype=np.int32)
@@ -400,6 +426,10 @@ class Stage:
     # ---- MTP drafter ----
     def mtp_init(self, seed, n_dvocab):
         self.lib.wzy_stage_mtp_init(self.h, int(seed), int(n_dvocab))
+
+    def mtp_load(self, mtp_dir, dvocab_path):
+        """The drafter from dense.txt / dense.bin / experts.bin in mtp_dir and a draft vocabulary file."""
+        self.lib.wzy_stage_mtp_load(self.h, str(mtp_dir).encode(), str(dvocab_path).encode())
 
     def mtp_reset(self):
         self.lib.wzy_stage_mtp_reset(self.h)
