@@ -89,6 +89,28 @@ int wzy_engine_verify_top16(const float* top_v, const int* top_i, const wzy_gen_
  * prefix of ids[0 .. n_ids-2], else 0 (src/wzy_engine_v2.cu:1963-1970). */
 int wzy_engine_reuse_prefix(const int* state, int n_state, const int* ids, int n_ids);
 
+/* What a new prompt does with the active session and the one parked session (the reference's
+ * two-slot longest-common-prefix reuse, src/wzy_engine_v2.cu:1962-1997):
+ *   WZY_SESS_REUSE       the active state's tokens are a prefix of the prompt: keep it (*reused =
+ *                        n_active cells);
+ *   WZY_SESS_SWAP        the parked session's tokens are a prefix and the active session is worth
+ *                        keeping: park the active one, restore the parked one (*reused = n_parked);
+ *   WZY_SESS_RESTORE     the parked session matches, the active one is dropped (the parked copy
+ *                        stays parked; *reused = n_parked);
+ *   WZY_SESS_PARK_RESET  neither matches; the active session is parked, then the state is reset;
+ *   WZY_SESS_RESET       neither matches; the state is reset (nothing worth parking, no_reuse, or
+ *                        a small side request must not evict a parked session twice its size).
+ * A session is worth parking when it holds WZY_PARK_MIN ..WZY_PARK_MAX cells. */
+#define WZY_SESS_REUSE 0
+#define WZY_SESS_SWAP 1
+#define WZY_SESS_RESTORE 2
+#define WZY_SESS_PARK_RESET 3
+#define WZY_SESS_RESET 4
+#define WZY_PARK_MIN 64
+#define WZY_PARK_MAX 98304
+int wzy_engine_session_plan(const int* active, int n_active, const int* parked, int n_parked, const int* ids,
+                            int n_ids, int no_reuse, int* reused);
+
 /* Tunables of the drafter's confidence gates (the reference reads them from WZY_SPEC_DEPTH,
  * WZY_SPEC_MIN_P and WZY_SPEC_GATE, src/wzy_engine_v2.cu:1436-1450). */
 typedef struct wzy_spec_gates {

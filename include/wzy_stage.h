@@ -93,6 +93,24 @@ int wzy_stage_commit_window_state(wzy_stage* st, int acc_idx, int acc_pos);
 int wzy_stage_reset_state(wzy_stage* st);
 int wzy_stage_sync(wzy_stage* st);
 
+/* ---- Parked sessions (ParkedSession, save_session_state / restore_session_state,
+ * src/wzy_engine_v2.cu:1636-1842) ----
+ * A session's state is what the decode of its next token reads: per GDN layer the conv history and
+ * the fp32 recurrent state; per QSA layer the INT8 K/V and scales of cells 0 .. n_cells-1, the
+ * indexer tail, placeholder and pooled keys of the blocks those cells reach; and, when the drafter
+ * is initialised, its KV ring and attention floor.  The reference copies them to pinned host
+ * memory; here a slot is a buffer in the same GPU's HBM (a 98,304-cell session of the BASELINE
+ * model is 1.4 GB), grown on the first save that needs more and kept until the stage is destroyed.
+ * save copies the live state into `slot`, restore copies a slot back (the slot keeps its copy);
+ * each is one copy launch on the stage stream and returns after it has finished.
+ * wzy_stage_session_cells() is the slot's cell count, -1 when empty; clear empties a slot. */
+#define WZY_SESSION_SLOTS 2
+size_t wzy_stage_session_bytes(const wzy_stage* st, int n_cells);
+int wzy_stage_session_save(wzy_stage* st, int slot, int n_cells);
+int wzy_stage_session_restore(wzy_stage* st, int slot);
+int wzy_stage_session_cells(const wzy_stage* st, int slot);
+int wzy_stage_session_clear(wzy_stage* st, int slot);
+
 /* Results of the last forward with run_head (after sync); host outputs. */
 int wzy_stage_greedy_ids(wzy_stage* st, int* out, int T);
 int wzy_stage_top16(wzy_stage* st, float* v, int* ids, int T);

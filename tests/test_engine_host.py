@@ -143,6 +143,53 @@ def test_reuse_prefix(wz, state, ids, want):
     assert wz.wzy_engine_reuse_prefix(s.ctypes.data, len(state), i.ctypes.data, len(ids)) == want
 
 
+# ---- two-slot session plan (src/wzy_engine_v2.cu:1962-1997) -----------------------------------------
+
+def _seq(start, n):
+    return list(range(start, start + n))
+
+
+A100 = _seq(1000, 100)       # a session worth parking (64 <= n <= 98304)
+P300 = _seq(5000, 300)
+
+
+@pytest.mark.parametrize("active,parked,ids,no_reuse,want,reused", [
+    # the active state is a prefix of the prompt: kept, whatever is parked
+    (A100, P300, A100 + [7, 8], 0, "REUSE", 100),
+    (_seq(1, 10), [], _seq(1, 12), 0, "REUSE", 10),
+    # the parked session is a prefix and the active one is worth keeping: they trade places
+    (A100, P300, P300 + [9], 0, "SWAP", 300),
+    (_seq(1, 64), P300, P300 + [9, 9], 0, "SWAP", 300),
+    # ... not worth keeping (under 64 cells, empty, or over 98,304): the parked copy comes back, stays parked
+    (_seq(1, 63), P300, P300 + [9], 0, "RESTORE", 300),
+    ([], P300, P300 + [9], 0, "RESTORE", 300),
+    (_seq(1, 98305), P300, P300 + [9], 0, "RESTORE", 300),
+    # the parked tokens must leave at least one prompt id to feed
+    (A100, P300, P300, 0, "RESET", 0),
+    # nothing matches: park the active session unless a parked one is more than twice its size
+    (A100, [], _seq(1, 5), 0, "PARK_RESET", 0),
+    (_seq(1, 150), P300, _seq(1, 5), 0, "PARK_RESET", 0),
+    (_seq(1, 149), P300, _seq(1, 5), 0, "RESET", 0),
+    (_seq(1, 63), [], _seq(1, 5), 0, "RESET", 0),
+    (_seq(1, 98305), [], _seq(1, 5), 0, "RESET", 0),
+    # the active session diverges from the prompt after a common prefix: not a prefix, not reused
+    (A100, [], A100[:50] + [3] + A100[51:] + [4], 0, "PARK_RESET", 0),
+    # no_reuse: reset, never park or restore
+    (A100, P300, A100 + [7], 1, "RESET", 0),
+    (A100, P300, P300 + [7], 1, "RESET", 0),
+])
+def test_session_plan(wz, active, parked, ids, no_reuse, want, reused):
+    names = {wzy_amd.SESS_REUSE: "REUSE", wzy_amd.SESS_SWAP: "SWAP", wzy_amd.SESS_RESTORE: "RESTORE",
+             wzy_amd.SESS_PARK_RESET: "PARK_RESET", wzy_amd.SESS_RESET: "RESET"}
+    a = np.array(active or [0], np.int32)
+    p = np.array(parked or [0], np.int32)
+    i = np.array(ids, np.int32)
+    r = C.c_int32(-1)
+    got = wz.wzy_engine_session_plan(a.ctypes.data, len(active), p.ctypes.data, len(parked), i.ctypes.data, len(ids),
+                                     no_reuse, C.byref(r))
+    assert names[got] == want and r.value == reused
+
+
 # ---- samplers ------------------------------------------------------------------------------------
 
 def test_greedy_is_argmax_with_lowest_index_on_ties(wz):

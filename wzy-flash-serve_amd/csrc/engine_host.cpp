@@ -350,6 +350,24 @@ extern "C" int wzy_engine_reuse_prefix(const int* state, int n_state, const int*
     return m == n_state ? m : 0;
 }
 
+extern "C" int wzy_engine_session_plan(const int* active, int n_active, const int* parked, int n_parked,
+                                       const int* ids, int n_ids, int no_reuse, int* reused) {
+    int r = 0;
+    auto keep = [](int n) { return n >= WZY_PARK_MIN && n <= WZY_PARK_MAX; };
+    if (reused) *reused = 0;
+    if (!no_reuse && (r = wzy_engine_reuse_prefix(active, n_active, ids, n_ids)) > 0) {
+        if (reused) *reused = r;
+        return WZY_SESS_REUSE;
+    }
+    if (!no_reuse && (r = wzy_engine_reuse_prefix(parked, n_parked, ids, n_ids)) > 0) {
+        if (reused) *reused = r;
+        return keep(n_active) ? WZY_SESS_SWAP : WZY_SESS_RESTORE;
+    }
+    if (!no_reuse && keep(n_active) && (n_parked <= 0 || 2LL * n_active >= (long long) n_parked))
+        return WZY_SESS_PARK_RESET;
+    return WZY_SESS_RESET;
+}
+
 extern "C" int wzy_engine_mtp_gate(const int* toks, const float* probs, int n, int next_tok, int last_cell,
                                    int ctx_max, const wzy_gen_cfg* cfg, int max_drafts,
                                    const wzy_spec_gates* gates) {

@@ -230,8 +230,29 @@ class Engine {
         const wzy_gen_cfg& g = r.cfg;
         const int n = (int) ids.size();
 
-        int reused = g.no_reuse ? 0 : wzy_engine_reuse_prefix(state_.data(), (int) state_.size(), ids.data(), n);
-        if (reused == 0) {
+        // Two-slot prefix reuse (src/wzy_engine_v2.cu:1962-1997): keep the active state, or bring
+        // the parked session back (parking the active one in its place when it is worth keeping),
+        // or park the active session before the reset for an unrelated prompt.
+        int reused = 0;
+        const int plan = wzy_engine_session_plan(state_.data(), (int) state_.size(), parked_.data(),
+                                                 (int) parked_.size(), ids.data(), n, g.no_reuse, &reused);
+        bool restored_park = false;
+        if (plan == WZY_SESS_SWAP) {
+            const int tmp = parked_slot_ ^ 1;
+            check(wzy_stage_session_save(st_, tmp, (int) state_.size()), "session_save");
+            check(wzy_stage_session_restore(st_, parked_slot_), "session_restore");
+            std::swap(state_, parked_);
+            parked_slot_ = tmp;
+            restored_park = true;
+        } else if (plan == WZY_SESS_RESTORE) {
+            check(wzy_stage_session_restore(st_, parked_slot_), "session_restore");
+            state_ = parked_;
+            restored_park = true;
+        } else if (plan == WZY_SESS_PARK_RESET) {
+            check(wzy_stage_session_save(st_, parked_slot_, (int) state_.size()), "session_save");
+            parked_ = state_;
+        }
+        if (plan == WZY_SESS_PARK_RESET || plan == WZY_SESS_RESET) {
             check(wzy_stage_reset_state(st_), "reset_state");
             state_.clear();
         }
@@ -272,6 +293,8 @@ class Engine {
         f.reused = reused;
         f.read = n - reused;
         f.prompt_ms = pf_ms;
+        f.restored_park = restored_park ? 1 : 0;
+        f.parked_tokens = (int) parked_.size();
         if (r.json) emit_fmt(WZY_FMT_PREFILL, f);
         else say("output :");
 
@@ -408,11 +431,14 @@ class Engine {
         emit_fmt(WZY_FMT_DONE, f);
     }
 
+    // RESET: empty state, no parked session (src/wzy_engine_v2.cu:1851)
     void reset() {
         check(wzy_stage_reset_state(st_), "reset_state");
         if (o_.mtp) check(wzy_stage_mtp_reset(st_), "mtp_reset");
         check(wzy_stage_sync(st_), "sync");
+        for (int s = 0; s < WZY_SESSION_SLOTS; ++s) check(wzy_stage_session_clear(st_, s), "session_clear");
         state_.clear();
+        parked_.clear();
     }
 
   private:
@@ -514,6 +540,8 @@ class Engine {
     std::mt19937 rng_;
     Mode mode_ = kGreedy;
     std::vector<int> state_;      // tokens whose cells the resident state holds
+    std::vector<int> parked_;     // tokens of the parked session (empty: none)
+    int parked_slot_ = 0;         // stage session slot holding it; the other slot is the swap spare
     std::vector<float> logits_;
     int greedy_[WZY_MAX_W] = {};
     float top_v_[WZY_MAX_W * 16] = {};

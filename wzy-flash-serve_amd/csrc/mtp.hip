@@ -588,7 +588,7 @@ int MtpState::init(const MtpDims& d, hipStream_t stream, const MtpMain& m, const
     WZY_TRY(alloc_t(&kv.ks, (size_t) MTP_RING * (KVD / 64))); reg("mtp.kv_ks", kv.ks, (size_t) MTP_RING * (KVD / 64) * 2);
     WZY_TRY(alloc_t(&kv.vq, (size_t) MTP_RING * KVD)); reg("mtp.kv_v", kv.vq, (size_t) MTP_RING * KVD);
     WZY_TRY(alloc_t(&kv.vs, (size_t) MTP_RING * (KVD / 64))); reg("mtp.kv_vs", kv.vs, (size_t) MTP_RING * (KVD / 64) * 2);
-    WZY_TRY(alloc_t(&d_floor, 1));
+    WZY_TRY(alloc_t(&d_floor, 1)); reg("mtp.kv_floor", d_floor, sizeof(int));
     WZY_TRY(alloc_t(&d_ctl, MTP_CTL_INTS));
 
     WZY_TRY(alloc_t(&rin, (size_t) W * HCD)); reg("mtp.act.rin", rin, (size_t) W * HCD * 4);

@@ -79,6 +79,25 @@ __global__ void __launch_bounds__(256) commit_kernel(const CommitJob* __restrict
         ((uint4*) dst)[i] = src[i];
 }
 
+// Plain device-to-device copies, every job of a table in one launch: grid (COPY_WGS, jobs).
+// Pointers are 16-byte aligned; a job's last bytes % 16 are copied one byte per lane.
+struct CopyJob {
+    unsigned char* dst;
+    const unsigned char* src;
+    size_t bytes;
+};
+constexpr int COPY_WGS = 128;
+constexpr int SESSION_MAX_JOBS = 1024;
+
+__global__ void __launch_bounds__(256) copy_jobs_kernel(const CopyJob* __restrict__ jobs) {
+    const CopyJob j = jobs[blockIdx.y];
+    const size_t n16 = j.bytes / 16;
+    const size_t stride = (size_t) COPY_WGS * 256;
+    for (size_t i = (size_t) blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+        ((uint4*) j.dst)[i] = ((const uint4*) j.src)[i];
+    for (size_t i = n16 * 16 + (size_t) blockIdx.x * 256 + threadIdx.x; i < j.bytes; i += stride) j.dst[i] = j.src[i];
+}
+
 struct Q8 {
     int8_t* q = nullptr;
     uint16_t* s = nullptr;
@@ -173,6 +192,18 @@ struct wzy_stage {
     bool loaded = false;
     MtpState* mtp = nullptr;        // MTP drafter (wzy_stage_mtp_init)
 
+    // parked sessions: per slot one HBM buffer holding a copy of the session state, and the
+    // device tables of the copies that save and restore it (one copy_jobs_kernel launch each)
+    struct SessionSlot {
+        unsigned char* buf = nullptr;
+        size_t cap = 0;
+        CopyJob* jobs = nullptr;        // [2][SESSION_MAX_JOBS]: save, restore
+        int n_jobs = 0;
+        int n_cells = -1;               // -1: empty
+    };
+    SessionSlot sess[WZY_SESSION_SLOTS];
+    void session_regions(int n_cells, std::vector<std::pair<void*, size_t>>& out) const;
+
     std::map<unsigned long long, hipGraphExec_t> graph_execs;
     CommitJob* commit_jobs = nullptr;   // device table of commit_window_state's copies
     int n_commit_jobs = 0;
@@ -207,6 +238,10 @@ wzy_stage::~wzy_stage() {
     (void) hipSetDevice(dev);
     if (stream) (void) hipStreamSynchronize(stream);
     delete mtp;
+    for (auto& sl : sess) {
+        if (sl.buf) (void) hipFree(sl.buf);
+        if (sl.jobs) (void) hipFree(sl.jobs);
+    }
     for (auto& kv : graph_execs)
         if (kv.second) (void) hipGraphExecDestroy(kv.second);
     for (void* p : allocs) (void) hipFree(p);
@@ -907,6 +942,138 @@ extern "C" int wzy_stage_reset_state(wzy_stage* st) {
         }
     }
     WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    return WZY_OK;
+}
+
+// The device regions of a session of n_cells cells, in a fixed order (save and restore walk the
+// same list): GDN conv history + state per GDN layer; per QSA layer the indexer tail, placeholder,
+// the pooled keys of blocks 0 .. n_cells/idx_blk + 1 (the last closed block and the open one), and
+// the K/V codes and scales of cells 0 .. n_cells-1; then the drafter's KV ring and floor.
+// reference: save_session_state (src/wzy_engine_v2.cu:1660-1749).
+void wzy_stage::session_regions(int n_cells, std::vector<std::pair<void*, size_t>>& out) const {
+    const wzy_stage_cfg& c = cfg;
+    out.clear();
+    const size_t nc = (size_t) n_cells;
+    const size_t blocks = std::min((size_t) max_b, nc / (size_t) c.idx_blk + 2);
+    for (const Layer& w : L) {
+        if (!w.qsa) {
+            out.emplace_back(w.conv_hist, (size_t) QKV * 3 * 4);
+            out.emplace_back(w.ssm, (size_t) c.gdn_hv * 128 * 128 * 4);
+        } else {
+            out.emplace_back(w.ix.tail, (size_t) (c.idx_blk - 1) * c.idx_dim * 4);
+            out.emplace_back(w.ix.dead, (size_t) c.idx_dim * 4);
+            out.emplace_back(w.ix.pooled, blocks * c.idx_dim * 2);
+            if (nc > 0) {
+                out.emplace_back(w.kv.kq, nc * KVD);
+                out.emplace_back(w.kv.ks, nc * (KVD / 64) * 2);
+                out.emplace_back(w.kv.vq, nc * KVD);
+                out.emplace_back(w.kv.vs, nc * (KVD / 64) * 2);
+            }
+        }
+    }
+    if (mtp) {
+        const size_t kvd = (size_t) mtp->c.kvh * mtp->c.hd;
+        out.emplace_back(mtp->kv.kq, (size_t) MTP_RING * kvd);
+        out.emplace_back(mtp->kv.ks, (size_t) MTP_RING * (kvd / 64) * 2);
+        out.emplace_back(mtp->kv.vq, (size_t) MTP_RING * kvd);
+        out.emplace_back(mtp->kv.vs, (size_t) MTP_RING * (kvd / 64) * 2);
+        out.emplace_back(mtp->d_floor, sizeof(int));
+    }
+}
+
+static size_t session_total(const std::vector<std::pair<void*, size_t>>& regs) {
+    size_t t = 0;
+    for (const auto& r : regs) t += (r.second + 255) & ~(size_t) 255;
+    return t;
+}
+
+extern "C" size_t wzy_stage_session_bytes(const wzy_stage* st, int n_cells) {
+    if (!st || n_cells < 0 || n_cells > st->cfg.ctx_max) return 0;
+    std::vector<std::pair<void*, size_t>> regs;
+    st->session_regions(n_cells, regs);
+    return session_total(regs);
+}
+
+extern "C" int wzy_stage_session_save(wzy_stage* st, int slot, int n_cells) {
+    WZY_REQUIRE(st, "session_save: null stage");
+    WZY_REQUIRE(slot >= 0 && slot < WZY_SESSION_SLOTS, "session_save: slot %d out of range", slot);
+    WZY_REQUIRE(n_cells >= 0 && n_cells <= st->cfg.ctx_max, "session_save: %d cells outside 0..%d", n_cells,
+                st->cfg.ctx_max);
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    auto& sl = st->sess[slot];
+    std::vector<std::pair<void*, size_t>> regs;
+    st->session_regions(n_cells, regs);
+    WZY_REQUIRE((int) regs.size() <= SESSION_MAX_JOBS, "session_save: %zu regions", regs.size());
+    const size_t need = session_total(regs);
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    if (need > sl.cap) {
+        if (sl.buf) {
+            WZY_HIP_TRY(hipFree(sl.buf));
+            st->dev_bytes -= sl.cap;
+        }
+        sl.buf = nullptr;
+        sl.cap = 0;
+        sl.n_cells = -1;
+        if (hipMalloc((void**) &sl.buf, need) != hipSuccess) {
+            (void) hipGetLastError();
+            sl.buf = nullptr;
+            set_error("session_save: hipMalloc(%zu) for slot %d failed", need, slot);
+            return WZY_ENOMEM;
+        }
+        sl.cap = need;
+        st->dev_bytes += need;
+    }
+    if (!sl.jobs) {
+        void* p = nullptr;
+        WZY_HIP_TRY(hipMalloc(&p, 2 * SESSION_MAX_JOBS * sizeof(CopyJob)));
+        sl.jobs = (CopyJob*) p;
+    }
+    std::vector<CopyJob> jobs(2 * regs.size());
+    size_t off = 0;
+    for (size_t i = 0; i < regs.size(); ++i) {
+        unsigned char* live = (unsigned char*) regs[i].first;
+        jobs[i] = CopyJob{sl.buf + off, live, regs[i].second};                   // save
+        jobs[regs.size() + i] = CopyJob{live, sl.buf + off, regs[i].second};     // restore
+        off += (regs[i].second + 255) & ~(size_t) 255;
+    }
+    WZY_HIP_TRY(hipMemcpy(sl.jobs, jobs.data(), regs.size() * sizeof(CopyJob), hipMemcpyHostToDevice));
+    WZY_HIP_TRY(hipMemcpy(sl.jobs + SESSION_MAX_JOBS, jobs.data() + regs.size(), regs.size() * sizeof(CopyJob),
+                          hipMemcpyHostToDevice));
+    sl.n_jobs = (int) regs.size();
+    hipLaunchKernelGGL(copy_jobs_kernel, dim3(COPY_WGS, sl.n_jobs), dim3(256), 0, st->stream, sl.jobs);
+    WZY_HIP_TRY(hipGetLastError());
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    sl.n_cells = n_cells;
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_session_restore(wzy_stage* st, int slot) {
+    WZY_REQUIRE(st, "session_restore: null stage");
+    WZY_REQUIRE(slot >= 0 && slot < WZY_SESSION_SLOTS, "session_restore: slot %d out of range", slot);
+    auto& sl = st->sess[slot];
+    WZY_REQUIRE(sl.n_cells >= 0, "session_restore: slot %d is empty", slot);
+    // the drafter could have been created after the save: the region list must be the saved one
+    std::vector<std::pair<void*, size_t>> regs;
+    st->session_regions(sl.n_cells, regs);
+    WZY_REQUIRE((int) regs.size() == sl.n_jobs, "session_restore: slot %d was saved with another layout", slot);
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    hipLaunchKernelGGL(copy_jobs_kernel, dim3(COPY_WGS, sl.n_jobs), dim3(256), 0, st->stream,
+                       sl.jobs + SESSION_MAX_JOBS);
+    WZY_HIP_TRY(hipGetLastError());
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    st->have_head = st->have_pre_head = false;
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_session_cells(const wzy_stage* st, int slot) {
+    if (!st || slot < 0 || slot >= WZY_SESSION_SLOTS) return -1;
+    return st->sess[slot].n_cells;
+}
+
+extern "C" int wzy_stage_session_clear(wzy_stage* st, int slot) {
+    WZY_REQUIRE(st, "session_clear: null stage");
+    WZY_REQUIRE(slot >= 0 && slot < WZY_SESSION_SLOTS, "session_clear: slot %d out of range", slot);
+    st->sess[slot].n_cells = -1;
     return WZY_OK;
 }
 

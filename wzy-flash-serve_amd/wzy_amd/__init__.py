@@ -104,6 +104,9 @@ class LineFields(C.Structure):
 
 LINE_KINDS = {0: "SKIP", 1: "PING", 2: "RESET", 3: "SAVE_PROFILE", 4: "QUIT", 5: "CANCEL", 6: "REQUEST"}
 FMT_PREFILL, FMT_DONE, FMT_DONE_EMPTY = 1, 2, 3
+# wzy_engine_session_plan results (include/wzy_engine.h)
+SESS_REUSE, SESS_SWAP, SESS_RESTORE, SESS_PARK_RESET, SESS_RESET = 0, 1, 2, 3, 4
+SESSION_SLOTS = 2
 
 # name -> (restype, argtypes, checked)
 _SIGS = {
@@ -114,6 +117,7 @@ _SIGS = {
     "wzy_engine_verify_full": (I32, [P, I32, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
     "wzy_engine_verify_top16": (I32, [P, P, C.POINTER(GenCfg), P, I32, I32, F32, C.POINTER(I32)], False),
     "wzy_engine_reuse_prefix": (I32, [P, I32, P, I32], False),
+    "wzy_engine_session_plan": (I32, [P, I32, P, I32, P, I32, I32, C.POINTER(I32)], False),
     "wzy_engine_spec_gates_default": (None, [C.POINTER(SpecGates)], False),
     "wzy_engine_mtp_gate": (I32, [P, P, I32, I32, I32, I32, C.POINTER(GenCfg), I32, C.POINTER(SpecGates)], False),
     "wzy_engine_format": (I32, [I32, C.POINTER(LineFields), C.c_char_p, I32], False),
@@ -129,6 +133,11 @@ _SIGS = {
     "wzy_stage_commit_window_state": (I32, [P, I32, I32], True),
     "wzy_stage_reset_state": (I32, [P], True),
     "wzy_stage_sync": (I32, [P], True),
+    "wzy_stage_session_bytes": (SZ, [P, I32], False),
+    "wzy_stage_session_save": (I32, [P, I32, I32], True),
+    "wzy_stage_session_restore": (I32, [P, I32], True),
+    "wzy_stage_session_cells": (I32, [P, I32], False),
+    "wzy_stage_session_clear": (I32, [P, I32], True),
     "wzy_stage_greedy_ids": (I32, [P, P, I32], True),
     "wzy_stage_top16": (I32, [P, P, P, I32], True),
     "wzy_stage_logits": (I32, [P, P, I32], True),
