@@ -130,6 +130,16 @@ size_t wzy_moe_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int T
 int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Dense projection of a prefill chunk on bf16 MFMA: y[m * ldy + n] = sum_k a[m * lda + k] * W[n][k]
+ * for m < M, n < N, with a bf16 [M x lda] and W Q8_0 (wq codes [N x K] + ws fp16 scales [N x K/32],
+ * each code * scale rounded to bf16) or bf16 (wb [N x K], wq NULL); fp32 accumulation; output fp32
+ * (y) or rounded to bf16 (yb, y NULL).  K a multiple of 64, lda >= K a multiple of 8, ldy >= N.
+ * Replaces the prefill's dequantise-then-cublasGemmEx pairs (dequant_q8p_to_fp16 /
+ * bf16_to_fp16_vec + tc_gemm_fp16, src/wzy_prefill_tc.cuh:681-711; src/wzy_kernels_v2.cuh:1836-1865)
+ * with bf16 operands. */
+int wzy_gemm_bf16(const uint16_t* a, int lda, int M, int K, const int8_t* wq, const uint16_t* ws, const uint16_t* wb,
+                  int N, float* y, uint16_t* yb, int ldy, void* stream);
+
 /* Bytes of device workspace wzy_moe_prefill needs for a chunk of n_tok tokens. */
 size_t wzy_moe_prefill_workspace_bytes(int n_embd, int n_ff, int n_exp, int top_k, int n_tok);
 

@@ -79,6 +79,23 @@ int wzy_stage_load_synthetic(wzy_stage* st, uint64_t seed, int n_ctx);
  * Replaces StageGpu::record_forward (src/wzy_stage_v2.cuh:476-857). */
 int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb, const int* toks, int T, int run_head,
                              int save_snaps, int want_top16, int snap_offset);
+/* Chunked prefill of B prompt cells at positions pos .. pos+B-1 (toks [B] host token ids, copied
+ * before the call returns): every layer runs over all B rows at once, with the dense projections
+ * on bf16 MFMA GEMMs (activations and dequantised Q8_0 weights rounded to bf16, fp32 accumulation),
+ * the GDN recurrence sequential over the rows, the QSA rows selecting and attending as a decode row
+ * would (attention with the reference prefill kernel's fp16 operands), and the MoE block of
+ * wzy_moe_prefill.  Updates the decode state of those cells (GDN conv/ssm, KV cells, indexer keys)
+ * and leaves the final residual rows [B x hc x n_embd] as the pre-head rows of the call
+ * (wzy_stage_pre_head, wzy_stage_mtp_front).  No logits.  Asynchronous (wzy_stage_sync).  The
+ * first call with a larger B allocates the workspace (BASELINE shapes: about 0.25 MB per row).
+ * Needs hc_lr a multiple of 64, n_exp a multiple of 64 (<= 1024), n_ff of 128, idx_dim 128.
+ * Replaces PrefillStageCtx::run_stage_prefill (src/wzy_prefill_tc.cuh:546-1058) for one stage
+ * holding every layer (no expert streaming: every expert is resident). */
+int wzy_stage_prefill(wzy_stage* st, int pos, const int* toks, int B);
+/* Same, timed: us_parts[6] = microseconds spent in the attention-half HC reads, GDN blocks, QSA
+ * blocks, FFN-half HC reads, MoE blocks and the rest (HIP events between the parts; synchronous).
+ * Counterpart of the reference's WZY_PF_PROF timers (src/wzy_prefill_tc.cuh:734-741,1048-1051). */
+int wzy_stage_prefill_time(wzy_stage* st, int pos, const int* toks, int B, float* us_parts);
 /* Cold-expert servicing and VRAM promotion: nothing is cold on one MI355X (no-ops, kept so a
  * reference driver links unchanged).  Replace StageGpu::service_cold_layers / promote_cold
  * (src/wzy_stage_v2.cuh:932,960). */

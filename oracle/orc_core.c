@@ -317,70 +317,96 @@ static float q8_bf16_value(const int8_t* q, const uint16_t* s, int cols, int r, 
 }
 
 int orc_moe_prefill(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts) {
+    return orc_moe_prefill_fn(w, x, T, comb, ids, wts, NULL, NULL, NULL, 0);
+}
+
+int orc_moe_prefill_fn(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
+                       float* logits_out, orc_blob_fn blob_fn, void* blob_ctx, int layer) {
     const int D = w->n_embd, F = w->n_ff, E = w->n_exp, K = w->top_k;
-    float* xb = (float*) malloc(sizeof(float) * (size_t) D);
     float* logits = (float*) malloc(sizeof(float) * (size_t) T * E);
     float* sg = (float*) malloc(sizeof(float) * (size_t) T);
-    float* act = (float*) malloc(sizeof(float) * (size_t) F);
-    double* out = (double*) malloc(sizeof(double) * (size_t) D);
     int rc = 0;
-    for (int t = 0; t < T; ++t) {
-        for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
-        for (int e = 0; e < E; ++e) {
-            double a = 0.0;
-            for (int d = 0; d < D; ++d) a += (double) orc_bf16_to_f32(w->router[(size_t) e * D + d]) * xb[d];
-            logits[(size_t) t * E + e] = (float) a;
+#pragma omp parallel
+    {
+        float* xb = (float*) malloc(sizeof(float) * (size_t) D);
+#pragma omp for schedule(static)
+        for (int t = 0; t < T; ++t) {
+            for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
+            for (int e = 0; e < E; ++e) {
+                double a = 0.0;
+                for (int d = 0; d < D; ++d) a += (double) orc_bf16_to_f32(w->router[(size_t) e * D + d]) * xb[d];
+                logits[(size_t) t * E + e] = (float) a;
+            }
+            double g = 0.0;
+            for (int d = 0; d < D; ++d) g += (double) orc_bf16_to_f32(w->sgate[d]) * xb[d];
+            sg[t] = (float) g;
         }
-        double g = 0.0;
-        for (int d = 0; d < D; ++d) g += (double) orc_bf16_to_f32(w->sgate[d]) * xb[d];
-        sg[t] = (float) g;
+        free(xb);
     }
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t) T * E);
     orc_router_topk(logits, E, K, T, ids, wts, NULL);
-    for (int t = 0; t < T && rc == 0; ++t) {
-        for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
-        /* shared expert */
-        for (int j = 0; j < F; ++j) {
-            double g = 0.0, u = 0.0;
-            for (int d = 0; d < D; ++d) {
-                g += (double) q8_bf16_value(w->sh_gate_q, w->sh_gate_s, D, j, d) * xb[d];
-                u += (double) q8_bf16_value(w->sh_up_q, w->sh_up_s, D, j, d) * xb[d];
-            }
-            act[j] = round_bf16(silu_f((float) g) * (float) u);
-        }
-        const double gate = (double) sigmoid_f(sg[t]);
-        for (int d = 0; d < D; ++d) {
-            double s = 0.0;
-            for (int j = 0; j < F; ++j) s += (double) q8_bf16_value(w->sh_down_q, w->sh_down_s, F, d, j) * act[j];
-            out[d] = (double) (float) s * gate;
-        }
-        /* routed experts */
-        for (int k = 0; k < K; ++k) {
-            const int e = ids[t * K + k];
-            const uint8_t* blob = w->blobs ? w->blobs[e] : NULL;
-            if (!blob) { rc = -1; break; }
-            const int gu_row = D / 64 * 36, d_row = F / 64 * 36;
-            const float* tail = (const float*) (blob + orc_blob_bytes(D, F) - 16);
-            for (int j = 0; j < F; ++j) {
-                double g = 0.0, u = 0.0;
-                const uint8_t* rg = blob + (size_t) j * gu_row;
-                const uint8_t* ru = blob + (size_t) (F + j) * gu_row;
-                for (int d = 0; d < D; ++d) {
-                    g += (double) nvfp4_value(rg, d, tail[0]) * xb[d];
-                    u += (double) nvfp4_value(ru, d, tail[1]) * xb[d];
-                }
-                act[j] = round_bf16(silu_f((float) g) * (float) u);
-            }
-            const uint8_t* dn = blob + (size_t) 2 * F * gu_row;
-            for (int d = 0; d < D; ++d) {
-                double s = 0.0;
-                const uint8_t* rd = dn + (size_t) d * d_row;
-                for (int j = 0; j < F; ++j) s += (double) nvfp4_value(rd, j, tail[2]) * act[j];
-                out[d] += (double) wts[t * K + k] * (double) (float) s;
-            }
-        }
-        for (int d = 0; d < D; ++d) comb[(size_t) t * D + d] = (float) out[d];
+    /* routed blobs are fetched before the parallel part (the fetch callback is not thread safe) */
+    const uint8_t** blobs = (const uint8_t**) malloc(sizeof(uint8_t*) * (size_t) T * K);
+    for (int i = 0; i < T * K && rc == 0; ++i) {
+        const int e = ids[i];
+        const uint8_t* b = w->blobs ? w->blobs[e] : NULL;
+        if (!b && blob_fn) b = blob_fn(blob_ctx, layer, e);
+        if (!b) rc = -1;
+        blobs[i] = b;
     }
-    free(xb); free(logits); free(sg); free(act); free(out);
+    if (rc == 0) {
+#pragma omp parallel
+        {
+            float* xb = (float*) malloc(sizeof(float) * (size_t) D);
+            float* act = (float*) malloc(sizeof(float) * (size_t) F);
+            double* out = (double*) malloc(sizeof(double) * (size_t) D);
+#pragma omp for schedule(dynamic)
+            for (int t = 0; t < T; ++t) {
+                for (int d = 0; d < D; ++d) xb[d] = round_bf16(x[(size_t) t * D + d]);
+                /* shared expert */
+                for (int j = 0; j < F; ++j) {
+                    double g = 0.0, u = 0.0;
+                    for (int d = 0; d < D; ++d) {
+                        g += (double) q8_bf16_value(w->sh_gate_q, w->sh_gate_s, D, j, d) * xb[d];
+                        u += (double) q8_bf16_value(w->sh_up_q, w->sh_up_s, D, j, d) * xb[d];
+                    }
+                    act[j] = round_bf16(silu_f((float) g) * (float) u);
+                }
+                const double gate = (double) sigmoid_f(sg[t]);
+                for (int d = 0; d < D; ++d) {
+                    double s = 0.0;
+                    for (int j = 0; j < F; ++j) s += (double) q8_bf16_value(w->sh_down_q, w->sh_down_s, F, d, j) * act[j];
+                    out[d] = (double) (float) s * gate;
+                }
+                /* routed experts */
+                for (int k = 0; k < K; ++k) {
+                    const uint8_t* blob = blobs[t * K + k];
+                    const int gu_row = D / 64 * 36, d_row = F / 64 * 36;
+                    const float* tail = (const float*) (blob + orc_blob_bytes(D, F) - 16);
+                    for (int j = 0; j < F; ++j) {
+                        double g = 0.0, u = 0.0;
+                        const uint8_t* rg = blob + (size_t) j * gu_row;
+                        const uint8_t* ru = blob + (size_t) (F + j) * gu_row;
+                        for (int d = 0; d < D; ++d) {
+                            g += (double) nvfp4_value(rg, d, tail[0]) * xb[d];
+                            u += (double) nvfp4_value(ru, d, tail[1]) * xb[d];
+                        }
+                        act[j] = round_bf16(silu_f((float) g) * (float) u);
+                    }
+                    const uint8_t* dn = blob + (size_t) 2 * F * gu_row;
+                    for (int d = 0; d < D; ++d) {
+                        double s = 0.0;
+                        const uint8_t* rd = dn + (size_t) d * d_row;
+                        for (int j = 0; j < F; ++j) s += (double) nvfp4_value(rd, j, tail[2]) * act[j];
+                        out[d] += (double) wts[t * K + k] * (double) (float) s;
+                    }
+                }
+                for (int d = 0; d < D; ++d) comb[(size_t) t * D + d] = (float) out[d];
+            }
+            free(xb); free(act); free(out);
+        }
+    }
+    free(blobs); free(logits); free(sg);
     return rc;
 }
 

@@ -13,7 +13,7 @@ static int cmp_desc_f(const void* a, const void* b) {
 }
 
 /* Gap between the k-th and (k+1)-th largest of v[0..n) (k >= 1), +huge if n <= k. */
-static float kth_gap(const float* v, int n, int k) {
+float orc_kth_gap(const float* v, int n, int k) {
     if (n <= k) return 1e30f;
     float* s = (float*) malloc(sizeof(float) * (size_t) n);
     memcpy(s, v, sizeof(float) * (size_t) n);
@@ -25,7 +25,7 @@ static float kth_gap(const float* v, int n, int k) {
 
 /* Relative score gap around the top-k threshold block of one row (how far a block score would have
  * to move to change the selected cell set); +huge when the row selects every cell. */
-static float select_margin(const float* scores, int n_kv, int blk, int topk) {
+float orc_select_margin(const float* scores, int n_kv, int blk, int topk) {
     if (n_kv <= topk) return 1e30f;
     const int nbid = n_kv / blk, nb = nbid + 1;
     float* s = (float*) malloc(sizeof(float) * (size_t) nb);
@@ -42,6 +42,11 @@ static float select_margin(const float* scores, int n_kv, int blk, int topk) {
         int j = i - 1;
         while (j >= 0 && s[j] < sv) { s[j + 1] = s[j]; w[j + 1] = w[j]; --j; }
         s[j + 1] = sv; w[j + 1] = wv;
+    }
+    if (n == 0) {
+        free(s);
+        free(w);
+        return 1e30f;
     }
     long cum = 0;
     int jt = n - 1;
@@ -183,7 +188,7 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
                     orc_block_scores(w->idx_pooled, w->idx_dead, q_idx + (size_t) t * IH * ID, n_kv, IH, ID, m->idx_blk,
                                      scores);
                 const int n = orc_topk_select(scores, n_kv, m->idx_blk, m->idx_topk, sel);
-                if (margins) margins[((size_t) l * T + t) * 2 + 1] = select_margin(scores, n_kv, m->idx_blk, m->idx_topk);
+                if (margins) margins[((size_t) l * T + t) * 2 + 1] = orc_select_margin(scores, n_kv, m->idx_blk, m->idx_topk);
                 if (tr && tr->scores) {
                     float* dst = tr->scores + ((size_t) qsa_i * T + t) * max_b;
                     memset(dst, 0, sizeof(float) * (size_t) max_b);
@@ -219,7 +224,7 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
         rc = orc_moe_block_fn(&mw, mixed, T, comb, ids, wts, rl, NULL, m->blob, m->blob_ctx, l);
         if (margins)
             for (int t = 0; t < T; ++t) {
-                margins[((size_t) l * T + t) * 2 + 0] = kth_gap(rl + (size_t) t * m->n_exp, m->n_exp, m->top_k);
+                margins[((size_t) l * T + t) * 2 + 0] = orc_kth_gap(rl + (size_t) t * m->n_exp, m->n_exp, m->top_k);
                 if (!w->qsa) margins[((size_t) l * T + t) * 2 + 1] = 1e30f;
             }
         if (tr && tr->router_logits)

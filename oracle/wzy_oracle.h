@@ -77,6 +77,10 @@ int orc_moe_block_fn(const orc_moe_weights* w, const float* x, int T, float* com
 /* Prefill MoE block with bf16 numerics (see orc_core.c); needs every routed blob in w->blobs.
  * Returns 0, or -1 if a routed blob is NULL. */
 int orc_moe_prefill(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts);
+/* Same, fetching blobs that w->blobs does not hold from blob_fn (layer `layer`); logits_out [T x E]
+ * (optional) receives the router logits. */
+int orc_moe_prefill_fn(const orc_moe_weights* w, const float* x, int T, float* comb, int* ids, float* wts,
+                       float* logits_out, orc_blob_fn blob_fn, void* blob_ctx, int layer);
 
 /* ---- hyper-connection read (src/wzy_kernels_v2.cuh:409-454,632-827): see orc_layers.c ---- */
 void orc_hc_read(const float* R_in, const float* emb_rows, const float* bo, const float* inj_prev, const float* norm_w,
@@ -178,6 +182,34 @@ typedef struct orc_trace {
 } orc_trace;
 int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T, float* logits, int* greedy,
                             float* pre_head, const orc_trace* tr);
+
+/* Decision margins: gap between the k-th and (k+1)-th largest of v[0..n) (1e30 if n <= k); relative
+ * indexer score gap around the top-k threshold block of a row (1e30 when it selects every cell). */
+float orc_kth_gap(const float* v, int n, int k);
+float orc_select_margin(const float* scores, int n_kv, int blk, int topk);
+
+/* ---- chunked prefill (PrefillStageCtx::run_stage_prefill, src/wzy_prefill_tc.cuh:546-1058): see
+ * orc_prefill.c for the operand roundings ---- */
+/* y[t*ldy + n] = sum_k A[t][k] * W[n][k]: A bf16-valued [M x K], W Q8_0 (q, s; rounded to bf16) or bf16 (wb) */
+void orc_pf_gemm(const float* A, int M, int K, const int8_t* q, const uint16_t* s, const uint16_t* wb, int N,
+                 float* y, int ldy);
+/* HC read of B rows (R [B][HC][D] updated in place with the pending block bo/inj_prev when bo != NULL) */
+void orc_hc_read_pf(float* R, const float* bo, const float* inj_prev, const float* norm_w, const int8_t* down_q,
+                    const uint16_t* down_s, const uint16_t* inj_w, const int8_t* up_q, const uint16_t* up_s, int D,
+                    int HC, int HCLR, float eps, int B, float* inj, float* mixed);
+void orc_hc_write(float* R, const float* blk, const float* inj, int D, int HC, int B);
+/* sparse GQA attention of one row with the prefill kernel's fp16 operands and 32-cell softmax steps */
+void orc_attend_pf(const float* qg, const int8_t* kq, const uint16_t* ks, const int8_t* vq, const uint16_t* vs,
+                   const int* sel, int n, int qh, int kvh, int hd, float* out);
+/* B prompt cells at positions pos .. pos+B-1 through every layer, updating the model's state; R_out
+ * [B][hc][n_embd] receives the final residual (the last MoE block written in); dbg (optional)
+ * [L][4][B][n_embd] as in orc_model_forward_dbg.  Returns 0, or -1. */
+int orc_model_prefill(const orc_model* m, int pos, const int* toks, int B, float* R_out, float* dbg);
+/* Same, also writing margins [L][B][2] (optional): the router logit gap between the top_k-th and
+ * next expert, and the relative indexer score gap around the top-k threshold (1e30 when the row
+ * selects every cell or the layer is GDN), as orc_model_forward_dbg. */
+int orc_model_prefill_dbg(const orc_model* m, int pos, const int* toks, int B, float* R_out, float* dbg,
+                          float* margins);
 
 /* ---- MTP drafter (src/wzy_mtp.cuh) ---- */
 /* Q2_0 expert blob size: 3*D*F/4 code bytes + 3*D*F/64 fp16 scales (src/wzy_mtp.cuh:6-10) */

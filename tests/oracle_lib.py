@@ -30,6 +30,10 @@ _SIGS = {
     "orc_expert_down": (None, [P, I32, I32, P, P, P]),
     "orc_moe_block": (I32, [C.POINTER(OrcMoeWeights), P, I32, P, P, P, P, P]),
     "orc_moe_prefill": (I32, [C.POINTER(OrcMoeWeights), P, I32, P, P, P]),
+    "orc_pf_gemm": (None, [P, I32, I32, P, P, P, I32, P, I32]),
+    "orc_hc_read_pf": (None, [P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, P]),
+    "orc_hc_write": (None, [P, P, P, I32, I32, I32]),
+    "orc_attend_pf": (None, [P, P, P, P, P, P, I32, I32, I32, I32, P]),
     "orc_hc_read": (None, [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, F32, I32, P, P, P, P, P]),
     "orc_gdn_step": (None, [P, P, P, P, P, P, P, P, P, F32, P, I32, I32, I32]),
     "orc_gdn_recurrence": (None, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32]),

@@ -189,6 +189,23 @@ class OracleModel:
         self.last_margins = tr["margins"]
         return logits, greedy, pre, tr
 
+    def prefill(self, pos, toks):
+        """orc_model_prefill_dbg over the cells of toks at pos ..: the final residual [B x hc x D];
+        per-layer activations [L x 4 x B x D] in last_layers and margins [L x B x 2] in last_margins."""
+        cfg = self.cfg
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        B = len(toks)
+        R = np.empty((B, cfg.hc, cfg.n_embd), np.float32)
+        dbg = np.empty((cfg.n_layers, 4, B, cfg.n_embd), np.float32)
+        mg = np.empty((cfg.n_layers, B, 2), np.float32)
+        fn = self.orc.orc_model_prefill_dbg
+        fn.restype = I32
+        fn.argtypes = [C.POINTER(OrcModel), I32, P, I32, P, P, P]
+        assert fn(C.byref(self.model), pos, toks.ctypes.data, B, R.ctypes.data, dbg.ctypes.data, mg.ctypes.data) == 0
+        self.last_layers = dbg
+        self.last_margins = mg
+        return R
+
     def decidable_rows(self, router_gap=0.02, select_gap=1e-3):
         """Rows of the last forward whose every routing / selection decision has a margin that the
         float-reordering drift between two implementations cannot cross."""

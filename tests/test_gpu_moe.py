@@ -377,19 +377,19 @@ def prefill_logits(m, x):
     return (X @ R.T).astype(np.float32)
 
 
-def assert_prefill_close(g, o, D, rtol=2e-2, atol=1e-2):
+def assert_prefill_close(g, o, D, rtol=2e-2, atol=1e-2, max_frac=1e-4):
     """Prefill block outputs against the oracle, rows of D values.  Elementwise |g - o| <= atol +
     rtol * |o|, except where the two round a SwiGLU activation that sits on a bf16 rounding tie in
     opposite directions (their fp32 sums differ in order): that moves the token's outputs by one bf16
     ulp of the activation times its down column, which can exceed the elementwise bound on the
-    token's small outputs.  Such elements must be fewer than 1 in 10^4 and within atol + rtol *
-    max |o| over their token row."""
+    token's small outputs.  Such elements must be fewer than max_frac (1 in 10^4) and within atol +
+    rtol * max |o| over their token row."""
     g = np.asarray(g, np.float64).reshape(-1, D)
     o = np.asarray(o, np.float64).reshape(-1, D)
     d = np.abs(g - o)
     out = d > atol + rtol * np.abs(o)
     n_out = int(out.sum())
-    assert n_out <= d.size // 10000, "%d of %d outside the elementwise tolerance" % (n_out, d.size)
+    assert n_out <= int(d.size * max_frac), "%d of %d outside the elementwise tolerance" % (n_out, d.size)
     row_bound = atol + rtol * np.abs(o).max(axis=1, keepdims=True)
     assert (d <= row_bound).all(), "max error %.3g above the row bound" % (d - row_bound).max()
 

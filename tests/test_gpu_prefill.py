@@ -1,0 +1,384 @@
+"""Chunked prefill on the GPU (wzy_stage_prefill, wzy_gemm_bf16) against the CPU oracle's restatement
+of the reference's prefill (orc_prefill.c; src/wzy_prefill_tc.cuh:546-1058).
+
+- The bf16 MFMA GEMM against orc_pf_gemm at the projection shapes of a chunk, including row / column
+  tails, Q8_0 and bf16 weights, fp32 and bf16 outputs.
+- Whole chunks at a small configuration: from an empty context, from a context the decode path
+  built (a chunk that starts inside an index block), and a chunk shorter than one index block.
+  The discrete decisions are checked where they are made (every MoE block on the GPU's own input,
+  every QSA row's selected cells bit-exact), and the rest of the chunk teacher-forced on them:
+  the independent composition of the prefill (prefill_compose, pinned against the oracle on the
+  CPU) takes the GPU's expert outputs and selections, and every layer's HC reads and blocks, the
+  final residual rows, the GDN state, the KV cells and the indexer state must agree elementwise.
+  (Without the forcing, the bf16 rounding of expert activations makes a 1e-4 input difference move
+  a synthetic MoE block's output by far more than the tolerance, and that compounds over layers.)
+- The decode row after a prefill, teacher-forced (teacher_forced.py) from the stage's prefilled state.
+- Chunking is exact: one chunk and the same cells in several chunks leave bit-identical state and
+  final rows (small configuration and BASELINE shapes, 2,100 rows: the GEMM tiling, the 2,048-row
+  score passes and the indexer's cross-chunk blocks at their real sizes).
+- BASELINE shapes (D=2048, 512 experts top-10, 16/16 GDN heads, 24/2 QSA heads, top-2048) on four
+  layers of a 4,000-cell context against the oracle.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle_lib
+import wzy_amd
+from layer_parity import ATOL, RTOL
+from oracle_lib import ptr
+from prefill_compose import compose_prefill, dims_of, moe_oracle, stage_weights, state_copy, tbf16
+from layer_parity import gpu_trace
+from stage_oracle import OracleModel, is_qsa, small_cfg
+from teacher_forced import TeacherForced
+from test_gpu_moe import assert_prefill_close
+
+pytestmark = pytest.mark.gpu
+
+SEED = 23
+DA = wzy_amd.DeviceArray
+
+
+def pf_cfg(ctx_max=1024, n_layers=4, topk=64):
+    """The small configuration with an expert count the MFMA MoE block takes (a multiple of 64)."""
+    c = small_cfg(wzy_amd, ctx_max=ctx_max, n_layers=n_layers, topk=topk)
+    c.n_exp, c.top_k = 64, 4
+    return c
+
+
+def bf16_bits(x):
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bits_to_f32(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- GEMM ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,kind,out", [
+    (1, 4, 64, "q8", "f32"),            # inject-like: one row, four outputs
+    (77, 320, 8192, "q8", "f32"),       # HC down at BASELINE width
+    (300, 512, 320, "q8", "bf16"),      # HC up: K = 320 (five 64-steps), bf16 output
+    (130, 200, 2048, "bf16", "f32"),    # bf16 weights (indexer / router)
+    (257, 129, 128, "q8", "f32"),       # row and column tails
+    (1024, 1024, 1024, "q8", "f32"),    # 8 x 8 tiles (the XCD-grouped numbering)
+])
+def test_gemm_bf16_parity(wz, orc, gpu, M, N, K, kind, out):
+    print("case gemm M=%d N=%d K=%d %s %s" % (M, N, K, kind, out), flush=True)
+    rng = np.random.default_rng(M + N + K)
+    lda = K + 8
+    a = bf16_bits(rng.normal(0, 1, (M, lda)))
+    af = bits_to_f32(a)
+    if kind == "q8":
+        wq = rng.integers(-127, 128, N * K).astype(np.int8)
+        ws = rng.uniform(0.0005, 0.002, N * K // 32).astype(np.float16).view(np.uint16)
+        wb = None
+    else:
+        wq = ws = None
+        wb = bf16_bits(rng.normal(0, 0.05, N * K))
+    ldy = N + 5
+    want = np.zeros((M, ldy), np.float32)
+    a_c = np.ascontiguousarray(af[:, :K])
+    orc.orc_pf_gemm(ptr(a_c), M, K, ptr(wq), ptr(ws), ptr(wb), N, ptr(want), ldy)
+    da = DA.from_numpy(a)
+    dq = DA.from_numpy(wq) if wq is not None else None
+    ds = DA.from_numpy(ws) if ws is not None else None
+    db = DA.from_numpy(wb) if wb is not None else None
+    if out == "f32":
+        dy = DA.from_numpy(np.full((M, ldy), -7.0, np.float32))
+        wz.wzy_gemm_bf16(da.ptr, lda, M, K, dq.ptr if dq else None, ds.ptr if ds else None, db.ptr if db else None,
+                         N, dy.ptr, None, ldy, None)
+    else:
+        dy = DA.from_numpy(np.full((M, ldy), 0xABCD, np.uint16))
+        wz.wzy_gemm_bf16(da.ptr, lda, M, K, dq.ptr if dq else None, ds.ptr if ds else None, db.ptr if db else None,
+                         N, None, dy.ptr, ldy, None)
+    wz.wzy_device_sync()
+    got = dy.numpy()
+    for arr in (da, dq, ds, db, dy):
+        if arr is not None:
+            arr.free()
+    # fp32 accumulation in another order: bounded by a small multiple of eps_f32 * sum |a w|
+    wfull = np.zeros((N, K), np.float64)
+    if kind == "q8":
+        wfull = bits_to_f32(bf16_bits(wq.astype(np.float32) *
+                                      np.repeat(ws.view(np.float16).astype(np.float32), 32))).reshape(N, K)
+    else:
+        wfull = bits_to_f32(wb).reshape(N, K)
+    mag = np.abs(a_c).astype(np.float64) @ np.abs(wfull).astype(np.float64).T
+    if out == "f32":
+        err = np.abs(got[:, :N] - want[:, :N])
+        assert (err <= 1e-5 * mag + 1e-7).all(), "max excess %.3g" % (err - 1e-5 * mag).max()
+        assert (got[:, N:] == -7.0).all(), "wrote past N"
+    else:
+        g = bits_to_f32(got[:, :N])
+        o = want[:, :N]
+        err = np.abs(g - o)
+        assert (err <= np.abs(o) * 2.0 ** -8 + 1e-5 * mag + 1e-7).all(), "bf16 output beyond one ulp"
+        assert (got[:, N:] == 0xABCD).all(), "wrote past N"
+
+
+# ---- whole chunks against the oracle, teacher-forced on the discrete decisions ---------------------
+def router_gaps(dm, w, x):
+    """top_k-th minus (top_k+1)-th router logit of bf16(x) rows (fp64 sums)"""
+    xb = tbf16(x).astype(np.float64)
+    R = bits_to_f32(w["router"]).astype(np.float64).reshape(dm.E, dm.D)
+    lg = np.sort(xb @ R.T, axis=1)[:, ::-1]
+    return lg[:, dm.K - 1] - lg[:, dm.K]
+
+
+def beyond(g, o):
+    """elements beyond |g - o| <= ATOL + RTOL * max(|o|, rms of o's row) (rows = last axis): the north
+    star's tolerance with the relative term floored at the row's RMS, as in teacher_forced.py -- a
+    residual stream element that nearly cancels (large terms, small sum) carries the terms' error"""
+    g = np.asarray(g, np.float64)
+    o = np.asarray(o, np.float64)
+    rms = np.sqrt(np.mean(o * o, axis=-1, keepdims=True))
+    return np.abs(g - o) > ATOL + RTOL * np.maximum(np.abs(o), rms)
+
+
+def check_chunk(wz, orc, st, om, cfg, p0, toks, label):
+    """The prefill of toks at p0 that `st` just ran (with the trace on), against the oracle:
+      1. every MoE block on the GPU's own FFN input (orc_moe_prefill), rows whose routing is a near
+         tie (router gap below 1e-4) excepted;
+      2. every QSA row's selected cells bit-exact against the reference top-k rule on the GPU's own
+         block scores, and those scores within tolerance of the composition's;
+      3. the independent composition of the prefill (prefill_compose) teacher-forced on the GPU's MoE
+         outputs and selections: every layer's HC read outputs and attention / GDN block, the final
+         residual rows (rel 2e-2 / abs 1e-2, the relative term floored at the row's RMS), the GDN
+         state, the KV cells and the indexer state.
+    Returns the composed state (for a decode step after the chunk)."""
+    dm = dims_of(cfg)
+    B = len(toks)
+    L = cfg.n_layers
+    qsa_layers = [l for l in range(L) if is_qsa(cfg, l)]
+    qi = {l: i for i, l in enumerate(qsa_layers)}
+    layers, state, glob = stage_weights(om, cfg)
+    state0 = state_copy(state)
+    tr = st.read(-1, "trace.pf", np.float32).reshape(L, 4, -1, cfg.n_embd)[:, :, :B]
+    nq = max(1, len(qsa_layers))
+    sel = st.read(-1, "trace.pf_sel", np.int32).reshape(nq, -1, cfg.idx_topk)[:, :B]
+    cnt = st.read(-1, "trace.pf_cnt", np.int32).reshape(nq, -1)[:, :B]
+    # 1. MoE blocks
+    n_moe_rows = 0
+    for l in range(L):
+        comb_o, _, _ = moe_oracle(orc, dm, layers[l], glob, l, tr[l, 2])
+        keep = router_gaps(dm, layers[l], tr[l, 2]) > 1e-4
+        n_moe_rows += int(keep.sum())
+        # inputs from real layers put more activations on bf16 rounding ties than N(0,1) rows do
+        assert_prefill_close(tr[l, 3][keep], comb_o[keep], cfg.n_embd, max_frac=1e-3)
+    # 2 + 3. composition forced on the GPU's decisions
+    sel_out = {}
+    R_c, dbg_c = compose_prefill(orc, dm, layers, state0, glob, p0, toks, moe=lambda l, x: tr[l, 3],
+                                 sel_force=lambda l, t: sel[qi[l], t, :cnt[qi[l], t]], sel_out=sel_out)
+    max_b = cfg.ctx_max // cfg.idx_blk + 2
+    scores = st.read(-1, "trace.pf_scores", np.float32).reshape(nq, -1, max_b)[:, :B]
+    n_sel = n_same = 0
+    sel_row = np.empty(cfg.idx_topk, np.int32)
+    for (l, t), (cells, margin, sc_o) in sel_out.items():
+        n_kv = p0 + t + 1
+        got = sel[qi[l], t, :cnt[qi[l], t]]
+        assert cnt[qi[l], t] == min(n_kv, cfg.idx_topk), (l, t)
+        if sc_o is None:                                  # every cell, in order
+            assert np.array_equal(got, np.arange(n_kv)), "%s layer %d row %d identity selection" % (label, l, t)
+        else:
+            # the exact top-k rule on the GPU's own block scores: bit-exact
+            sc_g = np.ascontiguousarray(scores[qi[l], t, :n_kv // cfg.idx_blk + 1])
+            n = orc.orc_topk_select(ptr(sc_g), n_kv, cfg.idx_blk, cfg.idx_topk, ptr(sel_row))
+            assert n == len(got) and np.array_equal(got, sel_row[:n]), "%s layer %d row %d selection" % (label, l, t)
+            # the scores themselves against the composition's, relative term floored at the row's RMS
+            # (a score is a sum of ReLU'd dots: where a dot sits near zero its share moves by the
+            # dot's noise, which scales with the row, not with the small score)
+            floor = np.sqrt(np.mean(np.asarray(sc_o, np.float64) ** 2))
+            bad = np.abs(sc_g - sc_o) > ATOL + RTOL * np.maximum(np.abs(sc_o), floor)
+            assert not bad.any(), "%s layer %d row %d block scores" % (label, l, t)
+        n_sel += 1
+        n_same += int(margin > 1e-3 and np.array_equal(got, cells))
+    for l in range(L):
+        for j, name in ((0, "attention HC read"), (1, "block"), (2, "FFN HC read")):
+            g, o = tr[l, j], dbg_c[l, j]
+            bad = beyond(g, o)
+            assert not bad.any(), "%s layer %d %s: %d elements beyond tolerance (max |diff| %.3g)" % (
+                label, l, name, bad.sum(), np.abs(g - o).max())
+    R_g = np.empty_like(R_c)
+    wz.wzy_stage_pre_head(st.h, R_g.ctypes.data, B)
+    bad = beyond(R_g, R_c)
+    assert not bad.any(), "%s final residual: %d elements beyond tolerance" % (label, bad.sum())
+    kvd = cfg.qsa_kvh * cfg.qsa_hd
+    for l in range(L):
+        s = state0[l]
+        if not is_qsa(cfg, l):
+            for name in ("ssm", "conv_hist"):
+                g = st.read(l, name, np.float32)
+                bad = np.abs(g - s[name]) > ATOL + RTOL * np.abs(s[name])
+                assert not bad.any(), "%s layer %d %s: %d beyond tolerance" % (label, l, name, bad.sum())
+        else:
+            cells = slice(p0 * kvd, (p0 + B) * kvd)
+            for name, key in (("kv_k", "kq"), ("kv_v", "vq")):
+                # the k / v inputs carry the bf16 rounding noise of every earlier layer (about 1e-3
+                # relative three layers deep), so a code may sit one step away from the oracle's
+                d = np.abs(st.read(l, name, np.int8)[cells].astype(int) - s[key][cells].astype(int))
+                assert d.max() <= 1 and (d == 0).mean() >= 0.9, "%s layer %d %s: max %d, %.4f exact" % (
+                    label, l, name, d.max(), (d == 0).mean())
+            for name, key in (("kv_ks", "ks"), ("kv_vs", "vs")):
+                sl = slice(p0 * kvd // 64, (p0 + B) * kvd // 64)
+                np.testing.assert_allclose(st.read(l, name, np.uint16)[sl].view(np.float16).astype(np.float32),
+                                           s[key][sl].view(np.float16).astype(np.float32), rtol=1e-2, atol=1e-6)
+            nb = (p0 + B) // cfg.idx_blk + 1
+            g = st.read_range(l, "idx_pooled", np.uint16, 0, nb * cfg.idx_dim).view(np.float16).astype(np.float32)
+            o = s["idx_pooled"][:nb * cfg.idx_dim].view(np.float16).astype(np.float32)
+            np.testing.assert_allclose(g, o, rtol=RTOL, atol=ATOL, err_msg="%s layer %d pooled keys" % (label, l))
+            for name in ("idx_tail", "idx_dead"):
+                np.testing.assert_allclose(st.read(l, name, np.float32), s[name], rtol=RTOL, atol=ATOL,
+                                           err_msg="%s layer %d %s" % (label, l, name))
+    print("%s: %d MoE rows, %d selections bit-exact on the GPU's scores (%d also equal to the composition's own), "
+          "every layer and the state within tolerance" % (label, n_moe_rows, n_sel, n_same), flush=True)
+    assert n_moe_rows >= 0.9 * L * B
+    assert n_sel == len(qsa_layers) * B
+    return state0
+
+
+@pytest.mark.parametrize("p0,B,prefix", [(0, 150, 0), (37, 100, 37), (0, 7, 0), (5, 300, 5)])
+def test_stage_prefill_matches_oracle(wz, orc, gpu, p0, B, prefix):
+    print("case prefill p0=%d B=%d" % (p0, B), flush=True)
+    cfg = pf_cfg()
+    rng = np.random.default_rng(p0 * 7 + B)
+    toks = [int(t) for t in rng.integers(0, cfg.n_vocab, p0 + B + 1)]
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(SEED, 0)
+        for p in range(0, prefix, 8):                         # the context before the chunk: decode windows
+            st.forward(p, toks[p:min(p + 8, prefix)], run_head=False)
+        st.sync()
+        wz.wzy_stage_set_trace(st.h, 1)
+        om = OracleModel(wz, st, cfg, SEED)                   # the oracle starts from the stage's state
+        st.prefill(p0, toks[p0:p0 + B])
+        st.sync()
+        check_chunk(wz, orc, st, om, cfg, p0, toks[p0:p0 + B], "p0=%d B=%d" % (p0, B))
+        # the decode row after the chunk, teacher-forced from the stage's prefilled state (the state
+        # itself was checked against the composition above)
+        tf = TeacherForced(wz, st, cfg, om)
+        tf.sync_from_stage()
+        pos = p0 + B
+        st.forward(pos, [toks[pos]])
+        st.sync()
+        gt = gpu_trace(st, cfg, 1, len([l for l in range(cfg.n_layers) if is_qsa(cfg, l)]))
+        tf.check_row("decode after prefill pos %d" % pos, pos, toks[pos], gt, st.logits(1), st.greedy(1), st.pre_head(1))
+        print("decode after prefill: " + tf.summary(), flush=True)
+    finally:
+        st.close()
+
+
+def run_chunks(cfg, toks, splits, seed=SEED, n_ctx=0):
+    st = wzy_amd.Stage(cfg)
+    st.load_synthetic(seed, n_ctx)
+    p = n_ctx
+    for n in splits:
+        st.prefill(p, toks[p - n_ctx:p - n_ctx + n])
+        p += n
+    st.sync()
+    last = np.empty((splits[-1], cfg.hc, cfg.n_embd), np.float32)
+    st.lib.wzy_stage_pre_head(st.h, last.ctypes.data, splits[-1])
+    return st, last
+
+
+def assert_same_state(a, b, cfg, n_cells):
+    kvd = cfg.qsa_kvh * cfg.qsa_hd
+    for l in range(cfg.n_layers):
+        if not is_qsa(cfg, l):
+            for name in ("ssm", "conv_hist"):
+                assert np.array_equal(a.read(l, name, np.float32), b.read(l, name, np.float32)), (l, name)
+        else:
+            for name, dt, per in (("kv_k", np.int8, kvd), ("kv_v", np.int8, kvd), ("kv_ks", np.uint16, kvd // 64),
+                                  ("kv_vs", np.uint16, kvd // 64)):
+                assert np.array_equal(a.read_range(l, name, dt, 0, n_cells * per),
+                                      b.read_range(l, name, dt, 0, n_cells * per)), (l, name)
+            nb = n_cells // cfg.idx_blk + 1
+            assert np.array_equal(a.read_range(l, "idx_pooled", np.uint16, 0, nb * cfg.idx_dim),
+                                  b.read_range(l, "idx_pooled", np.uint16, 0, nb * cfg.idx_dim)), (l, "pooled")
+            for name in ("idx_tail", "idx_dead"):
+                assert np.array_equal(a.read(l, name, np.float32), b.read(l, name, np.float32)), (l, name)
+
+
+def test_prefill_chunking_is_exact_small(wz, gpu):
+    print("case prefill_chunking_small", flush=True)
+    cfg = pf_cfg()
+    toks = [int(t) for t in np.random.default_rng(3).integers(0, cfg.n_vocab, 300)]
+    a, ra = run_chunks(cfg, toks, [200])
+    b, rb = run_chunks(cfg, toks, [61, 103, 36])
+    try:
+        assert_same_state(a, b, cfg, 200)
+        assert np.array_equal(ra[-36:], rb)
+    finally:
+        a.close()
+        b.close()
+
+
+def baseline_cfg(n_layers, ctx_max, qsa_period=4):
+    c = wzy_amd.StageCfg()
+    wzy_amd.lib().wzy_stage_cfg_default(C.byref(c), ctx_max)
+    c.n_layers = n_layers
+    c.qsa_period = qsa_period
+    return c
+
+
+def test_prefill_chunking_is_exact_baseline_shapes(wz, gpu):
+    """BASELINE shapes, 4 layers (3 GDN + 1 QSA) over a 3,000-cell synthetic context: 2,100 rows in
+    one chunk (two block-score passes of up to 2,048 rows) against 700 + 1,400."""
+    print("case prefill_chunking_baseline", flush=True)
+    cfg = baseline_cfg(4, 8192)
+    n_ctx = 3000
+    toks = [int(t) for t in np.random.default_rng(4).integers(0, cfg.n_vocab, 2100)]
+    a, ra = run_chunks(cfg, toks, [2100], n_ctx=n_ctx)
+    try:
+        b, rb = run_chunks(cfg, toks, [700, 1400], n_ctx=n_ctx)
+        try:
+            assert_same_state(a, b, cfg, n_ctx + 2100)
+            assert np.array_equal(ra[-1400:], rb)
+        finally:
+            b.close()
+    finally:
+        a.close()
+
+
+def test_prefill_baseline_shapes_match_oracle(wz, orc, gpu):
+    """BASELINE shapes on four layers (GDN, GDN, GDN, QSA) at a 4,000-cell context (the QSA layer
+    selects 2,048 of 4,000+ cells), a 40-cell chunk against the oracle."""
+    print("case prefill_baseline_oracle", flush=True)
+    cfg = baseline_cfg(4, 8192)
+    n_ctx, B = 4000, 40
+    toks = [int(t) for t in np.random.default_rng(5).integers(0, cfg.n_vocab, B)]
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(SEED, n_ctx)
+        wz.wzy_stage_set_trace(st.h, 1)
+        om = OracleModel(wz, st, cfg, SEED)
+        st.prefill(n_ctx, toks)
+        st.sync()
+        check_chunk(wz, orc, st, om, cfg, n_ctx, toks, "baseline")
+    finally:
+        st.close()
+
+
+def test_prefill_errors(wz, gpu):
+    cfg = small_cfg(wzy_amd, ctx_max=256, n_layers=2, topk=64)       # 16 experts: no MFMA MoE block
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(1, 0)
+        with pytest.raises(wzy_amd.WzyError):
+            st.prefill(0, list(range(10)))
+    finally:
+        st.close()
+    cfg = pf_cfg(ctx_max=256, n_layers=2)
+    st = wzy_amd.Stage(cfg)
+    try:
+        with pytest.raises(wzy_amd.WzyError):
+            st.prefill(0, [1, 2])                                      # not loaded
+        st.load_synthetic(1, 0)
+        with pytest.raises(wzy_amd.WzyError):
+            st.prefill(250, list(range(10)))                           # past ctx_max
+        with pytest.raises(wzy_amd.WzyError):
+            st.prefill(0, [])
+    finally:
+        st.close()

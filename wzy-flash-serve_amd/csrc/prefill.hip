@@ -1,0 +1,798 @@
+// prefill.hip -- kernels of the chunked prefill (B prompt cells per launch sequence) on gfx950.
+//
+//  pf_gemm       every dense projection of the chunk on bf16 MFMA (v_mfma_f32_32x32x16_bf16):
+//                128 x 128 output tiles, K in steps of 64 through two LDS buffers; Q8_0 weights are
+//                dequantised (code * fp16 scale, rounded to bf16) on their way into LDS, bf16
+//                weights copied.  Workgroups are numbered so that the eight XCDs take interleaved row
+//                tiles and each runs all weight tiles of its row tile back to back.
+//  HC read       pf_hc_norm (pending block folded in, per-stream RMSNorm, bf16), GEMMs for inject /
+//                down / up, pf_silu_div, pf_up_mean; pf_hc_write writes a block into the streams.
+//  GDN           pf_gdn_ab (gates), pf_gdn_conv (causal conv + SiLU + L2 of q/k heads over all rows
+//                at once), pf_gdn_hist (conv history), pf_gdn_recur (the delta rule, sequential over
+//                the rows: 8 lanes per state column, 16 rows each in registers, q/k staged in LDS
+//                16 steps at a time), pf_gdn_norm (gated RMS norm, bf16).
+//  QSA           pf_qsa_prep (q / k / indexer-q norms + RoPE, INT8 KV append), pf_idx_append (the
+//                indexer keys of every block the chunk completes, one workgroup per block, then
+//                pf_idx_tail), block scores and top-k with the decode kernels over all rows,
+//                pf_attn (sparse GQA attention on fp16 MFMA with a 32-cell online softmax).
+// reference: PrefillStageCtx::run_stage_prefill and its kernels (src/wzy_prefill_tc.cuh:20-98,
+// 546-1058; src/wzy_qsa_wmma.cuh:5-489), with cuBLAS fp16 GEMMs replaced by bf16 MFMA GEMMs.
+#include "wzy_device.h"
+#include "wzy_host.h"
+#include "wzy_prefill.h"
+#include "wzy_qsa.h"
+#include "wzy_qsa_dev.h"
+
+using namespace wzy;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+namespace {
+
+WZY_DEV uint16_t f_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16) f); }   // nearest even
+WZY_DEV uint32_t pack_bf16(float a, float b) { return (uint32_t) f_to_bf16(a) | ((uint32_t) f_to_bf16(b) << 16); }
+
+// ---------------------------------------------------------------------------------------------
+// dense GEMM
+// ---------------------------------------------------------------------------------------------
+constexpr int GM = 128, GN = 128, GK = 64, GLD = GK + 8;   // tile rows, weight rows, k step, LDS row (bf16)
+
+struct GemmArgs {
+    PfGemm g;
+    int mt, nt;
+};
+
+// 32 Q8_0 codes (one block, c0 | c1) times their fp16 scale, rounded to bf16, as four 16-byte pieces
+WZY_DEV uint4 q8_quarter_bf16(uint32_t a, uint32_t b, float sc) {
+    return make_uint4(pack_bf16((float) (int8_t) a * sc, (float) (int8_t) (a >> 8) * sc),
+                      pack_bf16((float) (int8_t) (a >> 16) * sc, (float) (int8_t) (a >> 24) * sc),
+                      pack_bf16((float) (int8_t) b * sc, (float) (int8_t) (b >> 8) * sc),
+                      pack_bf16((float) (int8_t) (b >> 16) * sc, (float) (int8_t) (b >> 24) * sc));
+}
+WZY_DEV void q8_block_bf16(uint4 c0, uint4 c1, float sc, uint4& o0, uint4& o1, uint4& o2, uint4& o3) {
+    o0 = q8_quarter_bf16(c0.x, c0.y, sc);
+    o1 = q8_quarter_bf16(c0.z, c0.w, sc);
+    o2 = q8_quarter_bf16(c1.x, c1.y, sc);
+    o3 = q8_quarter_bf16(c1.z, c1.w, sc);
+}
+
+__global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
+    __shared__ __align__(16) uint16_t sA[2][GM][GLD];
+    __shared__ __align__(16) uint16_t sW[2][GN][GLD];
+    const PfGemm& g = ga.g;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
+    const int b = blockIdx.x;
+    int mi, ni;
+    if ((ga.mt & 7) == 0) {
+        const int s = b >> 3;
+        mi = (s / ga.nt) * 8 + (b & 7);
+        ni = s % ga.nt;
+    } else {
+        mi = b / ga.nt;
+        ni = b % ga.nt;
+    }
+    const int m0 = mi * GM, n0 = ni * GN;
+    const int sr = tid >> 1, kh = (tid & 1) * 32;                  // staging: row sr, k kh .. kh+31
+    const uint16_t* ap = g.a + (size_t) min(m0 + sr, g.M - 1) * g.lda + kh;
+    const size_t wr = (size_t) min(n0 + sr, g.N - 1);
+    const bool q8 = g.wq != nullptr;
+    const int8_t* wqp = q8 ? g.wq + wr * g.K + kh : nullptr;
+    const uint16_t* wsp = q8 ? g.ws + wr * (g.K / 32) + kh / 32 : nullptr;
+    const uint16_t* wbp = q8 ? nullptr : g.wb + wr * g.K + kh;
+    const int nk = g.K / GK;
+
+    // staging registers are scalars: arrays captured by a lambda would live in scratch memory
+    uint4 ra0, ra1, ra2, ra3, rw0, rw1, rw2 = make_uint4(0, 0, 0, 0), rw3 = rw2;
+    float rs = 0.f;
+#define PF_GEMM_LOAD(ks)                                                         \
+    {                                                                            \
+        const size_t o_ = (size_t) (ks) * GK;                                    \
+        ra0 = *(const uint4*) (ap + o_);                                         \
+        ra1 = *(const uint4*) (ap + o_ + 8);                                     \
+        ra2 = *(const uint4*) (ap + o_ + 16);                                    \
+        ra3 = *(const uint4*) (ap + o_ + 24);                                    \
+        if (q8) {                                                                \
+            rw0 = *(const uint4*) (wqp + o_);                                    \
+            rw1 = *(const uint4*) (wqp + o_ + 16);                               \
+            rs = h16_to_f(wsp[(ks) * (GK / 32)]);                                \
+        } else {                                                                 \
+            rw0 = *(const uint4*) (wbp + o_);                                    \
+            rw1 = *(const uint4*) (wbp + o_ + 8);                                \
+            rw2 = *(const uint4*) (wbp + o_ + 16);                               \
+            rw3 = *(const uint4*) (wbp + o_ + 24);                               \
+        }                                                                        \
+    }
+#define PF_GEMM_STORE(buf)                                                       \
+    {                                                                            \
+        *(uint4*) &sA[buf][sr][kh] = ra0;                                        \
+        *(uint4*) &sA[buf][sr][kh + 8] = ra1;                                    \
+        *(uint4*) &sA[buf][sr][kh + 16] = ra2;                                   \
+        *(uint4*) &sA[buf][sr][kh + 24] = ra3;                                   \
+        if (q8) q8_block_bf16(rw0, rw1, rs, rw0, rw1, rw2, rw3);                  \
+        *(uint4*) &sW[buf][sr][kh] = rw0;                                        \
+        *(uint4*) &sW[buf][sr][kh + 8] = rw1;                                    \
+        *(uint4*) &sW[buf][sr][kh + 16] = rw2;                                   \
+        *(uint4*) &sW[buf][sr][kh + 24] = rw3;                                   \
+    }
+
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    PF_GEMM_LOAD(0);
+    PF_GEMM_STORE(0);
+    __syncthreads();
+    for (int ks = 0; ks < nk; ++ks) {
+        const int buf = ks & 1;
+        const bool more = ks + 1 < nk;
+        if (more) PF_GEMM_LOAD(ks + 1);                            // next step's loads in flight
+#pragma unroll
+        for (int kk = 0; kk < GK / 16; ++kk) {
+            bf16x8_t av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                av[i] = *(const bf16x8_t*) &sA[buf][wm * 64 + i * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bv[j] = *(const bf16x8_t*) &sW[buf][wn * 64 + j * 32 + (lane & 31)][kk * 16 + (lane >> 5) * 8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) PF_GEMM_STORE(buf ^ 1);
+        __syncthreads();
+    }
+#undef PF_GEMM_LOAD
+#undef PF_GEMM_STORE
+    // acc[i][j][r] = C[row 8*(r/4) + 4*(lane/32) + r%4][col lane%32] of block (i, j)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < g.M && col < g.N) {
+                    if (g.y) g.y[(size_t) row * g.ldy + col] = acc[i][j][r];
+                    else g.yb[(size_t) row * g.ldy + col] = f_to_bf16(acc[i][j][r]);
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------------------------
+// embedding and hyper-connection pieces
+// ---------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) pf_embed_kernel(PfEmb e, const int* __restrict__ toks, float* __restrict__ R,
+                                                        int D, int HC) {
+    const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D) return;
+    const int tok = toks[t];
+    float v;
+    if (e.emb_q) {                                   // stage_one_emb: out-of-range ids read row 0
+        const size_t tk = (tok < 0 || tok >= e.n_vocab) ? 0 : (size_t) tok;
+        v = h16_to_f(e.emb_s[(tk * D + d) / 32]) * (float) e.emb_q[tk * D + d];
+    } else {
+        const size_t tk = (size_t) max(0, min(tok, e.n_vocab - 1));
+        v = bf16_to_f(e.emb[tk * D + d]);
+    }
+    for (int c = 0; c < HC; ++c) R[((size_t) t * HC + c) * D + d] = v;
+}
+
+// per (stream c, row t): R += bo * 2 sigmoid(inj_prev / HC) when a block is pending; x = bf16(R *
+// rsqrt(mean R^2 + eps) * norm_w)  (pf_gr_norm_fp16, src/wzy_qsa_wmma.cuh:198-234)
+__global__ void __launch_bounds__(256) pf_hc_norm_kernel(float* __restrict__ R, const float* __restrict__ bo,
+                                                          const float* __restrict__ inj_prev,
+                                                          const float* __restrict__ norm_w, uint16_t* __restrict__ xn,
+                                                          int D, int HC, float eps) {
+    __shared__ float s_red[4];
+    const int c = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    float* r = R + ((size_t) t * HC + c) * D;
+    const float gate = bo ? 2.0f / (1.0f + __expf(-inj_prev[t * HC + c] / (float) HC)) : 0.0f;
+    float ss = 0.f;
+    for (int d = tid; d < D; d += 256) {
+        float v = r[d];
+        if (bo) {
+            v = fmaf(bo[(size_t) t * D + d], gate, v);
+            r[d] = v;
+        }
+        ss += v * v;
+    }
+    ss = block_sum<4>(ss, s_red);
+    const float inv = 1.0f / sqrtf(ss / (float) D + eps);
+    uint16_t* x = xn + (size_t) t * HC * D + (size_t) c * D;
+    for (int d = tid; d < D; d += 256) x[d] = f_to_bf16(r[d] * inv * norm_w[(size_t) c * D + d]);
+}
+
+__global__ void __launch_bounds__(256) pf_silu_div_kernel(const float* __restrict__ lo, uint16_t* __restrict__ loh,
+                                                           size_t n, float inv_hc) {
+    const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = lo[i] * inv_hc;
+    loh[i] = f_to_bf16(v / (1.0f + __expf(-v)));
+}
+
+// mixed[t][d] = (sum over streams in order of x / (1 + exp(-g))) / HC, fp32 and bf16
+// (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252)
+__global__ void __launch_bounds__(256) pf_up_mean_kernel(const uint16_t* __restrict__ xn, const uint16_t* __restrict__ gg,
+                                                          float* __restrict__ mixed, uint16_t* __restrict__ xh, int D,
+                                                          int HC) {
+    const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D) return;
+    const size_t base = (size_t) t * HC * D + d;
+    float acc = 0.f;
+    for (int c = 0; c < HC; ++c) {
+        const float x = bf16_to_f(xn[base + (size_t) c * D]);
+        const float g = bf16_to_f(gg[base + (size_t) c * D]);
+        acc += x / (1.0f + __expf(-g));
+    }
+    const float v = acc * (1.0f / (float) HC);
+    mixed[(size_t) t * D + d] = v;
+    xh[(size_t) t * D + d] = f_to_bf16(v);
+}
+
+// R[t][c][d] += blk[t][d] * 2 sigmoid(inj[t][c] / HC)  (gr_write_multi, src/wzy_kernels_v2.cuh:813-827)
+__global__ void __launch_bounds__(256) pf_hc_write_kernel(float* __restrict__ R, const float* __restrict__ blk,
+                                                           const float* __restrict__ inj, int D, int HC) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= HC * D) return;
+    const int c = i / D, d = i - c * D;
+    const float g = 2.0f / (1.0f + __expf(-inj[t * HC + c] / (float) HC));
+    float* r = R + (size_t) t * HC * D + i;
+    *r = fmaf(blk[(size_t) t * D + d], g, *r);
+}
+
+// ---------------------------------------------------------------------------------------------
+// GDN
+// ---------------------------------------------------------------------------------------------
+// decay = exp(softplus(a + dt) * ssm_a), beta = sigmoid(b)  (gdn_ab_act_pf_kernel)
+__global__ void __launch_bounds__(256) pf_gdn_ab_kernel(PfGdn g) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= g.B * g.hv) return;
+    const int t = i / g.hv, h = i - t * g.hv;
+    const float a = g.ab[(size_t) t * 2 * g.hv + h] + g.dt[h];
+    const float bv = g.ab[(size_t) t * 2 * g.hv + g.hv + h];
+    g.beta[i] = 1.0f / (1.0f + __expf(-bv));
+    const float sp = a > 20.0f ? a : log1pf(__expf(a));
+    g.decay[i] = __expf(sp * g.ssm_a[h]);
+}
+
+// causal depthwise conv (3 history taps + the row) + SiLU, L2 norm of each q / k head; grid
+// (QKV/128, B), 128 threads  (pf_gdn_conv_parallel, src/wzy_qsa_wmma.cuh:5-30)
+__global__ void __launch_bounds__(128) pf_gdn_conv_kernel(PfGdn g) {
+    __shared__ float s_red[2];
+    const int grp = blockIdx.x, t = blockIdx.y, ch = grp * 128 + threadIdx.x;
+    const int QKV = (2 * g.hk + g.hv) * 128;
+    const float* h = g.conv_hist + (size_t) ch * 3;
+    auto in = [&](int s) { return s >= 0 ? g.qkv[(size_t) s * QKV + ch] : h[3 + s]; };   // row s (s < 0: history)
+    const float v0 = in(t - 3), v1 = in(t - 2), v2 = in(t - 1), vx = g.qkv[(size_t) t * QKV + ch];
+    const float* w = g.conv_w + (size_t) ch * 4;
+    const float sum = v0 * w[0] + v1 * w[1] + v2 * w[2] + vx * w[3];
+    float y = sum / (1.0f + __expf(-sum));
+    if (grp < 2 * g.hk) {
+        const float ss = block_sum<2>(y * y, s_red);
+        y *= 1.0f / sqrtf(ss + g.eps);
+    }
+    g.conv_out[(size_t) t * QKV + ch] = y;
+}
+
+// conv history <- the last three raw rows (the older history where the chunk is shorter)
+__global__ void __launch_bounds__(256) pf_gdn_hist_kernel(PfGdn g) {
+    const int QKV = (2 * g.hk + g.hv) * 128;
+    const int ch = blockIdx.x * 256 + threadIdx.x;
+    if (ch >= QKV) return;
+    float* h = g.conv_hist + (size_t) ch * 3;
+    float v[3];
+    for (int j = 0; j < 3; ++j) {
+        const int s = g.B - 3 + j;
+        v[j] = s >= 0 ? g.qkv[(size_t) s * QKV + ch] : h[3 + s];
+    }
+    h[0] = v[0];
+    h[1] = v[1];
+    h[2] = v[2];
+}
+
+constexpr int GR_LPC = 8;                     // lanes per state column
+constexpr int GR_RPL = 128 / GR_LPC;          // state rows per lane
+constexpr int GR_CPW = 64 / GR_LPC;           // columns per wave
+constexpr int GR_WAVES = 4;
+constexpr int GR_COLS = GR_CPW * GR_WAVES;    // columns per workgroup (32)
+constexpr int GR_STEPS = 16;                  // rows staged per LDS buffer
+
+// Delta rule over the chunk's rows for one value head and GR_COLS state columns (each column of
+// the state evolves independently): per row, S *= decay; kv = S^T k; delta = (v - kv) * beta;
+// S += k delta^T; o = S^T q / sqrt(128).  grid (hv * 128 / GR_COLS), 256 threads.
+// (pf_gdn_recur_kh_kernel, src/wzy_qsa_wmma.cuh:56-195; fused_gdn_step_norm_multi,
+// src/wzy_kernels_v2.cuh:908-984)
+__global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
+    __shared__ __align__(16) float sq[2][GR_STEPS][128];
+    __shared__ __align__(16) float sk[2][GR_STEPS][128];
+    __shared__ float sv[2][GR_STEPS][GR_COLS];
+    __shared__ float sg[2][GR_STEPS], sb[2][GR_STEPS];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int h = blockIdx.x / (128 / GR_COLS), cb = blockIdx.x % (128 / GR_COLS);
+    const int kh = h % g.hk;
+    const int QKV = (2 * g.hk + g.hv) * 128, GV = g.hv * 128;
+    const int r8 = lane & (GR_LPC - 1), c8 = lane / GR_LPC;
+    const int lc = w * GR_CPW + c8, col = cb * GR_COLS + lc;
+    float* S = g.state + (size_t) h * 128 * 128;
+    float s[GR_RPL];
+#pragma unroll
+    for (int i = 0; i < GR_RPL; ++i) s[i] = S[(size_t) (r8 * GR_RPL + i) * 128 + col];
+
+    // staging of rows t0 .. t0+GR_STEPS-1: q and k (128 each) of key head kh, v of the columns, gates
+    constexpr int QK_PER = GR_STEPS * 2 * 128 / 256;      // floats per thread (16)
+    float rq[QK_PER];
+    float rv = 0.f, rg = 0.f;
+    auto load = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < QK_PER; ++u) {
+            const int e = u * 256 + tid, step = e / 256, which = (e / 128) & 1, i = e & 127;
+            const int t = t0 + step;
+            rq[u] = t < g.B ? g.conv_out[(size_t) t * QKV + (which ? g.hk * 128 : 0) + kh * 128 + i] : 0.f;
+        }
+        {
+            const int step = tid / GR_COLS, j = tid % GR_COLS, t = t0 + step;   // 256 = 8 steps x 32 cols
+            rv = t < g.B ? g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j] : 0.f;
+        }
+        {
+            const int step = tid & (GR_STEPS - 1), t = t0 + step;
+            rg = (t < g.B && tid < 2 * GR_STEPS) ? (tid < GR_STEPS ? g.decay : g.beta)[(size_t) t * g.hv + h] : 0.f;
+        }
+    };
+    float rv2 = 0.f;
+    auto load_v2 = [&](int t0) {                            // v of steps 8..15
+        const int step = 8 + tid / GR_COLS, j = tid % GR_COLS, t = t0 + step;
+        rv2 = t < g.B ? g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j] : 0.f;
+    };
+    auto store = [&](int bb) {
+#pragma unroll
+        for (int u = 0; u < QK_PER; ++u) {
+            const int e = u * 256 + tid, step = e / 256, which = (e / 128) & 1, i = e & 127;
+            (which ? sk : sq)[bb][step][i] = rq[u];
+        }
+        sv[bb][tid / GR_COLS][tid % GR_COLS] = rv;
+        sv[bb][8 + tid / GR_COLS][tid % GR_COLS] = rv2;
+        if (tid < GR_STEPS) sg[bb][tid] = rg;
+        else if (tid < 2 * GR_STEPS) sb[bb][tid - GR_STEPS] = rg;
+    };
+
+    const int nblk = (g.B + GR_STEPS - 1) / GR_STEPS;
+    load(0);
+    load_v2(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < nblk; ++kb) {
+        const int bb = kb & 1, t0 = kb * GR_STEPS;
+        if (kb + 1 < nblk) {
+            load(t0 + GR_STEPS);
+            load_v2(t0 + GR_STEPS);
+        }
+        const int n = min(GR_STEPS, g.B - t0);
+        for (int st = 0; st < n; ++st) {
+            float kr[GR_RPL], qr[GR_RPL];
+#pragma unroll
+            for (int i = 0; i < GR_RPL; i += 4) {
+                const float4 k4 = *(const float4*) &sk[bb][st][r8 * GR_RPL + i];
+                const float4 q4 = *(const float4*) &sq[bb][st][r8 * GR_RPL + i];
+                kr[i] = k4.x; kr[i + 1] = k4.y; kr[i + 2] = k4.z; kr[i + 3] = k4.w;
+                qr[i] = q4.x; qr[i + 1] = q4.y; qr[i + 2] = q4.z; qr[i + 3] = q4.w;
+            }
+            const float dec = sg[bb][st], beta = sb[bb][st];
+            float kv0 = 0.f, kv1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < GR_RPL; i += 2) {
+                s[i] *= dec;
+                s[i + 1] *= dec;
+                kv0 = fmaf(s[i], kr[i], kv0);
+                kv1 = fmaf(s[i + 1], kr[i + 1], kv1);
+            }
+            const float kv = sum8(kv0 + kv1);
+            const float delta = (sv[bb][st][lc] - kv) * beta;
+            float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < GR_RPL; i += 2) {
+                s[i] = fmaf(kr[i], delta, s[i]);
+                s[i + 1] = fmaf(kr[i + 1], delta, s[i + 1]);
+                o0 = fmaf(s[i], qr[i], o0);
+                o1 = fmaf(s[i + 1], qr[i + 1], o1);
+            }
+            const float o = sum8(o0 + o1) * 0.08838834764831845f;
+            if (r8 == 0) g.o[(size_t) (t0 + st) * GV + h * 128 + col] = o;
+        }
+        if (kb + 1 < nblk) store(bb ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < GR_RPL; ++i) S[(size_t) (r8 * GR_RPL + i) * 128 + col] = s[i];
+}
+
+// y = bf16(o * rsqrt(mean o^2 + eps) * gamma * sigmoid(z)) per (head, row); grid (hv, B), 128 threads
+// (pf_gdn_rmsnorm_gate_parallel, src/wzy_qsa_wmma.cuh:176-195)
+__global__ void __launch_bounds__(128) pf_gdn_norm_kernel(PfGdn g) {
+    __shared__ float s_red[2];
+    const int h = blockIdx.x, t = blockIdx.y, c = threadIdx.x;
+    const size_t i = ((size_t) t * g.hv + h) * 128 + c;
+    const float o = g.o[i];
+    const float ss = block_sum<2>(o * o, s_red);
+    const float sc = 1.0f / sqrtf(ss * (1.0f / 128.0f) + g.eps);
+    g.y[i] = f_to_bf16(o * sc * g.gamma[c] / (1.0f + __expf(-g.z[i])));
+}
+
+// ---------------------------------------------------------------------------------------------
+// QSA
+// ---------------------------------------------------------------------------------------------
+constexpr int PR_ROWS = 4;                    // rows per prep workgroup
+
+// grid (qh + kvh + ih, ceil(B / PR_ROWS)), 256 threads: q heads, kv heads (+ INT8 append), indexer q heads
+__global__ void __launch_bounds__(256) pf_qsa_prep_kernel(PfQsaPrep a, int B) {
+    __shared__ float s_vals[256];
+    __shared__ float s_red[4];
+    const QsaDims& dm = a.dm;
+    const int role = blockIdx.x, tid = threadIdx.x;
+    const int base = *a.pos, hd = dm.hd, kvd = dm.kvh * dm.hd;
+    for (int t = blockIdx.y * PR_ROWS; t < min(B, (int) (blockIdx.y + 1) * PR_ROWS); ++t) {
+        const int pos = base + t;
+        if (role < dm.qh) {
+            norm_rope(a.qg + (size_t) t * dm.qh * 2 * hd + (size_t) role * 2 * hd, hd, a.q_norm, a.cos_tab, a.sin_tab, pos,
+                      dm.n_rot, dm.eps, s_vals, s_red);
+        } else if (role < dm.qh + dm.kvh) {
+            const int j = role - dm.qh;
+            float* kp = a.kk + (size_t) t * kvd + (size_t) j * hd;
+            norm_rope(kp, hd, a.k_norm, a.cos_tab, a.sin_tab, pos, dm.n_rot, dm.eps, s_vals, s_red);
+            if (tid < hd) qsa_kv_store(dm, a.kv, pos, j, kp[tid], a.vv[(size_t) t * kvd + (size_t) j * hd + tid]);
+            __syncthreads();
+        } else {
+            const int i = role - dm.qh - dm.kvh;
+            norm_rope(a.q_idx + (size_t) t * dm.ih * dm.idim + (size_t) i * dm.idim, dm.idim, a.iq_norm, a.cos_tab,
+                      a.sin_tab, pos, dm.n_rot, dm.eps, s_vals, s_red);
+        }
+    }
+}
+
+// One workgroup per indexer event of the chunk [p0, p0 + B): event 0 is position 0 when the chunk
+// starts the context (its key doubles as the open-block placeholder "dead"), the others are the
+// positions that complete a block.  A block's cells before p0 come from the tail as it was before
+// the chunk.  The last event writes the placeholder row after its block (dead, recomputed from row
+// 0 when this chunk sets it).  Final state equals B single-row appends (qsa_indexer_append_multi,
+// src/wzy_qsa_256k.cuh:147-209).
+__global__ void __launch_bounds__(256) pf_idx_append_kernel(PfIdxAppend a, int p0, int B, int has0, int pc0,
+                                                             int n_ev) {
+    __shared__ float s_vals[256];
+    __shared__ float s_red[4];
+    const QsaDims& dm = a.dm;
+    const int D = dm.idim, BL = dm.iblk, d = threadIdx.x;
+    const int e = blockIdx.x;
+    const bool last = e == n_ev - 1;
+    auto raw = [&](int cell) { return d < D ? round_h16(a.idx_raw[(size_t) (cell - p0) * D + d]) : 0.f; };
+    if (has0 && e == 0) {
+        const float inc = raw(0);
+        const float y = idx_block_key(dm, [&](int) { return inc; }, a.ik_norm, a.cos_tab, a.sin_tab, 0, s_vals, s_red);
+        if (d < D) {
+            a.ix.dead[d] = y;
+            if (p0 + B - 1 < BL - 1) a.ix.pooled[d] = f_to_h16(y);     // block 0 stays open in this chunk
+        }
+        return;
+    }
+    const int p = pc0 + (e - has0) * BL, b = p / BL;
+    auto cell = [&](int jj) {
+        const int c = b * BL + jj;
+        return c >= p0 ? raw(c) : (d < D ? a.ix.tail[jj * D + d] : 0.f);
+    };
+    const float y = idx_block_key(dm, cell, a.ik_norm, a.cos_tab, a.sin_tab, BL * b, s_vals, s_red);
+    float dead = 0.f;
+    if (last) {
+        if (p0 == 0) {
+            const float inc = raw(0);
+            dead = idx_block_key(dm, [&](int) { return inc; }, a.ik_norm, a.cos_tab, a.sin_tab, 0, s_vals, s_red);
+        } else {
+            dead = d < D ? a.ix.dead[d] : 0.f;
+        }
+    }
+    if (d < D) {
+        a.ix.pooled[(size_t) b * D + d] = f_to_h16(y);
+        if (last) a.ix.pooled[(size_t) (b + 1) * D + d] = f_to_h16(dead);
+    }
+}
+
+// tail slot s <- the last chunk cell at a position with p % iblk == s (s < iblk - 1)
+__global__ void __launch_bounds__(128) pf_idx_tail_kernel(PfIdxAppend a, int p0, int B) {
+    const int D = a.dm.idim, BL = a.dm.iblk, d = threadIdx.x;
+    if (d >= D) return;
+    const int pe = p0 + B - 1;
+    for (int s = 0; s < BL - 1; ++s) {
+        const int c = pe - ((pe % BL) - s + BL) % BL;             // last position <= pe in slot s
+        if (c >= p0) a.ix.tail[s * D + d] = round_h16(a.idx_raw[(size_t) (c - p0) * D + d]);
+    }
+}
+
+// Sparse GQA attention of one row and one KV head (grid (kvh, B), 256 threads): the group's query
+// heads (up to 16, rows of a 16 x 16 fp16 MFMA tile) against the selected cells 32 at a time.  Per
+// step: K of 32 cells dequantised to fp16 in LDS (row major), scores on v_mfma_f32_16x16x16_f16
+// (waves: 2 cell halves x 2 dim halves, summed through LDS), an online softmax per head (fp16
+// weights), V dequantised into LDS transposed (dims x cells) and P.V on MFMA into the accumulators,
+// rescaled by exp(m_old - m_new) first.  The next step's K and V codes are loaded while a step
+// computes.  out = acc / max(l, 1e-20) * sigmoid(gate), bf16.
+constexpr int AT_C = 32;                      // cells per step
+constexpr int AT_QLD = 256 + 8;               // LDS row strides (halves)
+constexpr int AT_VLD = AT_C + 8;
+
+WZY_DEV f16x4_t h4_from(const _Float16* p) { return *(const f16x4_t*) p; }
+
+__global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
+    __shared__ __align__(16) _Float16 sQ[16][AT_QLD];
+    __shared__ __align__(16) _Float16 sK[AT_C][AT_QLD];
+    __shared__ __align__(16) _Float16 sVt[256][AT_VLD];
+    __shared__ __align__(16) _Float16 sP[16][AT_VLD];
+    __shared__ float sS[2][16][AT_C + 1];
+    __shared__ float s_m[16], s_l[16], s_al[16];
+    const QsaDims& dm = a.dm;
+    const int j = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hd = 256, kvd = dm.kvh * hd, gq = dm.qh / dm.kvh, scg = hd / 64;
+    const int n_kv = *a.pos + t + 1;
+    const int width = min(n_kv, dm.topk);
+    const int* ids = a.sel + (size_t) t * dm.topk;
+    const float* qg = a.qg + (size_t) t * dm.qh * 2 * hd;
+
+    for (int i = tid; i < 16 * hd; i += 256) {
+        const int h = i / hd, d = i % hd;
+        sQ[h][d] = (_Float16) (h < gq ? qg[(size_t) (j * gq + h) * 2 * hd + d] * 0.0625f : 0.f);
+    }
+    if (tid < 16) {
+        s_m[tid] = -1e30f;
+        s_l[tid] = 0.f;
+        s_al[tid] = 1.f;
+    }
+    // K staging: thread -> cell kc = tid / 8, dims 32 * (tid % 8) .. +31 (32 code bytes)
+    const int kc = tid >> 3, kd0 = (tid & 7) * 32;
+    // V staging: thread -> dim tid, all 32 cells (one byte each)
+    uint4 kq0, kq1;
+    uint16_t ksc = 0;
+    int8_t vcode[AT_C];
+    uint16_t vsc[AT_C];
+    auto load = [&](int base) {
+        const int cnt = min(AT_C, width - base);
+        if (kc < cnt) {
+            const size_t p = qsa_kv_slot(ids[base + kc], dm);
+            const int8_t* kp = a.kv.kq + p * kvd + (size_t) j * hd + kd0;
+            kq0 = *(const uint4*) kp;
+            kq1 = *(const uint4*) (kp + 16);
+            ksc = a.kv.ks[p * (kvd / 64) + (size_t) j * scg + kd0 / 64];
+        } else {
+            kq0 = kq1 = make_uint4(0, 0, 0, 0);
+            ksc = 0;
+        }
+#pragma unroll
+        for (int c = 0; c < AT_C; ++c) {
+            const bool ok = c < cnt;
+            const size_t p = qsa_kv_slot(ids[base + (ok ? c : 0)], dm);
+            vcode[c] = ok ? a.kv.vq[p * kvd + (size_t) j * hd + tid] : (int8_t) 0;
+            vsc[c] = ok ? a.kv.vs[p * (kvd / 64) + (size_t) j * scg + tid / 64] : (uint16_t) 0;
+        }
+    };
+    auto store = [&]() {
+        const _Float16 s = __builtin_bit_cast(_Float16, ksc);
+        const uint32_t wv[8] = {kq0.x, kq0.y, kq0.z, kq0.w, kq1.x, kq1.y, kq1.z, kq1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            f16x4_t v;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = (_Float16) (int8_t) (wv[i] >> (8 * u)) * s;
+            *(f16x4_t*) &sK[kc][kd0 + 4 * i] = v;
+        }
+#pragma unroll
+        for (int c = 0; c < AT_C; c += 4) {
+            f16x4_t v;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = (_Float16) vcode[c + u] * __builtin_bit_cast(_Float16, vsc[c + u]);
+            *(f16x4_t*) &sVt[tid][c] = v;
+        }
+    };
+
+    f32x4_t acc[4];                               // out[h = 4*(lane/16) + i][d = 64w + 16db + lane%16]
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int l16 = lane & 15, kq = lane >> 4;    // MFMA 16x16x16: row/col l16, k quad kq
+
+    if (width > 0) load(0);
+    __syncthreads();
+    if (width > 0) store();
+    __syncthreads();
+    for (int base = 0; base < width; base += AT_C) {
+        const int cnt = min(AT_C, width - base);
+        const bool more = base + AT_C < width;
+        if (more) load(base + AT_C);
+        // scores: wave w -> cells 16*(w&1) .., dims 128*(w>>1) ..
+        {
+            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+            const int cb = (w & 1) * 16, d0 = (w >> 1) * 128;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const f16x4_t av = h4_from(&sQ[l16][d0 + kk * 16 + 4 * kq]);
+                const f16x4_t bv = h4_from(&sK[cb + l16][d0 + kk * 16 + 4 * kq]);
+                sc = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, sc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sS[w >> 1][4 * kq + i][cb + l16] = sc[i];
+        }
+        __syncthreads();
+        // online softmax: wave w -> heads 4w .. 4w+3, two per pass (lane halves), lane = cell
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const int h = 4 * w + 2 * pass + (lane >> 5), c = lane & 31;
+            const bool ok = c < cnt && h < gq;
+            const float s = ok ? sS[0][h][c] + sS[1][h][c] : -1e30f;
+            const float rmax = max32(s);
+            const float m_old = s_m[h];
+            const float m_new = fmaxf(m_old, rmax);
+            const float al = h < gq ? __expf(m_old - m_new) : 1.f;
+            const float pw = ok ? __expf(s - m_new) : 0.f;
+            const float psum = sum32(pw);
+            sP[h][c] = (_Float16) pw;
+            if (c == 0 && h < gq) {
+                s_m[h] = m_new;
+                s_l[h] = s_l[h] * al + psum;
+                s_al[h] = al;
+            }
+        }
+        __syncthreads();
+        // P.V: wave w -> dims 64w .. 64w+63 (four 16-dim blocks), two k16 slices of cells
+        {
+            float al[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) al[i] = s_al[4 * kq + i];
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[db][i] *= al[i];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const f16x4_t pv = h4_from(&sP[l16][ks * 16 + 4 * kq]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const f16x4_t vv = h4_from(&sVt[64 * w + 16 * db + l16][ks * 16 + 4 * kq]);
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pv, vv, acc[db], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+        if (more) store();
+        __syncthreads();
+    }
+    // acc[db][i] = O[head 4*kq + i][dim 64w + 16db + l16]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int h = 4 * kq + i;
+        if (h >= gq) continue;
+        const float inv = 1.0f / fmaxf(s_l[h], 1e-20f);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 64 * w + 16 * db + l16;
+            const float gate = qg[(size_t) (j * gq + h) * 2 * hd + hd + d];
+            const float v = (acc[db][i] * inv) / (1.0f + __expf(-gate));
+            a.out[(size_t) t * dm.qh * hd + (size_t) (j * gq + h) * hd + d] = f_to_bf16(v);
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------------------------
+namespace wzy {
+
+int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
+    WZY_REQUIRE(g.a && (g.wq ? g.ws != nullptr : g.wb != nullptr) && (g.y || g.yb), "pf_gemm: null operand");
+    WZY_REQUIRE(g.M >= 1 && g.N >= 1 && g.K >= GK && g.K % GK == 0, "pf_gemm: M %d N %d K %d (K a multiple of %d)",
+                g.M, g.N, g.K, GK);
+    WZY_REQUIRE(g.lda >= g.K && g.lda % 8 == 0 && g.ldy >= g.N, "pf_gemm: bad leading dimensions");
+    GemmArgs ga;
+    ga.g = g;
+    ga.mt = (g.M + GM - 1) / GM;
+    ga.nt = (g.N + GN - 1) / GN;
+    WZY_REQUIRE((long long) ga.mt * ga.nt < (1LL << 31), "pf_gemm: too many tiles");
+    hipLaunchKernelGGL(pf_gemm_kernel, dim3(ga.mt * ga.nt), dim3(256), 0, st, ga);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_embed(const PfEmb& e, const int* toks, float* R, int D, int HC, int B, hipStream_t st) {
+    hipLaunchKernelGGL(pf_embed_kernel, dim3((D + 255) / 256, B), dim3(256), 0, st, e, toks, R, D, HC);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_hc_norm(float* R, const float* bo, const float* inj_prev, const float* norm_w, uint16_t* xn, int D,
+                      int HC, float eps, int B, hipStream_t st) {
+    hipLaunchKernelGGL(pf_hc_norm_kernel, dim3(HC, B), dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_silu_div(const float* lo, uint16_t* loh, size_t n, float inv_hc, hipStream_t st) {
+    hipLaunchKernelGGL(pf_silu_div_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, lo, loh, n, inv_hc);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_up_mean(const uint16_t* xn, const uint16_t* gg, float* mixed, uint16_t* xh, int D, int HC, int B,
+                      hipStream_t st) {
+    hipLaunchKernelGGL(pf_up_mean_kernel, dim3((D + 255) / 256, B), dim3(256), 0, st, xn, gg, mixed, xh, D, HC);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_hc_write(float* R, const float* blk, const float* inj, int D, int HC, int B, hipStream_t st) {
+    hipLaunchKernelGGL(pf_hc_write_kernel, dim3((HC * D + 255) / 256, B), dim3(256), 0, st, R, blk, inj, D, HC);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_gdn(const PfGdn& g, hipStream_t st) {
+    WZY_REQUIRE(g.hk >= 1 && g.hv % g.hk == 0 && g.B >= 1, "pf_gdn: bad heads / rows");
+    const int QKV = (2 * g.hk + g.hv) * 128;
+    hipLaunchKernelGGL(pf_gdn_ab_kernel, dim3((g.B * g.hv + 255) / 256), dim3(256), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_conv_kernel, dim3(QKV / 128, g.B), dim3(128), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_hist_kernel, dim3((QKV + 255) / 256), dim3(256), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_recur_kernel, dim3(g.hv * 128 / GR_COLS), dim3(256), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_norm_kernel, dim3(g.hv, g.B), dim3(128), 0, st, g);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_qsa_prep(const PfQsaPrep& a, int B, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a.dm));
+    const int roles = a.dm.qh + a.dm.kvh + a.dm.ih;
+    hipLaunchKernelGGL(pf_qsa_prep_kernel, dim3(roles, (B + PR_ROWS - 1) / PR_ROWS), dim3(256), 0, st, a, B);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_idx_append(const PfIdxAppend& a, int p0, int B, hipStream_t st) {
+    const int BL = a.dm.iblk;
+    WZY_REQUIRE(a.dm.idim <= 128 && BL >= 2 && p0 >= 0 && B >= 1 && p0 + B <= a.dm.ctx_max, "pf_idx_append: bad shape");
+    const int has0 = p0 == 0 ? 1 : 0;
+    const int pc0 = p0 + ((BL - 1 - p0 % BL) + BL) % BL;          // first position completing a block
+    const int pe = p0 + B - 1;
+    const int n_comp = pe >= pc0 ? (pe - pc0) / BL + 1 : 0;
+    const int n_ev = has0 + n_comp;
+    if (n_ev > 0)
+        hipLaunchKernelGGL(pf_idx_append_kernel, dim3(n_ev), dim3(256), 0, st, a, p0, B, has0, pc0, n_ev);
+    hipLaunchKernelGGL(pf_idx_tail_kernel, dim3(1), dim3(128), 0, st, a, p0, B);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_attn(const PfAttn& a, int B, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a.dm));
+    WZY_REQUIRE(a.dm.hd == 256 && a.dm.qh / a.dm.kvh <= 16 && a.dm.window == 0, "pf_attn: head layout unsupported");
+    WZY_REQUIRE(B >= 1 && B <= 65535, "pf_attn: %d rows", B);
+    hipLaunchKernelGGL(pf_attn_kernel, dim3(a.dm.kvh, B), dim3(256), 0, st, a);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+}  // namespace wzy
+
+// ---------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------
+extern "C" int wzy_gemm_bf16(const uint16_t* a, int lda, int M, int K, const int8_t* wq, const uint16_t* ws,
+                             const uint16_t* wb, int N, float* y, uint16_t* yb, int ldy, void* stream) {
+    WZY_REQUIRE((y == nullptr) != (yb == nullptr), "wzy_gemm_bf16: exactly one of y / yb");
+    WZY_REQUIRE((wq == nullptr) != (wb == nullptr), "wzy_gemm_bf16: exactly one of wq / wb");
+    PfGemm g{};
+    g.a = a; g.lda = lda; g.M = M; g.N = N; g.K = K;
+    g.wq = wq; g.ws = ws; g.wb = wb; g.y = y; g.yb = yb; g.ldy = ldy;
+    return launch_pf_gemm(g, (hipStream_t) stream);
+}

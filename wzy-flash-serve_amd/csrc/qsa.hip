@@ -15,39 +15,12 @@
 #include "wzy_device.h"
 #include "wzy_host.h"
 #include "wzy_qsa.h"
+#include "wzy_qsa_dev.h"
 
 using namespace wzy;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
-namespace {
-
-// RMSNorm(gamma) + NeoX RoPE (pairs i, i + n_rot/2) of one head vector p[0..hd) in place.
-// 256 threads, thread i owns element i.
-WZY_DEV void norm_rope(float* p, int hd, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
-                       int n_rot, float eps, float* s_vals, float* s_red) {
-    const int i = threadIdx.x;
-    const float x = i < hd ? p[i] : 0.f;
-    const float ss = block_sum<4>(x * x, s_red);
-    const float sc = 1.0f / sqrtf(ss / (float) hd + eps);
-    const float v = x * (sc * (i < hd ? gamma[i] : 0.f));
-    if (i < hd) s_vals[i] = v;
-    __syncthreads();
-    const int half = n_rot / 2;
-    if (i < hd) {
-        float y = v;
-        if (i < n_rot) {
-            const int pr = i % half;
-            const float c = cos_tab[(size_t) pos * half + pr], s = sin_tab[(size_t) pos * half + pr];
-            const float a = s_vals[pr], d = s_vals[pr + half];
-            y = (i < half) ? (a * c - d * s) : (a * s + d * c);
-        }
-        p[i] = y;
-    }
-    __syncthreads();
-}
-
-}  // namespace
 
 // ---------------------------------------------------------------------------------------------
 // prep
@@ -56,7 +29,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
     __shared__ float s_vals[256];
     __shared__ float s_red[4];
     const QsaDims& dm = a.dm;
-    const int wg = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wg = blockIdx.x, tid = threadIdx.x;
     const int base = *a.pos;
     const int hd = dm.hd, kvd = dm.kvh * dm.hd;
 
@@ -77,23 +50,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
             if (pos < 0 || pos >= dm.ctx_max) continue;
             float* kp = a.kk + (size_t) t * kvd + (size_t) j * hd;
             norm_rope(kp, hd, a.k_norm, a.cos_tab, a.sin_tab, pos, dm.n_rot, dm.eps, s_vals, s_red);
-            // per-64 INT8 quantisation: one wave per 64-element group (hd = 256 -> 4 groups)
-            if (tid < hd) {
-                const float kv = kp[tid];
-                const float vv = a.vv[(size_t) t * kvd + (size_t) j * hd + tid];
-                const float kmax = wave_max(fabsf(kv)), vmax = wave_max(fabsf(vv));
-                const uint16_t kh = f_to_h16(kmax / 127.0f), vh = f_to_h16(vmax / 127.0f);
-                const float kdq = h16_to_f(kh), vdq = h16_to_f(vh);
-                const int kqi = kdq > 0.f ? max(-127, min(127, rn_int(kv / kdq))) : 0;
-                const int vqi = vdq > 0.f ? max(-127, min(127, rn_int(vv / vdq))) : 0;
-                const size_t slot = qsa_kv_slot(pos, dm);
-                a.kv.kq[slot * kvd + (size_t) j * hd + tid] = (int8_t) kqi;
-                a.kv.vq[slot * kvd + (size_t) j * hd + tid] = (int8_t) vqi;
-                if (lane == 0) {
-                    a.kv.ks[slot * (kvd / 64) + (size_t) j * (hd / 64) + w] = kh;
-                    a.kv.vs[slot * (kvd / 64) + (size_t) j * (hd / 64) + w] = vh;
-                }
-            }
+            if (tid < hd) qsa_kv_store(dm, a.kv, pos, j, kp[tid], a.vv[(size_t) t * kvd + (size_t) j * hd + tid]);
             __syncthreads();
         }
         return;
@@ -110,7 +67,7 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
     }
     if (dm.window > 0) return;                      // no indexer in window mode
     // indexer append (one workgroup, thread d owns key dim d)
-    const int D = dm.idim, B = dm.iblk, half = dm.n_rot / 2;
+    const int D = dm.idim, B = dm.iblk;
     const int d = tid;
     for (int t = 0; t < T; ++t) {
         const int pos = base + t;
@@ -120,26 +77,9 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
         if (d < D && slot < B - 1) a.ix.tail[slot * D + d] = incoming;
         const int b = pos / B;
         if (pos == 0 || slot == B - 1) {
-            float sum = 0.f;
+            auto cell = [&](int jj) { return (pos == 0 || jj == B - 1) ? incoming : a.ix.tail[jj * D + d]; };
+            const float y = idx_block_key(dm, cell, a.ik_norm, a.cos_tab, a.sin_tab, pos == 0 ? 0 : B * b, s_vals, s_red);
             if (d < D) {
-                sum = (pos == 0) ? incoming : a.ix.tail[d];
-                for (int jj = 1; jj < B; ++jj) sum = sum + ((pos == 0 || jj == B - 1) ? incoming : a.ix.tail[jj * D + d]);
-            }
-            const float mean = sum * (1.0f / (float) B);
-            const float ss = block_sum<4>(mean * mean, s_red);
-            const float sc = 1.0f / sqrtf(ss / (float) D + dm.eps);
-            const float val = d < D ? sc * mean * a.ik_norm[d] : 0.f;
-            s_vals[d] = val;
-            __syncthreads();
-            if (d < D) {
-                const int rope_pos = (pos == 0) ? 0 : B * b;
-                float y = val;
-                if (d < dm.n_rot) {
-                    const int pr = d % half;
-                    const float c = a.cos_tab[(size_t) rope_pos * half + pr], s = a.sin_tab[(size_t) rope_pos * half + pr];
-                    const float x0 = s_vals[pr], z0 = s_vals[pr + half];
-                    y = (d < half) ? (x0 * c - z0 * s) : (x0 * s + z0 * c);
-                }
                 a.ix.pooled[(size_t) b * D + d] = f_to_h16(y);
                 if (pos == 0) a.ix.dead[d] = y;
                 else a.ix.pooled[(size_t) (b + 1) * D + d] = f_to_h16(a.ix.dead[d]);
@@ -161,14 +101,18 @@ __global__ void __launch_bounds__(256) qsa_prep_kernel(QsaPrepArgs a, int T) {
 // ---------------------------------------------------------------------------------------------
 constexpr int SC_BLOCKS_PER_WG = 64;
 
+// Rows: a group of up to T rows per blockIdx.y (rows r0 .. r0+T-1 of a.rows, r0 = T * blockIdx.y).
 template <int T>
 __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
     __shared__ h2_t s_q[T][4][64];          // fp16 indexer queries, ih <= 4, idim = 128
     const QsaDims& dm = a.dm;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int base = *a.pos;
+    const int r0 = blockIdx.y * T, nrows = min(T, a.rows - r0);
+    const int base = *a.pos + r0;
     const int D = dm.idim, B = dm.iblk, IH = dm.ih;
-    const int n_kv_max = base + T;
+    const float* q_idx = a.q_idx + (size_t) r0 * IH * D;
+    float* scores = a.scores + (size_t) r0 * a.max_b;
+    const int n_kv_max = base + nrows;
     if (n_kv_max <= dm.topk) return;                    // short context: identity selection
     const int b0 = blockIdx.x * SC_BLOCKS_PER_WG;
     const bool tail_wg = blockIdx.x == 0;
@@ -177,10 +121,13 @@ __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
     for (int i = tid; i < T * IH * (D / 2); i += blockDim.x) {
         const int t = i / (IH * (D / 2)), r = i % (IH * (D / 2));
         const int h = r / (D / 2), k = r % (D / 2);
-        const float* q = a.q_idx + (size_t) t * IH * D + (size_t) h * D + 2 * k;
         h2_t v;
-        v.x = (_Float16) q[0];
-        v.y = (_Float16) q[1];
+        v.x = v.y = (_Float16) 0.f;
+        if (t < nrows) {
+            const float* q = q_idx + (size_t) t * IH * D + (size_t) h * D + 2 * k;
+            v.x = (_Float16) q[0];
+            v.y = (_Float16) q[1];
+        }
         s_q[t][h][k] = v;
     }
     __syncthreads();
@@ -216,24 +163,24 @@ __global__ void __launch_bounds__(256) qsa_score_kernel(QsaScoreArgs a) {
                 dd = sum16(dd);
                 score += dd > 0.f ? dd : 0.f;
             }
-            if (li == 0 && n_kv > dm.topk && b < n_kv / B) a.scores[(size_t) t * a.max_b + b] = score;
+            if (li == 0 && t < nrows && n_kv > dm.topk && b < n_kv / B) scores[(size_t) t * a.max_b + b] = score;
         }
     }
     // open block: fp32 dot with the placeholder key (wave t handles row t)
     if (tail_wg) {
-        for (int t = w; t < T; t += 4) {
+        for (int t = w; t < nrows; t += 4) {
             const int n_kv = base + t + 1;
             const int nbid = n_kv / B;
             if (n_kv <= dm.topk || nbid >= a.max_b) continue;
             float score = 0.f;
             for (int h = 0; h < IH; ++h) {
                 float p = 0.f;
-                for (int k = lane; k < D; k += 64) p = fmaf(a.dead[k], a.q_idx[(size_t) t * IH * D + (size_t) h * D + k], p);
+                for (int k = lane; k < D; k += 64) p = fmaf(a.dead[k], q_idx[(size_t) t * IH * D + (size_t) h * D + k], p);
                 p = wave_sum(p);
                 score += p > 0.f ? p : 0.f;
             }
             if (n_kv % B != 0) score += 1e9f;
-            if (lane == 0) a.scores[(size_t) t * a.max_b + nbid] = score;
+            if (lane == 0) scores[(size_t) t * a.max_b + nbid] = score;
         }
     }
 }
@@ -280,10 +227,12 @@ int launch_qsa_prep(const QsaPrepArgs& a, int T, hipStream_t st) {
     return WZY_OK;
 }
 
-int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
-    WZY_TRY(qsa_check_dims(a.dm));
-    WZY_REQUIRE(a.dm.idim == 128, "qsa_score: indexer key width must be 128");
+int launch_qsa_score(const QsaScoreArgs& a0, int T, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a0.dm));
+    WZY_REQUIRE(a0.dm.idim == 128, "qsa_score: indexer key width must be 128");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "qsa_score: T out of range");
+    QsaScoreArgs a = a0;
+    a.rows = T;
     const int grid = (a.max_b + SC_BLOCKS_PER_WG - 1) / SC_BLOCKS_PER_WG;
     switch (T) {
 #define C_(TT) case TT: hipLaunchKernelGGL((qsa_score_kernel<TT>), dim3(grid), dim3(256), 0, st, a); break;
@@ -291,6 +240,19 @@ int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st) {
         default: hipLaunchKernelGGL((qsa_score_kernel<8>), dim3(grid), dim3(256), 0, st, a); break;
 #undef C_
     }
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_qsa_score_rows(const QsaScoreArgs& a0, int rows, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a0.dm));
+    WZY_REQUIRE(a0.dm.idim == 128, "qsa_score: indexer key width must be 128");
+    WZY_REQUIRE(rows >= 1 && (rows + WZY_MAX_W - 1) / WZY_MAX_W <= 65535, "qsa_score: %d rows", rows);
+    QsaScoreArgs a = a0;
+    a.rows = rows;
+    const int grid = (a.max_b + SC_BLOCKS_PER_WG - 1) / SC_BLOCKS_PER_WG;
+    hipLaunchKernelGGL((qsa_score_kernel<WZY_MAX_W>), dim3(grid, (rows + WZY_MAX_W - 1) / WZY_MAX_W), dim3(256), 0, st,
+                       a);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }

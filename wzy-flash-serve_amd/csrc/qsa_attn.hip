@@ -13,6 +13,7 @@
 #include "wzy_device.h"
 #include "wzy_host.h"
 #include "wzy_qsa.h"
+#include "wzy_prefill.h"
 
 using namespace wzy;
 
@@ -628,6 +629,25 @@ int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int 
     const int G = (max_b + TK_CHUNK - 1) / TK_CHUNK;
     WZY_REQUIRE(G <= TK_MAX_WG, "qsa_topk: %d indexer blocks exceed %d", max_b, TK_MAX_WG * TK_CHUNK);
     hipLaunchKernelGGL(qsa_topk_kernel, dim3(G, T), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b, hist, arrive,
+                       sel_ids, sel_cnt);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_qsa_topk_rows(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
+                         int rows, int max_n_kv, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(dm));
+    WZY_REQUIRE(rows >= 1 && rows <= 65535, "qsa_topk: %d rows", rows);
+    WZY_REQUIRE(max_b >= 1 && max_b <= (1 << 22), "qsa_topk: max_b %d out of range", max_b);
+    // every row must take the one-workgroup path (its blocks fit one workgroup's registers): the
+    // multi-workgroup merge keeps per-row counters for at most WZY_MAX_W rows
+    WZY_REQUIRE(max_n_kv / dm.iblk + 1 <= TK_CHUNK, "qsa_topk: %d cells exceed one workgroup's %d blocks", max_n_kv,
+                TK_CHUNK);
+    int* hist = nullptr;
+    unsigned* arrive = nullptr;
+    WZY_HIP_TRY(hipGetSymbolAddress((void**) &hist, HIP_SYMBOL(g_tk_hist)));
+    WZY_HIP_TRY(hipGetSymbolAddress((void**) &arrive, HIP_SYMBOL(g_tk_arrive)));
+    hipLaunchKernelGGL(qsa_topk_kernel, dim3(1, rows), dim3(TK_THREADS), 0, st, dm, pos, scores, max_b, hist, arrive,
                        sel_ids, sel_cnt);
     WZY_LAUNCH_CHECK();
     return WZY_OK;

@@ -26,6 +26,7 @@
 #include "wzy_host.h"
 #include "wzy_moe.h"
 #include "wzy_mtp.h"
+#include "wzy_prefill.h"
 #include "wzy_stage_int.h"
 #include "wzy_qsa.h"
 #include "wzy_reduce.h"
@@ -204,6 +205,34 @@ struct wzy_stage {
     SessionSlot sess[WZY_SESSION_SLOTS];
     void session_regions(int n_cells, std::vector<std::pair<void*, size_t>>& out) const;
 
+    // chunked-prefill workspace, sized for `cap` rows on the first prefill that needs it
+    struct PfWs {
+        int cap = 0;
+        void* base = nullptr;
+        size_t bytes = 0;
+        float *R = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
+        uint16_t *xn = nullptr, *loh = nullptr, *gg = nullptr, *xh = nullptr;
+        float *qkv = nullptr, *z = nullptr, *ab = nullptr, *conv_out = nullptr, *decay = nullptr, *beta = nullptr,
+              *o = nullptr;
+        float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
+        int *sel = nullptr, *cnt = nullptr;
+        float *block = nullptr, *comb = nullptr;
+        void* moe_ws = nullptr;
+        size_t moe_bytes = 0;
+        int* toks = nullptr;
+        int* pos8 = nullptr;        // [cap / 8 + 2]: p0 + 8 i
+        int sc_rows = 0;            // rows per block-score pass
+        float* tr = nullptr;        // per-layer trace [n_layers][4][tr_rows][D] (while tracing)
+        int* tr_sel = nullptr;      // per QSA layer: selected cells [n_qsa][tr_rows][topk], counts
+        int* tr_cnt = nullptr;      // [n_qsa][tr_rows]
+        float* tr_sc = nullptr;     // block scores [n_qsa][tr_rows][max_b]
+        int tr_rows = 0;
+    } pf;
+    bool pre_head_pf = false;       // the pre-head rows of the last call are the prefill's residual
+    const float* pre_head_rows() const { return pre_head_pf ? pf.R : R[r_pre_head]; }
+    int prefill_reserve(int B);
+    int enqueue_prefill(int p0, int B, float* us_parts);
+
     std::map<unsigned long long, hipGraphExec_t> graph_execs;
     CommitJob* commit_jobs = nullptr;   // device table of commit_window_state's copies
     int n_commit_jobs = 0;
@@ -242,6 +271,10 @@ wzy_stage::~wzy_stage() {
         if (sl.buf) (void) hipFree(sl.buf);
         if (sl.jobs) (void) hipFree(sl.jobs);
     }
+    if (pf.base) (void) hipFree(pf.base);
+    if (pf.tr) (void) hipFree(pf.tr);
+    if (pf.tr_sel) (void) hipFree(pf.tr_sel);
+    if (pf.tr_sc) (void) hipFree(pf.tr_sc);
     for (auto& kv : graph_execs)
         if (kv.second) (void) hipGraphExecDestroy(kv.second);
     for (void* p : allocs) (void) hipFree(p);
@@ -850,6 +883,7 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
     st->last_T = T;
     st->have_head = run_head == 1;
     st->have_pre_head = run_head != 0;
+    st->pre_head_pf = false;
     const bool use_graph = st->graphs && !st->profiling && !st->trace;
     if (!use_graph) return st->enqueue(T, emb != nullptr, run_head, save_snaps, want_top16, snap_offset);
     const unsigned long long key = ((unsigned long long) T << 16) | ((unsigned long long) snap_offset << 8) |
@@ -1101,7 +1135,7 @@ extern "C" int wzy_stage_logits(wzy_stage* st, float* out, int T) {
 }
 extern "C" int wzy_stage_pre_head(wzy_stage* st, float* out, int T) {
     WZY_REQUIRE(st && out && T >= 1 && T <= st->last_T && st->have_pre_head, "pre_head: no pre-head output");
-    WZY_HIP_TRY(hipMemcpy(out, st->R[st->r_pre_head], (size_t) T * st->HCD * 4, hipMemcpyDeviceToHost));
+    WZY_HIP_TRY(hipMemcpy(out, st->pre_head_rows(), (size_t) T * st->HCD * 4, hipMemcpyDeviceToHost));
     return WZY_OK;
 }
 
@@ -1201,7 +1235,7 @@ static int mtp_take_rows(wzy_stage* st, int src_row0, int n) {
     WZY_REQUIRE(st->have_pre_head && src_row0 >= 0 && src_row0 + n <= st->last_T,
                 "mtp: rows [%d, %d) are not pre-head rows of the last forward (%d rows%s)", src_row0, src_row0 + n,
                 st->last_T, st->have_pre_head ? "" : ", run without the head");
-    WZY_HIP_TRY(hipMemcpyAsync(st->mtp->rin, st->R[st->r_pre_head] + (size_t) src_row0 * st->HCD,
+    WZY_HIP_TRY(hipMemcpyAsync(st->mtp->rin, st->pre_head_rows() + (size_t) src_row0 * st->HCD,
                                (size_t) n * st->HCD * 4, hipMemcpyDeviceToDevice, st->stream));
     return WZY_OK;
 }
@@ -1335,4 +1369,307 @@ extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, f
     moe_ws_carve(nullptr, 0, st->D, st->cfg.n_ff, st->cfg.n_exp, st->cfg.top_k, WZY_MAX_W, &need);
     return wzy_moe_time_kernels(ws.data(), (int) ws.size(), T, st->mixed, st->moe_ws, need + 256, iters, us_gate_up,
                                 us_down, st->stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// chunked prefill (PrefillStageCtx::run_stage_prefill, src/wzy_prefill_tc.cuh:546-1058)
+// ------------------------------------------------------------------------------------------------
+namespace {
+constexpr int PF_SCORE_ROWS = 2048;     // rows per block-score pass (the reference's qsa_score_b)
+
+__global__ void pf_pos_kernel(int* pos8, int p0, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) pos8[i] = p0 + 8 * i;
+}
+}  // namespace
+
+int wzy_stage::prefill_reserve(int B) {
+    const wzy_stage_cfg& c = cfg;
+    if (trace && B > pf.tr_rows) {
+        WZY_HIP_TRY(hipStreamSynchronize(stream));
+        if (pf.tr) WZY_HIP_TRY(hipFree(pf.tr));
+        if (pf.tr_sel) WZY_HIP_TRY(hipFree(pf.tr_sel));
+        if (pf.tr_sc) WZY_HIP_TRY(hipFree(pf.tr_sc));
+        pf.tr = nullptr;
+        pf.tr_sel = pf.tr_cnt = nullptr;
+        pf.tr_sc = nullptr;
+        const size_t n = (size_t) c.n_layers * 4 * B * D;
+        WZY_HIP_TRY(hipMalloc((void**) &pf.tr, n * 4));
+        const size_t nq = (size_t) std::max(n_qsa, 1), ns = nq * B * c.idx_topk;
+        WZY_HIP_TRY(hipMalloc((void**) &pf.tr_sel, (ns + nq * B) * 4));
+        pf.tr_cnt = pf.tr_sel + ns;
+        const size_t nsc = nq * B * (size_t) max_b;
+        WZY_HIP_TRY(hipMalloc((void**) &pf.tr_sc, nsc * 4));
+        reg(-1, "trace.pf_scores", pf.tr_sc, nsc * 4);
+        pf.tr_rows = B;
+        reg(-1, "trace.pf", pf.tr, n * 4);
+        reg(-1, "trace.pf_sel", pf.tr_sel, ns * 4);
+        reg(-1, "trace.pf_cnt", pf.tr_cnt, nq * B * 4);
+    }
+    if (B <= pf.cap) return WZY_OK;
+    WZY_HIP_TRY(hipStreamSynchronize(stream));
+    if (pf.base) {
+        WZY_HIP_TRY(hipFree(pf.base));
+        dev_bytes -= pf.bytes;
+        float* keep_tr = pf.tr;
+        int *keep_sel = pf.tr_sel, *keep_cnt = pf.tr_cnt;
+        float* keep_sc = pf.tr_sc;
+        const int keep_rows = pf.tr_rows;
+        pf = PfWs{};
+        pf.tr = keep_tr;
+        pf.tr_sc = keep_sc;
+        pf.tr_sel = keep_sel;
+        pf.tr_cnt = keep_cnt;
+        pf.tr_rows = keep_rows;
+    }
+    const size_t b = (size_t) B, maxb = (size_t) max_b;
+    const int sc_rows = std::min(B, PF_SCORE_ROWS);
+    const size_t xh_w = (size_t) std::max(std::max(D, GV), QD);
+    const size_t moe_bytes = wzy_moe_prefill_workspace_bytes(D, c.n_ff, c.n_exp, c.top_k, B);
+    // layout: one allocation, 256-byte aligned pieces
+    size_t off = 0;
+    auto bump = [&](size_t bytes) {
+        const size_t r = off;
+        off += (bytes + 255) & ~(size_t) 255;
+        return r;
+    };
+    const size_t oR = bump(b * HCD * 4), oxn = bump(b * HCD * 2), olo = bump(b * c.hc_lr * 4),
+                 oloh = bump(b * c.hc_lr * 2), ogg = bump(b * HCD * 2), oia = bump(b * c.hc * 4),
+                 oif = bump(b * c.hc * 4), omx = bump(b * D * 4), oxh = bump(b * xh_w * 2), oblk = bump(b * D * 4),
+                 ocomb = bump(b * D * 4), otoks = bump(b * 4), opos = bump((b / 8 + 2) * 4);
+    // GDN and QSA scratch share one region (a layer uses one of them)
+    const size_t umark = off;
+    const size_t oqkv = bump(b * QKV * 4), oz = bump(b * GV * 4), oab = bump(b * 2 * c.gdn_hv * 4),
+                 oco = bump(b * QKV * 4), odec = bump(b * c.gdn_hv * 4), obet = bump(b * c.gdn_hv * 4),
+                 oo = bump(b * GV * 4);
+    const size_t gdn_end = off;
+    off = umark;
+    const size_t oqg = bump(b * 2 * QD * 4), okk = bump(b * KVD * 4), ovv = bump(b * KVD * 4),
+                 oir = bump(b * c.idx_dim * 4), oqi = bump(b * c.idx_heads * c.idx_dim * 4),
+                 osc = bump((size_t) sc_rows * maxb * 4), osel = bump(b * c.idx_topk * 4), ocnt = bump(b * 4);
+    off = std::max(off, gdn_end);
+    const size_t omoe = bump(moe_bytes);
+    void* base = nullptr;
+    if (hipMalloc(&base, off) != hipSuccess) {
+        (void) hipGetLastError();
+        set_error("prefill: hipMalloc(%zu) for a %d-row workspace failed", off, B);
+        return WZY_ENOMEM;
+    }
+    dev_bytes += off;
+    unsigned char* u = (unsigned char*) base;
+    pf.base = base;
+    pf.bytes = off;
+    pf.cap = B;
+    pf.sc_rows = sc_rows;
+    pf.R = (float*) (u + oR); pf.xn = (uint16_t*) (u + oxn); pf.lo = (float*) (u + olo);
+    pf.loh = (uint16_t*) (u + oloh); pf.gg = (uint16_t*) (u + ogg); pf.inj_a = (float*) (u + oia);
+    pf.inj_f = (float*) (u + oif); pf.mixed = (float*) (u + omx); pf.xh = (uint16_t*) (u + oxh);
+    pf.block = (float*) (u + oblk); pf.comb = (float*) (u + ocomb); pf.toks = (int*) (u + otoks);
+    pf.pos8 = (int*) (u + opos);
+    pf.qkv = (float*) (u + oqkv); pf.z = (float*) (u + oz); pf.ab = (float*) (u + oab);
+    pf.conv_out = (float*) (u + oco); pf.decay = (float*) (u + odec); pf.beta = (float*) (u + obet);
+    pf.o = (float*) (u + oo);
+    pf.qg = (float*) (u + oqg); pf.kk = (float*) (u + okk); pf.vv = (float*) (u + ovv);
+    pf.idx_raw = (float*) (u + oir); pf.q_idx = (float*) (u + oqi); pf.scores = (float*) (u + osc);
+    pf.sel = (int*) (u + osel); pf.cnt = (int*) (u + ocnt);
+    pf.moe_ws = u + omoe;
+    pf.moe_bytes = moe_bytes;
+    return WZY_OK;
+}
+
+// Layer sequence of one chunk (rows p0 .. p0+B-1, token ids already in pf.toks).  us_parts (optional,
+// host) receives event-timed microseconds per part: [0] attention-half HC reads, [1] GDN blocks, [2]
+// QSA blocks, [3] FFN-half HC reads, [4] MoE blocks, [5] everything else (embedding, writes).
+int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
+    const wzy_stage_cfg& c = cfg;
+    hipStream_t st = stream;
+    const int HC = c.hc, HCLR = c.hc_lr;
+    const float inv_hc = 1.0f / (float) HC;
+    hipEvent_t evs[2] = {nullptr, nullptr};
+    double part[6] = {0, 0, 0, 0, 0, 0};
+    int cur_part = 5;
+    if (us_parts) {
+        WZY_HIP_TRY(hipEventCreate(&evs[0]));
+        WZY_HIP_TRY(hipEventCreate(&evs[1]));
+        WZY_HIP_TRY(hipEventRecord(evs[0], st));
+    }
+    // close the running part and open `next` (event-timed; synchronises only when measuring)
+    auto mark = [&](int next) -> int {
+        if (!us_parts) return WZY_OK;
+        WZY_HIP_TRY(hipEventRecord(evs[1], st));
+        WZY_HIP_TRY(hipEventSynchronize(evs[1]));
+        float ms = 0.f;
+        WZY_HIP_TRY(hipEventElapsedTime(&ms, evs[0], evs[1]));
+        part[cur_part] += ms * 1000.0;
+        std::swap(evs[0], evs[1]);
+        cur_part = next;
+        return WZY_OK;
+    };
+    auto gemm = [&](const uint16_t* a, int lda, int K, const Q8* q, const uint16_t* wb, int N, float* y,
+                    uint16_t* yb, int ldy) {
+        PfGemm g{};
+        g.a = a; g.lda = lda; g.M = B; g.N = N; g.K = K;
+        if (q) { g.wq = q->q; g.ws = q->s; } else { g.wb = wb; }
+        g.y = y; g.yb = yb; g.ldy = ldy;
+        return launch_pf_gemm(g, st);
+    };
+    // hyper-connection read of the chunk: R (with the pending block folded in when bo != null) ->
+    // mixed fp32 + xh bf16, inject -> inj_out
+    auto hc_read = [&](const float* norm_w, const Q8& down, const uint16_t* inj_w, const Q8& up, const float* bo,
+                       const float* inj_prev, float* inj_out) -> int {
+        WZY_TRY(launch_pf_hc_norm(pf.R, bo, inj_prev, norm_w, pf.xn, D, HC, c.eps, B, st));
+        WZY_TRY(gemm(pf.xn, HCD, HCD, nullptr, inj_w, HC, inj_out, nullptr, HC));
+        WZY_TRY(gemm(pf.xn, HCD, HCD, &down, nullptr, HCLR, pf.lo, nullptr, HCLR));
+        WZY_TRY(launch_pf_silu_div(pf.lo, pf.loh, (size_t) B * HCLR, inv_hc, st));
+        WZY_TRY(gemm(pf.loh, HCLR, HCLR, &up, nullptr, HCD, nullptr, pf.gg, HCD));
+        return launch_pf_up_mean(pf.xn, pf.gg, pf.mixed, pf.xh, D, HC, B, st);
+    };
+
+    hipLaunchKernelGGL(pf_pos_kernel, dim3((B / 8 + 2 + 255) / 256), dim3(256), 0, st, pf.pos8, p0, B / 8 + 2);
+    PfEmb e{};
+    if (c.emb_q8) { e.emb_q = emb8.q; e.emb_s = emb8.s; } else { e.emb = emb; }
+    e.n_vocab = c.n_vocab;
+    WZY_TRY(launch_pf_embed(e, pf.toks, pf.R, D, HC, B, st));
+    const float* pend_bo = nullptr;
+    const float* pend_inj = nullptr;
+    QsaDims dm = qd;
+    // trace copies (wzy_stage_set_trace): [layer][slot][row][D], slots mixed_a, block, mixed_f, comb
+    auto tr = [&](int l, int slot, const float* src) -> int {
+        if (!trace || !pf.tr) return WZY_OK;
+        WZY_HIP_TRY(hipMemcpyAsync(pf.tr + (((size_t) l * 4 + slot) * pf.tr_rows) * D, src, (size_t) B * D * 4,
+                                   hipMemcpyDeviceToDevice, st));
+        return WZY_OK;
+    };
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer& w = L[l];
+        WZY_TRY(mark(0));
+        WZY_TRY(hc_read(w.hc_norm[0], w.hc_down[0], w.hc_inj[0], w.hc_up[0], pend_bo, pend_inj, pf.inj_a));
+        WZY_TRY(tr(l, 0, pf.mixed));
+        if (!w.qsa) {
+            WZY_TRY(mark(1));
+            const int hv = c.gdn_hv;
+            WZY_TRY(gemm(pf.xh, D, D, &w.qkv, nullptr, QKV, pf.qkv, nullptr, QKV));
+            WZY_TRY(gemm(pf.xh, D, D, &w.wgate, nullptr, GV, pf.z, nullptr, GV));
+            WZY_TRY(gemm(pf.xh, D, D, nullptr, w.alpha, hv, pf.ab, nullptr, 2 * hv));
+            WZY_TRY(gemm(pf.xh, D, D, nullptr, w.beta, hv, pf.ab + hv, nullptr, 2 * hv));
+            PfGdn g{};
+            g.hk = c.gdn_hk; g.hv = hv; g.B = B; g.eps = c.eps;
+            g.qkv = pf.qkv; g.z = pf.z; g.ab = pf.ab; g.dt = w.dt; g.ssm_a = w.ssm_a; g.conv_w = w.conv_w;
+            g.gamma = w.ssm_norm; g.conv_hist = w.conv_hist; g.state = w.ssm; g.conv_out = pf.conv_out;
+            g.decay = pf.decay; g.beta = pf.beta; g.o = pf.o; g.y = pf.xh;
+            WZY_TRY(launch_pf_gdn(g, st));
+            WZY_TRY(gemm(pf.xh, GV, GV, &w.wout, nullptr, D, pf.block, nullptr, D));
+        } else {
+            WZY_TRY(mark(2));
+            const int ID = c.idx_dim, IH = c.idx_heads;
+            WZY_TRY(gemm(pf.xh, D, D, &w.wq, nullptr, 2 * QD, pf.qg, nullptr, 2 * QD));
+            WZY_TRY(gemm(pf.xh, D, D, &w.wk, nullptr, KVD, pf.kk, nullptr, KVD));
+            WZY_TRY(gemm(pf.xh, D, D, &w.wv, nullptr, KVD, pf.vv, nullptr, KVD));
+            WZY_TRY(gemm(pf.xh, D, D, nullptr, w.idx_k, ID, pf.idx_raw, nullptr, ID));
+            WZY_TRY(gemm(pf.xh, D, D, nullptr, w.idx_q, IH * ID, pf.q_idx, nullptr, IH * ID));
+            PfQsaPrep pa{};
+            pa.dm = dm; pa.pos = pf.pos8; pa.qg = pf.qg; pa.kk = pf.kk; pa.vv = pf.vv; pa.q_idx = pf.q_idx;
+            pa.q_norm = w.q_norm; pa.k_norm = w.k_norm; pa.iq_norm = w.idx_qn; pa.cos_tab = cos_tab; pa.sin_tab = sin_tab;
+            pa.kv = w.kv;
+            WZY_TRY(launch_pf_qsa_prep(pa, B, st));
+            PfIdxAppend ia{};
+            ia.dm = dm; ia.idx_raw = pf.idx_raw; ia.ik_norm = w.idx_kn; ia.cos_tab = cos_tab; ia.sin_tab = sin_tab;
+            ia.ix = w.ix;
+            ia.ix.tail_snaps = nullptr; ia.ix.dead_snaps = nullptr; ia.ix.pool_snaps = nullptr;
+            WZY_TRY(launch_pf_idx_append(ia, p0, B, st));
+            for (int q0 = 0; q0 < B; q0 += pf.sc_rows) {
+                const int qb = std::min(pf.sc_rows, B - q0);
+                if (p0 + q0 + qb > c.idx_topk) {
+                    QsaScoreArgs sa{};
+                    sa.dm = dm; sa.pos = pf.pos8 + q0 / 8; sa.pooled = w.ix.pooled; sa.dead = w.ix.dead;
+                    sa.q_idx = pf.q_idx + (size_t) q0 * IH * ID; sa.scores = pf.scores; sa.max_b = max_b;
+                    WZY_TRY(launch_qsa_score_rows(sa, qb, st));
+                    if (trace && pf.tr_sc)
+                        WZY_HIP_TRY(hipMemcpyAsync(pf.tr_sc + ((size_t) w.local * pf.tr_rows + q0) * max_b, pf.scores,
+                                                   (size_t) qb * max_b * 4, hipMemcpyDeviceToDevice, st));
+                }
+                const int max_n_kv = p0 + q0 + qb;
+                if (max_n_kv / c.idx_blk + 1 <= 16384) {
+                    WZY_TRY(launch_qsa_topk_rows(dm, pf.pos8 + q0 / 8, pf.scores, max_b, pf.sel + (size_t) q0 * c.idx_topk,
+                                                 pf.cnt + q0, qb, max_n_kv, st));
+                } else {
+                    for (int g0 = 0; g0 < qb; g0 += WZY_MAX_W)
+                        WZY_TRY(launch_qsa_topk(dm, pf.pos8 + (q0 + g0) / 8, pf.scores + (size_t) g0 * max_b, max_b,
+                                                pf.sel + (size_t) (q0 + g0) * c.idx_topk, pf.cnt + q0 + g0,
+                                                std::min(WZY_MAX_W, qb - g0), st));
+                }
+            }
+            if (trace && pf.tr_sel) {
+                WZY_HIP_TRY(hipMemcpyAsync(pf.tr_sel + (size_t) w.local * pf.tr_rows * c.idx_topk, pf.sel,
+                                           (size_t) B * c.idx_topk * 4, hipMemcpyDeviceToDevice, st));
+                WZY_HIP_TRY(hipMemcpyAsync(pf.tr_cnt + (size_t) w.local * pf.tr_rows, pf.cnt, (size_t) B * 4,
+                                           hipMemcpyDeviceToDevice, st));
+            }
+            PfAttn at{};
+            at.dm = dm; at.pos = pf.pos8; at.qg = pf.qg; at.kv = w.kv; at.sel = pf.sel; at.out = pf.xh;
+            WZY_TRY(launch_pf_attn(at, B, st));
+            WZY_TRY(gemm(pf.xh, QD, QD, &w.wo, nullptr, D, pf.block, nullptr, D));
+        }
+        WZY_TRY(tr(l, 1, pf.block));
+        WZY_TRY(mark(5));
+        WZY_TRY(launch_pf_hc_write(pf.R, pf.block, pf.inj_a, D, HC, B, st));
+        WZY_TRY(mark(3));
+        WZY_TRY(hc_read(w.hc_norm[1], w.hc_down[1], w.hc_inj[1], w.hc_up[1], nullptr, nullptr, pf.inj_f));
+        WZY_TRY(tr(l, 2, pf.mixed));
+        WZY_TRY(mark(4));
+        WZY_TRY(wzy_moe_prefill(&w.moe, pf.mixed, B, pf.comb, nullptr, nullptr, pf.moe_ws, pf.moe_bytes, st));
+        WZY_TRY(tr(l, 3, pf.comb));
+        pend_bo = pf.comb;
+        pend_inj = pf.inj_f;
+    }
+    WZY_TRY(mark(5));
+    WZY_TRY(launch_pf_hc_write(pf.R, pend_bo, pend_inj, D, HC, B, st));
+    if (us_parts) {
+        WZY_TRY(mark(5));
+        for (int i = 0; i < 6; ++i) us_parts[i] = (float) part[i];
+        (void) hipEventDestroy(evs[0]);
+        (void) hipEventDestroy(evs[1]);
+    }
+    return WZY_OK;
+}
+
+static int prefill_checks(wzy_stage* st, int pos, const int* toks, int B) {
+    WZY_REQUIRE(st && st->loaded, "prefill: stage not loaded");
+    WZY_REQUIRE(toks && B >= 1 && B <= 65535, "prefill: B must be in [1, 65535] with token ids");
+    WZY_REQUIRE(pos >= 0 && pos + B <= st->cfg.ctx_max, "prefill: positions [%d, %d) exceed ctx_max %d", pos, pos + B,
+                st->cfg.ctx_max);
+    const wzy_stage_cfg& c = st->cfg;
+    WZY_REQUIRE(c.hc_lr % 64 == 0 && c.n_embd % 256 == 0 && c.n_ff % 128 == 0 && c.n_exp % 64 == 0 &&
+                    c.n_exp <= 1024 && c.idx_dim == 128,
+                "prefill: shape unsupported (hc_lr a multiple of 64, n_embd of 256, n_ff of 128, n_exp of 64 up to "
+                "1024, idx_dim 128)");
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_prefill(wzy_stage* st, int pos, const int* toks, int B) {
+    WZY_TRY(prefill_checks(st, pos, toks, B));
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    WZY_TRY(st->prefill_reserve(B));
+    WZY_HIP_TRY(hipMemcpyAsync(st->pf.toks, toks, (size_t) B * sizeof(int), hipMemcpyHostToDevice, st->stream));
+    WZY_TRY(st->enqueue_prefill(pos, B, nullptr));
+    st->last_T = B;
+    st->have_head = false;
+    st->have_pre_head = true;
+    st->pre_head_pf = true;
+    return WZY_OK;
+}
+
+extern "C" int wzy_stage_prefill_time(wzy_stage* st, int pos, const int* toks, int B, float* us_parts) {
+    WZY_REQUIRE(us_parts, "prefill_time: null output");
+    WZY_TRY(prefill_checks(st, pos, toks, B));
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    WZY_TRY(st->prefill_reserve(B));
+    WZY_HIP_TRY(hipMemcpyAsync(st->pf.toks, toks, (size_t) B * sizeof(int), hipMemcpyHostToDevice, st->stream));
+    WZY_TRY(st->enqueue_prefill(pos, B, us_parts));
+    WZY_HIP_TRY(hipStreamSynchronize(st->stream));
+    st->last_T = B;
+    st->have_head = false;
+    st->have_pre_head = true;
+    st->pre_head_pf = true;
+    return WZY_OK;
 }

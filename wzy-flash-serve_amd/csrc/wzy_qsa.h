@@ -87,8 +87,12 @@ struct QsaScoreArgs {
     const float* q_idx;                // [T][ih*idim]
     float* scores;                     // [T][max_b]
     int max_b;                         // ctx_max/iblk + 2
+    int rows = 0;                      // rows scored (set by the launchers)
 };
 int launch_qsa_score(const QsaScoreArgs& a, int T, hipStream_t st);
+// Block scores of `rows` consecutive rows (positions *pos + r), groups of 8 rows per grid row
+// (prefill chunks); q_idx [rows][ih*idim], scores [rows][max_b].
+int launch_qsa_score_rows(const QsaScoreArgs& a, int rows, hipStream_t st);
 int launch_qsa_topk(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids, int* sel_cnt,
                     int T, hipStream_t st);
 

@@ -128,6 +128,8 @@ _SIGS = {
     "wzy_stage_device_bytes": (SZ, [P], False),
     "wzy_stage_load_synthetic": (I32, [P, U64, I32], True),
     "wzy_stage_record_forward": (I32, [P, I32, P, P, I32, I32, I32, I32, I32], True),
+    "wzy_stage_prefill": (I32, [P, I32, P, I32], True),
+    "wzy_stage_prefill_time": (I32, [P, I32, P, I32, C.POINTER(F32)], True),
     "wzy_stage_service_cold_layers": (I32, [P], True),
     "wzy_stage_promote_cold": (I32, [P], True),
     "wzy_stage_commit_window_state": (I32, [P, I32, I32], True),
@@ -182,6 +184,7 @@ _SIGS = {
     "wzy_moe_workspace_bytes": (SZ, [I32, I32, I32, I32, I32], False),
     "wzy_moe_block": (I32, [C.POINTER(MoeWeights), P, I32, P, P, P, P, SZ, P], True),
     "wzy_moe_route": (I32, [P, I32, I32, I32, P, P, P], True),
+    "wzy_gemm_bf16": (I32, [P, I32, I32, I32, P, P, P, I32, P, P, I32, P], True),
     "wzy_moe_prefill_workspace_bytes": (SZ, [I32, I32, I32, I32, I32], False),
     "wzy_moe_prefill": (I32, [C.POINTER(MoeWeights), P, I32, P, P, P, P, SZ, P], True),
     "wzy_moe_prefill_time": (I32, [C.POINTER(MoeWeights), P, I32, P, P, SZ, I32, C.POINTER(F32), P], True),
@@ -381,6 +384,11 @@ class Stage:
         e = None if emb is None else np.ascontiguousarray(emb, dtype=np.float32)
         self.lib.wzy_stage_record_forward(self.h, int(pos), ptr(e), toks.ctypes.data, len(toks), int(run_head),
                                           int(save_snaps), int(want_top16), int(snap_offset))
+
+    def prefill(self, pos, toks):
+        import numpy as np
+        toks = np.ascontiguousarray(toks, dtype=np.int32)
+        self.lib.wzy_stage_prefill(self.h, int(pos), toks.ctypes.data, len(toks))
 
     def sync(self):
         self.lib.wzy_stage_sync(self.h)
