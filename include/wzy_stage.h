@@ -92,6 +92,10 @@ int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb, const int
  * Replaces PrefillStageCtx::run_stage_prefill (src/wzy_prefill_tc.cuh:546-1058) for one stage
  * holding every layer (no expert streaming: every expert is resident). */
 int wzy_stage_prefill(wzy_stage* st, int pos, const int* toks, int B);
+/* 1 when a stage of this configuration can run wzy_stage_prefill (the shape limits above), else 0
+ * (a host then feeds prompts through record_forward windows, as the reference does for short
+ * remainders). */
+int wzy_stage_can_prefill(const wzy_stage_cfg* cfg);
 /* Same, timed: us_parts[6] = microseconds spent in the attention-half HC reads, GDN blocks, QSA
  * blocks, FFN-half HC reads, MoE blocks and the rest (HIP events between the parts; synchronous).
  * Counterpart of the reference's WZY_PF_PROF timers (src/wzy_prefill_tc.cuh:734-741,1048-1051). */

@@ -382,3 +382,40 @@ def test_prefill_errors(wz, gpu):
             st.prefill(0, [])
     finally:
         st.close()
+
+
+def test_engine_prompt_through_chunked_prefill(wz, gpu):
+    """A prompt remainder above 192 cells goes through wzy_stage_prefill (run_prefill_range,
+    src/wzy_engine_v2.cu:1292-1376): the engine's stream equals an in-process stage running the same
+    prefill and decode steps; splitting the prompt into smaller chunks (--prefill-chunk) and
+    speculative decoding seeded from the prefill's pre-head rows leave the stream unchanged."""
+    from test_gpu_engine import SEED as ENGINE_SEED
+    from test_gpu_engine import EngineProc, greedy_req
+    print("case engine_prefill", flush=True)
+    cfg = pf_cfg(ctx_max=2048)
+    prompt = [int(t) for t in np.random.default_rng(6).integers(0, cfg.n_vocab, 300)]
+    n_new = 8
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_synthetic(ENGINE_SEED, 0)
+        st.prefill(0, prompt[:-1])
+        tok, pos, want = prompt[-1], len(prompt) - 1, []
+        for _ in range(n_new):
+            st.forward(pos, [tok])
+            st.sync()
+            tok = int(st.greedy(1)[0])
+            want.append(tok)
+            pos += 1
+    finally:
+        st.close()
+    for args in ((), ("--prefill-chunk", "100"), ("--spec-depth", "3")):
+        eng = EngineProc(cfg, *args)
+        try:
+            pf, toks, done = eng.request(greedy_req(prompt, n_new))
+            assert pf["read"] == 300 and done["generated"] == n_new
+            assert toks == want, "engine %s: %s vs in-process %s" % (args, toks, want)
+            # a follow-up that extends the state reuses it (a short remainder: decode windows)
+            pf2, _, _ = eng.request(greedy_req(prompt + toks[:-1] + [5], 2))
+            assert pf2["reused"] == 300 + n_new - 1
+        finally:
+            assert eng.close() == 0

@@ -102,6 +102,7 @@ struct Options {
     int mtp_dvocab = 114452;
     wzy_spec_gates gates{5, 0.30f, 1.0f};
     bool adapt_depth = true;
+    int prefill_chunk = 25600;    // cells per prefill chunk (the reference's PF_MAX default)
 };
 
 // "k=v,k=v" onto wzy_stage_cfg by field name.
@@ -165,6 +166,7 @@ int parse_options(int argc, char** argv, Options& o) {
     if (const char* e = getenv("WZY_SPEC_MIN_P")) o.gates.min_p = (float) atof(e);
     if (const char* e = getenv("WZY_SPEC_GATE")) o.gates.gate = (float) atof(e);
     if (const char* e = getenv("WZY_ADAPT_DEPTH")) o.adapt_depth = atoi(e) != 0;
+    if (const char* e = getenv("WZY_PREFILL_CHUNK")) o.prefill_chunk = atoi(e);
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto val = [&]() -> const char* {
@@ -184,12 +186,14 @@ int parse_options(int argc, char** argv, Options& o) {
         else if (a == "--no-graphs") o.graphs = false;
         else if (a == "--mtp") o.mtp = true;
         else if (a == "--spec-depth") o.spec_fixed = atoi(val()), o.mtp = true;
+        else if (a == "--prefill-chunk") o.prefill_chunk = atoi(val());
         else {
             fprintf(stderr, "[wzy-engine] unknown option %s\n", a.c_str());
             return 2;
         }
     }
     if (o.spec_fixed > 0) o.mtp = true;
+    o.prefill_chunk = std::max(1, std::min(o.prefill_chunk, 25600));
     o.spec_fixed = std::min(o.spec_fixed, WZY_MAX_W - 1);
     o.gates.depth = std::max(1, std::min(o.gates.depth, WZY_MAX_W - 1));
     return 0;
@@ -262,14 +266,25 @@ class Engine {
         // (seed_mtp_tail, src/wzy_engine_v2.cu:1266-1290).
         const int tail_floor = std::max(0, n - 1 - kMtpSeedTail);
         if (o_.mtp && reused == 0) check(wzy_stage_mtp_reset(st_), "mtp_reset");
-        for (int p = reused; p < n - 1; p += WZY_MAX_W) {
-            const int T = std::min(WZY_MAX_W, n - 1 - p);
+        // Up to kPrefillMin cells go through decode windows; more through chunked prefill
+        // (run_prefill_range, src/wzy_engine_v2.cu:1292-1376).  Either way the chunk's last
+        // kMtpSeedTail cells leave their pre-head rows, which seed the drafter 8 rows at a time.
+        const int n_feed = n - 1 - reused;
+        const int step = (n_feed > kPrefillMin && wzy_stage_can_prefill(&c_)) ? o_.prefill_chunk : WZY_MAX_W;
+        for (int p = reused; p < n - 1; p += step) {
+            const int T = std::min(step, n - 1 - p);
             const bool seed = o_.mtp && p + T > tail_floor;
-            check(wzy_stage_record_forward(st_, p, nullptr, &ids[p], T, seed ? 2 : 0, 0, 0, 0), "record_forward(prefill)");
+            if (step == WZY_MAX_W)
+                check(wzy_stage_record_forward(st_, p, nullptr, &ids[p], T, seed ? 2 : 0, 0, 0, 0), "record_forward(prefill)");
+            else
+                check(wzy_stage_prefill(st_, p, &ids[p], T), "prefill");
             if (seed) {
                 const int sub0 = std::max(0, tail_floor - p);
                 if (p + sub0 == tail_floor && tail_floor > 0) check(wzy_stage_mtp_set_floor(st_, tail_floor), "mtp_floor");
-                check(wzy_stage_mtp_front(st_, p + sub0, &ids[p + sub0 + 1], T - sub0, sub0), "mtp_front");
+                for (int off = sub0; off < T; off += WZY_MAX_W) {
+                    const int cnt = std::min(WZY_MAX_W, T - off);
+                    check(wzy_stage_mtp_front(st_, p + off, &ids[p + off + 1], cnt, off), "mtp_front");
+                }
             }
         }
         state_.insert(state_.end(), ids.begin() + reused, ids.end() - 1);
@@ -445,6 +460,8 @@ class Engine {
     enum Mode { kGreedy, kTop16, kFull };
 
     static constexpr int kMtpSeedTail = 512;   // prompt cells seeded into the drafter (src/wzy_mtp.cuh:12)
+    static constexpr int kPrefillMin = 192;    // longer prompt remainders take the chunked prefill
+                                               // (src/wzy_engine_v2.cu:1295)
 
     // Head outputs of the W rows of the last forward, as the selection mode needs them.
     void read_rows(int W) {

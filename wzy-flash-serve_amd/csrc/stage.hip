@@ -1633,14 +1633,17 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
     return WZY_OK;
 }
 
+extern "C" int wzy_stage_can_prefill(const wzy_stage_cfg* c) {
+    return c && c->hc_lr % 64 == 0 && c->n_embd % 256 == 0 && c->n_ff % 128 == 0 && c->n_exp % 64 == 0 &&
+           c->n_exp <= 1024 && c->idx_dim == 128;
+}
+
 static int prefill_checks(wzy_stage* st, int pos, const int* toks, int B) {
     WZY_REQUIRE(st && st->loaded, "prefill: stage not loaded");
     WZY_REQUIRE(toks && B >= 1 && B <= 65535, "prefill: B must be in [1, 65535] with token ids");
     WZY_REQUIRE(pos >= 0 && pos + B <= st->cfg.ctx_max, "prefill: positions [%d, %d) exceed ctx_max %d", pos, pos + B,
                 st->cfg.ctx_max);
-    const wzy_stage_cfg& c = st->cfg;
-    WZY_REQUIRE(c.hc_lr % 64 == 0 && c.n_embd % 256 == 0 && c.n_ff % 128 == 0 && c.n_exp % 64 == 0 &&
-                    c.n_exp <= 1024 && c.idx_dim == 128,
+    WZY_REQUIRE(wzy_stage_can_prefill(&st->cfg),
                 "prefill: shape unsupported (hc_lr a multiple of 64, n_embd of 256, n_ff of 128, n_exp of 64 up to "
                 "1024, idx_dim 128)");
     return WZY_OK;

@@ -129,6 +129,7 @@ _SIGS = {
     "wzy_stage_load_synthetic": (I32, [P, U64, I32], True),
     "wzy_stage_record_forward": (I32, [P, I32, P, P, I32, I32, I32, I32, I32], True),
     "wzy_stage_prefill": (I32, [P, I32, P, I32], True),
+    "wzy_stage_can_prefill": (I32, [C.POINTER(StageCfg)], False),
     "wzy_stage_prefill_time": (I32, [P, I32, P, I32, C.POINTER(F32)], True),
     "wzy_stage_service_cold_layers": (I32, [P], True),
     "wzy_stage_promote_cold": (I32, [P], True),
