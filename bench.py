@@ -17,6 +17,8 @@ Beside the tok/s line it reports
   prefill_moe   BASELINE config 5's chunked-prefill MoE block (8,192 tokens, one layer) on MFMA:
                 per-launch-group HIP event times, routed-expert TFLOP/s against the 2.5 PFLOP/s
                 dense bf16 MFMA peak;
+  stage_prefill BASELINE config 5's 8,192-token chunk through the whole 48-layer model (wzy_stage_prefill):
+                tok/s and the weight GEMMs' TFLOP/s against the dense bf16 MFMA peak;
   mtp_config5   BASELINE config 5's decode half: the MTP drafter at a fixed depth of 3 with T=4 verify
                 windows on the same stage (tok/s, acceptance, per-window split, and one draft step's
                 HBM bytes / event-timed duration against 8 TB/s);
@@ -86,6 +88,53 @@ def prefill_moe(wz, st, n_tok, iters, seed):
         "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
         "us_stages": st_us,
     }
+
+
+PF_PARTS = ("attn_hc_read", "gdn", "qsa", "ffn_hc_read", "moe", "rest")
+
+
+def stage_dense_macs(cfg):
+    """Multiply-accumulates per token of every weight GEMM in one prefill chunk (all layers): the two
+    hyper-connection reads per layer (inject, down, up projections), the GDN or QSA projections, the
+    router and the shared + top-k routed experts.  Attention and indexer scores are context-dependent
+    and not counted."""
+    D, HCD, L = cfg.n_embd, cfg.hc * cfg.n_embd, cfg.hc_lr
+    QKV, GV = 2 * cfg.gdn_hk * 128 + cfg.gdn_hv * 128, cfg.gdn_hv * 128
+    QD, KVD, ID, IH = cfg.qsa_qh * cfg.qsa_hd, cfg.qsa_kvh * cfg.qsa_hd, cfg.idx_dim, cfg.idx_heads
+    hc = 2 * (HCD * cfg.hc + 2 * HCD * L)
+    gdn = D * QKV + D * GV + 2 * D * cfg.gdn_hv + GV * D
+    qsa = D * 2 * QD + 2 * D * KVD + D * ID + D * IH * ID + QD * D
+    moe = D * cfg.n_exp + (1 + cfg.top_k) * 3 * cfg.n_ff * D
+    n_qsa = cfg.n_layers // cfg.qsa_period
+    return cfg.n_layers * (hc + moe) + n_qsa * qsa + (cfg.n_layers - n_qsa) * gdn
+
+
+def stage_prefill(wz, st, cfg, pos, n_tok, iters, seed):
+    """Config-5 chunked prefill of the whole 48-layer model: one chunk of n_tok prompt cells appended at
+    `pos` (after the prefilled context), every chunk re-run at the same cells.  One untimed run, `iters`
+    wall-clock timed runs (host clock around wzy_stage_prefill + stream sync), then one run split into
+    event-timed parts (wzy_stage_prefill_time; the part boundaries synchronise, so that run is slower)."""
+    import numpy as np
+    toks = np.random.default_rng(seed).integers(0, cfg.n_vocab, n_tok).astype(np.int32)
+    tp = toks.ctypes.data
+    wz.wzy_stage_prefill(st.h, pos, tp, n_tok)
+    wz.wzy_stage_sync(st.h)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        wz.wzy_stage_prefill(st.h, pos, tp, n_tok)
+    wz.wzy_stage_sync(st.h)
+    el = (time.perf_counter() - t0) / iters
+    us = (C.c_float * len(PF_PARTS))()
+    wz.wzy_stage_prefill_time(st.h, pos, tp, n_tok, us)
+    macs = stage_dense_macs(cfg)
+    tflops = 2.0 * macs * n_tok / el / 1e12
+    return {"workload": "config 5 chunked prefill: %d prompt cells in one chunk through all %d layers of the config-4 "
+                        "model, appended after a %d-cell context" % (n_tok, cfg.n_layers, pos),
+            "n_tok": n_tok, "iters": iters, "ms_per_chunk": round(1000 * el, 2), "tok_s": round(n_tok / el, 0),
+            "dense_gflop_per_token": round(2.0 * macs / 1e9, 3),
+            "dense_tflops": round(tflops, 1), "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+            "us_parts_synced_run": {k: round(us[i], 1) for i, k in enumerate(PF_PARTS)}}
 
 
 # config 2 per layer-step: fp32 state read + written (2 x 1 MiB), bf16 q, k, v (3 x 4,096 B), the two gates
@@ -302,6 +351,7 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
             "mtp_step": {"us": round(us.value, 3), "bytes": nb, "achieved_gbs": round(nb / (us.value * 1e-6) / 1e9, 1),
                          "frac": round(nb / (us.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "timed_steps": time_iters},
             "init_s": round(t_init, 2),
+            "pos_end": pos,
             "tok_s_at_acceptance": proj,
             "note": ("the synthetic drafter is random-initialised, so its drafts match the random main model's "
                      "greedy tokens about 1 time in 10^5 and measured acceptance is ~0; tok_s is the cost of "
@@ -424,6 +474,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true", help="direct kernel launches instead of graph replay")
     ap.add_argument("--prefill-tokens", type=int, default=8192, help="config-5 prefill MoE chunk (0: skip)")
     ap.add_argument("--prefill-iters", type=int, default=5)
+    ap.add_argument("--stage-prefill-tokens", type=int, default=8192,
+                    help="config-5 whole-model prefill chunk (0: skip)")
+    ap.add_argument("--stage-prefill-iters", type=int, default=3)
     ap.add_argument("--no-configs23", action="store_true", help="skip the config-2 GDN and config-3 QSA legs")
     ap.add_argument("--mtp-windows", type=int, default=64, help="config-5 speculative windows (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -443,7 +496,8 @@ def main():
         sys.exit(1)
     wz.wzy_dev_set(0)
 
-    ctx_max = args.n_ctx + args.warmup + args.steps + 64 + 8 * (args.mtp_windows + 4) + 64 + 64 + 128
+    ctx_max = (args.n_ctx + args.warmup + args.steps + 64 + 8 * (args.mtp_windows + 4) + 64 + 64 + 128 +
+               max(args.stage_prefill_tokens, 0))
     cfg = wzy_amd.default_cfg(ctx_max)
     t0 = time.perf_counter()
     st = wzy_amd.Stage(cfg)
@@ -494,6 +548,12 @@ def main():
         mtp5 = mtp_config5(wz, st, cfg, pos, args.mtp_windows)
         print("bench: config 5 MTP depth 3: %.1f tok/s, %.3f ms per window, step %.1f us" % (
             mtp5["tok_s"], mtp5["ms_per_window"], mtp5["mtp_step"]["us"]), file=sys.stderr, flush=True)
+        pos = mtp5.pop("pos_end")
+    spf = None
+    if args.stage_prefill_tokens > 0:
+        spf = stage_prefill(wz, st, cfg, pos, args.stage_prefill_tokens, args.stage_prefill_iters, args.seed + 1)
+        print("bench: config 5 whole-model prefill of %d tokens: %.1f ms per chunk, %.0f tok/s" % (
+            args.stage_prefill_tokens, spf["ms_per_chunk"], spf["tok_s"]), file=sys.stderr, flush=True)
     st.close()
 
     gdn2 = qsa3 = None
@@ -557,6 +617,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "prefill_moe": pf,
+        "stage_prefill": spf,
         "mtp_config5": mtp5,
         "gdn_config2": gdn2,
         "qsa_262k": qsa3,

@@ -88,7 +88,7 @@ int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb, const int
  * and leaves the final residual rows [B x hc x n_embd] as the pre-head rows of the call
  * (wzy_stage_pre_head, wzy_stage_mtp_front).  No logits.  Asynchronous (wzy_stage_sync).  The
  * first call with a larger B allocates the workspace (BASELINE shapes: about 0.25 MB per row).
- * Needs hc_lr a multiple of 64, n_exp a multiple of 64 (<= 1024), n_ff of 128, idx_dim 128.
+ * Needs hc_lr a multiple of 64, n_embd of 256, n_exp of 64 (<= 1024), n_ff of 128, idx_dim 128.
  * Replaces PrefillStageCtx::run_stage_prefill (src/wzy_prefill_tc.cuh:546-1058) for one stage
  * holding every layer (no expert streaming: every expert is resident). */
 int wzy_stage_prefill(wzy_stage* st, int pos, const int* toks, int B);
