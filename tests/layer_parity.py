@@ -7,7 +7,10 @@ wzy_stage_set_trace, the oracle with orc_model_forward_trace).  The comparison w
 each row in order:
 
   * hidden states elementwise: |gpu - oracle| <= ATOL + RTOL |oracle|  (north star: rel 2e-2,
-    abs 1e-2);
+    abs 1e-2); for the MoE output the relative term is floored at the row's RMS, because the block
+    requantises its input per 16 / 32 values and a one-step code difference (an fp32 sum of the
+    input landing on the other side of a rounding boundary) moves its outputs by about 1 % of the
+    row's scale (the rule of teacher_forced.row_excess);
   * expert ids of every layer bit-exact, in rank order, and the selected cells of every QSA layer
     bit-exact;
   * the logits elementwise and the greedy id bit-exact.
@@ -28,6 +31,15 @@ import numpy as np
 
 RTOL, ATOL = 2e-2, 1e-2
 HIDDEN = ("attention HC read", "attention block", "FFN HC read", "MoE output")
+
+
+def row_excess(g, o):
+    """Largest excess over ATOL + RTOL * max(|o|, rms(o)), and the plain elementwise one."""
+    g = np.asarray(g, np.float64).ravel()
+    o = np.asarray(o, np.float64).ravel()
+    d = np.abs(g - o)
+    rms = float(np.sqrt((o * o).mean())) if o.size else 0.0
+    return float((d - (ATOL + RTOL * np.maximum(np.abs(o), rms))).max()), float((d - (ATOL + RTOL * np.abs(o))).max())
 
 
 def excess(g, o):
@@ -143,7 +155,11 @@ class LayerParity:
             self.rows_full += 1
 
     def _hidden(self, tag, t, l, k, g, o):
-        v = excess(g["hidden"][l, k, t], o["hidden"][l, k, t])
+        if k == 3:
+            v, plain = row_excess(g["hidden"][l, k, t], o["hidden"][l, k, t])
+            self.worst["MoE output (plain)"] = max(self.worst.get("MoE output (plain)", -np.inf), plain)
+        else:
+            v = excess(g["hidden"][l, k, t], o["hidden"][l, k, t])
         self.worst[HIDDEN[k]] = max(self.worst[HIDDEN[k]], v)
         if self.hidden_mode == "report":
             self.drift[l] = max(self.drift.get(l, -np.inf), v)

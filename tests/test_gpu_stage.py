@@ -169,14 +169,20 @@ def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=F
 
 @pytest.mark.parametrize("seed,n_ctx", [(1234, 600), (77, 601), (5, 300)])
 def test_stage_multilayer_decode(wz, gpu, seed, n_ctx):
-    """Four layers (GDN, QSA, GDN, QSA): four single-token steps then a T=4 window, compared layer by
-    layer."""
+    """Four layers (GDN, QSA, GDN, QSA): four single-token steps, each checked component by component
+    against the oracle fed the GPU's own inputs and pre-row state (teacher-forced), then a T=4 window;
+    the discrete decisions of every row (expert ids, selected cells, greedy ids) are compared
+    free-running, layer by layer.  (Free-running hidden states are reported, not asserted: a one-step
+    int8 code difference in a block's requantised input, from fp32 sums run in another order, moves
+    the synthetic MoE's outputs by more than the float tolerance, and that compounds over layers.)"""
     print("case multilayer seed=%d n_ctx=%d" % (seed, n_ctx), flush=True)
     cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
     rng = np.random.default_rng(seed)
     windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
-    par, _ = run_layer_parity(wz, cfg, seed, n_ctx, windows)
+    par, tf = run_layer_parity(wz, cfg, seed, n_ctx, windows, teacher=True)
     print("multilayer: " + par.summary(), flush=True)
+    print("multilayer: " + tf.summary(), flush=True)
+    assert tf.counts["rows"] == 4 and tf.counts["layers"] == 16, tf.summary()
     assert par.rows_full >= 6 and par.layers_compared >= 28, par.summary()
 
 

@@ -48,8 +48,14 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
     __shared__ float s_w[WZY_MAX_W][4];
     __shared__ float s_kv[8][QC], s_o[8][QC];
     __shared__ int s_last;
-    const int h = blockIdx.x / GDN_NQ, cq = blockIdx.x % GDN_NQ;
     const int HK = a.hk, HV = a.hv, T = a.T;
+    // XCD-local numbering when HV % 8 == 0: workgroup b runs on XCD b % 8, which takes heads
+    // b % 8, b % 8 + 8, ... with all their column quarters, so a key head's shared conv history and
+    // weights are fetched from HBM once per XCD; otherwise consecutive workgroups of a head
+    const int b = blockIdx.x;
+    const bool xl = (HV & 7) == 0;
+    const int h = xl ? (b & 7) + 8 * ((b >> 3) / GDN_NQ) : b / GDN_NQ;
+    const int cq = xl ? (b >> 3) % GDN_NQ : b % GDN_NQ;
     const int kh = h % HK;
     const int QKV = 2 * HK * GS + HV * GS;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
