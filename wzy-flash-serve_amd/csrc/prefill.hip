@@ -9,12 +9,13 @@
 //                down / up, pf_silu_div, pf_up_mean; pf_hc_write writes a block into the streams.
 //  GDN           pf_gdn_ab (gates), pf_gdn_conv (causal conv + SiLU + L2 of q/k heads over all rows
 //                at once), pf_gdn_hist (conv history), pf_gdn_recur (the delta rule, sequential over
-//                the rows: 8 lanes per state column, 16 rows each in registers, q/k staged in LDS
+//                the rows: 32 lanes per state column, 4 rows each in registers, q/k staged in LDS
 //                16 steps at a time), pf_gdn_norm (gated RMS norm, bf16).
 //  QSA           pf_qsa_prep (q / k / indexer-q norms + RoPE, INT8 KV append), pf_idx_append (the
 //                indexer keys of every block the chunk completes, one workgroup per block, then
 //                pf_idx_tail), block scores and top-k with the decode kernels over all rows,
-//                pf_attn (sparse GQA attention on fp16 MFMA with a 32-cell online softmax).
+//                pf_attn (sparse GQA attention on fp16 MFMA, 64 cells per load step, a 32-cell
+//                online softmax).
 // reference: PrefillStageCtx::run_stage_prefill and its kernels (src/wzy_prefill_tc.cuh:20-98,
 // 546-1058; src/wzy_qsa_wmma.cuh:5-489), with cuBLAS fp16 GEMMs replaced by bf16 MFMA GEMMs.
 #include "wzy_device.h"
@@ -301,16 +302,32 @@ __global__ void __launch_bounds__(256) pf_gdn_hist_kernel(PfGdn g) {
     h[2] = v[2];
 }
 
-constexpr int GR_LPC = 8;                     // lanes per state column
-constexpr int GR_RPL = 128 / GR_LPC;          // state rows per lane
-constexpr int GR_CPW = 64 / GR_LPC;           // columns per wave
+// Sum over each 32-lane half: the 16-lane DPP sum, then the two rows of the half swapped in one
+// VALU op (v_permlane16_swap) and added; every lane of the half gets the same value.
+// (Written as inline assembly: through the builtin, this compiler hands both results of the swap in
+// one register when they feed one add.  The s_nops cover the VALU-write-to-permlane hazard.)
+WZY_DEV float sum32_pl(float v) {
+    v = sum16(v);
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+constexpr int GR_LPC = 32;                    // lanes per state column (half a wave)
+constexpr int GR_RPL = 128 / GR_LPC;          // state rows per lane (4)
+constexpr int GR_CPW = 64 / GR_LPC;           // columns per wave (2)
 constexpr int GR_WAVES = 4;
-constexpr int GR_COLS = GR_CPW * GR_WAVES;    // columns per workgroup (32)
+constexpr int GR_COLS = GR_CPW * GR_WAVES;    // columns per workgroup (8)
 constexpr int GR_STEPS = 16;                  // rows staged per LDS buffer
+static_assert(GR_STEPS * GR_COLS <= 256, "v staging: one value per thread");
+static_assert(GR_RPL == 4, "the row loop holds 4 state rows per lane");
 
 // Delta rule over the chunk's rows for one value head and GR_COLS state columns (each column of
 // the state evolves independently): per row, S *= decay; kv = S^T k; delta = (v - kv) * beta;
-// S += k delta^T; o = S^T q / sqrt(128).  grid (hv * 128 / GR_COLS), 256 threads.
+// S += k delta^T; o = S^T q / sqrt(128).  grid (hv * 128 / GR_COLS), 256 threads.  A column's 128
+// rows are spread over 32 lanes (4 per lane), so a row costs a few instructions per lane and two
+// 32-lane DPP / swizzle sums; the rows' q and k (all 128 of the key head) and the columns' v go
+// through LDS 16 rows at a time, the next 16 loaded while these run.
 // (pf_gdn_recur_kh_kernel, src/wzy_qsa_wmma.cuh:56-195; fused_gdn_step_norm_multi,
 // src/wzy_kernels_v2.cuh:908-984)
 __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
@@ -322,7 +339,7 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
     const int h = blockIdx.x / (128 / GR_COLS), cb = blockIdx.x % (128 / GR_COLS);
     const int kh = h % g.hk;
     const int QKV = (2 * g.hk + g.hv) * 128, GV = g.hv * 128;
-    const int r8 = lane & (GR_LPC - 1), c8 = lane / GR_LPC;
+    const int r8 = lane & (GR_LPC - 1), c8 = lane / GR_LPC;     // row slot, column of the wave
     const int lc = w * GR_CPW + c8, col = cb * GR_COLS + lc;
     float* S = g.state + (size_t) h * 128 * 128;
     float s[GR_RPL];
@@ -341,7 +358,7 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
             rq[u] = t < g.B ? g.conv_out[(size_t) t * QKV + (which ? g.hk * 128 : 0) + kh * 128 + i] : 0.f;
         }
         {
-            const int step = tid / GR_COLS, j = tid % GR_COLS, t = t0 + step;   // 256 = 8 steps x 32 cols
+            const int step = min(tid / GR_COLS, GR_STEPS - 1), j = tid % GR_COLS, t = t0 + step;
             rv = t < g.B ? g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j] : 0.f;
         }
         {
@@ -349,64 +366,54 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
             rg = (t < g.B && tid < 2 * GR_STEPS) ? (tid < GR_STEPS ? g.decay : g.beta)[(size_t) t * g.hv + h] : 0.f;
         }
     };
-    float rv2 = 0.f;
-    auto load_v2 = [&](int t0) {                            // v of steps 8..15
-        const int step = 8 + tid / GR_COLS, j = tid % GR_COLS, t = t0 + step;
-        rv2 = t < g.B ? g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j] : 0.f;
-    };
     auto store = [&](int bb) {
 #pragma unroll
         for (int u = 0; u < QK_PER; ++u) {
             const int e = u * 256 + tid, step = e / 256, which = (e / 128) & 1, i = e & 127;
             (which ? sk : sq)[bb][step][i] = rq[u];
         }
-        sv[bb][tid / GR_COLS][tid % GR_COLS] = rv;
-        sv[bb][8 + tid / GR_COLS][tid % GR_COLS] = rv2;
+        if (tid < GR_STEPS * GR_COLS) sv[bb][tid / GR_COLS][tid % GR_COLS] = rv;
         if (tid < GR_STEPS) sg[bb][tid] = rg;
         else if (tid < 2 * GR_STEPS) sb[bb][tid - GR_STEPS] = rg;
     };
 
     const int nblk = (g.B + GR_STEPS - 1) / GR_STEPS;
     load(0);
-    load_v2(0);
     store(0);
     __syncthreads();
     for (int kb = 0; kb < nblk; ++kb) {
         const int bb = kb & 1, t0 = kb * GR_STEPS;
-        if (kb + 1 < nblk) {
-            load(t0 + GR_STEPS);
-            load_v2(t0 + GR_STEPS);
-        }
+        if (kb + 1 < nblk) load(t0 + GR_STEPS);
         const int n = min(GR_STEPS, g.B - t0);
+        // the operands of a row come from LDS one row ahead, so their latency hides behind the
+        // previous row's reductions
+        float4 kn = *(const float4*) &sk[bb][0][r8 * GR_RPL], qn = *(const float4*) &sq[bb][0][r8 * GR_RPL];
+        float vn = sv[bb][0][lc], gn = sg[bb][0], bn = sb[bb][0];
         for (int st = 0; st < n; ++st) {
-            float kr[GR_RPL], qr[GR_RPL];
-#pragma unroll
-            for (int i = 0; i < GR_RPL; i += 4) {
-                const float4 k4 = *(const float4*) &sk[bb][st][r8 * GR_RPL + i];
-                const float4 q4 = *(const float4*) &sq[bb][st][r8 * GR_RPL + i];
-                kr[i] = k4.x; kr[i + 1] = k4.y; kr[i + 2] = k4.z; kr[i + 3] = k4.w;
-                qr[i] = q4.x; qr[i + 1] = q4.y; qr[i + 2] = q4.z; qr[i + 3] = q4.w;
+            const float4 k4 = kn, q4 = qn;
+            const float vv = vn, dec = gn, beta = bn;
+            if (st + 1 < n) {
+                kn = *(const float4*) &sk[bb][st + 1][r8 * GR_RPL];
+                qn = *(const float4*) &sq[bb][st + 1][r8 * GR_RPL];
+                vn = sv[bb][st + 1][lc];
+                gn = sg[bb][st + 1];
+                bn = sb[bb][st + 1];
             }
-            const float dec = sg[bb][st], beta = sb[bb][st];
-            float kv0 = 0.f, kv1 = 0.f;
-#pragma unroll
-            for (int i = 0; i < GR_RPL; i += 2) {
-                s[i] *= dec;
-                s[i + 1] *= dec;
-                kv0 = fmaf(s[i], kr[i], kv0);
-                kv1 = fmaf(s[i + 1], kr[i + 1], kv1);
-            }
-            const float kv = sum8(kv0 + kv1);
-            const float delta = (sv[bb][st][lc] - kv) * beta;
-            float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-            for (int i = 0; i < GR_RPL; i += 2) {
-                s[i] = fmaf(kr[i], delta, s[i]);
-                s[i + 1] = fmaf(kr[i + 1], delta, s[i + 1]);
-                o0 = fmaf(s[i], qr[i], o0);
-                o1 = fmaf(s[i + 1], qr[i + 1], o1);
-            }
-            const float o = sum8(o0 + o1) * 0.08838834764831845f;
+            // S^T k and S^T q of the state before the row, and k.q, reduced together:
+            //   kv = dec * (S^T k),  o = dec * (S^T q) + delta * (k.q)  (= (dec S + k delta^T)^T q)
+            float a = s[0] * k4.x, c = s[0] * q4.x, kq = k4.x * q4.x;
+            a = fmaf(s[1], k4.y, a); c = fmaf(s[1], q4.y, c); kq = fmaf(k4.y, q4.y, kq);
+            a = fmaf(s[2], k4.z, a); c = fmaf(s[2], q4.z, c); kq = fmaf(k4.z, q4.z, kq);
+            a = fmaf(s[3], k4.w, a); c = fmaf(s[3], q4.w, c); kq = fmaf(k4.w, q4.w, kq);
+            a = sum32_pl(a);
+            c = sum32_pl(c);
+            kq = sum32_pl(kq);
+            const float delta = (vv - dec * a) * beta;
+            const float o = fmaf(dec, c, delta * kq) * 0.08838834764831845f;
+            s[0] = fmaf(k4.x, delta, dec * s[0]);
+            s[1] = fmaf(k4.y, delta, dec * s[1]);
+            s[2] = fmaf(k4.z, delta, dec * s[2]);
+            s[3] = fmaf(k4.w, delta, dec * s[3]);
             if (r8 == 0) g.o[(size_t) (t0 + st) * GV + h * 128 + col] = o;
         }
         if (kb + 1 < nblk) store(bb ^ 1);
@@ -516,25 +523,27 @@ __global__ void __launch_bounds__(128) pf_idx_tail_kernel(PfIdxAppend a, int p0,
 }
 
 // Sparse GQA attention of one row and one KV head (grid (kvh, B), 256 threads): the group's query
-// heads (up to 16, rows of a 16 x 16 fp16 MFMA tile) against the selected cells 32 at a time.  Per
-// step: K of 32 cells dequantised to fp16 in LDS (row major), scores on v_mfma_f32_16x16x16_f16
-// (waves: 2 cell halves x 2 dim halves, summed through LDS), an online softmax per head (fp16
-// weights), V dequantised into LDS transposed (dims x cells) and P.V on MFMA into the accumulators,
-// rescaled by exp(m_old - m_new) first.  The next step's K and V codes are loaded while a step
-// computes.  out = acc / max(l, 1e-20) * sigmoid(gate), bf16.
-constexpr int AT_C = 32;                      // cells per step
+// heads (up to 16, rows of a 16 x 16 fp16 MFMA tile) against the selected cells, 64 per load step.
+// Per step: K of 64 cells dequantised to fp16 in LDS (row major), scores on
+// v_mfma_f32_16x16x16_f16 (wave w: cells 16w .. 16w+15, all 256 dims as two 128-dim chains added in
+// fp32), then two 32-cell softmax blocks in order (the online softmax per head with fp16 weights,
+// as the reference's 32-cell steps), V dequantised into LDS transposed (dims x cells) and P.V on
+// MFMA into the accumulators, rescaled by exp(m_old - m_new) before each block.  The next step's K
+// and V codes (32 KB) are loaded while a step computes.  out = acc / max(l, 1e-20) * sigmoid(gate),
+// bf16.
+constexpr int AT_C = 64;                      // cells per load step (two softmax blocks of 32)
+constexpr int AT_B = 32;                      // cells per softmax block
 constexpr int AT_QLD = 256 + 8;               // LDS row strides (halves)
 constexpr int AT_VLD = AT_C + 8;
 
 WZY_DEV f16x4_t h4_from(const _Float16* p) { return *(const f16x4_t*) p; }
 
 __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
-    __shared__ __align__(16) _Float16 sQ[16][AT_QLD];
     __shared__ __align__(16) _Float16 sK[AT_C][AT_QLD];
     __shared__ __align__(16) _Float16 sVt[256][AT_VLD];
-    __shared__ __align__(16) _Float16 sP[16][AT_VLD];
-    __shared__ float sS[2][16][AT_C + 1];
-    __shared__ float s_m[16], s_l[16], s_al[16];
+    __shared__ __align__(16) _Float16 sP[2][16][AT_B + 8];
+    __shared__ float sS[16][AT_C + 1];
+    __shared__ float s_m[16], s_l[16], s_al[2][16];
     const QsaDims& dm = a.dm;
     const int j = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int hd = 256, kvd = dm.kvh * hd, gq = dm.qh / dm.kvh, scg = hd / 64;
@@ -543,65 +552,75 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
     const int* ids = a.sel + (size_t) t * dm.topk;
     const float* qg = a.qg + (size_t) t * dm.qh * 2 * hd;
 
-    for (int i = tid; i < 16 * hd; i += 256) {
-        const int h = i / hd, d = i % hd;
-        sQ[h][d] = (_Float16) (h < gq ? qg[(size_t) (j * gq + h) * 2 * hd + d] * 0.0625f : 0.f);
+    const int l16 = lane & 15, kq4 = lane >> 4;   // MFMA 16x16x16: row/col l16, k quad kq4
+    // the A operand of every score MFMA, held in registers: q[head l16][16 kk + 4 kq4 .. +3] / 16
+    f16x4_t qa[16];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+        const float4 q4 = l16 < gq ? *(const float4*) (qg + (size_t) (j * gq + l16) * 2 * hd + kk * 16 + 4 * kq4)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        qa[kk] = f16x4_t{(_Float16) (q4.x * 0.0625f), (_Float16) (q4.y * 0.0625f), (_Float16) (q4.z * 0.0625f),
+                         (_Float16) (q4.w * 0.0625f)};
     }
     if (tid < 16) {
         s_m[tid] = -1e30f;
         s_l[tid] = 0.f;
-        s_al[tid] = 1.f;
     }
-    // K staging: thread -> cell kc = tid / 8, dims 32 * (tid % 8) .. +31 (32 code bytes)
-    const int kc = tid >> 3, kd0 = (tid & 7) * 32;
-    // V staging: thread -> dim tid, all 32 cells (one byte each)
-    uint4 kq0, kq1;
-    uint16_t ksc = 0;
-    int8_t vcode[AT_C];
-    uint16_t vsc[AT_C];
+    // K staging: thread -> cell kc = tid / 4, dims 64 * (tid % 4) .. +63 (64 code bytes, one scale)
+    const int kc = tid >> 2, kd0 = (tid & 3) * 64;
+    // V staging: thread -> cells 4 * (tid / 16) .. +3, dims 16 * (tid % 16) .. +15
+    const int vc0 = (tid >> 4) * 4, vd0 = (tid & 15) * 16;
+    uint4 kq[4], vq[4];
+    uint16_t ksc = 0, vsc[4];
     auto load = [&](int base) {
         const int cnt = min(AT_C, width - base);
-        if (kc < cnt) {
-            const size_t p = qsa_kv_slot(ids[base + kc], dm);
+        {
+            const bool ok = kc < cnt;
+            const size_t p = qsa_kv_slot(ids[base + (ok ? kc : 0)], dm);
             const int8_t* kp = a.kv.kq + p * kvd + (size_t) j * hd + kd0;
-            kq0 = *(const uint4*) kp;
-            kq1 = *(const uint4*) (kp + 16);
-            ksc = a.kv.ks[p * (kvd / 64) + (size_t) j * scg + kd0 / 64];
-        } else {
-            kq0 = kq1 = make_uint4(0, 0, 0, 0);
-            ksc = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kq[u] = ok ? *(const uint4*) (kp + 16 * u) : make_uint4(0, 0, 0, 0);
+            ksc = ok ? a.kv.ks[p * (kvd / 64) + (size_t) j * scg + kd0 / 64] : (uint16_t) 0;
         }
 #pragma unroll
-        for (int c = 0; c < AT_C; ++c) {
-            const bool ok = c < cnt;
-            const size_t p = qsa_kv_slot(ids[base + (ok ? c : 0)], dm);
-            vcode[c] = ok ? a.kv.vq[p * kvd + (size_t) j * hd + tid] : (int8_t) 0;
-            vsc[c] = ok ? a.kv.vs[p * (kvd / 64) + (size_t) j * scg + tid / 64] : (uint16_t) 0;
+        for (int u = 0; u < 4; ++u) {
+            const bool ok = vc0 + u < cnt;
+            const size_t p = qsa_kv_slot(ids[base + (ok ? vc0 + u : 0)], dm);
+            vq[u] = ok ? *(const uint4*) (a.kv.vq + p * kvd + (size_t) j * hd + vd0) : make_uint4(0, 0, 0, 0);
+            vsc[u] = ok ? a.kv.vs[p * (kvd / 64) + (size_t) j * scg + vd0 / 64] : (uint16_t) 0;
         }
     };
     auto store = [&]() {
         const _Float16 s = __builtin_bit_cast(_Float16, ksc);
-        const uint32_t wv[8] = {kq0.x, kq0.y, kq0.z, kq0.w, kq1.x, kq1.y, kq1.z, kq1.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            f16x4_t v;
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t wv[4] = {kq[u].x, kq[u].y, kq[u].z, kq[u].w};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = (_Float16) (int8_t) (wv[i] >> (8 * u)) * s;
-            *(f16x4_t*) &sK[kc][kd0 + 4 * i] = v;
+            for (int i = 0; i < 4; ++i) {
+                f16x4_t v;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) v[b] = (_Float16) (int8_t) (wv[i] >> (8 * b)) * s;
+                *(f16x4_t*) &sK[kc][kd0 + 16 * u + 4 * i] = v;
+            }
         }
+        _Float16 vs[4];
 #pragma unroll
-        for (int c = 0; c < AT_C; c += 4) {
+        for (int u = 0; u < 4; ++u) vs[u] = __builtin_bit_cast(_Float16, vsc[u]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {               // dim vd0 + i of the 4 cells
             f16x4_t v;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = (_Float16) vcode[c + u] * __builtin_bit_cast(_Float16, vsc[c + u]);
-            *(f16x4_t*) &sVt[tid][c] = v;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t word = i < 4 ? vq[u].x : i < 8 ? vq[u].y : i < 12 ? vq[u].z : vq[u].w;
+                v[u] = (_Float16) (int8_t) (word >> (8 * (i & 3))) * vs[u];
+            }
+            *(f16x4_t*) &sVt[vd0 + i][vc0] = v;
         }
     };
 
     f32x4_t acc[4];                               // out[h = 4*(lane/16) + i][d = 64w + 16db + lane%16]
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int l16 = lane & 15, kq = lane >> 4;    // MFMA 16x16x16: row/col l16, k quad kq
 
     if (width > 0) load(0);
     __syncthreads();
@@ -611,55 +630,64 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
         const int cnt = min(AT_C, width - base);
         const bool more = base + AT_C < width;
         if (more) load(base + AT_C);
-        // scores: wave w -> cells 16*(w&1) .., dims 128*(w>>1) ..
-        {
-            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
-            const int cb = (w & 1) * 16, d0 = (w >> 1) * 128;
+        // scores: wave w -> cells 16w .. 16w+15, dims 0-127 and 128-255 as separate chains
+        if (16 * w < cnt) {
+            f32x4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
-                const f16x4_t av = h4_from(&sQ[l16][d0 + kk * 16 + 4 * kq]);
-                const f16x4_t bv = h4_from(&sK[cb + l16][d0 + kk * 16 + 4 * kq]);
-                sc = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, sc, 0, 0, 0);
+                sc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[kk], h4_from(&sK[16 * w + l16][kk * 16 + 4 * kq4]), sc0,
+                                                            0, 0, 0);
+                sc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[8 + kk], h4_from(&sK[16 * w + l16][128 + kk * 16 + 4 * kq4]),
+                                                            sc1, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sS[w >> 1][4 * kq + i][cb + l16] = sc[i];
+            for (int i = 0; i < 4; ++i) sS[4 * kq4 + i][16 * w + l16] = sc0[i] + sc1[i];
         }
         __syncthreads();
-        // online softmax: wave w -> heads 4w .. 4w+3, two per pass (lane halves), lane = cell
+        // online softmax, two 32-cell blocks in order: wave w -> heads 4w .. 4w+3, two per pass
+        // (lane halves), lane = cell of the block
 #pragma unroll
         for (int pass = 0; pass < 2; ++pass) {
             const int h = 4 * w + 2 * pass + (lane >> 5), c = lane & 31;
-            const bool ok = c < cnt && h < gq;
-            const float s = ok ? sS[0][h][c] + sS[1][h][c] : -1e30f;
-            const float rmax = max32(s);
-            const float m_old = s_m[h];
-            const float m_new = fmaxf(m_old, rmax);
-            const float al = h < gq ? __expf(m_old - m_new) : 1.f;
-            const float pw = ok ? __expf(s - m_new) : 0.f;
-            const float psum = sum32(pw);
-            sP[h][c] = (_Float16) pw;
+            float m_run = h < gq ? s_m[h] : 0.f, l_run = h < gq ? s_l[h] : 0.f;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int cc = AT_B * sb + c;
+                const bool ok = cc < cnt && h < gq;
+                const float sv = ok ? sS[h][cc] : -1e30f;
+                const float rmax = max32(sv);
+                const float m_new = fmaxf(m_run, rmax);
+                const float al = h < gq ? __expf(m_run - m_new) : 1.f;
+                const float pw = ok ? __expf(sv - m_new) : 0.f;
+                const float psum = sum32(pw);
+                sP[sb][h][c] = (_Float16) pw;
+                l_run = l_run * al + psum;
+                m_run = m_new;
+                if (c == 0) s_al[sb][h] = al;
+            }
             if (c == 0 && h < gq) {
-                s_m[h] = m_new;
-                s_l[h] = s_l[h] * al + psum;
-                s_al[h] = al;
+                s_m[h] = m_run;
+                s_l[h] = l_run;
             }
         }
         __syncthreads();
-        // P.V: wave w -> dims 64w .. 64w+63 (four 16-dim blocks), two k16 slices of cells
-        {
+        // P.V: wave w -> dims 64w .. 64w+63 (four 16-dim blocks), per softmax block two k16 slices
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            if (AT_B * sb >= cnt) break;             // workgroup-uniform
             float al[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) al[i] = s_al[4 * kq + i];
+            for (int i = 0; i < 4; ++i) al[i] = s_al[sb][4 * kq4 + i];
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[db][i] *= al[i];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const f16x4_t pv = h4_from(&sP[l16][ks * 16 + 4 * kq]);
+                const f16x4_t pv = h4_from(&sP[sb][l16][ks * 16 + 4 * kq4]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const f16x4_t vv = h4_from(&sVt[64 * w + 16 * db + l16][ks * 16 + 4 * kq]);
+                    const f16x4_t vv = h4_from(&sVt[64 * w + 16 * db + l16][AT_B * sb + ks * 16 + 4 * kq4]);
                     acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pv, vv, acc[db], 0, 0, 0);
                 }
             }
@@ -668,10 +696,10 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
         if (more) store();
         __syncthreads();
     }
-    // acc[db][i] = O[head 4*kq + i][dim 64w + 16db + l16]
+    // acc[db][i] = O[head 4*kq4 + i][dim 64w + 16db + l16]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int h = 4 * kq + i;
+        const int h = 4 * kq4 + i;
         if (h >= gq) continue;
         const float inv = 1.0f / fmaxf(s_l[h], 1e-20f);
 #pragma unroll

@@ -36,14 +36,16 @@ WZY_DEV float siluf_(float x) { return x / (1.0f + __expf(-x)); }
 // DPP / swizzle wave reductions (64 lanes)
 // ---------------------------------------------------------------------------------------------
 // dpp_ctrl encodings (GCN3+ ISA): quad_perm = p0 | p1<<2 | p2<<4 | p3<<6, row_mirror 0x140,
-// row_half_mirror 0x141.  All four patterns read a valid lane, so bound_ctrl is irrelevant.
+// row_half_mirror 0x141.  All four patterns read a valid lane, so bound_ctrl is irrelevant; the
+// move has no old value, which lets the compiler fold it into the consuming VALU op as a DPP
+// operand (v_add_f32_dpp) instead of a copy, a DPP move and the op.
 template <int CTRL>
 WZY_DEV float dpp_f(float v) {
-    return as_f(__builtin_amdgcn_update_dpp(as_i(v), as_i(v), CTRL, 0xF, 0xF, false));
+    return as_f(__builtin_amdgcn_mov_dpp(as_i(v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 WZY_DEV int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
