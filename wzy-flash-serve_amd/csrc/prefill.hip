@@ -10,7 +10,7 @@
 //  GDN           pf_gdn_ab (gates), pf_gdn_conv (causal conv + SiLU + L2 of q/k heads over all rows
 //                at once), pf_gdn_hist (conv history), pf_gdn_recur (the delta rule, sequential over
 //                the rows: 32 lanes per state column, 4 rows each in registers, q/k staged in LDS
-//                16 steps at a time), pf_gdn_norm (gated RMS norm, bf16).
+//                32 steps at a time), pf_gdn_norm (gated RMS norm, bf16).
 //  QSA           pf_qsa_prep (q / k / indexer-q norms + RoPE, INT8 KV append), pf_idx_append (the
 //                indexer keys of every block the chunk completes, one workgroup per block, then
 //                pf_idx_tail), block scores and top-k with the decode kernels over all rows,
@@ -318,16 +318,18 @@ constexpr int GR_RPL = 128 / GR_LPC;          // state rows per lane (4)
 constexpr int GR_CPW = 64 / GR_LPC;           // columns per wave (2)
 constexpr int GR_WAVES = 4;
 constexpr int GR_COLS = GR_CPW * GR_WAVES;    // columns per workgroup (8)
-constexpr int GR_STEPS = 16;                  // rows staged per LDS buffer
+constexpr int GR_STEPS = 32;                  // rows staged per LDS buffer (= lanes per column: lane r
+                                              // keeps row r's output for one store per buffer)
 static_assert(GR_STEPS * GR_COLS <= 256, "v staging: one value per thread");
 static_assert(GR_RPL == 4, "the row loop holds 4 state rows per lane");
+static_assert(GR_STEPS == GR_LPC, "one output row per lane of a column");
 
 // Delta rule over the chunk's rows for one value head and GR_COLS state columns (each column of
 // the state evolves independently): per row, S *= decay; kv = S^T k; delta = (v - kv) * beta;
 // S += k delta^T; o = S^T q / sqrt(128).  grid (hv * 128 / GR_COLS), 256 threads.  A column's 128
-// rows are spread over 32 lanes (4 per lane), so a row costs a few instructions per lane and two
-// 32-lane DPP / swizzle sums; the rows' q and k (all 128 of the key head) and the columns' v go
-// through LDS 16 rows at a time, the next 16 loaded while these run.
+// rows are spread over 32 lanes (4 per lane), so a row costs a few instructions per lane and three
+// 32-lane sums (DPP within each 16-lane row, then a permlane swap); the rows' q and k (all 128 of the key head) and the columns' v go
+// through LDS 32 rows at a time, the next 32 loaded while these run.
 // (pf_gdn_recur_kh_kernel, src/wzy_qsa_wmma.cuh:56-195; fused_gdn_step_norm_multi,
 // src/wzy_kernels_v2.cuh:908-984)
 __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
@@ -347,7 +349,7 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
     for (int i = 0; i < GR_RPL; ++i) s[i] = S[(size_t) (r8 * GR_RPL + i) * 128 + col];
 
     // staging of rows t0 .. t0+GR_STEPS-1: q and k (128 each) of key head kh, v of the columns, gates
-    constexpr int QK_PER = GR_STEPS * 2 * 128 / 256;      // floats per thread (16)
+    constexpr int QK_PER = GR_STEPS * 2 * 128 / 256;      // floats per thread (32)
     float rq[QK_PER];
     float rv = 0.f, rg = 0.f;
     auto load = [&](int t0) {
@@ -389,6 +391,7 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
         // previous row's reductions
         float4 kn = *(const float4*) &sk[bb][0][r8 * GR_RPL], qn = *(const float4*) &sq[bb][0][r8 * GR_RPL];
         float vn = sv[bb][0][lc], gn = sg[bb][0], bn = sb[bb][0];
+        float o_row = 0.f;                                  // lane r8 keeps row t0 + r8's output
         for (int st = 0; st < n; ++st) {
             const float4 k4 = kn, q4 = qn;
             const float vv = vn, dec = gn, beta = bn;
@@ -414,8 +417,9 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
             s[1] = fmaf(k4.y, delta, dec * s[1]);
             s[2] = fmaf(k4.z, delta, dec * s[2]);
             s[3] = fmaf(k4.w, delta, dec * s[3]);
-            if (r8 == 0) g.o[(size_t) (t0 + st) * GV + h * 128 + col] = o;
+            o_row = r8 == st ? o : o_row;
         }
+        if (r8 < n) g.o[(size_t) (t0 + r8) * GV + h * 128 + col] = o_row;
         if (kb + 1 < nblk) store(bb ^ 1);
         __syncthreads();
     }
