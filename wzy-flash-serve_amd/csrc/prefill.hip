@@ -533,7 +533,7 @@ __global__ void __launch_bounds__(128) pf_idx_tail_kernel(PfIdxAppend a, int p0,
 // fp32), then two 32-cell softmax blocks in order (the online softmax per head with fp16 weights,
 // as the reference's 32-cell steps), V dequantised into LDS transposed (dims x cells) and P.V on
 // MFMA into the accumulators, rescaled by exp(m_old - m_new) before each block.  The next step's K
-// and V codes (32 KB) are loaded while a step computes.  out = acc / max(l, 1e-20) * sigmoid(gate),
+// and V codes (32 KB) are loaded while a step computes, from cell ids staged in LDS a step earlier.  out = acc / max(l, 1e-20) * sigmoid(gate),
 // bf16.
 constexpr int AT_C = 64;                      // cells per load step (two softmax blocks of 32)
 constexpr int AT_B = 32;                      // cells per softmax block
@@ -548,6 +548,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
     __shared__ __align__(16) _Float16 sP[2][16][AT_B + 8];
     __shared__ float sS[16][AT_C + 1];
     __shared__ float s_m[16], s_l[16], s_al[2][16];
+    __shared__ int sIds[2][AT_C];                 // selected cell ids of the next two steps
     const QsaDims& dm = a.dm;
     const int j = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int hd = 256, kvd = dm.kvh * hd, gq = dm.qh / dm.kvh, scg = hd / 64;
@@ -576,11 +577,18 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
     const int vc0 = (tid >> 4) * 4, vd0 = (tid & 15) * 16;
     uint4 kq[4], vq[4];
     uint16_t ksc = 0, vsc[4];
-    auto load = [&](int base) {
+    int rid = 0;
+    // the ids of a step are read from global memory two steps ahead and staged in LDS, so the K / V
+    // loads of the next step depend on no global load of their own step
+    auto load_ids = [&](int base) { rid = ids[base + min(tid & (AT_C - 1), width - base - 1)]; };
+    auto store_ids = [&](int slot) {
+        if (tid < AT_C) sIds[slot][tid] = rid;
+    };
+    auto load = [&](int base, int slot) {
         const int cnt = min(AT_C, width - base);
         {
             const bool ok = kc < cnt;
-            const size_t p = qsa_kv_slot(ids[base + (ok ? kc : 0)], dm);
+            const size_t p = qsa_kv_slot(sIds[slot][ok ? kc : 0], dm);
             const int8_t* kp = a.kv.kq + p * kvd + (size_t) j * hd + kd0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) kq[u] = ok ? *(const uint4*) (kp + 16 * u) : make_uint4(0, 0, 0, 0);
@@ -589,7 +597,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const bool ok = vc0 + u < cnt;
-            const size_t p = qsa_kv_slot(ids[base + (ok ? vc0 + u : 0)], dm);
+            const size_t p = qsa_kv_slot(sIds[slot][ok ? vc0 + u : 0], dm);
             vq[u] = ok ? *(const uint4*) (a.kv.vq + p * kvd + (size_t) j * hd + vd0) : make_uint4(0, 0, 0, 0);
             vsc[u] = ok ? a.kv.vs[p * (kvd / 64) + (size_t) j * scg + vd0 / 64] : (uint16_t) 0;
         }
@@ -626,14 +634,21 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    if (width > 0) load(0);
+    if (width > 0) {
+        load_ids(0);
+        store_ids(0);
+    }
     __syncthreads();
+    if (width > 0) load(0, 0);
+    if (AT_C < width) load_ids(AT_C);
     if (width > 0) store();
+    if (AT_C < width) store_ids(1);
     __syncthreads();
-    for (int base = 0; base < width; base += AT_C) {
+    for (int base = 0, stp = 0; base < width; base += AT_C, ++stp) {
         const int cnt = min(AT_C, width - base);
-        const bool more = base + AT_C < width;
-        if (more) load(base + AT_C);
+        const bool more = base + AT_C < width, more2 = base + 2 * AT_C < width;
+        if (more) load(base + AT_C, (stp + 1) & 1);
+        if (more2) load_ids(base + 2 * AT_C);
         // scores: wave w -> cells 16w .. 16w+15, dims 0-127 and 128-255 as separate chains
         if (16 * w < cnt) {
             f32x4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
@@ -698,6 +713,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
         }
         __syncthreads();
         if (more) store();
+        if (more2) store_ids(stp & 1);
         __syncthreads();
     }
     // acc[db][i] = O[head 4*kq4 + i][dim 64w + 16db + l16]
