@@ -64,6 +64,9 @@ def bits_to_f32(h):
     (130, 200, 2048, "bf16", "f32"),    # bf16 weights (indexer / router)
     (257, 129, 128, "q8", "f32"),       # row and column tails
     (1024, 1024, 1024, "q8", "f32"),    # 8 x 8 tiles (the XCD-grouped numbering)
+    (77, 4, 8192, "bf16", "f32"),       # HC inject: the skinny kernel (4 weight rows, K 8192)
+    (300, 16, 2048, "bf16", "f32"),     # GDN alpha / beta gates on the skinny kernel
+    (5, 7, 4096, "bf16", "f32"),        # skinny with a row count below one workgroup's 16
 ])
 def test_gemm_bf16_parity(wz, orc, gpu, M, N, K, kind, out):
     print("case gemm M=%d N=%d K=%d %s %s" % (M, N, K, kind, out), flush=True)

@@ -4,7 +4,8 @@
 //                128 x 128 output tiles, K in steps of 64 through two LDS buffers; Q8_0 weights are
 //                dequantised (code * fp16 scale, rounded to bf16) on their way into LDS, bf16
 //                weights copied.  Workgroups are numbered so that the eight XCDs take interleaved row
-//                tiles and each runs all weight tiles of its row tile back to back.
+//                tiles and each runs all weight tiles of its row tile back to back.  A few bf16
+//                weight rows (N <= 16) take pf_skinny instead (fp32 FMA dot products per row).
 //  HC read       pf_hc_norm (pending block folded in, per-stream RMSNorm, bf16), GEMMs for inject /
 //                down / up, pf_silu_div, pf_up_mean; pf_hc_write writes a block into the streams.
 //  GDN           pf_gdn_ab (gates), pf_gdn_conv (causal conv + SiLU + L2 of q/k heads over all rows
@@ -168,6 +169,64 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
                 }
             }
         }
+}
+
+// Skinny GEMM for a few bf16 weight rows (N <= 16: the hyper-connection inject, the GDN alpha /
+// beta gates), where 128 x 128 MFMA tiles would leave most of the chip idle and read every
+// activation row with 128-row tiles on 64 workgroups.  Each thread keeps its 8-value k slices of every
+// weight row in registers (k = 2048 j + 8 tid .. +7), walks RB rows, and the block sums its partial
+// dots (DPP within a wave, then four wave partials).  fp32 FMAs on the bf16 values.
+constexpr int SK_RB = 16;                    // rows per workgroup
+
+template <int NN, int KJ>
+__global__ void __launch_bounds__(256) pf_skinny_kernel(PfGemm g) {
+    __shared__ float s_red[2][4][NN];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    uint4 wv[NN][KJ];
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+        for (int j = 0; j < KJ; ++j)
+            wv[n][j] = *(const uint4*) (g.wb + (size_t) min(n, g.N - 1) * g.K + 2048 * j + 8 * tid);
+    const int r0 = blockIdx.x * SK_RB, r1 = min(r0 + SK_RB, g.M);
+    uint4 an[KJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) an[j] = *(const uint4*) (g.a + (size_t) r0 * g.lda + 2048 * j + 8 * tid);
+    for (int t = r0; t < r1; ++t) {
+        uint4 av[KJ];
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) av[j] = an[j];
+        if (t + 1 < r1) {                            // the next row's loads in flight
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) an[j] = *(const uint4*) (g.a + (size_t) (t + 1) * g.lda + 2048 * j + 8 * tid);
+        }
+        float acc[NN];
+#pragma unroll
+        for (int n = 0; n < NN; ++n) acc[n] = 0.f;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+            const uint32_t aw[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x0 = bf16_lo(aw[e]), x1 = bf16_hi(aw[e]);
+#pragma unroll
+                for (int n = 0; n < NN; ++n) {
+                    const uint32_t ww = e == 0 ? wv[n][j].x : e == 1 ? wv[n][j].y : e == 2 ? wv[n][j].z : wv[n][j].w;
+                    acc[n] = fmaf(x0, bf16_lo(ww), acc[n]);
+                    acc[n] = fmaf(x1, bf16_hi(ww), acc[n]);
+                }
+            }
+        }
+        const int pb = t & 1;                        // partials alternate buffers: one barrier per row
+#pragma unroll
+        for (int n = 0; n < NN; ++n) {
+            const float v = wave_sum(acc[n]);
+            if (lane == 0) s_red[pb][w][n] = v;
+        }
+        __syncthreads();
+        if (tid < g.N && tid < NN)
+            g.y[(size_t) t * g.ldy + tid] = (s_red[pb][0][tid] + s_red[pb][1][tid]) + (s_red[pb][2][tid] + s_red[pb][3][tid]);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -744,6 +803,20 @@ int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
     WZY_REQUIRE(g.M >= 1 && g.N >= 1 && g.K >= GK && g.K % GK == 0, "pf_gemm: M %d N %d K %d (K a multiple of %d)",
                 g.M, g.N, g.K, GK);
     WZY_REQUIRE(g.lda >= g.K && g.lda % 8 == 0 && g.ldy >= g.N, "pf_gemm: bad leading dimensions");
+    if (!g.wq && g.y && g.N <= 16 && g.K % 2048 == 0 && g.K <= 8192 && g.lda % 8 == 0) {
+        const int nn = g.N <= 4 ? 4 : g.N <= 8 ? 8 : 16, kj = g.K / 2048;
+        if (nn * kj <= 16) {                         // the weight slices fit 64 registers
+            const dim3 grid((g.M + SK_RB - 1) / SK_RB);
+            if (nn == 4 && kj == 4) hipLaunchKernelGGL((pf_skinny_kernel<4, 4>), grid, dim3(256), 0, st, g);
+            else if (nn == 4 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<4, 2>), grid, dim3(256), 0, st, g);
+            else if (nn == 4 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<4, 1>), grid, dim3(256), 0, st, g);
+            else if (nn == 8 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<8, 2>), grid, dim3(256), 0, st, g);
+            else if (nn == 8 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<8, 1>), grid, dim3(256), 0, st, g);
+            else hipLaunchKernelGGL((pf_skinny_kernel<16, 1>), grid, dim3(256), 0, st, g);
+            WZY_LAUNCH_CHECK();
+            return WZY_OK;
+        }
+    }
     GemmArgs ga;
     ga.g = g;
     ga.mt = (g.M + GM - 1) / GM;
