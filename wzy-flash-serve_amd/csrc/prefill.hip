@@ -14,7 +14,7 @@
 //                32 steps at a time), pf_gdn_norm (gated RMS norm, bf16).
 //  QSA           pf_qsa_prep (q / k / indexer-q norms + RoPE, INT8 KV append), pf_idx_append (the
 //                indexer keys of every block the chunk completes, one workgroup per block, then
-//                pf_idx_tail), block scores and top-k with the decode kernels over all rows,
+//                pf_idx_tail), block scores on fp16 MFMA (pf_score), top-k with the decode kernel,
 //                pf_attn (sparse GQA attention on fp16 MFMA, 64 cells per load step, a 32-cell
 //                online softmax).
 // reference: PrefillStageCtx::run_stage_prefill and its kernels (src/wzy_prefill_tc.cuh:20-98,
@@ -585,6 +585,105 @@ __global__ void __launch_bounds__(128) pf_idx_tail_kernel(PfIdxAppend a, int p0,
     }
 }
 
+// Indexer block scores of the chunk's rows on MFMA: score[t][b] = sum over heads h of
+// relu(q_h[t] . key[b]), fp16 queries and keys with fp32 products and sums (v_mfma_f32_32x32x16_f16,
+// as the reference's prefill scorer runs on WMMA).  Workgroup = 32 rows x 256 blocks, wave w: blocks
+// 64w .. 64w+63 as two 32 x 32 tiles, the four heads' accumulators side by side; the queries are
+// staged in LDS as fp16, each wave loads its keys' k slices straight into B fragments.  Only complete
+// blocks of rows whose context exceeds top_k are written; the row group's first workgroup also
+// scores the open block against the placeholder key (fp32, +1e9 while the block is partial), as the
+// decode scorer does.  (qsa_block_scores_wmma, src/wzy_qsa_wmma.cuh:492-612)
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+constexpr int PS_ROWS = 32, PS_BLOCKS = 256;
+
+__global__ void __launch_bounds__(256) pf_score_kernel(QsaScoreArgs a) {
+    __shared__ __align__(16) _Float16 sQ[4][PS_ROWS][128 + 8];
+    const QsaDims& dm = a.dm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r0 = blockIdx.y * PS_ROWS, nrows = min(PS_ROWS, a.rows - r0);
+    const int base = *a.pos + r0;
+    const int B = dm.iblk, IH = dm.ih;
+    const int n_kv_max = base + nrows;
+    if (n_kv_max <= dm.topk) return;                 // short context: identity selection
+    const int b0 = blockIdx.x * PS_BLOCKS;
+    const bool tail_wg = blockIdx.x == 0;
+    const int b_lim = min(a.max_b, n_kv_max / B);
+    if (b0 >= b_lim && !tail_wg) return;
+    const float* q_idx = a.q_idx + (size_t) r0 * IH * 128;
+    float* scores = a.scores + (size_t) r0 * a.max_b;
+
+    for (int i = tid; i < 4 * PS_ROWS * 32; i += 256) {     // (head, row, 4 k) -> fp16
+        const int h = i / (PS_ROWS * 32), r = (i / 32) % PS_ROWS, k4 = i % 32;
+        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nrows && h < IH) q = *(const float4*) (q_idx + (size_t) r * IH * 128 + (size_t) h * 128 + 4 * k4);
+        _Float16* d = &sQ[h][r][4 * k4];
+        d[0] = (_Float16) q.x; d[1] = (_Float16) q.y; d[2] = (_Float16) q.z; d[3] = (_Float16) q.w;
+    }
+    __syncthreads();
+
+    if (b0 + 64 * w < b_lim) {
+        f32x16_t acc[2][4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[c][h][i] = 0.f;
+        const int kb = (lane >> 5) * 8;
+        const _Float16* kp[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int b = min(b0 + 64 * w + 32 * c + (lane & 31), b_lim - 1);
+            kp[c] = (const _Float16*) a.pooled + (size_t) b * 128 + kb;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            f16x8_t bv[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) bv[c] = *(const f16x8_t*) (kp[c] + 16 * ks);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                if (h >= IH) break;                      // uniform
+                const f16x8_t av = *(const f16x8_t*) &sQ[h][lane & 31][16 * ks + kb];
+#pragma unroll
+                for (int c = 0; c < 2; ++c) acc[c][h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[c], acc[c][h], 0, 0, 0);
+            }
+        }
+        // acc[c][h][i] = q_h[row 8*(i/4) + 4*(lane/32) + i%4] . key[block 32c + lane%32]
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int b = b0 + 64 * w + 32 * c + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                float sc = 0.f;
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    if (h < IH) sc += acc[c][h][i] > 0.f ? acc[c][h][i] : 0.f;
+                const int n_kv = base + t + 1;
+                if (t < nrows && n_kv > dm.topk && b < n_kv / B) scores[(size_t) t * a.max_b + b] = sc;
+            }
+        }
+    }
+    // open block: fp32 dot with the placeholder key (wave w handles rows w, w + 4, ...)
+    if (tail_wg) {
+        for (int t = w; t < nrows; t += 4) {
+            const int n_kv = base + t + 1;
+            const int nbid = n_kv / B;
+            if (n_kv <= dm.topk || nbid >= a.max_b) continue;
+            float score = 0.f;
+            for (int h = 0; h < IH; ++h) {
+                float p = 0.f;
+                for (int k = lane; k < 128; k += 64) p = fmaf(a.dead[k], q_idx[(size_t) t * IH * 128 + (size_t) h * 128 + k], p);
+                p = wave_sum(p);
+                score += p > 0.f ? p : 0.f;
+            }
+            if (n_kv % B != 0) score += 1e9f;
+            if (lane == 0) scores[(size_t) t * a.max_b + nbid] = score;
+        }
+    }
+}
+
 // Sparse GQA attention of one row and one KV head (grid (kvh, B), 256 threads): the group's query
 // heads (up to 16, rows of a 16 x 16 fp16 MFMA tile) against the selected cells, 64 per load step.
 // Per step: K of 64 cells dequantised to fp16 in LDS (row major), scores on
@@ -890,6 +989,18 @@ int launch_pf_idx_append(const PfIdxAppend& a, int p0, int B, hipStream_t st) {
     if (n_ev > 0)
         hipLaunchKernelGGL(pf_idx_append_kernel, dim3(n_ev), dim3(256), 0, st, a, p0, B, has0, pc0, n_ev);
     hipLaunchKernelGGL(pf_idx_tail_kernel, dim3(1), dim3(128), 0, st, a, p0, B);
+    WZY_LAUNCH_CHECK();
+    return WZY_OK;
+}
+
+int launch_pf_scores(const QsaScoreArgs& a0, int rows, hipStream_t st) {
+    WZY_TRY(qsa_check_dims(a0.dm));
+    WZY_REQUIRE(a0.dm.idim == 128 && a0.dm.ih <= 4, "pf_scores: indexer layout unsupported");
+    WZY_REQUIRE(rows >= 1 && (rows + PS_ROWS - 1) / PS_ROWS <= 65535, "pf_scores: %d rows", rows);
+    QsaScoreArgs a = a0;
+    a.rows = rows;
+    const dim3 grid((a.max_b + PS_BLOCKS - 1) / PS_BLOCKS, (rows + PS_ROWS - 1) / PS_ROWS);
+    hipLaunchKernelGGL(pf_score_kernel, grid, dim3(256), 0, st, a);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }

@@ -1583,7 +1583,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
                     QsaScoreArgs sa{};
                     sa.dm = dm; sa.pos = pf.pos8 + q0 / 8; sa.pooled = w.ix.pooled; sa.dead = w.ix.dead;
                     sa.q_idx = pf.q_idx + (size_t) q0 * IH * ID; sa.scores = pf.scores; sa.max_b = max_b;
-                    WZY_TRY(launch_qsa_score_rows(sa, qb, st));
+                    WZY_TRY(launch_pf_scores(sa, qb, st));
                     if (trace && pf.tr_sc)
                         WZY_HIP_TRY(hipMemcpyAsync(pf.tr_sc + ((size_t) w.local * pf.tr_rows + q0) * max_b, pf.scores,
                                                    (size_t) qb * max_b * 4, hipMemcpyDeviceToDevice, st));

@@ -81,6 +81,8 @@ struct PfAttn {
     uint16_t* out;
 };
 int launch_pf_attn(const PfAttn& a, int B, hipStream_t st);
+// indexer block scores of `rows` consecutive rows on MFMA (same arguments as launch_qsa_score_rows)
+int launch_pf_scores(const QsaScoreArgs& a, int rows, hipStream_t st);
 // top-k of `rows` rows at one launch (every row's blocks must fit one workgroup); internal to
 // qsa_attn.hip
 int launch_qsa_topk_rows(const QsaDims& dm, const int* pos, const float* scores, int max_b, int* sel_ids,
