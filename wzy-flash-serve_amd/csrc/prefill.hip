@@ -250,6 +250,7 @@ __global__ void __launch_bounds__(256) pf_embed_kernel(PfEmb e, const int* __res
 
 // per (stream c, row t): R += bo * 2 sigmoid(inj_prev / HC) when a block is pending; x = bf16(R *
 // rsqrt(mean R^2 + eps) * norm_w)  (pf_gr_norm_fp16, src/wzy_qsa_wmma.cuh:198-234)
+constexpr int HN_PER = 16;                   // values per thread of pf_hc_norm (D <= 4096)
 __global__ void __launch_bounds__(256) pf_hc_norm_kernel(float* __restrict__ R, const float* __restrict__ bo,
                                                           const float* __restrict__ inj_prev,
                                                           const float* __restrict__ norm_w, uint16_t* __restrict__ xn,
@@ -259,18 +260,28 @@ __global__ void __launch_bounds__(256) pf_hc_norm_kernel(float* __restrict__ R, 
     float* r = R + ((size_t) t * HC + c) * D;
     const float gate = bo ? 2.0f / (1.0f + __expf(-inj_prev[t * HC + c] / (float) HC)) : 0.0f;
     float ss = 0.f;
-    for (int d = tid; d < D; d += 256) {
-        float v = r[d];
-        if (bo) {
-            v = fmaf(bo[(size_t) t * D + d], gate, v);
-            r[d] = v;
+    float v[HN_PER];                                 // the thread's values stay in registers (D <= 4096)
+#pragma unroll
+    for (int i = 0; i < HN_PER; ++i) {
+        const int d = tid + 256 * i;
+        v[i] = 0.f;
+        if (d < D) {
+            v[i] = r[d];
+            if (bo) {
+                v[i] = fmaf(bo[(size_t) t * D + d], gate, v[i]);
+                r[d] = v[i];
+            }
         }
-        ss += v * v;
+        ss += v[i] * v[i];
     }
     ss = block_sum<4>(ss, s_red);
     const float inv = 1.0f / sqrtf(ss / (float) D + eps);
     uint16_t* x = xn + (size_t) t * HC * D + (size_t) c * D;
-    for (int d = tid; d < D; d += 256) x[d] = f_to_bf16(r[d] * inv * norm_w[(size_t) c * D + d]);
+#pragma unroll
+    for (int i = 0; i < HN_PER; ++i) {
+        const int d = tid + 256 * i;
+        if (d < D) x[d] = f_to_bf16(v[i] * inv * norm_w[(size_t) c * D + d]);
+    }
 }
 
 __global__ void __launch_bounds__(256) pf_silu_div_kernel(const float* __restrict__ lo, uint16_t* __restrict__ loh,
@@ -934,6 +945,7 @@ int launch_pf_embed(const PfEmb& e, const int* toks, float* R, int D, int HC, in
 
 int launch_pf_hc_norm(float* R, const float* bo, const float* inj_prev, const float* norm_w, uint16_t* xn, int D,
                       int HC, float eps, int B, hipStream_t st) {
+    WZY_REQUIRE(D >= 1 && D <= 256 * HN_PER, "pf_hc_norm: n_embd %d above %d", D, 256 * HN_PER);
     hipLaunchKernelGGL(pf_hc_norm_kernel, dim3(HC, B), dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps);
     WZY_LAUNCH_CHECK();
     return WZY_OK;

@@ -1611,10 +1611,9 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
             WZY_TRY(gemm(pf.xh, QD, QD, &w.wo, nullptr, D, pf.block, nullptr, D));
         }
         WZY_TRY(tr(l, 1, pf.block));
-        WZY_TRY(mark(5));
-        WZY_TRY(launch_pf_hc_write(pf.R, pf.block, pf.inj_a, D, HC, B, st));
         WZY_TRY(mark(3));
-        WZY_TRY(hc_read(w.hc_norm[1], w.hc_down[1], w.hc_inj[1], w.hc_up[1], nullptr, nullptr, pf.inj_f));
+        // the block's write into the streams is folded into the FFN read (same arithmetic)
+        WZY_TRY(hc_read(w.hc_norm[1], w.hc_down[1], w.hc_inj[1], w.hc_up[1], pf.block, pf.inj_a, pf.inj_f));
         WZY_TRY(tr(l, 2, pf.mixed));
         WZY_TRY(mark(4));
         WZY_TRY(wzy_moe_prefill(&w.moe, pf.mixed, B, pf.comb, nullptr, nullptr, pf.moe_ws, pf.moe_bytes, st));
