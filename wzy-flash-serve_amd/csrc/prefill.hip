@@ -7,7 +7,8 @@
 //                tiles and each runs all weight tiles of its row tile back to back.  A few bf16
 //                weight rows (N <= 16) take pf_skinny instead (fp32 FMA dot products per row).
 //  HC read       pf_hc_norm (pending block folded in, per-stream RMSNorm, bf16), GEMMs for inject /
-//                down / up, pf_silu_div, pf_up_mean; pf_hc_write writes a block into the streams.
+//                down (K split by stream) / up (the stream mean as its epilogue), pf_silu_div; pf_hc_write
+//                writes a block into the streams.
 //  GDN           pf_gdn_ab (gates), pf_gdn_conv (causal conv + SiLU + L2 of q/k heads over all rows
 //                at once), pf_gdn_hist (conv history), pf_gdn_recur (the delta rule, sequential over
 //                the rows: 32 lanes per state column, 4 rows each in registers, q/k staged in LDS
@@ -61,12 +62,18 @@ WZY_DEV void q8_block_bf16(uint4 c0, uint4 c1, float sc, uint4& o0, uint4& o1, u
     o3 = q8_quarter_bf16(c1.z, c1.w, sc);
 }
 
+// UM: the HC up projection with the stream mean as its epilogue.  Tile column n holds stream
+// c = n % 4 of position d = n / 4 (weight row c * um_d + d), so a row's four stream gates sit in
+// one lane quad and are combined there in stream order.
+template <bool UM>
 __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
     __shared__ __align__(16) uint16_t sA[2][GM][GLD];
     __shared__ __align__(16) uint16_t sW[2][GN][GLD];
     const PfGemm& g = ga.g;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
-    const int b = blockIdx.x;
+    const int tiles = ga.mt * ga.nt;
+    const int ksp = (int) blockIdx.x / tiles;                      // K range of a split launch
+    const int b = (int) blockIdx.x - ksp * tiles;
     int mi, ni;
     if ((ga.mt & 7) == 0) {
         const int s = b >> 3;
@@ -78,13 +85,15 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
     }
     const int m0 = mi * GM, n0 = ni * GN;
     const int sr = tid >> 1, kh = (tid & 1) * 32;                  // staging: row sr, k kh .. kh+31
-    const uint16_t* ap = g.a + (size_t) min(m0 + sr, g.M - 1) * g.lda + kh;
-    const size_t wr = (size_t) min(n0 + sr, g.N - 1);
+    const int nk = g.K / GK / max(g.ksplit, 1);                    // k steps of this launch's range
+    const size_t k0 = (size_t) ksp * nk * GK;
+    const uint16_t* ap = g.a + (size_t) min(m0 + sr, g.M - 1) * g.lda + k0 + kh;
+    size_t wr = (size_t) min(n0 + sr, g.N - 1);
+    if (UM) wr = (wr & 3) * (size_t) g.um_d + (wr >> 2);
     const bool q8 = g.wq != nullptr;
-    const int8_t* wqp = q8 ? g.wq + wr * g.K + kh : nullptr;
-    const uint16_t* wsp = q8 ? g.ws + wr * (g.K / 32) + kh / 32 : nullptr;
-    const uint16_t* wbp = q8 ? nullptr : g.wb + wr * g.K + kh;
-    const int nk = g.K / GK;
+    const int8_t* wqp = q8 ? g.wq + wr * g.K + k0 + kh : nullptr;
+    const uint16_t* wsp = q8 ? g.ws + wr * (g.K / 32) + (k0 + kh) / 32 : nullptr;
+    const uint16_t* wbp = q8 ? nullptr : g.wb + wr * g.K + k0 + kh;
 
     // staging registers are scalars: arrays captured by a lambda would live in scratch memory
     uint4 ra0, ra1, ra2, ra3, rw0, rw1, rw2 = make_uint4(0, 0, 0, 0), rw3 = rw2;
@@ -155,6 +164,46 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
 #undef PF_GEMM_LOAD
 #undef PF_GEMM_STORE
     // acc[i][j][r] = C[row 8*(r/4) + 4*(lane/32) + r%4][col lane%32] of block (i, j)
+    if constexpr (UM) {
+        // mixed = (sum over streams in order of xn / (1 + exp(-bf16 gate))) / 4, fp32 and bf16
+        // (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252); the xn loads of all four blocks go first
+        const int D = g.um_d, c = lane & 3;
+        float xv[2][2][16];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int d = (n0 + wn * 64 + j * 32 + (lane & 31)) >> 2;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = min(m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), g.M - 1);
+                    xv[i][j][r] = bf16_to_f(g.um_xn[(size_t) row * 4 * D + (size_t) c * D + d]);
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int d = (n0 + wn * 64 + j * 32 + (lane & 31)) >> 2;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const float gq = bf16_to_f(f_to_bf16(acc[i][j][r]));
+                    const float term = xv[i][j][r] / (1.0f + __expf(-gq));
+                    float sum = 0.f + dpp_f<0x00>(term);             // quad lanes 0..3 = streams 0..3
+                    sum += dpp_f<0x55>(term);
+                    sum += dpp_f<0xAA>(term);
+                    sum += dpp_f<0xFF>(term);
+                    const float v = sum * 0.25f;
+                    if (c == 0 && row < g.M) {
+                        g.um_mixed[(size_t) row * D + d] = v;
+                        g.um_xh[(size_t) row * D + d] = f_to_bf16(v);
+                    }
+                }
+            }
+        return;
+    }
+    float* const y = g.y ? g.y + (size_t) ksp * g.M * g.ldy : nullptr;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -164,7 +213,7 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (row < g.M && col < g.N) {
-                    if (g.y) g.y[(size_t) row * g.ldy + col] = acc[i][j][r];
+                    if (y) y[(size_t) row * g.ldy + col] = acc[i][j][r];
                     else g.yb[(size_t) row * g.ldy + col] = f_to_bf16(acc[i][j][r]);
                 }
             }
@@ -250,65 +299,65 @@ __global__ void __launch_bounds__(256) pf_embed_kernel(PfEmb e, const int* __res
 
 // per (stream c, row t): R += bo * 2 sigmoid(inj_prev / HC) when a block is pending; x = bf16(R *
 // rsqrt(mean R^2 + eps) * norm_w)  (pf_gr_norm_fp16, src/wzy_qsa_wmma.cuh:198-234)
-constexpr int HN_PER = 16;                   // values per thread of pf_hc_norm (D <= 4096)
+// A thread holds NG groups of 4 consecutive values (group tid + 256 i), loaded and stored 16 bytes
+// at a time; NG = ceil(D / 1024), D a multiple of 4 and at most 4096.
+template <int NG>
 __global__ void __launch_bounds__(256) pf_hc_norm_kernel(float* __restrict__ R, const float* __restrict__ bo,
                                                           const float* __restrict__ inj_prev,
                                                           const float* __restrict__ norm_w, uint16_t* __restrict__ xn,
                                                           int D, int HC, float eps) {
     __shared__ float s_red[4];
     const int c = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    float* r = R + ((size_t) t * HC + c) * D;
+    const int ng = D / 4;
+    float4* r = (float4*) (R + ((size_t) t * HC + c) * D);
+    const float4* bp = bo ? (const float4*) (bo + (size_t) t * D) : nullptr;
     const float gate = bo ? 2.0f / (1.0f + __expf(-inj_prev[t * HC + c] / (float) HC)) : 0.0f;
-    float ss = 0.f;
-    float v[HN_PER];                                 // the thread's values stay in registers (D <= 4096)
+    float4 v[NG], bv[NG];
 #pragma unroll
-    for (int i = 0; i < HN_PER; ++i) {
-        const int d = tid + 256 * i;
-        v[i] = 0.f;
-        if (d < D) {
-            v[i] = r[d];
-            if (bo) {
-                v[i] = fmaf(bo[(size_t) t * D + d], gate, v[i]);
-                r[d] = v[i];
-            }
+    for (int i = 0; i < NG; ++i) {                   // clamped, unconditional loads
+        const int gi = min(tid + 256 * i, ng - 1);
+        v[i] = r[gi];
+        if (bo) bv[i] = bp[gi];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int gi = tid + 256 * i;
+        if (bo) {
+            v[i].x = fmaf(bv[i].x, gate, v[i].x);
+            v[i].y = fmaf(bv[i].y, gate, v[i].y);
+            v[i].z = fmaf(bv[i].z, gate, v[i].z);
+            v[i].w = fmaf(bv[i].w, gate, v[i].w);
+            if (gi < ng) r[gi] = v[i];
         }
-        ss += v[i] * v[i];
+        if (gi >= ng) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        ss += v[i].x * v[i].x;
+        ss += v[i].y * v[i].y;
+        ss += v[i].z * v[i].z;
+        ss += v[i].w * v[i].w;
     }
     ss = block_sum<4>(ss, s_red);
     const float inv = 1.0f / sqrtf(ss / (float) D + eps);
-    uint16_t* x = xn + (size_t) t * HC * D + (size_t) c * D;
+    const float4* wp = (const float4*) (norm_w + (size_t) c * D);
+    uint2* x = (uint2*) (xn + (size_t) t * HC * D + (size_t) c * D);
 #pragma unroll
-    for (int i = 0; i < HN_PER; ++i) {
-        const int d = tid + 256 * i;
-        if (d < D) x[d] = f_to_bf16(v[i] * inv * norm_w[(size_t) c * D + d]);
+    for (int i = 0; i < NG; ++i) {
+        const int gi = tid + 256 * i;
+        if (gi < ng) {
+            const float4 w = wp[gi];
+            x[gi] = make_uint2(pack_bf16(v[i].x * inv * w.x, v[i].y * inv * w.y),
+                               pack_bf16(v[i].z * inv * w.z, v[i].w * inv * w.w));
+        }
     }
 }
 
 __global__ void __launch_bounds__(256) pf_silu_div_kernel(const float* __restrict__ lo, uint16_t* __restrict__ loh,
-                                                           size_t n, float inv_hc) {
+                                                           size_t n, int nsplit, float inv_hc) {
     const size_t i = (size_t) blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float v = lo[i] * inv_hc;
+    const float s = nsplit == 4 ? (lo[i] + lo[n + i]) + (lo[2 * n + i] + lo[3 * n + i]) : lo[i];
+    const float v = s * inv_hc;
     loh[i] = f_to_bf16(v / (1.0f + __expf(-v)));
-}
-
-// mixed[t][d] = (sum over streams in order of x / (1 + exp(-g))) / HC, fp32 and bf16
-// (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252)
-__global__ void __launch_bounds__(256) pf_up_mean_kernel(const uint16_t* __restrict__ xn, const uint16_t* __restrict__ gg,
-                                                          float* __restrict__ mixed, uint16_t* __restrict__ xh, int D,
-                                                          int HC) {
-    const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
-    if (d >= D) return;
-    const size_t base = (size_t) t * HC * D + d;
-    float acc = 0.f;
-    for (int c = 0; c < HC; ++c) {
-        const float x = bf16_to_f(xn[base + (size_t) c * D]);
-        const float g = bf16_to_f(gg[base + (size_t) c * D]);
-        acc += x / (1.0f + __expf(-g));
-    }
-    const float v = acc * (1.0f / (float) HC);
-    mixed[(size_t) t * D + d] = v;
-    xh[(size_t) t * D + d] = f_to_bf16(v);
 }
 
 // R[t][c][d] += blk[t][d] * 2 sigmoid(inj[t][c] / HC)  (gr_write_multi, src/wzy_kernels_v2.cuh:813-827)
@@ -909,11 +958,18 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
 namespace wzy {
 
 int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
-    WZY_REQUIRE(g.a && (g.wq ? g.ws != nullptr : g.wb != nullptr) && (g.y || g.yb), "pf_gemm: null operand");
+    const bool um = g.um_mixed != nullptr;
+    const int ksplit = max(g.ksplit, 1);
+    WZY_REQUIRE(g.a && (g.wq ? g.ws != nullptr : g.wb != nullptr) && (um ? g.um_xn && g.um_xh : (g.y || g.yb)),
+                "pf_gemm: null operand");
     WZY_REQUIRE(g.M >= 1 && g.N >= 1 && g.K >= GK && g.K % GK == 0, "pf_gemm: M %d N %d K %d (K a multiple of %d)",
                 g.M, g.N, g.K, GK);
-    WZY_REQUIRE(g.lda >= g.K && g.lda % 8 == 0 && g.ldy >= g.N, "pf_gemm: bad leading dimensions");
-    if (!g.wq && g.y && g.N <= 16 && g.K % 2048 == 0 && g.K <= 8192 && g.lda % 8 == 0) {
+    WZY_REQUIRE(g.lda >= g.K && g.lda % 8 == 0 && (um || g.ldy >= g.N), "pf_gemm: bad leading dimensions");
+    WZY_REQUIRE(!um || (g.um_d >= 32 && g.um_d % 32 == 0 && g.N == 4 * g.um_d && ksplit == 1),
+                "pf_gemm: stream-mean epilogue needs N = 4 * n_embd (n_embd %d, a multiple of 32), no K split", g.um_d);
+    WZY_REQUIRE(ksplit <= 8 && (ksplit == 1 || (g.y && (g.K / GK) % ksplit == 0)),
+                "pf_gemm: K split %d needs fp32 output and %d k steps divisible by it", ksplit, g.K / GK);
+    if (!um && ksplit == 1 && !g.wq && g.y && g.N <= 16 && g.K % 2048 == 0 && g.K <= 8192 && g.lda % 8 == 0) {
         const int nn = g.N <= 4 ? 4 : g.N <= 8 ? 8 : 16, kj = g.K / 2048;
         if (nn * kj <= 16) {                         // the weight slices fit 64 registers
             const dim3 grid((g.M + SK_RB - 1) / SK_RB);
@@ -931,8 +987,9 @@ int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
     ga.g = g;
     ga.mt = (g.M + GM - 1) / GM;
     ga.nt = (g.N + GN - 1) / GN;
-    WZY_REQUIRE((long long) ga.mt * ga.nt < (1LL << 31), "pf_gemm: too many tiles");
-    hipLaunchKernelGGL(pf_gemm_kernel, dim3(ga.mt * ga.nt), dim3(256), 0, st, ga);
+    WZY_REQUIRE((long long) ga.mt * ga.nt * ksplit < (1LL << 31), "pf_gemm: too many tiles");
+    if (um) hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3(ga.mt * ga.nt), dim3(256), 0, st, ga);
+    else hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3(ga.mt * ga.nt * ksplit), dim3(256), 0, st, ga);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
@@ -945,21 +1002,22 @@ int launch_pf_embed(const PfEmb& e, const int* toks, float* R, int D, int HC, in
 
 int launch_pf_hc_norm(float* R, const float* bo, const float* inj_prev, const float* norm_w, uint16_t* xn, int D,
                       int HC, float eps, int B, hipStream_t st) {
-    WZY_REQUIRE(D >= 1 && D <= 256 * HN_PER, "pf_hc_norm: n_embd %d above %d", D, 256 * HN_PER);
-    hipLaunchKernelGGL(pf_hc_norm_kernel, dim3(HC, B), dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps);
+    WZY_REQUIRE(D >= 4 && D <= 4096 && D % 4 == 0, "pf_hc_norm: n_embd %d (a multiple of 4, at most 4096)", D);
+    const dim3 grid(HC, B);
+    switch ((D + 1023) / 1024) {
+        case 1: hipLaunchKernelGGL(pf_hc_norm_kernel<1>, grid, dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps); break;
+        case 2: hipLaunchKernelGGL(pf_hc_norm_kernel<2>, grid, dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps); break;
+        case 3: hipLaunchKernelGGL(pf_hc_norm_kernel<3>, grid, dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps); break;
+        default: hipLaunchKernelGGL(pf_hc_norm_kernel<4>, grid, dim3(256), 0, st, R, bo, inj_prev, norm_w, xn, D, HC, eps); break;
+    }
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
 
-int launch_pf_silu_div(const float* lo, uint16_t* loh, size_t n, float inv_hc, hipStream_t st) {
-    hipLaunchKernelGGL(pf_silu_div_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, lo, loh, n, inv_hc);
-    WZY_LAUNCH_CHECK();
-    return WZY_OK;
-}
-
-int launch_pf_up_mean(const uint16_t* xn, const uint16_t* gg, float* mixed, uint16_t* xh, int D, int HC, int B,
-                      hipStream_t st) {
-    hipLaunchKernelGGL(pf_up_mean_kernel, dim3((D + 255) / 256, B), dim3(256), 0, st, xn, gg, mixed, xh, D, HC);
+int launch_pf_silu_div(const float* lo, uint16_t* loh, size_t n, int nsplit, float inv_hc, hipStream_t st) {
+    WZY_REQUIRE(nsplit == 1 || nsplit == 4, "pf_silu_div: %d partial sums (1 or 4)", nsplit);
+    hipLaunchKernelGGL(pf_silu_div_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, lo, loh, n, nsplit,
+                       inv_hc);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }

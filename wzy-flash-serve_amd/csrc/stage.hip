@@ -211,7 +211,7 @@ struct wzy_stage {
         void* base = nullptr;
         size_t bytes = 0;
         float *R = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
-        uint16_t *xn = nullptr, *loh = nullptr, *gg = nullptr, *xh = nullptr;
+        uint16_t *xn = nullptr, *loh = nullptr, *xh = nullptr;
         float *qkv = nullptr, *z = nullptr, *ab = nullptr, *conv_out = nullptr, *decay = nullptr, *beta = nullptr,
               *o = nullptr;
         float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
@@ -1433,8 +1433,8 @@ int wzy_stage::prefill_reserve(int B) {
         off += (bytes + 255) & ~(size_t) 255;
         return r;
     };
-    const size_t oR = bump(b * HCD * 4), oxn = bump(b * HCD * 2), olo = bump(b * c.hc_lr * 4),
-                 oloh = bump(b * c.hc_lr * 2), ogg = bump(b * HCD * 2), oia = bump(b * c.hc * 4),
+    const size_t oR = bump(b * HCD * 4), oxn = bump(b * HCD * 2), olo = bump(4 * b * c.hc_lr * 4),
+                 oloh = bump(b * c.hc_lr * 2), oia = bump(b * c.hc * 4),
                  oif = bump(b * c.hc * 4), omx = bump(b * D * 4), oxh = bump(b * xh_w * 2), oblk = bump(b * D * 4),
                  ocomb = bump(b * D * 4), otoks = bump(b * 4), opos = bump((b / 8 + 2) * 4);
     // GDN and QSA scratch share one region (a layer uses one of them)
@@ -1462,7 +1462,7 @@ int wzy_stage::prefill_reserve(int B) {
     pf.cap = B;
     pf.sc_rows = sc_rows;
     pf.R = (float*) (u + oR); pf.xn = (uint16_t*) (u + oxn); pf.lo = (float*) (u + olo);
-    pf.loh = (uint16_t*) (u + oloh); pf.gg = (uint16_t*) (u + ogg); pf.inj_a = (float*) (u + oia);
+    pf.loh = (uint16_t*) (u + oloh); pf.inj_a = (float*) (u + oia);
     pf.inj_f = (float*) (u + oif); pf.mixed = (float*) (u + omx); pf.xh = (uint16_t*) (u + oxh);
     pf.block = (float*) (u + oblk); pf.comb = (float*) (u + ocomb); pf.toks = (int*) (u + otoks);
     pf.pos8 = (int*) (u + opos);
@@ -1515,14 +1515,26 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
     };
     // hyper-connection read of the chunk: R (with the pending block folded in when bo != null) ->
     // mixed fp32 + xh bf16, inject -> inj_out
+    // The down projection runs as four K ranges, one per stream (768 workgroups instead of 192 for
+    // its 320 outputs), summed ((p0 + p1) + (p2 + p3)) by pf_silu_div; the up projection combines
+    // its stream gates with xn in its epilogue, so the [B][4D] gates never reach memory.
+    const int down_split = (HCD / 64) % 4 == 0 ? 4 : 1;
     auto hc_read = [&](const float* norm_w, const Q8& down, const uint16_t* inj_w, const Q8& up, const float* bo,
                        const float* inj_prev, float* inj_out) -> int {
         WZY_TRY(launch_pf_hc_norm(pf.R, bo, inj_prev, norm_w, pf.xn, D, HC, c.eps, B, st));
         WZY_TRY(gemm(pf.xn, HCD, HCD, nullptr, inj_w, HC, inj_out, nullptr, HC));
-        WZY_TRY(gemm(pf.xn, HCD, HCD, &down, nullptr, HCLR, pf.lo, nullptr, HCLR));
-        WZY_TRY(launch_pf_silu_div(pf.lo, pf.loh, (size_t) B * HCLR, inv_hc, st));
-        WZY_TRY(gemm(pf.loh, HCLR, HCLR, &up, nullptr, HCD, nullptr, pf.gg, HCD));
-        return launch_pf_up_mean(pf.xn, pf.gg, pf.mixed, pf.xh, D, HC, B, st);
+        {
+            PfGemm g{};
+            g.a = pf.xn; g.lda = HCD; g.M = B; g.N = HCLR; g.K = HCD;
+            g.wq = down.q; g.ws = down.s; g.y = pf.lo; g.ldy = HCLR; g.ksplit = down_split;
+            WZY_TRY(launch_pf_gemm(g, st));
+        }
+        WZY_TRY(launch_pf_silu_div(pf.lo, pf.loh, (size_t) B * HCLR, down_split, inv_hc, st));
+        PfGemm g{};
+        g.a = pf.loh; g.lda = HCLR; g.M = B; g.N = HCD; g.K = HCLR;
+        g.wq = up.q; g.ws = up.s;
+        g.um_xn = pf.xn; g.um_mixed = pf.mixed; g.um_xh = pf.xh; g.um_d = D;
+        return launch_pf_gemm(g, st);
     };
 
     hipLaunchKernelGGL(pf_pos_kernel, dim3((B / 8 + 2 + 255) / 256), dim3(256), 0, st, pf.pos8, p0, B / 8 + 2);

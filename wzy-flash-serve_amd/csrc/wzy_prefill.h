@@ -10,12 +10,20 @@ namespace wzy {
 // C[m][n] = sum_k A[m][k] * W[n][k] on bf16 MFMA: A bf16 rows (lda elements apart); W Q8_0 (codes
 // [N][K], fp16 scales [N][K/32], code * scale rounded to bf16) or bf16 [N][K]; output fp32 (y) or
 // bf16 (yb), rows ldy apart.  K a multiple of 64.
+// ksplit > 1 (fp32 output only): K is cut into ksplit equal ranges whose partial sums go to
+// y + s * M * ldy (s = 0 .. ksplit-1); the consumer adds them.
+// um_mixed != null (the HC up projection, N = 4 * um_d): instead of storing C, each row's four stream
+// gates are combined with the normed streams (um_xn bf16 [M][4][um_d]):
+//   mixed[m][d] = (sum over c in order of xn[m][c][d] / (1 + exp(-bf16(C[m][c * um_d + d])))) / 4
+// written fp32 to um_mixed and bf16 to um_xh (both [M][um_d]).
 struct PfGemm {
     const uint16_t* a; int lda;
     int M, N, K;
     const int8_t* wq; const uint16_t* ws;
     const uint16_t* wb;
     float* y; uint16_t* yb; int ldy;
+    int ksplit;
+    const uint16_t* um_xn; float* um_mixed; uint16_t* um_xh; int um_d;
 };
 int launch_pf_gemm(const PfGemm& g, hipStream_t st);
 
@@ -30,9 +38,9 @@ int launch_pf_embed(const PfEmb& e, const int* toks, float* R, int D, int HC, in
 // HC read pieces (src/wzy_prefill_tc.cuh:690-715)
 int launch_pf_hc_norm(float* R, const float* bo, const float* inj_prev, const float* norm_w, uint16_t* xn, int D,
                       int HC, float eps, int B, hipStream_t st);
-int launch_pf_silu_div(const float* lo, uint16_t* loh, size_t n, float inv_hc, hipStream_t st);
-int launch_pf_up_mean(const uint16_t* xn, const uint16_t* gg, float* mixed, uint16_t* xh, int D, int HC, int B,
-                      hipStream_t st);
+// loh = bf16(silu(v)), v = lo * inv_hc; with nsplit == 4 partial sums lo[s * n + i],
+// v = ((p0 + p1) + (p2 + p3)) * inv_hc
+int launch_pf_silu_div(const float* lo, uint16_t* loh, size_t n, int nsplit, float inv_hc, hipStream_t st);
 int launch_pf_hc_write(float* R, const float* blk, const float* inj, int D, int HC, int B, hipStream_t st);
 
 // GDN (src/wzy_qsa_wmma.cuh:5-195, src/wzy_prefill_tc.cuh:54-67)
