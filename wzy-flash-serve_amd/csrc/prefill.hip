@@ -443,19 +443,39 @@ static_assert(GR_STEPS * GR_COLS <= 256, "v staging: one value per thread");
 static_assert(GR_RPL == 4, "the row loop holds 4 state rows per lane");
 static_assert(GR_STEPS == GR_LPC, "one output row per lane of a column");
 
+// k . q per (row, key head), with the recurrence's lane layout (lane r of a 32-lane half holds
+// elements 4r .. 4r+3) and its 32-lane sum: a parallel pass, so the sequential row loop below reads
+// one value per row instead of forming and reducing the product itself.  grid ceil(B * hk / 8), 256
+// threads (8 pairs per workgroup, one per 32-lane half).
+__global__ void __launch_bounds__(256) pf_gdn_kq_kernel(PfGdn g) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r8 = lane & 31;
+    const int np = g.B * g.hk, QKV = (2 * g.hk + g.hv) * 128;
+    const int p = blockIdx.x * 8 + w * 2 + (lane >> 5), pc = min(p, np - 1);
+    const int t = pc / g.hk, kh = pc - t * g.hk;
+    const float4 q4 = *(const float4*) (g.conv_out + (size_t) t * QKV + kh * 128 + r8 * GR_RPL);
+    const float4 k4 = *(const float4*) (g.conv_out + (size_t) t * QKV + (g.hk + kh) * 128 + r8 * GR_RPL);
+    float kq = k4.x * q4.x;
+    kq = fmaf(k4.y, q4.y, kq);
+    kq = fmaf(k4.z, q4.z, kq);
+    kq = fmaf(k4.w, q4.w, kq);
+    kq = sum32_pl(kq);
+    if (r8 == 0 && p < np) g.kq[p] = kq;
+}
+
 // Delta rule over the chunk's rows for one value head and GR_COLS state columns (each column of
 // the state evolves independently): per row, S *= decay; kv = S^T k; delta = (v - kv) * beta;
 // S += k delta^T; o = S^T q / sqrt(128).  grid (hv * 128 / GR_COLS), 256 threads.  A column's 128
-// rows are spread over 32 lanes (4 per lane), so a row costs a few instructions per lane and three
-// 32-lane sums (DPP within each 16-lane row, then a permlane swap); the rows' q and k (all 128 of the key head) and the columns' v go
-// through LDS 32 rows at a time, the next 32 loaded while these run.
+// rows are spread over 32 lanes (4 per lane), so a row costs a few instructions per lane and two
+// 32-lane sums (DPP within each 16-lane row, then a permlane swap); k . q comes precomputed.  The
+// rows' q and k (all 128 of the key head), the columns' v and the per-row scalars go through LDS 32
+// rows at a time, the next 32 loaded while these run.
 // (pf_gdn_recur_kh_kernel, src/wzy_qsa_wmma.cuh:56-195; fused_gdn_step_norm_multi,
 // src/wzy_kernels_v2.cuh:908-984)
 __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
     __shared__ __align__(16) float sq[2][GR_STEPS][128];
     __shared__ __align__(16) float sk[2][GR_STEPS][128];
     __shared__ float sv[2][GR_STEPS][GR_COLS];
-    __shared__ float sg[2][GR_STEPS], sb[2][GR_STEPS];
+    __shared__ float sg[2][GR_STEPS], sb[2][GR_STEPS], skq[2][GR_STEPS];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int h = blockIdx.x / (128 / GR_COLS), cb = blockIdx.x % (128 / GR_COLS);
     const int kh = h % g.hk;
@@ -467,35 +487,54 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
 #pragma unroll
     for (int i = 0; i < GR_RPL; ++i) s[i] = S[(size_t) (r8 * GR_RPL + i) * 128 + col];
 
-    // staging of rows t0 .. t0+GR_STEPS-1: q and k (128 each) of key head kh, v of the columns, gates
+    // staging of rows t0 .. t0+GR_STEPS-1: q and k (128 each) of key head kh, v of the columns, the
+    // per-row decay, beta and k . q.  Row indices are clamped (rows past the chunk are never used), so
+    // every load is unconditional.
     constexpr int QK_PER = GR_STEPS * 2 * 128 / 256;      // floats per thread (32)
     float rq[QK_PER];
     float rv = 0.f, rg = 0.f;
+    const int qk_off = (tid >= 128 ? g.hk * 128 : 0) + kh * 128 + (tid & 127);
     auto load = [&](int t0) {
 #pragma unroll
-        for (int u = 0; u < QK_PER; ++u) {
-            const int e = u * 256 + tid, step = e / 256, which = (e / 128) & 1, i = e & 127;
-            const int t = t0 + step;
-            rq[u] = t < g.B ? g.conv_out[(size_t) t * QKV + (which ? g.hk * 128 : 0) + kh * 128 + i] : 0.f;
+        for (int u = 0; u < QK_PER; ++u) rq[u] = g.conv_out[(size_t) min(t0 + u, g.B - 1) * QKV + qk_off];
+        {
+            const int step = min(tid / GR_COLS, GR_STEPS - 1), j = tid % GR_COLS, t = min(t0 + step, g.B - 1);
+            rv = g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j];
         }
         {
-            const int step = min(tid / GR_COLS, GR_STEPS - 1), j = tid % GR_COLS, t = t0 + step;
-            rv = t < g.B ? g.conv_out[(size_t) t * QKV + 2 * g.hk * 128 + h * 128 + cb * GR_COLS + j] : 0.f;
-        }
-        {
-            const int step = tid & (GR_STEPS - 1), t = t0 + step;
-            rg = (t < g.B && tid < 2 * GR_STEPS) ? (tid < GR_STEPS ? g.decay : g.beta)[(size_t) t * g.hv + h] : 0.f;
+            const int t = min(t0 + (tid & (GR_STEPS - 1)), g.B - 1);
+            const float* src = tid < GR_STEPS ? g.decay + (size_t) t * g.hv + h
+                               : tid < 2 * GR_STEPS ? g.beta + (size_t) t * g.hv + h
+                                                    : g.kq + (size_t) t * g.hk + kh;
+            rg = *src;
         }
     };
     auto store = [&](int bb) {
 #pragma unroll
-        for (int u = 0; u < QK_PER; ++u) {
-            const int e = u * 256 + tid, step = e / 256, which = (e / 128) & 1, i = e & 127;
-            (which ? sk : sq)[bb][step][i] = rq[u];
-        }
+        for (int u = 0; u < QK_PER; ++u) (tid >= 128 ? sk : sq)[bb][u][tid & 127] = rq[u];
         if (tid < GR_STEPS * GR_COLS) sv[bb][tid / GR_COLS][tid % GR_COLS] = rv;
         if (tid < GR_STEPS) sg[bb][tid] = rg;
         else if (tid < 2 * GR_STEPS) sb[bb][tid - GR_STEPS] = rg;
+        else if (tid < 3 * GR_STEPS) skq[bb][tid - 2 * GR_STEPS] = rg;
+    };
+
+    // one row of the delta rule from its operands (k . q precomputed):
+    //   kv = dec * (S^T k),  o = dec * (S^T q) + delta * (k.q)  (= (dec S + k delta^T)^T q)
+    float o_row = 0.f;                                      // lane r8 keeps row t0 + r8's output
+    auto row = [&](int st, const float4 k4, const float4 q4, float vv, float dec, float beta, float kq) {
+        float a = s[0] * k4.x, c = s[0] * q4.x;
+        a = fmaf(s[1], k4.y, a); c = fmaf(s[1], q4.y, c);
+        a = fmaf(s[2], k4.z, a); c = fmaf(s[2], q4.z, c);
+        a = fmaf(s[3], k4.w, a); c = fmaf(s[3], q4.w, c);
+        a = sum32_pl(a);
+        c = sum32_pl(c);
+        const float delta = (vv - dec * a) * beta;
+        const float o = fmaf(dec, c, delta * kq) * 0.08838834764831845f;
+        s[0] = fmaf(k4.x, delta, dec * s[0]);
+        s[1] = fmaf(k4.y, delta, dec * s[1]);
+        s[2] = fmaf(k4.z, delta, dec * s[2]);
+        s[3] = fmaf(k4.w, delta, dec * s[3]);
+        o_row = r8 == st ? o : o_row;
     };
 
     const int nblk = (g.B + GR_STEPS - 1) / GR_STEPS;
@@ -506,40 +545,28 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
         const int bb = kb & 1, t0 = kb * GR_STEPS;
         if (kb + 1 < nblk) load(t0 + GR_STEPS);
         const int n = min(GR_STEPS, g.B - t0);
-        // the operands of a row come from LDS one row ahead, so their latency hides behind the
-        // previous row's reductions
-        float4 kn = *(const float4*) &sk[bb][0][r8 * GR_RPL], qn = *(const float4*) &sq[bb][0][r8 * GR_RPL];
-        float vn = sv[bb][0][lc], gn = sg[bb][0], bn = sb[bb][0];
-        float o_row = 0.f;                                  // lane r8 keeps row t0 + r8's output
-        for (int st = 0; st < n; ++st) {
-            const float4 k4 = kn, q4 = qn;
-            const float vv = vn, dec = gn, beta = bn;
-            if (st + 1 < n) {
-                kn = *(const float4*) &sk[bb][st + 1][r8 * GR_RPL];
-                qn = *(const float4*) &sq[bb][st + 1][r8 * GR_RPL];
-                vn = sv[bb][st + 1][lc];
-                gn = sg[bb][st + 1];
-                bn = sb[bb][st + 1];
-            }
-            // S^T k and S^T q of the state before the row, and k.q, reduced together:
-            //   kv = dec * (S^T k),  o = dec * (S^T q) + delta * (k.q)  (= (dec S + k delta^T)^T q)
-            float a = s[0] * k4.x, c = s[0] * q4.x, kq = k4.x * q4.x;
-            a = fmaf(s[1], k4.y, a); c = fmaf(s[1], q4.y, c); kq = fmaf(k4.y, q4.y, kq);
-            a = fmaf(s[2], k4.z, a); c = fmaf(s[2], q4.z, c); kq = fmaf(k4.z, q4.z, kq);
-            a = fmaf(s[3], k4.w, a); c = fmaf(s[3], q4.w, c); kq = fmaf(k4.w, q4.w, kq);
-            a = sum32_pl(a);
-            c = sum32_pl(c);
-            kq = sum32_pl(kq);
-            const float delta = (vv - dec * a) * beta;
-            const float o = fmaf(dec, c, delta * kq) * 0.08838834764831845f;
-            s[0] = fmaf(k4.x, delta, dec * s[0]);
-            s[1] = fmaf(k4.y, delta, dec * s[1]);
-            s[2] = fmaf(k4.z, delta, dec * s[2]);
-            s[3] = fmaf(k4.w, delta, dec * s[3]);
-            o_row = r8 == st ? o : o_row;
+        // operands come from LDS one row ahead, alternating between two register sets (rows st and
+        // st + 1), so their latency hides behind the previous row and no copies are needed
+        float4 kA = *(const float4*) &sk[bb][0][r8 * GR_RPL], qA = *(const float4*) &sq[bb][0][r8 * GR_RPL];
+        float vA = sv[bb][0][lc], gA = sg[bb][0], bA = sb[bb][0], kqA = skq[bb][0];
+        float4 kB, qB;
+        float vB, gB, bB, kqB;
+        for (int st = 0; st < n; st += 2) {
+            const int s1 = min(st + 1, GR_STEPS - 1), s2 = min(st + 2, GR_STEPS - 1);
+            kB = *(const float4*) &sk[bb][s1][r8 * GR_RPL];
+            qB = *(const float4*) &sq[bb][s1][r8 * GR_RPL];
+            vB = sv[bb][s1][lc]; gB = sg[bb][s1]; bB = sb[bb][s1]; kqB = skq[bb][s1];
+            row(st, kA, qA, vA, gA, bA, kqA);
+            if (st + 1 >= n) break;                          // workgroup-uniform
+            kA = *(const float4*) &sk[bb][s2][r8 * GR_RPL];
+            qA = *(const float4*) &sq[bb][s2][r8 * GR_RPL];
+            vA = sv[bb][s2][lc]; gA = sg[bb][s2]; bA = sb[bb][s2]; kqA = skq[bb][s2];
+            row(st + 1, kB, qB, vB, gB, bB, kqB);
         }
-        if (r8 < n) g.o[(size_t) (t0 + r8) * GV + h * 128 + col] = o_row;
+        // the refill first: it waits for this buffer's loads, long arrived; the output store after it
+        // is then waited on by nothing before the next buffer's rows
         if (kb + 1 < nblk) store(bb ^ 1);
+        if (r8 < n) g.o[(size_t) (t0 + r8) * GV + h * 128 + col] = o_row;
         __syncthreads();
     }
 #pragma unroll
@@ -1034,6 +1061,7 @@ int launch_pf_gdn(const PfGdn& g, hipStream_t st) {
     hipLaunchKernelGGL(pf_gdn_ab_kernel, dim3((g.B * g.hv + 255) / 256), dim3(256), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_conv_kernel, dim3(QKV / 128, g.B), dim3(128), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_hist_kernel, dim3((QKV + 255) / 256), dim3(256), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_kq_kernel, dim3((g.B * g.hk + 7) / 8), dim3(256), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_recur_kernel, dim3(g.hv * 128 / GR_COLS), dim3(256), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_norm_kernel, dim3(g.hv, g.B), dim3(128), 0, st, g);
     WZY_LAUNCH_CHECK();

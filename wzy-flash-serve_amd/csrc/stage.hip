@@ -213,7 +213,7 @@ struct wzy_stage {
         float *R = nullptr, *lo = nullptr, *inj_a = nullptr, *inj_f = nullptr, *mixed = nullptr;
         uint16_t *xn = nullptr, *loh = nullptr, *xh = nullptr;
         float *qkv = nullptr, *z = nullptr, *ab = nullptr, *conv_out = nullptr, *decay = nullptr, *beta = nullptr,
-              *o = nullptr;
+              *kq = nullptr, *o = nullptr;
         float *qg = nullptr, *kk = nullptr, *vv = nullptr, *idx_raw = nullptr, *q_idx = nullptr, *scores = nullptr;
         int *sel = nullptr, *cnt = nullptr;
         float *block = nullptr, *comb = nullptr;
@@ -1441,6 +1441,7 @@ int wzy_stage::prefill_reserve(int B) {
     const size_t umark = off;
     const size_t oqkv = bump(b * QKV * 4), oz = bump(b * GV * 4), oab = bump(b * 2 * c.gdn_hv * 4),
                  oco = bump(b * QKV * 4), odec = bump(b * c.gdn_hv * 4), obet = bump(b * c.gdn_hv * 4),
+                 okq = bump(b * c.gdn_hk * 4),
                  oo = bump(b * GV * 4);
     const size_t gdn_end = off;
     off = umark;
@@ -1468,6 +1469,7 @@ int wzy_stage::prefill_reserve(int B) {
     pf.pos8 = (int*) (u + opos);
     pf.qkv = (float*) (u + oqkv); pf.z = (float*) (u + oz); pf.ab = (float*) (u + oab);
     pf.conv_out = (float*) (u + oco); pf.decay = (float*) (u + odec); pf.beta = (float*) (u + obet);
+    pf.kq = (float*) (u + okq);
     pf.o = (float*) (u + oo);
     pf.qg = (float*) (u + oqg); pf.kk = (float*) (u + okk); pf.vv = (float*) (u + ovv);
     pf.idx_raw = (float*) (u + oir); pf.q_idx = (float*) (u + oqi); pf.scores = (float*) (u + osc);
@@ -1568,7 +1570,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
             g.hk = c.gdn_hk; g.hv = hv; g.B = B; g.eps = c.eps;
             g.qkv = pf.qkv; g.z = pf.z; g.ab = pf.ab; g.dt = w.dt; g.ssm_a = w.ssm_a; g.conv_w = w.conv_w;
             g.gamma = w.ssm_norm; g.conv_hist = w.conv_hist; g.state = w.ssm; g.conv_out = pf.conv_out;
-            g.decay = pf.decay; g.beta = pf.beta; g.o = pf.o; g.y = pf.xh;
+            g.decay = pf.decay; g.beta = pf.beta; g.kq = pf.kq; g.o = pf.o; g.y = pf.xh;
             WZY_TRY(launch_pf_gdn(g, st));
             WZY_TRY(gemm(pf.xh, GV, GV, &w.wout, nullptr, D, pf.block, nullptr, D));
         } else {

@@ -55,6 +55,7 @@ struct PfGdn {
     float* state;                           // [hv][128][128]
     float* conv_out;                        // [B][QKV] scratch
     float* decay; float* beta;              // [B][hv] scratch
+    float* kq;                              // [B][hk] scratch: k . q per row and key head
     float* o;                               // [B][hv*128] scratch
     uint16_t* y;                            // [B][hv*128] bf16 output (gated RMS norm)
 };
