@@ -475,7 +475,7 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
     __shared__ __align__(16) float sq[2][GR_STEPS][128];
     __shared__ __align__(16) float sk[2][GR_STEPS][128];
     __shared__ float sv[2][GR_STEPS][GR_COLS];
-    __shared__ float sg[2][GR_STEPS], sb[2][GR_STEPS], skq[2][GR_STEPS];
+    __shared__ float4 sgb[2][GR_STEPS];                         // per row: decay, beta, k . q, unused
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int h = blockIdx.x / (128 / GR_COLS), cb = blockIdx.x % (128 / GR_COLS);
     const int kh = h % g.hk;
@@ -513,15 +513,14 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
 #pragma unroll
         for (int u = 0; u < QK_PER; ++u) (tid >= 128 ? sk : sq)[bb][u][tid & 127] = rq[u];
         if (tid < GR_STEPS * GR_COLS) sv[bb][tid / GR_COLS][tid % GR_COLS] = rv;
-        if (tid < GR_STEPS) sg[bb][tid] = rg;
-        else if (tid < 2 * GR_STEPS) sb[bb][tid - GR_STEPS] = rg;
-        else if (tid < 3 * GR_STEPS) skq[bb][tid - 2 * GR_STEPS] = rg;
+        if (tid < 3 * GR_STEPS) ((float*) &sgb[bb][tid & (GR_STEPS - 1)])[tid / GR_STEPS] = rg;
     };
 
     // one row of the delta rule from its operands (k . q precomputed):
     //   kv = dec * (S^T k),  o = dec * (S^T q) + delta * (k.q)  (= (dec S + k delta^T)^T q)
     float o_row = 0.f;                                      // lane r8 keeps row t0 + r8's output
-    auto row = [&](int st, const float4 k4, const float4 q4, float vv, float dec, float beta, float kq) {
+    auto row = [&](int st, const float4 k4, const float4 q4, float vv, const float4 gbk) {
+        const float dec = gbk.x, beta = gbk.y, kq = gbk.z;
         float a = s[0] * k4.x, c = s[0] * q4.x;
         a = fmaf(s[1], k4.y, a); c = fmaf(s[1], q4.y, c);
         a = fmaf(s[2], k4.z, a); c = fmaf(s[2], q4.z, c);
@@ -546,22 +545,32 @@ __global__ void __launch_bounds__(256) pf_gdn_recur_kernel(PfGdn g) {
         if (kb + 1 < nblk) load(t0 + GR_STEPS);
         const int n = min(GR_STEPS, g.B - t0);
         // operands come from LDS one row ahead, alternating between two register sets (rows st and
-        // st + 1), so their latency hides behind the previous row and no copies are needed
+        // st + 1), so their latency hides behind the previous row and no copies are needed.  The loop
+        // is unrolled over the whole buffer: every LDS address is a constant offset.
         float4 kA = *(const float4*) &sk[bb][0][r8 * GR_RPL], qA = *(const float4*) &sq[bb][0][r8 * GR_RPL];
-        float vA = sv[bb][0][lc], gA = sg[bb][0], bA = sb[bb][0], kqA = skq[bb][0];
-        float4 kB, qB;
-        float vB, gB, bB, kqB;
-        for (int st = 0; st < n; st += 2) {
+        float vA = sv[bb][0][lc];
+        float4 pA = sgb[bb][0];
+        float4 kB, qB, pB;
+        float vB;
+        auto pair = [&](int st) {                            // rows st (set A) and st + 1 (set B)
             const int s1 = min(st + 1, GR_STEPS - 1), s2 = min(st + 2, GR_STEPS - 1);
             kB = *(const float4*) &sk[bb][s1][r8 * GR_RPL];
             qB = *(const float4*) &sq[bb][s1][r8 * GR_RPL];
-            vB = sv[bb][s1][lc]; gB = sg[bb][s1]; bB = sb[bb][s1]; kqB = skq[bb][s1];
-            row(st, kA, qA, vA, gA, bA, kqA);
-            if (st + 1 >= n) break;                          // workgroup-uniform
+            vB = sv[bb][s1][lc];
+            pB = sgb[bb][s1];
+            row(st, kA, qA, vA, pA);
+            if (st + 1 >= n) return;                         // workgroup-uniform
             kA = *(const float4*) &sk[bb][s2][r8 * GR_RPL];
             qA = *(const float4*) &sq[bb][s2][r8 * GR_RPL];
-            vA = sv[bb][s2][lc]; gA = sg[bb][s2]; bA = sb[bb][s2]; kqA = skq[bb][s2];
-            row(st + 1, kB, qB, vB, gB, bB, kqB);
+            vA = sv[bb][s2][lc];
+            pA = sgb[bb][s2];
+            row(st + 1, kB, qB, vB, pB);
+        };
+        if (n == GR_STEPS) {
+#pragma unroll
+            for (int st = 0; st < GR_STEPS; st += 2) pair(st);
+        } else {
+            for (int st = 0; st < n; st += 2) pair(st);
         }
         // the refill first: it waits for this buffer's loads, long arrived; the output store after it
         // is then waited on by nothing before the next buffer's rows
