@@ -65,10 +65,15 @@ WZY_DEV void q8_block_bf16(uint4 c0, uint4 c1, float sc, uint4& o0, uint4& o1, u
 // UM: the HC up projection with the stream mean as its epilogue.  Tile column n holds stream
 // c = n % 4 of position d = n / 4 (weight row c * um_d + d), so a row's four stream gates sit in
 // one lane quad and are combined there in stream order.
-template <bool UM>
-__global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
-    __shared__ __align__(16) uint16_t sA[2][GM][GLD];
-    __shared__ __align__(16) uint16_t sW[2][GN][GLD];
+// SB: one LDS buffer (37 KB), so four workgroups share a CU (three with the UM epilogue, whose
+// registers allow no more); the next k step still loads into
+// registers during the MFMAs, and a second barrier per step guards the buffer.  Launches with at
+// least 512 tiles use it; smaller ones keep two buffers (74 KB, two workgroups per CU).
+template <bool UM, bool SB>
+__global__ void __launch_bounds__(256, SB ? (UM ? 3 : 4) : 2) pf_gemm_kernel(GemmArgs ga) {
+    constexpr int NBUF = SB ? 1 : 2;
+    __shared__ __align__(16) uint16_t sA[NBUF][GM][GLD];
+    __shared__ __align__(16) uint16_t sW[NBUF][GN][GLD];
     const PfGemm& g = ga.g;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
     const int tiles = ga.mt * ga.nt;
@@ -141,7 +146,7 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
     PF_GEMM_STORE(0);
     __syncthreads();
     for (int ks = 0; ks < nk; ++ks) {
-        const int buf = ks & 1;
+        const int buf = SB ? 0 : (ks & 1);
         const bool more = ks + 1 < nk;
         if (more) PF_GEMM_LOAD(ks + 1);                            // next step's loads in flight
 #pragma unroll
@@ -158,7 +163,12 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
-        if (more) PF_GEMM_STORE(buf ^ 1);
+        if constexpr (SB) {
+            __syncthreads();                                       // every wave is done with the buffer
+            if (more) PF_GEMM_STORE(0);
+        } else {
+            if (more) PF_GEMM_STORE(buf ^ 1);
+        }
         __syncthreads();
     }
 #undef PF_GEMM_LOAD
@@ -166,30 +176,24 @@ __global__ void __launch_bounds__(256, 2) pf_gemm_kernel(GemmArgs ga) {
     // acc[i][j][r] = C[row 8*(r/4) + 4*(lane/32) + r%4][col lane%32] of block (i, j)
     if constexpr (UM) {
         // mixed = (sum over streams in order of xn / (1 + exp(-bf16 gate))) / 4, fp32 and bf16
-        // (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252); the xn loads of all four blocks go first
+        // (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252); the xn loads of a 32 x 32 block go first
         const int D = g.um_d, c = lane & 3;
-        float xv[2][2][16];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int d = (n0 + wn * 64 + j * 32 + (lane & 31)) >> 2;
+                float xv[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = min(m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), g.M - 1);
-                    xv[i][j][r] = bf16_to_f(g.um_xn[(size_t) row * 4 * D + (size_t) c * D + d]);
+                    xv[r] = bf16_to_f(g.um_xn[(size_t) row * 4 * D + (size_t) c * D + d]);
                 }
-            }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int d = (n0 + wn * 64 + j * 32 + (lane & 31)) >> 2;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                     const float gq = bf16_to_f(f_to_bf16(acc[i][j][r]));
-                    const float term = xv[i][j][r] / (1.0f + __expf(-gq));
+                    const float term = xv[r] / (1.0f + __expf(-gq));
                     float sum = 0.f + dpp_f<0x00>(term);             // quad lanes 0..3 = streams 0..3
                     sum += dpp_f<0x55>(term);
                     sum += dpp_f<0xAA>(term);
@@ -1024,8 +1028,12 @@ int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
     ga.mt = (g.M + GM - 1) / GM;
     ga.nt = (g.N + GN - 1) / GN;
     WZY_REQUIRE((long long) ga.mt * ga.nt * ksplit < (1LL << 31), "pf_gemm: too many tiles");
-    if (um) hipLaunchKernelGGL(pf_gemm_kernel<true>, dim3(ga.mt * ga.nt), dim3(256), 0, st, ga);
-    else hipLaunchKernelGGL(pf_gemm_kernel<false>, dim3(ga.mt * ga.nt * ksplit), dim3(256), 0, st, ga);
+    const int grid = ga.mt * ga.nt * (um ? 1 : ksplit);
+    const bool sb = grid >= 512;
+    if (um && sb) hipLaunchKernelGGL((pf_gemm_kernel<true, true>), dim3(grid), dim3(256), 0, st, ga);
+    else if (um) hipLaunchKernelGGL((pf_gemm_kernel<true, false>), dim3(grid), dim3(256), 0, st, ga);
+    else if (sb) hipLaunchKernelGGL((pf_gemm_kernel<false, true>), dim3(grid), dim3(256), 0, st, ga);
+    else hipLaunchKernelGGL((pf_gemm_kernel<false, false>), dim3(grid), dim3(256), 0, st, ga);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
