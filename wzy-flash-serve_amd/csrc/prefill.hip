@@ -800,9 +800,13 @@ constexpr int AT_VLD = AT_C + 8;
 
 WZY_DEV f16x4_t h4_from(const _Float16* p) { return *(const f16x4_t*) p; }
 
-__global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
-    __shared__ __align__(16) _Float16 sK[AT_C][AT_QLD];
-    __shared__ __align__(16) _Float16 sVt[256][AT_VLD];
+__global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
+    // K of a step and then its V^T share one region (37 KB instead of 70), so three workgroups fit a
+    // CU: the scores read K, V is staged after every wave is done with K, P.V reads V^T.
+    __shared__ __align__(16) _Float16 sU[256 * AT_VLD];
+    _Float16 (*const sK)[AT_QLD] = (_Float16 (*)[AT_QLD]) sU;
+    _Float16 (*const sVt)[AT_VLD] = (_Float16 (*)[AT_VLD]) sU;
+    static_assert(AT_C * AT_QLD <= 256 * AT_VLD, "K fits the shared region");
     __shared__ __align__(16) _Float16 sP[2][16][AT_B + 8];
     __shared__ float sS[16][AT_C + 1];
     __shared__ float s_m[16], s_l[16], s_al[2][16];
@@ -842,7 +846,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
     auto store_ids = [&](int slot) {
         if (tid < AT_C) sIds[slot][tid] = rid;
     };
-    auto load = [&](int base, int slot) {
+    auto load_k = [&](int base, int slot) {
         const int cnt = min(AT_C, width - base);
         {
             const bool ok = kc < cnt;
@@ -852,6 +856,9 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
             for (int u = 0; u < 4; ++u) kq[u] = ok ? *(const uint4*) (kp + 16 * u) : make_uint4(0, 0, 0, 0);
             ksc = ok ? a.kv.ks[p * (kvd / 64) + (size_t) j * scg + kd0 / 64] : (uint16_t) 0;
         }
+    };
+    auto load_v = [&](int base, int slot) {
+        const int cnt = min(AT_C, width - base);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const bool ok = vc0 + u < cnt;
@@ -860,7 +867,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
             vsc[u] = ok ? a.kv.vs[p * (kvd / 64) + (size_t) j * scg + vd0 / 64] : (uint16_t) 0;
         }
     };
-    auto store = [&]() {
+    auto store_k = [&]() {
         const _Float16 s = __builtin_bit_cast(_Float16, ksc);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -873,6 +880,8 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
                 *(f16x4_t*) &sK[kc][kd0 + 16 * u + 4 * i] = v;
             }
         }
+    };
+    auto store_v = [&]() {
         _Float16 vs[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) vs[u] = __builtin_bit_cast(_Float16, vsc[u]);
@@ -897,15 +906,20 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
         store_ids(0);
     }
     __syncthreads();
-    if (width > 0) load(0, 0);
+    if (width > 0) {
+        load_k(0, 0);
+        load_v(0, 0);
+    }
     if (AT_C < width) load_ids(AT_C);
-    if (width > 0) store();
+    if (width > 0) store_k();
     if (AT_C < width) store_ids(1);
     __syncthreads();
+    // per step: the next step's K loads go out first; V of this step (in registers since the middle
+    // of the previous step) is staged once the scores are done, and the next step's V loads follow
     for (int base = 0, stp = 0; base < width; base += AT_C, ++stp) {
         const int cnt = min(AT_C, width - base);
         const bool more = base + AT_C < width, more2 = base + 2 * AT_C < width;
-        if (more) load(base + AT_C, (stp + 1) & 1);
+        if (more) load_k(base + AT_C, (stp + 1) & 1);
         if (more2) load_ids(base + 2 * AT_C);
         // scores: wave w -> cells 16w .. 16w+15, dims 0-127 and 128-255 as separate chains
         if (16 * w < cnt) {
@@ -921,6 +935,8 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
             for (int i = 0; i < 4; ++i) sS[4 * kq4 + i][16 * w + l16] = sc0[i] + sc1[i];
         }
         __syncthreads();
+        store_v();                                   // K is no longer read: V^T takes the region
+        if (more) load_v(base + AT_C, (stp + 1) & 1);
         // online softmax, two 32-cell blocks in order: wave w -> heads 4w .. 4w+3, two per pass
         // (lane halves), lane = cell of the block
 #pragma unroll
@@ -970,7 +986,7 @@ __global__ void __launch_bounds__(256) pf_attn_kernel(PfAttn a) {
             }
         }
         __syncthreads();
-        if (more) store();
+        if (more) store_k();
         if (more2) store_ids(stp & 1);
         __syncthreads();
     }
