@@ -392,21 +392,38 @@ __global__ void __launch_bounds__(256) pf_gdn_ab_kernel(PfGdn g) {
 
 // causal depthwise conv (3 history taps + the row) + SiLU, L2 norm of each q / k head; grid
 // (QKV/128, B), 128 threads  (pf_gdn_conv_parallel, src/wzy_qsa_wmma.cuh:5-30)
+// A thread runs CV_ROWS consecutive rows of its channel with a sliding window in registers, so every
+// raw row is read once; the q / k rows' L2 norms span the workgroup's 128 channels (one head).
+constexpr int CV_ROWS = 16;
 __global__ void __launch_bounds__(128) pf_gdn_conv_kernel(PfGdn g) {
-    __shared__ float s_red[2];
-    const int grp = blockIdx.x, t = blockIdx.y, ch = grp * 128 + threadIdx.x;
+    __shared__ float s_red[2][2];                  // per row parity: one barrier per row
+    const int grp = blockIdx.x, t0 = blockIdx.y * CV_ROWS, ch = grp * 128 + threadIdx.x, w = threadIdx.x >> 6;
     const int QKV = (2 * g.hk + g.hv) * 128;
     const float* h = g.conv_hist + (size_t) ch * 3;
-    auto in = [&](int s) { return s >= 0 ? g.qkv[(size_t) s * QKV + ch] : h[3 + s]; };   // row s (s < 0: history)
-    const float v0 = in(t - 3), v1 = in(t - 2), v2 = in(t - 1), vx = g.qkv[(size_t) t * QKV + ch];
-    const float* w = g.conv_w + (size_t) ch * 4;
-    const float sum = v0 * w[0] + v1 * w[1] + v2 * w[2] + vx * w[3];
-    float y = sum / (1.0f + __expf(-sum));
-    if (grp < 2 * g.hk) {
-        const float ss = block_sum<2>(y * y, s_red);
-        y *= 1.0f / sqrtf(ss + g.eps);
+    float win[CV_ROWS + 3];                        // rows t0-3 .. t0+CV_ROWS-1 (s < 0: history)
+#pragma unroll
+    for (int i = 0; i < CV_ROWS + 3; ++i) {
+        const int s = t0 - 3 + i;
+        win[i] = s < 0 ? h[3 + s] : g.qkv[(size_t) min(s, g.B - 1) * QKV + ch];
     }
-    g.conv_out[(size_t) t * QKV + ch] = y;
+    const float* wp = g.conv_w + (size_t) ch * 4;
+    const float w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3];
+    const bool qk = grp < 2 * g.hk;                // workgroup-uniform
+#pragma unroll
+    for (int r = 0; r < CV_ROWS; ++r) {
+        const int t = t0 + r;
+        if (t >= g.B) break;                       // workgroup-uniform
+        const float sum = win[r] * w0 + win[r + 1] * w1 + win[r + 2] * w2 + win[r + 3] * w3;
+        float y = sum / (1.0f + __expf(-sum));
+        if (qk) {
+            const float ws = wave_sum(y * y);
+            if ((threadIdx.x & 63) == 0) s_red[r & 1][w] = ws;
+            __syncthreads();
+            const float ss = 0.f + s_red[r & 1][0] + s_red[r & 1][1];
+            y *= 1.0f / sqrtf(ss + g.eps);
+        }
+        g.conv_out[(size_t) t * QKV + ch] = y;
+    }
 }
 
 // conv history <- the last three raw rows (the older history where the chunk is shorter)
@@ -1092,7 +1109,7 @@ int launch_pf_gdn(const PfGdn& g, hipStream_t st) {
     WZY_REQUIRE(g.hk >= 1 && g.hv % g.hk == 0 && g.B >= 1, "pf_gdn: bad heads / rows");
     const int QKV = (2 * g.hk + g.hv) * 128;
     hipLaunchKernelGGL(pf_gdn_ab_kernel, dim3((g.B * g.hv + 255) / 256), dim3(256), 0, st, g);
-    hipLaunchKernelGGL(pf_gdn_conv_kernel, dim3(QKV / 128, g.B), dim3(128), 0, st, g);
+    hipLaunchKernelGGL(pf_gdn_conv_kernel, dim3(QKV / 128, (g.B + CV_ROWS - 1) / CV_ROWS), dim3(128), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_hist_kernel, dim3((QKV + 255) / 256), dim3(256), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_kq_kernel, dim3((g.B * g.hk + 7) / 8), dim3(256), 0, st, g);
     hipLaunchKernelGGL(pf_gdn_recur_kernel, dim3(g.hv * 128 / GR_COLS), dim3(256), 0, st, g);
