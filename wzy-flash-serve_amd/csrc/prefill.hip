@@ -72,8 +72,11 @@ WZY_DEV void q8_block_bf16(uint4 c0, uint4 c1, float sc, uint4& o0, uint4& o1, u
 template <bool UM, bool SB>
 __global__ void __launch_bounds__(256, SB ? (UM ? 3 : 4) : 2) pf_gemm_kernel(GemmArgs ga) {
     constexpr int NBUF = SB ? 1 : 2;
-    __shared__ __align__(16) uint16_t sA[NBUF][GM][GLD];
-    __shared__ __align__(16) uint16_t sW[NBUF][GN][GLD];
+    __shared__ __align__(16) uint16_t sAW[NBUF * (GM + GN) * GLD];
+    uint16_t (*const sA)[GM][GLD] = (uint16_t (*)[GM][GLD]) sAW;
+    uint16_t (*const sW)[GN][GLD] = (uint16_t (*)[GN][GLD]) (sAW + NBUF * GM * GLD);
+    constexpr int XS_LD = GN + 8;                                  // UM epilogue: xn tile row stride
+    static_assert(GM * XS_LD <= NBUF * (GM + GN) * GLD, "the UM epilogue's xn tile fits the GEMM's LDS");
     const PfGemm& g = ga.g;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
     const int tiles = ga.mt * ga.nt;
@@ -177,7 +180,17 @@ __global__ void __launch_bounds__(256, SB ? (UM ? 3 : 4) : 2) pf_gemm_kernel(Gem
     if constexpr (UM) {
         // mixed = (sum over streams in order of xn / (1 + exp(-bf16 gate))) / 4, fp32 and bf16
         // (pf_gr_up_mean_fp16, src/wzy_qsa_wmma.cuh:236-252); the xn loads of a 32 x 32 block go first
-        const int D = g.um_d, c = lane & 3;
+        // The tile's xn (GM rows x 4 streams x GN/4 positions, bf16) is staged in the GEMM's LDS, whose
+        // last use ended at the loop's final barrier: 16-byte coalesced loads instead of 2-byte ones.
+        const int D = g.um_d, c = lane & 3, d0 = n0 >> 2;
+        uint16_t (*const xs)[XS_LD] = (uint16_t (*)[XS_LD]) sAW;     // [row][stream * GN/4 + position]
+#pragma unroll
+        for (int i = 0; i < GM * 4 * (GN / 4) / 8 / 256; ++i) {
+            const int pc = tid + 256 * i, rr = pc >> 4, sc = (pc >> 2) & 3, q = pc & 3;
+            const int row = min(m0 + rr, g.M - 1);
+            *(uint4*) &xs[rr][sc * (GN / 4) + 8 * q] = *(const uint4*) (g.um_xn + (size_t) row * 4 * D + (size_t) sc * D + d0 + 8 * q);
+        }
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -186,8 +199,8 @@ __global__ void __launch_bounds__(256, SB ? (UM ? 3 : 4) : 2) pf_gemm_kernel(Gem
                 float xv[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int row = min(m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), g.M - 1);
-                    xv[r] = bf16_to_f(g.um_xn[(size_t) row * 4 * D + (size_t) c * D + d]);
+                    const int rr = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    xv[r] = bf16_to_f(xs[rr][c * (GN / 4) + d - d0]);
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
