@@ -726,7 +726,7 @@ __global__ void __launch_bounds__(128) pf_idx_tail_kernel(PfIdxAppend a, int p0,
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 constexpr int PS_ROWS = 32, PS_BLOCKS = 256;
 
-__global__ void __launch_bounds__(256) pf_score_kernel(QsaScoreArgs a) {
+__global__ void __launch_bounds__(256, 3) pf_score_kernel(QsaScoreArgs a) {
     __shared__ __align__(16) _Float16 sQ[4][PS_ROWS][128 + 8];
     const QsaDims& dm = a.dm;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -752,44 +752,37 @@ __global__ void __launch_bounds__(256) pf_score_kernel(QsaScoreArgs a) {
     __syncthreads();
 
     if (b0 + 64 * w < b_lim) {
-        f32x16_t acc[2][4];
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int h = 0; h < 4; ++h)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[c][h][i] = 0.f;
+        // one 32-block tile at a time: 64 accumulator registers, so several workgroups share a CU
         const int kb = (lane >> 5) * 8;
-        const _Float16* kp[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int b = min(b0 + 64 * w + 32 * c + (lane & 31), b_lim - 1);
-            kp[c] = (const _Float16*) a.pooled + (size_t) b * 128 + kb;
-        }
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            f16x8_t bv[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) bv[c] = *(const f16x8_t*) (kp[c] + 16 * ks);
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                if (h >= IH) break;                      // uniform
-                const f16x8_t av = *(const f16x8_t*) &sQ[h][lane & 31][16 * ks + kb];
-#pragma unroll
-                for (int c = 0; c < 2; ++c) acc[c][h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[c], acc[c][h], 0, 0, 0);
-            }
-        }
-        // acc[c][h][i] = q_h[row 8*(i/4) + 4*(lane/32) + i%4] . key[block 32c + lane%32]
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int b = b0 + 64 * w + 32 * c + (lane & 31);
+            const _Float16* kp = (const _Float16*) a.pooled + (size_t) min(b, b_lim - 1) * 128 + kb;
+            f32x16_t acc[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[h][i] = 0.f;
+            f16x8_t bv[8];
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) bv[ks] = *(const f16x8_t*) (kp + 16 * ks);
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    if (h >= IH) break;                  // uniform
+                    const f16x8_t av = *(const f16x8_t*) &sQ[h][lane & 31][16 * ks + kb];
+                    acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv[ks], acc[h], 0, 0, 0);
+                }
+            }
+            // acc[h][i] = q_h[row 8*(i/4) + 4*(lane/32) + i%4] . key[block 32c + lane%32]
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int t = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
                 float sc = 0.f;
 #pragma unroll
                 for (int h = 0; h < 4; ++h)
-                    if (h < IH) sc += acc[c][h][i] > 0.f ? acc[c][h][i] : 0.f;
+                    if (h < IH) sc += acc[h][i] > 0.f ? acc[h][i] : 0.f;
                 const int n_kv = base + t + 1;
                 if (t < nrows && n_kv > dm.topk && b < n_kv / B) scores[(size_t) t * a.max_b + b] = sc;
             }
