@@ -24,6 +24,7 @@ Beside the tok/s line it reports
                 HBM bytes / event-timed duration against 8 TB/s);
   gdn_config2, qsa_262k   BASELINE configs 2 and 3 at their own workloads.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --profile {step,window,mtp} [--profile-units N]   (units for a rocprofv3 run)
 """
 import argparse
 import ctypes as C
@@ -412,37 +413,68 @@ def cpu_baseline(wz, seconds):
     blobs = [np.empty(nb, np.uint8) for _ in range(E)]
     for e in set(ids.tolist()):
         wz.wzy_synth_expert_blob(seed, layer, e, D, F, blobs[e].ctypes.data)
-    arr = (C.c_void_p * E)(*[b.ctypes.data for b in blobs])
+    # The GPU's timing burst cycles through 48 layers' experts so that no cache holds them; the CPU
+    # leg does the same with n_copies distinct host copies of the 10 routed experts (the same bytes
+    # at different addresses, 1.1 GB in all, beyond any host's last-level cache), one copy per call.
+    # The same call on one copy, whose 17.7 MB stay cache-resident, is reported beside it.
+    n_copies = 64
+    copies = [[blobs[e] if c == 0 else blobs[e].copy() for e in range(E) if e in set(ids.tolist())]
+              for c in range(n_copies)]
+    arrs = []
+    for c in range(n_copies):
+        ptrs = [0] * E
+        for e, b in zip(sorted(set(ids.tolist())), copies[c]):
+            ptrs[e] = b.ctypes.data
+        arrs.append((C.c_void_p * E)(*ptrs))
     out = np.empty(D, np.float32)
     n = cpu_threads()
     pool = orc.orc_cpu_pool_create(n, D, F)
     if not pool:
         return None
-    try:
-        args = (pool, C.cast(arr, C.c_void_p).value, ids.ctypes.data, wts.ctypes.data, 1, K, q16.ctypes.data,
-                s16.ctypes.data, out.ctypes.data)
-        for _ in range(20):
-            orc.orc_cpu_pool_run(*args)
+
+    def run(arr):
+        return orc.orc_cpu_pool_run(pool, C.cast(arr, C.c_void_p).value, ids.ctypes.data, wts.ctypes.data, 1, K,
+                                    q16.ctypes.data, s16.ctypes.data, out.ctypes.data)
+
+    def timed(secs, rotate):
         times = []
-        t_end = time.perf_counter() + seconds
+        i = 0
+        t_end = time.perf_counter() + secs
         while time.perf_counter() < t_end:
             t0 = time.perf_counter()
             for _ in range(10):
-                orc.orc_cpu_pool_run(*args)
+                run(arrs[i % n_copies] if rotate else arrs[0])
+                i += 1
             times.append((time.perf_counter() - t0) / 10)
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    try:
+        for c in range(n_copies):
+            run(arrs[c])
+        med, n_rot = timed(seconds * 0.75, True)
+        med_llc, n_llc = timed(seconds * 0.25, False)
     finally:
         orc.orc_cpu_pool_destroy(pool)
-    times.sort()
-    med = times[len(times) // 2]
+    try:
+        host_cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        host_cores = os.cpu_count() or 1
     return {
         "value": round(ROUTED_BYTES / med / 1e9, 2),
         "unit": "GB/s (NVFP4 MoE, routed experts, 1 token-layer)",
         "cores": n,
+        "host_cores": host_cores,
         "cpu_model": cpu_model(),
         "kind": "port",
         "us_per_token_layer": round(med * 1e6, 1),
-        "sample": "config 1 (seed 0, 1 token, top-10 of 512, D=2048 F=512), %d x 10 calls over %.0f s, median" % (
-            len(times), seconds),
+        "llc_resident": {"value": round(ROUTED_BYTES / med_llc / 1e9, 2), "us_per_token_layer": round(med_llc * 1e6, 1),
+                         "sample": "the same call on one copy of the 10 experts (17.7 MB, cache-resident), "
+                                   "%d x 10 calls, median" % n_llc},
+        "sample": "config 1 (seed 0, 1 token, top-10 of 512, D=2048 F=512) on %d threads of %d host cores, "
+                  "cycling through %d host copies of the routed experts (%.2f GB, not cache-resident) like the "
+                  "GPU burst cycles through 48 layers; %d x 10 calls over %.1f s, median" % (
+                      n, host_cores, n_copies, n_copies * ROUTED_BYTES / 1e9, n_rot, seconds * 0.75),
     }
 
 
@@ -459,6 +491,46 @@ def pmc_traffic(kernel_prefix):
     except OSError:
         return None
     return None
+
+
+def profile_units(wz, mode, n, n_ctx, graphs, warmup=2):
+    """Run the config-4 stage in one mode for a kernel trace or counter run, then return:
+      step    n single-token decode steps at the prefilled context
+      window  n T=4 verify windows (snapshots on), each followed by the commit of row 0 (a window whose
+              drafts are all rejected)
+      mtp     n drafter steps (114,452-row draft head) after one decode step
+    Kernels are launched directly unless `graphs`; each unit prints its wall time so that a trace can
+    be cut per unit."""
+    import numpy as np
+    import wzy_amd
+    cfg = wzy_amd.default_cfg(n_ctx + 8 * (n + warmup) + 64)
+    st = wzy_amd.Stage(cfg)
+    wz.wzy_stage_set_graphs(st.h, 1 if graphs else 0)
+    st.load_synthetic(3, n_ctx)
+    rng = np.random.default_rng(1)
+    pos = n_ctx
+    if mode == "mtp":
+        st.mtp_init(4, 114452)
+        st.forward(pos, [5])
+        st.sync()
+    for i in range(warmup + n):
+        t0 = time.perf_counter()
+        if mode == "step":
+            st.forward(pos, [int(rng.integers(0, cfg.n_vocab))])
+            st.sync()
+            pos += 1
+        elif mode == "window":
+            st.forward(pos, [int(x) for x in rng.integers(0, cfg.n_vocab, 4)], save_snaps=True)
+            st.sync()
+            st.lib.wzy_stage_commit_window_state(st.h, 0, pos)
+            st.sync()
+            pos += 1
+        else:
+            st.mtp_draft(pos, 7, 0, 1)
+        print("%s %d %.3f ms%s" % (mode, i, 1000 * (time.perf_counter() - t0), " (warm-up)" if i < warmup else ""),
+              flush=True)
+    st.close()
+    print("done", flush=True)
 
 
 def main():
@@ -482,6 +554,11 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the run, 3 device-to-device copies of this many MiB (the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counts)")
+    ap.add_argument("--profile", choices=("step", "window", "mtp"), default=None,
+                    help="instead of the benchmark, run --profile-units units of one mode for rocprofv3 "
+                         "(direct kernel launches unless --profile-graphs)")
+    ap.add_argument("--profile-units", type=int, default=8)
+    ap.add_argument("--profile-graphs", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU (all 512x48 experts resident in one MI355X's HBM); "
@@ -495,6 +572,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     wz.wzy_dev_set(0)
+    if args.profile:
+        profile_units(wz, args.profile, args.profile_units, args.n_ctx, args.profile_graphs)
+        return
 
     ctx_max = (args.n_ctx + args.warmup + args.steps + 64 + 8 * (args.mtp_windows + 4) + 64 + 64 + 128 +
                max(args.stage_prefill_tokens, 0))

@@ -5,7 +5,8 @@
  * message available from wzy_last_error().  All data pointers are DEVICE pointers unless stated
  * otherwise; no call synchronizes or takes ownership, and none allocates device memory except
  * wzy_row_argmax / wzy_row_top16 (a per-device scratch, allocated on first use) and the measurement
- * call wzy_moe_time_kernels.
+ * calls wzy_moe_time_kernels and wzy_gdn_time_recurrence (each allocates and frees a scratch of its
+ * own per call; the measurement calls also synchronize).
  *
  * Each function names the reference interface it replaces (reference = liaoyangr8-ai/wzy-flash-serve,
  * paths relative to its root).  The reference exposes these as `launch_*` helpers or bare

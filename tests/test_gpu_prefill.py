@@ -67,6 +67,13 @@ def bits_to_f32(h):
     (77, 4, 8192, "bf16", "f32"),       # HC inject: the skinny kernel (4 weight rows, K 8192)
     (300, 16, 2048, "bf16", "f32"),     # GDN alpha / beta gates on the skinny kernel
     (5, 7, 4096, "bf16", "f32"),        # skinny with a row count below one workgroup's 16
+    (77, 4, 6144, "bf16", "f32"),       # skinny, three 2,048-wide k slices (HC inject at n_embd 1,536)
+    (40, 8, 6144, "bf16", "f32"),       # 8 rows x 3 slices: no skinny kernel, the MFMA path
+    # 512 tiles and more: the one-LDS-buffer variants chosen for the chunk's large projections
+    (2048, 6144, 2048, "q8", "f32"),    # GDN qkv at 2,048 rows (768 tiles)
+    (2048, 4096, 1024, "q8", "bf16"),   # 512 tiles, bf16 output
+    (1024, 8192, 320, "q8", "f32"),     # HC up shape (K 320, N = 4 * 2,048) at 1,024 rows
+    (4100, 2048, 2048, "q8", "f32"),    # 528 tiles with a 4-row tail tile
 ])
 def test_gemm_bf16_parity(wz, orc, gpu, M, N, K, kind, out):
     print("case gemm M=%d N=%d K=%d %s %s" % (M, N, K, kind, out), flush=True)

@@ -1,4 +1,4 @@
-"""A wrapping KV ring is rejected before any device work (CPU only).
+"""Stage and QSA configurations this build cannot serve are rejected before any device work (CPU only).
 
 The reference keeps only a ring of recent cells in VRAM and reads older selected cells from a pinned
 host mirror (src/wzy_qsa_256k.cuh:17-29).  This build stores the full context in HBM, so a ring that
@@ -46,3 +46,14 @@ def test_qsa_entry_points_reject_wrapping_ring(wz, ctx_max, ring, sinks):
     assert "ring" in wz.wzy_last_error().decode() or "sinks" in wz.wzy_last_error().decode()
     assert wz.dll.wzy_qsa_select(dm, fake, fake, fake, fake, fake, ctx_max // 4 + 2, fake, fake, 1, None) == EINVAL
     assert wz.dll.wzy_qsa_attend(dm, fake, fake, fake, fake, fake, fake, fake, fake, fake, 1 << 30, 1, None) == EINVAL
+
+
+@pytest.mark.parametrize("n_embd", [1792, 2304, 2816, 3328, 3584, 3840])
+def test_stage_create_rejects_width_without_hc_kernel(wz, n_embd):
+    """A stream width that is a multiple of 256 but has no decode HC read kernel is refused when the
+    stage is created (before any weights are allocated), not on its first forward."""
+    c = stage_cfg(8192, 0, 0)
+    c.n_embd = n_embd
+    h = C.c_void_p()
+    assert wz.dll.wzy_stage_create(C.byref(c), 0, C.byref(h)) == EINVAL and not h.value
+    assert "HC read kernel" in wz.wzy_last_error().decode()

@@ -106,6 +106,14 @@ def test_gguf_reader_rejects_damaged_files(wz, tmp_path):
     (tmp_path / "off.gguf").write_bytes(bytes(b))
     assert wz.dll.wzy_gguf_open(str(tmp_path / "off.gguf").encode(), C.byref(h)) < 0
     assert "outside" in wz.wzy_last_error().decode()
+    # dimensions whose product wraps 64 bits (2^40 * 2^40 * 2^40 * 2^24 = 2^144 elements): an unchecked
+    # product would wrap to 0 bytes and pass the "inside the file" check
+    wrap = gf.write_gguf(tmp_path / "wrap.gguf", [("w", [1 << 40, 1 << 40, 1 << 40, 1 << 24], gf.F32, x.tobytes())])
+    assert wz.dll.wzy_gguf_open(str(wrap).encode(), C.byref(h)) < 0
+    assert "malformed" in wz.wzy_last_error().decode()
+    # 2^50 elements of four dims: no wrap, but far past the element bound
+    big = gf.write_gguf(tmp_path / "big.gguf", [("w", [1 << 10, 1 << 20, 1 << 20, 1], gf.F32, x.tobytes())])
+    assert wz.dll.wzy_gguf_open(str(big).encode(), C.byref(h)) < 0
 
 
 def test_q8_0_split_and_to_f32(wz):

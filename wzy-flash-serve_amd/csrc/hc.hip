@@ -463,6 +463,11 @@ void hc_carve_workspace(void* ws, int HC, int HCLR, int T, float** lo_part, floa
     *inj_part = (float*) ((char*) ws + align_up((size_t) T * HC * HCLR * sizeof(float), 256));
 }
 
+bool hc_width_supported(int D) {
+    int nw = 0, vpt = 0;
+    return pre_shape(D, nw, vpt);
+}
+
 int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st) {
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "hc_pre: T out of range");
     int nw = 0, vpt = 0;

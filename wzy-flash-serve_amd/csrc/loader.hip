@@ -135,8 +135,11 @@ extern "C" int wzy_gguf_open(const char* path, wzy_gguf** out) {
         uint64_t n = 1;
         for (int d = 0; d < 4; ++d) {
             t.dims[d] = d < (int) nd ? (int64_t) c.get<uint64_t>() : 1;
-            if (t.dims[d] < 1 || t.dims[d] > (int64_t) 1 << 40) c.bad = true;
-            else n *= (uint64_t) t.dims[d];
+            // each dimension and the element count are bounded (2^48 elements is far past any
+            // tensor a file of this size holds), so the product cannot wrap
+            if (t.dims[d] < 1 || t.dims[d] > (int64_t) 1 << 40 || __builtin_mul_overflow(n, (uint64_t) t.dims[d], &n) ||
+                n > (uint64_t) 1 << 48)
+                c.bad = true;
         }
         t.type = (int) c.get<uint32_t>();
         t.off = c.get<uint64_t>();

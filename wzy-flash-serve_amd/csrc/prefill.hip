@@ -1050,14 +1050,19 @@ int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
                 "pf_gemm: K split %d needs fp32 output and %d k steps divisible by it", ksplit, g.K / GK);
     if (!um && ksplit == 1 && !g.wq && g.y && g.N <= 16 && g.K % 2048 == 0 && g.K <= 8192 && g.lda % 8 == 0) {
         const int nn = g.N <= 4 ? 4 : g.N <= 8 ? 8 : 16, kj = g.K / 2048;
-        if (nn * kj <= 16) {                         // the weight slices fit 64 registers
-            const dim3 grid((g.M + SK_RB - 1) / SK_RB);
-            if (nn == 4 && kj == 4) hipLaunchKernelGGL((pf_skinny_kernel<4, 4>), grid, dim3(256), 0, st, g);
-            else if (nn == 4 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<4, 2>), grid, dim3(256), 0, st, g);
-            else if (nn == 4 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<4, 1>), grid, dim3(256), 0, st, g);
-            else if (nn == 8 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<8, 2>), grid, dim3(256), 0, st, g);
-            else if (nn == 8 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<8, 1>), grid, dim3(256), 0, st, g);
-            else hipLaunchKernelGGL((pf_skinny_kernel<16, 1>), grid, dim3(256), 0, st, g);
+        // one instantiation per (rows, k slices) whose weight slices fit 64 registers; any other
+        // combination takes the MFMA kernel below (a kernel for fewer k slices would drop a K range)
+        const dim3 grid((g.M + SK_RB - 1) / SK_RB);
+        bool done = true;
+        if (nn == 4 && kj == 4) hipLaunchKernelGGL((pf_skinny_kernel<4, 4>), grid, dim3(256), 0, st, g);
+        else if (nn == 4 && kj == 3) hipLaunchKernelGGL((pf_skinny_kernel<4, 3>), grid, dim3(256), 0, st, g);
+        else if (nn == 4 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<4, 2>), grid, dim3(256), 0, st, g);
+        else if (nn == 4 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<4, 1>), grid, dim3(256), 0, st, g);
+        else if (nn == 8 && kj == 2) hipLaunchKernelGGL((pf_skinny_kernel<8, 2>), grid, dim3(256), 0, st, g);
+        else if (nn == 8 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<8, 1>), grid, dim3(256), 0, st, g);
+        else if (nn == 16 && kj == 1) hipLaunchKernelGGL((pf_skinny_kernel<16, 1>), grid, dim3(256), 0, st, g);
+        else done = false;
+        if (done) {
             WZY_LAUNCH_CHECK();
             return WZY_OK;
         }

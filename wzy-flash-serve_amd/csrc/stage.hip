@@ -320,6 +320,9 @@ static int validate(const wzy_stage_cfg& c) {
     WZY_REQUIRE(c.n_embd >= 256 && c.n_embd % 256 == 0 && c.n_embd <= 8192, "stage: n_embd must be a multiple of 256 <= 8192");
     WZY_REQUIRE(c.hc == 4 && c.hc_lr % 32 == 0 && c.hc_lr >= 32 && c.hc_lr <= 512 && c.n_embd <= 4096,
                 "stage: bad hyper-connection shape");
+    WZY_REQUIRE(hc_width_supported(c.n_embd),
+                "stage: n_embd %d has no HC read kernel (256, 512, 768, 1024, 1280, 1536, 2048, 2560, 3072, 4096)",
+                c.n_embd);
     WZY_REQUIRE(c.gdn_hk >= 1 && c.gdn_hv % c.gdn_hk == 0, "stage: bad GDN heads");
     WZY_REQUIRE(c.qsa_hd == 256 && c.qsa_qh % c.qsa_kvh == 0 && c.qsa_qh / c.qsa_kvh <= 16, "stage: bad QSA heads");
     WZY_REQUIRE(c.idx_dim <= 128 && c.idx_heads <= 4 && c.idx_blk >= 2 && c.idx_topk >= 1, "stage: bad indexer");

@@ -46,6 +46,10 @@ struct HcPostArgs {
 size_t hc_workspace_bytes(int HC, int HCLR, int T);
 void hc_carve_workspace(void* ws, int HC, int HCLR, int T, float** lo_part, float** inj_part);
 
+// Whether the decode HC read has a kernel for stream width D (256 .. 4096 powers of two, 768, 1280,
+// 1536, 2560, 3072, 5120); the stage rejects other widths when it is created.
+bool hc_width_supported(int D);
+
 int launch_hc_pre(const HcPreArgs& a, int T, hipStream_t st);
 int launch_hc_post(const HcPostArgs& a, int T, hipStream_t st);
 
