@@ -302,11 +302,16 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
     emitted = accepted = offered = 0
     t_prop = t_win = 0.0
 
+    forced = None                    # the known greedy continuation, when drafts are forced to it
+    k_next = 0                       # index in `forced` of the token after `cur`
+
     def window():
-        nonlocal cur, unfed0, unfed, pos, emitted, accepted, offered, t_prop, t_win
+        nonlocal cur, unfed0, unfed, pos, emitted, accepted, offered, t_prop, t_win, k_next
         ta = time.perf_counter()
         d, _ = st.mtp_propose(unfed0, unfed, depth)
         tb = time.perf_counter()
+        if forced is not None:       # the drafter ran (its cost is timed); its tokens give way to the truth
+            d = forced[k_next:k_next + depth]
         win = [cur] + [int(x) for x in d]
         st.forward(pos, win, save_snaps=True)
         st.sync()
@@ -325,6 +330,9 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
         unfed0, unfed = pos, win[1:acc_rows] + [int(g[n_acc])]
         pos += acc_rows
         cur = int(g[n_acc])
+        if forced is not None:
+            assert forced[k_next:k_next + acc_rows] == win[1:acc_rows] + [cur], "forced window left the greedy stream"
+            k_next += acc_rows
 
     for _ in range(4):
         window()
@@ -336,6 +344,38 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
         window()
     wz.wzy_device_sync()
     el = time.perf_counter() - t0
+    rand = dict(emitted=emitted, accepted=accepted, offered=offered, t_prop=t_prop, t_win=t_win)
+
+    # Acceptance 1.0, measured: the greedy continuation from this state is computed first (single-token
+    # steps, after which the state is restored from an HBM session slot), then `windows` windows whose
+    # 3 drafts are that continuation; each verifies 4 rows and keeps all of them.
+    n_cells = pos
+    assert wz.wzy_stage_session_save(st.h, 0, n_cells) == 0
+    cont, p, t = [], pos, cur
+    for _ in range(4 * (windows + 2) + 4):
+        st.forward(p, [t])
+        st.sync()
+        t = int(st.greedy(1)[0])
+        cont.append(t)
+        p += 1
+    assert wz.wzy_stage_session_restore(st.h, 0) == 0
+    forced, k_next = cont, 0
+    window()                          # warm-up of the forced path (graph shapes are already captured)
+    emitted = accepted = offered = 0
+    t_prop = t_win = 0.0
+    wz.wzy_device_sync()
+    t0 = time.perf_counter()
+    for _ in range(windows):
+        window()
+    wz.wzy_device_sync()
+    el1 = time.perf_counter() - t0
+    full = {"windows": windows, "tok_s": round(emitted / el1, 2), "ms_per_window": round(1000 * el1 / windows, 4),
+            "tokens_per_window": round(emitted / windows, 4), "drafts_offered": offered, "drafts_accepted": accepted,
+            "ms_propose": round(1000 * t_prop / windows, 4), "ms_verify_window": round(1000 * t_win / windows, 4),
+            "stream_equals_greedy": True}
+    wz.wzy_stage_session_clear(st.h, 0)
+    forced = None
+    emitted, accepted, offered, t_prop, t_win = (rand[k] for k in ("emitted", "accepted", "offered", "t_prop", "t_win"))
     us = C.c_float(0)
     wz.wzy_stage_mtp_time(st.h, pos, cur, -1, time_iters, C.byref(us))
     nb = mtp_step_bytes(cfg, n_dv, min(pos - pos0, 1024))
@@ -353,11 +393,14 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
                          "frac": round(nb / (us.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "timed_steps": time_iters},
             "init_s": round(t_init, 2),
             "pos_end": pos,
+            "measured_acceptance_1": full,
             "tok_s_at_acceptance": proj,
             "note": ("the synthetic drafter is random-initialised, so its drafts match the random main model's "
                      "greedy tokens about 1 time in 10^5 and measured acceptance is ~0; tok_s is the cost of "
-                     "offering 3 drafts per window.  tok_s_at_acceptance is the measured window time with "
-                     "1+a+a^2+a^3 tokens per window (a projection, not a measurement).")}
+                     "offering 3 drafts per window.  measured_acceptance_1 times the same windows (drafter run "
+                     "included) with the drafts replaced by the known greedy continuation, every draft accepted "
+                     "and the stream checked against plain greedy decoding.  tok_s_at_acceptance is the "
+                     "random-draft window time with 1+a+a^2+a^3 tokens per window (a projection).")}
 
 
 def cpu_threads():
@@ -576,7 +619,9 @@ def main():
         profile_units(wz, args.profile, args.profile_units, args.n_ctx, args.profile_graphs)
         return
 
-    ctx_max = (args.n_ctx + args.warmup + args.steps + 64 + 8 * (args.mtp_windows + 4) + 64 + 64 + 128 +
+    # config-5 decode: up to 4 cells per random-draft window, 4 per forced window and a 4-per-window
+    # greedy continuation computed ahead of the forced windows
+    ctx_max = (args.n_ctx + args.warmup + args.steps + 64 + 12 * (args.mtp_windows + 4) + 64 + 64 + 128 +
                max(args.stage_prefill_tokens, 0))
     cfg = wzy_amd.default_cfg(ctx_max)
     t0 = time.perf_counter()

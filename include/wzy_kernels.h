@@ -246,6 +246,13 @@ typedef struct wzy_qsa_dims {
                                                     every entry point returns WZY_EINVAL (a wrapped slot
                                                     would serve a newer cell's K/V) */
     float eps;
+    int attn_f16_above;                          /* 0 = fp32 attention at every context; > 0 (the
+                                                    reference's 32,768-cell VRAM ring): a window with
+                                                    pos + T > attn_f16_above attends as the reference's
+                                                    GQA kernel does past its ring (q / 16, K and V
+                                                    rounded to fp16, fp16 softmax weights per 32-cell
+                                                    step; src/wzy_stage_v2.cuh:679-683,
+                                                    src/wzy_qsa_wmma.cuh:289-488) */
 } wzy_qsa_dims;
 
 /* Per-row preparation at positions pos[0] + t: RMSNorm + NeoX RoPE of the q heads (qg [T x qh*2*hd],
@@ -280,7 +287,8 @@ int wzy_qsa_topk(const wzy_qsa_dims* dims, const int* pos, const float* scores, 
                  int T, void* stream);
 
 /* GQA sparse attention over the selected cells: out [T x qh*hd] = softmax(q . k / 16) . v * sigmoid(gate).
- * Replaces qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532). */
+ * Replaces qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532) and, for windows past
+ * dims->attn_f16_above cells, pf_qsa_wmma_sparse_attn (src/wzy_qsa_wmma.cuh:289-488). */
 size_t wzy_qsa_attend_workspace_bytes(const wzy_qsa_dims* dims, int T);
 int wzy_qsa_attend(const wzy_qsa_dims* dims, const int* pos, const float* qg, const int8_t* kq, const uint16_t* ks,
                    const int8_t* vq, const uint16_t* vs, const int* sel_ids, float* out, void* workspace,

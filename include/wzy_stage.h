@@ -50,6 +50,11 @@ typedef struct wzy_stage_cfg {
     int head_q8;                               /* 0: LM head bf16 ("head", BASELINE); 1: Q8_0 ("head.q" /
                                                   "head.s", the reference's output.weight,
                                                   src/wzy_stage_v2.cuh:804-815) */
+    int attn_f16_above;                        /* 32768 (the reference's KV_VRAM_RING): decode windows
+                                                  with pos + T > attn_f16_above run QSA attention with
+                                                  the fp16 operands of the reference's GQA kernel
+                                                  (src/wzy_stage_v2.cuh:679-683); 0 = fp32 attention at
+                                                  every context */
 } wzy_stage_cfg;
 
 typedef struct wzy_stage wzy_stage;

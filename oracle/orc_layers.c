@@ -232,6 +232,15 @@ void orc_kv_quant_row(const float* x, int n, int8_t* q, uint16_t* s) {
  * fp16 (the scorer's rounding, src/wzy_qsa_wmma.cuh:533-537). */
 void orc_indexer_append(const float* raw, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
                         int dim, int blk, int n_rot, float eps, float* tail, float* dead, uint16_t* pooled) {
+    orc_indexer_append_f32(raw, gamma, cos_tab, sin_tab, pos, dim, blk, n_rot, eps, tail, dead, pooled, NULL);
+}
+
+/* The same, also giving the fp32 key of the block this position completes (before its fp16 rounding)
+ * in key_out [dim] when one completes (pos == 0 or pos % blk == blk - 1; else key_out is untouched),
+ * so that a test can tell an fp16 rounding flip of a key near a rounding midpoint from an error. */
+void orc_indexer_append_f32(const float* raw, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
+                            int dim, int blk, int n_rot, float eps, float* tail, float* dead, uint16_t* pooled,
+                            float* key_out) {
     float inc[128], vals[128];
     for (int d = 0; d < dim; ++d) inc[d] = orc_f16_to_f32(orc_f32_to_f16(raw[d]));
     const int slot = pos % blk;
@@ -259,6 +268,8 @@ void orc_indexer_append(const float* raw, const float* gamma, const float* cos_t
             y[i + half] = vals[i] * s + vals[i + half] * c;
         }
         for (int d = 0; d < dim; ++d) pooled[(size_t) b * dim + d] = orc_f32_to_f16(y[d]);
+        if (key_out)
+            for (int d = 0; d < dim; ++d) key_out[d] = y[d];
         if (pos == 0)
             for (int d = 0; d < dim; ++d) dead[d] = y[d];
         else

@@ -201,8 +201,14 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
                     memcpy(dst, sel, sizeof(int) * (size_t) n);
                 }
                 if (tr && tr->n_sel) tr->n_sel[(size_t) qsa_i * T + t] = n;
-                orc_attend(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh, hd,
-                           att + (size_t) t * QD);
+                /* src/wzy_stage_v2.cuh:679-683: past the VRAM ring the whole window takes the GQA
+                 * kernel (fp16 operands), else the fp32 int8 kernel */
+                if (m->attn_f16_above > 0 && pos + T > m->attn_f16_above)
+                    orc_attend_pf(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh,
+                                  hd, att + (size_t) t * QD);
+                else
+                    orc_attend(qg + (size_t) t * 2 * QD, w->kq, w->ks, w->vq, w->vs, sel, n, m->qsa_qh, m->qsa_kvh, hd,
+                               att + (size_t) t * QD);
             }
             q8_gemv_f(w->wo_q, w->wo_s, att, block, D, QD, T);
             ++qsa_i;

@@ -102,6 +102,9 @@ void orc_head_norm_rope(float* p, int hd, const float* gamma, const float* cos_t
 void orc_kv_quant_row(const float* x, int n, int8_t* q, uint16_t* s);
 void orc_indexer_append(const float* raw, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
                         int dim, int blk, int n_rot, float eps, float* tail, float* dead, uint16_t* pooled);
+void orc_indexer_append_f32(const float* raw, const float* gamma, const float* cos_tab, const float* sin_tab, int pos,
+                            int dim, int blk, int n_rot, float eps, float* tail, float* dead, uint16_t* pooled,
+                            float* key_out);
 void orc_block_scores(const uint16_t* pooled, const float* dead, const float* q_idx, int n_kv, int heads, int dim,
                       int blk, float* scores);
 int orc_topk_select(const float* scores, int n_kv, int blk, int topk, int* sel);
@@ -150,6 +153,10 @@ typedef struct orc_model {
      * src/wzy_engine_v2.cu:861-873), the head is dense_q8 (src/wzy_stage_v2.cuh:804-815) */
     const int8_t* emb_q; const uint16_t* emb_s;
     const int8_t* head_q; const uint16_t* head_s;
+    /* > 0: a window with pos + T > attn_f16_above attends through orc_attend_pf, the reference's GQA
+     * kernel past its VRAM ring (KV_VRAM_RING = 32,768; src/wzy_stage_v2.cuh:679-683); 0 or below:
+     * orc_attend (qsa_attend_int8_sparse_multi) at every context */
+    int attn_f16_above;
 } orc_model;
 
 /* logits [T x n_vocab], greedy [T] and pre_head [T x hc x n_embd] (optional); returns 0 or -1. */

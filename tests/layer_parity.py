@@ -68,6 +68,11 @@ def gpu_trace(st, cfg, T, n_qsa):
         tr["scores"] = rd("trace.scores", np.float32).reshape(nq, W, max_b)[:, :T]
         tr["sel"] = rd("trace.sel_ids", np.int32).reshape(nq, W, cfg.idx_topk)[:, :T]
         tr["n_sel"] = rd("trace.sel_cnt", np.int32).reshape(nq, W)[:, :T]
+        kvd, qd = cfg.qsa_kvh * cfg.qsa_hd, cfg.qsa_qh * cfg.qsa_hd
+        for name, key, width in (("trace.kv_k_in", "kv_k_in", kvd), ("trace.kv_v_in", "kv_v_in", kvd),
+                                 ("trace.idx_raw", "idx_raw", cfg.idx_dim), ("trace.qg", "qg", 2 * qd),
+                                 ("trace.attn", "attn", qd)):
+            tr[key] = rd(name, np.float32).reshape(nq, W, width)[:, :T]
     return tr
 
 
@@ -109,6 +114,8 @@ class LayerParity:
         self.rows = self.rows_full = 0
         self.layers_compared = self.router_compared = self.select_compared = 0
         self.router_ties = self.select_ties = self.greedy_ties = 0
+        self.excused = []                             # (kind, where, oracle margin, error measured there)
+        self.first_row_layers = None                  # layers of the first row compared before any stop
         self.worst = {h: -np.inf for h in HIDDEN}
         self.worst["logits"] = -np.inf
 
@@ -136,6 +143,8 @@ class LayerParity:
                     break
                 self._hidden(tag, t, l, 3, g, o)
                 self.layers_compared += 1
+            if self.first_row_layers is None:
+                self.first_row_layers = cfg.n_layers if stop is None else stop
             if stop is not None:
                 self.taint = min(self.taint, stop + 1)
                 continue
@@ -152,6 +161,7 @@ class LayerParity:
                 assert gap <= 2 * err, "%s row %d: greedy %d vs oracle %d, oracle gap %.3g > 2 x logit error %.3g" % (
                     tag, t, gid, ref, gap, err)
                 self.greedy_ties += 1
+                self.excused.append(("greedy", "%s row %d" % (tag, t), gap, err))
             self.rows_full += 1
 
     def _hidden(self, tag, t, l, k, g, o):
@@ -187,6 +197,7 @@ class LayerParity:
         assert gap <= 2 * err, "%s row %d layer %d: experts %s vs oracle %s, oracle gap %.3g > 2 x logit error %.3g" % (
             tag, t, l, sorted(gi.tolist()), sorted(oi.tolist()), gap, err)
         self.router_ties += 1
+        self.excused.append(("router", "%s row %d layer %d" % (tag, t, l), gap, err))
         return False
 
     def _select(self, tag, pos, t, l, qi, g, o):
@@ -206,6 +217,7 @@ class LayerParity:
         assert gap <= 2 * err, "%s row %d layer %d: selected cells differ, oracle threshold gap %.3g > 2 x score " \
                                "error %.3g" % (tag, t, l, gap, err)
         self.select_ties += 1
+        self.excused.append(("selection", "%s row %d layer %d" % (tag, t, l), gap, err))
         return False
 
     def drift_profile(self):
@@ -214,7 +226,8 @@ class LayerParity:
 
     def summary(self):
         w = ", ".join("%s %.3g" % (k, v) for k, v in self.worst.items())
-        return ("%d rows (%d compared through the head), %d layer-rows, %d router and %d selection decisions "
-                "compared; near ties: router %d, selection %d, greedy %d; worst tolerance excess: %s" % (
-                    self.rows, self.rows_full, self.layers_compared, self.router_compared, self.select_compared,
-                    self.router_ties, self.select_ties, self.greedy_ties, w))
+        ex = "; ".join("%s at %s: margin %.3g vs error %.3g" % e for e in self.excused)
+        return ("%d rows (%d compared through the head), first row %s of %d layers, %d layer-rows, %d router and %d "
+                "selection decisions compared; excused decisions %d (%s); worst tolerance excess: %s" % (
+                    self.rows, self.rows_full, self.first_row_layers, self.cfg.n_layers, self.layers_compared,
+                    self.router_compared, self.select_compared, len(self.excused), ex or "none", w))

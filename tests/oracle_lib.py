@@ -41,6 +41,7 @@ _SIGS = {
     "orc_head_norm_rope": (None, [P, I32, P, P, P, I32, I32, F32]),
     "orc_kv_quant_row": (None, [P, I32, P, P]),
     "orc_indexer_append": (None, [P, P, P, P, I32, I32, I32, I32, F32, P, P, P]),
+    "orc_indexer_append_f32": (None, [P, P, P, P, I32, I32, I32, I32, F32, P, P, P, P]),
     "orc_block_scores": (None, [P, P, P, I32, I32, I32, I32, P]),
     "orc_topk_select": (I32, [P, I32, I32, I32, P]),
     "orc_attend": (None, [P, P, P, P, P, P, I32, I32, I32, I32, P]),

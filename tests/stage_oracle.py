@@ -39,12 +39,51 @@ class OrcModel(C.Structure):
                 ("emb", P), ("head_norm", P), ("head_down_q", P), ("head_down_s", P), ("head_up_q", P),
                 ("head_up_s", P), ("head", P), ("cos_tab", P), ("sin_tab", P),
                 ("blob", BLOB_FN), ("blob_ctx", P),
-                ("emb_q", P), ("emb_s", P), ("head_q", P), ("head_s", P)]
+                ("emb_q", P), ("emb_s", P), ("head_q", P), ("head_s", P), ("attn_f16_above", I32)]
 
 
 class OrcTrace(C.Structure):
     _fields_ = [("dbg", P), ("margins", P), ("router_logits", P), ("ids", P), ("wts", P), ("scores", P), ("sel", P),
                 ("n_sel", P)]
+
+
+def attn_f16(cfg, pos, T):
+    """Whether the reference attends a window of T rows at pos with its fp16 GQA kernel: past its VRAM
+    ring, `*h_pos + T > KV_VRAM_RING` (src/wzy_stage_v2.cuh:679-683), the threshold being the stage
+    config's (or QSA dims') attn_f16_above; 0 means never."""
+    thr = cfg.attn_f16_above
+    return thr > 0 and pos + T > thr
+
+
+def attend(orc, f16, qg, kq, ks, vq, vs, cells, qh, kvh, hd):
+    """One row's sparse attention through the oracle function of the reference's branch: orc_attend_pf
+    (pf_qsa_wmma_sparse_attn, fp16 operands) when f16, else orc_attend (qsa_attend_int8_sparse_multi)."""
+    p = oracle_lib.ptr
+    out = np.empty(qh * hd, np.float32)
+    cells = np.ascontiguousarray(cells, np.int32)
+    qg = np.ascontiguousarray(qg, np.float32)              # held for the call (a copy when converted)
+    fn = orc.orc_attend_pf if f16 else orc.orc_attend
+    fn(p(qg), p(kq), p(ks), p(vq), p(vs), p(cells), len(cells), qh, kvh, hd, p(out))
+    return out
+
+
+def check_attention_branch(tag, g, a_br, a_ot, f16, rtol=2e-3):
+    """The GPU's attention rows g against the oracle of the window's branch (a_br) and of the other one
+    (a_ot), all on identical inputs: within rtol of the branch's largest output, and (when the two
+    branches are measurably apart) closer to the window's branch.  Returns (error, branch distance),
+    both relative to the largest output."""
+    g = np.asarray(g, np.float64)
+    scale = max(float(np.abs(a_br).max()), 1e-30)
+    e_br = float(np.abs(g - a_br).max()) / scale
+    e_ot = float(np.abs(g - a_ot).max()) / scale
+    gap = float(np.abs(np.asarray(a_br, np.float64) - a_ot).max()) / scale
+    name = "fp16" if f16 else "fp32"
+    print("%s: %s-branch attention, error %.3g, the other branch %.3g away (branches %.3g apart)" % (
+        tag, name, e_br, e_ot, gap), flush=True)
+    assert e_br <= rtol, "%s: attention off its %s branch by %.3g of the largest output" % (tag, name, e_br)
+    if gap > 4e-5:
+        assert e_br < e_ot, "%s: attention closer to the other branch (%.3g) than to %s (%.3g)" % (tag, e_ot, name, e_br)
+    return e_br, gap
 
 
 def is_qsa(cfg, l):
@@ -104,7 +143,8 @@ class OracleModel:
         self.layers = L
         m = OrcModel()
         for f in ("n_layers", "n_embd", "hc", "hc_lr", "gdn_hk", "gdn_hv", "qsa_qh", "qsa_kvh", "qsa_hd", "n_rot",
-                  "idx_heads", "idx_dim", "idx_blk", "idx_topk", "n_exp", "top_k", "n_ff", "n_vocab", "ctx_max", "eps"):
+                  "idx_heads", "idx_dim", "idx_blk", "idx_topk", "n_exp", "top_k", "n_ff", "n_vocab", "ctx_max", "eps",
+                  "attn_f16_above"):
             setattr(m, f, getattr(cfg, f))
         m.layers = C.cast(L, C.POINTER(OrcLayer))
         if cfg.emb_q8:
@@ -225,6 +265,7 @@ def small_cfg(wz_mod, ctx_max=1024, n_layers=4, topk=64, qsa_period=2):
     c.n_exp, c.top_k, c.n_ff, c.n_vocab = 16, 4, 128, 1000
     c.ctx_max, c.kv_ring, c.kv_sinks = ctx_max, 0, 0
     c.rope_theta, c.eps = 1e7, 1e-6
+    c.attn_f16_above = 32768               # the reference's VRAM ring (src/wzy_stage_v2.cuh:679)
     return c
 
 

@@ -27,20 +27,36 @@ For each layer l of a single-row forward at position pos:
 and then the head: oracle(R_f[L-1], comb[L-1], inj_f[L-1]) -> head HC read -> LM head vs the
 stage's pre-head residual, logits and greedy id.
 
-Tolerance: elementwise |gpu - oracle| <= ATOL + RTOL * max(|oracle|, rms(oracle row)) -- the north
-star's rel 2e-2 / abs 1e-2, with the relative term floored at the row's RMS: a component that
-requantises its input (every Q8 / NVFP4 GEMV) can still see a one-step code difference when an
-internal fp32 sum lands on a rounding boundary, which moves its outputs by about 1% of the row's
-scale, not of each element.  The largest plain elementwise excess is reported beside it.  Integer
-state (KV codes, fp16 keys / scales) may differ by one step for the same reason."""
+Tolerance: elementwise |gpu - oracle| <= ATOL + RTOL * |oracle| (the north star's rel 2e-2 /
+abs 1e-2).  Components that requantise their input (every Q8 / NVFP4 GEMV) can see a one-step code
+difference when an internal fp32 sum lands on a rounding boundary, which moves their outputs by about
+1% of the row's scale, not of each element; for those the relative term may be floored at the row's
+RMS, but every element that passes only through the floor is counted per component, printed, and
+bounded by the test (assert_bounds).  Byte work is bit-exact on identical inputs: the KV codes and
+fp16 scales of the row's cell are the oracle's quantisation of the very k / v rows the GPU quantised
+(traced), and the pooled indexer key of a completed block is the oracle's append of the GPU's raw
+key row, where an fp16 code may differ only at a rounding midpoint of the oracle's unrounded key
+(|key - midpoint| below 2^-17 of the key, the fp32 arithmetic's reach).  The attention output is
+checked tightly on identical inputs (the GPU's q | gate rows, KV store and selection) against the
+oracle function of the reference's branch for the window (orc_attend below the reference's VRAM
+ring, orc_attend_pf past it), and must sit closer to it than to the other branch.  Every excused
+discrete decision (router, selection, greedy) is recorded with its margin and the error measured at
+it, and their number is bounded by the test."""
 import ctypes as C
 
 import numpy as np
 
 import oracle_lib
 from oracle_lib import OrcMoeWeights, ptr
+from stage_oracle import attend, attn_f16
 
 RTOL, ATOL = 2e-2, 1e-2
+ATT_RTOL = 2e-3           # attention on identical inputs, relative to the row's largest output
+# components whose oracle recomputation requantises an input to int8 (a Q8 / NVFP4 GEMV or the HC
+# read's low-rank code): a one-step code flip moves such an output by ~1 % of its row's scale, so
+# their elements may pass through the row-RMS floor, in a bounded number (assert_bounds)
+# (measured: only the MoE output ever needs it, 2 elements in 16,384 at most)
+FLOOR_OK = ("MoE output",)
 
 
 def bf16_to_f32(h):
@@ -73,8 +89,12 @@ class TeacherForced:
                 self.state[(l, name)] = a.copy()
         self.worst = {}
         self.worst_plain = {}
-        self.counts = {"layers": 0, "router_ties": 0, "select_ties": 0, "greedy_ties": 0, "rows": 0, "kv_flips": 0,
-                       "key_ulps": 0}
+        self.floor_only = {}         # component -> elements within tolerance only through the RMS floor
+        self.n_elems = {}            # component -> elements compared
+        self.excused = []            # (kind, tag, oracle margin, error measured at the decision)
+        self.attn = []               # (tag, branch, error vs its branch, distance between the branches)
+        self.counts = {"layers": 0, "router_ties": 0, "select_ties": 0, "greedy_ties": 0, "rows": 0,
+                       "kv_bytes": 0, "key_midpoint_flips": 0}
         D = cfg.n_embd
         self.cos = om.arrays[(-1, "rope_cos")]
         self.sin = om.arrays[(-1, "rope_sin")]
@@ -95,6 +115,25 @@ class TeacherForced:
         self.worst_plain[what] = max(self.worst_plain.get(what, -np.inf), p)
         assert v <= 0, "%s: %s beyond tolerance by %.3g (max abs err %.3g)" % (
             tag, what, v, float(np.abs(np.asarray(g, np.float64) - o).max()))
+        gg = np.asarray(g, np.float64).ravel()
+        oo = np.asarray(o, np.float64).ravel()
+        self.floor_only[what] = self.floor_only.get(what, 0) + int((np.abs(gg - oo) > ATOL + RTOL * np.abs(oo)).sum())
+        self.n_elems[what] = self.n_elems.get(what, 0) + gg.size
+
+    def _excuse(self, kind, tag, margin, err):
+        self.excused.append((kind, tag, float(margin), float(err)))
+        self.counts[kind + "_ties"] += 1
+
+    def assert_bounds(self, max_floor_frac=5e-4, max_excused=1, floor_ok=FLOOR_OK):
+        """The plain elementwise tolerance holds on every component outside `floor_ok`; inside it, at
+        most max_floor_frac of a component's elements pass only through the RMS floor; at most
+        max_excused discrete decisions were excused."""
+        for what, n in self.floor_only.items():
+            lim = max_floor_frac * self.n_elems[what] if what in floor_ok else 0
+            assert n <= lim, "%s: %d of %d elements within tolerance only through the row-RMS floor (limit %d)" % (
+                what, n, self.n_elems[what], lim)
+        assert len(self.excused) <= max_excused, "%d excused decisions (limit %d): %s" % (
+            len(self.excused), max_excused, self.excused)
 
     def _q8(self, name, l, x, rows):
         cols = x.size
@@ -192,35 +231,53 @@ class TeacherForced:
                 for i in range(IH):
                     orc.orc_head_norm_rope(q_idx[i * ID:].ctypes.data, ID, ptr(self.A[(l, "idx_qn")]), ptr(self.cos),
                                            ptr(self.sin), pos, cfg.n_rot, cfg.eps)
-                # KV cell at pos: the oracle's quantisation of its k / v vs the stage's bytes
+                # the rows the GPU quantised (k after norm + RoPE, v, the raw indexer key) against the
+                # oracle's own rows, then the KV cell at pos: the oracle's quantisation of the GPU's rows,
+                # bit for bit (codes and fp16 scales)
+                gk, gv = g["kv_k_in"][qi, 0], g["kv_v_in"][qi, 0]
+                self._cmp("k row (norm + RoPE)", gk, kk, t)
+                self._cmp("v row", gv, vv, t)
                 ok, oks = np.zeros(KVD, np.int8), np.zeros(KVD // 64, np.uint16)
                 ov, ovs = np.zeros(KVD, np.int8), np.zeros(KVD // 64, np.uint16)
-                orc.orc_kv_quant_row(ptr(kk), KVD, ptr(ok), ptr(oks))
-                orc.orc_kv_quant_row(ptr(vv), KVD, ptr(ov), ptr(ovs))
+                orc.orc_kv_quant_row(ptr(np.ascontiguousarray(gk)), KVD, ptr(ok), ptr(oks))
+                orc.orc_kv_quant_row(ptr(np.ascontiguousarray(gv)), KVD, ptr(ov), ptr(ovs))
                 gcell = {n: st.read_range(l, n, dt, pos * w, w) for n, dt, w in
                          (("kv_k", np.int8, KVD), ("kv_v", np.int8, KVD), ("kv_ks", np.uint16, KVD // 64),
                           ("kv_vs", np.uint16, KVD // 64))}
                 for n, o in (("kv_k", ok), ("kv_v", ov), ("kv_ks", oks), ("kv_vs", ovs)):
-                    dd = np.abs(gcell[n].astype(np.int32) - o.astype(np.int32))
-                    assert dd.max() <= 1, "%s: KV %s of cell %d differs by %d steps" % (t, n, pos, dd.max())
-                    self.counts["kv_flips"] += int((dd > 0).sum())
+                    bad = np.flatnonzero(gcell[n] != o)
+                    assert bad.size == 0, "%s: KV %s of cell %d differs from the quantisation of the GPU's own " \
+                                          "row at %d of %d elements" % (t, n, pos, bad.size, o.size)
+                    self.counts["kv_bytes"] += o.size
                 for n in ("kv_k", "kv_v", "kv_ks", "kv_vs"):
                     w = gcell[n].size
                     arr = self.state[(l, n)]
                     arr[pos * w:(pos + 1) * w] = gcell[n]
                     new_state[(l, n)] = arr
-                # indexer append on the pre-row indexer state
+                # indexer append of the GPU's raw key row on the pre-row indexer state
+                gr = np.ascontiguousarray(g["idx_raw"][qi, 0])
+                self._cmp("indexer key row", gr, idx_raw, t)
                 tail, dead = self.state[(l, "idx_tail")].copy(), self.state[(l, "idx_dead")].copy()
                 pooled = self.state[(l, "idx_pooled")].copy()
-                orc.orc_indexer_append(ptr(idx_raw), ptr(self.A[(l, "idx_kn")]), ptr(self.cos), ptr(self.sin), pos, ID,
-                                       blk, cfg.n_rot, cfg.eps, ptr(tail), ptr(dead), ptr(pooled))
+                key = np.full(ID, np.nan, np.float32)
+                orc.orc_indexer_append_f32(ptr(gr), ptr(self.A[(l, "idx_kn")]), ptr(self.cos), ptr(self.sin), pos,
+                                           ID, blk, cfg.n_rot, cfg.eps, ptr(tail), ptr(dead), ptr(pooled), ptr(key))
                 g_tail, g_dead = st.read(l, "idx_tail", np.float32), st.read(l, "idx_dead", np.float32)
                 g_pooled = st.read(l, "idx_pooled", np.uint16)
-                self._cmp("indexer tail", g_tail, tail, t)
+                assert np.array_equal(g_tail, tail), "%s: indexer tail (fp16-rounded raw keys) differs" % t
                 self._cmp("indexer placeholder", g_dead, dead, t)
-                dk = np.abs(g_pooled.astype(np.int32) - pooled.astype(np.int32))
-                assert dk.max() <= 1, "%s: pooled indexer keys differ by %d fp16 steps" % (t, dk.max())
-                self.counts["key_ulps"] += int((dk > 0).sum())
+                for i in np.flatnonzero(g_pooled != pooled):
+                    b, d = divmod(int(i), ID)
+                    assert b == pos // blk and not np.isnan(key[d]), \
+                        "%s: pooled key %d dim %d differs, and no block completed there" % (t, b, d)
+                    lo_, hi_ = sorted((np.uint16(g_pooled[i]).view(np.float16).astype(np.float64),
+                                       np.uint16(pooled[i]).view(np.float16).astype(np.float64)))
+                    mid = 0.5 * (lo_ + hi_)
+                    assert np.nextafter(np.float16(lo_), np.float16(np.inf)) == np.float16(hi_) and \
+                        abs(float(key[d]) - mid) <= 2.0 ** -17 * abs(float(key[d])), \
+                        "%s: pooled key %d dim %d: fp16 %r vs %r, unrounded key %r is not at their midpoint" % (
+                            t, b, d, lo_, hi_, float(key[d]))
+                    self.counts["key_midpoint_flips"] += 1
                 new_state[(l, "idx_tail")], new_state[(l, "idx_dead")], new_state[(l, "idx_pooled")] = \
                     g_tail, g_dead, g_pooled
                 # block scores on the stage's post-row keys, then the selection
@@ -246,12 +303,31 @@ class TeacherForced:
                     gap = threshold_gap(scores, n_kv, blk, topk)
                     err = float(np.abs(gsc[:nb].astype(np.float64) - scores[:nb]).max())
                     assert gap <= 2 * err, "%s: selected cells differ, gap %.3g > 2 x score error %.3g" % (t, gap, err)
-                    self.counts["select_ties"] += 1
-                att = np.empty(QD, np.float32)
+                    self._excuse("select", t, gap, err)
                 sel = np.ascontiguousarray(gsel[:n])
                 S = self.state
-                orc.orc_attend(ptr(qg), ptr(S[(l, "kv_k")]), ptr(S[(l, "kv_ks")]), ptr(S[(l, "kv_v")]),
-                               ptr(S[(l, "kv_vs")]), ptr(sel), n, cfg.qsa_qh, cfg.qsa_kvh, hd, ptr(att))
+                kvs = (S[(l, "kv_k")], S[(l, "kv_ks")], S[(l, "kv_v")], S[(l, "kv_vs")])
+                f16 = attn_f16(cfg, pos, 1)
+                # the attention itself on identical inputs (the GPU's q | gate rows after norm + RoPE,
+                # its KV store and selection): close to the oracle of the window's branch, and closer to
+                # it than to the other branch
+                gq = np.ascontiguousarray(g["qg"][qi, 0])
+                self._cmp("q rows (norm + RoPE)", gq, qg, t)
+                a_br = attend(orc, f16, gq, *kvs, sel, cfg.qsa_qh, cfg.qsa_kvh, hd)
+                a_ot = attend(orc, not f16, gq, *kvs, sel, cfg.qsa_qh, cfg.qsa_kvh, hd)
+                ga = g["attn"][qi, 0].astype(np.float64)
+                scale = max(float(np.abs(a_br).max()), 1e-30)
+                e_br = float(np.abs(ga - a_br).max()) / scale
+                e_ot = float(np.abs(ga - a_ot).max()) / scale
+                gap_br = float(np.abs(a_br.astype(np.float64) - a_ot).max()) / scale
+                self.attn.append((t, "fp16" if f16 else "fp32", e_br, gap_br))
+                assert e_br <= ATT_RTOL, "%s: attention (%s branch) on identical inputs off by %.3g of its range" % (
+                    t, "fp16" if f16 else "fp32", e_br)
+                if gap_br > 4e-5:
+                    assert e_br < e_ot, "%s: attention is closer to the %s branch (%.3g) than to the window's " \
+                                        "(%.3g)" % (t, "fp32" if f16 else "fp16", e_ot, e_br)
+                # the chain from the oracle's own q rows, through the branch's attention and o projection
+                att = attend(orc, f16, qg, *kvs, sel, cfg.qsa_qh, cfg.qsa_kvh, hd)
                 block = self._q8("wo", l, att, D)
             self._cmp("attention block", g["hidden"][l, 1, 0], block, t)
             # ---- FFN HC read on the GPU's attention-half outputs
@@ -275,7 +351,7 @@ class TeacherForced:
                 else:
                     assert s[K - 1] - s[K] <= 2 * err, "%s: experts %s vs %s, gap %.3g > 2 x logit error %.3g" % (
                         t, sorted(gi.tolist()), sorted(ids.tolist()), s[K - 1] - s[K], err)
-                    self.counts["router_ties"] += 1
+                    self._excuse("router", t, s[K - 1] - s[K], err)
             else:
                 self._cmp("router weights", g["wts"][l, 0], wts, t)
                 self._cmp("MoE output", g["hidden"][l, 3, 0], comb, t)
@@ -294,7 +370,7 @@ class TeacherForced:
             err = float(np.abs(g_logits.ravel().astype(np.float64) - logits).max())
             gap = float(logits[ref]) - float(logits[gid])
             assert gap <= 2 * err, "%s: greedy %d vs %d, gap %.3g > 2 x logit error %.3g" % (tag, gid, ref, gap, err)
-            self.counts["greedy_ties"] += 1
+            self._excuse("greedy", tag, gap, err)
         # teacher forcing: the next row starts from the stage's own post-row state
         self.state.update(new_state)
 
@@ -322,7 +398,18 @@ class TeacherForced:
 
     def summary(self):
         w = ", ".join("%s %.3g (plain %.3g)" % (k, self.worst[k], self.worst_plain[k]) for k in self.worst)
-        return ("teacher-forced: %d rows, %d layer-rows; near ties: router %d, selection %d, greedy %d; KV codes "
-                "one step apart %d, pooled keys one fp16 step apart %d; worst tolerance excess (<= 0 passes): %s" % (
-                    self.counts["rows"], self.counts["layers"], self.counts["router_ties"], self.counts["select_ties"],
-                    self.counts["greedy_ties"], self.counts["kv_flips"], self.counts["key_ulps"], w))
+        fo = ", ".join("%s %d/%d" % (k, n, self.n_elems[k]) for k, n in self.floor_only.items() if n)
+        ex = "; ".join("%s at %s: margin %.3g vs error %.3g" % e for e in self.excused)
+        at = ""
+        if self.attn:
+            for br in ("fp32", "fp16"):
+                r = [a for a in self.attn if a[1] == br]
+                if r:
+                    at += " %s-branch attention on identical inputs: %d rows, max error %.3g, branches %.3g-%.3g " \
+                          "apart (relative to the row's largest output);" % (
+                              br, len(r), max(a[2] for a in r), min(a[3] for a in r), max(a[3] for a in r))
+        return ("teacher-forced: %d rows, %d layer-rows; KV bytes bit-exact on the GPU's rows %d, pooled-key fp16 "
+                "midpoint flips %d;%s excused decisions %d (%s); elements within tolerance only through the row-RMS "
+                "floor: %s; worst tolerance excess (<= 0 passes): %s" % (
+                    self.counts["rows"], self.counts["layers"], self.counts["kv_bytes"],
+                    self.counts["key_midpoint_flips"], at, len(self.excused), ex or "none", fo or "none", w))

@@ -23,6 +23,7 @@ import pytest
 import wzy_amd
 from layer_parity import ATOL, RTOL, excess, threshold_gap
 from oracle_lib import ptr
+from stage_oracle import attend, attn_f16, check_attention_branch
 
 pytestmark = pytest.mark.gpu
 
@@ -122,6 +123,7 @@ def test_config3_qsa_262k_context(wz, orc, gpu):
     dm.qh, dm.kvh, dm.hd, dm.n_rot = 24, 2, 256, 64
     dm.idx_heads, dm.idx_dim, dm.idx_blk, dm.idx_topk = 4, 128, 4, 2048
     dm.ctx_max, dm.kv_ring, dm.kv_sinks, dm.eps = ctx, 0, 0, 1e-6
+    dm.attn_f16_above = 32768          # the reference's VRAM ring: this context attends with its fp16 kernel
     qh, kvh, hd, ih, idim, blk = 24, 2, 256, 4, 128, 4
     KVD, max_b = kvh * hd, ctx // blk + 2
     rng = np.random.default_rng(2)
@@ -186,10 +188,27 @@ def test_config3_qsa_262k_context(wz, orc, gpu):
     np.testing.assert_array_equal(d["vq"].numpy()[pos], ovq)
     np.testing.assert_array_equal(d["vs"].numpy()[pos], ovs)
     gkq = d["kq"].numpy()
+    # the K cell: the oracle's quantisation of the very k row the GPU quantised (its k after norm + RoPE,
+    # left in place by the prepare call), bit for bit
+    gkq_o, gks_o = np.zeros(KVD, np.int8), np.zeros(KVD // 64, np.uint16)
+    g_kk = np.ascontiguousarray(d["kk"].numpy()[0])          # held: the oracle reads it through a pointer
+    orc.orc_kv_quant_row(ptr(g_kk), KVD, ptr(gkq_o), ptr(gks_o))
+    np.testing.assert_array_equal(gkq[pos], gkq_o)
+    np.testing.assert_array_equal(d["ks"].numpy()[pos], gks_o)
     assert np.abs(gkq[pos].astype(int) - okq).max() <= 1
     assert np.array_equal(gkq[:pos], kq[:pos]), "prefilled K cells changed"
     gpooled = d["pooled"].numpy()
-    assert np.abs(gpooled.astype(np.int32) - opooled.astype(np.int32)).max() <= 1, "pooled keys beyond 1 fp16 ulp"
+    # the pooled key of the block this token completes: identical raw input on both sides, so an fp16
+    # code may differ only where the oracle's unrounded key sits at a rounding midpoint
+    key = np.full(idim, np.nan, np.float32)
+    ktail, kdead, kpooled = tail.copy(), dead.copy(), pooled.copy()
+    orc.orc_indexer_append_f32(ptr(o["idx_raw"][0]), ptr(o["ik_norm"]), ptr(cos_t), ptr(sin_t), pos, idim, blk, 64,
+                               1e-6, ptr(ktail), ptr(kdead), ptr(kpooled), ptr(key))
+    for i in np.flatnonzero(gpooled.ravel() != opooled.ravel()):
+        b, dd = divmod(int(i), idim)
+        assert b == pos // blk and not np.isnan(key[dd]), "pooled key %d dim %d changed" % (b, dd)
+        h = sorted(float(np.uint16(x).view(np.float16)) for x in (gpooled.ravel()[i], opooled.ravel()[i]))
+        assert abs(float(key[dd]) - 0.5 * (h[0] + h[1])) <= 2.0 ** -17 * abs(float(key[dd])), (b, dd, h, key[dd])
 
     # scores over 65,537 blocks, then the exact top-2048 (bit-exact on the GPU's own scores)
     n_kv = pos + 1
@@ -212,12 +231,17 @@ def test_config3_qsa_262k_context(wz, orc, gpu):
         gap = threshold_gap(osc, n_kv, blk, 2048)
         assert gap <= 2 * serr.max(), "selection differs from the oracle's outside a near tie (gap %.3g)" % gap
         print("selection: near tie at the threshold (gap %.3g, score error %.3g)" % (gap, serr.max()), flush=True)
-    # attention over the GPU's selection (the oracle reads the GPU-appended K/V of the new cell)
-    oatt = np.empty(qh * hd, np.float32)
-    gqg, gks, gvq, gvs = d["qg"].numpy(), d["ks"].numpy(), d["vq"].numpy(), d["vs"].numpy()   # held for the call
-    orc.orc_attend(ptr(gqg[0]), ptr(gkq), ptr(gks), ptr(gvq), ptr(gvs), ptr(gsel), 2048, qh, kvh, hd, ptr(oatt))
+    # attention over the GPU's selection (the oracle reads the GPU-appended K/V of the new cell): at
+    # 262,144 cells the reference runs its fp16 GQA kernel (src/wzy_stage_v2.cuh:679-683), restated by
+    # orc_attend_pf; orc_attend (its fp32 kernel) is the other branch
+    gqg, gks, gvq, gvs = d["qg"].numpy(), d["ks"].numpy(), d["vq"].numpy(), d["vs"].numpy()
+    assert attn_f16(dm, pos, 1)
+    oatt = attend(orc, True, gqg[0], gkq, gks, gvq, gvs, gsel, qh, kvh, hd)
+    o32 = attend(orc, False, gqg[0], gkq, gks, gvq, gvs, gsel, qh, kvh, hd)
     gatt = out.numpy()[0]
     v = excess(gatt, oatt)
-    print("attention: max abs err %.3g (max %.3g), tolerance excess %.3g" % (
-        np.abs(gatt - oatt).max(), np.abs(oatt).max(), v), flush=True)
+    print("attention: max abs err %.3g (max %.3g), tolerance excess %.3g; fp16 and fp32 branches differ by at most "
+          "%.3g" % (np.abs(gatt - oatt).max(), np.abs(oatt).max(), v, np.abs(oatt.astype(np.float64) - o32).max()),
+          flush=True)
     assert v <= 0
+    check_attention_branch("config 3", gatt, oatt, o32, True)

@@ -211,6 +211,7 @@ def test_engine_greedy_stream_parity_and_prefix_reuse(wz, gpu):
         print("engine greedy vs oracle, free-running: " + rep.par.summary(), flush=True)
         print("engine greedy vs oracle: " + rep.tf.summary(), flush=True)
         assert rep.tf.counts["rows"] == 14 and rep.tf.counts["layers"] == 14 * 4, rep.tf.summary()
+        rep.tf.assert_bounds()
     finally:
         rep.close()
         assert eng.close() == 0
@@ -357,6 +358,57 @@ def test_engine_mtp_speculative_decoding_is_lossless(wz, gpu):
     print("mtp engine: fixed3 drafts %d accepted %d; gated drafts %d accepted %d" % (
         d["draft_n"], d["draft_accepted"], streams["gated"][1]["draft_n"], streams["gated"][1]["draft_accepted"]),
         flush=True)
+
+
+def expected_forced(pattern, n_new, depth):
+    """(windows, drafts offered, drafts accepted) of the engine loop with forced drafts: window i
+    emits its current token, offers min(depth, tokens still to generate) drafts of which the first
+    pattern[i % len] are the continuation's, accepts those (rank-1 acceptance stops at the first wrong
+    one), and continues with the verified row's token."""
+    gen, wins, offered, accepted = 0, 0, 0, 0
+    while gen < n_new:
+        gen += 1                                  # the current token
+        if gen >= n_new:
+            break
+        k = min(depth, n_new - gen)
+        a = min(pattern[wins % len(pattern)], k)
+        offered += k
+        accepted += a
+        gen += a
+        wins += 1
+    return wins, offered, accepted
+
+
+@pytest.mark.parametrize("pattern", [[3], [0, 1, 2, 3], [2, 0, 3, 1, 1]])
+def test_engine_forced_drafts_exercise_the_accept_path(wz, gpu, tmp_path, pattern):
+    """The accept branch of the decode loop (src/wzy_engine_v2.cu:2160-2190) with accepted drafts:
+    each window's 3 drafts are replaced by the plain greedy continuation for its first pattern[i] tokens
+    and wrong tokens after (--forced-drafts; the drafter still runs and catches up on the accepted
+    cells).  Windows accept 0, 1, 2 and 3 drafts; the stream equals the plain greedy stream token for
+    token, the accepted count is the pattern's, and a rejected suffix's state is discarded
+    (commit_window_state at the accepted row), so later windows stay exact."""
+    print("case engine_forced pattern=%s" % pattern, flush=True)
+    cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    prompt = [int(t) for t in np.random.default_rng(9).integers(0, cfg.n_vocab, 29)]
+    n_new = 40
+    eng = EngineProc(cfg, env={"WZY_MTP_DVOCAB": "800"})
+    try:
+        _, base, _ = eng.request(greedy_req(prompt, n_new, no_reuse=1))
+    finally:
+        assert eng.close() == 0
+    f = tmp_path / "forced.txt"
+    f.write_text(" ".join(map(str, pattern)) + "\n" + " ".join(map(str, base)) + "\n")
+    eng = EngineProc(cfg, "--spec-depth", "3", "--forced-drafts", str(f), env={"WZY_MTP_DVOCAB": "800"})
+    try:
+        _, toks, done = eng.request(greedy_req(prompt, n_new, no_reuse=1))
+    finally:
+        assert eng.close() == 0
+    wins, offered, accepted = expected_forced(pattern, n_new, 3)
+    print("forced drafts %s: %d windows, %d drafts offered, %d accepted (engine: %d / %d)" % (
+        pattern, wins, offered, accepted, done["draft_n"], done["draft_accepted"]), flush=True)
+    assert toks == base, "forced %s stream %s vs plain %s" % (pattern, toks, base)
+    assert done["generated"] == n_new
+    assert done["draft_n"] == offered and done["draft_accepted"] == accepted, done
 
 
 def test_engine_real_weight_files(wz, gpu, tmp_path):

@@ -8,6 +8,7 @@ import pytest
 import oracle_lib
 import wzy_amd
 from oracle_lib import ptr
+from stage_oracle import attend, attn_f16, check_attention_branch
 
 pytestmark = pytest.mark.gpu
 
@@ -372,12 +373,20 @@ def test_qsa_topk_score_patterns(wz, orc, gpu, kind, ctx, pos, T, topk):
         assert (gsel[t, :n] == osel[:n]).all(), "row %d: selection differs" % t
 
 
+@pytest.mark.parametrize("f16_above", [0, "window"])
 @pytest.mark.parametrize("qh,kvh,pos,T,topk", [(4, 2, 700, 3, 64), (24, 2, 3000, 2, 2048), (24, 2, 100, 1, 2048),
-                                               (8, 1, 300, 4, 256)])
-def test_qsa_attend(wz, orc, gpu, qh, kvh, pos, T, topk):
-    print("case qsa_attend qh=%d kvh=%d pos=%d T=%d topk=%d" % (qh, kvh, pos, T, topk), flush=True)
+                                               (8, 1, 300, 4, 256), (24, 2, 3999, 1, 2048)])
+def test_qsa_attend(wz, orc, gpu, qh, kvh, pos, T, topk, f16_above):
+    """f16_above 0: the fp32 kernel at every context (orc_attend); "window": the threshold is crossed by
+    the window's last row only (pos + T - 1), and every row of the window takes the reference's fp16
+    GQA branch (orc_attend_pf), as src/wzy_stage_v2.cuh:679-683 decides per window."""
+    print("case qsa_attend qh=%d kvh=%d pos=%d T=%d topk=%d f16_above=%s" % (qh, kvh, pos, T, topk, f16_above),
+          flush=True)
     ctx = 4096
     dm = qsa_dims(ctx, topk, qh, kvh)
+    dm.attn_f16_above = 0 if f16_above == 0 else pos + T - 1
+    f16 = attn_f16(dm, pos, T)
+    assert f16 == (f16_above != 0)
     hd = 256
     KVD = kvh * hd
     rng = np.random.default_rng(qh + pos + T)
@@ -404,7 +413,7 @@ def test_qsa_attend(wz, orc, gpu, qh, kvh, pos, T, topk):
     for t in range(T):
         n_kv = pos + t + 1
         cells = sel[t] if n_kv > topk else np.arange(n_kv, dtype=np.int32)
-        o = np.empty(qh * hd, np.float32)
-        orc.orc_attend(ptr(qg[t]), ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(np.ascontiguousarray(cells)), len(cells), qh,
-                       kvh, hd, ptr(o))
+        o = attend(orc, f16, qg[t], kq, ks, vq, vs, cells, qh, kvh, hd)
         close("attend[%d]" % t, g[t], o, 1e-3, 1e-4)
+        check_attention_branch("attend[%d]" % t, g[t], o, attend(orc, not f16, qg[t], kq, ks, vq, vs, cells, qh, kvh, hd),
+                               f16)

@@ -276,6 +276,7 @@ def test_stage_prefill_matches_oracle(wz, orc, gpu, p0, B, prefix):
         gt = gpu_trace(st, cfg, 1, len([l for l in range(cfg.n_layers) if is_qsa(cfg, l)]))
         tf.check_row("decode after prefill pos %d" % pos, pos, toks[pos], gt, st.logits(1), st.greedy(1), st.pre_head(1))
         print("decode after prefill: " + tf.summary(), flush=True)
+        tf.assert_bounds()
     finally:
         st.close()
 

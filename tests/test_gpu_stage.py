@@ -167,22 +167,24 @@ def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=F
         st.close()
 
 
-@pytest.mark.parametrize("seed,n_ctx", [(1234, 600), (77, 601), (5, 300)])
-def test_stage_multilayer_decode(wz, gpu, seed, n_ctx):
+@pytest.mark.parametrize("seed,n_ctx,f16_above", [(1234, 600, 32768), (77, 601, 603), (5, 300, 32768)])
+def test_stage_multilayer_decode(wz, gpu, seed, n_ctx, f16_above):
     """Four layers (GDN, QSA, GDN, QSA): four single-token steps, each checked component by component
     against the oracle fed the GPU's own inputs and pre-row state (teacher-forced), then a T=4 window;
     the discrete decisions of every row (expert ids, selected cells, greedy ids) are compared
     free-running, layer by layer.  (Free-running hidden states are reported, not asserted: a one-step
     int8 code difference in a block's requantised input, from fp32 sums run in another order, moves
     the synthetic MoE's outputs by more than the float tolerance, and that compounds over layers.)"""
-    print("case multilayer seed=%d n_ctx=%d" % (seed, n_ctx), flush=True)
+    print("case multilayer seed=%d n_ctx=%d f16_above=%d" % (seed, n_ctx, f16_above), flush=True)
     cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=4, topk=64)
+    cfg.attn_f16_above = f16_above         # 603: steps 601, 602 on the fp32 branch, then the fp16 one
     rng = np.random.default_rng(seed)
     windows = [[int(t)] for t in rng.integers(0, cfg.n_vocab, 4)] + [[int(t) for t in rng.integers(0, cfg.n_vocab, 4)]]
     par, tf = run_layer_parity(wz, cfg, seed, n_ctx, windows, teacher=True)
     print("multilayer: " + par.summary(), flush=True)
     print("multilayer: " + tf.summary(), flush=True)
     assert tf.counts["rows"] == 4 and tf.counts["layers"] == 16, tf.summary()
+    tf.assert_bounds()
     assert par.rows_full >= 6 and par.layers_compared >= 28, par.summary()
 
 
@@ -205,6 +207,7 @@ def test_stage_baseline_shapes_4_layers(wz, gpu):
     print("baseline 4 layers: " + par.summary(), flush=True)
     print("baseline 4 layers: " + tf.summary(), flush=True)
     assert tf.counts["rows"] == 4 and tf.counts["layers"] == 16
+    tf.assert_bounds()
     assert par.router_compared >= 12 and par.select_compared >= 3, par.summary()
 
 
@@ -221,8 +224,16 @@ def test_stage_baseline_48_layers_greedy(wz, gpu):
     print("baseline 48 layers: " + tf.summary(), flush=True)
     # every component of every layer of the four greedy steps, teacher-forced
     assert tf.counts["rows"] == 4 and tf.counts["layers"] == 4 * 48
-    # free-running: the first row's decisions are compared until the first near tie
-    assert par.router_compared >= 12 and par.select_compared >= 3, par.summary()
+    tf.assert_bounds()
+    # free-running (the oracle running the whole model on its own): each row's decisions are compared
+    # layer by layer until the first one whose oracle margin lies inside the error measured at it.  At
+    # these shapes that is the first QSA layer's top-2048 (layer 3): the free-running MoE outputs of
+    # layers 0-2 already differ by int8 requantisation flips amplified by the synthetic experts' gain
+    # (the teacher-forced check above holds every component on identical inputs), which moves the
+    # block scores by ~0.2 while the 2,048-cell threshold sits ~0.01 from the next block.  Every layer
+    # before it must agree, and each stop must be such a near tie (asserted inside LayerParity).
+    assert par.first_row_layers >= 3 and par.router_compared >= 3 * 5, par.summary()
+    assert all(kind == "selection" and "layer 3" in where for kind, where, _, _ in par.excused), par.summary()
 
 
 def real_cfg(n_layers, ctx_max):
@@ -247,6 +258,7 @@ def test_stage_reference_real_shape_4_layers(wz, gpu):
     print("real shape 4 layers: " + par.summary(), flush=True)
     print("real shape 4 layers: " + tf.summary(), flush=True)
     assert tf.counts["rows"] == 3 and tf.counts["layers"] == 12
+    tf.assert_bounds()
     assert par.router_compared >= 8 and par.select_compared >= 2, par.summary()
 
 
@@ -370,12 +382,16 @@ def test_stage_errors(wz, gpu):
         st.close()
 
 
-def test_stage_qsa_kernels_in_situ(wz, orc, gpu):
+@pytest.mark.parametrize("f16_above", [32768, 602])
+def test_stage_qsa_kernels_in_situ(wz, orc, gpu, f16_above):
     """Consecutive decode steps of a GDN+QSA stage: after each step, the QSA layer's block scores,
-    cell selection and attention output are recomputed by the oracle from the stage's own inputs."""
+    cell selection and attention output are recomputed by the oracle from the stage's own inputs.  With
+    attn_f16_above 602 the steps at 602 and later attend through the reference's fp16 GQA branch."""
     from oracle_lib import ptr
-    print("case stage_qsa_in_situ", flush=True)
+    from stage_oracle import attend, attn_f16, check_attention_branch
+    print("case stage_qsa_in_situ f16_above=%d" % f16_above, flush=True)
     cfg = small_cfg(wzy_amd, ctx_max=1024, n_layers=2, topk=64)
+    cfg.attn_f16_above = f16_above
     st = wzy_amd.Stage(cfg)
     try:
         st.load_synthetic(5, 600)
@@ -406,12 +422,15 @@ def test_stage_qsa_kernels_in_situ(wz, orc, gpu):
             n = orc.orc_topk_select(ptr(sc), n_kv, cfg.idx_blk, cfg.idx_topk, ptr(osel))
             assert cnt == n == min(n_kv, cfg.idx_topk)
             assert (sel[:n] == osel[:n]).all(), "step %d selection differs" % step
-            oatt = np.empty(QD, np.float32)
-            orc.orc_attend(ptr(qg), ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(np.ascontiguousarray(sel[:n])), n,
-                           cfg.qsa_qh, cfg.qsa_kvh, cfg.qsa_hd, ptr(oatt))
+            f16 = attn_f16(cfg, pos, 1)
+            assert f16 == (pos >= f16_above)
+            oatt = attend(orc, f16, qg, kq, ks, vq, vs, sel[:n], cfg.qsa_qh, cfg.qsa_kvh, cfg.qsa_hd)
             aerr = np.abs(att - oatt).max()
             print("step %d: attention max abs err %.3g (max %.3g)" % (step, aerr, np.abs(oatt).max()), flush=True)
             assert aerr < 1e-3, "step %d attention" % step
+            check_attention_branch("step %d" % step, att, oatt,
+                                   attend(orc, not f16, qg, kq, ks, vq, vs, sel[:n], cfg.qsa_qh, cfg.qsa_kvh,
+                                          cfg.qsa_hd), f16)
     finally:
         st.close()
 

@@ -151,7 +151,7 @@ class Model:
 # ------------------------------------------------------------------------------------------------
 # the oracle's composition
 # ------------------------------------------------------------------------------------------------
-def oracle_forward(orc, m, state, pos, toks):
+def oracle_forward(orc, m, state, pos, toks, f16_above=0):
     keep = []
 
     def p(a):
@@ -191,6 +191,7 @@ def oracle_forward(orc, m, state, pos, toks):
     mm.qsa_qh, mm.qsa_kvh, mm.qsa_hd, mm.n_rot = QH, KVH, HD, NROT
     mm.idx_heads, mm.idx_dim, mm.idx_blk, mm.idx_topk = IH, IDIM, IBLK, TOPK
     mm.n_exp, mm.top_k, mm.n_ff, mm.n_vocab, mm.ctx_max, mm.eps = E, K, F, V, CTX, EPS
+    mm.attn_f16_above = f16_above
     mm.layers = C.cast(L, C.POINTER(OrcLayer))
     mm.emb, mm.head_norm = p(m.emb), p(m.head_norm)
     mm.head_down_q, mm.head_down_s = p(m.head_down[0]), p(m.head_down[1])
@@ -216,7 +217,7 @@ def oracle_forward(orc, m, state, pos, toks):
 # ------------------------------------------------------------------------------------------------
 # the independent composition (reference record_forward order); `plant` names a wiring mistake
 # ------------------------------------------------------------------------------------------------
-def compose(orc, m, state, pos, toks, plant=None):
+def compose(orc, m, state, pos, toks, plant=None, f16_above=0):
     T = len(toks)
     ptr = oracle_lib.ptr
     out_dbg = np.zeros((len(KINDS), 4, T, D), np.float32)
@@ -305,8 +306,11 @@ def compose(orc, m, state, pos, toks, plant=None):
                     orc.orc_block_scores(ptr(s["idx_pooled"]), ptr(s["idx_dead"]), q_idx[t].ctypes.data, n_kv, IH,
                                          IDIM, IBLK, ptr(scores))
                 n = orc.orc_topk_select(ptr(scores), n_kv, IBLK, TOPK, ptr(sel))
-                orc.orc_attend(qg[t].ctypes.data, ptr(s["kq"]), ptr(s["ks"]), ptr(s["vq"]), ptr(s["vs"]), ptr(sel), n,
-                               QH, KVH, HD, att[t].ctypes.data)
+                # past the reference's VRAM ring the whole window runs its fp16 GQA kernel
+                # (`*h_pos + T > KV_VRAM_RING`, src/wzy_stage_v2.cuh:679-683)
+                fn = orc.orc_attend_pf if (f16_above > 0 and pos + T > f16_above) else orc.orc_attend
+                fn(qg[t].ctypes.data, ptr(s["kq"]), ptr(s["ks"]), ptr(s["vq"]), ptr(s["vs"]), ptr(sel), n,
+                   QH, KVH, HD, att[t].ctypes.data)
             block = q8_gemv(w["wo"], att, D, QD)
         out_dbg[l, 1] = block
         # ---- FFN half: the attention write (block, attention inject), then the FFN read
@@ -359,19 +363,25 @@ def model(wz, orc):
     return Model(wz, orc, 2024)
 
 
-def run_both(orc, m, plant=None):
+WINDOWS = ([7, 301, 42], [99], [5, 6])                # a 3-row window, a step, a 2-row window
+
+
+def run_both(orc, m, plant=None, f16_above=0):
     so, sc = m.state_copy(), m.state_copy()
     outs_o, outs_c = [], []
     pos = N_CTX
-    for toks in ([7, 301, 42], [99], [5, 6]):            # a 3-row window, a step, a 2-row window
-        outs_o.append(oracle_forward(orc, m, so, pos, toks))
-        outs_c.append(compose(orc, m, sc, pos, toks, plant))
+    for toks in WINDOWS:
+        outs_o.append(oracle_forward(orc, m, so, pos, toks, f16_above))
+        outs_c.append(compose(orc, m, sc, pos, toks, plant, f16_above))
         pos += len(toks)
     return outs_o, outs_c, so, sc
 
 
-def test_oracle_model_forward_matches_independent_composition(wz, orc, model):
-    outs_o, outs_c, so, sc = run_both(orc, model)
+# 0: the fp32 attention kernel throughout; 153: the 3-row window (cells 150-152) stays below the
+# threshold, the step at 153 and the window at 154-155 take the fp16 branch
+@pytest.mark.parametrize("f16_above", [0, 153])
+def test_oracle_model_forward_matches_independent_composition(wz, orc, model, f16_above):
+    outs_o, outs_c, so, sc = run_both(orc, model, f16_above=f16_above)
     for i, (o, c) in enumerate(zip(outs_o, outs_c)):
         lo_, go, po, do = o
         lc, gc, pc, dc = c
@@ -399,3 +409,31 @@ def test_composition_check_detects_wiring_mistakes(wz, orc, model, plant):
     outs_o, outs_c, _, _ = run_both(orc, model, plant)
     worst = max(max(max_violation(o[0], c[0]), max_violation(o[2], c[2])) for o, c in zip(outs_o, outs_c))
     assert worst > 0, "planted %s went unnoticed" % plant
+
+
+def test_attention_branch_switches_per_window(wz, orc, model):
+    """orc_model_forward takes the fp16 branch for exactly the windows with pos + T > attn_f16_above
+    (src/wzy_stage_v2.cuh:679: the whole window, not row by row).  The branches differ only in rounding
+    (inside the float tolerance, so the composition check cannot tell them apart), so this compares the
+    QSA layer's attention block of each window bit for bit against runs with the switch off and on
+    everywhere: a window below the threshold equals the fp32 run, one above equals the fp16 run, and
+    the two runs differ.  Windows: cells 150-152, 153, 154-155; a threshold of 152 puts the first
+    window (whose last row is cell 152, but pos + T = 153) on the fp16 branch, one of 153 does not."""
+    q = KINDS.index("qsa")
+
+    def blocks(f16_above):
+        st = model.state_copy()
+        out, pos = [], N_CTX
+        for toks in WINDOWS:
+            out.append(oracle_forward(orc, model, st, pos, toks, f16_above)[3][q, 1].copy())
+            pos += len(toks)
+        return out
+    b32, b16 = blocks(0), blocks(1)
+    assert all(not np.array_equal(a, b) for a, b in zip(b32, b16)), "the branches gave identical blocks"
+    for thr, want in ((152, (16, 16, 16)), (153, (32, 16, 16)), (155, (32, 32, 16)), (156, (32, 32, 32))):
+        got = blocks(thr)
+        # the QSA layer (layer 1) reads only the embedding and the GDN layer before it, so its inputs
+        # and KV / indexer state do not depend on which branch earlier windows took
+        for i, (g, w) in enumerate(zip(got, want)):
+            ref = b16[i] if w == 16 else b32[i]
+            assert np.array_equal(g, ref), "threshold %d window %d: not the fp%d branch" % (thr, i, w)

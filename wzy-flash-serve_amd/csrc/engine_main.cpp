@@ -23,6 +23,12 @@
 //                                     (WZY_SPEC_DEPTH, WZY_SPEC_MIN_P, WZY_SPEC_GATE, WZY_ADAPT_DEPTH)
 //   --spec-depth K / WZY_SPEC_FIXED=K every window offers exactly K drafts (no confidence gates)
 //   WZY_MTP_DVOCAB=N                  draft-vocabulary rows (default min(114452, n_vocab))
+//   --forced-drafts F                 testing the accept path: with --spec-depth, each window's drafts
+//                                     are replaced by tokens from file F (the drafter still runs, so its
+//                                     catch-up is exercised).  F holds two lines of token ids: a pattern
+//                                     a_0 a_1 ... (cycled over the windows: window i offers the next a_i
+//                                     tokens of the continuation, then wrong ones) and the continuation
+//                                     (the stream the engine is expected to generate, first token first)
 //   WZY_DEC_PROF=1                    per-request decode profile line on stderr
 // Exit status: 0 after QUIT/EXIT or end of input, 1 on any stage error (message on stderr), 2 on
 // bad options.
@@ -103,6 +109,7 @@ struct Options {
     wzy_spec_gates gates{5, 0.30f, 1.0f};
     bool adapt_depth = true;
     int prefill_chunk = 25600;    // cells per prefill chunk (the reference's PF_MAX default)
+    std::string forced_drafts;    // test file: draft pattern + expected continuation
 };
 
 // "k=v,k=v" onto wzy_stage_cfg by field name.
@@ -125,6 +132,7 @@ bool apply_cfg(wzy_stage_cfg& c, const std::string& spec) {
         {"kv_ring", &c.kv_ring, nullptr},     {"kv_sinks", &c.kv_sinks, nullptr},
         {"rope_theta", nullptr, &c.rope_theta}, {"eps", nullptr, &c.eps},
         {"emb_q8", &c.emb_q8, nullptr},       {"head_q8", &c.head_q8, nullptr},
+        {"attn_f16_above", &c.attn_f16_above, nullptr},
     };
     size_t at = 0;
     while (at < spec.size()) {
@@ -187,12 +195,17 @@ int parse_options(int argc, char** argv, Options& o) {
         else if (a == "--mtp") o.mtp = true;
         else if (a == "--spec-depth") o.spec_fixed = atoi(val()), o.mtp = true;
         else if (a == "--prefill-chunk") o.prefill_chunk = atoi(val());
+        else if (a == "--forced-drafts") o.forced_drafts = val();
         else {
             fprintf(stderr, "[wzy-engine] unknown option %s\n", a.c_str());
             return 2;
         }
     }
     if (o.spec_fixed > 0) o.mtp = true;
+    if (!o.forced_drafts.empty() && o.spec_fixed <= 0) {
+        fprintf(stderr, "[wzy-engine] --forced-drafts needs --spec-depth\n");
+        return 2;
+    }
     o.prefill_chunk = std::max(1, std::min(o.prefill_chunk, 25600));
     o.spec_fixed = std::min(o.spec_fixed, WZY_MAX_W - 1);
     o.gates.depth = std::max(1, std::min(o.gates.depth, WZY_MAX_W - 1));
@@ -214,6 +227,7 @@ class Engine {
     Engine(const Options& o, wzy_stage* st, const wzy_stage_cfg& c, Inbox& in)
         : o_(o), st_(st), c_(c), in_(in), rng_(o.have_seed ? o.seed : std::random_device{}()) {
         logits_.resize((size_t) WZY_MAX_W * c.n_vocab);
+        if (!o.forced_drafts.empty()) load_forced(o.forced_drafts);
     }
 
     // One request line (JSON or legacy), answered in the single-stream or multiplexed form.
@@ -362,6 +376,7 @@ class Engine {
                 const auto t_m = Clock::now();
                 propose(unfed_cell0, unfed_next, want_k, g, drafts);
                 mtp_ms += ms_since(t_m);
+                if (!forced_pattern_.empty()) force_drafts(wins, generated, drafts);
             }
             drafts_offered += (long long) drafts.size();
             win.assign(1, cur);
@@ -458,6 +473,41 @@ class Engine {
 
   private:
     enum Mode { kGreedy, kTop16, kFull };
+
+    // --forced-drafts: line 1 the pattern, line 2 the continuation (whitespace-separated ids)
+    void load_forced(const std::string& path) {
+        FILE* f = fopen(path.c_str(), "r");
+        if (!f) die("forced drafts: cannot open file");
+        std::vector<int>* dst = &forced_pattern_;
+        int ch, v = 0;
+        bool in_num = false;
+        while ((ch = fgetc(f)) != EOF) {
+            if (ch >= '0' && ch <= '9') {
+                v = v * 10 + (ch - '0');
+                in_num = true;
+                continue;
+            }
+            if (in_num) dst->push_back(v);
+            in_num = false;
+            v = 0;
+            if (ch == '\n' && dst == &forced_pattern_ && !forced_pattern_.empty()) dst = &forced_cont_;
+        }
+        if (in_num) dst->push_back(v);
+        fclose(f);
+        if (forced_pattern_.empty() || forced_cont_.empty()) die("forced drafts: need a pattern line and a continuation line");
+    }
+    // Window `win` (0-based) after `generated` emitted tokens: the drafts become the continuation's
+    // next a = pattern[win % len] tokens, then tokens that differ from the continuation's; the count
+    // the drafter proposed is kept (cut where the continuation ends).
+    void force_drafts(int win, int generated, std::vector<int>& drafts) {
+        const int a = forced_pattern_[(size_t) win % forced_pattern_.size()];
+        std::vector<int> out;
+        for (int j = 0; j < (int) drafts.size() && generated + j < (int) forced_cont_.size(); ++j) {
+            const int truth = forced_cont_[(size_t) generated + j];
+            out.push_back(j < a ? truth : (truth + 1) % c_.n_vocab);
+        }
+        drafts.swap(out);
+    }
 
     static constexpr int kMtpSeedTail = 512;   // prompt cells seeded into the drafter (src/wzy_mtp.cuh:12)
     static constexpr int kPrefillMin = 192;    // longer prompt remainders take the chunked prefill
@@ -563,6 +613,7 @@ class Engine {
     int greedy_[WZY_MAX_W] = {};
     float top_v_[WZY_MAX_W * 16] = {};
     int top_i_[WZY_MAX_W * 16] = {};
+    std::vector<int> forced_pattern_, forced_cont_;   // --forced-drafts (empty: the drafter's own)
 };
 
 // stdin reader: in multiplexed mode PING, CANCEL and QUIT are answered / recorded immediately (the

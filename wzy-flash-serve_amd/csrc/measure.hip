@@ -85,6 +85,7 @@ extern "C" int wzy_qsa_time_decode(const wzy_qsa_dims* dims, const wzy_qsa_layer
     dm.qh = dims->qh; dm.kvh = dims->kvh; dm.hd = dims->hd; dm.n_rot = dims->n_rot;
     dm.ih = dims->idx_heads; dm.idim = dims->idx_dim; dm.iblk = dims->idx_blk; dm.topk = dims->idx_topk;
     dm.ctx_max = dims->ctx_max; dm.ring_cap = dims->kv_ring; dm.sinks = dims->kv_sinks; dm.eps = dims->eps;
+    dm.f16_above = dims->attn_f16_above;
     WZY_TRY(qsa_check_dims(dm));
     WZY_REQUIRE(L->max_b >= dm.ctx_max / dm.iblk + 1, "qsa_time: max_b too small");
     QsaPrepArgs p{};

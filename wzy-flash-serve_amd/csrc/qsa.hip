@@ -267,6 +267,7 @@ static QsaDims dims_of(const wzy_qsa_dims* s) {
     d.qh = s->qh; d.kvh = s->kvh; d.hd = s->hd; d.n_rot = s->n_rot;
     d.ih = s->idx_heads; d.idim = s->idx_dim; d.iblk = s->idx_blk; d.topk = s->idx_topk;
     d.ctx_max = s->ctx_max; d.ring_cap = s->kv_ring; d.sinks = s->kv_sinks; d.eps = s->eps;
+    d.f16_above = s->attn_f16_above;
     return d;
 }
 

@@ -9,7 +9,10 @@
 //             loads, computes its heads' scores (wave = head, lane = cell), a local softmax, and the
 //             INT8 V sum (thread = dim).
 //  qsa_combine merges the chunks (max / sum rescaling) and applies sigmoid(gate).
-//             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532)
+//             reference: qsa_attend_int8_sparse_multi (src/wzy_qsa_256k.cuh:407-532); windows past
+//             the reference's VRAM ring take the operand rounding of its GQA kernel,
+//             pf_qsa_wmma_sparse_attn (src/wzy_qsa_wmma.cuh:289-488): fp16(q / 16), K and V as
+//             fp16(code * scale), fp16 softmax weights over 32-cell steps, fp32 sums.
 #include "wzy_device.h"
 #include "wzy_host.h"
 #include "wzy_qsa.h"
@@ -470,6 +473,8 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     if (c0 >= width) return;                         // workgroup-uniform
     const int ncell = min(QSA_ATT_CHUNK, width - c0);
     const int nch = (dm.topk + QSA_ATT_CHUNK - 1) / QSA_ATT_CHUNK;
+    // fp16 operands when the window reaches past f16_above cells (uniform over the launch)
+    const bool f16 = dm.f16_above > 0 && *a.pos + (int) gridDim.z > dm.f16_above;
 
     if (tid < QSA_ATT_CHUNK) {
         const int idx = c0 + tid;
@@ -482,9 +487,13 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     }
     {                                                // this slice's heads; rows past gq are zero
         const int hh = tid >> 6, d4 = tid & 63, h = hs * ATT_HPW + hh;
-        *(float4*) &s_q[hh][4 * d4] =
-            h < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + h) * 512 + 4 * d4)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 q = h < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + h) * 512 + 4 * d4)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (f16) {                                   // fp16(q / 16), as the reference's GQA kernel stages q
+            q.x = round_h16(q.x * 0.0625f); q.y = round_h16(q.y * 0.0625f);
+            q.z = round_h16(q.z * 0.0625f); q.w = round_h16(q.w * 0.0625f);
+        }
+        *(float4*) &s_q[hh][4 * d4] = q;
     }
     __syncthreads();
 
@@ -519,33 +528,69 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     {
         const int cell = lane;
         float acc = 0.f;
+        if (!f16) {                                  // int8 codes dotted with q, scaled per 64-group
 #pragma unroll 1
-        for (int g = 0; g < 4; ++g) {
-            float ag = 0.f;
+            for (int g = 0; g < 4; ++g) {
+                float ag = 0.f;
 #pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-                const int part = 4 * g + pp;
-                const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
-                const int8_t* kb = (const int8_t*) &kv;
-                const float4* qp = (const float4*) &s_q[w][part * 16];
-                const float4 q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
-                ag = fmaf((float) kb[0], q0.x, ag); ag = fmaf((float) kb[1], q0.y, ag);
-                ag = fmaf((float) kb[2], q0.z, ag); ag = fmaf((float) kb[3], q0.w, ag);
-                ag = fmaf((float) kb[4], q1.x, ag); ag = fmaf((float) kb[5], q1.y, ag);
-                ag = fmaf((float) kb[6], q1.z, ag); ag = fmaf((float) kb[7], q1.w, ag);
-                ag = fmaf((float) kb[8], q2.x, ag); ag = fmaf((float) kb[9], q2.y, ag);
-                ag = fmaf((float) kb[10], q2.z, ag); ag = fmaf((float) kb[11], q2.w, ag);
-                ag = fmaf((float) kb[12], q3.x, ag); ag = fmaf((float) kb[13], q3.y, ag);
-                ag = fmaf((float) kb[14], q3.z, ag); ag = fmaf((float) kb[15], q3.w, ag);
+                for (int pp = 0; pp < 4; ++pp) {
+                    const int part = 4 * g + pp;
+                    const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
+                    const int8_t* kb = (const int8_t*) &kv;
+                    const float4* qp = (const float4*) &s_q[w][part * 16];
+                    const float4 q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
+                    ag = fmaf((float) kb[0], q0.x, ag); ag = fmaf((float) kb[1], q0.y, ag);
+                    ag = fmaf((float) kb[2], q0.z, ag); ag = fmaf((float) kb[3], q0.w, ag);
+                    ag = fmaf((float) kb[4], q1.x, ag); ag = fmaf((float) kb[5], q1.y, ag);
+                    ag = fmaf((float) kb[6], q1.z, ag); ag = fmaf((float) kb[7], q1.w, ag);
+                    ag = fmaf((float) kb[8], q2.x, ag); ag = fmaf((float) kb[9], q2.y, ag);
+                    ag = fmaf((float) kb[10], q2.z, ag); ag = fmaf((float) kb[11], q2.w, ag);
+                    ag = fmaf((float) kb[12], q3.x, ag); ag = fmaf((float) kb[13], q3.y, ag);
+                    ag = fmaf((float) kb[14], q3.z, ag); ag = fmaf((float) kb[15], q3.w, ag);
+                }
+                acc = fmaf(ag, s_ks[cell][g], acc);
             }
-            acc = fmaf(ag, s_ks[cell][g], acc);
+            acc *= 0.0625f;
+        } else {                                     // fp16(code * scale) dotted with fp16(q / 16)
+#pragma unroll 1
+            for (int g = 0; g < 4; ++g) {
+                const float sc = s_ks[cell][g];
+#pragma unroll
+                for (int pp = 0; pp < 4; ++pp) {
+                    const int part = 4 * g + pp;
+                    const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
+                    const int8_t* kb = (const int8_t*) &kv;
+                    const float* qp = &s_q[w][part * 16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc = fmaf(round_h16((float) kb[i] * sc), qp[i], acc);
+                }
+            }
         }
         const int h = hs * ATT_HPW + w;
         if (h < gq) {                                // wave-uniform
-            const float s = cell < ncell ? acc * 0.0625f : -INFINITY;
-            const float m = wave_max(s);
-            const float e = cell < ncell ? __expf(s - m) : 0.f;
-            const float l = wave_sum(e);
+            const float s = cell < ncell ? acc : -INFINITY;
+            float m, e, l;
+            if (!f16) {
+                m = wave_max(s);
+                e = cell < ncell ? __expf(s - m) : 0.f;
+                l = wave_sum(e);
+            } else {
+                // the reference's online softmax over 32-cell steps (cells 0-31, 32-63 of the chunk):
+                // weights exp(s - m_step) rounded to fp16 for the V product, summed unrounded; the
+                // first step's weights rescaled by alpha = exp(m0 - m1) when the second step raises
+                // the running max (src/wzy_qsa_wmma.cuh:401-420).  The running max here starts at
+                // the chunk (the reference's carries over from earlier chunks): the fp16 rounding is
+                // relative either way, 2^-11 of a weight.
+                const float ms = max32(s);           // this lane's step maximum
+                const float m0 = as_f(__builtin_amdgcn_readlane(as_i(ms), 0));
+                const float m1 = fmaxf(m0, as_f(__builtin_amdgcn_readlane(as_i(ms), 32)));
+                const bool first = cell < 32;
+                const float ex = cell < ncell ? __expf(s - (first ? m0 : m1)) : 0.f;
+                const float alpha = first ? __expf(m0 - m1) : 1.0f;
+                l = wave_sum(ex * alpha);
+                e = round_h16(ex) * alpha;
+                m = m1;
+            }
             s_p[cell][w] = e;
             float* ml = a.part_ml + ((((size_t) t * dm.kvh + j) * nch + c) * gq + h) * 2;
             if (lane == 0) { ml[0] = m; ml[1] = l; }
@@ -563,7 +608,8 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
         for (int hh = 0; hh < ATT_HPW; ++hh) o[hh] = 0.f;
 #pragma unroll 4
         for (int cell = 0; cell < ncell; ++cell) {
-            const float pv = (float) s_v[cell * ATT_ROW + d] * s_vs[cell][d >> 6];
+            float pv = (float) s_v[cell * ATT_ROW + d] * s_vs[cell][d >> 6];
+            if (f16) pv = round_h16(pv);
             const float4 p = *(const float4*) s_p[cell];
             o[0] = fmaf(p.x, pv, o[0]);
             o[1] = fmaf(p.y, pv, o[1]);

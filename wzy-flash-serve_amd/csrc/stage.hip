@@ -242,11 +242,15 @@ struct wzy_stage {
 
     // per-layer trace of the last forward (direct launches while on): HC read outputs, block and
     // MoE outputs [n_layers][W][D], router logits / ids / weights [n_layers][W][E or K], and per QSA
-    // layer the block scores [n_qsa][W][max_b], selected cells [n_qsa][W][topk] and counts [n_qsa][W]
+    // layer the block scores [n_qsa][W][max_b], selected cells [n_qsa][W][topk] and counts [n_qsa][W],
+    // the rows the KV and indexer appends quantise (k after its norm + RoPE, v, the raw indexer key:
+    // [n_qsa][W][kvd or idim]), the q | gate rows the attention reads (after norm + RoPE,
+    // [n_qsa][W][2 qh hd]) and the attention output before the o projection ([n_qsa][W][qh hd])
     bool trace = false;
     float *tr_mixa = nullptr, *tr_block = nullptr, *tr_mixf = nullptr, *tr_comb = nullptr;
     float *tr_ra = nullptr, *tr_rf = nullptr, *tr_inja = nullptr, *tr_injf = nullptr;
     float *tr_logits = nullptr, *tr_wts = nullptr, *tr_scores = nullptr;
+    float *tr_kk = nullptr, *tr_vv = nullptr, *tr_iraw = nullptr, *tr_qg = nullptr, *tr_att = nullptr;
     int *tr_ids = nullptr, *tr_sel = nullptr, *tr_cnt = nullptr;
     int trace_alloc();
 
@@ -329,6 +333,7 @@ static int validate(const wzy_stage_cfg& c) {
     WZY_REQUIRE(c.n_exp >= 1 && c.n_exp <= 1024 && c.top_k >= 1 && c.top_k <= MOE_MAX_K && c.n_ff % 64 == 0,
                 "stage: bad MoE shape");
     WZY_REQUIRE(c.n_vocab >= 16 && c.ctx_max >= 8, "stage: bad vocab / context");
+    WZY_REQUIRE(c.attn_f16_above >= 0, "stage: attn_f16_above %d is negative", c.attn_f16_above);
     WZY_REQUIRE(2 * c.qsa_qh * c.qsa_hd <= 16384 && c.n_embd * 1 <= 8192, "stage: projection too wide");
     WZY_REQUIRE((c.n_vocab + 2047) / 2048 * 16 <= 2048, "stage: n_vocab too large for the top-16 merge");
     return qsa_check_ring(c.ctx_max, c.kv_ring, c.kv_sinks);
@@ -346,6 +351,7 @@ int wzy_stage::init_buffers() {
     qd.qh = c.qsa_qh; qd.kvh = c.qsa_kvh; qd.hd = c.qsa_hd; qd.n_rot = c.n_rot;
     qd.ih = c.idx_heads; qd.idim = c.idx_dim; qd.iblk = c.idx_blk; qd.topk = c.idx_topk;
     qd.ctx_max = c.ctx_max; qd.ring_cap = c.kv_ring; qd.sinks = c.kv_sinks; qd.eps = c.eps;
+    qd.f16_above = c.attn_f16_above;
     const size_t kv_slots = c.kv_ring > 0 ? (size_t) c.kv_ring : (size_t) c.ctx_max;
     const int W = WZY_MAX_W;
 
@@ -641,6 +647,10 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
                 p.ix.pool_snaps = pool_snaps + sl * 2 * c.idx_dim;
             }
             WZY_TRY(launch_qsa_prep(p, T, st));
+            WZY_TRY(tr(tr_kk, kk, w.local, KVD, 4));
+            WZY_TRY(tr(tr_vv, vv, w.local, KVD, 4));
+            WZY_TRY(tr(tr_iraw, idx_raw, w.local, c.idx_dim, 4));
+            WZY_TRY(tr(tr_qg, qg, w.local, 2 * QD, 4));
             QsaScoreArgs sa{};
             sa.dm = qd; sa.pos = d_pos; sa.pooled = w.ix.pooled; sa.dead = w.ix.dead; sa.q_idx = q_idx;
             sa.scores = scores; sa.max_b = max_b;
@@ -653,6 +663,7 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
             at.dm = qd; at.pos = d_pos; at.qg = qg; at.kv = w.kv; at.sel_ids = sel_ids; at.part = att_part;
             at.part_ml = att_ml; at.out = att_out;
             WZY_TRY(launch_qsa_attn(at, T, st));
+            WZY_TRY(tr(tr_att, att_out, w.local, QD, 4));
             GemvSegs o;
             o.n = 1;
             o.seg[0] = GemvSeg{w.wo.q, w.wo.s, block, D, GEMV_Q8, D, 0};
@@ -835,6 +846,7 @@ extern "C" void wzy_stage_cfg_default(wzy_stage_cfg* c, int ctx_max) {
     c->idx_heads = 4; c->idx_dim = 128; c->idx_blk = 4; c->idx_topk = 2048;
     c->n_exp = 512; c->top_k = 10; c->n_ff = 512; c->n_vocab = 151936;
     c->ctx_max = ctx_max; c->kv_ring = 0; c->kv_sinks = 0; c->rope_theta = 1e7f; c->eps = 1e-6f;
+    c->attn_f16_above = 32768;
 }
 
 extern "C" int wzy_stage_create(const wzy_stage_cfg* cfg, int device, wzy_stage** out) {
@@ -937,6 +949,11 @@ int wzy_stage::trace_alloc() {
     WZY_TRY(alloc_t(&tr_scores, nq * W * max_b)); reg(-1, "trace.scores", tr_scores, nq * W * max_b * 4);
     WZY_TRY(alloc_t(&tr_sel, nq * W * c.idx_topk)); reg(-1, "trace.sel_ids", tr_sel, nq * W * c.idx_topk * 4);
     WZY_TRY(alloc_t(&tr_cnt, nq * W)); reg(-1, "trace.sel_cnt", tr_cnt, nq * W * 4);
+    WZY_TRY(alloc_t(&tr_kk, nq * W * KVD)); reg(-1, "trace.kv_k_in", tr_kk, nq * W * KVD * 4);
+    WZY_TRY(alloc_t(&tr_vv, nq * W * KVD)); reg(-1, "trace.kv_v_in", tr_vv, nq * W * KVD * 4);
+    WZY_TRY(alloc_t(&tr_iraw, nq * W * c.idx_dim)); reg(-1, "trace.idx_raw", tr_iraw, nq * W * c.idx_dim * 4);
+    WZY_TRY(alloc_t(&tr_qg, nq * W * 2 * QD)); reg(-1, "trace.qg", tr_qg, nq * W * 2 * QD * 4);
+    WZY_TRY(alloc_t(&tr_att, nq * W * QD)); reg(-1, "trace.attn", tr_att, nq * W * QD * 4);
     return WZY_OK;
 }
 

@@ -15,6 +15,9 @@ struct QsaDims {
     float eps;
     int window = 0;                    // > 0: dense sliding-window attention over the last `window`
                                        // cells (no indexer; the ring may wrap, window <= ring_cap)
+    int f16_above = 0;                 // > 0: a window whose rows reach past this many cells
+                                       // (pos + T > f16_above) attends with fp16 operands, the
+                                       // numerics the reference switches to above its VRAM ring
 };
 
 // Attended span of a row whose context holds n_kv cells: positions p0 .. p0 + width - 1.  Sparse

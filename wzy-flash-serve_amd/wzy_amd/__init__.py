@@ -50,7 +50,7 @@ class QsaDims(C.Structure):
     """struct wzy_qsa_dims (include/wzy_kernels.h)"""
     _fields_ = [("qh", I32), ("kvh", I32), ("hd", I32), ("n_rot", I32),
                 ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
-                ("ctx_max", I32), ("kv_ring", I32), ("kv_sinks", I32), ("eps", F32)]
+                ("ctx_max", I32), ("kv_ring", I32), ("kv_sinks", I32), ("eps", F32), ("attn_f16_above", I32)]
 
 
 class QsaLayer(C.Structure):
@@ -69,7 +69,7 @@ class StageCfg(C.Structure):
                 ("n_rot", I32), ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
                 ("n_exp", I32), ("top_k", I32), ("n_ff", I32), ("n_vocab", I32), ("ctx_max", I32),
                 ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32),
-                ("emb_q8", I32), ("head_q8", I32)]
+                ("emb_q8", I32), ("head_q8", I32), ("attn_f16_above", I32)]
 
 
 WZY_MAX_STOPS = 64
