@@ -359,7 +359,14 @@ def mtp_config5(wz, st, cfg, pos0, windows, depth=3, n_dv=114452, seed=4, seed_c
         cont.append(t)
         p += 1
     assert wz.wzy_stage_session_restore(st.h, 0) == 0
-    forced, k_next = cont, 0
+    # the restored state has no pre-head rows for the drafter's catch-up: one plain step at `pos` gives
+    # them (and the continuation's first token), then the forced windows start after it
+    st.forward(pos, [cur])
+    st.sync()
+    assert int(st.greedy(1)[0]) == cont[0], "the restored state left the greedy stream"
+    unfed0, unfed, cur = pos, [cont[0]], cont[0]
+    pos += 1
+    forced, k_next = cont, 1
     window()                          # warm-up of the forced path (graph shapes are already captured)
     emitted = accepted = offered = 0
     t_prop = t_win = 0.0

@@ -129,8 +129,11 @@ static void gdn_head_step(float* S, const float* q, const float* k, const float*
 
 void orc_gdn_recurrence(const float* q, const float* k, const float* v, const float* decay, const float* beta,
                         const float* z, const float* gamma, float eps, float* state, float* y, int hk, int hv, int T) {
-    for (int t = 0; t < T; ++t)
-        for (int h = 0; h < hv; ++h) {
+    /* value heads are independent (each owns its state slice and output columns): heads in parallel,
+     * rows in order within a head -- the same arithmetic as the row-major loop */
+#pragma omp parallel for schedule(static) if (T * hv >= 256)
+    for (int h = 0; h < hv; ++h)
+        for (int t = 0; t < T; ++t) {
             const int kh = h % hk;
             gdn_head_step(state + (size_t) h * 128 * 128, q + (size_t) t * hk * 128 + kh * 128,
                           k + (size_t) t * hk * 128 + kh * 128, v + (size_t) t * hv * 128 + h * 128, decay[t * hv + h],

@@ -226,6 +226,7 @@ struct wzy_stage {
         int* tr_sel = nullptr;      // per QSA layer: selected cells [n_qsa][tr_rows][topk], counts
         int* tr_cnt = nullptr;      // [n_qsa][tr_rows]
         float* tr_sc = nullptr;     // block scores [n_qsa][tr_rows][max_b]
+        float* tr_kv = nullptr;     // rows the KV / indexer appends quantise: [n_qsa][tr_rows][kvd k | kvd v | idim]
         int tr_rows = 0;
     } pf;
     bool pre_head_pf = false;       // the pre-head rows of the last call are the prefill's residual
@@ -279,6 +280,7 @@ wzy_stage::~wzy_stage() {
     if (pf.tr) (void) hipFree(pf.tr);
     if (pf.tr_sel) (void) hipFree(pf.tr_sel);
     if (pf.tr_sc) (void) hipFree(pf.tr_sc);
+    if (pf.tr_kv) (void) hipFree(pf.tr_kv);
     for (auto& kv : graph_execs)
         if (kv.second) (void) hipGraphExecDestroy(kv.second);
     for (void* p : allocs) (void) hipFree(p);
@@ -1410,6 +1412,8 @@ int wzy_stage::prefill_reserve(int B) {
         if (pf.tr) WZY_HIP_TRY(hipFree(pf.tr));
         if (pf.tr_sel) WZY_HIP_TRY(hipFree(pf.tr_sel));
         if (pf.tr_sc) WZY_HIP_TRY(hipFree(pf.tr_sc));
+        if (pf.tr_kv) WZY_HIP_TRY(hipFree(pf.tr_kv));
+        pf.tr_kv = nullptr;
         pf.tr = nullptr;
         pf.tr_sel = pf.tr_cnt = nullptr;
         pf.tr_sc = nullptr;
@@ -1421,6 +1425,9 @@ int wzy_stage::prefill_reserve(int B) {
         const size_t nsc = nq * B * (size_t) max_b;
         WZY_HIP_TRY(hipMalloc((void**) &pf.tr_sc, nsc * 4));
         reg(-1, "trace.pf_scores", pf.tr_sc, nsc * 4);
+        const size_t nkv = nq * B * (size_t) (2 * KVD + c.idx_dim);
+        WZY_HIP_TRY(hipMalloc((void**) &pf.tr_kv, nkv * 4));
+        reg(-1, "trace.pf_kv", pf.tr_kv, nkv * 4);
         pf.tr_rows = B;
         reg(-1, "trace.pf", pf.tr, n * 4);
         reg(-1, "trace.pf_sel", pf.tr_sel, ns * 4);
@@ -1606,6 +1613,16 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
             pa.q_norm = w.q_norm; pa.k_norm = w.k_norm; pa.iq_norm = w.idx_qn; pa.cos_tab = cos_tab; pa.sin_tab = sin_tab;
             pa.kv = w.kv;
             WZY_TRY(launch_pf_qsa_prep(pa, B, st));
+            if (trace && pf.tr_kv) {                 // k (after norm + RoPE), v and the raw indexer key rows
+                const size_t rw = 2 * (size_t) KVD + ID;
+                float* dst = pf.tr_kv + (size_t) w.local * pf.tr_rows * rw;
+                WZY_HIP_TRY(hipMemcpy2DAsync(dst, rw * 4, pf.kk, (size_t) KVD * 4, (size_t) KVD * 4, B,
+                                             hipMemcpyDeviceToDevice, st));
+                WZY_HIP_TRY(hipMemcpy2DAsync(dst + KVD, rw * 4, pf.vv, (size_t) KVD * 4, (size_t) KVD * 4, B,
+                                             hipMemcpyDeviceToDevice, st));
+                WZY_HIP_TRY(hipMemcpy2DAsync(dst + 2 * KVD, rw * 4, pf.idx_raw, (size_t) ID * 4, (size_t) ID * 4, B,
+                                             hipMemcpyDeviceToDevice, st));
+            }
             PfIdxAppend ia{};
             ia.dm = dm; ia.idx_raw = pf.idx_raw; ia.ik_norm = w.idx_kn; ia.cos_tab = cos_tab; ia.sin_tab = sin_tab;
             ia.ix = w.ix;
