@@ -86,6 +86,17 @@ def check_attention_branch(tag, g, a_br, a_ot, f16, rtol=2e-3):
     return e_br, gap
 
 
+def key_flip_ok(y, a, b, key):
+    """Whether two fp16 codes a, b of one pooled indexer key element may both be roundings of the
+    oracle's unrounded value y: they are adjacent fp16 values and y lies at their midpoint within what
+    fp32 arithmetic can decide -- 2^-17 of y, or 2^-20 of the key's largest element (the RoPE rotation
+    forms small elements as differences of O(max) products, so their fp32 error is absolute)."""
+    lo, hi = sorted((float(np.uint16(a).view(np.float16)), float(np.uint16(b).view(np.float16))))
+    if np.nextafter(np.float16(lo), np.float16(np.inf)) != np.float16(hi):
+        return False
+    return abs(float(y) - 0.5 * (lo + hi)) <= 2.0 ** -17 * abs(float(y)) + 2.0 ** -20 * float(np.abs(key).max())
+
+
 def is_qsa(cfg, l):
     return (l % cfg.qsa_period) == cfg.qsa_period - 1
 

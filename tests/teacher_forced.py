@@ -48,7 +48,7 @@ import numpy as np
 
 import oracle_lib
 from oracle_lib import OrcMoeWeights, ptr
-from stage_oracle import attend, attn_f16
+from stage_oracle import attend, attn_f16, key_flip_ok
 
 RTOL, ATOL = 2e-2, 1e-2
 ATT_RTOL = 2e-3           # attention on identical inputs, relative to the row's largest output
@@ -270,13 +270,9 @@ class TeacherForced:
                     b, d = divmod(int(i), ID)
                     assert b == pos // blk and not np.isnan(key[d]), \
                         "%s: pooled key %d dim %d differs, and no block completed there" % (t, b, d)
-                    lo_, hi_ = sorted((np.uint16(g_pooled[i]).view(np.float16).astype(np.float64),
-                                       np.uint16(pooled[i]).view(np.float16).astype(np.float64)))
-                    mid = 0.5 * (lo_ + hi_)
-                    assert np.nextafter(np.float16(lo_), np.float16(np.inf)) == np.float16(hi_) and \
-                        abs(float(key[d]) - mid) <= 2.0 ** -17 * abs(float(key[d])), \
+                    assert key_flip_ok(key[d], g_pooled[i], pooled[i], key), \
                         "%s: pooled key %d dim %d: fp16 %r vs %r, unrounded key %r is not at their midpoint" % (
-                            t, b, d, lo_, hi_, float(key[d]))
+                            t, b, d, g_pooled[i], pooled[i], float(key[d]))
                     self.counts["key_midpoint_flips"] += 1
                 new_state[(l, "idx_tail")], new_state[(l, "idx_dead")], new_state[(l, "idx_pooled")] = \
                     g_tail, g_dead, g_pooled
