@@ -325,6 +325,39 @@ int wzy_qsa_time_decode(const wzy_qsa_dims* dims, const wzy_qsa_layer* layer, co
                         float* us_stages, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Per-layer embedding (PLE) at layer 1 of the reference's real model (not part of the synthetic
+ * BASELINE model)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Rows of the hashed 3-gram fp8 table (wzy_ple_table_rows() rows of head_bytes = n_embd / 16 codes,
+ * in device memory) for T window rows at positions *pos .. *pos+T-1 of tokens toks [T] (device):
+ * emb [T x n_embd] = the 16 heads' rows decoded (e4m3, NaN codes 0) times `scale`; emb_bf16 (nullable)
+ * the same rounded to bf16.  The tokens before the window are read from tok_hist [ctx_max] (device,
+ * cell p holding the token of position p), which the call extends with the window's tokens.  A
+ * context reaching past a missing token (position < 0) or `eos` hashes eos in its place.
+ * Replaces stage_ple_window + PleSrc::row (src/wzy_engine_v2.cu:943-978; src/wzy_stage_v2.cuh:215-324),
+ * which gather the rows on the host from the mmap-ed table. */
+uint64_t wzy_ple_table_rows(void);
+int wzy_ple_rows(const uint8_t* table, int head_bytes, float scale, int eos, const int* pos, const int* toks, int T,
+                 int* tok_hist, int ctx_max, float* emb, uint16_t* emb_bf16, void* stream);
+
+/* The PLE block on T rows of the hyper-connection streams R [T x hc x n_embd] (in place), decode form:
+ * the pending write bo [T x n_embd] (nullable) with inject inj_prev [T x hc] folded in first, then
+ * q = groupnorm(R, norm_q), k = groupnorm(wk . emb, norm_k), v = wv . emb (bf16 weights wk
+ * [hc*n_embd x n_embd], wv [n_embd x n_embd]), gate sigmoid(sign(s) sqrt(max(|s|, 1e-6))) of
+ * s = k_c . q_c / sqrt(n_embd), gat = v * gate, n = groupnorm(gat, norm_c), and per channel the
+ * 4-tap conv over its history hist [hc*n_embd x 9] (taps at 9, 6, 3 rows back and the current row,
+ * conv_w [hc*n_embd x 4]): R += gat + silu(conv).  hist_snaps (nullable) [T x hc*n_embd x 9] receives
+ * the history after each row.  workspace: wzy_ple_workspace_bytes(n_embd, hc, T) bytes.
+ * Replaces the PLE block of record_forward (src/wzy_stage_v2.cuh:583-597: ple_group_multi,
+ * dense_bf16, ple_gate_gv_multi, ple_conv_multi, src/wzy_kernels_v2.cuh:1299-1374). */
+size_t wzy_ple_workspace_bytes(int n_embd, int hc, int T);
+int wzy_ple_block(float* R, const float* bo, const float* inj_prev, const float* emb, const uint16_t* wk,
+                  const uint16_t* wv, const float* norm_q, const float* norm_k, const float* norm_c,
+                  const float* conv_w, float* hist, int n_embd, int hc, float eps, int T, float* hist_snaps,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Logit reductions
  * ------------------------------------------------------------------------------------------- */
 

@@ -55,6 +55,10 @@ typedef struct wzy_stage_cfg {
                                                   the fp16 operands of the reference's GQA kernel
                                                   (src/wzy_stage_v2.cuh:679-683); 0 = fp32 attention at
                                                   every context */
+    int ple;                                   /* 0 (BASELINE synthetic model); 1: the reference model's
+                                                  per-layer embedding at layer 1 (hashed 3-gram rows of
+                                                  an fp8 table in HBM, src/wzy_stage_v2.cuh:583-597) */
+    int ple_eos;                               /* end-of-sequence id of the PLE context (248044) */
 } wzy_stage_cfg;
 
 typedef struct wzy_stage wzy_stage;

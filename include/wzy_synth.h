@@ -56,6 +56,12 @@ void wzy_synth_kv_host(uint64_t seed, int layer, int is_v, int64_t first_pos, in
 int wzy_synth_kv_device(uint64_t seed, int layer, int is_v, int64_t first_pos, int n_cells, int kvd,
                         int8_t* codes, uint16_t* scales, void* stream);
 
+/* Synthetic per-layer-embedding table: row `row` (head_bytes fp8 codes: random sign and mantissa,
+ * exponent field 4..9), host version, and the whole wzy_ple_table_rows() x head_bytes table in device
+ * memory (identical bytes). */
+void wzy_synth_ple_row(uint64_t seed, uint64_t row, int head_bytes, uint8_t* out);
+int wzy_synth_ple_table_device(uint64_t seed, int head_bytes, uint8_t* table, void* stream);
+
 /* IEEE half conversions used by the generator (round-to-nearest-even). */
 uint16_t wzy_f32_to_f16(float f);
 float wzy_f16_to_f32(uint16_t h);

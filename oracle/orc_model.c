@@ -142,6 +142,18 @@ int orc_model_forward_trace(const orc_model* m, int pos, const int* toks, int T,
 
     for (int l = 0; l < m->n_layers && rc == 0; ++l) {
         const orc_layer* w = &m->layers[l];
+        if (l == 1 && m->ple) {
+            /* PLE at layer 1 (src/wzy_stage_v2.cuh:583-597): the pending FFN write of layer 0 is folded
+             * into the streams first, the block adds to them, and the attention read folds nothing */
+            const orc_ple_w* p = m->ple;
+            float* pe = (float*) malloc(sizeof(float) * (size_t) T * D);
+            orc_ple_rows(p->row, p->row_ctx, D / ORC_PLE_HEADS, p->scale, p->eos, toks, T, pos, p->tok_hist, pe);
+            orc_ple_block(R[cur], pend_bo, pend_inj, pe, p->wk, p->wv, p->norm_q, p->norm_k, p->norm_c, p->conv_w,
+                          p->hist, D, HC, m->eps, T, 0, NULL);
+            free(pe);
+            pend_bo = NULL;
+            pend_inj = NULL;
+        }
         /* attention half */
         orc_hc_read(l == 0 ? NULL : R[cur], l == 0 ? emb : NULL, pend_bo, pend_inj, w->hc_norm[0], w->hc_down_q[0],
                     w->hc_down_s[0], w->hc_inj[0], w->hc_up_q[0], w->hc_up_s[0], D, HC, L, m->eps, T, R[cur ^ 1], nsc, lo,

@@ -243,6 +243,17 @@ int orc_model_prefill_dbg(const orc_model* m, int pos, const int* toks, int B, f
     for (int l = 0; l < m->n_layers && rc == 0; ++l) {
         const orc_layer* w = &m->layers[l];
         float* dl = dbg ? dbg + (size_t) l * 4 * B * D : NULL;     /* [mixed_a | block | mixed_f | comb] */
+        if (l == 1 && m->ple) {
+            /* PLE at layer 1 (src/wzy_prefill_tc.cuh:808-823), its projections on bf16 operands */
+            const orc_ple_w* p = m->ple;
+            float* pe = (float*) malloc(sizeof(float) * (size_t) B * D);
+            orc_ple_rows(p->row, p->row_ctx, D / ORC_PLE_HEADS, p->scale, p->eos, toks, B, pos, p->tok_hist, pe);
+            orc_ple_block(R, pend_bo, pend_inj, pe, p->wk, p->wv, p->norm_q, p->norm_k, p->norm_c, p->conv_w, p->hist,
+                          D, HC, m->eps, B, 1, NULL);
+            free(pe);
+            pend_bo = NULL;
+            pend_inj = NULL;
+        }
         orc_hc_read_pf(R, pend_bo, pend_inj, w->hc_norm[0], w->hc_down_q[0], w->hc_down_s[0], w->hc_inj[0],
                        w->hc_up_q[0], w->hc_up_s[0], D, HC, L, m->eps, B, inj_a, mixed);
         if (dl) memcpy(dl, mixed, sizeof(float) * (size_t) B * D);

@@ -138,6 +138,19 @@ typedef struct orc_layer {
     const int8_t* sh_down_q; const uint16_t* sh_down_s;
 } orc_layer;
 
+/* PLE weights, table access and state of a model whose layer 1 carries the per-layer embedding
+ * (orc_ple.c; NULL in orc_model: no PLE, the BASELINE synthetic model) */
+typedef const uint8_t* (*orc_ple_row_fn)(void* ctx, uint32_t row);   /* the table row's head bytes */
+typedef struct orc_ple_w {
+    orc_ple_row_fn row; void* row_ctx;      /* fp8 table rows (16 heads x head bytes per token) */
+    float scale; int eos;                   /* table scale (strata.ple.scale), end-of-sequence id */
+    const uint16_t* wk; const uint16_t* wv; /* bf16 [HC*D x D], [D x D] */
+    const float* norm_q; const float* norm_k; const float* norm_c;   /* [HC*D] */
+    const float* conv_w;                    /* [HC*D x 4] */
+    float* hist;                            /* [HC*D x 9] state */
+    int* tok_hist;                          /* [ctx_max] token of each cell, written by every window */
+} orc_ple_w;
+
 typedef struct orc_model {
     int n_layers, n_embd, hc, hc_lr, gdn_hk, gdn_hv, qsa_qh, qsa_kvh, qsa_hd, n_rot;
     int idx_heads, idx_dim, idx_blk, idx_topk, n_exp, top_k, n_ff, n_vocab, ctx_max;
@@ -157,6 +170,7 @@ typedef struct orc_model {
      * kernel past its VRAM ring (KV_VRAM_RING = 32,768; src/wzy_stage_v2.cuh:679-683); 0 or below:
      * orc_attend (qsa_attend_int8_sparse_multi) at every context */
     int attn_f16_above;
+    const orc_ple_w* ple;      /* per-layer embedding at layer 1, or NULL (src/wzy_stage_v2.cuh:583-597) */
 } orc_model;
 
 /* logits [T x n_vocab], greedy [T] and pre_head [T x hc x n_embd] (optional); returns 0 or -1. */
@@ -280,6 +294,19 @@ int orc_cpu_pool_threads(const orc_cpu_pool* p);
  * CpuMoePool::run (src/wzy_cpu_moe.cuh:590-614); xq16/xs16 are per-16 activations [T x D]. */
 int orc_cpu_pool_run(orc_cpu_pool* p, const uint8_t* const* blobs, const int* ids, const float* wts, int T, int K,
                      const int8_t* xq16, const float* xs16, float* out);
+
+/* ---- per-layer embedding at layer 1 (src/wzy_engine_v2.cu:909-978; src/wzy_stage_v2.cuh:215-324,583-597;
+ *      src/wzy_kernels_v2.cuh:1299-1374); orc_ple.c ---- */
+#define ORC_PLE_HEADS 16
+uint64_t orc_ple_table_rows(void);
+void orc_ple_row_ids(int cur, int prev1, int prev2, int eos, uint32_t* rows);
+float orc_ple_fp8(uint8_t v, float scale);
+void orc_ple_rows(orc_ple_row_fn row, void* ctx, int head, float scale, int eos, const int* toks, int T, int pos,
+                  int* tok_hist, float* out);
+void orc_ple_block(float* R, const float* bo, const float* inj_prev, const float* emb, const uint16_t* wk,
+                   const uint16_t* wv, const float* norm_q, const float* norm_k, const float* norm_c,
+                   const float* conv_w, float* hist, int D, int HC, float eps, int T, int emb_bf16,
+                   float* hist_snaps);
 
 #ifdef __cplusplus
 }

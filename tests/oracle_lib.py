@@ -53,6 +53,11 @@ _SIGS = {
     "orc_q2_expert_down": (None, [P, I32, I32, P, P, P]),
     "orc_mtp_front": (None, [P, I32, P, P, I32, P, P, P]),
     "orc_mtp_step": (I32, [P, I32, I32, P, P, P, P, P, P]),
+    "orc_ple_table_rows": (C.c_uint64, []),
+    "orc_ple_row_ids": (None, [I32, I32, I32, I32, P]),
+    "orc_ple_fp8": (F32, [C.c_uint8, F32]),
+    "orc_ple_rows": (None, [P, P, I32, F32, I32, P, I32, I32, P, P]),
+    "orc_ple_block": (None, [P, P, P, P, P, P, P, P, P, P, P, I32, I32, F32, I32, I32, P]),
     "orc_cpu_pool_create": (P, [I32, I32, I32]),
     "orc_cpu_pool_destroy": (None, [P]),
     "orc_cpu_pool_threads": (I32, [P]),

@@ -70,6 +70,14 @@ def stage_weights(om, cfg):
         layers.append(w)
         state.append(s)
     glob = {"cos": A[(-1, "rope_cos")], "sin": A[(-1, "rope_sin")]}
+    if getattr(cfg, "ple", 0):
+        # per-layer embedding at layer 1: weights and the oracle's table access in glob, the conv
+        # history and the token history in layer 1's state
+        pw = om.ple_w
+        glob["ple"] = {"w": pw, "wk": A[(1, "ple_key")], "wv": A[(1, "ple_value")], "nq": A[(1, "ple_norm_query")],
+                       "nk": A[(1, "ple_norm_key")], "nc": A[(1, "ple_norm_conv")], "cw": A[(1, "ple_conv1d")]}
+        state[1]["ple_hist"] = A[(1, "ple_hist")]
+        state[1]["tok_hist"] = A[(-1, "tok_hist")]
     if cfg.emb_q8:
         glob["emb_q"], glob["emb_s"] = A[(-1, "emb.q")], A[(-1, "emb.s")]
     else:
@@ -162,6 +170,19 @@ def compose_prefill(orc, dm, layers, state, glob, pos, toks, plant=None, moe=Non
     pend = None
     for l, w in enumerate(layers):
         s = state[l]
+        if l == 1 and "ple" in glob:
+            # the per-layer embedding (src/wzy_prefill_tc.cuh:808-823): the pending FFN write folded into
+            # the streams, the block added to them (bf16 GEMM operands), nothing left pending
+            pg = glob["ple"]
+            emb = np.empty((B, D), np.float32)
+            tk = np.ascontiguousarray(toks, np.int32)
+            orc.orc_ple_rows(C.cast(pg["w"].row, C.c_void_p), None, D // 16, pg["w"].scale, pg["w"].eos, tk.ctypes.data,
+                             B, pos, s["tok_hist"].ctypes.data, emb.ctypes.data)
+            R = np.ascontiguousarray(R, np.float32)
+            bo, ip = (pend if pend is not None else (None, None))
+            orc.orc_ple_block(ptr(R), ptr(bo), ptr(ip), ptr(emb), ptr(pg["wk"]), ptr(pg["wv"]), ptr(pg["nq"]),
+                              ptr(pg["nk"]), ptr(pg["nc"]), ptr(pg["cw"]), ptr(s["ple_hist"]), D, HC, dm.EPS, B, 1, None)
+            pend = None
         if pend is not None and plant != "drop_pending_fold":
             R, mixed, inj_a = read(R, w, 0, *pend)
         else:

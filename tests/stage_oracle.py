@@ -39,7 +39,16 @@ class OrcModel(C.Structure):
                 ("emb", P), ("head_norm", P), ("head_down_q", P), ("head_down_s", P), ("head_up_q", P),
                 ("head_up_s", P), ("head", P), ("cos_tab", P), ("sin_tab", P),
                 ("blob", BLOB_FN), ("blob_ctx", P),
-                ("emb_q", P), ("emb_s", P), ("head_q", P), ("head_s", P), ("attn_f16_above", I32)]
+                ("emb_q", P), ("emb_s", P), ("head_q", P), ("head_s", P), ("attn_f16_above", I32), ("ple", P)]
+
+
+PLE_ROW_FN = C.CFUNCTYPE(P, P, C.c_uint32)
+
+
+class OrcPle(C.Structure):
+    """struct orc_ple_w (oracle/wzy_oracle.h)"""
+    _fields_ = [("row", PLE_ROW_FN), ("row_ctx", P), ("scale", F32), ("eos", I32), ("wk", P), ("wv", P),
+                ("norm_q", P), ("norm_k", P), ("norm_c", P), ("conv_w", P), ("hist", P), ("tok_hist", P)]
 
 
 class OrcTrace(C.Structure):
@@ -183,6 +192,30 @@ class OracleModel:
         self._blob_cb = BLOB_FN(blob_fn)
         m.blob = self._blob_cb
         m.blob_ctx = None
+        if getattr(cfg, "ple", 0):
+            # the per-layer embedding: weights and state from the stage, table rows read from the stage's
+            # table (its bytes are an input like every weight) as the oracle asks for them
+            head = cfg.n_embd // 16
+            self.ple_rows = {}
+
+            def row_fn(ctx, r):
+                b = self.ple_rows.get(r)
+                if b is None:
+                    b = st.read_range(-1, "ple_table", np.uint8, int(r) * head, head)
+                    self.ple_rows[r] = b
+                return b.ctypes.data
+
+            self._ple_cb = PLE_ROW_FN(row_fn)
+            pw = OrcPle()
+            pw.row, pw.row_ctx = self._ple_cb, None
+            pw.scale = float(st.read(-1, "ple_scale", np.float32)[0])
+            pw.eos = cfg.ple_eos
+            pw.wk, pw.wv = rd(1, "ple_key", np.uint16), rd(1, "ple_value", np.uint16)
+            pw.norm_q, pw.norm_k = rd(1, "ple_norm_query", np.float32), rd(1, "ple_norm_key", np.float32)
+            pw.norm_c, pw.conv_w = rd(1, "ple_norm_conv", np.float32), rd(1, "ple_conv1d", np.float32)
+            pw.hist, pw.tok_hist = rd(1, "ple_hist", np.float32), rd(-1, "tok_hist", np.int32)
+            self.ple_w = pw
+            m.ple = C.cast(C.pointer(pw), P)
         self.model = m
         self.orc = oracle_lib.load()
         self.orc.orc_model_forward_dbg.restype = I32
@@ -277,6 +310,7 @@ def small_cfg(wz_mod, ctx_max=1024, n_layers=4, topk=64, qsa_period=2):
     c.ctx_max, c.kv_ring, c.kv_sinks = ctx_max, 0, 0
     c.rope_theta, c.eps = 1e7, 1e-6
     c.attn_f16_above = 32768               # the reference's VRAM ring (src/wzy_stage_v2.cuh:679)
+    c.ple, c.ple_eos = 0, 248044           # PLE off (the synthetic model); the reference's PLE_EOS
     return c
 
 

@@ -85,7 +85,8 @@ class TeacherForced:
         self.qsa_layers = list(om.qsa_layers)
         self.state = {}
         for (l, name), a in om.arrays.items():
-            if name in ("conv_hist", "ssm", "idx_tail", "idx_dead", "idx_pooled", "kv_k", "kv_ks", "kv_v", "kv_vs"):
+            if name in ("conv_hist", "ssm", "idx_tail", "idx_dead", "idx_pooled", "kv_k", "kv_ks", "kv_v", "kv_vs",
+                        "ple_hist", "tok_hist"):
                 self.state[(l, name)] = a.copy()
         self.worst = {}
         self.worst_plain = {}
@@ -191,6 +192,29 @@ class TeacherForced:
             if l == 0:
                 emb_row = bf16_to_f32(self.emb[tok])
                 R_a, mixa, inj_a = self._hc_read(l, 0, None, emb_row, None, None)
+            elif l == 1 and getattr(cfg, "ple", 0):
+                # per-layer embedding: the row's table rows, the block on the GPU's layer-0 outputs and the
+                # pre-row conv history; the attention read then folds nothing
+                pw = self.om.ple_w
+                th = self.state[(-1, "tok_hist")].copy()
+                emb = np.empty(D, np.float32)
+                tk = np.array([tok], np.int32)
+                orc.orc_ple_rows(C.cast(pw.row, C.c_void_p), None, D // 16, pw.scale, pw.eos, tk.ctypes.data, 1, pos,
+                                 th.ctypes.data, emb.ctypes.data)
+                R = np.ascontiguousarray(g["R_f"][0, 0], np.float32).copy()
+                hist = self.state[(1, "ple_hist")].copy()
+                bo, ip = np.ascontiguousarray(g["hidden"][0, 3, 0]), np.ascontiguousarray(g["inj_f"][0, 0])
+                A = self.A
+                orc.orc_ple_block(ptr(R), ptr(bo), ptr(ip), ptr(emb), ptr(A[(1, "ple_key")]), ptr(A[(1, "ple_value")]),
+                                  ptr(A[(1, "ple_norm_query")]), ptr(A[(1, "ple_norm_key")]),
+                                  ptr(A[(1, "ple_norm_conv")]), ptr(A[(1, "ple_conv1d")]), ptr(hist), D, HC, cfg.eps, 1,
+                                  0, None)
+                g_hist = st.read(1, "ple_hist", np.float32)
+                self._cmp("PLE conv history", g_hist, hist, t)
+                new_state[(1, "ple_hist")] = g_hist
+                new_state[(-1, "tok_hist")] = st.read(-1, "tok_hist", np.int32)
+                assert new_state[(-1, "tok_hist")][pos] == tok, "%s: token history at %d" % (t, pos)
+                R_a, mixa, inj_a = self._hc_read(l, 0, R, None, None, None)
             else:
                 R_a, mixa, inj_a = self._hc_read(l, 0, g["R_f"][l - 1, 0], None, g["hidden"][l - 1, 3, 0],
                                                  g["inj_f"][l - 1, 0])

@@ -314,6 +314,12 @@ def check_chunk(wz, orc, st, om, cfg, p0, toks, label):
             for name in ("idx_tail", "idx_dead"):
                 np.testing.assert_allclose(st.read(l, name, np.float32), s[name], rtol=RTOL, atol=ATOL,
                                            err_msg="%s layer %d %s" % (label, l, name))
+    if "ple_hist" in state0[1]:
+        # the per-layer embedding's conv history after the chunk, and the chunk's tokens in the history
+        g = st.read(1, "ple_hist", np.float32)
+        bad = np.abs(g - state0[1]["ple_hist"]) > ATOL + RTOL * np.abs(state0[1]["ple_hist"])
+        assert not bad.any(), "%s PLE conv history: %d beyond tolerance" % (label, bad.sum())
+        assert np.array_equal(st.read_range(-1, "tok_hist", np.int32, p0, B), np.asarray(toks, np.int32))
     print("%s: %d of %d MoE rows compared (the rest within 1e-4 of a routing tie), %d selections bit-exact on the "
           "GPU's scores (%d also equal to the composition's own), %d KV bytes bit-exact on the GPU's rows, %d "
           "pooled-key fp16 midpoint flips, every layer and the state within tolerance" % (

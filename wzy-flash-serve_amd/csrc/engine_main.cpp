@@ -132,7 +132,8 @@ bool apply_cfg(wzy_stage_cfg& c, const std::string& spec) {
         {"kv_ring", &c.kv_ring, nullptr},     {"kv_sinks", &c.kv_sinks, nullptr},
         {"rope_theta", nullptr, &c.rope_theta}, {"eps", nullptr, &c.eps},
         {"emb_q8", &c.emb_q8, nullptr},       {"head_q8", &c.head_q8, nullptr},
-        {"attn_f16_above", &c.attn_f16_above, nullptr},
+        {"attn_f16_above", &c.attn_f16_above, nullptr}, {"ple", &c.ple, nullptr},
+        {"ple_eos", &c.ple_eos, nullptr},
     };
     size_t at = 0;
     while (at < spec.size()) {

@@ -23,6 +23,7 @@
 #include "wzy_gdn.h"
 #include "wzy_gemv.h"
 #include "wzy_hc.h"
+#include "wzy_ple.h"
 #include "wzy_host.h"
 #include "wzy_moe.h"
 #include "wzy_mtp.h"
@@ -54,6 +55,8 @@ enum TensorId {
     TI_IDXQN = 48, TI_IDXKN = 49,
     TI_EMB = 60, TI_HEAD_NORM = 61, TI_HEAD_DOWN = 62, TI_HEAD_UP = 63, TI_HEAD = 64,
     TS_CONV = 70, TS_SSM = 71, TS_TAIL = 72, TS_DEAD = 73, TS_POOLED = 74,
+    TI_PLE_K = 80, TI_PLE_V = 81, TI_PLE_NQ = 82, TI_PLE_NK = 83, TI_PLE_NC = 84, TI_PLE_CONV = 85,
+    TS_PLE_HIST = 86, TS_PLE_TOKS = 87,
 };
 constexpr uint32_t MODEL_LAYER = 0xFFFF;
 
@@ -193,6 +196,20 @@ struct wzy_stage {
     bool loaded = false;
     MtpState* mtp = nullptr;        // MTP drafter (wzy_stage_mtp_init)
 
+    // per-layer embedding at layer 1 (cfg.ple): weights, the fp8 table, state and W-row scratch
+    struct Ple {
+        uint16_t *wk = nullptr, *wv = nullptr;                  // bf16 [HCD x D], [D x D]
+        float *nq = nullptr, *nk = nullptr, *nc = nullptr;      // [HCD]
+        float* cw = nullptr;                                    // [HCD x 4]
+        float* hist = nullptr;                                  // [HCD x 9] state
+        float* snaps = nullptr;                                 // [W][HCD x 9]
+        uint8_t* table = nullptr;                               // [ple_table_rows() x D/16] fp8
+        float* scale_dev = nullptr;                             // the table scale (also kept on the host)
+        float scale = 0.125f;
+        int* tok_hist = nullptr;                                // [ctx_max + 4] token of each cell
+        float *emb = nullptr, *k = nullptr, *v = nullptr, *gat = nullptr, *n = nullptr;   // W rows
+    } ple;
+
     // parked sessions: per slot one HBM buffer holding a copy of the session state, and the
     // device tables of the copies that save and restore it (one copy_jobs_kernel launch each)
     struct SessionSlot {
@@ -220,6 +237,8 @@ struct wzy_stage {
         void* moe_ws = nullptr;
         size_t moe_bytes = 0;
         int* toks = nullptr;
+        float *ple_emb = nullptr, *ple_k = nullptr, *ple_v = nullptr, *ple_gat = nullptr, *ple_n = nullptr;
+        uint16_t* ple_embh = nullptr;   // the PLE rows as the bf16 GEMM operand
         int* pos8 = nullptr;        // [cap / 8 + 2]: p0 + 8 i
         int sc_rows = 0;            // rows per block-score pass
         float* tr = nullptr;        // per-layer trace [n_layers][4][tr_rows][D] (while tracing)
@@ -336,6 +355,8 @@ static int validate(const wzy_stage_cfg& c) {
                 "stage: bad MoE shape");
     WZY_REQUIRE(c.n_vocab >= 16 && c.ctx_max >= 8, "stage: bad vocab / context");
     WZY_REQUIRE(c.attn_f16_above >= 0, "stage: attn_f16_above %d is negative", c.attn_f16_above);
+    WZY_REQUIRE(!c.ple || (c.n_layers >= 2 && c.n_embd % 16 == 0 && c.n_embd <= 4096),
+                "stage: the per-layer embedding needs layer 1 and n_embd a multiple of 16 (<= 4096)");
     WZY_REQUIRE(2 * c.qsa_qh * c.qsa_hd <= 16384 && c.n_embd * 1 <= 8192, "stage: projection too wide");
     WZY_REQUIRE((c.n_vocab + 2047) / 2048 * 16 <= 2048, "stage: n_vocab too large for the top-16 merge");
     return qsa_check_ring(c.ctx_max, c.kv_ring, c.kv_sinks);
@@ -432,6 +453,23 @@ int wzy_stage::init_buffers() {
     WZY_TRY(alloc_q8(head_up, HCD, c.hc_lr, -1, "head_up"));
     if (c.head_q8) WZY_TRY(alloc_q8(head8, c.n_vocab, D, -1, "head"));
     else { WZY_TRY(alloc_t(&head, (size_t) c.n_vocab * D, false)); reg(-1, "head", head, (size_t) c.n_vocab * D * 2); }
+    if (c.ple) {
+        const size_t hcd = (size_t) HCD, tb = (size_t) ple_table_rows() * (size_t) (D / PLE_HEADS);
+        WZY_TRY(alloc_t(&ple.wk, hcd * D, false)); reg(1, "ple_key", ple.wk, hcd * D * 2);
+        WZY_TRY(alloc_t(&ple.wv, (size_t) D * D, false)); reg(1, "ple_value", ple.wv, (size_t) D * D * 2);
+        WZY_TRY(alloc_t(&ple.nq, hcd, false)); reg(1, "ple_norm_query", ple.nq, hcd * 4);
+        WZY_TRY(alloc_t(&ple.nk, hcd, false)); reg(1, "ple_norm_key", ple.nk, hcd * 4);
+        WZY_TRY(alloc_t(&ple.nc, hcd, false)); reg(1, "ple_norm_conv", ple.nc, hcd * 4);
+        WZY_TRY(alloc_t(&ple.cw, hcd * 4, false)); reg(1, "ple_conv1d", ple.cw, hcd * 16);
+        WZY_TRY(alloc_t(&ple.hist, hcd * PLE_HIST)); reg(1, "ple_hist", ple.hist, hcd * PLE_HIST * 4);
+        WZY_TRY(alloc_t(&ple.snaps, (size_t) W * hcd * PLE_HIST));
+        WZY_TRY(alloc_t(&ple.table, tb, false)); reg(-1, "ple_table", ple.table, tb);
+        WZY_TRY(alloc_t(&ple.scale_dev, 1)); reg(-1, "ple_scale", ple.scale_dev, 4);
+        WZY_TRY(alloc_t(&ple.tok_hist, (size_t) c.ctx_max + 4)); reg(-1, "tok_hist", ple.tok_hist, (size_t) c.ctx_max * 4);
+        WZY_TRY(alloc_t(&ple.emb, (size_t) W * D)); WZY_TRY(alloc_t(&ple.v, (size_t) W * D));
+        WZY_TRY(alloc_t(&ple.k, (size_t) W * hcd)); WZY_TRY(alloc_t(&ple.gat, (size_t) W * hcd));
+        WZY_TRY(alloc_t(&ple.n, (size_t) W * hcd));
+    }
 
     // RoPE tables: fp64 angles rounded to fp32 (src/wzy_qsa_256k.cuh:34-46)
     {
@@ -535,6 +573,9 @@ int wzy_stage::init_buffers() {
                                          (size_t) 2 * c.idx_dim * 2, (size_t) 2 * c.idx_dim * 2, 1, 1});
             }
         }
+        if (c.ple)        // the PLE conv history of the accepted row (commit_window_state, :953-956)
+            jobs.push_back(CommitJob{(unsigned char*) ple.hist, (const unsigned char*) ple.snaps,
+                                     (size_t) HCD * PLE_HIST * 4, (size_t) HCD * PLE_HIST * 4, 0, 0});
         for (const CommitJob& j : jobs)
             WZY_REQUIRE(j.bytes % 16 == 0 && j.src_stride % 16 == 0, "stage: snapshot sizes must be multiples of 16 bytes");
         n_commit_jobs = (int) jobs.size();
@@ -601,6 +642,29 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
 
     for (int l = 0; l < c.n_layers; ++l) {
         Layer& w = L[l];
+        if (l == 1 && c.ple) {
+            // per-layer embedding (src/wzy_stage_v2.cuh:583-597): the table rows of the window's
+            // 3-gram contexts, their k / v projections, then the block folds layer 0's pending FFN
+            // write into the streams and adds to them; the attention read below folds nothing
+            PleRowsArgs pr{};
+            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale = ple.scale; pr.eos = c.ple_eos;
+            pr.pos = d_pos; pr.toks = d_toks; pr.tok_hist = ple.tok_hist; pr.ctx_max = c.ctx_max; pr.emb = ple.emb;
+            WZY_TRY(launch_ple_rows(pr, T, st));
+            GemvSegs s;
+            s.n = 2;
+            s.seg[0] = GemvSeg{ple.wk, nullptr, ple.k, HCD, GEMV_BF16, HCD, 0};
+            s.seg[1] = GemvSeg{ple.wv, nullptr, ple.v, D, GEMV_BF16, D, 0};
+            WZY_TRY(launch_gemv_segs(s, ple.emb, D, T, st));
+            PleBlockArgs b{};
+            b.R = R[cur]; b.bo = pend_bo; b.inj_prev = pend_inj; b.k = ple.k; b.v = ple.v;
+            b.norm_q = ple.nq; b.norm_k = ple.nk; b.norm_c = ple.nc; b.conv_w = ple.cw; b.hist = ple.hist;
+            b.hist_snaps = save_snaps ? ple.snaps + (size_t) snap_offset * HCD * PLE_HIST : nullptr;
+            b.gat = ple.gat; b.n = ple.n; b.D = D; b.HC = c.hc; b.eps = c.eps;
+            WZY_TRY(launch_ple_mix(b, T, st));
+            WZY_TRY(launch_ple_conv(b, T, st));
+            pend_bo = nullptr;
+            pend_inj = nullptr;
+        }
         // ---------------- attention half ----------------
         WZY_TRY(hc_read(w.hc_norm[0], w.hc_down[0], w.hc_inj[0], w.hc_up[0], inj_a, l == 0));
         WZY_TRY(tr(tr_mixa, mixed, l, D, 4));
@@ -821,6 +885,26 @@ static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
                                              s->stream));
         }
     }
+    if (c.ple) {
+        auto& p = s->ple;
+        const size_t hcd = (size_t) s->HCD;
+        const float sd = (float) (1.0 / sqrt((double) D));
+        WZY_TRY(g.normal_bf16(p.wk, hcd * D, 1, TI_PLE_K, sd));
+        WZY_TRY(g.normal_bf16(p.wv, (size_t) D * D, 1, TI_PLE_V, sd));
+        WZY_TRY(g.normal_f32(p.nq, hcd, 1, TI_PLE_NQ, 1.0f, 0.02f));
+        WZY_TRY(g.normal_f32(p.nk, hcd, 1, TI_PLE_NK, 1.0f, 0.02f));
+        WZY_TRY(g.normal_f32(p.nc, hcd, 1, TI_PLE_NC, 1.0f, 0.02f));
+        WZY_TRY(g.normal_f32(p.cw, hcd * 4, 1, TI_PLE_CONV, 0.0f, 0.5f));
+        WZY_TRY(wzy_synth_ple_table_device(seed, D / PLE_HEADS, p.table, s->stream));
+        p.scale = 0.125f;
+        WZY_TRY(g.upload(p.scale_dev, &p.scale, 4));
+        // prefilled context: a conv history and the tokens of cells 0 .. n_ctx-1
+        WZY_TRY(g.normal_f32(p.hist, hcd * PLE_HIST, 1, TS_PLE_HIST, 0.0f, 1.0f, WZY_S_STATE));
+        std::vector<int> toks((size_t) n_ctx + 1);
+        for (int i = 0; i < n_ctx; ++i)
+            toks[i] = (int) (wzy_synth_hash(seed, g.stream(WZY_S_STATE, 1, TS_PLE_TOKS), (uint64_t) i) % (uint64_t) c.n_vocab);
+        if (n_ctx > 0) WZY_TRY(g.upload(p.tok_hist, toks.data(), (size_t) n_ctx * 4));
+    }
     if (c.emb_q8) WZY_TRY(g.q8(s->emb8, -1, TI_EMB, 1.0f));
     else WZY_TRY(g.normal_bf16(s->emb, (size_t) c.n_vocab * D, -1, TI_EMB, 1.0f));
     WZY_TRY(g.normal_f32(s->head_norm, s->HCD, -1, TI_HEAD_NORM, 1.0f, 0.02f));
@@ -849,6 +933,7 @@ extern "C" void wzy_stage_cfg_default(wzy_stage_cfg* c, int ctx_max) {
     c->n_exp = 512; c->top_k = 10; c->n_ff = 512; c->n_vocab = 151936;
     c->ctx_max = ctx_max; c->kv_ring = 0; c->kv_sinks = 0; c->rope_theta = 1e7f; c->eps = 1e-6f;
     c->attn_f16_above = 32768;
+    c->ple = 0; c->ple_eos = PLE_EOS_DEFAULT;
 }
 
 extern "C" int wzy_stage_create(const wzy_stage_cfg* cfg, int device, wzy_stage** out) {
@@ -882,6 +967,7 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
     WZY_REQUIRE(st && st->loaded, "record_forward: stage not loaded");
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "record_forward: T must be in [1, %d]", WZY_MAX_W);
     WZY_REQUIRE(emb || toks, "record_forward: need token ids or embedding rows");
+    WZY_REQUIRE(!st->cfg.ple || toks, "record_forward: the per-layer embedding needs the window's token ids");
     WZY_REQUIRE(pos >= 0 && pos + T <= st->cfg.ctx_max, "record_forward: positions [%d, %d) exceed ctx_max %d", pos,
                 pos + T, st->cfg.ctx_max);
     WZY_REQUIRE(!save_snaps || (snap_offset >= 0 && snap_offset + T <= WZY_MAX_W), "record_forward: bad snap_offset");
@@ -997,6 +1083,7 @@ extern "C" int wzy_stage_reset_state(wzy_stage* st) {
             WZY_HIP_TRY(hipMemsetAsync(w.ix.dead, 0, (size_t) c.idx_dim * 4, st->stream));
         }
     }
+    if (c.ple) WZY_HIP_TRY(hipMemsetAsync(st->ple.hist, 0, (size_t) st->HCD * PLE_HIST * 4, st->stream));
     WZY_HIP_TRY(hipStreamSynchronize(st->stream));
     return WZY_OK;
 }
@@ -1026,6 +1113,10 @@ void wzy_stage::session_regions(int n_cells, std::vector<std::pair<void*, size_t
                 out.emplace_back(w.kv.vs, nc * (KVD / 64) * 2);
             }
         }
+    }
+    if (c.ple) {                    // the PLE conv history and the tokens of the session's cells
+        out.emplace_back(ple.hist, (size_t) HCD * PLE_HIST * 4);
+        out.emplace_back(ple.tok_hist, nc * 4);
     }
     if (mtp) {
         const size_t kvd = (size_t) mtp->c.kvh * mtp->c.hd;
@@ -1477,6 +1568,11 @@ int wzy_stage::prefill_reserve(int B) {
                  osc = bump((size_t) sc_rows * maxb * 4), osel = bump(b * c.idx_topk * 4), ocnt = bump(b * 4);
     off = std::max(off, gdn_end);
     const size_t omoe = bump(moe_bytes);
+    size_t ope = 0, opeh = 0, opk = 0, opv = 0, opg = 0, opn = 0;
+    if (c.ple) {
+        ope = bump(b * D * 4); opeh = bump(b * D * 2); opk = bump(b * HCD * 4); opv = bump(b * D * 4);
+        opg = bump(b * HCD * 4); opn = bump(b * HCD * 4);
+    }
     void* base = nullptr;
     if (hipMalloc(&base, off) != hipSuccess) {
         (void) hipGetLastError();
@@ -1502,6 +1598,10 @@ int wzy_stage::prefill_reserve(int B) {
     pf.idx_raw = (float*) (u + oir); pf.q_idx = (float*) (u + oqi); pf.scores = (float*) (u + osc);
     pf.sel = (int*) (u + osel); pf.cnt = (int*) (u + ocnt);
     pf.moe_ws = u + omoe;
+    if (c.ple) {
+        pf.ple_emb = (float*) (u + ope); pf.ple_embh = (uint16_t*) (u + opeh); pf.ple_k = (float*) (u + opk);
+        pf.ple_v = (float*) (u + opv); pf.ple_gat = (float*) (u + opg); pf.ple_n = (float*) (u + opn);
+    }
     pf.moe_bytes = moe_bytes;
     return WZY_OK;
 }
@@ -1584,6 +1684,25 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
     for (int l = 0; l < c.n_layers; ++l) {
         Layer& w = L[l];
         WZY_TRY(mark(0));
+        if (l == 1 && c.ple) {
+            // per-layer embedding of the chunk (src/wzy_prefill_tc.cuh:808-823): table rows, the two
+            // projections on bf16 MFMA, the block over the rows in order
+            PleRowsArgs pr{};
+            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale = ple.scale; pr.eos = c.ple_eos;
+            pr.pos = pf.pos8; pr.toks = pf.toks; pr.tok_hist = ple.tok_hist; pr.ctx_max = c.ctx_max;
+            pr.emb = pf.ple_emb; pr.emb_bf16 = pf.ple_embh;
+            WZY_TRY(launch_ple_rows(pr, B, st));
+            WZY_TRY(gemm(pf.ple_embh, D, D, nullptr, ple.wk, HCD, pf.ple_k, nullptr, HCD));
+            WZY_TRY(gemm(pf.ple_embh, D, D, nullptr, ple.wv, D, pf.ple_v, nullptr, D));
+            PleBlockArgs pb{};
+            pb.R = pf.R; pb.bo = pend_bo; pb.inj_prev = pend_inj; pb.k = pf.ple_k; pb.v = pf.ple_v;
+            pb.norm_q = ple.nq; pb.norm_k = ple.nk; pb.norm_c = ple.nc; pb.conv_w = ple.cw; pb.hist = ple.hist;
+            pb.gat = pf.ple_gat; pb.n = pf.ple_n; pb.D = D; pb.HC = HC; pb.eps = c.eps;
+            WZY_TRY(launch_ple_mix(pb, B, st));
+            WZY_TRY(launch_ple_conv(pb, B, st));
+            pend_bo = nullptr;
+            pend_inj = nullptr;
+        }
         WZY_TRY(hc_read(w.hc_norm[0], w.hc_down[0], w.hc_inj[0], w.hc_up[0], pend_bo, pend_inj, pf.inj_a));
         WZY_TRY(tr(l, 0, pf.mixed));
         if (!w.qsa) {

@@ -30,6 +30,7 @@ enum {
     WZY_S_DENSE = 5,      // sub = tensor id (see wzy_synth.h)
     WZY_S_STATE = 6,
     WZY_S_INPUT = 7,
+    WZY_S_PLE = 9,        // per-layer embedding table codes
     WZY_S_Q2 = 8,         // MTP Q2_0 experts: sub = expert*4 + part (0 gate/up codes, 1 down codes,
                           // 2 gate/up scales, 3 down scales)
 };
@@ -107,4 +108,14 @@ WZY_HD int wzy_q2_scale_exp(int cols) {
     int l = 0;
     while ((1 << (l + 1)) <= cols) ++l;     // l = floor(log2(cols))
     return -((l + 1) / 2);                  // -ceil(l/2): 2048 (l=11) -> -6, 512 (l=9) -> -5
+}
+
+// One byte of the synthetic per-layer-embedding table: an fp8 (e4m3, bias 7) code with a random sign
+// and mantissa and an exponent field in 4..9 (|value| in [2^-3, 2^3) before the table scale), so no
+// code is subnormal or NaN.  Byte j of row `row` (head_bytes bytes per row); 4 bytes per hash.
+WZY_HD uint8_t wzy_ple_code(uint64_t seed, uint64_t row, int head_bytes, int j) {
+    const uint64_t lin = row * (uint64_t) head_bytes + (uint64_t) j;
+    const uint64_t h = wzy_hash3(seed, wzy_stream(WZY_S_PLE, 0, 0), lin >> 2);
+    const uint32_t b = (uint32_t) (h >> (16 * (lin & 3))) & 0xFFFFu;
+    return (uint8_t) (((b & 1u) << 7) | ((4u + (b >> 4) % 6u) << 3) | ((b >> 1) & 7u));
 }

@@ -69,7 +69,7 @@ class StageCfg(C.Structure):
                 ("n_rot", I32), ("idx_heads", I32), ("idx_dim", I32), ("idx_blk", I32), ("idx_topk", I32),
                 ("n_exp", I32), ("top_k", I32), ("n_ff", I32), ("n_vocab", I32), ("ctx_max", I32),
                 ("kv_ring", I32), ("kv_sinks", I32), ("rope_theta", F32), ("eps", F32),
-                ("emb_q8", I32), ("head_q8", I32), ("attn_f16_above", I32)]
+                ("emb_q8", I32), ("head_q8", I32), ("attn_f16_above", I32), ("ple", I32), ("ple_eos", I32)]
 
 
 WZY_MAX_STOPS = 64
@@ -197,6 +197,12 @@ _SIGS = {
     "wzy_row_top16_noalloc": (I32, [P, I32, I32, P, P, P, P], True),
     "wzy_gdn_time_recurrence": (I32, [P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P, P, P], True),
     "wzy_qsa_time_decode": (I32, [C.POINTER(QsaDims), C.POINTER(QsaLayer), P, I32, P, P], True),
+    "wzy_ple_table_rows": (U64, [], False),
+    "wzy_ple_rows": (I32, [P, I32, F32, I32, P, P, I32, P, I32, P, P, P], True),
+    "wzy_ple_workspace_bytes": (SZ, [I32, I32, I32], False),
+    "wzy_ple_block": (I32, [P, P, P, P, P, P, P, P, P, P, P, I32, I32, F32, I32, P, P, SZ, P], True),
+    "wzy_synth_ple_row": (None, [U64, U64, I32, P], False),
+    "wzy_synth_ple_table_device": (I32, [U64, I32, P, P], True),
     # synth
     "wzy_synth_hash": (U64, [U64, U64, U64], False),
     "wzy_synth_stream": (U64, [U32, U32, U32], False),
