@@ -27,6 +27,7 @@ extern "C" {
 #define WZY_GGUF_F16 1
 #define WZY_GGUF_Q8_0 8
 #define WZY_GGUF_BF16 30
+#define WZY_GGUF_I8 24
 
 /* ---- GGUF container (versions 2 and 3), memory-mapped read-only ---- */
 typedef struct wzy_gguf wzy_gguf;
@@ -64,15 +65,23 @@ int wzy_to_f32(int type, const void* src, size_t n, float* dst);
  * GDN, QSA, indexer and MoE shapes from their weights, emb_q8 / head_q8 from the tensor types;
  * top_k, n_rot, rope_theta and eps from the "<arch>.expert_used_count", ".rope.dimension_count",
  * ".rope.freq_base" and ".attention.layer_norm_rms_epsilon" metadata, or the reference's
- * constants (10, 64, 1e7, 1e-6) where absent; idx_blk 4, idx_topk 2048. */
+ * constants (10, 64, 1e7, 1e-6) where absent; idx_blk 4, idx_topk 2048; ple = 1 when the checkpoint
+ * carries blk.1.ple_key.weight (the reference's has_ple, src/wzy_engine_v2.cu:316). */
 int wzy_stage_cfg_from_gguf(const char* gguf_path, int ctx_max, wzy_stage_cfg* cfg);
 /* Load every weight of a created stage: the GGUF's per-layer tensors (Q8_0 projections as they
  * are, bf16 hyper-connection mixes quantised to Q8_0, bf16 / f32 vectors), the LM head and the
  * token embedding (from emb_path's token_embd.weight when emb_path is not NULL, the reference's
  * token-embd-bf16.gguf), and the NVFP4 experts from experts_path (blob l*n_exp + e of
- * wzy_nvfp4_blob_bytes(n_embd, n_ff) bytes each, repacked to the plane layout).  The recurrent
- * state starts empty (as after wzy_stage_reset_state). */
+ * wzy_nvfp4_blob_bytes(n_embd, n_ff) bytes each, repacked to the plane layout); with cfg.ple also
+ * layer 1's blk.1.ple_key / ple_value (bf16) and ple_norm_key / _query / _conv, ple_conv1d (f32)
+ * (src/wzy_engine_v2.cu:493-499).  The recurrent state starts empty (as after wzy_stage_reset_state). */
 int wzy_stage_load_gguf(wzy_stage* st, const char* gguf_path, const char* experts_path, const char* emb_path);
+/* The per-layer embedding table of a cfg.ple stage from the reference's ple-fp8.gguf: the
+ * per_layer_token_embd.weight tensor of 1-byte fp8 codes [rows = wzy_ple_table_rows()][n_embd / 16]
+ * copied into HBM (51 GB at the real shape), and its scale from the strata.ple.scale metadata (f32 or
+ * f64; 1 when absent).  Replaces PleSrc::open (src/wzy_stage_v2.cuh:228-287), which maps the file for
+ * the host gather. */
+int wzy_stage_load_ple(wzy_stage* st, const char* ple_path);
 /* The MTP drafter from mtp_dir/dense.txt ("name kind rows cols offset bytes" lines indexing
  * mtp_dir/dense.bin: Q8_0 blocks, bf16 or f32), mtp_dir/experts.bin (n_exp Q2_0 blobs) and the
  * draft vocabulary dvocab_path (int32 main-vocabulary ids; the draft head holds those rows of the

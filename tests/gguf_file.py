@@ -97,7 +97,7 @@ class Checkpoint:
     `t` keeps every tensor as written (name -> (ggml type, array))."""
 
     def __init__(self, wz, cfg, seed, out_dir, emb_q8=True, head_q8=True, f32_vectors_as=F32, bf16_from_f32=(),
-                 with_emb_file=False, with_mtp=False, n_dv=0, metadata=True):
+                 with_emb_file=False, with_mtp=False, n_dv=0, metadata=True, with_ple=False):
         self.cfg, self.seed, self.dir = cfg, seed, out_dir
         rng = np.random.default_rng(seed)
         D, HC, L = cfg.n_embd, cfg.hc, cfg.hc_lr
@@ -172,6 +172,13 @@ class Checkpoint:
                 add(b + "indexer.k_proj.weight", cfg.idx_dim, D, "bf16")
                 add(b + "indexer.q_norm.weight", 1, cfg.idx_dim, "f32", sd=0.02, mean=1.0)
                 add(b + "indexer.k_norm.weight", 1, cfg.idx_dim, "f32", sd=0.02, mean=1.0)
+            if with_ple and l == 1:               # layer 1's per-layer embedding block (wzy_engine_v2.cu:493-499)
+                add(b + "ple_key.weight", HCD, D, "bf16")
+                add(b + "ple_value.weight", D, D, "bf16")
+                add(b + "ple_norm_key.weight", 1, HCD, "f32", sd=0.02, mean=1.0)
+                add(b + "ple_norm_query.weight", 1, HCD, "f32", sd=0.02, mean=1.0)
+                add(b + "ple_norm_conv.weight", 1, HCD, "f32", sd=0.02, mean=1.0)
+                add(b + "ple_conv1d.weight", HCD, 4, "f32", sd=0.5)
             add(b + "ffn_gate_inp.weight", cfg.n_exp, D, "bf16", sd=0.02)
             add(b + "ffn_gate_inp_shexp.weight", 1, D, "bf16", sd=0.02)
             add(b + "ffn_gate_shexp.weight", cfg.n_ff, D, "q8")
@@ -274,3 +281,25 @@ class Checkpoint:
         self.dv_ids = np.sort(rng.choice(cfg.n_vocab, n_dv, replace=False)).astype(np.int32)
         self.dvocab = os.path.join(self.mtp_dir, "draft_vocab.bin")
         self.dv_ids.tofile(self.dvocab)
+
+
+def write_ple_table(path, head, n_rows, rows, scale=None, type_tag=24, dims=None):
+    """The reference's ple-fp8.gguf: one tensor per_layer_token_embd.weight of 1-byte fp8 codes
+    [n_rows][head] (dims [head, n_rows]) and the strata.ple.scale metadata (f32; absent when scale is
+    None).  Only the rows given (row -> head bytes) are written; the rest of the table is a hole of
+    the sparse file (codes 0), so the multi-gigabyte table costs no disk space."""
+    kvs = [] if scale is None else [("strata.ple.scale", KV_F32, float(scale))]
+    dims = [head, n_rows] if dims is None else dims
+    head_b = b"GGUF" + struct.pack("<IQQ", 3, 1, len(kvs))
+    for k, t, v in kvs:
+        head_b += _str(k) + struct.pack("<I", t) + _value(t, v)
+    head_b += _str("per_layer_token_embd.weight") + struct.pack("<I", len(dims))
+    head_b += b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", type_tag, 0)
+    data_at = (len(head_b) + 31) // 32 * 32
+    with open(path, "wb") as fh:
+        fh.write(head_b + b"\0" * (data_at - len(head_b)))
+        for r in sorted(rows):
+            fh.seek(data_at + r * head)
+            fh.write(bytes(rows[r]))
+        fh.truncate(data_at + int(np.prod(dims, dtype=np.uint64)))
+    return path

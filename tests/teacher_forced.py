@@ -99,7 +99,12 @@ class TeacherForced:
         D = cfg.n_embd
         self.cos = om.arrays[(-1, "rope_cos")]
         self.sin = om.arrays[(-1, "rope_sin")]
-        self.emb = om.arrays[(-1, "emb")].reshape(cfg.n_vocab, D)
+        self.emb_q8, self.head_q8 = bool(cfg.emb_q8), bool(cfg.head_q8)
+        if self.emb_q8:              # Q8_0 table: codes [n_vocab][D], fp16 scales per 32 (stage_one_emb)
+            self.emb_q = om.arrays[(-1, "emb.q")].reshape(cfg.n_vocab, D)
+            self.emb_s = om.arrays[(-1, "emb.s")].reshape(cfg.n_vocab, D // 32)
+        else:
+            self.emb = om.arrays[(-1, "emb")].reshape(cfg.n_vocab, D)
 
     def sync_from_stage(self):
         """Take the stage's current recurrent / KV / indexer state as the next row's pre-row state (after
@@ -190,7 +195,12 @@ class TeacherForced:
             t = "%s layer %d" % (tag, l)
             # ---- attention HC read
             if l == 0:
-                emb_row = bf16_to_f32(self.emb[tok])
+                if self.emb_q8:
+                    tq = tok if 0 <= tok < cfg.n_vocab else 0
+                    emb_row = (self.emb_s[tq].view(np.float16).astype(np.float32).repeat(32) *
+                               self.emb_q[tq].astype(np.float32)).astype(np.float32)
+                else:
+                    emb_row = bf16_to_f32(self.emb[tok])
                 R_a, mixa, inj_a = self._hc_read(l, 0, None, emb_row, None, None)
             elif l == 1 and getattr(cfg, "ple", 0):
                 # per-layer embedding: the row's table rows, the block on the GPU's layer-0 outputs and the
@@ -382,7 +392,8 @@ class TeacherForced:
                                      with_inj=False)
         # pre-head residual = R_f[L-1] with the last MoE write folded in (the head read's R_out)
         self._cmp("pre-head residual", g_pre.ravel(), R_h, tag)
-        logits = self._bf16(self.A[(-1, "head")], mixh, cfg.n_vocab)
+        logits = self._q8("head", -1, mixh, cfg.n_vocab) if self.head_q8 else self._bf16(self.A[(-1, "head")], mixh,
+                                                                                            cfg.n_vocab)
         self._cmp("logits", g_logits.ravel(), logits, tag)
         ref = int(np.argmax(logits))
         gid = int(g_greedy[0])

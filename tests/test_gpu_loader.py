@@ -4,6 +4,7 @@ embedding file, the mtp/ directory) is loaded with wzy_stage_load_gguf / wzy_sta
 stage tensor is compared with the conversion of the file's tensor, then the loaded model decodes and
 drafts against the oracle (which reads the stage's tensors)."""
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -13,6 +14,7 @@ import wzy_amd
 from layer_parity import excess
 from mtp_oracle import MtpTeacher, OracleMtp, gpu_acts
 from stage_oracle import OracleModel, small_cfg
+from test_gpu_stage import run_layer_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -171,6 +173,89 @@ def test_load_gguf_rejects_mismatches(wz, gpu, tmp_path):
             st.load_gguf(ck.gguf, short)
         with pytest.raises(wzy_amd.WzyError, match="emb_q8"):
             st.load_gguf(ck.gguf, ck.experts, ck.gguf)   # a bf16 embedding file for a Q8_0 stage
+    finally:
+        st.close()
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_load_ple_and_decode(wz, orc, gpu, tmp_path, q8):
+    """A checkpoint with layer 1's per-layer embedding block and the table file ple-fp8.gguf (sparse:
+    the rows the decode reads hold random codes, the rest zeros): the block's tensors and the table's
+    rows equal the files', the scale comes from strata.ple.scale, and the loaded model decodes against
+    the oracle (which reads the stage's table).  Tables of the wrong shape, truncated tables and stages
+    without PLE are refused before anything is copied."""
+    print("case load_ple q8=%d" % q8, flush=True)
+    ref = small_cfg(wzy_amd, ctx_max=256, n_layers=4, topk=64)
+    ref.gdn_hk, ref.gdn_hv = 2, 4
+    ck = gf.Checkpoint(wz, ref, 14, str(tmp_path), emb_q8=q8, head_q8=q8, with_ple=True)
+    cfg = wzy_amd.StageCfg()
+    wz.wzy_stage_cfg_from_gguf(str(ck.gguf).encode(), 256, C.byref(cfg))
+    assert cfg.ple == 1
+    head, n_rows = cfg.n_embd // 16, int(wz.wzy_ple_table_rows())
+    windows = [[5], [17], [999], [0], [3, 4, 5, 6]]   # the teacher follows single-token windows: T=4 last
+    toks = [t for w in windows for t in w]
+    rng = np.random.default_rng(14)
+
+    def codes():                                     # e4m3 codes of magnitude 2^-3 .. 2^2.9 (exponent field 4..9)
+        return (rng.integers(0, 2, head) << 7 | rng.integers(4, 10, head) << 3 | rng.integers(0, 8, head)).astype(
+            np.uint8)
+
+    rows, ids = {}, np.empty(16, np.uint32)
+    for p, t in enumerate(toks):                     # every row the decode reads
+        orc.orc_ple_row_ids(t, toks[p - 1] if p >= 1 else -1, toks[p - 2] if p >= 2 else -1, cfg.ple_eos,
+                            ids.ctypes.data)
+        for r in ids:
+            rows[int(r)] = codes()
+    for r in (0, n_rows - 1, 123456789):
+        rows[r] = rng.integers(0, 256, head, dtype=np.uint8)   # every code, NaN codes included
+    ple = gf.write_ple_table(tmp_path / "ple-fp8.gguf", head, n_rows, rows, scale=0.25)
+
+    def load(st):
+        st.load_gguf(ck.gguf, ck.experts)
+        st.load_ple(ple)
+        for suf, name, conv in (("ple_key.weight", "ple_key", "bf16"), ("ple_value.weight", "ple_value", "bf16"),
+                                ("ple_norm_key.weight", "ple_norm_key", "f32"),
+                                ("ple_norm_query.weight", "ple_norm_query", "f32"),
+                                ("ple_norm_conv.weight", "ple_norm_conv", "f32"),
+                                ("ple_conv1d.weight", "ple_conv1d", "f32")):
+            t, v = ck.t["blk.1." + suf]
+            check_tensor(st, 1, name, conv, t, v)
+        for r, b in rows.items():
+            assert np.array_equal(st.read_range(-1, "ple_table", np.uint8, r * head, head), b), "table row %d" % r
+        for r in (1, 20000003, n_rows - 2):
+            if r not in rows:
+                assert not st.read_range(-1, "ple_table", np.uint8, r * head, head).any(), "hole row %d" % r
+        assert st.read(-1, "ple_scale", np.float32)[0] == 0.25
+
+    # the loaded model decodes: the single-token steps component by component (teacher-forced) and
+    # every row's decisions layer by layer (free-running)
+    par, tf = run_layer_parity(wz, cfg, 14, 0, windows, teacher=True, load=load)
+    print("ple load: %d table rows written; %s; %s" % (len(rows), par.summary(), tf.summary()), flush=True)
+    assert tf.counts["rows"] == 4 and "PLE conv history" in tf.worst
+    tf.assert_bounds()
+    st = wzy_amd.Stage(cfg)
+    try:
+        st.load_gguf(ck.gguf, ck.experts)
+        with pytest.raises(wzy_amd.WzyError, match="table is not loaded"):
+            st.forward(0, [1])
+        # refused: a table of the wrong width, a truncated table (an I8 tag, and a tag this library does
+        # not know, read as raw bytes as the reference does), and a stage without PLE
+        bad = gf.write_ple_table(tmp_path / "wide.gguf", head, n_rows, {}, dims=[head + 1, n_rows])
+        with pytest.raises(wzy_amd.WzyError, match="1-byte codes"):
+            st.load_ple(bad)
+        for tag in (24, 200):
+            cut = gf.write_ple_table(tmp_path / ("cut%d.gguf" % tag), head, n_rows, {}, type_tag=tag)
+            with open(cut, "r+b") as fh:
+                fh.truncate(os.path.getsize(cut) - head)
+            with pytest.raises(wzy_amd.WzyError, match="outside the file"):
+                st.load_ple(cut)
+    finally:
+        st.close()
+    cfg.ple = 0
+    st = wzy_amd.Stage(cfg)
+    try:
+        with pytest.raises(wzy_amd.WzyError, match="cfg.ple = 0"):
+            st.load_ple(ple)
     finally:
         st.close()
 

@@ -123,8 +123,9 @@ def test_stage_single_layer_window_commit(wz, gpu, kind):
         st.close()
 
 
-def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=False):
-    """Load a stage, trace every window on both sides and compare layer by layer (free-running).  With
+def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=False, load=None):
+    """Load a stage (the synthetic model of seed with n_ctx cells, or load(stage) when given), trace
+    every window on both sides and compare layer by layer (free-running).  With
     greedy_feed, each single-row window's token is the GPU's greedy id of the previous row.  With
     teacher, every single-row window is also checked component by component against the oracle fed
     the GPU's own inputs and pre-row state (teacher_forced.TeacherForced), and the free-running
@@ -132,7 +133,10 @@ def run_layer_parity(wz, cfg, seed, n_ctx, windows, greedy_feed=False, teacher=F
     st = wzy_amd.Stage(cfg)
     try:
         t0 = time.time()
-        st.load_synthetic(seed, n_ctx)
+        if load is None:
+            st.load_synthetic(seed, n_ctx)
+        else:
+            load(st)
         st.lib.wzy_stage_set_trace(st.h, 1)
         orc = OracleModel(wz, st, cfg, seed)
         tf = TeacherForced(wz, st, cfg, orc) if teacher else None

@@ -212,7 +212,11 @@ def test_cfg_from_gguf(wz, tmp_path):
     ck2 = gf.Checkpoint(wz, ref, 3, str(tmp_path / "m2"), metadata=False)
     wz.wzy_stage_cfg_from_gguf(str(ck2.gguf).encode(), 512, C.byref(cfg))
     assert (cfg.top_k, cfg.n_rot, cfg.rope_theta) == (10, 64, pytest.approx(1e7))
-    assert cfg.emb_q8 == 1 and cfg.head_q8 == 1
+    assert cfg.emb_q8 == 1 and cfg.head_q8 == 1 and cfg.ple == 0
+    # blk.1.ple_key.weight switches the per-layer embedding on (has_ple)
+    ck3 = gf.Checkpoint(wz, ref, 3, str(tmp_path / "m3"), with_ple=True)
+    wz.wzy_stage_cfg_from_gguf(str(ck3.gguf).encode(), 512, C.byref(cfg))
+    assert cfg.ple == 1 and cfg.ple_eos == 248044
     # attention layers that break the period are rejected
     raw = bytearray(open(ck.gguf, "rb").read())
     i = raw.find(b"blk.3.attn_q.weight")

@@ -694,6 +694,7 @@ int main(int argc, char** argv) {
         const std::string experts = o.model_dir + "/pack/experts.bin";
         check(wzy_stage_load_gguf(st, gguf.c_str(), experts.c_str(), have_emb_file ? emb_file.c_str() : nullptr),
               "load_gguf");
+        if (c.ple) check(wzy_stage_load_ple(st, (o.model_dir + "/ple-fp8.gguf").c_str()), "load_ple");
     }
     if (o.mtp && o.model_dir.empty()) {
         const int n_dv = std::max(1, std::min(o.mtp_dvocab, c.n_vocab));

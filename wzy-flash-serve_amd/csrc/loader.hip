@@ -50,6 +50,7 @@ size_t type_bytes(int type, uint64_t n) {
         case WZY_GGUF_F32: return n * 4;
         case WZY_GGUF_F16: case WZY_GGUF_BF16: return n * 2;
         case WZY_GGUF_Q8_0: return n % 32 ? 0 : n / 32 * 34;
+        case WZY_GGUF_I8: return n;
         default: return 0;
     }
 }
@@ -384,6 +385,8 @@ extern "C" int wzy_stage_cfg_from_gguf(const char* gguf_path, int ctx_max, wzy_s
     WZY_REQUIRE(ne > 0 && nff > 0, "cfg_from_gguf: no router / shared expert in layer 0");
     cfg->n_exp = (int) ne;
     cfg->n_ff = (int) nff;
+    // the per-layer embedding at layer 1 (has_ple, src/wzy_engine_v2.cu:316,493-499)
+    cfg->ple = find_t(g, "blk.1.ple_key.weight") != nullptr ? 1 : 0;
     // metadata, where present
     const char* arch = nullptr;
     size_t alen = 0;
@@ -510,6 +513,14 @@ extern "C" int wzy_stage_load_gguf(wzy_stage* st, const char* gguf_path, const c
         WZY_TRY(put_gguf(st, l, "sh_up", g, blk(l, "ffn_up_shexp.weight"), C_Q8, c.n_ff, D));
         WZY_TRY(put_gguf(st, l, "sh_down", g, blk(l, "ffn_down_shexp.weight"), C_Q8, D, c.n_ff));
     }
+    if (c.ple) {      // layer 1's per-layer embedding block (src/wzy_engine_v2.cu:493-499)
+        WZY_TRY(put_gguf(st, 1, "ple_key", g, "blk.1.ple_key.weight", C_BF16, HCD, D));
+        WZY_TRY(put_gguf(st, 1, "ple_value", g, "blk.1.ple_value.weight", C_BF16, D, D));
+        WZY_TRY(put_gguf(st, 1, "ple_norm_key", g, "blk.1.ple_norm_key.weight", C_F32, 1, HCD));
+        WZY_TRY(put_gguf(st, 1, "ple_norm_query", g, "blk.1.ple_norm_query.weight", C_F32, 1, HCD));
+        WZY_TRY(put_gguf(st, 1, "ple_norm_conv", g, "blk.1.ple_norm_conv.weight", C_F32, 1, HCD));
+        WZY_TRY(put_gguf(st, 1, "ple_conv1d", g, "blk.1.ple_conv1d.weight", C_F32, HCD, 4));
+    }
     WZY_TRY(put_gguf(st, -1, "head_norm", g, "output_hc_norm.weight", C_F32, 1, HCD));
     WZY_TRY(put_gguf(st, -1, "head_down", g, "output_hc_down.weight", C_BF16_Q8, L, HCD));
     WZY_TRY(put_gguf(st, -1, "head_up", g, "output_hc_up.weight", C_BF16_Q8, HCD, L));
@@ -544,6 +555,45 @@ extern "C" int wzy_stage_load_gguf(wzy_stage* st, const char* gguf_path, const c
         WZY_TRY(wzy_stage_write_tensor_range(st, -1, "experts", b0 * rec, outp.data(), nb * rec));
     }
     return stage_set_loaded(st, true);
+}
+
+// ------------------------------------------------------------------------------------------------
+// per-layer embedding table
+// ------------------------------------------------------------------------------------------------
+extern "C" int wzy_stage_load_ple(wzy_stage* st, const char* ple_path) {
+    WZY_REQUIRE(st && ple_path, "load_ple: null argument");
+    const wzy_stage_cfg& c = *stage_cfg(st);
+    WZY_REQUIRE(c.ple, "load_ple: the stage has no per-layer embedding (cfg.ple = 0)");
+    Gg h;
+    WZY_TRY(wzy_gguf_open(ple_path, &h.g));
+    const wzy_gguf* g = h.g;
+    const TensorEnt* t = find_t(g, "per_layer_token_embd.weight");
+    WZY_REQUIRE(t, "load_ple: %s has no per_layer_token_embd.weight", ple_path);
+    const uint64_t head = (uint64_t) c.n_embd / 16, rows = wzy_ple_table_rows();
+    // the reference reads the tensor as raw bytes whatever its type tag: accept I8 and tags this
+    // library does not know (an fp8 tag), reject the types with wider elements
+    const bool one_byte = t->type == WZY_GGUF_I8 || type_bytes(t->type, 32) == 0;
+    WZY_REQUIRE(one_byte && t->n_dims == 2 && (uint64_t) t->dims[0] == head && (uint64_t) t->dims[1] == rows,
+                "load_ple: per_layer_token_embd.weight must be 1-byte codes [%llu x %llu] (type %d, %lld x %lld)",
+                (unsigned long long) head, (unsigned long long) rows, t->type, (long long) t->dims[0],
+                (long long) t->dims[1]);
+    WZY_REQUIRE(t->off <= g->size && g->size - t->off >= head * rows, "load_ple: %s: the table lies outside the file",
+                ple_path);
+    // the table scale (PleSrc::open reads strata.ple.scale when it is an f32 or f64; otherwise 1)
+    float scale = 1.f;
+    auto sk = g->kv.find("strata.ple.scale");
+    if (sk != g->kv.end() && sk->second.type == KV_F32) memcpy(&scale, g->base + sk->second.off, 4);
+    if (sk != g->kv.end() && sk->second.type == KV_F64) {
+        double v;
+        memcpy(&v, g->base + sk->second.off, 8);
+        scale = (float) v;
+    }
+    WZY_TRY(stage_set_ple_table(st, false, 0.f));
+    const uint8_t* src = g->base + t->off;
+    const size_t total = (size_t) (head * rows), chunk = (size_t) 256 << 20;
+    for (size_t o = 0; o < total; o += chunk)
+        WZY_TRY(wzy_stage_write_tensor_range(st, -1, "ple_table", o, src + o, std::min(chunk, total - o)));
+    return stage_set_ple_table(st, true, scale);
 }
 
 // ------------------------------------------------------------------------------------------------

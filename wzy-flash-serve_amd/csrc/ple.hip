@@ -65,8 +65,9 @@ __global__ void __launch_bounds__(64) ple_rows_kernel(PleRowsArgs a) {
     const uint64_t row = mixed % c_ple_vocab[h] + c_ple_off[h];
     const uint8_t* src = a.table + row * (uint64_t) a.head;
     const size_t o = (size_t) t * PLE_HEADS * a.head + (size_t) h * a.head;
+    const float scale = a.scale_dev ? *a.scale_dev : a.scale;
     for (int k = j; k < a.head; k += 64) {
-        const float v = ple_fp8(src[k]) * a.scale;
+        const float v = ple_fp8(src[k]) * scale;
         a.emb[o + k] = v;
         if (a.emb_bf16) a.emb_bf16[o + k] = ple_bf16(v);
     }

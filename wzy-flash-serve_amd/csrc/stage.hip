@@ -204,10 +204,10 @@ struct wzy_stage {
         float* hist = nullptr;                                  // [HCD x 9] state
         float* snaps = nullptr;                                 // [W][HCD x 9]
         uint8_t* table = nullptr;                               // [ple_table_rows() x D/16] fp8
-        float* scale_dev = nullptr;                             // the table scale (also kept on the host)
-        float scale = 0.125f;
+        float* scale_dev = nullptr;                             // the table scale, read by the row kernel
         int* tok_hist = nullptr;                                // [ctx_max + 4] token of each cell
         float *emb = nullptr, *k = nullptr, *v = nullptr, *gat = nullptr, *n = nullptr;   // W rows
+        bool table_ready = false;                               // table and scale loaded
     } ple;
 
     // parked sessions: per slot one HBM buffer holding a copy of the session state, and the
@@ -647,7 +647,7 @@ int wzy_stage::enqueue(int T, bool emb_host, int run_head, bool save_snaps, bool
             // 3-gram contexts, their k / v projections, then the block folds layer 0's pending FFN
             // write into the streams and adds to them; the attention read below folds nothing
             PleRowsArgs pr{};
-            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale = ple.scale; pr.eos = c.ple_eos;
+            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale_dev = ple.scale_dev; pr.eos = c.ple_eos;
             pr.pos = d_pos; pr.toks = d_toks; pr.tok_hist = ple.tok_hist; pr.ctx_max = c.ctx_max; pr.emb = ple.emb;
             WZY_TRY(launch_ple_rows(pr, T, st));
             GemvSegs s;
@@ -896,8 +896,9 @@ static int load_synthetic(wzy_stage* s, uint64_t seed, int n_ctx) {
         WZY_TRY(g.normal_f32(p.nc, hcd, 1, TI_PLE_NC, 1.0f, 0.02f));
         WZY_TRY(g.normal_f32(p.cw, hcd * 4, 1, TI_PLE_CONV, 0.0f, 0.5f));
         WZY_TRY(wzy_synth_ple_table_device(seed, D / PLE_HEADS, p.table, s->stream));
-        p.scale = 0.125f;
-        WZY_TRY(g.upload(p.scale_dev, &p.scale, 4));
+        const float scale = 0.125f;
+        WZY_TRY(g.upload(p.scale_dev, &scale, 4));
+        p.table_ready = true;
         // prefilled context: a conv history and the tokens of cells 0 .. n_ctx-1
         WZY_TRY(g.normal_f32(p.hist, hcd * PLE_HIST, 1, TS_PLE_HIST, 0.0f, 1.0f, WZY_S_STATE));
         std::vector<int> toks((size_t) n_ctx + 1);
@@ -968,6 +969,7 @@ extern "C" int wzy_stage_record_forward(wzy_stage* st, int pos, const float* emb
     WZY_REQUIRE(T >= 1 && T <= WZY_MAX_W, "record_forward: T must be in [1, %d]", WZY_MAX_W);
     WZY_REQUIRE(emb || toks, "record_forward: need token ids or embedding rows");
     WZY_REQUIRE(!st->cfg.ple || toks, "record_forward: the per-layer embedding needs the window's token ids");
+    WZY_REQUIRE(!st->cfg.ple || st->ple.table_ready, "record_forward: the per-layer embedding table is not loaded");
     WZY_REQUIRE(pos >= 0 && pos + T <= st->cfg.ctx_max, "record_forward: positions [%d, %d) exceed ctx_max %d", pos,
                 pos + T, st->cfg.ctx_max);
     WZY_REQUIRE(!save_snaps || (snap_offset >= 0 && snap_offset + T <= WZY_MAX_W), "record_forward: bad snap_offset");
@@ -1304,6 +1306,16 @@ extern "C" int wzy_stage_mtp_init(wzy_stage* st, uint64_t seed, int n_dvocab) {
 }
 
 namespace wzy {
+int stage_set_ple_table(wzy_stage* st, bool ready, float scale) {
+    WZY_REQUIRE(st && st->ple.scale_dev, "stage has no per-layer embedding");
+    WZY_HIP_TRY(hipSetDevice(st->dev));
+    st->ple.table_ready = false;
+    if (!ready) return WZY_OK;
+    WZY_HIP_TRY(hipMemcpy(st->ple.scale_dev, &scale, 4, hipMemcpyHostToDevice));
+    st->ple.table_ready = true;
+    return WZY_OK;
+}
+
 const wzy_stage_cfg* stage_cfg(const wzy_stage* st) { return &st->cfg; }
 int stage_set_loaded(wzy_stage* st, bool loaded) {
     WZY_HIP_TRY(hipSetDevice(st->dev));
@@ -1688,7 +1700,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
             // per-layer embedding of the chunk (src/wzy_prefill_tc.cuh:808-823): table rows, the two
             // projections on bf16 MFMA, the block over the rows in order
             PleRowsArgs pr{};
-            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale = ple.scale; pr.eos = c.ple_eos;
+            pr.table = ple.table; pr.head = D / PLE_HEADS; pr.scale_dev = ple.scale_dev; pr.eos = c.ple_eos;
             pr.pos = pf.pos8; pr.toks = pf.toks; pr.tok_hist = ple.tok_hist; pr.ctx_max = c.ctx_max;
             pr.emb = pf.ple_emb; pr.emb_bf16 = pf.ple_embh;
             WZY_TRY(launch_ple_rows(pr, B, st));
@@ -1809,6 +1821,7 @@ extern "C" int wzy_stage_can_prefill(const wzy_stage_cfg* c) {
 
 static int prefill_checks(wzy_stage* st, int pos, const int* toks, int B) {
     WZY_REQUIRE(st && st->loaded, "prefill: stage not loaded");
+    WZY_REQUIRE(!st->cfg.ple || st->ple.table_ready, "prefill: the per-layer embedding table is not loaded");
     WZY_REQUIRE(toks && B >= 1 && B <= 65535, "prefill: B must be in [1, 65535] with token ids");
     WZY_REQUIRE(pos >= 0 && pos + B <= st->cfg.ctx_max, "prefill: positions [%d, %d) exceed ctx_max %d", pos, pos + B,
                 st->cfg.ctx_max);

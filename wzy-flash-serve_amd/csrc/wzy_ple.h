@@ -18,6 +18,7 @@ struct PleRowsArgs {
     const uint8_t* table;             // [rows][head] fp8 codes, rows = ple_table_rows()
     int head;                         // bytes per head row (n_embd / 16)
     float scale;
+    const float* scale_dev;           // when set, the scale is read here (a graph replays the current one)
     int eos;
     const int* pos;                   // device: position of row 0
     const int* toks;                  // device [T]

@@ -10,5 +10,8 @@ const wzy_stage_cfg* stage_cfg(const wzy_stage* st);
 int stage_set_loaded(wzy_stage* st, bool loaded);
 // free the drafter (a loader that failed half way)
 void stage_mtp_drop(wzy_stage* st);
+// the per-layer embedding table of a cfg.ple stage: not ready (a load begins), or ready with its scale;
+// a stage runs no forward while its table is not ready
+int stage_set_ple_table(wzy_stage* st, bool ready, float scale);
 
 }  // namespace wzy

@@ -238,6 +238,7 @@ _SIGS = {
     "wzy_to_f32": (I32, [I32, P, SZ, P], True),
     "wzy_stage_cfg_from_gguf": (I32, [C.c_char_p, I32, C.POINTER(StageCfg)], True),
     "wzy_stage_load_gguf": (I32, [P, C.c_char_p, C.c_char_p, C.c_char_p], True),
+    "wzy_stage_load_ple": (I32, [P, C.c_char_p], True),
     "wzy_stage_mtp_load": (I32, [P, C.c_char_p, C.c_char_p], True),
     # runtime plumbing
     "wzy_dev_count": (I32, [C.POINTER(I32)], True),
@@ -384,6 +385,10 @@ class Stage:
         """Real weights: the GGUF checkpoint, the NVFP4 expert pack and optionally a bf16 embedding file."""
         self.lib.wzy_stage_load_gguf(self.h, str(gguf_path).encode(), str(experts_path).encode(),
                                      None if emb_path is None else str(emb_path).encode())
+
+    def load_ple(self, ple_path):
+        """The per-layer embedding table (the reference's ple-fp8.gguf) of a stage with cfg.ple."""
+        self.lib.wzy_stage_load_ple(self.h, str(ple_path).encode())
 
     def forward(self, pos, toks, run_head=True, save_snaps=False, want_top16=False, snap_offset=0, emb=None):
         import numpy as np
