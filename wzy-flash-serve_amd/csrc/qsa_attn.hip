@@ -22,6 +22,8 @@ using namespace wzy;
 
 namespace {
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
 constexpr int ATT_HPW = 4;           // q heads per attention workgroup (one per wave in the score phase)
 constexpr int ATT_ROW = 256 + 16;    // LDS bytes per cell row (hd = 256 codes + pad against bank conflicts)
 constexpr int ATT_CH_MAX = 32;       // chunks per row: topk <= 2048
@@ -487,13 +489,15 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
     }
     {                                                // this slice's heads; rows past gq are zero
         const int hh = tid >> 6, d4 = tid & 63, h = hs * ATT_HPW + hh;
-        float4 q = h < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + h) * 512 + 4 * d4)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (f16) {                                   // fp16(q / 16), as the reference's GQA kernel stages q
-            q.x = round_h16(q.x * 0.0625f); q.y = round_h16(q.y * 0.0625f);
-            q.z = round_h16(q.z * 0.0625f); q.w = round_h16(q.w * 0.0625f);
+        const float4 q = h < gq ? *(const float4*) (a.qg + (size_t) t * dm.qh * 512 + (size_t) (j * gq + h) * 512 + 4 * d4)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (f16) {                                   // fp16(q / 16) pairs, as the reference's GQA kernel stages q
+            half2_t* qh = (half2_t*) &s_q[hh][0];
+            qh[2 * d4] = half2_t{(_Float16) (q.x * 0.0625f), (_Float16) (q.y * 0.0625f)};
+            qh[2 * d4 + 1] = half2_t{(_Float16) (q.z * 0.0625f), (_Float16) (q.w * 0.0625f)};
+        } else {
+            *(float4*) &s_q[hh][4 * d4] = q;
         }
-        *(float4*) &s_q[hh][4 * d4] = q;
     }
     __syncthreads();
 
@@ -551,18 +555,32 @@ __global__ void __launch_bounds__(256) qsa_attn_kernel(QsaAttnArgs a) {
                 acc = fmaf(ag, s_ks[cell][g], acc);
             }
             acc *= 0.0625f;
-        } else {                                     // fp16(code * scale) dotted with fp16(q / 16)
+        } else {
+            // fp16(code * scale) dotted with fp16(q / 16), two values per step: the codes become exact
+            // fp16 pairs (the biased byte u = code + 128 under the exponent of 1024 is 1024 + u, minus
+            // 1152), the packed fp16 multiply rounds code * scale to nearest even as the reference's
+            // __hmul does, and v_dot2_f32_f16 adds the two exact products into the fp32 sum
+            const half2_t* qh = (const half2_t*) &s_q[w][0];
+            const half2_t bias = {(_Float16) 1152.0f, (_Float16) 1152.0f};
 #pragma unroll 1
             for (int g = 0; g < 4; ++g) {
-                const float sc = s_ks[cell][g];
+                const _Float16 sh = (_Float16) s_ks[cell][g];    // an fp16 value: exact
+                const half2_t sc2 = {sh, sh};
 #pragma unroll
                 for (int pp = 0; pp < 4; ++pp) {
                     const int part = 4 * g + pp;
                     const int4 kv = *(const int4*) (s_k + cell * ATT_ROW + part * 16);
-                    const int8_t* kb = (const int8_t*) &kv;
-                    const float* qp = &s_q[w][part * 16];
+                    const uint32_t wd[4] = {(uint32_t) kv.x, (uint32_t) kv.y, (uint32_t) kv.z, (uint32_t) kv.w};
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) acc = fmaf(round_h16((float) kb[i] * sc), qp[i], acc);
+                    for (int jw = 0; jw < 4; ++jw) {
+                        const uint32_t u = wd[jw] ^ 0x80808080u;
+                        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);   // bytes 0, 1
+                        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);   // bytes 2, 3
+                        const half2_t k01 = (__builtin_bit_cast(half2_t, lo) - bias) * sc2;
+                        const half2_t k23 = (__builtin_bit_cast(half2_t, hi) - bias) * sc2;
+                        acc = __builtin_amdgcn_fdot2(k01, qh[part * 8 + 2 * jw], acc, false);
+                        acc = __builtin_amdgcn_fdot2(k23, qh[part * 8 + 2 * jw + 1], acc, false);
+                    }
                 }
             }
         }
