@@ -666,8 +666,8 @@ def main():
     print("bench: %d steps in %.3f s" % (args.steps, elapsed), file=sys.stderr, flush=True)
 
     # live MoE kernel timing with HIP events on the stage stream (activations of the last step)
-    us_gu, us_dn = C.c_float(0), C.c_float(0)
-    wz.wzy_stage_time_moe(st.h, args.moe_iters, C.byref(us_gu), C.byref(us_dn))
+    us_gu, us_dn, us_blk = C.c_float(0), C.c_float(0), C.c_float(0)
+    wz.wzy_stage_time_moe(st.h, args.moe_iters, C.byref(us_gu), C.byref(us_dn), C.byref(us_blk))
     gu_gbs = GU_BYTES / (us_gu.value * 1e-6) / 1e9
     dn_gbs = DN_BYTES / (us_dn.value * 1e-6) / 1e9
     pf = None
@@ -746,6 +746,11 @@ def main():
             # the survey's config-1 unit: 17,694,880 routed-expert bytes per token-layer over the two launches
             "config1_routed_bytes": ROUTED_BYTES,
             "config1_frac": round(ROUTED_BYTES / ((us_gu.value + us_dn.value) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            # the block as a decode step runs it: each gate/up launch followed by its layer's down launch
+            "moe_block": {"us_per_block": round(us_blk.value, 3),
+                          "block_bytes": GU_BYTES + DN_BYTES,
+                          "achieved": round((GU_BYTES + DN_BYTES) / (us_blk.value * 1e-6) / 1e9, 1),
+                          "config1_frac": round(ROUTED_BYTES / (us_blk.value * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         },
         "cpu_baseline": cpu,
         "prefill_moe": pf,

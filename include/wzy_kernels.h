@@ -179,12 +179,14 @@ int wzy_moe_route(const float* logits, int n_exp, int top_k, int T, int* ids, fl
  * [T x n_embd] are computed for every layer first; then `iters` gate/up launches run back to back
  * cycling through the `n_layers` weight sets (so the 256 MB last-level cache cannot hold the
  * experts), each routing with its own layer's logits, and then `iters` down+combine launches the
- * same way.  Returns the mean duration in microseconds of one gate/up launch and of one down launch
- * (host pointers).  Layers must share one shape.  Allocates (and frees) its own scratch.
+ * same way.  With us_block non-NULL, `iters` blocks follow, each a gate/up launch and then its
+ * layer's down launch, as a decode step runs them.  Returns the mean duration in microseconds of
+ * one gate/up launch, one down launch and one block (host pointers).  Layers must share one shape.
+ * Allocates (and frees) its own scratch.
  * No counterpart in the reference: measurement support for the NVFP4 GEMV roofline. */
 int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, const float* x, void* workspace,
                          size_t workspace_bytes, int iters, float* us_gate_up, float* us_down,
-                         void* stream);
+                         float* us_block, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Hyper-connection read

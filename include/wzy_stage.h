@@ -228,8 +228,9 @@ int wzy_stage_mtp_time(wzy_stage* st, int cell, int tok, int src_row, int iters,
 
 /* Measurement support (no reference counterpart): time the NVFP4 expert kernels of every layer's
  * MoE block with hipEvents for `iters` iterations (cycling over layers with the routing of the
- * last forward's rows) -> mean microseconds of the gate/up launch and of the down launch. */
-int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down);
+ * last forward's rows) -> mean microseconds of the gate/up launch, of the down launch and (us_block
+ * non-NULL) of a gate/up launch followed by its down launch (wzy_moe_time_kernels). */
+int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down, float* us_block);
 
 /* Measurement support (no reference counterpart): the device pointers of one layer's MoE weights
  * (router, shared gate, shared expert, expert records), for the standalone MoE entry points of

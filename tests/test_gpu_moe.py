@@ -308,6 +308,37 @@ def test_moe_multirow_parity(wz, orc, gpu, T):
         np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_every_scale_code(wz, orc, gpu, T):
+    """All 256 e4m3 scale bytes in the gate/up and down scale planes (the sign bit is ignored and
+    code 0x7F reads as 480, the reference's unsigned reading; the oracle's decode is pinned on all
+    codes against torch): the kernels' hardware fp8 decode of the block scales gives the oracle's
+    experts, for the one-row kernels and the multi-row window kernels."""
+    print("case moe_every_scale_code T=%d" % T, flush=True)
+    D, F, E, K = 512, 128, 16, 4
+    m = mi.make_layer(wz, 23, 6, D, F, E, K)
+    for e in range(E):
+        b = m.blobs[e]
+        nb = (b.size - 16) // 36
+        blk = b[:nb * 36].reshape(nb, 36)
+        blk[:, :4] = ((np.arange(nb * 4) + 37 * e) % 256).astype(np.uint8).reshape(nb, 4)
+    x = mi.make_x(wz, 23, 6, T, D).ravel()
+    rec = wz.wzy_nvfp4_expert_bytes(D, F)
+    planes = np.empty(E * rec, np.uint8)
+    for e in range(E):
+        wz.wzy_nvfp4_repack_host(m.blobs[e].ctypes.data, planes[e * rec:].ctypes.data, D, F)
+    arr = mi.blob_ptr_array(m)
+    ow = mi.orc_weights(oracle_lib, m, arr)
+    comb_o = np.empty(T * D, np.float32); ids_o = np.empty(T * K, np.int32); wts_o = np.empty(T * K, np.float32)
+    logits = np.empty(T * E, np.float32)
+    assert orc.orc_moe_block(C.byref(ow), ptr(x), T, ptr(comb_o), ptr(ids_o), ptr(wts_o), ptr(logits), None) == 0
+    w, keep = device_layer(wz, m, planes=planes)
+    comb, ids, wts = run_gpu_moe(wz, w, x, T)
+    assert check_ids(orc, logits, E, K, T, ids, ids_o) == T
+    assert np.isfinite(comb).all()
+    np.testing.assert_allclose(comb, comb_o, rtol=2e-2, atol=1e-2)
+
+
 @pytest.mark.parametrize("V,T", [(151936, 1), (151936, 4), (248320, 2), (3000, 8)])
 def test_row_argmax_top16_parity(wz, orc, gpu, V, T):
     rng = np.random.default_rng(V + T)
@@ -349,9 +380,9 @@ def test_moe_time_kernels_bursts(wz, gpu):
     xd = dev(x)
     nws = wz.wzy_moe_workspace_bytes(D, F, E, K, T)
     ws = DA(nws, np.uint8, zero=True)
-    gu, dn = C.c_float(0), C.c_float(0)
-    wz.wzy_moe_time_kernels(arr, 3, T, xd.ptr, ws.ptr, nws, 12, C.byref(gu), C.byref(dn), None)
-    assert 0.5 < gu.value < 1000 and 0.5 < dn.value < 1000, (gu.value, dn.value)
+    gu, dn, bl = C.c_float(0), C.c_float(0), C.c_float(0)
+    wz.wzy_moe_time_kernels(arr, 3, T, xd.ptr, ws.ptr, nws, 12, C.byref(gu), C.byref(dn), C.byref(bl), None)
+    assert 0.5 < gu.value < 1000 and 0.5 < dn.value < 1000 and 1.0 < bl.value < 2000, (gu.value, dn.value, bl.value)
     after = run_gpu_moe(wz, layers[0], x, T)
     for a, b in zip(before, after):
         assert np.array_equal(a, b)

@@ -1,16 +1,19 @@
 // moe.hip -- NVFP4 mixture-of-experts decode block for gfx950.
 //
 // Launch sequence of wzy_moe_block (T window rows, K routed experts per row), three launches:
-//   1. router       logits [T x E] (bf16) + the shared-expert gate scalar row.  T > 1: moe_router,
-//                   whose last workgroup to finish routes the window once (softmax top-K, weights,
-//                   groups: each distinct expert of the window once, with its (row, slot) members,
-//                   so its weights stream from HBM once) and publishes the tables.  T = 1: a plain
-//                   gemv_segs launch, and every gate/up workgroup routes the row itself (one routing
-//                   pass plus a cross-workgroup handoff costs more than the in-workgroup routing).
-//   2. moe_gate_up  routed workgroup (group, 32-row tile): T > 1 reads its group's expert and issues
-//                   the weight loads at entry, staging its member rows of x quantised per 16 in LDS
-//                   meanwhile; T = 1 prefetches the logits, stages x, routes, then loads (workgroup 0
-//                   publishes the routing).  Then the gate+up NVFP4 GEMV, SwiGLU and the per-16 int8
+//   1. router       logits [T x E] (bf16) + the shared-expert gate scalar row.  T <= 4: a plain
+//                   gemv_segs launch, and the gate/up workgroups route the window themselves (one
+//                   routing pass plus a cross-workgroup handoff costs more).  T > 4: moe_router,
+//                   whose last workgroup to finish routes the window once and publishes the tables.
+//                   Routing = softmax top-K, weights, and groups: each distinct expert of the window
+//                   once, with its (row, slot) members, so its weights stream from HBM once.
+//   2. gate/up      T = 1, moe_gate_up_kernel: routed workgroup (expert, 32-row tile) prefetches the
+//                   logits, stages x, routes, then loads its weights (workgroup 0 publishes the
+//                   routing).  1 < T <= 4, moe_gate_up_window_kernel: one resident round of about one
+//                   workgroup per CU, each routing the window and then taking the (group, tile) items
+//                   bid, bid + n, ... with two register sets of weight loads in flight.  T > 4,
+//                   moe_gate_up_kernel with the published tables: workgroup (group, tile) issues its
+//                   weight loads at entry.  Then the gate+up NVFP4 GEMV, SwiGLU and the per-16 int8
 //                   requant.  Shared workgroups run the Q8_0 shared expert on x quantised per 32.
 //   3. moe_down     workgroup = 8 output rows for all groups + the shared expert, activations
 //                   staged in LDS, combine in LDS:
@@ -41,9 +44,21 @@ struct MoeRtArgs {
 };
 // work items whose loads a 16-lane slot issues together: a one-row window's 11 x 8 items fit in
 // one batch of 6 per slot, so every weight load of the workgroup is issued at once
-template <int T>
-constexpr int dn_batch() { return T == 1 ? 6 : 4; }
+// threads of a moe_down workgroup: 16 slots for one-row windows; for more rows 64 slots of 5 items
+// where one 32-value chunk per lane covers a row (n_ff <= 512), the activations are staged in LDS and
+// the registers allow it (T <= 4), so that a T = 4 window's up to 41 groups x 8 rows take one batch
+// round; otherwise 32 slots of 4 items (16 where a row takes three or four chunk rounds, whose
+// registers need a SIMD to itself)
+template <int T, int CI, bool STAGE>
+constexpr bool dn_wide() { return T > 1 && T <= 4 && CI == 1 && STAGE; }
+template <int T, int CI, bool STAGE>
+constexpr int dn_batch() { return T == 1 ? 6 : (dn_wide<T, CI, STAGE>() ? 5 : 4); }
+template <int T, int CI, bool STAGE>
+constexpr int dn_threads() { return T == 1 ? 256 : (dn_wide<T, CI, STAGE>() ? 1024 : (CI <= 2 ? 512 : 256)); }
 constexpr int MAX_ENT = WZY_MAX_W * MOE_MAX_K;
+// windows of up to this many rows route inside the gate/up workgroups (moe_gate_up_window_kernel for
+// T > 1); longer ones route once in moe_router
+constexpr int GU_WINDOW_MAX_T = 4;
 constexpr int DN_STAGE_BYTES = 48 * 1024;   // activation staging limit of moe_down
 
 
@@ -51,11 +66,21 @@ constexpr int DN_STAGE_BYTES = 48 * 1024;   // activation staging limit of moe_d
 // per-16 scales), accumulated the way the reference does per 16-block:
 // acc = fma(ws * xs, isum, acc)   (src/wzy_kernels_v2.cuh:1646-1647).
 // The e2m1 codes are expanded by the hardware fp4 -> f16 conversion with scale 2, which gives the
-// doubled codes 2*e2m1 (integers -12..12; ue4m3_half carries the matching 0.5), and the int8
+// doubled codes 2*e2m1 (integers -12..12; ue4m3x2_half carries the matching 0.5), and the int8
 // activations are held as f16 pairs: pair p of a 16-value sub-block is (x_p, x_{p+8}), matching code
 // byte p (value p in its low nibble, p+8 in its high one).  Every product and partial sum is an
 // integer below 2^24, so each f32 dot-2 chain equals the integer dot isum exactly.
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float v2f_t __attribute__((ext_vector_type(2)));
+// The two e4m3 block scales of a 16-bit scale pair (low byte first), each times 0.5 (the factor that
+// the doubled e2m1 codes carry): one hardware fp8 -> f32 conversion with scale 0.5, the sign bit
+// cleared.  Code 0x7F, NaN in OCP e4m3, is 480 in the unsigned reading of the reference's scales,
+// 240 after the halving: the NaN-discarding min gives it and leaves every other code (at most 224)
+// alone.  Equal to ue4m3_half on both bytes for all 128 codes.
+WZY_DEV v2f_t ue4m3x2_half(uint32_t s) {
+    const v2f_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(s & 0x7F7Fu, 0.5f, false);
+    return v2f_t{fminf(v.x, 240.0f), fminf(v.y, 240.0f)};
+}
 template <int J>
 WZY_DEV half2_t fp4x2_h(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, J); }
 WZY_DEV float e2m1_dot16_h(uint32_t w0, uint32_t w1, const half2_t* xp) {
@@ -75,6 +100,30 @@ WZY_DEV float nvfp4_chunk_fma_h(const uint4 c, float wsa, float wsb, const half2
     acc = fmaf(wsa * xsa, e2m1_dot16_h(c.x, c.y, &xp[0]), acc);
     acc = fmaf(wsb * xsb, e2m1_dot16_h(c.z, c.w, &xp[8]), acc);
     return acc;
+}
+
+// The 32 e2m1 codes of a 16-byte chunk as doubled f16 pairs in e2m1_dot16_h's order: wq[0..7] the
+// first 16-value sub-block, wq[8..15] the second.
+WZY_DEV void fp4_expand16(const int4 c, half2_t (&wq)[16]) {
+    const uint32_t w[4] = {(uint32_t) c.x, (uint32_t) c.y, (uint32_t) c.z, (uint32_t) c.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        wq[4 * d] = fp4x2_h<0>(w[d]);
+        wq[4 * d + 1] = fp4x2_h<1>(w[d]);
+        wq[4 * d + 2] = fp4x2_h<2>(w[d]);
+        wq[4 * d + 3] = fp4x2_h<3>(w[d]);
+    }
+}
+// e2m1_dot16_h on codes already expanded: pairs 0-3 and 4-7 in two chains (every product and partial
+// sum an integer below 2^24, so the result is the exact integer dot in any order)
+WZY_DEV float dot16_pairs(const half2_t* wq, const half2_t* xp) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        a = __builtin_amdgcn_fdot2(wq[p], xp[p], a, false);
+        b = __builtin_amdgcn_fdot2(wq[4 + p], xp[4 + p], b, false);
+    }
+    return a + b;
 }
 
 // Exclusive count of `pred` over threads 0..255 in thread order (4 waves); `total` = full count.
@@ -186,6 +235,8 @@ struct RouteLds {
     int n_groups;
     int c[8];
     uint64_t cand[4][64];          // per-wave candidate keys of route_row (waves 0-3 route)
+    uint32_t rows[1024];           // one-wave grouping: per expert the window rows that routed it,
+                                   // then its group number
 };
 
 // Logits of one row per wave: RV per lane (lane + 64*i), RV = 8 for E <= 512, 16 for E <= 1024.
@@ -246,8 +297,41 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
         if (lane < K) { r.ids[t * K + lane] = my_id; r.w[t * K + lane] = my_w / sc; }
     }
     __syncthreads();
-    // grouping: leader = first entry of an expert, slot = rank among the expert's entries
     const int n_ent = T * K;
+    if (n_ent <= 64) {
+        // grouping in one wave, lane = entry (row t = lane / K): an expert occurs at most once per
+        // row, so its entries are described by the mask of the rows that routed it (LDS OR per expert).
+        // An entry's slot is the number of earlier rows in that mask, the entry with slot 0 leads the
+        // group, and leaders are numbered in entry order by a ballot prefix count; every workgroup that
+        // routes the window gets the same tables.
+        if (wv == 0) {
+            const bool on = lane < n_ent;
+            const int id = on ? r.ids[lane] : 0, t = lane / K;
+            if (on) r.rows[id] = 0u;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            if (on) atomicOr(&r.rows[id], 1u << t);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const uint32_t m = on ? r.rows[id] : 0u;
+            const int slot = __popc(m & ((1u << t) - 1u));
+            const bool lead = on && slot == 0;
+            const uint64_t leads = __ballot(lead);
+            if (lead) r.rows[id] = 0x80000000u | (uint32_t) __builtin_amdgcn_mbcnt_hi(
+                                                       (uint32_t) (leads >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t) leads, 0));
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            if (on) {
+                const int g = (int) (r.rows[id] & 0xFFFFu);
+                if (slot < WZY_MAX_W) r.gmem[g][slot] = lane;
+                if (lead) {
+                    r.gexp[g] = id;
+                    r.gcnt[g] = min(__popc(m), WZY_MAX_W);
+                }
+            }
+            if (lane == 0) r.n_groups = __popcll(leads);
+        }
+        __syncthreads();
+        return;
+    }
+    // grouping: leader = first entry of an expert, slot = rank among the expert's entries
     int id = -1, leader = 0, slot = 0, cnt = 0;
     if (tid < n_ent) {
         id = r.ids[tid];
@@ -277,194 +361,58 @@ WZY_DEV void route_compute(float (&p)[(T + 3) / 4][RV], int E, int K, RouteLds& 
     __syncthreads();
 }
 
-}  // namespace
+// The routing tables of the window for moe_down (and the caller's ids / weights), written by one
+// workgroup: ids, weights, the group count and each group's expert, member count and members.
+WZY_DEV void publish_routing(const RouteLds& r, const MoeGuArgs& a, int n_ent) {
+    for (int i = threadIdx.x; i < n_ent; i += blockDim.x) {
+        a.ids[i] = r.ids[i];
+        a.wts[i] = r.w[i];
+        if (i < r.n_groups) {
+            a.grp_exp[i] = r.gexp[i];
+            a.grp_cnt[i] = r.gcnt[i];
+            for (int m = 0; m < WZY_MAX_W; ++m) a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
+        }
+    }
+    if (threadIdx.x == 0) *a.n_groups = r.n_groups;
+}
 
-// ---------------------------------------------------------------------------------------------
-// gate/up, eight waves per workgroup.  Routed workgroups: one (group, 32-row tile); wave w owns rows
-// j = 32*tile + 4w .. +3 of both gate and up, so SwiGLU and the 16-wide requant (two 16-row blocks)
-// stay inside the workgroup (D > 2048: 16-row tiles, two rows per wave).  With 32-row tiles the launch has few enough workgroups (10 experts x 16
-// + 32 shared at the BASELINE shapes) that each gets a CU of its own.
-// reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
-// Shared workgroups: 16 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32 requant of
-// silu_mul_quant32_multi runs in moe_down, so the 2.2 MB shared stream spreads over F/16 workgroups).
+// chunk `cc` of x row `t` ([rows x D] fp32) quantised per 16 into LDS slot i: 16 f16 pairs
+// (nvfp4_chunk_fma_h's order) and the two per-16 scales
+WZY_DEV void stage_x16(const float* __restrict__ x, int D, int t, int cc, int i, half2_t* s_xh, float2* s_xs2) {
+    const float4* xp = (const float4*) (x + (size_t) t * D + (size_t) cc * 32);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float4 f = xp[k];
+        v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+    half2_t xq[16];
+    float da, db;
+    quant16_pairs(v, xq, da, db);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xq[4 * k]),
+                                                           __builtin_bit_cast(uint32_t, xq[4 * k + 1]),
+                                                           __builtin_bit_cast(uint32_t, xq[4 * k + 2]),
+                                                           __builtin_bit_cast(uint32_t, xq[4 * k + 3]));
+    s_xs2[i] = make_float2(da, db);
+}
+
+// Shared-expert workgroup sb of a gate/up launch: rows j in [SJ*sb, SJ*sb + SJ) (SJ = 16, or 8 for
+// D > 2048), wave w owns SRW = SJ/8 consecutive rows of both gate and up; NCL 32-blocks of x per
+// lane.  The SwiGLU values go out as fp32; moe_down quantises them per 32.
 // reference: launch_gemm_q8p x2 + silu_mul_quant32_multi (src/wzy_stage_v2.cuh:711-713;
 // src/wzy_kernels_v2.cuh:1247-1280).
-// Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
-// scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
-// NCL = 32-column chunks of x per lane: 1 for D <= 2048, 2 for D <= 4096 (the reference's NE = 2560).
-// ---------------------------------------------------------------------------------------------
-template <int T, bool ROUTE, int RV, int NCL>
-__global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
-    extern __shared__ __align__(16) unsigned char s_dyn[];
-    __shared__ float s_act[WZY_MAX_W][32];
-    __shared__ int s_mem[WZY_MAX_W];
+// Dynamic LDS: x quantised per 32, [T][D/32] int4 first halves, [T][D/32] int4 second halves,
+// [T][D/32] float scales.
+template <int T, int NCL>
+WZY_DEV void gu_shared(const MoeGuArgs& a, int sb, unsigned char* s_dyn) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int bid = blockIdx.x;
-    const int D = a.D, F = a.F, K = a.K;
+    const int D = a.D, F = a.F;
     const int nc = D / 32;
-    // routed path: f16 activation pairs [T*nc][16] then per-16 scales [T*nc] float2; shared path:
-    // per-32 int8 halves [T*nc] int4 x2 then per-32 scales [T*nc] float (same allocation)
-    half2_t* s_xh = (half2_t*) s_dyn;
-    float2* s_xs2 = (float2*) (s_xh + (size_t) T * nc * 16);
     int4* s_qa = (int4*) s_dyn;
     int4* s_qb = s_qa + (size_t) T * nc;
     float* s_sc = (float*) (s_qb + (size_t) T * nc);
-
-    if (bid < a.n_routed_wg) {
-        constexpr int TR = gu_tile_rows(NCL), RPW = TR / 8;     // tile rows; gate (and up) rows per wave
-        const int tiles = F / TR;
-        const int g = bid / tiles, jt = bid - g * tiles;
-        const int j0 = jt * TR + RPW * w;
-        const MoeOffsets o = moe_offsets(D, F);
-        int e = 0, cnt = 0;
-        // lane chunks c = lane, lane + 64; rows rr < RPW gate j0 + rr, the others up j0 + rr - RPW
-        int4 code[NCL][2 * RPW];
-        uint32_t sc2[NCL][2 * RPW];
-        // the weight loads of the lane (clamped, unconditional), issued as soon as the expert is known
-        auto load_weights = [&](const uint8_t* rec) {
-#pragma unroll
-            for (int k = 0; k < NCL; ++k) {
-                const int c = min(lane + 64 * k, nc - 1);
-#pragma unroll
-                for (int rr = 0; rr < 2 * RPW; ++rr) {
-                    const int row = (rr < RPW) ? (j0 + rr) : (F + j0 + rr - RPW);
-                    code[k][rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
-                    sc2[k][rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
-                }
-            }
-        };
-        // chunk `cc` of x row `t` quantised per 16 into LDS slot i
-        auto stage16 = [&](int t, int cc, int i) {
-            const float4* xp = (const float4*) (a.x + (size_t) t * D + (size_t) cc * 32);
-            float v[32];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float4 f = xp[k];
-                v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-            }
-            half2_t xq[16];
-            float da, db;
-            quant16_pairs(v, xq, da, db);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xq[4 * k]),
-                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 1]),
-                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 2]),
-                                                                   __builtin_bit_cast(uint32_t, xq[4 * k + 3]));
-            s_xs2[i] = make_float2(da, db);
-        };
-        if constexpr (ROUTE) {
-            // in-workgroup routing (one-row windows): the logits are prefetched, x is staged while they
-            // arrive, every workgroup routes the row (workgroup 0 publishes the tables for moe_down)
-            __shared__ RouteLds r;
-            float p[(T + 3) / 4][RV];
-            route_prefetch<T, RV>(a.logits, a.E, p);
-            if (tid < 256)                               // item 0 on wave 1: wave 0 routes the first row
-                for (int i = (tid + 192) & 255; i < T * nc; i += 256) stage16(i / nc, i % nc, i);
-            route_compute<T, RV>(p, a.E, K, r);
-            if (g >= r.n_groups) return;                 // workgroup-uniform (workgroup 0 has g = 0)
-            e = __builtin_amdgcn_readfirstlane(r.gexp[g]);
-            cnt = r.gcnt[g];
-            load_weights(a.experts + (size_t) e * o.rec);
-            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? r.gmem[g][tid] : 0;
-            if (bid == 0) {
-                const int n_ent = T * K;
-                for (int i = tid; i < n_ent; i += blockDim.x) {
-                    a.ids[i] = r.ids[i];
-                    a.wts[i] = r.w[i];
-                    if (i < r.n_groups) {
-                        a.grp_exp[i] = r.gexp[i];
-                        a.grp_cnt[i] = r.gcnt[i];
-                        for (int m = 0; m < WZY_MAX_W; ++m)
-                            a.grp_mem[i * WZY_MAX_W + m] = m < r.gcnt[i] ? r.gmem[i][m] : 0;
-                    }
-                }
-                if (tid == 0) *a.n_groups = r.n_groups;
-            }
-        } else {
-            // routing tables published by moe_router: the expert is known at entry, its weights are
-            // requested before x is staged (member m's chunk cc at LDS slot m * nc + cc)
-            const int ng = *a.n_groups;
-            e = __builtin_amdgcn_readfirstlane(a.grp_exp[g]);
-            if (g >= ng) return;                         // workgroup-uniform
-            cnt = a.grp_cnt[g];
-            load_weights(a.experts + (size_t) e * o.rec);
-            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? a.grp_mem[g * WZY_MAX_W + tid] : 0;
-            for (int i = tid; i < cnt * nc; i += (int) blockDim.x) {
-                const int m = i / nc;
-                stage16(a.grp_mem[g * WZY_MAX_W + m] / K, i - m * nc, i);
-            }
-        }
-        const uint8_t* rec = a.experts + (size_t) e * o.rec;
-        const float sc_gate = ((const float*) (rec + o.tail))[0];
-        const float sc_up = ((const float*) (rec + o.tail))[1];
-        __syncthreads();
-        float acc[2 * RPW][T];
-#pragma unroll
-        for (int rr = 0; rr < 2 * RPW; ++rr)
-#pragma unroll
-            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
-#pragma unroll
-        for (int k = 0; k < NCL; ++k) {
-            const int c = lane + 64 * k;
-            if (c >= nc) continue;
-#pragma unroll
-            for (int m = 0; m < T; ++m) {
-                if (m < cnt) {
-                    const int xi = (ROUTE ? s_mem[m] / K : m) * nc + c;
-                    half2_t xp[16];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
-                        xp[4 * q] = __builtin_bit_cast(half2_t, u.x);
-                        xp[4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
-                        xp[4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
-                        xp[4 * q + 3] = __builtin_bit_cast(half2_t, u.w);
-                    }
-                    const float2 xs = s_xs2[xi];
-#pragma unroll
-                    for (int rr = 0; rr < 2 * RPW; ++rr) {
-                        const uint32_t sw = sc2[k][rr];
-                        const int4 cw = code[k][rr];
-                        const float wsa = ue4m3_half(sw & 0xFFu), wsb = ue4m3_half(sw >> 8);
-                        const uint4 cu = make_uint4((uint32_t) cw.x, (uint32_t) cw.y, (uint32_t) cw.z, (uint32_t) cw.w);
-                        acc[rr][m] = nvfp4_chunk_fma_h(cu, wsa, wsb, xp, xs.x, xs.y, acc[rr][m]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < T; ++m) {
-            if (m < cnt) {
-#pragma unroll
-                for (int q = 0; q < RPW; ++q) {
-                    const float gv = wave_sum(acc[q][m]) * sc_gate;
-                    const float uv = wave_sum(acc[RPW + q][m]) * sc_up;
-                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
-                }
-            }
-        }
-        __syncthreads();
-        if (tid < cnt * TR) {                            // one 16-lane row per (member, 16-row block)
-            const int m = tid / TR, jj = tid % TR, jl = jj & 15;
-            const int blk = (TR / 16) * jt + (jj >> 4);  // 16-row block of the F rows
-            const float v = s_act[m][jj];
-            const float amax = max16(fabsf(v));
-            const float d = amax / 127.0f;
-            const float inv = d > 0.f ? 127.0f / amax : 0.f;
-            const int q = max(-127, min(127, rn_int(v * inv)));
-            const int f = s_mem[m];
-            a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
-                __builtin_bit_cast(uint16_t, (_Float16) (float) q);
-            if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
-        }
-        return;
-    }
-
-    // shared expert: rows j in [SJ*sb, SJ*sb + SJ) (SJ = 16, or 8 for D > 2048), wave w owns SRW = SJ/8
-    // consecutive rows of both gate and up; NCL 32-blocks of x per lane.  The SwiGLU values go out as
-    // fp32; moe_down quantises them per 32.
-    const int sb = bid - a.n_routed_wg;
     constexpr int SJ = sh_tile_rows(NCL), SRW = SJ / 8;
     int4 c0[NCL][2 * SRW], c1[NCL][2 * SRW];
     uint32_t sraw[NCL][2 * SRW];     // 16-bit scales in 32-bit registers (no packing that waits for the load)
@@ -528,6 +476,313 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
             const float uv = wave_sum(acc[SRW + q][t]);
             if (lane == 0) a.shact[(size_t) t * F + j0 + q] = siluf_(gv) * uv;
         }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// gate/up, eight waves per workgroup.  Routed workgroups: one (group, 32-row tile); wave w owns rows
+// j = 32*tile + 4w .. +3 of both gate and up, so SwiGLU and the 16-wide requant (two 16-row blocks)
+// stay inside the workgroup (D > 2048: 16-row tiles, two rows per wave).  With 32-row tiles the launch has few enough workgroups (10 experts x 16
+// + 32 shared at the BASELINE shapes) that each gets a CU of its own.
+// reference: exp_gu_quant_grouped (src/wzy_kernels_v2.cuh:1583-1721).
+// Shared workgroups (gu_shared): 16 rows of the Q8_0 shared gate/up and SwiGLU (fp32 out; the per-32
+// requant of silu_mul_quant32_multi runs in moe_down, so the 2.2 MB shared stream spreads over F/16
+// workgroups).
+// Dynamic LDS: x quantised, [T][D/32] int4 first halves, [T][D/32] int4 second halves, then the
+// scales ([T][D/32] float2 per-16 pairs, or [T][D/32] float per-32).
+// NCL = 32-column chunks of x per lane: 1 for D <= 2048, 2 for D <= 4096 (the reference's NE = 2560).
+// ---------------------------------------------------------------------------------------------
+template <int T, bool ROUTE, int RV, int NCL>
+__global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    __shared__ float s_act[WZY_MAX_W][32];
+    __shared__ int s_mem[WZY_MAX_W];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int bid = blockIdx.x;
+    const int D = a.D, F = a.F, K = a.K;
+    const int nc = D / 32;
+    // routed path: f16 activation pairs [T*nc][16] then per-16 scales [T*nc] float2 (the shared path
+    // lays out its per-32 quantisation in the same allocation)
+    half2_t* s_xh = (half2_t*) s_dyn;
+    float2* s_xs2 = (float2*) (s_xh + (size_t) T * nc * 16);
+
+    if (bid < a.n_routed_wg) {
+        constexpr int TR = gu_tile_rows(NCL), RPW = TR / 8;     // tile rows; gate (and up) rows per wave
+        const int tiles = F / TR;
+        const int g = bid / tiles, jt = bid - g * tiles;
+        const int j0 = jt * TR + RPW * w;
+        const MoeOffsets o = moe_offsets(D, F);
+        int e = 0, cnt = 0;
+        // lane chunks c = lane, lane + 64; rows rr < RPW gate j0 + rr, the others up j0 + rr - RPW
+        int4 code[NCL][2 * RPW];
+        uint32_t sc2[NCL][2 * RPW];
+        // the weight loads of the lane (clamped, unconditional), issued as soon as the expert is known
+        auto load_weights = [&](const uint8_t* rec) {
+#pragma unroll
+            for (int k = 0; k < NCL; ++k) {
+                const int c = min(lane + 64 * k, nc - 1);
+#pragma unroll
+                for (int rr = 0; rr < 2 * RPW; ++rr) {
+                    const int row = (rr < RPW) ? (j0 + rr) : (F + j0 + rr - RPW);
+                    code[k][rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
+                    sc2[k][rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+                }
+            }
+        };
+        auto stage16 = [&](int t, int cc, int i) { stage_x16(a.x, D, t, cc, i, s_xh, s_xs2); };
+        if constexpr (ROUTE) {
+            // in-workgroup routing (one-row windows): the logits are prefetched, x is staged while they
+            // arrive, every workgroup routes the row (workgroup 0 publishes the tables for moe_down)
+            __shared__ RouteLds r;
+            float p[(T + 3) / 4][RV];
+            route_prefetch<T, RV>(a.logits, a.E, p);
+            if (tid < 256)                               // item 0 on wave 1: wave 0 routes the first row
+                for (int i = (tid + 192) & 255; i < T * nc; i += 256) stage16(i / nc, i % nc, i);
+            route_compute<T, RV>(p, a.E, K, r);
+            if (g >= r.n_groups) return;                 // workgroup-uniform (workgroup 0 has g = 0)
+            e = __builtin_amdgcn_readfirstlane(r.gexp[g]);
+            cnt = r.gcnt[g];
+            load_weights(a.experts + (size_t) e * o.rec);
+            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? r.gmem[g][tid] : 0;
+            if (bid == 0) publish_routing(r, a, T * K);
+        } else {
+            // routing tables published by moe_router: the expert is known at entry, its weights are
+            // requested before x is staged (member m's chunk cc at LDS slot m * nc + cc)
+            const int ng = *a.n_groups;
+            e = __builtin_amdgcn_readfirstlane(a.grp_exp[g]);
+            if (g >= ng) return;                         // workgroup-uniform
+            cnt = a.grp_cnt[g];
+            load_weights(a.experts + (size_t) e * o.rec);
+            if (tid < WZY_MAX_W) s_mem[tid] = tid < cnt ? a.grp_mem[g * WZY_MAX_W + tid] : 0;
+            for (int i = tid; i < cnt * nc; i += (int) blockDim.x) {
+                const int m = i / nc;
+                stage16(a.grp_mem[g * WZY_MAX_W + m] / K, i - m * nc, i);
+            }
+        }
+        const uint8_t* rec = a.experts + (size_t) e * o.rec;
+        const float sc_gate = ((const float*) (rec + o.tail))[0];
+        const float sc_up = ((const float*) (rec + o.tail))[1];
+        __syncthreads();
+        float acc[2 * RPW][T];
+#pragma unroll
+        for (int rr = 0; rr < 2 * RPW; ++rr)
+#pragma unroll
+            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NCL; ++k) {
+            const int c = lane + 64 * k;
+            if (c >= nc) continue;
+#pragma unroll
+            for (int m = 0; m < T; ++m) {
+                if (m < cnt) {
+                    const int xi = (ROUTE ? s_mem[m] / K : m) * nc + c;
+                    half2_t xp[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
+                        xp[4 * q] = __builtin_bit_cast(half2_t, u.x);
+                        xp[4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
+                        xp[4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
+                        xp[4 * q + 3] = __builtin_bit_cast(half2_t, u.w);
+                    }
+                    const float2 xs = s_xs2[xi];
+#pragma unroll
+                    for (int rr = 0; rr < 2 * RPW; ++rr) {
+                        const uint32_t sw = sc2[k][rr];
+                        const int4 cw = code[k][rr];
+                        const v2f_t ws = ue4m3x2_half(sw);
+                        const float wsa = ws.x, wsb = ws.y;
+                        const uint4 cu = make_uint4((uint32_t) cw.x, (uint32_t) cw.y, (uint32_t) cw.z, (uint32_t) cw.w);
+                        acc[rr][m] = nvfp4_chunk_fma_h(cu, wsa, wsb, xp, xs.x, xs.y, acc[rr][m]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < T; ++m) {
+            if (m < cnt) {
+#pragma unroll
+                for (int q = 0; q < RPW; ++q) {
+                    const float gv = wave_sum(acc[q][m]) * sc_gate;
+                    const float uv = wave_sum(acc[RPW + q][m]) * sc_up;
+                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < cnt * TR) {                            // one 16-lane row per (member, 16-row block)
+            const int m = tid / TR, jj = tid % TR, jl = jj & 15;
+            const int blk = (TR / 16) * jt + (jj >> 4);  // 16-row block of the F rows
+            const float v = s_act[m][jj];
+            const float amax = max16(fabsf(v));
+            const float d = amax / 127.0f;
+            const float inv = d > 0.f ? 127.0f / amax : 0.f;
+            const int q = max(-127, min(127, rn_int(v * inv)));
+            const int f = s_mem[m];
+            a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
+                __builtin_bit_cast(uint16_t, (_Float16) (float) q);
+            if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
+        }
+        return;
+    }
+
+    gu_shared<T, NCL>(a, bid - a.n_routed_wg, s_dyn);
+}
+
+// ---------------------------------------------------------------------------------------------
+// gate/up of multi-row windows (T > 1), one round of resident workgroups.  The first n_routed_wg
+// workgroups (about one per CU beside the shared ones) each route the window themselves from the
+// router logits (every workgroup computes the same tables; workgroup 0 publishes them for moe_down)
+// and stage all T rows of x quantised per 16 in LDS; then each takes the window's work items
+// (group, tile) bid, bid + n_routed_wg, ... in phases of MAXI items, issuing every weight load of a
+// phase before computing its first item.  The window's routing thus costs one pass per workgroup,
+// run in parallel, instead of a routing pass behind a cross-workgroup handoff, and no workgroup waits
+// for a second round of residency.  Items and arithmetic are those of moe_gate_up_kernel.
+// The remaining workgroups run the shared expert (gu_shared).
+// ---------------------------------------------------------------------------------------------
+template <int T, int RV, int NCL>
+__global__ void __launch_bounds__(512) moe_gate_up_window_kernel(MoeGuArgs a) {
+    extern __shared__ __align__(16) unsigned char s_dyn[];
+    __shared__ float s_act2[2][WZY_MAX_W][32];       // SwiGLU values, alternating between items
+    __shared__ RouteLds r;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int bid = blockIdx.x;
+    if (bid >= a.n_routed_wg) {
+        gu_shared<T, NCL>(a, bid - a.n_routed_wg, s_dyn);
+        return;
+    }
+    const int D = a.D, F = a.F, K = a.K;
+    const int nc = D / 32, nr = a.n_routed_wg;
+    half2_t* s_xh = (half2_t*) s_dyn;
+    float2* s_xs2 = (float2*) (s_xh + (size_t) T * nc * 16);
+    constexpr int TR = gu_tile_rows(NCL), RPW = TR / 8;         // tile rows; gate (and up) rows per wave
+    const int tiles = F / TR;
+    const MoeOffsets o = moe_offsets(D, F);
+    {
+        float p[(T + 3) / 4][RV];
+        route_prefetch<T, RV>(a.logits, a.E, p);
+        // waves 4-7 stage x first (waves 0-3 route)
+        for (int i = (tid + 256) & 511; i < T * nc; i += 512) stage_x16(a.x, D, i / nc, i % nc, i, s_xh, s_xs2);
+        route_compute<T, RV>(p, a.E, K, r);              // ends with a barrier
+    }
+    if (bid == 0) publish_routing(r, a, T * K);
+    const int n_items = r.n_groups * tiles;
+    // the weight loads of one item (group, tile) into one register set
+    auto load_item = [&](int item, int4 (&code)[NCL][2 * RPW], uint32_t (&sc2)[NCL][2 * RPW], float2& tail) {
+        const int g = item / tiles, jt = item - g * tiles;
+        const int e = __builtin_amdgcn_readfirstlane(r.gexp[g]);
+        const uint8_t* rec = a.experts + (size_t) e * o.rec;
+        const int j0 = jt * TR + RPW * w;
+#pragma unroll
+        for (int k = 0; k < NCL; ++k) {
+            const int c = min(lane + 64 * k, nc - 1);
+#pragma unroll
+            for (int rr = 0; rr < 2 * RPW; ++rr) {
+                const int row = (rr < RPW) ? (j0 + rr) : (F + j0 + rr - RPW);
+                code[k][rr] = ld_stream_i4(rec + o.gu_codes + (size_t) row * (D / 2) + (size_t) c * 16);
+                sc2[k][rr] = *(const uint16_t*) (rec + o.gu_scales + (size_t) row * (D / 16) + 2 * c);
+            }
+        }
+        tail = *(const float2*) (rec + o.tail);
+    };
+    // gate/up rows of one item for its members, SwiGLU, per-16 requant into ah16 / as16.  Each row's
+    // codes are expanded to f16 pairs once and dotted with every member's activations.
+    auto compute_item = [&](int item, const int4 (&code)[NCL][2 * RPW], const uint32_t (&sc2)[NCL][2 * RPW],
+                            float2 tail, float (&s_act)[WZY_MAX_W][32]) {
+        const int g = item / tiles, jt = item - g * tiles;
+        const int cnt = r.gcnt[g];
+        float acc[2 * RPW][T];
+#pragma unroll
+        for (int rr = 0; rr < 2 * RPW; ++rr)
+#pragma unroll
+            for (int m = 0; m < T; ++m) acc[rr][m] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NCL; ++k) {
+            const int c = lane + 64 * k;
+            if (c >= nc) continue;
+            half2_t xq[T][16];
+            float2 xs[T];
+#pragma unroll
+            for (int m = 0; m < T; ++m) {
+                if (m < cnt) {                           // workgroup-uniform
+                    const int xi = (r.gmem[g][m] / K) * nc + c;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
+                        xq[m][4 * q] = __builtin_bit_cast(half2_t, u.x);
+                        xq[m][4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
+                        xq[m][4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
+                        xq[m][4 * q + 3] = __builtin_bit_cast(half2_t, u.w);
+                    }
+                    xs[m] = s_xs2[xi];
+                }
+            }
+#pragma unroll
+            for (int rr = 0; rr < 2 * RPW; ++rr) {
+                const uint32_t sw = sc2[k][rr];
+                const v2f_t ws = ue4m3x2_half(sw);
+                const float wsa = ws.x, wsb = ws.y;
+                half2_t wq[16];
+                fp4_expand16(code[k][rr], wq);
+#pragma unroll
+                for (int m = 0; m < T; ++m) {
+                    if (m < cnt) {
+                        acc[rr][m] = fmaf(wsa * xs[m].x, dot16_pairs(&wq[0], &xq[m][0]), acc[rr][m]);
+                        acc[rr][m] = fmaf(wsb * xs[m].y, dot16_pairs(&wq[8], &xq[m][8]), acc[rr][m]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < T; ++m) {
+            if (m < cnt) {
+#pragma unroll
+                for (int q = 0; q < RPW; ++q) {
+                    const float gv = wave_sum(acc[q][m]) * tail.x;
+                    const float uv = wave_sum(acc[RPW + q][m]) * tail.y;
+                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < cnt * TR) {                            // one 16-lane row per (member, 16-row block)
+            const int m = tid / TR, jj = tid % TR, jl = jj & 15;
+            const int blk = (TR / 16) * jt + (jj >> 4);
+            const float v = s_act[m][jj];
+            const float amax = max16(fabsf(v));
+            const float d = amax / 127.0f;
+            const float inv = d > 0.f ? 127.0f / amax : 0.f;
+            const int q = max(-127, min(127, rn_int(v * inv)));
+            const int f = r.gmem[g][m];
+            a.ah16[((size_t) f * (F / 16) + blk) * 16 + (jl & 7) * 2 + (jl >> 3)] =
+                __builtin_bit_cast(uint16_t, (_Float16) (float) q);
+            if (jl == 0) a.as16[(size_t) f * (F / 16) + blk] = d;
+        }
+        // no barrier here: the next item writes the other s_act buffer, and the one after it passes
+        // the next item's barrier first
+    };
+    // items bid, bid + nr, bid + 2 nr, ... in two register sets: an item's loads are issued as soon
+    // as the set is free, so they are in flight while the other set's item is computed.  The loads are
+    // unconditional (an item past the end reloads the last one, whose lines are cached): a branch
+    // around them would make the compiler wait for every load in flight at the join.
+    int4 code_a[NCL][2 * RPW], code_b[NCL][2 * RPW];
+    uint32_t sc_a[NCL][2 * RPW], sc_b[NCL][2 * RPW];
+    float2 tail_a, tail_b;
+    const int last = n_items - 1;                    // >= 0: a window routes at least one group
+    int it_a = bid, it_b = bid + nr;
+    load_item(min(it_a, last), code_a, sc_a, tail_a);
+    load_item(min(it_b, last), code_b, sc_b, tail_b);
+    while (it_a < n_items) {                         // workgroup-uniform
+        compute_item(it_a, code_a, sc_a, tail_a, s_act2[0]);
+        it_a += 2 * nr;
+        if (it_b >= n_items) break;
+        load_item(min(it_a, last), code_a, sc_a, tail_a);
+        compute_item(it_b, code_b, sc_b, tail_b, s_act2[1]);
+        it_b += 2 * nr;
+        if (it_a >= n_items) break;
+        load_item(min(it_b, last), code_b, sc_b, tail_b);
     }
 }
 
@@ -639,16 +894,17 @@ __global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
 // ---------------------------------------------------------------------------------------------
 // down + combine.  Workgroup = DN_TILE output rows for every group and the shared expert, so the
 // combine comb = sigmoid(sgate)*shared + sum_k w_k * part_k (routed-slot order) stays in LDS.
-// Work items (group or shared, row) go round-robin to sixteen 16-lane slots; a slot issues the
-// loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
+// Work items (group or shared, row) go round-robin to the NT/16 16-lane slots (NT = 256 threads for
+// one-row windows, 1024 for windows of several rows, whose items are up to T*K + 1 groups x 8 rows);
+// a slot issues the loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
 // (F = 512: 16 chunks per row).  STAGE: the routed and shared activations are copied to LDS first
 // (dynamic LDS: routed activations as f16 pairs [n_ent][F/32][16], as [n_ent][F/16] float, shq
 // halves [T][F/32] x2 int4, shs [T][F/32] float).
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
 // ---------------------------------------------------------------------------------------------
-template <int T, bool STAGE, int CI>
-__global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
+template <int T, bool STAGE, int CI, int NT>
+__global__ void __launch_bounds__(NT) moe_down_kernel(MoeDnArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_part[MAX_ENT][DN_TILE];
     __shared__ float s_sh[WZY_MAX_W][DN_TILE];
@@ -659,7 +915,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     const int D = a.D, F = a.F, K = a.K;
     const int d0 = blockIdx.x * DN_TILE;
     const int nchunk = F / 32, n_ent = T * K;
-    constexpr int DN_BATCH = dn_batch<T>();
+    constexpr int DN_BATCH = dn_batch<T, CI, STAGE>(), NSLOT = NT / 16;
     // the group tables of every possible group are loaded without waiting for the group count
     const int ng = *a.n_groups;
     // shared activation quantised per 32 (both variants), then (STAGE) the routed activations
@@ -670,7 +926,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     float* s_as = (float*) (s_ah + (size_t) n_ent * nchunk * 4);
     // Item `tid` of every table and staging copy is loaded (clamped index, no branch) before the
     // first LDS write: a stride loop per table would wait for one table's loads before requesting
-    // the next.  Only copies of more than 256 items loop for the rest.
+    // the next.  Only copies of more than NT items loop for the rest.
     const int n_aq = n_ent * nchunk, n_as4 = n_ent * (F / 16) / 4, n_sh = T * nchunk;
     {
         const int ie = min(tid, n_ent - 1);
@@ -718,7 +974,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             }
         }
     }
-    for (int i = tid + 256; i < n_ent; i += 256) {
+    for (int i = tid + NT; i < n_ent; i += NT) {
         s_gexp[i] = a.grp_exp[i];
         s_gcnt[i] = a.grp_cnt[i];
 #pragma unroll
@@ -726,14 +982,14 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         s_wts[i] = a.wts[i];
     }
     if (STAGE) {
-        for (int i = tid + 256; i < n_aq; i += 256) {
+        for (int i = tid + NT; i < n_aq; i += NT) {
             const uint4* xp = (const uint4*) (a.ah16 + (size_t) i * 32);
 #pragma unroll
             for (int k = 0; k < 4; ++k) s_ah[(size_t) i * 4 + k] = xp[k];
         }
-        for (int i = tid + 256; i < n_as4; i += 256) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
+        for (int i = tid + NT; i < n_as4; i += NT) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
     }
-    for (int i = tid + 256; i < 4 * n_sh; i += 256) {  // whole quads leave the loop together
+    for (int i = tid + NT; i < 4 * n_sh; i += NT) {  // whole quads leave the loop together
         const float4* hp = (const float4*) (a.shact + (size_t) (i >> 2) * 32 + (i & 3) * 8);
         const float4 f0 = hp[0], f1 = hp[1];
         const float hv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
@@ -747,14 +1003,14 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
     const MoeOffsets o = moe_offsets(D, F);
     const int slot = tid >> 4, li = tid & 15;
     const int n_items = (ng + 1) * DN_TILE;          // group ng = shared expert
-    for (int i0 = slot; i0 < n_items; i0 += 16 * DN_BATCH) {
+    for (int i0 = slot; i0 < n_items; i0 += NSLOT * DN_BATCH) {
         float acc[DN_BATCH][T];
         float sdn[DN_BATCH];
 #pragma unroll
         for (int b = 0; b < DN_BATCH; ++b) {
             // tensor scale of the item's expert, loaded with the first codes (shared items read
             // expert 0's and ignore it)
-            const int item = min(i0 + 16 * b, n_items - 1);
+            const int item = min(i0 + NSLOT * b, n_items - 1);
             const int g = item / DN_TILE;
             const uint8_t* rec = a.experts + (g < ng ? (size_t) s_gexp[g] * o.rec : 0);
             sdn[b] = ((const float*) (rec + o.tail))[2];
@@ -774,7 +1030,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             uint32_t sraw[DN_BATCH];
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
-                const int item = min(i0 + 16 * b, n_items - 1);
+                const int item = min(i0 + NSLOT * b, n_items - 1);
                 const int g = item / DN_TILE, d = d0 + item % DN_TILE;
                 const bool routed = g < ng;
                 const uint8_t* rec = a.experts + (routed ? (size_t) s_gexp[g] * o.rec : 0);
@@ -788,13 +1044,14 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
             }
 #pragma unroll
             for (int b = 0; b < DN_BATCH; ++b) {
-                const int item = i0 + 16 * b;
+                const int item = i0 + NSLOT * b;
                 if (item >= n_items || !cvalid) continue;
                 const int g = item / DN_TILE;
                 if (g < ng) {
                     const uint4 cu = make_uint4((uint32_t) c0[b].x, (uint32_t) c0[b].y, (uint32_t) c0[b].z,
                                                 (uint32_t) c0[b].w);
-                    const float wsa = ue4m3_half(sraw[b] & 0xFFu), wsb = ue4m3_half(sraw[b] >> 8);
+                    const v2f_t ws = ue4m3x2_half(sraw[b]);
+                    const float wsa = ws.x, wsb = ws.y;
                     const int cnt = s_gcnt[g];
 #pragma unroll
                     for (int m = 0; m < T; ++m) {
@@ -830,7 +1087,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(MoeDnArgs a) {
         // 16-lane sums (every lane of a slot holds the same item, so the groups are uniform)
 #pragma unroll
         for (int b = 0; b < DN_BATCH; ++b) {
-            const int item = i0 + 16 * b;
+            const int item = i0 + NSLOT * b;
             const bool valid = item < n_items;
             const int g = valid ? item / DN_TILE : 0, rl = item % DN_TILE;
             const int cnt = (valid && g < ng) ? s_gcnt[g] : T;
@@ -922,7 +1179,7 @@ static void launch_rt_t(const MoeRtArgs& a, hipStream_t st) {
 }
 
 int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T, hipStream_t st) {
-    if (T == 1) {                                    // logits only; moe_gate_up routes
+    if (T <= GU_WINDOW_MAX_T) {                      // logits only; the gate/up workgroups route
         GemvSegs segs;
         segs.n = 2;
         segs.seg[0] = GemvSeg{w->router, nullptr, ws.logits, w->n_exp, GEMV_BF16, 0, 0};
@@ -949,6 +1206,19 @@ int moe_launch_route(const wzy_moe_weights* w, const MoeWs& ws, const float* x, 
     return WZY_OK;
 }
 
+// compute units of the current device (queried once per device)
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float* x, int T) {
     MoeGuArgs a{};
     a.experts = w->experts; a.D = w->n_embd; a.F = w->n_ff; a.E = w->n_exp; a.K = w->top_k;
@@ -957,7 +1227,14 @@ static MoeGuArgs gu_args(const wzy_moe_weights* w, const MoeWs& ws, const float*
     a.grp_mem = ws.grp_mem; a.ah16 = ws.ah16; a.as16 = ws.as16;
     a.shg_q = w->sh_gate_q; a.shg_s = w->sh_gate_s; a.shu_q = w->sh_up_q; a.shu_s = w->sh_up_s;
     a.shact = ws.shact;
-    a.n_routed_wg = (w->n_ff / gu_tile_rows(w->n_embd > 2048 ? 2 : 1)) * T * w->top_k;
+    const int ncl = w->n_embd > 2048 ? 2 : 1;
+    const int items = (w->n_ff / gu_tile_rows(ncl)) * T * w->top_k;   // the most (group, tile) items
+    if (T == 1 || T > GU_WINDOW_MAX_T) {
+        a.n_routed_wg = items;                       // one item per workgroup
+    } else {                                         // one round of resident workgroups
+        const int n_sh = w->n_ff / sh_tile_rows(ncl);
+        a.n_routed_wg = std::max(8, std::min(items, device_cus() - n_sh));
+    }
     return a;
 }
 static MoeDnArgs dn_args(const wzy_moe_weights* w, const MoeWs& ws, float* comb) {
@@ -975,9 +1252,16 @@ template <int T, int NCL>
 static void launch_gu_tn(const MoeGuArgs& a, hipStream_t st) {
     const size_t lds = (size_t) T * (a.D / 32) * (16 * sizeof(uint32_t) + sizeof(float2));   // >= the shared path's
     const dim3 grid(a.n_routed_wg + a.F / sh_tile_rows(NCL));
-    if (T > 1) hipLaunchKernelGGL((moe_gate_up_kernel<T, false, 8, NCL>), grid, dim3(512), lds, st, a);
-    else if (a.E <= 512) hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 8, NCL>), grid, dim3(512), lds, st, a);
-    else hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 16, NCL>), grid, dim3(512), lds, st, a);
+    if constexpr (T > GU_WINDOW_MAX_T) {
+        hipLaunchKernelGGL((moe_gate_up_kernel<T, false, 8, NCL>), grid, dim3(512), lds, st, a);
+    } else if constexpr (T > 1) {
+        if (a.E <= 512) hipLaunchKernelGGL((moe_gate_up_window_kernel<T, 8, NCL>), grid, dim3(512), lds, st, a);
+        else hipLaunchKernelGGL((moe_gate_up_window_kernel<T, 16, NCL>), grid, dim3(512), lds, st, a);
+    } else if (a.E <= 512) {
+        hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 8, NCL>), grid, dim3(512), lds, st, a);
+    } else {
+        hipLaunchKernelGGL((moe_gate_up_kernel<1, true, 16, NCL>), grid, dim3(512), lds, st, a);
+    }
 }
 template <int T>
 static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
@@ -987,10 +1271,11 @@ static void launch_gu_t(const MoeGuArgs& a, hipStream_t st) {
 template <int T, int CI>
 static void launch_dn_tc(const MoeDnArgs& a, size_t lds, hipStream_t st) {
     const size_t lds_sh = dn_shared_lds(T, a.F / 32);
+    constexpr int NTS = dn_threads<T, CI, true>(), NTD = dn_threads<T, CI, false>();
     if (lds <= (size_t) DN_STAGE_BYTES)
-        hipLaunchKernelGGL((moe_down_kernel<T, true, CI>), dim3(a.D / DN_TILE), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((moe_down_kernel<T, true, CI, NTS>), dim3(a.D / DN_TILE), dim3(NTS), lds, st, a);
     else
-        hipLaunchKernelGGL((moe_down_kernel<T, false, CI>), dim3(a.D / DN_TILE), dim3(256), lds_sh, st, a);
+        hipLaunchKernelGGL((moe_down_kernel<T, false, CI, NTD>), dim3(a.D / DN_TILE), dim3(NTD), lds_sh, st, a);
 }
 template <int T>
 static void launch_dn_t(const MoeDnArgs& a, hipStream_t st) {
@@ -1063,7 +1348,7 @@ extern "C" int wzy_moe_block(const wzy_moe_weights* w, const float* x, int T, fl
 
 extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers, int T, const float* x, void* workspace,
                                     size_t workspace_bytes, int iters, float* us_gate_up, float* us_down,
-                                    void* stream) {
+                                    float* us_block, void* stream) {
     WZY_REQUIRE(layers && n_layers >= 1 && iters >= 1 && us_gate_up && us_down && x, "wzy_moe_time_kernels: bad args");
     for (int l = 0; l < n_layers; ++l) WZY_TRY(moe_check(&layers[l], T));
     size_t need = 0;
@@ -1079,8 +1364,9 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
     // Every layer is routed first into a workspace of its own, so that the timed region holds nothing
     // but back-to-back launches of one kernel: `iters` gate/up launches cycling through the layers
     // (each with its own layer's routing), then `iters` down launches (each reading the activations
-    // its layer's last gate/up wrote).  Two events per burst: their own cost is spread over `iters`
-    // launches.
+    // its layer's last gate/up wrote), then (us_block) `iters` blocks of one gate/up launch followed
+    // by its layer's down launch, the order of a decode step.  Two events per burst: their own cost is
+    // spread over `iters` launches.
     (void) ws;
     float* comb = nullptr;
     unsigned char* lws = nullptr;
@@ -1094,7 +1380,7 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
     auto layer_ws = [&](int l) {
         return moe_ws_carve(lws + per * l, per, layers[0].n_embd, layers[0].n_ff, E, layers[0].top_k, T, nullptr);
     };
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
     int rc = WZY_OK;
     for (auto& e : ev)
         if (rc == WZY_OK && hipEventCreate(&e) != hipSuccess) rc = WZY_EHIP;
@@ -1113,15 +1399,24 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
             launch_dn(dn_args(&layers[l], layer_ws(l), comb), T, st);
         }
         (void) hipEventRecord(ev[2], st);
-        if (hipGetLastError() != hipSuccess || hipEventSynchronize(ev[2]) != hipSuccess) {
+        if (us_block) {
+            for (int it = 0; it < iters; ++it) {
+                const int l = it % n_layers;
+                launch_gu(gu_args(&layers[l], layer_ws(l), x, T), T, st);
+                launch_dn(dn_args(&layers[l], layer_ws(l), comb), T, st);
+            }
+        }
+        (void) hipEventRecord(ev[3], st);
+        if (hipGetLastError() != hipSuccess || hipEventSynchronize(ev[3]) != hipSuccess) {
             set_error("wzy_moe_time_kernels: launch failed");
             rc = WZY_EHIP;
         }
     }
-    float a = 0.f, b = 0.f;
+    float a = 0.f, b = 0.f, c = 0.f;
     if (rc == WZY_OK) {
         (void) hipEventElapsedTime(&a, ev[0], ev[1]);
         (void) hipEventElapsedTime(&b, ev[1], ev[2]);
+        (void) hipEventElapsedTime(&c, ev[2], ev[3]);
     }
     for (auto& e : ev)
         if (e) (void) hipEventDestroy(e);
@@ -1130,6 +1425,7 @@ extern "C" int wzy_moe_time_kernels(const wzy_moe_weights* layers, int n_layers,
     if (rc != WZY_OK) return rc;
     *us_gate_up = 1000.0f * a / (float) iters;
     *us_down = 1000.0f * b / (float) iters;
+    if (us_block) *us_block = 1000.0f * c / (float) iters;
     return WZY_OK;
 }
 

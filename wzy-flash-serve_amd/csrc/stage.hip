@@ -1485,7 +1485,7 @@ extern "C" int wzy_stage_moe_weights(wzy_stage* st, int layer, wzy_moe_weights* 
     return WZY_OK;
 }
 
-extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down) {
+extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, float* us_down, float* us_block) {
     WZY_REQUIRE(st && st->loaded && iters >= 1 && us_gate_up && us_down, "time_moe: bad arguments");
     const int T = st->last_T > 0 ? st->last_T : 1;
     std::vector<wzy_moe_weights> ws;
@@ -1493,7 +1493,7 @@ extern "C" int wzy_stage_time_moe(wzy_stage* st, int iters, float* us_gate_up, f
     size_t need = 0;
     moe_ws_carve(nullptr, 0, st->D, st->cfg.n_ff, st->cfg.n_exp, st->cfg.top_k, WZY_MAX_W, &need);
     return wzy_moe_time_kernels(ws.data(), (int) ws.size(), T, st->mixed, st->moe_ws, need + 256, iters, us_gate_up,
-                                us_down, st->stream);
+                                us_down, us_block, st->stream);
 }
 
 // ------------------------------------------------------------------------------------------------

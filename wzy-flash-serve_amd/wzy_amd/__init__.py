@@ -153,7 +153,7 @@ _SIGS = {
     "wzy_stage_tensor_bytes": (SZ, [P, I32, C.c_char_p], False),
     "wzy_stage_read_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
     "wzy_stage_write_tensor": (I32, [P, I32, C.c_char_p, P, SZ], True),
-    "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32)], True),
+    "wzy_stage_time_moe": (I32, [P, I32, C.POINTER(F32), C.POINTER(F32), C.POINTER(F32)], True),
     "wzy_stage_mtp_init": (I32, [P, U64, I32], True),
     "wzy_stage_mtp_init_vocab": (I32, [P, P, I32], True),
     "wzy_stage_mtp_reset": (I32, [P], True),
@@ -191,7 +191,7 @@ _SIGS = {
     "wzy_moe_prefill_time": (I32, [C.POINTER(MoeWeights), P, I32, P, P, SZ, I32, C.POINTER(F32), P], True),
     "wzy_stage_moe_weights": (I32, [P, I32, C.POINTER(MoeWeights)], True),
     "wzy_moe_time_kernels": (I32, [C.POINTER(MoeWeights), I32, I32, P, P, SZ, I32, C.POINTER(F32),
-                                   C.POINTER(F32), P], True),
+                                   C.POINTER(F32), C.POINTER(F32), P], True),
     "wzy_row_argmax": (I32, [P, I32, I32, P, P], True),
     "wzy_row_top16": (I32, [P, I32, I32, P, P, P, P], True),
     "wzy_row_top16_noalloc": (I32, [P, I32, I32, P, P, P, P], True),
