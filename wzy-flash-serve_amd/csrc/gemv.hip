@@ -616,12 +616,14 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
         gb = gp[1];
         ssv = *(const float4*) (gn.ss + ((size_t) t * (cols / 128) + (r * 8) / 128) * GDN_NQ);
     };
+    // NX items per thread in straight-line code: NBL cover one row (nb*4 <= 256*NBL), so windows of
+    // up to 8 / NBL rows are staged with every x load in flight at once; nitem % 4 == 0, so a 4-lane
+    // group is all in or all out
+    constexpr int NX = (T * NBL <= 8) ? T * NBL : NBL;
     {
-        // NBL items per thread cover one row (nb*4 <= 256*NBL); nitem % 4 == 0, so a 4-lane group is
-        // all in or all out
-        float4 xa[NBL], xb[NBL];
+        float4 xa[NX], xb[NX];
 #pragma unroll
-        for (int k = 0; k < NBL; ++k) {
+        for (int k = 0; k < NX; ++k) {
             const int i = min(tid + 256 * k, nitem - 1);
             const int t = i / (nb * 4), r = i - t * (nb * 4);
             const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
@@ -629,22 +631,22 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
             xb[k] = xp[1];
         }
         if constexpr (GDN) {
-            float4 za[NBL], zb[NBL], ga[NBL], gb[NBL], ssv[NBL];
+            float4 za[NX], zb[NX], ga[NX], gb[NX], ssv[NX];
 #pragma unroll
-            for (int k = 0; k < NBL; ++k) {
+            for (int k = 0; k < NX; ++k) {
                 const int i = min(tid + 256 * k, nitem - 1);
                 const int t = i / (nb * 4), r = i - t * (nb * 4);
                 gdn_load(t, r, za[k], zb[k], ga[k], gb[k], ssv[k]);
             }
 #pragma unroll
-            for (int k = 0; k < NBL; ++k) gdn_apply(xa[k], xb[k], za[k], zb[k], ga[k], gb[k], ssv[k]);
+            for (int k = 0; k < NX; ++k) gdn_apply(xa[k], xb[k], za[k], zb[k], ga[k], gb[k], ssv[k]);
         }
 #pragma unroll
-        for (int k = 0; k < NBL; ++k)
+        for (int k = 0; k < NX; ++k)
             if (tid + 256 * k < nitem) stage(xa[k], xb[k], tid + 256 * k);
     }
-    if (T * nb * 4 > 256 * NBL) {
-        for (int i = tid + 256 * NBL; i < nitem; i += 256) {
+    if (nitem > 256 * NX) {
+        for (int i = tid + 256 * NX; i < nitem; i += 256) {
             const int t = i / (nb * 4), r = i - t * (nb * 4);
             const float4* xp = (const float4*) (x + (size_t) t * cols + (size_t) r * 8);
             float4 va = xp[0], vb = xp[1];

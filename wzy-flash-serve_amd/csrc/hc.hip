@@ -174,11 +174,8 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
         for (int o = 0; o < 4; ++o) iw[o] = ld_bf16_raw<VPT>(a.inj_w + (size_t) o * HCD + (size_t) c * D + d0);
     }
 
-#pragma unroll 1
-    for (int t = 0; t < T; ++t) {
-        // 2. residual (or embedding) and fold inputs of this row
-        float v[VPT], bv[VPT];
-        float ip = 0.f;
+    // 2. residual (or embedding) of row t with the pending block folded in
+    auto load_row = [&](int t, float (&v)[VPT]) {
         if (a.emb_table) {
             int tok = a.toks[t];
             tok = tok < 0 ? 0 : (tok >= a.n_vocab ? a.n_vocab - 1 : tok);
@@ -200,21 +197,23 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
             ld_f32<VPT>(a.R_in + ((size_t) t * HC4 + c) * D + d0, v);
         }
         if (fold) {
+            float bv[VPT];
             ld_f32<VPT>(a.bo + (size_t) t * D + d0, bv);
-            ip = a.inj_prev[t * HC4 + c];
+            const float ip = a.inj_prev[t * HC4 + c];
             const float gw = 2.0f / (1.0f + __expf(-ip / (float) HC4));
 #pragma unroll
             for (int j = 0; j < VPT; ++j) v[j] = fmaf(bv[j], gw, v[j]);
         }
-        // 3. stream scale
+    };
+    auto sum_sq = [&](const float (&v)[VPT]) {
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) ss = fmaf(v[j], v[j], ss);
-        ss = wave_sum(ss);
-        if (lane == 0) s_red[w][0] = ss;
-        __syncthreads();
-        const float sc = 1.0f / sqrtf(waves_sum<NW>(s_red, 0) / (float) D + a.eps);
-        __syncthreads();                              // s_red is reused below
+        return wave_sum(ss);
+    };
+    // 3. given the stream scale sc of row t: R_out, nsc and the inject partials (aux workgroups), or
+    //    quant32(xn) into LDS (row workgroups)
+    auto finish_row = [&](int t, const float (&v)[VPT], float sc) {
         float xn[VPT];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) xn[j] = v[j] * sc * nw[j];
@@ -244,9 +243,9 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
                     for (int o = 0; o < 4; ++o) a.inj_part[((size_t) t * HC4 + c) * HC4 + o] = acc[o];
                 __syncthreads();                      // s_red free for the next row
             }
-            continue;
+            return;
         }
-        // 4. quant32(xn) into LDS: G consecutive threads share one 32-block
+        // quant32(xn) into LDS: G consecutive threads share one 32-block
         float am = 0.f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) am = fmaxf(am, fabsf(xn[j]));
@@ -268,6 +267,38 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
         else if constexpr (VPT == 2) *(int16_t*) dst = (int16_t) pk[0];
         else *dst = (int8_t) pk[0];
         if ((tid % G) == 0) s_xs[t * NB + tid / G] = dq;
+    };
+    if constexpr (T <= 4) {
+        // windows of up to four rows: every row's inputs are loaded before any is used, and the four
+        // stream sums meet in one barrier (s_red holds one column per row)
+        float v[T][VPT];
+#pragma unroll
+        for (int t = 0; t < T; ++t) load_row(t, v[t]);
+        float ssv[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) ssv[t] = sum_sq(v[t]);
+        if (lane == 0)
+#pragma unroll
+            for (int t = 0; t < T; ++t) s_red[w][t] = ssv[t];
+        __syncthreads();
+        float sc[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) sc[t] = 1.0f / sqrtf(waves_sum<NW>(s_red, t) / (float) D + a.eps);
+        __syncthreads();                              // s_red is reused below
+#pragma unroll
+        for (int t = 0; t < T; ++t) finish_row(t, v[t], sc[t]);
+    } else {
+#pragma unroll 1
+        for (int t = 0; t < T; ++t) {
+            float v[VPT];
+            load_row(t, v);
+            const float ss = sum_sq(v);
+            if (lane == 0) s_red[w][0] = ss;
+            __syncthreads();
+            const float sc = 1.0f / sqrtf(waves_sum<NW>(s_red, 0) / (float) D + a.eps);
+            __syncthreads();                          // s_red is reused below
+            finish_row(t, v, sc);
+        }
     }
     if (aux) return;                                   // workgroup-uniform
     __syncthreads();
