@@ -716,16 +716,17 @@ __global__ void __launch_bounds__(256) gemv_segs_lds_kernel(GemvSegs segs, const
         }
     }
     const int rpw = q8 ? RPW : RPWB;
+    // all RPW x T sums in transposed reductions (the same sum tree for every T, so a window row's
+    // outputs equal a one-row launch's bit for bit)
+    float v[RPW * T];
 #pragma unroll
-    for (int s = 0; s < RPW; ++s) {
-        const int r = row0 + s;
+    for (int s = 0; s < RPW; ++s)
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float v = wave_sum(acc[s][t]);
-            if (lane == 0 && s < rpw && r < sg.rows)
-                sg.y[(size_t) t * sg.y_stride + r] = sg.act == GEMV_ACT_SIGMOID ? gdn_gate(v) : v;
-        }
-    }
+        for (int t = 0; t < T; ++t) v[s * T + t] = acc[s][t];
+    reduce_wave_store<RPW * T>(v, [&](int i, float tot) {
+        const int s = i / T, t = i - (i / T) * T, r = row0 + s;
+        if (s < rpw && r < sg.rows) sg.y[(size_t) t * sg.y_stride + r] = sg.act == GEMV_ACT_SIGMOID ? gdn_gate(tot) : tot;
+    });
 }
 
 template <int T>

@@ -324,15 +324,16 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
                                  acc[s][t]);
         }
     }
+    // all RPW x T sums in transposed reductions (the same sum tree for every T)
+    float v[RPW * T];
 #pragma unroll
-    for (int s = 0; s < RPW; ++s) {
-        const int r = row0 + s;
+    for (int s = 0; s < RPW; ++s)
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float v = wave_sum(acc[s][t]);
-            if (lane == 0 && r < L) a.lo_part[((size_t) t * HC4 + c) * L + r] = v;
-        }
-    }
+        for (int t = 0; t < T; ++t) v[s * T + t] = acc[s][t];
+    reduce_wave_store<RPW * T>(v, [&](int i, float tot) {
+        const int s = i / T, t = i - (i / T) * T, r = row0 + s;
+        if (r < L) a.lo_part[((size_t) t * HC4 + c) * L + r] = tot;
+    });
 }
 
 // hc_post: wave handles 2 output positions d; 16 lanes per (d, stream) row of `up`, one 32-block

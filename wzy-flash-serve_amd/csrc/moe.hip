@@ -603,12 +603,13 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
 #pragma unroll
         for (int m = 0; m < T; ++m) {
             if (m < cnt) {
+                // lane q < RPW: gate row q and (moved down from lane q + RPW) up row q
+                float v[2 * RPW];
 #pragma unroll
-                for (int q = 0; q < RPW; ++q) {
-                    const float gv = wave_sum(acc[q][m]) * sc_gate;
-                    const float uv = wave_sum(acc[RPW + q][m]) * sc_up;
-                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
-                }
+                for (int rr = 0; rr < 2 * RPW; ++rr) v[rr] = acc[rr][m];
+                const float tot = reduce_wave<2 * RPW>(v);
+                const float up = RPW == 4 ? dpp_f<DPP_ROW_SHL4>(tot) : (RPW == 2 ? dpp_f<DPP_ROW_SHL2>(tot) : dpp_f<DPP_ROW_SHL1>(tot));
+                if (lane < RPW) s_act[m][RPW * w + lane] = siluf_(tot * sc_gate) * (up * sc_up);
             }
         }
         __syncthreads();
@@ -738,12 +739,13 @@ __global__ void __launch_bounds__(512) moe_gate_up_window_kernel(MoeGuArgs a) {
 #pragma unroll
         for (int m = 0; m < T; ++m) {
             if (m < cnt) {
+                // lane q < RPW: gate row q and (moved down from lane q + RPW) up row q
+                float v[2 * RPW];
 #pragma unroll
-                for (int q = 0; q < RPW; ++q) {
-                    const float gv = wave_sum(acc[q][m]) * tail.x;
-                    const float uv = wave_sum(acc[RPW + q][m]) * tail.y;
-                    if (lane == 0) s_act[m][RPW * w + q] = siluf_(gv) * uv;
-                }
+                for (int rr = 0; rr < 2 * RPW; ++rr) v[rr] = acc[rr][m];
+                const float tot = reduce_wave<2 * RPW>(v);
+                const float up = RPW == 4 ? dpp_f<DPP_ROW_SHL4>(tot) : (RPW == 2 ? dpp_f<DPP_ROW_SHL2>(tot) : dpp_f<DPP_ROW_SHL1>(tot));
+                if (lane < RPW) s_act[m][RPW * w + lane] = siluf_(tot * tail.x) * (up * tail.y);
             }
         }
         __syncthreads();

@@ -88,6 +88,67 @@ WZY_DEV float wave_sum(float v) {
     const float b = as_f(__builtin_amdgcn_readlane(as_i(v), 32));
     return a + b;
 }
+// Sums over the wave of N per-lane values (N = 1, 2, 4, 8 or 16), transposed: lane l returns the
+// sum of a[l % N] over all 64 lanes.  Six partner levels run in one fixed order: the row rotation by
+// 8 (partner lane bit 3), the half mirror (partner l ^ 7 inside each 8), the quad permutations xor 2
+// and xor 1, then the permlane16 and permlane32 swaps.  A level whose bit is among the low log2(N)
+// splits the values a lane holds (each lane keeps the half its partner does not); the others add all
+// of them.  Either way a value's sum at every level is own + partner, so (addition being commutative)
+// every value gets the same sum tree, bit for bit, whatever N: results do not depend on how many
+// values share the reduction (e.g. a window's row count).  About 3N/2 + 8 VALU operations and no
+// LDS swizzle or lane reads, against N wave sums.  (The swaps are written as inline assembly: the
+// compiler's builtin hands both results in one register when they feed one add; the s_nops cover
+// the VALU-write-to-permlane hazard.)
+constexpr int DPP_ROW_ROR8 = 0x128;     // lane i <- lane (i + 8) mod 16 within each row
+constexpr int DPP_ROW_SHL1 = 0x101;     // lane i <- lane i + 1 within each row (0 past its end)
+constexpr int DPP_ROW_SHL2 = 0x102;     // lane i <- lane i + 2 within each row
+constexpr int DPP_ROW_SHL4 = 0x104;     // lane i <- lane i + 4 within each row
+template <int CTRL, int M, int SPLIT>
+WZY_DEV void reduce_level(const float (&in)[M], float (&out)[SPLIT ? M / 2 : M], bool upper) {
+    if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < M / 2; ++i) out[i] = (upper ? in[i + M / 2] : in[i]) + dpp_f<CTRL>(upper ? in[i] : in[i + M / 2]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < M; ++i) out[i] = in[i] + dpp_f<CTRL>(in[i]);
+    }
+}
+template <int N>
+WZY_DEV float reduce_wave(const float (&a)[N]) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "reduce_wave: N must be a power of 2 <= 16");
+    const int lane = threadIdx.x & 63;
+    constexpr int M3 = N >= 16 ? N / 2 : N, M2 = N >= 8 ? M3 / 2 : M3, M1 = N >= 4 ? M2 / 2 : M2;
+    float b[M3], c[M2], d[M1], e[1];
+    reduce_level<DPP_ROW_ROR8, N, (N >= 16)>(a, b, (lane & 8) != 0);
+    reduce_level<DPP_HALF_MIRROR, M3, (N >= 8)>(b, c, (lane & 4) != 0);
+    reduce_level<DPP_XOR2, M2, (N >= 4)>(c, d, (lane & 2) != 0);
+    reduce_level<DPP_XOR1, M1, (N >= 2)>(d, e, (lane & 1) != 0);
+    uint32_t x = __builtin_bit_cast(uint32_t, e[0]), y = x;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+    const float f = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+    x = __builtin_bit_cast(uint32_t, f);
+    y = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+    return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
+// NV wave sums through reduce_wave, stored by the lanes that hold them: store(i, sum of v[i]) runs
+// on one lane per i.  NV is padded with zeros to a power of 2, or cut into groups of 16; each value's
+// sum tree is reduce_wave's, whatever NV.
+template <int NV, typename F>
+WZY_DEV void reduce_wave_store(const float (&v)[NV], F&& store) {
+    constexpr int P = NV <= 1 ? 1 : NV <= 2 ? 2 : NV <= 4 ? 4 : NV <= 8 ? 8 : 16;
+    constexpr int NG = (NV + 15) / 16;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int g = 0; g < (NV > 16 ? NG : 1); ++g) {
+        float w[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) w[i] = (16 * g + i < NV) ? v[16 * g + i] : 0.f;
+        const float tot = reduce_wave<P>(w);
+        const int idx = 16 * g + lane;
+        if (lane < P && idx < NV) store(idx, tot);
+    }
+}
 WZY_DEV float max16(float v) {
     v = fmaxf(v, dpp_f<DPP_XOR1>(v));
     v = fmaxf(v, dpp_f<DPP_XOR2>(v));
