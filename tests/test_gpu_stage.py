@@ -243,6 +243,44 @@ def test_stage_baseline_48_layers_greedy(wz, gpu):
                for kind, where, _, _ in par.excused), par.summary()
 
 
+@pytest.mark.parametrize("T", [2, 4, 8])
+def test_stage_window_rows_equal_single_steps(wz, gpu, T):
+    """A window of T rows gives each row the logits and leaves the state that T single-token forwards
+    give, bit for bit (BASELINE shapes, layers GDN, GDN, GDN, QSA, graph replay).  Speculative
+    decoding relies on it: a verify window's accepted rows must be what plain decoding computes, so
+    the MTP stream equals the greedy one token for token.  Every kernel's per-row arithmetic, and each
+    reduction's sum tree, is the same for every window size."""
+    print("case window_equals_steps T=%d" % T, flush=True)
+    cfg = baseline_cfg(4, ctx_max=4096)
+    toks = [int(t) for t in np.random.default_rng(40 + T).integers(0, cfg.n_vocab, T)]
+    res = []
+    for window in (False, True):
+        st = wzy_amd.Stage(cfg)
+        try:
+            st.load_synthetic(7, 3000)
+            if window:
+                st.forward(3000, toks)
+                st.sync()
+                logits = st.logits(T)
+            else:
+                rows = []
+                for i, t in enumerate(toks):
+                    st.forward(3000 + i, [t])
+                    st.sync()
+                    rows.append(st.logits(1)[0])
+                logits = np.stack(rows)
+            state = {(l, n): st.read(l, n, np.uint8) for l in range(cfg.n_layers)
+                     for n in (("conv_hist", "ssm") if not is_qsa(cfg, l) else ("kv_k", "kv_v", "idx_tail"))}
+            res.append((logits, state))
+        finally:
+            st.close()
+    (l1, s1), (lw, sw) = res
+    for t in range(T):
+        assert np.array_equal(l1[t].view(np.uint32), lw[t].view(np.uint32)), "row %d logits differ" % t
+    for k in s1:
+        assert np.array_equal(s1[k], sw[k]), "state %s differs" % (k,)
+
+
 def real_cfg(n_layers, ctx_max):
     """The reference model's real shapes (src/wzy_kernels_v2.cuh:8-19): NE 2560, NFF 640, 48 GDN value
     heads over 16 key heads, vocab 248,320; everything else as the BASELINE model."""

@@ -780,7 +780,10 @@ int launch_gemv_segs(GemvSegs segs, const float* x, int cols, int T, hipStream_t
     for (int i = 0; i < segs.n; ++i) flags |= segs.seg[i].kind == GEMV_Q8 ? 1 : 2;
     const size_t lds = (size_t) T * cols * (((flags & 2) ? 4 : 0) + ((flags & 1) ? 1 : 0)) +
                        ((flags & 1) ? (size_t) T * (cols / 32) * 4 : 0);
-    const bool use_lds = lds <= 48 * 1024;
+    // gfx950 gives a workgroup up to 160 KB of LDS: every window size of the decode projections (up to
+    // 8 rows of 2,048 columns of both kinds, 8,192 of Q8_0) stays on this kernel, so a window row
+    // computes what a one-row launch does
+    const bool use_lds = lds <= 96 * 1024;
     WZY_REQUIRE(!segs.gdn.ss || (use_lds && cols % 128 == 0), "gemv_segs: the GDN staging transform needs the LDS path");
     // rows per wave: the LDS kernel holds RPW Q8_0 rows or RPW/2 bf16 rows per wave (RPW = 4 for one
     // 32-block per lane, else 2; 2 also when 4 would leave CUs without a workgroup); the other kernel

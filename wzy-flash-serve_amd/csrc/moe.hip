@@ -852,12 +852,9 @@ __global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
         __syncthreads();
     }
     // the workgroup's outputs go to global memory from wave 0 alone, so that one release fence (an
-    // agent-scope fence writes back L2) covers every store before the arrival
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const float v = wave_sum(acc[t]);
-        if (lane == 0) s_out[w][t] = v;
-    }
+    // agent-scope fence writes back L2) covers every store before the arrival.  The lane partials and
+    // the sum tree are gemv_segs' for a bf16 row, so the logits equal those of one-row windows.
+    reduce_wave_store<T>(acc, [&](int t, float v) { s_out[w][t] = v; });
     __syncthreads();
     if (w == 0) {
         if (lane < RT_ROWS * T) {
