@@ -31,13 +31,27 @@ WZY_DEV void sort_keys_desc(uint64_t (&k)[RV]) {
             }
 }
 
+// Number of keys in the lane's 16-lane row that are larger than its own: the row's 15 other lanes
+// reach it by row rotations (one DPP move per half and one compare each, no scalar round trip).
+template <int R>
+WZY_DEV int row_count_above(uint64_t k) {
+    if constexpr (R == 0) {
+        return 0;
+    } else {
+        const uint32_t lo = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) k, 0x120 + R, 0xF, 0xF, true);
+        const uint32_t hi = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) (k >> 32), 0x120 + R, 0xF, 0xF, true);
+        return ((((uint64_t) hi << 32) | lo) > k ? 1 : 0) + row_count_above<R - 1>(k);
+    }
+}
+
 // Softmax top-K of one row in one wave (ranking: probability desc, expert id asc).  Every lane
 // sorts the keys of its RV probabilities once.  Candidates: thr = the K-th largest probability word
 // among the 64 lane heads with its low 18 bits cleared (bisection on ballot counts over bits 29..18;
 // probabilities are <= 1, so bits 31 and 30 are clear); the K largest heads are K distinct keys
 // >= thr, so every key with a probability word >= thr is a superset of the top K.  When at most 64
 // keys qualify, they are gathered into `cand` (this wave's LDS scratch) and each ranks itself
-// against the others (broadcast by readlane); otherwise K rounds each take the DPP wave maximum
+// against the others (by row rotations when at most 16 qualify, else broadcast by readlane);
+// otherwise K rounds each take the DPP wave maximum
 // over the lane heads and the winner lane pops its head.  Lane k ends with the k-th routed (id, probability); wsum is their sum
 // in rank order.
 template <int RV>
@@ -90,10 +104,15 @@ WZY_DEV void route_row(float (&p)[RV], int E, int K, int& my_id, float& my_w, fl
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         const uint64_t mine = lane < n_cand ? cand[lane] : 0ull;
         int rank = 0;
-        for (int j = 0; j < n_cand; ++j) {
-            const uint32_t jl = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) mine, j);
-            const uint32_t jh = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (mine >> 32), j);
-            rank += ((((uint64_t) jh << 32) | jl) > mine) ? 1 : 0;
+        if (n_cand <= 16) {                                         // wave-uniform; the usual case
+            // every candidate sits in row 0, whose other lanes hold key 0 (below every real key)
+            rank = row_count_above<15>(mine);
+        } else {
+            for (int j = 0; j < n_cand; ++j) {
+                const uint32_t jl = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) mine, j);
+                const uint32_t jh = (uint32_t) __builtin_amdgcn_readlane((int) (uint32_t) (mine >> 32), j);
+                rank += ((((uint64_t) jh << 32) | jl) > mine) ? 1 : 0;
+            }
         }
         rank = lane < n_cand ? rank : 64;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
