@@ -157,6 +157,36 @@ def test_gdn_step(wz, orc, gpu, hk, hv, T):
         close("hist_snap[%d]" % t, hn[t], ohn[t], 0, 0)
 
 
+@pytest.mark.parametrize("hk,hv", [(16, 16), (16, 48)])
+def test_gdn_step_launch_forms_agree(wz, gpu, hk, hv):
+    """Windows of up to three rows run a head in one workgroup with the output norm in the kernel;
+    longer ones use four column-quarter workgroups and the norm kernel.  Both forms compute every
+    row alike: four single steps equal one four-row window bit for bit (outputs, state, history)."""
+    print("case gdn_step forms hk=%d hv=%d" % (hk, hv), flush=True)
+    T = 4
+    a = gdn_inputs(hk, hv, T, 7 * hk + hv)
+    QKV, GV = a["qkv"].shape[1], a["z"].shape[1]
+    win = {k: dev(v) for k, v in a.items()}
+    y4 = DA((T, GV), np.float32)
+    wz.wzy_gdn_step(win["qkv"].ptr, win["z"].ptr, win["ab"].ptr, win["dt"].ptr, win["ssm_a"].ptr,
+                    win["conv_w"].ptr, win["hist"].ptr, win["state"].ptr, win["gamma"].ptr, C.c_float(1e-6),
+                    y4.ptr, hk, hv, T, None, None, None)
+    one = {k: dev(v) for k, v in a.items() if k in ("dt", "ssm_a", "conv_w", "hist", "state", "gamma")}
+    y1 = np.empty((T, GV), np.float32)
+    for t in range(T):
+        qkv, z, ab = dev(a["qkv"][t:t + 1]), dev(a["z"][t:t + 1]), dev(a["ab"][t:t + 1])
+        yt = DA((1, GV), np.float32)
+        wz.wzy_gdn_step(qkv.ptr, z.ptr, ab.ptr, one["dt"].ptr, one["ssm_a"].ptr, one["conv_w"].ptr,
+                        one["hist"].ptr, one["state"].ptr, one["gamma"].ptr, C.c_float(1e-6), yt.ptr, hk, hv, 1,
+                        None, None, None)
+        wz.wzy_device_sync()
+        y1[t] = yt.numpy()[0]
+    wz.wzy_device_sync()
+    np.testing.assert_array_equal(y1, y4.numpy())
+    np.testing.assert_array_equal(one["state"].numpy(), win["state"].numpy())
+    np.testing.assert_array_equal(one["hist"].numpy(), win["hist"].numpy())
+
+
 @pytest.mark.parametrize("hk,hv,T", [(2, 4, 2), (16, 16, 1)])
 def test_gdn_recurrence(wz, orc, gpu, hk, hv, T):
     print("case gdn_recurrence hk=%d hv=%d T=%d" % (hk, hv, T), flush=True)

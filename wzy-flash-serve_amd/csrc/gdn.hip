@@ -17,7 +17,10 @@
 // The output RMS norm spans the head's 128 columns, i.e. four workgroups: the kernel writes
 // o * 1/sqrt(128) and, per (row, head, column quarter), the partial sum of its squares; the norm
 // and gate y = o * rsqrt(sum/128 + eps) * gamma * sigmoid(z) are applied by the consumer (the
-// out-projection GEMV's staging in the stage, gdn_norm_kernel for the standalone entry points).
+// out-projection GEMV's staging in the stage).  The standalone entry points, whose output is final,
+// run each head of a window of up to three rows in one 1024-thread workgroup instead (the same thread
+// mapping, four column quarters side by side) and apply the norm in the kernel from the same quarter
+// partials, so a step is one launch; longer windows use the quarters and gdn_norm_kernel.
 //
 // Per step t:  S *= decay;  kv_j = sum_i S_ij k_i;  delta_j = (v_j - kv_j) * beta;
 //              S_ij += k_i delta_j;  o_j = sum_i S_ij q_i;  o *= 1/sqrt(128);
@@ -31,22 +34,31 @@
 using namespace wzy;
 
 constexpr int GS = 128;              // state / head dim
-constexpr int QC = GS / GDN_NQ;      // state columns per workgroup
+// Windows of up to this many rows with final outputs run a head in one workgroup (one launch, the
+// norm in the kernel); longer ones spread a head over GDN_NQ workgroups and finish with
+// gdn_norm_kernel (per row a CU's share of the recurrence then costs more than the second launch).
+constexpr int GDN_ONE_WG_MAX_T = 3;
 constexpr int GDN_MAX_HK = 1024;
 constexpr int GDN_MAX_HV = 1024;
 
 // Completion counters of the shared q/k conv history, one per key head; every launch leaves them
 // at zero.  Launches on one device must not overlap.
 __device__ int g_gdn_qk_sync[GDN_MAX_HK];
-// Partial sums of squares of the standalone entry points ([T][HV][GDN_NQ]).
+// Partial sums of squares of the standalone entry points' longer windows ([T][HV][GDN_NQ]).
 __device__ float g_gdn_ss[WZY_MAX_W * GDN_MAX_HV * GDN_NQ];
 
-template <bool FUSED>
-__global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__ o_ss) {
+// NQ = workgroups per value head (GDN_NQ column quarters in the stage, whose out-projection applies
+// the output norm; 1 in the standalone entry points, where one 1024-thread workgroup holds the whole
+// head and applies the norm itself, from the same four quarter partials, so no second launch is
+// needed).  Thread (column c, row group rg) = (tid % QC, tid / QC).
+template <bool FUSED, int NQ>
+__global__ void __launch_bounds__(8 * (GS / NQ)) gdn_kernel(GdnArgs a, float* __restrict__ o_ss) {
+    constexpr int QC = GS / NQ;                     // state columns per workgroup
     __shared__ float s_q[WZY_MAX_W][GS], s_k[WZY_MAX_W][GS], s_v[WZY_MAX_W][QC];
     __shared__ float s_dec[WZY_MAX_W], s_beta[WZY_MAX_W];
     __shared__ float s_w[WZY_MAX_W][4];
     __shared__ float s_kv[8][QC], s_o[8][QC];
+    __shared__ float s_ss[WZY_MAX_W][4];
     __shared__ int s_last;
     const int HK = a.hk, HV = a.hv, T = a.T;
     // XCD-local numbering when HV % 8 == 0: workgroup b runs on XCD b % 8, which takes heads
@@ -54,13 +66,14 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
     // weights are fetched from HBM once per XCD; otherwise consecutive workgroups of a head
     const int b = blockIdx.x;
     const bool xl = (HV & 7) == 0;
-    const int h = xl ? (b & 7) + 8 * ((b >> 3) / GDN_NQ) : b / GDN_NQ;
-    const int cq = xl ? (b >> 3) % GDN_NQ : b % GDN_NQ;
+    const int h = xl ? (b & 7) + 8 * ((b >> 3) / NQ) : b / NQ;
+    const int cq = xl ? (b >> 3) % NQ : b % NQ;
     const int kh = h % HK;
     const int QKV = 2 * HK * GS + HV * GS;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int c = lane & (QC - 1), rg = 2 * wv + (lane >> 5);
+    const int c = tid & (QC - 1), rg = tid / QC;
     const int j = cq * QC + c;                      // state column of this thread
+    const bool qk_thr = tid < 2 * GS;               // q/k channel threads (all of a 256-thread workgroup)
 
     // ---- 0. every load, issued before any is used ----
     float s[16];
@@ -68,7 +81,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = sbase[(size_t) r * GS];
     // q/k channel tid (q for tid < 128); v channel 32*cq + (tid % 32) of head h; gates on threads 128 + t
-    const int qk_ch = (tid < GS ? 0 : HK * GS - GS) + kh * GS + tid;
+    const int qk_ch = (tid < GS ? 0 : HK * GS - GS) + kh * GS + min(tid, 2 * GS - 1);
     const int v_ch = 2 * HK * GS + h * GS + cq * QC + (tid & (QC - 1));
     float qh[3], qw[4], vh[3], vw[4], qx[WZY_MAX_W], vx[WZY_MAX_W];
     float g_a, g_b, g_dt = 0.f, g_sa = 0.f;
@@ -92,7 +105,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
 #pragma unroll
         for (int t = 0; t < WZY_MAX_W; ++t) {
             const int tc = t < T ? t : 0;
-            qx[t] = tid < GS ? a.q[(size_t) tc * HK * GS + kh * GS + tid] : a.k[(size_t) tc * HK * GS + kh * GS + tid - GS];
+            qx[t] = tid < GS ? a.q[(size_t) tc * HK * GS + kh * GS + tid] : a.k[(size_t) tc * HK * GS + kh * GS + min(tid, 2 * GS - 1) - GS];
             vx[t] = a.v[(size_t) tc * HV * GS + h * GS + cq * QC + (tid & (QC - 1))];
         }
         g_a = a.decay[tg * HV + h];
@@ -109,7 +122,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
             if (t >= T) break;
             const float sum = h0 * qw[0] + h1 * qw[1] + h2 * qw[2] + qx[t] * qw[3];
             h0 = h1; h1 = h2; h2 = qx[t];
-            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = sum / (1.0f + __expf(-sum));
+            if (qk_thr) (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = sum / (1.0f + __expf(-sum));
             if (tid < QC) {
                 const float sv = u0 * vw[0] + u1 * vw[1] + u2 * vw[2] + vx[t] * vw[3];
                 u0 = u1; u1 = u2; u2 = vx[t];
@@ -119,7 +132,7 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
                     hs[0] = u0; hs[1] = u1; hs[2] = u2;
                 }
             }
-            if (a.hist_snaps && h == kh && cq == 0) {   // q/k snapshots: one writer per key head
+            if (a.hist_snaps && h == kh && cq == 0 && qk_thr) {   // q/k snapshots: one writer per key head
                 float* hs = a.hist_snaps + (size_t) t * QKV * 3 + (size_t) qk_ch * 3;
                 hs[0] = h0; hs[1] = h1; hs[2] = h2;
             }
@@ -142,22 +155,24 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
         if (tid == 0)
             qk_order = __hip_atomic_fetch_add(&g_gdn_qk_sync[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // per-head L2 norm of q and k: waves 0-1 reduce q, waves 2-3 reduce k
-        for (int t = 0; t < T; ++t) {
-            const float y = (tid < GS ? s_q : s_k)[t][tid & (GS - 1)];
-            const float sq = wave_sum(y * y);
-            if (lane == 0) s_w[t][wv] = sq;
-        }
+        if (qk_thr)                                     // wave-uniform
+            for (int t = 0; t < T; ++t) {
+                const float y = (tid < GS ? s_q : s_k)[t][tid & (GS - 1)];
+                const float sq = wave_sum(y * y);
+                if (lane == 0) s_w[t][wv] = sq;
+            }
         __syncthreads();
-        for (int t = 0; t < T; ++t) {
-            const float ss = (tid < GS) ? (s_w[t][0] + s_w[t][1]) : (s_w[t][2] + s_w[t][3]);
-            const float r = 1.0f / sqrtf(ss + a.eps);
-            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] *= r;
-        }
+        if (qk_thr)
+            for (int t = 0; t < T; ++t) {
+                const float ss = (tid < GS) ? (s_w[t][0] + s_w[t][1]) : (s_w[t][2] + s_w[t][3]);
+                const float r = 1.0f / sqrtf(ss + a.eps);
+                (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] *= r;
+            }
     } else {
 #pragma unroll
         for (int t = 0; t < WZY_MAX_W; ++t) {
             if (t >= T) break;
-            (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = qx[t];
+            if (qk_thr) (tid < GS ? s_q : s_k)[t][tid & (GS - 1)] = qx[t];
             if (tid < QC) s_v[t][tid] = vx[t];
         }
         if (tid >= GS && tid < GS + T) { s_dec[tid - GS] = g_a; s_beta[tid - GS] = g_b; }
@@ -199,12 +214,25 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
         }
         s_o[rg][c] = o;
         __syncthreads();
-        if (tid < QC) {                                 // wave 0, lanes 0-31: the 32 columns
-            const float oc = (((s_o[0][c] + s_o[1][c]) + (s_o[2][c] + s_o[3][c])) +
-                              ((s_o[4][c] + s_o[5][c]) + (s_o[6][c] + s_o[7][c]))) * 0.08838834764831845f;
-            a.y[(size_t) t * HV * GS + h * GS + j] = oc;
+        float oc = 0.f;
+        const size_t yi = (size_t) t * HV * GS + h * GS + j;
+        if (tid < QC) {                                 // the workgroup's columns (32 lanes per quarter)
+            oc = (((s_o[0][c] + s_o[1][c]) + (s_o[2][c] + s_o[3][c])) +
+                  ((s_o[4][c] + s_o[5][c]) + (s_o[6][c] + s_o[7][c]))) * 0.08838834764831845f;
             const float sq = sum32(oc * oc);
-            if (tid == 0) o_ss[((size_t) t * HV + h) * GDN_NQ + cq] = sq;
+            if constexpr (NQ == GDN_NQ) {
+                a.y[yi] = oc;
+                if (tid == 0) o_ss[((size_t) t * HV + h) * GDN_NQ + cq] = sq;
+            } else {
+                if ((tid & 31) == 0) s_ss[t][tid >> 5] = sq;   // the four quarter partials
+            }
+        }
+        if constexpr (NQ != GDN_NQ) {
+            // the whole head is here: the output norm and gate (gdn_norm_gate) on the same partials
+            __syncthreads();
+            if (tid < QC)
+                a.y[yi] = gdn_norm_gate(oc, s_ss[t], a.z ? a.z[yi] : 0.0f, a.z != nullptr,
+                                        a.gamma ? a.gamma[j] : 1.0f, a.eps);
         }
     }
 #pragma unroll
@@ -212,9 +240,9 @@ __global__ void __launch_bounds__(256) gdn_kernel(GdnArgs a, float* __restrict__
 
     // ---- 3. the last workgroup of the key head writes the shared q/k history ----
     if (FUSED) {
-        if (tid == 0) s_last = qk_order == (HV / HK) * GDN_NQ - 1;
+        if (tid == 0) s_last = qk_order == (HV / HK) * NQ - 1;
         __syncthreads();
-        if (s_last) {
+        if (s_last && qk_thr) {
             a.conv_hist[qk_ch * 3 + 0] = qh[0]; a.conv_hist[qk_ch * 3 + 1] = qh[1]; a.conv_hist[qk_ch * 3 + 2] = qh[2];
             if (tid == 0) __hip_atomic_store(&g_gdn_qk_sync[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -238,18 +266,24 @@ int launch_gdn(const GdnArgs& a, bool fused, hipStream_t st) {
     WZY_REQUIRE(a.hk >= 1 && a.hk <= GDN_MAX_HK && a.hv >= a.hk && a.hv % a.hk == 0 && a.hv <= GDN_MAX_HV,
                 "gdn: bad head counts");
     WZY_REQUIRE(a.state && a.y, "gdn: null state/output");
-    float* ss = a.o_ss;
-    if (!ss) WZY_HIP_TRY(hipGetSymbolAddress((void**) &ss, HIP_SYMBOL(g_gdn_ss)));
-    const dim3 grid(a.hv * GDN_NQ);
-    if (fused) {
-        WZY_REQUIRE(a.qkv && a.ab && a.dt && a.ssm_a && a.conv_w && a.conv_hist, "gdn: fused mode inputs missing");
-        hipLaunchKernelGGL(gdn_kernel<true>, grid, dim3(256), 0, st, a, ss);
+    if (fused) WZY_REQUIRE(a.qkv && a.ab && a.dt && a.ssm_a && a.conv_w && a.conv_hist, "gdn: fused mode inputs missing");
+    else WZY_REQUIRE(a.q && a.k && a.v && a.decay && a.beta, "gdn: recurrence inputs missing");
+    if (!a.o_ss && a.T <= GDN_ONE_WG_MAX_T) {
+        // final outputs of a short window: one workgroup per head applies the norm itself
+        const dim3 grid(a.hv);
+        if (fused) hipLaunchKernelGGL((gdn_kernel<true, 1>), grid, dim3(8 * GS), 0, st, a, nullptr);
+        else hipLaunchKernelGGL((gdn_kernel<false, 1>), grid, dim3(8 * GS), 0, st, a, nullptr);
     } else {
-        WZY_REQUIRE(a.q && a.k && a.v && a.decay && a.beta, "gdn: recurrence inputs missing");
-        hipLaunchKernelGGL(gdn_kernel<false>, grid, dim3(256), 0, st, a, ss);
+        // a head over GDN_NQ workgroups; the output norm from their quarter partials is applied by the
+        // caller, or here by gdn_norm_kernel when the outputs are final
+        float* ss = a.o_ss;
+        if (!ss) WZY_HIP_TRY(hipGetSymbolAddress((void**) &ss, HIP_SYMBOL(g_gdn_ss)));
+        const dim3 grid(a.hv * GDN_NQ);
+        if (fused) hipLaunchKernelGGL((gdn_kernel<true, GDN_NQ>), grid, dim3(8 * GS / GDN_NQ), 0, st, a, ss);
+        else hipLaunchKernelGGL((gdn_kernel<false, GDN_NQ>), grid, dim3(8 * GS / GDN_NQ), 0, st, a, ss);
+        if (!a.o_ss)
+            hipLaunchKernelGGL(gdn_norm_kernel, dim3(a.hv, a.T), dim3(GS), 0, st, a.y, ss, a.z, a.gamma, a.eps, a.hv);
     }
-    if (!a.o_ss)
-        hipLaunchKernelGGL(gdn_norm_kernel, dim3(a.hv, a.T), dim3(GS), 0, st, a.y, ss, a.z, a.gamma, a.eps, a.hv);
     WZY_LAUNCH_CHECK();
     return WZY_OK;
 }
