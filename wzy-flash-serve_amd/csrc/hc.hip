@@ -110,6 +110,16 @@ WZY_DEV float waves_sum(const float (*sh)[4], int o) {
     return s;
 }
 
+// waves_sum over column o of a wider table (the same pairing)
+template <int NW, int W>
+WZY_DEV float waves_sum_w(const float (*sh)[W], int o) {
+    if constexpr (NW == 4) return (sh[0][o] + sh[1][o]) + (sh[2][o] + sh[3][o]);
+    float s = sh[0][o];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) s += sh[i][o];
+    return s;
+}
+
 // sum of 4 values per thread over the NW-wave workgroup; results valid on thread 0
 template <int NW>
 WZY_DEV void block_sum4_t0(float (&v)[4], float (*sh)[4]) {
@@ -135,6 +145,7 @@ template <int T, int VPT, int NBL, int RPW, int NW>
 __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
     extern __shared__ __align__(16) unsigned char s_dyn[];
     __shared__ float s_red[NW][4];
+    __shared__ float s_inj[NW][4 * (T <= 4 ? T : 1)];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = a.D, HCD = HC4 * D, NB = D / 32, L = a.HCLR;
     constexpr int G = 32 / VPT;                        // threads per 32-block
@@ -285,6 +296,50 @@ __global__ void __launch_bounds__(64 * NW) hc_pre_kernel(HcPreArgs a) {
 #pragma unroll
         for (int t = 0; t < T; ++t) sc[t] = 1.0f / sqrtf(waves_sum<NW>(s_red, t) / (float) D + a.eps);
         __syncthreads();                              // s_red is reused below
+        if (do_inj) {
+            // R_out, nsc and every row's inject partials, reduced together behind one barrier (the
+            // per-value sums of block_sum4_t0: wave_sum, then the waves in waves_sum's pairing)
+            float acc[T][4];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                float xn[VPT];
+#pragma unroll
+                for (int j = 0; j < VPT; ++j) xn[j] = v[t][j] * sc[t] * nw[j];
+                float* ro = a.R_out + ((size_t) t * HC4 + c) * D + d0;
+                if constexpr (VPT >= 4) {
+#pragma unroll
+                    for (int k = 0; k < VPT / 4; ++k)
+                        ((float4*) ro)[k] = make_float4(v[t][4 * k], v[t][4 * k + 1], v[t][4 * k + 2], v[t][4 * k + 3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < VPT; ++j) ro[j] = v[t][j];
+                }
+                if (tid == 0) a.nsc[t * HC4 + c] = sc[t];
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+                    acc[t][o] = 0.f;
+#pragma unroll
+                    for (int j = 0; j < VPT; ++j) acc[t][o] = fmaf(bf16_at<VPT>(iw[o], j), xn[j], acc[t][o]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int o = 0; o < 4; ++o) acc[t][o] = wave_sum(acc[t][o]);
+            if (lane == 0)
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int o = 0; o < 4; ++o) s_inj[w][4 * t + o] = acc[t][o];
+            __syncthreads();
+            if (tid == 0)
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int o = 0; o < 4; ++o)
+                        a.inj_part[((size_t) t * HC4 + c) * HC4 + o] = waves_sum_w<NW, 4 * (T <= 4 ? T : 1)>(s_inj, 4 * t + o);
+            return;                                   // the inject workgroup is done
+        }
 #pragma unroll
         for (int t = 0; t < T; ++t) finish_row(t, v[t], sc[t]);
     } else {

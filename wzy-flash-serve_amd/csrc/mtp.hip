@@ -72,33 +72,43 @@ struct MtpInArgs {
 };
 
 // grid (1 + HC, T): workgroup 0 the embedding row, 1 + c residual stream c
+// NV = values per thread (D / 256 rounded up to the instantiation): every load of the thread is
+// issued before the first is used (a loop over a runtime width would wait for each load in turn).
+template <int NV>
 __global__ void __launch_bounds__(256) mtp_in_kernel(MtpInArgs a) {
     __shared__ float s_red[4];
     const int r = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, D = a.D;
+    float v[NV], g[NV];
     if (r == 0) {
         int tok = a.toks[t];
         if (tok < 0 || tok >= a.n_vocab) tok = 0;     // stage_one_emb, src/wzy_engine_v2.cu:862-863
         // embedding value d of the row: bf16, or d * q of the Q8_0 row (stage_one_emb)
-        auto ev = [&](int d) -> float {
-            if (a.emb) return bf16_to_f(a.emb[(size_t) tok * D + d]);
-            return h16_to_f(a.emb_s[(size_t) tok * (D / 32) + d / 32]) * (float) a.emb_q[(size_t) tok * D + d];
-        };
-        float ss = 0.f;
-        for (int d = tid; d < D; d += 256) {
-            const float v = ev(d);
-            ss = fmaf(v, v, ss);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int d = min(tid + 256 * k, D - 1);
+            v[k] = a.emb ? bf16_to_f(a.emb[(size_t) tok * D + d])
+                         : h16_to_f(a.emb_s[(size_t) tok * (D / 32) + d / 32]) * (float) a.emb_q[(size_t) tok * D + d];
+            g[k] = a.g_emb[d];
         }
-        const float sc = 1.0f / sqrtf(block_sum<4>(ss, s_red) / (float) D + a.eps);
-        for (int d = tid; d < D; d += 256) a.en[(size_t) t * D + d] = ev(d) * sc * a.g_emb[d];
-        return;
+    } else {
+        const int c = r - 1;
+        const float* src = a.rin + ((size_t) t * a.HC + c) * D;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int d = min(tid + 256 * k, D - 1);
+            v[k] = src[d];
+            g[k] = a.g_hid[(size_t) c * D + d];
+        }
     }
-    const int c = r - 1;
-    const float* src = a.rin + ((size_t) t * a.HC + c) * D;
     float ss = 0.f;
-    for (int d = tid; d < D; d += 256) ss = fmaf(src[d], src[d], ss);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        if (tid + 256 * k < D) ss = fmaf(v[k], v[k], ss);
     const float sc = 1.0f / sqrtf(block_sum<4>(ss, s_red) / (float) D + a.eps);
-    float* dst = a.hn + ((size_t) t * a.HC + c) * D;
-    for (int d = tid; d < D; d += 256) dst[d] = src[d] * sc * a.g_hid[(size_t) c * D + d];
+    float* dst = r == 0 ? a.en + (size_t) t * D : a.hn + ((size_t) t * a.HC + (r - 1)) * D;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        if (tid + 256 * k < D) dst[tid + 256 * k] = v[k] * sc * g[k];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -805,7 +815,9 @@ int MtpState::enqueue_front(int T, bool with_q) {
     const int D = c.D, HCD = c.HC * D, QD = c.qh * c.hd, KVD = c.kvh * c.hd;
     MtpInArgs ia{main.emb, main.emb_q, main.emb_s, c.n_vocab, d_ctl + 1, rin, pre_norm_emb, pre_norm_hid, en, hn, D,
                  c.HC, c.eps};
-    hipLaunchKernelGGL(mtp_in_kernel, dim3(1 + c.HC, T), dim3(256), 0, st, ia);
+    if (D <= 2048) hipLaunchKernelGGL(mtp_in_kernel<8>, dim3(1 + c.HC, T), dim3(256), 0, st, ia);
+    else if (D <= 4096) hipLaunchKernelGGL(mtp_in_kernel<16>, dim3(1 + c.HC, T), dim3(256), 0, st, ia);
+    else hipLaunchKernelGGL(mtp_in_kernel<32>, dim3(1 + c.HC, T), dim3(256), 0, st, ia);
     WZY_LAUNCH_CHECK();
     {
         GemvSegs s;
