@@ -1036,7 +1036,30 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
 // ---------------------------------------------------------------------------------------------
 namespace wzy {
 
-int launch_pf_gemm(const PfGemm& g, hipStream_t st) {
+// Q8_0 rows -> bf16 (one thread per 8 values): out = bf16(q * fp16 scale), the rounding the GEMM's
+// own staging applies (q8_quarter_bf16), so a GEMM on the expanded rows computes the same values.
+__global__ void __launch_bounds__(256) pf_q8_to_bf16_kernel(const int8_t* __restrict__ q, const uint16_t* __restrict__ s,
+                                                            uint16_t* __restrict__ out, size_t n8) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n8) return;
+    const uint2 c = *(const uint2*) (q + 8 * i);
+    const float sc = h16_to_f(s[i / 4]);
+    const uint4 o0 = q8_quarter_bf16(c.x, c.y, sc);
+    *(uint4*) (out + 8 * i) = o0;
+}
+
+int launch_pf_gemm(const PfGemm& g0, hipStream_t st) {
+    PfGemm g = g0;
+    if (g.wq && g.wscratch && g.M >= PF_DEQ_MIN_M && (size_t) g.N * g.K <= g.wscratch_elems && g.K % 32 == 0) {
+        // many row tiles read each weight tile: expand the Q8_0 weights to bf16 once
+        const size_t n8 = (size_t) g.N * g.K / 8;
+        hipLaunchKernelGGL(pf_q8_to_bf16_kernel, dim3((unsigned) ((n8 + 255) / 256)), dim3(256), 0, st, g.wq, g.ws,
+                           g.wscratch, n8);
+        WZY_LAUNCH_CHECK();
+        g.wb = g.wscratch;
+        g.wq = nullptr;
+        g.ws = nullptr;
+    }
     const bool um = g.um_mixed != nullptr;
     const int ksplit = max(g.ksplit, 1);
     WZY_REQUIRE(g.a && (g.wq ? g.ws != nullptr : g.wb != nullptr) && (um ? g.um_xn && g.um_xh : (g.y || g.yb)),

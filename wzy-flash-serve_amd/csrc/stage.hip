@@ -239,6 +239,8 @@ struct wzy_stage {
         int* toks = nullptr;
         float *ple_emb = nullptr, *ple_k = nullptr, *ple_v = nullptr, *ple_gat = nullptr, *ple_n = nullptr;
         uint16_t* ple_embh = nullptr;   // the PLE rows as the bf16 GEMM operand
+        uint16_t* wbf = nullptr;    // bf16 expansion of the Q8_0 weights of the running GEMM
+        size_t wbf_elems = 0;
         int* pos8 = nullptr;        // [cap / 8 + 2]: p0 + 8 i
         int sc_rows = 0;            // rows per block-score pass
         float* tr = nullptr;        // per-layer trace [n_layers][4][tr_rows][D] (while tracing)
@@ -1580,6 +1582,10 @@ int wzy_stage::prefill_reserve(int B) {
                  osc = bump((size_t) sc_rows * maxb * 4), osel = bump(b * c.idx_topk * 4), ocnt = bump(b * 4);
     off = std::max(off, gdn_end);
     const size_t omoe = bump(moe_bytes);
+    // the largest Q8_0 projection a chunk GEMM expands to bf16 (N x K values)
+    const size_t wbf_elems = std::max({(size_t) 2 * QD * D, (size_t) D * QD, (size_t) QKV * D, (size_t) GV * D,
+                                       (size_t) D * GV, (size_t) c.hc_lr * HCD});
+    const size_t owbf = bump(wbf_elems * 2);
     size_t ope = 0, opeh = 0, opk = 0, opv = 0, opg = 0, opn = 0;
     if (c.ple) {
         ope = bump(b * D * 4); opeh = bump(b * D * 2); opk = bump(b * HCD * 4); opv = bump(b * D * 4);
@@ -1610,6 +1616,8 @@ int wzy_stage::prefill_reserve(int B) {
     pf.idx_raw = (float*) (u + oir); pf.q_idx = (float*) (u + oqi); pf.scores = (float*) (u + osc);
     pf.sel = (int*) (u + osel); pf.cnt = (int*) (u + ocnt);
     pf.moe_ws = u + omoe;
+    pf.wbf = (uint16_t*) (u + owbf);
+    pf.wbf_elems = wbf_elems;
     if (c.ple) {
         pf.ple_emb = (float*) (u + ope); pf.ple_embh = (uint16_t*) (u + opeh); pf.ple_k = (float*) (u + opk);
         pf.ple_v = (float*) (u + opv); pf.ple_gat = (float*) (u + opg); pf.ple_n = (float*) (u + opn);
@@ -1652,6 +1660,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
         g.a = a; g.lda = lda; g.M = B; g.N = N; g.K = K;
         if (q) { g.wq = q->q; g.ws = q->s; } else { g.wb = wb; }
         g.y = y; g.yb = yb; g.ldy = ldy;
+        g.wscratch = pf.wbf; g.wscratch_elems = pf.wbf_elems;
         return launch_pf_gemm(g, st);
     };
     // hyper-connection read of the chunk: R (with the pending block folded in when bo != null) ->
@@ -1668,6 +1677,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
             PfGemm g{};
             g.a = pf.xn; g.lda = HCD; g.M = B; g.N = HCLR; g.K = HCD;
             g.wq = down.q; g.ws = down.s; g.y = pf.lo; g.ldy = HCLR; g.ksplit = down_split;
+            g.wscratch = pf.wbf; g.wscratch_elems = pf.wbf_elems;
             WZY_TRY(launch_pf_gemm(g, st));
         }
         WZY_TRY(launch_pf_silu_div(pf.lo, pf.loh, (size_t) B * HCLR, down_split, inv_hc, st));
@@ -1675,6 +1685,7 @@ int wzy_stage::enqueue_prefill(int p0, int B, float* us_parts) {
         g.a = pf.loh; g.lda = HCLR; g.M = B; g.N = HCD; g.K = HCLR;
         g.wq = up.q; g.ws = up.s;
         g.um_xn = pf.xn; g.um_mixed = pf.mixed; g.um_xh = pf.xh; g.um_d = D;
+        g.wscratch = pf.wbf; g.wscratch_elems = pf.wbf_elems;
         return launch_pf_gemm(g, st);
     };
 

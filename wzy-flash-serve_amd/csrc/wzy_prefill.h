@@ -24,7 +24,11 @@ struct PfGemm {
     float* y; uint16_t* yb; int ldy;
     int ksplit;
     const uint16_t* um_xn; float* um_mixed; uint16_t* um_xh; int um_d;
+    // optional bf16 scratch of at least N x K values: Q8_0 weights of a launch with PF_DEQ_MIN_M or more
+    // rows are expanded into it once (bf16(q * scale), the kernel's own rounding) and read as bf16
+    uint16_t* wscratch; size_t wscratch_elems;
 };
+constexpr int PF_DEQ_MIN_M = 512;
 int launch_pf_gemm(const PfGemm& g, hipStream_t st);
 
 // token embeddings of B rows broadcast to the HC streams: R [B][hc][D]
