@@ -858,8 +858,12 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
     }
     // K staging: thread -> cell kc = tid / 4, dims 64 * (tid % 4) .. +63 (64 code bytes, one scale)
     const int kc = tid >> 2, kd0 = (tid & 3) * 64;
-    // V staging: thread -> cells 4 * (tid / 16) .. +3, dims 16 * (tid % 16) .. +15
+    // V staging: thread -> cells 4 * (tid / 16) .. +3, dims 16 * (tid % 16) .. +15.  Row d of V^T holds
+    // its cells rotated by vt_rot(d) = 16 * ((d / 16) % 8) (mod 64): the 16 threads that store one cell
+    // group write rows 16 apart, which would otherwise start in one LDS bank (a row is 36 words), and the
+    // 16 rows a P.V read spans share one rotation.
     const int vc0 = (tid >> 4) * 4, vd0 = (tid & 15) * 16;
+    auto vt_col = [](int d, int c) { return (c + 16 * ((d >> 4) & 7)) & (AT_C - 1); };
     uint4 kq[4], vq[4];
     uint16_t ksc = 0, vsc[4];
     int rid = 0;
@@ -916,7 +920,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
                 const uint32_t word = i < 4 ? vq[u].x : i < 8 ? vq[u].y : i < 12 ? vq[u].z : vq[u].w;
                 v[u] = (_Float16) (int8_t) (word >> (8 * (i & 3))) * vs[u];
             }
-            *(f16x4_t*) &sVt[vd0 + i][vc0] = v;
+            *(f16x4_t*) &sVt[vd0 + i][vt_col(vd0, vc0)] = v;
         }
     };
 
@@ -1003,7 +1007,8 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
                 const f16x4_t pv = h4_from(&sP[sb][l16][ks * 16 + 4 * kq4]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const f16x4_t vv = h4_from(&sVt[64 * w + 16 * db + l16][AT_B * sb + ks * 16 + 4 * kq4]);
+                    const int d = 64 * w + 16 * db + l16;
+                    const f16x4_t vv = h4_from(&sVt[d][vt_col(d, AT_B * sb + ks * 16 + 4 * kq4)]);
                     acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pv, vv, acc[db], 0, 0, 0);
                 }
             }
