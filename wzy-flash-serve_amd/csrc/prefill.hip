@@ -819,7 +819,17 @@ __global__ void __launch_bounds__(256, 3) pf_score_kernel(QsaScoreArgs a) {
 constexpr int AT_C = 64;                      // cells per load step (two softmax blocks of 32)
 constexpr int AT_B = 32;                      // cells per softmax block
 constexpr int AT_QLD = 256 + 8;               // LDS row strides (halves)
-constexpr int AT_VLD = AT_C + 8;
+constexpr int AT_VLD = AT_C + 4;
+
+// LDS placement of K dim d in a cell row: the upper 128 dims swap neighbouring 4-dim groups, so the
+// 64 lanes of a K staging store (16 cells x 4 dim quarters; quarters q and q + 2 lie 64 words apart)
+// start in 32 different banks.  The score reads take one 16-dim slice, so they see the same pattern
+// as without the swap.
+WZY_DEV int at_kcol(int d) { return d ^ ((d >> 5) & 4); }
+// LDS column of cell c in row d of V^T: the cells are rotated by 8 * ((d / 16) % 8) (mod 64), so the
+// 16 lanes that stage one cell group (rows 16 apart) start in different banks; the 16 rows a P.V read
+// spans share one rotation.
+WZY_DEV int at_vcol(int d, int c) { return (c + 8 * ((d >> 4) & 7)) & (AT_C - 1); }
 
 WZY_DEV f16x4_t h4_from(const _Float16* p) { return *(const f16x4_t*) p; }
 
@@ -831,7 +841,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
     _Float16 (*const sVt)[AT_VLD] = (_Float16 (*)[AT_VLD]) sU;
     static_assert(AT_C * AT_QLD <= 256 * AT_VLD, "K fits the shared region");
     __shared__ __align__(16) _Float16 sP[2][16][AT_B + 8];
-    __shared__ float sS[16][AT_C + 1];
+    __shared__ float sS[16][AT_C + 4];
     __shared__ float s_m[16], s_l[16], s_al[2][16];
     __shared__ int sIds[2][AT_C];                 // selected cell ids of the next two steps
     const QsaDims& dm = a.dm;
@@ -858,12 +868,8 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
     }
     // K staging: thread -> cell kc = tid / 4, dims 64 * (tid % 4) .. +63 (64 code bytes, one scale)
     const int kc = tid >> 2, kd0 = (tid & 3) * 64;
-    // V staging: thread -> cells 4 * (tid / 16) .. +3, dims 16 * (tid % 16) .. +15.  Row d of V^T holds
-    // its cells rotated by vt_rot(d) = 16 * ((d / 16) % 8) (mod 64): the 16 threads that store one cell
-    // group write rows 16 apart, which would otherwise start in one LDS bank (a row is 36 words), and the
-    // 16 rows a P.V read spans share one rotation.
+    // V staging: thread -> cells 4 * (tid / 16) .. +3, dims 16 * (tid % 16) .. +15
     const int vc0 = (tid >> 4) * 4, vd0 = (tid & 15) * 16;
-    auto vt_col = [](int d, int c) { return (c + 16 * ((d >> 4) & 7)) & (AT_C - 1); };
     uint4 kq[4], vq[4];
     uint16_t ksc = 0, vsc[4];
     int rid = 0;
@@ -904,7 +910,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
                 f16x4_t v;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) v[b] = (_Float16) (int8_t) (wv[i] >> (8 * b)) * s;
-                *(f16x4_t*) &sK[kc][kd0 + 16 * u + 4 * i] = v;
+                *(f16x4_t*) &sK[kc][at_kcol(kd0 + 16 * u + 4 * i)] = v;
             }
         }
     };
@@ -920,7 +926,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
                 const uint32_t word = i < 4 ? vq[u].x : i < 8 ? vq[u].y : i < 12 ? vq[u].z : vq[u].w;
                 v[u] = (_Float16) (int8_t) (word >> (8 * (i & 3))) * vs[u];
             }
-            *(f16x4_t*) &sVt[vd0 + i][vt_col(vd0, vc0)] = v;
+            *(f16x4_t*) &sVt[vd0 + i][at_vcol(vd0, vc0)] = v;
         }
     };
 
@@ -955,7 +961,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
             for (int kk = 0; kk < 8; ++kk) {
                 sc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[kk], h4_from(&sK[16 * w + l16][kk * 16 + 4 * kq4]), sc0,
                                                             0, 0, 0);
-                sc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[8 + kk], h4_from(&sK[16 * w + l16][128 + kk * 16 + 4 * kq4]),
+                sc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(qa[8 + kk], h4_from(&sK[16 * w + l16][at_kcol(128 + kk * 16 + 4 * kq4)]),
                                                             sc1, 0, 0, 0);
             }
 #pragma unroll
@@ -1008,7 +1014,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const int d = 64 * w + 16 * db + l16;
-                    const f16x4_t vv = h4_from(&sVt[d][vt_col(d, AT_B * sb + ks * 16 + 4 * kq4)]);
+                    const f16x4_t vv = h4_from(&sVt[d][at_vcol(d, AT_B * sb + ks * 16 + 4 * kq4)]);
                     acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pv, vv, acc[db], 0, 0, 0);
                 }
             }
