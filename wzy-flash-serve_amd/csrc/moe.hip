@@ -376,9 +376,11 @@ WZY_DEV void publish_routing(const RouteLds& r, const MoeGuArgs& a, int n_ent) {
     if (threadIdx.x == 0) *a.n_groups = r.n_groups;
 }
 
-// chunk `cc` of x row `t` ([rows x D] fp32) quantised per 16 into LDS slot i: 16 f16 pairs
-// (nvfp4_chunk_fma_h's order) and the two per-16 scales
-WZY_DEV void stage_x16(const float* __restrict__ x, int D, int t, int cc, int i, half2_t* s_xh, float2* s_xs2) {
+// chunk `cc` of x row `t` ([rows x D] fp32) quantised per 16 into LDS slot i of nx: 16 f16 pairs
+// (nvfp4_chunk_fma_h's order) as four 16-byte quarters, quarter q at uint4 index q * nx + i (lanes
+// that read consecutive slots then read consecutive 16-byte words, not words 64 bytes apart in one
+// bank group), and the two per-16 scales
+WZY_DEV void stage_x16(const float* __restrict__ x, int D, int t, int cc, int i, int nx, half2_t* s_xh, float2* s_xs2) {
     const float4* xp = (const float4*) (x + (size_t) t * D + (size_t) cc * 32);
     float v[32];
 #pragma unroll
@@ -391,7 +393,7 @@ WZY_DEV void stage_x16(const float* __restrict__ x, int D, int t, int cc, int i,
     quant16_pairs(v, xq, da, db);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        ((uint4*) (s_xh + (size_t) i * 16))[k] = make_uint4(__builtin_bit_cast(uint32_t, xq[4 * k]),
+        ((uint4*) s_xh)[(size_t) k * nx + i] = make_uint4(__builtin_bit_cast(uint32_t, xq[4 * k]),
                                                            __builtin_bit_cast(uint32_t, xq[4 * k + 1]),
                                                            __builtin_bit_cast(uint32_t, xq[4 * k + 2]),
                                                            __builtin_bit_cast(uint32_t, xq[4 * k + 3]));
@@ -531,7 +533,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
                 }
             }
         };
-        auto stage16 = [&](int t, int cc, int i) { stage_x16(a.x, D, t, cc, i, s_xh, s_xs2); };
+        auto stage16 = [&](int t, int cc, int i) { stage_x16(a.x, D, t, cc, i, T * nc, s_xh, s_xs2); };
         if constexpr (ROUTE) {
             // in-workgroup routing (one-row windows): the logits are prefetched, x is staged while they
             // arrive, every workgroup routes the row (workgroup 0 publishes the tables for moe_down)
@@ -581,7 +583,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_kernel(MoeGuArgs a) {
                     half2_t xp[16];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
+                        const uint4 u = ((const uint4*) s_xh)[(size_t) q * (T * nc) + xi];
                         xp[4 * q] = __builtin_bit_cast(half2_t, u.x);
                         xp[4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
                         xp[4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
@@ -665,7 +667,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_window_kernel(MoeGuArgs a) {
         float p[(T + 3) / 4][RV];
         route_prefetch<T, RV>(a.logits, a.E, p);
         // waves 4-7 stage x first (waves 0-3 route)
-        for (int i = (tid + 256) & 511; i < T * nc; i += 512) stage_x16(a.x, D, i / nc, i % nc, i, s_xh, s_xs2);
+        for (int i = (tid + 256) & 511; i < T * nc; i += 512) stage_x16(a.x, D, i / nc, i % nc, i, T * nc, s_xh, s_xs2);
         route_compute<T, RV>(p, a.E, K, r);              // ends with a barrier
     }
     if (bid == 0) publish_routing(r, a, T * K);
@@ -711,7 +713,7 @@ __global__ void __launch_bounds__(512) moe_gate_up_window_kernel(MoeGuArgs a) {
                     const int xi = (r.gmem[g][m] / K) * nc + c;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        const uint4 u = ((const uint4*) (s_xh + (size_t) xi * 16))[q];
+                        const uint4 u = ((const uint4*) s_xh)[(size_t) q * (T * nc) + xi];
                         xq[m][4 * q] = __builtin_bit_cast(half2_t, u.x);
                         xq[m][4 * q + 1] = __builtin_bit_cast(half2_t, u.y);
                         xq[m][4 * q + 2] = __builtin_bit_cast(half2_t, u.z);
@@ -897,7 +899,7 @@ __global__ void __launch_bounds__(256) moe_router_kernel(MoeRtArgs a) {
 // one-row windows, 1024 for windows of several rows, whose items are up to T*K + 1 groups x 8 rows);
 // a slot issues the loads of DN_BATCH items before computing any of them.  One 32-value chunk per lane per item
 // (F = 512: 16 chunks per row).  STAGE: the routed and shared activations are copied to LDS first
-// (dynamic LDS: routed activations as f16 pairs [n_ent][F/32][16], as [n_ent][F/16] float, shq
+// (dynamic LDS: routed activations as f16 pairs in 16-byte quarters [4][n_ent * F/32], as [n_ent][F/16] float, shq
 // halves [T][F/32] x2 int4, shs [T][F/32] float).
 // reference: exp_down_2r_grouped (src/wzy_kernels_v2.cuh:1725-1834), shared down launch_gemm_q8p
 // (src/wzy_stage_v2.cuh:714), moe_combine_shared_multi (src/wzy_kernels_v2.cuh:1281-1294).
@@ -921,7 +923,7 @@ __global__ void __launch_bounds__(NT) moe_down_kernel(MoeDnArgs a) {
     int4* s_sha = (int4*) s_dyn;                      // [T * nchunk] first / second 16-byte halves
     int4* s_shb = s_sha + (size_t) T * nchunk;
     float* s_shs = (float*) (s_shb + (size_t) T * nchunk);
-    uint4* s_ah = (uint4*) (s_shs + dn_shs_floats(T, nchunk));   // [n_ent * nchunk][4]: 16 f16 pairs per chunk
+    uint4* s_ah = (uint4*) (s_shs + dn_shs_floats(T, nchunk));   // [4][n_ent * nchunk]: quarter k of a chunk's 16 f16 pairs
     float* s_as = (float*) (s_ah + (size_t) n_ent * nchunk * 4);
     // Item `tid` of every table and staging copy is loaded (clamped index, no branch) before the
     // first LDS write: a stride loop per table would wait for one table's loads before requesting
@@ -960,7 +962,7 @@ __global__ void __launch_bounds__(NT) moe_down_kernel(MoeDnArgs a) {
         if (STAGE) {
             if (tid < n_aq)
 #pragma unroll
-                for (int k = 0; k < 4; ++k) s_ah[(size_t) tid * 4 + k] = xh[k];
+                for (int k = 0; k < 4; ++k) s_ah[(size_t) k * n_aq + tid] = xh[k];
             if (tid < n_as4) ((float4*) s_as)[tid] = xs4;
         }
         {                                             // silu_mul_quant32: d = amax/127, q = rint(v*127/amax)
@@ -984,7 +986,7 @@ __global__ void __launch_bounds__(NT) moe_down_kernel(MoeDnArgs a) {
         for (int i = tid + NT; i < n_aq; i += NT) {
             const uint4* xp = (const uint4*) (a.ah16 + (size_t) i * 32);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) s_ah[(size_t) i * 4 + k] = xp[k];
+            for (int k = 0; k < 4; ++k) s_ah[(size_t) k * n_aq + i] = xp[k];
         }
         for (int i = tid + NT; i < n_as4; i += NT) ((float4*) s_as)[i] = ((const float4*) a.as16)[i];
     }
@@ -1057,13 +1059,14 @@ __global__ void __launch_bounds__(NT) moe_down_kernel(MoeDnArgs a) {
                         if (m < cnt) {
                             const int f = s_gmem[g][m];
                             const int xi = f * nchunk + c;
-                            const uint4* xq = STAGE ? s_ah + (size_t) xi * 4 : (const uint4*) (a.ah16 + (size_t) xi * 32);
+                            const uint4* xq = STAGE ? s_ah + xi : (const uint4*) (a.ah16 + (size_t) xi * 32);
+                            const size_t xstep = STAGE ? (size_t) n_aq : 1;   // LDS: quarter-major
                             const float2 xs = STAGE ? ((const float2*) s_as)[xi]
                                                     : *(const float2*) (a.as16 + (size_t) f * (F / 16) + 2 * c);
                             half2_t xp[16];
 #pragma unroll
                             for (int k = 0; k < 4; ++k) {
-                                const uint4 u = xq[k];
+                                const uint4 u = xq[k * xstep];
                                 xp[4 * k] = __builtin_bit_cast(half2_t, u.x);
                                 xp[4 * k + 1] = __builtin_bit_cast(half2_t, u.y);
                                 xp[4 * k + 2] = __builtin_bit_cast(half2_t, u.z);
