@@ -823,12 +823,13 @@ constexpr int AT_VLD = AT_C + 4;
 
 // LDS placement of K dim d in a cell row: the upper 128 dims swap neighbouring 4-dim groups, so the
 // 64 lanes of a K staging store (16 cells x 4 dim quarters; quarters q and q + 2 lie 64 words apart)
-// start in 32 different banks.  The score reads take one 16-dim slice, so they see the same pattern
-// as without the swap.
+// spread over more banks.  The score reads take one 16-dim slice, so their pattern is unchanged.
+// This swap, the V^T rotation below and the pitches of V^T and sS were chosen by measuring LDS bank
+// conflict counts and the prefill time of variants.
 WZY_DEV int at_kcol(int d) { return d ^ ((d >> 5) & 4); }
 // LDS column of cell c in row d of V^T: the cells are rotated by 8 * ((d / 16) % 8) (mod 64), so the
-// 16 lanes that stage one cell group (rows 16 apart) start in different banks; the 16 rows a P.V read
-// spans share one rotation.
+// 16 lanes that stage one cell group (rows 16 apart, which the pitch alone would put in one bank
+// group) start in different banks; the 16 rows a P.V read spans share one rotation.
 WZY_DEV int at_vcol(int d, int c) { return (c + 8 * ((d >> 4) & 7)) & (AT_C - 1); }
 
 WZY_DEV f16x4_t h4_from(const _Float16* p) { return *(const f16x4_t*) p; }
@@ -841,7 +842,7 @@ __global__ void __launch_bounds__(256, 3) pf_attn_kernel(PfAttn a) {
     _Float16 (*const sVt)[AT_VLD] = (_Float16 (*)[AT_VLD]) sU;
     static_assert(AT_C * AT_QLD <= 256 * AT_VLD, "K fits the shared region");
     __shared__ __align__(16) _Float16 sP[2][16][AT_B + 8];
-    __shared__ float sS[16][AT_C + 4];
+    __shared__ float sS[16][AT_C + 4];                 // pitch 68: a wave's score writes (rows 4 apart) hit distinct banks
     __shared__ float s_m[16], s_l[16], s_al[2][16];
     __shared__ int sIds[2][AT_C];                 // selected cell ids of the next two steps
     const QsaDims& dm = a.dm;
